@@ -1,0 +1,76 @@
+/* include/sepia_hip_ext.h -- additive entry points of libsepia_hip.so that have
+ * no counterpart in the reference's src/sepia_gpu.h. Nothing here changes
+ * the 30 drop-in functions; sepia.c keeps working without these.
+ *
+ * Same conventions as sepia_gpu.h: 1 / non-NULL on success, 0 / NULL after a
+ * "sepia: hip: ..." log line on failure, single host thread, one stream,
+ * every op needs an open batch.
+ */
+#ifndef SEPIA_HIP_EXT_H
+#define SEPIA_HIP_EXT_H
+#include "sepia_gpu.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* GGUF type ids the reference's src/quants.h:6-10 lacks (ggml enum values,
+ * reference tools/gguf_inspect.py:71-77). */
+#define SEPIA_T_Q2_K    10
+#define SEPIA_T_Q3_K    11
+#define SEPIA_T_IQ2_XXS 16
+
+/* One projection of a stack of experts: expert e's row-major quantized
+ * matrix starts at byte off + e * stride of buf (GGUF stores routed experts
+ * as one 3-D tensor, so the stride is uniform). */
+typedef struct {
+    SepiaGpuBuf *buf;
+    size_t off;
+    size_t stride;
+    int ggml_type;
+} SepiaExpertTensor;
+
+/* One sparse MoE layer (reference src/sepia.c:1377-1470 and :3831-3974;
+ * spec docs/architecture-notes.md:342-474). */
+typedef struct {
+    int64_t hidden;                 /* 6144 for Inkling */
+    int64_t inter;                  /* moe_intermediate_size, 3072 */
+    int n_routed, n_shared, topk;   /* 256, 2, 6 */
+    float route_scale;              /* 8.0 */
+    float global_scale;             /* per-layer ffn_gscale */
+    SepiaGpuBuf *router_w;          /* f32 [n_routed + n_shared, hidden] */
+    size_t router_w_off;
+    SepiaGpuBuf *router_bias;       /* f32 [n_routed], selection only */
+    size_t router_bias_off;
+    SepiaExpertTensor gate, up;     /* routed, [inter, hidden] each */
+    SepiaExpertTensor down;         /* routed, [hidden, inter] */
+    SepiaExpertTensor s_gate, s_up; /* shared, [inter, hidden] */
+    SepiaExpertTensor s_down;       /* shared, [hidden, inter] */
+} SepiaMoeLayerDesc;
+
+/* y = MoE(x) for one token, entirely on the GPU (router, selection, the
+ * selected and shared experts, weighted sum) with no host round trip.
+ * x, y: f32 [hidden] at offset 0. route_out (optional, may be NULL): receives
+ * int32 idx[topk] followed by f32 w[topk + n_shared] (routed weights, then
+ * shared gammas) -- the content of the reference's --route-log record. */
+int sepia_gpu_moe_decode(const SepiaMoeLayerDesc *layer, SepiaGpuBuf *x, SepiaGpuBuf *y,
+                         SepiaGpuBuf *route_out);
+
+/* Benchmark and test support. Fills n_blocks blocks of `ggml_type` at byte
+ * `off` of buf with seeded random bytes, then sets every f16 scale field of
+ * each block to a value uniform in [lo, hi] (rounded to f16). */
+int sepia_hip_synth_blocks(int ggml_type, SepiaGpuBuf *buf, size_t off, int64_t n_blocks,
+                           uint64_t seed, float lo, float hi);
+
+/* Installs the 256-entry IQ2_XXS codebook (u64 per entry, byte j = magnitude
+ * of weight j). The real table is not available to this build; until one is
+ * installed IQ2_XXS is rejected as unsupported. Needs init. */
+int sepia_hip_set_iq2xxs_grid(const uint64_t *grid256);
+
+/* The hipStream_t every op is issued on (for hipEvent timing). */
+void *sepia_hip_stream(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

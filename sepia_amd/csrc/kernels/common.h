@@ -1,0 +1,61 @@
+// common.h -- device helpers shared by every sepia kernel (gfx950, wave64).
+//
+// The whole code object is compiled with -ffp-contract=off: products and
+// sums round separately unless a kernel asks for a fused multiply-add
+// explicitly with __builtin_fmaf. The dequantizers rely on that for bit
+// exactness; the accumulating kernels use explicit FMAs.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define SEPIA_WAVE 64
+
+// Type ids: the GGUF ggml_type enum (reference src/quants.h:6-10 plus Q2_K,
+// Q3_K, IQ2_XXS from tools/gguf_inspect.py:62-84).
+enum {
+    ST_F32 = 0, ST_F16 = 1, ST_Q8_0 = 8, ST_Q2_K = 10, ST_Q3_K = 11, ST_Q4_K = 12,
+    ST_Q5_K = 13, ST_Q6_K = 14, ST_IQ2_XXS = 16, ST_IQ2_XS = 17, ST_IQ3_XXS = 18, ST_IQ4_XS = 23,
+};
+
+__device__ __forceinline__ uint32_t ld_u8(const uint8_t *p) { return *p; }
+__device__ __forceinline__ uint32_t ld_u16(const uint8_t *p) { return (uint32_t)p[0] | ((uint32_t)p[1] << 8); }
+__device__ __forceinline__ uint32_t ld_u32(const uint8_t *p) {
+    return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
+}
+
+// binary16 -> binary32 through the hardware conversion: exact for every
+// finite value and infinity (f16 subnormals become f32 normals).
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
+    _Float16 v = __builtin_bit_cast(_Float16, (uint16_t)h);
+    return (float)v;
+}
+
+// binary16 -> binary32 with the integer recipe that also keeps NaN payloads
+// unquieted (reference src/quants.c:77-96); used where the raw f16 value is
+// the output (the F16 dequant), not for block scales.
+__device__ __forceinline__ float f16_bits_to_f32_exact(uint32_t h) {
+    uint32_t sign = (h >> 15) << 31;
+    int32_t e = (h >> 10) & 31;
+    uint32_t m = h & 0x3FFu, out;
+    if (e == 31) {
+        out = sign | 0x7F800000u | (m << 13);
+    } else if (e != 0) {
+        out = sign | ((uint32_t)(e + 112) << 23) | (m << 13);
+    } else if (m == 0) {
+        out = sign;
+    } else {
+        int32_t lz = __builtin_clz(m) - 21;      // shifts that bring bit 10 up
+        out = sign | ((uint32_t)(113 - lz) << 23) | (((m << lz) & 0x3FFu) << 13);
+    }
+    return __builtin_bit_cast(float, out);
+}
+
+// Sum over the 64 lanes of a wave; every lane gets the total.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, SEPIA_WAVE);
+    return v;
+}
+
+__device__ __forceinline__ float sigmoid_f32(float x) { return 1.0f / (1.0f + expf(-x)); }
+__device__ __forceinline__ float silu_f32(float x) { return x * sigmoid_f32(x); }

@@ -1,0 +1,898 @@
+/* sepia_hip.c -- HIP host backend for SEPIA's GPU ABI on AMD Instinct MI355X.
+ *
+ * The counterpart of the reference's src/sepia_metal.m: it implements every
+ * function of include/sepia_gpu.h (reference src/sepia_gpu.h) plus the
+ * additive entries of include/sepia_hip_ext.h, over the HIP runtime C API.
+ * Kernels are prebuilt for gfx950 into sepia_kernels.hsaco and loaded with
+ * hipModuleLoad from the directory given to sepia_gpu_init (the reference
+ * compiles metal_dir's *.metal at the same point, src/sepia_metal.m:103-149).
+ *
+ * Single host thread, no locking, one in-order HIP stream at default
+ * priority. Every function logs one "sepia: hip: ..." line and returns 0/NULL
+ * on failure; nothing exits (src/sepia_gpu.h:1-3, src/sepia_metal.m:15-18).
+ */
+#define __HIP_PLATFORM_AMD__ 1
+#include <hip/hip_runtime_api.h>
+
+#include "../../include/sepia_gpu.h"
+#include "../../include/sepia_hip_ext.h"
+
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+#include <unistd.h>
+
+static void logf_(const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    fprintf(stderr, "sepia: hip: ");
+    vfprintf(stderr, fmt, ap);
+    fprintf(stderr, "\n");
+    va_end(ap);
+}
+#define LOG(...) logf_(__VA_ARGS__)
+
+/* ------------------------------------------------------------ kernels --- */
+enum {
+    K_DQ_Q8_0, K_DQ_Q2_K, K_DQ_Q3_K, K_DQ_Q4_K, K_DQ_Q5_K, K_DQ_Q6_K,
+    K_DQ_IQ2_XXS, K_DQ_IQ2_XS, K_DQ_IQ3_XXS, K_DQ_IQ4_XS, K_DQ_F16,
+    K_MV_Q8_0, K_MV_Q2_K, K_MV_Q3_K, K_MV_Q4_K, K_MV_Q5_K, K_MV_Q6_K,
+    K_MV_IQ2_XXS, K_MV_IQ2_XS, K_MV_IQ3_XXS, K_MV_IQ4_XS,
+    K_MATVEC_F32, K_SILU_MUL, K_ADD, K_SCALE, K_COPY, K_TOUCH, K_RMSNORM, K_SOFTMAX,
+    K_SCONV, K_SCONV_HIST, K_MOE_SELECT, K_MOE_GATEUP, K_MOE_DOWN, K_SYNTH_FILL, K_SYNTH_F16,
+    K_COUNT
+};
+static const char *const k_names[K_COUNT] = {
+    "sepia_dequant_rows_q8_0", "sepia_dequant_rows_q2_k", "sepia_dequant_rows_q3_k",
+    "sepia_dequant_rows_q4_k", "sepia_dequant_rows_q5_k", "sepia_dequant_rows_q6_k",
+    "sepia_dequant_rows_iq2_xxs", "sepia_dequant_rows_iq2_xs", "sepia_dequant_rows_iq3_xxs",
+    "sepia_dequant_rows_iq4_xs", "sepia_dequant_rows_f16",
+    "sepia_matvec_generic_q8_0", "sepia_matvec_generic_q2_k", "sepia_matvec_generic_q3_k",
+    "sepia_matvec_generic_q4_k", "sepia_matvec_generic_q5_k", "sepia_matvec_generic_q6_k",
+    "sepia_matvec_generic_iq2_xxs", "sepia_matvec_generic_iq2_xs", "sepia_matvec_generic_iq3_xxs",
+    "sepia_matvec_generic_iq4_xs",
+    "sepia_matvec_f32", "sepia_silu_mul_f32", "sepia_add_f32", "sepia_scale_f32", "sepia_copy_f32",
+    "sepia_touch_f32", "sepia_rmsnorm_f32", "sepia_softmax_f32", "sepia_sconv_f32",
+    "sepia_sconv_hist_roll_f32", "sepia_moe_select", "sepia_moe_gateup", "sepia_moe_down",
+    "sepia_synth_fill", "sepia_synth_patch_f16",
+};
+
+/* GGUF block geometry (reference src/quants.c:46-51; tools/gguf_inspect.py:109-117). */
+typedef struct {
+    int type;
+    int64_t elems;
+    size_t bytes;
+    int parts;      /* 32-weight parts per block (dequant threads per block) */
+    int k_dq, k_mv; /* kernel ids, -1 if none */
+    int f16_off[2]; /* byte offsets of f16 scale fields, -1 = none */
+} TypeInfo;
+static const TypeInfo k_types[] = {
+    { 1, 1, 2, 1, K_DQ_F16, -1, { -1, -1 } },
+    { 8, 32, 34, 1, K_DQ_Q8_0, K_MV_Q8_0, { 0, -1 } },
+    { 10, 256, 84, 8, K_DQ_Q2_K, K_MV_Q2_K, { 80, 82 } },
+    { 11, 256, 110, 8, K_DQ_Q3_K, K_MV_Q3_K, { 108, -1 } },
+    { 12, 256, 144, 8, K_DQ_Q4_K, K_MV_Q4_K, { 0, 2 } },
+    { 13, 256, 176, 8, K_DQ_Q5_K, K_MV_Q5_K, { 0, 2 } },
+    { 14, 256, 210, 8, K_DQ_Q6_K, K_MV_Q6_K, { 208, -1 } },
+    { 16, 256, 66, 8, K_DQ_IQ2_XXS, K_MV_IQ2_XXS, { 0, -1 } },
+    { 17, 256, 74, 8, K_DQ_IQ2_XS, K_MV_IQ2_XS, { 0, -1 } },
+    { 18, 256, 98, 8, K_DQ_IQ3_XXS, K_MV_IQ3_XXS, { 0, -1 } },
+    { 23, 256, 136, 8, K_DQ_IQ4_XS, K_MV_IQ4_XS, { 0, -1 } },
+};
+
+static int g_available;
+static int g_have_iq2xxs;
+static char g_device_name[256];
+static hipModule_t g_module;
+static hipStream_t g_stream;
+static hipFunction_t g_fn[K_COUNT];
+static int g_batch_open;
+
+static const TypeInfo *type_info(int t) {
+    for (size_t i = 0; i < sizeof k_types / sizeof k_types[0]; i++) {
+        if (k_types[i].type != t) continue;
+        if (t == SEPIA_T_IQ2_XXS && !g_have_iq2xxs) return NULL;
+        return &k_types[i];
+    }
+    return NULL;
+}
+
+/* ------------------------------------------------------------ buffers --- */
+enum { BUF_SHARED = 0, BUF_PRIVATE = 1, BUF_WRAPPED = 2 };
+
+/* Device allocations are padded by DEV_PAD bytes so a vectorised kernel may
+ * read a full 16-byte line that straddles the logical end of a buffer. */
+#define DEV_ALIGN 256u
+#define DEV_PAD 256u
+
+struct SepiaGpuBuf {
+    uint8_t *dev;
+    void *host;        /* pinned copy (shared), caller's base (wrapped), NULL (private) */
+    size_t len;
+    int kind;
+    int exposed;       /* host_ptr handed out: the host may write it */
+    int host_newer;    /* upload before the next device access */
+    int dev_newer;     /* download at sepia_gpu_end */
+    struct SepiaGpuBuf *prev, *next; /* registry of shared buffers */
+};
+static SepiaGpuBuf *g_shared;
+
+static size_t dev_bytes(size_t len) { return ((len + DEV_ALIGN - 1) / DEV_ALIGN) * DEV_ALIGN + DEV_PAD; }
+
+static int need_init(const char *op) {
+    if (!g_available) {
+        LOG("%s: GPU not initialized", op);
+        return 0;
+    }
+    return 1;
+}
+
+static int need_batch(const char *op) {
+    if (!need_init(op)) return 0;
+    if (!g_batch_open) {
+        LOG("%s: no active batch (call sepia_gpu_begin first)", op);
+        return 0;
+    }
+    return 1;
+}
+
+/* b holds [off, off + n) */
+static int chk(const SepiaGpuBuf *b, size_t off, size_t n, const char *op, const char *what) {
+    if (!b || !b->dev) {
+        LOG("%s: %s buffer is NULL", op, what);
+        return 0;
+    }
+    if (off > b->len || n > b->len - off) {
+        LOG("%s: %s range [%zu, +%zu) exceeds its buffer of %zu bytes", op, what, off, n, b->len);
+        return 0;
+    }
+    return 1;
+}
+
+/* Bring the device copy up to date before a kernel touches the buffer. */
+static int sync_in(SepiaGpuBuf *b, const char *op) {
+    if (b->kind == BUF_SHARED && b->host_newer) {
+        hipError_t e = hipMemcpyAsync(b->dev, b->host, b->len, hipMemcpyHostToDevice, g_stream);
+        if (e != hipSuccess) {
+            LOG("%s: upload failed: %s", op, hipGetErrorString(e));
+            return 0;
+        }
+        b->host_newer = 0;
+    }
+    return 1;
+}
+
+static int prep_in(SepiaGpuBuf *b, const char *op) { return sync_in(b, op); }
+static int prep_out(SepiaGpuBuf *b, const char *op) {
+    if (!sync_in(b, op)) return 0;
+    if (b->kind == BUF_SHARED) b->dev_newer = 1;
+    return 1;
+}
+
+static SepiaGpuBuf *new_buf(size_t len, int kind) {
+    SepiaGpuBuf *b = (SepiaGpuBuf *)calloc(1, sizeof *b);
+    if (!b) {
+        LOG("alloc: out of host memory");
+        return NULL;
+    }
+    b->len = len;
+    b->kind = kind;
+    hipError_t e = hipMalloc((void **)&b->dev, dev_bytes(len));
+    if (e != hipSuccess) {
+        LOG("alloc: hipMalloc(%zu) failed: %s", dev_bytes(len), hipGetErrorString(e));
+        free(b);
+        return NULL;
+    }
+    return b;
+}
+
+SepiaGpuBuf *sepia_gpu_alloc(size_t len, int gpu_private) {
+    if (!need_init("alloc")) return NULL;
+    if (len == 0) {
+        LOG("alloc: zero length");
+        return NULL;
+    }
+    SepiaGpuBuf *b = new_buf(len, gpu_private ? BUF_PRIVATE : BUF_SHARED);
+    if (!b) return NULL;
+    hipError_t e = hipMemsetAsync(b->dev, 0, dev_bytes(len), g_stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(g_stream);
+    if (e != hipSuccess) {
+        LOG("alloc: clearing the buffer failed: %s", hipGetErrorString(e));
+        hipFree(b->dev);
+        free(b);
+        return NULL;
+    }
+    if (b->kind == BUF_SHARED) {
+        e = hipHostMalloc(&b->host, len, hipHostMallocDefault);
+        if (e != hipSuccess) {
+            LOG("alloc: pinned host copy of %zu bytes failed: %s", len, hipGetErrorString(e));
+            hipFree(b->dev);
+            free(b);
+            return NULL;
+        }
+        memset(b->host, 0, len);
+        b->next = g_shared;
+        if (g_shared) g_shared->prev = b;
+        g_shared = b;
+    }
+    return b;
+}
+
+SepiaGpuBuf *sepia_gpu_wrap_mmap(void *base, size_t len) {
+    if (!need_init("wrap_mmap")) return NULL;
+    if (!base || len == 0) {
+        LOG("wrap_mmap: invalid base/len");
+        return NULL;
+    }
+    const size_t page = (size_t)sysconf(_SC_PAGESIZE);
+    if ((uintptr_t)base % page) {
+        LOG("wrap_mmap: base %p is not page-aligned (page=%zu)", base, page);
+        return NULL;
+    }
+    SepiaGpuBuf *b = new_buf(len, BUF_WRAPPED);
+    if (!b) return NULL;
+    hipError_t e = hipMemsetAsync(b->dev + len, 0, dev_bytes(len) - len, g_stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(b->dev, base, len, hipMemcpyHostToDevice, g_stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(g_stream);
+    if (e != hipSuccess) {
+        LOG("wrap_mmap: copy of %zu bytes into HBM failed: %s", len, hipGetErrorString(e));
+        hipFree(b->dev);
+        free(b);
+        return NULL;
+    }
+    b->host = base;
+    return b;
+}
+
+void sepia_gpu_free(SepiaGpuBuf *b) {
+    if (!b) return;
+    if (g_available) hipStreamSynchronize(g_stream);
+    if (b->kind == BUF_SHARED) {
+        if (b->prev) b->prev->next = b->next;
+        else g_shared = b->next;
+        if (b->next) b->next->prev = b->prev;
+        if (b->host) hipHostFree(b->host);
+    }
+    if (b->dev) hipFree(b->dev);
+    free(b);
+}
+
+void *sepia_gpu_host_ptr(SepiaGpuBuf *b) {
+    if (!b) return NULL;
+    if (b->kind == BUF_PRIVATE) return NULL;
+    if (b->kind == BUF_SHARED) {
+        b->exposed = 1;
+        b->host_newer = 1;
+    }
+    return b->host;
+}
+
+uint64_t sepia_gpu_gpu_addr(SepiaGpuBuf *b) { return b ? (uint64_t)(uintptr_t)b->dev : 0; }
+
+/* ------------------------------------------------------------ lifecycle - */
+int sepia_gpu_available(void) { return g_available; }
+
+int sepia_gpu_init(const char *kernel_dir) {
+    if (g_available) return 1;
+    if (!kernel_dir || !kernel_dir[0]) {
+        LOG("init requires the directory holding sepia_kernels.hsaco");
+        return 0;
+    }
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n < 1) {
+        LOG("no HIP device available (%s)", e == hipSuccess ? "0 devices" : hipGetErrorString(e));
+        return 0;
+    }
+    if ((e = hipSetDevice(0)) != hipSuccess) {
+        LOG("hipSetDevice(0) failed: %s", hipGetErrorString(e));
+        return 0;
+    }
+    hipDeviceProp_t prop;
+    if ((e = hipGetDeviceProperties(&prop, 0)) != hipSuccess) {
+        LOG("hipGetDeviceProperties failed: %s", hipGetErrorString(e));
+        return 0;
+    }
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+        LOG("device 0 is %s (%s); this library is built for gfx950 only", prop.name, prop.gcnArchName);
+        return 0;
+    }
+    char path[4096];
+    if ((size_t)snprintf(path, sizeof path, "%s/sepia_kernels.hsaco", kernel_dir) >= sizeof path) {
+        LOG("init: kernel_dir path too long");
+        return 0;
+    }
+    if ((e = hipStreamCreate(&g_stream)) != hipSuccess) {
+        LOG("failed to create a stream: %s", hipGetErrorString(e));
+        return 0;
+    }
+    if ((e = hipModuleLoad(&g_module, path)) != hipSuccess) {
+        LOG("cannot load %s: %s", path, hipGetErrorString(e));
+        hipStreamDestroy(g_stream);
+        return 0;
+    }
+    for (int k = 0; k < K_COUNT; k++) {
+        if ((e = hipModuleGetFunction(&g_fn[k], g_module, k_names[k])) != hipSuccess) {
+            LOG("kernel \"%s\" not found in %s: %s", k_names[k], path, hipGetErrorString(e));
+            hipModuleUnload(g_module);
+            hipStreamDestroy(g_stream);
+            return 0;
+        }
+    }
+    snprintf(g_device_name, sizeof g_device_name, "%s", prop.name);
+    g_available = 1;
+    g_batch_open = 0;
+    g_have_iq2xxs = 0;
+    return 1;
+}
+
+static void *g_scratch;
+static size_t g_scratch_len;
+
+void sepia_gpu_shutdown(void) {
+    if (!g_available) return;
+    hipStreamSynchronize(g_stream);
+    if (g_scratch) hipFree(g_scratch);
+    g_scratch = NULL;
+    g_scratch_len = 0;
+    hipModuleUnload(g_module);
+    hipStreamDestroy(g_stream);
+    g_available = 0;
+    g_batch_open = 0;
+    g_have_iq2xxs = 0;
+    g_device_name[0] = '\0';
+}
+
+const char *sepia_gpu_device_name(void) { return g_available ? g_device_name : NULL; }
+
+void *sepia_hip_stream(void) { return g_available ? (void *)g_stream : NULL; }
+
+/* ------------------------------------------------------------ batching -- */
+int sepia_gpu_begin(void) {
+    if (!need_init("begin")) return 0;
+    if (g_batch_open) {
+        LOG("begin: a batch is already active");
+        return 0;
+    }
+    g_batch_open = 1;
+    return 1;
+}
+
+/* Ops are launched as they are issued, so the queued work is already in
+ * the GPU's hands; flush keeps the batch open (src/sepia_gpu.h:72-79). */
+int sepia_gpu_flush(void) {
+    if (!need_init("flush")) return 0;
+    if (!g_batch_open) {
+        LOG("flush: no active batch");
+        return 0;
+    }
+    return 1;
+}
+
+int sepia_gpu_end(void) {
+    if (!need_init("end")) return 0;
+    if (!g_batch_open) {
+        LOG("end: no active batch");
+        return 0;
+    }
+    g_batch_open = 0;
+    hipError_t e = hipSuccess;
+    for (SepiaGpuBuf *b = g_shared; b && e == hipSuccess; b = b->next) {
+        if (!b->dev_newer) continue;
+        e = hipMemcpyAsync(b->host, b->dev, b->len, hipMemcpyDeviceToHost, g_stream);
+        b->dev_newer = 0;
+    }
+    hipError_t s = hipStreamSynchronize(g_stream);
+    if (e == hipSuccess) e = s;
+    for (SepiaGpuBuf *b = g_shared; b; b = b->next)
+        if (b->exposed) b->host_newer = 1;
+    if (e != hipSuccess) {
+        LOG("end: batch failed: %s", hipGetErrorString(e));
+        return 0;
+    }
+    return 1;
+}
+
+static int launch(int k, unsigned grid, unsigned block, void **args, const char *op) {
+    if (grid == 0) return 1;
+    hipError_t e = hipModuleLaunchKernel(g_fn[k], grid, 1, 1, block, 1, 1, 0, g_stream, args, NULL);
+    if (e != hipSuccess) {
+        LOG("%s: launch of %s failed: %s", op, k_names[k], hipGetErrorString(e));
+        return 0;
+    }
+    return 1;
+}
+
+static unsigned blocks_for(int64_t n, int64_t per) { return (unsigned)((n + per - 1) / per); }
+
+#define MAX_GRID ((int64_t)0x7FFFFFFF)
+
+/* ------------------------------------------------------------ f32 ops --- */
+static int f32_off_ok(size_t off, const char *op, const char *what) {
+    if (off % 4) {
+        LOG("%s: %s offset %zu is not 4-byte aligned", op, what, off);
+        return 0;
+    }
+    return 1;
+}
+
+static int do_matvec_f32(const char *op, SepiaGpuBuf *w, size_t w_off, SepiaGpuBuf *x, SepiaGpuBuf *y,
+                         int64_t out_dim, int64_t in_dim) {
+    if (!w || !x || !y || out_dim <= 0 || in_dim <= 0 || (out_dim + 3) / 4 > MAX_GRID) {
+        LOG("%s: invalid arguments", op);
+        return 0;
+    }
+    if (!f32_off_ok(w_off, op, "w") ||
+        !chk(w, w_off, (size_t)out_dim * (size_t)in_dim * 4, op, "w") ||
+        !chk(x, 0, (size_t)in_dim * 4, op, "x") || !chk(y, 0, (size_t)out_dim * 4, op, "y"))
+        return 0;
+    if (!need_batch(op) || !prep_in(w, op) || !prep_in(x, op) || !prep_out(y, op)) return 0;
+    const float *wp = (const float *)(w->dev + w_off);
+    int64_t ld = in_dim;
+    void *args[] = { &wp, &ld, &x->dev, &y->dev, &out_dim, &in_dim };
+    return launch(K_MATVEC_F32, blocks_for(out_dim, 4), 256, args, op);
+}
+
+int sepia_gpu_matvec(SepiaGpuBuf *w, SepiaGpuBuf *x, SepiaGpuBuf *y, int64_t out_dim, int64_t in_dim) {
+    return do_matvec_f32("matvec", w, 0, x, y, out_dim, in_dim);
+}
+
+int sepia_gpu_matvec_off(SepiaGpuBuf *w, size_t w_off, SepiaGpuBuf *x, SepiaGpuBuf *y, int64_t out_dim,
+                         int64_t in_dim) {
+    return do_matvec_f32("matvec_off", w, w_off, x, y, out_dim, in_dim);
+}
+
+static int do_rmsnorm(const char *op, SepiaGpuBuf *w, size_t w_off, SepiaGpuBuf *x, SepiaGpuBuf *y,
+                      int64_t rows, int64_t n, float eps) {
+    if (!w || !x || !y || rows <= 0 || n <= 0 || rows > MAX_GRID) {
+        LOG("%s: invalid arguments", op);
+        return 0;
+    }
+    if (!f32_off_ok(w_off, op, "w") || !chk(w, w_off, (size_t)n * 4, op, "w") ||
+        !chk(x, 0, (size_t)rows * (size_t)n * 4, op, "x") || !chk(y, 0, (size_t)rows * (size_t)n * 4, op, "y"))
+        return 0;
+    if (!need_batch(op) || !prep_in(w, op) || !prep_in(x, op) || !prep_out(y, op)) return 0;
+    const float *wp = (const float *)(w->dev + w_off);
+    void *args[] = { &wp, &x->dev, &y->dev, &n, &eps };
+    return launch(K_RMSNORM, (unsigned)rows, 256, args, op);
+}
+
+int sepia_gpu_rmsnorm(SepiaGpuBuf *w, SepiaGpuBuf *x, SepiaGpuBuf *y, int64_t rows, int64_t n, float eps) {
+    return do_rmsnorm("rmsnorm", w, 0, x, y, rows, n, eps);
+}
+
+int sepia_gpu_rmsnorm_off(SepiaGpuBuf *w, size_t w_off, SepiaGpuBuf *x, SepiaGpuBuf *y, int64_t rows, int64_t n,
+                          float eps) {
+    return do_rmsnorm("rmsnorm_off", w, w_off, x, y, rows, n, eps);
+}
+
+static int elementwise_ok(const char *op, int64_t n) {
+    if (n <= 0 || (n + 255) / 256 > MAX_GRID) {
+        LOG("%s: invalid arguments", op);
+        return 0;
+    }
+    return 1;
+}
+
+int sepia_gpu_silu_mul(SepiaGpuBuf *g, SepiaGpuBuf *u, SepiaGpuBuf *z, int64_t n) {
+    const char *op = "silu_mul";
+    if (!g || !u || !z || !elementwise_ok(op, n)) {
+        if (!g || !u || !z) LOG("%s: invalid arguments", op);
+        return 0;
+    }
+    size_t nb = (size_t)n * 4;
+    if (!chk(g, 0, nb, op, "g") || !chk(u, 0, nb, op, "u") || !chk(z, 0, nb, op, "z")) return 0;
+    if (!need_batch(op) || !prep_in(g, op) || !prep_in(u, op) || !prep_out(z, op)) return 0;
+    void *args[] = { &g->dev, &u->dev, &z->dev, &n };
+    return launch(K_SILU_MUL, blocks_for(n, 256), 256, args, op);
+}
+
+int sepia_gpu_add(SepiaGpuBuf *a, SepiaGpuBuf *b, SepiaGpuBuf *out, int64_t n) {
+    const char *op = "add";
+    if (!a || !b || !out || !elementwise_ok(op, n)) {
+        if (!a || !b || !out) LOG("%s: invalid arguments", op);
+        return 0;
+    }
+    size_t nb = (size_t)n * 4;
+    if (!chk(a, 0, nb, op, "a") || !chk(b, 0, nb, op, "b") || !chk(out, 0, nb, op, "out")) return 0;
+    if (!need_batch(op) || !prep_in(a, op) || !prep_in(b, op) || !prep_out(out, op)) return 0;
+    void *args[] = { &a->dev, &b->dev, &out->dev, &n };
+    return launch(K_ADD, blocks_for(n, 256), 256, args, op);
+}
+
+int sepia_gpu_scale(float scale, SepiaGpuBuf *x, SepiaGpuBuf *y, int64_t n) {
+    const char *op = "scale";
+    if (!x || !y || !elementwise_ok(op, n)) {
+        if (!x || !y) LOG("%s: invalid arguments", op);
+        return 0;
+    }
+    size_t nb = (size_t)n * 4;
+    if (!chk(x, 0, nb, op, "x") || !chk(y, 0, nb, op, "y")) return 0;
+    if (!need_batch(op) || !prep_in(x, op) || !prep_out(y, op)) return 0;
+    void *args[] = { &x->dev, &y->dev, &n, &scale };
+    return launch(K_SCALE, blocks_for(n, 256), 256, args, op);
+}
+
+int sepia_gpu_copy(SepiaGpuBuf *src, size_t src_off, SepiaGpuBuf *dst, size_t dst_off, int64_t n) {
+    const char *op = "copy";
+    if (!src || !dst || !elementwise_ok(op, n)) {
+        if (!src || !dst) LOG("%s: invalid arguments", op);
+        return 0;
+    }
+    size_t nb = (size_t)n * 4;
+    if (!f32_off_ok(src_off, op, "src") || !f32_off_ok(dst_off, op, "dst") ||
+        !chk(src, src_off, nb, op, "src") || !chk(dst, dst_off, nb, op, "dst"))
+        return 0;
+    if (!need_batch(op) || !prep_in(src, op) || !prep_out(dst, op)) return 0;
+    const uint8_t *s = src->dev + src_off;
+    uint8_t *d = dst->dev + dst_off;
+    void *args[] = { &s, &d, &n };
+    return launch(K_COPY, blocks_for(n, 256), 256, args, op);
+}
+
+int sepia_gpu_softmax(SepiaGpuBuf *x, SepiaGpuBuf *y, int64_t rows, int64_t n) {
+    const char *op = "softmax";
+    if (!x || !y || rows <= 0 || n <= 0 || rows > MAX_GRID) {
+        LOG("%s: invalid arguments", op);
+        return 0;
+    }
+    size_t nb = (size_t)rows * (size_t)n * 4;
+    if (!chk(x, 0, nb, op, "x") || !chk(y, 0, nb, op, "y")) return 0;
+    if (!need_batch(op) || !prep_in(x, op) || !prep_out(y, op)) return 0;
+    void *args[] = { &x->dev, &y->dev, &n };
+    return launch(K_SOFTMAX, (unsigned)rows, 256, args, op);
+}
+
+static int do_sconv(const char *op, SepiaGpuBuf *w, size_t w_off, SepiaGpuBuf *hist, SepiaGpuBuf *in,
+                    SepiaGpuBuf *out, int64_t C, int64_t K, int64_t T) {
+    if (!w || !hist || !in || !out || C <= 0 || K <= 0 || T <= 0 || C > 0x7FFFFFFF || K > 0x7FFFFFFF ||
+        T > 0x7FFFFFFF || (C * T + 255) / 256 > MAX_GRID) {
+        LOG("%s: invalid arguments", op);
+        return 0;
+    }
+    size_t cs = (size_t)C * 4;
+    if (!f32_off_ok(w_off, op, "w") || !chk(w, w_off, cs * (size_t)K, op, "w") ||
+        !chk(hist, 0, cs * (size_t)(K - 1), op, "hist") || !chk(in, 0, cs * (size_t)T, op, "in") ||
+        !chk(out, 0, cs * (size_t)T, op, "out"))
+        return 0;
+    if (!need_batch(op) || !prep_in(w, op) || !prep_in(hist, op) || !prep_in(in, op) || !prep_out(out, op))
+        return 0;
+    const float *wp = (const float *)(w->dev + w_off);
+    int32_t c = (int32_t)C, k = (int32_t)K, t = (int32_t)T;
+    void *args[] = { &wp, &hist->dev, &in->dev, &out->dev, &c, &k, &t };
+    return launch(K_SCONV, blocks_for(C * T, 256), 256, args, op);
+}
+
+int sepia_gpu_sconv(SepiaGpuBuf *w, SepiaGpuBuf *hist, SepiaGpuBuf *in, SepiaGpuBuf *out, int64_t C, int64_t K,
+                    int64_t T) {
+    return do_sconv("sconv", w, 0, hist, in, out, C, K, T);
+}
+
+int sepia_gpu_sconv_off(SepiaGpuBuf *w, size_t w_off, SepiaGpuBuf *hist, SepiaGpuBuf *in, SepiaGpuBuf *out,
+                        int64_t C, int64_t K, int64_t T) {
+    return do_sconv("sconv_off", w, w_off, hist, in, out, C, K, T);
+}
+
+int sepia_gpu_sconv_hist_roll(SepiaGpuBuf *hist, SepiaGpuBuf *in, int64_t C, int64_t K, int64_t T) {
+    const char *op = "sconv_hist_roll";
+    if (!hist || !in || C <= 0 || K <= 0 || T <= 0 || C > 0x7FFFFFFF || T > 0x7FFFFFFF) {
+        LOG("%s: invalid arguments", op);
+        return 0;
+    }
+    int64_t km1 = K - 1;
+    if (km1 > 15) {
+        LOG("%s: K-1=%lld exceeds the supported maximum (15)", op, (long long)km1);
+        return 0;
+    }
+    if (km1 == 0) return 1;
+    if (!chk(hist, 0, (size_t)km1 * (size_t)C * 4, op, "hist") || !chk(in, 0, (size_t)T * (size_t)C * 4, op, "in"))
+        return 0;
+    if (!need_batch(op) || !prep_in(in, op) || !prep_out(hist, op)) return 0;
+    int32_t c = (int32_t)C, k = (int32_t)km1, t = (int32_t)T;
+    void *args[] = { &hist->dev, &in->dev, &c, &k, &t };
+    return launch(K_SCONV_HIST, blocks_for(C, 256), 256, args, op);
+}
+
+int sepia_gpu_rel_project(SepiaGpuBuf *r_vec, SepiaGpuBuf *rel_proj, SepiaGpuBuf *rel_logits, int64_t T, int64_t H,
+                          int64_t d_rel, int64_t rel_extent) {
+    (void)r_vec; (void)rel_proj; (void)rel_logits; (void)T; (void)H; (void)d_rel; (void)rel_extent;
+    LOG("rel_project: banded attention is not implemented by this backend");
+    return 0;
+}
+
+int sepia_gpu_rel_project_off(SepiaGpuBuf *r_vec, SepiaGpuBuf *rel_proj, size_t rel_proj_off,
+                              SepiaGpuBuf *rel_logits, int64_t T, int64_t H, int64_t d_rel, int64_t rel_extent) {
+    (void)r_vec; (void)rel_proj; (void)rel_proj_off; (void)rel_logits; (void)T; (void)H; (void)d_rel;
+    (void)rel_extent;
+    LOG("rel_project_off: banded attention is not implemented by this backend");
+    return 0;
+}
+
+int sepia_gpu_banded_attn(SepiaGpuBuf *q, SepiaGpuBuf *k, SepiaGpuBuf *v, SepiaGpuBuf *rel_logits,
+                          SepiaGpuBuf *attn_out, const int64_t *kv_lo, const int64_t *kv_hi, const float *tau,
+                          int64_t T, int64_t H, int64_t Hkv, int64_t Dh, int64_t rel_extent, int64_t q_pos_base,
+                          int64_t kv_dim, float inv_head_dim) {
+    (void)q; (void)k; (void)v; (void)rel_logits; (void)attn_out; (void)kv_lo; (void)kv_hi; (void)tau;
+    (void)T; (void)H; (void)Hkv; (void)Dh; (void)rel_extent; (void)q_pos_base; (void)kv_dim; (void)inv_head_dim;
+    LOG("banded_attn: banded attention is not implemented by this backend");
+    return 0;
+}
+
+int sepia_gpu_selftest_touch(SepiaGpuBuf *buf, size_t n_floats) {
+    const char *op = "selftest_touch";
+    if (!need_init(op)) return 0;
+    if (!buf || n_floats == 0 || n_floats > (size_t)MAX_GRID * 256) {
+        LOG("%s: invalid buf/n_floats", op);
+        return 0;
+    }
+    if (!chk(buf, 0, n_floats * 4, op, "buf") || !sync_in(buf, op)) return 0;
+    int64_t n = (int64_t)n_floats;
+    void *args[] = { &buf->dev, &n };
+    if (!launch(K_TOUCH, blocks_for(n, 256), 256, args, op)) return 0;
+    hipError_t e = hipSuccess;
+    if (buf->kind == BUF_SHARED) e = hipMemcpyAsync(buf->host, buf->dev, buf->len, hipMemcpyDeviceToHost, g_stream);
+    hipError_t s = hipStreamSynchronize(g_stream);
+    if (e == hipSuccess) e = s;
+    if (e != hipSuccess) {
+        LOG("%s: failed: %s", op, hipGetErrorString(e));
+        return 0;
+    }
+    return 1;
+}
+
+/* --------------------------------------------------------- quantized ---- */
+int sepia_gpu_matvec_q(int ggml_type, SepiaGpuBuf *w, size_t w_off, SepiaGpuBuf *x, SepiaGpuBuf *y,
+                       int64_t out_dim, int64_t in_dim) {
+    const char *op = "matvec_q";
+    if (!w || !x || !y || out_dim <= 0 || in_dim <= 0 || (out_dim + 3) / 4 > MAX_GRID) {
+        LOG("%s: invalid arguments", op);
+        return 0;
+    }
+    const TypeInfo *ti = type_info(ggml_type);
+    if (!ti || ti->k_mv < 0) {
+        LOG("%s: no GPU kernel for ggml type %d", op, ggml_type);
+        return 0;
+    }
+    if (in_dim % ti->elems) {
+        LOG("%s: in_dim %lld not a multiple of block size %lld (type %d)", op, (long long)in_dim,
+            (long long)ti->elems, ggml_type);
+        return 0;
+    }
+    int64_t n_blocks = in_dim / ti->elems;
+    uint64_t row_bytes = (uint64_t)n_blocks * ti->bytes;
+    if (!chk(w, w_off, (size_t)out_dim * row_bytes, op, "w") || !chk(x, 0, (size_t)in_dim * 4, op, "x") ||
+        !chk(y, 0, (size_t)out_dim * 4, op, "y"))
+        return 0;
+    if (!need_batch(op) || !prep_in(w, op) || !prep_in(x, op) || !prep_out(y, op)) return 0;
+    const uint8_t *wp = w->dev + w_off;
+    void *args[] = { &wp, &row_bytes, &n_blocks, &x->dev, &y->dev, &out_dim };
+    return launch(ti->k_mv, blocks_for(out_dim, 4), 256, args, op);
+}
+
+int sepia_gpu_dequant_rows(int ggml_type, SepiaGpuBuf *raw, size_t raw_off, SepiaGpuBuf *out, int64_t n) {
+    const char *op = "dequant_rows";
+    if (!raw || !out || n <= 0) {
+        LOG("%s: invalid arguments", op);
+        return 0;
+    }
+    const TypeInfo *ti = type_info(ggml_type);
+    if (!ti) {
+        LOG("%s: no GPU kernel for ggml type %d", op, ggml_type);
+        return 0;
+    }
+    if (n % ti->elems) {
+        LOG("%s: n %lld not a multiple of block size %lld (type %d)", op, (long long)n, (long long)ti->elems,
+            ggml_type);
+        return 0;
+    }
+    int64_t nb = n / ti->elems;
+    int64_t threads = nb * ti->parts;
+    if ((threads + 255) / 256 > MAX_GRID) {
+        LOG("%s: n too large", op);
+        return 0;
+    }
+    if (!chk(raw, raw_off, (size_t)nb * ti->bytes, op, "raw") || !chk(out, 0, (size_t)n * 4, op, "out")) return 0;
+    if (!need_batch(op) || !prep_in(raw, op) || !prep_out(out, op)) return 0;
+    const uint8_t *rp = raw->dev + raw_off;
+    void *args[] = { &rp, &out->dev, &threads };
+    return launch(ti->k_dq, blocks_for(threads, 256), 256, args, op);
+}
+
+int sepia_hip_set_iq2xxs_grid(const uint64_t *grid256) {
+    const char *op = "set_iq2xxs_grid";
+    if (!need_init(op)) return 0;
+    if (!grid256) {
+        LOG("%s: NULL table", op);
+        return 0;
+    }
+    hipDeviceptr_t p;
+    size_t sz = 0;
+    hipError_t e = hipModuleGetGlobal(&p, &sz, g_module, "g_iq2xxs_grid");
+    if (e == hipSuccess && sz != 256 * sizeof(uint64_t)) e = hipErrorInvalidValue;
+    if (e == hipSuccess) e = hipMemcpyHtoDAsync(p, (void *)grid256, sz, g_stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(g_stream);
+    if (e != hipSuccess) {
+        LOG("%s: failed: %s", op, hipGetErrorString(e));
+        return 0;
+    }
+    g_have_iq2xxs = 1;
+    return 1;
+}
+
+/* ------------------------------------------------------------- synth ---- */
+int sepia_hip_synth_blocks(int ggml_type, SepiaGpuBuf *buf, size_t off, int64_t n_blocks, uint64_t seed, float lo,
+                           float hi) {
+    const char *op = "synth_blocks";
+    const TypeInfo *ti = NULL;
+    for (size_t i = 0; i < sizeof k_types / sizeof k_types[0]; i++)
+        if (k_types[i].type == ggml_type) ti = &k_types[i];
+    if (!buf || n_blocks <= 0 || !ti || off % 4) {
+        LOG("%s: invalid arguments", op);
+        return 0;
+    }
+    size_t nbytes = (size_t)n_blocks * ti->bytes;
+    if (!chk(buf, off, nbytes, op, "buf")) return 0;
+    if (!need_batch(op) || !prep_out(buf, op)) return 0;
+    uint8_t *p = buf->dev + off;
+    uint64_t n = nbytes;
+    void *a1[] = { &p, &n, &seed };
+    unsigned grid = blocks_for((int64_t)(nbytes / 4) + 1, 256);
+    if (grid > 16384) grid = 16384;
+    if (!launch(K_SYNTH_FILL, grid, 256, a1, op)) return 0;
+    for (int f = 0; f < 2; f++) {
+        if (ti->f16_off[f] < 0) continue;
+        uint64_t nbk = (uint64_t)n_blocks;
+        uint32_t bb = (uint32_t)ti->bytes, fo = (uint32_t)ti->f16_off[f];
+        uint64_t s = seed * 31u + (uint64_t)f + 1u;
+        void *a2[] = { &p, &nbk, &bb, &fo, &s, &lo, &hi };
+        unsigned g2 = blocks_for(n_blocks, 256);
+        if (g2 > 16384) g2 = 16384;
+        if (!launch(K_SYNTH_F16, g2, 256, a2, op)) return 0;
+    }
+    return 1;
+}
+
+/* --------------------------------------------------------------- MoE ---- */
+/* Mirrors struct MoeProj in kernels/moe.h field for field. */
+typedef struct {
+    const uint8_t *base;
+    uint64_t stride;
+    uint64_t row_bytes;
+    int64_t n_blocks;
+    int32_t type;
+    int32_t pad;
+} MoeProj;
+
+static int moe_proj(const char *op, const char *what, const SepiaExpertTensor *t, int n_experts, int64_t rows,
+                    int64_t cols, MoeProj *out) {
+    const TypeInfo *ti = type_info(t->ggml_type);
+    if (!ti || ti->k_mv < 0) {
+        LOG("%s: %s: no GPU kernel for ggml type %d", op, what, t->ggml_type);
+        return 0;
+    }
+    if (cols % ti->elems) {
+        LOG("%s: %s: row length %lld not a multiple of block size %lld", op, what, (long long)cols,
+            (long long)ti->elems);
+        return 0;
+    }
+    uint64_t rb = (uint64_t)(cols / ti->elems) * ti->bytes;
+    size_t mat = (size_t)rows * rb;
+    if (n_experts > 1 && t->stride < mat) {
+        LOG("%s: %s: expert stride %zu is smaller than one matrix (%zu bytes)", op, what, t->stride, mat);
+        return 0;
+    }
+    size_t span = (size_t)(n_experts - 1) * t->stride + mat;
+    if (!chk(t->buf, t->off, span, op, what)) return 0;
+    out->base = t->buf->dev + t->off;
+    out->stride = t->stride;
+    out->row_bytes = rb;
+    out->n_blocks = cols / ti->elems;
+    out->type = t->ggml_type;
+    out->pad = 0;
+    return 1;
+}
+
+static void *scratch(size_t need, const char *op) {
+    if (need <= g_scratch_len) return g_scratch;
+    hipStreamSynchronize(g_stream);
+    if (g_scratch) hipFree(g_scratch);
+    g_scratch = NULL;
+    g_scratch_len = 0;
+    size_t want = need < (1u << 20) ? (1u << 20) : need;
+    hipError_t e = hipMalloc(&g_scratch, want);
+    if (e != hipSuccess) {
+        LOG("%s: scratch allocation of %zu bytes failed: %s", op, want, hipGetErrorString(e));
+        g_scratch = NULL;
+        return NULL;
+    }
+    g_scratch_len = want;
+    return g_scratch;
+}
+
+int sepia_gpu_moe_decode(const SepiaMoeLayerDesc *L, SepiaGpuBuf *x, SepiaGpuBuf *y, SepiaGpuBuf *route_out) {
+    const char *op = "moe_decode";
+    if (!L || !x || !y || L->hidden <= 0 || L->inter <= 0 || L->n_routed < 1 || L->n_routed > 1024 ||
+        L->n_shared < 0 || L->topk < 1 || L->topk > L->n_routed || L->topk + L->n_shared > 64 || !L->router_w ||
+        !L->router_bias) {
+        LOG("%s: invalid layer description", op);
+        return 0;
+    }
+    if (L->n_shared > 0 && (!L->s_gate.buf || !L->s_up.buf || !L->s_down.buf)) {
+        LOG("%s: shared expert tensors missing", op);
+        return 0;
+    }
+    const int64_t H = L->hidden, I = L->inter;
+    const int n_tot = L->n_routed + L->n_shared, n_slots = L->topk + L->n_shared;
+    MoeProj g, u, d, sg, su, sd;
+    memset(&sg, 0, sizeof sg);
+    memset(&su, 0, sizeof su);
+    memset(&sd, 0, sizeof sd);
+    if (!moe_proj(op, "gate", &L->gate, L->n_routed, I, H, &g) || !moe_proj(op, "up", &L->up, L->n_routed, I, H, &u) ||
+        !moe_proj(op, "down", &L->down, L->n_routed, H, I, &d))
+        return 0;
+    if (L->n_shared > 0 &&
+        (!moe_proj(op, "shared gate", &L->s_gate, L->n_shared, I, H, &sg) ||
+         !moe_proj(op, "shared up", &L->s_up, L->n_shared, I, H, &su) ||
+         !moe_proj(op, "shared down", &L->s_down, L->n_shared, H, I, &sd)))
+        return 0;
+    if (!f32_off_ok(L->router_w_off, op, "router_w") || !f32_off_ok(L->router_bias_off, op, "router_bias") ||
+        !chk(L->router_w, L->router_w_off, (size_t)n_tot * (size_t)H * 4, op, "router_w") ||
+        !chk(L->router_bias, L->router_bias_off, (size_t)L->n_routed * 4, op, "router_bias") ||
+        !chk(x, 0, (size_t)H * 4, op, "x") || !chk(y, 0, (size_t)H * 4, op, "y"))
+        return 0;
+    const size_t route_bytes = (size_t)(2 * L->topk + L->n_shared) * 4;
+    if (route_out && !chk(route_out, 0, route_bytes, op, "route_out")) return 0;
+    if ((int64_t)n_slots * ((I + 3) / 4) > MAX_GRID || (H + 3) / 4 > MAX_GRID) {
+        LOG("%s: layer too large", op);
+        return 0;
+    }
+    if (!need_batch(op)) return 0;
+
+    /* scratch: logits | sel_idx | sel_w | h, each 256-byte aligned */
+    const size_t o_logits = 0;
+    const size_t o_idx = o_logits + (((size_t)n_tot * 4 + 255) & ~(size_t)255);
+    const size_t o_w = o_idx + 256;
+    const size_t o_h = o_w + 256;
+    const size_t need = o_h + (size_t)n_slots * (size_t)I * 4;
+    uint8_t *s = (uint8_t *)scratch(need, op);
+    if (!s) return 0;
+    float *logits = (float *)(s + o_logits), *sel_w = (float *)(s + o_w), *h = (float *)(s + o_h);
+    int32_t *sel_idx = (int32_t *)(s + o_idx);
+
+    SepiaGpuBuf *ins[] = { L->router_w, L->router_bias, x, L->gate.buf, L->up.buf, L->down.buf, L->s_gate.buf,
+                           L->s_up.buf, L->s_down.buf };
+    for (size_t i = 0; i < sizeof ins / sizeof ins[0]; i++)
+        if (ins[i] && !prep_in(ins[i], op)) return 0;
+    if (!prep_out(y, op) || (route_out && !prep_out(route_out, op))) return 0;
+
+    const float *rw = (const float *)(L->router_w->dev + L->router_w_off);
+    const float *rb = (const float *)(L->router_bias->dev + L->router_bias_off);
+    int64_t n_tot64 = n_tot, ld = H, hid = H, inter = I;
+    void *a_router[] = { &rw, &ld, &x->dev, &logits, &n_tot64, &hid };
+    if (!launch(K_MATVEC_F32, blocks_for(n_tot, 4), 256, a_router, op)) return 0;
+
+    int32_t nr = L->n_routed, ns = L->n_shared, tk = L->topk;
+    float rs = L->route_scale, gs = L->global_scale;
+    void *a_sel[] = { &logits, &rb, &nr, &ns, &tk, &rs, &gs, &sel_idx, &sel_w };
+    if (!launch(K_MOE_SELECT, 1, 256, a_sel, op)) return 0;
+
+    void *a_gu[] = { &g, &u, &sg, &su, &sel_idx, &tk, &inter, &x->dev, &h };
+    if (!launch(K_MOE_GATEUP, (unsigned)(n_slots * ((I + 3) / 4)), 256, a_gu, op)) return 0;
+
+    void *a_dn[] = { &d, &sd, &sel_idx, &sel_w, &tk, &ns, &inter, &hid, &h, &y->dev };
+    if (!launch(K_MOE_DOWN, blocks_for(H, 4), 256, a_dn, op)) return 0;
+
+    if (route_out) {
+        hipError_t e = hipMemcpyAsync(route_out->dev, sel_idx, (size_t)L->topk * 4, hipMemcpyDeviceToDevice, g_stream);
+        if (e == hipSuccess)
+            e = hipMemcpyAsync(route_out->dev + (size_t)L->topk * 4, sel_w, (size_t)n_slots * 4,
+                               hipMemcpyDeviceToDevice, g_stream);
+        if (e != hipSuccess) {
+            LOG("%s: route_out copy failed: %s", op, hipGetErrorString(e));
+            return 0;
+        }
+    }
+    return 1;
+}

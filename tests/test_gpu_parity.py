@@ -1,0 +1,395 @@
+"""GPU parity: libsepia_hip.so (through its C ABI) against the CPU oracle.
+
+Bars:
+  * dequantized weights bit-exact against the reference's dequantize_row;
+  * matvec and MoE outputs within max|diff| <= 1e-4 * ||y||_inf of the oracle
+    (which accumulates in float64), and the reference's own GPU gate
+    (relative error with a 1e-3 * scale floor <= 2e-4, src/sepia.c:4557-4589).
+"""
+import glob
+import os
+import struct
+import zlib
+
+import numpy as np
+import pytest
+
+import np_quants
+from conftest import GOLDEN
+from sepia_amd import hip, synth
+
+pytestmark = pytest.mark.gpu
+
+THREADS = min(16, os.cpu_count() or 1)
+TOL = 1e-4
+
+
+@pytest.fixture(scope="module")
+def dev():
+    return hip.Device()
+
+
+def assert_close(got, want, tol=TOL, what=""):
+    """max|got - want| <= tol * ||want||_inf, and the reference's GPU gate."""
+    got = np.asarray(got, dtype=np.float64)
+    want = np.asarray(want, dtype=np.float64)
+    assert np.all(np.isfinite(got)), what
+    scale = float(np.max(np.abs(want))) if want.size else 0.0
+    err = float(np.max(np.abs(got - want))) if want.size else 0.0
+    assert err <= tol * scale, "%s: max|diff| %.3e > %.1e * %.3e" % (what, err, tol, scale)
+    floor = max(1e-6, 1e-3 * scale)
+    rel = np.abs(got - want) / np.maximum(np.abs(want), floor)
+    assert float(rel.max()) <= 2e-4, "%s: reference gate rel %.3e" % (what, float(rel.max()))
+
+
+def gpu_dequant(dev, t, raw, n, raw_off=0):
+    rb = dev.alloc(raw.nbytes + raw_off + 1)
+    dev.upload(rb, raw, offset=raw_off)
+    ob = dev.alloc(n * 4)
+    dev.run(dev.L.sepia_gpu_dequant_rows, t, rb, raw_off, ob, n)
+    out = dev.download(ob, n)
+    dev.free(rb)
+    dev.free(ob)
+    return out
+
+
+def gpu_matvec_q(dev, t, w, out_dim, in_dim, x, w_off=0):
+    wb = dev.alloc(w.nbytes + w_off)
+    dev.upload(wb, w, offset=w_off)
+    xb = dev.shared_from(x)
+    yb = dev.alloc(out_dim * 4)
+    dev.run(dev.L.sepia_gpu_matvec_q, t, wb, w_off, xb, yb, out_dim, in_dim)
+    y = dev.download(yb, out_dim)
+    for b in (wb, xb, yb):
+        dev.free(b)
+    return y
+
+
+def test_device(dev):
+    assert dev.L.sepia_gpu_available() == 1
+    assert dev.name
+    print("device:", dev.name)
+
+
+# --------------------------------------------------------------- dequant
+SQFX = sorted(p for p in glob.glob(os.path.join(GOLDEN, "quants", "*.bin"))
+              if not os.path.basename(p).startswith("qlinear"))
+
+
+@pytest.mark.parametrize("path", SQFX, ids=lambda p: os.path.basename(p))
+def test_dequant_golden_bitwise(dev, path):
+    """The reference's --gpu-quants gate (src/sepia.c:5944-6004) on its own fixtures."""
+    with open(path, "rb") as f:
+        magic, ver, t, nb, be, bb = struct.unpack("<6I", f.read(24))
+        raw = np.frombuffer(f.read(nb * bb), dtype=np.uint8)
+        expect = np.frombuffer(f.read(nb * be * 4), dtype="<f4")
+    got = gpu_dequant(dev, t, raw, nb * be)
+    assert np.array_equal(got.view(np.uint32), expect.view(np.uint32))
+
+
+ALL_Q = [8, 10, 11, 12, 13, 14, 17, 18, 23]
+
+
+@pytest.fixture(scope="module")
+def stand_in_iq2xxs(dev, orc):
+    """IQ2_XXS's codebook is unavailable offline: a seeded stand-in table (magnitudes
+    from the format's 3 levels) exercises the decode structure on both sides."""
+    rng = np.random.default_rng(2024)
+    levels = np.array([0x08, 0x19, 0x2B], dtype=np.uint64)
+    grid = np.zeros(256, dtype=np.uint64)
+    for k in range(8):
+        grid |= levels[rng.integers(0, 3, 256)] << np.uint64(8 * k)
+    g = np.ascontiguousarray(grid)
+    assert dev.L.sepia_hip_set_iq2xxs_grid(g.ctypes.data) == 1
+    orc.set_iq2xxs_grid(grid)
+    yield grid
+    orc.set_iq2xxs_grid(None)
+
+
+@pytest.mark.parametrize("t", ALL_Q + [16])
+@pytest.mark.parametrize("raw_off", [0, 2, 3])
+def test_dequant_random_bitwise(dev, orc, stand_in_iq2xxs, t, raw_off):
+    rng = np.random.default_rng(100 * t + raw_off)
+    be, bb = orc.GEOM[t]
+    nb = 1024 if be == 256 else 4096
+    raw = synth.random_blocks(t, nb, rng)
+    got = gpu_dequant(dev, t, raw, nb * be, raw_off)
+    want = orc.dequantize(t, raw, nb * be)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    if t == 16:
+        assert np.array_equal(want.view(np.uint32), np_quants.iq2_xxs(raw, stand_in_iq2xxs).view(np.uint32))
+
+
+@pytest.mark.parametrize("t", ALL_Q)
+def test_dequant_raw_bytes(dev, orc, t):
+    """Fully random blocks: subnormal/inf/NaN scale fields. Finite results are
+    bit-exact; NaN positions agree."""
+    rng = np.random.default_rng(7 * t)
+    be, bb = orc.GEOM[t]
+    nb = 512
+    raw = rng.integers(0, 256, nb * bb, dtype=np.uint8)
+    got = gpu_dequant(dev, t, raw, nb * be)
+    want = orc.dequantize(t, raw, nb * be)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
+def test_dequant_f16_all_patterns(dev, orc):
+    bits = np.arange(65536, dtype=np.uint16).view(np.uint8)
+    got = gpu_dequant(dev, 1, bits, 65536)
+    want = orc.dequantize(1, bits, 65536)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+# ---------------------------------------------------------------- matvec
+def check_matvec(dev, orc, t, out_dim, in_dim, seed, w_off=0):
+    rng = np.random.default_rng(seed)
+    w = synth.random_matrix(t, out_dim, in_dim, rng)
+    x = synth.normal_vector(rng, in_dim)
+    y = gpu_matvec_q(dev, t, w, out_dim, in_dim, x, w_off)
+    want = orc.qlinear(t, w, out_dim, in_dim, x, threads=THREADS)
+    assert_close(y, want, what="type %d %dx%d off %d" % (t, out_dim, in_dim, w_off))
+
+
+@pytest.mark.parametrize("t", ALL_Q + [16])
+@pytest.mark.parametrize("shape", [(1, 256), (5, 512), (64, 2048), (257, 3072)], ids=str)
+def test_matvec_q_small(dev, orc, stand_in_iq2xxs, t, shape):
+    out_dim, in_dim = shape
+    check_matvec(dev, orc, t, out_dim, in_dim, seed=t * 1000 + out_dim)
+
+
+@pytest.mark.parametrize("t", [11, 12, 17])
+@pytest.mark.parametrize("w_off", [2, 6, 130])
+def test_matvec_q_weight_offset(dev, orc, t, w_off):
+    check_matvec(dev, orc, t, 33, 1024, seed=99 + w_off, w_off=w_off)
+
+
+def test_matvec_q_reference_fixture_gate(dev, orc):
+    """The reference's gate reshapes each SQFX fixture into a 4-row matrix with
+    x from rand_r; here x is seeded uniform [-1, 1) (src/sepia.c:6006-6043)."""
+    for path in SQFX:
+        with open(path, "rb") as f:
+            magic, ver, t, nb, be, bb = struct.unpack("<6I", f.read(24))
+            raw = np.frombuffer(f.read(nb * bb), dtype=np.uint8)
+        if t == 1:
+            continue
+        out_dim = 4
+        in_dim = nb // out_dim * be
+        x = np.random.default_rng(20260720 ^ t).uniform(-1, 1, in_dim).astype(np.float32)
+        y = gpu_matvec_q(dev, t, raw, out_dim, in_dim, x)
+        assert_close(y, orc.qlinear(t, raw, out_dim, in_dim, x), what=os.path.basename(path))
+
+
+CONFIG_SHAPES = [
+    ("C1 q4_k 4096x4096", 12, 4096, 4096),
+    ("C2 gate q2_k 3072x6144", 10, 3072, 6144),
+    ("C2 down q3_k 6144x3072", 11, 6144, 3072),
+    ("C3 shared q4_k 3072x6144", 12, 3072, 6144),
+    ("C4 iq3_xxs 6144x6144", 18, 6144, 6144),
+    ("C4 sub iq2_xs 6144x6144", 17, 6144, 6144),
+    ("real gate iq2_xs 3072x6144", 17, 3072, 6144),
+    ("real down iq4_xs 6144x3072", 23, 6144, 3072),
+    ("real shared q5_k 3072x6144", 13, 3072, 6144),
+    ("real shared q6_k 6144x3072", 14, 6144, 3072),
+]
+
+
+@pytest.mark.parametrize("name,t,out_dim,in_dim", CONFIG_SHAPES, ids=[c[0] for c in CONFIG_SHAPES])
+def test_matvec_q_config_shapes(dev, orc, name, t, out_dim, in_dim):
+    check_matvec(dev, orc, t, out_dim, in_dim, seed=zlib.crc32(name.encode()) & 0xFFFF)
+
+
+def test_matvec_q_rejections(dev):
+    L = dev.L
+    w = dev.alloc(144 * 4)
+    x = dev.alloc(256 * 4)
+    y = dev.alloc(16)
+    assert L.sepia_gpu_matvec_q(12, w, 0, x, y, 4, 256) == 0          # no batch
+    dev.begin()
+    try:
+        assert L.sepia_gpu_matvec_q(2, w, 0, x, y, 4, 256) == 0       # Q4_0: unsupported
+        assert L.sepia_gpu_matvec_q(12, w, 0, x, y, 4, 255) == 0      # ragged in_dim
+        assert L.sepia_gpu_matvec_q(12, w, 2, x, y, 4, 256) == 0      # past the end of w
+        assert L.sepia_gpu_matvec_q(12, w, 0, x, y, 5, 256) == 0      # y too small / w too small
+        assert L.sepia_gpu_matvec_q(12, w, 0, x, y, 0, 256) == 0
+        assert L.sepia_gpu_dequant_rows(12, w, 0, x, 300) == 0
+        assert L.sepia_gpu_matvec_q(12, w, 0, x, y, 4, 256) == 1
+    finally:
+        assert L.sepia_gpu_end() == 1
+    assert L.sepia_gpu_begin() == 1
+    assert L.sepia_gpu_begin() == 0                                    # already open
+    assert L.sepia_gpu_flush() == 1
+    assert L.sepia_gpu_end() == 1
+    assert L.sepia_gpu_end() == 0
+    for b in (w, x, y):
+        dev.free(b)
+
+
+# ---------------------------------------------------------------- f32 ops
+def test_f32_ops(dev, orc):
+    L = dev.L
+    rng = np.random.default_rng(5)
+    n, rows, out_dim = 1000, 3, 77
+    a = rng.standard_normal(rows * n).astype(np.float32)
+    b = rng.standard_normal(rows * n).astype(np.float32)
+    wv = rng.standard_normal(n).astype(np.float32)
+    W = rng.standard_normal((out_dim, n)).astype(np.float32)
+    ba, bbuf, bw, bW = dev.shared_from(a), dev.shared_from(b), dev.shared_from(wv), dev.shared_from(W, extra=64)
+    out = dev.alloc(rows * n * 4)
+
+    dev.run(L.sepia_gpu_silu_mul, ba, bbuf, out, rows * n)
+    z = dev.download(out, rows * n)
+    assert np.allclose(z, orc.silu_mul(a, b), rtol=2e-6, atol=1e-7)
+
+    dev.run(L.sepia_gpu_add, ba, bbuf, out, rows * n)
+    assert np.array_equal(dev.download(out, rows * n), a + b)
+
+    dev.run(L.sepia_gpu_scale, float(np.float32(0.37)), ba, out, rows * n)
+    assert np.array_equal(dev.download(out, rows * n), a * np.float32(0.37))
+
+    dev.run(L.sepia_gpu_copy, ba, 8, out, 4, n)
+    assert np.array_equal(dev.download(out, n, offset=4), a[2:2 + n])
+
+    dev.run(L.sepia_gpu_matvec, bW, ba, out, out_dim, n)
+    assert_close(dev.download(out, out_dim), orc.linear_f32(W, a[:n]), what="matvec f32")
+    # matvec_off at a 4-byte (not 16-byte) offset: the scalar-load path
+    flat = rng.standard_normal(out_dim * n + 1).astype(np.float32)
+    bflat = dev.shared_from(flat)
+    dev.run(L.sepia_gpu_matvec_off, bflat, 4, ba, out, out_dim, n)
+    assert_close(dev.download(out, out_dim), orc.linear_f32(flat[1:].reshape(out_dim, n), a[:n]),
+                 what="matvec_off")
+    dev.free(bflat)
+
+    dev.run(L.sepia_gpu_rmsnorm, bw, ba, out, rows, n, 1e-6)
+    x2 = a.reshape(rows, n).astype(np.float64)
+    ref = wv * (x2 / np.sqrt((x2 ** 2).mean(axis=1, keepdims=True) + 1e-6))
+    assert np.allclose(dev.download(out, rows * n).reshape(rows, n), ref, rtol=1e-5, atol=1e-6)
+
+    dev.run(L.sepia_gpu_softmax, ba, out, rows, n)
+    e = np.exp(x2 - x2.max(axis=1, keepdims=True))
+    assert np.allclose(dev.download(out, rows * n).reshape(rows, n), e / e.sum(axis=1, keepdims=True),
+                       rtol=1e-5, atol=1e-9)
+    for buf in (ba, bbuf, bw, bW, out):
+        dev.free(buf)
+
+
+def test_sconv_and_hist_roll(dev):
+    L = dev.L
+    rng = np.random.default_rng(9)
+    C, K = 40, 4
+    for T in (1, 2, 3, 7):
+        w = rng.standard_normal((C, K)).astype(np.float32)
+        hist = rng.standard_normal((K - 1, C)).astype(np.float32)
+        inp = rng.standard_normal((T, C)).astype(np.float32)
+        bw, bh, bi, bo = dev.shared_from(w), dev.shared_from(hist), dev.shared_from(inp), dev.alloc(T * C * 4)
+        dev.run(L.sepia_gpu_sconv, bw, bh, bi, bo, C, K, T)
+        win = np.concatenate([hist, inp]).astype(np.float64)
+        ref = inp + np.stack([(w * win[t:t + K].T).sum(axis=1) for t in range(T)])
+        assert np.allclose(dev.download(bo, T * C).reshape(T, C), ref, rtol=1e-5, atol=1e-5)
+        dev.run(L.sepia_gpu_sconv_hist_roll, bh, bi, C, K, T)
+        assert np.array_equal(dev.download(bh, (K - 1) * C).reshape(K - 1, C),
+                              np.concatenate([hist, inp])[-(K - 1):])
+        for b in (bw, bh, bi, bo):
+            dev.free(b)
+
+
+def test_selftest_touch_and_wrap(dev):
+    import mmap
+    L = dev.L
+    m = mmap.mmap(-1, 8192)
+    arr = np.frombuffer(m, dtype=np.float32)
+    arr[:] = np.arange(2048, dtype=np.float32)
+    import ctypes
+    addr = ctypes.addressof(ctypes.c_char.from_buffer(m))
+    wb = L.sepia_gpu_wrap_mmap(addr, 8192)
+    assert wb
+    assert L.sepia_gpu_host_ptr(wb) == addr
+    assert L.sepia_gpu_wrap_mmap(addr + 4, 100) is None          # not page-aligned
+    out = dev.alloc(8192)
+    dev.run(L.sepia_gpu_copy, wb, 0, out, 0, 2048)
+    assert np.array_equal(dev.download(out, 2048), np.arange(2048, dtype=np.float32))
+    assert L.sepia_gpu_selftest_touch(out, 2048) == 1
+    assert np.array_equal(dev.download(out, 2048), np.arange(2048, dtype=np.float32))
+    dev.free(out)
+    dev.free(wb)
+    del arr
+    m.close()
+
+
+# ------------------------------------------------------------------- MoE
+def make_layer(dev, rng, hidden, inter, n_routed, n_shared, tg, tu, td, ts):
+    """Shared buffers with seeded host data; returns (desc, spec, keep)."""
+    gate = [synth.random_matrix(tg, inter, hidden, rng) for _ in range(n_routed)]
+    up = [synth.random_matrix(tu, inter, hidden, rng) for _ in range(n_routed)]
+    down = [synth.random_matrix(td, hidden, inter, rng) for _ in range(n_routed)]
+    sg = [synth.random_matrix(ts, inter, hidden, rng) for _ in range(n_shared)]
+    su = [synth.random_matrix(ts, inter, hidden, rng) for _ in range(n_shared)]
+    sd = [synth.random_matrix(ts, hidden, inter, rng) for _ in range(n_shared)]
+    rw = (rng.standard_normal((n_routed + n_shared, hidden)) * 0.02).astype(np.float32)
+    rb = rng.uniform(-0.1, 0.1, n_routed).astype(np.float32)
+    bufs = {k: dev.shared_from(np.concatenate(v)) for k, v in
+            dict(gate=gate, up=up, down=down, s_gate=sg, s_up=su, s_down=sd).items()}
+    bufs["rw"] = dev.shared_from(rw)
+    bufs["rb"] = dev.shared_from(rb)
+    d = hip.MoeLayerDesc()
+    d.hidden, d.inter, d.n_routed, d.n_shared, d.topk = hidden, inter, n_routed, n_shared, 6
+    d.route_scale, d.global_scale = 8.0, 1.0
+    d.router_w, d.router_bias = bufs["rw"], bufs["rb"]
+    for name, t, lst in (("gate", tg, gate), ("up", tu, up), ("down", td, down),
+                         ("s_gate", ts, sg), ("s_up", ts, su), ("s_down", ts, sd)):
+        setattr(d, name, hip.ExpertTensor(bufs[name], 0, lst[0].nbytes, t))
+    spec = dict(hidden=hidden, inter=inter, n_routed=n_routed, n_shared=n_shared, topk=6, route_scale=8.0,
+                global_scale=1.0, router_w=rw, router_bias=rb, t_gate=tg, t_up=tu, t_down=td,
+                ts_gate=ts, ts_up=ts, ts_down=ts, gate=gate, up=up, down=down, s_gate=sg, s_up=su, s_down=sd)
+    return d, spec, bufs
+
+
+def run_moe(dev, desc, x):
+    import ctypes
+    xb = dev.shared_from(x)
+    yb = dev.alloc(x.nbytes)
+    rb = dev.alloc(64 * 4)
+    dev.run(dev.L.sepia_gpu_moe_decode, ctypes.byref(desc), xb, yb, rb)
+    y = dev.download(yb, x.size)
+    idx = dev.download(rb, desc.topk, dtype=np.int32)
+    w = dev.download(rb, desc.topk + desc.n_shared, offset=desc.topk * 4)
+    for b in (xb, yb, rb):
+        dev.free(b)
+    return y, idx, w
+
+
+def check_route(orc, spec, logits, idx_gpu, w_gpu):
+    """Selection must match the oracle's, or differ only across a near-tie of the
+    selection scores (the reference's near-tie protocol); weights then follow
+    the GPU's selection."""
+    idx_ref, w_ref = orc.route_select(logits, spec["router_bias"], spec["n_routed"], spec["n_shared"],
+                                      spec["topk"], spec["route_scale"], spec["global_scale"])
+    if list(idx_gpu) != list(idx_ref):
+        score = 1.0 / (1.0 + np.exp(-logits[:spec["n_routed"]].astype(np.float64))) + spec["router_bias"]
+        s_sorted = np.sort(score)[::-1]
+        gap = s_sorted[spec["topk"] - 1] - s_sorted[spec["topk"]]
+        assert gap < 1e-5 and set(idx_gpu) ^ set(idx_ref), (idx_gpu, idx_ref, gap)
+        w_ref = orc.route_weights(logits, spec["n_routed"], spec["n_shared"], idx_gpu, spec["route_scale"],
+                                  spec["global_scale"])
+    assert np.allclose(w_gpu, w_ref, rtol=1e-5, atol=0)
+    return list(idx_gpu)
+
+
+@pytest.mark.parametrize("types", [(10, 10, 11, 12), (17, 17, 18, 13), (17, 17, 23, 14)],
+                         ids=["q2k_q3k_q4k", "iq2xs_iq3xxs_q5k", "iq2xs_iq4xs_q6k"])
+@pytest.mark.parametrize("seed", [0, 1])
+def test_moe_decode_small(dev, orc, types, seed):
+    rng = np.random.default_rng(seed)
+    tg, tu, td, ts = types
+    desc, spec, bufs = make_layer(dev, rng, hidden=1024, inter=512, n_routed=32, n_shared=2,
+                                  tg=tg, tu=tu, td=td, ts=ts)
+    x = synth.normal_vector(rng, 1024)
+    y, idx, w = run_moe(dev, desc, x)
+    y_ref, logits, idx_ref, w_ref = orc.moe_layer(spec, x, threads=THREADS)
+    chosen = check_route(orc, spec, logits, idx, w)
+    if chosen != list(idx_ref):
+        y_ref, _, _, _ = orc.moe_layer(spec, x, force_idx=chosen, threads=THREADS)
+    assert_close(y, y_ref, what="moe small")
+    for b in bufs.values():
+        dev.free(b)
