@@ -1,0 +1,466 @@
+#!/usr/bin/env python3
+"""Benchmark of SEPIA's quantized-weight decode path on one MI355X.
+
+Headline workload ("C2"): one routed expert FFN at
+decode batch 1, hidden 6144, intermediate 3072, gate/up Q2_K [3072x6144] and
+down Q3_K [6144x3072], y = down(silu(gate x) * up x), through the library's C
+ABI (sepia_gpu_expert_ffn). A step is one expert FFN on one token. 40 experts
+(820 MB) are resident in HBM and the steps rotate over them, so each step's
+20.5 MB of weights come from HBM rather than the 256 MB Infinity Cache.
+
+value  = algorithmic bytes per step (packed weights + f32 x, h, y) / time per
+         step, with the K timed steps replayed from one HIP graph (inputs
+         resident in HBM, host issue overhead out of the timed region).
+roofline.achieved = algorithmic bytes of the dominant kernel per launch /
+         its average launch duration, from HIP events recorded around each
+         launch on the library's stream (sepia_hip_profile_*).
+cpu_baseline = the C oracle's scalar expert FFN (the reference's qlinear loop:
+         per-row dequant + double accumulate) on one host core, on the same
+         expert's bytes, over a bounded sample.
+extra  = the other BASELINE configurations (C1 Q4_K matvec, C3 full MoE
+         decode layer, C4 IQ matvecs) measured the same way.
+"""
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "quantized-weight GB/s (% of HBM peak); MoE layer µs/token at decode batch 1"
+SCALE_LO, SCALE_HI = 2.0 ** -10, 2.0 ** -6
+Q2_K, Q3_K, Q4_K, IQ2_XXS, IQ2_XS, IQ3_XXS = 10, 11, 12, 16, 17, 18
+GEOM = {10: (256, 84), 11: (256, 110), 12: (256, 144), 16: (256, 66), 17: (256, 74), 18: (256, 98)}
+
+
+def log(*a):
+    print("bench:", *a, file=sys.stderr, flush=True)
+
+
+def mat_bytes(t, rows, cols):
+    be, bb = GEOM[t]
+    return rows * (cols // be) * bb
+
+
+class HipRT:
+    """The few HIP runtime calls the benchmark needs (events, stream capture)."""
+
+    def __init__(self):
+        self.L = ctypes.CDLL("libamdhip64.so")
+
+    def ok(self, e, what):
+        if e != 0:
+            raise RuntimeError("%s failed with hipError %d" % (what, e))
+
+    def event(self):
+        ev = ctypes.c_void_p()
+        self.ok(self.L.hipEventCreate(ctypes.byref(ev)), "hipEventCreate")
+        return ev
+
+    def record(self, ev, stream):
+        self.ok(self.L.hipEventRecord(ev, ctypes.c_void_p(stream)), "hipEventRecord")
+
+    def elapsed_ms(self, a, b):
+        self.ok(self.L.hipEventSynchronize(b), "hipEventSynchronize")
+        ms = ctypes.c_float()
+        self.ok(self.L.hipEventElapsedTime(ctypes.byref(ms), a, b), "hipEventElapsedTime")
+        return ms.value
+
+    def sync(self, stream):
+        self.ok(self.L.hipStreamSynchronize(ctypes.c_void_p(stream)), "hipStreamSynchronize")
+
+    def capture(self, stream, issue):
+        """Capture everything issue() launches on `stream` into an executable graph."""
+        self.ok(self.L.hipStreamBeginCapture(ctypes.c_void_p(stream), 1), "hipStreamBeginCapture")
+        try:
+            issue()
+        finally:
+            graph = ctypes.c_void_p()
+            e = self.L.hipStreamEndCapture(ctypes.c_void_p(stream), ctypes.byref(graph))
+        self.ok(e, "hipStreamEndCapture")
+        exe = ctypes.c_void_p()
+        self.ok(self.L.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, ctypes.c_size_t(0)),
+                "hipGraphInstantiate")
+        self.L.hipGraphDestroy(graph)
+        return exe
+
+    def launch_graph(self, exe, stream):
+        self.ok(self.L.hipGraphLaunch(exe, ctypes.c_void_p(stream)), "hipGraphLaunch")
+
+    def destroy_graph(self, exe):
+        self.L.hipGraphExecDestroy(exe)
+
+
+class Bench:
+    def __init__(self, dev):
+        from sepia_amd import hip
+        self.hip = hip
+        self.dev = dev
+        self.L = dev.L
+        self.rt = HipRT()
+        self.stream = dev.stream()
+
+    def private(self, nbytes):
+        return self.dev.alloc(nbytes, private=True)
+
+    def synth(self, t, buf, n_blocks, seed):
+        self.dev.run(self.L.sepia_hip_synth_blocks, t, buf, 0, n_blocks, seed, SCALE_LO, SCALE_HI)
+
+    def vectors(self, n, count, seed, scale=1.0):
+        """count private f32 [n] buffers holding N(0, scale^2) vectors (host copies returned)."""
+        rng = np.random.default_rng(seed)
+        host, bufs = [], []
+        for _ in range(count):
+            v = (rng.standard_normal(n) * scale).astype(np.float32)
+            sb = self.dev.shared_from(v)
+            pb = self.private(n * 4)
+            self.dev.run(self.L.sepia_gpu_copy, sb, 0, pb, 0, n)
+            self.dev.free(sb)
+            host.append(v)
+            bufs.append(pb)
+        return host, bufs
+
+    def fetch(self, buf, off, nbytes):
+        """Bytes [off, off + nbytes) of a private buffer (nbytes and off multiples of 4)."""
+        sb = self.dev.alloc(nbytes)
+        self.dev.run(self.L.sepia_gpu_copy, buf, off, sb, 0, nbytes // 4)
+        out = self.dev.download(sb, nbytes, dtype=np.uint8)
+        self.dev.free(sb)
+        return out
+
+    def timed_steps(self, step, warmup, steps):
+        """W untimed warmup steps, then exactly `steps` steps replayed from one captured
+        HIP graph between two events; returns ms per step."""
+        dev = self.dev
+        dev.begin()
+        for i in range(warmup):
+            dev.check(step(i), "warmup step")
+        dev.end()
+        dev.begin()
+        g = self.rt.capture(self.stream, lambda: [dev.check(step(warmup + i), "captured step") for i in range(steps)])
+        dev.end()
+        self.rt.launch_graph(g, self.stream)         # first replay: graph upload, untimed
+        self.rt.sync(self.stream)
+        e0, e1 = self.rt.event(), self.rt.event()
+        self.rt.record(e0, self.stream)
+        self.rt.launch_graph(g, self.stream)
+        self.rt.record(e1, self.stream)
+        ms = self.rt.elapsed_ms(e0, e1)
+        self.rt.destroy_graph(g)
+        return ms / steps
+
+    def kernel_ms(self, step, n, kernels):
+        """Average per-launch duration of each named kernel over n eager steps."""
+        dev = self.dev
+        self.L.sepia_hip_profile_reset()
+        dev.begin()
+        dev.check(self.L.sepia_hip_profile_start(), "profile_start")
+        for i in range(n):
+            dev.check(step(i), "profiled step")
+        dev.check(self.L.sepia_hip_profile_stop(), "profile_stop")
+        dev.end()
+        out = {}
+        for k in kernels:
+            cnt, tot = ctypes.c_int64(), ctypes.c_double()
+            dev.check(self.L.sepia_hip_profile_query(k.encode(), ctypes.byref(cnt), ctypes.byref(tot)), "query")
+            out[k] = tot.value / max(cnt.value, 1)
+        return out
+
+
+def cpu_sample(fn, min_seconds, max_calls):
+    """Run fn until min_seconds have passed (at least once, at most max_calls); mean s/call."""
+    n, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= min_seconds or n >= max_calls:
+            return el / n, n
+
+
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+# ------------------------------------------------------------------ configs
+def run_c2(B, warmup, steps, cpu_seconds):
+    """one routed expert FFN, Q2_K gate/up, Q3_K down."""
+    hip, L = B.hip, B.L
+    H, I, NE = 6144, 3072, 40
+    gb, ub, db = mat_bytes(Q2_K, I, H), mat_bytes(Q2_K, I, H), mat_bytes(Q3_K, H, I)
+    bufs = [B.private(NE * gb), B.private(NE * ub), B.private(NE * db)]
+    B.synth(Q2_K, bufs[0], NE * I * H // 256, 11)
+    B.synth(Q2_K, bufs[1], NE * I * H // 256, 12)
+    B.synth(Q3_K, bufs[2], NE * H * I // 256, 13)
+    xs_host, xs = B.vectors(H, 1, 21)
+    y = B.private(H * 4)
+    tg, tu, td = hip.ExpertTensor(bufs[0], 0, gb, Q2_K), hip.ExpertTensor(bufs[1], 0, ub, Q2_K), \
+        hip.ExpertTensor(bufs[2], 0, db, Q3_K)
+    ref = (ctypes.byref(tg), ctypes.byref(tu), ctypes.byref(td))
+
+    def step(i):
+        return L.sepia_gpu_expert_ffn(*ref, NE, i % NE, H, I, xs[0], y)
+
+    ms = B.timed_steps(step, warmup, steps)
+    step_bytes = gb + ub + db + H * 4 + I * 4 + H * 4
+    kms = B.kernel_ms(step, min(steps, 4 * NE), ["sepia_moe_gateup", "sepia_moe_down"])
+    gu_bytes = gb + ub + H * 4 + I * 4
+    dn_bytes = db + I * 4 + H * 4
+
+    # graph replay == eager result (the last captured step used expert (warmup+steps-1) % NE)
+    e_last = (warmup + steps - 1) % NE
+    yb = B.dev.alloc(H * 4)
+    B.dev.begin()
+    B.dev.check(L.sepia_gpu_copy(y, 0, yb, 0, H), "copy")
+    B.dev.end()
+    y_graph = B.dev.download(yb, H)
+    B.dev.run(L.sepia_gpu_expert_ffn, *ref, NE, e_last, H, I, xs[0], y)
+    B.dev.begin()
+    B.dev.check(L.sepia_gpu_copy(y, 0, yb, 0, H), "copy")
+    B.dev.end()
+    y_eager = B.dev.download(yb, H)
+    B.dev.free(yb)
+    if not np.array_equal(y_graph.view(np.uint32), y_eager.view(np.uint32)):
+        raise RuntimeError("graph replay differs from the eager result")
+
+    # CPU baseline on the same expert's bytes; parity check of the GPU result
+    import oracle
+    wg = B.fetch(bufs[0], e_last * gb, gb)
+    wu = B.fetch(bufs[1], e_last * ub, ub)
+    wd = B.fetch(bufs[2], e_last * db, db)
+    want = oracle.expert_ffn(Q2_K, wg, Q2_K, wu, Q3_K, wd, H, I, xs_host[0], threads=min(16, os.cpu_count() or 1))
+    err = float(np.max(np.abs(y_eager - want)))
+    scale = float(np.max(np.abs(want)))
+    if err > 1e-4 * scale:
+        raise RuntimeError("C2 parity: max|diff| %g > 1e-4 * %g" % (err, scale))
+    s1, n1 = cpu_sample(lambda: oracle.expert_ffn(Q2_K, wg, Q2_K, wu, Q3_K, wd, H, I, xs_host[0], threads=1),
+                        cpu_seconds, 1000)
+    nthr = min(16, os.cpu_count() or 1)
+    sN, nN = cpu_sample(lambda: oracle.expert_ffn(Q2_K, wg, Q2_K, wu, Q3_K, wd, H, I, xs_host[0], threads=nthr),
+                        cpu_seconds / 4, 1000)
+    for b in bufs + xs + [y]:
+        B.dev.free(b)
+    dom = "sepia_moe_gateup"
+    return dict(
+        ms=ms, step_bytes=step_bytes, value=step_bytes / (ms * 1e-3) / 1e9,
+        parity=dict(max_abs_diff=err, y_inf=scale, bound="1e-4*||y||_inf"),
+        roofline=dict(bound="hbm", kernel=dom, achieved=gu_bytes / (kms[dom] * 1e-3) / 1e9, peak=HBM_PEAK_GBS,
+                      unit="GB/s", bytes_per_launch=gu_bytes, avg_launch_us=kms[dom] * 1e3,
+                      other_kernels={"sepia_moe_down": dict(bytes_per_launch=dn_bytes, avg_launch_us=kms["sepia_moe_down"] * 1e3,
+                                                            achieved=dn_bytes / (kms["sepia_moe_down"] * 1e-3) / 1e9)}),
+        cpu=dict(s1=s1, n1=n1, sN=sN, nN=nN, threads=nthr))
+
+
+def run_matvec_rotation(B, name, t, rows, cols, warmup, steps, cpu_seconds, seed):
+    """One quantized matvec per step, rotating over >= 512 MB of weight copies."""
+    L = B.L
+    mb = mat_bytes(t, rows, cols)
+    ncopy = max(2, -(-512 * 2 ** 20 // mb))
+    w = B.private(ncopy * mb)
+    B.synth(t, w, ncopy * rows * cols // 256, seed)
+    xh, xs = B.vectors(cols, 1, seed + 1)
+    y = B.private(rows * 4)
+
+    def step(i):
+        return L.sepia_gpu_matvec_q(t, w, (i % ncopy) * mb, xs[0], y, rows, cols)
+
+    ms = B.timed_steps(step, warmup, steps)
+    kname = {12: "sepia_matvec_generic_q4_k", 17: "sepia_matvec_generic_iq2_xs", 18: "sepia_matvec_generic_iq3_xxs",
+             16: "sepia_matvec_generic_iq2_xxs"}[t]
+    kms = B.kernel_ms(step, min(steps, 2 * ncopy), [kname])[kname]
+    nbytes = mb + cols * 4 + rows * 4
+    import oracle
+    wh = B.fetch(w, 0, mb)
+    s1, n1 = cpu_sample(lambda: oracle.qlinear(t, wh, rows, cols, xh[0], threads=1), cpu_seconds, 1000)
+    B.dev.free(w)
+    B.dev.free(xs[0])
+    B.dev.free(y)
+    return dict(name=name, ms_per_step=ms, bytes_per_step=nbytes, gbs=nbytes / (ms * 1e-3) / 1e9,
+                hbm_frac=nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, copies_rotated=ncopy,
+                kernel=kname, kernel_avg_us=kms * 1e3, kernel_gbs=nbytes / (kms * 1e-3) / 1e9,
+                cpu_1core_ms=s1 * 1e3, cpu_1core_gbs=mb / s1 / 1e9)
+
+
+def run_c3(B, warmup, steps, cpu_seconds, n_layers=3):
+    """full MoE decode layer, 256 routed (Q2_K/Q3_K) + 2 shared (Q4_K)
+    experts resident, f32 router [258, 6144], top-6, no host round trip."""
+    hip, L = B.hip, B.L
+    H, I, NR, NS = 6144, 3072, 256, 2
+    gb, db = mat_bytes(Q2_K, I, H), mat_bytes(Q3_K, H, I)
+    sgb, sdb = mat_bytes(Q4_K, I, H), mat_bytes(Q4_K, H, I)
+    rng = np.random.default_rng(31)
+    layers, host_router = [], []
+    for li in range(n_layers):
+        lb = dict(gate=B.private(NR * gb), up=B.private(NR * gb), down=B.private(NR * db),
+                  s_gate=B.private(NS * sgb), s_up=B.private(NS * sgb), s_down=B.private(NS * sdb))
+        B.synth(Q2_K, lb["gate"], NR * I * H // 256, 100 * li + 1)
+        B.synth(Q2_K, lb["up"], NR * I * H // 256, 100 * li + 2)
+        B.synth(Q3_K, lb["down"], NR * H * I // 256, 100 * li + 3)
+        B.synth(Q4_K, lb["s_gate"], NS * I * H // 256, 100 * li + 4)
+        B.synth(Q4_K, lb["s_up"], NS * I * H // 256, 100 * li + 5)
+        B.synth(Q4_K, lb["s_down"], NS * H * I // 256, 100 * li + 6)
+        rw = (rng.standard_normal((NR + NS, H)) * 0.02).astype(np.float32)
+        rb = rng.uniform(-0.1, 0.1, NR).astype(np.float32)
+        for key, arr in (("rw", rw), ("rb", rb)):
+            sb = B.dev.shared_from(arr)
+            lb[key] = B.private(arr.nbytes)
+            B.dev.run(L.sepia_gpu_copy, sb, 0, lb[key], 0, arr.size)
+            B.dev.free(sb)
+        host_router.append((rw, rb))
+        d = hip.MoeLayerDesc(hidden=H, inter=I, n_routed=NR, n_shared=NS, topk=6, route_scale=8.0,
+                             global_scale=1.0, router_w=lb["rw"], router_bias=lb["rb"])
+        d.gate, d.up, d.down = hip.ExpertTensor(lb["gate"], 0, gb, Q2_K), hip.ExpertTensor(lb["up"], 0, gb, Q2_K), \
+            hip.ExpertTensor(lb["down"], 0, db, Q3_K)
+        d.s_gate, d.s_up, d.s_down = hip.ExpertTensor(lb["s_gate"], 0, sgb, Q4_K), \
+            hip.ExpertTensor(lb["s_up"], 0, sgb, Q4_K), hip.ExpertTensor(lb["s_down"], 0, sdb, Q4_K)
+        layers.append((d, lb))
+    nx = 64
+    xh, xs = B.vectors(H, nx, 41)
+    y = B.private(H * 4)
+
+    def step(i):
+        d = layers[i % n_layers][0]
+        return L.sepia_gpu_moe_decode(ctypes.byref(d), xs[i % nx], y, None)
+
+    ms = B.timed_steps(step, warmup, steps)
+    per_token = (NR + NS) * H * 4 + 6 * (2 * gb + db) + NS * (2 * sgb + sdb)
+    kms = B.kernel_ms(step, min(steps, 60), ["sepia_matvec_f32", "sepia_moe_select", "sepia_moe_gateup",
+                                             "sepia_moe_down"])
+
+    # parity at full size: route + output of one token against the oracle
+    import oracle
+    d, lb = layers[0]
+    route = B.dev.alloc(64)
+    yb = B.dev.alloc(H * 4)
+    B.dev.run(L.sepia_gpu_moe_decode, ctypes.byref(d), xs[0], yb, route)
+    y_gpu = B.dev.download(yb, H)
+    idx = B.dev.download(route, 6, dtype=np.int32)
+    rw, rb = host_router[0]
+    spec = dict(hidden=H, inter=I, n_routed=NR, n_shared=NS, topk=6, route_scale=8.0, global_scale=1.0,
+                router_w=rw, router_bias=rb, t_gate=Q2_K, t_up=Q2_K, t_down=Q3_K, ts_gate=Q4_K, ts_up=Q4_K,
+                ts_down=Q4_K, gate=[None] * NR, up=[None] * NR, down=[None] * NR,
+                s_gate=[B.fetch(lb["s_gate"], s * sgb, sgb) for s in range(NS)],
+                s_up=[B.fetch(lb["s_up"], s * sgb, sgb) for s in range(NS)],
+                s_down=[B.fetch(lb["s_down"], s * sdb, sdb) for s in range(NS)])
+    for e in idx:
+        spec["gate"][e] = B.fetch(lb["gate"], int(e) * gb, gb)
+        spec["up"][e] = B.fetch(lb["up"], int(e) * gb, gb)
+        spec["down"][e] = B.fetch(lb["down"], int(e) * db, db)
+    logits = oracle.linear_f32(rw, xh[0])
+    idx_ref, _ = oracle.route_select(logits, rb, NR, NS, 6, 8.0, 1.0)
+    nthr = min(16, os.cpu_count() or 1)
+    want, _, _, _ = oracle.moe_layer(spec, xh[0], force_idx=idx, threads=nthr)
+    err = float(np.max(np.abs(y_gpu - want)))
+    scale = float(np.max(np.abs(want)))
+    if err > 1e-4 * scale:
+        raise RuntimeError("C3 parity: max|diff| %g > 1e-4 * %g" % (err, scale))
+    s1, n1 = cpu_sample(lambda: oracle.moe_layer(spec, xh[0], force_idx=idx, threads=1), cpu_seconds, 100)
+    B.dev.free(route)
+    B.dev.free(yb)
+    for d, lb in layers:
+        for b in lb.values():
+            B.dev.free(b)
+    for b in xs + [y]:
+        B.dev.free(b)
+    return dict(us_per_token=ms * 1e3, bytes_per_token=per_token, gbs=per_token / (ms * 1e-3) / 1e9,
+                roofline_us=per_token / (HBM_PEAK_GBS * 1e9) * 1e6,
+                target_us=1.5 * per_token / (HBM_PEAK_GBS * 1e9) * 1e6,
+                layers_rotated=n_layers, x_vectors=nx,
+                kernels_avg_us={k: v * 1e3 for k, v in kms.items()},
+                parity=dict(max_abs_diff=err, y_inf=scale, selection=[int(v) for v in idx],
+                            oracle_selection=[int(v) for v in idx_ref]),
+                cpu_1core_ms_per_token=s1 * 1e3)
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--only", choices=["c2", "c1", "c3", "c4"], default=None,
+                    help="run one configuration (profiling runs); default: all")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py: this build measures one GPU only (the path has no multi-GPU "
+              "component; sharding is described in DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    from sepia_amd import hip
+    dev = hip.Device()
+    B = Bench(dev)
+    log("device", dev.name)
+    extra = {}
+    res = None
+    t0 = time.time()
+    if args.only in (None, "c2"):
+        res = run_c2(B, args.warmup, args.steps, args.cpu_seconds)
+        log("C2 %.2f us/step %.1f GB/s (%.1f%%) in %.0fs" % (res["ms"] * 1e3, res["value"],
+                                                             100 * res["value"] / HBM_PEAK_GBS, time.time() - t0))
+    if args.only in (None, "c1"):
+        extra["C1_q4_k_4096x4096"] = run_matvec_rotation(B, "C1", Q4_K, 4096, 4096, args.warmup, args.steps,
+                                                         min(3.0, args.cpu_seconds), 51)
+        log("C1", json.dumps(extra["C1_q4_k_4096x4096"]))
+    if args.only in (None, "c4"):
+        for key, t in (("C4_iq3_xxs_6144x6144", IQ3_XXS), ("C4_iq2_xs_6144x6144_substitute", IQ2_XS)):
+            extra[key] = run_matvec_rotation(B, key, t, 6144, 6144, args.warmup, args.steps,
+                                             min(3.0, args.cpu_seconds), 61 + t)
+            log(key, json.dumps(extra[key]))
+    if args.only in (None, "c3"):
+        extra["C3_moe_decode_layer"] = run_c3(B, args.warmup, min(args.steps, 200), min(5.0, args.cpu_seconds))
+        log("C3", json.dumps(extra["C3_moe_decode_layer"]))
+    if res is None:
+        print(json.dumps(extra, indent=1))
+        return
+
+    value = res["value"]
+    rf = res["roofline"]
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(res["ms"], 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded random GGUF blocks, f16 scales U[2^-10,2^-6]; x ~ N(0,1))",
+        "config": {"workload": "C2: one routed expert FFN, decode batch 1, hidden 6144, inter 3072, "
+                               "gate/up Q2_K [3072x6144], down Q3_K [6144x3072]; 40 experts (820 MB) "
+                               "resident in HBM, rotated per step",
+                   "bytes_per_step": res["step_bytes"], "hbm_frac": round(value / HBM_PEAK_GBS, 4)},
+        "roofline": {"bound": "hbm", "achieved": round(rf["achieved"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(rf["achieved"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": rf["kernel"], "bytes_per_launch": rf["bytes_per_launch"],
+                     "avg_launch_us": round(rf["avg_launch_us"], 3), "other_kernels": rf["other_kernels"]},
+        "cpu_baseline": {"value": round(res["step_bytes"] / res["cpu"]["s1"] / 1e9, 4), "unit": "GB/s", "cores": 1,
+                         "kind": "port",
+                         "sample": "oracle expert FFN (per-row dequant + double accumulate, the reference's qlinear "
+                                   "loop) on the same expert, %d calls, %.1f ms/call; %d threads: %.1f ms/call"
+                                   % (res["cpu"]["n1"], res["cpu"]["s1"] * 1e3, res["cpu"]["threads"],
+                                      res["cpu"]["sN"] * 1e3),
+                         "cpu_model": cpu_model()},
+        "parity": res["parity"],
+        "extra": extra,
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

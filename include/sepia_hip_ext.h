@@ -56,6 +56,23 @@ typedef struct {
 int sepia_gpu_moe_decode(const SepiaMoeLayerDesc *layer, SepiaGpuBuf *x, SepiaGpuBuf *y,
                          SepiaGpuBuf *route_out);
 
+/* One routed expert: y = down(silu(gate x) * up x) for expert `expert` of
+ * stacks holding n_experts experts (reference src/sepia.c:2993-3017,
+ * real_expert_ffn), as two launches (fused gate/up/SwiGLU, then down).
+ * x, y: f32 [hidden] at offset 0. */
+int sepia_gpu_expert_ffn(const SepiaExpertTensor *gate, const SepiaExpertTensor *up, const SepiaExpertTensor *down,
+                         int n_experts, int expert, int64_t hidden, int64_t inter, SepiaGpuBuf *x, SepiaGpuBuf *y);
+
+/* Launch timing: between start and stop every launch is bracketed by a pair
+ * of HIP events on the stream it runs on; stop waits for the stream and adds
+ * each launch's duration to its kernel's total. query reads the totals of a
+ * kernel by name (e.g. "sepia_moe_gateup"); reset clears them. Not for use
+ * inside a stream capture. */
+int sepia_hip_profile_start(void);
+int sepia_hip_profile_stop(void);
+int sepia_hip_profile_query(const char *kernel, int64_t *launches, double *total_ms);
+void sepia_hip_profile_reset(void);
+
 /* Benchmark and test support. Fills n_blocks blocks of `ggml_type` at byte
  * `off` of buf with seeded random bytes, then sets every f16 scale field of
  * each block to a value uniform in [lo, hi] (rounded to f16). */

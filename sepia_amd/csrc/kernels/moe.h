@@ -110,16 +110,17 @@ __device__ __forceinline__ const uint8_t *moe_row(const MoeProj &P, int64_t e, i
     return P.base + e * P.stride + r * P.row_bytes;
 }
 
-// One wave per (slot, intermediate row); 4 rows per workgroup.
+// One wave per (slot, intermediate row); 4 rows per workgroup. sel_idx may be
+// NULL: then slot s < topk is expert fixed_expert + s (a single-expert FFN).
 extern "C" __global__ __launch_bounds__(256) void sepia_moe_gateup(
     MoeProj gate, MoeProj up, MoeProj s_gate, MoeProj s_up, const int32_t *__restrict__ sel_idx,
-    int32_t topk, int64_t inter, const float *__restrict__ x, float *__restrict__ h) {
+    int32_t fixed_expert, int32_t topk, int64_t inter, const float *__restrict__ x, float *__restrict__ h) {
     const int64_t tiles = (inter + 3) / 4;
     const int32_t slot = (int32_t)(blockIdx.x / tiles);
     const int64_t row = (blockIdx.x % tiles) * 4 + (threadIdx.x >> 6);
     if (row >= inter) return;
     const bool routed = slot < topk;
-    const int64_t e = routed ? sel_idx[slot] : slot - topk;
+    const int64_t e = routed ? (sel_idx ? sel_idx[slot] : fixed_expert + slot) : slot - topk;
     const MoeProj &G = routed ? gate : s_gate;
     const MoeProj &U = routed ? up : s_up;
     const float g = row_dot_any(G.type, moe_row(G, e, row), G.n_blocks, x);
@@ -128,20 +129,22 @@ extern "C" __global__ __launch_bounds__(256) void sepia_moe_gateup(
 }
 
 // One wave per output row d; it walks every slot, so the weighted sum is
-// formed in registers in a fixed order (deterministic, no atomics).
+// formed in registers in a fixed order (deterministic, no atomics). With
+// sel_idx NULL the routed slots are experts fixed_expert + s and, with sel_w
+// NULL, every weight is 1.
 extern "C" __global__ __launch_bounds__(256) void sepia_moe_down(
     MoeProj down, MoeProj s_down, const int32_t *__restrict__ sel_idx, const float *__restrict__ sel_w,
-    int32_t topk, int32_t n_shared, int64_t inter, int64_t hidden, const float *__restrict__ h,
-    float *__restrict__ y) {
+    int32_t fixed_expert, int32_t topk, int32_t n_shared, int64_t inter, int64_t hidden,
+    const float *__restrict__ h, float *__restrict__ y) {
     const int64_t d = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (d >= hidden) return;
     float acc = 0.0f;
     for (int32_t slot = 0; slot < topk + n_shared; slot++) {
         const bool routed = slot < topk;
         const MoeProj &P = routed ? down : s_down;
-        const int64_t e = routed ? sel_idx[slot] : slot - topk;
+        const int64_t e = routed ? (sel_idx ? sel_idx[slot] : fixed_expert + slot) : slot - topk;
         const float v = row_dot_any(P.type, moe_row(P, e, d), P.n_blocks, h + (int64_t)slot * inter);
-        acc = __builtin_fmaf(sel_w[slot], v, acc);
+        acc = sel_w ? __builtin_fmaf(sel_w[slot], v, acc) : acc + v;
     }
     if ((threadIdx.x & 63) == 0) y[d] = acc;
 }

@@ -321,7 +321,10 @@ int sepia_gpu_init(const char *kernel_dir) {
             return 0;
         }
     }
-    snprintf(g_device_name, sizeof g_device_name, "%s", prop.name);
+    if (prop.name[0])
+        snprintf(g_device_name, sizeof g_device_name, "%s", prop.name);
+    else
+        snprintf(g_device_name, sizeof g_device_name, "AMD %.200s", prop.gcnArchName);
     g_available = 1;
     g_batch_open = 0;
     g_have_iq2xxs = 0;
@@ -395,14 +398,102 @@ int sepia_gpu_end(void) {
     return 1;
 }
 
+/* Launch profiling (sepia_hip_profile_*): while on, every launch is
+ * bracketed by a pair of HIP events recorded on the launch stream. */
+#define PROF_MAX 16384
+static int g_prof_on;
+static int g_prof_n;
+static int g_prof_overflow;
+static hipEvent_t g_prof_ev[PROF_MAX][2];
+static int g_prof_kid[PROF_MAX];
+static int g_prof_ev_made;
+static double g_prof_ms[K_COUNT];
+static int64_t g_prof_cnt[K_COUNT];
+
 static int launch(int k, unsigned grid, unsigned block, void **args, const char *op) {
     if (grid == 0) return 1;
+    int slot = -1;
+    if (g_prof_on) {
+        if (g_prof_n < g_prof_ev_made) {
+            slot = g_prof_n++;
+            hipEventRecord(g_prof_ev[slot][0], g_stream);
+        } else {
+            g_prof_overflow = 1;
+        }
+    }
     hipError_t e = hipModuleLaunchKernel(g_fn[k], grid, 1, 1, block, 1, 1, 0, g_stream, args, NULL);
+    if (slot >= 0) {
+        hipEventRecord(g_prof_ev[slot][1], g_stream);
+        g_prof_kid[slot] = k;
+    }
     if (e != hipSuccess) {
         LOG("%s: launch of %s failed: %s", op, k_names[k], hipGetErrorString(e));
         return 0;
     }
     return 1;
+}
+
+int sepia_hip_profile_start(void) {
+    if (!need_init("profile_start")) return 0;
+    if (g_prof_on) {
+        LOG("profile_start: profiling is already on");
+        return 0;
+    }
+    while (g_prof_ev_made < PROF_MAX) {
+        if (hipEventCreate(&g_prof_ev[g_prof_ev_made][0]) != hipSuccess) break;
+        if (hipEventCreate(&g_prof_ev[g_prof_ev_made][1]) != hipSuccess) {
+            hipEventDestroy(g_prof_ev[g_prof_ev_made][0]);
+            break;
+        }
+        g_prof_ev_made++;
+    }
+    if (g_prof_ev_made == 0) {
+        LOG("profile_start: cannot create events");
+        return 0;
+    }
+    g_prof_on = 1;
+    g_prof_n = 0;
+    return 1;
+}
+
+int sepia_hip_profile_stop(void) {
+    if (!need_init("profile_stop")) return 0;
+    if (!g_prof_on) {
+        LOG("profile_stop: profiling is off");
+        return 0;
+    }
+    g_prof_on = 0;
+    hipError_t e = hipStreamSynchronize(g_stream);
+    for (int i = 0; i < g_prof_n && e == hipSuccess; i++) {
+        float ms = 0.0f;
+        e = hipEventElapsedTime(&ms, g_prof_ev[i][0], g_prof_ev[i][1]);
+        g_prof_ms[g_prof_kid[i]] += ms;
+        g_prof_cnt[g_prof_kid[i]]++;
+    }
+    g_prof_n = 0;
+    if (e != hipSuccess) {
+        LOG("profile_stop: %s", hipGetErrorString(e));
+        return 0;
+    }
+    if (g_prof_overflow) LOG("profile_stop: more than %d launches; the rest were not timed", g_prof_ev_made);
+    g_prof_overflow = 0;
+    return 1;
+}
+
+int sepia_hip_profile_query(const char *kernel, int64_t *launches, double *total_ms) {
+    for (int k = 0; k < K_COUNT; k++) {
+        if (!kernel || strcmp(kernel, k_names[k]) != 0) continue;
+        if (launches) *launches = g_prof_cnt[k];
+        if (total_ms) *total_ms = g_prof_ms[k];
+        return 1;
+    }
+    LOG("profile_query: unknown kernel \"%s\"", kernel ? kernel : "(null)");
+    return 0;
+}
+
+void sepia_hip_profile_reset(void) {
+    memset(g_prof_ms, 0, sizeof g_prof_ms);
+    memset(g_prof_cnt, 0, sizeof g_prof_cnt);
 }
 
 static unsigned blocks_for(int64_t n, int64_t per) { return (unsigned)((n + per - 1) / per); }
@@ -878,10 +969,11 @@ int sepia_gpu_moe_decode(const SepiaMoeLayerDesc *L, SepiaGpuBuf *x, SepiaGpuBuf
     void *a_sel[] = { &logits, &rb, &nr, &ns, &tk, &rs, &gs, &sel_idx, &sel_w };
     if (!launch(K_MOE_SELECT, 1, 256, a_sel, op)) return 0;
 
-    void *a_gu[] = { &g, &u, &sg, &su, &sel_idx, &tk, &inter, &x->dev, &h };
+    int32_t no_fixed = 0;
+    void *a_gu[] = { &g, &u, &sg, &su, &sel_idx, &no_fixed, &tk, &inter, &x->dev, &h };
     if (!launch(K_MOE_GATEUP, (unsigned)(n_slots * ((I + 3) / 4)), 256, a_gu, op)) return 0;
 
-    void *a_dn[] = { &d, &sd, &sel_idx, &sel_w, &tk, &ns, &inter, &hid, &h, &y->dev };
+    void *a_dn[] = { &d, &sd, &sel_idx, &sel_w, &no_fixed, &tk, &ns, &inter, &hid, &h, &y->dev };
     if (!launch(K_MOE_DOWN, blocks_for(H, 4), 256, a_dn, op)) return 0;
 
     if (route_out) {
@@ -895,4 +987,34 @@ int sepia_gpu_moe_decode(const SepiaMoeLayerDesc *L, SepiaGpuBuf *x, SepiaGpuBuf
         }
     }
     return 1;
+}
+
+int sepia_gpu_expert_ffn(const SepiaExpertTensor *gate, const SepiaExpertTensor *up, const SepiaExpertTensor *down,
+                         int n_experts, int expert, int64_t hidden, int64_t inter, SepiaGpuBuf *x, SepiaGpuBuf *y) {
+    const char *op = "expert_ffn";
+    if (!gate || !up || !down || !x || !y || hidden <= 0 || inter <= 0 || n_experts < 1 || expert < 0 ||
+        expert >= n_experts || (inter + 3) / 4 > MAX_GRID || (hidden + 3) / 4 > MAX_GRID) {
+        LOG("%s: invalid arguments", op);
+        return 0;
+    }
+    MoeProj g, u, d, none;
+    memset(&none, 0, sizeof none);
+    if (!moe_proj(op, "gate", gate, n_experts, inter, hidden, &g) || !moe_proj(op, "up", up, n_experts, inter, hidden, &u) ||
+        !moe_proj(op, "down", down, n_experts, hidden, inter, &d))
+        return 0;
+    if (!chk(x, 0, (size_t)hidden * 4, op, "x") || !chk(y, 0, (size_t)hidden * 4, op, "y")) return 0;
+    if (!need_batch(op)) return 0;
+    float *h = (float *)scratch((size_t)inter * 4, op);
+    if (!h) return 0;
+    if (!prep_in(gate->buf, op) || !prep_in(up->buf, op) || !prep_in(down->buf, op) || !prep_in(x, op) ||
+        !prep_out(y, op))
+        return 0;
+    const int32_t *no_idx = NULL;
+    const float *no_w = NULL;
+    int32_t e = expert, one = 1, zero = 0;
+    int64_t in64 = inter, hid = hidden;
+    void *a_gu[] = { &g, &u, &none, &none, &no_idx, &e, &one, &in64, &x->dev, &h };
+    if (!launch(K_MOE_GATEUP, blocks_for(inter, 4), 256, a_gu, op)) return 0;
+    void *a_dn[] = { &d, &none, &no_idx, &no_w, &e, &one, &zero, &in64, &hid, &h, &y->dev };
+    return launch(K_MOE_DOWN, blocks_for(hidden, 4), 256, a_dn, op);
 }

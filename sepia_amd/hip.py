@@ -73,6 +73,12 @@ PROTOTYPES = {
     "sepia_gpu_scale": (_I, [_F, _P, _P, _I64]),
     "sepia_gpu_sconv_hist_roll": (_I, [_P, _P, _I64, _I64, _I64]),
     "sepia_gpu_moe_decode": (_I, [ctypes.POINTER(MoeLayerDesc), _P, _P, _P]),
+    "sepia_gpu_expert_ffn": (_I, [ctypes.POINTER(ExpertTensor), ctypes.POINTER(ExpertTensor),
+                                  ctypes.POINTER(ExpertTensor), _I, _I, _I64, _I64, _P, _P]),
+    "sepia_hip_profile_start": (_I, []),
+    "sepia_hip_profile_stop": (_I, []),
+    "sepia_hip_profile_query": (_I, [ctypes.c_char_p, ctypes.POINTER(_I64), ctypes.POINTER(ctypes.c_double)]),
+    "sepia_hip_profile_reset": (None, []),
     "sepia_hip_synth_blocks": (_I, [_I, _P, _SZ, _I64, ctypes.c_uint64, _F, _F]),
     "sepia_hip_set_iq2xxs_grid": (_I, [_P]),
     "sepia_hip_stream": (_P, []),
