@@ -214,24 +214,15 @@ def run_c2(B, warmup, steps, cpu_seconds):
         return L.sepia_gpu_expert_ffn(*ref, NE, i % NE, H, I, xs[0], y)
 
     ms = B.timed_steps(step, warmup, steps)
+    # graph replay == eager result (the last captured step used expert (warmup+steps-1) % NE)
+    e_last = (warmup + steps - 1) % NE
+    y_graph = B.fetch(y, 0, H * 4).view(np.float32)
     step_bytes = gb + ub + db + H * 4 + I * 4 + H * 4
     kms = B.kernel_ms(step, min(steps, 4 * NE), ["sepia_moe_gateup", "sepia_moe_down"])
     gu_bytes = gb + ub + H * 4 + I * 4
     dn_bytes = db + I * 4 + H * 4
-
-    # graph replay == eager result (the last captured step used expert (warmup+steps-1) % NE)
-    e_last = (warmup + steps - 1) % NE
-    yb = B.dev.alloc(H * 4)
-    B.dev.begin()
-    B.dev.check(L.sepia_gpu_copy(y, 0, yb, 0, H), "copy")
-    B.dev.end()
-    y_graph = B.dev.download(yb, H)
     B.dev.run(L.sepia_gpu_expert_ffn, *ref, NE, e_last, H, I, xs[0], y)
-    B.dev.begin()
-    B.dev.check(L.sepia_gpu_copy(y, 0, yb, 0, H), "copy")
-    B.dev.end()
-    y_eager = B.dev.download(yb, H)
-    B.dev.free(yb)
+    y_eager = B.fetch(y, 0, H * 4).view(np.float32)
     if not np.array_equal(y_graph.view(np.uint32), y_eager.view(np.uint32)):
         raise RuntimeError("graph replay differs from the eager result")
 

@@ -87,6 +87,11 @@ int sepia_hip_set_iq2xxs_grid(const uint64_t *grid256);
 /* The hipStream_t every op is issued on (for hipEvent timing). */
 void *sepia_hip_stream(void);
 
+/* Kernel-selection switches for tests and tuning: "tile" 1/0 enables or
+ * disables the split-K tile kernels (disabled = the generic one-wave-per-row
+ * kernels); "tile_j" 0/2/4 = automatic or forced rows per thread. */
+int sepia_hip_set_option(const char *name, int value);
+
 #ifdef __cplusplus
 }
 #endif

@@ -197,5 +197,16 @@ extern "C" __global__ __launch_bounds__(256) void sepia_sconv_hist_roll_f32(
     }
 }
 
+// ------------------------------------------------------------------------
+// Split-K tile matvec with integer dot products (mv.h), per format and rows
+// per thread J.
+#include "mv.h"
+SEPIA_MV_KERNEL(q2_k, ST_Q2_K, 2)
+SEPIA_MV_KERNEL(q2_k, ST_Q2_K, 4)
+SEPIA_MV_KERNEL(q3_k, ST_Q3_K, 2)
+SEPIA_MV_KERNEL(q3_k, ST_Q3_K, 4)
+SEPIA_MV_KERNEL(q4_k, ST_Q4_K, 2)
+SEPIA_MV_KERNEL(q4_k, ST_Q4_K, 4)
+
 #include "moe.h"
 #include "synth.h"

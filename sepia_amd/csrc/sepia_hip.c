@@ -42,6 +42,7 @@ enum {
     K_MV_IQ2_XXS, K_MV_IQ2_XS, K_MV_IQ3_XXS, K_MV_IQ4_XS,
     K_MATVEC_F32, K_SILU_MUL, K_ADD, K_SCALE, K_COPY, K_TOUCH, K_RMSNORM, K_SOFTMAX,
     K_SCONV, K_SCONV_HIST, K_MOE_SELECT, K_MOE_GATEUP, K_MOE_DOWN, K_SYNTH_FILL, K_SYNTH_F16,
+    K_MV_Q2_K_J2, K_MV_Q2_K_J4, K_MV_Q3_K_J2, K_MV_Q3_K_J4, K_MV_Q4_K_J2, K_MV_Q4_K_J4,
     K_COUNT
 };
 static const char *const k_names[K_COUNT] = {
@@ -57,6 +58,8 @@ static const char *const k_names[K_COUNT] = {
     "sepia_touch_f32", "sepia_rmsnorm_f32", "sepia_softmax_f32", "sepia_sconv_f32",
     "sepia_sconv_hist_roll_f32", "sepia_moe_select", "sepia_moe_gateup", "sepia_moe_down",
     "sepia_synth_fill", "sepia_synth_patch_f16",
+    "sepia_mv_q2_k_j2", "sepia_mv_q2_k_j4", "sepia_mv_q3_k_j2", "sepia_mv_q3_k_j4",
+    "sepia_mv_q4_k_j2", "sepia_mv_q4_k_j4",
 };
 
 /* GGUF block geometry (reference src/quants.c:46-51; tools/gguf_inspect.py:109-117). */
@@ -67,20 +70,27 @@ typedef struct {
     int parts;      /* 32-weight parts per block (dequant threads per block) */
     int k_dq, k_mv; /* kernel ids, -1 if none */
     int f16_off[2]; /* byte offsets of f16 scale fields, -1 = none */
+    int k_tile[2];  /* split-K tile kernels (J = 2, 4 rows per thread), -1 if none */
+    int align;      /* byte alignment the tile kernels need for a matrix base */
 } TypeInfo;
 static const TypeInfo k_types[] = {
-    { 1, 1, 2, 1, K_DQ_F16, -1, { -1, -1 } },
-    { 8, 32, 34, 1, K_DQ_Q8_0, K_MV_Q8_0, { 0, -1 } },
-    { 10, 256, 84, 8, K_DQ_Q2_K, K_MV_Q2_K, { 80, 82 } },
-    { 11, 256, 110, 8, K_DQ_Q3_K, K_MV_Q3_K, { 108, -1 } },
-    { 12, 256, 144, 8, K_DQ_Q4_K, K_MV_Q4_K, { 0, 2 } },
-    { 13, 256, 176, 8, K_DQ_Q5_K, K_MV_Q5_K, { 0, 2 } },
-    { 14, 256, 210, 8, K_DQ_Q6_K, K_MV_Q6_K, { 208, -1 } },
-    { 16, 256, 66, 8, K_DQ_IQ2_XXS, K_MV_IQ2_XXS, { 0, -1 } },
-    { 17, 256, 74, 8, K_DQ_IQ2_XS, K_MV_IQ2_XS, { 0, -1 } },
-    { 18, 256, 98, 8, K_DQ_IQ3_XXS, K_MV_IQ3_XXS, { 0, -1 } },
-    { 23, 256, 136, 8, K_DQ_IQ4_XS, K_MV_IQ4_XS, { 0, -1 } },
+    { 1, 1, 2, 1, K_DQ_F16, -1, { -1, -1 }, { -1, -1 }, 1 },
+    { 8, 32, 34, 1, K_DQ_Q8_0, K_MV_Q8_0, { 0, -1 }, { -1, -1 }, 1 },
+    { 10, 256, 84, 8, K_DQ_Q2_K, K_MV_Q2_K, { 80, 82 }, { K_MV_Q2_K_J2, K_MV_Q2_K_J4 }, 4 },
+    { 11, 256, 110, 8, K_DQ_Q3_K, K_MV_Q3_K, { 108, -1 }, { K_MV_Q3_K_J2, K_MV_Q3_K_J4 }, 2 },
+    { 12, 256, 144, 8, K_DQ_Q4_K, K_MV_Q4_K, { 0, 2 }, { K_MV_Q4_K_J2, K_MV_Q4_K_J4 }, 4 },
+    { 13, 256, 176, 8, K_DQ_Q5_K, K_MV_Q5_K, { 0, 2 }, { -1, -1 }, 1 },
+    { 14, 256, 210, 8, K_DQ_Q6_K, K_MV_Q6_K, { 208, -1 }, { -1, -1 }, 1 },
+    { 16, 256, 66, 8, K_DQ_IQ2_XXS, K_MV_IQ2_XXS, { 0, -1 }, { -1, -1 }, 1 },
+    { 17, 256, 74, 8, K_DQ_IQ2_XS, K_MV_IQ2_XS, { 0, -1 }, { -1, -1 }, 1 },
+    { 18, 256, 98, 8, K_DQ_IQ3_XXS, K_MV_IQ3_XXS, { 0, -1 }, { -1, -1 }, 1 },
+    { 23, 256, 136, 8, K_DQ_IQ4_XS, K_MV_IQ4_XS, { 0, -1 }, { -1, -1 }, 1 },
 };
+
+/* Split-K tile geometry (kernels/mv.h): 4 blocks per column slice, 16 rows
+ * per workgroup step, J rows per thread. */
+#define TILE_NBC 4
+#define TILE_RS 16
 
 static int g_available;
 static int g_have_iq2xxs;
@@ -170,6 +180,38 @@ static int prep_out(SepiaGpuBuf *b, const char *op) {
     if (b->kind == BUF_SHARED) b->dev_newer = 1;
     return 1;
 }
+
+/* Library scratch in HBM: a region of arrival counters (zeroed once; every
+ * kernel that uses one leaves it at zero again) followed by a data region
+ * for partial sums and intermediate vectors, grown on demand. */
+#define CNT_BYTES (64u * 1024u)
+static void *g_scratch;
+static size_t g_scratch_len;
+
+/* Data region of at least `need` bytes (the counters sit in front of it).
+ * Growing waits for the stream, since queued kernels may still use the old
+ * region; the new allocation is cleared so every counter starts at zero. */
+static void *scratch(size_t need, const char *op) {
+    if (g_scratch && need <= g_scratch_len - CNT_BYTES) return (uint8_t *)g_scratch + CNT_BYTES;
+    hipStreamSynchronize(g_stream);
+    if (g_scratch) hipFree(g_scratch);
+    g_scratch = NULL;
+    g_scratch_len = 0;
+    size_t want = CNT_BYTES + (need < (4u << 20) ? (4u << 20) : need);
+    hipError_t e = hipMalloc(&g_scratch, want);
+    if (e == hipSuccess) e = hipMemsetAsync(g_scratch, 0, want, g_stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(g_stream);
+    if (e != hipSuccess) {
+        LOG("%s: scratch allocation of %zu bytes failed: %s", op, want, hipGetErrorString(e));
+        if (g_scratch) hipFree(g_scratch);
+        g_scratch = NULL;
+        return NULL;
+    }
+    g_scratch_len = want;
+    return (uint8_t *)g_scratch + CNT_BYTES;
+}
+
+static uint32_t *scratch_counters(void) { return (uint32_t *)g_scratch; }
 
 static SepiaGpuBuf *new_buf(size_t len, int kind) {
     SepiaGpuBuf *b = (SepiaGpuBuf *)calloc(1, sizeof *b);
@@ -330,9 +372,6 @@ int sepia_gpu_init(const char *kernel_dir) {
     g_have_iq2xxs = 0;
     return 1;
 }
-
-static void *g_scratch;
-static size_t g_scratch_len;
 
 void sepia_gpu_shutdown(void) {
     if (!g_available) return;
@@ -734,6 +773,41 @@ int sepia_gpu_selftest_touch(SepiaGpuBuf *buf, size_t n_floats) {
 }
 
 /* --------------------------------------------------------- quantized ---- */
+/* Tuning switches (sepia_hip_set_option): "tile" 0 forces the generic
+ * one-wave-per-row kernels; "tile_j" 2 or 4 forces the rows per thread of the
+ * split-K tile kernels (0 = automatic). */
+static int g_opt_tile = 1;
+static int g_opt_tile_j = 0;
+
+int sepia_hip_set_option(const char *name, int value) {
+    if (!name) {
+        LOG("set_option: NULL name");
+        return 0;
+    }
+    if (strcmp(name, "tile") == 0 && (value == 0 || value == 1)) {
+        g_opt_tile = value;
+        return 1;
+    }
+    if (strcmp(name, "tile_j") == 0 && (value == 0 || value == 2 || value == 4)) {
+        g_opt_tile_j = value;
+        return 1;
+    }
+    LOG("set_option: unknown option %s=%d", name, value);
+    return 0;
+}
+
+/* Rows per thread (2 or 4) of the split-K tile kernel for this matrix, or 0
+ * when the generic kernel must run: the format has no tile decoder, the row
+ * is not a whole number of 4-block column slices, the base is not aligned as
+ * the decoder loads it, or there are more row tiles than arrival counters. */
+static int tile_plan(const TypeInfo *ti, int64_t n_blocks, uintptr_t base, int64_t rows) {
+    if (!g_opt_tile || ti->k_tile[0] < 0 || n_blocks % TILE_NBC || base % (uintptr_t)ti->align) return 0;
+    const int64_t n_ks = n_blocks / TILE_NBC;
+    int J = g_opt_tile_j;
+    if (!J) J = ((rows + 4 * TILE_RS - 1) / (4 * TILE_RS)) * n_ks >= 512 ? 4 : 2;
+    if ((rows + TILE_RS * J - 1) / (TILE_RS * J) > (int64_t)(CNT_BYTES / 4)) return 0;
+    return J;
+}
 int sepia_gpu_matvec_q(int ggml_type, SepiaGpuBuf *w, size_t w_off, SepiaGpuBuf *x, SepiaGpuBuf *y,
                        int64_t out_dim, int64_t in_dim) {
     const char *op = "matvec_q";
@@ -758,6 +832,16 @@ int sepia_gpu_matvec_q(int ggml_type, SepiaGpuBuf *w, size_t w_off, SepiaGpuBuf 
         return 0;
     if (!need_batch(op) || !prep_in(w, op) || !prep_in(x, op) || !prep_out(y, op)) return 0;
     const uint8_t *wp = w->dev + w_off;
+    int J = tile_plan(ti, n_blocks, (uintptr_t)wp, out_dim);
+    if (J) {
+        int32_t n_ks = (int32_t)(n_blocks / TILE_NBC);
+        int64_t tiles = (out_dim + TILE_RS * J - 1) / (TILE_RS * J);
+        float *part = (float *)scratch((size_t)n_ks * (size_t)out_dim * 4, op);
+        if (!part) return 0;
+        uint32_t *cnt = scratch_counters();
+        void *args[] = { &wp, &row_bytes, &out_dim, &n_ks, &x->dev, &y->dev, &part, &cnt };
+        return launch(ti->k_tile[J == 4], (unsigned)(tiles * n_ks), 256, args, op);
+    }
     void *args[] = { &wp, &row_bytes, &n_blocks, &x->dev, &y->dev, &out_dim };
     return launch(ti->k_mv, blocks_for(out_dim, 4), 256, args, op);
 }
@@ -883,23 +967,6 @@ static int moe_proj(const char *op, const char *what, const SepiaExpertTensor *t
     out->type = t->ggml_type;
     out->pad = 0;
     return 1;
-}
-
-static void *scratch(size_t need, const char *op) {
-    if (need <= g_scratch_len) return g_scratch;
-    hipStreamSynchronize(g_stream);
-    if (g_scratch) hipFree(g_scratch);
-    g_scratch = NULL;
-    g_scratch_len = 0;
-    size_t want = need < (1u << 20) ? (1u << 20) : need;
-    hipError_t e = hipMalloc(&g_scratch, want);
-    if (e != hipSuccess) {
-        LOG("%s: scratch allocation of %zu bytes failed: %s", op, want, hipGetErrorString(e));
-        g_scratch = NULL;
-        return NULL;
-    }
-    g_scratch_len = want;
-    return g_scratch;
 }
 
 int sepia_gpu_moe_decode(const SepiaMoeLayerDesc *L, SepiaGpuBuf *x, SepiaGpuBuf *y, SepiaGpuBuf *route_out) {

@@ -200,6 +200,56 @@ def test_matvec_q_config_shapes(dev, orc, name, t, out_dim, in_dim):
     check_matvec(dev, orc, t, out_dim, in_dim, seed=zlib.crc32(name.encode()) & 0xFFFF)
 
 
+@pytest.fixture
+def kernel_path(dev, request):
+    """Force one kernel family: the generic per-row kernel, or the split-K tile
+    kernel with 2 or 4 rows per thread."""
+    L = dev.L
+    mode = request.param
+    if mode == "generic":
+        assert L.sepia_hip_set_option(b"tile", 0) == 1
+    else:
+        assert L.sepia_hip_set_option(b"tile_j", {"j2": 2, "j4": 4}[mode]) == 1
+    yield mode
+    L.sepia_hip_set_option(b"tile", 1)
+    L.sepia_hip_set_option(b"tile_j", 0)
+
+
+TILE_SHAPES = [(10, 3072, 6144), (11, 6144, 3072), (12, 4096, 4096), (12, 33, 1024), (10, 17, 2048),
+               (11, 1, 3072), (12, 200, 6144)]
+
+
+@pytest.mark.parametrize("kernel_path", ["generic", "j2", "j4"], indirect=True)
+@pytest.mark.parametrize("t,out_dim,in_dim", TILE_SHAPES, ids=lambda v: str(v))
+def test_matvec_q_kernel_paths(dev, orc, kernel_path, t, out_dim, in_dim):
+    check_matvec(dev, orc, t, out_dim, in_dim, seed=out_dim * 7 + t)
+
+
+@pytest.mark.parametrize("t,w_off", [(10, 4), (10, 132), (12, 4), (12, 1028), (11, 2), (11, 4)])
+def test_matvec_q_tile_offsets(dev, orc, t, w_off):
+    check_matvec(dev, orc, t, 100, 2048, seed=3 + w_off, w_off=w_off)
+
+
+def test_matvec_q_repeat_stable(dev, orc):
+    """Back-to-back calls reuse the arrival counters: results stay identical."""
+    rng = np.random.default_rng(8)
+    t, out_dim, in_dim = 10, 3072, 6144
+    w = synth.random_matrix(t, out_dim, in_dim, rng)
+    x = synth.normal_vector(rng, in_dim)
+    wb, xb, yb = dev.shared_from(w), dev.shared_from(x), dev.alloc(out_dim * 4)
+    outs = []
+    for _ in range(3):
+        dev.begin()
+        for _ in range(5):
+            assert dev.L.sepia_gpu_matvec_q(t, wb, 0, xb, yb, out_dim, in_dim) == 1
+        dev.end()
+        outs.append(dev.download(yb, out_dim))
+    assert all(np.array_equal(o.view(np.uint32), outs[0].view(np.uint32)) for o in outs)
+    assert_close(outs[0], orc.qlinear(t, w, out_dim, in_dim, x, threads=THREADS))
+    for b in (wb, xb, yb):
+        dev.free(b)
+
+
 def test_matvec_q_rejections(dev):
     L = dev.L
     w = dev.alloc(144 * 4)
