@@ -38,13 +38,13 @@ __device__ __forceinline__ void mv_stage_x(const float *__restrict__ x, int64_t 
     float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, SEPIA_WAVE));
-    // m in [2^e, 2^(e+1)): scale 2^(e-21) keeps |x / scale| < 2^22
-    const int e = (m > 0.0f) ? (int)((__float_as_uint(m) >> 23) & 0xFF) - 127 : 0;
+    // |x| * inv <= 8355000 < 127 * (65536 + 256 + 1): three balanced int8 digits
+    const float inv = (m > 0.0f) ? 8355000.0f / m : 0.0f;
     const float vals[4] = {v.x, v.y, v.z, v.w};
     uint32_t w0 = 0, w1 = 0, w2 = 0;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        const int32_t q = (int32_t)__builtin_rintf(__builtin_ldexpf(vals[i], 21 - e));
+        const int32_t q = (int32_t)__builtin_rintf(vals[i] * inv);
         const int32_t lo = (int32_t)(int8_t)q;       // balanced base-256 digits
         const int32_t r1 = (q - lo) >> 8;
         const int32_t mid = (int32_t)(int8_t)r1;
@@ -60,7 +60,7 @@ __device__ __forceinline__ void mv_stage_x(const float *__restrict__ x, int64_t 
     s += __shfl_xor(s, 1, SEPIA_WAVE);
     s += __shfl_xor(s, 2, SEPIA_WAVE);
     if ((t & 3) == 0) L.gsum[t >> 2] = s;
-    if ((t & 63) == 0) L.scale[t >> 6] = __builtin_ldexpf(1.0f, e - 21);
+    if ((t & 63) == 0) L.scale[t >> 6] = (m > 0.0f) ? 1.0f / inv : 0.0f;
 }
 
 template <int T>
@@ -88,22 +88,28 @@ __device__ __forceinline__ int64_t mv_row(int64_t r0, int j) {
     return r0 + (int64_t)j * MV_RS + wave * MV_RW + lane / MV_UC;
 }
 
-// Partial dots of J rows of matrix W (rows x n_blocks blocks, row stride
-// row_bytes) over column slice ks, for this thread's unit. Rows past `rows`
-// read row rows-1 (in bounds) and are discarded by the caller.
+// Issue the loads of this thread's unit for J rows of matrix W (rows x
+// n_blocks blocks, row stride row_bytes) in column slice ks. Rows past `rows`
+// read row rows-1 (in bounds) and are discarded by the caller. Loads are
+// issued before x is staged so their latency overlaps the staging.
 template <int T, int J>
-__device__ __forceinline__ void mv_rows(const uint8_t *__restrict__ W, uint64_t row_bytes, int64_t rows,
-                                        int64_t r0, int ks, const XU &X, float (&acc)[J]) {
+__device__ __forceinline__ void mv_issue(const uint8_t *__restrict__ W, uint64_t row_bytes, int64_t rows,
+                                         int64_t r0, int ks, typename QU<T>::Data (&d)[J]) {
     const int unit = threadIdx.x & (MV_UC - 1);
     const int bl = unit >> 2, k = unit & 3;
     const uint64_t col_off = (uint64_t)(ks * MV_NBC + bl) * QU<T>::bytes;
-    typename QU<T>::Data d[J];
 #pragma unroll
     for (int j = 0; j < J; j++) {
         int64_t r = mv_row(r0, j);
         r = r < rows ? r : rows - 1;
         d[j] = QU<T>::load(W + (uint64_t)r * row_bytes + col_off, k);
     }
+}
+
+// Row sums of the issued units: each 16-lane group adds its unit partials.
+template <int T, int J>
+__device__ __forceinline__ void mv_finish(const typename QU<T>::Data (&d)[J], const XU &X, float (&acc)[J]) {
+    const int k = threadIdx.x & 3;
 #pragma unroll
     for (int j = 0; j < J; j++) {
         float a = QU<T>::dot(d[j], k, X);
@@ -113,21 +119,32 @@ __device__ __forceinline__ void mv_rows(const uint8_t *__restrict__ W, uint64_t 
     }
 }
 
-// After every thread stored its partials: returns true in the workgroup that
-// arrives last at counter *cnt (of `expect` arrivals), which then resets it.
+// Partial sums cross workgroups (and XCDs, whose L2s are not coherent with
+// each other) as agent-scope atomic stores and loads, which go to the
+// coherent level directly; no L2 writeback or invalidate is needed.
+__device__ __forceinline__ void part_store(float *p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float part_load(const float *p) {
+    return __hip_atomic_load((float *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// After every thread stored its partials with part_store: returns true in the
+// workgroup that arrives last at counter *cnt (of `expect` arrivals), which
+// then resets the counter. Each wave waits for its stores to be acknowledged
+// (vmcnt 0) before the barrier, so every partial is in place before the
+// workgroup's arrival is counted; nothing ever waits on another workgroup.
 __device__ __forceinline__ bool mv_last_arrival(uint32_t *cnt, uint32_t expect, MvLds &L) {
-    __threadfence();
+    __builtin_amdgcn_s_waitcnt(0x0F70);   // gfx9 encoding: vmcnt(0), expcnt/lgkmcnt untouched
     __syncthreads();
     if (threadIdx.x == 0) {
-        const uint32_t old = atomicAdd(cnt, 1u);
+        const uint32_t old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         const uint32_t last = (old == expect - 1) ? 1u : 0u;
-        if (last) atomicExch(cnt, 0u);
+        if (last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         L.last = last;
     }
     __syncthreads();
-    const bool last = L.last != 0;
-    if (last) __threadfence();
-    return last;
+    return L.last != 0;
 }
 
 // y = W x for one quantized matrix. grid = n_tiles * KS; tile = blockIdx / KS.
@@ -139,12 +156,14 @@ __device__ __forceinline__ void mv_kernel_body(const uint8_t *__restrict__ W, ui
     const int64_t tile = blockIdx.x / n_ks;
     const int ks = (int)(blockIdx.x % n_ks);
     const int64_t r0 = tile * (MV_RS * J);
+    typename QU<T>::Data d[J];
+    mv_issue<T, J>(W, row_bytes, rows, r0, ks, d);
     mv_stage_x(x, (int64_t)ks * MV_NBC * 256, L);
     __syncthreads();
     XU X;
     mv_load_xu<T>(L, threadIdx.x & (MV_UC - 1), X);
     float acc[J];
-    mv_rows<T, J>(W, row_bytes, rows, r0, ks, X, acc);
+    mv_finish<T, J>(d, X, acc);
     const bool writer = (threadIdx.x & (MV_UC - 1)) == 0;
     if (n_ks == 1) {
 #pragma unroll
@@ -157,14 +176,14 @@ __device__ __forceinline__ void mv_kernel_body(const uint8_t *__restrict__ W, ui
 #pragma unroll
     for (int j = 0; j < J; j++) {
         const int64_t r = mv_row(r0, j);
-        if (writer && r < rows) part[(int64_t)ks * rows + r] = acc[j];
+        if (writer && r < rows) part_store(&part[(int64_t)ks * rows + r], acc[j]);
     }
     if (!mv_last_arrival(&cnt[tile], (uint32_t)n_ks, L)) return;
     for (int i = threadIdx.x; i < MV_RS * J; i += MV_THREADS) {
         const int64_t r = r0 + i;
         if (r >= rows) break;
         float s = 0.0f;
-        for (int p = 0; p < n_ks; p++) s += part[(int64_t)p * rows + r];
+        for (int p = 0; p < n_ks; p++) s += part_load(&part[(int64_t)p * rows + r]);
         y[r] = s;
     }
 }

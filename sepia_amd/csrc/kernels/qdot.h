@@ -1,9 +1,9 @@
 // qdot.h -- integer dot products of quantized 64-weight units with x.
 //
 // x is staged per workgroup as three signed int8 digit planes: within each
-// 256-column block, x[c] ~= xs * (p0 * 65536 + p1 * 256 + p2), with xs a
-// power of two chosen from the block's max |x| so that |x / xs| < 2^22. The
-// truncation error is below 2^-22 of the block's largest |x| -- far inside
+// 256-column block, x[c] ~= xs * (p0 * 65536 + p1 * 256 + p2), with
+// xs = max|x| / 8355000 so that the digits stay within int8. The rounding
+// error is below 6e-8 of the block's largest |x| -- far inside
 // the 1e-4 * ||y||_inf bar (16-bit planes are not: up to 7e-5 measured on
 // these formats) -- and the weight side is exact integers, so each unit's dot
 // is formed exactly with v_dot4_i32_i8 (4 weights x 1 plane per instruction)
@@ -20,7 +20,7 @@
 struct XU {
     int32_t p[3][16];  // plane k, word 4*seg + w = columns seg_col(seg) + 4w .. + 3 (byte j = column +j)
     float gsum[4];     // f32 sum of x over each segment
-    float xs;          // block scale (power of two)
+    float xs;          // block scale
 };
 
 __device__ __forceinline__ int32_t sdot4(int32_t a, int32_t b, int32_t c) {
