@@ -155,6 +155,15 @@ class Bench:
         self.rt.destroy_graph(g)
         return ms / steps
 
+    def kernel_used(self, step, n, candidates):
+        """(name, average ms) of the candidate kernel that the steps launch."""
+        self.kernel_ms(step, n, [])
+        for k in candidates:
+            cnt, tot = ctypes.c_int64(), ctypes.c_double()
+            if self.L.sepia_hip_profile_query(k.encode(), ctypes.byref(cnt), ctypes.byref(tot)) and cnt.value:
+                return k, tot.value / cnt.value
+        raise RuntimeError("none of %s ran" % candidates)
+
     def kernel_ms(self, step, n, kernels):
         """Average per-launch duration of each named kernel over n eager steps."""
         dev = self.dev
@@ -218,7 +227,7 @@ def run_c2(B, warmup, steps, cpu_seconds):
     e_last = (warmup + steps - 1) % NE
     y_graph = B.fetch(y, 0, H * 4).view(np.float32)
     step_bytes = gb + ub + db + H * 4 + I * 4 + H * 4
-    kms = B.kernel_ms(step, min(steps, 4 * NE), ["sepia_moe_gateup", "sepia_moe_down"])
+    kms = B.kernel_ms(step, min(steps, 4 * NE), ["sepia_ffn_gateup", "sepia_ffn_down"])
     gu_bytes = gb + ub + H * 4 + I * 4
     dn_bytes = db + I * 4 + H * 4
     B.dev.run(L.sepia_gpu_expert_ffn, *ref, NE, e_last, H, I, xs[0], y)
@@ -243,14 +252,14 @@ def run_c2(B, warmup, steps, cpu_seconds):
                         cpu_seconds / 4, 1000)
     for b in bufs + xs + [y]:
         B.dev.free(b)
-    dom = "sepia_moe_gateup"
+    dom = "sepia_ffn_gateup"
     return dict(
         ms=ms, step_bytes=step_bytes, value=step_bytes / (ms * 1e-3) / 1e9,
         parity=dict(max_abs_diff=err, y_inf=scale, bound="1e-4*||y||_inf"),
         roofline=dict(bound="hbm", kernel=dom, achieved=gu_bytes / (kms[dom] * 1e-3) / 1e9, peak=HBM_PEAK_GBS,
                       unit="GB/s", bytes_per_launch=gu_bytes, avg_launch_us=kms[dom] * 1e3,
-                      other_kernels={"sepia_moe_down": dict(bytes_per_launch=dn_bytes, avg_launch_us=kms["sepia_moe_down"] * 1e3,
-                                                            achieved=dn_bytes / (kms["sepia_moe_down"] * 1e-3) / 1e9)}),
+                      other_kernels={"sepia_ffn_down": dict(bytes_per_launch=dn_bytes, avg_launch_us=kms["sepia_ffn_down"] * 1e3,
+                                                           achieved=dn_bytes / (kms["sepia_ffn_down"] * 1e-3) / 1e9)}),
         cpu=dict(s1=s1, n1=n1, sN=sN, nN=nN, threads=nthr))
 
 
@@ -268,9 +277,9 @@ def run_matvec_rotation(B, name, t, rows, cols, warmup, steps, cpu_seconds, seed
         return L.sepia_gpu_matvec_q(t, w, (i % ncopy) * mb, xs[0], y, rows, cols)
 
     ms = B.timed_steps(step, warmup, steps)
-    kname = {12: "sepia_matvec_generic_q4_k", 17: "sepia_matvec_generic_iq2_xs", 18: "sepia_matvec_generic_iq3_xxs",
-             16: "sepia_matvec_generic_iq2_xxs"}[t]
-    kms = B.kernel_ms(step, min(steps, 2 * ncopy), [kname])[kname]
+    tname = {12: "q4_k", 17: "iq2_xs", 18: "iq3_xxs", 16: "iq2_xxs"}[t]
+    cands = ["sepia_mv_%s_j2" % tname, "sepia_mv_%s_j4" % tname, "sepia_matvec_generic_%s" % tname]
+    kname, kms = B.kernel_used(step, min(steps, 2 * ncopy), cands)
     nbytes = mb + cols * 4 + rows * 4
     import oracle
     wh = B.fetch(w, 0, mb)
@@ -327,8 +336,8 @@ def run_c3(B, warmup, steps, cpu_seconds, n_layers=3):
 
     ms = B.timed_steps(step, warmup, steps)
     per_token = (NR + NS) * H * 4 + 6 * (2 * gb + db) + NS * (2 * sgb + sdb)
-    kms = B.kernel_ms(step, min(steps, 60), ["sepia_matvec_f32", "sepia_moe_select", "sepia_moe_gateup",
-                                             "sepia_moe_down"])
+    kms = B.kernel_ms(step, min(steps, 60), ["sepia_matvec_f32", "sepia_moe_select", "sepia_ffn_gateup",
+                                             "sepia_ffn_down"])
 
     # parity at full size: route + output of one token against the oracle
     import oracle

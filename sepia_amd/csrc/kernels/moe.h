@@ -13,17 +13,7 @@
 #pragma once
 #include "common.h"
 #include "matvec.h"
-
-// One projection family: expert e's [rows, cols] quant rows start at
-// base + e * stride; row r at + r * row_bytes; n_blocks blocks per row.
-struct MoeProj {
-    const uint8_t *base;
-    uint64_t stride;
-    uint64_t row_bytes;
-    int64_t n_blocks;
-    int32_t type;
-    int32_t pad;
-};
+#include "mv.h"
 
 struct ArgBest {
     float v;
@@ -112,7 +102,7 @@ __device__ __forceinline__ const uint8_t *moe_row(const MoeProj &P, int64_t e, i
 
 // One wave per (slot, intermediate row); 4 rows per workgroup. sel_idx may be
 // NULL: then slot s < topk is expert fixed_expert + s (a single-expert FFN).
-extern "C" __global__ __launch_bounds__(256) void sepia_moe_gateup(
+extern "C" __global__ __launch_bounds__(256) void sepia_moe_gateup_generic(
     MoeProj gate, MoeProj up, MoeProj s_gate, MoeProj s_up, const int32_t *__restrict__ sel_idx,
     int32_t fixed_expert, int32_t topk, int64_t inter, const float *__restrict__ x, float *__restrict__ h) {
     const int64_t tiles = (inter + 3) / 4;
@@ -132,7 +122,7 @@ extern "C" __global__ __launch_bounds__(256) void sepia_moe_gateup(
 // formed in registers in a fixed order (deterministic, no atomics). With
 // sel_idx NULL the routed slots are experts fixed_expert + s and, with sel_w
 // NULL, every weight is 1.
-extern "C" __global__ __launch_bounds__(256) void sepia_moe_down(
+extern "C" __global__ __launch_bounds__(256) void sepia_moe_down_generic(
     MoeProj down, MoeProj s_down, const int32_t *__restrict__ sel_idx, const float *__restrict__ sel_w,
     int32_t fixed_expert, int32_t topk, int32_t n_shared, int64_t inter, int64_t hidden,
     const float *__restrict__ h, float *__restrict__ y) {

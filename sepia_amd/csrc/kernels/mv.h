@@ -1,197 +1,292 @@
-// mv.h -- split-K tile matvec for quantized rows (decode, batch 1).
+// mv.h -- full-row tile matvec for quantized rows (decode, batch 1).
 //
-// A 256-thread workgroup owns a tile: R = 16 * J rows x one column slice of
-// NBC blocks (NBC * 256 columns). It
-//   1. stages its slice of x in LDS as three int8 digit planes, a power-of-two
-//      scale per block and f32 sums per 16 columns (one wave per block);
-//   2. gives each lane one 64-weight unit of the slice (lane % 16 -> unit,
-//      NBC = 4 gives 16 units per row slice): the lane keeps that unit's x
-//      planes in registers and walks J rows, 4 rows per wave step, so 16
-//      consecutive lanes cover one row and 64 lanes four consecutive rows;
-//   3. sums the 16 lane partials of each row with butterfly shuffles.
-// With KS = n_blocks / NBC > 1 slices, partial row sums go to a scratch array
-// and the last workgroup to finish a row tile (an atomic arrival counter, no
-// waiting) adds the KS partials in slice order -- deterministic, and it
-// leaves the counter at zero for the next launch.
+// A 384-thread workgroup owns S*J whole rows. The row's U = in_dim / 64
+// units (64-weight pieces of a block) are spread over U lanes and each lane
+// keeps its unit's x planes in registers while it walks J rows, S rows per
+// step (S = 384 / U; U must divide 384: 3072, 4096 and 6144 columns give
+// U = 48, 64, 96). Per workgroup:
+//   1. the lane issues the loads of its unit for all J rows;
+//   2. while they are in flight the workgroup stages x in LDS in XP form
+//      (qdot.h) -- or, when x already comes in XP form from the previous
+//      kernel, reads it from there;
+//   3. integer unit dots (qdot.h), a butterfly over the `seg` lanes of the
+//      row that share a wave, then a short LDS sum across waves.
+// Rows never span workgroups, so no workgroup waits for or talks to another.
 #pragma once
 #include "common.h"
 #include "qdot.h"
 
-#define MV_THREADS 256
-#define MV_NBC 4
-#define MV_UC (4 * MV_NBC)           // units per row slice
-#define MV_RW (SEPIA_WAVE / MV_UC)   // rows per wave step
-#define MV_RS (4 * MV_RW)            // rows per workgroup step
+#ifndef MV_NT
+#define MV_NT 384
+#endif
 
-struct __attribute__((aligned(16))) MvLds {
-    int32_t planes[3][MV_NBC * 256 / 4];  // plane k, columns 4i..4i+3 in word i
-    float scale[MV_NBC];
-    float gsum[MV_NBC * 16];
-    uint32_t last;
+struct MvGeo {
+    int32_t U;     // units per row
+    int32_t S;     // rows per step (384 / U)
+    int32_t seg;   // lanes per in-wave partial sum (largest power of two dividing U, <= 64)
+    int32_t pad;
 };
 
-// Stage x[c0 .. c0 + NBC*256) (f32) into LDS. Thread t handles columns 4t..4t+3;
-// wave w covers block w, so the block max is a wave reduction.
-__device__ __forceinline__ void mv_stage_x(const float *__restrict__ x, int64_t c0, MvLds &L) {
-    const int t = threadIdx.x;
-    const float4 v = *(const float4 *)(x + c0 + 4 * t);
-    float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+// LDS carve-up: x planes (3n bytes), scales and sums (n/16 floats each),
+// row partials (S * J * (U / seg) floats), then scratch floats.
+struct MvSmem {
+    int8_t *planes;
+    float *scale, *sum, *red, *extra;
+};
+__device__ __forceinline__ MvSmem mv_smem(uint8_t *base, int64_t n, int rows_red) {
+    MvSmem m;
+    m.planes = (int8_t *)base;
+    m.scale = (float *)(base + 3 * n);
+    m.sum = m.scale + n / 16;
+    m.red = m.sum + n / 16;
+    m.extra = m.red + ((rows_red + 3) & ~3);   // keep extra 16-byte aligned
+    return m;
+}
+
+// x staging is split in two so that x's loads are issued before the weight
+// loads: a wave's loads retire in order, so a wait for x issued after the
+// weights would also wait for every weight. Each thread holds up to MV_XQ
+// quads (n <= 4 * 384 * MV_XQ = 9216 columns).
+#ifndef MV_XQ
+#define MV_XQ 6
+#endif
+struct XQuads {
+    float4 v[MV_XQ];
+};
+
+__device__ __forceinline__ void mv_load_x(const float *__restrict__ x, int64_t n, XQuads &xq) {
+    const float4 *x4 = (const float4 *)x;
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, SEPIA_WAVE));
-    // |x| * inv <= 8355000 < 127 * (65536 + 256 + 1): three balanced int8 digits
-    const float inv = (m > 0.0f) ? 8355000.0f / m : 0.0f;
-    const float vals[4] = {v.x, v.y, v.z, v.w};
-    uint32_t w0 = 0, w1 = 0, w2 = 0;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int32_t q = (int32_t)__builtin_rintf(vals[i] * inv);
-        const int32_t lo = (int32_t)(int8_t)q;       // balanced base-256 digits
-        const int32_t r1 = (q - lo) >> 8;
-        const int32_t mid = (int32_t)(int8_t)r1;
-        const int32_t hi = (r1 - mid) >> 8;
-        w0 |= ((uint32_t)hi & 0xFFu) << (8 * i);
-        w1 |= ((uint32_t)mid & 0xFFu) << (8 * i);
-        w2 |= ((uint32_t)lo & 0xFFu) << (8 * i);
+    for (int p = 0; p < MV_XQ; p++) {
+        const int64_t q = threadIdx.x + (int64_t)p * MV_NT;
+        xq.v[p] = q < n / 4 ? x4[q] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
-    L.planes[0][t] = (int32_t)w0;
-    L.planes[1][t] = (int32_t)w1;
-    L.planes[2][t] = (int32_t)w2;
-    float s = (v.x + v.y) + (v.z + v.w);
-    s += __shfl_xor(s, 1, SEPIA_WAVE);
-    s += __shfl_xor(s, 2, SEPIA_WAVE);
-    if ((t & 3) == 0) L.gsum[t >> 2] = s;
-    if ((t & 63) == 0) L.scale[t >> 6] = (m > 0.0f) ? 1.0f / inv : 0.0f;
 }
 
-template <int T>
-__device__ __forceinline__ void mv_load_xu(const MvLds &L, int unit, XU &X) {
-    const int bl = unit >> 2, k = unit & 3;
+// The loaded quads -> XP in LDS (n a multiple of 16, so each 4-lane segment
+// group is entirely inside or outside the vector).
+__device__ __forceinline__ void mv_stage_x(const XQuads &xq, int64_t n, const MvSmem &m) {
 #pragma unroll
-    for (int s = 0; s < 4; s++) {
-        const int col = 256 * bl + QU<T>::seg_col(k, s);
-#pragma unroll
-        for (int p = 0; p < 3; p++) {
-            const int4 v = *(const int4 *)&L.planes[p][col >> 2];
-            X.p[p][4 * s + 0] = v.x;
-            X.p[p][4 * s + 1] = v.y;
-            X.p[p][4 * s + 2] = v.z;
-            X.p[p][4 * s + 3] = v.w;
-        }
-        X.gsum[s] = L.gsum[col >> 4];
+    for (int p = 0; p < MV_XQ; p++) {
+        const int64_t q = threadIdx.x + (int64_t)p * MV_NT;
+        if (q < n / 4) xp_quad(xq.v[p], q, m.planes, m.scale, m.sum, n);
     }
-    X.xs = L.scale[bl];
 }
 
-// Row handled by this thread at step j of a tile starting at r0.
-__device__ __forceinline__ int64_t mv_row(int64_t r0, int j) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    return r0 + (int64_t)j * MV_RS + wave * MV_RW + lane / MV_UC;
-}
-
-// Issue the loads of this thread's unit for J rows of matrix W (rows x
-// n_blocks blocks, row stride row_bytes) in column slice ks. Rows past `rows`
-// read row rows-1 (in bounds) and are discarded by the caller. Loads are
-// issued before x is staged so their latency overlaps the staging.
 template <int T, int J>
 __device__ __forceinline__ void mv_issue(const uint8_t *__restrict__ W, uint64_t row_bytes, int64_t rows,
-                                         int64_t r0, int ks, typename QU<T>::Data (&d)[J]) {
-    const int unit = threadIdx.x & (MV_UC - 1);
-    const int bl = unit >> 2, k = unit & 3;
-    const uint64_t col_off = (uint64_t)(ks * MV_NBC + bl) * QU<T>::bytes;
+                                         int64_t r0, const MvGeo &g, typename QU<T>::Data (&d)[J]) {
+    const int t = threadIdx.x, u = t % g.U, s = t / g.U;
+    const uint64_t col_off = (uint64_t)(u >> 2) * QU<T>::bytes;
 #pragma unroll
     for (int j = 0; j < J; j++) {
-        int64_t r = mv_row(r0, j);
+        int64_t r = r0 + (int64_t)j * g.S + s;
         r = r < rows ? r : rows - 1;
-        d[j] = QU<T>::load(W + (uint64_t)r * row_bytes + col_off, k);
+        d[j] = QU<T>::load(W + (uint64_t)r * row_bytes + col_off, u & 3);
     }
 }
 
-// Row sums of the issued units: each 16-lane group adds its unit partials.
+// Unit dots of J rows, summed over the row's lanes within each wave; the
+// first lane of each `seg` group stores its partial at red[(j*S + s) * nseg + u/seg].
 template <int T, int J>
-__device__ __forceinline__ void mv_finish(const typename QU<T>::Data (&d)[J], const XU &X, float (&acc)[J]) {
-    const int k = threadIdx.x & 3;
+__device__ __forceinline__ void mv_partials(const typename QU<T>::Data (&d)[J], const XU &X, const MvGeo &g,
+                                            float *red) {
+    const int t = threadIdx.x, u = t % g.U, s = t / g.U;
+    const int nseg = g.U / g.seg;
 #pragma unroll
     for (int j = 0; j < J; j++) {
-        float a = QU<T>::dot(d[j], k, X);
+        float a = QU<T>::dot(d[j], u & 3, X);
 #pragma unroll
-        for (int off = MV_UC / 2; off >= 1; off >>= 1) a += __shfl_xor(a, off, SEPIA_WAVE);
-        acc[j] = a;
+        for (int off = 32; off >= 1; off >>= 1)
+            if (off < g.seg) a += __shfl_xor(a, off, SEPIA_WAVE);
+        if ((u & (g.seg - 1)) == 0) red[(j * g.S + s) * nseg + u / g.seg] = a;
     }
 }
 
-// Partial sums cross workgroups (and XCDs, whose L2s are not coherent with
-// each other) as agent-scope atomic stores and loads, which go to the
-// coherent level directly; no L2 writeback or invalidate is needed.
-__device__ __forceinline__ void part_store(float *p, float v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float part_load(const float *p) {
-    return __hip_atomic_load((float *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// Row rr (0 <= rr < S*J) of the tile from the partials.
+__device__ __forceinline__ float mv_row_sum(const float *red, int rr, const MvGeo &g) {
+    const int nseg = g.U / g.seg;
+    float s = 0.0f;
+    for (int i = 0; i < nseg; i++) s += red[rr * nseg + i];
+    return s;
 }
 
-// After every thread stored its partials with part_store: returns true in the
-// workgroup that arrives last at counter *cnt (of `expect` arrivals), which
-// then resets the counter. Each wave waits for its stores to be acknowledged
-// (vmcnt 0) before the barrier, so every partial is in place before the
-// workgroup's arrival is counted; nothing ever waits on another workgroup.
-__device__ __forceinline__ bool mv_last_arrival(uint32_t *cnt, uint32_t expect, MvLds &L) {
-    __builtin_amdgcn_s_waitcnt(0x0F70);   // gfx9 encoding: vmcnt(0), expcnt/lgkmcnt untouched
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const uint32_t old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const uint32_t last = (old == expect - 1) ? 1u : 0u;
-        if (last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        L.last = last;
-    }
-    __syncthreads();
-    return L.last != 0;
-}
-
-// y = W x for one quantized matrix. grid = n_tiles * KS; tile = blockIdx / KS.
+// y = W x for one quantized matrix; grid = ceil(rows / (S*J)).
 template <int T, int J>
-__device__ __forceinline__ void mv_kernel_body(const uint8_t *__restrict__ W, uint64_t row_bytes, int64_t rows,
-                                               int32_t n_ks, const float *__restrict__ x, float *__restrict__ y,
-                                               float *__restrict__ part, uint32_t *__restrict__ cnt) {
-    __shared__ MvLds L;
-    const int64_t tile = blockIdx.x / n_ks;
-    const int ks = (int)(blockIdx.x % n_ks);
-    const int64_t r0 = tile * (MV_RS * J);
+__device__ __forceinline__ void mv_full_body(const uint8_t *__restrict__ W, uint64_t row_bytes, int64_t rows,
+                                             int64_t n, MvGeo g, const float *__restrict__ x,
+                                             float *__restrict__ y) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const MvSmem m = mv_smem(smem, n, g.S * J * (g.U / g.seg));
+    const int64_t r0 = (int64_t)blockIdx.x * g.S * J;
+    XQuads xq;
+    mv_load_x(x, n, xq);
     typename QU<T>::Data d[J];
-    mv_issue<T, J>(W, row_bytes, rows, r0, ks, d);
-    mv_stage_x(x, (int64_t)ks * MV_NBC * 256, L);
+    mv_issue<T, J>(W, row_bytes, rows, r0, g, d);
+    mv_stage_x(xq, n, m);
     __syncthreads();
     XU X;
-    mv_load_xu<T>(L, threadIdx.x & (MV_UC - 1), X);
-    float acc[J];
-    mv_finish<T, J>(d, X, acc);
-    const bool writer = (threadIdx.x & (MV_UC - 1)) == 0;
-    if (n_ks == 1) {
-#pragma unroll
-        for (int j = 0; j < J; j++) {
-            const int64_t r = mv_row(r0, j);
-            if (writer && r < rows) y[r] = acc[j];
-        }
-        return;
-    }
-#pragma unroll
-    for (int j = 0; j < J; j++) {
-        const int64_t r = mv_row(r0, j);
-        if (writer && r < rows) part_store(&part[(int64_t)ks * rows + r], acc[j]);
-    }
-    if (!mv_last_arrival(&cnt[tile], (uint32_t)n_ks, L)) return;
-    for (int i = threadIdx.x; i < MV_RS * J; i += MV_THREADS) {
-        const int64_t r = r0 + i;
-        if (r >= rows) break;
-        float s = 0.0f;
-        for (int p = 0; p < n_ks; p++) s += part_load(&part[(int64_t)p * rows + r]);
-        y[r] = s;
-    }
+    const int u = threadIdx.x % g.U;
+    load_xu<T>(XPView{m.planes, m.scale, m.sum, n}, u >> 2, u & 3, X);
+    mv_partials<T, J>(d, X, g, m.red);
+    __syncthreads();
+    const int rr = threadIdx.x;
+    if (rr < g.S * J && r0 + rr < rows) y[r0 + rr] = mv_row_sum(m.red, rr, g);
 }
 
 #define SEPIA_MV_KERNEL(name, T, J)                                                                 \
-    extern "C" __global__ __launch_bounds__(MV_THREADS) void sepia_mv_##name##_j##J(              \
-        const uint8_t *__restrict__ W, uint64_t row_bytes, int64_t rows, int32_t n_ks,            \
-        const float *__restrict__ x, float *__restrict__ y, float *__restrict__ part,             \
-        uint32_t *__restrict__ cnt) {                                                             \
-        mv_kernel_body<T, J>(W, row_bytes, rows, n_ks, x, y, part, cnt);                          \
+    extern "C" __global__ __launch_bounds__(MV_NT) void sepia_mv_##name##_j##J(                   \
+        const uint8_t *__restrict__ W, uint64_t row_bytes, int64_t rows, int64_t n, MvGeo g,      \
+        const float *__restrict__ x, float *__restrict__ y) {                                     \
+        mv_full_body<T, J>(W, row_bytes, rows, n, g, x, y);                                       \
     }
+
+// ------------------------------------------------------------------ FFN ---
+// One projection family of a stack of experts: expert e's quant rows start
+// at base + e * stride, row r at + r * row_bytes.
+struct MoeProj {
+    const uint8_t *base;
+    uint64_t stride;
+    uint64_t row_bytes;
+    int64_t n_blocks;
+    int32_t type;
+    int32_t pad;
+};
+
+// Per-slot XP arrays of the SwiGLU activations h (inter columns each).
+struct HxpArgs {
+    int8_t *planes;   // [slot][3][inter]
+    float *scale;     // [slot][inter / 16]
+    float *sum;       // [slot][inter / 16]
+};
+
+__device__ __forceinline__ int64_t slot_expert(const int32_t *sel_idx, int32_t fixed, int32_t slot, int32_t topk) {
+    return slot < topk ? (sel_idx ? (int64_t)sel_idx[slot] : (int64_t)fixed + slot) : (int64_t)(slot - topk);
+}
+
+// h[slot, i] = silu(gate_i . x) * (up_i . x) for S*J rows i of one slot; h is
+// written in XP form (S*J is a multiple of 16, so the tile holds whole
+// segments) and, if h32 is set, as f32.
+template <int T, int J>
+__device__ __forceinline__ void ffn_gateup_tile(const MoeProj &G, const MoeProj &Up, int64_t e, int64_t inter,
+                                                int64_t hidden, MvGeo g, int32_t slot, int64_t r0,
+                                                const float *__restrict__ x, const HxpArgs &hx,
+                                                float *__restrict__ h32, const MvSmem &m) {
+    const uint8_t *wg = G.base + e * G.stride, *wu = Up.base + e * Up.stride;
+    XQuads xq;
+    mv_load_x(x, hidden, xq);
+    typename QU<T>::Data dg[J], du[J];
+    mv_issue<T, J>(wg, G.row_bytes, inter, r0, g, dg);
+    mv_issue<T, J>(wu, Up.row_bytes, inter, r0, g, du);
+    mv_stage_x(xq, hidden, m);
+    __syncthreads();
+    XU X;
+    const int u = threadIdx.x % g.U;
+    load_xu<T>(XPView{m.planes, m.scale, m.sum, hidden}, u >> 2, u & 3, X);
+    const int nred = g.S * J * (g.U / g.seg);
+    mv_partials<T, J>(dg, X, g, m.red);
+    mv_partials<T, J>(du, X, g, m.red + nred);
+    __syncthreads();
+    const int rr = threadIdx.x;
+    float *hv = m.extra;                                   // S*J activations of this tile
+    if (rr < g.S * J) {
+        const float gv = mv_row_sum(m.red, rr, g);
+        const float uv = mv_row_sum(m.red + nred, rr, g);
+        const float hval = (r0 + rr < inter) ? silu_f32(gv) * uv : 0.0f;
+        hv[rr] = hval;
+        if (h32 && r0 + rr < inter) h32[(int64_t)slot * inter + r0 + rr] = hval;
+    }
+    __syncthreads();
+    const int q = threadIdx.x;                             // one quad of h per thread
+    if (q < g.S * J / 4 && r0 + 4 * q < inter) {
+        const float4 v = *(const float4 *)&hv[4 * q];
+        xp_quad(v, r0 / 4 + q, hx.planes + (int64_t)slot * 3 * inter, hx.scale + (int64_t)slot * (inter / 16),
+                hx.sum + (int64_t)slot * (inter / 16), inter);
+    }
+}
+
+// grid = n_slots * ceil(inter / (S*J)). Routed slots (< topk) take their
+// expert from sel_idx (or fixed_expert + slot); later slots are the shared
+// experts. Workgroups with blockIdx < zero_blocks also clear y_zero[0..y_n).
+extern "C" __global__ __launch_bounds__(MV_NT) void sepia_ffn_gateup(
+    MoeProj gate, MoeProj up, MoeProj s_gate, MoeProj s_up, const int32_t *__restrict__ sel_idx,
+    int32_t fixed_expert, int32_t topk, int64_t inter, int64_t hidden, MvGeo g, int32_t J,
+    const float *__restrict__ x, HxpArgs hx, float *__restrict__ h32, float *__restrict__ y_zero, int64_t y_n) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    if (y_zero) {
+        for (int64_t i = (int64_t)blockIdx.x * MV_NT + threadIdx.x; i < y_n; i += (int64_t)gridDim.x * MV_NT)
+            y_zero[i] = 0.0f;
+    }
+    const int64_t rows_per = (int64_t)g.S * J;
+    const int64_t tiles = (inter + rows_per - 1) / rows_per;
+    const int32_t slot = (int32_t)(blockIdx.x / tiles);
+    const int64_t r0 = (blockIdx.x % tiles) * rows_per;
+    const bool routed = slot < topk;
+    const MoeProj &G = routed ? gate : s_gate;
+    const MoeProj &U = routed ? up : s_up;
+    const int64_t e = slot_expert(sel_idx, fixed_expert, slot, topk);
+    // the red area holds the gate and the up partials; extra follows both
+    const MvSmem mm = mv_smem(smem, hidden, 2 * g.S * J * (g.U / g.seg));
+#define GU_CASE(TT, JJ)                                                                          \
+    if (G.type == TT && J == JJ) {                                                               \
+        ffn_gateup_tile<TT, JJ>(G, U, e, inter, hidden, g, slot, r0, x, hx, h32, mm);            \
+        return;                                                                                  \
+    }
+    GU_CASE(ST_Q2_K, 2) GU_CASE(ST_Q2_K, 4) GU_CASE(ST_Q3_K, 2) GU_CASE(ST_Q3_K, 4)
+    GU_CASE(ST_Q4_K, 2) GU_CASE(ST_Q4_K, 4)
+#undef GU_CASE
+}
+
+// y[d] (+)= w_slot * (down_slot[d, :] . h_slot) for S*J rows d of one slot,
+// with h_slot read in XP form from global memory.
+template <int T, int J>
+__device__ __forceinline__ void ffn_down_tile(const MoeProj &P, int64_t e, int64_t inter, int64_t hidden, MvGeo g,
+                                              int32_t slot, int64_t r0, const HxpArgs &hx, float w,
+                                              float *__restrict__ y, bool accumulate, const MvSmem &m) {
+    typename QU<T>::Data d[J];
+    mv_issue<T, J>(P.base + e * P.stride, P.row_bytes, hidden, r0, g, d);
+    XU X;
+    const int u = threadIdx.x % g.U;
+    const XPView xv{hx.planes + (int64_t)slot * 3 * inter, hx.scale + (int64_t)slot * (inter / 16),
+                    hx.sum + (int64_t)slot * (inter / 16), inter};
+    load_xu<T>(xv, u >> 2, u & 3, X);
+    mv_partials<T, J>(d, X, g, m.red);
+    __syncthreads();
+    const int rr = threadIdx.x;
+    if (rr < g.S * J && r0 + rr < hidden) {
+        const float v = mv_row_sum(m.red, rr, g);
+        if (accumulate)
+            atomicAdd(&y[r0 + rr], w * v);
+        else
+            y[r0 + rr] = w * v;
+    }
+}
+
+// grid = n_slots * ceil(hidden / (S*J)). With one slot and no weights y is
+// stored; otherwise every slot adds w_slot * its rows into y (cleared by
+// sepia_ffn_gateup), the routed weights then the shared gammas of sel_w.
+extern "C" __global__ __launch_bounds__(MV_NT) void sepia_ffn_down(
+    MoeProj down, MoeProj s_down, const int32_t *__restrict__ sel_idx, const float *__restrict__ sel_w,
+    int32_t fixed_expert, int32_t topk, int32_t n_slots, int64_t inter, int64_t hidden, MvGeo g, int32_t J,
+    HxpArgs hx, float *__restrict__ y) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int64_t rows_per = (int64_t)g.S * J;
+    const int64_t tiles = (hidden + rows_per - 1) / rows_per;
+    const int32_t slot = (int32_t)(blockIdx.x / tiles);
+    const int64_t r0 = (blockIdx.x % tiles) * rows_per;
+    const bool routed = slot < topk;
+    const MoeProj &P = routed ? down : s_down;
+    const int64_t e = slot_expert(sel_idx, fixed_expert, slot, topk);
+    const float w = sel_w ? sel_w[slot] : 1.0f;
+    const bool accumulate = n_slots > 1;
+    MvSmem m;
+    m.red = (float *)smem;
+#define DN_CASE(TT, JJ)                                                                          \
+    if (P.type == TT && J == JJ) {                                                               \
+        ffn_down_tile<TT, JJ>(P, e, inter, hidden, g, slot, r0, hx, w, y, accumulate, m);        \
+        return;                                                                                  \
+    }
+    DN_CASE(ST_Q2_K, 2) DN_CASE(ST_Q2_K, 4) DN_CASE(ST_Q3_K, 2) DN_CASE(ST_Q3_K, 4)
+    DN_CASE(ST_Q4_K, 2) DN_CASE(ST_Q4_K, 4)
+#undef DN_CASE
+}

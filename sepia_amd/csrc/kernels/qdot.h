@@ -1,14 +1,18 @@
 // qdot.h -- integer dot products of quantized 64-weight units with x.
 //
-// x is staged per workgroup as three signed int8 digit planes: within each
-// 256-column block, x[c] ~= xs * (p0 * 65536 + p1 * 256 + p2), with
-// xs = max|x| / 8355000 so that the digits stay within int8. The rounding
-// error is below 6e-8 of the block's largest |x| -- far inside
-// the 1e-4 * ||y||_inf bar (16-bit planes are not: up to 7e-5 measured on
-// these formats) -- and the weight side is exact integers, so each unit's dot
-// is formed exactly with v_dot4_i32_i8 (4 weights x 1 plane per instruction)
-// and scaled once. The K-quant "min" terms use the exact f32 sums of x over
-// 16-column groups, also staged per block.
+// x is carried as "x planes" (XP): per 16-column segment, a scale xs and three
+// signed int8 digit planes with x[c] ~= xs * (p0 * 65536 + p1 * 256 + p2),
+// xs = max|x over the segment| / 8355000 so the digits stay within int8. The
+// rounding error is below 6e-8 of the segment's largest |x|, far inside the
+// 1e-4 * ||y||_inf bar (16-bit planes are not: up to 7e-5 measured on these
+// formats). Each segment also carries its exact f32 sum, used by the
+// K-quant "min" and "-4" terms. The weight side is exact integers, so a
+// segment's dot is formed exactly with v_dot4_i32_i8 (4 weights x 1 plane per
+// instruction) and scaled once.
+//
+// XP memory layout for a vector of n columns (n a multiple of 16), in global
+// memory or LDS: int8 planes[3][n] (plane-major), float scale[n / 16],
+// float sum[n / 16].
 //
 // A unit is 64 weights of one block that the format stores together; its
 // columns are four 16-column segments (seg_col). Each decoder loads a unit's
@@ -19,8 +23,15 @@
 
 struct XU {
     int32_t p[3][16];  // plane k, word 4*seg + w = columns seg_col(seg) + 4w .. + 3 (byte j = column +j)
+    float xs[4];       // segment scales
     float gsum[4];     // f32 sum of x over each segment
-    float xs;          // block scale
+};
+
+struct XPView {
+    const int8_t *planes;  // [3][n]
+    const float *scale;    // [n / 16]
+    const float *sum;      // [n / 16]
+    int64_t n;
 };
 
 __device__ __forceinline__ int32_t sdot4(int32_t a, int32_t b, int32_t c) {
@@ -41,18 +52,13 @@ __device__ __forceinline__ uint4 ld128_a2(const uint8_t *p) {
     return make_uint4(__builtin_amdgcn_alignbyte(a.y, a.x, sh), __builtin_amdgcn_alignbyte(a.z, a.y, sh),
                       __builtin_amdgcn_alignbyte(a.w, a.z, sh), __builtin_amdgcn_alignbyte(e, a.w, sh));
 }
-__device__ __forceinline__ uint32_t ld32_a2(const uint8_t *p) {
-    const uint8_t *b = (const uint8_t *)((uintptr_t)p & ~(uintptr_t)3);
-    const uint32_t sh = (uint32_t)((uintptr_t)p & 3);
-    return __builtin_amdgcn_alignbyte(*(const uint32_t *)(b + 4), *(const uint32_t *)b, sh);
-}
 
 __device__ __forceinline__ float half_lo(uint32_t v) { return f16_bits_to_f32(v & 0xFFFFu); }
 __device__ __forceinline__ float half_hi(uint32_t v) { return f16_bits_to_f32(v >> 16); }
 
-// Combine the three plane sums into f32: T0 * 65536 + T1 * 256 + T2.
-__device__ __forceinline__ float planes_f(int32_t t0, int32_t t1, int32_t t2) {
-    return __builtin_fmaf((float)t0, 65536.0f, __builtin_fmaf((float)t1, 256.0f, (float)t2));
+// xs * (a0 * 65536 + a1 * 256 + a2): one segment's dot in f32.
+__device__ __forceinline__ float seg_f(int32_t a0, int32_t a1, int32_t a2, float xs) {
+    return xs * __builtin_fmaf((float)a0, 65536.0f, __builtin_fmaf((float)a1, 256.0f, (float)a2));
 }
 
 template <int T> struct QU;
@@ -64,6 +70,7 @@ template <int T> struct QU;
 // (min << 4 | scale). Segment s = those 16 weights.
 template <> struct QU<ST_Q2_K> {
     static constexpr int bytes = 84;
+    static constexpr int align = 4;
     struct Data { uint4 q; uint2 sc; uint32_t dd; };
     __device__ static int seg_col(int k, int s) { return 128 * (k >> 1) + 32 * s + 16 * (k & 1); }
     __device__ static Data load(const uint8_t *blk, int k) {
@@ -76,8 +83,7 @@ template <> struct QU<ST_Q2_K> {
     __device__ static float dot(const Data &r, int k, const XU &x) {
         const int g = k & 1;
         const uint32_t qw[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
-        int32_t t0 = 0, t1 = 0, t2 = 0;
-        float mn = 0.0f;
+        float acc = 0.0f, mn = 0.0f;
 #pragma unroll
         for (int s = 0; s < 4; s++) {
             int32_t a0 = 0, a1 = 0, a2 = 0;
@@ -90,14 +96,10 @@ template <> struct QU<ST_Q2_K> {
             }
             const int bi = 2 * s + g;                                  // byte in r.sc
             const uint32_t scb = ((bi < 4 ? r.sc.x : r.sc.y) >> (8 * (bi & 3))) & 0xFFu;
-            const int32_t sc = (int32_t)(scb & 15u);
-            t0 += __mul24(sc, a0);
-            t1 += __mul24(sc, a1);
-            t2 += __mul24(sc, a2);
+            acc = __builtin_fmaf((float)(scb & 15u), seg_f(a0, a1, a2, x.xs[s]), acc);
             mn = __builtin_fmaf((float)(scb >> 4), x.gsum[s], mn);
         }
-        const float d = half_lo(r.dd), dmin = half_hi(r.dd);
-        return __builtin_fmaf(d * x.xs, planes_f(t0, t1, t2), -(dmin * mn));
+        return __builtin_fmaf(half_lo(r.dd), acc, -(half_hi(r.dd) * mn));
     }
 };
 
@@ -110,6 +112,7 @@ template <> struct QU<ST_Q2_K> {
 // high nibble, top two bits from byte 8 + j % 4 at shift 2 * (j / 4).
 template <> struct QU<ST_Q3_K> {
     static constexpr int bytes = 110;
+    static constexpr int align = 2;
     struct Data { uint4 q, hm; uint32_t s0, s1, s2, d; };
     __device__ static int seg_col(int k, int s) { return 128 * (k >> 1) + 32 * s + 16 * (k & 1); }
     __device__ static Data load(const uint8_t *blk, int k) {
@@ -127,8 +130,7 @@ template <> struct QU<ST_Q3_K> {
         const int h = k >> 1, g = k & 1;
         const uint32_t qw[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
         const uint32_t hw[4] = {r.hm.x, r.hm.y, r.hm.z, r.hm.w};
-        int32_t t0 = 0, t1 = 0, t2 = 0;
-        float sx = 0.0f;
+        float acc = 0.0f;
 #pragma unroll
         for (int s = 0; s < 4; s++) {
             int32_t a0 = 0, a1 = 0, a2 = 0;
@@ -146,15 +148,11 @@ template <> struct QU<ST_Q3_K> {
             const uint32_t lob = ((jb < 4 ? r.s0 : r.s1) >> (8 * (jb & 3))) & 0xFFu;
             const uint32_t nib = (j < 8) ? (lob & 15u) : (lob >> 4);
             const uint32_t top = (r.s2 >> (8 * (j & 3) + 2 * (j >> 2))) & 3u;
-            const int32_t sc = (int32_t)(nib | (top << 4)) - 32;
-            t0 += __mul24(sc, a0);
-            t1 += __mul24(sc, a1);
-            t2 += __mul24(sc, a2);
-            sx = __builtin_fmaf((float)sc, x.gsum[s], sx);
+            const float sc = (float)((int32_t)(nib | (top << 4)) - 32);
+            // sum over the group of (q + 4) x - 4 x
+            acc = __builtin_fmaf(sc, __builtin_fmaf(-4.0f, x.gsum[s], seg_f(a0, a1, a2, x.xs[s])), acc);
         }
-        const float d = half_lo(r.d);
-        // sum (q + 4) x - 4 sum x, per group scale
-        return d * __builtin_fmaf(x.xs, planes_f(t0, t1, t2), -4.0f * sx);
+        return half_lo(r.d) * acc;
     }
 };
 
@@ -164,6 +162,7 @@ template <> struct QU<ST_Q3_K> {
 // high nibbles sub-block 2k+1 (64k+32..64k+63); y = d*sc*q - dmin*m.
 template <> struct QU<ST_Q4_K> {
     static constexpr int bytes = 144;
+    static constexpr int align = 4;
     struct Data { uint4 qa, qb; uint32_t s0, s1, s2, dd; };
     __device__ static int seg_col(int k, int s) { return 64 * k + 16 * s; }
     __device__ static Data load(const uint8_t *blk, int k) {
@@ -177,41 +176,98 @@ template <> struct QU<ST_Q4_K> {
         r.s2 = h.w;
         return r;
     }
-    // 6-bit (scale, min) of sub-block j from the packed bytes s[0..11].
-    __device__ static void scale_min(const Data &r, int j, int32_t &sc, int32_t &mn) {
+    // 6-bit (scale, min) of sub-block j from the packed bytes s[0..11]
+    // (reference src/quants.c:115-121).
+    __device__ static void scale_min(const Data &r, int j, uint32_t &sc, uint32_t &mn) {
         const uint32_t b[3] = {r.s0, r.s1, r.s2};
         auto byte = [&](int i) -> uint32_t { return (b[i >> 2] >> (8 * (i & 3))) & 0xFFu; };
         if (j < 4) {
-            sc = (int32_t)(byte(j) & 63u);
-            mn = (int32_t)(byte(j + 4) & 63u);
+            sc = byte(j) & 63u;
+            mn = byte(j + 4) & 63u;
         } else {
-            sc = (int32_t)((byte(j + 4) & 15u) | ((byte(j - 4) >> 6) << 4));
-            mn = (int32_t)((byte(j + 4) >> 4) | ((byte(j) >> 6) << 4));
+            sc = (byte(j + 4) & 15u) | ((byte(j - 4) >> 6) << 4);
+            mn = (byte(j + 4) >> 4) | ((byte(j) >> 6) << 4);
         }
     }
     __device__ static float dot(const Data &r, int k, const XU &x) {
         const uint32_t qw[8] = {r.qa.x, r.qa.y, r.qa.z, r.qa.w, r.qb.x, r.qb.y, r.qb.z, r.qb.w};
-        int32_t t0 = 0, t1 = 0, t2 = 0;
-        float mn_acc = 0.0f;
+        float acc = 0.0f, mn_acc = 0.0f;
 #pragma unroll
         for (int half = 0; half < 2; half++) {
-            int32_t a0 = 0, a1 = 0, a2 = 0;
+            float sub = 0.0f;
 #pragma unroll
-            for (int w = 0; w < 8; w++) {
-                const int32_t v = (int32_t)((qw[w] >> (4 * half)) & 0x0F0F0F0Fu);
-                // sub-block half covers segments 2*half, 2*half+1: word w -> segment 2*half + w/4
-                a0 = sdot4(v, x.p[0][8 * half + w], a0);
-                a1 = sdot4(v, x.p[1][8 * half + w], a1);
-                a2 = sdot4(v, x.p[2][8 * half + w], a2);
+            for (int sg = 0; sg < 2; sg++) {       // the two segments of the sub-block
+                int32_t a0 = 0, a1 = 0, a2 = 0;
+#pragma unroll
+                for (int w = 0; w < 4; w++) {
+                    const int32_t v = (int32_t)((qw[4 * sg + w] >> (4 * half)) & 0x0F0F0F0Fu);
+                    const int xi = 8 * half + 4 * sg + w;
+                    a0 = sdot4(v, x.p[0][xi], a0);
+                    a1 = sdot4(v, x.p[1][xi], a1);
+                    a2 = sdot4(v, x.p[2][xi], a2);
+                }
+                sub += seg_f(a0, a1, a2, x.xs[2 * half + sg]);
             }
-            int32_t sc, mn;
+            uint32_t sc, mn;
             scale_min(r, 2 * k + half, sc, mn);
-            t0 += __mul24(sc, a0);
-            t1 += __mul24(sc, a1);
-            t2 += __mul24(sc, a2);
+            acc = __builtin_fmaf((float)sc, sub, acc);
             mn_acc = __builtin_fmaf((float)mn, x.gsum[2 * half] + x.gsum[2 * half + 1], mn_acc);
         }
-        const float d = half_lo(r.dd), dmin = half_hi(r.dd);
-        return __builtin_fmaf(d * x.xs, planes_f(t0, t1, t2), -(dmin * mn_acc));
+        return __builtin_fmaf(half_lo(r.dd), acc, -(half_hi(r.dd) * mn_acc));
     }
 };
+
+// Load a unit's x planes (its four segments) from an XP array.
+template <int T>
+__device__ __forceinline__ void load_xu(const XPView &xp, int64_t block, int k, XU &X) {
+#pragma unroll
+    for (int s = 0; s < 4; s++) {
+        const int64_t col = 256 * block + QU<T>::seg_col(k, s);
+#pragma unroll
+        for (int p = 0; p < 3; p++) {
+            const int4 v = *(const int4 *)(xp.planes + p * xp.n + col);
+            X.p[p][4 * s + 0] = v.x;
+            X.p[p][4 * s + 1] = v.y;
+            X.p[p][4 * s + 2] = v.z;
+            X.p[p][4 * s + 3] = v.w;
+        }
+        X.xs[s] = xp.scale[col >> 4];
+        X.gsum[s] = xp.sum[col >> 4];
+    }
+}
+
+// Convert 4 consecutive values (one quad; 4 quads = one segment, held by 4
+// consecutive lanes) to XP form: the lanes of a segment agree on its scale
+// through two shuffles. Writes plane bytes at columns 4q .. 4q+3 and, from
+// the segment's first lane, its scale and sum.
+__device__ __forceinline__ void xp_quad(float4 v, int64_t q, int8_t *planes, float *scale, float *sum, int64_t n) {
+    float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    m = fmaxf(m, __shfl_xor(m, 1, SEPIA_WAVE));
+    m = fmaxf(m, __shfl_xor(m, 2, SEPIA_WAVE));
+    // |x| * inv <= 8355000 (1 + 2^-22) < 127 * (65536 + 256 + 1): three balanced
+    // int8 digits. inv * scale = rcp(m) * m is 1 within 2^-22, so x ~= scale * q.
+    const float inv = (m > 0.0f) ? 8355000.0f * __builtin_amdgcn_rcpf(m) : 0.0f;
+    const float vals[4] = {v.x, v.y, v.z, v.w};
+    uint32_t w0 = 0, w1 = 0, w2 = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int32_t qv = (int32_t)__builtin_rintf(vals[i] * inv);
+        const int32_t lo = (int32_t)(int8_t)qv;      // balanced base-256 digits
+        const int32_t r1 = (qv - lo) >> 8;
+        const int32_t mid = (int32_t)(int8_t)r1;
+        const int32_t hi = (r1 - mid) >> 8;
+        w0 |= ((uint32_t)hi & 0xFFu) << (8 * i);
+        w1 |= ((uint32_t)mid & 0xFFu) << (8 * i);
+        w2 |= ((uint32_t)lo & 0xFFu) << (8 * i);
+    }
+    *(uint32_t *)(planes + 4 * q) = w0;
+    *(uint32_t *)(planes + n + 4 * q) = w1;
+    *(uint32_t *)(planes + 2 * n + 4 * q) = w2;
+    float s = (v.x + v.y) + (v.z + v.w);
+    s += __shfl_xor(s, 1, SEPIA_WAVE);
+    s += __shfl_xor(s, 2, SEPIA_WAVE);
+    if ((q & 3) == 0) {
+        scale[q >> 2] = m * (1.0f / 8355000.0f);
+        sum[q >> 2] = s;
+    }
+}

@@ -43,6 +43,7 @@ enum {
     K_MATVEC_F32, K_SILU_MUL, K_ADD, K_SCALE, K_COPY, K_TOUCH, K_RMSNORM, K_SOFTMAX,
     K_SCONV, K_SCONV_HIST, K_MOE_SELECT, K_MOE_GATEUP, K_MOE_DOWN, K_SYNTH_FILL, K_SYNTH_F16,
     K_MV_Q2_K_J2, K_MV_Q2_K_J4, K_MV_Q3_K_J2, K_MV_Q3_K_J4, K_MV_Q4_K_J2, K_MV_Q4_K_J4,
+    K_FFN_GATEUP, K_FFN_DOWN,
     K_COUNT
 };
 static const char *const k_names[K_COUNT] = {
@@ -56,10 +57,11 @@ static const char *const k_names[K_COUNT] = {
     "sepia_matvec_generic_iq4_xs",
     "sepia_matvec_f32", "sepia_silu_mul_f32", "sepia_add_f32", "sepia_scale_f32", "sepia_copy_f32",
     "sepia_touch_f32", "sepia_rmsnorm_f32", "sepia_softmax_f32", "sepia_sconv_f32",
-    "sepia_sconv_hist_roll_f32", "sepia_moe_select", "sepia_moe_gateup", "sepia_moe_down",
+    "sepia_sconv_hist_roll_f32", "sepia_moe_select", "sepia_moe_gateup_generic", "sepia_moe_down_generic",
     "sepia_synth_fill", "sepia_synth_patch_f16",
     "sepia_mv_q2_k_j2", "sepia_mv_q2_k_j4", "sepia_mv_q3_k_j2", "sepia_mv_q3_k_j4",
     "sepia_mv_q4_k_j2", "sepia_mv_q4_k_j4",
+    "sepia_ffn_gateup", "sepia_ffn_down",
 };
 
 /* GGUF block geometry (reference src/quants.c:46-51; tools/gguf_inspect.py:109-117). */
@@ -87,10 +89,26 @@ static const TypeInfo k_types[] = {
     { 23, 256, 136, 8, K_DQ_IQ4_XS, K_MV_IQ4_XS, { 0, -1 }, { -1, -1 }, 1 },
 };
 
-/* Split-K tile geometry (kernels/mv.h): 4 blocks per column slice, 16 rows
- * per workgroup step, J rows per thread. */
-#define TILE_NBC 4
-#define TILE_RS 16
+/* Full-row tile geometry (kernels/mv.h): 384 threads; a row of U 64-weight
+ * units takes U lanes, S = 384 / U rows run side by side, J rows per lane. */
+#define TILE_NT 384
+#define TILE_MAX_COLS 9216   /* x staged per workgroup: 6 quads per thread */
+typedef struct {
+    int32_t U, S, seg, pad;
+} MvGeo;
+
+/* Geometry for rows of n_blocks 256-weight blocks; 0 if U does not divide 384. */
+static int tile_geo(int64_t n_blocks, MvGeo *g) {
+    const int64_t U = 4 * n_blocks;
+    if (U <= 0 || U > TILE_NT || TILE_NT % U) return 0;
+    g->U = (int32_t)U;
+    g->S = (int32_t)(TILE_NT / U);
+    int seg = 64;
+    while (U % seg) seg >>= 1;
+    g->seg = seg;
+    g->pad = 0;
+    return 1;
+}
 
 static int g_available;
 static int g_have_iq2xxs;
@@ -210,8 +228,6 @@ static void *scratch(size_t need, const char *op) {
     g_scratch_len = want;
     return (uint8_t *)g_scratch + CNT_BYTES;
 }
-
-static uint32_t *scratch_counters(void) { return (uint32_t *)g_scratch; }
 
 static SepiaGpuBuf *new_buf(size_t len, int kind) {
     SepiaGpuBuf *b = (SepiaGpuBuf *)calloc(1, sizeof *b);
@@ -449,27 +465,36 @@ static int g_prof_ev_made;
 static double g_prof_ms[K_COUNT];
 static int64_t g_prof_cnt[K_COUNT];
 
-static int launch(int k, unsigned grid, unsigned block, void **args, const char *op) {
+/* AMD's launch extension (declared in the C++-only hip/hip_ext.h): the
+ * start/stop events are attached to the dispatch itself, so their interval
+ * is the kernel's execution, not the surrounding queue traffic. */
+extern hipError_t hipExtModuleLaunchKernel(hipFunction_t f, uint32_t globalWorkSizeX, uint32_t globalWorkSizeY,
+                                           uint32_t globalWorkSizeZ, uint32_t localWorkSizeX,
+                                           uint32_t localWorkSizeY, uint32_t localWorkSizeZ, size_t sharedMemBytes,
+                                           hipStream_t hStream, void **kernelParams, void **extra,
+                                           hipEvent_t startEvent, hipEvent_t stopEvent, uint32_t flags);
+
+static int launch_lds(int k, unsigned grid, unsigned block, size_t lds, void **args, const char *op) {
     if (grid == 0) return 1;
-    int slot = -1;
-    if (g_prof_on) {
-        if (g_prof_n < g_prof_ev_made) {
-            slot = g_prof_n++;
-            hipEventRecord(g_prof_ev[slot][0], g_stream);
-        } else {
-            g_prof_overflow = 1;
-        }
-    }
-    hipError_t e = hipModuleLaunchKernel(g_fn[k], grid, 1, 1, block, 1, 1, 0, g_stream, args, NULL);
-    if (slot >= 0) {
-        hipEventRecord(g_prof_ev[slot][1], g_stream);
+    hipError_t e;
+    if (g_prof_on && g_prof_n < g_prof_ev_made) {
+        const int slot = g_prof_n++;
         g_prof_kid[slot] = k;
+        e = hipExtModuleLaunchKernel(g_fn[k], grid * block, 1, 1, block, 1, 1, lds, g_stream, args, NULL,
+                                     g_prof_ev[slot][0], g_prof_ev[slot][1], 0);
+    } else {
+        if (g_prof_on) g_prof_overflow = 1;
+        e = hipModuleLaunchKernel(g_fn[k], grid, 1, 1, block, 1, 1, (unsigned)lds, g_stream, args, NULL);
     }
     if (e != hipSuccess) {
         LOG("%s: launch of %s failed: %s", op, k_names[k], hipGetErrorString(e));
         return 0;
     }
     return 1;
+}
+
+static int launch(int k, unsigned grid, unsigned block, void **args, const char *op) {
+    return launch_lds(k, grid, block, 0, args, op);
 }
 
 int sepia_hip_profile_start(void) {
@@ -800,13 +825,20 @@ int sepia_hip_set_option(const char *name, int value) {
  * when the generic kernel must run: the format has no tile decoder, the row
  * is not a whole number of 4-block column slices, the base is not aligned as
  * the decoder loads it, or there are more row tiles than arrival counters. */
-static int tile_plan(const TypeInfo *ti, int64_t n_blocks, uintptr_t base, int64_t rows) {
-    if (!g_opt_tile || ti->k_tile[0] < 0 || n_blocks % TILE_NBC || base % (uintptr_t)ti->align) return 0;
-    const int64_t n_ks = n_blocks / TILE_NBC;
+static int tile_plan(const TypeInfo *ti, int64_t n_blocks, uintptr_t base, int64_t rows, MvGeo *g) {
+    if (!g_opt_tile || ti->k_tile[0] < 0 || base % (uintptr_t)ti->align || n_blocks * 256 > TILE_MAX_COLS ||
+        !tile_geo(n_blocks, g))
+        return 0;
     int J = g_opt_tile_j;
-    if (!J) J = ((rows + 4 * TILE_RS - 1) / (4 * TILE_RS)) * n_ks >= 512 ? 4 : 2;
-    if ((rows + TILE_RS * J - 1) / (TILE_RS * J) > (int64_t)(CNT_BYTES / 4)) return 0;
+    if (!J) J = (rows + 4 * g->S - 1) / (4 * g->S) >= 256 ? 4 : 2;
     return J;
+}
+
+/* Dynamic LDS of a tile workgroup: x planes of n columns (when staged),
+ * `mats` matrices' row partials, `extra` floats. */
+static size_t tile_lds(int64_t n_staged, const MvGeo *g, int J, int mats, int extra) {
+    const size_t red = (size_t)(mats * g->S * J * (g->U / g->seg) + 3) & ~(size_t)3;
+    return (size_t)(3 * n_staged + 2 * (n_staged / 16) * 4) + 4 * (red + (size_t)extra);
 }
 int sepia_gpu_matvec_q(int ggml_type, SepiaGpuBuf *w, size_t w_off, SepiaGpuBuf *x, SepiaGpuBuf *y,
                        int64_t out_dim, int64_t in_dim) {
@@ -832,15 +864,13 @@ int sepia_gpu_matvec_q(int ggml_type, SepiaGpuBuf *w, size_t w_off, SepiaGpuBuf 
         return 0;
     if (!need_batch(op) || !prep_in(w, op) || !prep_in(x, op) || !prep_out(y, op)) return 0;
     const uint8_t *wp = w->dev + w_off;
-    int J = tile_plan(ti, n_blocks, (uintptr_t)wp, out_dim);
+    MvGeo geo;
+    int J = tile_plan(ti, n_blocks, (uintptr_t)wp, out_dim, &geo);
     if (J) {
-        int32_t n_ks = (int32_t)(n_blocks / TILE_NBC);
-        int64_t tiles = (out_dim + TILE_RS * J - 1) / (TILE_RS * J);
-        float *part = (float *)scratch((size_t)n_ks * (size_t)out_dim * 4, op);
-        if (!part) return 0;
-        uint32_t *cnt = scratch_counters();
-        void *args[] = { &wp, &row_bytes, &out_dim, &n_ks, &x->dev, &y->dev, &part, &cnt };
-        return launch(ti->k_tile[J == 4], (unsigned)(tiles * n_ks), 256, args, op);
+        int64_t n = in_dim;
+        int64_t tiles = (out_dim + (int64_t)geo.S * J - 1) / ((int64_t)geo.S * J);
+        void *args[] = { &wp, &row_bytes, &out_dim, &n, &geo, &x->dev, &y->dev };
+        return launch_lds(ti->k_tile[J == 4], (unsigned)tiles, TILE_NT, tile_lds(n, &geo, J, 1, 0), args, op);
     }
     void *args[] = { &wp, &row_bytes, &n_blocks, &x->dev, &y->dev, &out_dim };
     return launch(ti->k_mv, blocks_for(out_dim, 4), 256, args, op);
@@ -969,6 +999,83 @@ static int moe_proj(const char *op, const char *what, const SepiaExpertTensor *t
     return 1;
 }
 
+/* Mirrors struct HxpArgs in kernels/mv.h. */
+typedef struct {
+    int8_t *planes;
+    float *scale;
+    float *sum;
+} HxpArgs;
+
+/* Scratch bytes the FFN launch needs for n_slots activation vectors of
+ * length I: f32 for the generic kernels or XP form (3 planes + scale + sum
+ * per 16 columns) for the tile kernels, whichever is larger. */
+static size_t ffn_scratch_bytes(int n_slots, int64_t I) {
+    const size_t f32 = (size_t)n_slots * (size_t)I * 4;
+    const size_t xp = (size_t)n_slots * ((size_t)I * 3 + (size_t)(I / 16) * 8) + 512;
+    return f32 > xp ? f32 : xp;
+}
+
+static int tile_type(int t) { return t == SEPIA_T_Q2_K || t == SEPIA_T_Q3_K || t == 12; }
+
+static int proj_aligned(const MoeProj *p) {
+    const TypeInfo *ti = type_info(p->type);
+    const uintptr_t a = ti ? (uintptr_t)ti->align : 1;
+    return ((uintptr_t)p->base % a) == 0 && p->stride % a == 0 && p->row_bytes % a == 0;
+}
+
+/* The SwiGLU expert FFN over n_slots = topk + n_shared slots: routed slot s
+ * uses expert sel_idx[s] (or fixed + s when sel_idx is NULL), then come the
+ * shared experts. One slot without weights stores y; several slots add
+ * sel_w[s] * their output into y. Uses the tile kernels (integer dots, h
+ * handed over in XP form) when every projection has a tile decoder and the
+ * shapes fit, else the generic one-wave-per-row kernels. */
+static int ffn_launch(const char *op, const MoeProj *g, const MoeProj *u, const MoeProj *d, const MoeProj *sg,
+                      const MoeProj *su, const MoeProj *sd, const int32_t *sel_idx, const float *sel_w, int32_t fixed,
+                      int32_t topk, int32_t n_shared, int64_t H, int64_t I, const uint8_t *xdev, float *ydev,
+                      uint8_t *scr) {
+    int32_t n_slots = topk + n_shared;
+    MvGeo gu_geo, dn_geo;
+    int tile = g_opt_tile && H % 256 == 0 && I % 256 == 0 && H <= TILE_MAX_COLS && tile_geo(H / 256, &gu_geo) &&
+               tile_geo(I / 256, &dn_geo) && tile_type(g->type) && g->type == u->type && tile_type(d->type) &&
+               proj_aligned(g) && proj_aligned(u) && proj_aligned(d);
+    if (tile && n_shared > 0)
+        tile = tile_type(sg->type) && sg->type == su->type && tile_type(sd->type) && proj_aligned(sg) &&
+               proj_aligned(su) && proj_aligned(sd);
+    int32_t j_gu = 0, j_dn = 0;
+    if (tile) {
+        j_gu = (gu_geo.S * 2) % 16 == 0 ? 2 : ((gu_geo.S * 4) % 16 == 0 ? 4 : 0);
+        j_dn = g_opt_tile_j ? g_opt_tile_j : ((H + 4 * dn_geo.S - 1) / (4 * dn_geo.S) * n_slots >= 256 ? 4 : 2);
+        if (g_opt_tile_j && (gu_geo.S * g_opt_tile_j) % 16 == 0) j_gu = g_opt_tile_j;
+        tile = j_gu != 0;
+    }
+    int64_t inter = I, hid = H;
+    if (tile) {
+        HxpArgs hx;
+        hx.planes = (int8_t *)scr;
+        hx.scale = (float *)(scr + (((size_t)n_slots * 3 * (size_t)I + 255) & ~(size_t)255));
+        hx.sum = hx.scale + (size_t)n_slots * (size_t)(I / 16);
+        float *no_h32 = NULL;
+        float *y_zero = n_slots > 1 ? ydev : NULL;
+        int64_t y_n = H;
+        const int64_t gu_rows = (int64_t)gu_geo.S * j_gu, dn_rows = (int64_t)dn_geo.S * j_dn;
+        const int64_t gu_tiles = (I + gu_rows - 1) / gu_rows, dn_tiles = (H + dn_rows - 1) / dn_rows;
+        void *a_gu[] = { (void *)g, (void *)u, (void *)sg, (void *)su, &sel_idx, &fixed, &topk, &inter, &hid,
+                         &gu_geo, &j_gu, &xdev, &hx, &no_h32, &y_zero, &y_n };
+        if (!launch_lds(K_FFN_GATEUP, (unsigned)(n_slots * gu_tiles), TILE_NT,
+                        tile_lds(H, &gu_geo, j_gu, 2, (int)gu_rows), a_gu, op))
+            return 0;
+        void *a_dn[] = { (void *)d, (void *)sd, &sel_idx, &sel_w, &fixed, &topk, &n_slots, &inter, &hid,
+                         &dn_geo, &j_dn, &hx, &ydev };
+        return launch_lds(K_FFN_DOWN, (unsigned)(n_slots * dn_tiles), TILE_NT, tile_lds(0, &dn_geo, j_dn, 1, 0),
+                          a_dn, op);
+    }
+    float *h = (float *)scr;
+    void *a_gu[] = { (void *)g, (void *)u, (void *)sg, (void *)su, &sel_idx, &fixed, &topk, &inter, &xdev, &h };
+    if (!launch(K_MOE_GATEUP, (unsigned)(n_slots * ((I + 3) / 4)), 256, a_gu, op)) return 0;
+    void *a_dn[] = { (void *)d, (void *)sd, &sel_idx, &sel_w, &fixed, &topk, &n_shared, &inter, &hid, &h, &ydev };
+    return launch(K_MOE_DOWN, blocks_for(H, 4), 256, a_dn, op);
+}
+
 int sepia_gpu_moe_decode(const SepiaMoeLayerDesc *L, SepiaGpuBuf *x, SepiaGpuBuf *y, SepiaGpuBuf *route_out) {
     const char *op = "moe_decode";
     if (!L || !x || !y || L->hidden <= 0 || L->inter <= 0 || L->n_routed < 1 || L->n_routed > 1024 ||
@@ -1008,15 +1115,14 @@ int sepia_gpu_moe_decode(const SepiaMoeLayerDesc *L, SepiaGpuBuf *x, SepiaGpuBuf
     }
     if (!need_batch(op)) return 0;
 
-    /* scratch: logits | sel_idx | sel_w | h, each 256-byte aligned */
+    /* scratch: logits | sel_idx | sel_w | FFN intermediates, each 256-byte aligned */
     const size_t o_logits = 0;
     const size_t o_idx = o_logits + (((size_t)n_tot * 4 + 255) & ~(size_t)255);
     const size_t o_w = o_idx + 256;
     const size_t o_h = o_w + 256;
-    const size_t need = o_h + (size_t)n_slots * (size_t)I * 4;
-    uint8_t *s = (uint8_t *)scratch(need, op);
+    uint8_t *s = (uint8_t *)scratch(o_h + ffn_scratch_bytes(n_slots, I), op);
     if (!s) return 0;
-    float *logits = (float *)(s + o_logits), *sel_w = (float *)(s + o_w), *h = (float *)(s + o_h);
+    float *logits = (float *)(s + o_logits), *sel_w = (float *)(s + o_w);
     int32_t *sel_idx = (int32_t *)(s + o_idx);
 
     SepiaGpuBuf *ins[] = { L->router_w, L->router_bias, x, L->gate.buf, L->up.buf, L->down.buf, L->s_gate.buf,
@@ -1027,7 +1133,7 @@ int sepia_gpu_moe_decode(const SepiaMoeLayerDesc *L, SepiaGpuBuf *x, SepiaGpuBuf
 
     const float *rw = (const float *)(L->router_w->dev + L->router_w_off);
     const float *rb = (const float *)(L->router_bias->dev + L->router_bias_off);
-    int64_t n_tot64 = n_tot, ld = H, hid = H, inter = I;
+    int64_t n_tot64 = n_tot, ld = H, hid = H;
     void *a_router[] = { &rw, &ld, &x->dev, &logits, &n_tot64, &hid };
     if (!launch(K_MATVEC_F32, blocks_for(n_tot, 4), 256, a_router, op)) return 0;
 
@@ -1036,12 +1142,9 @@ int sepia_gpu_moe_decode(const SepiaMoeLayerDesc *L, SepiaGpuBuf *x, SepiaGpuBuf
     void *a_sel[] = { &logits, &rb, &nr, &ns, &tk, &rs, &gs, &sel_idx, &sel_w };
     if (!launch(K_MOE_SELECT, 1, 256, a_sel, op)) return 0;
 
-    int32_t no_fixed = 0;
-    void *a_gu[] = { &g, &u, &sg, &su, &sel_idx, &no_fixed, &tk, &inter, &x->dev, &h };
-    if (!launch(K_MOE_GATEUP, (unsigned)(n_slots * ((I + 3) / 4)), 256, a_gu, op)) return 0;
-
-    void *a_dn[] = { &d, &sd, &sel_idx, &sel_w, &no_fixed, &tk, &ns, &inter, &hid, &h, &y->dev };
-    if (!launch(K_MOE_DOWN, blocks_for(H, 4), 256, a_dn, op)) return 0;
+    if (!ffn_launch(op, &g, &u, &d, &sg, &su, &sd, sel_idx, sel_w, 0, tk, ns, H, I, x->dev, (float *)y->dev,
+                    s + o_h))
+        return 0;
 
     if (route_out) {
         hipError_t e = hipMemcpyAsync(route_out->dev, sel_idx, (size_t)L->topk * 4, hipMemcpyDeviceToDevice, g_stream);
@@ -1071,17 +1174,11 @@ int sepia_gpu_expert_ffn(const SepiaExpertTensor *gate, const SepiaExpertTensor 
         return 0;
     if (!chk(x, 0, (size_t)hidden * 4, op, "x") || !chk(y, 0, (size_t)hidden * 4, op, "y")) return 0;
     if (!need_batch(op)) return 0;
-    float *h = (float *)scratch((size_t)inter * 4, op);
-    if (!h) return 0;
+    uint8_t *scr = (uint8_t *)scratch(ffn_scratch_bytes(1, inter), op);
+    if (!scr) return 0;
     if (!prep_in(gate->buf, op) || !prep_in(up->buf, op) || !prep_in(down->buf, op) || !prep_in(x, op) ||
         !prep_out(y, op))
         return 0;
-    const int32_t *no_idx = NULL;
-    const float *no_w = NULL;
-    int32_t e = expert, one = 1, zero = 0;
-    int64_t in64 = inter, hid = hidden;
-    void *a_gu[] = { &g, &u, &none, &none, &no_idx, &e, &one, &in64, &x->dev, &h };
-    if (!launch(K_MOE_GATEUP, blocks_for(inter, 4), 256, a_gu, op)) return 0;
-    void *a_dn[] = { &d, &none, &no_idx, &no_w, &e, &one, &zero, &in64, &hid, &h, &y->dev };
-    return launch(K_MOE_DOWN, blocks_for(hidden, 4), 256, a_dn, op);
+    return ffn_launch(op, &g, &u, &d, &none, &none, &none, NULL, NULL, expert, 1, 0, hidden, inter, x->dev,
+                      (float *)y->dev, scr);
 }
