@@ -289,3 +289,42 @@ def test_expert_ffn_is_composition(orc):
     y = orc.expert_ffn(10, g, 10, u, 11, dn, H, I, x)
     h = orc.silu_mul(orc.qlinear(10, g, I, H, x), orc.qlinear(10, u, I, H, x))
     assert np.array_equal(y, orc.qlinear(11, dn, H, I, h))
+
+
+def _inkling_golden():
+    return np.load(os.path.join(GOLDEN, "inkling_moe.npz"))
+
+
+def test_route_select_vs_transformers_inkling(orc):
+    """Selection set and mixing weights against the third-party InklingTopkRouter
+    (float64), vectors written by tests/golden/make_inkling_moe.py."""
+    d = _inkling_golden()
+    nr, ns, k = d["router_b"].size, d["router_w"].shape[0] - d["router_b"].size, int(d["topk"])
+    for t in range(d["x"].shape[0]):
+        logits = orc.linear_f32(d["router_w"], d["x"][t])
+        np.testing.assert_allclose(logits[:nr], d["logits"][t], rtol=0, atol=1e-6)
+        idx, w = orc.route_select(logits, d["router_b"], nr, ns, k, float(d["route_scale"]), float(d["global_scale"]))
+        order = np.argsort(idx)
+        assert np.array_equal(np.asarray(idx)[order], d["idx"][t])
+        np.testing.assert_allclose(np.asarray(w[:k])[order], d["w_routed"][t], rtol=2e-6)
+        np.testing.assert_allclose(w[k:], d["gammas"][t], rtol=2e-6)
+
+
+def test_moe_layer_vs_transformers_inkling(orc):
+    """Whole-layer composition (routed weight after down, shared gamma before
+    down, sum) against the third-party InklingMoE (float64), f32 weights."""
+    d = _inkling_golden()
+    nr, ns = d["router_b"].size, d["router_w"].shape[0] - d["router_b"].size
+    H, I = d["x"].shape[1], d["gate"].shape[1]
+    as_bytes = lambda a: [np.ascontiguousarray(m, dtype=np.float32).view(np.uint8).ravel() for m in a]
+    spec = dict(hidden=H, inter=I, n_routed=nr, n_shared=ns, topk=int(d["topk"]),
+                route_scale=float(d["route_scale"]), global_scale=float(d["global_scale"]),
+                router_w=d["router_w"], router_bias=d["router_b"], t_gate=0, t_up=0, t_down=0,
+                ts_gate=0, ts_up=0, ts_down=0, gate=as_bytes(d["gate"]), up=as_bytes(d["up"]),
+                down=as_bytes(d["down"]), s_gate=as_bytes(d["s_gate"]), s_up=as_bytes(d["s_up"]),
+                s_down=as_bytes(d["s_down"]))
+    for t in range(d["x"].shape[0]):
+        y, _, idx, _ = orc.moe_layer(spec, d["x"][t])
+        assert np.array_equal(np.sort(idx), d["idx"][t])
+        want = d["y"][t]
+        assert np.max(np.abs(y - want)) <= 2e-6 * np.max(np.abs(want))
