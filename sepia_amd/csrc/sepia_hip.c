@@ -5,18 +5,22 @@
  * additive entries of include/sepia_hip_ext.h, over the HIP runtime C API.
  * Kernels are prebuilt for gfx950 into sepia_kernels.hsaco and loaded with
  * hipModuleLoad from the directory given to sepia_gpu_init (the reference
- * compiles metal_dir's *.metal at the same point, src/sepia_metal.m:103-149).
+ * compiles metal_dir's *.metal at the same point, src/sepia_metal.m:103-149);
+ * when that directory holds no code object (sepia.c passes "metal",
+ * src/sepia.c:6181) the one next to this library is used.
  *
  * Single host thread, no locking, one in-order HIP stream at default
  * priority. Every function logs one "sepia: hip: ..." line and returns 0/NULL
  * on failure; nothing exits (src/sepia_gpu.h:1-3, src/sepia_metal.m:15-18).
  */
+#define _GNU_SOURCE 1
 #define __HIP_PLATFORM_AMD__ 1
 #include <hip/hip_runtime_api.h>
 
 #include "../../include/sepia_gpu.h"
 #include "../../include/sepia_hip_ext.h"
 
+#include <dlfcn.h>
 #include <stdarg.h>
 #include <stdint.h>
 #include <stdio.h>
@@ -332,12 +336,27 @@ uint64_t sepia_gpu_gpu_addr(SepiaGpuBuf *b) { return b ? (uint64_t)(uintptr_t)b-
 /* ------------------------------------------------------------ lifecycle - */
 int sepia_gpu_available(void) { return g_available; }
 
+/* dir/sepia_kernels.hsaco if that file exists, else the code object beside
+ * this shared library. 0 if neither path fits in `path`. */
+static int kernel_path(const char *dir, char *path, size_t cap) {
+    if (dir && dir[0]) {
+        if ((size_t)snprintf(path, cap, "%s/sepia_kernels.hsaco", dir) >= cap) return 0;
+        if (access(path, R_OK) == 0) return 1;
+    }
+    Dl_info info;
+    if (dladdr((void *)&sepia_gpu_init, &info) && info.dli_fname) {
+        const char *slash = strrchr(info.dli_fname, '/');
+        const int len = slash ? (int)(slash - info.dli_fname) : 1;
+        const char *base = slash ? info.dli_fname : ".";
+        if ((size_t)snprintf(path, cap, "%.*s/sepia_kernels.hsaco", len, base) >= cap) return 0;
+        if (access(path, R_OK) == 0) return 1;
+    }
+    if (dir && dir[0]) snprintf(path, cap, "%s/sepia_kernels.hsaco", dir);  /* report the caller's path */
+    return 1;
+}
+
 int sepia_gpu_init(const char *kernel_dir) {
     if (g_available) return 1;
-    if (!kernel_dir || !kernel_dir[0]) {
-        LOG("init requires the directory holding sepia_kernels.hsaco");
-        return 0;
-    }
     int n = 0;
     hipError_t e = hipGetDeviceCount(&n);
     if (e != hipSuccess || n < 1) {
@@ -358,8 +377,8 @@ int sepia_gpu_init(const char *kernel_dir) {
         return 0;
     }
     char path[4096];
-    if ((size_t)snprintf(path, sizeof path, "%s/sepia_kernels.hsaco", kernel_dir) >= sizeof path) {
-        LOG("init: kernel_dir path too long");
+    if (!kernel_path(kernel_dir, path, sizeof path)) {
+        LOG("init: kernel directory path too long");
         return 0;
     }
     if ((e = hipStreamCreate(&g_stream)) != hipSuccess) {
