@@ -227,7 +227,8 @@ def run_c2(B, warmup, steps, cpu_seconds):
     e_last = (warmup + steps - 1) % NE
     y_graph = B.fetch(y, 0, H * 4).view(np.float32)
     step_bytes = gb + ub + db + H * 4 + I * 4 + H * 4
-    kms = B.kernel_ms(step, min(steps, 4 * NE), ["sepia_ffn_gateup", "sepia_ffn_down"])
+    K_GU, K_DN = "sepia_ffn_gateup_22", "sepia_ffn_down_33"
+    kms = B.kernel_ms(step, min(steps, 4 * NE), [K_GU, K_DN])
     gu_bytes = gb + ub + H * 4 + I * 4
     dn_bytes = db + I * 4 + H * 4
     B.dev.run(L.sepia_gpu_expert_ffn, *ref, NE, e_last, H, I, xs[0], y)
@@ -252,14 +253,14 @@ def run_c2(B, warmup, steps, cpu_seconds):
                         cpu_seconds / 4, 1000)
     for b in bufs + xs + [y]:
         B.dev.free(b)
-    dom = "sepia_ffn_gateup"
+    dom = K_GU
     return dict(
         ms=ms, step_bytes=step_bytes, value=step_bytes / (ms * 1e-3) / 1e9,
         parity=dict(max_abs_diff=err, y_inf=scale, bound="1e-4*||y||_inf"),
         roofline=dict(bound="hbm", kernel=dom, achieved=gu_bytes / (kms[dom] * 1e-3) / 1e9, peak=HBM_PEAK_GBS,
                       unit="GB/s", bytes_per_launch=gu_bytes, avg_launch_us=kms[dom] * 1e3,
-                      other_kernels={"sepia_ffn_down": dict(bytes_per_launch=dn_bytes, avg_launch_us=kms["sepia_ffn_down"] * 1e3,
-                                                           achieved=dn_bytes / (kms["sepia_ffn_down"] * 1e-3) / 1e9)}),
+                      other_kernels={K_DN: dict(bytes_per_launch=dn_bytes, avg_launch_us=kms[K_DN] * 1e3,
+                                                achieved=dn_bytes / (kms[K_DN] * 1e-3) / 1e9)}),
         cpu=dict(s1=s1, n1=n1, sN=sN, nN=nN, threads=nthr))
 
 
@@ -278,7 +279,7 @@ def run_matvec_rotation(B, name, t, rows, cols, warmup, steps, cpu_seconds, seed
 
     ms = B.timed_steps(step, warmup, steps)
     tname = {12: "q4_k", 17: "iq2_xs", 18: "iq3_xxs", 16: "iq2_xxs"}[t]
-    cands = ["sepia_mv_%s_j2" % tname, "sepia_mv_%s_j4" % tname, "sepia_matvec_generic_%s" % tname]
+    cands = ["sepia_mv_%s" % tname, "sepia_matvec_generic_%s" % tname]
     kname, kms = B.kernel_used(step, min(steps, 2 * ncopy), cands)
     nbytes = mb + cols * 4 + rows * 4
     import oracle
@@ -336,8 +337,7 @@ def run_c3(B, warmup, steps, cpu_seconds, n_layers=3):
 
     ms = B.timed_steps(step, warmup, steps)
     per_token = (NR + NS) * H * 4 + 6 * (2 * gb + db) + NS * (2 * sgb + sdb)
-    kms = B.kernel_ms(step, min(steps, 60), ["sepia_matvec_f32", "sepia_moe_select", "sepia_ffn_gateup",
-                                             "sepia_ffn_down"])
+    kms = B.kernel_ms(step, min(steps, 60), ["sepia_moe_route", "sepia_ffn_gateup_24_xp", "sepia_ffn_down_34"])
 
     # parity at full size: route + output of one token against the oracle
     import oracle

@@ -1,144 +1,168 @@
-// mv.h -- full-row tile matvec for quantized rows (decode, batch 1).
+// mv.h -- tile kernels for quantized matvecs at decode batch 1: the plain
+// matvec, the fused gate/up/SwiGLU launch and the down launch of the expert
+// FFN (one launch covers every expert slot of a MoE layer).
 //
-// A 384-thread workgroup owns S*J whole rows. The row's U = in_dim / 64
-// units (64-weight pieces of a block) are spread over U lanes and each lane
-// keeps its unit's x planes in registers while it walks J rows, S rows per
-// step (S = 384 / U; U must divide 384: 3072, 4096 and 6144 columns give
-// U = 48, 64, 96). Per workgroup:
-//   1. the lane issues the loads of its unit for all J rows;
-//   2. while they are in flight the workgroup stages x in LDS in XP form
-//      (qdot.h) -- or, when x already comes in XP form from the previous
-//      kernel, reads it from there;
-//   3. integer unit dots (qdot.h), a butterfly over the `seg` lanes of the
-//      row that share a wave, then a short LDS sum across waves.
+// A 384-thread workgroup owns T*S whole rows of one matrix (two for
+// gate/up). A row of U = in_dim / 64 units (64-weight pieces of a block) is
+// spread over U lanes; S = 384 / U rows sit side by side and the workgroup
+// walks T such steps. U is a multiple of 16 dividing 384 (in_dim 1024,
+// 2048, 3072, 4096, 6144, ..., 24576), so every row's lanes start on a
+// 16-lane DPP row.
+//
+// Per workgroup:
+//   1. each lane issues its x loads (or x-plane loads), then the loads of
+//      its unit for all T rows (and both matrices), in the order they are
+//      consumed -- a wave's loads retire in order, so the first row's dot can
+//      start while later rows are still in flight;
+//   2. with the weights in flight the workgroup converts x into digit planes
+//      in LDS (qdot.h) -- one 16-column segment per thread, v_perm packing --
+//      unless x already comes as planes from an earlier launch;
+//   3. each lane loads its unit's planes into registers once and forms one
+//      integer unit dot per row; a 16-lane DPP sum and a short LDS sum give
+//      each row.
 // Rows never span workgroups, so no workgroup waits for or talks to another.
+// The grid is sized to the 256 CUs (T chosen so that the matrix takes about
+// one workgroup per CU), and a MoE launch simply stacks the slots' tiles.
 #pragma once
 #include "common.h"
 #include "qdot.h"
 
-#ifndef MV_NT
-#define MV_NT 384
-#endif
+#define MV_NT 384     // threads per workgroup
+#define MV_JMAX 3     // row steps per workgroup (loads in flight per lane and matrix)
+#define MV_XSEG 2     // x segments converted per thread: in_dim <= 2 * 16 * 384
 
-struct MvGeo {
-    int32_t U;     // units per row
-    int32_t S;     // rows per step (384 / U)
-    int32_t seg;   // lanes per in-wave partial sum (largest power of two dividing U, <= 64)
-    int32_t pad;
+struct TileGeo {
+    int32_t U;      // units per row
+    int32_t S;      // rows per step (MV_NT / U)
+    int32_t T;      // steps per workgroup, 1..MV_JMAX
+    int32_t tiles;  // workgroups per matrix: ceil(ceil(rows / S) / T)
 };
 
-// LDS carve-up: x planes (3n bytes), scales and sums (n/16 floats each),
-// row partials (S * J * (U / seg) floats), then scratch floats.
-struct MvSmem {
+// Dynamic LDS: x planes (3n bytes), xs and gs (n/16 floats each), then the
+// row partials (MATS * T * S * U/16 floats).
+struct TileSmem {
     int8_t *planes;
-    float *scale, *sum, *red, *extra;
+    float *xs, *gs, *red;
 };
-__device__ __forceinline__ MvSmem mv_smem(uint8_t *base, int64_t n, int rows_red) {
-    MvSmem m;
+__device__ __forceinline__ TileSmem tile_smem(uint8_t *base, int64_t n) {
+    TileSmem m;
     m.planes = (int8_t *)base;
-    m.scale = (float *)(base + 3 * n);
-    m.sum = m.scale + n / 16;
-    m.red = m.sum + n / 16;
-    m.extra = m.red + ((rows_red + 3) & ~3);   // keep extra 16-byte aligned
+    m.xs = (float *)(base + 3 * n);
+    m.gs = m.xs + n / 16;
+    m.red = m.gs + n / 16;
     return m;
 }
 
-// x staging is split in two so that x's loads are issued before the weight
-// loads: a wave's loads retire in order, so a wait for x issued after the
-// weights would also wait for every weight. Each thread holds up to MV_XQ
-// quads (n <= 4 * 384 * MV_XQ = 9216 columns).
-#ifndef MV_XQ
-#define MV_XQ 6
-#endif
-struct XQuads {
-    float4 v[MV_XQ];
+// ---- x staging: f32 x -> XP in LDS, one segment per thread and round.
+struct XStage {
+    float4 v[MV_XSEG][4];
 };
-
-__device__ __forceinline__ void mv_load_x(const float *__restrict__ x, int64_t n, XQuads &xq) {
+__device__ __forceinline__ void xs_load(const float *__restrict__ x, int64_t n, XStage &st) {
     const float4 *x4 = (const float4 *)x;
 #pragma unroll
-    for (int p = 0; p < MV_XQ; p++) {
-        const int64_t q = threadIdx.x + (int64_t)p * MV_NT;
-        xq.v[p] = q < n / 4 ? x4[q] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    }
-}
-
-// The loaded quads -> XP in LDS (n a multiple of 16, so each 4-lane segment
-// group is entirely inside or outside the vector).
-__device__ __forceinline__ void mv_stage_x(const XQuads &xq, int64_t n, const MvSmem &m) {
+    for (int i = 0; i < MV_XSEG; i++) {
+        const int64_t seg = threadIdx.x + (int64_t)i * MV_NT;
+        if (seg < n / 16) {
 #pragma unroll
-    for (int p = 0; p < MV_XQ; p++) {
-        const int64_t q = threadIdx.x + (int64_t)p * MV_NT;
-        if (q < n / 4) xp_quad(xq.v[p], q, m.planes, m.scale, m.sum, n);
+            for (int c = 0; c < 4; c++) st.v[i][c] = x4[4 * seg + c];
+        }
+    }
+}
+__device__ __forceinline__ void xs_convert(const XStage &st, int64_t n, const TileSmem &m) {
+#pragma unroll
+    for (int i = 0; i < MV_XSEG; i++) {
+        const int64_t seg = threadIdx.x + (int64_t)i * MV_NT;
+        if (seg < n / 16) xp_store(xp_segment(st.v[i]), m.planes, m.xs, m.gs, n, seg);
     }
 }
 
-template <int T, int J>
-__device__ __forceinline__ void mv_issue(const uint8_t *__restrict__ W, uint64_t row_bytes, int64_t rows,
-                                         int64_t r0, const MvGeo &g, typename QU<T>::Data (&d)[J]) {
-    const int t = threadIdx.x, u = t % g.U, s = t / g.U;
+// ---- DPP sum over the 16 lanes of a row (every lane gets the sum).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float sum16(float v) {
+    v += dpp_f32<0xB1>(v);    // quad_perm [1,0,3,2]
+    v += dpp_f32<0x4E>(v);    // quad_perm [2,3,0,1]
+    v += dpp_f32<0x141>(v);   // row_half_mirror
+    v += dpp_f32<0x140>(v);   // row_mirror
+    return v;
+}
+
+// ---- weights of MATS matrices for the lane's unit, T rows from row0.
+template <int T, int MATS>
+struct TileData {
+    typename QU<T>::Data d[MV_JMAX][MATS];
+};
+template <int T, int MATS>
+__device__ __forceinline__ void tile_issue(const uint8_t *const (&W)[MATS], uint64_t row_bytes, int64_t rows,
+                                           int64_t r0, const TileGeo &g, int u, int s, TileData<T, MATS> &td) {
     const uint64_t col_off = (uint64_t)(u >> 2) * QU<T>::bytes;
 #pragma unroll
-    for (int j = 0; j < J; j++) {
-        int64_t r = r0 + (int64_t)j * g.S + s;
-        r = r < rows ? r : rows - 1;
-        d[j] = QU<T>::load(W + (uint64_t)r * row_bytes + col_off, u & 3);
+    for (int j = 0; j < MV_JMAX; j++) {
+        if (j < g.T) {
+            int64_t r = r0 + (int64_t)j * g.S + s;
+            r = r < rows ? r : rows - 1;   // tail rows load a valid row; their sums are dropped
+#pragma unroll
+            for (int mt = 0; mt < MATS; mt++) td.d[j][mt] = QU<T>::load(W[mt] + (uint64_t)r * row_bytes + col_off, u & 3);
+        }
     }
 }
 
-// Unit dots of J rows, summed over the row's lanes within each wave; the
-// first lane of each `seg` group stores its partial at red[(j*S + s) * nseg + u/seg].
-template <int T, int J>
-__device__ __forceinline__ void mv_partials(const typename QU<T>::Data (&d)[J], const XU &X, const MvGeo &g,
-                                            float *red) {
-    const int t = threadIdx.x, u = t % g.U, s = t / g.U;
-    const int nseg = g.U / g.seg;
+// Unit dots, 16-lane sums, partials to red[(mt*T*S + j*S + s) * U/16 + u/16].
+template <int T, int MATS>
+__device__ __forceinline__ void tile_dots(const TileData<T, MATS> &td, const XU &X, const TileGeo &g, int u, int s,
+                                          float *red) {
+    const int nq = g.U >> 4;
 #pragma unroll
-    for (int j = 0; j < J; j++) {
-        float a = QU<T>::dot(d[j], u & 3, X);
+    for (int j = 0; j < MV_JMAX; j++) {
+        if (j < g.T) {
 #pragma unroll
-        for (int off = 32; off >= 1; off >>= 1)
-            if (off < g.seg) a += __shfl_xor(a, off, SEPIA_WAVE);
-        if ((u & (g.seg - 1)) == 0) red[(j * g.S + s) * nseg + u / g.seg] = a;
+            for (int mt = 0; mt < MATS; mt++) {
+                const float a = sum16(QU<T>::dot(td.d[j][mt], u & 3, X));
+                if ((u & 15) == 0) red[((mt * g.T + j) * g.S + s) * nq + (u >> 4)] = a;
+            }
+        }
     }
 }
 
-// Row rr (0 <= rr < S*J) of the tile from the partials.
-__device__ __forceinline__ float mv_row_sum(const float *red, int rr, const MvGeo &g) {
-    const int nseg = g.U / g.seg;
-    float s = 0.0f;
-    for (int i = 0; i < nseg; i++) s += red[rr * nseg + i];
-    return s;
+// Sum of row i (= j*S + s) of matrix mt from the partials.
+__device__ __forceinline__ float tile_row(const float *red, int mt, int i, const TileGeo &g) {
+    const int nq = g.U >> 4;
+    const float *p = red + (mt * g.T * g.S + i) * nq;
+    float v = 0.0f;
+    for (int q = 0; q < nq; q++) v += p[q];
+    return v;
 }
 
-// y = W x for one quantized matrix; grid = ceil(rows / (S*J)).
-template <int T, int J>
-__device__ __forceinline__ void mv_full_body(const uint8_t *__restrict__ W, uint64_t row_bytes, int64_t rows,
-                                             int64_t n, MvGeo g, const float *__restrict__ x,
-                                             float *__restrict__ y) {
+// ---- y = W x for one matrix; grid = g.tiles.
+template <int T>
+__device__ __forceinline__ void mv_tile(const uint8_t *__restrict__ W, uint64_t row_bytes, int64_t rows, int64_t n,
+                                        const TileGeo &g, const float *__restrict__ x, float *__restrict__ y) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    const MvSmem m = mv_smem(smem, n, g.S * J * (g.U / g.seg));
-    const int64_t r0 = (int64_t)blockIdx.x * g.S * J;
-    XQuads xq;
-    mv_load_x(x, n, xq);
-    typename QU<T>::Data d[J];
-    mv_issue<T, J>(W, row_bytes, rows, r0, g, d);
-    mv_stage_x(xq, n, m);
+    const TileSmem m = tile_smem(smem, n);
+    const int u = threadIdx.x % g.U, s = threadIdx.x / g.U;
+    const int64_t r0 = (int64_t)blockIdx.x * g.T * g.S;
+    XStage st;
+    xs_load(x, n, st);
+    TileData<T, 1> td;
+    const uint8_t *const Wm[1] = {W};
+    tile_issue<T, 1>(Wm, row_bytes, rows, r0, g, u, s, td);
+    xs_convert(st, n, m);
     __syncthreads();
     XU X;
-    const int u = threadIdx.x % g.U;
-    load_xu<T>(XPView{m.planes, m.scale, m.sum, n}, u >> 2, u & 3, X);
-    mv_partials<T, J>(d, X, g, m.red);
+    load_xu<T>(m.planes, m.xs, m.gs, n, u >> 2, u & 3, X);
+    tile_dots<T, 1>(td, X, g, u, s, m.red);
     __syncthreads();
-    const int rr = threadIdx.x;
-    if (rr < g.S * J && r0 + rr < rows) y[r0 + rr] = mv_row_sum(m.red, rr, g);
+    const int i = threadIdx.x;
+    if (i < g.T * g.S && r0 + i < rows) y[r0 + i] = tile_row(m.red, 0, i, g);
 }
 
-#define SEPIA_MV_KERNEL(name, T, J)                                                                 \
-    extern "C" __global__ __launch_bounds__(MV_NT) void sepia_mv_##name##_j##J(                   \
-        const uint8_t *__restrict__ W, uint64_t row_bytes, int64_t rows, int64_t n, MvGeo g,      \
+#define SEPIA_MV_KERNEL(name, T)                                                                  \
+    extern "C" __global__ __launch_bounds__(MV_NT) void sepia_mv_##name(                          \
+        const uint8_t *__restrict__ W, uint64_t row_bytes, int64_t rows, int64_t n, TileGeo g,    \
         const float *__restrict__ x, float *__restrict__ y) {                                     \
-        mv_full_body<T, J>(W, row_bytes, rows, n, g, x, y);                                       \
+        mv_tile<T>(W, row_bytes, rows, n, g, x, y);                                               \
     }
 
 // ------------------------------------------------------------------ FFN ---
@@ -153,140 +177,142 @@ struct MoeProj {
     int32_t pad;
 };
 
-// Per-slot XP arrays of the SwiGLU activations h (inter columns each).
-struct HxpArgs {
-    int8_t *planes;   // [slot][3][inter]
-    float *scale;     // [slot][inter / 16]
-    float *sum;       // [slot][inter / 16]
+// x in digit-plane form in global memory (written by the router launch).
+struct XpArgs {
+    const int8_t *planes;   // [3][n]
+    const float *xs;        // [n / 16]
+    const float *gs;        // [n / 16]
 };
 
 __device__ __forceinline__ int64_t slot_expert(const int32_t *sel_idx, int32_t fixed, int32_t slot, int32_t topk) {
     return slot < topk ? (sel_idx ? (int64_t)sel_idx[slot] : (int64_t)fixed + slot) : (int64_t)(slot - topk);
 }
 
-// h[slot, i] = silu(gate_i . x) * (up_i . x) for S*J rows i of one slot; h is
-// written in XP form (S*J is a multiple of 16, so the tile holds whole
-// segments) and, if h32 is set, as f32.
-template <int T, int J>
-__device__ __forceinline__ void ffn_gateup_tile(const MoeProj &G, const MoeProj &Up, int64_t e, int64_t inter,
-                                                int64_t hidden, MvGeo g, int32_t slot, int64_t r0,
-                                                const float *__restrict__ x, const HxpArgs &hx,
-                                                float *__restrict__ h32, const MvSmem &m) {
-    const uint8_t *wg = G.base + e * G.stride, *wu = Up.base + e * Up.stride;
-    XQuads xq;
-    mv_load_x(x, hidden, xq);
-    typename QU<T>::Data dg[J], du[J];
-    mv_issue<T, J>(wg, G.row_bytes, inter, r0, g, dg);
-    mv_issue<T, J>(wu, Up.row_bytes, inter, r0, g, du);
-    mv_stage_x(xq, hidden, m);
-    __syncthreads();
+// h[slot, i] = silu(gate_i . x) * (up_i . x) for the T*S rows i of one tile.
+// XP_IN: x's planes come from global memory (xp); else x is f32 and is
+// converted in LDS.
+template <int T, bool XP_IN>
+__device__ __forceinline__ void gateup_tile(const MoeProj &G, const MoeProj &Up, int64_t e, int64_t inter,
+                                            int64_t hidden, const TileGeo &g, int32_t slot, int64_t r0,
+                                            const float *__restrict__ x, const XpArgs &xp, float *__restrict__ h) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int u = threadIdx.x % g.U, s = threadIdx.x / g.U;
+    const uint8_t *const Wm[2] = {G.base + e * G.stride, Up.base + e * Up.stride};
+    TileData<T, 2> td;
     XU X;
-    const int u = threadIdx.x % g.U;
-    load_xu<T>(XPView{m.planes, m.scale, m.sum, hidden}, u >> 2, u & 3, X);
-    const int nred = g.S * J * (g.U / g.seg);
-    mv_partials<T, J>(dg, X, g, m.red);
-    mv_partials<T, J>(du, X, g, m.red + nred);
-    __syncthreads();
-    const int rr = threadIdx.x;
-    float *hv = m.extra;                                   // S*J activations of this tile
-    if (rr < g.S * J) {
-        const float gv = mv_row_sum(m.red, rr, g);
-        const float uv = mv_row_sum(m.red + nred, rr, g);
-        const float hval = (r0 + rr < inter) ? silu_f32(gv) * uv : 0.0f;
-        hv[rr] = hval;
-        if (h32 && r0 + rr < inter) h32[(int64_t)slot * inter + r0 + rr] = hval;
+    float *red;
+    if (XP_IN) {
+        red = (float *)smem;
+        load_xu<T>(xp.planes, xp.xs, xp.gs, hidden, u >> 2, u & 3, X);
+        tile_issue<T, 2>(Wm, G.row_bytes, inter, r0, g, u, s, td);
+    } else {
+        const TileSmem m = tile_smem(smem, hidden);
+        red = m.red;
+        XStage st;
+        xs_load(x, hidden, st);
+        tile_issue<T, 2>(Wm, G.row_bytes, inter, r0, g, u, s, td);
+        xs_convert(st, hidden, m);
+        __syncthreads();
+        load_xu<T>(m.planes, m.xs, m.gs, hidden, u >> 2, u & 3, X);
     }
+    tile_dots<T, 2>(td, X, g, u, s, red);
     __syncthreads();
-    const int q = threadIdx.x;                             // one quad of h per thread
-    if (q < g.S * J / 4 && r0 + 4 * q < inter) {
-        const float4 v = *(const float4 *)&hv[4 * q];
-        xp_quad(v, r0 / 4 + q, hx.planes + (int64_t)slot * 3 * inter, hx.scale + (int64_t)slot * (inter / 16),
-                hx.sum + (int64_t)slot * (inter / 16), inter);
+    const int i = threadIdx.x;
+    if (i < g.T * g.S && r0 + i < inter) {
+        const float gv = tile_row(red, 0, i, g), uv = tile_row(red, 1, i, g);
+        h[(int64_t)slot * inter + r0 + i] = silu_f32(gv) * uv;
     }
 }
 
-// grid = n_slots * ceil(inter / (S*J)). Routed slots (< topk) take their
-// expert from sel_idx (or fixed_expert + slot); later slots are the shared
-// experts. Workgroups with blockIdx < zero_blocks also clear y_zero[0..y_n).
-extern "C" __global__ __launch_bounds__(MV_NT) void sepia_ffn_gateup(
-    MoeProj gate, MoeProj up, MoeProj s_gate, MoeProj s_up, const int32_t *__restrict__ sel_idx,
-    int32_t fixed_expert, int32_t topk, int64_t inter, int64_t hidden, MvGeo g, int32_t J,
-    const float *__restrict__ x, HxpArgs hx, float *__restrict__ h32, float *__restrict__ y_zero, int64_t y_n) {
-    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+// grid = n_slots * g.tiles. Routed slots (< topk) use type TR and take their
+// expert from sel_idx (or fixed_expert + slot); the later (shared) slots use
+// type TS. Workgroups also clear y_zero[0 .. y_n) when it is set (the down
+// launch then accumulates into it).
+template <int TR, int TS, bool XP_IN>
+__device__ __forceinline__ void ffn_gateup_body(const MoeProj &gate, const MoeProj &up, const MoeProj &s_gate,
+                                                const MoeProj &s_up, const int32_t *__restrict__ sel_idx,
+                                                int32_t fixed_expert, int32_t topk, int64_t inter, int64_t hidden,
+                                                const TileGeo &g, const float *__restrict__ x, const XpArgs &xp,
+                                                float *__restrict__ h, float *__restrict__ y_zero, int64_t y_n) {
     if (y_zero) {
         for (int64_t i = (int64_t)blockIdx.x * MV_NT + threadIdx.x; i < y_n; i += (int64_t)gridDim.x * MV_NT)
             y_zero[i] = 0.0f;
     }
-    const int64_t rows_per = (int64_t)g.S * J;
-    const int64_t tiles = (inter + rows_per - 1) / rows_per;
-    const int32_t slot = (int32_t)(blockIdx.x / tiles);
-    const int64_t r0 = (blockIdx.x % tiles) * rows_per;
-    const bool routed = slot < topk;
-    const MoeProj &G = routed ? gate : s_gate;
-    const MoeProj &U = routed ? up : s_up;
+    const int32_t slot = (int32_t)(blockIdx.x / g.tiles);
+    const int64_t r0 = (int64_t)(blockIdx.x % g.tiles) * g.T * g.S;
     const int64_t e = slot_expert(sel_idx, fixed_expert, slot, topk);
-    // the red area holds the gate and the up partials; extra follows both
-    const MvSmem mm = mv_smem(smem, hidden, 2 * g.S * J * (g.U / g.seg));
-#define GU_CASE(TT, JJ)                                                                          \
-    if (G.type == TT && J == JJ) {                                                               \
-        ffn_gateup_tile<TT, JJ>(G, U, e, inter, hidden, g, slot, r0, x, hx, h32, mm);            \
-        return;                                                                                  \
-    }
-    GU_CASE(ST_Q2_K, 2) GU_CASE(ST_Q2_K, 4) GU_CASE(ST_Q3_K, 2) GU_CASE(ST_Q3_K, 4)
-    GU_CASE(ST_Q4_K, 2) GU_CASE(ST_Q4_K, 4)
-#undef GU_CASE
+    if (slot < topk)
+        gateup_tile<TR, XP_IN>(gate, up, e, inter, hidden, g, slot, r0, x, xp, h);
+    else
+        gateup_tile<TS, XP_IN>(s_gate, s_up, e, inter, hidden, g, slot, r0, x, xp, h);
 }
 
-// y[d] (+)= w_slot * (down_slot[d, :] . h_slot) for S*J rows d of one slot,
-// with h_slot read in XP form from global memory.
-template <int T, int J>
-__device__ __forceinline__ void ffn_down_tile(const MoeProj &P, int64_t e, int64_t inter, int64_t hidden, MvGeo g,
-                                              int32_t slot, int64_t r0, const HxpArgs &hx, float w,
-                                              float *__restrict__ y, bool accumulate, const MvSmem &m) {
-    typename QU<T>::Data d[J];
-    mv_issue<T, J>(P.base + e * P.stride, P.row_bytes, hidden, r0, g, d);
-    XU X;
-    const int u = threadIdx.x % g.U;
-    const XPView xv{hx.planes + (int64_t)slot * 3 * inter, hx.scale + (int64_t)slot * (inter / 16),
-                    hx.sum + (int64_t)slot * (inter / 16), inter};
-    load_xu<T>(xv, u >> 2, u & 3, X);
-    mv_partials<T, J>(d, X, g, m.red);
-    __syncthreads();
-    const int rr = threadIdx.x;
-    if (rr < g.S * J && r0 + rr < hidden) {
-        const float v = mv_row_sum(m.red, rr, g);
-        if (accumulate)
-            atomicAdd(&y[r0 + rr], w * v);
-        else
-            y[r0 + rr] = w * v;
+#define SEPIA_FFN_GATEUP(name, TR, TS, XP_IN)                                                        \
+    extern "C" __global__ __launch_bounds__(MV_NT) void sepia_ffn_gateup_##name(                     \
+        MoeProj gate, MoeProj up, MoeProj s_gate, MoeProj s_up, const int32_t *__restrict__ sel_idx, \
+        int32_t fixed_expert, int32_t topk, int64_t inter, int64_t hidden, TileGeo g,                \
+        const float *__restrict__ x, XpArgs xp, float *__restrict__ h, float *__restrict__ y_zero,   \
+        int64_t y_n) {                                                                               \
+        ffn_gateup_body<TR, TS, XP_IN>(gate, up, s_gate, s_up, sel_idx, fixed_expert, topk, inter,   \
+                                       hidden, g, x, xp, h, y_zero, y_n);                            \
     }
-}
 
-// grid = n_slots * ceil(hidden / (S*J)). With one slot and no weights y is
-// stored; otherwise every slot adds w_slot * its rows into y (cleared by
-// sepia_ffn_gateup), the routed weights then the shared gammas of sel_w.
-extern "C" __global__ __launch_bounds__(MV_NT) void sepia_ffn_down(
-    MoeProj down, MoeProj s_down, const int32_t *__restrict__ sel_idx, const float *__restrict__ sel_w,
-    int32_t fixed_expert, int32_t topk, int32_t n_slots, int64_t inter, int64_t hidden, MvGeo g, int32_t J,
-    HxpArgs hx, float *__restrict__ y) {
+// y[d] (+)= w_slot * (down_slot[d, :] . h_slot) for the T*S rows d of one tile.
+template <int T>
+__device__ __forceinline__ void down_tile(const MoeProj &P, int64_t e, int64_t inter, int64_t hidden,
+                                          const TileGeo &g, int64_t r0, const float *__restrict__ hs, float w,
+                                          float *__restrict__ y, bool accumulate) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    const int64_t rows_per = (int64_t)g.S * J;
-    const int64_t tiles = (hidden + rows_per - 1) / rows_per;
-    const int32_t slot = (int32_t)(blockIdx.x / tiles);
-    const int64_t r0 = (blockIdx.x % tiles) * rows_per;
-    const bool routed = slot < topk;
-    const MoeProj &P = routed ? down : s_down;
+    const TileSmem m = tile_smem(smem, inter);
+    const int u = threadIdx.x % g.U, s = threadIdx.x / g.U;
+    XStage st;
+    xs_load(hs, inter, st);
+    TileData<T, 1> td;
+    const uint8_t *const Wm[1] = {P.base + e * P.stride};
+    tile_issue<T, 1>(Wm, P.row_bytes, hidden, r0, g, u, s, td);
+    xs_convert(st, inter, m);
+    __syncthreads();
+    XU X;
+    load_xu<T>(m.planes, m.xs, m.gs, inter, u >> 2, u & 3, X);
+    tile_dots<T, 1>(td, X, g, u, s, m.red);
+    __syncthreads();
+    const int i = threadIdx.x;
+    if (i < g.T * g.S && r0 + i < hidden) {
+        const float v = tile_row(m.red, 0, i, g);
+        if (accumulate)
+            atomicAdd(&y[r0 + i], w * v);
+        else
+            y[r0 + i] = w * v;
+    }
+}
+
+// grid = n_slots * g.tiles; h is [n_slots][inter] f32. With one slot and no
+// weights y is stored; otherwise every slot adds sel_w[slot] * its rows into
+// y (cleared by the gate/up launch): the routed weights, then the shared
+// gammas (the shared gamma scales the down output, src/sepia.c:3953-3957,
+// equal to scaling h before down as src/sepia.c:1441 does).
+template <int TR, int TS>
+__device__ __forceinline__ void ffn_down_body(const MoeProj &down, const MoeProj &s_down,
+                                              const int32_t *__restrict__ sel_idx, const float *__restrict__ sel_w,
+                                              int32_t fixed_expert, int32_t topk, int32_t n_slots, int64_t inter,
+                                              int64_t hidden, const TileGeo &g, const float *__restrict__ h,
+                                              float *__restrict__ y) {
+    const int32_t slot = (int32_t)(blockIdx.x / g.tiles);
+    const int64_t r0 = (int64_t)(blockIdx.x % g.tiles) * g.T * g.S;
     const int64_t e = slot_expert(sel_idx, fixed_expert, slot, topk);
     const float w = sel_w ? sel_w[slot] : 1.0f;
-    const bool accumulate = n_slots > 1;
-    MvSmem m;
-    m.red = (float *)smem;
-#define DN_CASE(TT, JJ)                                                                          \
-    if (P.type == TT && J == JJ) {                                                               \
-        ffn_down_tile<TT, JJ>(P, e, inter, hidden, g, slot, r0, hx, w, y, accumulate, m);        \
-        return;                                                                                  \
-    }
-    DN_CASE(ST_Q2_K, 2) DN_CASE(ST_Q2_K, 4) DN_CASE(ST_Q3_K, 2) DN_CASE(ST_Q3_K, 4)
-    DN_CASE(ST_Q4_K, 2) DN_CASE(ST_Q4_K, 4)
-#undef DN_CASE
+    const float *hs = h + (int64_t)slot * inter;
+    if (slot < topk)
+        down_tile<TR>(down, e, inter, hidden, g, r0, hs, w, y, n_slots > 1);
+    else
+        down_tile<TS>(s_down, e, inter, hidden, g, r0, hs, w, y, n_slots > 1);
 }
+
+#define SEPIA_FFN_DOWN(name, TR, TS)                                                                 \
+    extern "C" __global__ __launch_bounds__(MV_NT) void sepia_ffn_down_##name(                       \
+        MoeProj down, MoeProj s_down, const int32_t *__restrict__ sel_idx,                           \
+        const float *__restrict__ sel_w, int32_t fixed_expert, int32_t topk, int32_t n_slots,        \
+        int64_t inter, int64_t hidden, TileGeo g, const float *__restrict__ h, float *__restrict__ y) { \
+        ffn_down_body<TR, TS>(down, s_down, sel_idx, sel_w, fixed_expert, topk, n_slots, inter,     \
+                              hidden, g, h, y);                                                      \
+    }

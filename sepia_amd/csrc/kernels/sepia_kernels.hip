@@ -198,15 +198,28 @@ extern "C" __global__ __launch_bounds__(256) void sepia_sconv_hist_roll_f32(
 }
 
 // ------------------------------------------------------------------------
-// Split-K tile matvec with integer dot products (mv.h), per format and rows
-// per thread J.
+// Tile kernels with integer dot products (mv.h): the matvec per format, and
+// the expert-FFN launches per (routed, shared) format pair; gate/up comes in
+// two flavours, x as f32 (converted per workgroup) or as digit planes
+// written by the router launch (_xp).
 #include "mv.h"
-SEPIA_MV_KERNEL(q2_k, ST_Q2_K, 2)
-SEPIA_MV_KERNEL(q2_k, ST_Q2_K, 4)
-SEPIA_MV_KERNEL(q3_k, ST_Q3_K, 2)
-SEPIA_MV_KERNEL(q3_k, ST_Q3_K, 4)
-SEPIA_MV_KERNEL(q4_k, ST_Q4_K, 2)
-SEPIA_MV_KERNEL(q4_k, ST_Q4_K, 4)
+SEPIA_MV_KERNEL(q2_k, ST_Q2_K)
+SEPIA_MV_KERNEL(q3_k, ST_Q3_K)
+SEPIA_MV_KERNEL(q4_k, ST_Q4_K)
+
+#define SEPIA_FFN_PAIR(a, b, TA, TB)                                                              \
+    SEPIA_FFN_GATEUP(a##b, TA, TB, false)                                                         \
+    SEPIA_FFN_GATEUP(a##b##_xp, TA, TB, true)                                                     \
+    SEPIA_FFN_DOWN(a##b, TA, TB)
+SEPIA_FFN_PAIR(2, 2, ST_Q2_K, ST_Q2_K)
+SEPIA_FFN_PAIR(2, 3, ST_Q2_K, ST_Q3_K)
+SEPIA_FFN_PAIR(2, 4, ST_Q2_K, ST_Q4_K)
+SEPIA_FFN_PAIR(3, 2, ST_Q3_K, ST_Q2_K)
+SEPIA_FFN_PAIR(3, 3, ST_Q3_K, ST_Q3_K)
+SEPIA_FFN_PAIR(3, 4, ST_Q3_K, ST_Q4_K)
+SEPIA_FFN_PAIR(4, 2, ST_Q4_K, ST_Q2_K)
+SEPIA_FFN_PAIR(4, 3, ST_Q4_K, ST_Q3_K)
+SEPIA_FFN_PAIR(4, 4, ST_Q4_K, ST_Q4_K)
 
 #include "moe.h"
 #include "synth.h"

@@ -45,11 +45,14 @@ enum {
     K_MV_Q8_0, K_MV_Q2_K, K_MV_Q3_K, K_MV_Q4_K, K_MV_Q5_K, K_MV_Q6_K,
     K_MV_IQ2_XXS, K_MV_IQ2_XS, K_MV_IQ3_XXS, K_MV_IQ4_XS,
     K_MATVEC_F32, K_SILU_MUL, K_ADD, K_SCALE, K_COPY, K_TOUCH, K_RMSNORM, K_SOFTMAX,
-    K_SCONV, K_SCONV_HIST, K_MOE_SELECT, K_MOE_GATEUP, K_MOE_DOWN, K_SYNTH_FILL, K_SYNTH_F16,
-    K_MV_Q2_K_J2, K_MV_Q2_K_J4, K_MV_Q3_K_J2, K_MV_Q3_K_J4, K_MV_Q4_K_J2, K_MV_Q4_K_J4,
-    K_FFN_GATEUP, K_FFN_DOWN,
-    K_COUNT
+    K_SCONV, K_SCONV_HIST, K_MOE_ROUTE, K_MOE_GATEUP, K_MOE_DOWN, K_SYNTH_FILL, K_SYNTH_F16,
+    K_TILE_Q2_K, K_TILE_Q3_K, K_TILE_Q4_K,
+    /* expert-FFN tile kernels: 9 (routed, shared) format pairs over
+     * {Q2_K, Q3_K, Q4_K}, each gate/up (x f32), gate/up (x planes), down */
+    K_FFN_BASE,
+    K_COUNT = K_FFN_BASE + 27
 };
+#define FFN_NAMES(p) "sepia_ffn_gateup_" p, "sepia_ffn_gateup_" p "_xp", "sepia_ffn_down_" p
 static const char *const k_names[K_COUNT] = {
     "sepia_dequant_rows_q8_0", "sepia_dequant_rows_q2_k", "sepia_dequant_rows_q3_k",
     "sepia_dequant_rows_q4_k", "sepia_dequant_rows_q5_k", "sepia_dequant_rows_q6_k",
@@ -61,12 +64,13 @@ static const char *const k_names[K_COUNT] = {
     "sepia_matvec_generic_iq4_xs",
     "sepia_matvec_f32", "sepia_silu_mul_f32", "sepia_add_f32", "sepia_scale_f32", "sepia_copy_f32",
     "sepia_touch_f32", "sepia_rmsnorm_f32", "sepia_softmax_f32", "sepia_sconv_f32",
-    "sepia_sconv_hist_roll_f32", "sepia_moe_select", "sepia_moe_gateup_generic", "sepia_moe_down_generic",
+    "sepia_sconv_hist_roll_f32", "sepia_moe_route", "sepia_moe_gateup_generic", "sepia_moe_down_generic",
     "sepia_synth_fill", "sepia_synth_patch_f16",
-    "sepia_mv_q2_k_j2", "sepia_mv_q2_k_j4", "sepia_mv_q3_k_j2", "sepia_mv_q3_k_j4",
-    "sepia_mv_q4_k_j2", "sepia_mv_q4_k_j4",
-    "sepia_ffn_gateup", "sepia_ffn_down",
+    "sepia_mv_q2_k", "sepia_mv_q3_k", "sepia_mv_q4_k",
+    FFN_NAMES("22"), FFN_NAMES("23"), FFN_NAMES("24"), FFN_NAMES("32"), FFN_NAMES("33"), FFN_NAMES("34"),
+    FFN_NAMES("42"), FFN_NAMES("43"), FFN_NAMES("44"),
 };
+#undef FFN_NAMES
 
 /* GGUF block geometry (reference src/quants.c:46-51; tools/gguf_inspect.py:109-117). */
 typedef struct {
@@ -76,42 +80,59 @@ typedef struct {
     int parts;      /* 32-weight parts per block (dequant threads per block) */
     int k_dq, k_mv; /* kernel ids, -1 if none */
     int f16_off[2]; /* byte offsets of f16 scale fields, -1 = none */
-    int k_tile[2];  /* split-K tile kernels (J = 2, 4 rows per thread), -1 if none */
+    int k_tile;     /* tile matvec kernel (kernels/mv.h), -1 if none */
     int align;      /* byte alignment the tile kernels need for a matrix base */
 } TypeInfo;
 static const TypeInfo k_types[] = {
-    { 1, 1, 2, 1, K_DQ_F16, -1, { -1, -1 }, { -1, -1 }, 1 },
-    { 8, 32, 34, 1, K_DQ_Q8_0, K_MV_Q8_0, { 0, -1 }, { -1, -1 }, 1 },
-    { 10, 256, 84, 8, K_DQ_Q2_K, K_MV_Q2_K, { 80, 82 }, { K_MV_Q2_K_J2, K_MV_Q2_K_J4 }, 4 },
-    { 11, 256, 110, 8, K_DQ_Q3_K, K_MV_Q3_K, { 108, -1 }, { K_MV_Q3_K_J2, K_MV_Q3_K_J4 }, 2 },
-    { 12, 256, 144, 8, K_DQ_Q4_K, K_MV_Q4_K, { 0, 2 }, { K_MV_Q4_K_J2, K_MV_Q4_K_J4 }, 4 },
-    { 13, 256, 176, 8, K_DQ_Q5_K, K_MV_Q5_K, { 0, 2 }, { -1, -1 }, 1 },
-    { 14, 256, 210, 8, K_DQ_Q6_K, K_MV_Q6_K, { 208, -1 }, { -1, -1 }, 1 },
-    { 16, 256, 66, 8, K_DQ_IQ2_XXS, K_MV_IQ2_XXS, { 0, -1 }, { -1, -1 }, 1 },
-    { 17, 256, 74, 8, K_DQ_IQ2_XS, K_MV_IQ2_XS, { 0, -1 }, { -1, -1 }, 1 },
-    { 18, 256, 98, 8, K_DQ_IQ3_XXS, K_MV_IQ3_XXS, { 0, -1 }, { -1, -1 }, 1 },
-    { 23, 256, 136, 8, K_DQ_IQ4_XS, K_MV_IQ4_XS, { 0, -1 }, { -1, -1 }, 1 },
+    { 1, 1, 2, 1, K_DQ_F16, -1, { -1, -1 }, -1, 1 },
+    { 8, 32, 34, 1, K_DQ_Q8_0, K_MV_Q8_0, { 0, -1 }, -1, 1 },
+    { 10, 256, 84, 8, K_DQ_Q2_K, K_MV_Q2_K, { 80, 82 }, K_TILE_Q2_K, 4 },
+    { 11, 256, 110, 8, K_DQ_Q3_K, K_MV_Q3_K, { 108, -1 }, K_TILE_Q3_K, 2 },
+    { 12, 256, 144, 8, K_DQ_Q4_K, K_MV_Q4_K, { 0, 2 }, K_TILE_Q4_K, 4 },
+    { 13, 256, 176, 8, K_DQ_Q5_K, K_MV_Q5_K, { 0, 2 }, -1, 1 },
+    { 14, 256, 210, 8, K_DQ_Q6_K, K_MV_Q6_K, { 208, -1 }, -1, 1 },
+    { 16, 256, 66, 8, K_DQ_IQ2_XXS, K_MV_IQ2_XXS, { 0, -1 }, -1, 1 },
+    { 17, 256, 74, 8, K_DQ_IQ2_XS, K_MV_IQ2_XS, { 0, -1 }, -1, 1 },
+    { 18, 256, 98, 8, K_DQ_IQ3_XXS, K_MV_IQ3_XXS, { 0, -1 }, -1, 1 },
+    { 23, 256, 136, 8, K_DQ_IQ4_XS, K_MV_IQ4_XS, { 0, -1 }, -1, 1 },
 };
 
-/* Full-row tile geometry (kernels/mv.h): 384 threads; a row of U 64-weight
- * units takes U lanes, S = 384 / U rows run side by side, J rows per lane. */
+/* Tile geometry (kernels/mv.h, struct TileGeo): 384-thread workgroups; a
+ * row of U = in_dim / 64 units takes U lanes (U a multiple of 16 dividing
+ * 384), S = 384 / U rows run side by side and a workgroup walks T <= 3 such
+ * steps. x is converted per workgroup, at most two 16-column segments per
+ * thread. */
 #define TILE_NT 384
-#define TILE_MAX_COLS 9216   /* x staged per workgroup: 6 quads per thread */
+#define TILE_TMAX 3
+#define TILE_MAX_COLS (2 * 16 * TILE_NT)
+#define TILE_CUS 256    /* MI355X compute units: the grid aims at one workgroup per CU */
 typedef struct {
-    int32_t U, S, seg, pad;
-} MvGeo;
+    int32_t U, S, T, tiles;
+} TileGeo;
 
-/* Geometry for rows of n_blocks 256-weight blocks; 0 if U does not divide 384. */
-static int tile_geo(int64_t n_blocks, MvGeo *g) {
+static int g_opt_tile = 1;   /* sepia_hip_set_option("tile", 0) forces the generic kernels */
+static int g_opt_tile_t = 0; /* sepia_hip_set_option("tile_t", T) forces T steps per workgroup */
+
+/* Geometry for `mats` stacked copies of a [rows, 256 * n_blocks] matrix; 0
+ * when the row length does not fit the tile kernels. T is the smallest step
+ * count that keeps the whole launch within about one workgroup per CU. */
+static int tile_geo(int64_t n_blocks, int64_t rows, int64_t mats, TileGeo *g) {
     const int64_t U = 4 * n_blocks;
-    if (U <= 0 || U > TILE_NT || TILE_NT % U) return 0;
+    if (U <= 0 || U % 16 || TILE_NT % U || 256 * n_blocks > TILE_MAX_COLS || rows <= 0) return 0;
     g->U = (int32_t)U;
     g->S = (int32_t)(TILE_NT / U);
-    int seg = 64;
-    while (U % seg) seg >>= 1;
-    g->seg = seg;
-    g->pad = 0;
+    const int64_t steps = (rows + g->S - 1) / g->S;
+    int64_t T = (mats * steps + TILE_CUS - 1) / TILE_CUS;
+    if (g_opt_tile_t) T = g_opt_tile_t;
+    g->T = (int32_t)(T < 1 ? 1 : (T > TILE_TMAX ? TILE_TMAX : T));
+    g->tiles = (int32_t)((steps + g->T - 1) / g->T);
     return 1;
+}
+
+/* Dynamic LDS of a tile workgroup: x planes, scales and sums of n staged
+ * columns, then `mats` matrices' row partials. */
+static size_t tile_lds(int64_t n_staged, const TileGeo *g, int mats) {
+    return (size_t)(3 * n_staged + 2 * (n_staged / 16) * 4) + 4 * (size_t)(mats * g->T * g->S * (g->U / 16));
 }
 
 static int g_available;
@@ -818,11 +839,8 @@ int sepia_gpu_selftest_touch(SepiaGpuBuf *buf, size_t n_floats) {
 
 /* --------------------------------------------------------- quantized ---- */
 /* Tuning switches (sepia_hip_set_option): "tile" 0 forces the generic
- * one-wave-per-row kernels; "tile_j" 2 or 4 forces the rows per thread of the
- * split-K tile kernels (0 = automatic). */
-static int g_opt_tile = 1;
-static int g_opt_tile_j = 0;
-
+ * one-wave-per-row kernels; "tile_t" 1..3 forces the row steps per
+ * workgroup of the tile kernels (0 = automatic). */
 int sepia_hip_set_option(const char *name, int value) {
     if (!name) {
         LOG("set_option: NULL name");
@@ -832,33 +850,20 @@ int sepia_hip_set_option(const char *name, int value) {
         g_opt_tile = value;
         return 1;
     }
-    if (strcmp(name, "tile_j") == 0 && (value == 0 || value == 2 || value == 4)) {
-        g_opt_tile_j = value;
+    if (strcmp(name, "tile_t") == 0 && value >= 0 && value <= TILE_TMAX) {
+        g_opt_tile_t = value;
         return 1;
     }
     LOG("set_option: unknown option %s=%d", name, value);
     return 0;
 }
 
-/* Rows per thread (2 or 4) of the split-K tile kernel for this matrix, or 0
- * when the generic kernel must run: the format has no tile decoder, the row
- * is not a whole number of 4-block column slices, the base is not aligned as
- * the decoder loads it, or there are more row tiles than arrival counters. */
-static int tile_plan(const TypeInfo *ti, int64_t n_blocks, uintptr_t base, int64_t rows, MvGeo *g) {
-    if (!g_opt_tile || ti->k_tile[0] < 0 || base % (uintptr_t)ti->align || n_blocks * 256 > TILE_MAX_COLS ||
-        !tile_geo(n_blocks, g))
-        return 0;
-    int J = g_opt_tile_j;
-    if (!J) J = (rows + 4 * g->S - 1) / (4 * g->S) >= 256 ? 4 : 2;
-    return J;
+/* 1 if the tile matvec runs this matrix: the format has a tile decoder, the
+ * base is aligned as the decoder loads it and the row length fits. */
+static int tile_plan(const TypeInfo *ti, int64_t n_blocks, uintptr_t base, int64_t rows, TileGeo *g) {
+    return g_opt_tile && ti->k_tile >= 0 && base % (uintptr_t)ti->align == 0 && tile_geo(n_blocks, rows, 1, g);
 }
 
-/* Dynamic LDS of a tile workgroup: x planes of n columns (when staged),
- * `mats` matrices' row partials, `extra` floats. */
-static size_t tile_lds(int64_t n_staged, const MvGeo *g, int J, int mats, int extra) {
-    const size_t red = (size_t)(mats * g->S * J * (g->U / g->seg) + 3) & ~(size_t)3;
-    return (size_t)(3 * n_staged + 2 * (n_staged / 16) * 4) + 4 * (red + (size_t)extra);
-}
 int sepia_gpu_matvec_q(int ggml_type, SepiaGpuBuf *w, size_t w_off, SepiaGpuBuf *x, SepiaGpuBuf *y,
                        int64_t out_dim, int64_t in_dim) {
     const char *op = "matvec_q";
@@ -883,13 +888,11 @@ int sepia_gpu_matvec_q(int ggml_type, SepiaGpuBuf *w, size_t w_off, SepiaGpuBuf 
         return 0;
     if (!need_batch(op) || !prep_in(w, op) || !prep_in(x, op) || !prep_out(y, op)) return 0;
     const uint8_t *wp = w->dev + w_off;
-    MvGeo geo;
-    int J = tile_plan(ti, n_blocks, (uintptr_t)wp, out_dim, &geo);
-    if (J) {
+    TileGeo geo;
+    if (tile_plan(ti, n_blocks, (uintptr_t)wp, out_dim, &geo)) {
         int64_t n = in_dim;
-        int64_t tiles = (out_dim + (int64_t)geo.S * J - 1) / ((int64_t)geo.S * J);
         void *args[] = { &wp, &row_bytes, &out_dim, &n, &geo, &x->dev, &y->dev };
-        return launch_lds(ti->k_tile[J == 4], (unsigned)tiles, TILE_NT, tile_lds(n, &geo, J, 1, 0), args, op);
+        return launch_lds(ti->k_tile, (unsigned)geo.tiles, TILE_NT, tile_lds(n, &geo, 1), args, op);
     }
     void *args[] = { &wp, &row_bytes, &n_blocks, &x->dev, &y->dev, &out_dim };
     return launch(ti->k_mv, blocks_for(out_dim, 4), 256, args, op);
@@ -1018,23 +1021,18 @@ static int moe_proj(const char *op, const char *what, const SepiaExpertTensor *t
     return 1;
 }
 
-/* Mirrors struct HxpArgs in kernels/mv.h. */
+/* Mirrors struct XpArgs in kernels/mv.h: x in digit-plane form. */
 typedef struct {
-    int8_t *planes;
-    float *scale;
-    float *sum;
-} HxpArgs;
+    const int8_t *planes;
+    const float *xs;
+    const float *gs;
+} XpArgs;
 
-/* Scratch bytes the FFN launch needs for n_slots activation vectors of
- * length I: f32 for the generic kernels or XP form (3 planes + scale + sum
- * per 16 columns) for the tile kernels, whichever is larger. */
-static size_t ffn_scratch_bytes(int n_slots, int64_t I) {
-    const size_t f32 = (size_t)n_slots * (size_t)I * 4;
-    const size_t xp = (size_t)n_slots * ((size_t)I * 3 + (size_t)(I / 16) * 8) + 512;
-    return f32 > xp ? f32 : xp;
-}
+/* Scratch bytes for n_slots f32 activation vectors of length I. */
+static size_t ffn_scratch_bytes(int n_slots, int64_t I) { return (size_t)n_slots * (size_t)I * 4; }
 
-static int tile_type(int t) { return t == SEPIA_T_Q2_K || t == SEPIA_T_Q3_K || t == 12; }
+/* Index of a format among the tile kernels' {Q2_K, Q3_K, Q4_K}, -1 if none. */
+static int tile_code(int t) { return t == SEPIA_T_Q2_K ? 0 : (t == SEPIA_T_Q3_K ? 1 : (t == 12 ? 2 : -1)); }
 
 static int proj_aligned(const MoeProj *p) {
     const TypeInfo *ti = type_info(p->type);
@@ -1045,50 +1043,39 @@ static int proj_aligned(const MoeProj *p) {
 /* The SwiGLU expert FFN over n_slots = topk + n_shared slots: routed slot s
  * uses expert sel_idx[s] (or fixed + s when sel_idx is NULL), then come the
  * shared experts. One slot without weights stores y; several slots add
- * sel_w[s] * their output into y. Uses the tile kernels (integer dots, h
- * handed over in XP form) when every projection has a tile decoder and the
- * shapes fit, else the generic one-wave-per-row kernels. */
+ * sel_w[s] * their output into y. Uses the tile kernels (integer dots) when
+ * every projection has a tile decoder and the shapes fit, else the generic
+ * one-wave-per-row kernels. xp, when set, holds x in digit-plane form. */
 static int ffn_launch(const char *op, const MoeProj *g, const MoeProj *u, const MoeProj *d, const MoeProj *sg,
                       const MoeProj *su, const MoeProj *sd, const int32_t *sel_idx, const float *sel_w, int32_t fixed,
-                      int32_t topk, int32_t n_shared, int64_t H, int64_t I, const uint8_t *xdev, float *ydev,
-                      uint8_t *scr) {
+                      int32_t topk, int32_t n_shared, int64_t H, int64_t I, const uint8_t *xdev, const XpArgs *xp,
+                      float *ydev, uint8_t *scr) {
     int32_t n_slots = topk + n_shared;
-    MvGeo gu_geo, dn_geo;
-    int tile = g_opt_tile && H % 256 == 0 && I % 256 == 0 && H <= TILE_MAX_COLS && tile_geo(H / 256, &gu_geo) &&
-               tile_geo(I / 256, &dn_geo) && tile_type(g->type) && g->type == u->type && tile_type(d->type) &&
-               proj_aligned(g) && proj_aligned(u) && proj_aligned(d);
+    const int cr = tile_code(g->type), cdr = tile_code(d->type);
+    const int cs = n_shared > 0 ? tile_code(sg->type) : cr, cds = n_shared > 0 ? tile_code(sd->type) : cdr;
+    TileGeo gu, dn;
+    int tile = g_opt_tile && cr >= 0 && cs >= 0 && cdr >= 0 && cds >= 0 && g->type == u->type && H % 256 == 0 &&
+               I % 256 == 0 && proj_aligned(g) && proj_aligned(u) && proj_aligned(d) &&
+               tile_geo(H / 256, I, 2 * (int64_t)n_slots, &gu) && tile_geo(I / 256, H, n_slots, &dn);
     if (tile && n_shared > 0)
-        tile = tile_type(sg->type) && sg->type == su->type && tile_type(sd->type) && proj_aligned(sg) &&
-               proj_aligned(su) && proj_aligned(sd);
-    int32_t j_gu = 0, j_dn = 0;
-    if (tile) {
-        j_gu = (gu_geo.S * 2) % 16 == 0 ? 2 : ((gu_geo.S * 4) % 16 == 0 ? 4 : 0);
-        j_dn = g_opt_tile_j ? g_opt_tile_j : ((H + 4 * dn_geo.S - 1) / (4 * dn_geo.S) * n_slots >= 256 ? 4 : 2);
-        if (g_opt_tile_j && (gu_geo.S * g_opt_tile_j) % 16 == 0) j_gu = g_opt_tile_j;
-        tile = j_gu != 0;
-    }
+        tile = sg->type == su->type && proj_aligned(sg) && proj_aligned(su) && proj_aligned(sd);
     int64_t inter = I, hid = H;
+    float *h = (float *)scr;
     if (tile) {
-        HxpArgs hx;
-        hx.planes = (int8_t *)scr;
-        hx.scale = (float *)(scr + (((size_t)n_slots * 3 * (size_t)I + 255) & ~(size_t)255));
-        hx.sum = hx.scale + (size_t)n_slots * (size_t)(I / 16);
-        float *no_h32 = NULL;
+        XpArgs xa = { NULL, NULL, NULL };
+        if (xp) xa = *xp;
         float *y_zero = n_slots > 1 ? ydev : NULL;
         int64_t y_n = H;
-        const int64_t gu_rows = (int64_t)gu_geo.S * j_gu, dn_rows = (int64_t)dn_geo.S * j_dn;
-        const int64_t gu_tiles = (I + gu_rows - 1) / gu_rows, dn_tiles = (H + dn_rows - 1) / dn_rows;
+        const int k_gu = K_FFN_BASE + 3 * (3 * cr + cs) + (xp ? 1 : 0);
+        const int k_dn = K_FFN_BASE + 3 * (3 * cdr + cds) + 2;
         void *a_gu[] = { (void *)g, (void *)u, (void *)sg, (void *)su, &sel_idx, &fixed, &topk, &inter, &hid,
-                         &gu_geo, &j_gu, &xdev, &hx, &no_h32, &y_zero, &y_n };
-        if (!launch_lds(K_FFN_GATEUP, (unsigned)(n_slots * gu_tiles), TILE_NT,
-                        tile_lds(H, &gu_geo, j_gu, 2, (int)gu_rows), a_gu, op))
+                         &gu, &xdev, &xa, &h, &y_zero, &y_n };
+        if (!launch_lds(k_gu, (unsigned)(n_slots * gu.tiles), TILE_NT, tile_lds(xp ? 0 : H, &gu, 2), a_gu, op))
             return 0;
         void *a_dn[] = { (void *)d, (void *)sd, &sel_idx, &sel_w, &fixed, &topk, &n_slots, &inter, &hid,
-                         &dn_geo, &j_dn, &hx, &ydev };
-        return launch_lds(K_FFN_DOWN, (unsigned)(n_slots * dn_tiles), TILE_NT, tile_lds(0, &dn_geo, j_dn, 1, 0),
-                          a_dn, op);
+                         &dn, &h, &ydev };
+        return launch_lds(k_dn, (unsigned)(n_slots * dn.tiles), TILE_NT, tile_lds(I, &dn, 1), a_dn, op);
     }
-    float *h = (float *)scr;
     void *a_gu[] = { (void *)g, (void *)u, (void *)sg, (void *)su, &sel_idx, &fixed, &topk, &inter, &xdev, &h };
     if (!launch(K_MOE_GATEUP, (unsigned)(n_slots * ((I + 3) / 4)), 256, a_gu, op)) return 0;
     void *a_dn[] = { (void *)d, (void *)sd, &sel_idx, &sel_w, &fixed, &topk, &n_shared, &inter, &hid, &h, &ydev };
@@ -1134,15 +1121,19 @@ int sepia_gpu_moe_decode(const SepiaMoeLayerDesc *L, SepiaGpuBuf *x, SepiaGpuBuf
     }
     if (!need_batch(op)) return 0;
 
-    /* scratch: logits | sel_idx | sel_w | FFN intermediates, each 256-byte aligned */
+    /* scratch: logits | sel_idx | sel_w | x planes | FFN activations, each
+     * 256-byte aligned; the router's arrival counter is the first word of
+     * the counter region */
     const size_t o_logits = 0;
     const size_t o_idx = o_logits + (((size_t)n_tot * 4 + 255) & ~(size_t)255);
     const size_t o_w = o_idx + 256;
-    const size_t o_h = o_w + 256;
+    const size_t o_xp = o_w + 256;
+    const size_t o_h = o_xp + (((size_t)H * 3 + (size_t)(H / 16) * 8 + 255) & ~(size_t)255);
     uint8_t *s = (uint8_t *)scratch(o_h + ffn_scratch_bytes(n_slots, I), op);
     if (!s) return 0;
     float *logits = (float *)(s + o_logits), *sel_w = (float *)(s + o_w);
     int32_t *sel_idx = (int32_t *)(s + o_idx);
+    uint32_t *counter = (uint32_t *)g_scratch;
 
     SepiaGpuBuf *ins[] = { L->router_w, L->router_bias, x, L->gate.buf, L->up.buf, L->down.buf, L->s_gate.buf,
                            L->s_up.buf, L->s_down.buf };
@@ -1152,17 +1143,24 @@ int sepia_gpu_moe_decode(const SepiaMoeLayerDesc *L, SepiaGpuBuf *x, SepiaGpuBuf
 
     const float *rw = (const float *)(L->router_w->dev + L->router_w_off);
     const float *rb = (const float *)(L->router_bias->dev + L->router_bias_off);
-    int64_t n_tot64 = n_tot, ld = H, hid = H;
-    void *a_router[] = { &rw, &ld, &x->dev, &logits, &n_tot64, &hid };
-    if (!launch(K_MATVEC_F32, blocks_for(n_tot, 4), 256, a_router, op)) return 0;
-
+    /* the router also writes x's digit planes when its loads are 16-byte
+     * vectors (aligned router rows) and x splits into 16-column segments */
+    const int xp_ok = ((uintptr_t)rw % 16) == 0 && H % 16 == 0 && H <= 8192;   /* kernels/moe.h RT_C4 */
+    XpArgs xp;
+    xp.planes = (const int8_t *)(s + o_xp);
+    xp.xs = (const float *)(s + o_xp + (size_t)H * 3);
+    xp.gs = xp.xs + H / 16;
+    int8_t *xp_planes = xp_ok ? (int8_t *)xp.planes : NULL;
+    float *xp_xs = (float *)xp.xs, *xp_gs = (float *)xp.gs;
+    int64_t ld = H, hid = H;
     int32_t nr = L->n_routed, ns = L->n_shared, tk = L->topk;
-    float rs = L->route_scale, gs = L->global_scale;
-    void *a_sel[] = { &logits, &rb, &nr, &ns, &tk, &rs, &gs, &sel_idx, &sel_w };
-    if (!launch(K_MOE_SELECT, 1, 256, a_sel, op)) return 0;
+    float rs = L->route_scale, gsc = L->global_scale;
+    void *a_route[] = { &rw, &ld, &rb, &x->dev, &hid, &nr, &ns, &tk, &rs, &gsc, &logits, &sel_idx, &sel_w, &counter,
+                        &xp_planes, &xp_xs, &xp_gs };
+    if (!launch(K_MOE_ROUTE, (unsigned)((n_tot + 1) / 2), 256, a_route, op)) return 0;
 
-    if (!ffn_launch(op, &g, &u, &d, &sg, &su, &sd, sel_idx, sel_w, 0, tk, ns, H, I, x->dev, (float *)y->dev,
-                    s + o_h))
+    if (!ffn_launch(op, &g, &u, &d, &sg, &su, &sd, sel_idx, sel_w, 0, tk, ns, H, I, x->dev, xp_ok ? &xp : NULL,
+                    (float *)y->dev, s + o_h))
         return 0;
 
     if (route_out) {
@@ -1198,6 +1196,6 @@ int sepia_gpu_expert_ffn(const SepiaExpertTensor *gate, const SepiaExpertTensor 
     if (!prep_in(gate->buf, op) || !prep_in(up->buf, op) || !prep_in(down->buf, op) || !prep_in(x, op) ||
         !prep_out(y, op))
         return 0;
-    return ffn_launch(op, &g, &u, &d, &none, &none, &none, NULL, NULL, expert, 1, 0, hidden, inter, x->dev,
+    return ffn_launch(op, &g, &u, &d, &none, &none, &none, NULL, NULL, expert, 1, 0, hidden, inter, x->dev, NULL,
                       (float *)y->dev, scr);
 }

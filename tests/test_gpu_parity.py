@@ -29,14 +29,21 @@ def dev():
     return hip.Device()
 
 
-def assert_close(got, want, tol=TOL, what=""):
-    """max|got - want| <= tol * ||want||_inf, and the reference's GPU gate."""
+def assert_close(got, want, tol=TOL, what="", gate=True):
+    """max|got - want| <= tol * ||want||_inf (BASELINE's bar) and, for single
+    ops (gate=True), the reference's per-op GPU gate (src/sepia.c:4557-4589:
+    |got - want| / max(|want|, 1e-3 * max|want|) <= 2e-4). Composite outputs
+    (the expert FFN, the MoE layer, whose slots add into y with atomics in
+    completion order) are held to BASELINE's bar only: the reference applies
+    its gate per op kind, never to a whole layer."""
     got = np.asarray(got, dtype=np.float64)
     want = np.asarray(want, dtype=np.float64)
     assert np.all(np.isfinite(got)), what
     scale = float(np.max(np.abs(want))) if want.size else 0.0
     err = float(np.max(np.abs(got - want))) if want.size else 0.0
     assert err <= tol * scale, "%s: max|diff| %.3e > %.1e * %.3e" % (what, err, tol, scale)
+    if not gate:
+        return
     floor = max(1e-6, 1e-3 * scale)
     rel = np.abs(got - want) / np.maximum(np.abs(want), floor)
     assert float(rel.max()) <= 2e-4, "%s: reference gate rel %.3e" % (what, float(rel.max()))
@@ -202,24 +209,24 @@ def test_matvec_q_config_shapes(dev, orc, name, t, out_dim, in_dim):
 
 @pytest.fixture
 def kernel_path(dev, request):
-    """Force one kernel family: the generic per-row kernel, or the split-K tile
-    kernel with 2 or 4 rows per thread."""
+    """Force one kernel family: the generic per-row kernel, or the tile kernels
+    with 1, 2 or 3 row steps per workgroup."""
     L = dev.L
     mode = request.param
     if mode == "generic":
         assert L.sepia_hip_set_option(b"tile", 0) == 1
     else:
-        assert L.sepia_hip_set_option(b"tile_j", {"j2": 2, "j4": 4}[mode]) == 1
+        assert L.sepia_hip_set_option(b"tile_t", {"t1": 1, "t2": 2, "t3": 3}[mode]) == 1
     yield mode
     L.sepia_hip_set_option(b"tile", 1)
-    L.sepia_hip_set_option(b"tile_j", 0)
+    L.sepia_hip_set_option(b"tile_t", 0)
 
 
 TILE_SHAPES = [(10, 3072, 6144), (11, 6144, 3072), (12, 4096, 4096), (12, 33, 1024), (10, 17, 2048),
-               (11, 1, 3072), (12, 200, 6144)]
+               (11, 1, 3072), (12, 200, 6144), (10, 50, 8192), (12, 40, 12288), (11, 70, 12288)]
 
 
-@pytest.mark.parametrize("kernel_path", ["generic", "j2", "j4"], indirect=True)
+@pytest.mark.parametrize("kernel_path", ["generic", "t1", "t2", "t3"], indirect=True)
 @pytest.mark.parametrize("t,out_dim,in_dim", TILE_SHAPES, ids=lambda v: str(v))
 def test_matvec_q_kernel_paths(dev, orc, kernel_path, t, out_dim, in_dim):
     check_matvec(dev, orc, t, out_dim, in_dim, seed=out_dim * 7 + t)
@@ -368,8 +375,9 @@ def test_selftest_touch_and_wrap(dev):
 
 
 # ------------------------------------------------------------------- MoE
-def make_layer(dev, rng, hidden, inter, n_routed, n_shared, tg, tu, td, ts):
-    """Shared buffers with seeded host data; returns (desc, spec, keep)."""
+def make_layer(dev, rng, hidden, inter, n_routed, n_shared, tg, tu, td, ts, rw_off=0):
+    """Shared buffers with seeded host data; returns (desc, spec, keep). The
+    router matrix starts rw_off bytes into its buffer."""
     gate = [synth.random_matrix(tg, inter, hidden, rng) for _ in range(n_routed)]
     up = [synth.random_matrix(tu, inter, hidden, rng) for _ in range(n_routed)]
     down = [synth.random_matrix(td, hidden, inter, rng) for _ in range(n_routed)]
@@ -380,12 +388,14 @@ def make_layer(dev, rng, hidden, inter, n_routed, n_shared, tg, tu, td, ts):
     rb = rng.uniform(-0.1, 0.1, n_routed).astype(np.float32)
     bufs = {k: dev.shared_from(np.concatenate(v)) for k, v in
             dict(gate=gate, up=up, down=down, s_gate=sg, s_up=su, s_down=sd).items()}
-    bufs["rw"] = dev.shared_from(rw)
+    bufs["rw"] = dev.alloc(rw.nbytes + rw_off)
+    dev.upload(bufs["rw"], rw, offset=rw_off)
     bufs["rb"] = dev.shared_from(rb)
     d = hip.MoeLayerDesc()
     d.hidden, d.inter, d.n_routed, d.n_shared, d.topk = hidden, inter, n_routed, n_shared, 6
     d.route_scale, d.global_scale = 8.0, 1.0
     d.router_w, d.router_bias = bufs["rw"], bufs["rb"]
+    d.router_w_off = rw_off
     for name, t, lst in (("gate", tg, gate), ("up", tu, up), ("down", td, down),
                          ("s_gate", ts, sg), ("s_up", ts, su), ("s_down", ts, sd)):
         setattr(d, name, hip.ExpertTensor(bufs[name], 0, lst[0].nbytes, t))
@@ -440,6 +450,81 @@ def test_moe_decode_small(dev, orc, types, seed):
     chosen = check_route(orc, spec, logits, idx, w)
     if chosen != list(idx_ref):
         y_ref, _, _, _ = orc.moe_layer(spec, x, force_idx=chosen, threads=THREADS)
-    assert_close(y, y_ref, what="moe small")
+    assert_close(y, y_ref, what="moe small", gate=False)
     for b in bufs.values():
+        dev.free(b)
+
+
+@pytest.mark.parametrize("kernel_path", ["generic", "t1", "t3"], indirect=True)
+@pytest.mark.parametrize("types", [(10, 10, 11, 12), (12, 12, 12, 10), (11, 11, 10, 11)],
+                         ids=["q2k_q3k_q4k", "q4k_q4k_q2k", "q3k_q2k_q3k"])
+def test_moe_decode_tile_shapes(dev, orc, kernel_path, types):
+    """Tile-eligible layer (hidden 2048, inter 1024): router + x planes +
+    mixed-format gate/up and down launches."""
+    rng = np.random.default_rng(zlib.crc32(repr(types).encode()) & 0xFFFF)
+    tg, tu, td, ts = types
+    desc, spec, bufs = make_layer(dev, rng, hidden=2048, inter=1024, n_routed=16, n_shared=2,
+                                  tg=tg, tu=tu, td=td, ts=ts)
+    x = synth.normal_vector(rng, 2048)
+    y, idx, w = run_moe(dev, desc, x)
+    y_ref, logits, idx_ref, w_ref = orc.moe_layer(spec, x, threads=THREADS)
+    chosen = check_route(orc, spec, logits, idx, w)
+    if chosen != list(idx_ref):
+        y_ref, _, _, _ = orc.moe_layer(spec, x, force_idx=chosen, threads=THREADS)
+    assert_close(y, y_ref, what="moe tile %s" % kernel_path, gate=False)
+    for b in bufs.values():
+        dev.free(b)
+
+
+@pytest.mark.parametrize("rw_off", [0, 4])
+def test_moe_decode_c3_shape(dev, orc, rw_off):
+    """BASELINE configs[2] shapes (hidden 6144, inter 3072, Q2_K/Q3_K routed,
+    Q4_K shared, top-6) with 16 routed experts resident; rw_off 4 takes the
+    router's unaligned path (x then reaches gate/up as f32)."""
+    rng = np.random.default_rng(300 + rw_off)
+    desc, spec, bufs = make_layer(dev, rng, hidden=6144, inter=3072, n_routed=16, n_shared=2,
+                                  tg=10, tu=10, td=11, ts=12, rw_off=rw_off)
+    x = synth.normal_vector(rng, 6144)
+    y, idx, w = run_moe(dev, desc, x)
+    y_ref, logits, idx_ref, w_ref = orc.moe_layer(spec, x, threads=THREADS)
+    chosen = check_route(orc, spec, logits, idx, w)
+    if chosen != list(idx_ref):
+        y_ref, _, _, _ = orc.moe_layer(spec, x, force_idx=chosen, threads=THREADS)
+    assert_close(y, y_ref, what="moe c3 shape", gate=False)
+    for b in bufs.values():
+        dev.free(b)
+
+
+def run_expert_ffn(dev, tensors, n_experts, expert, hidden, inter, x):
+    import ctypes
+    xb = dev.shared_from(x)
+    yb = dev.alloc(hidden * 4)
+    g, u, d = (ctypes.byref(t) for t in tensors)
+    dev.run(dev.L.sepia_gpu_expert_ffn, g, u, d, n_experts, expert, hidden, inter, xb, yb)
+    y = dev.download(yb, hidden)
+    dev.free(xb)
+    dev.free(yb)
+    return y
+
+
+@pytest.mark.parametrize("kernel_path", ["generic", "t1", "t2", "t3"], indirect=True)
+@pytest.mark.parametrize("types,hidden,inter", [((10, 10, 11), 6144, 3072), ((12, 12, 12), 4096, 2048),
+                                                ((11, 11, 10), 2048, 1024)],
+                         ids=["c2_q2k_q3k", "q4k_4096", "q3k_q2k_2048"])
+def test_expert_ffn(dev, orc, kernel_path, types, hidden, inter):
+    """One routed expert (BASELINE configs[1] at its real shape first) picked
+    out of a stack of three."""
+    rng = np.random.default_rng(hidden + inter + types[0])
+    tg, tu, td = types
+    n_e, e = 3, 1
+    gate = [synth.random_matrix(tg, inter, hidden, rng) for _ in range(n_e)]
+    up = [synth.random_matrix(tu, inter, hidden, rng) for _ in range(n_e)]
+    down = [synth.random_matrix(td, hidden, inter, rng) for _ in range(n_e)]
+    bufs = [dev.shared_from(np.concatenate(v)) for v in (gate, up, down)]
+    tensors = [hip.ExpertTensor(b, 0, v[0].nbytes, t) for b, v, t in zip(bufs, (gate, up, down), types)]
+    x = synth.normal_vector(rng, hidden)
+    y = run_expert_ffn(dev, tensors, n_e, e, hidden, inter, x)
+    want = orc.expert_ffn(tg, gate[e], tu, up[e], td, down[e], hidden, inter, x, threads=THREADS)
+    assert_close(y, want, what="expert ffn %s" % kernel_path, gate=False)
+    for b in bufs:
         dev.free(b)
