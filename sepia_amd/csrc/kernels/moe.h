@@ -37,10 +37,8 @@ __device__ __forceinline__ float logsigmoid_f32(float x) {
 }
 
 // ------------------------------------------------------------------ router
-// Router logits, x in digit-plane form and the selection, in one launch.
-// Workgroup w computes router rows 2w, 2w + 1 (f32 FMA chains, 16-byte loads
-// issued up front) and converts x segments w, w + grid, ... into XP form for
-// the gate/up launch. Each workgroup publishes its logits with agent-scope
+// Router logits and the selection, in one launch. Workgroup w computes
+// router row w (f32 FMA chains, 16-byte loads issued up front). Each workgroup publishes its logits with agent-scope
 // stores, waits for them to complete and bumps an arrival counter; the
 // workgroup that arrives last sees every logit, runs the selection and puts
 // the counter back to zero (so the launch can be replayed from a graph).
@@ -53,7 +51,7 @@ __device__ __forceinline__ float logsigmoid_f32(float x) {
 // global_scale, rounded to float. Slots 0..topk-1 of sel_w are the routed
 // weights (router order), then the shared gammas.
 #define RT_NT 256
-#define RT_ROWS 2
+#define RT_ROWS 1
 #define RT_C4 8   // float4 chunks per thread and row: hidden <= 256 * 4 * 8
 
 // ---- wave-wide reductions without LDS: DPP within each 16-lane row, then
@@ -144,8 +142,7 @@ extern "C" __global__ __launch_bounds__(RT_NT) void sepia_moe_route(
     const float *__restrict__ rw, int64_t ld, const float *__restrict__ bias, const float *__restrict__ x,
     int64_t hidden, int32_t n_routed, int32_t n_shared, int32_t topk, float route_scale, float global_scale,
     float *__restrict__ logits, int32_t *__restrict__ sel_idx, float *__restrict__ sel_w,
-    uint32_t *__restrict__ counter, int8_t *__restrict__ xp_planes, float *__restrict__ xp_xs,
-    float *__restrict__ xp_gs) {
+    uint32_t *__restrict__ counter) {
     __shared__ float part[RT_NT / SEPIA_WAVE][RT_ROWS];
     __shared__ float lg[1024 + 64];
     __shared__ float score[1024];
@@ -202,15 +199,6 @@ extern "C" __global__ __launch_bounds__(RT_NT) void sepia_moe_route(
                 const int64_t row = (r0 + r < n_tot) ? r0 + r : n_tot - 1;
                 acc[r] = __builtin_fmaf(rw[row * ld + i], x[i], acc[r]);
             }
-        }
-    }
-    // x segments to XP form for the gate/up launch (16-byte aligned x only)
-    if (xp_planes && vec && (hidden & 15) == 0) {
-        const int64_t seg = (int64_t)blockIdx.x + (int64_t)gridDim.x * t;
-        if (seg < hidden / 16) {
-            const float4 *x4 = (const float4 *)x + 4 * seg;
-            const float4 v[4] = {x4[0], x4[1], x4[2], x4[3]};
-            xp_store(xp_segment(v), xp_planes, xp_xs, xp_gs, hidden, seg);
         }
     }
 #pragma unroll

@@ -221,5 +221,17 @@ SEPIA_FFN_PAIR(4, 2, ST_Q4_K, ST_Q2_K)
 SEPIA_FFN_PAIR(4, 3, ST_Q4_K, ST_Q3_K)
 SEPIA_FFN_PAIR(4, 4, ST_Q4_K, ST_Q4_K)
 
+#include "mq.h"
 #include "moe.h"
 #include "synth.h"
+
+// ------------------------------------------------------------------------
+// Matrix-core quantized matvecs (mq.h), CH = 1 or 2 blocks per wave.
+#define SEPIA_MQ_MV_ALL(name, T) SEPIA_MQ_MV(name, T, 1) SEPIA_MQ_MV(name, T, 2)
+SEPIA_MQ_MV_ALL(q2_k, ST_Q2_K)
+SEPIA_MQ_MV_ALL(q3_k, ST_Q3_K)
+SEPIA_MQ_MV_ALL(q4_k, ST_Q4_K)
+// expert FFN: gate/up with CH = 1 or 2 blocks per wave, down with 1
+SEPIA_MQ_GATEUP(1)
+SEPIA_MQ_GATEUP(2)
+SEPIA_MQ_DOWN(1)

@@ -50,7 +50,13 @@ enum {
     /* expert-FFN tile kernels: 9 (routed, shared) format pairs over
      * {Q2_K, Q3_K, Q4_K}, each gate/up (x f32), gate/up (x planes), down */
     K_FFN_BASE,
-    K_COUNT = K_FFN_BASE + 27
+    /* matrix-core matvecs (kernels/mq.h): {Q2_K, Q3_K, Q4_K} x {1, 2}
+     * blocks per wave */
+    K_MQ_MV = K_FFN_BASE + 27,
+    /* matrix-core expert FFN: gate/up CH {1, 2}, down CH 1 */
+    K_MQ_GU = K_MQ_MV + 6,
+    K_MQ_DN = K_MQ_GU + 2,
+    K_COUNT = K_MQ_DN + 1
 };
 #define FFN_NAMES(p) "sepia_ffn_gateup_" p, "sepia_ffn_gateup_" p "_xp", "sepia_ffn_down_" p
 static const char *const k_names[K_COUNT] = {
@@ -69,6 +75,9 @@ static const char *const k_names[K_COUNT] = {
     "sepia_mv_q2_k", "sepia_mv_q3_k", "sepia_mv_q4_k",
     FFN_NAMES("22"), FFN_NAMES("23"), FFN_NAMES("24"), FFN_NAMES("32"), FFN_NAMES("33"), FFN_NAMES("34"),
     FFN_NAMES("42"), FFN_NAMES("43"), FFN_NAMES("44"),
+    "sepia_mq_mv_q2_k_c1", "sepia_mq_mv_q2_k_c2", "sepia_mq_mv_q3_k_c1", "sepia_mq_mv_q3_k_c2",
+    "sepia_mq_mv_q4_k_c1", "sepia_mq_mv_q4_k_c2",
+    "sepia_mq_gateup_c1", "sepia_mq_gateup_c2", "sepia_mq_down_c1",
 };
 #undef FFN_NAMES
 
@@ -111,6 +120,8 @@ typedef struct {
 } TileGeo;
 
 static int g_opt_tile = 1;   /* sepia_hip_set_option("tile", 0) forces the generic kernels */
+static int g_opt_mq = 1;     /* sepia_hip_set_option("mq", 0) disables the matrix-core kernels */
+static int g_opt_mq_ch = 0;  /* sepia_hip_set_option("mq_ch", 1|2) forces blocks per wave (0 = automatic) */
 static int g_opt_tile_t = 0; /* sepia_hip_set_option("tile_t", T) forces T steps per workgroup */
 
 /* Geometry for `mats` stacked copies of a [rows, 256 * n_blocks] matrix; 0
@@ -136,6 +147,7 @@ static size_t tile_lds(int64_t n_staged, const TileGeo *g, int mats) {
 }
 
 static int g_available;
+static size_t g_lds_max = 65536;    /* per-workgroup LDS limit, from the device at init */
 static int g_have_iq2xxs;
 static char g_device_name[256];
 static hipModule_t g_module;
@@ -397,6 +409,7 @@ int sepia_gpu_init(const char *kernel_dir) {
         LOG("device 0 is %s (%s); this library is built for gfx950 only", prop.name, prop.gcnArchName);
         return 0;
     }
+    g_lds_max = prop.sharedMemPerBlock ? prop.sharedMemPerBlock : 65536;
     char path[4096];
     if (!kernel_path(kernel_dir, path, sizeof path)) {
         LOG("init: kernel directory path too long");
@@ -850,12 +863,53 @@ int sepia_hip_set_option(const char *name, int value) {
         g_opt_tile = value;
         return 1;
     }
+    if (strcmp(name, "mq") == 0 && (value == 0 || value == 1)) {
+        g_opt_mq = value;
+        return 1;
+    }
+    if (strcmp(name, "mq_ch") == 0 && (value == 0 || value == 1 || value == 2)) {
+        g_opt_mq_ch = value;
+        return 1;
+    }
     if (strcmp(name, "tile_t") == 0 && value >= 0 && value <= TILE_TMAX) {
         g_opt_tile_t = value;
         return 1;
     }
     LOG("set_option: unknown option %s=%d", name, value);
     return 0;
+}
+
+/* Matrix-core kernels (kernels/mq.h). A workgroup owns row groups of 16
+ * rows; its waves split a row's blocks in chunks of CH. x (or h) is staged
+ * once per workgroup as XQ digit planes in LDS (3.75 bytes per column,
+ * rounded up to 16) behind a 128-byte zero area; then come two buffers of
+ * per-wave row partials. Workgroups are persistent: each walks row groups
+ * blockIdx.x, + gridDim.x, ... with the next group's loads in flight. */
+#define MQ_MAX_BLOCKS 32
+#define MQ_CUS 256                  /* MI355X compute units */
+static size_t mq_xq_bytes(int64_t n) { return ((size_t)(3 * n + 3 * (n / 16) * 4) + 15) & ~(size_t)15; }
+static int mq_code(int t) { return t == SEPIA_T_Q2_K ? 0 : (t == SEPIA_T_Q3_K ? 1 : (t == 12 ? 2 : -1)); }
+/* blocks per wave: the smallest of `opts` that keeps the workgroup at <= 16 waves */
+static int mq_ch(int64_t nb, const int *opts, int n_opts) {
+    for (int i = 0; i < n_opts; i++)
+        if ((nb + opts[i] - 1) / opts[i] <= 16) return opts[i];
+    return 0;
+}
+static int mq_plan(int type, int64_t n_blocks, int64_t rows, uintptr_t base, const TypeInfo *ti, int *waves,
+                   size_t *lds, unsigned *grid) {
+    static const int opts[2] = { 1, 2 };
+    const int mc = mq_code(type);
+    if (!g_opt_mq || mc < 0 || n_blocks < 1 || n_blocks > MQ_MAX_BLOCKS || base % (uintptr_t)ti->align) return -1;
+    int ch = mq_ch(n_blocks, opts, 2);
+    if (g_opt_mq_ch) ch = g_opt_mq_ch;
+    if (!ch || (n_blocks + ch - 1) / ch > 16) return -1;
+    *waves = (int)((n_blocks + ch - 1) / ch);
+    const int64_t tiles = (rows + 15) / 16;
+    *grid = (unsigned)(tiles < MQ_CUS ? tiles : MQ_CUS);
+    const int64_t nk = (tiles + *grid - 1) / *grid;     /* row groups per workgroup */
+    *lds = 128 + mq_xq_bytes(256 * n_blocks) + 2 * (size_t)(*waves) * 16 * 4 + (size_t)nk * 16 * 4;
+    if (*lds > g_lds_max) return -1;
+    return K_MQ_MV + 2 * mc + (ch == 1 ? 0 : 1);
 }
 
 /* 1 if the tile matvec runs this matrix: the format has a tile decoder, the
@@ -888,6 +942,15 @@ int sepia_gpu_matvec_q(int ggml_type, SepiaGpuBuf *w, size_t w_off, SepiaGpuBuf 
         return 0;
     if (!need_batch(op) || !prep_in(w, op) || !prep_in(x, op) || !prep_out(y, op)) return 0;
     const uint8_t *wp = w->dev + w_off;
+    int mq_waves;
+    size_t mq_lds;
+    unsigned mq_grid;
+    const int kmq = mq_plan(ggml_type, n_blocks, out_dim, (uintptr_t)wp, ti, &mq_waves, &mq_lds, &mq_grid);
+    if (kmq >= 0) {
+        int32_t nb32 = (int32_t)n_blocks;
+        void *args[] = { &wp, &row_bytes, &out_dim, &nb32, &x->dev, &y->dev };
+        return launch_lds(kmq, mq_grid, 64u * (unsigned)mq_waves, mq_lds, args, op);
+    }
     TileGeo geo;
     if (tile_plan(ti, n_blocks, (uintptr_t)wp, out_dim, &geo)) {
         int64_t n = in_dim;
@@ -1040,17 +1103,77 @@ static int proj_aligned(const MoeProj *p) {
     return ((uintptr_t)p->base % a) == 0 && p->stride % a == 0 && p->row_bytes % a == 0;
 }
 
+/* Matrix-core FFN plan (kernels/mq.h): every projection in {Q2_K, Q3_K,
+ * Q4_K}, gate and up of one format per slot kind, down of one row length,
+ * aligned bases, H and I multiples of 256 that fit the workgroup (<= 16
+ * waves of CH <= 2 blocks, LDS within the device limit). gate/up runs
+ * wps workgroups per slot, each persistent over its row groups; down runs
+ * persistent workgroups over row groups of y, each through every slot. */
+typedef struct {
+    int k_gu, k_dn;
+    unsigned gu_threads, dn_threads, gu_grid, dn_grid;
+    int32_t wps;
+    size_t gu_lds, dn_lds;
+} MqFfnPlan;
+static int mq_ffn_plan(const MoeProj *g, const MoeProj *u, const MoeProj *d, const MoeProj *sg, const MoeProj *su,
+                       const MoeProj *sd, int32_t topk, int32_t n_shared, int64_t H, int64_t I, MqFfnPlan *pl) {
+    static const int opts[2] = { 1, 2 };
+    if (!g_opt_mq || H % 256 || I % 256) return 0;
+    const MoeProj *ps[6] = { g, u, d, sg, su, sd };
+    for (int i = 0; i < (n_shared > 0 ? 6 : 3); i++)
+        if (mq_code(ps[i]->type) < 0 || !proj_aligned(ps[i])) return 0;
+    if (g->type != u->type || (n_shared > 0 && sg->type != su->type)) return 0;
+    const int64_t nbh = H / 256, nbi = I / 256;
+    const int cgu = mq_ch(nbh, opts, 2), cdn = mq_ch(nbi, opts, 1);
+    if (!cgu || !cdn) return 0;
+    const int n_slots = topk + n_shared;
+    const int wgu = (int)((nbh + cgu - 1) / cgu), wdn = (int)((nbi + cdn - 1) / cdn);
+    pl->k_gu = K_MQ_GU + (cgu - 1);
+    pl->k_dn = K_MQ_DN;
+    pl->gu_threads = 64u * (unsigned)wgu;
+    pl->dn_threads = 64u * (unsigned)wdn;
+    const int64_t tiles_i0 = (I + 15) / 16;
+    int64_t wps0 = MQ_CUS / n_slots;
+    if (wps0 < 1) wps0 = 1;
+    if (wps0 > tiles_i0) wps0 = tiles_i0;
+    pl->gu_lds = 128 + mq_xq_bytes(H) + 2 * (size_t)wgu * 16 * 4 + (size_t)((tiles_i0 + wps0 - 1) / wps0) * 16 * 4;
+    const int64_t tiles_i = (I + 15) / 16, tiles_h = (H + 15) / 16;
+    const int64_t dn_grid = tiles_h < MQ_CUS ? tiles_h : MQ_CUS;
+    const int64_t nk = (tiles_h + dn_grid - 1) / dn_grid;   /* row groups per down workgroup */
+    pl->dn_lds = 128 + (size_t)n_slots * mq_xq_bytes(I) + 2 * (size_t)wdn * 16 * 4 + (size_t)nk * 16 * 4 +
+                 (size_t)n_slots * 8;
+    if (pl->gu_lds > g_lds_max || pl->dn_lds > g_lds_max) return 0;
+    int64_t wps = MQ_CUS / n_slots;
+    if (wps < 1) wps = 1;
+    if (wps > tiles_i) wps = tiles_i;
+    pl->wps = (int32_t)wps;
+    pl->gu_grid = (unsigned)(wps * n_slots);
+    pl->dn_grid = (unsigned)dn_grid;
+    return 1;
+}
+
 /* The SwiGLU expert FFN over n_slots = topk + n_shared slots: routed slot s
  * uses expert sel_idx[s] (or fixed + s when sel_idx is NULL), then come the
  * shared experts. One slot without weights stores y; several slots add
- * sel_w[s] * their output into y. Uses the tile kernels (integer dots) when
- * every projection has a tile decoder and the shapes fit, else the generic
- * one-wave-per-row kernels. xp, when set, holds x in digit-plane form. */
+ * sel_w[s] * their output into y. Uses the matrix-core kernels when the
+ * formats and shapes fit, else the tile kernels, else the generic
+ * one-wave-per-row kernels. scr: scratch for the slots' f32 h vectors. */
 static int ffn_launch(const char *op, const MoeProj *g, const MoeProj *u, const MoeProj *d, const MoeProj *sg,
                       const MoeProj *su, const MoeProj *sd, const int32_t *sel_idx, const float *sel_w, int32_t fixed,
-                      int32_t topk, int32_t n_shared, int64_t H, int64_t I, const uint8_t *xdev, const XpArgs *xp,
-                      float *ydev, uint8_t *scr) {
+                      int32_t topk, int32_t n_shared, int64_t H, int64_t I, const uint8_t *xdev, float *ydev,
+                      uint8_t *scr) {
     int32_t n_slots = topk + n_shared;
+    int64_t inter = I, hid = H;
+    MqFfnPlan pl;
+    if (mq_ffn_plan(g, u, d, sg, su, sd, topk, n_shared, H, I, &pl)) {
+        int32_t inter32 = (int32_t)I, wps = pl.wps;
+        float *h = (float *)scr;
+        void *a_gu[] = { (void *)g, (void *)u, (void *)sg, (void *)su, &sel_idx, &fixed, &topk, &inter32, &wps, &xdev,
+                         &h };
+        if (!launch_lds(pl.k_gu, pl.gu_grid, pl.gu_threads, pl.gu_lds, a_gu, op)) return 0;
+        void *a_dn[] = { (void *)d, (void *)sd, &sel_idx, &sel_w, &fixed, &topk, &n_shared, &inter32, &hid, &h, &ydev };
+        return launch_lds(pl.k_dn, pl.dn_grid, pl.dn_threads, pl.dn_lds, a_dn, op);
+    }
     const int cr = tile_code(g->type), cdr = tile_code(d->type);
     const int cs = n_shared > 0 ? tile_code(sg->type) : cr, cds = n_shared > 0 ? tile_code(sd->type) : cdr;
     TileGeo gu, dn;
@@ -1059,18 +1182,16 @@ static int ffn_launch(const char *op, const MoeProj *g, const MoeProj *u, const 
                tile_geo(H / 256, I, 2 * (int64_t)n_slots, &gu) && tile_geo(I / 256, H, n_slots, &dn);
     if (tile && n_shared > 0)
         tile = sg->type == su->type && proj_aligned(sg) && proj_aligned(su) && proj_aligned(sd);
-    int64_t inter = I, hid = H;
     float *h = (float *)scr;
     if (tile) {
         XpArgs xa = { NULL, NULL, NULL };
-        if (xp) xa = *xp;
         float *y_zero = n_slots > 1 ? ydev : NULL;
         int64_t y_n = H;
-        const int k_gu = K_FFN_BASE + 3 * (3 * cr + cs) + (xp ? 1 : 0);
+        const int k_gu = K_FFN_BASE + 3 * (3 * cr + cs);
         const int k_dn = K_FFN_BASE + 3 * (3 * cdr + cds) + 2;
         void *a_gu[] = { (void *)g, (void *)u, (void *)sg, (void *)su, &sel_idx, &fixed, &topk, &inter, &hid,
                          &gu, &xdev, &xa, &h, &y_zero, &y_n };
-        if (!launch_lds(k_gu, (unsigned)(n_slots * gu.tiles), TILE_NT, tile_lds(xp ? 0 : H, &gu, 2), a_gu, op))
+        if (!launch_lds(k_gu, (unsigned)(n_slots * gu.tiles), TILE_NT, tile_lds(H, &gu, 2), a_gu, op))
             return 0;
         void *a_dn[] = { (void *)d, (void *)sd, &sel_idx, &sel_w, &fixed, &topk, &n_slots, &inter, &hid,
                          &dn, &h, &ydev };
@@ -1121,14 +1242,13 @@ int sepia_gpu_moe_decode(const SepiaMoeLayerDesc *L, SepiaGpuBuf *x, SepiaGpuBuf
     }
     if (!need_batch(op)) return 0;
 
-    /* scratch: logits | sel_idx | sel_w | x planes | FFN activations, each
-     * 256-byte aligned; the router's arrival counter is the first word of
-     * the counter region */
+    /* scratch: logits | sel_idx | sel_w | FFN activations, each 256-byte
+     * aligned; the router's arrival counter is the first word of the
+     * counter region */
     const size_t o_logits = 0;
     const size_t o_idx = o_logits + (((size_t)n_tot * 4 + 255) & ~(size_t)255);
     const size_t o_w = o_idx + 256;
-    const size_t o_xp = o_w + 256;
-    const size_t o_h = o_xp + (((size_t)H * 3 + (size_t)(H / 16) * 8 + 255) & ~(size_t)255);
+    const size_t o_h = o_w + 256;
     uint8_t *s = (uint8_t *)scratch(o_h + ffn_scratch_bytes(n_slots, I), op);
     if (!s) return 0;
     float *logits = (float *)(s + o_logits), *sel_w = (float *)(s + o_w);
@@ -1143,24 +1263,13 @@ int sepia_gpu_moe_decode(const SepiaMoeLayerDesc *L, SepiaGpuBuf *x, SepiaGpuBuf
 
     const float *rw = (const float *)(L->router_w->dev + L->router_w_off);
     const float *rb = (const float *)(L->router_bias->dev + L->router_bias_off);
-    /* the router also writes x's digit planes when its loads are 16-byte
-     * vectors (aligned router rows) and x splits into 16-column segments */
-    const int xp_ok = ((uintptr_t)rw % 16) == 0 && H % 16 == 0 && H <= 8192;   /* kernels/moe.h RT_C4 */
-    XpArgs xp;
-    xp.planes = (const int8_t *)(s + o_xp);
-    xp.xs = (const float *)(s + o_xp + (size_t)H * 3);
-    xp.gs = xp.xs + H / 16;
-    int8_t *xp_planes = xp_ok ? (int8_t *)xp.planes : NULL;
-    float *xp_xs = (float *)xp.xs, *xp_gs = (float *)xp.gs;
     int64_t ld = H, hid = H;
     int32_t nr = L->n_routed, ns = L->n_shared, tk = L->topk;
     float rs = L->route_scale, gsc = L->global_scale;
-    void *a_route[] = { &rw, &ld, &rb, &x->dev, &hid, &nr, &ns, &tk, &rs, &gsc, &logits, &sel_idx, &sel_w, &counter,
-                        &xp_planes, &xp_xs, &xp_gs };
-    if (!launch(K_MOE_ROUTE, (unsigned)((n_tot + 1) / 2), 256, a_route, op)) return 0;
+    void *a_route[] = { &rw, &ld, &rb, &x->dev, &hid, &nr, &ns, &tk, &rs, &gsc, &logits, &sel_idx, &sel_w, &counter };
+    if (!launch(K_MOE_ROUTE, (unsigned)n_tot, 256, a_route, op)) return 0;
 
-    if (!ffn_launch(op, &g, &u, &d, &sg, &su, &sd, sel_idx, sel_w, 0, tk, ns, H, I, x->dev, xp_ok ? &xp : NULL,
-                    (float *)y->dev, s + o_h))
+    if (!ffn_launch(op, &g, &u, &d, &sg, &su, &sd, sel_idx, sel_w, 0, tk, ns, H, I, x->dev, (float *)y->dev, s + o_h))
         return 0;
 
     if (route_out) {
@@ -1196,6 +1305,6 @@ int sepia_gpu_expert_ffn(const SepiaExpertTensor *gate, const SepiaExpertTensor 
     if (!prep_in(gate->buf, op) || !prep_in(up->buf, op) || !prep_in(down->buf, op) || !prep_in(x, op) ||
         !prep_out(y, op))
         return 0;
-    return ffn_launch(op, &g, &u, &d, &none, &none, &none, NULL, NULL, expert, 1, 0, hidden, inter, x->dev, NULL,
+    return ffn_launch(op, &g, &u, &d, &none, &none, &none, NULL, NULL, expert, 1, 0, hidden, inter, x->dev,
                       (float *)y->dev, scr);
 }

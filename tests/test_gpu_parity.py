@@ -209,15 +209,19 @@ def test_matvec_q_config_shapes(dev, orc, name, t, out_dim, in_dim):
 
 @pytest.fixture
 def kernel_path(dev, request):
-    """Force one kernel family: the generic per-row kernel, or the tile kernels
-    with 1, 2 or 3 row steps per workgroup."""
+    """Force one kernel family: the matrix-core kernels (the default), the
+    generic per-row kernel, or the tile kernels with 1, 2 or 3 row steps per
+    workgroup."""
     L = dev.L
     mode = request.param
+    if mode != "mq":
+        assert L.sepia_hip_set_option(b"mq", 0) == 1
     if mode == "generic":
         assert L.sepia_hip_set_option(b"tile", 0) == 1
-    else:
+    elif mode != "mq":
         assert L.sepia_hip_set_option(b"tile_t", {"t1": 1, "t2": 2, "t3": 3}[mode]) == 1
     yield mode
+    L.sepia_hip_set_option(b"mq", 1)
     L.sepia_hip_set_option(b"tile", 1)
     L.sepia_hip_set_option(b"tile_t", 0)
 
@@ -226,7 +230,7 @@ TILE_SHAPES = [(10, 3072, 6144), (11, 6144, 3072), (12, 4096, 4096), (12, 33, 10
                (11, 1, 3072), (12, 200, 6144), (10, 50, 8192), (12, 40, 12288), (11, 70, 12288)]
 
 
-@pytest.mark.parametrize("kernel_path", ["generic", "t1", "t2", "t3"], indirect=True)
+@pytest.mark.parametrize("kernel_path", ["mq", "generic", "t1", "t2", "t3"], indirect=True)
 @pytest.mark.parametrize("t,out_dim,in_dim", TILE_SHAPES, ids=lambda v: str(v))
 def test_matvec_q_kernel_paths(dev, orc, kernel_path, t, out_dim, in_dim):
     check_matvec(dev, orc, t, out_dim, in_dim, seed=out_dim * 7 + t)
@@ -455,7 +459,7 @@ def test_moe_decode_small(dev, orc, types, seed):
         dev.free(b)
 
 
-@pytest.mark.parametrize("kernel_path", ["generic", "t1", "t3"], indirect=True)
+@pytest.mark.parametrize("kernel_path", ["mq", "generic", "t1", "t3"], indirect=True)
 @pytest.mark.parametrize("types", [(10, 10, 11, 12), (12, 12, 12, 10), (11, 11, 10, 11)],
                          ids=["q2k_q3k_q4k", "q4k_q4k_q2k", "q3k_q2k_q3k"])
 def test_moe_decode_tile_shapes(dev, orc, kernel_path, types):
@@ -507,7 +511,7 @@ def run_expert_ffn(dev, tensors, n_experts, expert, hidden, inter, x):
     return y
 
 
-@pytest.mark.parametrize("kernel_path", ["generic", "t1", "t2", "t3"], indirect=True)
+@pytest.mark.parametrize("kernel_path", ["mq", "generic", "t1", "t2", "t3"], indirect=True)
 @pytest.mark.parametrize("types,hidden,inter", [((10, 10, 11), 6144, 3072), ((12, 12, 12), 4096, 2048),
                                                 ((11, 11, 10), 2048, 1024)],
                          ids=["c2_q2k_q3k", "q4k_4096", "q3k_q2k_2048"])
