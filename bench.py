@@ -227,7 +227,7 @@ def run_c2(B, warmup, steps, cpu_seconds):
     e_last = (warmup + steps - 1) % NE
     y_graph = B.fetch(y, 0, H * 4).view(np.float32)
     step_bytes = gb + ub + db + H * 4 + I * 4 + H * 4
-    K_GU, K_DN = "sepia_mq_gateup_c2", "sepia_mq_down_c1"
+    K_GU, K_DN = "sepia_mq_gateup", "sepia_mq_down"
     kms = B.kernel_ms(step, min(steps, 4 * NE), [K_GU, K_DN])
     gu_bytes = gb + ub + H * 4 + I * 4
     dn_bytes = db + I * 4 + H * 4
@@ -279,8 +279,7 @@ def run_matvec_rotation(B, name, t, rows, cols, warmup, steps, cpu_seconds, seed
 
     ms = B.timed_steps(step, warmup, steps)
     tname = {10: "q2_k", 11: "q3_k", 12: "q4_k", 17: "iq2_xs", 18: "iq3_xxs", 16: "iq2_xxs"}[t]
-    cands = ["sepia_mq_mv_%s_c%d" % (tname, c) for c in (1, 2)] + ["sepia_mv_%s" % tname,
-                                                                      "sepia_matvec_generic_%s" % tname]
+    cands = ["sepia_mq_mv_%s" % tname, "sepia_mv_%s" % tname, "sepia_matvec_generic_%s" % tname]
     kname, kms = B.kernel_used(step, min(steps, 2 * ncopy), cands)
     nbytes = mb + cols * 4 + rows * 4
     import oracle
@@ -338,7 +337,7 @@ def run_c3(B, warmup, steps, cpu_seconds, n_layers=3):
 
     ms = B.timed_steps(step, warmup, steps)
     per_token = (NR + NS) * H * 4 + 6 * (2 * gb + db) + NS * (2 * sgb + sdb)
-    kms = B.kernel_ms(step, min(steps, 60), ["sepia_moe_route", "sepia_mq_gateup_c2", "sepia_mq_down_c1"])
+    kms = B.kernel_ms(step, min(steps, 60), ["sepia_moe_route", "sepia_mq_gateup", "sepia_mq_down"])
 
     # parity at full size: route + output of one token against the oracle
     import oracle

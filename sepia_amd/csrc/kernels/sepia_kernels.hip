@@ -226,12 +226,9 @@ SEPIA_FFN_PAIR(4, 4, ST_Q4_K, ST_Q4_K)
 #include "synth.h"
 
 // ------------------------------------------------------------------------
-// Matrix-core quantized matvecs (mq.h), CH = 1 or 2 blocks per wave.
-#define SEPIA_MQ_MV_ALL(name, T) SEPIA_MQ_MV(name, T, 1) SEPIA_MQ_MV(name, T, 2)
-SEPIA_MQ_MV_ALL(q2_k, ST_Q2_K)
-SEPIA_MQ_MV_ALL(q3_k, ST_Q3_K)
-SEPIA_MQ_MV_ALL(q4_k, ST_Q4_K)
-// expert FFN: gate/up with CH = 1 or 2 blocks per wave, down with 1
-SEPIA_MQ_GATEUP(1)
-SEPIA_MQ_GATEUP(2)
-SEPIA_MQ_DOWN(1)
+// Matrix-core quantized matvecs and expert FFN (mq.h).
+SEPIA_MQ_MV(q2_k, ST_Q2_K)
+SEPIA_MQ_MV(q3_k, ST_Q3_K)
+SEPIA_MQ_MV(q4_k, ST_Q4_K)
+SEPIA_MQ_GATEUP()
+SEPIA_MQ_DOWN()

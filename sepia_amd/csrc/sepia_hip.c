@@ -50,12 +50,11 @@ enum {
     /* expert-FFN tile kernels: 9 (routed, shared) format pairs over
      * {Q2_K, Q3_K, Q4_K}, each gate/up (x f32), gate/up (x planes), down */
     K_FFN_BASE,
-    /* matrix-core matvecs (kernels/mq.h): {Q2_K, Q3_K, Q4_K} x {1, 2}
-     * blocks per wave */
+    /* matrix-core matvecs (kernels/mq.h): Q2_K, Q3_K, Q4_K */
     K_MQ_MV = K_FFN_BASE + 27,
-    /* matrix-core expert FFN: gate/up CH {1, 2}, down CH 1 */
-    K_MQ_GU = K_MQ_MV + 6,
-    K_MQ_DN = K_MQ_GU + 2,
+    /* matrix-core expert FFN: gate/up, down */
+    K_MQ_GU = K_MQ_MV + 3,
+    K_MQ_DN = K_MQ_GU + 1,
     K_COUNT = K_MQ_DN + 1
 };
 #define FFN_NAMES(p) "sepia_ffn_gateup_" p, "sepia_ffn_gateup_" p "_xp", "sepia_ffn_down_" p
@@ -75,9 +74,7 @@ static const char *const k_names[K_COUNT] = {
     "sepia_mv_q2_k", "sepia_mv_q3_k", "sepia_mv_q4_k",
     FFN_NAMES("22"), FFN_NAMES("23"), FFN_NAMES("24"), FFN_NAMES("32"), FFN_NAMES("33"), FFN_NAMES("34"),
     FFN_NAMES("42"), FFN_NAMES("43"), FFN_NAMES("44"),
-    "sepia_mq_mv_q2_k_c1", "sepia_mq_mv_q2_k_c2", "sepia_mq_mv_q3_k_c1", "sepia_mq_mv_q3_k_c2",
-    "sepia_mq_mv_q4_k_c1", "sepia_mq_mv_q4_k_c2",
-    "sepia_mq_gateup_c1", "sepia_mq_gateup_c2", "sepia_mq_down_c1",
+    "sepia_mq_mv_q2_k", "sepia_mq_mv_q3_k", "sepia_mq_mv_q4_k", "sepia_mq_gateup", "sepia_mq_down",
 };
 #undef FFN_NAMES
 
@@ -121,7 +118,10 @@ typedef struct {
 
 static int g_opt_tile = 1;   /* sepia_hip_set_option("tile", 0) forces the generic kernels */
 static int g_opt_mq = 1;     /* sepia_hip_set_option("mq", 0) disables the matrix-core kernels */
-static int g_opt_mq_ch = 0;  /* sepia_hip_set_option("mq_ch", 1|2) forces blocks per wave (0 = automatic) */
+/* sepia_hip_set_option("mq_p" | "mq_c" | "mq_s", v) force the matrix-core
+ * workgroup geometry (parts per item, item lanes, ring stages of the largest
+ * format; 0 = planned) */
+static int g_opt_mq_p = 0, g_opt_mq_c = 0, g_opt_mq_s = 0;
 static int g_opt_tile_t = 0; /* sepia_hip_set_option("tile_t", T) forces T steps per workgroup */
 
 /* Geometry for `mats` stacked copies of a [rows, 256 * n_blocks] matrix; 0
@@ -867,8 +867,16 @@ int sepia_hip_set_option(const char *name, int value) {
         g_opt_mq = value;
         return 1;
     }
-    if (strcmp(name, "mq_ch") == 0 && (value == 0 || value == 1 || value == 2)) {
-        g_opt_mq_ch = value;
+    if (strcmp(name, "mq_p") == 0 && value >= 0 && value <= 16) {
+        g_opt_mq_p = value;
+        return 1;
+    }
+    if (strcmp(name, "mq_c") == 0 && value >= 0 && value <= 16) {
+        g_opt_mq_c = value;
+        return 1;
+    }
+    if (strcmp(name, "mq_s") == 0 && value >= 0 && value <= 4) {
+        g_opt_mq_s = value;
         return 1;
     }
     if (strcmp(name, "tile_t") == 0 && value >= 0 && value <= TILE_TMAX) {
@@ -879,37 +887,97 @@ int sepia_hip_set_option(const char *name, int value) {
     return 0;
 }
 
-/* Matrix-core kernels (kernels/mq.h). A workgroup owns row groups of 16
- * rows; its waves split a row's blocks in chunks of CH. x (or h) is staged
- * once per workgroup as XQ digit planes in LDS (3.75 bytes per column,
- * rounded up to 16) behind a 128-byte zero area; then come two buffers of
- * per-wave row partials. Workgroups are persistent: each walks row groups
- * blockIdx.x, + gridDim.x, ... with the next group's loads in flight. */
-#define MQ_MAX_BLOCKS 32
+/* Matrix-core kernels (kernels/mq.h). x (or h) is staged once per
+ * workgroup as XQ digit planes in LDS (4 bytes per column) behind a
+ * 768-byte zero area; then come the items' partial row sums and one LDS
+ * ring per wave. An item is 16 rows of one matrix; a wave step is 16 rows x
+ * 4 blocks ("quad"), fetched by LDS DMA as Wp 16-byte words per lane (Q2_K
+ * and Q3_K 7, Q4_K 9). nw = C * P waves: P parts split each item's quads, C
+ * items run side by side; every wave's ring holds S = min(4, ring / Wp KB)
+ * steps in flight. */
 #define MQ_CUS 256                  /* MI355X compute units */
-static size_t mq_xq_bytes(int64_t n) { return ((size_t)(3 * n + 3 * (n / 16) * 4) + 15) & ~(size_t)15; }
+#define MQ_ZERO 768
+typedef struct {
+    int32_t P, ring;                /* as struct MqGeo in kernels/mq.h */
+} MqGeo;
+/* In-kernel selection by the gate/up launch (struct MqRoute in
+ * kernels/mq.h); logits NULL: the experts come from sel_idx. */
+typedef struct {
+    const float *logits;
+    const float *bias;
+    int32_t n_routed, n_shared;
+    float route_scale, global_scale;
+    int32_t *idx_out;
+    float *w_out;
+} MqRoute;
+#define MQ_SEL_BYTES 512            /* the gate/up kernel's selection area in LDS */
+static size_t mq_xq_bytes(int64_t n) { return (size_t)(n / 256) * 832 + 3 * (size_t)(n / 16) * 4; }
 static int mq_code(int t) { return t == SEPIA_T_Q2_K ? 0 : (t == SEPIA_T_Q3_K ? 1 : (t == 12 ? 2 : -1)); }
-/* blocks per wave: the smallest of `opts` that keeps the workgroup at <= 16 waves */
-static int mq_ch(int64_t nb, const int *opts, int n_opts) {
-    for (int i = 0; i < n_opts; i++)
-        if ((nb + opts[i] - 1) / opts[i] <= 16) return opts[i];
-    return 0;
+static const int k_mq_words[3] = { 7, 7, 9 };   /* padded words per lane (MQ<T>::Wp) */
+static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+/* Geometry for workgroups of n_items items of nq quads; mc is the format
+ * most items use, wmax the most words of any format the workgroup may run.
+ * LDS = align256(fixed + 64 * n_items * P) + nw * ring; the rings take the
+ * rest of the LDS (each at least one step of wmax words). Chooses the fewest
+ * steps per wave of format mc, counting a one-stage ring with several steps
+ * as 1.6 steps each (its loads do not overlap its compute), then the most
+ * steps in flight, then the most waves. Returns 0 when nothing fits. */
+static int mq_geo(int mc, int wmax, int64_t n_items, int64_t nq, size_t fixed, unsigned *threads, MqGeo *geo,
+                  size_t *lds) {
+    const size_t w1 = (size_t)k_mq_words[mc] * 1024, wm = (size_t)wmax * 1024;
+    int64_t best_cost = -1, best_fl = 0;
+    int best_nw = 0;
+    for (int P = 1; P <= 16 && P <= nq; P++) {
+        if (g_opt_mq_p && P != g_opt_mq_p) continue;
+        for (int C = 1; C * P <= 16 && C <= n_items; C++) {
+            if (g_opt_mq_c && C != g_opt_mq_c) continue;
+            const int nw = C * P;
+            const int64_t spw = ((n_items + C - 1) / C) * ((nq + P - 1) / P);
+            const size_t base = align256(fixed + (size_t)n_items * P * 64);
+            if (base + (size_t)nw * wm > g_lds_max) continue;
+            size_t ring = ((g_lds_max - base) / (size_t)nw) & ~(size_t)1023;
+            if (ring > 4 * wm) ring = 4 * wm;
+            if (g_opt_mq_s) {
+                ring = (size_t)g_opt_mq_s * wm;
+                if (base + (size_t)nw * ring > g_lds_max) continue;
+            }
+            int64_t S = (int64_t)(ring / w1);
+            if (S > 4) S = 4;
+            if (S > spw) S = spw;
+            const int64_t cost = spw * ((S >= 2 || spw == 1) ? 10 : 16);
+            const int64_t fl = (int64_t)nw * S;
+            if (best_cost < 0 || cost < best_cost || (cost == best_cost && (fl > best_fl || (fl == best_fl && nw > best_nw)))) {
+                best_cost = cost;
+                best_fl = fl;
+                best_nw = nw;
+                geo->P = P;
+                geo->ring = (int32_t)ring;
+                *threads = 64u * (unsigned)nw;
+                *lds = base + (size_t)nw * ring;
+            }
+        }
+    }
+    return best_cost >= 0;
 }
-static int mq_plan(int type, int64_t n_blocks, int64_t rows, uintptr_t base, const TypeInfo *ti, int *waves,
-                   size_t *lds, unsigned *grid) {
-    static const int opts[2] = { 1, 2 };
+
+/* Shapes the matrix-core kernels take: a format with a decoder, 4-byte
+ * aligned rows of a multiple of 4 blocks, row offsets within 32 bits. */
+static int mq_shape_ok(int type, int64_t n_blocks, int64_t rows, uintptr_t base, uint64_t row_bytes) {
+    return g_opt_mq && mq_code(type) >= 0 && n_blocks >= 4 && n_blocks % 4 == 0 && base % 4 == 0 &&
+           row_bytes % 4 == 0 && (uint64_t)rows * row_bytes < (1ull << 32);
+}
+
+static int mq_plan(int type, int64_t n_blocks, int64_t rows, uintptr_t base, uint64_t row_bytes, unsigned *threads,
+                   size_t *lds, unsigned *grid, MqGeo *geo) {
+    if (!mq_shape_ok(type, n_blocks, rows, base, row_bytes)) return -1;
     const int mc = mq_code(type);
-    if (!g_opt_mq || mc < 0 || n_blocks < 1 || n_blocks > MQ_MAX_BLOCKS || base % (uintptr_t)ti->align) return -1;
-    int ch = mq_ch(n_blocks, opts, 2);
-    if (g_opt_mq_ch) ch = g_opt_mq_ch;
-    if (!ch || (n_blocks + ch - 1) / ch > 16) return -1;
-    *waves = (int)((n_blocks + ch - 1) / ch);
     const int64_t tiles = (rows + 15) / 16;
-    *grid = (unsigned)(tiles < MQ_CUS ? tiles : MQ_CUS);
-    const int64_t nk = (tiles + *grid - 1) / *grid;     /* row groups per workgroup */
-    *lds = 128 + mq_xq_bytes(256 * n_blocks) + 2 * (size_t)(*waves) * 16 * 4 + (size_t)nk * 16 * 4;
-    if (*lds > g_lds_max) return -1;
-    return K_MQ_MV + 2 * mc + (ch == 1 ? 0 : 1);
+    const int64_t per = (tiles + MQ_CUS - 1) / MQ_CUS;     /* row groups per workgroup */
+    *grid = (unsigned)((tiles + per - 1) / per);
+    if (!mq_geo(mc, k_mq_words[mc], per, n_blocks / 4, MQ_ZERO + mq_xq_bytes(256 * n_blocks), threads, geo, lds))
+        return -1;
+    return K_MQ_MV + mc;
 }
 
 /* 1 if the tile matvec runs this matrix: the format has a tile decoder, the
@@ -942,14 +1010,15 @@ int sepia_gpu_matvec_q(int ggml_type, SepiaGpuBuf *w, size_t w_off, SepiaGpuBuf 
         return 0;
     if (!need_batch(op) || !prep_in(w, op) || !prep_in(x, op) || !prep_out(y, op)) return 0;
     const uint8_t *wp = w->dev + w_off;
-    int mq_waves;
+    unsigned mq_threads, mq_grid;
     size_t mq_lds;
-    unsigned mq_grid;
-    const int kmq = mq_plan(ggml_type, n_blocks, out_dim, (uintptr_t)wp, ti, &mq_waves, &mq_lds, &mq_grid);
+    MqGeo mgeo;
+    const int kmq = mq_plan(ggml_type, n_blocks, out_dim, (uintptr_t)wp, row_bytes, &mq_threads, &mq_lds, &mq_grid,
+                            &mgeo);
     if (kmq >= 0) {
         int32_t nb32 = (int32_t)n_blocks;
-        void *args[] = { &wp, &row_bytes, &out_dim, &nb32, &x->dev, &y->dev };
-        return launch_lds(kmq, mq_grid, 64u * (unsigned)mq_waves, mq_lds, args, op);
+        void *args[] = { &wp, &row_bytes, &out_dim, &nb32, &x->dev, &y->dev, &mgeo };
+        return launch_lds(kmq, mq_grid, mq_threads, mq_lds, args, op);
     }
     TileGeo geo;
     if (tile_plan(ti, n_blocks, (uintptr_t)wp, out_dim, &geo)) {
@@ -1104,51 +1173,50 @@ static int proj_aligned(const MoeProj *p) {
 }
 
 /* Matrix-core FFN plan (kernels/mq.h): every projection in {Q2_K, Q3_K,
- * Q4_K}, gate and up of one format per slot kind, down of one row length,
- * aligned bases, H and I multiples of 256 that fit the workgroup (<= 16
- * waves of CH <= 2 blocks, LDS within the device limit). gate/up runs
- * wps workgroups per slot, each persistent over its row groups; down runs
- * persistent workgroups over row groups of y, each through every slot. */
+ * Q4_K} with a shape the kernels take, gate and up of one format per slot
+ * kind, H and I multiples of 1024 (rows of whole quads), LDS within the
+ * device limit. gate/up runs wps workgroups per slot, each over its row
+ * groups (gate and up rows as two items each); down runs workgroups over
+ * row groups of y, each through every slot. */
 typedef struct {
-    int k_gu, k_dn;
     unsigned gu_threads, dn_threads, gu_grid, dn_grid;
     int32_t wps;
     size_t gu_lds, dn_lds;
+    MqGeo gu_geo, dn_geo;
 } MqFfnPlan;
+static int mq_proj_ok(const MoeProj *p, int64_t rows) {
+    return mq_shape_ok(p->type, p->n_blocks, rows, (uintptr_t)p->base, p->row_bytes) && p->stride % 4 == 0;
+}
 static int mq_ffn_plan(const MoeProj *g, const MoeProj *u, const MoeProj *d, const MoeProj *sg, const MoeProj *su,
                        const MoeProj *sd, int32_t topk, int32_t n_shared, int64_t H, int64_t I, MqFfnPlan *pl) {
-    static const int opts[2] = { 1, 2 };
-    if (!g_opt_mq || H % 256 || I % 256) return 0;
+    if (!g_opt_mq || H % 1024 || I % 1024) return 0;
     const MoeProj *ps[6] = { g, u, d, sg, su, sd };
+    const int64_t rows[6] = { I, I, H, I, I, H };
     for (int i = 0; i < (n_shared > 0 ? 6 : 3); i++)
-        if (mq_code(ps[i]->type) < 0 || !proj_aligned(ps[i])) return 0;
+        if (!mq_proj_ok(ps[i], rows[i])) return 0;
     if (g->type != u->type || (n_shared > 0 && sg->type != su->type)) return 0;
-    const int64_t nbh = H / 256, nbi = I / 256;
-    const int cgu = mq_ch(nbh, opts, 2), cdn = mq_ch(nbi, opts, 1);
-    if (!cgu || !cdn) return 0;
     const int n_slots = topk + n_shared;
-    const int wgu = (int)((nbh + cgu - 1) / cgu), wdn = (int)((nbi + cdn - 1) / cdn);
-    pl->k_gu = K_MQ_GU + (cgu - 1);
-    pl->k_dn = K_MQ_DN;
-    pl->gu_threads = 64u * (unsigned)wgu;
-    pl->dn_threads = 64u * (unsigned)wdn;
-    const int64_t tiles_i0 = (I + 15) / 16;
-    int64_t wps0 = MQ_CUS / n_slots;
-    if (wps0 < 1) wps0 = 1;
-    if (wps0 > tiles_i0) wps0 = tiles_i0;
-    pl->gu_lds = 128 + mq_xq_bytes(H) + 2 * (size_t)wgu * 16 * 4 + (size_t)((tiles_i0 + wps0 - 1) / wps0) * 16 * 4;
+    /* both slot kinds share a geometry: planned for the format of the
+     * routed slots (the shared ones when there are none), with rings that
+     * hold a step of either */
+    const int kg = mq_code(topk > 0 ? g->type : sg->type), kd = mq_code(topk > 0 ? d->type : sd->type);
+    int wgu = k_mq_words[kg], wdn = k_mq_words[kd];
+    if (n_shared > 0 && k_mq_words[mq_code(sg->type)] > wgu) wgu = k_mq_words[mq_code(sg->type)];
+    if (n_shared > 0 && k_mq_words[mq_code(sd->type)] > wdn) wdn = k_mq_words[mq_code(sd->type)];
     const int64_t tiles_i = (I + 15) / 16, tiles_h = (H + 15) / 16;
-    const int64_t dn_grid = tiles_h < MQ_CUS ? tiles_h : MQ_CUS;
-    const int64_t nk = (tiles_h + dn_grid - 1) / dn_grid;   /* row groups per down workgroup */
-    pl->dn_lds = 128 + (size_t)n_slots * mq_xq_bytes(I) + 2 * (size_t)wdn * 16 * 4 + (size_t)nk * 16 * 4 +
-                 (size_t)n_slots * 8;
-    if (pl->gu_lds > g_lds_max || pl->dn_lds > g_lds_max) return 0;
     int64_t wps = MQ_CUS / n_slots;
     if (wps < 1) wps = 1;
     if (wps > tiles_i) wps = tiles_i;
+    const int64_t nk_gu = (tiles_i + wps - 1) / wps;
+    if (!mq_geo(kg, wgu, 2 * nk_gu, H / 1024, MQ_ZERO + mq_xq_bytes(H) + MQ_SEL_BYTES, &pl->gu_threads, &pl->gu_geo,
+                &pl->gu_lds))
+        return 0;
+    const int64_t per = (tiles_h + MQ_CUS - 1) / MQ_CUS;   /* down row groups per workgroup */
+    const size_t dn_fixed = MQ_ZERO + (size_t)n_slots * mq_xq_bytes(I) + (size_t)n_slots * 4 + 256;
+    if (!mq_geo(kd, wdn, per * n_slots, I / 1024, dn_fixed, &pl->dn_threads, &pl->dn_geo, &pl->dn_lds)) return 0;
     pl->wps = (int32_t)wps;
     pl->gu_grid = (unsigned)(wps * n_slots);
-    pl->dn_grid = (unsigned)dn_grid;
+    pl->dn_grid = (unsigned)((tiles_h + per - 1) / per);
     return 1;
 }
 
@@ -1161,18 +1229,26 @@ static int mq_ffn_plan(const MoeProj *g, const MoeProj *u, const MoeProj *d, con
 static int ffn_launch(const char *op, const MoeProj *g, const MoeProj *u, const MoeProj *d, const MoeProj *sg,
                       const MoeProj *su, const MoeProj *sd, const int32_t *sel_idx, const float *sel_w, int32_t fixed,
                       int32_t topk, int32_t n_shared, int64_t H, int64_t I, const uint8_t *xdev, float *ydev,
-                      uint8_t *scr) {
+                      uint8_t *scr, const MqRoute *route) {
     int32_t n_slots = topk + n_shared;
     int64_t inter = I, hid = H;
     MqFfnPlan pl;
     if (mq_ffn_plan(g, u, d, sg, su, sd, topk, n_shared, H, I, &pl)) {
         int32_t inter32 = (int32_t)I, wps = pl.wps;
         float *h = (float *)scr;
+        MqRoute rt;
+        memset(&rt, 0, sizeof rt);
+        if (route) rt = *route;
         void *a_gu[] = { (void *)g, (void *)u, (void *)sg, (void *)su, &sel_idx, &fixed, &topk, &inter32, &wps, &xdev,
-                         &h };
-        if (!launch_lds(pl.k_gu, pl.gu_grid, pl.gu_threads, pl.gu_lds, a_gu, op)) return 0;
-        void *a_dn[] = { (void *)d, (void *)sd, &sel_idx, &sel_w, &fixed, &topk, &n_shared, &inter32, &hid, &h, &ydev };
-        return launch_lds(pl.k_dn, pl.dn_grid, pl.dn_threads, pl.dn_lds, a_dn, op);
+                         &h, &pl.gu_geo, &rt };
+        if (!launch_lds(K_MQ_GU, pl.gu_grid, pl.gu_threads, pl.gu_lds, a_gu, op)) return 0;
+        void *a_dn[] = { (void *)d, (void *)sd, &sel_idx, &sel_w, &fixed, &topk, &n_shared, &inter32, &hid, &h, &ydev,
+                         &pl.dn_geo };
+        return launch_lds(K_MQ_DN, pl.dn_grid, pl.dn_threads, pl.dn_lds, a_dn, op);
+    }
+    if (route) {
+        LOG("%s: in-kernel selection needs the matrix-core FFN", op);
+        return 0;
     }
     const int cr = tile_code(g->type), cdr = tile_code(d->type);
     const int cs = n_shared > 0 ? tile_code(sg->type) : cr, cds = n_shared > 0 ? tile_code(sd->type) : cdr;
@@ -1266,10 +1342,18 @@ int sepia_gpu_moe_decode(const SepiaMoeLayerDesc *L, SepiaGpuBuf *x, SepiaGpuBuf
     int64_t ld = H, hid = H;
     int32_t nr = L->n_routed, ns = L->n_shared, tk = L->topk;
     float rs = L->route_scale, gsc = L->global_scale;
-    void *a_route[] = { &rw, &ld, &rb, &x->dev, &hid, &nr, &ns, &tk, &rs, &gsc, &logits, &sel_idx, &sel_w, &counter };
+    /* with the matrix-core FFN the gate/up launch selects from the logits;
+     * otherwise the router's last workgroup does */
+    MqFfnPlan pl;
+    const int in_kernel = mq_ffn_plan(&g, &u, &d, &sg, &su, &sd, tk, ns, H, I, &pl);
+    int32_t select = !in_kernel;
+    void *a_route[] = { &rw, &ld, &rb, &x->dev, &hid, &nr, &ns, &tk, &rs, &gsc, &logits, &sel_idx, &sel_w, &counter,
+                        &select };
     if (!launch(K_MOE_ROUTE, (unsigned)n_tot, 256, a_route, op)) return 0;
 
-    if (!ffn_launch(op, &g, &u, &d, &sg, &su, &sd, sel_idx, sel_w, 0, tk, ns, H, I, x->dev, (float *)y->dev, s + o_h))
+    const MqRoute rt = { logits, rb, nr, ns, rs, gsc, sel_idx, sel_w };
+    if (!ffn_launch(op, &g, &u, &d, &sg, &su, &sd, sel_idx, sel_w, 0, tk, ns, H, I, x->dev, (float *)y->dev, s + o_h,
+                    in_kernel ? &rt : NULL))
         return 0;
 
     if (route_out) {
@@ -1306,5 +1390,5 @@ int sepia_gpu_expert_ffn(const SepiaExpertTensor *gate, const SepiaExpertTensor 
         !prep_out(y, op))
         return 0;
     return ffn_launch(op, &g, &u, &d, &none, &none, &none, NULL, NULL, expert, 1, 0, hidden, inter, x->dev,
-                      (float *)y->dev, scr);
+                      (float *)y->dev, scr, NULL);
 }

@@ -236,6 +236,74 @@ def test_matvec_q_kernel_paths(dev, orc, kernel_path, t, out_dim, in_dim):
     check_matvec(dev, orc, t, out_dim, in_dim, seed=out_dim * 7 + t)
 
 
+class Launches:
+    """Counts, per kernel name, the launches of the dev.run calls made inside
+    the block (the library's launch profiler, sepia_hip_profile_*)."""
+
+    def __init__(self, dev):
+        self.dev = dev
+
+    def __enter__(self):
+        dev, L = self.dev, self.dev.L
+        self.orig = dev.run
+        L.sepia_hip_profile_reset()
+
+        def run(fn, *args):
+            dev.begin()
+            try:
+                assert L.sepia_hip_profile_start() == 1
+                ok = fn(*args)
+                assert L.sepia_hip_profile_stop() == 1
+            finally:
+                end_ok = L.sepia_gpu_end()
+            dev.check(ok, fn.__name__)
+            dev.check(end_ok, "end")
+
+        dev.run = run
+        return self
+
+    def __exit__(self, *exc):
+        self.dev.run = self.orig
+
+    def count(self, kernel):
+        import ctypes
+        n, ms = ctypes.c_int64(), ctypes.c_double()
+        assert self.dev.L.sepia_hip_profile_query(kernel.encode(), ctypes.byref(n), ctypes.byref(ms)) == 1
+        return n.value
+
+
+@pytest.fixture
+def mq_geometry(dev, request):
+    """Force the matrix-core workgroup geometry: P parts per item, C items side
+    by side, S ring stages per wave."""
+    L = dev.L
+    for k, v in zip(("mq_p", "mq_c", "mq_s"), request.param):
+        assert L.sepia_hip_set_option(k.encode(), v) == 1
+    yield request.param
+    for k in ("mq_p", "mq_c", "mq_s"):
+        L.sepia_hip_set_option(k.encode(), 0)
+
+
+MQ_NAMES = {10: "sepia_mq_mv_q2_k", 11: "sepia_mq_mv_q3_k", 12: "sepia_mq_mv_q4_k"}
+# (type, rows, cols, (P, C, S)): several items per workgroup (12288 and 8200
+# rows), long rows (12288 columns: 12 quads), partial row groups, every ring
+# depth, parts that do not divide the quads.
+MQ_GEOMETRIES = [
+    (10, 12288, 2048, (1, 1, 1)), (10, 12288, 2048, (1, 1, 3)), (10, 12288, 2048, (2, 1, 2)),
+    (10, 12288, 2048, (1, 3, 2)), (10, 12288, 2048, (2, 2, 3)),
+    (11, 70, 12288, (1, 1, 3)), (11, 70, 12288, (5, 1, 2)), (11, 70, 12288, (3, 1, 1)),
+    (12, 8200, 4096, (1, 1, 2)), (12, 8200, 4096, (4, 3, 1)), (12, 8200, 4096, (3, 2, 2)),
+]
+
+
+@pytest.mark.parametrize("t,out_dim,in_dim,mq_geometry", MQ_GEOMETRIES, indirect=["mq_geometry"],
+                         ids=lambda v: str(v))
+def test_matvec_mq_geometries(dev, orc, t, out_dim, in_dim, mq_geometry):
+    with Launches(dev) as n:
+        check_matvec(dev, orc, t, out_dim, in_dim, seed=out_dim + in_dim + t)
+        assert n.count(MQ_NAMES[t]) == 1, "the matrix-core kernel did not run"
+
+
 @pytest.mark.parametrize("t,w_off", [(10, 4), (10, 132), (12, 4), (12, 1028), (11, 2), (11, 4)])
 def test_matvec_q_tile_offsets(dev, orc, t, w_off):
     check_matvec(dev, orc, t, 100, 2048, seed=3 + w_off, w_off=w_off)
@@ -495,6 +563,27 @@ def test_moe_decode_c3_shape(dev, orc, rw_off):
     if chosen != list(idx_ref):
         y_ref, _, _, _ = orc.moe_layer(spec, x, force_idx=chosen, threads=THREADS)
     assert_close(y, y_ref, what="moe c3 shape", gate=False)
+    for b in bufs.values():
+        dev.free(b)
+
+
+@pytest.mark.parametrize("mq_geometry", [(1, 1, 1), (1, 3, 2), (3, 1, 2), (2, 1, 3)], indirect=True,
+                         ids=lambda v: str(v))
+def test_moe_decode_mq_geometries(dev, orc, mq_geometry):
+    """C3 layer shapes (16 routed experts resident) under forced matrix-core
+    geometries; both FFN kernels must be the matrix-core ones."""
+    rng = np.random.default_rng(77)
+    desc, spec, bufs = make_layer(dev, rng, hidden=6144, inter=3072, n_routed=16, n_shared=2,
+                                  tg=10, tu=10, td=11, ts=12)
+    x = synth.normal_vector(rng, 6144)
+    with Launches(dev) as n:
+        y, idx, w = run_moe(dev, desc, x)
+        assert n.count("sepia_mq_gateup") == 1 and n.count("sepia_mq_down") == 1
+    y_ref, logits, idx_ref, w_ref = orc.moe_layer(spec, x, threads=THREADS)
+    chosen = check_route(orc, spec, logits, idx, w)
+    if chosen != list(idx_ref):
+        y_ref, _, _, _ = orc.moe_layer(spec, x, force_idx=chosen, threads=THREADS)
+    assert_close(y, y_ref, what="moe mq %s" % (mq_geometry,), gate=False)
     for b in bufs.values():
         dev.free(b)
 
