@@ -653,16 +653,22 @@ struct MqRoute {
     float *w_out;
 };
 
-// grid = n_slots * wps: workgroup k serves slot k / wps and its row groups
-// k % wps, + wps, ... Routed slots (< topk) take their expert from the
-// selection, sel_idx or fixed + slot; the later slots are the shared
-// experts. h is [n_slots][inter] f32.
+// grid = topk * wps_r + n_shared * wps_s: the first topk * wps_r workgroups
+// serve the routed slots, wps_r each (workgroup k: slot k / wps_r, row
+// groups k % wps_r, + wps_r, ...), the rest the shared slots, wps_s each.
+// Routed slots take their expert from the selection, sel_idx or fixed +
+// slot; shared slot topk + i is shared expert i. h is [n_slots][inter] f32.
 __device__ __forceinline__ void mq_gateup(const MqProj &gate, const MqProj &up, const MqProj &s_gate,
                                           const MqProj &s_up, const int32_t *__restrict__ sel_idx, int32_t fixed,
-                                          int32_t topk, int32_t inter, int32_t wps, const float *__restrict__ x,
-                                          float *__restrict__ h, MqGeo geo, const MqRoute &rt) {
+                                          int32_t topk, int32_t inter, int32_t wps_r, int32_t wps_s,
+                                          const float *__restrict__ x, float *__restrict__ h, MqGeo geo,
+                                          const MqRoute &rt) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    const int32_t slot = (int32_t)blockIdx.x / wps, j0 = (int32_t)blockIdx.x - slot * wps;
+    const int32_t bid = (int32_t)blockIdx.x;
+    const bool rk = bid < topk * wps_r;
+    const int32_t wps = rk ? wps_r : wps_s;
+    const int32_t k0 = rk ? bid : bid - topk * wps_r;
+    const int32_t slot = (rk ? 0 : topk) + k0 / wps, j0 = k0 % wps;
     int64_t e;
     if (rt.logits && slot < topk) {
         int32_t *si = (int32_t *)(smem + MQ_ZERO + mq_xq_bytes(256 * gate.n_blocks));
@@ -694,98 +700,116 @@ __device__ __forceinline__ void mq_gateup(const MqProj &gate, const MqProj &up, 
 #define SEPIA_MQ_GATEUP()                                                                                \
     extern "C" __global__ __launch_bounds__(1024) void sepia_mq_gateup(                                  \
         MqProj gate, MqProj up, MqProj s_gate, MqProj s_up, const int32_t *__restrict__ sel_idx,         \
-        int32_t fixed, int32_t topk, int32_t inter, int32_t wps, const float *__restrict__ x,            \
-        float *__restrict__ h, MqGeo geo, MqRoute rt) {                                                  \
-        mq_gateup(gate, up, s_gate, s_up, sel_idx, fixed, topk, inter, wps, x, h, geo, rt);              \
+        int32_t fixed, int32_t topk, int32_t inter, int32_t wps_r, int32_t wps_s,                        \
+        const float *__restrict__ x, float *__restrict__ h, MqGeo geo, MqRoute rt) {                     \
+        mq_gateup(gate, up, s_gate, s_up, sel_idx, fixed, topk, inter, wps_r, wps_s, x, h, geo, rt);     \
     }
 
-// Down of every slot for the workgroup's row groups of y (rg_k =
-// blockIdx.x + k * gridDim.x, k < nk). The slots run in two phases, the
-// routed ones (format of `down`) then the shared ones (format of `s_down`),
-// each its own pipeline over items (k, slot). Each row's slot sums are added
-// in slot order, weighted by sel_w (routed weights, then the shared gammas;
-// the shared gamma scales the down output as src/sepia.c:3953-3957 does);
-// y is stored once at the end -- deterministic, no atomics. h
-// [n_slots][inter] f32 is staged as XQ once per workgroup.
-// LDS: [zero][n_slots x XQ of h][red: nk x n_slots x P x 16 f32]
-//      [n_slots i32 experts][rings].
-// One phase: the items (k, slot) of slots slot0 .. slot0 + nsl - 1. When
-// hs is set, the workgroup stages the n_slots h vectors as XQ between the
-// phase's first DMAs and its compute, so that both overlap.
+// Down, one slot per workgroup: workgroups [0, topk * wps_r) serve the
+// routed slots (wps_r each), the rest the shared slots (wps_s each). A
+// workgroup owns row groups j0, j0 + jstep, ... of y for its slot (one item
+// each) and stages only its slot's h as XQ. With a single slot (the expert
+// FFN) it stores w * its rows into y. With several it publishes its rows to
+// ypart[slot] (agent-scope stores, waited for), then bumps each of its row
+// groups' arrival counters; the workgroup that completes a row group adds
+// the n_slots partial rows in slot order, weighted by sel_w (routed weights,
+// then the shared gammas; the shared gamma scales the down output as
+// src/sepia.c:3953-3957 does), into y and puts the counter back to zero --
+// deterministic whatever the arrival order.
+// LDS: [zero][XQ of h_slot][red: nk x P x 16 f32][flags: nk i32][rings].
 template <int T>
-__device__ __forceinline__ void mq_dn_phase(const MqProj &Pj, const int32_t *e_lds, int slot0, int nsl, int n_slots,
-                                            int nk, int64_t hidden, int inter, uint32_t xqb, MqGeo geo,
-                                            uint8_t *rings, uint8_t *lds0, float *red, const float *hs) {
+__device__ __forceinline__ void mq_dn_slot(const uint8_t *Wd, uint64_t row_bytes, int32_t nb, int32_t inter,
+                                           int64_t hidden, int32_t j0, int32_t jstep, int nk,
+                                           const float *__restrict__ hs, MqGeo geo, float *red, uint8_t *rings,
+                                           uint8_t *lds0) {
     auto item_of = [&](int i) {
-        const int k = i / nsl, slot = slot0 + (i - k * nsl);
-        const int64_t e = __builtin_amdgcn_readfirstlane(e_lds[slot]);
         MqItem it;
-        it.base = Pj.base + e * Pj.stride;
-        it.row0 = ((int64_t)blockIdx.x + (int64_t)k * gridDim.x) * 16;
+        it.base = Wd;
+        it.row0 = ((int64_t)j0 + (int64_t)i * jstep) * 16;
         it.rows = hidden;
-        it.xoff = MQ_ZERO + (uint32_t)slot * xqb;
-        it.red = k * n_slots + slot;
+        it.xoff = MQ_ZERO;
+        it.red = i;
         return it;
     };
-    MqWave<T, decltype(item_of)> wv(item_of, nk * nsl, (int)(Pj.n_blocks >> 2), inter, (uint32_t)Pj.row_bytes, geo,
-                                    rings);
+    MqWave<T, decltype(item_of)> wv(item_of, nk, nb >> 2, inter, (uint32_t)row_bytes, geo, rings);
     wv.prologue();
-    if (hs) mq_stage_xq(hs, inter, n_slots, inter, lds0, MQ_ZERO, xqb);
+    mq_stage_xq(hs, 0, 1, inter, lds0, MQ_ZERO, 0u);
     wv.run(lds0, red);
-}
-
-__device__ __forceinline__ void mq_dn_any(const MqProj &Pj, const int32_t *e_lds, int slot0, int nsl, int n_slots,
-                                          int nk, int64_t hidden, int inter, uint32_t xqb, MqGeo geo, uint8_t *rings,
-                                          uint8_t *lds0, float *red, const float *hs) {
-    switch (Pj.type) {
-    case ST_Q2_K: mq_dn_phase<ST_Q2_K>(Pj, e_lds, slot0, nsl, n_slots, nk, hidden, inter, xqb, geo, rings, lds0, red, hs); break;
-    case ST_Q3_K: mq_dn_phase<ST_Q3_K>(Pj, e_lds, slot0, nsl, n_slots, nk, hidden, inter, xqb, geo, rings, lds0, red, hs); break;
-    default: mq_dn_phase<ST_Q4_K>(Pj, e_lds, slot0, nsl, n_slots, nk, hidden, inter, xqb, geo, rings, lds0, red, hs); break;
-    }
 }
 
 __device__ __forceinline__ void mq_down(const MqProj &down, const MqProj &s_down, const int32_t *__restrict__ sel_idx,
                                         const float *__restrict__ sel_w, int32_t fixed, int32_t topk,
                                         int32_t n_shared, int32_t inter, int64_t hidden, const float *__restrict__ h,
-                                        float *__restrict__ y, MqGeo geo) {
+                                        float *__restrict__ y, MqGeo geo, int32_t wps_r, int32_t wps_s,
+                                        float *__restrict__ ypart, uint32_t *__restrict__ cnt) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int n_slots = topk + n_shared;
-    const int64_t tiles = (hidden + 15) >> 4, G = gridDim.x;
-    const int nk = tiles > blockIdx.x ? (int)((tiles - blockIdx.x + G - 1) / G) : 0;
-    const uint32_t xqb = (uint32_t)mq_xq_bytes(inter);
-    const size_t o_red = MQ_ZERO + (size_t)n_slots * xqb;
-    const size_t red_bytes = (size_t)nk * n_slots * geo.P * 64;
+    const int32_t bid = (int32_t)blockIdx.x;
+    const bool routed = bid < topk * wps_r;
+    const int32_t jstep = routed ? wps_r : wps_s;
+    const int32_t k0 = routed ? bid : bid - topk * wps_r;
+    const int32_t slot = (routed ? 0 : topk) + k0 / jstep, j0 = k0 % jstep;
+    const int64_t e = mq_slot_expert(sel_idx, fixed, slot, topk);
+    const MqProj &Pj = routed ? down : s_down;
+    const uint8_t *Wd = Pj.base + e * Pj.stride;
+    const int tiles = (int)((hidden + 15) >> 4);
+    const int nk = j0 < tiles ? (tiles - j0 + jstep - 1) / jstep : 0;
+    const size_t o_red = MQ_ZERO + mq_xq_bytes(inter);
     float *red = (float *)(smem + o_red);
-    int32_t *e_lds = (int32_t *)(smem + o_red + red_bytes);
-    uint8_t *rings = smem + ((o_red + red_bytes + (size_t)n_slots * 4 + 255) & ~(size_t)255);
-    if (threadIdx.x < n_slots) e_lds[threadIdx.x] = (int32_t)mq_slot_expert(sel_idx, fixed, threadIdx.x, topk);
+    int32_t *flag = (int32_t *)(smem + o_red + (size_t)nk * geo.P * 64);
+    uint8_t *rings = smem + ((o_red + (size_t)nk * geo.P * 64 + (size_t)nk * 4 + 255) & ~(size_t)255);
+    const float *hs = h + (int64_t)slot * inter;
+    const int32_t nb = (int32_t)Pj.n_blocks;
+    switch (Pj.type) {
+    case ST_Q2_K: mq_dn_slot<ST_Q2_K>(Wd, Pj.row_bytes, nb, inter, hidden, j0, jstep, nk, hs, geo, red, rings, smem); break;
+    case ST_Q3_K: mq_dn_slot<ST_Q3_K>(Wd, Pj.row_bytes, nb, inter, hidden, j0, jstep, nk, hs, geo, red, rings, smem); break;
+    default: mq_dn_slot<ST_Q4_K>(Wd, Pj.row_bytes, nb, inter, hidden, j0, jstep, nk, hs, geo, red, rings, smem); break;
+    }
     __syncthreads();
-    // the rings have one place per wave whatever the phase's format: a wave
-    // may start the second phase while another still reads its ring of the
-    // first
-    if (topk > 0) {
-        mq_dn_any(down, e_lds, 0, topk, n_slots, nk, hidden, inter, xqb, geo, rings, smem, red, h);
-        if (n_shared > 0)
-            mq_dn_any(s_down, e_lds, topk, n_shared, n_slots, nk, hidden, inter, xqb, geo, rings, smem, red, nullptr);
-    } else {
-        mq_dn_any(s_down, e_lds, 0, n_shared, n_slots, nk, hidden, inter, xqb, geo, rings, smem, red, h);
+    if (n_slots == 1) {
+        const float w = sel_w ? sel_w[0] : 1.0f;
+        for (int i = threadIdx.x; i < nk * 16; i += blockDim.x) {
+            const int64_t r = ((int64_t)j0 + (int64_t)(i >> 4) * jstep) * 16 + (i & 15);
+            if (r < hidden) y[r] = w * mq_red_sum(red, i >> 4, geo.P, i & 15);
+        }
+        return;
+    }
+    for (int i = threadIdx.x; i < nk * 16; i += blockDim.x) {
+        const int64_t r = ((int64_t)j0 + (int64_t)(i >> 4) * jstep) * 16 + (i & 15);
+        if (r < hidden)
+            __hip_atomic_store(&ypart[(int64_t)slot * hidden + r], mq_red_sum(red, i >> 4, geo.P, i & 15),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __builtin_amdgcn_s_waitcnt(0);   // this thread's partial stores have completed
+    __syncthreads();
+    for (int k = threadIdx.x; k < nk; k += blockDim.x) {
+        const uint32_t prev =
+            __hip_atomic_fetch_add(&cnt[j0 + k * jstep], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        flag[k] = prev == (uint32_t)(n_slots - 1);
     }
     __syncthreads();
     for (int i = threadIdx.x; i < nk * 16; i += blockDim.x) {
-        const int k = i >> 4, t = i & 15;
-        const int64_t r = ((int64_t)blockIdx.x + (int64_t)k * G) * 16 + t;
+        if (!flag[i >> 4]) continue;
+        const int64_t r = ((int64_t)j0 + (int64_t)(i >> 4) * jstep) * 16 + (i & 15);
         if (r >= hidden) continue;
         float acc = 0.0f;
         for (int sl = 0; sl < n_slots; sl++)
-            acc = __builtin_fmaf(sel_w ? sel_w[sl] : 1.0f, mq_red_sum(red, k * n_slots + sl, geo.P, t), acc);
+            acc = __builtin_fmaf(sel_w ? sel_w[sl] : 1.0f,
+                                 __hip_atomic_load(&ypart[(int64_t)sl * hidden + r], __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT),
+                                 acc);
         y[r] = acc;
     }
+    for (int k = threadIdx.x; k < nk; k += blockDim.x)
+        if (flag[k]) __hip_atomic_store(&cnt[j0 + k * jstep], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 #define SEPIA_MQ_DOWN()                                                                                  \
     extern "C" __global__ __launch_bounds__(1024) void sepia_mq_down(                                    \
         MqProj down, MqProj s_down, const int32_t *__restrict__ sel_idx, const float *__restrict__ sel_w, \
         int32_t fixed, int32_t topk, int32_t n_shared, int32_t inter, int64_t hidden,                    \
-        const float *__restrict__ h, float *__restrict__ y, MqGeo geo) {                                 \
-        mq_down(down, s_down, sel_idx, sel_w, fixed, topk, n_shared, inter, hidden, h, y, geo);          \
+        const float *__restrict__ h, float *__restrict__ y, MqGeo geo, int32_t wps_r, int32_t wps_s,     \
+        float *__restrict__ ypart, uint32_t *__restrict__ cnt) {                                         \
+        mq_down(down, s_down, sel_idx, sel_w, fixed, topk, n_shared, inter, hidden, h, y, geo, wps_r,    \
+                wps_s, ypart, cnt);                                                                      \
     }

@@ -1161,7 +1161,11 @@ typedef struct {
 } XpArgs;
 
 /* Scratch bytes for n_slots f32 activation vectors of length I. */
-static size_t ffn_scratch_bytes(int n_slots, int64_t I) { return (size_t)n_slots * (size_t)I * 4; }
+/* FFN scratch: h [n_slots][I] f32, then the down partial rows [n_slots][H]
+ * f32 (matrix-core path with several slots). */
+static size_t ffn_scratch_bytes(int n_slots, int64_t I, int64_t H) {
+    return (size_t)n_slots * (size_t)I * 4 + (size_t)n_slots * (size_t)H * 4;
+}
 
 /* Index of a format among the tile kernels' {Q2_K, Q3_K, Q4_K}, -1 if none. */
 static int tile_code(int t) { return t == SEPIA_T_Q2_K ? 0 : (t == SEPIA_T_Q3_K ? 1 : (t == 12 ? 2 : -1)); }
@@ -1175,17 +1179,31 @@ static int proj_aligned(const MoeProj *p) {
 /* Matrix-core FFN plan (kernels/mq.h): every projection in {Q2_K, Q3_K,
  * Q4_K} with a shape the kernels take, gate and up of one format per slot
  * kind, H and I multiples of 1024 (rows of whole quads), LDS within the
- * device limit. gate/up runs wps workgroups per slot, each over its row
- * groups (gate and up rows as two items each); down runs workgroups over
- * row groups of y, each through every slot. */
+ * device limit. Both launches give each slot its own workgroups, wps_r per
+ * routed slot and wps_s per shared one, in proportion to the slot's bytes
+ * (about one workgroup per CU in all); a workgroup walks row groups j0,
+ * j0 + wps, ... of its slot. Down workgroups combine the slots' partial rows
+ * through per-row-group arrival counters (in the counter region, after the
+ * router's). */
 typedef struct {
     unsigned gu_threads, dn_threads, gu_grid, dn_grid;
-    int32_t wps;
+    int32_t gu_wps_r, gu_wps_s, dn_wps_r, dn_wps_s;
     size_t gu_lds, dn_lds;
     MqGeo gu_geo, dn_geo;
 } MqFfnPlan;
+#define MQ_DN_CNT_OFF 64            /* first down arrival counter (u32 index in the counter region) */
 static int mq_proj_ok(const MoeProj *p, int64_t rows) {
     return mq_shape_ok(p->type, p->n_blocks, rows, (uintptr_t)p->base, p->row_bytes) && p->stride % 4 == 0;
+}
+/* Workgroups per slot for slots of byte weights br (routed) and bs (shared):
+ * about MQ_CUS in all, at most `tiles` per slot. */
+static void mq_split(int32_t topk, int32_t n_shared, double br, double bs, int64_t tiles, int32_t *wr, int32_t *ws) {
+    const double tot = topk * br + n_shared * bs;
+    int64_t r = (int64_t)(MQ_CUS * br / tot + 0.5), sh = (int64_t)(MQ_CUS * bs / tot + 0.5);
+    if (r < 1) r = 1;
+    if (sh < 1) sh = 1;
+    *wr = (int32_t)(r < tiles ? r : tiles);
+    *ws = (int32_t)(sh < tiles ? sh : tiles);
 }
 static int mq_ffn_plan(const MoeProj *g, const MoeProj *u, const MoeProj *d, const MoeProj *sg, const MoeProj *su,
                        const MoeProj *sd, int32_t topk, int32_t n_shared, int64_t H, int64_t I, MqFfnPlan *pl) {
@@ -1195,7 +1213,8 @@ static int mq_ffn_plan(const MoeProj *g, const MoeProj *u, const MoeProj *d, con
     for (int i = 0; i < (n_shared > 0 ? 6 : 3); i++)
         if (!mq_proj_ok(ps[i], rows[i])) return 0;
     if (g->type != u->type || (n_shared > 0 && sg->type != su->type)) return 0;
-    const int n_slots = topk + n_shared;
+    const int64_t tiles_i = (I + 15) / 16, tiles_h = (H + 15) / 16;
+    if (n_shared + topk > 1 && MQ_DN_CNT_OFF + tiles_h > CNT_BYTES / 4) return 0;
     /* both slot kinds share a geometry: planned for the format of the
      * routed slots (the shared ones when there are none), with rings that
      * hold a step of either */
@@ -1203,20 +1222,21 @@ static int mq_ffn_plan(const MoeProj *g, const MoeProj *u, const MoeProj *d, con
     int wgu = k_mq_words[kg], wdn = k_mq_words[kd];
     if (n_shared > 0 && k_mq_words[mq_code(sg->type)] > wgu) wgu = k_mq_words[mq_code(sg->type)];
     if (n_shared > 0 && k_mq_words[mq_code(sd->type)] > wdn) wdn = k_mq_words[mq_code(sd->type)];
-    const int64_t tiles_i = (I + 15) / 16, tiles_h = (H + 15) / 16;
-    int64_t wps = MQ_CUS / n_slots;
-    if (wps < 1) wps = 1;
-    if (wps > tiles_i) wps = tiles_i;
-    const int64_t nk_gu = (tiles_i + wps - 1) / wps;
+    mq_split(topk, n_shared, (double)g->row_bytes, n_shared > 0 ? (double)sg->row_bytes : 1.0, tiles_i,
+             &pl->gu_wps_r, &pl->gu_wps_s);
+    mq_split(topk, n_shared, (double)d->row_bytes, n_shared > 0 ? (double)sd->row_bytes : 1.0, tiles_h,
+             &pl->dn_wps_r, &pl->dn_wps_s);
+    const int32_t gmin = pl->gu_wps_r < pl->gu_wps_s || n_shared == 0 ? pl->gu_wps_r : pl->gu_wps_s;
+    const int32_t dmin = pl->dn_wps_r < pl->dn_wps_s || n_shared == 0 ? pl->dn_wps_r : pl->dn_wps_s;
+    const int64_t nk_gu = (tiles_i + gmin - 1) / gmin, nk_dn = (tiles_h + dmin - 1) / dmin;
     if (!mq_geo(kg, wgu, 2 * nk_gu, H / 1024, MQ_ZERO + mq_xq_bytes(H) + MQ_SEL_BYTES, &pl->gu_threads, &pl->gu_geo,
                 &pl->gu_lds))
         return 0;
-    const int64_t per = (tiles_h + MQ_CUS - 1) / MQ_CUS;   /* down row groups per workgroup */
-    const size_t dn_fixed = MQ_ZERO + (size_t)n_slots * mq_xq_bytes(I) + (size_t)n_slots * 4 + 256;
-    if (!mq_geo(kd, wdn, per * n_slots, I / 1024, dn_fixed, &pl->dn_threads, &pl->dn_geo, &pl->dn_lds)) return 0;
-    pl->wps = (int32_t)wps;
-    pl->gu_grid = (unsigned)(wps * n_slots);
-    pl->dn_grid = (unsigned)((tiles_h + per - 1) / per);
+    if (!mq_geo(kd, wdn, nk_dn, I / 1024, MQ_ZERO + mq_xq_bytes(I) + (size_t)nk_dn * 4 + 256, &pl->dn_threads,
+                &pl->dn_geo, &pl->dn_lds))
+        return 0;
+    pl->gu_grid = (unsigned)(topk * pl->gu_wps_r + n_shared * pl->gu_wps_s);
+    pl->dn_grid = (unsigned)(topk * pl->dn_wps_r + n_shared * pl->dn_wps_s);
     return 1;
 }
 
@@ -1234,16 +1254,18 @@ static int ffn_launch(const char *op, const MoeProj *g, const MoeProj *u, const 
     int64_t inter = I, hid = H;
     MqFfnPlan pl;
     if (mq_ffn_plan(g, u, d, sg, su, sd, topk, n_shared, H, I, &pl)) {
-        int32_t inter32 = (int32_t)I, wps = pl.wps;
+        int32_t inter32 = (int32_t)I;
         float *h = (float *)scr;
+        float *ypart = (float *)(scr + (size_t)n_slots * (size_t)I * 4);
+        uint32_t *cnt = (uint32_t *)g_scratch + MQ_DN_CNT_OFF;
         MqRoute rt;
         memset(&rt, 0, sizeof rt);
         if (route) rt = *route;
-        void *a_gu[] = { (void *)g, (void *)u, (void *)sg, (void *)su, &sel_idx, &fixed, &topk, &inter32, &wps, &xdev,
-                         &h, &pl.gu_geo, &rt };
+        void *a_gu[] = { (void *)g, (void *)u, (void *)sg, (void *)su, &sel_idx, &fixed, &topk, &inter32, &pl.gu_wps_r,
+                         &pl.gu_wps_s, &xdev, &h, &pl.gu_geo, &rt };
         if (!launch_lds(K_MQ_GU, pl.gu_grid, pl.gu_threads, pl.gu_lds, a_gu, op)) return 0;
         void *a_dn[] = { (void *)d, (void *)sd, &sel_idx, &sel_w, &fixed, &topk, &n_shared, &inter32, &hid, &h, &ydev,
-                         &pl.dn_geo };
+                         &pl.dn_geo, &pl.dn_wps_r, &pl.dn_wps_s, &ypart, &cnt };
         return launch_lds(K_MQ_DN, pl.dn_grid, pl.dn_threads, pl.dn_lds, a_dn, op);
     }
     if (route) {
@@ -1325,7 +1347,7 @@ int sepia_gpu_moe_decode(const SepiaMoeLayerDesc *L, SepiaGpuBuf *x, SepiaGpuBuf
     const size_t o_idx = o_logits + (((size_t)n_tot * 4 + 255) & ~(size_t)255);
     const size_t o_w = o_idx + 256;
     const size_t o_h = o_w + 256;
-    uint8_t *s = (uint8_t *)scratch(o_h + ffn_scratch_bytes(n_slots, I), op);
+    uint8_t *s = (uint8_t *)scratch(o_h + ffn_scratch_bytes(n_slots, I, H), op);
     if (!s) return 0;
     float *logits = (float *)(s + o_logits), *sel_w = (float *)(s + o_w);
     int32_t *sel_idx = (int32_t *)(s + o_idx);
@@ -1384,7 +1406,7 @@ int sepia_gpu_expert_ffn(const SepiaExpertTensor *gate, const SepiaExpertTensor 
         return 0;
     if (!chk(x, 0, (size_t)hidden * 4, op, "x") || !chk(y, 0, (size_t)hidden * 4, op, "y")) return 0;
     if (!need_batch(op)) return 0;
-    uint8_t *scr = (uint8_t *)scratch(ffn_scratch_bytes(1, inter), op);
+    uint8_t *scr = (uint8_t *)scratch(ffn_scratch_bytes(1, inter, hidden), op);
     if (!scr) return 0;
     if (!prep_in(gate->buf, op) || !prep_in(up->buf, op) || !prep_in(down->buf, op) || !prep_in(x, op) ||
         !prep_out(y, op))
