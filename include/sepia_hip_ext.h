@@ -56,6 +56,18 @@ typedef struct {
 int sepia_gpu_moe_decode(const SepiaMoeLayerDesc *layer, SepiaGpuBuf *x, SepiaGpuBuf *y,
                          SepiaGpuBuf *route_out);
 
+/* The same layer for n_tokens tokens at once (prefill; reference
+ * src/sepia.c:1377-1470 applied to each token): y[t] = MoE(x[t]) with each
+ * token's routing exactly as sepia_gpu_moe_decode's up to the summation
+ * order of the router's f32 dot products. Tokens are grouped by expert and
+ * every expert's weights are read once per 32 tokens, on the bf16 matrix
+ * cores (weights and activations as bf16 hi + lo pairs, f32 accumulate).
+ * Projection formats: Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, IQ2_XS, IQ3_XXS,
+ * IQ4_XS. x, y: f32 [n_tokens][hidden] at offset 0. route_out (optional):
+ * int32 idx[n_tokens][topk] followed by f32 w[n_tokens][topk + n_shared]. */
+int sepia_gpu_moe_prefill(const SepiaMoeLayerDesc *layer, int64_t n_tokens, SepiaGpuBuf *x, SepiaGpuBuf *y,
+                          SepiaGpuBuf *route_out);
+
 /* One routed expert: y = down(silu(gate x) * up x) for expert `expert` of
  * stacks holding n_experts experts (reference src/sepia.c:2993-3017,
  * real_expert_ffn), as two launches (fused gate/up/SwiGLU, then down).

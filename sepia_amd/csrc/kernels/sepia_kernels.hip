@@ -223,6 +223,7 @@ SEPIA_FFN_PAIR(4, 4, ST_Q4_K, ST_Q4_K)
 
 #include "mq.h"
 #include "moe.h"
+#include "prefill.h"
 #include "synth.h"
 
 // ------------------------------------------------------------------------

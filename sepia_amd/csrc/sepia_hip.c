@@ -55,7 +55,9 @@ enum {
     /* matrix-core expert FFN: gate/up, down */
     K_MQ_GU = K_MQ_MV + 3,
     K_MQ_DN = K_MQ_GU + 1,
-    K_COUNT = K_MQ_DN + 1
+    /* batched prefill MoE layer (kernels/prefill.h) */
+    K_PF_ROUTE = K_MQ_DN + 1, K_PF_SELECT, K_PF_GROUP, K_PF_GATEUP, K_PF_DOWN, K_PF_COMBINE,
+    K_COUNT
 };
 #define FFN_NAMES(p) "sepia_ffn_gateup_" p, "sepia_ffn_gateup_" p "_xp", "sepia_ffn_down_" p
 static const char *const k_names[K_COUNT] = {
@@ -75,6 +77,7 @@ static const char *const k_names[K_COUNT] = {
     FFN_NAMES("22"), FFN_NAMES("23"), FFN_NAMES("24"), FFN_NAMES("32"), FFN_NAMES("33"), FFN_NAMES("34"),
     FFN_NAMES("42"), FFN_NAMES("43"), FFN_NAMES("44"),
     "sepia_mq_mv_q2_k", "sepia_mq_mv_q3_k", "sepia_mq_mv_q4_k", "sepia_mq_gateup", "sepia_mq_down",
+    "sepia_pf_route", "sepia_pf_select", "sepia_pf_group", "sepia_pf_gateup", "sepia_pf_down", "sepia_pf_combine",
 };
 #undef FFN_NAMES
 
@@ -527,23 +530,29 @@ extern hipError_t hipExtModuleLaunchKernel(hipFunction_t f, uint32_t globalWorkS
                                            hipStream_t hStream, void **kernelParams, void **extra,
                                            hipEvent_t startEvent, hipEvent_t stopEvent, uint32_t flags);
 
-static int launch_lds(int k, unsigned grid, unsigned block, size_t lds, void **args, const char *op) {
-    if (grid == 0) return 1;
+/* Launch of kernel k on a gx x gy grid of `block`-thread workgroups with
+ * `lds` bytes of dynamic LDS (timed when the profiler is on). */
+static int launch2(int k, unsigned gx, unsigned gy, unsigned block, size_t lds, void **args, const char *op) {
+    if (gx == 0 || gy == 0) return 1;
     hipError_t e;
     if (g_prof_on && g_prof_n < g_prof_ev_made) {
         const int slot = g_prof_n++;
         g_prof_kid[slot] = k;
-        e = hipExtModuleLaunchKernel(g_fn[k], grid * block, 1, 1, block, 1, 1, lds, g_stream, args, NULL,
+        e = hipExtModuleLaunchKernel(g_fn[k], gx * block, gy, 1, block, 1, 1, lds, g_stream, args, NULL,
                                      g_prof_ev[slot][0], g_prof_ev[slot][1], 0);
     } else {
         if (g_prof_on) g_prof_overflow = 1;
-        e = hipModuleLaunchKernel(g_fn[k], grid, 1, 1, block, 1, 1, (unsigned)lds, g_stream, args, NULL);
+        e = hipModuleLaunchKernel(g_fn[k], gx, gy, 1, block, 1, 1, (unsigned)lds, g_stream, args, NULL);
     }
     if (e != hipSuccess) {
         LOG("%s: launch of %s failed: %s", op, k_names[k], hipGetErrorString(e));
         return 0;
     }
     return 1;
+}
+
+static int launch_lds(int k, unsigned grid, unsigned block, size_t lds, void **args, const char *op) {
+    return launch2(k, grid, 1, block, lds, args, op);
 }
 
 static int launch(int k, unsigned grid, unsigned block, void **args, const char *op) {
@@ -1237,6 +1246,121 @@ static int mq_ffn_plan(const MoeProj *g, const MoeProj *u, const MoeProj *d, con
         return 0;
     pl->gu_grid = (unsigned)(topk * pl->gu_wps_r + n_shared * pl->gu_wps_s);
     pl->dn_grid = (unsigned)(topk * pl->dn_wps_r + n_shared * pl->dn_wps_s);
+    return 1;
+}
+
+/* Formats the prefill projections decode (kernels/prefill.h). */
+static int pf_type_ok(int t) {
+    return t == SEPIA_T_Q2_K || t == SEPIA_T_Q3_K || t == 12 || t == 13 || t == 14 || t == 17 || t == 18 || t == 23;
+}
+
+int sepia_gpu_moe_prefill(const SepiaMoeLayerDesc *L, int64_t n_tokens, SepiaGpuBuf *x, SepiaGpuBuf *y,
+                          SepiaGpuBuf *route_out) {
+    const char *op = "moe_prefill";
+    if (!L || !x || !y || n_tokens < 1 || n_tokens > (1 << 20) || L->hidden <= 0 || L->inter <= 0 ||
+        L->n_routed < 1 || L->n_routed > 1024 || L->n_shared < 0 || L->topk < 1 || L->topk > L->n_routed ||
+        L->topk + L->n_shared > 64 || !L->router_w || !L->router_bias) {
+        LOG("%s: invalid layer description", op);
+        return 0;
+    }
+    if (L->n_shared > 0 && (!L->s_gate.buf || !L->s_up.buf || !L->s_down.buf)) {
+        LOG("%s: shared expert tensors missing", op);
+        return 0;
+    }
+    const int64_t H = L->hidden, I = L->inter, T = n_tokens;
+    const int32_t nr = L->n_routed, ns = L->n_shared, tk = L->topk, n_sel = tk + ns;
+    const int64_t n_tot = nr + ns;
+    MoeProj g, u, d, sg, su, sd;
+    memset(&sg, 0, sizeof sg);
+    memset(&su, 0, sizeof su);
+    memset(&sd, 0, sizeof sd);
+    if (!moe_proj(op, "gate", &L->gate, nr, I, H, &g) || !moe_proj(op, "up", &L->up, nr, I, H, &u) ||
+        !moe_proj(op, "down", &L->down, nr, H, I, &d))
+        return 0;
+    if (ns > 0 && (!moe_proj(op, "shared gate", &L->s_gate, ns, I, H, &sg) ||
+                   !moe_proj(op, "shared up", &L->s_up, ns, I, H, &su) ||
+                   !moe_proj(op, "shared down", &L->s_down, ns, H, I, &sd)))
+        return 0;
+    const MoeProj *ps[6] = { &g, &u, &d, &sg, &su, &sd };
+    for (int i = 0; i < (ns > 0 ? 6 : 3); i++)
+        if (!pf_type_ok(ps[i]->type) || ((uintptr_t)ps[i]->base | ps[i]->stride | ps[i]->row_bytes) & 1) {
+            LOG("%s: projection %d: ggml type %d or its layout is not supported by the prefill kernels", op, i,
+                ps[i]->type);
+            return 0;
+        }
+    if (g.type != u.type || (ns > 0 && sg.type != su.type)) {
+        LOG("%s: gate and up must share a format", op);
+        return 0;
+    }
+    if (!f32_off_ok(L->router_w_off, op, "router_w") || !f32_off_ok(L->router_bias_off, op, "router_bias") ||
+        !chk(L->router_w, L->router_w_off, (size_t)n_tot * (size_t)H * 4, op, "router_w") ||
+        !chk(L->router_bias, L->router_bias_off, (size_t)nr * 4, op, "router_bias") ||
+        !chk(x, 0, (size_t)T * H * 4, op, "x") || !chk(y, 0, (size_t)T * H * 4, op, "y"))
+        return 0;
+    const size_t route_bytes = (size_t)T * (size_t)(tk + n_sel) * 4;
+    if (route_out && !chk(route_out, 0, route_bytes, op, "route_out")) return 0;
+    /* units of <= 32 pairs: routed pairs split over at most n_routed experts,
+     * each shared expert takes every token */
+    const int64_t umax = (T * tk + 31) / 32 + nr + (int64_t)ns * ((T + 31) / 32) + 1;
+    if (umax > 65535 || (H + 255) / 256 > MAX_GRID) {
+        LOG("%s: batch too large", op);
+        return 0;
+    }
+    if (!need_batch(op)) return 0;
+
+    const int64_t P = T * n_sel;
+    size_t o = 0;
+#define PF_REGION(name, bytes) const size_t name = o; o += ((size_t)(bytes) + 255) & ~(size_t)255
+    PF_REGION(o_logits, T * n_tot * 4);
+    PF_REGION(o_idx, T * tk * 4);
+    PF_REGION(o_w, P * 4);
+    PF_REGION(o_list, P * 4);
+    PF_REGION(o_units, umax * 12);
+    PF_REGION(o_nu, 4);
+    PF_REGION(o_h, P * I * 4);
+    PF_REGION(o_yp, P * H * 4);
+#undef PF_REGION
+    uint8_t *s = (uint8_t *)scratch(o, op);
+    if (!s) return 0;
+    float *logits = (float *)(s + o_logits), *sel_w = (float *)(s + o_w), *h = (float *)(s + o_h),
+          *yp = (float *)(s + o_yp);
+    int32_t *sel_idx = (int32_t *)(s + o_idx), *list = (int32_t *)(s + o_list), *units = (int32_t *)(s + o_units),
+            *n_units = (int32_t *)(s + o_nu);
+
+    SepiaGpuBuf *ins[] = { L->router_w, L->router_bias, x, L->gate.buf, L->up.buf, L->down.buf, L->s_gate.buf,
+                           L->s_up.buf, L->s_down.buf };
+    for (size_t i = 0; i < sizeof ins / sizeof ins[0]; i++)
+        if (ins[i] && !prep_in(ins[i], op)) return 0;
+    if (!prep_out(y, op) || (route_out && !prep_out(route_out, op))) return 0;
+
+    const float *rw = (const float *)(L->router_w->dev + L->router_w_off);
+    const float *rb = (const float *)(L->router_bias->dev + L->router_bias_off);
+    int64_t ld = H, hid = H, inter = I, tt = T, ntot = n_tot;
+    float rs = L->route_scale, gsc = L->global_scale;
+    int32_t nr32 = nr, ns32 = ns, tk32 = tk, nsel32 = n_sel;
+    void *a_rt[] = { &x->dev, &tt, &rw, &ld, &ntot, &hid, &logits };
+    if (!launch2(K_PF_ROUTE, (unsigned)((T + 31) / 32), (unsigned)((n_tot + 31) / 32), 256, 0, a_rt, op)) return 0;
+    void *a_sel[] = { &logits, &rb, &nr32, &ns32, &tk32, &rs, &gsc, &sel_idx, &sel_w };
+    if (!launch(K_PF_SELECT, (unsigned)T, 64, a_sel, op)) return 0;
+    void *a_grp[] = { &sel_idx, &tt, &nr32, &ns32, &tk32, &list, &units, &n_units };
+    if (!launch(K_PF_GROUP, 1, 1024, a_grp, op)) return 0;
+    void *a_gu[] = { (void *)&g, (void *)&u, (void *)&sg, (void *)&su, &nr32, &nsel32, &inter, &hid, &x->dev, &list,
+                     &units, &n_units, &h };
+    if (!launch2(K_PF_GATEUP, (unsigned)umax, (unsigned)((I + 31) / 32), 256, 0, a_gu, op)) return 0;
+    void *a_dn[] = { (void *)&d, (void *)&sd, &nr32, &inter, &hid, &h, &list, &units, &n_units, &yp };
+    if (!launch2(K_PF_DOWN, (unsigned)umax, (unsigned)((H + 63) / 64), 256, 0, a_dn, op)) return 0;
+    void *a_cb[] = { &yp, &sel_w, &nsel32, &tt, &hid, &y->dev };
+    if (!launch2(K_PF_COMBINE, (unsigned)((H + 255) / 256), (unsigned)T, 256, 0, a_cb, op)) return 0;
+    if (route_out) {
+        hipError_t e = hipMemcpyAsync(route_out->dev, sel_idx, (size_t)T * tk * 4, hipMemcpyDeviceToDevice, g_stream);
+        if (e == hipSuccess)
+            e = hipMemcpyAsync(route_out->dev + (size_t)T * tk * 4, sel_w, (size_t)P * 4, hipMemcpyDeviceToDevice,
+                               g_stream);
+        if (e != hipSuccess) {
+            LOG("%s: route_out copy failed: %s", op, hipGetErrorString(e));
+            return 0;
+        }
+    }
     return 1;
 }
 

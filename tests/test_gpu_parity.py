@@ -588,6 +588,76 @@ def test_moe_decode_mq_geometries(dev, orc, mq_geometry):
         dev.free(b)
 
 
+def run_prefill(dev, desc, X):
+    import ctypes
+    T, H = X.shape
+    n_sel = desc.topk + desc.n_shared
+    xb = dev.shared_from(X)
+    yb = dev.alloc(X.nbytes)
+    rb = dev.alloc(T * (desc.topk + n_sel) * 4)
+    dev.run(dev.L.sepia_gpu_moe_prefill, ctypes.byref(desc), T, xb, yb, rb)
+    y = dev.download(yb, T * H).reshape(T, H)
+    idx = dev.download(rb, T * desc.topk, dtype=np.int32).reshape(T, desc.topk)
+    w = dev.download(rb, T * n_sel, offset=T * desc.topk * 4).reshape(T, n_sel)
+    for b in (xb, yb, rb):
+        dev.free(b)
+    return y, idx, w
+
+
+def bf16_normal(rng, shape):
+    """N(0,1) f32 values rounded toward zero to bf16 (exactly representable in bf16)."""
+    v = rng.standard_normal(shape).astype(np.float32)
+    return (v.view(np.uint32) & np.uint32(0xFFFF0000)).view(np.float32)
+
+
+# (hidden, inter, n_routed, n_shared), (gate/up, down, shared) formats, tokens
+PREFILL_CASES = [
+    ((2048, 1024, 16, 2), (10, 11, 12), 40),
+    ((6144, 3072, 16, 2), (10, 11, 12), 48),      # BASELINE configs[4] shapes, 16 experts resident
+    ((2048, 1024, 12, 1), (17, 18, 14), 33),      # IQ2_XS / IQ3_XXS routed, Q6_K shared
+    ((1024, 2048, 8, 2), (13, 23, 11), 20),       # Q5_K / IQ4_XS routed, Q3_K shared
+]
+
+
+@pytest.mark.parametrize("shape,types,T", PREFILL_CASES, ids=lambda v: str(v))
+def test_moe_prefill(dev, orc, shape, types, T):
+    """Every token of the batch against the oracle's single-token layer (its
+    own routing, near-ties per the reference protocol); two runs bitwise equal."""
+    hidden, inter, n_routed, n_shared = shape
+    tgu, td, ts = types
+    rng = np.random.default_rng(hidden + 7 * T + tgu)
+    desc, spec, bufs = make_layer(dev, rng, hidden=hidden, inter=inter, n_routed=n_routed, n_shared=n_shared,
+                                  tg=tgu, tu=tgu, td=td, ts=ts)
+    X = bf16_normal(rng, (T, hidden))
+    y, idx, w = run_prefill(dev, desc, X)
+    y2, _, _ = run_prefill(dev, desc, X)
+    assert np.array_equal(y.view(np.uint32), y2.view(np.uint32))
+    for t in range(T):
+        y_ref, logits, idx_ref, w_ref = orc.moe_layer(spec, X[t], threads=THREADS)
+        chosen = check_route(orc, spec, logits, idx[t], w[t])
+        if chosen != list(idx_ref):
+            y_ref, _, _, _ = orc.moe_layer(spec, X[t], force_idx=chosen, threads=THREADS)
+        assert_close(y[t], y_ref, what="prefill %s token %d" % (types, t), gate=False)
+    for b in bufs.values():
+        dev.free(b)
+
+
+def test_moe_prefill_matches_decode(dev, orc):
+    """A prefill batch and token-by-token decode of the same layer agree to the
+    layer bar (their routers sum the logits in different orders)."""
+    rng = np.random.default_rng(4242)
+    desc, spec, bufs = make_layer(dev, rng, hidden=2048, inter=1024, n_routed=16, n_shared=2,
+                                  tg=10, tu=10, td=11, ts=12)
+    X = bf16_normal(rng, (12, 2048))
+    y, idx, _ = run_prefill(dev, desc, X)
+    for t in range(12):
+        yd, idd, _ = run_moe(dev, desc, X[t].copy())
+        if list(idd) == list(idx[t]):
+            assert_close(y[t], yd, what="prefill vs decode token %d" % t, gate=False)
+    for b in bufs.values():
+        dev.free(b)
+
+
 def run_expert_ffn(dev, tensors, n_experts, expert, hidden, inter, x):
     import ctypes
     xb = dev.shared_from(x)
