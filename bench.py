@@ -18,7 +18,8 @@ cpu_baseline = the C oracle's scalar expert FFN (the reference's qlinear loop:
          per-row dequant + double accumulate) on one host core, on the same
          expert's bytes, over a bounded sample.
 extra  = the other BASELINE configurations (C1 Q4_K matvec, C3 full MoE
-         decode layer, C4 IQ matvecs) measured the same way.
+         decode layer, C4 IQ matvecs, C5 512-token prefill MoE layer)
+         measured the same way.
 """
 import argparse
 import ctypes
@@ -165,7 +166,12 @@ class Bench:
         raise RuntimeError("none of %s ran" % candidates)
 
     def kernel_ms(self, step, n, kernels):
-        """Average per-launch duration of each named kernel over n eager steps."""
+        """Average per-launch duration of each named kernel over n eager steps
+        (kernels that did not run are left out)."""
+        return {k: ms for k, (cnt, ms) in self.kernel_stats(step, n, kernels).items() if cnt}
+
+    def kernel_stats(self, step, n, kernels):
+        """(launches, average ms per launch) of each named kernel over n eager steps."""
         dev = self.dev
         self.L.sepia_hip_profile_reset()
         dev.begin()
@@ -178,7 +184,7 @@ class Bench:
         for k in kernels:
             cnt, tot = ctypes.c_int64(), ctypes.c_double()
             dev.check(self.L.sepia_hip_profile_query(k.encode(), ctypes.byref(cnt), ctypes.byref(tot)), "query")
-            out[k] = tot.value / max(cnt.value, 1)
+            out[k] = (cnt.value, tot.value / max(cnt.value, 1))
         return out
 
 
@@ -227,8 +233,8 @@ def run_c2(B, warmup, steps, cpu_seconds):
     e_last = (warmup + steps - 1) % NE
     y_graph = B.fetch(y, 0, H * 4).view(np.float32)
     step_bytes = gb + ub + db + H * 4 + I * 4 + H * 4
-    K_GU, K_DN = "sepia_mq_gateup", "sepia_mq_down"
-    kms = B.kernel_ms(step, min(steps, 4 * NE), [K_GU, K_DN])
+    K_FUSED, K_GU, K_DN = "sepia_mq_moe", "sepia_mq_gateup", "sepia_mq_down"
+    kms = B.kernel_ms(step, min(steps, 4 * NE), [K_FUSED, K_GU, K_DN])
     gu_bytes = gb + ub + H * 4 + I * 4
     dn_bytes = db + I * 4 + H * 4
     B.dev.run(L.sepia_gpu_expert_ffn, *ref, NE, e_last, H, I, xs[0], y)
@@ -253,15 +259,19 @@ def run_c2(B, warmup, steps, cpu_seconds):
                         cpu_seconds / 4, 1000)
     for b in bufs + xs + [y]:
         B.dev.free(b)
-    dom = K_GU
+    if K_FUSED in kms:      # the whole FFN in one launch: its bytes are the step's
+        roof = dict(bound="hbm", kernel=K_FUSED, achieved=step_bytes / (kms[K_FUSED] * 1e-3) / 1e9,
+                    peak=HBM_PEAK_GBS, unit="GB/s", bytes_per_launch=step_bytes,
+                    avg_launch_us=kms[K_FUSED] * 1e3)
+    else:
+        roof = dict(bound="hbm", kernel=K_GU, achieved=gu_bytes / (kms[K_GU] * 1e-3) / 1e9, peak=HBM_PEAK_GBS,
+                    unit="GB/s", bytes_per_launch=gu_bytes, avg_launch_us=kms[K_GU] * 1e3,
+                    other_kernels={K_DN: dict(bytes_per_launch=dn_bytes, avg_launch_us=kms[K_DN] * 1e3,
+                                              achieved=dn_bytes / (kms[K_DN] * 1e-3) / 1e9)})
     return dict(
         ms=ms, step_bytes=step_bytes, value=step_bytes / (ms * 1e-3) / 1e9,
         parity=dict(max_abs_diff=err, y_inf=scale, bound="1e-4*||y||_inf"),
-        roofline=dict(bound="hbm", kernel=dom, achieved=gu_bytes / (kms[dom] * 1e-3) / 1e9, peak=HBM_PEAK_GBS,
-                      unit="GB/s", bytes_per_launch=gu_bytes, avg_launch_us=kms[dom] * 1e3,
-                      other_kernels={K_DN: dict(bytes_per_launch=dn_bytes, avg_launch_us=kms[K_DN] * 1e3,
-                                                achieved=dn_bytes / (kms[K_DN] * 1e-3) / 1e9)}),
-        cpu=dict(s1=s1, n1=n1, sN=sN, nN=nN, threads=nthr))
+        roofline=roof, cpu=dict(s1=s1, n1=n1, sN=sN, nN=nN, threads=nthr))
 
 
 def run_matvec_rotation(B, name, t, rows, cols, warmup, steps, cpu_seconds, seed):
@@ -294,9 +304,10 @@ def run_matvec_rotation(B, name, t, rows, cols, warmup, steps, cpu_seconds, seed
                 cpu_1core_ms=s1 * 1e3, cpu_1core_gbs=mb / s1 / 1e9)
 
 
-def run_c3(B, warmup, steps, cpu_seconds, n_layers=3):
-    """BASELINE configs[2]: full MoE decode layer, 256 routed (Q2_K/Q3_K) + 2 shared (Q4_K)
-    experts resident, f32 router [258, 6144], top-6, no host round trip."""
+def build_moe_layers(B, n_layers):
+    """n_layers Inkling-shaped MoE layers resident in HBM: 256 routed experts (gate/up Q2_K
+    [3072x6144], down Q3_K [6144x3072]), 2 shared Q4_K, f32 router [258, 6144] ~ N(0, 0.02),
+    bias U(-0.1, 0.1). Returns (layers [(desc, buffers)], host routers [(rw, rb)], sizes)."""
     hip, L = B.hip, B.L
     H, I, NR, NS = 6144, 3072, 256, 2
     gb, db = mat_bytes(Q2_K, I, H), mat_bytes(Q3_K, H, I)
@@ -327,6 +338,32 @@ def run_c3(B, warmup, steps, cpu_seconds, n_layers=3):
         d.s_gate, d.s_up, d.s_down = hip.ExpertTensor(lb["s_gate"], 0, sgb, Q4_K), \
             hip.ExpertTensor(lb["s_up"], 0, sgb, Q4_K), hip.ExpertTensor(lb["s_down"], 0, sdb, Q4_K)
         layers.append((d, lb))
+    return layers, host_router, (H, I, NR, NS, gb, db, sgb, sdb)
+
+
+def layer_spec(B, lb, host_router, sizes, experts):
+    """Oracle spec of a layer with the bytes of the given routed experts and the shared ones."""
+    H, I, NR, NS, gb, db, sgb, sdb = sizes
+    rw, rb = host_router
+    spec = dict(hidden=H, inter=I, n_routed=NR, n_shared=NS, topk=6, route_scale=8.0, global_scale=1.0,
+                router_w=rw, router_bias=rb, t_gate=Q2_K, t_up=Q2_K, t_down=Q3_K, ts_gate=Q4_K, ts_up=Q4_K,
+                ts_down=Q4_K, gate=[None] * NR, up=[None] * NR, down=[None] * NR,
+                s_gate=[B.fetch(lb["s_gate"], s * sgb, sgb) for s in range(NS)],
+                s_up=[B.fetch(lb["s_up"], s * sgb, sgb) for s in range(NS)],
+                s_down=[B.fetch(lb["s_down"], s * sdb, sdb) for s in range(NS)])
+    for e in sorted(set(int(v) for v in experts)):
+        spec["gate"][e] = B.fetch(lb["gate"], e * gb, gb)
+        spec["up"][e] = B.fetch(lb["up"], e * gb, gb)
+        spec["down"][e] = B.fetch(lb["down"], e * db, db)
+    return spec
+
+
+def run_c3(B, warmup, steps, cpu_seconds, n_layers=3):
+    """BASELINE configs[2]: full MoE decode layer, 256 routed (Q2_K/Q3_K) + 2 shared (Q4_K)
+    experts resident, f32 router [258, 6144], top-6, no host round trip."""
+    L = B.L
+    layers, host_router, sizes = build_moe_layers(B, n_layers)
+    H, I, NR, NS, gb, db, sgb, sdb = sizes
     nx = 64
     xh, xs = B.vectors(H, nx, 41)
     y = B.private(H * 4)
@@ -337,7 +374,7 @@ def run_c3(B, warmup, steps, cpu_seconds, n_layers=3):
 
     ms = B.timed_steps(step, warmup, steps)
     per_token = (NR + NS) * H * 4 + 6 * (2 * gb + db) + NS * (2 * sgb + sdb)
-    kms = B.kernel_ms(step, min(steps, 60), ["sepia_moe_route", "sepia_mq_gateup", "sepia_mq_down"])
+    kms = B.kernel_ms(step, min(steps, 60), ["sepia_mq_moe", "sepia_moe_route", "sepia_mq_gateup", "sepia_mq_down"])
 
     # parity at full size: route + output of one token against the oracle
     import oracle
@@ -348,16 +385,7 @@ def run_c3(B, warmup, steps, cpu_seconds, n_layers=3):
     y_gpu = B.dev.download(yb, H)
     idx = B.dev.download(route, 6, dtype=np.int32)
     rw, rb = host_router[0]
-    spec = dict(hidden=H, inter=I, n_routed=NR, n_shared=NS, topk=6, route_scale=8.0, global_scale=1.0,
-                router_w=rw, router_bias=rb, t_gate=Q2_K, t_up=Q2_K, t_down=Q3_K, ts_gate=Q4_K, ts_up=Q4_K,
-                ts_down=Q4_K, gate=[None] * NR, up=[None] * NR, down=[None] * NR,
-                s_gate=[B.fetch(lb["s_gate"], s * sgb, sgb) for s in range(NS)],
-                s_up=[B.fetch(lb["s_up"], s * sgb, sgb) for s in range(NS)],
-                s_down=[B.fetch(lb["s_down"], s * sdb, sdb) for s in range(NS)])
-    for e in idx:
-        spec["gate"][e] = B.fetch(lb["gate"], int(e) * gb, gb)
-        spec["up"][e] = B.fetch(lb["up"], int(e) * gb, gb)
-        spec["down"][e] = B.fetch(lb["down"], int(e) * db, db)
+    spec = layer_spec(B, lb, host_router[0], sizes, idx)
     logits = oracle.linear_f32(rw, xh[0])
     idx_ref, _ = oracle.route_select(logits, rb, NR, NS, 6, 8.0, 1.0)
     nthr = min(16, os.cpu_count() or 1)
@@ -384,12 +412,72 @@ def run_c3(B, warmup, steps, cpu_seconds, n_layers=3):
                 cpu_1core_ms_per_token=s1 * 1e3)
 
 
+def run_c5(B, warmup, steps, cpu_seconds, T=512):
+    """the MoE layer for a batch of T tokens (prefill) with all 256 routed +
+    2 shared experts resident, x ~ N(0,1) rounded to bf16-representable f32."""
+    L = B.L
+    layers, host_router, sizes = build_moe_layers(B, 1)
+    H, I, NR, NS, gb, db, sgb, sdb = sizes
+    d, lb = layers[0]
+    rng = np.random.default_rng(55)
+    X = rng.standard_normal((T, H)).astype(np.float32)
+    X = (X.view(np.uint32) & np.uint32(0xFFFF0000)).view(np.float32)
+    sb = B.dev.shared_from(X)
+    xb = B.private(X.nbytes)
+    B.dev.run(L.sepia_gpu_copy, sb, 0, xb, 0, X.size)
+    B.dev.free(sb)
+    y = B.private(X.nbytes)
+
+    def step(i):
+        return L.sepia_gpu_moe_prefill(ctypes.byref(d), T, xb, y, None)
+
+    ms = B.timed_steps(step, warmup, steps)
+    knames = ["sepia_pf_route", "sepia_pf_select", "sepia_pf_group", "sepia_pf_gateup", "sepia_pf_down",
+              "sepia_pf_combine"]
+    kms = B.kernel_ms(step, min(steps, 5), knames)
+    n_sel = 6 + NS
+    route = B.dev.alloc(T * (6 + n_sel) * 4)
+    yb = B.dev.alloc(X.nbytes)
+    B.dev.run(L.sepia_gpu_moe_prefill, ctypes.byref(d), T, xb, yb, route)
+    idx = B.dev.download(route, T * 6, dtype=np.int32).reshape(T, 6)
+    touched = len(set(int(v) for v in idx.ravel()))
+    wbytes = touched * (2 * gb + db) + NS * (2 * sgb + sdb) + (NR + NS) * H * 4
+    act_bytes = 2 * T * H * 4
+    flops = 2.0 * T * (6 * 3 * I * H + NS * 3 * I * H + (NR + NS) * H)
+    # parity: a sample of tokens against the oracle's single-token layer
+    import oracle
+    sample = [0, 1, T // 2, T - 1]
+    spec = layer_spec(B, lb, host_router[0], sizes, idx[sample].ravel())
+    y_gpu = B.dev.download(yb, T * H).reshape(T, H)
+    nthr = min(16, os.cpu_count() or 1)
+    err, scale = 0.0, 0.0
+    for t in sample:
+        want, _, _, _ = oracle.moe_layer(spec, X[t], force_idx=idx[t], threads=nthr)
+        err = max(err, float(np.max(np.abs(y_gpu[t] - want))))
+        scale = max(scale, float(np.max(np.abs(want))))
+    if err > 1e-4 * scale:
+        raise RuntimeError("C5 parity: max|diff| %g > 1e-4 * %g" % (err, scale))
+    s1, n1 = cpu_sample(lambda: oracle.moe_layer(spec, X[0], force_idx=idx[0], threads=1), cpu_seconds, 20)
+    for b in list(lb.values()) + [xb, y, yb, route]:
+        B.dev.free(b)
+    sec = ms * 1e-3
+    return dict(ms_per_layer=ms, tokens=T, tokens_per_s=T / sec, experts_touched=touched,
+                weight_bytes=wbytes, hbm_gbs=(wbytes + act_bytes) / sec / 1e9,
+                hbm_frac=(wbytes + act_bytes) / sec / 1e9 / HBM_PEAK_GBS,
+                hbm_roofline_ms=(wbytes + act_bytes) / (HBM_PEAK_GBS * 1e9) * 1e3,
+                gflop=flops / 1e9, tflops=flops / sec / 1e12, mfma_util_bf16=flops / sec / 2.5e15,
+                mfma_util_issued=3 * flops / sec / 2.5e15,
+                kernels_avg_ms={k: v for k, v in kms.items()},
+                parity=dict(tokens=sample, max_abs_diff=err, y_inf=scale, bound="1e-4*||y||_inf"),
+                cpu_1core_ms_per_token=s1 * 1e3)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--only", choices=["c2", "c1", "c3", "c4"], default=None,
+    ap.add_argument("--only", choices=["c2", "c1", "c3", "c4", "c5"], default=None,
                     help="run one configuration (profiling runs); default: all")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     args = ap.parse_args()
@@ -422,6 +510,9 @@ def main():
     if args.only in (None, "c3"):
         extra["C3_moe_decode_layer"] = run_c3(B, args.warmup, min(args.steps, 200), min(5.0, args.cpu_seconds))
         log("C3", json.dumps(extra["C3_moe_decode_layer"]))
+    if args.only in (None, "c5"):
+        extra["C5_moe_prefill_512"] = run_c5(B, min(args.warmup, 2), min(args.steps, 10), min(3.0, args.cpu_seconds))
+        log("C5", json.dumps(extra["C5_moe_prefill_512"]))
     if res is None:
         print(json.dumps(extra, indent=1))
         return
@@ -448,7 +539,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(rf["achieved"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(rf["achieved"] / HBM_PEAK_GBS, 4), "traffic": None,
                      "kernel": rf["kernel"], "bytes_per_launch": rf["bytes_per_launch"],
-                     "avg_launch_us": round(rf["avg_launch_us"], 3), "other_kernels": rf["other_kernels"]},
+                     "avg_launch_us": round(rf["avg_launch_us"], 3), "other_kernels": rf.get("other_kernels", {})},
         "cpu_baseline": {"value": round(res["step_bytes"] / res["cpu"]["s1"] / 1e9, 4), "unit": "GB/s", "cores": 1,
                          "kind": "port",
                          "sample": "oracle expert FFN (per-row dequant + double accumulate, the reference's qlinear "

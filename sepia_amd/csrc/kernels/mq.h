@@ -460,20 +460,22 @@ struct MqWave {
     int nqw, Tn;               // quads per item and steps of this wave
     int ik, im, islot;         // issue cursor: item, quad, ring slot
 
+    // Waves first, first + 1, ... share the items (waves below `first` get
+    // none); each wave keeps its own ring.
     __device__ __forceinline__ MqWave(const ItemFn &f, int n_items_, int nq_, int n_, uint32_t rb_, MqGeo geo,
-                                      uint8_t *ring_lds)
+                                      uint8_t *ring_lds, int first = 0)
         : item_of(f), n_items(n_items_), nq(nq_), n(n_), rb(rb_) {
-        const int nw = (int)(blockDim.x >> 6), w = mq_wave_id();
+        const int w = mq_wave_id(), nw = (int)(blockDim.x >> 6) - first, wk = w - first;
         P = geo.P;
         S = geo.ring / (Wp * 1024);
         S = S < 4 ? S : 4;
         C = nw / P;
-        c = w / P;
-        p = w - c * P;
+        c = wk >= 0 ? wk / P : 0;
+        p = wk - c * P;
         ringp = ring_lds + (size_t)w * geo.ring;
         ring = mq_lds_addr(ringp);
         L = mq_lane();
-        const int ni = n_items > c ? (n_items - c + C - 1) / C : 0;
+        const int ni = (wk >= 0 && n_items > c) ? (n_items - c + C - 1) / C : 0;
         nqw = nq > p ? (nq - p + P - 1) / P : 0;
         Tn = ni * nqw;
         ik = im = islot = 0;

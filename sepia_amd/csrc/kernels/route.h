@@ -61,6 +61,9 @@ __device__ void route_pick(const float *logits, const float *__restrict__ bias, 
         if constexpr (ATOMIC) return __hip_atomic_load(&logits[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         else return logits[i];
     };
+    const int n_sel = topk + n_shared;
+    // the shared experts' sink logits load with the routed ones (one round trip)
+    const float sink = (lane >= topk && lane < n_sel) ? ld(n_routed + (lane - topk)) : 0.0f;
     float lv[EM], sc[EM];
     bool ok[EM];
 #pragma unroll
@@ -96,9 +99,8 @@ __device__ void route_pick(const float *logits, const float *__restrict__ bias, 
             my_raw = raw;
         }
     }
-    const int n_sel = topk + n_shared;
     const bool on = lane < n_sel;
-    const float raw = on ? ((lane < topk) ? my_raw : ld(n_routed + (lane - topk))) : 0.0f;
+    const float raw = on ? ((lane < topk) ? my_raw : sink) : 0.0f;
     const float lp = on ? logsigmoid_f32(raw) : -INFINITY;
     const float lmax = wave_max_dpp(lp);
     const double e = on ? exp((double)(lp - lmax)) : 0.0;

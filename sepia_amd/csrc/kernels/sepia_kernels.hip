@@ -222,6 +222,7 @@ SEPIA_FFN_PAIR(4, 3, ST_Q4_K, ST_Q3_K)
 SEPIA_FFN_PAIR(4, 4, ST_Q4_K, ST_Q4_K)
 
 #include "mq.h"
+#include "mq_fused.h"
 #include "moe.h"
 #include "prefill.h"
 #include "synth.h"
@@ -233,3 +234,4 @@ SEPIA_MQ_MV(q3_k, ST_Q3_K)
 SEPIA_MQ_MV(q4_k, ST_Q4_K)
 SEPIA_MQ_GATEUP()
 SEPIA_MQ_DOWN()
+SEPIA_MQ_FUSED()

@@ -55,8 +55,10 @@ enum {
     /* matrix-core expert FFN: gate/up, down */
     K_MQ_GU = K_MQ_MV + 3,
     K_MQ_DN = K_MQ_GU + 1,
+    /* the whole MoE layer / expert FFN in one launch (kernels/mq_fused.h) */
+    K_MQ_MOE = K_MQ_DN + 1,
     /* batched prefill MoE layer (kernels/prefill.h) */
-    K_PF_ROUTE = K_MQ_DN + 1, K_PF_SELECT, K_PF_GROUP, K_PF_GATEUP, K_PF_DOWN, K_PF_COMBINE,
+    K_PF_ROUTE = K_MQ_MOE + 1, K_PF_SELECT, K_PF_GROUP, K_PF_GATEUP, K_PF_DOWN, K_PF_COMBINE,
     K_COUNT
 };
 #define FFN_NAMES(p) "sepia_ffn_gateup_" p, "sepia_ffn_gateup_" p "_xp", "sepia_ffn_down_" p
@@ -76,7 +78,7 @@ static const char *const k_names[K_COUNT] = {
     "sepia_mv_q2_k", "sepia_mv_q3_k", "sepia_mv_q4_k",
     FFN_NAMES("22"), FFN_NAMES("23"), FFN_NAMES("24"), FFN_NAMES("32"), FFN_NAMES("33"), FFN_NAMES("34"),
     FFN_NAMES("42"), FFN_NAMES("43"), FFN_NAMES("44"),
-    "sepia_mq_mv_q2_k", "sepia_mq_mv_q3_k", "sepia_mq_mv_q4_k", "sepia_mq_gateup", "sepia_mq_down",
+    "sepia_mq_mv_q2_k", "sepia_mq_mv_q3_k", "sepia_mq_mv_q4_k", "sepia_mq_gateup", "sepia_mq_down", "sepia_mq_moe",
     "sepia_pf_route", "sepia_pf_select", "sepia_pf_group", "sepia_pf_gateup", "sepia_pf_down", "sepia_pf_combine",
 };
 #undef FFN_NAMES
@@ -125,6 +127,7 @@ static int g_opt_mq = 1;     /* sepia_hip_set_option("mq", 0) disables the matri
  * workgroup geometry (parts per item, item lanes, ring stages of the largest
  * format; 0 = planned) */
 static int g_opt_mq_p = 0, g_opt_mq_c = 0, g_opt_mq_s = 0;
+static int g_opt_fuse = 0;   /* sepia_hip_set_option("fuse", 1) runs the MoE layer / expert FFN as one launch */
 static int g_opt_tile_t = 0; /* sepia_hip_set_option("tile_t", T) forces T steps per workgroup */
 
 /* Geometry for `mats` stacked copies of a [rows, 256 * n_blocks] matrix; 0
@@ -151,6 +154,8 @@ static size_t tile_lds(int64_t n_staged, const TileGeo *g, int mats) {
 
 static int g_available;
 static size_t g_lds_max = 65536;    /* per-workgroup LDS limit, from the device at init */
+static int g_cus = 0;               /* compute units, from the device at init */
+static int g_fused_pending = 0;     /* a fused launch ran in the open batch: check its error flag at end */
 static int g_have_iq2xxs;
 static char g_device_name[256];
 static hipModule_t g_module;
@@ -243,6 +248,8 @@ static int prep_out(SepiaGpuBuf *b, const char *op) {
  * kernel that uses one leaves it at zero again) followed by a data region
  * for partial sums and intermediate vectors, grown on demand. */
 #define CNT_BYTES (64u * 1024u)
+#define MQ_BAR_WORD 1               /* fused launches' grid-barrier counter (never reset) */
+#define MQ_ERR_WORD 2               /* fused launches' barrier time-out flag */
 static void *g_scratch;
 static size_t g_scratch_len;
 
@@ -413,6 +420,7 @@ int sepia_gpu_init(const char *kernel_dir) {
         return 0;
     }
     g_lds_max = prop.sharedMemPerBlock ? prop.sharedMemPerBlock : 65536;
+    g_cus = prop.multiProcessorCount;
     char path[4096];
     if (!kernel_path(kernel_dir, path, sizeof path)) {
         LOG("init: kernel directory path too long");
@@ -505,6 +513,25 @@ int sepia_gpu_end(void) {
     if (e != hipSuccess) {
         LOG("end: batch failed: %s", hipGetErrorString(e));
         return 0;
+    }
+    if (g_fused_pending) {
+        /* a fused launch whose grid barrier timed out leaves its flag (word
+         * MQ_ERR_WORD of the counter region) set; its results are invalid */
+        g_fused_pending = 0;
+        uint32_t flag = 0;
+        e = hipMemcpy(&flag, (uint32_t *)g_scratch + MQ_ERR_WORD, 4, hipMemcpyDeviceToHost);
+        if (e == hipSuccess && flag) {
+            /* clear the flag and realign the barrier counter (a workgroup that
+             * gave up left it between multiples of the grid size) */
+            const uint32_t zero[2] = { 0, 0 };
+            hipMemcpy((uint32_t *)g_scratch + MQ_BAR_WORD, zero, 8, hipMemcpyHostToDevice);
+            LOG("end: a fused MoE launch timed out at a grid barrier; the batch's results are invalid");
+            return 0;
+        }
+        if (e != hipSuccess) {
+            LOG("end: reading the fused-launch flag failed: %s", hipGetErrorString(e));
+            return 0;
+        }
     }
     return 1;
 }
@@ -876,6 +903,10 @@ int sepia_hip_set_option(const char *name, int value) {
         g_opt_mq = value;
         return 1;
     }
+    if (strcmp(name, "fuse") == 0 && (value == 0 || value == 1)) {
+        g_opt_fuse = value;
+        return 1;
+    }
     if (strcmp(name, "mq_p") == 0 && value >= 0 && value <= 16) {
         g_opt_mq_p = value;
         return 1;
@@ -1205,14 +1236,27 @@ static int mq_proj_ok(const MoeProj *p, int64_t rows) {
     return mq_shape_ok(p->type, p->n_blocks, rows, (uintptr_t)p->base, p->row_bytes) && p->stride % 4 == 0;
 }
 /* Workgroups per slot for slots of byte weights br (routed) and bs (shared):
- * about MQ_CUS in all, at most `tiles` per slot. */
+ * at most MQ_CUS in all (unless one per slot is already more), at most
+ * `tiles` per slot, the bytes per workgroup as even as whole counts allow
+ * (proportional shares rounded down, then one more workgroup at a time to
+ * the kind with the most bytes per workgroup while it fits). */
 static void mq_split(int32_t topk, int32_t n_shared, double br, double bs, int64_t tiles, int32_t *wr, int32_t *ws) {
     const double tot = topk * br + n_shared * bs;
-    int64_t r = (int64_t)(MQ_CUS * br / tot + 0.5), sh = (int64_t)(MQ_CUS * bs / tot + 0.5);
+    int64_t r = (int64_t)(MQ_CUS * br / tot), sh = (int64_t)(MQ_CUS * bs / tot);
     if (r < 1) r = 1;
     if (sh < 1) sh = 1;
-    *wr = (int32_t)(r < tiles ? r : tiles);
-    *ws = (int32_t)(sh < tiles ? sh : tiles);
+    if (r > tiles) r = tiles;
+    if (sh > tiles) sh = tiles;
+    for (;;) {
+        const int64_t used = topk * r + n_shared * sh;
+        const int can_r = topk > 0 && r < tiles && used + topk <= MQ_CUS;
+        const int can_s = n_shared > 0 && sh < tiles && used + n_shared <= MQ_CUS;
+        if (can_r && (!can_s || br / (double)r >= bs / (double)sh)) r++;
+        else if (can_s) sh++;
+        else break;
+    }
+    *wr = (int32_t)r;
+    *ws = (int32_t)sh;
 }
 static int mq_ffn_plan(const MoeProj *g, const MoeProj *u, const MoeProj *d, const MoeProj *sg, const MoeProj *su,
                        const MoeProj *sd, int32_t topk, int32_t n_shared, int64_t H, int64_t I, MqFfnPlan *pl) {
@@ -1364,6 +1408,183 @@ int sepia_gpu_moe_prefill(const SepiaMoeLayerDesc *L, int64_t n_tokens, SepiaGpu
     return 1;
 }
 
+/* The fused MoE layer / expert FFN (kernels/mq_fused.h): exactly MQ_CUS
+ * workgroups, one per CU (the LDS it asks for admits no second), launched
+ * only when the device has that many CUs and the occupancy query confirms
+ * that every workgroup is resident at once -- its grid barriers rely on it.
+ * Gate/up runs on waves 1.. (wave 0 is the control wave), down on every
+ * wave; both phases share the workgroup size and the rings (ring bytes per
+ * wave: what the LDS leaves after the phases' tables). */
+typedef struct {
+    MqGeo gu, dn;
+    int32_t dn_wps_r, dn_wps_s;
+    uint32_t o_sel, o_gred, o_xqh, o_dred, o_flag, o_rings;
+} MqFuseGeo;
+typedef struct {
+    const float *rw;
+    int64_t ld;
+    const float *bias;
+    const float *x;
+    int32_t n_routed, n_shared, topk, fixed;
+    float route_scale, global_scale;
+    int64_t inter, hidden;
+    float *logits;
+    int32_t *sel_idx;
+    float *sel_w;
+    uint8_t *xq_h;
+    float *ypart;
+    uint32_t *cnt, *bar, *err;
+    float *y;
+} MqFuseIo;
+typedef struct {
+    MqFuseGeo geo;
+    unsigned threads;
+    size_t lds;
+} MqFusePlan;
+#define MQ_FSEL_BYTES 1024          /* the fused kernel's selection area: idx[64], w[64], flag */
+
+/* Gate/up units of workgroup b of G (mirror of mq_gu_range in
+ * kernels/mq_fused.h): the units whose first weight byte lies in
+ * [b T / G, (b + 1) T / G), us shared units of ws bytes first, then ur
+ * routed ones of wr bytes. */
+static int64_t cdiv_pos(int64_t a, int64_t d) { return a <= 0 ? 0 : (a + d - 1) / d; }
+static void mq_gu_range(int64_t us, int64_t ws, int64_t ur, int64_t wr, int64_t G, int64_t b, int64_t *ns,
+                        int64_t *nr) {
+    const int64_t S = us * ws, T = S + ur * wr;
+    const int64_t lo = T * b / G, hi = T * (b + 1) / G;
+    int64_t a0 = 0, a1 = 0;
+    if (us > 0) {
+        a0 = cdiv_pos(lo, ws);
+        a1 = cdiv_pos(hi, ws);
+        if (a0 > us) a0 = us;
+        if (a1 > us) a1 = us;
+    }
+    int64_t b0 = cdiv_pos(lo - S, wr), b1 = cdiv_pos(hi - S, wr);
+    if (b0 > ur) b0 = ur;
+    if (b1 > ur) b1 = ur;
+    *ns = a1 - a0;
+    *nr = b1 - b0;
+}
+
+/* Steps of one phase for the busiest wave: n_items items of nq quads on nw
+ * waves of P parts, 10 per step when the ring holds two or more steps. */
+static int64_t mq_phase_cost(int mc, int64_t n_items, int64_t nq, int P, int nw, size_t ring) {
+    const int C = nw / P;
+    const int64_t spw = ((n_items + C - 1) / C) * ((nq + P - 1) / P);
+    int64_t S = (int64_t)(ring / ((size_t)k_mq_words[mc] * 1024));
+    if (S > 4) S = 4;
+    if (S > spw) S = spw;
+    return spw * ((S >= 2 || spw == 1) ? 10 : 16);
+}
+
+static int mq_fuse_plan(const MoeProj *g, const MoeProj *u, const MoeProj *d, const MoeProj *sg, const MoeProj *su,
+                        const MoeProj *sd, int32_t topk, int32_t n_shared, int64_t H, int64_t I, MqFusePlan *fp) {
+    static int told = 0;   /* a device or layer the fused launch cannot take: said once */
+    MqFfnPlan pl;
+    if (!g_opt_fuse || topk < 1 || !mq_ffn_plan(g, u, d, sg, su, sd, topk, n_shared, H, I, &pl)) return 0;
+    if (g_cus < MQ_CUS) {
+        if (!told++) LOG("fused MoE launch off: %d compute units (it needs %d)", g_cus, MQ_CUS);
+        return 0;
+    }
+    if ((int64_t)topk * pl.dn_wps_r + (int64_t)n_shared * pl.dn_wps_s > MQ_CUS) return 0;
+    const int kg = mq_code(g->type), kd = mq_code(d->type);
+    int wg = k_mq_words[kg], wd = k_mq_words[kd];
+    if (n_shared > 0 && k_mq_words[mq_code(sg->type)] > wg) wg = k_mq_words[mq_code(sg->type)];
+    if (n_shared > 0 && k_mq_words[mq_code(sd->type)] > wd) wd = k_mq_words[mq_code(sd->type)];
+    const int wmax = wg > wd ? wg : wd;
+    const int64_t tiles_i = (I + 15) / 16, tiles_h = (H + 15) / 16;
+    /* the most gate/up units any workgroup gets */
+    int64_t nu_max = 0;
+    for (int64_t b = 0; b < MQ_CUS; b++) {
+        int64_t ns, nr;
+        mq_gu_range(n_shared * tiles_i, 32 * (int64_t)(n_shared > 0 ? sg->row_bytes : 0), topk * tiles_i,
+                    32 * (int64_t)g->row_bytes, MQ_CUS, b, &ns, &nr);
+        if (ns + nr > nu_max) nu_max = ns + nr;
+    }
+    if (nu_max < 1) nu_max = 1;
+    const int32_t dmin = (pl.dn_wps_r < pl.dn_wps_s || n_shared == 0) ? pl.dn_wps_r : pl.dn_wps_s;
+    const int64_t dnk = (tiles_h + dmin - 1) / dmin;
+    const int64_t nqg = H / 1024, nqd = I / 1024;
+    int64_t best = -1;
+    for (int nw = 3; nw <= 16; nw++)
+        for (int Pg = 1; Pg <= nw - 1 && Pg <= nqg; Pg++) {
+            if ((nw - 1) % Pg) continue;
+            for (int Pd = 1; Pd <= nw && Pd <= nqd; Pd++) {
+                if (nw % Pd) continue;
+                size_t o = MQ_ZERO + mq_xq_bytes(H);
+                const size_t o_sel = o;
+                o += MQ_FSEL_BYTES;
+                const size_t o_gred = o;
+                o += (size_t)2 * nu_max * Pg * 64;
+                const size_t o_xqh = align256(o);
+                o = o_xqh + mq_xq_bytes(I);
+                const size_t o_dred = o;
+                o += (size_t)dnk * Pd * 64;
+                const size_t o_flag = o;
+                o += (size_t)dnk * 4;
+                const size_t o_rings = align256(o);
+                if (o_rings + (size_t)nw * wmax * 1024 > g_lds_max) continue;
+                size_t ring = ((g_lds_max - o_rings) / (size_t)nw) & ~(size_t)1023;
+                if (ring > (size_t)4 * wmax * 1024) ring = (size_t)4 * wmax * 1024;
+                const int64_t cost = mq_phase_cost(kg, 2 * nu_max, nqg, Pg, nw - 1, ring) +
+                                     mq_phase_cost(kd, dnk, nqd, Pd, nw, ring);
+                if (best < 0 || cost < best) {
+                    best = cost;
+                    MqFuseGeo *G = &fp->geo;
+                    G->gu.P = Pg;
+                    G->dn.P = Pd;
+                    G->gu.ring = G->dn.ring = (int32_t)ring;
+                    G->dn_wps_r = pl.dn_wps_r;
+                    G->dn_wps_s = pl.dn_wps_s;
+                    G->o_sel = (uint32_t)o_sel;
+                    G->o_gred = (uint32_t)o_gred;
+                    G->o_xqh = (uint32_t)o_xqh;
+                    G->o_dred = (uint32_t)o_dred;
+                    G->o_flag = (uint32_t)o_flag;
+                    G->o_rings = (uint32_t)o_rings;
+                    fp->threads = 64u * (unsigned)nw;
+                    fp->lds = o_rings + (size_t)nw * ring;
+                }
+            }
+        }
+    if (best < 0) {
+        if (!told++) LOG("fused MoE launch off: no geometry fits %zu bytes of LDS", g_lds_max);
+        return 0;
+    }
+    /* every workgroup resident at once: at most one per CU by LDS, and the
+     * device has MQ_CUS of them */
+    int nb = 0;
+    const hipError_t e = hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&nb, g_fn[K_MQ_MOE], (int)fp->threads,
+                                                                             fp->lds);
+    if (e != hipSuccess || nb < 1 || (int64_t)nb * g_cus < MQ_CUS) {
+        if (!told++)
+            LOG("fused MoE launch off: occupancy query %s, %d workgroups of %u threads and %zu bytes LDS per CU",
+                hipGetErrorString(e), nb, fp->threads, fp->lds);
+        return 0;
+    }
+    return 1;
+}
+
+/* Scratch of a fused launch after `base`: XQ(h) [n_slots][XQ of I], then the
+ * down partial rows [n_slots][H] f32. */
+static size_t mq_fuse_scratch(int n_slots, int64_t H, int64_t I) {
+    return (((size_t)n_slots * mq_xq_bytes(I) + 255) & ~(size_t)255) + (size_t)n_slots * (size_t)H * 4;
+}
+
+static int mq_fuse_launch(const char *op, const MoeProj *g, const MoeProj *u, const MoeProj *d, const MoeProj *sg,
+                          const MoeProj *su, const MoeProj *sd, MqFuseIo *io, uint8_t *scr, const MqFusePlan *fp) {
+    io->xq_h = scr;
+    io->ypart = (float *)(scr + (((size_t)(io->topk + io->n_shared) * mq_xq_bytes(io->inter) + 255) & ~(size_t)255));
+    io->cnt = (uint32_t *)g_scratch + MQ_DN_CNT_OFF;
+    io->bar = (uint32_t *)g_scratch + MQ_BAR_WORD;
+    io->err = (uint32_t *)g_scratch + MQ_ERR_WORD;
+    MqFuseGeo geo = fp->geo;
+    void *args[] = { (void *)g, (void *)u, (void *)d, (void *)sg, (void *)su, (void *)sd, io, &geo };
+    if (!launch_lds(K_MQ_MOE, MQ_CUS, fp->threads, fp->lds, args, op)) return 0;
+    g_fused_pending = 1;
+    return 1;
+}
+
 /* The SwiGLU expert FFN over n_slots = topk + n_shared slots: routed slot s
  * uses expert sel_idx[s] (or fixed + s when sel_idx is NULL), then come the
  * shared experts. One slot without weights stores y; several slots add
@@ -1471,7 +1692,8 @@ int sepia_gpu_moe_decode(const SepiaMoeLayerDesc *L, SepiaGpuBuf *x, SepiaGpuBuf
     const size_t o_idx = o_logits + (((size_t)n_tot * 4 + 255) & ~(size_t)255);
     const size_t o_w = o_idx + 256;
     const size_t o_h = o_w + 256;
-    uint8_t *s = (uint8_t *)scratch(o_h + ffn_scratch_bytes(n_slots, I, H), op);
+    const size_t need_f = mq_fuse_scratch(n_slots, H, I), need_s = ffn_scratch_bytes(n_slots, I, H);
+    uint8_t *s = (uint8_t *)scratch(o_h + (need_f > need_s ? need_f : need_s), op);
     if (!s) return 0;
     float *logits = (float *)(s + o_logits), *sel_w = (float *)(s + o_w);
     int32_t *sel_idx = (int32_t *)(s + o_idx);
@@ -1488,6 +1710,27 @@ int sepia_gpu_moe_decode(const SepiaMoeLayerDesc *L, SepiaGpuBuf *x, SepiaGpuBuf
     int64_t ld = H, hid = H;
     int32_t nr = L->n_routed, ns = L->n_shared, tk = L->topk;
     float rs = L->route_scale, gsc = L->global_scale;
+    MqFusePlan fp;
+    if (mq_fuse_plan(&g, &u, &d, &sg, &su, &sd, tk, ns, H, I, &fp)) {
+        MqFuseIo io;
+        memset(&io, 0, sizeof io);
+        io.rw = rw;
+        io.ld = ld;
+        io.bias = rb;
+        io.x = (const float *)x->dev;
+        io.n_routed = nr;
+        io.n_shared = ns;
+        io.topk = tk;
+        io.route_scale = rs;
+        io.global_scale = gsc;
+        io.inter = I;
+        io.hidden = H;
+        io.logits = logits;
+        io.sel_idx = sel_idx;
+        io.sel_w = sel_w;
+        io.y = (float *)y->dev;
+        if (!mq_fuse_launch(op, &g, &u, &d, &sg, &su, &sd, &io, s + o_h, &fp)) return 0;
+    } else {
     /* with the matrix-core FFN the gate/up launch selects from the logits;
      * otherwise the router's last workgroup does */
     MqFfnPlan pl;
@@ -1501,6 +1744,7 @@ int sepia_gpu_moe_decode(const SepiaMoeLayerDesc *L, SepiaGpuBuf *x, SepiaGpuBuf
     if (!ffn_launch(op, &g, &u, &d, &sg, &su, &sd, sel_idx, sel_w, 0, tk, ns, H, I, x->dev, (float *)y->dev, s + o_h,
                     in_kernel ? &rt : NULL))
         return 0;
+    }
 
     if (route_out) {
         hipError_t e = hipMemcpyAsync(route_out->dev, sel_idx, (size_t)L->topk * 4, hipMemcpyDeviceToDevice, g_stream);
@@ -1530,11 +1774,24 @@ int sepia_gpu_expert_ffn(const SepiaExpertTensor *gate, const SepiaExpertTensor 
         return 0;
     if (!chk(x, 0, (size_t)hidden * 4, op, "x") || !chk(y, 0, (size_t)hidden * 4, op, "y")) return 0;
     if (!need_batch(op)) return 0;
-    uint8_t *scr = (uint8_t *)scratch(ffn_scratch_bytes(1, inter, hidden), op);
+    const size_t need_f = mq_fuse_scratch(1, hidden, inter), need_s = ffn_scratch_bytes(1, inter, hidden);
+    uint8_t *scr = (uint8_t *)scratch(need_f > need_s ? need_f : need_s, op);
     if (!scr) return 0;
     if (!prep_in(gate->buf, op) || !prep_in(up->buf, op) || !prep_in(down->buf, op) || !prep_in(x, op) ||
         !prep_out(y, op))
         return 0;
+    MqFusePlan fp;
+    if (mq_fuse_plan(&g, &u, &d, &none, &none, &none, 1, 0, hidden, inter, &fp)) {
+        MqFuseIo io;
+        memset(&io, 0, sizeof io);
+        io.x = (const float *)x->dev;
+        io.topk = 1;
+        io.fixed = expert;
+        io.inter = inter;
+        io.hidden = hidden;
+        io.y = (float *)y->dev;
+        return mq_fuse_launch(op, &g, &u, &d, &none, &none, &none, &io, scr, &fp);
+    }
     return ffn_launch(op, &g, &u, &d, &none, &none, &none, NULL, NULL, expert, 1, 0, hidden, inter, x->dev,
                       (float *)y->dev, scr, NULL);
 }

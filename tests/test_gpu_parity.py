@@ -210,17 +210,21 @@ def test_matvec_q_config_shapes(dev, orc, name, t, out_dim, in_dim):
 @pytest.fixture
 def kernel_path(dev, request):
     """Force one kernel family: the matrix-core kernels (the default), the
-    generic per-row kernel, or the tile kernels with 1, 2 or 3 row steps per
+    matrix-core MoE layer / expert FFN as one launch ("fused"), the generic
+    per-row kernel, or the tile kernels with 1, 2 or 3 row steps per
     workgroup."""
     L = dev.L
     mode = request.param
-    if mode != "mq":
+    if mode == "fused":
+        assert L.sepia_hip_set_option(b"fuse", 1) == 1
+    elif mode != "mq":
         assert L.sepia_hip_set_option(b"mq", 0) == 1
     if mode == "generic":
         assert L.sepia_hip_set_option(b"tile", 0) == 1
-    elif mode != "mq":
+    elif mode not in ("mq", "fused"):
         assert L.sepia_hip_set_option(b"tile_t", {"t1": 1, "t2": 2, "t3": 3}[mode]) == 1
     yield mode
+    L.sepia_hip_set_option(b"fuse", 0)
     L.sepia_hip_set_option(b"mq", 1)
     L.sepia_hip_set_option(b"tile", 1)
     L.sepia_hip_set_option(b"tile_t", 0)
@@ -279,6 +283,7 @@ def mq_geometry(dev, request):
     L = dev.L
     for k, v in zip(("mq_p", "mq_c", "mq_s"), request.param):
         assert L.sepia_hip_set_option(k.encode(), v) == 1
+    assert L.sepia_hip_set_option(b"fuse", 0) == 1      # the separate gate/up and down launches
     yield request.param
     for k in ("mq_p", "mq_c", "mq_s"):
         L.sepia_hip_set_option(k.encode(), 0)
@@ -527,7 +532,7 @@ def test_moe_decode_small(dev, orc, types, seed):
         dev.free(b)
 
 
-@pytest.mark.parametrize("kernel_path", ["mq", "generic", "t1", "t3"], indirect=True)
+@pytest.mark.parametrize("kernel_path", ["mq", "fused", "generic", "t1", "t3"], indirect=True)
 @pytest.mark.parametrize("types", [(10, 10, 11, 12), (12, 12, 12, 10), (11, 11, 10, 11)],
                          ids=["q2k_q3k_q4k", "q4k_q4k_q2k", "q3k_q2k_q3k"])
 def test_moe_decode_tile_shapes(dev, orc, kernel_path, types):
@@ -584,6 +589,35 @@ def test_moe_decode_mq_geometries(dev, orc, mq_geometry):
     if chosen != list(idx_ref):
         y_ref, _, _, _ = orc.moe_layer(spec, x, force_idx=chosen, threads=THREADS)
     assert_close(y, y_ref, what="moe mq %s" % (mq_geometry,), gate=False)
+    for b in bufs.values():
+        dev.free(b)
+
+
+@pytest.mark.parametrize("fuse", [1, 0], ids=["fused", "three_launches"])
+@pytest.mark.parametrize("types", [(10, 10, 11, 12), (12, 12, 12, 10), (11, 11, 10, 11)],
+                         ids=["q2k_q3k_q4k", "q4k_q4k_q2k", "q3k_q2k_q3k"])
+def test_moe_decode_fused(dev, orc, fuse, types):
+    """The one-launch layer (grid barriers) and the three-launch layer give the
+    oracle's result; the launch counts show which ran."""
+    rng = np.random.default_rng(9000 + 10 * fuse + types[0])
+    tg, tu, td, ts = types
+    desc, spec, bufs = make_layer(dev, rng, hidden=6144, inter=3072, n_routed=16, n_shared=2,
+                                  tg=tg, tu=tu, td=td, ts=ts)
+    assert dev.L.sepia_hip_set_option(b"fuse", fuse) == 1
+    try:
+        for rep in range(2):
+            x = synth.normal_vector(rng, 6144)
+            with Launches(dev) as n:
+                y, idx, w = run_moe(dev, desc, x)
+                assert n.count("sepia_mq_moe") == fuse
+                assert n.count("sepia_mq_gateup") == 1 - fuse
+            y_ref, logits, idx_ref, w_ref = orc.moe_layer(spec, x, threads=THREADS)
+            chosen = check_route(orc, spec, logits, idx, w)
+            if chosen != list(idx_ref):
+                y_ref, _, _, _ = orc.moe_layer(spec, x, force_idx=chosen, threads=THREADS)
+            assert_close(y, y_ref, what="moe fuse=%d rep %d" % (fuse, rep), gate=False)
+    finally:
+        dev.L.sepia_hip_set_option(b"fuse", 0)
     for b in bufs.values():
         dev.free(b)
 
@@ -670,7 +704,7 @@ def run_expert_ffn(dev, tensors, n_experts, expert, hidden, inter, x):
     return y
 
 
-@pytest.mark.parametrize("kernel_path", ["mq", "generic", "t1", "t2", "t3"], indirect=True)
+@pytest.mark.parametrize("kernel_path", ["mq", "fused", "generic", "t1", "t2", "t3"], indirect=True)
 @pytest.mark.parametrize("types,hidden,inter", [((10, 10, 11), 6144, 3072), ((12, 12, 12), 4096, 2048),
                                                 ((11, 11, 10), 2048, 1024)],
                          ids=["c2_q2k_q3k", "q4k_4096", "q3k_q2k_2048"])
