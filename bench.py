@@ -188,6 +188,12 @@ class Bench:
         return out
 
 
+# HBM bytes per launch of the C2 kernels, measured with rocprofv3's FETCH_SIZE and WRITE_SIZE
+# counters and scaled by what the same counters read for the copy kernel of known size
+# (profiles/expert_ffn_c2_hbm_traffic.md). Reported as roofline.traffic for the dominant kernel.
+MEASURED_TRAFFIC = {"sepia_mq_gateup": 12792754, "sepia_mq_down": 8419297}
+
+
 def cpu_sample(fn, min_seconds, max_calls):
     """Run fn until min_seconds have passed (at least once, at most max_calls); mean s/call."""
     n, t0 = 0, time.perf_counter()
@@ -302,6 +308,23 @@ def run_matvec_rotation(B, name, t, rows, cols, warmup, steps, cpu_seconds, seed
                 hbm_frac=nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, copies_rotated=ncopy,
                 kernel=kname, kernel_avg_us=kms * 1e3, kernel_gbs=nbytes / (kms * 1e-3) / 1e9,
                 cpu_1core_ms=s1 * 1e3, cpu_1core_gbs=mb / s1 / 1e9)
+
+
+def run_copy(B, steps):
+    """sepia_copy_f32 over 256 MiB (read 256 MiB, write 256 MiB) per launch: the known-size
+    kernel against which rocprofv3's FETCH_SIZE and WRITE_SIZE counters are scaled."""
+    L = B.L
+    n = 64 * 2 ** 20
+    src, dst = B.private(4 * n), B.private(4 * n)
+
+    def step(i):
+        return L.sepia_gpu_copy(src, 0, dst, 0, n)
+
+    kms = B.kernel_ms(step, min(steps, 10), ["sepia_copy_f32"])
+    B.dev.free(src)
+    B.dev.free(dst)
+    return dict(bytes_read=4 * n, bytes_written=4 * n, launches=min(steps, 10),
+                avg_launch_us=kms["sepia_copy_f32"] * 1e3, gbs=8 * n / (kms["sepia_copy_f32"] * 1e-3) / 1e9)
 
 
 def build_moe_layers(B, n_layers):
@@ -477,8 +500,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--only", choices=["c2", "c1", "c3", "c4", "c5"], default=None,
-                    help="run one configuration (profiling runs); default: all")
+    ap.add_argument("--only", choices=["c2", "c1", "c3", "c4", "c5", "copy"], default=None,
+                    help="run one configuration (profiling runs; 'copy': the library's f32 copy kernel over "
+                         "256 MiB, the reference for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE); default: all")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -513,6 +537,9 @@ def main():
     if args.only in (None, "c5"):
         extra["C5_moe_prefill_512"] = run_c5(B, min(args.warmup, 2), min(args.steps, 10), min(3.0, args.cpu_seconds))
         log("C5", json.dumps(extra["C5_moe_prefill_512"]))
+    if args.only == "copy":
+        extra["copy_f32_256MiB"] = run_copy(B, args.steps)
+        log("copy", json.dumps(extra["copy_f32_256MiB"]))
     if res is None:
         print(json.dumps(extra, indent=1))
         return
@@ -537,7 +564,7 @@ def main():
                                "resident in HBM, rotated per step",
                    "bytes_per_step": res["step_bytes"], "hbm_frac": round(value / HBM_PEAK_GBS, 4)},
         "roofline": {"bound": "hbm", "achieved": round(rf["achieved"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(rf["achieved"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(rf["achieved"] / HBM_PEAK_GBS, 4), "traffic": MEASURED_TRAFFIC.get(rf["kernel"]),
                      "kernel": rf["kernel"], "bytes_per_launch": rf["bytes_per_launch"],
                      "avg_launch_us": round(rf["avg_launch_us"], 3), "other_kernels": rf.get("other_kernels", {})},
         "cpu_baseline": {"value": round(res["step_bytes"] / res["cpu"]["s1"] / 1e9, 4), "unit": "GB/s", "cores": 1,
