@@ -70,7 +70,8 @@ int sepia_gpu_moe_prefill(const SepiaMoeLayerDesc *layer, int64_t n_tokens, Sepi
 
 /* One routed expert: y = down(silu(gate x) * up x) for expert `expert` of
  * stacks holding n_experts experts (reference src/sepia.c:2993-3017,
- * real_expert_ffn), as two launches (fused gate/up/SwiGLU, then down).
+ * real_expert_ffn), as two launches (fused gate/up/SwiGLU, then down), or
+ * one with the "fuse" option.
  * x, y: f32 [hidden] at offset 0. */
 int sepia_gpu_expert_ffn(const SepiaExpertTensor *gate, const SepiaExpertTensor *up, const SepiaExpertTensor *down,
                          int n_experts, int expert, int64_t hidden, int64_t inter, SepiaGpuBuf *x, SepiaGpuBuf *y);
@@ -99,9 +100,16 @@ int sepia_hip_set_iq2xxs_grid(const uint64_t *grid256);
 /* The hipStream_t every op is issued on (for hipEvent timing). */
 void *sepia_hip_stream(void);
 
-/* Kernel-selection switches for tests and tuning: "tile" 1/0 enables or
- * disables the split-K tile kernels (disabled = the generic one-wave-per-row
- * kernels); "tile_j" 0/2/4 = automatic or forced rows per thread. */
+/* Kernel-selection switches for tests and tuning (returns 1 if name and
+ * value are known):
+ *   "mq" 1/0      the matrix-core kernels for Q2_K/Q3_K/Q4_K (default 1);
+ *   "fuse" 0/1    the MoE layer and the expert FFN as one launch of
+ *                 sepia_mq_moe instead of router + gate/up + down (default 0);
+ *   "tile" 1/0    the tile kernels where the matrix-core ones do not apply
+ *                 (0 = the generic one-wave-per-row kernels);
+ *   "tile_t" 0..  automatic or forced row steps per tile workgroup;
+ *   "mq_p", "mq_c", "mq_s" 0..  automatic or forced matrix-core geometry
+ *                 (parts per item, items side by side, ring stages). */
 int sepia_hip_set_option(const char *name, int value);
 
 #ifdef __cplusplus
