@@ -504,6 +504,8 @@ def main():
                     help="run one configuration (profiling runs; 'copy': the library's f32 copy kernel over "
                          "256 MiB, the reference for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE); default: all")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--fuse", type=int, choices=[0, 1], default=None,
+                    help="library option 'fuse': the MoE layer / expert FFN as one launch (default: library default)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -515,6 +517,8 @@ def main():
     dev = hip.Device()
     B = Bench(dev)
     log("device", dev.name)
+    if args.fuse is not None and dev.L.sepia_hip_set_option(b"fuse", args.fuse) != 1:
+        raise RuntimeError("option fuse not accepted")
     extra = {}
     res = None
     t0 = time.time()

@@ -129,6 +129,30 @@ __device__ __forceinline__ void xq_store(const XqSeg &r, uint8_t *xq, int64_t n,
 // n columns (vector k at src + k * ld floats) to LDS offsets xoff + k * xqb.
 // Each thread converts whole 16-column segments. Also clears the zero area
 // at lds0; ends with a barrier.
+// The n-float vector src (n a multiple of 256, src 4-byte aligned) into LDS
+// at raw by LDS DMA, 1 KB per wave instruction, chunk c by wave c % waves.
+// The caller waits for it (these DMAs are older than anything it issues
+// next) before mq_stage_xq_lds.
+__device__ __forceinline__ void mq_dma16(const uint8_t *base, uint32_t voff, uint32_t lds);
+__device__ __forceinline__ void mq_dma_vec(const float *src, int n, uint32_t raw) {
+    const int nw = (int)(blockDim.x >> 6), w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const uint32_t lane = threadIdx.x & 63;
+    for (int c = w; c < (n >> 8); c += nw) mq_dma16((const uint8_t *)src, (uint32_t)c * 1024u + 16u * lane, raw + (uint32_t)c * 1024u);
+}
+// XQ of an n-float vector already in LDS (raw, 16-byte aligned).
+__device__ __forceinline__ void mq_stage_xq_lds(const float *raw, int n, uint8_t *lds0, uint32_t xoff) {
+    const int segs = n >> 4;
+    for (int seg = threadIdx.x; seg < segs; seg += blockDim.x) {
+        const float4 *x4 = (const float4 *)raw + 4 * seg;
+        const float4 v0 = x4[0], v1 = x4[1], v2 = x4[2], v3 = x4[3];
+        const float a[16] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w,
+                             v2.x, v2.y, v2.z, v2.w, v3.x, v3.y, v3.z, v3.w};
+        xq_store(xq_segment(a), lds0 + xoff, n, seg);
+    }
+    if (threadIdx.x < MQ_ZERO / 16) ((uint4 *)(lds0))[threadIdx.x] = make_uint4(0, 0, 0, 0);
+    __syncthreads();
+}
+
 __device__ __forceinline__ void mq_stage_xq(const float *__restrict__ src, int64_t ld, int count, int n,
                                             uint8_t *lds0, uint32_t xoff, uint32_t xqb) {
     const int segs = n >> 4, total = segs * count;
@@ -155,8 +179,13 @@ __device__ __forceinline__ uint32_t mq_lds_addr(const void *p) {
 // own vmcnt waits stay correct because vector memory operations retire in
 // issue order.
 // M0 holds the LDS address: the "{m0}" operand lets the compiler write it.
+// The base is uniform by construction; readfirstlane states it, so that the
+// "s" operand never depends on the compiler's uniformity analysis.
 __device__ __forceinline__ void mq_dma16(const uint8_t *base, uint32_t voff, uint32_t lds) {
-    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"(base), "{m0}"(lds) : "memory");
+    const uint64_t b = (uint64_t)(uintptr_t)base;
+    const uint64_t bs = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(b >> 32)) << 32) |
+                        (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)b);
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"((const uint8_t *)(uintptr_t)bs), "{m0}"(lds) : "memory");
 }
 // s_waitcnt immediates (gfx9 encoding): vmcnt(n) alone, and lgkmcnt(0) alone.
 __device__ __forceinline__ constexpr int mq_wc_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
@@ -168,7 +197,8 @@ __device__ __forceinline__ void mq_wait_stages(int n) {
     if (n <= 0) __builtin_amdgcn_s_waitcnt(mq_wc_vm(0));
     else if (n == 1) __builtin_amdgcn_s_waitcnt(mq_wc_vm(W));
     else if (n == 2) __builtin_amdgcn_s_waitcnt(mq_wc_vm(2 * W));
-    else __builtin_amdgcn_s_waitcnt(mq_wc_vm(3 * W));
+    else if (n == 3) __builtin_amdgcn_s_waitcnt(mq_wc_vm(3 * W));
+    else __builtin_amdgcn_s_waitcnt(mq_wc_vm(4 * W));
 }
 
 // ------------------------------------------------------- weight blocks ----
@@ -439,8 +469,11 @@ struct MqItem {
 // of the row's nq = nb / 4 quads. Every wave has a private ring of `ring`
 // bytes at LDS offset rings + w * ring, which holds S = min(4, ring / Wp KB)
 // stages of a format of Wp padded words.
+// xraw: LDS offset of a raw f32 copy of the workgroup's vector (0: the
+// vector is read from global memory directly), orings: LDS offset of the
+// rings (for the kernels whose LDS layout the host plans).
 struct MqGeo {
-    int32_t P, ring;
+    int32_t P, ring, xraw, orings;
 };
 
 // The pipeline of one wave over n_items items of format T, in two halves:
@@ -460,8 +493,9 @@ struct MqWave {
     int nqw, Tn;               // quads per item and steps of this wave
     int ik, im, islot;         // issue cursor: item, quad, ring slot
 
-    // Waves first, first + 1, ... share the items (waves below `first` get
-    // none); each wave keeps its own ring.
+    // Waves first, first + 1, ... share the items as C = (waves - first) / P
+    // columns of P parts; waves below `first` and past the last full column
+    // get none. Each wave keeps its own ring.
     __device__ __forceinline__ MqWave(const ItemFn &f, int n_items_, int nq_, int n_, uint32_t rb_, MqGeo geo,
                                       uint8_t *ring_lds, int first = 0)
         : item_of(f), n_items(n_items_), nq(nq_), n(n_), rb(rb_) {
@@ -475,7 +509,7 @@ struct MqWave {
         ringp = ring_lds + (size_t)w * geo.ring;
         ring = mq_lds_addr(ringp);
         L = mq_lane();
-        const int ni = (wk >= 0 && n_items > c) ? (n_items - c + C - 1) / C : 0;
+        const int ni = (wk >= 0 && wk < C * P && n_items > c) ? (n_items - c + C - 1) / C : 0;
         nqw = nq > p ? (nq - p + P - 1) / P : 0;
         Tn = ni * nqw;
         ik = im = islot = 0;
@@ -505,6 +539,27 @@ struct MqWave {
     }
     __device__ __forceinline__ void prologue() {
         for (int t = 0; t < S && t < Tn; t++) issue();
+    }
+    // Wait for this wave's memory operations older than its prologue.
+    __device__ __forceinline__ void wait_before_prologue() const { mq_wait_stages<Wp>(S < Tn ? S : Tn); }
+    // The workgroup's vector: from global memory, or (geo.xraw) by LDS DMA
+    // ahead of the prologue and converted once it has landed, so that the
+    // vector does not queue behind the workgroup's weight stream.
+    __device__ __forceinline__ void start(const float *src, const MqGeo &geo, uint8_t *lds0, uint32_t xoff) {
+        if (geo.xraw) {
+            mq_dma_vec(src, n, mq_lds_addr(lds0 + geo.xraw));
+            // every wave's vector DMAs are issued before any weight DMA, so
+            // the CU's queue holds the whole vector ahead of the weights
+            // (a bare s_barrier: nothing waits for the loads here)
+            __builtin_amdgcn_s_barrier();
+            prologue();
+            wait_before_prologue();
+            __syncthreads();
+            mq_stage_xq_lds((const float *)(lds0 + geo.xraw), n, lds0, xoff);
+        } else {
+            prologue();
+            mq_stage_xq(src, 0, 1, n, lds0, xoff, 0u);
+        }
     }
     __device__ __forceinline__ void run(const uint8_t *lds0, float *red) {
         int ck = 0, cm = 0, cslot = 0;
@@ -549,7 +604,7 @@ __device__ __forceinline__ float mq_red_sum(const float *red, int i, int P, int 
 // ------------------------------------------------------------ matvec ------
 // y = W x for one matrix of nb blocks per row (nb % 4 == 0). Workgroup k
 // owns row groups rg = k, k + G, ... (G = gridDim.x), one item each.
-// LDS: [zero][XQ of x][red: nk x P x 16 f32][rings].
+// LDS: [zero][XQ of x][red: nk x P x 16 f32][raw x, if geo.xraw][rings at geo.orings].
 template <int T>
 __device__ __forceinline__ void mq_mv(const uint8_t *__restrict__ W, uint64_t row_bytes, int64_t rows, int32_t nb,
                                       const float *__restrict__ x, float *__restrict__ y, MqGeo geo) {
@@ -559,7 +614,7 @@ __device__ __forceinline__ void mq_mv(const uint8_t *__restrict__ W, uint64_t ro
     const int nk = tiles > blockIdx.x ? (int)((tiles - blockIdx.x + G - 1) / G) : 0;
     const uint32_t xoff = MQ_ZERO;
     float *red = (float *)(smem + xoff + mq_xq_bytes(n));
-    uint8_t *rings = smem + ((xoff + mq_xq_bytes(n) + (size_t)nk * geo.P * 64 + 255) & ~(size_t)255);
+    uint8_t *rings = smem + geo.orings;
     auto item_of = [&](int i) {
         MqItem it;
         it.base = W;
@@ -570,8 +625,7 @@ __device__ __forceinline__ void mq_mv(const uint8_t *__restrict__ W, uint64_t ro
         return it;
     };
     MqWave<T, decltype(item_of)> wv(item_of, nk, nb >> 2, n, (uint32_t)row_bytes, geo, rings);
-    wv.prologue();
-    mq_stage_xq(x, 0, 1, n, smem, xoff, 0u);
+    wv.start(x, geo, smem, xoff);
     wv.run(smem, red);
     __syncthreads();
     for (int i = threadIdx.x; i < nk * 16; i += blockDim.x) {
@@ -606,7 +660,7 @@ __device__ __forceinline__ int64_t mq_slot_expert(const int32_t *sel_idx, int32_
 // Gate/up of one slot: the workgroup owns row groups j0, j0 + jstep, ... of
 // the slot's inter rows; item 2k is the gate rows of its k-th row group,
 // item 2k + 1 the up rows. h[r] = silu(gate_r . x) * (up_r . x) (f32).
-// LDS: [zero][XQ of x][selection: 64 i32 + 64 f32][red: 2 nk x P x 16 f32]
+// LDS: [zero][XQ of x][selection: 64 i32 + 64 f32][red: 2 nk x P x 16 f32][raw x]
 //      [rings].
 #define MQ_SEL_BYTES 512
 template <int T>
@@ -619,8 +673,7 @@ __device__ __forceinline__ void mq_gateup_slot(const uint8_t *Wg, const uint8_t 
     const int nk = j0 < tiles ? (tiles - j0 + jstep - 1) / jstep : 0;
     const uint32_t xoff = MQ_ZERO;
     float *red = (float *)(smem + xoff + mq_xq_bytes(n) + MQ_SEL_BYTES);
-    uint8_t *rings =
-        smem + ((xoff + mq_xq_bytes(n) + MQ_SEL_BYTES + (size_t)2 * nk * geo.P * 64 + 255) & ~(size_t)255);
+    uint8_t *rings = smem + geo.orings;
     auto item_of = [&](int i) {
         MqItem it;
         it.base = (i & 1) ? Wu : Wg;
@@ -631,8 +684,7 @@ __device__ __forceinline__ void mq_gateup_slot(const uint8_t *Wg, const uint8_t 
         return it;
     };
     MqWave<T, decltype(item_of)> wv(item_of, 2 * nk, nb >> 2, n, (uint32_t)row_bytes, geo, rings);
-    wv.prologue();
-    mq_stage_xq(x, 0, 1, n, smem, xoff, 0u);
+    wv.start(x, geo, smem, xoff);
     wv.run(smem, red);
     __syncthreads();
     for (int i = threadIdx.x; i < nk * 16; i += blockDim.x) {
@@ -718,7 +770,7 @@ __device__ __forceinline__ void mq_gateup(const MqProj &gate, const MqProj &up, 
 // then the shared gammas; the shared gamma scales the down output as
 // src/sepia.c:3953-3957 does), into y and puts the counter back to zero --
 // deterministic whatever the arrival order.
-// LDS: [zero][XQ of h_slot][red: nk x P x 16 f32][flags: nk i32][rings].
+// LDS: [zero][XQ of h_slot][red: nk x P x 16 f32][flags: nk i32][raw h][rings].
 template <int T>
 __device__ __forceinline__ void mq_dn_slot(const uint8_t *Wd, uint64_t row_bytes, int32_t nb, int32_t inter,
                                            int64_t hidden, int32_t j0, int32_t jstep, int nk,
@@ -734,8 +786,7 @@ __device__ __forceinline__ void mq_dn_slot(const uint8_t *Wd, uint64_t row_bytes
         return it;
     };
     MqWave<T, decltype(item_of)> wv(item_of, nk, nb >> 2, inter, (uint32_t)row_bytes, geo, rings);
-    wv.prologue();
-    mq_stage_xq(hs, 0, 1, inter, lds0, MQ_ZERO, 0u);
+    wv.start(hs, geo, lds0, MQ_ZERO);
     wv.run(lds0, red);
 }
 
@@ -759,7 +810,7 @@ __device__ __forceinline__ void mq_down(const MqProj &down, const MqProj &s_down
     const size_t o_red = MQ_ZERO + mq_xq_bytes(inter);
     float *red = (float *)(smem + o_red);
     int32_t *flag = (int32_t *)(smem + o_red + (size_t)nk * geo.P * 64);
-    uint8_t *rings = smem + ((o_red + (size_t)nk * geo.P * 64 + (size_t)nk * 4 + 255) & ~(size_t)255);
+    uint8_t *rings = smem + geo.orings;
     const float *hs = h + (int64_t)slot * inter;
     const int32_t nb = (int32_t)Pj.n_blocks;
     switch (Pj.type) {

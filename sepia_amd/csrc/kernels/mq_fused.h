@@ -10,7 +10,8 @@
 //       published), runs the selection (route.h) into LDS and raises an LDS
 //       flag. The other waves meanwhile stream the shared experts' gate/up
 //       rows, which need no selection, then wait for the flag and stream the
-//       routed experts' rows. The gate/up work of all slots is cut into
+//       routed experts' rows. (Without a router, the expert FFN, wave 0
+//       streams as well.) The gate/up work of all slots is cut into
 //       units of 16 rows (gate and up) and dealt to the workgroups in
 //       contiguous runs of equal weight bytes, shared units first.
 //       h = silu(g) * u leaves as XQ segments of 16 rows (agent-scope stores);
@@ -234,6 +235,7 @@ __device__ __forceinline__ void mq_fz_gu(const MqProj &gate, const MqProj &up, c
     uint8_t *rings = smem + geo.o_rings;
     float *gred = (float *)(smem + geo.o_gred);
     int32_t *flag = si + MQ_SEL_FLAG;
+    const int first = io.rw ? 1 : 0;   // without a router wave 0 streams too
     if (w == 0) {
         if (io.rw) {
             if (threadIdx.x == 0) mq_grid_wait(io.bar, target1, io.err);
@@ -248,7 +250,7 @@ __device__ __forceinline__ void mq_fz_gu(const MqProj &gate, const MqProj &up, c
             si[threadIdx.x] = io.fixed + (int32_t)threadIdx.x;
         }
         if (threadIdx.x == 0) __hip_atomic_store(flag, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
-        return;
+        if (first) return;
     }
     // shared unit u: slot topk + u / tiles_i, expert u / tiles_i
     auto sitem = [&](int i) {
@@ -264,7 +266,7 @@ __device__ __forceinline__ void mq_fz_gu(const MqProj &gate, const MqProj &up, c
     };
     {
         MqWave<TS, decltype(sitem)> sp(sitem, 2 * gr.ns, (int)(s_gate.n_blocks >> 2), (int)(256 * s_gate.n_blocks),
-                                       (uint32_t)s_gate.row_bytes, geo.gu, rings, 1);
+                                       (uint32_t)s_gate.row_bytes, geo.gu, rings, first);
         sp.prologue();
         sp.run(smem, gred);
     }
@@ -294,7 +296,7 @@ __device__ __forceinline__ void mq_fz_gu(const MqProj &gate, const MqProj &up, c
         return it;
     };
     MqWave<TG, decltype(ritem)> rp(ritem, 2 * gr.nr, nbh >> 2, (int)(256 * nbh), (uint32_t)gate.row_bytes, geo.gu,
-                                   rings, 1);
+                                   rings, first);
     rp.prologue();
     rp.run(smem, gred);
 }

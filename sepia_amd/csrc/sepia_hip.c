@@ -127,6 +127,7 @@ static int g_opt_mq = 1;     /* sepia_hip_set_option("mq", 0) disables the matri
  * workgroup geometry (parts per item, item lanes, ring stages of the largest
  * format; 0 = planned) */
 static int g_opt_mq_p = 0, g_opt_mq_c = 0, g_opt_mq_s = 0;
+static int g_opt_mq_x = 0;   /* "mq_x": 0 = planner's choice, 1 = vector from global, 2 = vector by LDS DMA */
 static int g_opt_fuse = 0;   /* sepia_hip_set_option("fuse", 1) runs the MoE layer / expert FFN as one launch */
 static int g_opt_tile_t = 0; /* sepia_hip_set_option("tile_t", T) forces T steps per workgroup */
 
@@ -903,6 +904,10 @@ int sepia_hip_set_option(const char *name, int value) {
         g_opt_mq = value;
         return 1;
     }
+    if (strcmp(name, "mq_x") == 0 && value >= 0 && value <= 2) {
+        g_opt_mq_x = value;
+        return 1;
+    }
     if (strcmp(name, "fuse") == 0 && (value == 0 || value == 1)) {
         g_opt_fuse = value;
         return 1;
@@ -938,7 +943,7 @@ int sepia_hip_set_option(const char *name, int value) {
 #define MQ_CUS 256                  /* MI355X compute units */
 #define MQ_ZERO 768
 typedef struct {
-    int32_t P, ring;                /* as struct MqGeo in kernels/mq.h */
+    int32_t P, ring, xraw, orings;  /* as struct MqGeo in kernels/mq.h */
 } MqGeo;
 /* In-kernel selection by the gate/up launch (struct MqRoute in
  * kernels/mq.h); logits NULL: the experts come from sel_idx. */
@@ -951,6 +956,7 @@ typedef struct {
     float *w_out;
 } MqRoute;
 #define MQ_SEL_BYTES 512            /* the gate/up kernel's selection area in LDS */
+#define MQ_XDMA_GAIN 40             /* mq_geo: cost units the vector's LDS DMA saves (measured ~2 us a launch) */
 static size_t mq_xq_bytes(int64_t n) { return (size_t)(n / 256) * 832 + 3 * (size_t)(n / 16) * 4; }
 static int mq_code(int t) { return t == SEPIA_T_Q2_K ? 0 : (t == SEPIA_T_Q3_K ? 1 : (t == 12 ? 2 : -1)); }
 static const int k_mq_words[3] = { 7, 7, 9 };   /* padded words per lane (MQ<T>::Wp) */
@@ -958,47 +964,59 @@ static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 /* Geometry for workgroups of n_items items of nq quads; mc is the format
  * most items use, wmax the most words of any format the workgroup may run.
- * LDS = align256(fixed + 64 * n_items * P) + nw * ring; the rings take the
- * rest of the LDS (each at least one step of wmax words). Chooses the fewest
- * steps per wave of format mc, counting a one-stage ring with several steps
- * as 1.6 steps each (its loads do not overlap its compute), then the most
- * steps in flight, then the most waves. Returns 0 when nothing fits. */
-static int mq_geo(int mc, int wmax, int64_t n_items, int64_t nq, size_t fixed, unsigned *threads, MqGeo *geo,
-                  size_t *lds) {
+ * LDS = o_raw = align256(fixed + 64 * n_items * P), then (if the vector of
+ * raw_bytes goes by LDS DMA) the raw vector, then nw rings at orings; the
+ * rings take the rest of the LDS (each at least one step of wmax words).
+ * Chooses the fewest steps per wave of format mc, counting a one-stage ring
+ * with several steps as 1.6 steps each (its loads do not overlap its
+ * compute) and crediting the vector's DMA, then the most steps in flight,
+ * then the most waves. Returns 0 when nothing fits. */
+static int mq_geo(int mc, int wmax, int64_t n_items, int64_t nq, size_t fixed, size_t raw_bytes, unsigned *threads,
+                  MqGeo *geo, size_t *lds) {
     const size_t w1 = (size_t)k_mq_words[mc] * 1024, wm = (size_t)wmax * 1024;
-    int64_t best_cost = -1, best_fl = 0;
-    int best_nw = 0;
-    for (int P = 1; P <= 16 && P <= nq; P++) {
-        if (g_opt_mq_p && P != g_opt_mq_p) continue;
-        for (int C = 1; C * P <= 16 && C <= n_items; C++) {
-            if (g_opt_mq_c && C != g_opt_mq_c) continue;
-            const int nw = C * P;
-            const int64_t spw = ((n_items + C - 1) / C) * ((nq + P - 1) / P);
-            const size_t base = align256(fixed + (size_t)n_items * P * 64);
-            if (base + (size_t)nw * wm > g_lds_max) continue;
-            size_t ring = ((g_lds_max - base) / (size_t)nw) & ~(size_t)1023;
-            if (ring > 4 * wm) ring = 4 * wm;
-            if (g_opt_mq_s) {
-                ring = (size_t)g_opt_mq_s * wm;
-                if (base + (size_t)nw * ring > g_lds_max) continue;
-            }
-            int64_t S = (int64_t)(ring / w1);
-            if (S > 4) S = 4;
-            if (S > spw) S = spw;
-            const int64_t cost = spw * ((S >= 2 || spw == 1) ? 10 : 16);
-            const int64_t fl = (int64_t)nw * S;
-            if (best_cost < 0 || cost < best_cost || (cost == best_cost && (fl > best_fl || (fl == best_fl && nw > best_nw)))) {
-                best_cost = cost;
-                best_fl = fl;
-                best_nw = nw;
-                geo->P = P;
-                geo->ring = (int32_t)ring;
-                *threads = 64u * (unsigned)nw;
-                *lds = base + (size_t)nw * ring;
+    int64_t best_cost = 0, best_fl = 0;
+    int best_nw = 0, found = 0;
+    for (int xr = 0; xr <= (raw_bytes > 0); xr++) {
+        if ((g_opt_mq_x == 1 && xr) || (g_opt_mq_x == 2 && !xr)) continue;
+        for (int P = 1; P <= 16 && P <= nq; P++) {
+            if (g_opt_mq_p && P != g_opt_mq_p) continue;
+            for (int C = 1; C * P <= 16 && C <= n_items; C++) {
+                if (g_opt_mq_c && C != g_opt_mq_c) continue;
+                const int nw = C * P;
+                const int64_t spw = ((n_items + C - 1) / C) * ((nq + P - 1) / P);
+                const size_t o_raw = align256(fixed + (size_t)n_items * P * 64);
+                const size_t base = xr ? align256(o_raw + raw_bytes) : o_raw;
+                if (base + (size_t)nw * wm > g_lds_max) continue;
+                size_t ring = ((g_lds_max - base) / (size_t)nw) & ~(size_t)1023;
+                if (ring > 4 * wm) ring = 4 * wm;
+                if (g_opt_mq_s) {
+                    ring = (size_t)g_opt_mq_s * wm;
+                    if (base + (size_t)nw * ring > g_lds_max) continue;
+                }
+                int64_t S = (int64_t)(ring / w1);
+                if (S > 4) S = 4;
+                if (S > spw) S = spw;
+                /* the vector by DMA ahead of the weights saves about as
+                 * much as MQ_XDMA_GAIN cost units */
+                const int64_t cost = spw * ((S >= 2 || spw == 1) ? 10 : 16) - (xr ? MQ_XDMA_GAIN : 0);
+                const int64_t fl = (int64_t)nw * S;
+                if (!found || cost < best_cost ||
+                    (cost == best_cost && (fl > best_fl || (fl == best_fl && nw > best_nw)))) {
+                    found = 1;
+                    best_cost = cost;
+                    best_fl = fl;
+                    best_nw = nw;
+                    geo->P = P;
+                    geo->ring = (int32_t)ring;
+                    geo->xraw = xr ? (int32_t)o_raw : 0;
+                    geo->orings = (int32_t)base;
+                    *threads = 64u * (unsigned)nw;
+                    *lds = base + (size_t)nw * ring;
+                }
             }
         }
     }
-    return best_cost >= 0;
+    return found;
 }
 
 /* Shapes the matrix-core kernels take: a format with a decoder, 4-byte
@@ -1015,7 +1033,8 @@ static int mq_plan(int type, int64_t n_blocks, int64_t rows, uintptr_t base, uin
     const int64_t tiles = (rows + 15) / 16;
     const int64_t per = (tiles + MQ_CUS - 1) / MQ_CUS;     /* row groups per workgroup */
     *grid = (unsigned)((tiles + per - 1) / per);
-    if (!mq_geo(mc, k_mq_words[mc], per, n_blocks / 4, MQ_ZERO + mq_xq_bytes(256 * n_blocks), threads, geo, lds))
+    if (!mq_geo(mc, k_mq_words[mc], per, n_blocks / 4, MQ_ZERO + mq_xq_bytes(256 * n_blocks),
+                (size_t)1024 * n_blocks, threads, geo, lds))
         return -1;
     return K_MQ_MV + mc;
 }
@@ -1282,11 +1301,11 @@ static int mq_ffn_plan(const MoeProj *g, const MoeProj *u, const MoeProj *d, con
     const int32_t gmin = pl->gu_wps_r < pl->gu_wps_s || n_shared == 0 ? pl->gu_wps_r : pl->gu_wps_s;
     const int32_t dmin = pl->dn_wps_r < pl->dn_wps_s || n_shared == 0 ? pl->dn_wps_r : pl->dn_wps_s;
     const int64_t nk_gu = (tiles_i + gmin - 1) / gmin, nk_dn = (tiles_h + dmin - 1) / dmin;
-    if (!mq_geo(kg, wgu, 2 * nk_gu, H / 1024, MQ_ZERO + mq_xq_bytes(H) + MQ_SEL_BYTES, &pl->gu_threads, &pl->gu_geo,
-                &pl->gu_lds))
+    if (!mq_geo(kg, wgu, 2 * nk_gu, H / 1024, MQ_ZERO + mq_xq_bytes(H) + MQ_SEL_BYTES, (size_t)H * 4, &pl->gu_threads,
+                &pl->gu_geo, &pl->gu_lds))
         return 0;
-    if (!mq_geo(kd, wdn, nk_dn, I / 1024, MQ_ZERO + mq_xq_bytes(I) + (size_t)nk_dn * 4 + 256, &pl->dn_threads,
-                &pl->dn_geo, &pl->dn_lds))
+    if (!mq_geo(kd, wdn, nk_dn, I / 1024, MQ_ZERO + mq_xq_bytes(I) + (size_t)nk_dn * 4 + 256, (size_t)I * 4,
+                &pl->dn_threads, &pl->dn_geo, &pl->dn_lds))
         return 0;
     pl->gu_grid = (unsigned)(topk * pl->gu_wps_r + n_shared * pl->gu_wps_s);
     pl->dn_grid = (unsigned)(topk * pl->dn_wps_r + n_shared * pl->dn_wps_s);
@@ -1478,7 +1497,8 @@ static int64_t mq_phase_cost(int mc, int64_t n_items, int64_t nq, int P, int nw,
 }
 
 static int mq_fuse_plan(const MoeProj *g, const MoeProj *u, const MoeProj *d, const MoeProj *sg, const MoeProj *su,
-                        const MoeProj *sd, int32_t topk, int32_t n_shared, int64_t H, int64_t I, MqFusePlan *fp) {
+                        const MoeProj *sd, int32_t topk, int32_t n_shared, int64_t H, int64_t I, int router,
+                        MqFusePlan *fp) {
     static int told = 0;   /* a device or layer the fused launch cannot take: said once */
     MqFfnPlan pl;
     if (!g_opt_fuse || topk < 1 || !mq_ffn_plan(g, u, d, sg, su, sd, topk, n_shared, H, I, &pl)) return 0;
@@ -1506,11 +1526,12 @@ static int mq_fuse_plan(const MoeProj *g, const MoeProj *u, const MoeProj *d, co
     const int64_t dnk = (tiles_h + dmin - 1) / dmin;
     const int64_t nqg = H / 1024, nqd = I / 1024;
     int64_t best = -1;
-    for (int nw = 3; nw <= 16; nw++)
-        for (int Pg = 1; Pg <= nw - 1 && Pg <= nqg; Pg++) {
-            if ((nw - 1) % Pg) continue;
+    /* gate/up runs on the waves after the control wave (all of them without
+     * a router), down on every wave; waves past the last full column of P
+     * parts idle in that phase */
+    for (int nw = 2; nw <= 16; nw++)
+        for (int Pg = 1; Pg <= nw - router && Pg <= nqg; Pg++) {
             for (int Pd = 1; Pd <= nw && Pd <= nqd; Pd++) {
-                if (nw % Pd) continue;
                 size_t o = MQ_ZERO + mq_xq_bytes(H);
                 const size_t o_sel = o;
                 o += MQ_FSEL_BYTES;
@@ -1526,11 +1547,12 @@ static int mq_fuse_plan(const MoeProj *g, const MoeProj *u, const MoeProj *d, co
                 if (o_rings + (size_t)nw * wmax * 1024 > g_lds_max) continue;
                 size_t ring = ((g_lds_max - o_rings) / (size_t)nw) & ~(size_t)1023;
                 if (ring > (size_t)4 * wmax * 1024) ring = (size_t)4 * wmax * 1024;
-                const int64_t cost = mq_phase_cost(kg, 2 * nu_max, nqg, Pg, nw - 1, ring) +
+                const int64_t cost = mq_phase_cost(kg, 2 * nu_max, nqg, Pg, nw - router, ring) +
                                      mq_phase_cost(kd, dnk, nqd, Pd, nw, ring);
                 if (best < 0 || cost < best) {
                     best = cost;
                     MqFuseGeo *G = &fp->geo;
+                    memset(G, 0, sizeof *G);
                     G->gu.P = Pg;
                     G->dn.P = Pd;
                     G->gu.ring = G->dn.ring = (int32_t)ring;
@@ -1711,7 +1733,7 @@ int sepia_gpu_moe_decode(const SepiaMoeLayerDesc *L, SepiaGpuBuf *x, SepiaGpuBuf
     int32_t nr = L->n_routed, ns = L->n_shared, tk = L->topk;
     float rs = L->route_scale, gsc = L->global_scale;
     MqFusePlan fp;
-    if (mq_fuse_plan(&g, &u, &d, &sg, &su, &sd, tk, ns, H, I, &fp)) {
+    if (mq_fuse_plan(&g, &u, &d, &sg, &su, &sd, tk, ns, H, I, 1, &fp)) {
         MqFuseIo io;
         memset(&io, 0, sizeof io);
         io.rw = rw;
@@ -1781,7 +1803,7 @@ int sepia_gpu_expert_ffn(const SepiaExpertTensor *gate, const SepiaExpertTensor 
         !prep_out(y, op))
         return 0;
     MqFusePlan fp;
-    if (mq_fuse_plan(&g, &u, &d, &none, &none, &none, 1, 0, hidden, inter, &fp)) {
+    if (mq_fuse_plan(&g, &u, &d, &none, &none, &none, 1, 0, hidden, inter, 0, &fp)) {
         MqFuseIo io;
         memset(&io, 0, sizeof io);
         io.x = (const float *)x->dev;

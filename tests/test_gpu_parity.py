@@ -452,6 +452,24 @@ def test_selftest_touch_and_wrap(dev):
 
 
 # ------------------------------------------------------------------- MoE
+@pytest.fixture
+def mq_vector(dev, request):
+    """Force how the matrix-core kernels read their vector: 1 = from global
+    memory after the weight prologue, 2 = by LDS DMA ahead of it."""
+    assert dev.L.sepia_hip_set_option(b"mq_x", request.param) == 1
+    yield request.param
+    dev.L.sepia_hip_set_option(b"mq_x", 0)
+
+
+@pytest.mark.parametrize("mq_vector", [1, 2], indirect=True, ids=["global", "dma"])
+@pytest.mark.parametrize("t,out_dim,in_dim", [(12, 4096, 4096), (10, 3072, 6144), (11, 6144, 3072),
+                                              (10, 12288, 2048), (12, 40, 12288)], ids=lambda v: str(v))
+def test_matvec_mq_vector_paths(dev, orc, mq_vector, t, out_dim, in_dim):
+    with Launches(dev) as n:
+        check_matvec(dev, orc, t, out_dim, in_dim, seed=out_dim + in_dim + t)
+        assert n.count(MQ_NAMES[t]) == 1
+
+
 def make_layer(dev, rng, hidden, inter, n_routed, n_shared, tg, tu, td, ts, rw_off=0):
     """Shared buffers with seeded host data; returns (desc, spec, keep). The
     router matrix starts rw_off bytes into its buffer."""
@@ -618,6 +636,27 @@ def test_moe_decode_fused(dev, orc, fuse, types):
             assert_close(y, y_ref, what="moe fuse=%d rep %d" % (fuse, rep), gate=False)
     finally:
         dev.L.sepia_hip_set_option(b"fuse", 0)
+    for b in bufs.values():
+        dev.free(b)
+
+
+@pytest.mark.parametrize("mq_vector", [1, 2], indirect=True, ids=["global", "dma"])
+def test_moe_decode_mq_vector_paths(dev, orc, mq_vector):
+    """C3 layer shapes with 16 routed experts resident; gate/up and down read x
+    and h either way."""
+    rng = np.random.default_rng(500 + mq_vector)
+    desc, spec, bufs = make_layer(dev, rng, hidden=6144, inter=3072, n_routed=16, n_shared=2,
+                                  tg=10, tu=10, td=11, ts=12)
+    for rep in range(2):
+        x = synth.normal_vector(rng, 6144)
+        with Launches(dev) as n:
+            y, idx, w = run_moe(dev, desc, x)
+            assert n.count("sepia_mq_gateup") == 1 and n.count("sepia_mq_down") == 1
+        y_ref, logits, idx_ref, w_ref = orc.moe_layer(spec, x, threads=THREADS)
+        chosen = check_route(orc, spec, logits, idx, w)
+        if chosen != list(idx_ref):
+            y_ref, _, _, _ = orc.moe_layer(spec, x, force_idx=chosen, threads=THREADS)
+        assert_close(y, y_ref, what="moe mq_x %d rep %d" % (mq_vector, rep), gate=False)
     for b in bufs.values():
         dev.free(b)
 
