@@ -12,28 +12,31 @@
 //   sepia_pf_group    one workgroup: the (token, slot) pairs p = t * n_sel + k
 //                     sorted by expert (shared expert s is expert
 //                     n_routed + s) and cut into units of <= 32 pairs
-//   sepia_pf_gateup   per (unit, 32-row tile): h[p][.] = silu(g) * u
-//   sepia_pf_down     per (unit, 64-row tile): yp[p][.] = down_e . h[p]
+//   sepia_pf_split    x as bf16 hi / lo and its 16-column sums
+//   sepia_pf_gateup   per (32-row tile, unit): h[p][.] = silu(g) * u (bf16 hi / lo)
+//   sepia_pf_down     per (64-row tile, unit): yp[p][.] = down_e . h[p]
 //   sepia_pf_combine  y[t] = sum_k w[t][k] yp[t * n_sel + k], slot order
-// The projections dequantize 128-column tiles of their weights with the
-// bit-exact decoders (decode.h) from raw blocks staged in LDS, split every
-// weight and activation into bf16 hi + lo (hi = bf16(v), lo = bf16(v - hi),
-// together within 2^-17 |v|) and run v_mfma_f32_16x16x32_bf16 three times
-// per step (hi.hi + hi.lo + lo.hi), accumulating in f32. A single bf16 term
-// would miss the 1e-4 ||y||_inf bar by an order of magnitude. Results do not
-// depend on how pairs are grouped into units: every output element is its
-// own dot product in a fixed column order.
+// The projections stream raw weight blocks and the unit's activation rows
+// into LDS by DMA ahead of use and run the bf16 matrix cores with f32
+// accumulation. Q2_K, Q3_K and Q4_K go in as their exact integer codes
+// (scales applied per block or sub-block in f32), the other formats are
+// dequantized bit-exactly and split into bf16 hi + lo; activations are
+// always hi + lo (hi = bf16(v), lo = bf16(v - hi), together within 2^-17
+// |v|; a single bf16 term would miss the 1e-4 ||y||_inf bar by an order of
+// magnitude), and the lo terms are skipped when every lo is zero. Results do
+// not depend on how pairs are grouped into units: every output element is
+// its own dot product in a fixed column order.
 #pragma once
 #include "common.h"
 #include "decode.h"
+#include "mq.h"
 #include "route.h"
 
 typedef __bf16 pf_bf16x8 __attribute__((ext_vector_type(8)));
 typedef float pf_f32x4 __attribute__((ext_vector_type(4)));
 
 #define PF_MT 32     // pairs per unit (two 16-row M tiles)
-#define PF_KC 128    // columns per staged tile (half a 256-column block)
-#define PF_LD 136    // LDS row stride of bf16 tiles (PF_KC + 8: conflict-free fragment reads)
+
 
 // ------------------------------------------------------------- router ----
 // logits[t][r] = sum_k x[t][k] * Rw[r][k]: 32 tokens x 32 rows per
@@ -94,7 +97,9 @@ extern "C" __global__ __launch_bounds__(1024) void sepia_pf_group(const int32_t 
                                                                   int32_t n_routed, int32_t n_shared, int32_t topk,
                                                                   int32_t *__restrict__ list,
                                                                   int32_t *__restrict__ units,
-                                                                  int32_t *__restrict__ n_units) {
+                                                                  int32_t *__restrict__ n_units,
+                                                                  uint32_t *__restrict__ lo_any) {
+    if (threadIdx.x == 0) *lo_any = 0u;
     __shared__ int32_t cnt[1088], off[1089], fill[1088], uoff[1089];
     const int E = n_routed + n_shared, n_sel = topk + n_shared;
     const int64_t P = T * n_sel;
@@ -137,67 +142,165 @@ extern "C" __global__ __launch_bounds__(1024) void sepia_pf_group(const int32_t 
     }
 }
 
-// --------------------------------------------------------- tile helpers --
-// v = hi + lo with hi = bf16(v), lo = bf16(v - hi) (round to nearest even).
+// ---------------------------------------------------- activations split --
+// hi[i] = bf16(x[i]), lo[i] = bf16(x[i] - hi[i]) (round to nearest even).
 __device__ __forceinline__ void pf_split(float v, __bf16 &hi, __bf16 &lo) {
     hi = (__bf16)v;
     lo = (__bf16)(v - (float)hi);
 }
-
-// Stage PF_KC columns [k0, k0 + PF_KC) of nr f32 rows (row i at src_row(i),
-// zero rows beyond nv) as bf16 hi / lo tiles [32][PF_LD].
-template <class RowFn>
-__device__ __forceinline__ void pf_stage_act(const RowFn &src_row, int nv, int64_t k0, __bf16 (*ah)[PF_LD],
-                                             __bf16 (*al)[PF_LD]) {
-    for (int i = threadIdx.x; i < 32 * (PF_KC / 4); i += blockDim.x) {
-        const int m = i / (PF_KC / 4), c4 = i - m * (PF_KC / 4);
-        float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        if (m < nv) v = *(const float4 *)(src_row(m) + k0 + 4 * c4);
-        const float a[4] = {v.x, v.y, v.z, v.w};
+// Segment i (16 values) of x: hi / lo as above, s16[i] = their f32 sum in
+// column order (the K-quant min terms of the integer pipelines).
+// lo_any (zeroed by sepia_pf_group) becomes nonzero if any lo is: with it
+// zero, x is bf16-representable and the projections skip the lo terms (an
+// exact shortcut).
+extern "C" __global__ __launch_bounds__(256) void sepia_pf_split(const float *__restrict__ x, int64_t n_seg,
+                                                                 __bf16 *__restrict__ hi, __bf16 *__restrict__ lo,
+                                                                 float *__restrict__ s16, uint32_t *__restrict__ lo_any) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n_seg) return;
+    const float4 *x4 = (const float4 *)(x + 16 * i);
+    float v[16];
 #pragma unroll
-        for (int j = 0; j < 4; j++) pf_split(a[j], ah[m][4 * c4 + j], al[m][4 * c4 + j]);
+    for (int c = 0; c < 4; c++) {
+        const float4 t = x4[c];
+        v[4 * c] = t.x;
+        v[4 * c + 1] = t.y;
+        v[4 * c + 2] = t.z;
+        v[4 * c + 3] = t.w;
+    }
+    __bf16 h[16], l[16];
+    float sum = 0.0f;
+    bool nz = false;
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+        pf_split(v[k], h[k], l[k]);
+        sum += v[k];
+        nz |= (float)l[k] != 0.0f;
+    }
+    if (__ballot(nz) && (threadIdx.x & 63) == __builtin_ctzll(__ballot(nz)))
+        __hip_atomic_fetch_or(lo_any, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    uint4 *ho = (uint4 *)(hi + 16 * i), *lw = (uint4 *)(lo + 16 * i);
+    ho[0] = ((const uint4 *)h)[0];
+    ho[1] = ((const uint4 *)h)[1];
+    lw[0] = ((const uint4 *)l)[0];
+    lw[1] = ((const uint4 *)l)[1];
+    s16[i] = sum;
+}
+
+// ----------------------------------------------------------- pipelines ---
+// A projection workgroup computes a 32-pair x R-row tile (R = 32 gate and
+// 32 up rows, or 64 down rows) over K = the projection's input width, one
+// 256-column block per step:
+//   step b: wait for block b's DMAs; issue block b + 1's (activations as
+//           bf16 hi / lo rows, weights as raw blocks); dequantize block b's
+//           raw weights (bit-exact decoders) into bf16 hi / lo tiles; three
+//           MFMAs per 32 columns (hi.hi + hi.lo + lo.hi).
+// Everything a step reads arrives by LDS DMA one step ahead, so the loads
+// of block b + 1 fly while block b computes.
+// Tiles are [rows][256] bf16 with 512-byte rows; the 16-byte chunk c of row
+// r sits at chunk c ^ (r & 15), so the 16 rows of an MFMA fragment read hit
+// 16 different bank groups.
+#define PF_RDMAX 54   // dwords of a staged raw block window (Q6_K: 210 bytes + misalignment)
+#define PF_TILE 16384 // bytes of a [32][256] bf16 tile
+
+__device__ __forceinline__ uint32_t pf_lds(const void *p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t *)p;
+}
+__device__ __forceinline__ const uint8_t *pf_uniform(const void *p) {
+    const uint64_t b = (uint64_t)(uintptr_t)p;
+    return (const uint8_t *)(uintptr_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(b >> 32))
+                                         << 32) |
+                                        (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)b));
+}
+// LDS DMA: lane l's 16 (or 4) bytes at base + voff land at lds + 16 l (4 l).
+__device__ __forceinline__ void pf_dma16(const void *base, uint32_t voff, uint32_t lds) {
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"(pf_uniform(base)), "{m0}"(lds) : "memory");
+}
+__device__ __forceinline__ void pf_dma4(const void *base, uint32_t voff, uint32_t lds) {
+    asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, %1" : : "v"(voff), "s"(pf_uniform(base)), "{m0}"(lds) : "memory");
+}
+__device__ __forceinline__ uint32_t pf_swz(int r, int chunk) { return (uint32_t)r * 512u + ((uint32_t)(chunk ^ (r & 15)) << 4); }
+
+// Activation rows of the unit into a tile pair (hi, lo) at dst: row m comes
+// from element offset roff[m] (bf16 units) + 256 b of src_hi / src_lo. One
+// wave instruction moves two rows of one of the two tiles.
+__device__ __forceinline__ void pf_issue_act(const __bf16 *src_hi, const __bf16 *src_lo, const uint32_t *roff,
+                                             int64_t b, uint8_t *dst, bool with_lo = true) {
+    const int nw = (int)(blockDim.x >> 6), w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int lane = threadIdx.x & 63;
+    for (int j = w; j < (with_lo ? 32 : 16); j += nw) {
+        const int hl = j >> 4, rp = j & 15, row = 2 * rp + (lane >> 5), p = lane & 31;
+        const uint32_t voff = 2u * (roff[row] + 256u * (uint32_t)b) + ((uint32_t)(p ^ (row & 15)) << 4);
+        pf_dma16(hl ? (const void *)src_lo : (const void *)src_hi, voff, pf_lds(dst + hl * PF_TILE + 2 * rp * 512));
     }
 }
 
-// Raw bytes of block blk of rows r0 .. r0 + nr - 1 (rows past `rows` repeat
-// the last one) into LDS, 2 bytes at a time (blocks are 2-byte aligned).
+// Raw blocks b of nr rows (rows r0 .. r0 + nr - 1 of a matrix of `rows`
+// rows; rows past the end repeat the last one) into dst, row k at k * 4 RD:
+// each row's 4-byte-aligned window that holds the block.
 template <int T>
-__device__ __forceinline__ void pf_stage_raw(const uint8_t *W, uint64_t row_bytes, int64_t rows, int64_t r0, int nr,
-                                             int64_t blk, uint8_t *raw) {
-    constexpr int bb = Fmt<T>::bytes, hw = bb / 2;
-    for (int i = threadIdx.x; i < nr * hw; i += blockDim.x) {
-        const int r = i / hw, c = i - r * hw;
-        int64_t row = r0 + r;
-        row = row < rows ? row : rows - 1;
-        ((uint16_t *)raw)[r * hw + c] = *(const uint16_t *)(W + row * row_bytes + blk * bb + 2 * c);
+__device__ __forceinline__ void pf_issue_raw(const uint8_t *W, uint64_t row_bytes, int64_t rows, int64_t r0, int nr,
+                                             int64_t b, uint8_t *dst) {
+    constexpr int BB = Fmt<T>::bytes, RD = (BB + 6) / 4;
+    const int nw = (int)(blockDim.x >> 6), w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int lane = threadIdx.x & 63;
+    const uint8_t *Wa = (const uint8_t *)((uintptr_t)W & ~(uintptr_t)3);
+    const uint32_t delta = (uint32_t)((uintptr_t)W & 3);
+    const int n_ins = (nr * RD + 63) >> 6;
+    for (int j = w; j < n_ins; j += nw) {
+        const int i = 64 * j + lane;
+        if (i < nr * RD) {
+            const int r = i / RD, d = i - r * RD;
+            int64_t rr = r0 + r;
+            rr = rr < rows ? rr : rows - 1;
+            const uint64_t off = delta + (uint64_t)rr * row_bytes + (uint64_t)b * BB;
+            pf_dma4(Wa, (uint32_t)(off & ~(uint64_t)3) + 4u * (uint32_t)d, pf_lds(dst + 256 * j));
+        }
     }
 }
 
-// Dequantize parts h4 .. h4 + 3 (PF_KC columns) of the nr staged blocks to
-// bf16 hi / lo tiles [nr][PF_LD]: thread i takes part i % 4 of row i / 4.
+// Dequantize the staged raw blocks into bf16 (hi, lo) tiles: nper rows of
+// W0 into dst0 and, with W1, nper rows of W1 (staged after them) into dst1;
+// each lo tile lies lo_off bytes after its hi tile. 64 rows x 8 parts of
+// 32 weights: one part per thread at 512 threads.
 template <int T>
-__device__ __forceinline__ void pf_dequant(const uint8_t *raw, int nr, int h4, __bf16 (*bh)[PF_LD],
-                                           __bf16 (*bl)[PF_LD]) {
-    for (int i = threadIdx.x; i < nr * 4; i += blockDim.x) {
-        const int r = i >> 2, q = i & 3;
+__device__ __forceinline__ void pf_dequant_raw(const uint8_t *raw, const uint8_t *W0, const uint8_t *W1, int nper,
+                                               uint64_t row_bytes, int64_t rows, int64_t r0, int64_t b, uint8_t *dst0,
+                                               uint8_t *dst1, uint32_t lo_off) {
+    constexpr int BB = Fmt<T>::bytes, RD = (BB + 6) / 4;
+    const int nr = W1 ? 2 * nper : nper;
+    for (int i = threadIdx.x; i < nr * 8; i += blockDim.x) {
+        const int q = i & 7, rg = i >> 3;
+        const int mat = rg >= nper, r = rg - mat * nper;
+        const uint8_t *W = mat ? W1 : W0;
+        int64_t rr = r0 + r;
+        rr = rr < rows ? rr : rows - 1;
+        const uint32_t mis = (uint32_t)(((uintptr_t)W & 3) + (uint64_t)rr * row_bytes + (uint64_t)b * BB) & 3u;
         float v[32];
-        decode_part<T>(raw + r * Fmt<T>::bytes, h4 + q, v);
+        decode_part<T>(raw + (size_t)(mat * nper + r) * RD * 4 + mis, q, v);
+        uint8_t *dst = mat ? dst1 : dst0;
 #pragma unroll
-        for (int j = 0; j < 32; j++) pf_split(v[j], bh[r][32 * q + j], bl[r][32 * q + j]);
+        for (int c = 0; c < 4; c++) {
+            __bf16 hh[8], ll[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) pf_split(v[8 * c + j], hh[j], ll[j]);
+            const uint32_t o = pf_swz(r, 4 * q + c);
+            *(uint4 *)(dst + o) = *(const uint4 *)hh;
+            *(uint4 *)(dst + lo_off + o) = *(const uint4 *)ll;
+        }
     }
 }
 
-// acc += A[m0 .. m0+15][.] . B[n0 .. n0+15][.]^T over the staged PF_KC
-// columns, three MFMAs (hi.hi, hi.lo, lo.hi) per 32 columns.
-__device__ __forceinline__ void pf_mma(pf_f32x4 &acc, __bf16 (*ah)[PF_LD], __bf16 (*al)[PF_LD], int m0,
-                                       __bf16 (*bh)[PF_LD], __bf16 (*bl)[PF_LD], int n0) {
-    const int l = threadIdx.x & 63, r = l & 15, kq = 8 * (l >> 4);
+// acc += A[m0 .. m0 + 15][.] . B[n0 .. n0 + 15][.]^T over the 256 staged
+// columns (A: a 32-row tile pair hi, lo; B: hi tile, its lo b_lo bytes on).
+__device__ __forceinline__ void pf_mma256(pf_f32x4 &acc, const uint8_t *A, int m0, const uint8_t *B, int n0,
+                                          uint32_t b_lo) {
+    const int l = threadIdx.x & 63, r = l & 15, g = l >> 4;
 #pragma unroll
-    for (int kk = 0; kk < PF_KC; kk += 32) {
-        const pf_bf16x8 a_h = *(const pf_bf16x8 *)&ah[m0 + r][kk + kq];
-        const pf_bf16x8 a_l = *(const pf_bf16x8 *)&al[m0 + r][kk + kq];
-        const pf_bf16x8 b_h = *(const pf_bf16x8 *)&bh[n0 + r][kk + kq];
-        const pf_bf16x8 b_l = *(const pf_bf16x8 *)&bl[n0 + r][kk + kq];
+    for (int kk = 0; kk < 256; kk += 32) {
+        const uint32_t oa = pf_swz(m0 + r, kk / 8 + g), ob = pf_swz(n0 + r, kk / 8 + g);
+        const pf_bf16x8 a_h = *(const pf_bf16x8 *)(A + oa), a_l = *(const pf_bf16x8 *)(A + PF_TILE + oa);
+        const pf_bf16x8 b_h = *(const pf_bf16x8 *)(B + ob), b_l = *(const pf_bf16x8 *)(B + b_lo + ob);
         acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_h, b_h, acc, 0, 0, 0);
         acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_h, b_l, acc, 0, 0, 0);
         acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_l, b_h, acc, 0, 0, 0);
@@ -214,131 +317,488 @@ struct PfProj {
     int32_t pad;
 };
 
-// ------------------------------------------------------------- gate/up ---
-// Workgroup (unit u, rows 32 by .. 32 by + 31 of I): wave w computes the
-// 16x16 tile (pairs 16 (w >> 1) .., rows 16 (w & 1) ..) of gate and of up;
-// h[p][row] = silu(gate) * up.
-// LDS of the gate/up workgroup (one set for every format).
-struct PfGuLds {
-    __bf16 ah[32][PF_LD], al[32][PF_LD];
-    __bf16 gh[32][PF_LD], gl[32][PF_LD], uh[32][PF_LD], ul[32][PF_LD];
-    uint8_t rawg[32 * 212], rawu[32 * 212];
+// LDS of both projection kernels (PF_LDS_BYTES, dynamic): two activation
+// tile pairs (steps b, b + 1), the weight tile pairs, two raw areas.
+#define PF_O_B (4 * PF_TILE)
+#define PF_O_RAW (8 * PF_TILE)
+#define PF_RAW_BYTES (64 * PF_RDMAX * 4)
+#define PF_LDS_BYTES 163840                        // the whole 160 KB
+#define PF_O_ROFF (PF_LDS_BYTES - 2 * PF_MT * 4)   // row tables at the top (both paths)
+
+// ------------------------------------------------- integer K-quant path ---
+// For Q2_K, Q3_K and Q4_K the B operand is the weights' integer codes, exact
+// in bf16: Q2_K and Q3_K with their 16-weight sub-block scale folded in
+// (sc * q in 0..45 and (sc - 32) * q in -124..128), Q4_K the bare 4-bit
+// code. Per weight row n and block (src/quants.c and the ggml layouts):
+//   Q2_K  y += d_n sum_k B_k x_k - dmin_n sum_sb m_sb S_sb(x)
+//   Q3_K  y += d_n sum_k B_k x_k
+//   Q4_K  y += sum_j (d_n sc_j sum_{k in j} q_k x_k - dmin_n m_j S32_j(x))
+// with S the 16-column sums of x (S32_j = S_2j + S_2j+1). The Q2_K min term
+// is one K=16 MFMA over the 16 sub-blocks (m exact in bf16, S as hi + lo).
+// Only x carries a hi / lo split: two MFMAs per 32 columns, and a third of
+// the VALU work of decoding to f32 and splitting.
+#define PF_O_RS (PF_O_B + 2 * PF_TILE)   // per-row scalars [64][16] f32 (after the 32 KB of code tiles)
+#define PF_O_BM (PF_O_RS + 64 * 16 * 4)   // Q2_K mins [64][16] bf16
+#define PF_O_S16 (PF_O_BM + 64 * 16 * 2)  // 16-column sums of the unit's x rows [2][32][16] f32
+
+typedef short pf_s16x4 __attribute__((ext_vector_type(4)));
+
+// u32 at a 2-byte-aligned LDS address (LDS loads through an address-space-3
+// pointer: a generic one would become a flat load, which waits on vmcnt).
+typedef const __attribute__((address_space(3))) uint32_t pf_lds_u32;
+__device__ __forceinline__ uint32_t pf_ld32(const uint8_t *p) {
+    const uint32_t a = pf_lds(p);
+    pf_lds_u32 *q = (pf_lds_u32 *)(size_t)(a & ~3u);
+    if ((a & 3) == 0) return q[0];
+    return __builtin_amdgcn_alignbyte(q[1], q[0], a & 3u);   // byte shift
+}
+__device__ __forceinline__ uint4 pf_pack8(const float (&f)[8]) {
+    __bf16 h[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) h[i] = (__bf16)f[i];
+    return *(const uint4 *)h;
+}
+// Bytes of u (each < 256) as floats.
+__device__ __forceinline__ void pf_bytes(uint32_t u, float *f) {
+    f[0] = mq_ubyte<0>(u);
+    f[1] = mq_ubyte<1>(u);
+    f[2] = mq_ubyte<2>(u);
+    f[3] = mq_ubyte<3>(u);
+}
+
+template <int T> struct PfInt;
+// Q2_K (ggml): weight k = 128 h + 32 s + 16 g + l: q = (qs[32 h + 16 g + l]
+// >> 2 s) & 3, sub-block k / 16, scale byte lo nibble sc, hi nibble m.
+template <> struct PfInt<ST_Q2_K> {
+    static constexpr bool min16 = true, per_sub = false;
+    static __device__ __forceinline__ uint4 chunk(const uint8_t *b, int c) {
+        const int h = c >> 4, s = (c >> 2) & 3;
+        const uint8_t *q = b + 16 + 32 * h + 8 * (c & 3);
+        const uint32_t sc = ld_u8(b + (c >> 1)) & 15u;
+        const uint32_t v0 = ((pf_ld32(q) >> (2 * s)) & 0x03030303u) * sc;
+        const uint32_t v1 = ((pf_ld32(q + 4) >> (2 * s)) & 0x03030303u) * sc;
+        float f[8];
+        pf_bytes(v0, f);
+        pf_bytes(v1, f + 4);
+        return pf_pack8(f);
+    }
+    // item j (0 .. 15) of a row's scalars
+    static __device__ __forceinline__ void scalar(const uint8_t *b, int j, float *rs, __bf16 *bm) {
+        bm[j] = (__bf16)(float)(ld_u8(b + j) >> 4);
+        if (j < 2) rs[j] = h2f(b + 80 + 2 * j);
+    }
+};
+// Q3_K: Q2_K's indexing; q - 4 unless hmask[16 g + l] bit (4 h + s).
+template <> struct PfInt<ST_Q3_K> {
+    static constexpr bool min16 = false, per_sub = false;
+    static __device__ __forceinline__ uint4 chunk(const uint8_t *b, int c) {
+        const int h = c >> 4, s = (c >> 2) & 3, l0 = 8 * (c & 3);
+        const uint8_t *q = b + 32 + 32 * h + l0, *hm = b + l0;
+        const float sc = (float)q3_scale(b + 96, c >> 1);
+        const uint32_t v0 = ((pf_ld32(q) >> (2 * s)) & 0x03030303u) + 4u * ((pf_ld32(hm) >> (4 * h + s)) & 0x01010101u);
+        const uint32_t v1 =
+            ((pf_ld32(q + 4) >> (2 * s)) & 0x03030303u) + 4u * ((pf_ld32(hm + 4) >> (4 * h + s)) & 0x01010101u);
+        float f[8];
+        pf_bytes(v0, f);
+        pf_bytes(v1, f + 4);
+#pragma unroll
+        for (int i = 0; i < 8; i++) f[i] = (f[i] - 4.0f) * sc;
+        return pf_pack8(f);
+    }
+    static __device__ __forceinline__ void scalar(const uint8_t *b, int j, float *rs, __bf16 *) {
+        if (j == 0) rs[0] = h2f(b + 108);
+    }
+};
+// Q4_K: weight k = 64 p + 32 n + l: nibble n of qs[32 p + l], sub-block
+// j = 2 p + n with its (sc, m) pair.
+template <> struct PfInt<ST_Q4_K> {
+    static constexpr bool min16 = false, per_sub = true;
+    static __device__ __forceinline__ uint4 chunk(const uint8_t *b, int c) {
+        const int j = c >> 2;
+        const uint8_t *q = b + 16 + 32 * (j >> 1) + 8 * (c & 3);
+        const int sh = 4 * (j & 1);
+        float f[8];
+        pf_bytes((pf_ld32(q) >> sh) & 0x0F0F0F0Fu, f);
+        pf_bytes((pf_ld32(q + 4) >> sh) & 0x0F0F0F0Fu, f + 4);
+        return pf_pack8(f);
+    }
+    static __device__ __forceinline__ void scalar(const uint8_t *b, int j, float *rs, __bf16 *) {
+        if (j >= 8) return;
+        int sc, mn;
+        k4_scale_min(b + 4, j, sc, mn);
+        rs[j] = h2f(b) * (float)sc;
+        rs[8 + j] = h2f(b + 2) * (float)mn;
+    }
 };
 
+// B tiles (codes) and per-row scalars of the staged raw blocks: nper rows of
+// W0 into B0 and, with W1, nper rows of W1 into B1; rows counted across
+// both (rg) index rs[rg][16] and bm[rg][16].
 template <int T>
-__device__ __forceinline__ void pf_gateup_t(PfGuLds &S, const uint8_t *Wg, const uint8_t *Wu, uint64_t row_bytes,
-                                            int64_t nb, int64_t I, int64_t H, const float *__restrict__ x, int n_sel,
-                                            const int32_t *pairs, int nv, int64_t r0, float *__restrict__ h) {
-    auto &ah = S.ah, &al = S.al, &gh = S.gh, &gl = S.gl, &uh = S.uh, &ul = S.ul;
-    uint8_t *rawg = S.rawg, *rawu = S.rawu;
-    const int w = threadIdx.x >> 6, m0 = 16 * (w >> 1), n0 = 16 * (w & 1);
-    pf_f32x4 g = {0.0f, 0.0f, 0.0f, 0.0f}, u = {0.0f, 0.0f, 0.0f, 0.0f};
-    auto xrow = [&](int m) { return x + (int64_t)(pairs[m] / n_sel) * H; };
-    for (int64_t blk = 0; blk < nb; blk++) {
-        pf_stage_raw<T>(Wg, row_bytes, I, r0, 32, blk, rawg);
-        pf_stage_raw<T>(Wu, row_bytes, I, r0, 32, blk, rawu);
-        __syncthreads();
-        for (int h4 = 0; h4 < 8; h4 += 4) {
-            pf_stage_act(xrow, nv, blk * 256 + 32 * h4, ah, al);
-            pf_dequant<T>(rawg, 32, h4, gh, gl);
-            pf_dequant<T>(rawu, 32, h4, uh, ul);
-            __syncthreads();
-            pf_mma(g, ah, al, m0, gh, gl, n0);
-            pf_mma(u, ah, al, m0, uh, ul, n0);
-            __syncthreads();
+__device__ __forceinline__ void pf_int_build(const uint8_t *raw, const uint8_t *W0, const uint8_t *W1, int nper,
+                                             uint64_t row_bytes, int64_t rows, int64_t r0, int64_t b, uint8_t *B0,
+                                             uint8_t *B1, float *rs, __bf16 *bm) {
+    constexpr int BB = Fmt<T>::bytes, RD = (BB + 6) / 4;
+    const int nr = W1 ? 2 * nper : nper;
+    auto blk = [&](int rg) {
+        const int mat = rg >= nper, r = rg - mat * nper;
+        int64_t rr = r0 + r;
+        rr = rr < rows ? rr : rows - 1;
+        const uint32_t mis =
+            (uint32_t)((((uintptr_t)(mat ? W1 : W0)) & 3) + (uint64_t)rr * row_bytes + (uint64_t)b * BB) & 3u;
+        return raw + (size_t)rg * RD * 4 + mis;
+    };
+    // 64 rows x 32 chunks and 64 rows x 16 scalar items over 512 threads
+    // (blockDim.x == 512: four chunks and two items each)
+    uint4 v[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int i = threadIdx.x + 512 * k, rg = i >> 5;
+        v[k] = rg < nr ? PfInt<T>::chunk(blk(rg), i & 31) : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int i = threadIdx.x + 512 * k, rg = i >> 5;
+        if (rg < nr) {
+            const int mat = rg >= nper, r = rg - mat * nper;
+            *(uint4 *)((mat ? B1 : B0) + pf_swz(r, i & 31)) = v[k];
         }
+    }
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+        const int i = threadIdx.x + 512 * k, rg = i >> 4;
+        if (rg < nr) PfInt<T>::scalar(blk(rg), i & 15, rs + 16 * rg, bm + 16 * rg);
+    }
+}
+
+// acc (rows m0.., columns n0.. of the tile) += this block's share. rsr, bmr:
+// the scalars of the lane's column n0 + (l & 15); s16: [32][16] sums of the
+// unit's x rows over this block.
+template <int T>
+__device__ __forceinline__ void pf_int_mma(pf_f32x4 &acc, const uint8_t *A, int m0, const uint8_t *B, int n0,
+                                           const float *rsr, const __bf16 *bmr, const float *s16, bool xlo) {
+    const int l = threadIdx.x & 63, r = l & 15, g = l >> 4;
+    if constexpr (!PfInt<T>::per_sub) {
+        pf_f32x4 bacc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int kk = 0; kk < 256; kk += 32) {
+            const uint32_t oa = pf_swz(m0 + r, kk / 8 + g), ob = pf_swz(n0 + r, kk / 8 + g);
+            const pf_bf16x8 a_h = *(const pf_bf16x8 *)(A + oa), a_l = *(const pf_bf16x8 *)(A + PF_TILE + oa);
+            const pf_bf16x8 bq = *(const pf_bf16x8 *)(B + ob);
+            bacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_h, bq, bacc, 0, 0, 0);
+            if (xlo) bacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_l, bq, bacc, 0, 0, 0);
+        }
+        const float d = rsr[0];
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[i] = __builtin_fmaf(d, bacc[i], acc[i]);
+        if constexpr (PfInt<T>::min16) {
+            // A[row r][k = 4 g + i] = S of token m0 + r, sub-block 4 g + i
+            __bf16 sh[4], sl[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) pf_split(s16[(m0 + r) * 16 + 4 * g + i], sh[i], sl[i]);
+            const pf_s16x4 ah = *(const pf_s16x4 *)sh, al = *(const pf_s16x4 *)sl;
+            const pf_s16x4 bv = *(const pf_s16x4 *)(bmr + 4 * g);
+            pf_f32x4 macc = {0.0f, 0.0f, 0.0f, 0.0f};
+            macc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ah, bv, macc, 0, 0, 0);
+            macc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(al, bv, macc, 0, 0, 0);
+            const float dmin = rsr[1];
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc[i] = __builtin_fmaf(-dmin, macc[i], acc[i]);
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int kk = 32 * j;
+            const uint32_t oa = pf_swz(m0 + r, kk / 8 + g), ob = pf_swz(n0 + r, kk / 8 + g);
+            const pf_bf16x8 a_h = *(const pf_bf16x8 *)(A + oa), a_l = *(const pf_bf16x8 *)(A + PF_TILE + oa);
+            const pf_bf16x8 bq = *(const pf_bf16x8 *)(B + ob);
+            pf_f32x4 bacc = {0.0f, 0.0f, 0.0f, 0.0f};
+            bacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_h, bq, bacc, 0, 0, 0);
+            if (xlo) bacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_l, bq, bacc, 0, 0, 0);
+            const float ds = rsr[j], dm = rsr[8 + j];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float *sr = s16 + (m0 + 4 * g + i) * 16 + 2 * j;
+                acc[i] = __builtin_fmaf(ds, bacc[i], acc[i]);
+                acc[i] = __builtin_fmaf(-dm, sr[0] + sr[1], acc[i]);
+            }
+        }
+    }
+}
+
+// ------------------------------------------------------------- gate/up ---
+// Workgroup (rows 32 bx .. 32 bx + 31 of I, unit by), 8 waves: wave w
+// computes the 16x16 tile (pairs 16 ((w >> 1) & 1) .., rows 16 (w & 1) ..)
+// of gate (w < 4) or up (w >= 4); the up waves hand their tile to the gate
+// waves through LDS, which store h[p][row] = silu(gate) * up as bf16 hi / lo
+// for the down kernel. The grid runs a unit's row tiles side by side, so
+// its activation rows stay in L2.
+template <int T>
+__device__ __forceinline__ void pf_gateup_t(uint8_t *smem, const uint8_t *Wg, const uint8_t *Wu, uint64_t row_bytes,
+                                            int64_t nb, int64_t I, const __bf16 *xh, const __bf16 *xl,
+                                            const uint32_t *roff, const int32_t *pair, int nv, int64_t r0,
+                                            __bf16 *__restrict__ hh, __bf16 *__restrict__ hl) {
+    const int w = threadIdx.x >> 6, m0 = 16 * ((w >> 1) & 1), n0 = 16 * (w & 1), up_w = w >> 2;
+    uint8_t *Bg = smem + PF_O_B, *Bu = smem + PF_O_B + 2 * PF_TILE;
+    pf_f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    auto issue = [&](int64_t b) {
+        const int buf = (int)(b & 1);
+        pf_issue_act(xh, xl, roff, b, smem + buf * 2 * PF_TILE);
+        uint8_t *raw = smem + PF_O_RAW + buf * PF_RAW_BYTES;
+        pf_issue_raw<T>(Wg, row_bytes, I, r0, 32, b, raw);
+        pf_issue_raw<T>(Wu, row_bytes, I, r0, 32, b, raw + 32 * ((Fmt<T>::bytes + 6) / 4) * 4);
+    };
+    issue(0);
+    for (int64_t b = 0; b < nb; b++) {
+        __builtin_amdgcn_s_waitcnt(0);   // this wave's DMAs of step b
+        __syncthreads();                 // everyone's, and step b - 1's reads are done
+        if (b + 1 < nb) issue(b + 1);
+        const int buf = (int)(b & 1);
+        pf_dequant_raw<T>(smem + PF_O_RAW + buf * PF_RAW_BYTES, Wg, Wu, 32, row_bytes, I, r0, b, Bg, Bu, PF_TILE);
+        __syncthreads();
+        const uint8_t *A = smem + buf * 2 * PF_TILE;
+        pf_mma256(acc, A, m0, up_w ? Bu : Bg, n0, PF_TILE);
+    }
+    // the up tiles through LDS (the raw areas are free now)
+    __syncthreads();
+    const int l = threadIdx.x & 63;
+    float *xch = (float *)(smem + PF_O_RAW) + (w & 3) * 256 + l * 4;
+    if (up_w) *(pf_f32x4 *)xch = acc;
+    __syncthreads();
+    if (up_w) return;
+    const pf_f32x4 u = *(const pf_f32x4 *)xch;
+    const int64_t row = r0 + n0 + (l & 15);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int m = m0 + 4 * (l >> 4) + i;
+        if (m < nv && row < I) {
+            __bf16 a, c;
+            pf_split(silu_f32(acc[i]) * u[i], a, c);
+            hh[(int64_t)pair[m] * I + row] = a;
+            hl[(int64_t)pair[m] * I + row] = c;
+        }
+    }
+}
+
+// The unit's 16-column sums of x for block b into dst [32][16] f32 (two
+// wave instructions, 4 lanes per row).
+__device__ __forceinline__ void pf_issue_s16(const float *s16, const uint32_t *roff, int64_t b, uint8_t *dst) {
+    const int nw = (int)(blockDim.x >> 6), w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int lane = threadIdx.x & 63;
+    for (int j = w; j < 2; j += nw) {
+        const int row = 16 * j + (lane >> 2), qd = lane & 3;
+        const uint32_t voff = 4u * (roff[row] / 16u + 16u * (uint32_t)b) + 16u * (uint32_t)qd;
+        pf_dma16(s16, voff, pf_lds(dst + 1024 * j));
+    }
+}
+
+// vmcnt(n) for a run-time n (0 .. 63).
+__device__ __forceinline__ void pf_wait_vm(int n) {
+    switch (n) {
+#define PF_W(k) case k: __builtin_amdgcn_s_waitcnt(mq_wc_vm(k)); break;
+        PF_W(0) PF_W(1) PF_W(2) PF_W(3) PF_W(4) PF_W(5) PF_W(6) PF_W(7) PF_W(8) PF_W(9) PF_W(10) PF_W(11)
+        PF_W(12) PF_W(13) PF_W(14) PF_W(15) PF_W(16) PF_W(17) PF_W(18) PF_W(19) PF_W(20) PF_W(21) PF_W(22)
+        PF_W(23) PF_W(24) PF_W(25) PF_W(26) PF_W(27) PF_W(28) PF_W(29) PF_W(30) PF_W(31) PF_W(32) PF_W(33)
+        PF_W(34) PF_W(35) PF_W(36) PF_W(37) PF_W(38) PF_W(39) PF_W(40) PF_W(41) PF_W(42) PF_W(43) PF_W(44)
+        PF_W(45) PF_W(46) PF_W(47)
+#undef PF_W
+    default: __builtin_amdgcn_s_waitcnt(mq_wc_vm(0)); break;
+    }
+}
+// Wave instructions of j = w, w + nw, ... below n.
+__device__ __forceinline__ int pf_share(int n, int w, int nw) { return n > w ? (n - w + nw - 1) / nw : 0; }
+
+// The integer path as an S-stage pipeline: stage s of a ring holds block b's
+// activation tiles (hi, and lo unless x is bf16-representable), raw weight
+// windows and 16-column sums; S - 1 blocks are in flight while one
+// computes (S = 2 .. 4, what the LDS holds for the format).
+// LDS: [codes: 32 KB][row scalars 4 KB][mins 2 KB][stages][row tables].
+// GU: 8 waves, wave w computes the 16x16 tile (pairs 16 ((w >> 1) & 1),
+// rows 16 (w & 1)) of gate (w < 4) or up (w >= 4) over 32 rows of each;
+// the down kernel: rows 16 (w & 3) of the M tile w >> 2 over 64 rows.
+#define PF_I_RS (2 * PF_TILE)
+#define PF_I_BM (PF_I_RS + 64 * 16 * 4)
+#define PF_I_ST (PF_I_BM + 64 * 16 * 2)
+template <int T, bool GU>
+__device__ __forceinline__ void pf_int_pipe(uint8_t *smem, const uint8_t *W0, const uint8_t *W1, uint64_t row_bytes,
+                                            int64_t nb, int64_t rows, const __bf16 *ah, const __bf16 *al,
+                                            const float *s16, const uint32_t *roff, const int32_t *pair, int nv,
+                                            int64_t r0, bool xlo, __bf16 *__restrict__ hh, __bf16 *__restrict__ hl,
+                                            float *__restrict__ yp, int64_t ld_out) {
+    constexpr int RD = (Fmt<T>::bytes + 6) / 4;
+    constexpr bool need_s = GU && (PfInt<T>::min16 || PfInt<T>::per_sub);
+    constexpr int nper = GU ? 32 : 64;
+    const int w = threadIdx.x >> 6, l = threadIdx.x & 63, nw = (int)(blockDim.x >> 6);
+    const int m0 = GU ? 16 * ((w >> 1) & 1) : 16 * (w >> 2), n0 = GU ? 16 * (w & 1) : 16 * (w & 3);
+    const int up_w = GU ? (w >> 2) : 0;
+    uint8_t *B0 = smem, *B1 = smem + PF_TILE;
+    float *rs = (float *)(smem + PF_I_RS);
+    __bf16 *bm = (__bf16 *)(smem + PF_I_BM);
+    const int rg = (GU ? 32 * up_w : 0) + n0 + (l & 15);
+    // stage layout
+    const uint32_t a_bytes = xlo ? 2 * PF_TILE : PF_TILE, raw_bytes = 64 * RD * 4, s_bytes = need_s ? 2048 : 0;
+    const uint32_t st_bytes = a_bytes + raw_bytes + s_bytes;
+    int S = (int)((PF_O_ROFF - PF_I_ST) / st_bytes);
+    S = S < 4 ? S : 4;
+    auto stage = [&](int64_t b) { return smem + PF_I_ST + (uint32_t)(b % S) * st_bytes; };
+    // DMA instructions of this wave per stage
+    const int n_raw = (nper * RD + 63) >> 6;
+    const int per_stage = pf_share(xlo ? 32 : 16, w, nw) + (GU ? 2 : 1) * pf_share(n_raw, w, nw) +
+                          (need_s ? pf_share(2, w, nw) : 0);
+    auto issue = [&](int64_t b) {
+        uint8_t *st = stage(b);
+        pf_issue_act(ah, al, roff, b, st, xlo);
+        uint8_t *raw = st + a_bytes;
+        pf_issue_raw<T>(W0, row_bytes, rows, r0, nper, b, raw);
+        if (GU) pf_issue_raw<T>(W1, row_bytes, rows, r0, nper, b, raw + nper * RD * 4);
+        if constexpr (need_s) pf_issue_s16(s16, roff, b, st + a_bytes + raw_bytes);
+    };
+    for (int64_t b = 0; b < S - 1 && b < nb; b++) issue(b);
+    pf_f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int64_t b = 0; b < nb; b++) {
+        // blocks b + 1 .. min(b + S - 2, nb - 1) may stay in flight
+        const int64_t ahead = (nb - 1 - b) < (S - 2) ? (nb - 1 - b) : (S - 2);
+        pf_wait_vm(per_stage * (int)ahead);
+        __syncthreads();
+        if (b + S - 1 < nb) issue(b + S - 1);
+        uint8_t *st = stage(b);
+        pf_int_build<T>(st + a_bytes, W0, GU ? W1 : nullptr, nper, row_bytes, rows, r0, b, B0, GU ? B1 : nullptr, rs,
+                        bm);
+        __syncthreads();
+        pf_int_mma<T>(acc, st, m0, (GU && up_w) ? B1 : B0, n0, rs + 16 * rg, bm + 16 * rg,
+                      (const float *)(st + a_bytes + raw_bytes), xlo);
+    }
+    if constexpr (GU) {
+        __syncthreads();
+        float *xch = (float *)(smem + PF_I_ST) + (w & 3) * 256 + l * 4;
+        if (up_w) *(pf_f32x4 *)xch = acc;
+        __syncthreads();
+        if (up_w) return;
+        const pf_f32x4 u = *(const pf_f32x4 *)xch;
+        const int64_t row = r0 + n0 + (l & 15);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int m = m0 + 4 * (l >> 4) + i;
+            if (m < nv && row < rows) {
+                __bf16 a, c;
+                pf_split(silu_f32(acc[i]) * u[i], a, c);
+                hh[(int64_t)pair[m] * rows + row] = a;
+                hl[(int64_t)pair[m] * rows + row] = c;
+            }
+        }
+    } else {
+        const int64_t row = r0 + n0 + (l & 15);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int m = m0 + 4 * (l >> 4) + i;
+            if (m < nv && row < rows) yp[(int64_t)pair[m] * ld_out + row] = acc[i];
+        }
+    }
+}
+
+// The unit's rows: roff[m] = element offset of pair m's activation row (rows
+// past nv repeat row 0), pair[m] its pair index.
+__device__ __forceinline__ void pf_unit_rows(const int32_t *pairs, int nv, bool by_token, int32_t n_sel, int64_t ld,
+                                             uint8_t *smem, uint32_t *&roff, int32_t *&pair) {
+    roff = (uint32_t *)(smem + PF_O_ROFF);
+    pair = (int32_t *)(roff + PF_MT);
+    if (threadIdx.x < PF_MT) {
+        const int m = threadIdx.x < (unsigned)nv ? (int)threadIdx.x : 0;
+        const int32_t p = pairs[m];
+        pair[threadIdx.x] = p;
+        roff[threadIdx.x] = (uint32_t)((by_token ? (int64_t)(p / n_sel) : (int64_t)p) * ld);
+    }
+    __syncthreads();
+}
+
+extern "C" __global__ __launch_bounds__(512) void sepia_pf_gateup(
+    PfProj gate, PfProj up, PfProj s_gate, PfProj s_up, int32_t n_routed, int32_t n_sel, int64_t I, int64_t H,
+    const __bf16 *__restrict__ xh, const __bf16 *__restrict__ xl, const float *__restrict__ s16,
+    const uint32_t *__restrict__ lo_any, const int32_t *__restrict__ list, const int32_t *__restrict__ units,
+    const int32_t *__restrict__ n_units, __bf16 *__restrict__ hh, __bf16 *__restrict__ hl) {
+    if ((int32_t)blockIdx.y >= n_units[0]) return;
+    extern __shared__ __attribute__((aligned(16))) uint8_t pf_smem[];
+    uint8_t *smem = pf_smem;
+    const int32_t *un = units + 3 * blockIdx.y;
+    const int32_t e = un[0], nv = un[2];
+    const bool routed = e < n_routed;
+    const PfProj &G = routed ? gate : s_gate, &U = routed ? up : s_up;
+    const int64_t ei = routed ? e : e - n_routed;
+    const uint8_t *wg = G.base + ei * G.stride, *wu = U.base + ei * U.stride;
+    const int64_t r0 = (int64_t)blockIdx.x * 32;
+    uint32_t *roff;
+    int32_t *pair;
+    pf_unit_rows(list + un[1], nv, true, n_sel, H, smem, roff, pair);
+    const bool xlo = __builtin_amdgcn_readfirstlane((int)*lo_any) != 0;
+    switch (G.type) {
+#define PF_GU(TT) case TT: pf_gateup_t<TT>(smem, wg, wu, G.row_bytes, G.n_blocks, I, xh, xl, roff, pair, nv, r0, hh, hl); break;
+#define PF_GI(TT) case TT: pf_int_pipe<TT, true>(smem, wg, wu, G.row_bytes, G.n_blocks, I, xh, xl, s16, roff, pair, nv, r0, xlo, hh, hl, nullptr, 0); break;
+        PF_GI(ST_Q2_K) PF_GI(ST_Q3_K) PF_GI(ST_Q4_K) PF_GU(ST_Q5_K) PF_GU(ST_Q6_K)
+        PF_GU(ST_IQ2_XS) PF_GU(ST_IQ3_XXS) PF_GU(ST_IQ4_XS)
+#undef PF_GU
+#undef PF_GI
+    default: break;
+    }
+}
+
+// ---------------------------------------------------------------- down ---
+// Workgroup (rows 64 bx .. 64 bx + 63 of H, unit by), 8 waves: wave w
+// computes rows 16 (w & 3) .. of the 16-pair M tile w >> 2;
+// yp[p][row] = down . h[p].
+template <int T>
+__device__ __forceinline__ void pf_down_t(uint8_t *smem, const uint8_t *Wd, uint64_t row_bytes, int64_t nb, int64_t H,
+                                          const __bf16 *hh, const __bf16 *hl, const uint32_t *roff, const int32_t *pair,
+                                          int nv, int64_t r0, float *__restrict__ yp) {
+    const int w = threadIdx.x >> 6, n0 = 16 * (w & 3), m0 = 16 * (w >> 2);
+    uint8_t *Bt = smem + PF_O_B;   // [64][256] hi, then lo (2 PF_TILE on)
+    pf_f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    auto issue = [&](int64_t b) {
+        const int buf = (int)(b & 1);
+        pf_issue_act(hh, hl, roff, b, smem + buf * 2 * PF_TILE);
+        pf_issue_raw<T>(Wd, row_bytes, H, r0, 64, b, smem + PF_O_RAW + buf * PF_RAW_BYTES);
+    };
+    issue(0);
+    for (int64_t b = 0; b < nb; b++) {
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (b + 1 < nb) issue(b + 1);
+        const int buf = (int)(b & 1);
+        pf_dequant_raw<T>(smem + PF_O_RAW + buf * PF_RAW_BYTES, Wd, nullptr, 64, row_bytes, H, r0, b, Bt, nullptr,
+                          2 * PF_TILE);
+        __syncthreads();
+        const uint8_t *A = smem + buf * 2 * PF_TILE;
+        pf_mma256(acc, A, m0, Bt, n0, 2 * PF_TILE);
     }
     const int l = threadIdx.x & 63;
     const int64_t row = r0 + n0 + (l & 15);
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const int m = m0 + 4 * (l >> 4) + i;
-        if (m < nv && row < I) h[(int64_t)pairs[m] * I + row] = silu_f32(g[i]) * u[i];
+        if (m < nv && row < H) yp[(int64_t)pair[m] * H + row] = acc[i];
     }
 }
 
-extern "C" __global__ __launch_bounds__(256) void sepia_pf_gateup(
-    PfProj gate, PfProj up, PfProj s_gate, PfProj s_up, int32_t n_routed, int32_t n_sel, int64_t I, int64_t H,
-    const float *__restrict__ x, const int32_t *__restrict__ list, const int32_t *__restrict__ units,
-    const int32_t *__restrict__ n_units, float *__restrict__ h) {
-    if ((int32_t)blockIdx.x >= n_units[0]) return;
-    const int32_t *un = units + 3 * blockIdx.x;
+extern "C" __global__ __launch_bounds__(512) void sepia_pf_down(
+    PfProj down, PfProj s_down, int32_t n_routed, int64_t I, int64_t H, const __bf16 *__restrict__ hh,
+    const __bf16 *__restrict__ hl, const int32_t *__restrict__ list, const int32_t *__restrict__ units,
+    const int32_t *__restrict__ n_units, float *__restrict__ yp) {
+    if ((int32_t)blockIdx.y >= n_units[0]) return;
+    extern __shared__ __attribute__((aligned(16))) uint8_t pf_smem[];
+    uint8_t *smem = pf_smem;
+    const int32_t *un = units + 3 * blockIdx.y;
     const int32_t e = un[0], nv = un[2];
-    const int32_t *pairs = list + un[1];
-    const bool routed = e < n_routed;
-    const PfProj &G = routed ? gate : s_gate, &U = routed ? up : s_up;
-    const int64_t ei = routed ? e : e - n_routed;
-    const uint8_t *wg = G.base + ei * G.stride, *wu = U.base + ei * U.stride;
-    const int64_t r0 = (int64_t)blockIdx.y * 32;
-    __shared__ __attribute__((aligned(16))) PfGuLds S;
-    switch (G.type) {
-#define PF_GU(TT) case TT: pf_gateup_t<TT>(S, wg, wu, G.row_bytes, G.n_blocks, I, H, x, n_sel, pairs, nv, r0, h); break;
-        PF_GU(ST_Q2_K) PF_GU(ST_Q3_K) PF_GU(ST_Q4_K) PF_GU(ST_Q5_K) PF_GU(ST_Q6_K)
-        PF_GU(ST_IQ2_XS) PF_GU(ST_IQ3_XXS) PF_GU(ST_IQ4_XS)
-#undef PF_GU
-    default: break;
-    }
-}
-
-// ---------------------------------------------------------------- down ---
-// Workgroup (unit u, rows 64 by .. 64 by + 63 of H): wave w computes the
-// rows 16 w .. for both 16-pair M tiles; yp[p][row] = down . h[p].
-// LDS of the down workgroup.
-struct PfDnLds {
-    __bf16 ah[32][PF_LD], al[32][PF_LD];
-    __bf16 bh[64][PF_LD], bl[64][PF_LD];
-    uint8_t raw[64 * 212];
-};
-
-template <int T>
-__device__ __forceinline__ void pf_down_t(PfDnLds &S, const uint8_t *Wd, uint64_t row_bytes, int64_t nb, int64_t I,
-                                          int64_t H, const float *__restrict__ h, const int32_t *pairs, int nv,
-                                          int64_t r0, float *__restrict__ yp) {
-    auto &ah = S.ah, &al = S.al;
-    auto &bh = S.bh, &bl = S.bl;
-    uint8_t *raw = S.raw;
-    const int w = threadIdx.x >> 6, n0 = 16 * w;
-    pf_f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
-    auto hrow = [&](int m) { return h + (int64_t)pairs[m] * I; };
-    for (int64_t blk = 0; blk < nb; blk++) {
-        pf_stage_raw<T>(Wd, row_bytes, H, r0, 64, blk, raw);
-        __syncthreads();
-        for (int h4 = 0; h4 < 8; h4 += 4) {
-            pf_stage_act(hrow, nv, blk * 256 + 32 * h4, ah, al);
-            pf_dequant<T>(raw, 64, h4, bh, bl);
-            __syncthreads();
-            pf_mma(acc0, ah, al, 0, bh, bl, n0);
-            pf_mma(acc1, ah, al, 16, bh, bl, n0);
-            __syncthreads();
-        }
-    }
-    const int l = threadIdx.x & 63;
-    const int64_t row = r0 + n0 + (l & 15);
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int m = 4 * (l >> 4) + i;
-        if (m < nv && row < H) yp[(int64_t)pairs[m] * H + row] = acc0[i];
-        if (m + 16 < nv && row < H) yp[(int64_t)pairs[m + 16] * H + row] = acc1[i];
-    }
-}
-
-extern "C" __global__ __launch_bounds__(256) void sepia_pf_down(
-    PfProj down, PfProj s_down, int32_t n_routed, int64_t I, int64_t H, const float *__restrict__ h,
-    const int32_t *__restrict__ list, const int32_t *__restrict__ units, const int32_t *__restrict__ n_units,
-    float *__restrict__ yp) {
-    if ((int32_t)blockIdx.x >= n_units[0]) return;
-    const int32_t *un = units + 3 * blockIdx.x;
-    const int32_t e = un[0], nv = un[2];
-    const int32_t *pairs = list + un[1];
     const bool routed = e < n_routed;
     const PfProj &D = routed ? down : s_down;
     const int64_t ei = routed ? e : e - n_routed;
     const uint8_t *wd = D.base + ei * D.stride;
-    const int64_t r0 = (int64_t)blockIdx.y * 64;
-    __shared__ __attribute__((aligned(16))) PfDnLds S;
+    const int64_t r0 = (int64_t)blockIdx.x * 64;
+    uint32_t *roff;
+    int32_t *pair;
+    pf_unit_rows(list + un[1], nv, false, 1, I, smem, roff, pair);
     switch (D.type) {
-#define PF_DN(TT) case TT: pf_down_t<TT>(S, wd, D.row_bytes, D.n_blocks, I, H, h, pairs, nv, r0, yp); break;
-        PF_DN(ST_Q2_K) PF_DN(ST_Q3_K) PF_DN(ST_Q4_K) PF_DN(ST_Q5_K) PF_DN(ST_Q6_K)
+#define PF_DN(TT) case TT: pf_down_t<TT>(smem, wd, D.row_bytes, D.n_blocks, H, hh, hl, roff, pair, nv, r0, yp); break;
+    case ST_Q3_K: pf_int_pipe<ST_Q3_K, false>(smem, wd, nullptr, D.row_bytes, D.n_blocks, H, hh, hl, nullptr, roff, pair, nv, r0, true, nullptr, nullptr, yp, H); break;
+        PF_DN(ST_Q2_K) PF_DN(ST_Q4_K) PF_DN(ST_Q5_K) PF_DN(ST_Q6_K)
         PF_DN(ST_IQ2_XS) PF_DN(ST_IQ3_XXS) PF_DN(ST_IQ4_XS)
 #undef PF_DN
     default: break;

@@ -58,7 +58,7 @@ enum {
     /* the whole MoE layer / expert FFN in one launch (kernels/mq_fused.h) */
     K_MQ_MOE = K_MQ_DN + 1,
     /* batched prefill MoE layer (kernels/prefill.h) */
-    K_PF_ROUTE = K_MQ_MOE + 1, K_PF_SELECT, K_PF_GROUP, K_PF_GATEUP, K_PF_DOWN, K_PF_COMBINE,
+    K_PF_ROUTE = K_MQ_MOE + 1, K_PF_SELECT, K_PF_GROUP, K_PF_GATEUP, K_PF_DOWN, K_PF_COMBINE, K_PF_SPLIT,
     K_COUNT
 };
 #define FFN_NAMES(p) "sepia_ffn_gateup_" p, "sepia_ffn_gateup_" p "_xp", "sepia_ffn_down_" p
@@ -80,6 +80,7 @@ static const char *const k_names[K_COUNT] = {
     FFN_NAMES("42"), FFN_NAMES("43"), FFN_NAMES("44"),
     "sepia_mq_mv_q2_k", "sepia_mq_mv_q3_k", "sepia_mq_mv_q4_k", "sepia_mq_gateup", "sepia_mq_down", "sepia_mq_moe",
     "sepia_pf_route", "sepia_pf_select", "sepia_pf_group", "sepia_pf_gateup", "sepia_pf_down", "sepia_pf_combine",
+    "sepia_pf_split",
 };
 #undef FFN_NAMES
 
@@ -1312,6 +1313,9 @@ static int mq_ffn_plan(const MoeProj *g, const MoeProj *u, const MoeProj *d, con
     return 1;
 }
 
+/* LDS of the prefill projection kernels (PF_LDS_BYTES in kernels/prefill.h):
+ * the whole 160 KB (tiles, raw-block stages, row tables at the top). */
+#define PF_LDS_BYTES 163840
 /* Formats the prefill projections decode (kernels/prefill.h). */
 static int pf_type_ok(int t) {
     return t == SEPIA_T_Q2_K || t == SEPIA_T_Q3_K || t == 12 || t == 13 || t == 14 || t == 17 || t == 18 || t == 23;
@@ -1365,13 +1369,19 @@ int sepia_gpu_moe_prefill(const SepiaMoeLayerDesc *L, int64_t n_tokens, SepiaGpu
     /* units of <= 32 pairs: routed pairs split over at most n_routed experts,
      * each shared expert takes every token */
     const int64_t umax = (T * tk + 31) / 32 + nr + (int64_t)ns * ((T + 31) / 32) + 1;
-    if (umax > 65535 || (H + 255) / 256 > MAX_GRID) {
+    const int64_t P = T * n_sel;
+    /* the pipelines address activation rows with 32-bit byte offsets */
+    if (umax > 65535 || (H + 255) / 256 > MAX_GRID || (uint64_t)T * H * 2 >= (1ull << 32) ||
+        (uint64_t)P * I * 2 >= (1ull << 32) || (T * H + 255) / 256 > MAX_GRID) {
         LOG("%s: batch too large", op);
+        return 0;
+    }
+    if (H % 256 || I % 256) {
+        LOG("%s: hidden and inter must be multiples of 256", op);
         return 0;
     }
     if (!need_batch(op)) return 0;
 
-    const int64_t P = T * n_sel;
     size_t o = 0;
 #define PF_REGION(name, bytes) const size_t name = o; o += ((size_t)(bytes) + 255) & ~(size_t)255
     PF_REGION(o_logits, T * n_tot * 4);
@@ -1379,14 +1389,19 @@ int sepia_gpu_moe_prefill(const SepiaMoeLayerDesc *L, int64_t n_tokens, SepiaGpu
     PF_REGION(o_w, P * 4);
     PF_REGION(o_list, P * 4);
     PF_REGION(o_units, umax * 12);
-    PF_REGION(o_nu, 4);
-    PF_REGION(o_h, P * I * 4);
+    PF_REGION(o_nu, 8);   /* n_units, then the "x has a nonzero lo part" flag */
+    PF_REGION(o_s16, T * H / 16 * 4);
+    PF_REGION(o_xh, T * H * 2);
+    PF_REGION(o_xl, T * H * 2);
+    PF_REGION(o_hh, P * I * 2);
+    PF_REGION(o_hl, P * I * 2);
     PF_REGION(o_yp, P * H * 4);
 #undef PF_REGION
     uint8_t *s = (uint8_t *)scratch(o, op);
     if (!s) return 0;
-    float *logits = (float *)(s + o_logits), *sel_w = (float *)(s + o_w), *h = (float *)(s + o_h),
-          *yp = (float *)(s + o_yp);
+    float *logits = (float *)(s + o_logits), *sel_w = (float *)(s + o_w), *yp = (float *)(s + o_yp);
+    void *xh = s + o_xh, *xl = s + o_xl, *hh = s + o_hh, *hl = s + o_hl, *s16 = s + o_s16;
+    uint32_t *lo_any = (uint32_t *)(s + o_nu) + 1;
     int32_t *sel_idx = (int32_t *)(s + o_idx), *list = (int32_t *)(s + o_list), *units = (int32_t *)(s + o_units),
             *n_units = (int32_t *)(s + o_nu);
 
@@ -1405,13 +1420,16 @@ int sepia_gpu_moe_prefill(const SepiaMoeLayerDesc *L, int64_t n_tokens, SepiaGpu
     if (!launch2(K_PF_ROUTE, (unsigned)((T + 31) / 32), (unsigned)((n_tot + 31) / 32), 256, 0, a_rt, op)) return 0;
     void *a_sel[] = { &logits, &rb, &nr32, &ns32, &tk32, &rs, &gsc, &sel_idx, &sel_w };
     if (!launch(K_PF_SELECT, (unsigned)T, 64, a_sel, op)) return 0;
-    void *a_grp[] = { &sel_idx, &tt, &nr32, &ns32, &tk32, &list, &units, &n_units };
+    void *a_grp[] = { &sel_idx, &tt, &nr32, &ns32, &tk32, &list, &units, &n_units, &lo_any };
     if (!launch(K_PF_GROUP, 1, 1024, a_grp, op)) return 0;
-    void *a_gu[] = { (void *)&g, (void *)&u, (void *)&sg, (void *)&su, &nr32, &nsel32, &inter, &hid, &x->dev, &list,
-                     &units, &n_units, &h };
-    if (!launch2(K_PF_GATEUP, (unsigned)umax, (unsigned)((I + 31) / 32), 256, 0, a_gu, op)) return 0;
-    void *a_dn[] = { (void *)&d, (void *)&sd, &nr32, &inter, &hid, &h, &list, &units, &n_units, &yp };
-    if (!launch2(K_PF_DOWN, (unsigned)umax, (unsigned)((H + 63) / 64), 256, 0, a_dn, op)) return 0;
+    int64_t nseg = T * H / 16;
+    void *a_sp[] = { &x->dev, &nseg, &xh, &xl, &s16, &lo_any };
+    if (!launch(K_PF_SPLIT, (unsigned)((nseg + 255) / 256), 256, a_sp, op)) return 0;
+    void *a_gu[] = { (void *)&g, (void *)&u, (void *)&sg, (void *)&su, &nr32, &nsel32, &inter, &hid, &xh, &xl, &s16,
+                     &lo_any, &list, &units, &n_units, &hh, &hl };
+    if (!launch2(K_PF_GATEUP, (unsigned)((I + 31) / 32), (unsigned)umax, 512, PF_LDS_BYTES, a_gu, op)) return 0;
+    void *a_dn[] = { (void *)&d, (void *)&sd, &nr32, &inter, &hid, &hh, &hl, &list, &units, &n_units, &yp };
+    if (!launch2(K_PF_DOWN, (unsigned)((H + 63) / 64), (unsigned)umax, 512, PF_LDS_BYTES, a_dn, op)) return 0;
     void *a_cb[] = { &yp, &sel_w, &nsel32, &tt, &hid, &y->dev };
     if (!launch2(K_PF_COMBINE, (unsigned)((H + 255) / 256), (unsigned)T, 256, 0, a_cb, op)) return 0;
     if (route_out) {

@@ -692,16 +692,19 @@ PREFILL_CASES = [
 ]
 
 
+@pytest.mark.parametrize("x_kind", ["bf16", "f32"])
 @pytest.mark.parametrize("shape,types,T", PREFILL_CASES, ids=lambda v: str(v))
-def test_moe_prefill(dev, orc, shape, types, T):
+def test_moe_prefill(dev, orc, shape, types, T, x_kind):
     """Every token of the batch against the oracle's single-token layer (its
-    own routing, near-ties per the reference protocol); two runs bitwise equal."""
+    own routing, near-ties per the reference protocol); two runs bitwise equal.
+    x either bf16-representable (the projections skip the zero lo terms) or
+    full f32."""
     hidden, inter, n_routed, n_shared = shape
     tgu, td, ts = types
     rng = np.random.default_rng(hidden + 7 * T + tgu)
     desc, spec, bufs = make_layer(dev, rng, hidden=hidden, inter=inter, n_routed=n_routed, n_shared=n_shared,
                                   tg=tgu, tu=tgu, td=td, ts=ts)
-    X = bf16_normal(rng, (T, hidden))
+    X = bf16_normal(rng, (T, hidden)) if x_kind == "bf16" else rng.standard_normal((T, hidden)).astype(np.float32)
     y, idx, w = run_prefill(dev, desc, X)
     y2, _, _ = run_prefill(dev, desc, X)
     assert np.array_equal(y.view(np.uint32), y2.view(np.uint32))
