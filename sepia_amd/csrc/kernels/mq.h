@@ -234,6 +234,7 @@ struct MqCtx {
     const uint8_t *lds0;
     uint32_t abase;
     const float *xsb, *gvb;
+    const uint8_t *tab;   // the format's codebook in LDS (IQ formats)
 };
 // A operand of the segment starting at column col of the block (col a
 // multiple of 16): segment col / 16 of the record, 48 bytes each.
@@ -255,6 +256,7 @@ template <int T> struct MQ;
 // Words: 0 = scales, 1..4 = qs, 5 = bytes 68..83 (d | dmin in its .w).
 template <> struct MQ<ST_Q2_K> {
     static constexpr int bytes = 84, W = 6, Wp = 7, sum_sel = 1;
+    static constexpr uint32_t table_bytes = 0;
     __device__ static uint32_t shift(uint32_t) { return 0u; }
     __device__ static uint32_t word(int k) { return k < 5 ? 16u * (uint32_t)k : 68u; }
     // Segment s: s = 0 mask 0x03, s = 1 mask 0x0C (4 q), s = 2 and 3 the same
@@ -316,6 +318,7 @@ template <> struct MQ<ST_Q2_K> {
 // contribution = d * sum_s (sc_s - 32) * ((q + 4 hbit) . x^ - 4 sum x^)_s.
 template <> struct MQ<ST_Q3_K> {
     static constexpr int bytes = 110, W = 7, Wp = 7, sum_sel = 2;   // the -4 is part of the weight: gq
+    static constexpr uint32_t table_bytes = 0;
     __device__ static uint32_t shift(uint32_t boff) { return boff & 3u; }
     __device__ static uint32_t word(int k) { return 16u * (uint32_t)k; }
     __device__ static float block(const uint4 (&w)[W], uint32_t sh, const MqCtx &x) {
@@ -382,6 +385,7 @@ template <> struct MQ<ST_Q3_K> {
 // Words: 0 = d | dmin, scales[12]; 1..8 = qs.
 template <> struct MQ<ST_Q4_K> {
     static constexpr int bytes = 144, W = 9, Wp = 9, sum_sel = 1;
+    static constexpr uint32_t table_bytes = 0;
     __device__ static uint32_t shift(uint32_t) { return 0u; }
     __device__ static uint32_t word(int k) { return 16u * (uint32_t)k; }
     // (scale, min) of sub-block j = 2u + half. For j < 4 both are the low 6
@@ -428,6 +432,120 @@ template <> struct MQ<ST_Q4_K> {
             mn += __builtin_fmaf(mn0, gv[0] + gv[1], mn1 * (gv[2] + gv[3]));
         }
         return __builtin_fmaf(mq_half_lo(w[0].x), acc, -(mq_half_hi(w[0].x) * mn));
+    }
+};
+
+// ------------------------------------------------------------- IQ formats
+// Weights are a codebook entry (small positive bytes), a sign and a scale
+// per 16 (IQ2_XS) or 32 (IQ3_XXS) weights: the signed codebook bytes are the
+// B operand, exact in int8, and the scale multiplies the segment dot. The
+// codebook sits in LDS (MqCtx::tab). Both block sizes leave every other
+// block 2 bytes past a 4-byte boundary: the lane fetches W words from the
+// boundary at or below (shift 0 or 2) and realigns as Q3_K does.
+// Signs: bit j of the sign byte negates weight j (iq_signs adds the parity
+// bit); four bits become four 0x00 / 0xFF byte masks by the spread
+// s * 0x00204081, and a byte is negated as (g ^ m) + (m & 1) (no carries:
+// no codebook byte is 0).
+// The three plane dots of a segment combined in f32: with codebook weights
+// up to 62 the exact integer can pass 2^31 (mq_combine holds it for weights
+// <= 15 only); each term is exact in f32, their sum rounds once or twice.
+__device__ __forceinline__ float mq_combine_f(const mq_v4i &d) {
+    return __builtin_fmaf((float)d[0], 65536.0f, __builtin_fmaf((float)d[1], 256.0f, (float)d[2]));
+}
+__device__ __forceinline__ uint32_t mq_iq_signed(uint32_t g, uint32_t s4) {
+    const uint32_t m = ((s4 * 0x00204081u) & 0x01010101u) * 0xFFu;
+    return (g ^ m) + (m & 0x01010101u);
+}
+
+// IQ2_XS {d@0, u16 qs[32]@2, scales[8]@66} (74 bytes, reference
+// src/quants.c:179-201): 32-weight group ib has 4 entries qs[4 ib + l]
+// (9-bit index into the 512 x 8-byte codebook, 7-bit sign index) and the
+// scale nibble (l < 2: low, else high): w = d (0.5 + nibble) / 4 * entry.
+// Segment sg = 2 ib + half covers entries l = 2 half, 2 half + 1.
+template <> struct MQ<ST_IQ2_XS> {
+    static constexpr int bytes = 74, W = 5, Wp = 5, sum_sel = 1;
+    static constexpr uint32_t table_bytes = 512 * 8;
+    __device__ static uint32_t shift(uint32_t boff) { return boff & 3u; }
+    __device__ static uint32_t word(int k) { return 16u * (uint32_t)k; }
+    __device__ static float block(const uint4 (&w)[W], uint32_t sh, const MqCtx &x) {
+        uint32_t raw[4 * W + 1];
+#pragma unroll
+        for (int k = 0; k < W; k++) {
+            raw[4 * k] = w[k].x;
+            raw[4 * k + 1] = w[k].y;
+            raw[4 * k + 2] = w[k].z;
+            raw[4 * k + 3] = w[k].w;
+        }
+        raw[4 * W] = 0u;
+        auto L = [&](int m) { return __builtin_amdgcn_alignbyte(raw[m + 1], raw[m], sh); };
+        const float d = mq_half_lo(L(0));
+        // scales bytes 66..73: the 8 nibble pairs
+        const uint32_t sc_lo = __builtin_amdgcn_alignbyte(L(17), L(16), 2u), sc_hi = __builtin_amdgcn_alignbyte(L(18), L(17), 2u);
+        float acc = 0.0f;
+#pragma unroll
+        for (int sg = 0; sg < 16; sg++) {
+            const int ib = sg >> 1, half = sg & 1;
+            // u16 entries 4 ib + 2 half and + 1: bytes 2 + 8 ib + 4 half .. + 3
+            const uint32_t e = __builtin_amdgcn_alignbyte(L(2 * ib + half + 1), L(2 * ib + half), 2u);
+            const uint32_t v0 = e & 0xFFFFu, v1 = e >> 16;
+            const uint2 g0 = *(const uint2 *)(x.tab + 8u * (v0 & 511u));
+            const uint2 g1 = *(const uint2 *)(x.tab + 8u * (v1 & 511u));
+            const uint32_t s0 = iq_signs(v0 >> 9), s1 = iq_signs(v1 >> 9);
+            const mq_v4i b = {(int32_t)mq_iq_signed(g0.x, s0 & 15u), (int32_t)mq_iq_signed(g0.y, s0 >> 4),
+                              (int32_t)mq_iq_signed(g1.x, s1 & 15u), (int32_t)mq_iq_signed(g1.y, s1 >> 4)};
+            const mq_v4i D = mq_mfma(mq_a(x, 16 * sg), b);
+            const uint32_t scb = ((ib < 4 ? sc_lo : sc_hi) >> (8 * (ib & 3))) & 0xFFu;
+            const float nib = (float)(half ? (scb >> 4) : (scb & 15u));
+            const float db = d * (0.5f + nib) * 0.25f;
+            acc = __builtin_fmaf(db * x.xsb[sg], mq_combine_f(D), acc);
+        }
+        return acc;
+    }
+};
+
+// IQ3_XXS {d@0, qs[64]@2, scales_signs[32]@66} (98 bytes, reference
+// src/quants.c:203-226): group ib has the word aux = scales_signs[4 ib ..]
+// (4 x 7-bit sign indices, 4-bit scale on top) and bytes qs[8 ib .. 8 ib +
+// 7] (indices into the 256 x 4-byte codebook, two per 8 weights):
+// w = d (0.5 + aux >> 28) / 2 * entry. Segment sg = 2 ib + half covers
+// index bytes 8 ib + 4 half .. + 3 and sign indices 2 half, 2 half + 1.
+template <> struct MQ<ST_IQ3_XXS> {
+    static constexpr int bytes = 98, W = 7, Wp = 7, sum_sel = 1;
+    static constexpr uint32_t table_bytes = 256 * 4;
+    __device__ static uint32_t shift(uint32_t boff) { return boff & 3u; }
+    __device__ static uint32_t word(int k) { return 16u * (uint32_t)k; }
+    __device__ static float block(const uint4 (&w)[W], uint32_t sh, const MqCtx &x) {
+        uint32_t raw[4 * W + 1];
+#pragma unroll
+        for (int k = 0; k < W; k++) {
+            raw[4 * k] = w[k].x;
+            raw[4 * k + 1] = w[k].y;
+            raw[4 * k + 2] = w[k].z;
+            raw[4 * k + 3] = w[k].w;
+        }
+        raw[4 * W] = 0u;
+        auto L = [&](int m) { return __builtin_amdgcn_alignbyte(raw[m + 1], raw[m], sh); };
+        const float d = mq_half_lo(L(0));
+        float acc = 0.0f;
+#pragma unroll
+        for (int ib = 0; ib < 8; ib++) {
+            const uint32_t aux = __builtin_amdgcn_alignbyte(L(17 + ib), L(16 + ib), 2u);
+            const float db = d * (0.5f + (float)(aux >> 28)) * 0.5f;
+#pragma unroll
+            for (int half = 0; half < 2; half++) {
+                const int sg = 2 * ib + half;
+                const uint32_t idx = __builtin_amdgcn_alignbyte(L(2 * ib + half + 1), L(2 * ib + half), 2u);
+                const uint32_t sa = iq_signs((aux >> (14 * half)) & 127u), sb = iq_signs((aux >> (14 * half + 7)) & 127u);
+                const uint32_t *tab = (const uint32_t *)x.tab;
+                const mq_v4i b = {(int32_t)mq_iq_signed(tab[idx & 0xFFu], sa & 15u),
+                                  (int32_t)mq_iq_signed(tab[(idx >> 8) & 0xFFu], sa >> 4),
+                                  (int32_t)mq_iq_signed(tab[(idx >> 16) & 0xFFu], sb & 15u),
+                                  (int32_t)mq_iq_signed(tab[idx >> 24], sb >> 4)};
+                const mq_v4i D = mq_mfma(mq_a(x, 16 * sg), b);
+                acc = __builtin_fmaf(db * x.xsb[sg], mq_combine_f(D), acc);
+            }
+        }
+        return acc;
     }
 };
 
@@ -492,6 +610,7 @@ struct MqWave {
     MqLane L;
     int nqw, Tn;               // quads per item and steps of this wave
     int ik, im, islot;         // issue cursor: item, quad, ring slot
+    const uint8_t *tab = nullptr;   // codebook in LDS (IQ formats)
 
     // Waves first, first + 1, ... share the items as C = (waves - first) / P
     // columns of P parts; waves below `first` and past the last full column
@@ -581,6 +700,7 @@ struct MqWave {
             x.abase = L.a_lane ? it.xoff + MQ_BREC * b + 16u * (uint32_t)L.p : 0u;
             x.xsb = (const float *)(lds0 + it.xoff + mq_xq_planes(n)) + 16u * b;
             x.gvb = x.xsb + MQ<T>::sum_sel * (n >> 4);
+            x.tab = tab;
             acc += MQ<T>::block(w, MQ<T>::shift((uint32_t)MQ<T>::bytes * b), x);
             if (++cm == nqw) {
                 cm = 0;
@@ -604,7 +724,8 @@ __device__ __forceinline__ float mq_red_sum(const float *red, int i, int P, int 
 // ------------------------------------------------------------ matvec ------
 // y = W x for one matrix of nb blocks per row (nb % 4 == 0). Workgroup k
 // owns row groups rg = k, k + G, ... (G = gridDim.x), one item each.
-// LDS: [zero][XQ of x][red: nk x P x 16 f32][raw x, if geo.xraw][rings at geo.orings].
+// LDS: [zero][XQ of x][codebook (IQ formats)][red: nk x P x 16 f32][raw x, if geo.xraw]
+//      [rings at geo.orings].
 template <int T>
 __device__ __forceinline__ void mq_mv(const uint8_t *__restrict__ W, uint64_t row_bytes, int64_t rows, int32_t nb,
                                       const float *__restrict__ x, float *__restrict__ y, MqGeo geo) {
@@ -613,8 +734,14 @@ __device__ __forceinline__ void mq_mv(const uint8_t *__restrict__ W, uint64_t ro
     const int64_t tiles = (rows + 15) >> 4, G = gridDim.x;
     const int nk = tiles > blockIdx.x ? (int)((tiles - blockIdx.x + G - 1) / G) : 0;
     const uint32_t xoff = MQ_ZERO;
-    float *red = (float *)(smem + xoff + mq_xq_bytes(n));
+    uint8_t *tab = smem + xoff + mq_xq_bytes(n);   // codebook (IQ formats), then the row sums
+    float *red = (float *)(tab + MQ<T>::table_bytes);
     uint8_t *rings = smem + geo.orings;
+    if constexpr (T == ST_IQ2_XS) {
+        for (int i = threadIdx.x; i < 512; i += blockDim.x) ((uint64_t *)tab)[i] = c_iq2xs_grid[i];
+    } else if constexpr (T == ST_IQ3_XXS) {
+        for (int i = threadIdx.x; i < 256; i += blockDim.x) ((uint32_t *)tab)[i] = c_iq3xxs_grid[i];
+    }
     auto item_of = [&](int i) {
         MqItem it;
         it.base = W;
@@ -625,7 +752,8 @@ __device__ __forceinline__ void mq_mv(const uint8_t *__restrict__ W, uint64_t ro
         return it;
     };
     MqWave<T, decltype(item_of)> wv(item_of, nk, nb >> 2, n, (uint32_t)row_bytes, geo, rings);
-    wv.start(x, geo, smem, xoff);
+    wv.tab = tab;
+    wv.start(x, geo, smem, xoff);   // its barrier also publishes the codebook
     wv.run(smem, red);
     __syncthreads();
     for (int i = threadIdx.x; i < nk * 16; i += blockDim.x) {

@@ -232,6 +232,8 @@ SEPIA_FFN_PAIR(4, 4, ST_Q4_K, ST_Q4_K)
 SEPIA_MQ_MV(q2_k, ST_Q2_K)
 SEPIA_MQ_MV(q3_k, ST_Q3_K)
 SEPIA_MQ_MV(q4_k, ST_Q4_K)
+SEPIA_MQ_MV(iq2_xs, ST_IQ2_XS)
+SEPIA_MQ_MV(iq3_xxs, ST_IQ3_XXS)
 SEPIA_MQ_GATEUP()
 SEPIA_MQ_DOWN()
 SEPIA_MQ_FUSED()

@@ -53,7 +53,7 @@ enum {
     /* matrix-core matvecs (kernels/mq.h): Q2_K, Q3_K, Q4_K */
     K_MQ_MV = K_FFN_BASE + 27,
     /* matrix-core expert FFN: gate/up, down */
-    K_MQ_GU = K_MQ_MV + 3,
+    K_MQ_GU = K_MQ_MV + 5,
     K_MQ_DN = K_MQ_GU + 1,
     /* the whole MoE layer / expert FFN in one launch (kernels/mq_fused.h) */
     K_MQ_MOE = K_MQ_DN + 1,
@@ -78,7 +78,8 @@ static const char *const k_names[K_COUNT] = {
     "sepia_mv_q2_k", "sepia_mv_q3_k", "sepia_mv_q4_k",
     FFN_NAMES("22"), FFN_NAMES("23"), FFN_NAMES("24"), FFN_NAMES("32"), FFN_NAMES("33"), FFN_NAMES("34"),
     FFN_NAMES("42"), FFN_NAMES("43"), FFN_NAMES("44"),
-    "sepia_mq_mv_q2_k", "sepia_mq_mv_q3_k", "sepia_mq_mv_q4_k", "sepia_mq_gateup", "sepia_mq_down", "sepia_mq_moe",
+    "sepia_mq_mv_q2_k", "sepia_mq_mv_q3_k", "sepia_mq_mv_q4_k", "sepia_mq_mv_iq2_xs", "sepia_mq_mv_iq3_xxs",
+    "sepia_mq_gateup", "sepia_mq_down", "sepia_mq_moe",
     "sepia_pf_route", "sepia_pf_select", "sepia_pf_group", "sepia_pf_gateup", "sepia_pf_down", "sepia_pf_combine",
     "sepia_pf_split",
 };
@@ -959,8 +960,20 @@ typedef struct {
 #define MQ_SEL_BYTES 512            /* the gate/up kernel's selection area in LDS */
 #define MQ_XDMA_GAIN 40             /* mq_geo: cost units the vector's LDS DMA saves (measured ~2 us a launch) */
 static size_t mq_xq_bytes(int64_t n) { return (size_t)(n / 256) * 832 + 3 * (size_t)(n / 16) * 4; }
-static int mq_code(int t) { return t == SEPIA_T_Q2_K ? 0 : (t == SEPIA_T_Q3_K ? 1 : (t == 12 ? 2 : -1)); }
-static const int k_mq_words[3] = { 7, 7, 9 };   /* padded words per lane (MQ<T>::Wp) */
+/* matrix-core format codes: 0..2 the K-quants (matvec and the FFN kernels),
+ * 3..4 IQ2_XS and IQ3_XXS (matvec) */
+static int mq_code(int t) {
+    switch (t) {
+    case SEPIA_T_Q2_K: return 0;
+    case SEPIA_T_Q3_K: return 1;
+    case 12: return 2;
+    case 17: return 3;
+    case 18: return 4;
+    default: return -1;
+    }
+}
+static const int k_mq_words[5] = { 7, 7, 9, 5, 7 };   /* padded words per lane (MQ<T>::Wp) */
+static const size_t k_mq_table[5] = { 0, 0, 0, 4096, 1024 };   /* LDS codebook bytes (MQ<T>::table_bytes) */
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 /* Geometry for workgroups of n_items items of nq quads; mc is the format
@@ -1034,7 +1047,7 @@ static int mq_plan(int type, int64_t n_blocks, int64_t rows, uintptr_t base, uin
     const int64_t tiles = (rows + 15) / 16;
     const int64_t per = (tiles + MQ_CUS - 1) / MQ_CUS;     /* row groups per workgroup */
     *grid = (unsigned)((tiles + per - 1) / per);
-    if (!mq_geo(mc, k_mq_words[mc], per, n_blocks / 4, MQ_ZERO + mq_xq_bytes(256 * n_blocks),
+    if (!mq_geo(mc, k_mq_words[mc], per, n_blocks / 4, MQ_ZERO + mq_xq_bytes(256 * n_blocks) + k_mq_table[mc],
                 (size_t)1024 * n_blocks, threads, geo, lds))
         return -1;
     return K_MQ_MV + mc;
@@ -1253,7 +1266,8 @@ typedef struct {
 } MqFfnPlan;
 #define MQ_DN_CNT_OFF 64            /* first down arrival counter (u32 index in the counter region) */
 static int mq_proj_ok(const MoeProj *p, int64_t rows) {
-    return mq_shape_ok(p->type, p->n_blocks, rows, (uintptr_t)p->base, p->row_bytes) && p->stride % 4 == 0;
+    return mq_code(p->type) <= 2 && mq_shape_ok(p->type, p->n_blocks, rows, (uintptr_t)p->base, p->row_bytes) &&
+           p->stride % 4 == 0;
 }
 /* Workgroups per slot for slots of byte weights br (routed) and bs (shared):
  * at most MQ_CUS in all (unless one per slot is already more), at most

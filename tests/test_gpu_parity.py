@@ -289,7 +289,8 @@ def mq_geometry(dev, request):
         L.sepia_hip_set_option(k.encode(), 0)
 
 
-MQ_NAMES = {10: "sepia_mq_mv_q2_k", 11: "sepia_mq_mv_q3_k", 12: "sepia_mq_mv_q4_k"}
+MQ_NAMES = {10: "sepia_mq_mv_q2_k", 11: "sepia_mq_mv_q3_k", 12: "sepia_mq_mv_q4_k", 17: "sepia_mq_mv_iq2_xs",
+            18: "sepia_mq_mv_iq3_xxs"}
 # (type, rows, cols, (P, C, S)): several items per workgroup (12288 and 8200
 # rows), long rows (12288 columns: 12 quads), partial row groups, every ring
 # depth, parts that do not divide the quads.
@@ -298,6 +299,8 @@ MQ_GEOMETRIES = [
     (10, 12288, 2048, (1, 3, 2)), (10, 12288, 2048, (2, 2, 3)),
     (11, 70, 12288, (1, 1, 3)), (11, 70, 12288, (5, 1, 2)), (11, 70, 12288, (3, 1, 1)),
     (12, 8200, 4096, (1, 1, 2)), (12, 8200, 4096, (4, 3, 1)), (12, 8200, 4096, (3, 2, 2)),
+    (17, 12288, 2048, (1, 2, 2)), (17, 70, 12288, (3, 1, 3)), (17, 6144, 6144, (2, 2, 1)),
+    (18, 12288, 2048, (2, 1, 2)), (18, 70, 12288, (4, 1, 2)), (18, 6144, 6144, (1, 2, 3)),
 ]
 
 
@@ -463,7 +466,9 @@ def mq_vector(dev, request):
 
 @pytest.mark.parametrize("mq_vector", [1, 2], indirect=True, ids=["global", "dma"])
 @pytest.mark.parametrize("t,out_dim,in_dim", [(12, 4096, 4096), (10, 3072, 6144), (11, 6144, 3072),
-                                              (10, 12288, 2048), (12, 40, 12288)], ids=lambda v: str(v))
+                                              (10, 12288, 2048), (12, 40, 12288), (17, 6144, 6144),
+                                              (18, 6144, 6144), (18, 257, 3072), (17, 33, 1024)],
+                         ids=lambda v: str(v))
 def test_matvec_mq_vector_paths(dev, orc, mq_vector, t, out_dim, in_dim):
     with Launches(dev) as n:
         check_matvec(dev, orc, t, out_dim, in_dim, seed=out_dim + in_dim + t)
