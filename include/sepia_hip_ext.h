@@ -102,14 +102,18 @@ void *sepia_hip_stream(void);
 
 /* Kernel-selection switches for tests and tuning (returns 1 if name and
  * value are known):
- *   "mq" 1/0      the matrix-core kernels for Q2_K/Q3_K/Q4_K (default 1);
+ *   "mq" 1/0      the matrix-core kernels for Q2_K/Q3_K/Q4_K and, in the
+ *                 matvec, IQ2_XS/IQ3_XXS (default 1);
  *   "fuse" 0/1    the MoE layer and the expert FFN as one launch of
  *                 sepia_mq_moe instead of router + gate/up + down (default 0);
  *   "tile" 1/0    the tile kernels where the matrix-core ones do not apply
  *                 (0 = the generic one-wave-per-row kernels);
  *   "tile_t" 0..  automatic or forced row steps per tile workgroup;
  *   "mq_p", "mq_c", "mq_s" 0..  automatic or forced matrix-core geometry
- *                 (parts per item, items side by side, ring stages). */
+ *                 (parts per item, items side by side, ring stages);
+ *   "mq_x" 0..2   how matrix-core kernels fetch their vector: 0 = the
+ *                 planner's choice, 1 = loads from global memory, 2 = LDS
+ *                 DMA issued ahead of the weight prologue. */
 int sepia_hip_set_option(const char *name, int value);
 
 #ifdef __cplusplus
