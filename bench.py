@@ -239,8 +239,8 @@ def run_c2(B, warmup, steps, cpu_seconds):
     e_last = (warmup + steps - 1) % NE
     y_graph = B.fetch(y, 0, H * 4).view(np.float32)
     step_bytes = gb + ub + db + H * 4 + I * 4 + H * 4
-    K_FUSED, K_GU, K_DN = "sepia_mq_moe", "sepia_mq_gateup", "sepia_mq_down"
-    kms = B.kernel_ms(step, min(steps, 4 * NE), [K_FUSED, K_GU, K_DN])
+    K_FLOW, K_FUSED, K_GU, K_DN = "sepia_mq_ffn", "sepia_mq_moe", "sepia_mq_gateup", "sepia_mq_down"
+    kms = B.kernel_ms(step, min(steps, 4 * NE), [K_FLOW, K_FUSED, K_GU, K_DN])
     gu_bytes = gb + ub + H * 4 + I * 4
     dn_bytes = db + I * 4 + H * 4
     B.dev.run(L.sepia_gpu_expert_ffn, *ref, NE, e_last, H, I, xs[0], y)
@@ -265,10 +265,11 @@ def run_c2(B, warmup, steps, cpu_seconds):
                         cpu_seconds / 4, 1000)
     for b in bufs + xs + [y]:
         B.dev.free(b)
-    if K_FUSED in kms:      # the whole FFN in one launch: its bytes are the step's
-        roof = dict(bound="hbm", kernel=K_FUSED, achieved=step_bytes / (kms[K_FUSED] * 1e-3) / 1e9,
+    one = [k for k in (K_FLOW, K_FUSED) if k in kms]
+    if one:                 # the whole FFN in one launch: its bytes are the step's
+        roof = dict(bound="hbm", kernel=one[0], achieved=step_bytes / (kms[one[0]] * 1e-3) / 1e9,
                     peak=HBM_PEAK_GBS, unit="GB/s", bytes_per_launch=step_bytes,
-                    avg_launch_us=kms[K_FUSED] * 1e3)
+                    avg_launch_us=kms[one[0]] * 1e3)
     else:
         roof = dict(bound="hbm", kernel=K_GU, achieved=gu_bytes / (kms[K_GU] * 1e-3) / 1e9, peak=HBM_PEAK_GBS,
                     unit="GB/s", bytes_per_launch=gu_bytes, avg_launch_us=kms[K_GU] * 1e3,
@@ -504,6 +505,9 @@ def main():
                     help="run one configuration (profiling runs; 'copy': the library's f32 copy kernel over "
                          "256 MiB, the reference for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE); default: all")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--flow", type=int, choices=[0, 1], default=None,
+                    help="library option 'flow': the expert FFN as one launch of gate/up and down waves "
+                         "(default: library default)")
     ap.add_argument("--fuse", type=int, choices=[0, 1], default=None,
                     help="library option 'fuse': the MoE layer / expert FFN as one launch (default: library default)")
     args = ap.parse_args()
@@ -519,6 +523,8 @@ def main():
     log("device", dev.name)
     if args.fuse is not None and dev.L.sepia_hip_set_option(b"fuse", args.fuse) != 1:
         raise RuntimeError("option fuse not accepted")
+    if args.flow is not None and dev.L.sepia_hip_set_option(b"flow", args.flow) != 1:
+        raise RuntimeError("option flow not accepted")
     extra = {}
     res = None
     t0 = time.time()

@@ -111,9 +111,15 @@ void *sepia_hip_stream(void);
  *   "tile_t" 0..  automatic or forced row steps per tile workgroup;
  *   "mq_p", "mq_c", "mq_s" 0..  automatic or forced matrix-core geometry
  *                 (parts per item, items side by side, ring stages);
- *   "mq_x" 0..2   how matrix-core kernels fetch their vector: 0 = the
+ *   "mq_x" 0..3   how matrix-core kernels fetch their vector: 0 = the
  *                 planner's choice, 1 = loads from global memory, 2 = LDS
- *                 DMA issued ahead of the weight prologue. */
+ *                 DMA issued ahead of the weight prologue, 3 = converter
+ *                 waves (DMA into the XQ place, converted there while the
+ *                 other waves decode their first step);
+ *   "flow" 0/1    the expert FFN as one launch of sepia_mq_ffn, gate/up
+ *                 and down waves side by side (default 0);
+ *   "flow_delay"  ticks (10 ns) the flow launch's workgroups without
+ *                 gate/up rows hold their down weights back (default 250). */
 int sepia_hip_set_option(const char *name, int value);
 
 #ifdef __cplusplus

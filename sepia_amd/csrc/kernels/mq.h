@@ -204,18 +204,14 @@ __device__ __forceinline__ void mq_wait_stages(int n) {
 // ------------------------------------------------------- weight blocks ----
 __device__ __forceinline__ float mq_half_lo(uint32_t v) { return f16_bits_to_f32(v & 0xFFFFu); }
 __device__ __forceinline__ float mq_half_hi(uint32_t v) { return f16_bits_to_f32(v >> 16); }
-// Byte b of v as a float: one v_cvt_f32_ubyte<b> (the compiler otherwise
-// folds a preceding mask into a v_bfe and converts byte 0). The operand is
-// an ordinary VALU result, never an MFMA result (inline asm is invisible to
-// the compiler's MFMA hazard recognizer).
+// Byte B of v as a float, in plain C (one v_cvt_f32_ubyte<B>, or a bit-field
+// extract and a convert when the compiler folds a mask into it). Never
+// inline asm here: the compiler's hazard recognizer cannot see what an asm
+// statement writes, and it placed such converts onto the operand and result
+// registers of MFMAs still in flight.
 template <int B>
 __device__ __forceinline__ float mq_ubyte(uint32_t v) {
-    float r;
-    if constexpr (B == 0) asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(r) : "v"(v));
-    else if constexpr (B == 1) asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(r) : "v"(v));
-    else if constexpr (B == 2) asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(r) : "v"(v));
-    else asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(r) : "v"(v));
-    return r;
+    return (float)((v >> (8 * B)) & 0xFFu);
 }
 // (p0 << 16) + (p1 << 8) + p2 of one segment's three plane dots: the exact
 // integer sum of w * q (|.| < 2^31 for 16 weights <= 15 and |q| <= QMAX + 1).
@@ -257,6 +253,7 @@ template <int T> struct MQ;
 template <> struct MQ<ST_Q2_K> {
     static constexpr int bytes = 84, W = 6, Wp = 7, sum_sel = 1;
     static constexpr uint32_t table_bytes = 0;
+    static constexpr bool has_pre = true;
     __device__ static uint32_t shift(uint32_t) { return 0u; }
     __device__ static uint32_t word(int k) { return k < 5 ? 16u * (uint32_t)k : 68u; }
     // Segment s: s = 0 mask 0x03, s = 1 mask 0x0C (4 q), s = 2 and 3 the same
@@ -300,6 +297,60 @@ template <> struct MQ<ST_Q2_K> {
         }
         return __builtin_fmaf(mq_half_lo(w[5].w), acc, -(mq_half_hi(w[5].w) * mn));
     }
+    // block() in two halves: pre() needs only the weights (B operands and
+    // scales), post() the vector; the same operations in the same order.
+    struct Pre {
+        mq_v4i b[16];
+        uint32_t scw[4], mw[4];
+        uint32_t dd;
+    };
+    __device__ static Pre pre(const uint4 (&w)[W], uint32_t) {
+        Pre r;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const uint32_t s_lo = h ? w[0].z : w[0].x, s_hi = h ? w[0].w : w[0].y;
+#pragma unroll
+            for (int up = 0; up < 2; up++) {
+                const uint4 q = w[1 + 2 * h + up];
+#pragma unroll
+                for (int s = 0; s < 4; s++) r.b[4 * (2 * h + up) + s] = bop(q, s);
+                const uint32_t sb = __builtin_amdgcn_perm(s_hi, s_lo, up ? 0x07050301u : 0x06040200u);
+                r.scw[2 * h + up] = sb & 0x0F0F0F0Fu;
+                r.mw[2 * h + up] = (sb >> 4) & 0x0F0F0F0Fu;
+            }
+        }
+        r.dd = w[5].w;
+        return r;
+    }
+    __device__ static float post(const Pre &r, const MqCtx &x) {
+        float acc = 0.0f, mn = 0.0f;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            float xs[8], gv[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                xs[i] = x.xsb[8 * h + i];
+                gv[i] = x.gvb[8 * h + i];
+            }
+#pragma unroll
+            for (int up = 0; up < 2; up++) {
+                mq_v4i D[4];
+#pragma unroll
+                for (int s = 0; s < 4; s++) D[s] = mq_mfma(mq_a(x, 128 * h + 32 * s + 16 * up), r.b[4 * (2 * h + up) + s]);
+                const uint32_t scw = r.scw[2 * h + up], mw = r.mw[2 * h + up];
+                const float a1 = __builtin_fmaf(mq_combine(D[0]), mq_ubyte<0>(scw) * xs[up],
+                                                mq_combine(D[2]) * (mq_ubyte<2>(scw) * xs[4 + up]));
+                const float a4 = __builtin_fmaf(mq_combine(D[1]), mq_ubyte<1>(scw) * xs[2 + up],
+                                                mq_combine(D[3]) * (mq_ubyte<3>(scw) * xs[6 + up]));
+                acc += __builtin_fmaf(0.25f, a4, a1);
+                float m = mq_ubyte<0>(mw) * gv[up];
+                m = __builtin_fmaf(mq_ubyte<1>(mw), gv[2 + up], m);
+                m = __builtin_fmaf(mq_ubyte<2>(mw), gv[4 + up], m);
+                mn += __builtin_fmaf(mq_ubyte<3>(mw), gv[6 + up], m);
+            }
+        }
+        return __builtin_fmaf(mq_half_lo(r.dd), acc, -(mq_half_hi(r.dd) * mn));
+    }
 };
 
 // ---------------------------------------------------------------- Q3_K
@@ -319,6 +370,7 @@ template <> struct MQ<ST_Q2_K> {
 template <> struct MQ<ST_Q3_K> {
     static constexpr int bytes = 110, W = 7, Wp = 7, sum_sel = 2;   // the -4 is part of the weight: gq
     static constexpr uint32_t table_bytes = 0;
+    static constexpr bool has_pre = true;
     __device__ static uint32_t shift(uint32_t boff) { return boff & 3u; }
     __device__ static uint32_t word(int k) { return 16u * (uint32_t)k; }
     __device__ static float block(const uint4 (&w)[W], uint32_t sh, const MqCtx &x) {
@@ -373,6 +425,77 @@ template <> struct MQ<ST_Q3_K> {
         }
         return mq_half_lo(c3) * acc;
     }
+    // block() in two halves (see MQ<ST_Q2_K>::Pre).
+    struct Pre {
+        mq_v4i b[16];
+        float sc[16];
+        uint32_t dd;
+    };
+    __device__ static Pre pre(const uint4 (&w)[W], uint32_t sh) {
+        uint32_t raw[4 * W + 1];
+#pragma unroll
+        for (int k = 0; k < W; k++) {
+            raw[4 * k] = w[k].x;
+            raw[4 * k + 1] = w[k].y;
+            raw[4 * k + 2] = w[k].z;
+            raw[4 * k + 3] = w[k].w;
+        }
+        raw[4 * W] = 0u;
+        auto L = [&](int m) { return __builtin_amdgcn_alignbyte(raw[m + 1], raw[m], sh); };
+        const uint32_t c0 = L(24), c1 = L(25), c2 = L(26), c3 = L(27);
+        Pre r;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+#pragma unroll
+            for (int up = 0; up < 2; up++) {
+                const int u = 2 * h + up;
+#pragma unroll
+                for (int s = 0; s < 4; s++) {
+#pragma unroll
+                    for (int t = 0; t < 4; t++) {
+                        const uint32_t qw = L(8 + 4 * u + t), hw = L(4 * up + t);
+                        const uint32_t hf = h ? (hw >> 2) : (hw << 2);
+                        r.b[4 * u + s][t] = (int32_t)(((qw >> (2 * s)) & 0x03030303u) | ((hf >> s) & 0x04040404u));
+                    }
+                }
+                const uint32_t base = 8u * (uint32_t)up + 4u * (uint32_t)h;
+#pragma unroll
+                for (int s = 0; s < 4; s++) {
+                    const uint32_t lw = (s < 2) ? c0 : c1;
+                    const uint32_t low4 = __builtin_amdgcn_ubfe(lw, 16u * (s & 1) + base, 4u);
+                    const uint32_t top2 = __builtin_amdgcn_ubfe(c2, 16u * (s & 1) + 2u * (s >> 1) + base, 2u);
+                    r.sc[4 * u + s] = (float)((int32_t)(low4 | (top2 << 4)) - 32);
+                }
+            }
+        }
+        r.dd = c3;
+        return r;
+    }
+    __device__ static float post(const Pre &r, const MqCtx &x) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            float xs[8], gv[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                xs[i] = x.xsb[8 * h + i];
+                gv[i] = x.gvb[8 * h + i];
+            }
+#pragma unroll
+            for (int up = 0; up < 2; up++) {
+                const int u = 2 * h + up;
+                mq_v4i D[4];
+#pragma unroll
+                for (int s = 0; s < 4; s++) D[s] = mq_mfma(mq_a(x, 128 * h + 32 * s + 16 * up), r.b[4 * u + s]);
+#pragma unroll
+                for (int s = 0; s < 4; s++) {
+                    const int li = 2 * s + up;
+                    acc = __builtin_fmaf(r.sc[4 * u + s], __builtin_fmaf(-4.0f, gv[li], mq_combine(D[s]) * xs[li]), acc);
+                }
+            }
+        }
+        return mq_half_lo(r.dd) * acc;
+    }
 };
 
 // ---------------------------------------------------------------- Q4_K
@@ -386,6 +509,7 @@ template <> struct MQ<ST_Q3_K> {
 template <> struct MQ<ST_Q4_K> {
     static constexpr int bytes = 144, W = 9, Wp = 9, sum_sel = 1;
     static constexpr uint32_t table_bytes = 0;
+    static constexpr bool has_pre = true;
     __device__ static uint32_t shift(uint32_t) { return 0u; }
     __device__ static uint32_t word(int k) { return 16u * (uint32_t)k; }
     // (scale, min) of sub-block j = 2u + half. For j < 4 both are the low 6
@@ -433,6 +557,50 @@ template <> struct MQ<ST_Q4_K> {
         }
         return __builtin_fmaf(mq_half_lo(w[0].x), acc, -(mq_half_hi(w[0].x) * mn));
     }
+    // block() in two halves (see MQ<ST_Q2_K>::Pre).
+    struct Pre {
+        mq_v4i b[16];
+        float sc[8], mn[8];
+        uint32_t dd;
+    };
+    __device__ static Pre pre(const uint4 (&w)[W], uint32_t) {
+        Pre r;
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const uint4 a = w[1 + 2 * u], b = w[2 + 2 * u];
+#pragma unroll
+            for (int s = 0; s < 4; s++) {
+                const uint4 q = (s & 1) ? b : a;
+                const uint32_t sh = (s & 2) ? 4u : 0u, m = 0x0F0F0F0Fu;
+                r.b[4 * u + s] = mq_v4i{(int32_t)((q.x >> sh) & m), (int32_t)((q.y >> sh) & m),
+                                        (int32_t)((q.z >> sh) & m), (int32_t)((q.w >> sh) & m)};
+            }
+            scale_min(w[0], u, 0, r.sc[2 * u], r.mn[2 * u]);
+            scale_min(w[0], u, 1, r.sc[2 * u + 1], r.mn[2 * u + 1]);
+        }
+        r.dd = w[0].x;
+        return r;
+    }
+    __device__ static float post(const Pre &r, const MqCtx &x) {
+        float acc = 0.0f, mn = 0.0f;
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            mq_v4i D[4];
+#pragma unroll
+            for (int s = 0; s < 4; s++) D[s] = mq_mfma(mq_a(x, 64 * u + 16 * s), r.b[4 * u + s]);
+            float xs[4], gv[4];
+#pragma unroll
+            for (int s = 0; s < 4; s++) {
+                xs[s] = x.xsb[4 * u + s];
+                gv[s] = x.gvb[4 * u + s];
+            }
+            const float sub0 = __builtin_fmaf(mq_combine(D[0]), xs[0], mq_combine(D[1]) * xs[1]);
+            const float sub1 = __builtin_fmaf(mq_combine(D[2]), xs[2], mq_combine(D[3]) * xs[3]);
+            acc += __builtin_fmaf(r.sc[2 * u], sub0, r.sc[2 * u + 1] * sub1);
+            mn += __builtin_fmaf(r.mn[2 * u], gv[0] + gv[1], r.mn[2 * u + 1] * (gv[2] + gv[3]));
+        }
+        return __builtin_fmaf(mq_half_lo(r.dd), acc, -(mq_half_hi(r.dd) * mn));
+    }
 };
 
 // ------------------------------------------------------------- IQ formats
@@ -465,6 +633,7 @@ __device__ __forceinline__ uint32_t mq_iq_signed(uint32_t g, uint32_t s4) {
 template <> struct MQ<ST_IQ2_XS> {
     static constexpr int bytes = 74, W = 5, Wp = 5, sum_sel = 1;
     static constexpr uint32_t table_bytes = 512 * 8;
+    static constexpr bool has_pre = false;
     __device__ static uint32_t shift(uint32_t boff) { return boff & 3u; }
     __device__ static uint32_t word(int k) { return 16u * (uint32_t)k; }
     __device__ static float block(const uint4 (&w)[W], uint32_t sh, const MqCtx &x) {
@@ -512,6 +681,7 @@ template <> struct MQ<ST_IQ2_XS> {
 template <> struct MQ<ST_IQ3_XXS> {
     static constexpr int bytes = 98, W = 7, Wp = 7, sum_sel = 1;
     static constexpr uint32_t table_bytes = 256 * 4;
+    static constexpr bool has_pre = false;
     __device__ static uint32_t shift(uint32_t boff) { return boff & 3u; }
     __device__ static uint32_t word(int k) { return 16u * (uint32_t)k; }
     __device__ static float block(const uint4 (&w)[W], uint32_t sh, const MqCtx &x) {
@@ -564,6 +734,144 @@ __device__ __forceinline__ MqLane mq_lane() {
 }
 __device__ __forceinline__ int mq_wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
 
+// ------------------------------------------- vector by converter waves ----
+// Wait bounds in s_memrealtime ticks (100 MHz): 2 s (a grid barrier, an LDS
+// counter), twice that for the LDS flag that follows a grid barrier.
+#define MQ_WAIT_TICKS 200000000ull
+
+// Wait until the LDS counter c reaches target (acquire), bounded in time.
+__device__ __forceinline__ void mq_waves_wait(uint32_t *c, uint32_t target, int lane, uint32_t *err) {
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+    while (__hip_atomic_load(c, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < target) {
+        __builtin_amdgcn_s_sleep(1);
+        if (__builtin_amdgcn_s_memrealtime() - t0 > MQ_WAIT_TICKS) {
+            if (lane == 0 && err) __hip_atomic_store(err, 5u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            return;
+        }
+    }
+}
+
+// Quad (4-lane) exchanges by DPP: lane l reads lane l ^ 1, l ^ 2.
+__device__ __forceinline__ float mq_quad_x1(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float mq_quad_x2(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+}
+__device__ __forceinline__ int mq_quad_x1i(int v) { return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false); }
+__device__ __forceinline__ int mq_quad_x2i(int v) { return __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false); }
+
+// XQ of one 16-column segment by a quad: lane j holds columns 4j .. 4j + 3
+// (a), gets word j of each digit plane (p0, p1 + 128, p2 + 128 bytes) and
+// the segment's xs, gs and gq. The same values as xq_segment but for the
+// order of the gs sum.
+struct XqQuad {
+    uint32_t p0, p1, p2;
+    float xs, gs, gq;
+};
+__device__ __forceinline__ XqQuad mq_xq_quad(const float (&a)[4]) {
+    float m = fmaxf(fmaxf(fabsf(a[0]), fabsf(a[1])), fmaxf(fabsf(a[2]), fabsf(a[3])));
+    m = fmaxf(m, mq_quad_x1(m));
+    m = fmaxf(m, mq_quad_x2(m));
+    const float inv = (m > 0.0f) ? MQ_QMAX * __builtin_amdgcn_rcpf(m) : 0.0f;
+    XqQuad r;
+    r.xs = m * (1.0f / MQ_QMAX);
+    uint32_t q[4];
+    int32_t qs = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int32_t v = mq_round(a[i] * inv);
+        qs += v;
+        q[i] = (uint32_t)v + 0x8080u;
+    }
+    qs += mq_quad_x1i(qs);
+    qs += mq_quad_x2i(qs);
+    float sum = (a[0] + a[1]) + (a[2] + a[3]);
+    sum += mq_quad_x1(sum);
+    sum += mq_quad_x2(sum);
+    const uint32_t t01 = __builtin_amdgcn_perm(q[1], q[0], 0x05010400u);
+    const uint32_t t23 = __builtin_amdgcn_perm(q[3], q[2], 0x05010400u);
+    const uint32_t u01 = __builtin_amdgcn_perm(q[1], q[0], 0x06020602u);
+    const uint32_t u23 = __builtin_amdgcn_perm(q[3], q[2], 0x06020602u);
+    r.p0 = __builtin_amdgcn_perm(u23, u01, 0x05040100u);
+    r.p1 = __builtin_amdgcn_perm(t23, t01, 0x07060302u) ^ 0x80808080u;
+    r.p2 = __builtin_amdgcn_perm(t23, t01, 0x05040100u) ^ 0x80808080u;
+    r.gs = sum;
+    r.gq = r.xs * (float)qs;
+    return r;
+}
+
+// Waves first .. first + count - 1 of the workgroup wait for one another:
+// arrival k of each (k = 1, 2, ...) completes when the counter at c
+// reaches k * count. Bounded in time (error flag 5 on expiry).
+__device__ __forceinline__ void mq_waves_sync(uint32_t *c, uint32_t target, int lane, uint32_t *err) {
+    if (lane == 0) __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+    mq_waves_wait(c, target, lane, err);
+}
+
+// The n-float vector x becomes its XQ form at LDS offset xoff, in place,
+// by the waves of threads first .. first + count - 1 (count a multiple of
+// 64) alone: they DMA x (1 KB a wave instruction), wait for their own
+// DMAs, then four lanes per 16-column segment -- lane j of a quad holds
+// columns 4j .. 4j + 3 and writes word j of each digit plane, the segment's
+// max and sums by quad exchanges -- in up to MQ_XQP passes of count / 4
+// segments (n / 16 <= MQ_XQP count / 4). The same XQ as xq_segment but for
+// the order of the gs sum. Every float is read before any byte is written.
+// Three arrivals at the counter c (landed, read, written): other waves may
+// use the XQ vector once it reaches 3 (count / 64). Clears the zero area.
+#define MQ_XQP 8
+__device__ __forceinline__ void mq_xq_dma_by(const float *src, int n, uint8_t *lds0, uint32_t xoff, int first,
+                                             int count) {
+    const int nw = count >> 6, w = mq_wave_id() - (first >> 6);
+    const uint32_t lane = threadIdx.x & 63, raw = mq_lds_addr(lds0 + xoff);
+    // the conversion gates every gate/up wave: these waves go first on the
+    // SIMDs until it is written (back to 0 at its end)
+    __builtin_amdgcn_s_setprio(3);
+    for (int c = w; c < (n >> 8); c += nw) mq_dma16((const uint8_t *)src, (uint32_t)c * 1024u + 16u * lane, raw + (uint32_t)c * 1024u);
+}
+__device__ __forceinline__ void mq_xq_in_place_by(int n, uint8_t *lds0, uint32_t xoff, int first, int count,
+                                                  uint32_t *c, uint32_t *err) {
+    const int t = (int)threadIdx.x - first, segs = n >> 4, per = count >> 2, lane = t & 63;
+    const uint32_t nw = (uint32_t)(count >> 6);
+    const int j = t & 3, s0 = t >> 2;
+    __builtin_amdgcn_s_waitcnt(mq_wc_vm(0));   // this wave's DMAs of x
+    mq_waves_sync(c, nw, lane, err);
+    float4 v[MQ_XQP];
+#pragma unroll
+    for (int k = 0; k < MQ_XQP; k++) {
+        const int seg = s0 + k * per;
+        v[k] = ((const float4 *)(lds0 + xoff))[4 * (seg < segs ? seg : segs - 1) + j];
+    }
+    if (t < MQ_ZERO / 16) ((uint4 *)(lds0))[t] = make_uint4(0, 0, 0, 0);
+    mq_waves_sync(c, 2 * nw, lane, err);
+    float *xsv = (float *)(lds0 + xoff + mq_xq_planes(n));
+    // straight-line passes (a segment past the end converts a copy of the
+    // last and stores nothing), so that they interleave
+    XqQuad r[MQ_XQP];
+#pragma unroll
+    for (int k = 0; k < MQ_XQP; k++) {
+        const float a[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
+        r[k] = mq_xq_quad(a);
+    }
+#pragma unroll
+    for (int k = 0; k < MQ_XQP; k++) {
+        const int seg = s0 + k * per;
+        if (seg < segs) {
+            uint8_t *pl = lds0 + xoff + (seg >> 4) * MQ_BREC + (seg & 15) * 48 + 4 * j;
+            *(uint32_t *)(pl) = r[k].p0;
+            *(uint32_t *)(pl + 16) = r[k].p1;
+            *(uint32_t *)(pl + 32) = r[k].p2;
+            if (j == 0) {
+                xsv[seg] = r[k].xs;
+                xsv[segs + seg] = r[k].gs;
+                xsv[2 * segs + seg] = r[k].gq;
+            }
+        }
+    }
+    if (lane == 0) __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+    __builtin_amdgcn_s_setprio(0);
+}
+
 // Row sum over the four block lanes (l, l + 16, l + 32, l + 48) of a wave.
 __device__ __forceinline__ float mq_sum_units(float v) {
     v += __shfl_xor(v, 16, SEPIA_WAVE);
@@ -589,9 +897,12 @@ struct MqItem {
 // stages of a format of Wp padded words.
 // xraw: LDS offset of a raw f32 copy of the workgroup's vector (0: the
 // vector is read from global memory directly), orings: LDS offset of the
-// rings (for the kernels whose LDS layout the host plans).
+// rings (for the kernels whose LDS layout the host plans). conv > 0: the
+// last conv waves of the workgroup DMA the vector straight into its XQ
+// place and convert it there while the others stream and decode their
+// first step; xraw is then the LDS offset of 16 bytes of control words.
 struct MqGeo {
-    int32_t P, ring, xraw, orings;
+    int32_t P, ring, xraw, orings, conv;
 };
 
 // The pipeline of one wave over n_items items of format T, in two halves:
@@ -612,20 +923,21 @@ struct MqWave {
     int ik, im, islot;         // issue cursor: item, quad, ring slot
     const uint8_t *tab = nullptr;   // codebook in LDS (IQ formats)
 
-    // Waves first, first + 1, ... share the items as C = (waves - first) / P
-    // columns of P parts; waves below `first` and past the last full column
-    // get none. Each wave keeps its own ring.
+    // Waves first, first + 1, ... (count of them, or all the rest) share the
+    // items as C = count / P columns of P parts; waves outside them and past
+    // the last full column get none. Wave first + k keeps ring k.
     __device__ __forceinline__ MqWave(const ItemFn &f, int n_items_, int nq_, int n_, uint32_t rb_, MqGeo geo,
-                                      uint8_t *ring_lds, int first = 0)
+                                      uint8_t *ring_lds, int first = 0, int count = -1)
         : item_of(f), n_items(n_items_), nq(nq_), n(n_), rb(rb_) {
-        const int w = mq_wave_id(), nw = (int)(blockDim.x >> 6) - first, wk = w - first;
+        const int w = mq_wave_id(), wk = w - first;
+        const int nw = count >= 0 ? count : (int)(blockDim.x >> 6) - first;
         P = geo.P;
         S = geo.ring / (Wp * 1024);
         S = S < 4 ? S : 4;
         C = nw / P;
         c = wk >= 0 ? wk / P : 0;
         p = wk - c * P;
-        ringp = ring_lds + (size_t)w * geo.ring;
+        ringp = ring_lds + (ptrdiff_t)wk * geo.ring;
         ring = mq_lds_addr(ringp);
         L = mq_lane();
         const int ni = (wk >= 0 && wk < C * P && n_items > c) ? (n_items - c + C - 1) / C : 0;
@@ -680,10 +992,91 @@ struct MqWave {
             mq_stage_xq(src, 0, 1, n, lds0, xoff, 0u);
         }
     }
-    __device__ __forceinline__ void run(const uint8_t *lds0, float *red) {
+    // The first step split around the wait for the vector: pre_first()
+    // waits for its stage, refills the slot and decodes the weights (no x
+    // needed); run_after() finishes it once the XQ vector is in LDS and runs
+    // the remaining steps as run() does. Only for Tn >= 1.
+    template <int TT = T>
+    __device__ __forceinline__ typename MQ<TT>::Pre pre_first() {
+        mq_wait_stages<Wp>((S < Tn ? S : Tn) - 1);
+        uint4 w[W];
+        const uint8_t *src = ringp + 16 * Wp * L.lane;
+#pragma unroll
+        for (int k = 0; k < W; k++) w[k] = *(const uint4 *)(src + 16 * k);
+        __builtin_amdgcn_s_waitcnt(MQ_WC_LGKM0);
+        if (S < Tn) issue();
+        const uint32_t b = 4u * (uint32_t)p + (uint32_t)L.g;
+        return MQ<TT>::pre(w, MQ<TT>::shift((uint32_t)MQ<TT>::bytes * b));
+    }
+    template <int TT = T>
+    __device__ __forceinline__ void run_after(const uint8_t *lds0, float *red, const typename MQ<TT>::Pre &pr) {
+        float acc;
+        {
+            const MqItem it = item_of(c);
+            const uint32_t b = 4u * (uint32_t)p + (uint32_t)L.g;
+            MqCtx x;
+            x.lds0 = lds0;
+            x.abase = L.a_lane ? it.xoff + MQ_BREC * b + 16u * (uint32_t)L.p : 0u;
+            x.xsb = (const float *)(lds0 + it.xoff + mq_xq_planes(n)) + 16u * b;
+            x.gvb = x.xsb + MQ<T>::sum_sel * (n >> 4);
+            x.tab = tab;
+            acc = MQ<TT>::post(pr, x);
+        }
+        steps(lds0, red, 1, acc);
+    }
+    __device__ __forceinline__ void run(const uint8_t *lds0, float *red) { steps(lds0, red, 0, 0.0f); }
+    // start() and run() in one. With geo.conv the last geo.conv waves turn
+    // the vector into XQ (at raised priority) while the others issue their
+    // weights and decode their first step, and wait only for the XQ vector
+    // to finish it; the converter waves return at once after. Every wave of
+    // the workgroup calls this.
+    __device__ __forceinline__ void go(const float *src, const MqGeo &geo, uint8_t *lds0, uint32_t xoff, float *red) {
+        if (geo.conv == 0) {
+            start(src, geo, lds0, xoff);
+            run(lds0, red);
+            return;
+        }
+        const int nconv = 64 * geo.conv, first = (int)blockDim.x - nconv;
+        uint32_t *ctl = (uint32_t *)(lds0 + geo.xraw);
+        const bool cv = (int)threadIdx.x >= first;
+        if (threadIdx.x == 0) ctl[0] = 0u;
+        if (cv) mq_xq_dma_by(src, n, lds0, xoff, first, nconv);
+        // a bare barrier: the vector's DMAs are queued ahead of every weight
+        // DMA, and the control word (and any table in LDS) is written
+        __builtin_amdgcn_s_waitcnt(MQ_WC_LGKM0);
+        __builtin_amdgcn_s_barrier();
+        if (cv) {
+            mq_xq_in_place_by(n, lds0, xoff, first, nconv, ctl, nullptr);
+            return;
+        }
+        prologue();
+        const uint32_t ready = 3u * (uint32_t)geo.conv;
+        if constexpr (MQ<T>::has_pre) {
+            if (Tn > 0) {
+                const typename MQ<T>::Pre pr = pre_first();
+                mq_waves_wait(ctl, ready, L.lane, nullptr);
+                run_after(lds0, red, pr);
+            }
+        } else {
+            mq_waves_wait(ctl, ready, L.lane, nullptr);
+            run(lds0, red);
+        }
+    }
+    // Steps t0 .. Tn - 1 (t0 <= 1), acc0 the sum so far of step 0's item.
+    __device__ __forceinline__ void steps(const uint8_t *lds0, float *red, int t0, float acc0) {
         int ck = 0, cm = 0, cslot = 0;
-        float acc = 0.0f;
-        for (int t = 0; t < Tn; t++) {
+        float acc = acc0;
+        if (t0 == 1) {
+            if (++cm == nqw) {
+                cm = 0;
+                acc = mq_sum_units(acc);
+                if (L.lane < 16) red[((int64_t)item_of(c).red * P + p) * 16 + L.lane] = acc;
+                acc = 0.0f;
+                ++ck;
+            }
+            if (++cslot == S) cslot = 0;
+        }
+        for (int t = t0; t < Tn; t++) {
             const int after = (Tn - 1 - t) < (S - 1) ? (Tn - 1 - t) : (S - 1);
             mq_wait_stages<Wp>(after);
             uint4 w[W];
@@ -751,10 +1144,10 @@ __device__ __forceinline__ void mq_mv(const uint8_t *__restrict__ W, uint64_t ro
         it.red = i;
         return it;
     };
-    MqWave<T, decltype(item_of)> wv(item_of, nk, nb >> 2, n, (uint32_t)row_bytes, geo, rings);
+    MqWave<T, decltype(item_of)> wv(item_of, nk, nb >> 2, n, (uint32_t)row_bytes, geo, rings, 0,
+                                    (int)(blockDim.x >> 6) - geo.conv);
     wv.tab = tab;
-    wv.start(x, geo, smem, xoff);   // its barrier also publishes the codebook
-    wv.run(smem, red);
+    wv.go(x, geo, smem, xoff, red);   // its first barrier also publishes the codebook
     __syncthreads();
     for (int i = threadIdx.x; i < nk * 16; i += blockDim.x) {
         const int64_t r = ((int64_t)blockIdx.x + (int64_t)(i >> 4) * G) * 16 + (i & 15);
@@ -811,9 +1204,9 @@ __device__ __forceinline__ void mq_gateup_slot(const uint8_t *Wg, const uint8_t 
         it.red = i;
         return it;
     };
-    MqWave<T, decltype(item_of)> wv(item_of, 2 * nk, nb >> 2, n, (uint32_t)row_bytes, geo, rings);
-    wv.start(x, geo, smem, xoff);
-    wv.run(smem, red);
+    MqWave<T, decltype(item_of)> wv(item_of, 2 * nk, nb >> 2, n, (uint32_t)row_bytes, geo, rings, 0,
+                                    (int)(blockDim.x >> 6) - geo.conv);
+    wv.go(x, geo, smem, xoff, red);
     __syncthreads();
     for (int i = threadIdx.x; i < nk * 16; i += blockDim.x) {
         const int k = i >> 4, t = i & 15;
@@ -913,9 +1306,9 @@ __device__ __forceinline__ void mq_dn_slot(const uint8_t *Wd, uint64_t row_bytes
         it.red = i;
         return it;
     };
-    MqWave<T, decltype(item_of)> wv(item_of, nk, nb >> 2, inter, (uint32_t)row_bytes, geo, rings);
-    wv.start(hs, geo, lds0, MQ_ZERO);
-    wv.run(lds0, red);
+    MqWave<T, decltype(item_of)> wv(item_of, nk, nb >> 2, inter, (uint32_t)row_bytes, geo, rings, 0,
+                                    (int)(blockDim.x >> 6) - geo.conv);
+    wv.go(hs, geo, lds0, MQ_ZERO, red);
 }
 
 __device__ __forceinline__ void mq_down(const MqProj &down, const MqProj &s_down, const int32_t *__restrict__ sel_idx,

@@ -33,9 +33,6 @@
 #pragma once
 #include "mq.h"
 
-// Wait bounds in s_memrealtime ticks (100 MHz): 2 s for a grid barrier,
-// twice that for the LDS flag that follows one.
-#define MQ_WAIT_TICKS 200000000ull
 
 // Thread 0: wait until the barrier counter reaches target.
 __device__ __forceinline__ void mq_grid_wait(const uint32_t *bar, uint32_t target, uint32_t *err) {

@@ -59,6 +59,8 @@ enum {
     K_MQ_MOE = K_MQ_DN + 1,
     /* batched prefill MoE layer (kernels/prefill.h) */
     K_PF_ROUTE = K_MQ_MOE + 1, K_PF_SELECT, K_PF_GROUP, K_PF_GATEUP, K_PF_DOWN, K_PF_COMBINE, K_PF_SPLIT,
+    /* one expert's FFN in one launch, gate/up and down waves side by side (kernels/mq_flow.h) */
+    K_MQ_FFN,
     K_COUNT
 };
 #define FFN_NAMES(p) "sepia_ffn_gateup_" p, "sepia_ffn_gateup_" p "_xp", "sepia_ffn_down_" p
@@ -81,7 +83,7 @@ static const char *const k_names[K_COUNT] = {
     "sepia_mq_mv_q2_k", "sepia_mq_mv_q3_k", "sepia_mq_mv_q4_k", "sepia_mq_mv_iq2_xs", "sepia_mq_mv_iq3_xxs",
     "sepia_mq_gateup", "sepia_mq_down", "sepia_mq_moe",
     "sepia_pf_route", "sepia_pf_select", "sepia_pf_group", "sepia_pf_gateup", "sepia_pf_down", "sepia_pf_combine",
-    "sepia_pf_split",
+    "sepia_pf_split", "sepia_mq_ffn",
 };
 #undef FFN_NAMES
 
@@ -129,8 +131,12 @@ static int g_opt_mq = 1;     /* sepia_hip_set_option("mq", 0) disables the matri
  * workgroup geometry (parts per item, item lanes, ring stages of the largest
  * format; 0 = planned) */
 static int g_opt_mq_p = 0, g_opt_mq_c = 0, g_opt_mq_s = 0;
-static int g_opt_mq_x = 0;   /* "mq_x": 0 = planner's choice, 1 = vector from global, 2 = vector by LDS DMA */
+static int g_opt_mq_x = 0;   /* "mq_x": 0 = planner's choice, 1 = vector from global, 2 = vector by LDS DMA,
+                              * 3 = converter waves */
 static int g_opt_fuse = 0;   /* sepia_hip_set_option("fuse", 1) runs the MoE layer / expert FFN as one launch */
+static int g_opt_flow = 0;   /* "flow": 1 runs the expert FFN as one sepia_mq_ffn launch (gate/up and down waves) */
+static int g_opt_flow_delay = 250;   /* "flow_delay": s_memrealtime ticks (10 ns) a flow workgroup without
+                                      * gate/up units holds its down weights back */
 static int g_opt_tile_t = 0; /* sepia_hip_set_option("tile_t", T) forces T steps per workgroup */
 
 /* Geometry for `mats` stacked copies of a [rows, 256 * n_blocks] matrix; 0
@@ -252,7 +258,10 @@ static int prep_out(SepiaGpuBuf *b, const char *op) {
  * for partial sums and intermediate vectors, grown on demand. */
 #define CNT_BYTES (64u * 1024u)
 #define MQ_BAR_WORD 1               /* fused launches' grid-barrier counter (never reset) */
-#define MQ_ERR_WORD 2               /* fused launches' barrier time-out flag */
+#define MQ_ERR_WORD 2               /* fused and flow launches' time-out flag */
+#define MQ_FLOW_HCNT_WORD 3         /* flow launches: units of h published (back to zero at the end) */
+#define MQ_FLOW_FLAG_OFF 8192       /* flow launches: workgroup b's h flag at word OFF + 32 b (lowered again) */
+#define MQ_FLOW_FLAG_WORDS (32 * 256)
 static void *g_scratch;
 static size_t g_scratch_len;
 
@@ -524,11 +533,14 @@ int sepia_gpu_end(void) {
         uint32_t flag = 0;
         e = hipMemcpy(&flag, (uint32_t *)g_scratch + MQ_ERR_WORD, 4, hipMemcpyDeviceToHost);
         if (e == hipSuccess && flag) {
-            /* clear the flag and realign the barrier counter (a workgroup that
-             * gave up left it between multiples of the grid size) */
-            const uint32_t zero[2] = { 0, 0 };
-            hipMemcpy((uint32_t *)g_scratch + MQ_BAR_WORD, zero, 8, hipMemcpyHostToDevice);
-            LOG("end: a fused MoE launch timed out at a grid barrier; the batch's results are invalid");
+            /* clear the flag, realign the barrier counter (a workgroup that
+             * gave up left it between multiples of the grid size) and zero
+             * the flow counters */
+            const uint32_t zero[3] = { 0, 0, 0 };
+            hipMemcpy((uint32_t *)g_scratch + MQ_BAR_WORD, zero, 12, hipMemcpyHostToDevice);
+            hipMemset((uint32_t *)g_scratch + MQ_FLOW_FLAG_OFF, 0, MQ_FLOW_FLAG_WORDS * 4);
+            hipDeviceSynchronize();
+            LOG("end: a one-launch FFN timed out waiting (flag %u); the batch's results are invalid", flag);
             return 0;
         }
         if (e != hipSuccess) {
@@ -906,12 +918,20 @@ int sepia_hip_set_option(const char *name, int value) {
         g_opt_mq = value;
         return 1;
     }
-    if (strcmp(name, "mq_x") == 0 && value >= 0 && value <= 2) {
+    if (strcmp(name, "mq_x") == 0 && value >= 0 && value <= 3) {
         g_opt_mq_x = value;
         return 1;
     }
     if (strcmp(name, "fuse") == 0 && (value == 0 || value == 1)) {
         g_opt_fuse = value;
+        return 1;
+    }
+    if (strcmp(name, "flow") == 0 && (value == 0 || value == 1)) {
+        g_opt_flow = value;
+        return 1;
+    }
+    if (strcmp(name, "flow_delay") == 0 && value >= 0 && value <= 100000) {
+        g_opt_flow_delay = value;
         return 1;
     }
     if (strcmp(name, "mq_p") == 0 && value >= 0 && value <= 16) {
@@ -945,7 +965,7 @@ int sepia_hip_set_option(const char *name, int value) {
 #define MQ_CUS 256                  /* MI355X compute units */
 #define MQ_ZERO 768
 typedef struct {
-    int32_t P, ring, xraw, orings;  /* as struct MqGeo in kernels/mq.h */
+    int32_t P, ring, xraw, orings, conv;   /* as struct MqGeo in kernels/mq.h */
 } MqGeo;
 /* In-kernel selection by the gate/up launch (struct MqRoute in
  * kernels/mq.h); logits NULL: the experts come from sel_idx. */
@@ -959,6 +979,10 @@ typedef struct {
 } MqRoute;
 #define MQ_SEL_BYTES 512            /* the gate/up kernel's selection area in LDS */
 #define MQ_XDMA_GAIN 40             /* mq_geo: cost units the vector's LDS DMA saves (measured ~2 us a launch) */
+#define MQ_CONV_GAIN 60             /* mq_geo: cost units converter waves save (XQ off the weights' path); by
+                                     * default only for the IQ formats, where they measured faster (C4 IQ3_XXS
+                                     * 12.2 -> 11.2 us); the K-quants' stepping waves need all 16 */
+#define MQ_XQ_SEGS_PER_WAVE 128     /* segments a converter wave turns into XQ at most (MQ_XQP passes of 16) */
 static size_t mq_xq_bytes(int64_t n) { return (size_t)(n / 256) * 832 + 3 * (size_t)(n / 16) * 4; }
 /* matrix-core format codes: 0..2 the K-quants (matvec and the FFN kernels),
  * 3..4 IQ2_XS and IQ3_XXS (matvec) */
@@ -979,27 +1003,40 @@ static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 /* Geometry for workgroups of n_items items of nq quads; mc is the format
  * most items use, wmax the most words of any format the workgroup may run.
  * LDS = o_raw = align256(fixed + 64 * n_items * P), then (if the vector of
- * raw_bytes goes by LDS DMA) the raw vector, then nw rings at orings; the
- * rings take the rest of the LDS (each at least one step of wmax words).
+ * raw_bytes goes by LDS DMA) the raw vector, or (with converter waves) 16
+ * bytes of control words, then nw rings at orings; the rings take the rest
+ * of the LDS (each at least one step of wmax words). Converter waves come
+ * on top of the nw stepping waves: enough for the vector (at most
+ * MQ_XQ_SEGS_PER_WAVE segments each), up to 4 where the 16 allow.
  * Chooses the fewest steps per wave of format mc, counting a one-stage ring
  * with several steps as 1.6 steps each (its loads do not overlap its
- * compute) and crediting the vector's DMA, then the most steps in flight,
- * then the most waves. Returns 0 when nothing fits. */
+ * compute) and crediting the vector's DMA or converter waves, then the most
+ * steps in flight, then the most waves. Returns 0 when nothing fits. */
 static int mq_geo(int mc, int wmax, int64_t n_items, int64_t nq, size_t fixed, size_t raw_bytes, unsigned *threads,
                   MqGeo *geo, size_t *lds) {
     const size_t w1 = (size_t)k_mq_words[mc] * 1024, wm = (size_t)wmax * 1024;
     int64_t best_cost = 0, best_fl = 0;
     int best_nw = 0, found = 0;
-    for (int xr = 0; xr <= (raw_bytes > 0); xr++) {
-        if ((g_opt_mq_x == 1 && xr) || (g_opt_mq_x == 2 && !xr)) continue;
+    /* vector modes: 0 from global memory, 1 by LDS DMA into a raw copy, 2 by
+     * converter waves (DMA into the XQ place, converted there); 1 and 2 need
+     * the vector's size (raw_bytes) */
+    const int64_t segs = (int64_t)raw_bytes / 64, cv_need = (segs + MQ_XQ_SEGS_PER_WAVE - 1) / MQ_XQ_SEGS_PER_WAVE;
+    for (int mode = 0; mode <= (raw_bytes > 0 ? 2 : 0); mode++) {
+        if (g_opt_mq_x ? g_opt_mq_x != mode + 1 : (mode == 2 && mc < 3)) continue;
         for (int P = 1; P <= 16 && P <= nq; P++) {
             if (g_opt_mq_p && P != g_opt_mq_p) continue;
             for (int C = 1; C * P <= 16 && C <= n_items; C++) {
                 if (g_opt_mq_c && C != g_opt_mq_c) continue;
                 const int nw = C * P;
+                int cv = 0;
+                if (mode == 2) {
+                    if (nw + cv_need > 16) continue;
+                    cv = 16 - nw < 4 ? 16 - nw : 4;
+                    if (cv < cv_need) cv = (int)cv_need;
+                }
                 const int64_t spw = ((n_items + C - 1) / C) * ((nq + P - 1) / P);
                 const size_t o_raw = align256(fixed + (size_t)n_items * P * 64);
-                const size_t base = xr ? align256(o_raw + raw_bytes) : o_raw;
+                const size_t base = mode == 1 ? align256(o_raw + raw_bytes) : mode == 2 ? align256(o_raw + 16) : o_raw;
                 if (base + (size_t)nw * wm > g_lds_max) continue;
                 size_t ring = ((g_lds_max - base) / (size_t)nw) & ~(size_t)1023;
                 if (ring > 4 * wm) ring = 4 * wm;
@@ -1011,8 +1048,9 @@ static int mq_geo(int mc, int wmax, int64_t n_items, int64_t nq, size_t fixed, s
                 if (S > 4) S = 4;
                 if (S > spw) S = spw;
                 /* the vector by DMA ahead of the weights saves about as
-                 * much as MQ_XDMA_GAIN cost units */
-                const int64_t cost = spw * ((S >= 2 || spw == 1) ? 10 : 16) - (xr ? MQ_XDMA_GAIN : 0);
+                 * much as MQ_XDMA_GAIN cost units, converter waves more */
+                const int64_t cost = spw * ((S >= 2 || spw == 1) ? 10 : 16) -
+                                     (mode == 1 ? MQ_XDMA_GAIN : mode == 2 ? MQ_CONV_GAIN : 0);
                 const int64_t fl = (int64_t)nw * S;
                 if (!found || cost < best_cost ||
                     (cost == best_cost && (fl > best_fl || (fl == best_fl && nw > best_nw)))) {
@@ -1022,9 +1060,10 @@ static int mq_geo(int mc, int wmax, int64_t n_items, int64_t nq, size_t fixed, s
                     best_nw = nw;
                     geo->P = P;
                     geo->ring = (int32_t)ring;
-                    geo->xraw = xr ? (int32_t)o_raw : 0;
+                    geo->xraw = mode ? (int32_t)o_raw : 0;
                     geo->orings = (int32_t)base;
-                    *threads = 64u * (unsigned)nw;
+                    geo->conv = cv;
+                    *threads = 64u * (unsigned)(nw + cv);
                     *lds = base + (size_t)nw * ring;
                 }
             }
@@ -1301,7 +1340,7 @@ static int mq_ffn_plan(const MoeProj *g, const MoeProj *u, const MoeProj *d, con
         if (!mq_proj_ok(ps[i], rows[i])) return 0;
     if (g->type != u->type || (n_shared > 0 && sg->type != su->type)) return 0;
     const int64_t tiles_i = (I + 15) / 16, tiles_h = (H + 15) / 16;
-    if (n_shared + topk > 1 && MQ_DN_CNT_OFF + tiles_h > CNT_BYTES / 4) return 0;
+    if (n_shared + topk > 1 && MQ_DN_CNT_OFF + tiles_h > MQ_FLOW_FLAG_OFF) return 0;
     /* both slot kinds share a geometry: planned for the format of the
      * routed slots (the shared ones when there are none), with rings that
      * hold a step of either */
@@ -1639,6 +1678,186 @@ static int mq_fuse_launch(const char *op, const MoeProj *g, const MoeProj *u, co
     return 1;
 }
 
+/* One expert's FFN as one launch of sepia_mq_ffn (kernels/mq_flow.h):
+ * MQ_CUS workgroups of 16 waves, one per CU. Workgroup b owns gate/up units
+ * [b U / G, (b + 1) U / G) (U = I / 16 units of 16 gate and 16 up rows) on
+ * waves 0 .. ngu - 1 and down row groups on the next nd1 waves; workgroups
+ * without units run down only (nd0 waves) and take dh row groups instead of
+ * dl, chosen so that every workgroup streams about the same bytes. Geometry
+ * per role as mq_geo: the fewest steps for the busiest wave, every step in
+ * flight at the start where the LDS allows. Mirrors struct MqFlowGeo. */
+typedef struct {
+    MqGeo gu, d1, d0;
+    int32_t ngu, nd1, nd0;
+    int32_t dl, dh, drem;
+    int32_t free_delay;
+    uint32_t o_xqh, o_gred, o_dred, o_ctl, o_rings;
+} MqFlowGeo;
+typedef struct {
+    const float *x;
+    float *y;
+    int64_t inter, hidden;
+    uint8_t *xq_h;
+    uint32_t *hcnt, *flags, *err;
+} MqFlowIo;
+#define MQ_FLOW_WAVES 16
+
+/* Best split of n_items items of nq quads over at most max_waves waves with
+ * rings from `budget` bytes: P parts, C columns, S stages. Cost: the
+ * busiest wave's steps, each step not in flight at the start counted
+ * `late` more. Returns the cost, or -1 when nothing fits. */
+static int64_t mq_flow_role(int mc, int64_t n_items, int64_t nq, int max_waves, size_t budget, int64_t per_step,
+                            int64_t late, int *Pb, int *Cb, int *Sb) {
+    const size_t w1 = (size_t)k_mq_words[mc] * 1024;
+    int64_t best = -1;
+    for (int P = 1; P <= max_waves && P <= nq; P++)
+        for (int C = 1; C * P <= max_waves && C <= n_items; C++) {
+            const int64_t spw = ((n_items + C - 1) / C) * ((nq + P - 1) / P);
+            int64_t S = spw < 4 ? spw : 4;
+            while (S > 1 && (size_t)(C * P) * (size_t)S * w1 > budget) S--;
+            if ((size_t)(C * P) * (size_t)S * w1 > budget) continue;
+            const int64_t cost = per_step * spw + late * (spw - S);
+            if (best < 0 || cost < best || (cost == best && C * P < *Pb * *Cb)) {
+                best = cost;
+                *Pb = P;
+                *Cb = C;
+                *Sb = (int)S;
+            }
+        }
+    return best;
+}
+
+static int mq_flow_plan(const MoeProj *g, const MoeProj *u, const MoeProj *d, int64_t H, int64_t I, MqFlowGeo *G,
+                        unsigned *threads, size_t *lds) {
+    static int told = 0;
+    if (!g_opt_flow || g->type != u->type || g->row_bytes != u->row_bytes || !mq_proj_ok(g, I) || !mq_proj_ok(u, I) ||
+        !mq_proj_ok(d, H) || H % 256 || I % 256)
+        return 0;
+    if (g_cus < MQ_CUS) {
+        if (!told++) LOG("flow FFN launch off: %d compute units (it needs %d)", g_cus, MQ_CUS);
+        return 0;
+    }
+    const int kg = mq_code(g->type), kd = mq_code(d->type);
+    const int64_t Gn = MQ_CUS, U = I / 16, D = H / 16;
+    const int64_t n_unit = U < Gn ? U : Gn, n_free = Gn - n_unit, nu_max = (U + Gn - 1) / Gn;
+    const int64_t wu = 32 * (int64_t)g->row_bytes, wd = 16 * (int64_t)d->row_bytes;
+    /* down row groups: dl per workgroup with units, dh per other, one more
+     * for the first drem workgroups */
+    int64_t best = -1, dl = 0, dh = 0, drem = 0;
+    for (int64_t l = 0; l * n_unit <= D; l++) {
+        const int64_t R = D - l * n_unit;
+        int64_t h = 0, r = R;
+        if (n_free > 0) {
+            h = R / n_free;
+            r = R - h * n_free;
+        } else if (R >= Gn) {
+            continue;
+        }
+        int64_t c = nu_max * wu + (l + (r > 0)) * wd;
+        if (n_free > 0 && (h + (r > 0)) * wd > c) c = (h + (r > 0)) * wd;
+        if (best < 0 || c < best) {
+            best = c;
+            dl = l;
+            dh = h;
+            drem = r;
+        }
+    }
+    if (best < 0) return 0;
+    const int64_t items_d1 = dl + (drem > 0), items_d0 = n_free > 0 ? dh + (drem > 0) : 0;
+    const int64_t nqg = H / 1024, nqd = I / 1024;
+    memset(G, 0, sizeof *G);
+    size_t o = MQ_ZERO + mq_xq_bytes(H);
+    G->o_xqh = (uint32_t)align256(o);
+    o = G->o_xqh + mq_xq_bytes(I);
+    G->o_gred = (uint32_t)o;
+    o += (size_t)2 * nu_max * MQ_FLOW_WAVES * 64;
+    G->o_dred = (uint32_t)o;
+    o += (size_t)(items_d1 > items_d0 ? items_d1 : items_d0) * MQ_FLOW_WAVES * 64;
+    G->o_ctl = (uint32_t)o;
+    o += 64;
+    G->o_rings = (uint32_t)align256(o);
+    if (G->o_rings >= g_lds_max) return 0;
+    const size_t budget = g_lds_max - G->o_rings;
+    const size_t wg1 = (size_t)k_mq_words[kg] * 1024, wd1 = (size_t)k_mq_words[kd] * 1024;
+    /* workgroups with units: gate/up (critical: it gates every down wave)
+     * and down waves share the 16 waves and the ring budget */
+    int64_t bu = -1;
+    for (int ngu = 1; ngu < MQ_FLOW_WAVES; ngu++) {
+        /* the waves past the gate/up ones turn x into XQ: four lanes per
+         * segment, at most 8 passes (MQ_XQP in kernels/mq_flow.h) */
+        if (H / 16 > 8 * 16 * (MQ_FLOW_WAVES - ngu)) break;
+        int Pg = 0, Cg = 0, Sg = 0;
+        const int64_t cg = mq_flow_role(kg, 2 * nu_max, nqg, ngu, budget, 10, 6, &Pg, &Cg, &Sg);
+        if (cg < 0 || Pg * Cg != ngu) continue;
+        const size_t used = (size_t)ngu * (size_t)Sg * wg1;
+        int Pd = 1, Cd = 0, Sd = 0;
+        int64_t cd = 0;
+        if (items_d1 > 0) {
+            cd = mq_flow_role(kd, items_d1, nqd, MQ_FLOW_WAVES - ngu, budget - used, 4, 10, &Pd, &Cd, &Sd);
+            if (cd < 0) continue;
+        }
+        if (bu < 0 || cg + cd < bu) {
+            bu = cg + cd;
+            G->gu.P = Pg;
+            G->gu.ring = (int32_t)((size_t)Sg * wg1);
+            G->ngu = ngu;
+            G->d1.P = Pd;
+            G->d1.ring = (int32_t)((size_t)(Sd > 0 ? Sd : 1) * wd1);
+            G->nd1 = Pd * Cd;
+        }
+    }
+    if (bu < 0) {
+        if (!told++) LOG("flow FFN launch off: no geometry fits %zu bytes of LDS", g_lds_max);
+        return 0;
+    }
+    size_t need = G->o_rings + (size_t)G->ngu * G->gu.ring + (size_t)G->nd1 * G->d1.ring;
+    G->d0.P = 1;
+    G->d0.ring = (int32_t)wd1;
+    if (items_d0 > 0) {
+        int P = 0, C = 0, S = 0;
+        if (mq_flow_role(kd, items_d0, nqd, MQ_FLOW_WAVES, budget, 4, 10, &P, &C, &S) < 0) return 0;
+        G->d0.P = P;
+        G->d0.ring = (int32_t)((size_t)S * wd1);
+        G->nd0 = P * C;
+        const size_t n0 = G->o_rings + (size_t)G->nd0 * G->d0.ring;
+        if (n0 > need) need = n0;
+    }
+    G->dl = (int32_t)dl;
+    G->dh = (int32_t)dh;
+    G->drem = (int32_t)drem;
+    G->free_delay = g_opt_flow_delay;
+    *threads = 64u * MQ_FLOW_WAVES;
+    *lds = need;
+    int nb = 0;
+    const hipError_t e = hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&nb, g_fn[K_MQ_FFN], (int)*threads, *lds);
+    if (e != hipSuccess || nb < 1 || (int64_t)nb * g_cus < MQ_CUS) {
+        if (!told++)
+            LOG("flow FFN launch off: occupancy query %s, %d workgroups of %u threads and %zu bytes LDS per CU",
+                hipGetErrorString(e), nb, *threads, *lds);
+        return 0;
+    }
+    return 1;
+}
+
+static int mq_flow_launch(const char *op, const MoeProj *g, const MoeProj *u, const MoeProj *d, int32_t expert,
+                          int64_t H, int64_t I, const uint8_t *xdev, float *ydev, uint8_t *scr, const MqFlowGeo *fg,
+                          unsigned threads, size_t lds) {
+    MqFlowIo io;
+    io.x = (const float *)xdev;
+    io.y = ydev;
+    io.inter = I;
+    io.hidden = H;
+    io.xq_h = scr;
+    io.hcnt = (uint32_t *)g_scratch + MQ_FLOW_HCNT_WORD;
+    io.flags = (uint32_t *)g_scratch + MQ_FLOW_FLAG_OFF;
+    io.err = (uint32_t *)g_scratch + MQ_ERR_WORD;
+    MqFlowGeo geo = *fg;
+    void *args[] = { (void *)g, (void *)u, (void *)d, &expert, &io, &geo };
+    if (!launch_lds(K_MQ_FFN, MQ_CUS, threads, lds, args, op)) return 0;
+    g_fused_pending = 1;
+    return 1;
+}
+
 /* The SwiGLU expert FFN over n_slots = topk + n_shared slots: routed slot s
  * uses expert sel_idx[s] (or fixed + s when sel_idx is NULL), then come the
  * shared experts. One slot without weights stores y; several slots add
@@ -1834,6 +2053,12 @@ int sepia_gpu_expert_ffn(const SepiaExpertTensor *gate, const SepiaExpertTensor 
     if (!prep_in(gate->buf, op) || !prep_in(up->buf, op) || !prep_in(down->buf, op) || !prep_in(x, op) ||
         !prep_out(y, op))
         return 0;
+    MqFlowGeo flg;
+    unsigned fl_threads;
+    size_t fl_lds;
+    if (mq_flow_plan(&g, &u, &d, hidden, inter, &flg, &fl_threads, &fl_lds))
+        return mq_flow_launch(op, &g, &u, &d, expert, hidden, inter, x->dev, (float *)y->dev, scr, &flg, fl_threads,
+                              fl_lds);
     MqFusePlan fp;
     if (mq_fuse_plan(&g, &u, &d, &none, &none, &none, 1, 0, hidden, inter, 0, &fp)) {
         MqFuseIo io;

@@ -210,21 +210,25 @@ def test_matvec_q_config_shapes(dev, orc, name, t, out_dim, in_dim):
 @pytest.fixture
 def kernel_path(dev, request):
     """Force one kernel family: the matrix-core kernels (the default), the
-    matrix-core MoE layer / expert FFN as one launch ("fused"), the generic
-    per-row kernel, or the tile kernels with 1, 2 or 3 row steps per
+    matrix-core MoE layer / expert FFN as one launch ("fused"), the expert
+    FFN as one launch of gate/up and down waves side by side ("flow"), the
+    generic per-row kernel, or the tile kernels with 1, 2 or 3 row steps per
     workgroup."""
     L = dev.L
     mode = request.param
     if mode == "fused":
         assert L.sepia_hip_set_option(b"fuse", 1) == 1
+    elif mode == "flow":
+        assert L.sepia_hip_set_option(b"flow", 1) == 1
     elif mode != "mq":
         assert L.sepia_hip_set_option(b"mq", 0) == 1
     if mode == "generic":
         assert L.sepia_hip_set_option(b"tile", 0) == 1
-    elif mode not in ("mq", "fused"):
+    elif mode not in ("mq", "fused", "flow"):
         assert L.sepia_hip_set_option(b"tile_t", {"t1": 1, "t2": 2, "t3": 3}[mode]) == 1
     yield mode
     L.sepia_hip_set_option(b"fuse", 0)
+    L.sepia_hip_set_option(b"flow", 0)
     L.sepia_hip_set_option(b"mq", 1)
     L.sepia_hip_set_option(b"tile", 1)
     L.sepia_hip_set_option(b"tile_t", 0)
@@ -458,13 +462,15 @@ def test_selftest_touch_and_wrap(dev):
 @pytest.fixture
 def mq_vector(dev, request):
     """Force how the matrix-core kernels read their vector: 1 = from global
-    memory after the weight prologue, 2 = by LDS DMA ahead of it."""
+    memory after the weight prologue, 2 = by LDS DMA ahead of it, 3 = by
+    converter waves (DMA into the XQ place, converted there while the other
+    waves decode their first step)."""
     assert dev.L.sepia_hip_set_option(b"mq_x", request.param) == 1
     yield request.param
     dev.L.sepia_hip_set_option(b"mq_x", 0)
 
 
-@pytest.mark.parametrize("mq_vector", [1, 2], indirect=True, ids=["global", "dma"])
+@pytest.mark.parametrize("mq_vector", [1, 2, 3], indirect=True, ids=["global", "dma", "conv"])
 @pytest.mark.parametrize("t,out_dim,in_dim", [(12, 4096, 4096), (10, 3072, 6144), (11, 6144, 3072),
                                               (10, 12288, 2048), (12, 40, 12288), (17, 6144, 6144),
                                               (18, 6144, 6144), (18, 257, 3072), (17, 33, 1024)],
@@ -645,7 +651,7 @@ def test_moe_decode_fused(dev, orc, fuse, types):
         dev.free(b)
 
 
-@pytest.mark.parametrize("mq_vector", [1, 2], indirect=True, ids=["global", "dma"])
+@pytest.mark.parametrize("mq_vector", [1, 2, 3], indirect=True, ids=["global", "dma", "conv"])
 def test_moe_decode_mq_vector_paths(dev, orc, mq_vector):
     """C3 layer shapes with 16 routed experts resident; gate/up and down read x
     and h either way."""
@@ -751,7 +757,7 @@ def run_expert_ffn(dev, tensors, n_experts, expert, hidden, inter, x):
     return y
 
 
-@pytest.mark.parametrize("kernel_path", ["mq", "fused", "generic", "t1", "t2", "t3"], indirect=True)
+@pytest.mark.parametrize("kernel_path", ["mq", "fused", "flow", "generic", "t1", "t2", "t3"], indirect=True)
 @pytest.mark.parametrize("types,hidden,inter", [((10, 10, 11), 6144, 3072), ((12, 12, 12), 4096, 2048),
                                                 ((11, 11, 10), 2048, 1024)],
                          ids=["c2_q2k_q3k", "q4k_4096", "q3k_q2k_2048"])
@@ -772,3 +778,34 @@ def test_expert_ffn(dev, orc, kernel_path, types, hidden, inter):
     assert_close(y, want, what="expert ffn %s" % kernel_path, gate=False)
     for b in bufs:
         dev.free(b)
+
+
+@pytest.mark.parametrize("types,hidden,inter", [((10, 10, 11), 6144, 3072), ((12, 12, 10), 4096, 2048),
+                                                ((11, 11, 12), 2048, 8192), ((10, 10, 10), 1024, 1024),
+                                                ((12, 12, 11), 3072, 4096)],
+                         ids=["c2", "units_half", "two_units_per_wg", "tiny", "q4k_q3k"])
+def test_expert_ffn_flow(dev, orc, types, hidden, inter):
+    """The one-launch expert FFN with gate/up and down waves side by side,
+    over splits with free workgroups (fewer units than CUs), several units
+    per workgroup and fewer down row groups than workgroups. Each shape
+    runs twice: the second launch needs the h counters the first one put
+    back to zero."""
+    rng = np.random.default_rng(7 * hidden + inter)
+    tg, tu, td = types
+    n_e, e = 2, 1
+    gate = [synth.random_matrix(tg, inter, hidden, rng) for _ in range(n_e)]
+    up = [synth.random_matrix(tu, inter, hidden, rng) for _ in range(n_e)]
+    down = [synth.random_matrix(td, hidden, inter, rng) for _ in range(n_e)]
+    bufs = [dev.shared_from(np.concatenate(v)) for v in (gate, up, down)]
+    tensors = [hip.ExpertTensor(b, 0, v[0].nbytes, t) for b, v, t in zip(bufs, (gate, up, down), types)]
+    assert dev.L.sepia_hip_set_option(b"flow", 1) == 1
+    try:
+        for k in range(2):
+            x = synth.normal_vector(rng, hidden)
+            y = run_expert_ffn(dev, tensors, n_e, e, hidden, inter, x)
+            want = orc.expert_ffn(tg, gate[e], tu, up[e], td, down[e], hidden, inter, x, threads=THREADS)
+            assert_close(y, want, what="flow expert ffn %dx%d run %d" % (hidden, inter, k), gate=False)
+    finally:
+        dev.L.sepia_hip_set_option(b"flow", 0)
+        for b in bufs:
+            dev.free(b)
