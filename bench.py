@@ -398,7 +398,7 @@ def run_c3(B, warmup, steps, cpu_seconds, n_layers=3):
 
     ms = B.timed_steps(step, warmup, steps)
     per_token = (NR + NS) * H * 4 + 6 * (2 * gb + db) + NS * (2 * sgb + sdb)
-    kms = B.kernel_ms(step, min(steps, 60), ["sepia_mq_moe", "sepia_moe_route", "sepia_mq_gateup", "sepia_mq_down"])
+    kms = B.kernel_ms(step, min(steps, 60), ["sepia_mq_moe", "sepia_moe_route", "sepia_mq_gateup", "sepia_mq_gateup_mix", "sepia_mq_down"])
 
     # parity at full size: route + output of one token against the oracle
     import oracle

@@ -119,7 +119,12 @@ void *sepia_hip_stream(void);
  *   "flow" 0/1    the expert FFN as one launch of sepia_mq_ffn, gate/up
  *                 and down waves side by side (default 0);
  *   "flow_delay"  ticks (10 ns) the flow launch's workgroups without
- *                 gate/up rows hold their down weights back (default 250). */
+ *                 gate/up rows hold their down weights back (default 250);
+ *   "mix" 0/1     the MoE decode's gate/up as sepia_mq_gateup_mix: every
+ *                 workgroup streams shared-expert rows while its wave 0
+ *                 selects, then routed rows (default 0);
+ *   "route_sel" 0/1  the router launch's last workgroup selects the experts
+ *                 even for the matrix-core FFN (default 0: gate/up selects). */
 int sepia_hip_set_option(const char *name, int value);
 
 #ifdef __cplusplus

@@ -125,6 +125,56 @@ __device__ __forceinline__ void xq_store(const XqSeg &r, uint8_t *xq, int64_t n,
     xs[n / 8 + seg] = r.gq;
 }
 
+// Quad (4-lane) exchanges by DPP: lane l reads lane l ^ 1, l ^ 2.
+__device__ __forceinline__ float mq_quad_x1(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float mq_quad_x2(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+}
+__device__ __forceinline__ int mq_quad_x1i(int v) { return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false); }
+__device__ __forceinline__ int mq_quad_x2i(int v) { return __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false); }
+
+// XQ of one 16-column segment by a quad: lane j holds columns 4j .. 4j + 3
+// (a), gets word j of each digit plane (p0, p1 + 128, p2 + 128 bytes) and
+// the segment's xs, gs and gq. The same values as xq_segment but for the
+// order of the gs sum.
+struct XqQuad {
+    uint32_t p0, p1, p2;
+    float xs, gs, gq;
+};
+__device__ __forceinline__ XqQuad mq_xq_quad(const float (&a)[4]) {
+    float m = fmaxf(fmaxf(fabsf(a[0]), fabsf(a[1])), fmaxf(fabsf(a[2]), fabsf(a[3])));
+    m = fmaxf(m, mq_quad_x1(m));
+    m = fmaxf(m, mq_quad_x2(m));
+    const float inv = (m > 0.0f) ? MQ_QMAX * __builtin_amdgcn_rcpf(m) : 0.0f;
+    XqQuad r;
+    r.xs = m * (1.0f / MQ_QMAX);
+    uint32_t q[4];
+    int32_t qs = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int32_t v = mq_round(a[i] * inv);
+        qs += v;
+        q[i] = (uint32_t)v + 0x8080u;
+    }
+    qs += mq_quad_x1i(qs);
+    qs += mq_quad_x2i(qs);
+    float sum = (a[0] + a[1]) + (a[2] + a[3]);
+    sum += mq_quad_x1(sum);
+    sum += mq_quad_x2(sum);
+    const uint32_t t01 = __builtin_amdgcn_perm(q[1], q[0], 0x05010400u);
+    const uint32_t t23 = __builtin_amdgcn_perm(q[3], q[2], 0x05010400u);
+    const uint32_t u01 = __builtin_amdgcn_perm(q[1], q[0], 0x06020602u);
+    const uint32_t u23 = __builtin_amdgcn_perm(q[3], q[2], 0x06020602u);
+    r.p0 = __builtin_amdgcn_perm(u23, u01, 0x05040100u);
+    r.p1 = __builtin_amdgcn_perm(t23, t01, 0x07060302u) ^ 0x80808080u;
+    r.p2 = __builtin_amdgcn_perm(t23, t01, 0x05040100u) ^ 0x80808080u;
+    r.gs = sum;
+    r.gq = r.xs * (float)qs;
+    return r;
+}
+
 // ---- f32 vectors -> XQ in LDS, by the whole workgroup: `count` vectors of
 // n columns (vector k at src + k * ld floats) to LDS offsets xoff + k * xqb.
 // Each thread converts whole 16-column segments. Also clears the zero area
@@ -139,7 +189,9 @@ __device__ __forceinline__ void mq_dma_vec(const float *src, int n, uint32_t raw
     const uint32_t lane = threadIdx.x & 63;
     for (int c = w; c < (n >> 8); c += nw) mq_dma16((const uint8_t *)src, (uint32_t)c * 1024u + 16u * lane, raw + (uint32_t)c * 1024u);
 }
-// XQ of an n-float vector already in LDS (raw, 16-byte aligned).
+// XQ of an n-float vector already in LDS (raw, 16-byte aligned), one
+// thread per 16-column segment (fewer wave instructions than four lanes
+// per segment, which measured slower here). Ends with a barrier.
 __device__ __forceinline__ void mq_stage_xq_lds(const float *raw, int n, uint8_t *lds0, uint32_t xoff) {
     const int segs = n >> 4;
     for (int seg = threadIdx.x; seg < segs; seg += blockDim.x) {
@@ -751,56 +803,6 @@ __device__ __forceinline__ void mq_waves_wait(uint32_t *c, uint32_t target, int 
     }
 }
 
-// Quad (4-lane) exchanges by DPP: lane l reads lane l ^ 1, l ^ 2.
-__device__ __forceinline__ float mq_quad_x1(float v) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
-}
-__device__ __forceinline__ float mq_quad_x2(float v) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
-}
-__device__ __forceinline__ int mq_quad_x1i(int v) { return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false); }
-__device__ __forceinline__ int mq_quad_x2i(int v) { return __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false); }
-
-// XQ of one 16-column segment by a quad: lane j holds columns 4j .. 4j + 3
-// (a), gets word j of each digit plane (p0, p1 + 128, p2 + 128 bytes) and
-// the segment's xs, gs and gq. The same values as xq_segment but for the
-// order of the gs sum.
-struct XqQuad {
-    uint32_t p0, p1, p2;
-    float xs, gs, gq;
-};
-__device__ __forceinline__ XqQuad mq_xq_quad(const float (&a)[4]) {
-    float m = fmaxf(fmaxf(fabsf(a[0]), fabsf(a[1])), fmaxf(fabsf(a[2]), fabsf(a[3])));
-    m = fmaxf(m, mq_quad_x1(m));
-    m = fmaxf(m, mq_quad_x2(m));
-    const float inv = (m > 0.0f) ? MQ_QMAX * __builtin_amdgcn_rcpf(m) : 0.0f;
-    XqQuad r;
-    r.xs = m * (1.0f / MQ_QMAX);
-    uint32_t q[4];
-    int32_t qs = 0;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int32_t v = mq_round(a[i] * inv);
-        qs += v;
-        q[i] = (uint32_t)v + 0x8080u;
-    }
-    qs += mq_quad_x1i(qs);
-    qs += mq_quad_x2i(qs);
-    float sum = (a[0] + a[1]) + (a[2] + a[3]);
-    sum += mq_quad_x1(sum);
-    sum += mq_quad_x2(sum);
-    const uint32_t t01 = __builtin_amdgcn_perm(q[1], q[0], 0x05010400u);
-    const uint32_t t23 = __builtin_amdgcn_perm(q[3], q[2], 0x05010400u);
-    const uint32_t u01 = __builtin_amdgcn_perm(q[1], q[0], 0x06020602u);
-    const uint32_t u23 = __builtin_amdgcn_perm(q[3], q[2], 0x06020602u);
-    r.p0 = __builtin_amdgcn_perm(u23, u01, 0x05040100u);
-    r.p1 = __builtin_amdgcn_perm(t23, t01, 0x07060302u) ^ 0x80808080u;
-    r.p2 = __builtin_amdgcn_perm(t23, t01, 0x05040100u) ^ 0x80808080u;
-    r.gs = sum;
-    r.gq = r.xs * (float)qs;
-    return r;
-}
-
 // Waves first .. first + count - 1 of the workgroup wait for one another:
 // arrival k of each (k = 1, 2, ...) completes when the counter at c
 // reaches k * count. Bounded in time (error flag 5 on expiry).
@@ -830,11 +832,11 @@ __device__ __forceinline__ void mq_xq_dma_by(const float *src, int n, uint8_t *l
     for (int c = w; c < (n >> 8); c += nw) mq_dma16((const uint8_t *)src, (uint32_t)c * 1024u + 16u * lane, raw + (uint32_t)c * 1024u);
 }
 __device__ __forceinline__ void mq_xq_in_place_by(int n, uint8_t *lds0, uint32_t xoff, int first, int count,
-                                                  uint32_t *c, uint32_t *err) {
+                                                  uint32_t *c, uint32_t *err, bool waited = false) {
     const int t = (int)threadIdx.x - first, segs = n >> 4, per = count >> 2, lane = t & 63;
     const uint32_t nw = (uint32_t)(count >> 6);
     const int j = t & 3, s0 = t >> 2;
-    __builtin_amdgcn_s_waitcnt(mq_wc_vm(0));   // this wave's DMAs of x
+    if (!waited) __builtin_amdgcn_s_waitcnt(mq_wc_vm(0));   // this wave's DMAs of x (or the caller waited)
     mq_waves_sync(c, nw, lane, err);
     float4 v[MQ_XQP];
 #pragma unroll
@@ -976,9 +978,12 @@ struct MqWave {
     // The workgroup's vector: from global memory, or (geo.xraw) by LDS DMA
     // ahead of the prologue and converted once it has landed, so that the
     // vector does not queue behind the workgroup's weight stream.
+    // x_issued: the caller already DMA'd the vector into the raw copy (a
+    // mode-1 geometry) before work of its own, e.g. the expert selection.
+    bool x_issued = false;
     __device__ __forceinline__ void start(const float *src, const MqGeo &geo, uint8_t *lds0, uint32_t xoff) {
         if (geo.xraw) {
-            mq_dma_vec(src, n, mq_lds_addr(lds0 + geo.xraw));
+            if (!x_issued) mq_dma_vec(src, n, mq_lds_addr(lds0 + geo.xraw));
             // every wave's vector DMAs are issued before any weight DMA, so
             // the CU's queue holds the whole vector ahead of the weights
             // (a bare s_barrier: nothing waits for the loads here)
@@ -1187,7 +1192,7 @@ __device__ __forceinline__ int64_t mq_slot_expert(const int32_t *sel_idx, int32_
 template <int T>
 __device__ __forceinline__ void mq_gateup_slot(const uint8_t *Wg, const uint8_t *Wu, uint64_t row_bytes, int32_t nb,
                                                int32_t inter, int32_t j0, int32_t jstep, const float *__restrict__ x,
-                                               float *__restrict__ h, MqGeo geo) {
+                                               float *__restrict__ h, MqGeo geo, bool x_issued) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int n = 256 * nb;
     const int tiles = (inter + 15) >> 4;
@@ -1206,6 +1211,7 @@ __device__ __forceinline__ void mq_gateup_slot(const uint8_t *Wg, const uint8_t 
     };
     MqWave<T, decltype(item_of)> wv(item_of, 2 * nk, nb >> 2, n, (uint32_t)row_bytes, geo, rings, 0,
                                     (int)(blockDim.x >> 6) - geo.conv);
+    wv.x_issued = x_issued;
     wv.go(x, geo, smem, xoff, red);
     __syncthreads();
     for (int i = threadIdx.x; i < nk * 16; i += blockDim.x) {
@@ -1245,7 +1251,14 @@ __device__ __forceinline__ void mq_gateup(const MqProj &gate, const MqProj &up, 
     const int32_t k0 = rk ? bid : bid - topk * wps_r;
     const int32_t slot = (rk ? 0 : topk) + k0 / wps, j0 = k0 % wps;
     int64_t e;
+    bool x_issued = false;
     if (rt.logits && slot < topk) {
+        // the vector does not depend on the selection: with a raw-copy
+        // geometry its DMA goes out first and lands while wave 0 selects
+        if (geo.xraw && geo.conv == 0) {
+            mq_dma_vec(x, (int)(256 * gate.n_blocks), mq_lds_addr(smem + geo.xraw));
+            x_issued = true;
+        }
         int32_t *si = (int32_t *)(smem + MQ_ZERO + mq_xq_bytes(256 * gate.n_blocks));
         float *sw = (float *)(si + 64);
         if (threadIdx.x < SEPIA_WAVE)
@@ -1266,9 +1279,9 @@ __device__ __forceinline__ void mq_gateup(const MqProj &gate, const MqProj &up, 
     float *hs = h + (int64_t)slot * inter;
     const int32_t nb = (int32_t)G.n_blocks;
     switch (G.type) {
-    case ST_Q2_K: mq_gateup_slot<ST_Q2_K>(wg, wu, G.row_bytes, nb, inter, j0, wps, x, hs, geo); break;
-    case ST_Q3_K: mq_gateup_slot<ST_Q3_K>(wg, wu, G.row_bytes, nb, inter, j0, wps, x, hs, geo); break;
-    default: mq_gateup_slot<ST_Q4_K>(wg, wu, G.row_bytes, nb, inter, j0, wps, x, hs, geo); break;
+    case ST_Q2_K: mq_gateup_slot<ST_Q2_K>(wg, wu, G.row_bytes, nb, inter, j0, wps, x, hs, geo, x_issued); break;
+    case ST_Q3_K: mq_gateup_slot<ST_Q3_K>(wg, wu, G.row_bytes, nb, inter, j0, wps, x, hs, geo, x_issued); break;
+    default: mq_gateup_slot<ST_Q4_K>(wg, wu, G.row_bytes, nb, inter, j0, wps, x, hs, geo, x_issued); break;
     }
 }
 

@@ -224,6 +224,7 @@ SEPIA_FFN_PAIR(4, 4, ST_Q4_K, ST_Q4_K)
 #include "mq.h"
 #include "mq_fused.h"
 #include "mq_flow.h"
+#include "mq_mix.h"
 #include "moe.h"
 #include "prefill.h"
 #include "synth.h"
@@ -239,3 +240,4 @@ SEPIA_MQ_GATEUP()
 SEPIA_MQ_DOWN()
 SEPIA_MQ_FUSED()
 SEPIA_MQ_FLOW()
+SEPIA_MQ_MIX()

@@ -61,6 +61,8 @@ enum {
     K_PF_ROUTE = K_MQ_MOE + 1, K_PF_SELECT, K_PF_GROUP, K_PF_GATEUP, K_PF_DOWN, K_PF_COMBINE, K_PF_SPLIT,
     /* one expert's FFN in one launch, gate/up and down waves side by side (kernels/mq_flow.h) */
     K_MQ_FFN,
+    /* MoE gate/up with the selection behind shared-expert streaming (kernels/mq_mix.h) */
+    K_MQ_GU_MIX,
     K_COUNT
 };
 #define FFN_NAMES(p) "sepia_ffn_gateup_" p, "sepia_ffn_gateup_" p "_xp", "sepia_ffn_down_" p
@@ -83,7 +85,7 @@ static const char *const k_names[K_COUNT] = {
     "sepia_mq_mv_q2_k", "sepia_mq_mv_q3_k", "sepia_mq_mv_q4_k", "sepia_mq_mv_iq2_xs", "sepia_mq_mv_iq3_xxs",
     "sepia_mq_gateup", "sepia_mq_down", "sepia_mq_moe",
     "sepia_pf_route", "sepia_pf_select", "sepia_pf_group", "sepia_pf_gateup", "sepia_pf_down", "sepia_pf_combine",
-    "sepia_pf_split", "sepia_mq_ffn",
+    "sepia_pf_split", "sepia_mq_ffn", "sepia_mq_gateup_mix",
 };
 #undef FFN_NAMES
 
@@ -134,6 +136,10 @@ static int g_opt_mq_p = 0, g_opt_mq_c = 0, g_opt_mq_s = 0;
 static int g_opt_mq_x = 0;   /* "mq_x": 0 = planner's choice, 1 = vector from global, 2 = vector by LDS DMA,
                               * 3 = converter waves */
 static int g_opt_fuse = 0;   /* sepia_hip_set_option("fuse", 1) runs the MoE layer / expert FFN as one launch */
+static int g_opt_mix = 0;    /* "mix": 1 runs the MoE decode's gate/up as sepia_mq_gateup_mix (every workgroup
+                              * streams shared units while its wave 0 selects, then routed ones) */
+static int g_opt_route_sel = 0;   /* "route_sel": 1 = the router launch's last workgroup selects the
+                                   * experts even for the matrix-core FFN (0: its gate/up launch does) */
 static int g_opt_flow = 0;   /* "flow": 1 runs the expert FFN as one sepia_mq_ffn launch (gate/up and down waves) */
 static int g_opt_flow_delay = 250;   /* "flow_delay": s_memrealtime ticks (10 ns) a flow workgroup without
                                       * gate/up units holds its down weights back */
@@ -924,6 +930,14 @@ int sepia_hip_set_option(const char *name, int value) {
     }
     if (strcmp(name, "fuse") == 0 && (value == 0 || value == 1)) {
         g_opt_fuse = value;
+        return 1;
+    }
+    if (strcmp(name, "mix") == 0 && (value == 0 || value == 1)) {
+        g_opt_mix = value;
+        return 1;
+    }
+    if (strcmp(name, "route_sel") == 0 && (value == 0 || value == 1)) {
+        g_opt_route_sel = value;
         return 1;
     }
     if (strcmp(name, "flow") == 0 && (value == 0 || value == 1)) {
@@ -1858,6 +1872,71 @@ static int mq_flow_launch(const char *op, const MoeProj *g, const MoeProj *u, co
     return 1;
 }
 
+/* The MoE decode's gate/up as one launch of sepia_mq_gateup_mix
+ * (kernels/mq_mix.h): MQ_CUS workgroups of 16 waves; wave 0 selects, waves
+ * 1..15 stream. Workgroup b takes shared units [b us / G, (b + 1) us / G)
+ * and routed units up to about T (b + 1) / G bytes in all (a unit: 16 rows
+ * of one slot's gate and up). Mirrors struct MqMixGeo. */
+typedef struct {
+    MqGeo gu;
+    uint32_t o_sel, o_ctl, o_gred, o_rings;
+    int32_t nstream;
+} MqMixGeo;
+static int64_t mq_mix_rbefore(int64_t us, int64_t ws, int64_t ur, int64_t wr, int64_t G, int64_t b) {
+    const int64_t T = us * ws + ur * wr;
+    const int64_t f = T * b / G - (b * us / G) * ws;
+    const int64_t r = f <= 0 ? 0 : f / wr;
+    return r < ur ? r : ur;
+}
+static int mq_mix_plan(const MoeProj *g, const MoeProj *sg, int32_t topk, int32_t n_shared, int64_t H, int64_t I,
+                       MqMixGeo *G, unsigned *threads, size_t *lds) {
+    if (!g_opt_mix || topk < 1 || H / 16 > 8 * 15 * 16 || I % 16) return 0;
+    const int64_t Gn = MQ_CUS, tiles_i = I / 16, us = (int64_t)n_shared * tiles_i, ur = (int64_t)topk * tiles_i;
+    const int64_t ws = n_shared > 0 ? 32 * (int64_t)sg->row_bytes : 0, wr = 32 * (int64_t)g->row_bytes;
+    const int64_t T = us * ws + ur * wr;
+    /* the routed split is monotone when no workgroup's shared units outweigh its byte share */
+    if (T / Gn < ws * ((us + Gn - 1) / Gn)) return 0;
+    int64_t nu_max = 1;
+    for (int64_t b = 0; b < Gn; b++) {
+        const int64_t ns = (b + 1) * us / Gn - b * us / Gn;
+        const int64_t nr = mq_mix_rbefore(us, ws, ur, wr, Gn, b + 1) - mq_mix_rbefore(us, ws, ur, wr, Gn, b);
+        if (nr < 0) return 0;
+        if (ns + nr > nu_max) nu_max = ns + nr;
+    }
+    int wmax = k_mq_words[mq_code(g->type)];
+    if (n_shared > 0 && k_mq_words[mq_code(sg->type)] > wmax) wmax = k_mq_words[mq_code(sg->type)];
+    const size_t wm = (size_t)wmax * 1024;
+    const int64_t nq = H / 1024;
+    memset(G, 0, sizeof *G);
+    size_t o = MQ_ZERO + mq_xq_bytes(H);
+    G->o_sel = (uint32_t)align256(o);
+    G->o_ctl = G->o_sel + MQ_FSEL_BYTES;
+    G->o_gred = G->o_ctl + 64;
+    int64_t best = -1;
+    for (int P = 1; P <= 15 && P <= nq; P++) {
+        if (g_opt_mq_p && P != g_opt_mq_p) continue;
+        const int C = g_opt_mq_c && g_opt_mq_c * P <= 15 ? g_opt_mq_c : 15 / P;
+        const size_t o_rings = align256((size_t)G->o_gred + (size_t)2 * nu_max * P * 64);
+        if (o_rings + (size_t)(P * C) * wm > g_lds_max) continue;
+        size_t ring = ((g_lds_max - o_rings) / (size_t)(P * C)) & ~(size_t)1023;
+        if (ring > 4 * wm) ring = 4 * wm;
+        const int64_t spw = ((2 * nu_max + C - 1) / C) * ((nq + P - 1) / P);
+        const int64_t S = (int64_t)(ring / wm);
+        const int64_t cost = spw * ((S >= 2 || spw == 1) ? 10 : 16);
+        if (best < 0 || cost < best) {
+            best = cost;
+            G->gu.P = P;
+            G->gu.ring = (int32_t)ring;
+            G->o_rings = (uint32_t)o_rings;
+            G->nstream = P * C;
+            *lds = o_rings + (size_t)(P * C) * ring;
+        }
+    }
+    if (best < 0) return 0;
+    *threads = 1024;
+    return 1;
+}
+
 /* The SwiGLU expert FFN over n_slots = topk + n_shared slots: routed slot s
  * uses expert sel_idx[s] (or fixed + s when sel_idx is NULL), then come the
  * shared experts. One slot without weights stores y; several slots add
@@ -1879,9 +1958,18 @@ static int ffn_launch(const char *op, const MoeProj *g, const MoeProj *u, const 
         MqRoute rt;
         memset(&rt, 0, sizeof rt);
         if (route) rt = *route;
-        void *a_gu[] = { (void *)g, (void *)u, (void *)sg, (void *)su, &sel_idx, &fixed, &topk, &inter32, &pl.gu_wps_r,
-                         &pl.gu_wps_s, &xdev, &h, &pl.gu_geo, &rt };
-        if (!launch_lds(K_MQ_GU, pl.gu_grid, pl.gu_threads, pl.gu_lds, a_gu, op)) return 0;
+        MqMixGeo mg;
+        unsigned mix_threads;
+        size_t mix_lds;
+        if (route && mq_mix_plan(g, sg, topk, n_shared, H, I, &mg, &mix_threads, &mix_lds)) {
+            void *a_mx[] = { (void *)g, (void *)u, (void *)sg, (void *)su, &rt, &topk, &n_shared, &inter32, &xdev, &h,
+                             &mg };
+            if (!launch_lds(K_MQ_GU_MIX, MQ_CUS, mix_threads, mix_lds, a_mx, op)) return 0;
+        } else {
+            void *a_gu[] = { (void *)g, (void *)u, (void *)sg, (void *)su, &sel_idx, &fixed, &topk, &inter32,
+                             &pl.gu_wps_r, &pl.gu_wps_s, &xdev, &h, &pl.gu_geo, &rt };
+            if (!launch_lds(K_MQ_GU, pl.gu_grid, pl.gu_threads, pl.gu_lds, a_gu, op)) return 0;
+        }
         void *a_dn[] = { (void *)d, (void *)sd, &sel_idx, &sel_w, &fixed, &topk, &n_shared, &inter32, &hid, &h, &ydev,
                          &pl.dn_geo, &pl.dn_wps_r, &pl.dn_wps_s, &ypart, &cnt };
         return launch_lds(K_MQ_DN, pl.dn_grid, pl.dn_threads, pl.dn_lds, a_dn, op);
@@ -2007,7 +2095,7 @@ int sepia_gpu_moe_decode(const SepiaMoeLayerDesc *L, SepiaGpuBuf *x, SepiaGpuBuf
     /* with the matrix-core FFN the gate/up launch selects from the logits;
      * otherwise the router's last workgroup does */
     MqFfnPlan pl;
-    const int in_kernel = mq_ffn_plan(&g, &u, &d, &sg, &su, &sd, tk, ns, H, I, &pl);
+    const int in_kernel = !g_opt_route_sel && mq_ffn_plan(&g, &u, &d, &sg, &su, &sd, tk, ns, H, I, &pl);
     int32_t select = !in_kernel;
     void *a_route[] = { &rw, &ld, &rb, &x->dev, &hid, &nr, &ns, &tk, &rs, &gsc, &logits, &sel_idx, &sel_w, &counter,
                         &select };

@@ -481,9 +481,10 @@ def test_matvec_mq_vector_paths(dev, orc, mq_vector, t, out_dim, in_dim):
         assert n.count(MQ_NAMES[t]) == 1
 
 
-def make_layer(dev, rng, hidden, inter, n_routed, n_shared, tg, tu, td, ts, rw_off=0):
+def make_layer(dev, rng, hidden, inter, n_routed, n_shared, tg, tu, td, ts, rw_off=0, topk=6):
     """Shared buffers with seeded host data; returns (desc, spec, keep). The
-    router matrix starts rw_off bytes into its buffer."""
+    router matrix starts rw_off bytes into its buffer. Without shared experts
+    their buffers hold a placeholder (never read)."""
     gate = [synth.random_matrix(tg, inter, hidden, rng) for _ in range(n_routed)]
     up = [synth.random_matrix(tu, inter, hidden, rng) for _ in range(n_routed)]
     down = [synth.random_matrix(td, hidden, inter, rng) for _ in range(n_routed)]
@@ -492,20 +493,20 @@ def make_layer(dev, rng, hidden, inter, n_routed, n_shared, tg, tu, td, ts, rw_o
     sd = [synth.random_matrix(ts, hidden, inter, rng) for _ in range(n_shared)]
     rw = (rng.standard_normal((n_routed + n_shared, hidden)) * 0.02).astype(np.float32)
     rb = rng.uniform(-0.1, 0.1, n_routed).astype(np.float32)
-    bufs = {k: dev.shared_from(np.concatenate(v)) for k, v in
+    bufs = {k: dev.shared_from(np.concatenate(v) if v else np.zeros(256, np.uint8)) for k, v in
             dict(gate=gate, up=up, down=down, s_gate=sg, s_up=su, s_down=sd).items()}
     bufs["rw"] = dev.alloc(rw.nbytes + rw_off)
     dev.upload(bufs["rw"], rw, offset=rw_off)
     bufs["rb"] = dev.shared_from(rb)
     d = hip.MoeLayerDesc()
-    d.hidden, d.inter, d.n_routed, d.n_shared, d.topk = hidden, inter, n_routed, n_shared, 6
+    d.hidden, d.inter, d.n_routed, d.n_shared, d.topk = hidden, inter, n_routed, n_shared, topk
     d.route_scale, d.global_scale = 8.0, 1.0
     d.router_w, d.router_bias = bufs["rw"], bufs["rb"]
     d.router_w_off = rw_off
     for name, t, lst in (("gate", tg, gate), ("up", tu, up), ("down", td, down),
                          ("s_gate", ts, sg), ("s_up", ts, su), ("s_down", ts, sd)):
-        setattr(d, name, hip.ExpertTensor(bufs[name], 0, lst[0].nbytes, t))
-    spec = dict(hidden=hidden, inter=inter, n_routed=n_routed, n_shared=n_shared, topk=6, route_scale=8.0,
+        setattr(d, name, hip.ExpertTensor(bufs[name], 0, lst[0].nbytes if lst else 0, t))
+    spec = dict(hidden=hidden, inter=inter, n_routed=n_routed, n_shared=n_shared, topk=topk, route_scale=8.0,
                 global_scale=1.0, router_w=rw, router_bias=rb, t_gate=tg, t_up=tu, t_down=td,
                 ts_gate=ts, ts_up=ts, ts_down=ts, gate=gate, up=up, down=down, s_gate=sg, s_up=su, s_down=sd)
     return d, spec, bufs
@@ -647,6 +648,35 @@ def test_moe_decode_fused(dev, orc, fuse, types):
             assert_close(y, y_ref, what="moe fuse=%d rep %d" % (fuse, rep), gate=False)
     finally:
         dev.L.sepia_hip_set_option(b"fuse", 0)
+    for b in bufs.values():
+        dev.free(b)
+
+
+@pytest.mark.parametrize("types,n_routed,n_shared,topk",
+                         [((10, 10, 11, 12), 16, 2, 6), ((12, 12, 12, 10), 16, 2, 6), ((11, 11, 10, 11), 16, 2, 6),
+                          ((10, 10, 11, 12), 16, 0, 6), ((10, 10, 11, 12), 8, 1, 1)],
+                         ids=["q2k_q3k_q4k", "q4k_q4k_q2k", "q3k_q2k_q3k", "no_shared", "top1"])
+def test_moe_decode_mix(dev, orc, types, n_routed, n_shared, topk):
+    """The gate/up launch that streams shared units while wave 0 selects
+    (sepia_mq_gateup_mix) gives the oracle's result, twice in a row."""
+    rng = np.random.default_rng(9100 + types[0] + n_shared + topk)
+    tg, tu, td, ts = types
+    desc, spec, bufs = make_layer(dev, rng, hidden=6144, inter=3072, n_routed=n_routed, n_shared=n_shared,
+                                  tg=tg, tu=tu, td=td, ts=ts, topk=topk)
+    assert dev.L.sepia_hip_set_option(b"mix", 1) == 1
+    try:
+        for rep in range(2):
+            x = synth.normal_vector(rng, 6144)
+            with Launches(dev) as n:
+                y, idx, w = run_moe(dev, desc, x)
+                assert n.count("sepia_mq_gateup_mix") == 1
+            y_ref, logits, idx_ref, w_ref = orc.moe_layer(spec, x, threads=THREADS)
+            chosen = check_route(orc, spec, logits, idx, w)
+            if chosen != list(idx_ref):
+                y_ref, _, _, _ = orc.moe_layer(spec, x, force_idx=chosen, threads=THREADS)
+            assert_close(y, y_ref, what="moe mix rep %d" % rep, gate=False)
+    finally:
+        dev.L.sepia_hip_set_option(b"mix", 0)
     for b in bufs.values():
         dev.free(b)
 
