@@ -124,7 +124,9 @@ void *sepia_hip_stream(void);
  *                 workgroup streams shared-expert rows while its wave 0
  *                 selects, then routed rows (default 0);
  *   "route_sel" 0/1  the router launch's last workgroup selects the experts
- *                 even for the matrix-core FFN (default 0: gate/up selects). */
+ *                 even for the matrix-core FFN (default 0: gate/up selects);
+ *   "dnrows" 0/1  the MoE decode's down as sepia_mq_down_rows: every slot of
+ *                 a row group in one workgroup, summed in LDS (default 0). */
 int sepia_hip_set_option(const char *name, int value);
 
 #ifdef __cplusplus

@@ -225,6 +225,7 @@ SEPIA_FFN_PAIR(4, 4, ST_Q4_K, ST_Q4_K)
 #include "mq_fused.h"
 #include "mq_flow.h"
 #include "mq_mix.h"
+#include "mq_rows.h"
 #include "moe.h"
 #include "prefill.h"
 #include "synth.h"
@@ -241,3 +242,4 @@ SEPIA_MQ_DOWN()
 SEPIA_MQ_FUSED()
 SEPIA_MQ_FLOW()
 SEPIA_MQ_MIX()
+SEPIA_MQ_ROWS()

@@ -63,6 +63,8 @@ enum {
     K_MQ_FFN,
     /* MoE gate/up with the selection behind shared-expert streaming (kernels/mq_mix.h) */
     K_MQ_GU_MIX,
+    /* MoE down with every slot of a row group in one workgroup (kernels/mq_rows.h) */
+    K_MQ_DN_ROWS,
     K_COUNT
 };
 #define FFN_NAMES(p) "sepia_ffn_gateup_" p, "sepia_ffn_gateup_" p "_xp", "sepia_ffn_down_" p
@@ -85,7 +87,7 @@ static const char *const k_names[K_COUNT] = {
     "sepia_mq_mv_q2_k", "sepia_mq_mv_q3_k", "sepia_mq_mv_q4_k", "sepia_mq_mv_iq2_xs", "sepia_mq_mv_iq3_xxs",
     "sepia_mq_gateup", "sepia_mq_down", "sepia_mq_moe",
     "sepia_pf_route", "sepia_pf_select", "sepia_pf_group", "sepia_pf_gateup", "sepia_pf_down", "sepia_pf_combine",
-    "sepia_pf_split", "sepia_mq_ffn", "sepia_mq_gateup_mix",
+    "sepia_pf_split", "sepia_mq_ffn", "sepia_mq_gateup_mix", "sepia_mq_down_rows",
 };
 #undef FFN_NAMES
 
@@ -138,6 +140,8 @@ static int g_opt_mq_x = 0;   /* "mq_x": 0 = planner's choice, 1 = vector from gl
 static int g_opt_fuse = 0;   /* sepia_hip_set_option("fuse", 1) runs the MoE layer / expert FFN as one launch */
 static int g_opt_mix = 0;    /* "mix": 1 runs the MoE decode's gate/up as sepia_mq_gateup_mix (every workgroup
                               * streams shared units while its wave 0 selects, then routed ones) */
+static int g_opt_dnrows = 0; /* "dnrows": 1 runs the MoE decode's down as sepia_mq_down_rows (all slots of
+                              * a row group in one workgroup, summed in LDS) */
 static int g_opt_route_sel = 0;   /* "route_sel": 1 = the router launch's last workgroup selects the
                                    * experts even for the matrix-core FFN (0: its gate/up launch does) */
 static int g_opt_flow = 0;   /* "flow": 1 runs the expert FFN as one sepia_mq_ffn launch (gate/up and down waves) */
@@ -934,6 +938,10 @@ int sepia_hip_set_option(const char *name, int value) {
     }
     if (strcmp(name, "mix") == 0 && (value == 0 || value == 1)) {
         g_opt_mix = value;
+        return 1;
+    }
+    if (strcmp(name, "dnrows") == 0 && (value == 0 || value == 1)) {
+        g_opt_dnrows = value;
         return 1;
     }
     if (strcmp(name, "route_sel") == 0 && (value == 0 || value == 1)) {
@@ -1937,6 +1945,65 @@ static int mq_mix_plan(const MoeProj *g, const MoeProj *sg, int32_t topk, int32_
     return 1;
 }
 
+/* The MoE decode's down as one launch of sepia_mq_down_rows
+ * (kernels/mq_rows.h): MQ_CUS workgroups of 16 waves; workgroup b owns row
+ * groups [b T / G, (b + 1) T / G) of every slot, with every slot's XQ(h) in
+ * its LDS; routed and shared rows stream on their own waves at once. The
+ * split of waves and ring stages: the fewest steps for the busier role, then
+ * the most stages. Mirrors struct MqRowsGeo. */
+typedef struct {
+    MqGeo gr, gs;
+    int32_t nwr, nws;
+    uint32_t o_red, o_rings_s;
+} MqRowsGeo;
+static int mq_rows_plan(const MoeProj *d, const MoeProj *sd, int32_t topk, int32_t n_shared, int64_t H, int64_t I,
+                        MqRowsGeo *G, unsigned *threads, size_t *lds) {
+    const int n_slots = topk + n_shared;
+    if (!g_opt_dnrows || topk < 1 || n_slots < 2 || topk > 64 || H % 16 || (I / 16) * n_slots > 4 * 1024) return 0;
+    const int64_t T = H / 16, nrg = (T + MQ_CUS - 1) / MQ_CUS, nq = I / 1024;
+    const int kd = mq_code(d->type), ks = n_shared > 0 ? mq_code(sd->type) : kd;
+    const size_t wr1 = (size_t)k_mq_words[kd] * 1024, ws1 = (size_t)k_mq_words[ks] * 1024;
+    const size_t xq_all = (size_t)n_slots * 4 * (size_t)I;
+    int64_t best = -1, best_fl = 0;
+    memset(G, 0, sizeof *G);
+    for (int Pr = 1; Pr <= 16 && Pr <= nq; Pr++)
+        for (int Cr = 1; Pr * Cr <= 16 && Cr <= topk * nrg; Cr++)
+            for (int Ps = 1; Ps <= nq; Ps++)
+                for (int Cs = (n_shared > 0 ? 1 : 0); Pr * Cr + Ps * Cs <= 16 && Cs <= n_shared * nrg; Cs++) {
+                    const int nwr = Pr * Cr, nws = Ps * Cs;
+                    const size_t o_red = align256(MQ_ZERO + xq_all + 256);   /* the experts just below */
+                    const size_t o_rings =
+                        align256(o_red + (size_t)topk * nrg * Pr * 64 + (size_t)n_shared * nrg * Ps * 64);
+                    const size_t avail = g_lds_max;
+                    if (o_rings + (size_t)nwr * wr1 + (size_t)nws * ws1 > avail) continue;
+                    const int64_t spw_r = ((topk * nrg + Cr - 1) / Cr) * ((nq + Pr - 1) / Pr);
+                    const int64_t spw_s = Cs ? ((n_shared * nrg + Cs - 1) / Cs) * ((nq + Ps - 1) / Ps) : 0;
+                    /* stages: as many as the LDS holds, the same number for both roles */
+                    int64_t S = 4;
+                    while (S > 1 && o_rings + (size_t)nwr * S * wr1 + (size_t)nws * S * ws1 > avail) S--;
+                    const int64_t spw = spw_r > spw_s ? spw_r : spw_s;
+                    const int64_t cost = spw * ((S >= 2 || spw == 1) ? 10 : 16);
+                    const int64_t fl = (int64_t)(nwr + nws) * S;
+                    if (best < 0 || cost < best || (cost == best && fl > best_fl)) {
+                        best = cost;
+                        best_fl = fl;
+                        G->gr.P = Pr;
+                        G->gr.ring = (int32_t)(S * wr1);
+                        G->gr.orings = (int32_t)o_rings;
+                        G->gs.P = Ps;
+                        G->gs.ring = (int32_t)(S * ws1);
+                        G->nwr = nwr;
+                        G->nws = nws;
+                        G->o_red = (uint32_t)o_red;
+                        G->o_rings_s = (uint32_t)(o_rings + (size_t)nwr * S * wr1);
+                        *lds = G->o_rings_s + (size_t)nws * S * ws1;
+                    }
+                }
+    if (best < 0) return 0;
+    *threads = 1024;
+    return 1;
+}
+
 /* The SwiGLU expert FFN over n_slots = topk + n_shared slots: routed slot s
  * uses expert sel_idx[s] (or fixed + s when sel_idx is NULL), then come the
  * shared experts. One slot without weights stores y; several slots add
@@ -1969,6 +2036,13 @@ static int ffn_launch(const char *op, const MoeProj *g, const MoeProj *u, const 
             void *a_gu[] = { (void *)g, (void *)u, (void *)sg, (void *)su, &sel_idx, &fixed, &topk, &inter32,
                              &pl.gu_wps_r, &pl.gu_wps_s, &xdev, &h, &pl.gu_geo, &rt };
             if (!launch_lds(K_MQ_GU, pl.gu_grid, pl.gu_threads, pl.gu_lds, a_gu, op)) return 0;
+        }
+        MqRowsGeo rg;
+        unsigned rows_threads;
+        size_t rows_lds;
+        if (sel_idx && sel_w && mq_rows_plan(d, sd, topk, n_shared, H, I, &rg, &rows_threads, &rows_lds)) {
+            void *a_rw[] = { (void *)d, (void *)sd, &sel_idx, &sel_w, &topk, &n_shared, &inter32, &hid, &h, &ydev, &rg };
+            return launch_lds(K_MQ_DN_ROWS, MQ_CUS, rows_threads, rows_lds, a_rw, op);
         }
         void *a_dn[] = { (void *)d, (void *)sd, &sel_idx, &sel_w, &fixed, &topk, &n_shared, &inter32, &hid, &h, &ydev,
                          &pl.dn_geo, &pl.dn_wps_r, &pl.dn_wps_s, &ypart, &cnt };

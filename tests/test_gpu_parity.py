@@ -656,27 +656,31 @@ def test_moe_decode_fused(dev, orc, fuse, types):
                          [((10, 10, 11, 12), 16, 2, 6), ((12, 12, 12, 10), 16, 2, 6), ((11, 11, 10, 11), 16, 2, 6),
                           ((10, 10, 11, 12), 16, 0, 6), ((10, 10, 11, 12), 8, 1, 1)],
                          ids=["q2k_q3k_q4k", "q4k_q4k_q2k", "q3k_q2k_q3k", "no_shared", "top1"])
-def test_moe_decode_mix(dev, orc, types, n_routed, n_shared, topk):
+@pytest.mark.parametrize("opt", ["mix", "dnrows"])
+def test_moe_decode_mix(dev, orc, types, n_routed, n_shared, topk, opt):
     """The gate/up launch that streams shared units while wave 0 selects
-    (sepia_mq_gateup_mix) gives the oracle's result, twice in a row."""
+    (sepia_mq_gateup_mix), and the down launch with every slot of a row group
+    in one workgroup (sepia_mq_down_rows), give the oracle's result, twice in
+    a row."""
     rng = np.random.default_rng(9100 + types[0] + n_shared + topk)
     tg, tu, td, ts = types
     desc, spec, bufs = make_layer(dev, rng, hidden=6144, inter=3072, n_routed=n_routed, n_shared=n_shared,
                                   tg=tg, tu=tu, td=td, ts=ts, topk=topk)
-    assert dev.L.sepia_hip_set_option(b"mix", 1) == 1
+    kname = {"mix": "sepia_mq_gateup_mix", "dnrows": "sepia_mq_down_rows"}[opt]
+    assert dev.L.sepia_hip_set_option(opt.encode(), 1) == 1
     try:
         for rep in range(2):
             x = synth.normal_vector(rng, 6144)
             with Launches(dev) as n:
                 y, idx, w = run_moe(dev, desc, x)
-                assert n.count("sepia_mq_gateup_mix") == 1
+                assert n.count(kname) == 1
             y_ref, logits, idx_ref, w_ref = orc.moe_layer(spec, x, threads=THREADS)
             chosen = check_route(orc, spec, logits, idx, w)
             if chosen != list(idx_ref):
                 y_ref, _, _, _ = orc.moe_layer(spec, x, force_idx=chosen, threads=THREADS)
-            assert_close(y, y_ref, what="moe mix rep %d" % rep, gate=False)
+            assert_close(y, y_ref, what="moe %s rep %d" % (opt, rep), gate=False)
     finally:
-        dev.L.sepia_hip_set_option(b"mix", 0)
+        dev.L.sepia_hip_set_option(opt.encode(), 0)
     for b in bufs.values():
         dev.free(b)
 
