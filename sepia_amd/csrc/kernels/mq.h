@@ -903,8 +903,10 @@ struct MqItem {
 // last conv waves of the workgroup DMA the vector straight into its XQ
 // place and convert it there while the others stream and decode their
 // first step; xraw is then the LDS offset of 16 bytes of control words.
+// dyn: the steps are dealt at run time (MqDyn; P is then the quads per
+// row, the partials' count per item).
 struct MqGeo {
-    int32_t P, ring, xraw, orings, conv;
+    int32_t P, ring, xraw, orings, conv, dyn;
 };
 
 // The pipeline of one wave over n_items items of format T, in two halves:
@@ -1107,6 +1109,141 @@ struct MqWave {
                 acc = 0.0f;
                 ++ck;
             }
+            if (++cslot == S) cslot = 0;
+        }
+    }
+};
+
+// The same pipeline with the steps dealt at run time: the workgroup's
+// steps (item i, quad q) are numbered i * nq + q, and each wave takes the
+// next number from an LDS counter whenever it refills a ring slot, so that a
+// wave whose bytes arrive early takes more steps (with one step in flight
+// per wave, fixed shares make the slowest wave's chain of round trips the
+// workgroup's time). Every step writes its own 16 row partials to
+// red[(i * nq + q) * 16 ..]: mq_red_sum(red, i, nq, t) sums them in quad
+// order whichever waves ran them, so the result does not depend on the
+// schedule. Waves first .. first + count - 1 take part; ctr: an LDS word,
+// zero before the workgroup's first barrier of the run.
+template <int T, class ItemFn>
+struct MqDyn {
+    static constexpr int W = MQ<T>::W, Wp = MQ<T>::Wp;
+    const ItemFn &item_of;
+    int total, nq, n;
+    uint32_t rb;
+    int S;
+    uint32_t ring;
+    const uint8_t *ringp;
+    uint32_t *ctr;
+    MqLane L;
+    bool on;
+    // the step in ring slot k (-1: none), as four scalars: a private array
+    // indexed at run time would live in scratch memory, whose loads count
+    // in vmcnt and would upset the DMA waits
+    int ss0, ss1, ss2, ss3;
+    __device__ __forceinline__ int sget(int k) const { return k == 0 ? ss0 : k == 1 ? ss1 : k == 2 ? ss2 : ss3; }
+    __device__ __forceinline__ void sset(int k, int v) {
+        ss0 = k == 0 ? v : ss0;
+        ss1 = k == 1 ? v : ss1;
+        ss2 = k == 2 ? v : ss2;
+        ss3 = k == 3 ? v : ss3;
+    }
+    int islot;
+    const uint8_t *tab = nullptr;
+    __device__ __forceinline__ MqDyn(const ItemFn &f, int n_items, int nq_, int n_, uint32_t rb_, MqGeo geo,
+                                     uint8_t *ring_lds, uint32_t *ctr_, int first = 0, int count = -1)
+        : item_of(f), total(n_items * nq_), nq(nq_), n(n_), rb(rb_), ctr(ctr_) {
+        const int w = mq_wave_id(), wk = w - first;
+        const int nw = count >= 0 ? count : (int)(blockDim.x >> 6) - first;
+        on = wk >= 0 && wk < nw;
+        S = geo.ring / (Wp * 1024);
+        S = S < 4 ? S : 4;
+        ringp = ring_lds + (ptrdiff_t)wk * geo.ring;
+        ring = mq_lds_addr(ringp);
+        L = mq_lane();
+        islot = 0;
+        ss0 = ss1 = ss2 = ss3 = -1;
+    }
+    // Takes the next step into ring slot islot (none once they are all dealt).
+    __device__ __forceinline__ void issue() {
+        uint32_t st = 0;
+        if (L.lane == 0) st = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        const int step = __builtin_amdgcn_readfirstlane((int)st);
+        const int k = islot;
+        if (++islot == S) islot = 0;
+        if (step >= total) {
+            sset(k, -1);
+            return;
+        }
+        sset(k, step);
+        const int item = step / nq, qd = step - item * nq;
+        const MqItem it = item_of(item);
+        const uint32_t q4 = 4u * (uint32_t)qd;
+        const uint32_t dst = ring + (uint32_t)k * (uint32_t)(Wp * 1024);
+        const uint32_t rmax = (uint32_t)(it.rows - 1 - it.row0);
+        const uint32_t rbase = (uint32_t)it.row0 * rb;
+#pragma unroll
+        for (int d = 0; d < Wp; d++) {
+            const uint32_t i = 64u * (uint32_t)d + (uint32_t)L.lane;
+            const uint32_t cl = i / (uint32_t)Wp, kk = i - cl * (uint32_t)Wp;
+            const uint32_t j = cl & 15u, r = j < rmax ? j : rmax;
+            const uint32_t boff = (uint32_t)MQ<T>::bytes * (q4 + (cl >> 4));
+            const uint32_t off = rbase + r * rb + boff - MQ<T>::shift(boff) + MQ<T>::word(kk < (uint32_t)W ? kk : W - 1);
+            mq_dma16(it.base, off, dst + 1024u * (uint32_t)d);
+        }
+    }
+    __device__ __forceinline__ void prologue() {
+        if (!on) return;
+        for (int t = 0; t < S; t++) issue();
+    }
+    // The vector by LDS DMA into a raw copy (geo.xraw), ahead of the
+    // weights, then converted once it has landed (as MqWave::start); the
+    // step counter is zeroed before the barrier that precedes any step.
+    __device__ __forceinline__ void start(const float *src, const MqGeo &geo, uint8_t *lds0, uint32_t xoff) {
+        mq_dma_vec(src, n, mq_lds_addr(lds0 + geo.xraw));
+        if (threadIdx.x == 0) *ctr = 0u;
+        __builtin_amdgcn_s_waitcnt(MQ_WC_LGKM0);
+        __builtin_amdgcn_s_barrier();
+        prologue();
+        int c = 0;
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+            if (k < S && sget(k) >= 0) c++;
+        mq_wait_stages<Wp>(c);   // this wave's vector DMAs (older than its weights)
+        __syncthreads();
+        mq_stage_xq_lds((const float *)(lds0 + geo.xraw), n, lds0, xoff);
+    }
+    // Stages in flight after slot k, counted in ring order.
+    __device__ __forceinline__ int after(int k) const {
+        int c = 0;
+#pragma unroll
+        for (int d = 1; d < 4; d++)
+            if (d < S && sget((k + d) % S) >= 0) c++;
+        return c;
+    }
+    __device__ __forceinline__ void run(const uint8_t *lds0, float *red) {
+        if (!on) return;
+        int cslot = 0;
+        while (sget(cslot) >= 0) {
+            const int step = sget(cslot);
+            mq_wait_stages<Wp>(after(cslot));
+            uint4 w[W];
+            const uint8_t *src = ringp + (size_t)cslot * (Wp * 1024) + 16 * Wp * L.lane;
+#pragma unroll
+            for (int k = 0; k < W; k++) w[k] = *(const uint4 *)(src + 16 * k);
+            __builtin_amdgcn_s_waitcnt(MQ_WC_LGKM0);
+            islot = cslot;
+            issue();   // refills this slot (or marks it empty)
+            const int item = step / nq, qd = step - item * nq;
+            const MqItem it = item_of(item);
+            const uint32_t b = 4u * (uint32_t)qd + (uint32_t)L.g;
+            MqCtx x;
+            x.lds0 = lds0;
+            x.abase = L.a_lane ? it.xoff + MQ_BREC * b + 16u * (uint32_t)L.p : 0u;
+            x.xsb = (const float *)(lds0 + it.xoff + mq_xq_planes(n)) + 16u * b;
+            x.gvb = x.xsb + MQ<T>::sum_sel * (n >> 4);
+            x.tab = tab;
+            const float acc = mq_sum_units(MQ<T>::block(w, MQ<T>::shift((uint32_t)MQ<T>::bytes * b), x));
+            if (L.lane < 16) red[((int64_t)it.red * nq + qd) * 16 + L.lane] = acc;
             if (++cslot == S) cslot = 0;
         }
     }
@@ -1319,6 +1456,14 @@ __device__ __forceinline__ void mq_dn_slot(const uint8_t *Wd, uint64_t row_bytes
         it.red = i;
         return it;
     };
+    if (geo.dyn) {
+        // the step counter sits after the arrival flags (host slack)
+        uint32_t *ctr = (uint32_t *)((uint8_t *)red + (size_t)nk * geo.P * 64 + (size_t)nk * 4);
+        MqDyn<T, decltype(item_of)> dw(item_of, nk, nb >> 2, inter, (uint32_t)row_bytes, geo, rings, ctr);
+        dw.start(hs, geo, lds0, MQ_ZERO);
+        dw.run(lds0, red);
+        return;
+    }
     MqWave<T, decltype(item_of)> wv(item_of, nk, nb >> 2, inter, (uint32_t)row_bytes, geo, rings, 0,
                                     (int)(blockDim.x >> 6) - geo.conv);
     wv.go(hs, geo, lds0, MQ_ZERO, red);

@@ -142,6 +142,7 @@ static int g_opt_mix = 0;    /* "mix": 1 runs the MoE decode's gate/up as sepia_
                               * streams shared units while its wave 0 selects, then routed ones) */
 static int g_opt_dnrows = 0; /* "dnrows": 1 runs the MoE decode's down as sepia_mq_down_rows (all slots of
                               * a row group in one workgroup, summed in LDS) */
+static int g_opt_dyn = 0;    /* "dyn": 1 deals the MoE down launch's steps at run time (MqDyn) */
 static int g_opt_route_sel = 0;   /* "route_sel": 1 = the router launch's last workgroup selects the
                                    * experts even for the matrix-core FFN (0: its gate/up launch does) */
 static int g_opt_flow = 0;   /* "flow": 1 runs the expert FFN as one sepia_mq_ffn launch (gate/up and down waves) */
@@ -944,6 +945,10 @@ int sepia_hip_set_option(const char *name, int value) {
         g_opt_dnrows = value;
         return 1;
     }
+    if (strcmp(name, "dyn") == 0 && (value == 0 || value == 1)) {
+        g_opt_dyn = value;
+        return 1;
+    }
     if (strcmp(name, "route_sel") == 0 && (value == 0 || value == 1)) {
         g_opt_route_sel = value;
         return 1;
@@ -987,7 +992,7 @@ int sepia_hip_set_option(const char *name, int value) {
 #define MQ_CUS 256                  /* MI355X compute units */
 #define MQ_ZERO 768
 typedef struct {
-    int32_t P, ring, xraw, orings, conv;   /* as struct MqGeo in kernels/mq.h */
+    int32_t P, ring, xraw, orings, conv, dyn;   /* as struct MqGeo in kernels/mq.h */
 } MqGeo;
 /* In-kernel selection by the gate/up launch (struct MqRoute in
  * kernels/mq.h); logits NULL: the experts come from sel_idx. */
@@ -1085,10 +1090,47 @@ static int mq_geo(int mc, int wmax, int64_t n_items, int64_t nq, size_t fixed, s
                     geo->xraw = mode ? (int32_t)o_raw : 0;
                     geo->orings = (int32_t)base;
                     geo->conv = cv;
+                    geo->dyn = 0;
                     *threads = 64u * (unsigned)(nw + cv);
                     *lds = base + (size_t)nw * ring;
                 }
             }
+        }
+    }
+    return found;
+}
+
+/* mq_geo for a launch whose steps are dealt at run time (MqDyn): every
+ * quad of an item has its partial (P = nq), the vector comes by LDS DMA
+ * into a raw copy, and the waves and ring stages give the most steps in
+ * flight (then the most waves). */
+static int mq_geo_dyn(int mc, int wmax, int64_t n_items, int64_t nq, size_t fixed, size_t raw_bytes, unsigned *threads,
+                      MqGeo *geo, size_t *lds) {
+    if (raw_bytes == 0 || nq > 16) return 0;
+    const size_t w1 = (size_t)k_mq_words[mc] * 1024, wm = (size_t)wmax * 1024;
+    const size_t o_raw = align256(fixed + (size_t)n_items * nq * 64);
+    const size_t base = align256(o_raw + raw_bytes);
+    int64_t best = -1;
+    int found = 0;
+    for (int nw = 16; nw >= 1; nw--) {
+        if (base + (size_t)nw * wm > g_lds_max) continue;
+        size_t ring = ((g_lds_max - base) / (size_t)nw) & ~(size_t)1023;
+        if (ring > 4 * wm) ring = 4 * wm;
+        int64_t S = (int64_t)(ring / w1);
+        if (S > 4) S = 4;
+        int64_t fl = (int64_t)nw * S;
+        if (fl > n_items * nq) fl = n_items * nq;
+        if (fl > best) {
+            best = fl;
+            found = 1;
+            geo->P = (int32_t)nq;
+            geo->ring = (int32_t)ring;
+            geo->xraw = (int32_t)o_raw;
+            geo->orings = (int32_t)base;
+            geo->conv = 0;
+            geo->dyn = 1;
+            *threads = 64u * (unsigned)nw;
+            *lds = base + (size_t)nw * ring;
         }
     }
     return found;
@@ -1380,8 +1422,10 @@ static int mq_ffn_plan(const MoeProj *g, const MoeProj *u, const MoeProj *d, con
     if (!mq_geo(kg, wgu, 2 * nk_gu, H / 1024, MQ_ZERO + mq_xq_bytes(H) + MQ_SEL_BYTES, (size_t)H * 4, &pl->gu_threads,
                 &pl->gu_geo, &pl->gu_lds))
         return 0;
-    if (!mq_geo(kd, wdn, nk_dn, I / 1024, MQ_ZERO + mq_xq_bytes(I) + (size_t)nk_dn * 4 + 256, (size_t)I * 4,
-                &pl->dn_threads, &pl->dn_geo, &pl->dn_lds))
+    const size_t dn_fixed = MQ_ZERO + mq_xq_bytes(I) + (size_t)nk_dn * 4 + 256;
+    if (!(g_opt_dyn && !g_opt_mq_x && mq_geo_dyn(kd, wdn, nk_dn, I / 1024, dn_fixed, (size_t)I * 4, &pl->dn_threads,
+                                                 &pl->dn_geo, &pl->dn_lds)) &&
+        !mq_geo(kd, wdn, nk_dn, I / 1024, dn_fixed, (size_t)I * 4, &pl->dn_threads, &pl->dn_geo, &pl->dn_lds))
         return 0;
     pl->gu_grid = (unsigned)(topk * pl->gu_wps_r + n_shared * pl->gu_wps_s);
     pl->dn_grid = (unsigned)(topk * pl->dn_wps_r + n_shared * pl->dn_wps_s);

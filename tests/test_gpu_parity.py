@@ -656,17 +656,17 @@ def test_moe_decode_fused(dev, orc, fuse, types):
                          [((10, 10, 11, 12), 16, 2, 6), ((12, 12, 12, 10), 16, 2, 6), ((11, 11, 10, 11), 16, 2, 6),
                           ((10, 10, 11, 12), 16, 0, 6), ((10, 10, 11, 12), 8, 1, 1)],
                          ids=["q2k_q3k_q4k", "q4k_q4k_q2k", "q3k_q2k_q3k", "no_shared", "top1"])
-@pytest.mark.parametrize("opt", ["mix", "dnrows"])
+@pytest.mark.parametrize("opt", ["mix", "dnrows", "dyn"])
 def test_moe_decode_mix(dev, orc, types, n_routed, n_shared, topk, opt):
     """The gate/up launch that streams shared units while wave 0 selects
-    (sepia_mq_gateup_mix), and the down launch with every slot of a row group
-    in one workgroup (sepia_mq_down_rows), give the oracle's result, twice in
-    a row."""
+    (sepia_mq_gateup_mix), the down launch with every slot of a row group in
+    one workgroup (sepia_mq_down_rows) and the down launch whose steps are
+    dealt at run time (dyn) give the oracle's result, twice in a row."""
     rng = np.random.default_rng(9100 + types[0] + n_shared + topk)
     tg, tu, td, ts = types
     desc, spec, bufs = make_layer(dev, rng, hidden=6144, inter=3072, n_routed=n_routed, n_shared=n_shared,
                                   tg=tg, tu=tu, td=td, ts=ts, topk=topk)
-    kname = {"mix": "sepia_mq_gateup_mix", "dnrows": "sepia_mq_down_rows"}[opt]
+    kname = {"mix": "sepia_mq_gateup_mix", "dnrows": "sepia_mq_down_rows", "dyn": "sepia_mq_down"}[opt]
     assert dev.L.sepia_hip_set_option(opt.encode(), 1) == 1
     try:
         for rep in range(2):
