@@ -126,7 +126,9 @@ void *sepia_hip_stream(void);
  *   "route_sel" 0/1  the router launch's last workgroup selects the experts
  *                 even for the matrix-core FFN (default 0: gate/up selects);
  *   "dnrows" 0/1  the MoE decode's down as sepia_mq_down_rows: every slot of
- *                 a row group in one workgroup, summed in LDS (default 0). */
+ *                 a row group in one workgroup, summed in LDS (default 0);
+ *   "dyn" 0/1     the FFN down launch deals its steps at run time from an
+ *                 LDS counter (default 0). */
 int sepia_hip_set_option(const char *name, int value);
 
 #ifdef __cplusplus
