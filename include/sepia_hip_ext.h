@@ -115,7 +115,9 @@ void *sepia_hip_stream(void);
  *                 planner's choice, 1 = loads from global memory, 2 = LDS
  *                 DMA issued ahead of the weight prologue, 3 = converter
  *                 waves (DMA into the XQ place, converted there while the
- *                 other waves decode their first step);
+ *                 other waves decode their first step; matvec launches
+ *                 only). The FFN down launch reads h in XQ form as the
+ *                 gate/up launch wrote it, whatever this says;
  *   "flow" 0/1    the expert FFN as one launch of sepia_mq_ffn, gate/up
  *                 and down waves side by side (default 0);
  *   "flow_delay"  ticks (10 ns) the flow launch's workgroups without
@@ -128,7 +130,9 @@ void *sepia_hip_stream(void);
  *   "dnrows" 0/1  the MoE decode's down as sepia_mq_down_rows: every slot of
  *                 a row group in one workgroup, summed in LDS (default 0);
  *   "dyn" 0/1     the FFN down launch deals its steps at run time from an
- *                 LDS counter (default 0). */
+ *                 LDS counter (default 0);
+ *   "hxq" 0/1     h crosses from the gate/up to the down launch in XQ form
+ *                 instead of f32 (default 0). */
 int sepia_hip_set_option(const char *name, int value);
 
 #ifdef __cplusplus

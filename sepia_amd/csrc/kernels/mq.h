@@ -905,8 +905,10 @@ struct MqItem {
 // first step; xraw is then the LDS offset of 16 bytes of control words.
 // dyn: the steps are dealt at run time (MqDyn; P is then the quads per
 // row, the partials' count per item).
+// xq_in: the vector arrives already in XQ form (written so by the previous
+// launch) and is only DMA'd into place.
 struct MqGeo {
-    int32_t P, ring, xraw, orings, conv, dyn;
+    int32_t P, ring, xraw, orings, conv, dyn, xq_in;
 };
 
 // The pipeline of one wave over n_items items of format T, in two halves:
@@ -1036,9 +1038,24 @@ struct MqWave {
     // the vector into XQ (at raised priority) while the others issue their
     // weights and decode their first step, and wait only for the XQ vector
     // to finish it; the converter waves return at once after. Every wave of
-    // the workgroup calls this.
+    // the workgroup calls this. CONV false compiles that path out (the host
+    // never plans it for such a kernel), which keeps the kernel's registers
+    // for its own pipeline. With geo.xq_in the vector is already XQ bytes:
+    // DMA'd straight into place, ahead of the weights.
+    template <bool CONV = true>
     __device__ __forceinline__ void go(const float *src, const MqGeo &geo, uint8_t *lds0, uint32_t xoff, float *red) {
-        if (geo.conv == 0) {
+        if (geo.xq_in) {
+            mq_dma_vec(src, n, mq_lds_addr(lds0 + xoff));
+            if (threadIdx.x < MQ_ZERO / 16) ((uint4 *)(lds0))[threadIdx.x] = make_uint4(0, 0, 0, 0);
+            __builtin_amdgcn_s_waitcnt(MQ_WC_LGKM0);
+            __builtin_amdgcn_s_barrier();
+            prologue();
+            wait_before_prologue();
+            __syncthreads();
+            run(lds0, red);
+            return;
+        }
+        if (!CONV || geo.conv == 0) {
             start(src, geo, lds0, xoff);
             run(lds0, red);
             return;
@@ -1058,7 +1075,9 @@ struct MqWave {
         }
         prologue();
         const uint32_t ready = 3u * (uint32_t)geo.conv;
-        if constexpr (MQ<T>::has_pre) {
+        if constexpr (!CONV) {
+            return;
+        } else if constexpr (MQ<T>::has_pre) {
             if (Tn > 0) {
                 const typename MQ<T>::Pre pr = pre_first();
                 mq_waves_wait(ctl, ready, L.lane, nullptr);
@@ -1329,7 +1348,7 @@ __device__ __forceinline__ int64_t mq_slot_expert(const int32_t *sel_idx, int32_
 template <int T>
 __device__ __forceinline__ void mq_gateup_slot(const uint8_t *Wg, const uint8_t *Wu, uint64_t row_bytes, int32_t nb,
                                                int32_t inter, int32_t j0, int32_t jstep, const float *__restrict__ x,
-                                               float *__restrict__ h, MqGeo geo, bool x_issued) {
+                                               float *__restrict__ h, MqGeo geo, bool x_issued, bool hxq) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int n = 256 * nb;
     const int tiles = (inter + 15) >> 4;
@@ -1349,8 +1368,37 @@ __device__ __forceinline__ void mq_gateup_slot(const uint8_t *Wg, const uint8_t 
     MqWave<T, decltype(item_of)> wv(item_of, 2 * nk, nb >> 2, n, (uint32_t)row_bytes, geo, rings, 0,
                                     (int)(blockDim.x >> 6) - geo.conv);
     wv.x_issued = x_issued;
-    wv.go(x, geo, smem, xoff, red);
+    wv.template go<false>(x, geo, smem, xoff, red);
     __syncthreads();
+    if (hxq) {
+        // h in XQ form for the down launch, in one pass: a row group is one
+        // 16-column segment of h (inter is a multiple of 16), four lanes a
+        // segment (lane j: rows 4j .. 4j + 3, mq_xq_quad); only the waves
+        // that own row groups (16 a wave), every quad the same iterations
+        const int j = (int)threadIdx.x & 3, per = (int)(blockDim.x >> 2);
+        float *xsv = (float *)((uint8_t *)h + mq_xq_planes(inter));
+        for (int k0 = 0; k0 < nk && 16 * mq_wave_id() < nk - k0; k0 += per) {
+            const int k = k0 + (int)(threadIdx.x >> 2), kk = k < nk ? k : nk - 1;
+            float a[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                a[i] = silu_f32(mq_red_sum(red, 2 * kk, geo.P, 4 * j + i)) * mq_red_sum(red, 2 * kk + 1, geo.P, 4 * j + i);
+            const XqQuad r = mq_xq_quad(a);
+            if (k < nk) {
+                const int64_t seg = (int64_t)j0 + (int64_t)k * jstep;
+                uint32_t *pl = (uint32_t *)((uint8_t *)h + (seg >> 4) * MQ_BREC + (seg & 15) * 48) + j;
+                pl[0] = r.p0;
+                pl[4] = r.p1;
+                pl[8] = r.p2;
+                if (j == 0) {
+                    xsv[seg] = r.xs;
+                    xsv[inter / 16 + seg] = r.gs;
+                    xsv[inter / 8 + seg] = r.gq;
+                }
+            }
+        }
+        return;
+    }
     for (int i = threadIdx.x; i < nk * 16; i += blockDim.x) {
         const int k = i >> 4, t = i & 15;
         const int64_t r = ((int64_t)j0 + (int64_t)k * jstep) * 16 + t;
@@ -1375,12 +1423,14 @@ struct MqRoute {
 // serve the routed slots, wps_r each (workgroup k: slot k / wps_r, row
 // groups k % wps_r, + wps_r, ...), the rest the shared slots, wps_s each.
 // Routed slots take their expert from the selection, sel_idx or fixed +
-// slot; shared slot topk + i is shared expert i. h is [n_slots][inter] f32.
+// slot; shared slot topk + i is shared expert i. h is [n_slots][inter] f32,
+// or with hxq each slot's XQ form (the same 4 inter bytes), which the down
+// launch then only DMAs into place.
 __device__ __forceinline__ void mq_gateup(const MqProj &gate, const MqProj &up, const MqProj &s_gate,
                                           const MqProj &s_up, const int32_t *__restrict__ sel_idx, int32_t fixed,
                                           int32_t topk, int32_t inter, int32_t wps_r, int32_t wps_s,
                                           const float *__restrict__ x, float *__restrict__ h, MqGeo geo,
-                                          const MqRoute &rt) {
+                                          const MqRoute &rt, int32_t hxq) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int32_t bid = (int32_t)blockIdx.x;
     const bool rk = bid < topk * wps_r;
@@ -1416,9 +1466,9 @@ __device__ __forceinline__ void mq_gateup(const MqProj &gate, const MqProj &up, 
     float *hs = h + (int64_t)slot * inter;
     const int32_t nb = (int32_t)G.n_blocks;
     switch (G.type) {
-    case ST_Q2_K: mq_gateup_slot<ST_Q2_K>(wg, wu, G.row_bytes, nb, inter, j0, wps, x, hs, geo, x_issued); break;
-    case ST_Q3_K: mq_gateup_slot<ST_Q3_K>(wg, wu, G.row_bytes, nb, inter, j0, wps, x, hs, geo, x_issued); break;
-    default: mq_gateup_slot<ST_Q4_K>(wg, wu, G.row_bytes, nb, inter, j0, wps, x, hs, geo, x_issued); break;
+    case ST_Q2_K: mq_gateup_slot<ST_Q2_K>(wg, wu, G.row_bytes, nb, inter, j0, wps, x, hs, geo, x_issued, hxq); break;
+    case ST_Q3_K: mq_gateup_slot<ST_Q3_K>(wg, wu, G.row_bytes, nb, inter, j0, wps, x, hs, geo, x_issued, hxq); break;
+    default: mq_gateup_slot<ST_Q4_K>(wg, wu, G.row_bytes, nb, inter, j0, wps, x, hs, geo, x_issued, hxq); break;
     }
 }
 
@@ -1426,8 +1476,8 @@ __device__ __forceinline__ void mq_gateup(const MqProj &gate, const MqProj &up, 
     extern "C" __global__ __launch_bounds__(1024) void sepia_mq_gateup(                                  \
         MqProj gate, MqProj up, MqProj s_gate, MqProj s_up, const int32_t *__restrict__ sel_idx,         \
         int32_t fixed, int32_t topk, int32_t inter, int32_t wps_r, int32_t wps_s,                        \
-        const float *__restrict__ x, float *__restrict__ h, MqGeo geo, MqRoute rt) {                     \
-        mq_gateup(gate, up, s_gate, s_up, sel_idx, fixed, topk, inter, wps_r, wps_s, x, h, geo, rt);     \
+        const float *__restrict__ x, float *__restrict__ h, MqGeo geo, MqRoute rt, int32_t hxq) {        \
+        mq_gateup(gate, up, s_gate, s_up, sel_idx, fixed, topk, inter, wps_r, wps_s, x, h, geo, rt, hxq); \
     }
 
 // Down, one slot per workgroup: workgroups [0, topk * wps_r) serve the
@@ -1466,7 +1516,7 @@ __device__ __forceinline__ void mq_dn_slot(const uint8_t *Wd, uint64_t row_bytes
     }
     MqWave<T, decltype(item_of)> wv(item_of, nk, nb >> 2, inter, (uint32_t)row_bytes, geo, rings, 0,
                                     (int)(blockDim.x >> 6) - geo.conv);
-    wv.go(hs, geo, lds0, MQ_ZERO, red);
+    wv.template go<false>(hs, geo, lds0, MQ_ZERO, red);
 }
 
 __device__ __forceinline__ void mq_down(const MqProj &down, const MqProj &s_down, const int32_t *__restrict__ sel_idx,

@@ -142,6 +142,7 @@ static int g_opt_mix = 0;    /* "mix": 1 runs the MoE decode's gate/up as sepia_
                               * streams shared units while its wave 0 selects, then routed ones) */
 static int g_opt_dnrows = 0; /* "dnrows": 1 runs the MoE decode's down as sepia_mq_down_rows (all slots of
                               * a row group in one workgroup, summed in LDS) */
+static int g_opt_hxq = 0;    /* "hxq": 1 = h crosses from gate/up to down in XQ form (measured slower: the XQ epilogue costs gate/up more than it saves down), 0 = f32 */
 static int g_opt_dyn = 0;    /* "dyn": 1 deals the MoE down launch's steps at run time (MqDyn) */
 static int g_opt_route_sel = 0;   /* "route_sel": 1 = the router launch's last workgroup selects the
                                    * experts even for the matrix-core FFN (0: its gate/up launch does) */
@@ -945,6 +946,10 @@ int sepia_hip_set_option(const char *name, int value) {
         g_opt_dnrows = value;
         return 1;
     }
+    if (strcmp(name, "hxq") == 0 && (value == 0 || value == 1)) {
+        g_opt_hxq = value;
+        return 1;
+    }
     if (strcmp(name, "dyn") == 0 && (value == 0 || value == 1)) {
         g_opt_dyn = value;
         return 1;
@@ -992,7 +997,7 @@ int sepia_hip_set_option(const char *name, int value) {
 #define MQ_CUS 256                  /* MI355X compute units */
 #define MQ_ZERO 768
 typedef struct {
-    int32_t P, ring, xraw, orings, conv, dyn;   /* as struct MqGeo in kernels/mq.h */
+    int32_t P, ring, xraw, orings, conv, dyn, xq_in;   /* as struct MqGeo in kernels/mq.h */
 } MqGeo;
 /* In-kernel selection by the gate/up launch (struct MqRoute in
  * kernels/mq.h); logits NULL: the experts come from sel_idx. */
@@ -1039,8 +1044,8 @@ static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
  * with several steps as 1.6 steps each (its loads do not overlap its
  * compute) and crediting the vector's DMA or converter waves, then the most
  * steps in flight, then the most waves. Returns 0 when nothing fits. */
-static int mq_geo(int mc, int wmax, int64_t n_items, int64_t nq, size_t fixed, size_t raw_bytes, unsigned *threads,
-                  MqGeo *geo, size_t *lds) {
+static int mq_geo(int mc, int wmax, int64_t n_items, int64_t nq, size_t fixed, size_t raw_bytes, int allow_conv,
+                  unsigned *threads, MqGeo *geo, size_t *lds) {
     const size_t w1 = (size_t)k_mq_words[mc] * 1024, wm = (size_t)wmax * 1024;
     int64_t best_cost = 0, best_fl = 0;
     int best_nw = 0, found = 0;
@@ -1048,8 +1053,11 @@ static int mq_geo(int mc, int wmax, int64_t n_items, int64_t nq, size_t fixed, s
      * converter waves (DMA into the XQ place, converted there); 1 and 2 need
      * the vector's size (raw_bytes) */
     const int64_t segs = (int64_t)raw_bytes / 64, cv_need = (segs + MQ_XQ_SEGS_PER_WAVE - 1) / MQ_XQ_SEGS_PER_WAVE;
-    for (int mode = 0; mode <= (raw_bytes > 0 ? 2 : 0); mode++) {
-        if (g_opt_mq_x ? g_opt_mq_x != mode + 1 : (mode == 2 && mc < 3)) continue;
+    /* a forced mode the launch cannot take (converter waves for the FFN
+     * launches) leaves the choice to the planner */
+    const int forced = (g_opt_mq_x == 3 && !allow_conv) ? 0 : g_opt_mq_x;
+    for (int mode = 0; mode <= (raw_bytes > 0 ? (allow_conv ? 2 : 1) : 0); mode++) {
+        if (raw_bytes > 0 && (forced ? forced != mode + 1 : (mode == 2 && mc < 3))) continue;
         for (int P = 1; P <= 16 && P <= nq; P++) {
             if (g_opt_mq_p && P != g_opt_mq_p) continue;
             for (int C = 1; C * P <= 16 && C <= n_items; C++) {
@@ -1091,6 +1099,7 @@ static int mq_geo(int mc, int wmax, int64_t n_items, int64_t nq, size_t fixed, s
                     geo->orings = (int32_t)base;
                     geo->conv = cv;
                     geo->dyn = 0;
+                    geo->xq_in = 0;
                     *threads = 64u * (unsigned)(nw + cv);
                     *lds = base + (size_t)nw * ring;
                 }
@@ -1129,6 +1138,7 @@ static int mq_geo_dyn(int mc, int wmax, int64_t n_items, int64_t nq, size_t fixe
             geo->orings = (int32_t)base;
             geo->conv = 0;
             geo->dyn = 1;
+            geo->xq_in = 0;
             *threads = 64u * (unsigned)nw;
             *lds = base + (size_t)nw * ring;
         }
@@ -1151,7 +1161,7 @@ static int mq_plan(int type, int64_t n_blocks, int64_t rows, uintptr_t base, uin
     const int64_t per = (tiles + MQ_CUS - 1) / MQ_CUS;     /* row groups per workgroup */
     *grid = (unsigned)((tiles + per - 1) / per);
     if (!mq_geo(mc, k_mq_words[mc], per, n_blocks / 4, MQ_ZERO + mq_xq_bytes(256 * n_blocks) + k_mq_table[mc],
-                (size_t)1024 * n_blocks, threads, geo, lds))
+                (size_t)1024 * n_blocks, 1, threads, geo, lds))
         return -1;
     return K_MQ_MV + mc;
 }
@@ -1366,6 +1376,7 @@ typedef struct {
     int32_t gu_wps_r, gu_wps_s, dn_wps_r, dn_wps_s;
     size_t gu_lds, dn_lds;
     MqGeo gu_geo, dn_geo;
+    int32_t gu_hxq;                 /* gate/up writes h in XQ form, the down launch takes it so */
 } MqFfnPlan;
 #define MQ_DN_CNT_OFF 64            /* first down arrival counter (u32 index in the counter region) */
 static int mq_proj_ok(const MoeProj *p, int64_t rows) {
@@ -1419,14 +1430,22 @@ static int mq_ffn_plan(const MoeProj *g, const MoeProj *u, const MoeProj *d, con
     const int32_t gmin = pl->gu_wps_r < pl->gu_wps_s || n_shared == 0 ? pl->gu_wps_r : pl->gu_wps_s;
     const int32_t dmin = pl->dn_wps_r < pl->dn_wps_s || n_shared == 0 ? pl->dn_wps_r : pl->dn_wps_s;
     const int64_t nk_gu = (tiles_i + gmin - 1) / gmin, nk_dn = (tiles_h + dmin - 1) / dmin;
-    if (!mq_geo(kg, wgu, 2 * nk_gu, H / 1024, MQ_ZERO + mq_xq_bytes(H) + MQ_SEL_BYTES, (size_t)H * 4, &pl->gu_threads,
-                &pl->gu_geo, &pl->gu_lds))
+    if (!mq_geo(kg, wgu, 2 * nk_gu, H / 1024, MQ_ZERO + mq_xq_bytes(H) + MQ_SEL_BYTES, (size_t)H * 4, 0,
+                &pl->gu_threads, &pl->gu_geo, &pl->gu_lds))
         return 0;
     const size_t dn_fixed = MQ_ZERO + mq_xq_bytes(I) + (size_t)nk_dn * 4 + 256;
-    if (!(g_opt_dyn && !g_opt_mq_x && mq_geo_dyn(kd, wdn, nk_dn, I / 1024, dn_fixed, (size_t)I * 4, &pl->dn_threads,
-                                                 &pl->dn_geo, &pl->dn_lds)) &&
-        !mq_geo(kd, wdn, nk_dn, I / 1024, dn_fixed, (size_t)I * 4, &pl->dn_threads, &pl->dn_geo, &pl->dn_lds))
+    /* h crosses in XQ form (the down launch only DMAs it into place) unless
+     * an experimental launch that reads f32 h is switched on */
+    pl->gu_hxq = g_opt_hxq && !(g_opt_mix || g_opt_dnrows || g_opt_dyn);
+    if (pl->gu_hxq) {
+        if (!mq_geo(kd, wdn, nk_dn, I / 1024, dn_fixed, 0, 0, &pl->dn_threads, &pl->dn_geo, &pl->dn_lds)) return 0;
+        pl->dn_geo.xq_in = 1;
+    } else if (!(g_opt_dyn && !g_opt_mq_x && mq_geo_dyn(kd, wdn, nk_dn, I / 1024, dn_fixed, (size_t)I * 4,
+                                                         &pl->dn_threads, &pl->dn_geo, &pl->dn_lds)) &&
+               !mq_geo(kd, wdn, nk_dn, I / 1024, dn_fixed, (size_t)I * 4, 0, &pl->dn_threads, &pl->dn_geo,
+                       &pl->dn_lds)) {
         return 0;
+    }
     pl->gu_grid = (unsigned)(topk * pl->gu_wps_r + n_shared * pl->gu_wps_s);
     pl->dn_grid = (unsigned)(topk * pl->dn_wps_r + n_shared * pl->dn_wps_s);
     return 1;
@@ -2078,7 +2097,7 @@ static int ffn_launch(const char *op, const MoeProj *g, const MoeProj *u, const 
             if (!launch_lds(K_MQ_GU_MIX, MQ_CUS, mix_threads, mix_lds, a_mx, op)) return 0;
         } else {
             void *a_gu[] = { (void *)g, (void *)u, (void *)sg, (void *)su, &sel_idx, &fixed, &topk, &inter32,
-                             &pl.gu_wps_r, &pl.gu_wps_s, &xdev, &h, &pl.gu_geo, &rt };
+                             &pl.gu_wps_r, &pl.gu_wps_s, &xdev, &h, &pl.gu_geo, &rt, &pl.gu_hxq };
             if (!launch_lds(K_MQ_GU, pl.gu_grid, pl.gu_threads, pl.gu_lds, a_gu, op)) return 0;
         }
         MqRowsGeo rg;

@@ -464,7 +464,8 @@ def mq_vector(dev, request):
     """Force how the matrix-core kernels read their vector: 1 = from global
     memory after the weight prologue, 2 = by LDS DMA ahead of it, 3 = by
     converter waves (DMA into the XQ place, converted there while the other
-    waves decode their first step)."""
+    waves decode their first step; matvec launches only, the FFN launches
+    then keep the planner's choice)."""
     assert dev.L.sepia_hip_set_option(b"mq_x", request.param) == 1
     yield request.param
     dev.L.sepia_hip_set_option(b"mq_x", 0)
