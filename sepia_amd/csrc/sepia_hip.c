@@ -65,6 +65,8 @@ enum {
     K_MQ_GU_MIX,
     /* MoE down with every slot of a row group in one workgroup (kernels/mq_rows.h) */
     K_MQ_DN_ROWS,
+    /* prefill gate/up of the integer formats with 16 waves a workgroup (kernels/prefill.h) */
+    K_PF_GATEUP_I,
     K_COUNT
 };
 #define FFN_NAMES(p) "sepia_ffn_gateup_" p, "sepia_ffn_gateup_" p "_xp", "sepia_ffn_down_" p
@@ -87,7 +89,7 @@ static const char *const k_names[K_COUNT] = {
     "sepia_mq_mv_q2_k", "sepia_mq_mv_q3_k", "sepia_mq_mv_q4_k", "sepia_mq_mv_iq2_xs", "sepia_mq_mv_iq3_xxs",
     "sepia_mq_gateup", "sepia_mq_down", "sepia_mq_moe",
     "sepia_pf_route", "sepia_pf_select", "sepia_pf_group", "sepia_pf_gateup", "sepia_pf_down", "sepia_pf_combine",
-    "sepia_pf_split", "sepia_mq_ffn", "sepia_mq_gateup_mix", "sepia_mq_down_rows",
+    "sepia_pf_split", "sepia_mq_ffn", "sepia_mq_gateup_mix", "sepia_mq_down_rows", "sepia_pf_gateup_i",
 };
 #undef FFN_NAMES
 
@@ -144,6 +146,8 @@ static int g_opt_dnrows = 0; /* "dnrows": 1 runs the MoE decode's down as sepia_
                               * a row group in one workgroup, summed in LDS) */
 static int g_opt_hxq = 0;    /* "hxq": 1 = h crosses from gate/up to down in XQ form (measured slower: the XQ epilogue costs gate/up more than it saves down), 0 = f32 */
 static int g_opt_dyn = 0;    /* "dyn": 1 deals the MoE down launch's steps at run time (MqDyn) */
+static int g_opt_pf_gu16 = 1;   /* "pf_gu16": 1 = a prefill layer whose gate/up projections are all Q2_K, Q3_K
+                                 * or Q4_K runs them as sepia_pf_gateup_i (16 waves), 0 = sepia_pf_gateup */
 static int g_opt_route_sel = 0;   /* "route_sel": 1 = the router launch's last workgroup selects the
                                    * experts even for the matrix-core FFN (0: its gate/up launch does) */
 static int g_opt_flow = 0;   /* "flow": 1 runs the expert FFN as one sepia_mq_ffn launch (gate/up and down waves) */
@@ -954,6 +958,10 @@ int sepia_hip_set_option(const char *name, int value) {
         g_opt_dyn = value;
         return 1;
     }
+    if (strcmp(name, "pf_gu16") == 0 && (value == 0 || value == 1)) {
+        g_opt_pf_gu16 = value;
+        return 1;
+    }
     if (strcmp(name, "route_sel") == 0 && (value == 0 || value == 1)) {
         g_opt_route_sel = value;
         return 1;
@@ -1458,6 +1466,8 @@ static int mq_ffn_plan(const MoeProj *g, const MoeProj *u, const MoeProj *d, con
 static int pf_type_ok(int t) {
     return t == SEPIA_T_Q2_K || t == SEPIA_T_Q3_K || t == 12 || t == 13 || t == 14 || t == 17 || t == 18 || t == 23;
 }
+/* Formats the prefill integer pipelines take as exact codes (Q2_K, Q3_K, Q4_K). */
+static int pf_type_int(int t) { return t == SEPIA_T_Q2_K || t == SEPIA_T_Q3_K || t == 12; }
 
 int sepia_gpu_moe_prefill(const SepiaMoeLayerDesc *L, int64_t n_tokens, SepiaGpuBuf *x, SepiaGpuBuf *y,
                           SepiaGpuBuf *route_out) {
@@ -1565,7 +1575,10 @@ int sepia_gpu_moe_prefill(const SepiaMoeLayerDesc *L, int64_t n_tokens, SepiaGpu
     if (!launch(K_PF_SPLIT, (unsigned)((nseg + 255) / 256), 256, a_sp, op)) return 0;
     void *a_gu[] = { (void *)&g, (void *)&u, (void *)&sg, (void *)&su, &nr32, &nsel32, &inter, &hid, &xh, &xl, &s16,
                      &lo_any, &list, &units, &n_units, &hh, &hl };
-    if (!launch2(K_PF_GATEUP, (unsigned)((I + 31) / 32), (unsigned)umax, 512, PF_LDS_BYTES, a_gu, op)) return 0;
+    const int gu16 = g_opt_pf_gu16 && pf_type_int(g.type) && (ns == 0 || pf_type_int(sg.type));
+    if (!launch2(gu16 ? K_PF_GATEUP_I : K_PF_GATEUP, (unsigned)((I + 31) / 32), (unsigned)umax, gu16 ? 1024 : 512,
+                 PF_LDS_BYTES, a_gu, op))
+        return 0;
     void *a_dn[] = { (void *)&d, (void *)&sd, &nr32, &inter, &hid, &hh, &hl, &list, &units, &n_units, &yp };
     if (!launch2(K_PF_DOWN, (unsigned)((H + 63) / 64), (unsigned)umax, 512, PF_LDS_BYTES, a_dn, op)) return 0;
     void *a_cb[] = { &yp, &sel_w, &nsel32, &tt, &hid, &y->dev };
