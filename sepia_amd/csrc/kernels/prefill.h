@@ -771,6 +771,187 @@ extern "C" __global__ __launch_bounds__(512) void sepia_pf_gateup(
     }
 }
 
+// ------------------------------------------ gate/up, codes in registers ---
+// Both M tiles (pairs 0 .. 15, 16 .. 31) of one 16-row N tile += this
+// block's share, the B fragments decoded by each lane from its own row's
+// staged raw block `blk` (lane l: row l & 15, codes k = 32 j + 8 (l >> 4) ..
+// + 7) and used for both tiles. Same per-block arithmetic as pf_int_mma.
+template <int T>
+__device__ __forceinline__ void pf_reg_mma(pf_f32x4 &acc0, pf_f32x4 &acc1, const uint8_t *A, const uint8_t *blk,
+                                           const float *s16, bool xlo) {
+    const int l = threadIdx.x & 63, r = l & 15, g = l >> 4;
+    if constexpr (!PfInt<T>::per_sub) {
+        pf_f32x4 b0 = {0.0f, 0.0f, 0.0f, 0.0f}, b1 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const uint4 q = PfInt<T>::chunk(blk, 4 * j + g);
+            const pf_bf16x8 bq = *(const pf_bf16x8 *)&q;
+            const uint32_t o0 = pf_swz(r, 4 * j + g), o1 = pf_swz(16 + r, 4 * j + g);
+            b0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(const pf_bf16x8 *)(A + o0), bq, b0, 0, 0, 0);
+            b1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(const pf_bf16x8 *)(A + o1), bq, b1, 0, 0, 0);
+            if (xlo) {
+                b0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(const pf_bf16x8 *)(A + PF_TILE + o0), bq, b0, 0, 0, 0);
+                b1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(const pf_bf16x8 *)(A + PF_TILE + o1), bq, b1, 0, 0, 0);
+            }
+        }
+        const float d = h2f(blk + (T == ST_Q2_K ? 80 : 108));
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            acc0[i] = __builtin_fmaf(d, b0[i], acc0[i]);
+            acc1[i] = __builtin_fmaf(d, b1[i], acc1[i]);
+        }
+        if constexpr (PfInt<T>::min16) {
+            // B[k = 4 g + i][row r] = min of sub-block 4 g + i; A[pair][k] = S
+            __bf16 bmv[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) bmv[i] = (__bf16)(float)(ld_u8(blk + 4 * g + i) >> 4);
+            const pf_s16x4 bv = *(const pf_s16x4 *)bmv;
+            const float dmin = h2f(blk + 82);
+#pragma unroll
+            for (int mt = 0; mt < 2; mt++) {
+                __bf16 sh[4], sl[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) pf_split(s16[(16 * mt + r) * 16 + 4 * g + i], sh[i], sl[i]);
+                pf_f32x4 macc = {0.0f, 0.0f, 0.0f, 0.0f};
+                macc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(*(const pf_s16x4 *)sh, bv, macc, 0, 0, 0);
+                macc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(*(const pf_s16x4 *)sl, bv, macc, 0, 0, 0);
+                pf_f32x4 &acc = mt ? acc1 : acc0;
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc[i] = __builtin_fmaf(-dmin, macc[i], acc[i]);
+            }
+        }
+    } else {
+        const float d = h2f(blk), dmin = h2f(blk + 2);
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            int sc, mn;
+            k4_scale_min(blk + 4, j, sc, mn);
+            const float ds = d * (float)sc, dm = dmin * (float)mn;
+            const uint4 q = PfInt<T>::chunk(blk, 4 * j + g);
+            const pf_bf16x8 bq = *(const pf_bf16x8 *)&q;
+            const uint32_t o0 = pf_swz(r, 4 * j + g), o1 = pf_swz(16 + r, 4 * j + g);
+            pf_f32x4 b0 = {0.0f, 0.0f, 0.0f, 0.0f}, b1 = {0.0f, 0.0f, 0.0f, 0.0f};
+            b0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(const pf_bf16x8 *)(A + o0), bq, b0, 0, 0, 0);
+            b1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(const pf_bf16x8 *)(A + o1), bq, b1, 0, 0, 0);
+            if (xlo) {
+                b0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(const pf_bf16x8 *)(A + PF_TILE + o0), bq, b0, 0, 0, 0);
+                b1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(const pf_bf16x8 *)(A + PF_TILE + o1), bq, b1, 0, 0, 0);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float *s0 = s16 + (4 * g + i) * 16 + 2 * j, *s1 = s16 + (16 + 4 * g + i) * 16 + 2 * j;
+                acc0[i] = __builtin_fmaf(ds, b0[i], acc0[i]);
+                acc0[i] = __builtin_fmaf(-dm, s0[0] + s0[1], acc0[i]);
+                acc1[i] = __builtin_fmaf(ds, b1[i], acc1[i]);
+                acc1[i] = __builtin_fmaf(-dm, s1[0] + s1[1], acc1[i]);
+            }
+        }
+    }
+}
+
+// Gate/up of the integer formats with the codes in registers: workgroup
+// (rows 64 bx .. 64 bx + 63 of I, unit by), 8 waves; wave w takes rows
+// 16 (w & 3) .. of gate (w < 4) or up (w >= 4) for all 32 pairs. A stage
+// holds block b's activation tiles, the raw windows of 64 gate and 64 up
+// rows and the 16-column sums; S - 1 blocks fly while one computes, one
+// barrier a step (no code tiles to build). The up waves hand their tiles
+// to the gate waves through LDS at the end.
+template <int T>
+__device__ __forceinline__ void pf_reg_gateup(uint8_t *smem, const uint8_t *Wg, const uint8_t *Wu, uint64_t row_bytes,
+                                              int64_t nb, int64_t rows, const __bf16 *ah, const __bf16 *al,
+                                              const float *s16, const uint32_t *roff, const int32_t *pair, int nv,
+                                              int64_t r0, bool xlo, __bf16 *__restrict__ hh, __bf16 *__restrict__ hl) {
+    constexpr int BB = Fmt<T>::bytes, RD = (BB + 6) / 4;
+    constexpr bool need_s = PfInt<T>::min16 || PfInt<T>::per_sub;
+    const int w = threadIdx.x >> 6, l = threadIdx.x & 63, r = l & 15, nw = (int)(blockDim.x >> 6);
+    const int mat = w >> 2, n0 = 16 * (w & 3);
+    const uint32_t a_bytes = xlo ? 2 * PF_TILE : PF_TILE, raw_bytes = 128 * RD * 4, s_bytes = need_s ? 2048 : 0;
+    const uint32_t st_bytes = a_bytes + raw_bytes + s_bytes;
+    int S = (int)(PF_O_ROFF / st_bytes);
+    S = S < 4 ? S : 4;   // >= 3 for every format (Q4_K with lo terms: 53,760-byte stages)
+    auto stage = [&](int64_t b) { return smem + (uint32_t)((int)b % S) * st_bytes; };
+    const int n_raw = (64 * RD + 63) >> 6;
+    const int per_stage =
+        pf_share(xlo ? 32 : 16, w, nw) + 2 * pf_share(n_raw, w, nw) + (need_s ? pf_share(2, w, nw) : 0);
+    auto issue = [&](int64_t b) {
+        uint8_t *st = stage(b);
+        pf_issue_act(ah, al, roff, b, st, xlo);
+        pf_issue_raw<T>(Wg, row_bytes, rows, r0, 64, b, st + a_bytes);
+        pf_issue_raw<T>(Wu, row_bytes, rows, r0, 64, b, st + a_bytes + 64 * RD * 4);
+        if constexpr (need_s) pf_issue_s16(s16, roff, b, st + a_bytes + raw_bytes);
+    };
+    // this lane's row (clamped as pf_issue_raw clamps it) and its byte offset
+    int64_t rr = r0 + n0 + r;
+    rr = rr < rows ? rr : rows - 1;
+    const uint64_t rowoff = (uint64_t)((uintptr_t)(mat ? Wu : Wg) & 3) + (uint64_t)rr * row_bytes;
+    const uint32_t slot = (uint32_t)(64 * mat + n0 + r) * RD * 4;
+    for (int64_t b = 0; b < S - 1 && b < nb; b++) issue(b);
+    pf_f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int64_t b = 0; b < nb; b++) {
+        const int64_t ahead = (nb - 1 - b) < (S - 2) ? (nb - 1 - b) : (S - 2);
+        pf_wait_vm(per_stage * (int)ahead);
+        __syncthreads();   // every wave's DMAs of block b; block b - 1's reads are done
+        if (b + S - 1 < nb) issue(b + S - 1);
+        const uint8_t *st = stage(b);
+        const uint32_t mis = (uint32_t)(rowoff + (uint64_t)b * BB) & 3u;
+        pf_reg_mma<T>(acc0, acc1, st, st + a_bytes + slot + mis, (const float *)(st + a_bytes + raw_bytes), xlo);
+    }
+    __syncthreads();
+    float *xch = (float *)smem + (w & 3) * 512 + l * 8;
+    if (mat) {
+        *(pf_f32x4 *)xch = acc0;
+        *(pf_f32x4 *)(xch + 4) = acc1;
+    }
+    __syncthreads();
+    if (mat) return;
+    const pf_f32x4 u0 = *(const pf_f32x4 *)xch, u1 = *(const pf_f32x4 *)(xch + 4);
+    const int64_t row = r0 + n0 + r;
+#pragma unroll
+    for (int mt = 0; mt < 2; mt++) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int m = 16 * mt + 4 * (l >> 4) + i;
+            if (m < nv && row < rows) {
+                __bf16 a, c;
+                pf_split(silu_f32(mt ? acc1[i] : acc0[i]) * (mt ? u1[i] : u0[i]), a, c);
+                hh[(int64_t)pair[m] * rows + row] = a;
+                hl[(int64_t)pair[m] * rows + row] = c;
+            }
+        }
+    }
+}
+
+// Gate/up of the integer formats with the codes in registers
+// (pf_reg_gateup): the same result layout as sepia_pf_gateup over 64-row
+// tiles. The host launches it only when every gate/up projection of the
+// layer is Q2_K, Q3_K or Q4_K.
+extern "C" __global__ __launch_bounds__(512) void sepia_pf_gateup_r(
+    PfProj gate, PfProj up, PfProj s_gate, PfProj s_up, int32_t n_routed, int32_t n_sel, int64_t I, int64_t H,
+    const __bf16 *__restrict__ xh, const __bf16 *__restrict__ xl, const float *__restrict__ s16,
+    const uint32_t *__restrict__ lo_any, const int32_t *__restrict__ list, const int32_t *__restrict__ units,
+    const int32_t *__restrict__ n_units, __bf16 *__restrict__ hh, __bf16 *__restrict__ hl) {
+    if ((int32_t)blockIdx.y >= n_units[0]) return;
+    extern __shared__ __attribute__((aligned(16))) uint8_t pf_smem[];
+    uint8_t *smem = pf_smem;
+    const int32_t *un = units + 3 * blockIdx.y;
+    const int32_t e = un[0], nv = un[2];
+    const bool routed = e < n_routed;
+    const PfProj &G = routed ? gate : s_gate, &U = routed ? up : s_up;
+    const int64_t ei = routed ? e : e - n_routed;
+    const uint8_t *wg = G.base + ei * G.stride, *wu = U.base + ei * U.stride;
+    const int64_t r0 = (int64_t)blockIdx.x * 64;
+    uint32_t *roff;
+    int32_t *pair;
+    pf_unit_rows(list + un[1], nv, true, n_sel, H, smem, roff, pair);
+    const bool xlo = __builtin_amdgcn_readfirstlane((int)*lo_any) != 0;
+    switch (G.type) {
+#define PF_GR(TT) case TT: pf_reg_gateup<TT>(smem, wg, wu, G.row_bytes, G.n_blocks, I, xh, xl, s16, roff, pair, nv, r0, xlo, hh, hl); break;
+        PF_GR(ST_Q2_K) PF_GR(ST_Q3_K) PF_GR(ST_Q4_K)
+#undef PF_GR
+    default: break;
+    }
+}
+
 // The integer formats' gate/up with 16 waves a workgroup (pf_int_pipe NT =
 // 1024): the same tiles and result layout as sepia_pf_gateup, each stage's
 // code build and DMA issue spread over twice the waves, and each block's

@@ -67,6 +67,8 @@ enum {
     K_MQ_DN_ROWS,
     /* prefill gate/up of the integer formats with 16 waves a workgroup (kernels/prefill.h) */
     K_PF_GATEUP_I,
+    /* prefill gate/up of the integer formats with the codes in registers (kernels/prefill.h) */
+    K_PF_GATEUP_R,
     K_COUNT
 };
 #define FFN_NAMES(p) "sepia_ffn_gateup_" p, "sepia_ffn_gateup_" p "_xp", "sepia_ffn_down_" p
@@ -90,6 +92,7 @@ static const char *const k_names[K_COUNT] = {
     "sepia_mq_gateup", "sepia_mq_down", "sepia_mq_moe",
     "sepia_pf_route", "sepia_pf_select", "sepia_pf_group", "sepia_pf_gateup", "sepia_pf_down", "sepia_pf_combine",
     "sepia_pf_split", "sepia_mq_ffn", "sepia_mq_gateup_mix", "sepia_mq_down_rows", "sepia_pf_gateup_i",
+    "sepia_pf_gateup_r",
 };
 #undef FFN_NAMES
 
@@ -146,8 +149,9 @@ static int g_opt_dnrows = 0; /* "dnrows": 1 runs the MoE decode's down as sepia_
                               * a row group in one workgroup, summed in LDS) */
 static int g_opt_hxq = 0;    /* "hxq": 1 = h crosses from gate/up to down in XQ form (measured slower: the XQ epilogue costs gate/up more than it saves down), 0 = f32 */
 static int g_opt_dyn = 0;    /* "dyn": 1 deals the MoE down launch's steps at run time (MqDyn) */
-static int g_opt_pf_gu16 = 1;   /* "pf_gu16": 1 = a prefill layer whose gate/up projections are all Q2_K, Q3_K
-                                 * or Q4_K runs them as sepia_pf_gateup_i (16 waves), 0 = sepia_pf_gateup */
+static int g_opt_pf_gu = 2;   /* "pf_gu": the gate/up launch of a prefill layer whose gate/up projections are
+                               * all Q2_K, Q3_K or Q4_K: 2 = sepia_pf_gateup_r (codes in registers), 1 =
+                               * sepia_pf_gateup_i (16 waves), 0 = sepia_pf_gateup (other layers always) */
 static int g_opt_route_sel = 0;   /* "route_sel": 1 = the router launch's last workgroup selects the
                                    * experts even for the matrix-core FFN (0: its gate/up launch does) */
 static int g_opt_flow = 0;   /* "flow": 1 runs the expert FFN as one sepia_mq_ffn launch (gate/up and down waves) */
@@ -958,8 +962,8 @@ int sepia_hip_set_option(const char *name, int value) {
         g_opt_dyn = value;
         return 1;
     }
-    if (strcmp(name, "pf_gu16") == 0 && (value == 0 || value == 1)) {
-        g_opt_pf_gu16 = value;
+    if (strcmp(name, "pf_gu") == 0 && value >= 0 && value <= 2) {
+        g_opt_pf_gu = value;
         return 1;
     }
     if (strcmp(name, "route_sel") == 0 && (value == 0 || value == 1)) {
@@ -1575,8 +1579,10 @@ int sepia_gpu_moe_prefill(const SepiaMoeLayerDesc *L, int64_t n_tokens, SepiaGpu
     if (!launch(K_PF_SPLIT, (unsigned)((nseg + 255) / 256), 256, a_sp, op)) return 0;
     void *a_gu[] = { (void *)&g, (void *)&u, (void *)&sg, (void *)&su, &nr32, &nsel32, &inter, &hid, &xh, &xl, &s16,
                      &lo_any, &list, &units, &n_units, &hh, &hl };
-    const int gu16 = g_opt_pf_gu16 && pf_type_int(g.type) && (ns == 0 || pf_type_int(sg.type));
-    if (!launch2(gu16 ? K_PF_GATEUP_I : K_PF_GATEUP, (unsigned)((I + 31) / 32), (unsigned)umax, gu16 ? 1024 : 512,
+    const int gu_mode = pf_type_int(g.type) && (ns == 0 || pf_type_int(sg.type)) ? g_opt_pf_gu : 0;
+    const int gu_k = gu_mode == 2 ? K_PF_GATEUP_R : gu_mode == 1 ? K_PF_GATEUP_I : K_PF_GATEUP;
+    const int64_t gu_rows = gu_mode == 2 ? 64 : 32;
+    if (!launch2(gu_k, (unsigned)((I + gu_rows - 1) / gu_rows), (unsigned)umax, gu_mode == 1 ? 1024 : 512,
                  PF_LDS_BYTES, a_gu, op))
         return 0;
     void *a_dn[] = { (void *)&d, (void *)&sd, &nr32, &inter, &hid, &hh, &hl, &list, &units, &n_units, &yp };

@@ -738,29 +738,29 @@ PREFILL_CASES = [
 ]
 
 
-@pytest.mark.parametrize("gu16", [1, 0])
+@pytest.mark.parametrize("gu", [2, 1, 0])
 @pytest.mark.parametrize("x_kind", ["bf16", "f32"])
 @pytest.mark.parametrize("shape,types,T", PREFILL_CASES, ids=lambda v: str(v))
-def test_moe_prefill(dev, orc, shape, types, T, x_kind, gu16):
+def test_moe_prefill(dev, orc, shape, types, T, x_kind, gu):
     """Every token of the batch against the oracle's single-token layer (its
     own routing, near-ties per the reference protocol); two runs bitwise equal.
     x either bf16-representable (the projections skip the zero lo terms) or
-    full f32. gu16: integer-format gate/up on the 16-wave kernel (the
-    default) or on the 8-wave one (option pf_gu16 0)."""
+    full f32. gu (option pf_gu): integer-format gate/up with the codes in
+    registers (2, the default), on 16 waves (1) or on the 8-wave kernel (0)."""
     hidden, inter, n_routed, n_shared = shape
     tgu, td, ts = types
-    if not gu16 and (tgu not in (10, 11, 12) or ts not in (10, 11, 12)):
-        pytest.skip("pf_gu16 0 changes nothing outside Q2_K / Q3_K / Q4_K gate/up layers")
+    if gu != 2 and (tgu not in (10, 11, 12) or ts not in (10, 11, 12)):
+        pytest.skip("pf_gu changes nothing outside Q2_K / Q3_K / Q4_K gate/up layers")
     rng = np.random.default_rng(hidden + 7 * T + tgu)
     desc, spec, bufs = make_layer(dev, rng, hidden=hidden, inter=inter, n_routed=n_routed, n_shared=n_shared,
                                   tg=tgu, tu=tgu, td=td, ts=ts)
     X = bf16_normal(rng, (T, hidden)) if x_kind == "bf16" else rng.standard_normal((T, hidden)).astype(np.float32)
-    assert dev.L.sepia_hip_set_option(b"pf_gu16", gu16) == 1
+    assert dev.L.sepia_hip_set_option(b"pf_gu", gu) == 1
     try:
         y, idx, w = run_prefill(dev, desc, X)
         y2, _, _ = run_prefill(dev, desc, X)
     finally:
-        dev.L.sepia_hip_set_option(b"pf_gu16", 1)
+        dev.L.sepia_hip_set_option(b"pf_gu", 2)
     assert np.array_equal(y.view(np.uint32), y2.view(np.uint32))
     for t in range(T):
         y_ref, logits, idx_ref, w_ref = orc.moe_layer(spec, X[t], threads=THREADS)
