@@ -952,6 +952,157 @@ extern "C" __global__ __launch_bounds__(512) void sepia_pf_gateup_r(
     }
 }
 
+// ---------------------------------------------- down, codes in registers ---
+// As pf_reg_mma for a projection whose input (h) has no staged 16-column
+// sums: the min terms come from one more MFMA per 32 columns with a B
+// fragment that holds the row's min code (Q2_K: the 16-column segment's min
+// nibble; Q4_K: ones, scaled by the sub-block's d_min m in f32).
+template <int T>
+__device__ __forceinline__ void pf_reg_mma_dn(pf_f32x4 &acc0, pf_f32x4 &acc1, const uint8_t *A, const uint8_t *blk,
+                                              bool xlo) {
+    const int l = threadIdx.x & 63, r = l & 15, g = l >> 4;
+    auto mm2 = [&](pf_f32x4 &c0, pf_f32x4 &c1, const pf_bf16x8 &bq, uint32_t o0, uint32_t o1) {
+        c0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(const pf_bf16x8 *)(A + o0), bq, c0, 0, 0, 0);
+        c1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(const pf_bf16x8 *)(A + o1), bq, c1, 0, 0, 0);
+        if (xlo) {
+            c0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(const pf_bf16x8 *)(A + PF_TILE + o0), bq, c0, 0, 0, 0);
+            c1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(const pf_bf16x8 *)(A + PF_TILE + o1), bq, c1, 0, 0, 0);
+        }
+    };
+    auto splat = [](float v) {
+        const __bf16 h = (__bf16)v;
+        pf_bf16x8 o;
+#pragma unroll
+        for (int i = 0; i < 8; i++) o[i] = h;
+        return o;
+    };
+    if constexpr (!PfInt<T>::per_sub) {
+        pf_f32x4 b0 = {0.0f, 0.0f, 0.0f, 0.0f}, b1 = {0.0f, 0.0f, 0.0f, 0.0f};
+        pf_f32x4 n0 = {0.0f, 0.0f, 0.0f, 0.0f}, n1 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const uint4 q = PfInt<T>::chunk(blk, 4 * j + g);
+            const uint32_t o0 = pf_swz(r, 4 * j + g), o1 = pf_swz(16 + r, 4 * j + g);
+            mm2(b0, b1, *(const pf_bf16x8 *)&q, o0, o1);
+            if constexpr (PfInt<T>::min16) mm2(n0, n1, splat((float)(ld_u8(blk + 2 * j + (g >> 1)) >> 4)), o0, o1);
+        }
+        const float d = h2f(blk + (T == ST_Q2_K ? 80 : 108));
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            acc0[i] = __builtin_fmaf(d, b0[i], acc0[i]);
+            acc1[i] = __builtin_fmaf(d, b1[i], acc1[i]);
+        }
+        if constexpr (PfInt<T>::min16) {
+            const float dmin = h2f(blk + 82);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                acc0[i] = __builtin_fmaf(-dmin, n0[i], acc0[i]);
+                acc1[i] = __builtin_fmaf(-dmin, n1[i], acc1[i]);
+            }
+        }
+    } else {
+        const float d = h2f(blk), dmin = h2f(blk + 2);
+        const pf_bf16x8 ones = splat(1.0f);
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            int sc, mn;
+            k4_scale_min(blk + 4, j, sc, mn);
+            const float ds = d * (float)sc, dm = dmin * (float)mn;
+            const uint4 q = PfInt<T>::chunk(blk, 4 * j + g);
+            const uint32_t o0 = pf_swz(r, 4 * j + g), o1 = pf_swz(16 + r, 4 * j + g);
+            pf_f32x4 b0 = {0.0f, 0.0f, 0.0f, 0.0f}, b1 = {0.0f, 0.0f, 0.0f, 0.0f};
+            pf_f32x4 s0 = {0.0f, 0.0f, 0.0f, 0.0f}, s1 = {0.0f, 0.0f, 0.0f, 0.0f};
+            mm2(b0, b1, *(const pf_bf16x8 *)&q, o0, o1);
+            mm2(s0, s1, ones, o0, o1);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                acc0[i] = __builtin_fmaf(ds, b0[i], acc0[i]);
+                acc0[i] = __builtin_fmaf(-dm, s0[i], acc0[i]);
+                acc1[i] = __builtin_fmaf(ds, b1[i], acc1[i]);
+                acc1[i] = __builtin_fmaf(-dm, s1[i], acc1[i]);
+            }
+        }
+    }
+}
+
+// Down of the integer formats with the codes in registers: workgroup (rows
+// 128 bx .. 128 bx + 127 of H, unit by), 8 waves; wave w takes rows
+// 16 w .. for all 32 pairs. A stage holds block b's h tiles (hi and lo) and
+// the raw windows of 128 rows; S - 1 blocks fly while one computes.
+// yp[p][row] = down . h[p].
+template <int T>
+__device__ __forceinline__ void pf_reg_down(uint8_t *smem, const uint8_t *Wd, uint64_t row_bytes, int64_t nb,
+                                            int64_t rows, const __bf16 *ah, const __bf16 *al, const uint32_t *roff,
+                                            const int32_t *pair, int nv, int64_t r0, float *__restrict__ yp) {
+    constexpr int BB = Fmt<T>::bytes, RD = (BB + 6) / 4;
+    const int w = threadIdx.x >> 6, l = threadIdx.x & 63, r = l & 15, nw = (int)(blockDim.x >> 6);
+    const int n0 = 16 * w;
+    const uint32_t a_bytes = 2 * PF_TILE, raw_bytes = 128 * RD * 4;
+    const uint32_t st_bytes = a_bytes + raw_bytes;
+    int S = (int)(PF_O_ROFF / st_bytes);
+    S = S < 4 ? S : 4;   // 3 for Q4_K (51,712-byte stages)
+    auto stage = [&](int64_t b) { return smem + (uint32_t)((int)b % S) * st_bytes; };
+    const int per_stage = pf_share(32, w, nw) + pf_share((128 * RD + 63) >> 6, w, nw);
+    auto issue = [&](int64_t b) {
+        uint8_t *st = stage(b);
+        pf_issue_act(ah, al, roff, b, st, true);
+        pf_issue_raw<T>(Wd, row_bytes, rows, r0, 128, b, st + a_bytes);
+    };
+    int64_t rr = r0 + n0 + r;
+    rr = rr < rows ? rr : rows - 1;
+    const uint64_t rowoff = (uint64_t)((uintptr_t)Wd & 3) + (uint64_t)rr * row_bytes;
+    const uint32_t slot = (uint32_t)(n0 + r) * RD * 4;
+    for (int64_t b = 0; b < S - 1 && b < nb; b++) issue(b);
+    pf_f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int64_t b = 0; b < nb; b++) {
+        const int64_t ahead = (nb - 1 - b) < (S - 2) ? (nb - 1 - b) : (S - 2);
+        pf_wait_vm(per_stage * (int)ahead);
+        __syncthreads();   // every wave's DMAs of block b; block b - 1's reads are done
+        if (b + S - 1 < nb) issue(b + S - 1);
+        const uint8_t *st = stage(b);
+        const uint32_t mis = (uint32_t)(rowoff + (uint64_t)b * BB) & 3u;
+        pf_reg_mma_dn<T>(acc0, acc1, st, st + a_bytes + slot + mis, true);
+    }
+    const int64_t row = r0 + n0 + r;
+#pragma unroll
+    for (int mt = 0; mt < 2; mt++) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int m = 16 * mt + 4 * (l >> 4) + i;
+            if (m < nv && row < rows) yp[(int64_t)pair[m] * rows + row] = mt ? acc1[i] : acc0[i];
+        }
+    }
+}
+
+// Down of the integer formats with the codes in registers (pf_reg_down):
+// the same result layout as sepia_pf_down over 128-row tiles. The host
+// launches it only when every down projection of the layer is Q2_K, Q3_K
+// or Q4_K.
+extern "C" __global__ __launch_bounds__(512) void sepia_pf_down_r(
+    PfProj down, PfProj s_down, int32_t n_routed, int64_t I, int64_t H, const __bf16 *__restrict__ hh,
+    const __bf16 *__restrict__ hl, const int32_t *__restrict__ list, const int32_t *__restrict__ units,
+    const int32_t *__restrict__ n_units, float *__restrict__ yp) {
+    if ((int32_t)blockIdx.y >= n_units[0]) return;
+    extern __shared__ __attribute__((aligned(16))) uint8_t pf_smem[];
+    uint8_t *smem = pf_smem;
+    const int32_t *un = units + 3 * blockIdx.y;
+    const int32_t e = un[0], nv = un[2];
+    const bool routed = e < n_routed;
+    const PfProj &D = routed ? down : s_down;
+    const int64_t ei = routed ? e : e - n_routed;
+    const uint8_t *wd = D.base + ei * D.stride;
+    const int64_t r0 = (int64_t)blockIdx.x * 128;
+    uint32_t *roff;
+    int32_t *pair;
+    pf_unit_rows(list + un[1], nv, false, 1, I, smem, roff, pair);
+    switch (D.type) {
+#define PF_DR(TT) case TT: pf_reg_down<TT>(smem, wd, D.row_bytes, D.n_blocks, H, hh, hl, roff, pair, nv, r0, yp); break;
+        PF_DR(ST_Q2_K) PF_DR(ST_Q3_K) PF_DR(ST_Q4_K)
+#undef PF_DR
+    default: break;
+    }
+}
+
 // The integer formats' gate/up with 16 waves a workgroup (pf_int_pipe NT =
 // 1024): the same tiles and result layout as sepia_pf_gateup, each stage's
 // code build and DMA issue spread over twice the waves, and each block's

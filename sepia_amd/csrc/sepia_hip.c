@@ -69,6 +69,8 @@ enum {
     K_PF_GATEUP_I,
     /* prefill gate/up of the integer formats with the codes in registers (kernels/prefill.h) */
     K_PF_GATEUP_R,
+    /* prefill down of the integer formats with the codes in registers (kernels/prefill.h) */
+    K_PF_DOWN_R,
     K_COUNT
 };
 #define FFN_NAMES(p) "sepia_ffn_gateup_" p, "sepia_ffn_gateup_" p "_xp", "sepia_ffn_down_" p
@@ -92,7 +94,7 @@ static const char *const k_names[K_COUNT] = {
     "sepia_mq_gateup", "sepia_mq_down", "sepia_mq_moe",
     "sepia_pf_route", "sepia_pf_select", "sepia_pf_group", "sepia_pf_gateup", "sepia_pf_down", "sepia_pf_combine",
     "sepia_pf_split", "sepia_mq_ffn", "sepia_mq_gateup_mix", "sepia_mq_down_rows", "sepia_pf_gateup_i",
-    "sepia_pf_gateup_r",
+    "sepia_pf_gateup_r", "sepia_pf_down_r",
 };
 #undef FFN_NAMES
 
@@ -152,6 +154,8 @@ static int g_opt_dyn = 0;    /* "dyn": 1 deals the MoE down launch's steps at ru
 static int g_opt_pf_gu = 2;   /* "pf_gu": the gate/up launch of a prefill layer whose gate/up projections are
                                * all Q2_K, Q3_K or Q4_K: 2 = sepia_pf_gateup_r (codes in registers), 1 =
                                * sepia_pf_gateup_i (16 waves), 0 = sepia_pf_gateup (other layers always) */
+static int g_opt_pf_dn = 1;   /* "pf_dn": 1 = a prefill layer whose down projections are all Q2_K, Q3_K or Q4_K
+                               * runs them as sepia_pf_down_r (codes in registers), 0 = sepia_pf_down */
 static int g_opt_route_sel = 0;   /* "route_sel": 1 = the router launch's last workgroup selects the
                                    * experts even for the matrix-core FFN (0: its gate/up launch does) */
 static int g_opt_flow = 0;   /* "flow": 1 runs the expert FFN as one sepia_mq_ffn launch (gate/up and down waves) */
@@ -966,6 +970,10 @@ int sepia_hip_set_option(const char *name, int value) {
         g_opt_pf_gu = value;
         return 1;
     }
+    if (strcmp(name, "pf_dn") == 0 && (value == 0 || value == 1)) {
+        g_opt_pf_dn = value;
+        return 1;
+    }
     if (strcmp(name, "route_sel") == 0 && (value == 0 || value == 1)) {
         g_opt_route_sel = value;
         return 1;
@@ -1586,7 +1594,10 @@ int sepia_gpu_moe_prefill(const SepiaMoeLayerDesc *L, int64_t n_tokens, SepiaGpu
                  PF_LDS_BYTES, a_gu, op))
         return 0;
     void *a_dn[] = { (void *)&d, (void *)&sd, &nr32, &inter, &hid, &hh, &hl, &list, &units, &n_units, &yp };
-    if (!launch2(K_PF_DOWN, (unsigned)((H + 63) / 64), (unsigned)umax, 512, PF_LDS_BYTES, a_dn, op)) return 0;
+    const int dn_r = g_opt_pf_dn && pf_type_int(d.type) && (ns == 0 || pf_type_int(sd.type));
+    if (!launch2(dn_r ? K_PF_DOWN_R : K_PF_DOWN, (unsigned)(dn_r ? (H + 127) / 128 : (H + 63) / 64), (unsigned)umax,
+                 512, PF_LDS_BYTES, a_dn, op))
+        return 0;
     void *a_cb[] = { &yp, &sel_w, &nsel32, &tt, &hid, &y->dev };
     if (!launch2(K_PF_COMBINE, (unsigned)((H + 255) / 256), (unsigned)T, 256, 0, a_cb, op)) return 0;
     if (route_out) {

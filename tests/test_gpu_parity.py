@@ -735,6 +735,7 @@ PREFILL_CASES = [
     ((6144, 3072, 16, 2), (10, 11, 12), 48),      # BASELINE configs[4] shapes, 16 experts resident
     ((2048, 1024, 12, 1), (17, 18, 14), 33),      # IQ2_XS / IQ3_XXS routed, Q6_K shared
     ((1024, 2048, 8, 2), (13, 23, 11), 20),       # Q5_K / IQ4_XS routed, Q3_K shared
+    ((2048, 1024, 12, 1), (11, 10, 10), 37),      # Q3_K / Q2_K routed, Q2_K shared
 ]
 
 
@@ -746,21 +747,25 @@ def test_moe_prefill(dev, orc, shape, types, T, x_kind, gu):
     own routing, near-ties per the reference protocol); two runs bitwise equal.
     x either bf16-representable (the projections skip the zero lo terms) or
     full f32. gu (option pf_gu): integer-format gate/up with the codes in
-    registers (2, the default), on 16 waves (1) or on the 8-wave kernel (0)."""
+    registers (2, the default), on 16 waves (1) or on the 8-wave kernel (0);
+    gu 0 also runs the integer-format down on sepia_pf_down (option pf_dn 0)
+    instead of sepia_pf_down_r."""
     hidden, inter, n_routed, n_shared = shape
     tgu, td, ts = types
-    if gu != 2 and (tgu not in (10, 11, 12) or ts not in (10, 11, 12)):
-        pytest.skip("pf_gu changes nothing outside Q2_K / Q3_K / Q4_K gate/up layers")
+    if gu != 2 and not ({tgu, td, ts} & {10, 11, 12}):
+        pytest.skip("pf_gu / pf_dn change nothing in layers without Q2_K / Q3_K / Q4_K projections")
     rng = np.random.default_rng(hidden + 7 * T + tgu)
     desc, spec, bufs = make_layer(dev, rng, hidden=hidden, inter=inter, n_routed=n_routed, n_shared=n_shared,
                                   tg=tgu, tu=tgu, td=td, ts=ts)
     X = bf16_normal(rng, (T, hidden)) if x_kind == "bf16" else rng.standard_normal((T, hidden)).astype(np.float32)
     assert dev.L.sepia_hip_set_option(b"pf_gu", gu) == 1
+    assert dev.L.sepia_hip_set_option(b"pf_dn", 1 if gu else 0) == 1
     try:
         y, idx, w = run_prefill(dev, desc, X)
         y2, _, _ = run_prefill(dev, desc, X)
     finally:
         dev.L.sepia_hip_set_option(b"pf_gu", 2)
+        dev.L.sepia_hip_set_option(b"pf_dn", 1)
     assert np.array_equal(y.view(np.uint32), y2.view(np.uint32))
     for t in range(T):
         y_ref, logits, idx_ref, w_ref = orc.moe_layer(spec, X[t], threads=THREADS)
