@@ -771,6 +771,50 @@ extern "C" __global__ __launch_bounds__(512) void sepia_pf_gateup(
     }
 }
 
+// Raw blocks b of nr rows as pf_issue_raw, in 16-byte pieces: row k's
+// 16-byte-aligned window of PF_P16 pieces that holds the block lands at
+// dst + 16 PF_P16 k (the block at byte (row address) & 15 of it). A wave
+// instruction moves 1 KB, a quarter of the instructions of 4-byte pieces.
+template <int T> struct PfP16 { static constexpr int n = (Fmt<T>::bytes + 15 + 15) / 16; };
+template <int T>
+__device__ __forceinline__ void pf_issue_raw16(const uint8_t *W, uint64_t row_bytes, int64_t rows, int64_t r0, int nr,
+                                               int64_t b, uint8_t *dst) {
+    constexpr int BB = Fmt<T>::bytes, P16 = PfP16<T>::n;
+    const int nw = (int)(blockDim.x >> 6), w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int lane = threadIdx.x & 63;
+    const uint8_t *Wa = (const uint8_t *)((uintptr_t)W & ~(uintptr_t)15);
+    const uint32_t delta = (uint32_t)((uintptr_t)W & 15);
+    const int n_ins = (nr * P16 + 63) >> 6;
+    for (int j = w; j < n_ins; j += nw) {
+        const int i = 64 * j + lane;
+        if (i < nr * P16) {
+            const int r = i / P16, d = i - r * P16;
+            int64_t rr = r0 + r;
+            rr = rr < rows ? rr : rows - 1;
+            const uint64_t off = delta + (uint64_t)rr * row_bytes + (uint64_t)b * BB;
+            pf_dma16(Wa, (uint32_t)(off & ~(uint64_t)15) + 16u * (uint32_t)d, pf_lds(dst + 1024 * j));
+        }
+    }
+}
+
+// The staged raw window of a row for the register pipelines: 16-byte
+// pieces when their number is odd (Q2_K: 7), else pf_issue_raw's 4-byte
+// window (Q3_K: 29 dwords, Q4_K: 37). Either way the row stride is an odd
+// number of dwords times 4 at most, so the 16 rows a lane group decodes
+// from fall in different LDS banks (a stride of 32 dwords put them all in
+// one).
+template <int T> struct PfRaw {
+    static constexpr bool w16 = (PfP16<T>::n & 1) != 0;
+    static constexpr int bytes = w16 ? 16 * PfP16<T>::n : 4 * ((Fmt<T>::bytes + 6) / 4);
+    static constexpr uint32_t align = w16 ? 15u : 3u;
+    static __device__ __forceinline__ int ins(int nr) { return (nr * bytes / (w16 ? 16 : 4) + 63) >> 6; }
+    static __device__ __forceinline__ void issue(const uint8_t *W, uint64_t row_bytes, int64_t rows, int64_t r0,
+                                                 int nr, int64_t b, uint8_t *dst) {
+        if constexpr (w16) pf_issue_raw16<T>(W, row_bytes, rows, r0, nr, b, dst);
+        else pf_issue_raw<T>(W, row_bytes, rows, r0, nr, b, dst);
+    }
+};
+
 // ------------------------------------------ gate/up, codes in registers ---
 // Both M tiles (pairs 0 .. 15, 16 .. 31) of one 16-row N tile += this
 // block's share, the B fragments decoded by each lane from its own row's
@@ -861,30 +905,30 @@ __device__ __forceinline__ void pf_reg_gateup(uint8_t *smem, const uint8_t *Wg, 
                                               int64_t nb, int64_t rows, const __bf16 *ah, const __bf16 *al,
                                               const float *s16, const uint32_t *roff, const int32_t *pair, int nv,
                                               int64_t r0, bool xlo, __bf16 *__restrict__ hh, __bf16 *__restrict__ hl) {
-    constexpr int BB = Fmt<T>::bytes, RD = (BB + 6) / 4;
+    constexpr int BB = Fmt<T>::bytes, RW = PfRaw<T>::bytes;   // raw window bytes a row
     constexpr bool need_s = PfInt<T>::min16 || PfInt<T>::per_sub;
     const int w = threadIdx.x >> 6, l = threadIdx.x & 63, r = l & 15, nw = (int)(blockDim.x >> 6);
     const int mat = w >> 2, n0 = 16 * (w & 3);
-    const uint32_t a_bytes = xlo ? 2 * PF_TILE : PF_TILE, raw_bytes = 128 * RD * 4, s_bytes = need_s ? 2048 : 0;
+    const uint32_t a_bytes = xlo ? 2 * PF_TILE : PF_TILE, raw_bytes = 128 * RW, s_bytes = need_s ? 2048 : 0;
     const uint32_t st_bytes = a_bytes + raw_bytes + s_bytes;
     int S = (int)(PF_O_ROFF / st_bytes);
     S = S < 4 ? S : 4;   // >= 3 for every format (Q4_K with lo terms: 53,760-byte stages)
     auto stage = [&](int64_t b) { return smem + (uint32_t)((int)b % S) * st_bytes; };
-    const int n_raw = (64 * RD + 63) >> 6;
+    const int n_raw = PfRaw<T>::ins(64);
     const int per_stage =
         pf_share(xlo ? 32 : 16, w, nw) + 2 * pf_share(n_raw, w, nw) + (need_s ? pf_share(2, w, nw) : 0);
     auto issue = [&](int64_t b) {
         uint8_t *st = stage(b);
         pf_issue_act(ah, al, roff, b, st, xlo);
-        pf_issue_raw<T>(Wg, row_bytes, rows, r0, 64, b, st + a_bytes);
-        pf_issue_raw<T>(Wu, row_bytes, rows, r0, 64, b, st + a_bytes + 64 * RD * 4);
+        PfRaw<T>::issue(Wg, row_bytes, rows, r0, 64, b, st + a_bytes);
+        PfRaw<T>::issue(Wu, row_bytes, rows, r0, 64, b, st + a_bytes + 64 * RW);
         if constexpr (need_s) pf_issue_s16(s16, roff, b, st + a_bytes + raw_bytes);
     };
-    // this lane's row (clamped as pf_issue_raw clamps it) and its byte offset
+    // this lane's row (clamped as the raw issue clamps it) and its byte offset
     int64_t rr = r0 + n0 + r;
     rr = rr < rows ? rr : rows - 1;
-    const uint64_t rowoff = (uint64_t)((uintptr_t)(mat ? Wu : Wg) & 3) + (uint64_t)rr * row_bytes;
-    const uint32_t slot = (uint32_t)(64 * mat + n0 + r) * RD * 4;
+    const uint64_t rowoff = (uint64_t)((uintptr_t)(mat ? Wu : Wg) & PfRaw<T>::align) + (uint64_t)rr * row_bytes;
+    const uint32_t slot = (uint32_t)(64 * mat + n0 + r) * RW;
     for (int64_t b = 0; b < S - 1 && b < nb; b++) issue(b);
     pf_f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
     for (int64_t b = 0; b < nb; b++) {
@@ -893,7 +937,7 @@ __device__ __forceinline__ void pf_reg_gateup(uint8_t *smem, const uint8_t *Wg, 
         __syncthreads();   // every wave's DMAs of block b; block b - 1's reads are done
         if (b + S - 1 < nb) issue(b + S - 1);
         const uint8_t *st = stage(b);
-        const uint32_t mis = (uint32_t)(rowoff + (uint64_t)b * BB) & 3u;
+        const uint32_t mis = (uint32_t)(rowoff + (uint64_t)b * BB) & PfRaw<T>::align;
         pf_reg_mma<T>(acc0, acc1, st, st + a_bytes + slot + mis, (const float *)(st + a_bytes + raw_bytes), xlo);
     }
     __syncthreads();
@@ -1034,24 +1078,24 @@ template <int T>
 __device__ __forceinline__ void pf_reg_down(uint8_t *smem, const uint8_t *Wd, uint64_t row_bytes, int64_t nb,
                                             int64_t rows, const __bf16 *ah, const __bf16 *al, const uint32_t *roff,
                                             const int32_t *pair, int nv, int64_t r0, float *__restrict__ yp) {
-    constexpr int BB = Fmt<T>::bytes, RD = (BB + 6) / 4;
+    constexpr int BB = Fmt<T>::bytes, RW = PfRaw<T>::bytes;   // raw window bytes a row
     const int w = threadIdx.x >> 6, l = threadIdx.x & 63, r = l & 15, nw = (int)(blockDim.x >> 6);
     const int n0 = 16 * w;
-    const uint32_t a_bytes = 2 * PF_TILE, raw_bytes = 128 * RD * 4;
+    const uint32_t a_bytes = 2 * PF_TILE, raw_bytes = 128 * RW;
     const uint32_t st_bytes = a_bytes + raw_bytes;
     int S = (int)(PF_O_ROFF / st_bytes);
     S = S < 4 ? S : 4;   // 3 for Q4_K (51,712-byte stages)
     auto stage = [&](int64_t b) { return smem + (uint32_t)((int)b % S) * st_bytes; };
-    const int per_stage = pf_share(32, w, nw) + pf_share((128 * RD + 63) >> 6, w, nw);
+    const int per_stage = pf_share(32, w, nw) + pf_share(PfRaw<T>::ins(128), w, nw);
     auto issue = [&](int64_t b) {
         uint8_t *st = stage(b);
         pf_issue_act(ah, al, roff, b, st, true);
-        pf_issue_raw<T>(Wd, row_bytes, rows, r0, 128, b, st + a_bytes);
+        PfRaw<T>::issue(Wd, row_bytes, rows, r0, 128, b, st + a_bytes);
     };
     int64_t rr = r0 + n0 + r;
     rr = rr < rows ? rr : rows - 1;
-    const uint64_t rowoff = (uint64_t)((uintptr_t)Wd & 3) + (uint64_t)rr * row_bytes;
-    const uint32_t slot = (uint32_t)(n0 + r) * RD * 4;
+    const uint64_t rowoff = (uint64_t)((uintptr_t)Wd & PfRaw<T>::align) + (uint64_t)rr * row_bytes;
+    const uint32_t slot = (uint32_t)(n0 + r) * RW;
     for (int64_t b = 0; b < S - 1 && b < nb; b++) issue(b);
     pf_f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
     for (int64_t b = 0; b < nb; b++) {
@@ -1060,7 +1104,7 @@ __device__ __forceinline__ void pf_reg_down(uint8_t *smem, const uint8_t *Wd, ui
         __syncthreads();   // every wave's DMAs of block b; block b - 1's reads are done
         if (b + S - 1 < nb) issue(b + S - 1);
         const uint8_t *st = stage(b);
-        const uint32_t mis = (uint32_t)(rowoff + (uint64_t)b * BB) & 3u;
+        const uint32_t mis = (uint32_t)(rowoff + (uint64_t)b * BB) & PfRaw<T>::align;
         pf_reg_mma_dn<T>(acc0, acc1, st, st + a_bytes + slot + mis, true);
     }
     const int64_t row = r0 + n0 + r;
