@@ -456,7 +456,7 @@ def run_c5(B, warmup, steps, cpu_seconds, T=512):
         return L.sepia_gpu_moe_prefill(ctypes.byref(d), T, xb, y, None)
 
     ms = B.timed_steps(step, warmup, steps)
-    knames = ["sepia_pf_route", "sepia_pf_select", "sepia_pf_group", "sepia_pf_split", "sepia_pf_gateup",
+    knames = ["sepia_pf_route", "sepia_pf_route_m", "sepia_pf_select", "sepia_pf_group", "sepia_pf_split", "sepia_pf_gateup",
               "sepia_pf_gateup_i", "sepia_pf_gateup_r", "sepia_pf_down_r",
               "sepia_pf_down", "sepia_pf_combine"]
     kms = B.kernel_ms(step, min(steps, 5), knames)

@@ -75,6 +75,61 @@ extern "C" __global__ __launch_bounds__(256) void sepia_pf_route(const float *__
         }
 }
 
+// The same logits on the f32 matrix cores: one wave per 16-token x 16-row
+// tile (grid: T / 16 x n_tot / 16 waves), K in steps of 16 columns. Lane l
+// loads columns 4 (l >> 4) .. + 3 of the step for token / row l & 15 as one
+// float4; MFMA i of the step takes component i, so the four MFMAs cover the
+// step's 16 columns once each (f32 products, f32 sums; only the summation
+// order differs from sepia_pf_route). Needs x, rw and ld 16-byte aligned and
+// H a multiple of 128 (the host checks).
+typedef float pf_f32x4v __attribute__((ext_vector_type(4)));
+extern "C" __global__ __launch_bounds__(64) void sepia_pf_route_m(const float *__restrict__ x, int64_t T,
+                                                                  const float *__restrict__ rw, int64_t ld,
+                                                                  int64_t n_tot, int64_t H, float *__restrict__ logits) {
+    const int l = threadIdx.x & 63, r = l & 15, g = l >> 4;
+    const int64_t t0 = (int64_t)blockIdx.x * 16, r0 = (int64_t)blockIdx.y * 16;
+    const int64_t t = t0 + r < T ? t0 + r : T - 1, rr = r0 + r < n_tot ? r0 + r : n_tot - 1;
+    const pf_f32x4v *xa = (const pf_f32x4v *)(x + t * H) + g, *wa = (const pf_f32x4v *)(rw + rr * ld) + g;
+    pf_f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    // eight steps in registers while the next eight load (n a multiple of 8)
+    const int64_t n = H / 16;
+    pf_f32x4v a[8], b[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+        a[u] = xa[4 * u];
+        b[u] = wa[4 * u];
+    }
+    for (int64_t k = 0; k < n; k += 8) {
+        pf_f32x4v a2[8], b2[8];
+        const bool more = k + 8 < n;
+        if (more) {
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                a2[u] = xa[4 * (k + 8 + u)];
+                b2[u] = wa[4 * (k + 8 + u)];
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u][i], b[u][i], acc, 0, 0, 0);
+        }
+        if (more) {
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                a[u] = a2[u];
+                b[u] = b2[u];
+            }
+        }
+    }
+    // acc[i]: token t0 + 4 g + i, row r0 + r
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int64_t tt = t0 + 4 * g + i, ro = r0 + r;
+        if (tt < T && ro < n_tot) logits[tt * n_tot + ro] = acc[i];
+    }
+}
+
 // One wave per token (route.h).
 extern "C" __global__ __launch_bounds__(64) void sepia_pf_select(const float *__restrict__ logits,
                                                                  const float *__restrict__ bias, int32_t n_routed,

@@ -71,6 +71,8 @@ enum {
     K_PF_GATEUP_R,
     /* prefill down of the integer formats with the codes in registers (kernels/prefill.h) */
     K_PF_DOWN_R,
+    /* prefill router logits on the f32 matrix cores (kernels/prefill.h) */
+    K_PF_ROUTE_M,
     K_COUNT
 };
 #define FFN_NAMES(p) "sepia_ffn_gateup_" p, "sepia_ffn_gateup_" p "_xp", "sepia_ffn_down_" p
@@ -94,7 +96,7 @@ static const char *const k_names[K_COUNT] = {
     "sepia_mq_gateup", "sepia_mq_down", "sepia_mq_moe",
     "sepia_pf_route", "sepia_pf_select", "sepia_pf_group", "sepia_pf_gateup", "sepia_pf_down", "sepia_pf_combine",
     "sepia_pf_split", "sepia_mq_ffn", "sepia_mq_gateup_mix", "sepia_mq_down_rows", "sepia_pf_gateup_i",
-    "sepia_pf_gateup_r", "sepia_pf_down_r",
+    "sepia_pf_gateup_r", "sepia_pf_down_r", "sepia_pf_route_m",
 };
 #undef FFN_NAMES
 
@@ -154,6 +156,9 @@ static int g_opt_dyn = 0;    /* "dyn": 1 deals the MoE down launch's steps at ru
 static int g_opt_pf_gu = 2;   /* "pf_gu": the gate/up launch of a prefill layer whose gate/up projections are
                                * all Q2_K, Q3_K or Q4_K: 2 = sepia_pf_gateup_r (codes in registers), 1 =
                                * sepia_pf_gateup_i (16 waves), 0 = sepia_pf_gateup (other layers always) */
+static int g_opt_pf_route_m = 1;   /* "pf_route_m": 1 = prefill router logits on the f32 matrix cores
+                                    * (sepia_pf_route_m) when x and the router rows are 16-byte aligned,
+                                    * 0 = sepia_pf_route */
 static int g_opt_pf_dn = 1;   /* "pf_dn": 1 = a prefill layer whose down projections are all Q2_K, Q3_K or Q4_K
                                * runs them as sepia_pf_down_r (codes in registers), 0 = sepia_pf_down */
 static int g_opt_route_sel = 0;   /* "route_sel": 1 = the router launch's last workgroup selects the
@@ -970,6 +975,10 @@ int sepia_hip_set_option(const char *name, int value) {
         g_opt_pf_gu = value;
         return 1;
     }
+    if (strcmp(name, "pf_route_m") == 0 && (value == 0 || value == 1)) {
+        g_opt_pf_route_m = value;
+        return 1;
+    }
     if (strcmp(name, "pf_dn") == 0 && (value == 0 || value == 1)) {
         g_opt_pf_dn = value;
         return 1;
@@ -1577,7 +1586,10 @@ int sepia_gpu_moe_prefill(const SepiaMoeLayerDesc *L, int64_t n_tokens, SepiaGpu
     float rs = L->route_scale, gsc = L->global_scale;
     int32_t nr32 = nr, ns32 = ns, tk32 = tk, nsel32 = n_sel;
     void *a_rt[] = { &x->dev, &tt, &rw, &ld, &ntot, &hid, &logits };
-    if (!launch2(K_PF_ROUTE, (unsigned)((T + 31) / 32), (unsigned)((n_tot + 31) / 32), 256, 0, a_rt, op)) return 0;
+    const int rt_m = g_opt_pf_route_m && ((((uintptr_t)x->dev | (uintptr_t)rw) & 15) == 0) && (ld % 4) == 0 && H % 128 == 0;
+    if (rt_m ? !launch2(K_PF_ROUTE_M, (unsigned)((T + 15) / 16), (unsigned)((n_tot + 15) / 16), 64, 0, a_rt, op)
+             : !launch2(K_PF_ROUTE, (unsigned)((T + 31) / 32), (unsigned)((n_tot + 31) / 32), 256, 0, a_rt, op))
+        return 0;
     void *a_sel[] = { &logits, &rb, &nr32, &ns32, &tk32, &rs, &gsc, &sel_idx, &sel_w };
     if (!launch(K_PF_SELECT, (unsigned)T, 64, a_sel, op)) return 0;
     void *a_grp[] = { &sel_idx, &tt, &nr32, &ns32, &tk32, &list, &units, &n_units, &lo_any };

@@ -749,23 +749,26 @@ def test_moe_prefill(dev, orc, shape, types, T, x_kind, gu):
     full f32. gu (option pf_gu): integer-format gate/up with the codes in
     registers (2, the default), on 16 waves (1) or on the 8-wave kernel (0);
     gu 0 also runs the integer-format down on sepia_pf_down (option pf_dn 0)
-    instead of sepia_pf_down_r."""
+    instead of sepia_pf_down_r and the router on sepia_pf_route (option
+    pf_route_m 0) instead of the matrix-core one."""
     hidden, inter, n_routed, n_shared = shape
     tgu, td, ts = types
-    if gu != 2 and not ({tgu, td, ts} & {10, 11, 12}):
-        pytest.skip("pf_gu / pf_dn change nothing in layers without Q2_K / Q3_K / Q4_K projections")
+    if gu == 1 and not ({tgu, ts} <= {10, 11, 12}):
+        pytest.skip("pf_gu 1 changes nothing in layers whose gate/up is not all Q2_K / Q3_K / Q4_K")
     rng = np.random.default_rng(hidden + 7 * T + tgu)
     desc, spec, bufs = make_layer(dev, rng, hidden=hidden, inter=inter, n_routed=n_routed, n_shared=n_shared,
                                   tg=tgu, tu=tgu, td=td, ts=ts)
     X = bf16_normal(rng, (T, hidden)) if x_kind == "bf16" else rng.standard_normal((T, hidden)).astype(np.float32)
     assert dev.L.sepia_hip_set_option(b"pf_gu", gu) == 1
     assert dev.L.sepia_hip_set_option(b"pf_dn", 1 if gu else 0) == 1
+    assert dev.L.sepia_hip_set_option(b"pf_route_m", 1 if gu else 0) == 1
     try:
         y, idx, w = run_prefill(dev, desc, X)
         y2, _, _ = run_prefill(dev, desc, X)
     finally:
         dev.L.sepia_hip_set_option(b"pf_gu", 2)
         dev.L.sepia_hip_set_option(b"pf_dn", 1)
+        dev.L.sepia_hip_set_option(b"pf_route_m", 1)
     assert np.array_equal(y.view(np.uint32), y2.view(np.uint32))
     for t in range(T):
         y_ref, logits, idx_ref, w_ref = orc.moe_layer(spec, X[t], threads=THREADS)
