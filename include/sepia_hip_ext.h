@@ -132,7 +132,14 @@ void *sepia_hip_stream(void);
  *   "dyn" 0/1     the FFN down launch deals its steps at run time from an
  *                 LDS counter (default 0);
  *   "hxq" 0/1     h crosses from the gate/up to the down launch in XQ form
- *                 instead of f32 (default 0). */
+ *                 instead of f32 (default 0);
+ *   "pf_gu" 2/1/0 prefill gate/up of a layer whose gate/up projections are
+ *                 all Q2_K/Q3_K/Q4_K: codes decoded into registers (2,
+ *                 default), 16 waves with code tiles in LDS (1), 8 waves (0);
+ *   "pf_dn" 1/0   prefill down with the codes in registers when every down
+ *                 projection is Q2_K/Q3_K/Q4_K (default 1);
+ *   "pf_route_m" 1/0  prefill router logits on the f32 matrix cores when x
+ *                 and the router rows are 16-byte aligned (default 1). */
 int sepia_hip_set_option(const char *name, int value);
 
 #ifdef __cplusplus
