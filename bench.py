@@ -191,7 +191,7 @@ class Bench:
 # HBM bytes per launch of the C2 kernels, measured with rocprofv3's FETCH_SIZE and WRITE_SIZE
 # counters and scaled by what the same counters read for the copy kernel of known size
 # (profiles/expert_ffn_c2_hbm_traffic.md). Reported as roofline.traffic for the dominant kernel.
-MEASURED_TRAFFIC = {"sepia_mq_gateup": 12864276, "sepia_mq_down": 8485596}
+MEASURED_TRAFFIC = {"sepia_mq_gateup": 12847014, "sepia_mq_down": 8474192}
 
 
 def cpu_sample(fn, min_seconds, max_calls):
