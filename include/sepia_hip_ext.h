@@ -70,8 +70,7 @@ int sepia_gpu_moe_prefill(const SepiaMoeLayerDesc *layer, int64_t n_tokens, Sepi
 
 /* One routed expert: y = down(silu(gate x) * up x) for expert `expert` of
  * stacks holding n_experts experts (reference src/sepia.c:2993-3017,
- * real_expert_ffn), as two launches (fused gate/up/SwiGLU, then down), or
- * one with the "fuse" option.
+ * real_expert_ffn), as two launches (fused gate/up/SwiGLU, then down).
  * x, y: f32 [hidden] at offset 0. */
 int sepia_gpu_expert_ffn(const SepiaExpertTensor *gate, const SepiaExpertTensor *up, const SepiaExpertTensor *down,
                          int n_experts, int expert, int64_t hidden, int64_t inter, SepiaGpuBuf *x, SepiaGpuBuf *y);
@@ -97,6 +96,20 @@ int sepia_hip_synth_blocks(int ggml_type, SepiaGpuBuf *buf, size_t off, int64_t 
  * installed IQ2_XXS is rejected as unsupported. Needs init. */
 int sepia_hip_set_iq2xxs_grid(const uint64_t *grid256);
 
+/* Grows the library's scratch region (router logits, selections, h, partial
+ * rows) to at least `bytes` now, so that later calls of the same or smaller
+ * shapes allocate nothing. A call whose scratch would have to grow while the
+ * stream is being captured fails instead (an allocation cannot be captured):
+ * run the call once, or reserve, before beginning a capture. Needs init. */
+int sepia_hip_reserve_scratch(size_t bytes);
+
+/* Bytes copied from shared buffers' host copies to their device copies since
+ * init. sepia_gpu_host_ptr marks a whole shared buffer host-written; each op
+ * then uploads only the 1 MiB chunks of the ranges it reads that are still
+ * marked, once, so a weight slab filled once is uploaded once however many
+ * batches read it (tests read this counter to check that). */
+uint64_t sepia_hip_uploaded_bytes(void);
+
 /* The hipStream_t every op is issued on (for hipEvent timing). */
 void *sepia_hip_stream(void);
 
@@ -104,8 +117,6 @@ void *sepia_hip_stream(void);
  * value are known):
  *   "mq" 1/0      the matrix-core kernels for Q2_K/Q3_K/Q4_K and, in the
  *                 matvec, IQ2_XS/IQ3_XXS (default 1);
- *   "fuse" 0/1    the MoE layer and the expert FFN as one launch of
- *                 sepia_mq_moe instead of router + gate/up + down (default 0);
  *   "tile" 1/0    the tile kernels where the matrix-core ones do not apply
  *                 (0 = the generic one-wave-per-row kernels);
  *   "tile_t" 0..  automatic or forced row steps per tile workgroup;
@@ -116,28 +127,10 @@ void *sepia_hip_stream(void);
  *                 DMA issued ahead of the weight prologue, 3 = converter
  *                 waves (DMA into the XQ place, converted there while the
  *                 other waves decode their first step; matvec launches
- *                 only). The FFN down launch reads h in XQ form as the
- *                 gate/up launch wrote it, whatever this says;
- *   "flow" 0/1    the expert FFN as one launch of sepia_mq_ffn, gate/up
- *                 and down waves side by side (default 0);
- *   "flow_delay"  ticks (10 ns) the flow launch's workgroups without
- *                 gate/up rows hold their down weights back (default 250);
- *   "mix" 0/1     the MoE decode's gate/up as sepia_mq_gateup_mix: every
- *                 workgroup streams shared-expert rows while its wave 0
- *                 selects, then routed rows (default 0);
- *   "route_sel" 0/1  the router launch's last workgroup selects the experts
- *                 even for the matrix-core FFN (default 0: gate/up selects);
- *   "dnrows" 0/1  the MoE decode's down as sepia_mq_down_rows: every slot of
- *                 a row group in one workgroup, summed in LDS (default 0);
- *   "dyn" 0/1     the FFN down launch deals its steps at run time from an
- *                 LDS counter (default 0);
- *   "hxq" 0/1     h crosses from the gate/up to the down launch in XQ form
- *                 instead of f32 (default 0);
- *   "pf_gu" 2/1/0 prefill gate/up of a layer whose gate/up projections are
- *                 all Q2_K/Q3_K/Q4_K: codes decoded into registers (2,
- *                 default), 16 waves with code tiles in LDS (1), 8 waves (0);
- *   "pf_dn" 1/0   prefill down with the codes in registers when every down
- *                 projection is Q2_K/Q3_K/Q4_K (default 1);
+ *                 only);
+ *   "pf_reg" 1/0  prefill gate/up and down of layers whose projections are
+ *                 all Q2_K/Q3_K/Q4_K with the codes decoded into registers
+ *                 (1, default), or on the LDS-tile kernels (0);
  *   "pf_route_m" 1/0  prefill router logits on the f32 matrix cores when x
  *                 and the router rows are 16-byte aligned (default 1). */
 int sepia_hip_set_option(const char *name, int value);

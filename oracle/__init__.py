@@ -27,7 +27,7 @@ GEOM = {F32: (1, 4), F16: (1, 2), Q8_0: (32, 34), Q2_K: (256, 84), Q3_K: (256, 1
 # Byte offsets of the f16 scale fields inside one block.
 F16_FIELDS = {Q8_0: (0,), Q2_K: (80, 82), Q3_K: (108,), Q4_K: (0, 2), Q5_K: (0, 2), Q6_K: (208,),
               IQ2_XXS: (0,), IQ2_XS: (0,), IQ3_XXS: (0,), IQ4_XS: (0,)}
-# Types the reference's src/quants.c decodes (src/quants.c:46-51).
+# Types the reference's src/quants.c decodes (src/quants.c:28-56).
 REF_TYPES = (F16, Q8_0, Q4_K, Q5_K, Q6_K, IQ2_XS, IQ3_XXS, IQ4_XS)
 
 _lib = None

@@ -48,7 +48,7 @@ void orc_set_iq2xxs_grid(const uint64_t *grid256) {
 }
 
 /* ------------------------------------------------------------ sizes ---- */
-/* Block geometry: src/quants.c:46-51 for the reference's types,
+/* Block geometry: src/quants.c:28-56 for the reference's types,
  * tools/gguf_inspect.py:109-117 for Q2_K (84 B), Q3_K (110 B), IQ2_XXS (66 B). */
 static int geom(int t, int64_t *elems, size_t *bytes) {
     int64_t e; size_t b;
@@ -82,7 +82,7 @@ size_t orc_row_bytes(int t, int64_t n) {
 }
 
 /* ------------------------------------------------------------ f16 ------ */
-/* src/quants.c:77-96: exact IEEE binary16 -> binary32, subnormals normalised,
+/* src/quants.c:58-77: exact IEEE binary16 -> binary32, subnormals normalised,
  * inf/nan keep their payload. */
 float orc_f16_to_f32(uint16_t h) {
     uint32_t sign = (uint32_t)(h >> 15) << 31;
@@ -114,14 +114,14 @@ static inline float h2f(const uint8_t *p) { return orc_f16_to_f32(rd16(p)); }
 /* Each decodes ONE block into out[]. Rounding order per the reference line
  * cited; every `a * b - c` is two separately rounded operations. */
 
-/* src/quants.c:104-113: y = d * q, q int8. */
+/* src/quants.c:85-94: y = d * q, q int8. */
 static void blk_q8_0(const uint8_t *b, float *out) {
     const float d = h2f(b);
     for (int i = 0; i < 32; i++) out[i] = d * (float)(int8_t)b[2 + i];
 }
 
 /* 6-bit (scale, min) pair number j of the 12 packed K-quant scale bytes
- * (src/quants.c:115-121): j < 4 keeps the low 6 bits of bytes j and j+4;
+ * (src/quants.c:96-102): j < 4 keeps the low 6 bits of bytes j and j+4;
  * j >= 4 joins a nibble of byte j+4 with the top 2 bits of byte j-4 / j. */
 static void k4_scale_min(const uint8_t *s, int j, int *sc, int *mn) {
     if (j < 4) {
@@ -133,7 +133,7 @@ static void k4_scale_min(const uint8_t *s, int j, int *sc, int *mn) {
     }
 }
 
-/* src/quants.c:123-144. Layout {f16 d@0, f16 dmin@2, scales[12]@4, qs[128]@16}.
+/* src/quants.c:104-125. Layout {f16 d@0, f16 dmin@2, scales[12]@4, qs[128]@16}.
  * 64-weight chunk c: low nibbles of qs[32c..32c+31] are sub-block 2c, high
  * nibbles sub-block 2c+1; y = (d*sc)*q - (dmin*m). */
 static void blk_q4_k(const uint8_t *b, float *out) {
@@ -152,7 +152,7 @@ static void blk_q4_k(const uint8_t *b, float *out) {
     }
 }
 
-/* src/quants.c:146-170. Layout {d@0, dmin@2, scales[12]@4, qh[32]@16, ql[128]@48}.
+/* src/quants.c:127-151. Layout {d@0, dmin@2, scales[12]@4, qh[32]@16, ql[128]@48}.
  * As Q4_K plus a fifth bit: qh[l] bit (2c + half) adds 16. */
 static void blk_q5_k(const uint8_t *b, float *out) {
     const float d = h2f(b), dmin = h2f(b + 2);
@@ -171,7 +171,7 @@ static void blk_q5_k(const uint8_t *b, float *out) {
     }
 }
 
-/* src/quants.c:172-196. Layout {ql[128]@0, qh[64]@128, int8 sc[16]@192, f16 d@208}.
+/* src/quants.c:153-177. Layout {ql[128]@0, qh[64]@128, int8 sc[16]@192, f16 d@208}.
  * Half h (128 weights) uses ql[64h..], qh[32h..], sc[8h..]. Weight 32r + l of
  * the half (r = 0..3, l = 0..31): low 4 bits from ql[l + 32*(r&1)] (nibble r>>1),
  * 2 high bits from qh[l] >> 2r, minus 32; y = (d * sc[r*2 + l/16]) * q. */
@@ -248,7 +248,7 @@ static inline uint8_t sign_bits(int idx7) {
     return (uint8_t)(idx7 | ((__builtin_popcount((unsigned)idx7) & 1) << 7));
 }
 
-/* src/quants.c:198-220. Layout {d@0, u16 qs[32]@2, scales[8]@66}. Group of
+/* src/quants.c:179-201. Layout {d@0, u16 qs[32]@2, scales[8]@66}. Group of
  * 32 (ib): db = (d * (0.5 + nibble)) * 0.25, low nibble for its first 16
  * weights, high for the last 16; each u16 = 9-bit grid index | 7-bit signs. */
 static void blk_iq2_xs(const uint8_t *b, float *out) {
@@ -289,7 +289,7 @@ static void blk_iq2_xxs(const uint8_t *b, float *out) {
     }
 }
 
-/* src/quants.c:222-245. Layout {d@0, qs[64]@2, scales_and_signs[32]@66}.
+/* src/quants.c:203-226. Layout {d@0, qs[64]@2, scales_and_signs[32]@66}.
  * Group ib: u32 a at 66 + 4ib; db = (d * (0.5 + (a >> 28))) * 0.5; eight
  * weights per step l take grid entries qs[8ib + 2l], qs[8ib + 2l + 1] and
  * signs (a >> 7l) & 127. */
@@ -312,7 +312,7 @@ static void blk_iq3_xxs(const uint8_t *b, float *out) {
     }
 }
 
-/* src/quants.c:247-267. Layout {d@0, u16 scales_h@2, scales_l[4]@4, qs[128]@8}.
+/* src/quants.c:228-248. Layout {d@0, u16 scales_h@2, scales_l[4]@4, qs[128]@8}.
  * Group ib: 6-bit ls = nibble ib of scales_l | 2 bits of scales_h << 4;
  * dl = d * (ls - 32); y = dl * kvalues[nibble]. */
 static void blk_iq4_xs(const uint8_t *b, float *out) {
@@ -329,7 +329,7 @@ static void blk_iq4_xs(const uint8_t *b, float *out) {
     }
 }
 
-/* src/quants.c:269-284: per-type dispatch over whole blocks. */
+/* src/quants.c:250-265: per-type dispatch over whole blocks. */
 int orc_dequantize_row(int t, const void *src, float *dst, int64_t n) {
     int64_t e; size_t bb;
     if (!geom(t, &e, &bb) || n < 0 || n % e) return 0;

@@ -31,7 +31,7 @@ __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
 }
 
 // binary16 -> binary32 with the integer recipe that also keeps NaN payloads
-// unquieted (reference src/quants.c:77-96); used where the raw f16 value is
+// unquieted (reference src/quants.c:58-77); used where the raw f16 value is
 // the output (the F16 dequant), not for block scales.
 __device__ __forceinline__ float f16_bits_to_f32_exact(uint32_t h) {
     uint32_t sign = (h >> 15) << 31;

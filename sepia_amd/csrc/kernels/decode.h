@@ -2,7 +2,7 @@
 //
 // decode_part<T>(blk, p, out) writes weights 32p .. 32p+31 of the block at
 // `blk` into out[0..31], rounding exactly like the reference CPU decoder
-// (src/quants.c:104-267): every product and difference rounds on its own
+// (src/quants.c:85-248): every product and difference rounds on its own
 // (the code object is compiled with -ffp-contract=off) and operands combine
 // in the reference's order. Q2_K, Q3_K and IQ2_XXS are not in the
 // reference; they follow the public ggml layout. These are the decoders of
@@ -39,7 +39,7 @@ __device__ __forceinline__ uint32_t iq_signs(uint32_t idx7) {
 }
 
 // 6-bit (scale, min) pair j of the packed K-quant scale bytes
-// (src/quants.c:115-121).
+// (src/quants.c:96-102).
 __device__ __forceinline__ void k4_scale_min(const uint8_t *s, int j, int &sc, int &mn) {
     if (j < 4) {
         sc = ld_u8(s + j) & 63;
@@ -52,14 +52,14 @@ __device__ __forceinline__ void k4_scale_min(const uint8_t *s, int j, int &sc, i
 
 template <int T> __device__ void decode_part(const uint8_t *b, int p, float *out);
 
-// src/quants.c:104-113
+// src/quants.c:85-94
 template <> __device__ void decode_part<ST_Q8_0>(const uint8_t *b, int, float *out) {
     const float d = h2f(b);
 #pragma unroll
     for (int i = 0; i < 32; i++) out[i] = d * (float)(int8_t)ld_u8(b + 2 + i);
 }
 
-// src/quants.c:123-144: part p = sub-block p; nibble (p & 1) of qs[32*(p/2) + l].
+// src/quants.c:104-125: part p = sub-block p; nibble (p & 1) of qs[32*(p/2) + l].
 template <> __device__ void decode_part<ST_Q4_K>(const uint8_t *b, int p, float *out) {
     const float d = h2f(b), dmin = h2f(b + 2);
     int sc, mn;
@@ -71,7 +71,7 @@ template <> __device__ void decode_part<ST_Q4_K>(const uint8_t *b, int p, float 
     for (int l = 0; l < 32; l++) out[l] = ds * (float)((ld_u8(qs + l) >> sh) & 15) - dm;
 }
 
-// src/quants.c:146-170: as Q4_K plus bit p of qh[l] worth 16.
+// src/quants.c:127-151: as Q4_K plus bit p of qh[l] worth 16.
 template <> __device__ void decode_part<ST_Q5_K>(const uint8_t *b, int p, float *out) {
     const float d = h2f(b), dmin = h2f(b + 2);
     int sc, mn;
@@ -87,7 +87,7 @@ template <> __device__ void decode_part<ST_Q5_K>(const uint8_t *b, int p, float 
     }
 }
 
-// src/quants.c:172-196: part p = 32r + l rows of half h = p/4, r = p%4.
+// src/quants.c:153-177: part p = 32r + l rows of half h = p/4, r = p%4.
 template <> __device__ void decode_part<ST_Q6_K>(const uint8_t *b, int p, float *out) {
     const float d = h2f(b + 208);
     const int h = p >> 2, r = p & 3;
@@ -140,7 +140,7 @@ template <> __device__ void decode_part<ST_Q3_K>(const uint8_t *b, int p, float 
     }
 }
 
-// src/quants.c:198-220
+// src/quants.c:179-201
 template <> __device__ void decode_part<ST_IQ2_XS>(const uint8_t *b, int p, float *out) {
     const float d = h2f(b);
     const uint32_t sb = ld_u8(b + 66 + p);
@@ -172,7 +172,7 @@ template <> __device__ void decode_part<ST_IQ2_XXS>(const uint8_t *b, int p, flo
     }
 }
 
-// src/quants.c:222-245
+// src/quants.c:203-226
 template <> __device__ void decode_part<ST_IQ3_XXS>(const uint8_t *b, int p, float *out) {
     const float d = h2f(b);
     const uint32_t a = ld_u32(b + 66 + 4 * p);
@@ -192,7 +192,7 @@ template <> __device__ void decode_part<ST_IQ3_XXS>(const uint8_t *b, int p, flo
     }
 }
 
-// src/quants.c:247-267
+// src/quants.c:228-248
 template <> __device__ void decode_part<ST_IQ4_XS>(const uint8_t *b, int p, float *out) {
     const float d = h2f(b);
     const uint32_t sh = ld_u16(b + 2);

@@ -903,12 +903,8 @@ struct MqItem {
 // last conv waves of the workgroup DMA the vector straight into its XQ
 // place and convert it there while the others stream and decode their
 // first step; xraw is then the LDS offset of 16 bytes of control words.
-// dyn: the steps are dealt at run time (MqDyn; P is then the quads per
-// row, the partials' count per item).
-// xq_in: the vector arrives already in XQ form (written so by the previous
-// launch) and is only DMA'd into place.
 struct MqGeo {
-    int32_t P, ring, xraw, orings, conv, dyn, xq_in;
+    int32_t P, ring, xraw, orings, conv;
 };
 
 // The pipeline of one wave over n_items items of format T, in two halves:
@@ -1040,21 +1036,9 @@ struct MqWave {
     // to finish it; the converter waves return at once after. Every wave of
     // the workgroup calls this. CONV false compiles that path out (the host
     // never plans it for such a kernel), which keeps the kernel's registers
-    // for its own pipeline. With geo.xq_in the vector is already XQ bytes:
-    // DMA'd straight into place, ahead of the weights.
+    // for its own pipeline.
     template <bool CONV = true>
     __device__ __forceinline__ void go(const float *src, const MqGeo &geo, uint8_t *lds0, uint32_t xoff, float *red) {
-        if (geo.xq_in) {
-            mq_dma_vec(src, n, mq_lds_addr(lds0 + xoff));
-            if (threadIdx.x < MQ_ZERO / 16) ((uint4 *)(lds0))[threadIdx.x] = make_uint4(0, 0, 0, 0);
-            __builtin_amdgcn_s_waitcnt(MQ_WC_LGKM0);
-            __builtin_amdgcn_s_barrier();
-            prologue();
-            wait_before_prologue();
-            __syncthreads();
-            run(lds0, red);
-            return;
-        }
         if (!CONV || geo.conv == 0) {
             start(src, geo, lds0, xoff);
             run(lds0, red);
@@ -1128,141 +1112,6 @@ struct MqWave {
                 acc = 0.0f;
                 ++ck;
             }
-            if (++cslot == S) cslot = 0;
-        }
-    }
-};
-
-// The same pipeline with the steps dealt at run time: the workgroup's
-// steps (item i, quad q) are numbered i * nq + q, and each wave takes the
-// next number from an LDS counter whenever it refills a ring slot, so that a
-// wave whose bytes arrive early takes more steps (with one step in flight
-// per wave, fixed shares make the slowest wave's chain of round trips the
-// workgroup's time). Every step writes its own 16 row partials to
-// red[(i * nq + q) * 16 ..]: mq_red_sum(red, i, nq, t) sums them in quad
-// order whichever waves ran them, so the result does not depend on the
-// schedule. Waves first .. first + count - 1 take part; ctr: an LDS word,
-// zero before the workgroup's first barrier of the run.
-template <int T, class ItemFn>
-struct MqDyn {
-    static constexpr int W = MQ<T>::W, Wp = MQ<T>::Wp;
-    const ItemFn &item_of;
-    int total, nq, n;
-    uint32_t rb;
-    int S;
-    uint32_t ring;
-    const uint8_t *ringp;
-    uint32_t *ctr;
-    MqLane L;
-    bool on;
-    // the step in ring slot k (-1: none), as four scalars: a private array
-    // indexed at run time would live in scratch memory, whose loads count
-    // in vmcnt and would upset the DMA waits
-    int ss0, ss1, ss2, ss3;
-    __device__ __forceinline__ int sget(int k) const { return k == 0 ? ss0 : k == 1 ? ss1 : k == 2 ? ss2 : ss3; }
-    __device__ __forceinline__ void sset(int k, int v) {
-        ss0 = k == 0 ? v : ss0;
-        ss1 = k == 1 ? v : ss1;
-        ss2 = k == 2 ? v : ss2;
-        ss3 = k == 3 ? v : ss3;
-    }
-    int islot;
-    const uint8_t *tab = nullptr;
-    __device__ __forceinline__ MqDyn(const ItemFn &f, int n_items, int nq_, int n_, uint32_t rb_, MqGeo geo,
-                                     uint8_t *ring_lds, uint32_t *ctr_, int first = 0, int count = -1)
-        : item_of(f), total(n_items * nq_), nq(nq_), n(n_), rb(rb_), ctr(ctr_) {
-        const int w = mq_wave_id(), wk = w - first;
-        const int nw = count >= 0 ? count : (int)(blockDim.x >> 6) - first;
-        on = wk >= 0 && wk < nw;
-        S = geo.ring / (Wp * 1024);
-        S = S < 4 ? S : 4;
-        ringp = ring_lds + (ptrdiff_t)wk * geo.ring;
-        ring = mq_lds_addr(ringp);
-        L = mq_lane();
-        islot = 0;
-        ss0 = ss1 = ss2 = ss3 = -1;
-    }
-    // Takes the next step into ring slot islot (none once they are all dealt).
-    __device__ __forceinline__ void issue() {
-        uint32_t st = 0;
-        if (L.lane == 0) st = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-        const int step = __builtin_amdgcn_readfirstlane((int)st);
-        const int k = islot;
-        if (++islot == S) islot = 0;
-        if (step >= total) {
-            sset(k, -1);
-            return;
-        }
-        sset(k, step);
-        const int item = step / nq, qd = step - item * nq;
-        const MqItem it = item_of(item);
-        const uint32_t q4 = 4u * (uint32_t)qd;
-        const uint32_t dst = ring + (uint32_t)k * (uint32_t)(Wp * 1024);
-        const uint32_t rmax = (uint32_t)(it.rows - 1 - it.row0);
-        const uint32_t rbase = (uint32_t)it.row0 * rb;
-#pragma unroll
-        for (int d = 0; d < Wp; d++) {
-            const uint32_t i = 64u * (uint32_t)d + (uint32_t)L.lane;
-            const uint32_t cl = i / (uint32_t)Wp, kk = i - cl * (uint32_t)Wp;
-            const uint32_t j = cl & 15u, r = j < rmax ? j : rmax;
-            const uint32_t boff = (uint32_t)MQ<T>::bytes * (q4 + (cl >> 4));
-            const uint32_t off = rbase + r * rb + boff - MQ<T>::shift(boff) + MQ<T>::word(kk < (uint32_t)W ? kk : W - 1);
-            mq_dma16(it.base, off, dst + 1024u * (uint32_t)d);
-        }
-    }
-    __device__ __forceinline__ void prologue() {
-        if (!on) return;
-        for (int t = 0; t < S; t++) issue();
-    }
-    // The vector by LDS DMA into a raw copy (geo.xraw), ahead of the
-    // weights, then converted once it has landed (as MqWave::start); the
-    // step counter is zeroed before the barrier that precedes any step.
-    __device__ __forceinline__ void start(const float *src, const MqGeo &geo, uint8_t *lds0, uint32_t xoff) {
-        mq_dma_vec(src, n, mq_lds_addr(lds0 + geo.xraw));
-        if (threadIdx.x == 0) *ctr = 0u;
-        __builtin_amdgcn_s_waitcnt(MQ_WC_LGKM0);
-        __builtin_amdgcn_s_barrier();
-        prologue();
-        int c = 0;
-#pragma unroll
-        for (int k = 0; k < 4; k++)
-            if (k < S && sget(k) >= 0) c++;
-        mq_wait_stages<Wp>(c);   // this wave's vector DMAs (older than its weights)
-        __syncthreads();
-        mq_stage_xq_lds((const float *)(lds0 + geo.xraw), n, lds0, xoff);
-    }
-    // Stages in flight after slot k, counted in ring order.
-    __device__ __forceinline__ int after(int k) const {
-        int c = 0;
-#pragma unroll
-        for (int d = 1; d < 4; d++)
-            if (d < S && sget((k + d) % S) >= 0) c++;
-        return c;
-    }
-    __device__ __forceinline__ void run(const uint8_t *lds0, float *red) {
-        if (!on) return;
-        int cslot = 0;
-        while (sget(cslot) >= 0) {
-            const int step = sget(cslot);
-            mq_wait_stages<Wp>(after(cslot));
-            uint4 w[W];
-            const uint8_t *src = ringp + (size_t)cslot * (Wp * 1024) + 16 * Wp * L.lane;
-#pragma unroll
-            for (int k = 0; k < W; k++) w[k] = *(const uint4 *)(src + 16 * k);
-            __builtin_amdgcn_s_waitcnt(MQ_WC_LGKM0);
-            islot = cslot;
-            issue();   // refills this slot (or marks it empty)
-            const int item = step / nq, qd = step - item * nq;
-            const MqItem it = item_of(item);
-            const uint32_t b = 4u * (uint32_t)qd + (uint32_t)L.g;
-            MqCtx x;
-            x.lds0 = lds0;
-            x.abase = L.a_lane ? it.xoff + MQ_BREC * b + 16u * (uint32_t)L.p : 0u;
-            x.xsb = (const float *)(lds0 + it.xoff + mq_xq_planes(n)) + 16u * b;
-            x.gvb = x.xsb + MQ<T>::sum_sel * (n >> 4);
-            x.tab = tab;
-            const float acc = mq_sum_units(MQ<T>::block(w, MQ<T>::shift((uint32_t)MQ<T>::bytes * b), x));
-            if (L.lane < 16) red[((int64_t)it.red * nq + qd) * 16 + L.lane] = acc;
             if (++cslot == S) cslot = 0;
         }
     }
@@ -1348,7 +1197,7 @@ __device__ __forceinline__ int64_t mq_slot_expert(const int32_t *sel_idx, int32_
 template <int T>
 __device__ __forceinline__ void mq_gateup_slot(const uint8_t *Wg, const uint8_t *Wu, uint64_t row_bytes, int32_t nb,
                                                int32_t inter, int32_t j0, int32_t jstep, const float *__restrict__ x,
-                                               float *__restrict__ h, MqGeo geo, bool x_issued, bool hxq) {
+                                               float *__restrict__ h, MqGeo geo, bool x_issued) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int n = 256 * nb;
     const int tiles = (inter + 15) >> 4;
@@ -1370,35 +1219,6 @@ __device__ __forceinline__ void mq_gateup_slot(const uint8_t *Wg, const uint8_t 
     wv.x_issued = x_issued;
     wv.template go<false>(x, geo, smem, xoff, red);
     __syncthreads();
-    if (hxq) {
-        // h in XQ form for the down launch, in one pass: a row group is one
-        // 16-column segment of h (inter is a multiple of 16), four lanes a
-        // segment (lane j: rows 4j .. 4j + 3, mq_xq_quad); only the waves
-        // that own row groups (16 a wave), every quad the same iterations
-        const int j = (int)threadIdx.x & 3, per = (int)(blockDim.x >> 2);
-        float *xsv = (float *)((uint8_t *)h + mq_xq_planes(inter));
-        for (int k0 = 0; k0 < nk && 16 * mq_wave_id() < nk - k0; k0 += per) {
-            const int k = k0 + (int)(threadIdx.x >> 2), kk = k < nk ? k : nk - 1;
-            float a[4];
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-                a[i] = silu_f32(mq_red_sum(red, 2 * kk, geo.P, 4 * j + i)) * mq_red_sum(red, 2 * kk + 1, geo.P, 4 * j + i);
-            const XqQuad r = mq_xq_quad(a);
-            if (k < nk) {
-                const int64_t seg = (int64_t)j0 + (int64_t)k * jstep;
-                uint32_t *pl = (uint32_t *)((uint8_t *)h + (seg >> 4) * MQ_BREC + (seg & 15) * 48) + j;
-                pl[0] = r.p0;
-                pl[4] = r.p1;
-                pl[8] = r.p2;
-                if (j == 0) {
-                    xsv[seg] = r.xs;
-                    xsv[inter / 16 + seg] = r.gs;
-                    xsv[inter / 8 + seg] = r.gq;
-                }
-            }
-        }
-        return;
-    }
     for (int i = threadIdx.x; i < nk * 16; i += blockDim.x) {
         const int k = i >> 4, t = i & 15;
         const int64_t r = ((int64_t)j0 + (int64_t)k * jstep) * 16 + t;
@@ -1430,7 +1250,7 @@ __device__ __forceinline__ void mq_gateup(const MqProj &gate, const MqProj &up, 
                                           const MqProj &s_up, const int32_t *__restrict__ sel_idx, int32_t fixed,
                                           int32_t topk, int32_t inter, int32_t wps_r, int32_t wps_s,
                                           const float *__restrict__ x, float *__restrict__ h, MqGeo geo,
-                                          const MqRoute &rt, int32_t hxq) {
+                                          const MqRoute &rt) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int32_t bid = (int32_t)blockIdx.x;
     const bool rk = bid < topk * wps_r;
@@ -1466,9 +1286,9 @@ __device__ __forceinline__ void mq_gateup(const MqProj &gate, const MqProj &up, 
     float *hs = h + (int64_t)slot * inter;
     const int32_t nb = (int32_t)G.n_blocks;
     switch (G.type) {
-    case ST_Q2_K: mq_gateup_slot<ST_Q2_K>(wg, wu, G.row_bytes, nb, inter, j0, wps, x, hs, geo, x_issued, hxq); break;
-    case ST_Q3_K: mq_gateup_slot<ST_Q3_K>(wg, wu, G.row_bytes, nb, inter, j0, wps, x, hs, geo, x_issued, hxq); break;
-    default: mq_gateup_slot<ST_Q4_K>(wg, wu, G.row_bytes, nb, inter, j0, wps, x, hs, geo, x_issued, hxq); break;
+    case ST_Q2_K: mq_gateup_slot<ST_Q2_K>(wg, wu, G.row_bytes, nb, inter, j0, wps, x, hs, geo, x_issued); break;
+    case ST_Q3_K: mq_gateup_slot<ST_Q3_K>(wg, wu, G.row_bytes, nb, inter, j0, wps, x, hs, geo, x_issued); break;
+    default: mq_gateup_slot<ST_Q4_K>(wg, wu, G.row_bytes, nb, inter, j0, wps, x, hs, geo, x_issued); break;
     }
 }
 
@@ -1476,8 +1296,8 @@ __device__ __forceinline__ void mq_gateup(const MqProj &gate, const MqProj &up, 
     extern "C" __global__ __launch_bounds__(1024) void sepia_mq_gateup(                                  \
         MqProj gate, MqProj up, MqProj s_gate, MqProj s_up, const int32_t *__restrict__ sel_idx,         \
         int32_t fixed, int32_t topk, int32_t inter, int32_t wps_r, int32_t wps_s,                        \
-        const float *__restrict__ x, float *__restrict__ h, MqGeo geo, MqRoute rt, int32_t hxq) {        \
-        mq_gateup(gate, up, s_gate, s_up, sel_idx, fixed, topk, inter, wps_r, wps_s, x, h, geo, rt, hxq); \
+        const float *__restrict__ x, float *__restrict__ h, MqGeo geo, MqRoute rt) {                      \
+        mq_gateup(gate, up, s_gate, s_up, sel_idx, fixed, topk, inter, wps_r, wps_s, x, h, geo, rt);      \
     }
 
 // Down, one slot per workgroup: workgroups [0, topk * wps_r) serve the
@@ -1506,14 +1326,6 @@ __device__ __forceinline__ void mq_dn_slot(const uint8_t *Wd, uint64_t row_bytes
         it.red = i;
         return it;
     };
-    if (geo.dyn) {
-        // the step counter sits after the arrival flags (host slack)
-        uint32_t *ctr = (uint32_t *)((uint8_t *)red + (size_t)nk * geo.P * 64 + (size_t)nk * 4);
-        MqDyn<T, decltype(item_of)> dw(item_of, nk, nb >> 2, inter, (uint32_t)row_bytes, geo, rings, ctr);
-        dw.start(hs, geo, lds0, MQ_ZERO);
-        dw.run(lds0, red);
-        return;
-    }
     MqWave<T, decltype(item_of)> wv(item_of, nk, nb >> 2, inter, (uint32_t)row_bytes, geo, rings, 0,
                                     (int)(blockDim.x >> 6) - geo.conv);
     wv.template go<false>(hs, geo, lds0, MQ_ZERO, red);

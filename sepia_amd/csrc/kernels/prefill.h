@@ -488,8 +488,8 @@ template <> struct PfInt<ST_Q4_K> {
 
 // B tiles (codes) and per-row scalars of the staged raw blocks: nper rows of
 // W0 into B0 and, with W1, nper rows of W1 into B1; rows counted across
-// both (rg) index rs[rg][16] and bm[rg][16]. NT = blockDim.x.
-template <int T, int NT = 512>
+// both (rg) index rs[rg][16] and bm[rg][16]. 512 threads.
+template <int T>
 __device__ __forceinline__ void pf_int_build(const uint8_t *raw, const uint8_t *W0, const uint8_t *W1, int nper,
                                              uint64_t row_bytes, int64_t rows, int64_t r0, int64_t b, uint8_t *B0,
                                              uint8_t *B1, float *rs, __bf16 *bm) {
@@ -503,9 +503,9 @@ __device__ __forceinline__ void pf_int_build(const uint8_t *raw, const uint8_t *
             (uint32_t)((((uintptr_t)(mat ? W1 : W0)) & 3) + (uint64_t)rr * row_bytes + (uint64_t)b * BB) & 3u;
         return raw + (size_t)rg * RD * 4 + mis;
     };
-    // 64 rows x 32 chunks and 64 rows x 16 scalar items over NT threads
-    // (2048 / NT chunks and 1024 / NT items each)
-    constexpr int NC = 2048 / NT, NI = 1024 / NT;
+    // 64 rows x 32 chunks and 64 rows x 16 scalar items over 512 threads
+    // (4 chunks and 2 items each)
+    constexpr int NT = 512, NC = 2048 / NT, NI = 1024 / NT;
     uint4 v[NC];
 #pragma unroll
     for (int k = 0; k < NC; k++) {
@@ -529,16 +529,15 @@ __device__ __forceinline__ void pf_int_build(const uint8_t *raw, const uint8_t *
 
 // acc (rows m0.., columns n0.. of the tile) += this block's share. rsr, bmr:
 // the scalars of the lane's column n0 + (l & 15); s16: [32][16] sums of the
-// unit's x rows over this block. KS: 0 the whole block, 1 its columns 0 ..
-// 127 (with the Q2_K min term), 2 its columns 128 .. 255.
-template <int T, int KS = 0>
+// unit's x rows over this block.
+template <int T>
 __device__ __forceinline__ void pf_int_mma(pf_f32x4 &acc, const uint8_t *A, int m0, const uint8_t *B, int n0,
                                            const float *rsr, const __bf16 *bmr, const float *s16, bool xlo) {
     const int l = threadIdx.x & 63, r = l & 15, g = l >> 4;
     if constexpr (!PfInt<T>::per_sub) {
         pf_f32x4 bacc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int kk = KS == 2 ? 128 : 0; kk < (KS == 1 ? 128 : 256); kk += 32) {
+        for (int kk = 0; kk < 256; kk += 32) {
             const uint32_t oa = pf_swz(m0 + r, kk / 8 + g), ob = pf_swz(n0 + r, kk / 8 + g);
             const pf_bf16x8 a_h = *(const pf_bf16x8 *)(A + oa), a_l = *(const pf_bf16x8 *)(A + PF_TILE + oa);
             const pf_bf16x8 bq = *(const pf_bf16x8 *)(B + ob);
@@ -548,7 +547,7 @@ __device__ __forceinline__ void pf_int_mma(pf_f32x4 &acc, const uint8_t *A, int 
         const float d = rsr[0];
 #pragma unroll
         for (int i = 0; i < 4; i++) acc[i] = __builtin_fmaf(d, bacc[i], acc[i]);
-        if constexpr (PfInt<T>::min16 && KS != 2) {
+        if constexpr (PfInt<T>::min16) {
             // A[row r][k = 4 g + i] = S of token m0 + r, sub-block 4 g + i
             __bf16 sh[4], sl[4];
 #pragma unroll
@@ -564,7 +563,7 @@ __device__ __forceinline__ void pf_int_mma(pf_f32x4 &acc, const uint8_t *A, int 
         }
     } else {
 #pragma unroll
-        for (int j = KS == 2 ? 4 : 0; j < (KS == 1 ? 4 : 8); j++) {
+        for (int j = 0; j < 8; j++) {
             const int kk = 32 * j;
             const uint32_t oa = pf_swz(m0 + r, kk / 8 + g), ob = pf_swz(n0 + r, kk / 8 + g);
             const pf_bf16x8 a_h = *(const pf_bf16x8 *)(A + oa), a_l = *(const pf_bf16x8 *)(A + PF_TILE + oa);
@@ -673,13 +672,10 @@ __device__ __forceinline__ int pf_share(int n, int w, int nw) { return n > w ? (
 // GU: 8 waves, wave w computes the 16x16 tile (pairs 16 ((w >> 1) & 1),
 // rows 16 (w & 1)) of gate (w < 4) or up (w >= 4) over 32 rows of each;
 // the down kernel: rows 16 (w & 3) of the M tile w >> 2 over 64 rows.
-// NT = 1024 (GU only): 16 waves, wave w takes wave w & 7's tile over
-// columns 128 (w >> 3) .. + 127 of each block; the halves meet in LDS at the
-// end, gate = first + second, up = first + second.
 #define PF_I_RS (2 * PF_TILE)
 #define PF_I_BM (PF_I_RS + 64 * 16 * 4)
 #define PF_I_ST (PF_I_BM + 64 * 16 * 2)
-template <int T, bool GU, int NT = 512>
+template <int T, bool GU>
 __device__ __forceinline__ void pf_int_pipe(uint8_t *smem, const uint8_t *W0, const uint8_t *W1, uint64_t row_bytes,
                                             int64_t nb, int64_t rows, const __bf16 *ah, const __bf16 *al,
                                             const float *s16, const uint32_t *roff, const int32_t *pair, int nv,
@@ -688,11 +684,9 @@ __device__ __forceinline__ void pf_int_pipe(uint8_t *smem, const uint8_t *W0, co
     constexpr int RD = (Fmt<T>::bytes + 6) / 4;
     constexpr bool need_s = GU && (PfInt<T>::min16 || PfInt<T>::per_sub);
     constexpr int nper = GU ? 32 : 64;
-    static_assert(NT == 512 || (NT == 1024 && GU), "16 waves: gate/up only");
     const int w = threadIdx.x >> 6, l = threadIdx.x & 63, nw = (int)(blockDim.x >> 6);
-    const int wt = NT == 1024 ? (w & 7) : w, half = NT == 1024 ? (w >> 3) : 0;
-    const int m0 = GU ? 16 * ((wt >> 1) & 1) : 16 * (wt >> 2), n0 = GU ? 16 * (wt & 1) : 16 * (wt & 3);
-    const int up_w = GU ? (wt >> 2) : 0;
+    const int m0 = GU ? 16 * ((w >> 1) & 1) : 16 * (w >> 2), n0 = GU ? 16 * (w & 1) : 16 * (w & 3);
+    const int up_w = GU ? (w >> 2) : 0;
     uint8_t *B0 = smem, *B1 = smem + PF_TILE;
     float *rs = (float *)(smem + PF_I_RS);
     __bf16 *bm = (__bf16 *)(smem + PF_I_BM);
@@ -724,42 +718,20 @@ __device__ __forceinline__ void pf_int_pipe(uint8_t *smem, const uint8_t *W0, co
         __syncthreads();
         if (b + S - 1 < nb) issue(b + S - 1);
         uint8_t *st = stage(b);
-        pf_int_build<T, NT>(st + a_bytes, W0, GU ? W1 : nullptr, nper, row_bytes, rows, r0, b, B0, GU ? B1 : nullptr,
+        pf_int_build<T>(st + a_bytes, W0, GU ? W1 : nullptr, nper, row_bytes, rows, r0, b, B0, GU ? B1 : nullptr,
                             rs, bm);
         __syncthreads();
         const uint8_t *Bw = (GU && up_w) ? B1 : B0;
         const float *s16b = (const float *)(st + a_bytes + raw_bytes);
-        if constexpr (NT == 512) {
-            pf_int_mma<T>(acc, st, m0, Bw, n0, rs + 16 * rg, bm + 16 * rg, s16b, xlo);
-        } else if (half == 0) {
-            pf_int_mma<T, 1>(acc, st, m0, Bw, n0, rs + 16 * rg, bm + 16 * rg, s16b, xlo);
-        } else {
-            pf_int_mma<T, 2>(acc, st, m0, Bw, n0, rs + 16 * rg, bm + 16 * rg, s16b, xlo);
-        }
+        pf_int_mma<T>(acc, st, m0, Bw, n0, rs + 16 * rg, bm + 16 * rg, s16b, xlo);
     }
     if constexpr (GU) {
         __syncthreads();
-        pf_f32x4 u;
-        if constexpr (NT == 512) {
-            float *xch = (float *)(smem + PF_I_ST) + (w & 3) * 256 + l * 4;
-            if (up_w) *(pf_f32x4 *)xch = acc;
-            __syncthreads();
-            if (up_w) return;
-            u = *(const pf_f32x4 *)xch;
-        } else {
-            // waves 4 .. 15 hand their tiles to the gate waves 0 .. 3
-            float *xch = (float *)(smem + PF_I_ST) + l * 4;
-            if (w >= 4) *(pf_f32x4 *)(xch + w * 256) = acc;
-            __syncthreads();
-            if (w >= 4) return;
-            const pf_f32x4 g1 = *(const pf_f32x4 *)(xch + (w + 8) * 256);
-            const pf_f32x4 u0 = *(const pf_f32x4 *)(xch + (w + 4) * 256), u1 = *(const pf_f32x4 *)(xch + (w + 12) * 256);
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                acc[i] = acc[i] + g1[i];
-                u[i] = u0[i] + u1[i];
-            }
-        }
+        float *xch = (float *)(smem + PF_I_ST) + (w & 3) * 256 + l * 4;
+        if (up_w) *(pf_f32x4 *)xch = acc;
+        __syncthreads();
+        if (up_w) return;
+        const pf_f32x4 u = *(const pf_f32x4 *)xch;
         const int64_t row = r0 + n0 + (l & 15);
 #pragma unroll
         for (int i = 0; i < 4; i++) {
@@ -1198,38 +1170,6 @@ extern "C" __global__ __launch_bounds__(512) void sepia_pf_down_r(
 #define PF_DR(TT) case TT: pf_reg_down<TT>(smem, wd, D.row_bytes, D.n_blocks, H, hh, hl, roff, pair, nv, r0, yp); break;
         PF_DR(ST_Q2_K) PF_DR(ST_Q3_K) PF_DR(ST_Q4_K)
 #undef PF_DR
-    default: break;
-    }
-}
-
-// The integer formats' gate/up with 16 waves a workgroup (pf_int_pipe NT =
-// 1024): the same tiles and result layout as sepia_pf_gateup, each stage's
-// code build and DMA issue spread over twice the waves, and each block's
-// columns split between two waves per tile. The host launches it only when
-// every gate/up projection of the layer is Q2_K, Q3_K or Q4_K.
-extern "C" __global__ __launch_bounds__(1024) void sepia_pf_gateup_i(
-    PfProj gate, PfProj up, PfProj s_gate, PfProj s_up, int32_t n_routed, int32_t n_sel, int64_t I, int64_t H,
-    const __bf16 *__restrict__ xh, const __bf16 *__restrict__ xl, const float *__restrict__ s16,
-    const uint32_t *__restrict__ lo_any, const int32_t *__restrict__ list, const int32_t *__restrict__ units,
-    const int32_t *__restrict__ n_units, __bf16 *__restrict__ hh, __bf16 *__restrict__ hl) {
-    if ((int32_t)blockIdx.y >= n_units[0]) return;
-    extern __shared__ __attribute__((aligned(16))) uint8_t pf_smem[];
-    uint8_t *smem = pf_smem;
-    const int32_t *un = units + 3 * blockIdx.y;
-    const int32_t e = un[0], nv = un[2];
-    const bool routed = e < n_routed;
-    const PfProj &G = routed ? gate : s_gate, &U = routed ? up : s_up;
-    const int64_t ei = routed ? e : e - n_routed;
-    const uint8_t *wg = G.base + ei * G.stride, *wu = U.base + ei * U.stride;
-    const int64_t r0 = (int64_t)blockIdx.x * 32;
-    uint32_t *roff;
-    int32_t *pair;
-    pf_unit_rows(list + un[1], nv, true, n_sel, H, smem, roff, pair);
-    const bool xlo = __builtin_amdgcn_readfirstlane((int)*lo_any) != 0;
-    switch (G.type) {
-#define PF_GI(TT) case TT: pf_int_pipe<TT, true, 1024>(smem, wg, wu, G.row_bytes, G.n_blocks, I, xh, xl, s16, roff, pair, nv, r0, xlo, hh, hl, nullptr, 0); break;
-        PF_GI(ST_Q2_K) PF_GI(ST_Q3_K) PF_GI(ST_Q4_K)
-#undef PF_GI
     default: break;
     }
 }

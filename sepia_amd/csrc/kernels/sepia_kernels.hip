@@ -38,7 +38,7 @@ SEPIA_DEQUANT_KERNEL(iq2_xs, ST_IQ2_XS)
 SEPIA_DEQUANT_KERNEL(iq3_xxs, ST_IQ3_XXS)
 SEPIA_DEQUANT_KERNEL(iq4_xs, ST_IQ4_XS)
 
-// F16 rows: the integer conversion keeps NaN payloads (src/quants.c:77-96).
+// F16 rows: the integer conversion keeps NaN payloads (src/quants.c:58-77).
 extern "C" __global__ __launch_bounds__(256) void sepia_dequant_rows_f16(
     const uint8_t *__restrict__ raw, float *__restrict__ out, int64_t n) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -222,10 +222,6 @@ SEPIA_FFN_PAIR(4, 3, ST_Q4_K, ST_Q3_K)
 SEPIA_FFN_PAIR(4, 4, ST_Q4_K, ST_Q4_K)
 
 #include "mq.h"
-#include "mq_fused.h"
-#include "mq_flow.h"
-#include "mq_mix.h"
-#include "mq_rows.h"
 #include "moe.h"
 #include "prefill.h"
 #include "synth.h"
@@ -239,7 +235,3 @@ SEPIA_MQ_MV(iq2_xs, ST_IQ2_XS)
 SEPIA_MQ_MV(iq3_xxs, ST_IQ3_XXS)
 SEPIA_MQ_GATEUP()
 SEPIA_MQ_DOWN()
-SEPIA_MQ_FUSED()
-SEPIA_MQ_FLOW()
-SEPIA_MQ_MIX()
-SEPIA_MQ_ROWS()

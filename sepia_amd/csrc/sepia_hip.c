@@ -55,22 +55,10 @@ enum {
     /* matrix-core expert FFN: gate/up, down */
     K_MQ_GU = K_MQ_MV + 5,
     K_MQ_DN = K_MQ_GU + 1,
-    /* the whole MoE layer / expert FFN in one launch (kernels/mq_fused.h) */
-    K_MQ_MOE = K_MQ_DN + 1,
     /* batched prefill MoE layer (kernels/prefill.h) */
-    K_PF_ROUTE = K_MQ_MOE + 1, K_PF_SELECT, K_PF_GROUP, K_PF_GATEUP, K_PF_DOWN, K_PF_COMBINE, K_PF_SPLIT,
-    /* one expert's FFN in one launch, gate/up and down waves side by side (kernels/mq_flow.h) */
-    K_MQ_FFN,
-    /* MoE gate/up with the selection behind shared-expert streaming (kernels/mq_mix.h) */
-    K_MQ_GU_MIX,
-    /* MoE down with every slot of a row group in one workgroup (kernels/mq_rows.h) */
-    K_MQ_DN_ROWS,
-    /* prefill gate/up of the integer formats with 16 waves a workgroup (kernels/prefill.h) */
-    K_PF_GATEUP_I,
-    /* prefill gate/up of the integer formats with the codes in registers (kernels/prefill.h) */
-    K_PF_GATEUP_R,
-    /* prefill down of the integer formats with the codes in registers (kernels/prefill.h) */
-    K_PF_DOWN_R,
+    K_PF_ROUTE = K_MQ_DN + 1, K_PF_SELECT, K_PF_GROUP, K_PF_GATEUP, K_PF_DOWN, K_PF_COMBINE, K_PF_SPLIT,
+    /* prefill gate/up and down of the integer formats with the codes in registers (kernels/prefill.h) */
+    K_PF_GATEUP_R, K_PF_DOWN_R,
     /* prefill router logits on the f32 matrix cores (kernels/prefill.h) */
     K_PF_ROUTE_M,
     K_COUNT
@@ -93,14 +81,13 @@ static const char *const k_names[K_COUNT] = {
     FFN_NAMES("22"), FFN_NAMES("23"), FFN_NAMES("24"), FFN_NAMES("32"), FFN_NAMES("33"), FFN_NAMES("34"),
     FFN_NAMES("42"), FFN_NAMES("43"), FFN_NAMES("44"),
     "sepia_mq_mv_q2_k", "sepia_mq_mv_q3_k", "sepia_mq_mv_q4_k", "sepia_mq_mv_iq2_xs", "sepia_mq_mv_iq3_xxs",
-    "sepia_mq_gateup", "sepia_mq_down", "sepia_mq_moe",
+    "sepia_mq_gateup", "sepia_mq_down",
     "sepia_pf_route", "sepia_pf_select", "sepia_pf_group", "sepia_pf_gateup", "sepia_pf_down", "sepia_pf_combine",
-    "sepia_pf_split", "sepia_mq_ffn", "sepia_mq_gateup_mix", "sepia_mq_down_rows", "sepia_pf_gateup_i",
-    "sepia_pf_gateup_r", "sepia_pf_down_r", "sepia_pf_route_m",
+    "sepia_pf_split", "sepia_pf_gateup_r", "sepia_pf_down_r", "sepia_pf_route_m",
 };
 #undef FFN_NAMES
 
-/* GGUF block geometry (reference src/quants.c:46-51; tools/gguf_inspect.py:109-117). */
+/* GGUF block geometry (reference src/quants.c:28-56; tools/gguf_inspect.py:109-117). */
 typedef struct {
     int type;
     int64_t elems;
@@ -146,26 +133,13 @@ static int g_opt_mq = 1;     /* sepia_hip_set_option("mq", 0) disables the matri
 static int g_opt_mq_p = 0, g_opt_mq_c = 0, g_opt_mq_s = 0;
 static int g_opt_mq_x = 0;   /* "mq_x": 0 = planner's choice, 1 = vector from global, 2 = vector by LDS DMA,
                               * 3 = converter waves */
-static int g_opt_fuse = 0;   /* sepia_hip_set_option("fuse", 1) runs the MoE layer / expert FFN as one launch */
-static int g_opt_mix = 0;    /* "mix": 1 runs the MoE decode's gate/up as sepia_mq_gateup_mix (every workgroup
-                              * streams shared units while its wave 0 selects, then routed ones) */
-static int g_opt_dnrows = 0; /* "dnrows": 1 runs the MoE decode's down as sepia_mq_down_rows (all slots of
-                              * a row group in one workgroup, summed in LDS) */
-static int g_opt_hxq = 0;    /* "hxq": 1 = h crosses from gate/up to down in XQ form (measured slower: the XQ epilogue costs gate/up more than it saves down), 0 = f32 */
-static int g_opt_dyn = 0;    /* "dyn": 1 deals the MoE down launch's steps at run time (MqDyn) */
-static int g_opt_pf_gu = 2;   /* "pf_gu": the gate/up launch of a prefill layer whose gate/up projections are
-                               * all Q2_K, Q3_K or Q4_K: 2 = sepia_pf_gateup_r (codes in registers), 1 =
-                               * sepia_pf_gateup_i (16 waves), 0 = sepia_pf_gateup (other layers always) */
 static int g_opt_pf_route_m = 1;   /* "pf_route_m": 1 = prefill router logits on the f32 matrix cores
                                     * (sepia_pf_route_m) when x and the router rows are 16-byte aligned,
                                     * 0 = sepia_pf_route */
-static int g_opt_pf_dn = 1;   /* "pf_dn": 1 = a prefill layer whose down projections are all Q2_K, Q3_K or Q4_K
-                               * runs them as sepia_pf_down_r (codes in registers), 0 = sepia_pf_down */
-static int g_opt_route_sel = 0;   /* "route_sel": 1 = the router launch's last workgroup selects the
-                                   * experts even for the matrix-core FFN (0: its gate/up launch does) */
-static int g_opt_flow = 0;   /* "flow": 1 runs the expert FFN as one sepia_mq_ffn launch (gate/up and down waves) */
-static int g_opt_flow_delay = 250;   /* "flow_delay": s_memrealtime ticks (10 ns) a flow workgroup without
-                                      * gate/up units holds its down weights back */
+static int g_opt_pf_reg = 1;   /* "pf_reg": 1 = a prefill layer whose gate/up (down) projections are all Q2_K,
+                                * Q3_K or Q4_K runs them as sepia_pf_gateup_r (sepia_pf_down_r), the codes
+                                * decoded into registers; 0 = the LDS-tile kernels sepia_pf_gateup / _down,
+                                * which every other format always takes */
 static int g_opt_tile_t = 0; /* sepia_hip_set_option("tile_t", T) forces T steps per workgroup */
 
 /* Geometry for `mats` stacked copies of a [rows, 256 * n_blocks] matrix; 0
@@ -193,7 +167,6 @@ static size_t tile_lds(int64_t n_staged, const TileGeo *g, int mats) {
 static int g_available;
 static size_t g_lds_max = 65536;    /* per-workgroup LDS limit, from the device at init */
 static int g_cus = 0;               /* compute units, from the device at init */
-static int g_fused_pending = 0;     /* a fused launch ran in the open batch: check its error flag at end */
 static int g_have_iq2xxs;
 static char g_device_name[256];
 static hipModule_t g_module;
@@ -218,13 +191,24 @@ enum { BUF_SHARED = 0, BUF_PRIVATE = 1, BUF_WRAPPED = 2 };
 #define DEV_ALIGN 256u
 #define DEV_PAD 256u
 
+/* Shared buffers keep a pinned host copy beside the device allocation. The
+ * host may write the copy only through a pointer from sepia_gpu_host_ptr,
+ * so that call marks every chunk (SHADOW_CHUNK bytes) of the buffer
+ * host-dirty; an op uploads the dirty chunks of the byte range it reads
+ * right before it is queued and marks them clean, and a buffer a kernel
+ * writes is downloaded whole at sepia_gpu_end. A slab the host fills once is
+ * therefore uploaded once, however many batches read it, and a host write
+ * that lands after an earlier op of the batch read other chunks still
+ * reaches the op that reads it. */
+#define SHADOW_CHUNK ((size_t)1 << 20)
 struct SepiaGpuBuf {
     uint8_t *dev;
     void *host;        /* pinned copy (shared), caller's base (wrapped), NULL (private) */
     size_t len;
     int kind;
-    int exposed;       /* host_ptr handed out: the host may write it */
-    int host_newer;    /* upload before the next device access */
+    int host_dirty;    /* some chunk of the host copy is newer than the device copy */
+    uint64_t *dirty;   /* per-chunk host-dirty bits (shared buffers) */
+    size_t nchunks;
     int dev_newer;     /* download at sepia_gpu_end */
     struct SepiaGpuBuf *prev, *next; /* registry of shared buffers */
 };
@@ -262,20 +246,47 @@ static int chk(const SepiaGpuBuf *b, size_t off, size_t n, const char *op, const
     return 1;
 }
 
-/* Bring the device copy up to date before a kernel touches the buffer. */
-static int sync_in(SepiaGpuBuf *b, const char *op) {
-    if (b->kind == BUF_SHARED && b->host_newer) {
-        hipError_t e = hipMemcpyAsync(b->dev, b->host, b->len, hipMemcpyHostToDevice, g_stream);
-        if (e != hipSuccess) {
-            LOG("%s: upload failed: %s", op, hipGetErrorString(e));
+/* Bytes uploaded to shared buffers' device copies since init (tests read it
+ * through sepia_hip_uploaded_bytes). */
+static uint64_t g_uploaded;
+
+/* Bring [off, off + n) of the device copy up to date before a kernel reads
+ * it: upload its host-dirty chunks, coalesced into runs, and mark them clean. */
+static int sync_in_range(SepiaGpuBuf *b, size_t off, size_t n, const char *op) {
+    if (b->kind != BUF_SHARED || !b->host_dirty || n == 0) return 1;
+    if (off >= b->len) return 1;
+    if (n > b->len - off) n = b->len - off;
+    const size_t c0 = off / SHADOW_CHUNK, c1 = (off + n - 1) / SHADOW_CHUNK;
+    size_t c = c0;
+    while (c <= c1) {
+        if (!((b->dirty[c >> 6] >> (c & 63)) & 1u)) {
+            c++;
+            continue;
+        }
+        size_t e = c;
+        while (e + 1 <= c1 && ((b->dirty[(e + 1) >> 6] >> ((e + 1) & 63)) & 1u)) e++;
+        const size_t lo = c * SHADOW_CHUNK, hi = (e + 1) * SHADOW_CHUNK < b->len ? (e + 1) * SHADOW_CHUNK : b->len;
+        hipError_t err = hipMemcpyAsync(b->dev + lo, (uint8_t *)b->host + lo, hi - lo, hipMemcpyHostToDevice, g_stream);
+        if (err != hipSuccess) {
+            LOG("%s: upload failed: %s", op, hipGetErrorString(err));
             return 0;
         }
-        b->host_newer = 0;
+        g_uploaded += hi - lo;
+        for (size_t k = c; k <= e; k++) b->dirty[k >> 6] &= ~((uint64_t)1 << (k & 63));
+        c = e + 1;
     }
+    int any = 0;
+    for (size_t k = 0; k < (b->nchunks + 63) / 64 && !any; k++) any = b->dirty[k] != 0;
+    b->host_dirty = any;
     return 1;
 }
+static int sync_in(SepiaGpuBuf *b, const char *op) { return sync_in_range(b, 0, b->len, op); }
 
+/* An input read over [off, off + n) (the whole buffer with prep_in). */
+static int prep_in_r(SepiaGpuBuf *b, size_t off, size_t n, const char *op) { return sync_in_range(b, off, n, op); }
 static int prep_in(SepiaGpuBuf *b, const char *op) { return sync_in(b, op); }
+/* An output: the whole device copy is made current first, since the buffer
+ * is downloaded whole at sepia_gpu_end. */
 static int prep_out(SepiaGpuBuf *b, const char *op) {
     if (!sync_in(b, op)) return 0;
     if (b->kind == BUF_SHARED) b->dev_newer = 1;
@@ -286,19 +297,24 @@ static int prep_out(SepiaGpuBuf *b, const char *op) {
  * kernel that uses one leaves it at zero again) followed by a data region
  * for partial sums and intermediate vectors, grown on demand. */
 #define CNT_BYTES (64u * 1024u)
-#define MQ_BAR_WORD 1               /* fused launches' grid-barrier counter (never reset) */
-#define MQ_ERR_WORD 2               /* fused and flow launches' time-out flag */
-#define MQ_FLOW_HCNT_WORD 3         /* flow launches: units of h published (back to zero at the end) */
-#define MQ_FLOW_FLAG_OFF 8192       /* flow launches: workgroup b's h flag at word OFF + 32 b (lowered again) */
-#define MQ_FLOW_FLAG_WORDS (32 * 256)
 static void *g_scratch;
 static size_t g_scratch_len;
 
 /* Data region of at least `need` bytes (the counters sit in front of it).
  * Growing waits for the stream, since queued kernels may still use the old
- * region; the new allocation is cleared so every counter starts at zero. */
+ * region; the new allocation is cleared so every counter starts at zero.
+ * None of that may enter a stream capture: while the library's stream is
+ * being captured a region that is too small is an error (run the same call
+ * once before the capture, or reserve with sepia_hip_reserve_scratch). */
 static void *scratch(size_t need, const char *op) {
     if (g_scratch && need <= g_scratch_len - CNT_BYTES) return (uint8_t *)g_scratch + CNT_BYTES;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(g_stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) {
+        LOG("%s: needs %zu bytes of scratch but has %zu, and the stream is being captured (growing it would "
+            "allocate); run the call once before the capture or call sepia_hip_reserve_scratch",
+            op, need, g_scratch ? g_scratch_len - CNT_BYTES : (size_t)0);
+        return NULL;
+    }
     hipStreamSynchronize(g_stream);
     if (g_scratch) hipFree(g_scratch);
     g_scratch = NULL;
@@ -315,6 +331,11 @@ static void *scratch(size_t need, const char *op) {
     }
     g_scratch_len = want;
     return (uint8_t *)g_scratch + CNT_BYTES;
+}
+
+int sepia_hip_reserve_scratch(size_t bytes) {
+    if (!need_init("reserve_scratch")) return 0;
+    return scratch(bytes, "reserve_scratch") != NULL;
 }
 
 static SepiaGpuBuf *new_buf(size_t len, int kind) {
@@ -359,6 +380,15 @@ SepiaGpuBuf *sepia_gpu_alloc(size_t len, int gpu_private) {
             return NULL;
         }
         memset(b->host, 0, len);
+        b->nchunks = (len + SHADOW_CHUNK - 1) / SHADOW_CHUNK;
+        b->dirty = (uint64_t *)calloc((b->nchunks + 63) / 64, sizeof(uint64_t));
+        if (!b->dirty) {
+            LOG("alloc: out of host memory");
+            hipHostFree(b->host);
+            hipFree(b->dev);
+            free(b);
+            return NULL;
+        }
         b->next = g_shared;
         if (g_shared) g_shared->prev = b;
         g_shared = b;
@@ -400,6 +430,7 @@ void sepia_gpu_free(SepiaGpuBuf *b) {
         else g_shared = b->next;
         if (b->next) b->next->prev = b->prev;
         if (b->host) hipHostFree(b->host);
+        free(b->dirty);
     }
     if (b->dev) hipFree(b->dev);
     free(b);
@@ -409,13 +440,17 @@ void *sepia_gpu_host_ptr(SepiaGpuBuf *b) {
     if (!b) return NULL;
     if (b->kind == BUF_PRIVATE) return NULL;
     if (b->kind == BUF_SHARED) {
-        b->exposed = 1;
-        b->host_newer = 1;
+        /* the caller may write anywhere in the copy from now on */
+        memset(b->dirty, 0xFF, ((b->nchunks + 63) / 64) * sizeof(uint64_t));
+        if (b->nchunks % 64) b->dirty[b->nchunks / 64] = ((uint64_t)1 << (b->nchunks % 64)) - 1;
+        b->host_dirty = 1;
     }
     return b->host;
 }
 
 uint64_t sepia_gpu_gpu_addr(SepiaGpuBuf *b) { return b ? (uint64_t)(uintptr_t)b->dev : 0; }
+
+uint64_t sepia_hip_uploaded_bytes(void) { return g_uploaded; }
 
 /* ------------------------------------------------------------ lifecycle - */
 int sepia_gpu_available(void) { return g_available; }
@@ -549,33 +584,9 @@ int sepia_gpu_end(void) {
     }
     hipError_t s = hipStreamSynchronize(g_stream);
     if (e == hipSuccess) e = s;
-    for (SepiaGpuBuf *b = g_shared; b; b = b->next)
-        if (b->exposed) b->host_newer = 1;
     if (e != hipSuccess) {
         LOG("end: batch failed: %s", hipGetErrorString(e));
         return 0;
-    }
-    if (g_fused_pending) {
-        /* a fused launch whose grid barrier timed out leaves its flag (word
-         * MQ_ERR_WORD of the counter region) set; its results are invalid */
-        g_fused_pending = 0;
-        uint32_t flag = 0;
-        e = hipMemcpy(&flag, (uint32_t *)g_scratch + MQ_ERR_WORD, 4, hipMemcpyDeviceToHost);
-        if (e == hipSuccess && flag) {
-            /* clear the flag, realign the barrier counter (a workgroup that
-             * gave up left it between multiples of the grid size) and zero
-             * the flow counters */
-            const uint32_t zero[3] = { 0, 0, 0 };
-            hipMemcpy((uint32_t *)g_scratch + MQ_BAR_WORD, zero, 12, hipMemcpyHostToDevice);
-            hipMemset((uint32_t *)g_scratch + MQ_FLOW_FLAG_OFF, 0, MQ_FLOW_FLAG_WORDS * 4);
-            hipDeviceSynchronize();
-            LOG("end: a one-launch FFN timed out waiting (flag %u); the batch's results are invalid", flag);
-            return 0;
-        }
-        if (e != hipSuccess) {
-            LOG("end: reading the fused-launch flag failed: %s", hipGetErrorString(e));
-            return 0;
-        }
     }
     return 1;
 }
@@ -716,7 +727,9 @@ static int do_matvec_f32(const char *op, SepiaGpuBuf *w, size_t w_off, SepiaGpuB
         !chk(w, w_off, (size_t)out_dim * (size_t)in_dim * 4, op, "w") ||
         !chk(x, 0, (size_t)in_dim * 4, op, "x") || !chk(y, 0, (size_t)out_dim * 4, op, "y"))
         return 0;
-    if (!need_batch(op) || !prep_in(w, op) || !prep_in(x, op) || !prep_out(y, op)) return 0;
+    if (!need_batch(op) || !prep_in_r(w, w_off, (size_t)out_dim * (size_t)in_dim * 4, op) || !prep_in(x, op) ||
+        !prep_out(y, op))
+        return 0;
     const float *wp = (const float *)(w->dev + w_off);
     int64_t ld = in_dim;
     void *args[] = { &wp, &ld, &x->dev, &y->dev, &out_dim, &in_dim };
@@ -741,7 +754,7 @@ static int do_rmsnorm(const char *op, SepiaGpuBuf *w, size_t w_off, SepiaGpuBuf 
     if (!f32_off_ok(w_off, op, "w") || !chk(w, w_off, (size_t)n * 4, op, "w") ||
         !chk(x, 0, (size_t)rows * (size_t)n * 4, op, "x") || !chk(y, 0, (size_t)rows * (size_t)n * 4, op, "y"))
         return 0;
-    if (!need_batch(op) || !prep_in(w, op) || !prep_in(x, op) || !prep_out(y, op)) return 0;
+    if (!need_batch(op) || !prep_in_r(w, w_off, (size_t)n * 4, op) || !prep_in(x, op) || !prep_out(y, op)) return 0;
     const float *wp = (const float *)(w->dev + w_off);
     void *args[] = { &wp, &x->dev, &y->dev, &n, &eps };
     return launch(K_RMSNORM, (unsigned)rows, 256, args, op);
@@ -845,7 +858,8 @@ static int do_sconv(const char *op, SepiaGpuBuf *w, size_t w_off, SepiaGpuBuf *h
         !chk(hist, 0, cs * (size_t)(K - 1), op, "hist") || !chk(in, 0, cs * (size_t)T, op, "in") ||
         !chk(out, 0, cs * (size_t)T, op, "out"))
         return 0;
-    if (!need_batch(op) || !prep_in(w, op) || !prep_in(hist, op) || !prep_in(in, op) || !prep_out(out, op))
+    if (!need_batch(op) || !prep_in_r(w, w_off, cs * (size_t)K, op) || !prep_in(hist, op) || !prep_in(in, op) ||
+        !prep_out(out, op))
         return 0;
     const float *wp = (const float *)(w->dev + w_off);
     int32_t c = (int32_t)C, k = (int32_t)K, t = (int32_t)T;
@@ -951,48 +965,12 @@ int sepia_hip_set_option(const char *name, int value) {
         g_opt_mq_x = value;
         return 1;
     }
-    if (strcmp(name, "fuse") == 0 && (value == 0 || value == 1)) {
-        g_opt_fuse = value;
-        return 1;
-    }
-    if (strcmp(name, "mix") == 0 && (value == 0 || value == 1)) {
-        g_opt_mix = value;
-        return 1;
-    }
-    if (strcmp(name, "dnrows") == 0 && (value == 0 || value == 1)) {
-        g_opt_dnrows = value;
-        return 1;
-    }
-    if (strcmp(name, "hxq") == 0 && (value == 0 || value == 1)) {
-        g_opt_hxq = value;
-        return 1;
-    }
-    if (strcmp(name, "dyn") == 0 && (value == 0 || value == 1)) {
-        g_opt_dyn = value;
-        return 1;
-    }
-    if (strcmp(name, "pf_gu") == 0 && value >= 0 && value <= 2) {
-        g_opt_pf_gu = value;
+    if (strcmp(name, "pf_reg") == 0 && (value == 0 || value == 1)) {
+        g_opt_pf_reg = value;
         return 1;
     }
     if (strcmp(name, "pf_route_m") == 0 && (value == 0 || value == 1)) {
         g_opt_pf_route_m = value;
-        return 1;
-    }
-    if (strcmp(name, "pf_dn") == 0 && (value == 0 || value == 1)) {
-        g_opt_pf_dn = value;
-        return 1;
-    }
-    if (strcmp(name, "route_sel") == 0 && (value == 0 || value == 1)) {
-        g_opt_route_sel = value;
-        return 1;
-    }
-    if (strcmp(name, "flow") == 0 && (value == 0 || value == 1)) {
-        g_opt_flow = value;
-        return 1;
-    }
-    if (strcmp(name, "flow_delay") == 0 && value >= 0 && value <= 100000) {
-        g_opt_flow_delay = value;
         return 1;
     }
     if (strcmp(name, "mq_p") == 0 && value >= 0 && value <= 16) {
@@ -1026,7 +1004,7 @@ int sepia_hip_set_option(const char *name, int value) {
 #define MQ_CUS 256                  /* MI355X compute units */
 #define MQ_ZERO 768
 typedef struct {
-    int32_t P, ring, xraw, orings, conv, dyn, xq_in;   /* as struct MqGeo in kernels/mq.h */
+    int32_t P, ring, xraw, orings, conv;   /* as struct MqGeo in kernels/mq.h */
 } MqGeo;
 /* In-kernel selection by the gate/up launch (struct MqRoute in
  * kernels/mq.h); logits NULL: the experts come from sel_idx. */
@@ -1127,49 +1105,10 @@ static int mq_geo(int mc, int wmax, int64_t n_items, int64_t nq, size_t fixed, s
                     geo->xraw = mode ? (int32_t)o_raw : 0;
                     geo->orings = (int32_t)base;
                     geo->conv = cv;
-                    geo->dyn = 0;
-                    geo->xq_in = 0;
                     *threads = 64u * (unsigned)(nw + cv);
                     *lds = base + (size_t)nw * ring;
                 }
             }
-        }
-    }
-    return found;
-}
-
-/* mq_geo for a launch whose steps are dealt at run time (MqDyn): every
- * quad of an item has its partial (P = nq), the vector comes by LDS DMA
- * into a raw copy, and the waves and ring stages give the most steps in
- * flight (then the most waves). */
-static int mq_geo_dyn(int mc, int wmax, int64_t n_items, int64_t nq, size_t fixed, size_t raw_bytes, unsigned *threads,
-                      MqGeo *geo, size_t *lds) {
-    if (raw_bytes == 0 || nq > 16) return 0;
-    const size_t w1 = (size_t)k_mq_words[mc] * 1024, wm = (size_t)wmax * 1024;
-    const size_t o_raw = align256(fixed + (size_t)n_items * nq * 64);
-    const size_t base = align256(o_raw + raw_bytes);
-    int64_t best = -1;
-    int found = 0;
-    for (int nw = 16; nw >= 1; nw--) {
-        if (base + (size_t)nw * wm > g_lds_max) continue;
-        size_t ring = ((g_lds_max - base) / (size_t)nw) & ~(size_t)1023;
-        if (ring > 4 * wm) ring = 4 * wm;
-        int64_t S = (int64_t)(ring / w1);
-        if (S > 4) S = 4;
-        int64_t fl = (int64_t)nw * S;
-        if (fl > n_items * nq) fl = n_items * nq;
-        if (fl > best) {
-            best = fl;
-            found = 1;
-            geo->P = (int32_t)nq;
-            geo->ring = (int32_t)ring;
-            geo->xraw = (int32_t)o_raw;
-            geo->orings = (int32_t)base;
-            geo->conv = 0;
-            geo->dyn = 1;
-            geo->xq_in = 0;
-            *threads = 64u * (unsigned)nw;
-            *lds = base + (size_t)nw * ring;
         }
     }
     return found;
@@ -1223,7 +1162,9 @@ int sepia_gpu_matvec_q(int ggml_type, SepiaGpuBuf *w, size_t w_off, SepiaGpuBuf 
     if (!chk(w, w_off, (size_t)out_dim * row_bytes, op, "w") || !chk(x, 0, (size_t)in_dim * 4, op, "x") ||
         !chk(y, 0, (size_t)out_dim * 4, op, "y"))
         return 0;
-    if (!need_batch(op) || !prep_in(w, op) || !prep_in(x, op) || !prep_out(y, op)) return 0;
+    if (!need_batch(op) || !prep_in_r(w, w_off, (size_t)out_dim * row_bytes, op) || !prep_in(x, op) ||
+        !prep_out(y, op))
+        return 0;
     const uint8_t *wp = w->dev + w_off;
     unsigned mq_threads, mq_grid;
     size_t mq_lds;
@@ -1268,7 +1209,7 @@ int sepia_gpu_dequant_rows(int ggml_type, SepiaGpuBuf *raw, size_t raw_off, Sepi
         return 0;
     }
     if (!chk(raw, raw_off, (size_t)nb * ti->bytes, op, "raw") || !chk(out, 0, (size_t)n * 4, op, "out")) return 0;
-    if (!need_batch(op) || !prep_in(raw, op) || !prep_out(out, op)) return 0;
+    if (!need_batch(op) || !prep_in_r(raw, raw_off, (size_t)nb * ti->bytes, op) || !prep_out(out, op)) return 0;
     const uint8_t *rp = raw->dev + raw_off;
     void *args[] = { &rp, &out->dev, &threads };
     return launch(ti->k_dq, blocks_for(threads, 256), 256, args, op);
@@ -1368,6 +1309,28 @@ static int moe_proj(const char *op, const char *what, const SepiaExpertTensor *t
     return 1;
 }
 
+/* Uploads what a layer's launches may read of its shared buffers: the router
+ * rows and bias, x, and the spans of every expert stack (the selection
+ * happens on the device, so any expert may be read). */
+static int prep_layer(const SepiaMoeLayerDesc *L, const MoeProj *g, const MoeProj *u, const MoeProj *d,
+                      const MoeProj *sg, const MoeProj *su, const MoeProj *sd, SepiaGpuBuf *x, size_t x_bytes,
+                      const char *op) {
+    const int64_t n_tot = L->n_routed + L->n_shared;
+    if (!prep_in_r(L->router_w, L->router_w_off, (size_t)n_tot * (size_t)L->hidden * 4, op) ||
+        !prep_in_r(L->router_bias, L->router_bias_off, (size_t)L->n_routed * 4, op) ||
+        !prep_in_r(x, 0, x_bytes, op))
+        return 0;
+    const SepiaExpertTensor *ts[6] = { &L->gate, &L->up, &L->down, &L->s_gate, &L->s_up, &L->s_down };
+    const MoeProj *ps[6] = { g, u, d, sg, su, sd };
+    const int64_t rows[6] = { L->inter, L->inter, L->hidden, L->inter, L->inter, L->hidden };
+    for (int i = 0; i < (L->n_shared > 0 ? 6 : 3); i++) {
+        const int ne = i < 3 ? L->n_routed : L->n_shared;
+        const size_t span = (size_t)(ne - 1) * ts[i]->stride + (size_t)rows[i] * ps[i]->row_bytes;
+        if (!prep_in_r(ts[i]->buf, ts[i]->off, span, op)) return 0;
+    }
+    return 1;
+}
+
 /* Mirrors struct XpArgs in kernels/mv.h: x in digit-plane form. */
 typedef struct {
     const int8_t *planes;
@@ -1405,7 +1368,6 @@ typedef struct {
     int32_t gu_wps_r, gu_wps_s, dn_wps_r, dn_wps_s;
     size_t gu_lds, dn_lds;
     MqGeo gu_geo, dn_geo;
-    int32_t gu_hxq;                 /* gate/up writes h in XQ form, the down launch takes it so */
 } MqFfnPlan;
 #define MQ_DN_CNT_OFF 64            /* first down arrival counter (u32 index in the counter region) */
 static int mq_proj_ok(const MoeProj *p, int64_t rows) {
@@ -1444,7 +1406,7 @@ static int mq_ffn_plan(const MoeProj *g, const MoeProj *u, const MoeProj *d, con
         if (!mq_proj_ok(ps[i], rows[i])) return 0;
     if (g->type != u->type || (n_shared > 0 && sg->type != su->type)) return 0;
     const int64_t tiles_i = (I + 15) / 16, tiles_h = (H + 15) / 16;
-    if (n_shared + topk > 1 && MQ_DN_CNT_OFF + tiles_h > MQ_FLOW_FLAG_OFF) return 0;
+    if (n_shared + topk > 1 && MQ_DN_CNT_OFF + tiles_h > CNT_BYTES / 4) return 0;
     /* both slot kinds share a geometry: planned for the format of the
      * routed slots (the shared ones when there are none), with rings that
      * hold a step of either */
@@ -1463,18 +1425,8 @@ static int mq_ffn_plan(const MoeProj *g, const MoeProj *u, const MoeProj *d, con
                 &pl->gu_threads, &pl->gu_geo, &pl->gu_lds))
         return 0;
     const size_t dn_fixed = MQ_ZERO + mq_xq_bytes(I) + (size_t)nk_dn * 4 + 256;
-    /* h crosses in XQ form (the down launch only DMAs it into place) unless
-     * an experimental launch that reads f32 h is switched on */
-    pl->gu_hxq = g_opt_hxq && !(g_opt_mix || g_opt_dnrows || g_opt_dyn);
-    if (pl->gu_hxq) {
-        if (!mq_geo(kd, wdn, nk_dn, I / 1024, dn_fixed, 0, 0, &pl->dn_threads, &pl->dn_geo, &pl->dn_lds)) return 0;
-        pl->dn_geo.xq_in = 1;
-    } else if (!(g_opt_dyn && !g_opt_mq_x && mq_geo_dyn(kd, wdn, nk_dn, I / 1024, dn_fixed, (size_t)I * 4,
-                                                         &pl->dn_threads, &pl->dn_geo, &pl->dn_lds)) &&
-               !mq_geo(kd, wdn, nk_dn, I / 1024, dn_fixed, (size_t)I * 4, 0, &pl->dn_threads, &pl->dn_geo,
-                       &pl->dn_lds)) {
+    if (!mq_geo(kd, wdn, nk_dn, I / 1024, dn_fixed, (size_t)I * 4, 0, &pl->dn_threads, &pl->dn_geo, &pl->dn_lds))
         return 0;
-    }
     pl->gu_grid = (unsigned)(topk * pl->gu_wps_r + n_shared * pl->gu_wps_s);
     pl->dn_grid = (unsigned)(topk * pl->dn_wps_r + n_shared * pl->dn_wps_s);
     return 1;
@@ -1574,10 +1526,7 @@ int sepia_gpu_moe_prefill(const SepiaMoeLayerDesc *L, int64_t n_tokens, SepiaGpu
     int32_t *sel_idx = (int32_t *)(s + o_idx), *list = (int32_t *)(s + o_list), *units = (int32_t *)(s + o_units),
             *n_units = (int32_t *)(s + o_nu);
 
-    SepiaGpuBuf *ins[] = { L->router_w, L->router_bias, x, L->gate.buf, L->up.buf, L->down.buf, L->s_gate.buf,
-                           L->s_up.buf, L->s_down.buf };
-    for (size_t i = 0; i < sizeof ins / sizeof ins[0]; i++)
-        if (ins[i] && !prep_in(ins[i], op)) return 0;
+    if (!prep_layer(L, &g, &u, &d, &sg, &su, &sd, x, (size_t)T * H * 4, op)) return 0;
     if (!prep_out(y, op) || (route_out && !prep_out(route_out, op))) return 0;
 
     const float *rw = (const float *)(L->router_w->dev + L->router_w_off);
@@ -1599,14 +1548,13 @@ int sepia_gpu_moe_prefill(const SepiaMoeLayerDesc *L, int64_t n_tokens, SepiaGpu
     if (!launch(K_PF_SPLIT, (unsigned)((nseg + 255) / 256), 256, a_sp, op)) return 0;
     void *a_gu[] = { (void *)&g, (void *)&u, (void *)&sg, (void *)&su, &nr32, &nsel32, &inter, &hid, &xh, &xl, &s16,
                      &lo_any, &list, &units, &n_units, &hh, &hl };
-    const int gu_mode = pf_type_int(g.type) && (ns == 0 || pf_type_int(sg.type)) ? g_opt_pf_gu : 0;
-    const int gu_k = gu_mode == 2 ? K_PF_GATEUP_R : gu_mode == 1 ? K_PF_GATEUP_I : K_PF_GATEUP;
-    const int64_t gu_rows = gu_mode == 2 ? 64 : 32;
-    if (!launch2(gu_k, (unsigned)((I + gu_rows - 1) / gu_rows), (unsigned)umax, gu_mode == 1 ? 1024 : 512,
+    const int gu_r = g_opt_pf_reg && pf_type_int(g.type) && (ns == 0 || pf_type_int(sg.type));
+    const int64_t gu_rows = gu_r ? 64 : 32;
+    if (!launch2(gu_r ? K_PF_GATEUP_R : K_PF_GATEUP, (unsigned)((I + gu_rows - 1) / gu_rows), (unsigned)umax, 512,
                  PF_LDS_BYTES, a_gu, op))
         return 0;
     void *a_dn[] = { (void *)&d, (void *)&sd, &nr32, &inter, &hid, &hh, &hl, &list, &units, &n_units, &yp };
-    const int dn_r = g_opt_pf_dn && pf_type_int(d.type) && (ns == 0 || pf_type_int(sd.type));
+    const int dn_r = g_opt_pf_reg && pf_type_int(d.type) && (ns == 0 || pf_type_int(sd.type));
     if (!launch2(dn_r ? K_PF_DOWN_R : K_PF_DOWN, (unsigned)(dn_r ? (H + 127) / 128 : (H + 63) / 64), (unsigned)umax,
                  512, PF_LDS_BYTES, a_dn, op))
         return 0;
@@ -1622,490 +1570,6 @@ int sepia_gpu_moe_prefill(const SepiaMoeLayerDesc *L, int64_t n_tokens, SepiaGpu
             return 0;
         }
     }
-    return 1;
-}
-
-/* The fused MoE layer / expert FFN (kernels/mq_fused.h): exactly MQ_CUS
- * workgroups, one per CU (the LDS it asks for admits no second), launched
- * only when the device has that many CUs and the occupancy query confirms
- * that every workgroup is resident at once -- its grid barriers rely on it.
- * Gate/up runs on waves 1.. (wave 0 is the control wave), down on every
- * wave; both phases share the workgroup size and the rings (ring bytes per
- * wave: what the LDS leaves after the phases' tables). */
-typedef struct {
-    MqGeo gu, dn;
-    int32_t dn_wps_r, dn_wps_s;
-    uint32_t o_sel, o_gred, o_xqh, o_dred, o_flag, o_rings;
-} MqFuseGeo;
-typedef struct {
-    const float *rw;
-    int64_t ld;
-    const float *bias;
-    const float *x;
-    int32_t n_routed, n_shared, topk, fixed;
-    float route_scale, global_scale;
-    int64_t inter, hidden;
-    float *logits;
-    int32_t *sel_idx;
-    float *sel_w;
-    uint8_t *xq_h;
-    float *ypart;
-    uint32_t *cnt, *bar, *err;
-    float *y;
-} MqFuseIo;
-typedef struct {
-    MqFuseGeo geo;
-    unsigned threads;
-    size_t lds;
-} MqFusePlan;
-#define MQ_FSEL_BYTES 1024          /* the fused kernel's selection area: idx[64], w[64], flag */
-
-/* Gate/up units of workgroup b of G (mirror of mq_gu_range in
- * kernels/mq_fused.h): the units whose first weight byte lies in
- * [b T / G, (b + 1) T / G), us shared units of ws bytes first, then ur
- * routed ones of wr bytes. */
-static int64_t cdiv_pos(int64_t a, int64_t d) { return a <= 0 ? 0 : (a + d - 1) / d; }
-static void mq_gu_range(int64_t us, int64_t ws, int64_t ur, int64_t wr, int64_t G, int64_t b, int64_t *ns,
-                        int64_t *nr) {
-    const int64_t S = us * ws, T = S + ur * wr;
-    const int64_t lo = T * b / G, hi = T * (b + 1) / G;
-    int64_t a0 = 0, a1 = 0;
-    if (us > 0) {
-        a0 = cdiv_pos(lo, ws);
-        a1 = cdiv_pos(hi, ws);
-        if (a0 > us) a0 = us;
-        if (a1 > us) a1 = us;
-    }
-    int64_t b0 = cdiv_pos(lo - S, wr), b1 = cdiv_pos(hi - S, wr);
-    if (b0 > ur) b0 = ur;
-    if (b1 > ur) b1 = ur;
-    *ns = a1 - a0;
-    *nr = b1 - b0;
-}
-
-/* Steps of one phase for the busiest wave: n_items items of nq quads on nw
- * waves of P parts, 10 per step when the ring holds two or more steps. */
-static int64_t mq_phase_cost(int mc, int64_t n_items, int64_t nq, int P, int nw, size_t ring) {
-    const int C = nw / P;
-    const int64_t spw = ((n_items + C - 1) / C) * ((nq + P - 1) / P);
-    int64_t S = (int64_t)(ring / ((size_t)k_mq_words[mc] * 1024));
-    if (S > 4) S = 4;
-    if (S > spw) S = spw;
-    return spw * ((S >= 2 || spw == 1) ? 10 : 16);
-}
-
-static int mq_fuse_plan(const MoeProj *g, const MoeProj *u, const MoeProj *d, const MoeProj *sg, const MoeProj *su,
-                        const MoeProj *sd, int32_t topk, int32_t n_shared, int64_t H, int64_t I, int router,
-                        MqFusePlan *fp) {
-    static int told = 0;   /* a device or layer the fused launch cannot take: said once */
-    MqFfnPlan pl;
-    if (!g_opt_fuse || topk < 1 || !mq_ffn_plan(g, u, d, sg, su, sd, topk, n_shared, H, I, &pl)) return 0;
-    if (g_cus < MQ_CUS) {
-        if (!told++) LOG("fused MoE launch off: %d compute units (it needs %d)", g_cus, MQ_CUS);
-        return 0;
-    }
-    if ((int64_t)topk * pl.dn_wps_r + (int64_t)n_shared * pl.dn_wps_s > MQ_CUS) return 0;
-    const int kg = mq_code(g->type), kd = mq_code(d->type);
-    int wg = k_mq_words[kg], wd = k_mq_words[kd];
-    if (n_shared > 0 && k_mq_words[mq_code(sg->type)] > wg) wg = k_mq_words[mq_code(sg->type)];
-    if (n_shared > 0 && k_mq_words[mq_code(sd->type)] > wd) wd = k_mq_words[mq_code(sd->type)];
-    const int wmax = wg > wd ? wg : wd;
-    const int64_t tiles_i = (I + 15) / 16, tiles_h = (H + 15) / 16;
-    /* the most gate/up units any workgroup gets */
-    int64_t nu_max = 0;
-    for (int64_t b = 0; b < MQ_CUS; b++) {
-        int64_t ns, nr;
-        mq_gu_range(n_shared * tiles_i, 32 * (int64_t)(n_shared > 0 ? sg->row_bytes : 0), topk * tiles_i,
-                    32 * (int64_t)g->row_bytes, MQ_CUS, b, &ns, &nr);
-        if (ns + nr > nu_max) nu_max = ns + nr;
-    }
-    if (nu_max < 1) nu_max = 1;
-    const int32_t dmin = (pl.dn_wps_r < pl.dn_wps_s || n_shared == 0) ? pl.dn_wps_r : pl.dn_wps_s;
-    const int64_t dnk = (tiles_h + dmin - 1) / dmin;
-    const int64_t nqg = H / 1024, nqd = I / 1024;
-    int64_t best = -1;
-    /* gate/up runs on the waves after the control wave (all of them without
-     * a router), down on every wave; waves past the last full column of P
-     * parts idle in that phase */
-    for (int nw = 2; nw <= 16; nw++)
-        for (int Pg = 1; Pg <= nw - router && Pg <= nqg; Pg++) {
-            for (int Pd = 1; Pd <= nw && Pd <= nqd; Pd++) {
-                size_t o = MQ_ZERO + mq_xq_bytes(H);
-                const size_t o_sel = o;
-                o += MQ_FSEL_BYTES;
-                const size_t o_gred = o;
-                o += (size_t)2 * nu_max * Pg * 64;
-                const size_t o_xqh = align256(o);
-                o = o_xqh + mq_xq_bytes(I);
-                const size_t o_dred = o;
-                o += (size_t)dnk * Pd * 64;
-                const size_t o_flag = o;
-                o += (size_t)dnk * 4;
-                const size_t o_rings = align256(o);
-                if (o_rings + (size_t)nw * wmax * 1024 > g_lds_max) continue;
-                size_t ring = ((g_lds_max - o_rings) / (size_t)nw) & ~(size_t)1023;
-                if (ring > (size_t)4 * wmax * 1024) ring = (size_t)4 * wmax * 1024;
-                const int64_t cost = mq_phase_cost(kg, 2 * nu_max, nqg, Pg, nw - router, ring) +
-                                     mq_phase_cost(kd, dnk, nqd, Pd, nw, ring);
-                if (best < 0 || cost < best) {
-                    best = cost;
-                    MqFuseGeo *G = &fp->geo;
-                    memset(G, 0, sizeof *G);
-                    G->gu.P = Pg;
-                    G->dn.P = Pd;
-                    G->gu.ring = G->dn.ring = (int32_t)ring;
-                    G->dn_wps_r = pl.dn_wps_r;
-                    G->dn_wps_s = pl.dn_wps_s;
-                    G->o_sel = (uint32_t)o_sel;
-                    G->o_gred = (uint32_t)o_gred;
-                    G->o_xqh = (uint32_t)o_xqh;
-                    G->o_dred = (uint32_t)o_dred;
-                    G->o_flag = (uint32_t)o_flag;
-                    G->o_rings = (uint32_t)o_rings;
-                    fp->threads = 64u * (unsigned)nw;
-                    fp->lds = o_rings + (size_t)nw * ring;
-                }
-            }
-        }
-    if (best < 0) {
-        if (!told++) LOG("fused MoE launch off: no geometry fits %zu bytes of LDS", g_lds_max);
-        return 0;
-    }
-    /* every workgroup resident at once: at most one per CU by LDS, and the
-     * device has MQ_CUS of them */
-    int nb = 0;
-    const hipError_t e = hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&nb, g_fn[K_MQ_MOE], (int)fp->threads,
-                                                                             fp->lds);
-    if (e != hipSuccess || nb < 1 || (int64_t)nb * g_cus < MQ_CUS) {
-        if (!told++)
-            LOG("fused MoE launch off: occupancy query %s, %d workgroups of %u threads and %zu bytes LDS per CU",
-                hipGetErrorString(e), nb, fp->threads, fp->lds);
-        return 0;
-    }
-    return 1;
-}
-
-/* Scratch of a fused launch after `base`: XQ(h) [n_slots][XQ of I], then the
- * down partial rows [n_slots][H] f32. */
-static size_t mq_fuse_scratch(int n_slots, int64_t H, int64_t I) {
-    return (((size_t)n_slots * mq_xq_bytes(I) + 255) & ~(size_t)255) + (size_t)n_slots * (size_t)H * 4;
-}
-
-static int mq_fuse_launch(const char *op, const MoeProj *g, const MoeProj *u, const MoeProj *d, const MoeProj *sg,
-                          const MoeProj *su, const MoeProj *sd, MqFuseIo *io, uint8_t *scr, const MqFusePlan *fp) {
-    io->xq_h = scr;
-    io->ypart = (float *)(scr + (((size_t)(io->topk + io->n_shared) * mq_xq_bytes(io->inter) + 255) & ~(size_t)255));
-    io->cnt = (uint32_t *)g_scratch + MQ_DN_CNT_OFF;
-    io->bar = (uint32_t *)g_scratch + MQ_BAR_WORD;
-    io->err = (uint32_t *)g_scratch + MQ_ERR_WORD;
-    MqFuseGeo geo = fp->geo;
-    void *args[] = { (void *)g, (void *)u, (void *)d, (void *)sg, (void *)su, (void *)sd, io, &geo };
-    if (!launch_lds(K_MQ_MOE, MQ_CUS, fp->threads, fp->lds, args, op)) return 0;
-    g_fused_pending = 1;
-    return 1;
-}
-
-/* One expert's FFN as one launch of sepia_mq_ffn (kernels/mq_flow.h):
- * MQ_CUS workgroups of 16 waves, one per CU. Workgroup b owns gate/up units
- * [b U / G, (b + 1) U / G) (U = I / 16 units of 16 gate and 16 up rows) on
- * waves 0 .. ngu - 1 and down row groups on the next nd1 waves; workgroups
- * without units run down only (nd0 waves) and take dh row groups instead of
- * dl, chosen so that every workgroup streams about the same bytes. Geometry
- * per role as mq_geo: the fewest steps for the busiest wave, every step in
- * flight at the start where the LDS allows. Mirrors struct MqFlowGeo. */
-typedef struct {
-    MqGeo gu, d1, d0;
-    int32_t ngu, nd1, nd0;
-    int32_t dl, dh, drem;
-    int32_t free_delay;
-    uint32_t o_xqh, o_gred, o_dred, o_ctl, o_rings;
-} MqFlowGeo;
-typedef struct {
-    const float *x;
-    float *y;
-    int64_t inter, hidden;
-    uint8_t *xq_h;
-    uint32_t *hcnt, *flags, *err;
-} MqFlowIo;
-#define MQ_FLOW_WAVES 16
-
-/* Best split of n_items items of nq quads over at most max_waves waves with
- * rings from `budget` bytes: P parts, C columns, S stages. Cost: the
- * busiest wave's steps, each step not in flight at the start counted
- * `late` more. Returns the cost, or -1 when nothing fits. */
-static int64_t mq_flow_role(int mc, int64_t n_items, int64_t nq, int max_waves, size_t budget, int64_t per_step,
-                            int64_t late, int *Pb, int *Cb, int *Sb) {
-    const size_t w1 = (size_t)k_mq_words[mc] * 1024;
-    int64_t best = -1;
-    for (int P = 1; P <= max_waves && P <= nq; P++)
-        for (int C = 1; C * P <= max_waves && C <= n_items; C++) {
-            const int64_t spw = ((n_items + C - 1) / C) * ((nq + P - 1) / P);
-            int64_t S = spw < 4 ? spw : 4;
-            while (S > 1 && (size_t)(C * P) * (size_t)S * w1 > budget) S--;
-            if ((size_t)(C * P) * (size_t)S * w1 > budget) continue;
-            const int64_t cost = per_step * spw + late * (spw - S);
-            if (best < 0 || cost < best || (cost == best && C * P < *Pb * *Cb)) {
-                best = cost;
-                *Pb = P;
-                *Cb = C;
-                *Sb = (int)S;
-            }
-        }
-    return best;
-}
-
-static int mq_flow_plan(const MoeProj *g, const MoeProj *u, const MoeProj *d, int64_t H, int64_t I, MqFlowGeo *G,
-                        unsigned *threads, size_t *lds) {
-    static int told = 0;
-    if (!g_opt_flow || g->type != u->type || g->row_bytes != u->row_bytes || !mq_proj_ok(g, I) || !mq_proj_ok(u, I) ||
-        !mq_proj_ok(d, H) || H % 256 || I % 256)
-        return 0;
-    if (g_cus < MQ_CUS) {
-        if (!told++) LOG("flow FFN launch off: %d compute units (it needs %d)", g_cus, MQ_CUS);
-        return 0;
-    }
-    const int kg = mq_code(g->type), kd = mq_code(d->type);
-    const int64_t Gn = MQ_CUS, U = I / 16, D = H / 16;
-    const int64_t n_unit = U < Gn ? U : Gn, n_free = Gn - n_unit, nu_max = (U + Gn - 1) / Gn;
-    const int64_t wu = 32 * (int64_t)g->row_bytes, wd = 16 * (int64_t)d->row_bytes;
-    /* down row groups: dl per workgroup with units, dh per other, one more
-     * for the first drem workgroups */
-    int64_t best = -1, dl = 0, dh = 0, drem = 0;
-    for (int64_t l = 0; l * n_unit <= D; l++) {
-        const int64_t R = D - l * n_unit;
-        int64_t h = 0, r = R;
-        if (n_free > 0) {
-            h = R / n_free;
-            r = R - h * n_free;
-        } else if (R >= Gn) {
-            continue;
-        }
-        int64_t c = nu_max * wu + (l + (r > 0)) * wd;
-        if (n_free > 0 && (h + (r > 0)) * wd > c) c = (h + (r > 0)) * wd;
-        if (best < 0 || c < best) {
-            best = c;
-            dl = l;
-            dh = h;
-            drem = r;
-        }
-    }
-    if (best < 0) return 0;
-    const int64_t items_d1 = dl + (drem > 0), items_d0 = n_free > 0 ? dh + (drem > 0) : 0;
-    const int64_t nqg = H / 1024, nqd = I / 1024;
-    memset(G, 0, sizeof *G);
-    size_t o = MQ_ZERO + mq_xq_bytes(H);
-    G->o_xqh = (uint32_t)align256(o);
-    o = G->o_xqh + mq_xq_bytes(I);
-    G->o_gred = (uint32_t)o;
-    o += (size_t)2 * nu_max * MQ_FLOW_WAVES * 64;
-    G->o_dred = (uint32_t)o;
-    o += (size_t)(items_d1 > items_d0 ? items_d1 : items_d0) * MQ_FLOW_WAVES * 64;
-    G->o_ctl = (uint32_t)o;
-    o += 64;
-    G->o_rings = (uint32_t)align256(o);
-    if (G->o_rings >= g_lds_max) return 0;
-    const size_t budget = g_lds_max - G->o_rings;
-    const size_t wg1 = (size_t)k_mq_words[kg] * 1024, wd1 = (size_t)k_mq_words[kd] * 1024;
-    /* workgroups with units: gate/up (critical: it gates every down wave)
-     * and down waves share the 16 waves and the ring budget */
-    int64_t bu = -1;
-    for (int ngu = 1; ngu < MQ_FLOW_WAVES; ngu++) {
-        /* the waves past the gate/up ones turn x into XQ: four lanes per
-         * segment, at most 8 passes (MQ_XQP in kernels/mq_flow.h) */
-        if (H / 16 > 8 * 16 * (MQ_FLOW_WAVES - ngu)) break;
-        int Pg = 0, Cg = 0, Sg = 0;
-        const int64_t cg = mq_flow_role(kg, 2 * nu_max, nqg, ngu, budget, 10, 6, &Pg, &Cg, &Sg);
-        if (cg < 0 || Pg * Cg != ngu) continue;
-        const size_t used = (size_t)ngu * (size_t)Sg * wg1;
-        int Pd = 1, Cd = 0, Sd = 0;
-        int64_t cd = 0;
-        if (items_d1 > 0) {
-            cd = mq_flow_role(kd, items_d1, nqd, MQ_FLOW_WAVES - ngu, budget - used, 4, 10, &Pd, &Cd, &Sd);
-            if (cd < 0) continue;
-        }
-        if (bu < 0 || cg + cd < bu) {
-            bu = cg + cd;
-            G->gu.P = Pg;
-            G->gu.ring = (int32_t)((size_t)Sg * wg1);
-            G->ngu = ngu;
-            G->d1.P = Pd;
-            G->d1.ring = (int32_t)((size_t)(Sd > 0 ? Sd : 1) * wd1);
-            G->nd1 = Pd * Cd;
-        }
-    }
-    if (bu < 0) {
-        if (!told++) LOG("flow FFN launch off: no geometry fits %zu bytes of LDS", g_lds_max);
-        return 0;
-    }
-    size_t need = G->o_rings + (size_t)G->ngu * G->gu.ring + (size_t)G->nd1 * G->d1.ring;
-    G->d0.P = 1;
-    G->d0.ring = (int32_t)wd1;
-    if (items_d0 > 0) {
-        int P = 0, C = 0, S = 0;
-        if (mq_flow_role(kd, items_d0, nqd, MQ_FLOW_WAVES, budget, 4, 10, &P, &C, &S) < 0) return 0;
-        G->d0.P = P;
-        G->d0.ring = (int32_t)((size_t)S * wd1);
-        G->nd0 = P * C;
-        const size_t n0 = G->o_rings + (size_t)G->nd0 * G->d0.ring;
-        if (n0 > need) need = n0;
-    }
-    G->dl = (int32_t)dl;
-    G->dh = (int32_t)dh;
-    G->drem = (int32_t)drem;
-    G->free_delay = g_opt_flow_delay;
-    *threads = 64u * MQ_FLOW_WAVES;
-    *lds = need;
-    int nb = 0;
-    const hipError_t e = hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&nb, g_fn[K_MQ_FFN], (int)*threads, *lds);
-    if (e != hipSuccess || nb < 1 || (int64_t)nb * g_cus < MQ_CUS) {
-        if (!told++)
-            LOG("flow FFN launch off: occupancy query %s, %d workgroups of %u threads and %zu bytes LDS per CU",
-                hipGetErrorString(e), nb, *threads, *lds);
-        return 0;
-    }
-    return 1;
-}
-
-static int mq_flow_launch(const char *op, const MoeProj *g, const MoeProj *u, const MoeProj *d, int32_t expert,
-                          int64_t H, int64_t I, const uint8_t *xdev, float *ydev, uint8_t *scr, const MqFlowGeo *fg,
-                          unsigned threads, size_t lds) {
-    MqFlowIo io;
-    io.x = (const float *)xdev;
-    io.y = ydev;
-    io.inter = I;
-    io.hidden = H;
-    io.xq_h = scr;
-    io.hcnt = (uint32_t *)g_scratch + MQ_FLOW_HCNT_WORD;
-    io.flags = (uint32_t *)g_scratch + MQ_FLOW_FLAG_OFF;
-    io.err = (uint32_t *)g_scratch + MQ_ERR_WORD;
-    MqFlowGeo geo = *fg;
-    void *args[] = { (void *)g, (void *)u, (void *)d, &expert, &io, &geo };
-    if (!launch_lds(K_MQ_FFN, MQ_CUS, threads, lds, args, op)) return 0;
-    g_fused_pending = 1;
-    return 1;
-}
-
-/* The MoE decode's gate/up as one launch of sepia_mq_gateup_mix
- * (kernels/mq_mix.h): MQ_CUS workgroups of 16 waves; wave 0 selects, waves
- * 1..15 stream. Workgroup b takes shared units [b us / G, (b + 1) us / G)
- * and routed units up to about T (b + 1) / G bytes in all (a unit: 16 rows
- * of one slot's gate and up). Mirrors struct MqMixGeo. */
-typedef struct {
-    MqGeo gu;
-    uint32_t o_sel, o_ctl, o_gred, o_rings;
-    int32_t nstream;
-} MqMixGeo;
-static int64_t mq_mix_rbefore(int64_t us, int64_t ws, int64_t ur, int64_t wr, int64_t G, int64_t b) {
-    const int64_t T = us * ws + ur * wr;
-    const int64_t f = T * b / G - (b * us / G) * ws;
-    const int64_t r = f <= 0 ? 0 : f / wr;
-    return r < ur ? r : ur;
-}
-static int mq_mix_plan(const MoeProj *g, const MoeProj *sg, int32_t topk, int32_t n_shared, int64_t H, int64_t I,
-                       MqMixGeo *G, unsigned *threads, size_t *lds) {
-    if (!g_opt_mix || topk < 1 || H / 16 > 8 * 15 * 16 || I % 16) return 0;
-    const int64_t Gn = MQ_CUS, tiles_i = I / 16, us = (int64_t)n_shared * tiles_i, ur = (int64_t)topk * tiles_i;
-    const int64_t ws = n_shared > 0 ? 32 * (int64_t)sg->row_bytes : 0, wr = 32 * (int64_t)g->row_bytes;
-    const int64_t T = us * ws + ur * wr;
-    /* the routed split is monotone when no workgroup's shared units outweigh its byte share */
-    if (T / Gn < ws * ((us + Gn - 1) / Gn)) return 0;
-    int64_t nu_max = 1;
-    for (int64_t b = 0; b < Gn; b++) {
-        const int64_t ns = (b + 1) * us / Gn - b * us / Gn;
-        const int64_t nr = mq_mix_rbefore(us, ws, ur, wr, Gn, b + 1) - mq_mix_rbefore(us, ws, ur, wr, Gn, b);
-        if (nr < 0) return 0;
-        if (ns + nr > nu_max) nu_max = ns + nr;
-    }
-    int wmax = k_mq_words[mq_code(g->type)];
-    if (n_shared > 0 && k_mq_words[mq_code(sg->type)] > wmax) wmax = k_mq_words[mq_code(sg->type)];
-    const size_t wm = (size_t)wmax * 1024;
-    const int64_t nq = H / 1024;
-    memset(G, 0, sizeof *G);
-    size_t o = MQ_ZERO + mq_xq_bytes(H);
-    G->o_sel = (uint32_t)align256(o);
-    G->o_ctl = G->o_sel + MQ_FSEL_BYTES;
-    G->o_gred = G->o_ctl + 64;
-    int64_t best = -1;
-    for (int P = 1; P <= 15 && P <= nq; P++) {
-        if (g_opt_mq_p && P != g_opt_mq_p) continue;
-        const int C = g_opt_mq_c && g_opt_mq_c * P <= 15 ? g_opt_mq_c : 15 / P;
-        const size_t o_rings = align256((size_t)G->o_gred + (size_t)2 * nu_max * P * 64);
-        if (o_rings + (size_t)(P * C) * wm > g_lds_max) continue;
-        size_t ring = ((g_lds_max - o_rings) / (size_t)(P * C)) & ~(size_t)1023;
-        if (ring > 4 * wm) ring = 4 * wm;
-        const int64_t spw = ((2 * nu_max + C - 1) / C) * ((nq + P - 1) / P);
-        const int64_t S = (int64_t)(ring / wm);
-        const int64_t cost = spw * ((S >= 2 || spw == 1) ? 10 : 16);
-        if (best < 0 || cost < best) {
-            best = cost;
-            G->gu.P = P;
-            G->gu.ring = (int32_t)ring;
-            G->o_rings = (uint32_t)o_rings;
-            G->nstream = P * C;
-            *lds = o_rings + (size_t)(P * C) * ring;
-        }
-    }
-    if (best < 0) return 0;
-    *threads = 1024;
-    return 1;
-}
-
-/* The MoE decode's down as one launch of sepia_mq_down_rows
- * (kernels/mq_rows.h): MQ_CUS workgroups of 16 waves; workgroup b owns row
- * groups [b T / G, (b + 1) T / G) of every slot, with every slot's XQ(h) in
- * its LDS; routed and shared rows stream on their own waves at once. The
- * split of waves and ring stages: the fewest steps for the busier role, then
- * the most stages. Mirrors struct MqRowsGeo. */
-typedef struct {
-    MqGeo gr, gs;
-    int32_t nwr, nws;
-    uint32_t o_red, o_rings_s;
-} MqRowsGeo;
-static int mq_rows_plan(const MoeProj *d, const MoeProj *sd, int32_t topk, int32_t n_shared, int64_t H, int64_t I,
-                        MqRowsGeo *G, unsigned *threads, size_t *lds) {
-    const int n_slots = topk + n_shared;
-    if (!g_opt_dnrows || topk < 1 || n_slots < 2 || topk > 64 || H % 16 || (I / 16) * n_slots > 4 * 1024) return 0;
-    const int64_t T = H / 16, nrg = (T + MQ_CUS - 1) / MQ_CUS, nq = I / 1024;
-    const int kd = mq_code(d->type), ks = n_shared > 0 ? mq_code(sd->type) : kd;
-    const size_t wr1 = (size_t)k_mq_words[kd] * 1024, ws1 = (size_t)k_mq_words[ks] * 1024;
-    const size_t xq_all = (size_t)n_slots * 4 * (size_t)I;
-    int64_t best = -1, best_fl = 0;
-    memset(G, 0, sizeof *G);
-    for (int Pr = 1; Pr <= 16 && Pr <= nq; Pr++)
-        for (int Cr = 1; Pr * Cr <= 16 && Cr <= topk * nrg; Cr++)
-            for (int Ps = 1; Ps <= nq; Ps++)
-                for (int Cs = (n_shared > 0 ? 1 : 0); Pr * Cr + Ps * Cs <= 16 && Cs <= n_shared * nrg; Cs++) {
-                    const int nwr = Pr * Cr, nws = Ps * Cs;
-                    const size_t o_red = align256(MQ_ZERO + xq_all + 256);   /* the experts just below */
-                    const size_t o_rings =
-                        align256(o_red + (size_t)topk * nrg * Pr * 64 + (size_t)n_shared * nrg * Ps * 64);
-                    const size_t avail = g_lds_max;
-                    if (o_rings + (size_t)nwr * wr1 + (size_t)nws * ws1 > avail) continue;
-                    const int64_t spw_r = ((topk * nrg + Cr - 1) / Cr) * ((nq + Pr - 1) / Pr);
-                    const int64_t spw_s = Cs ? ((n_shared * nrg + Cs - 1) / Cs) * ((nq + Ps - 1) / Ps) : 0;
-                    /* stages: as many as the LDS holds, the same number for both roles */
-                    int64_t S = 4;
-                    while (S > 1 && o_rings + (size_t)nwr * S * wr1 + (size_t)nws * S * ws1 > avail) S--;
-                    const int64_t spw = spw_r > spw_s ? spw_r : spw_s;
-                    const int64_t cost = spw * ((S >= 2 || spw == 1) ? 10 : 16);
-                    const int64_t fl = (int64_t)(nwr + nws) * S;
-                    if (best < 0 || cost < best || (cost == best && fl > best_fl)) {
-                        best = cost;
-                        best_fl = fl;
-                        G->gr.P = Pr;
-                        G->gr.ring = (int32_t)(S * wr1);
-                        G->gr.orings = (int32_t)o_rings;
-                        G->gs.P = Ps;
-                        G->gs.ring = (int32_t)(S * ws1);
-                        G->nwr = nwr;
-                        G->nws = nws;
-                        G->o_red = (uint32_t)o_red;
-                        G->o_rings_s = (uint32_t)(o_rings + (size_t)nwr * S * wr1);
-                        *lds = G->o_rings_s + (size_t)nws * S * ws1;
-                    }
-                }
-    if (best < 0) return 0;
-    *threads = 1024;
     return 1;
 }
 
@@ -2130,25 +1594,9 @@ static int ffn_launch(const char *op, const MoeProj *g, const MoeProj *u, const 
         MqRoute rt;
         memset(&rt, 0, sizeof rt);
         if (route) rt = *route;
-        MqMixGeo mg;
-        unsigned mix_threads;
-        size_t mix_lds;
-        if (route && mq_mix_plan(g, sg, topk, n_shared, H, I, &mg, &mix_threads, &mix_lds)) {
-            void *a_mx[] = { (void *)g, (void *)u, (void *)sg, (void *)su, &rt, &topk, &n_shared, &inter32, &xdev, &h,
-                             &mg };
-            if (!launch_lds(K_MQ_GU_MIX, MQ_CUS, mix_threads, mix_lds, a_mx, op)) return 0;
-        } else {
-            void *a_gu[] = { (void *)g, (void *)u, (void *)sg, (void *)su, &sel_idx, &fixed, &topk, &inter32,
-                             &pl.gu_wps_r, &pl.gu_wps_s, &xdev, &h, &pl.gu_geo, &rt, &pl.gu_hxq };
-            if (!launch_lds(K_MQ_GU, pl.gu_grid, pl.gu_threads, pl.gu_lds, a_gu, op)) return 0;
-        }
-        MqRowsGeo rg;
-        unsigned rows_threads;
-        size_t rows_lds;
-        if (sel_idx && sel_w && mq_rows_plan(d, sd, topk, n_shared, H, I, &rg, &rows_threads, &rows_lds)) {
-            void *a_rw[] = { (void *)d, (void *)sd, &sel_idx, &sel_w, &topk, &n_shared, &inter32, &hid, &h, &ydev, &rg };
-            return launch_lds(K_MQ_DN_ROWS, MQ_CUS, rows_threads, rows_lds, a_rw, op);
-        }
+        void *a_gu[] = { (void *)g, (void *)u, (void *)sg, (void *)su, &sel_idx, &fixed, &topk, &inter32,
+                         &pl.gu_wps_r, &pl.gu_wps_s, &xdev, &h, &pl.gu_geo, &rt };
+        if (!launch_lds(K_MQ_GU, pl.gu_grid, pl.gu_threads, pl.gu_lds, a_gu, op)) return 0;
         void *a_dn[] = { (void *)d, (void *)sd, &sel_idx, &sel_w, &fixed, &topk, &n_shared, &inter32, &hid, &h, &ydev,
                          &pl.dn_geo, &pl.dn_wps_r, &pl.dn_wps_s, &ypart, &cnt };
         return launch_lds(K_MQ_DN, pl.dn_grid, pl.dn_threads, pl.dn_lds, a_dn, op);
@@ -2232,17 +1680,13 @@ int sepia_gpu_moe_decode(const SepiaMoeLayerDesc *L, SepiaGpuBuf *x, SepiaGpuBuf
     const size_t o_idx = o_logits + (((size_t)n_tot * 4 + 255) & ~(size_t)255);
     const size_t o_w = o_idx + 256;
     const size_t o_h = o_w + 256;
-    const size_t need_f = mq_fuse_scratch(n_slots, H, I), need_s = ffn_scratch_bytes(n_slots, I, H);
-    uint8_t *s = (uint8_t *)scratch(o_h + (need_f > need_s ? need_f : need_s), op);
+    uint8_t *s = (uint8_t *)scratch(o_h + ffn_scratch_bytes(n_slots, I, H), op);
     if (!s) return 0;
     float *logits = (float *)(s + o_logits), *sel_w = (float *)(s + o_w);
     int32_t *sel_idx = (int32_t *)(s + o_idx);
     uint32_t *counter = (uint32_t *)g_scratch;
 
-    SepiaGpuBuf *ins[] = { L->router_w, L->router_bias, x, L->gate.buf, L->up.buf, L->down.buf, L->s_gate.buf,
-                           L->s_up.buf, L->s_down.buf };
-    for (size_t i = 0; i < sizeof ins / sizeof ins[0]; i++)
-        if (ins[i] && !prep_in(ins[i], op)) return 0;
+    if (!prep_layer(L, &g, &u, &d, &sg, &su, &sd, x, (size_t)H * 4, op)) return 0;
     if (!prep_out(y, op) || (route_out && !prep_out(route_out, op))) return 0;
 
     const float *rw = (const float *)(L->router_w->dev + L->router_w_off);
@@ -2250,31 +1694,10 @@ int sepia_gpu_moe_decode(const SepiaMoeLayerDesc *L, SepiaGpuBuf *x, SepiaGpuBuf
     int64_t ld = H, hid = H;
     int32_t nr = L->n_routed, ns = L->n_shared, tk = L->topk;
     float rs = L->route_scale, gsc = L->global_scale;
-    MqFusePlan fp;
-    if (mq_fuse_plan(&g, &u, &d, &sg, &su, &sd, tk, ns, H, I, 1, &fp)) {
-        MqFuseIo io;
-        memset(&io, 0, sizeof io);
-        io.rw = rw;
-        io.ld = ld;
-        io.bias = rb;
-        io.x = (const float *)x->dev;
-        io.n_routed = nr;
-        io.n_shared = ns;
-        io.topk = tk;
-        io.route_scale = rs;
-        io.global_scale = gsc;
-        io.inter = I;
-        io.hidden = H;
-        io.logits = logits;
-        io.sel_idx = sel_idx;
-        io.sel_w = sel_w;
-        io.y = (float *)y->dev;
-        if (!mq_fuse_launch(op, &g, &u, &d, &sg, &su, &sd, &io, s + o_h, &fp)) return 0;
-    } else {
     /* with the matrix-core FFN the gate/up launch selects from the logits;
      * otherwise the router's last workgroup does */
     MqFfnPlan pl;
-    const int in_kernel = !g_opt_route_sel && mq_ffn_plan(&g, &u, &d, &sg, &su, &sd, tk, ns, H, I, &pl);
+    const int in_kernel = mq_ffn_plan(&g, &u, &d, &sg, &su, &sd, tk, ns, H, I, &pl);
     int32_t select = !in_kernel;
     void *a_route[] = { &rw, &ld, &rb, &x->dev, &hid, &nr, &ns, &tk, &rs, &gsc, &logits, &sel_idx, &sel_w, &counter,
                         &select };
@@ -2284,7 +1707,6 @@ int sepia_gpu_moe_decode(const SepiaMoeLayerDesc *L, SepiaGpuBuf *x, SepiaGpuBuf
     if (!ffn_launch(op, &g, &u, &d, &sg, &su, &sd, sel_idx, sel_w, 0, tk, ns, H, I, x->dev, (float *)y->dev, s + o_h,
                     in_kernel ? &rt : NULL))
         return 0;
-    }
 
     if (route_out) {
         hipError_t e = hipMemcpyAsync(route_out->dev, sel_idx, (size_t)L->topk * 4, hipMemcpyDeviceToDevice, g_stream);
@@ -2314,30 +1736,13 @@ int sepia_gpu_expert_ffn(const SepiaExpertTensor *gate, const SepiaExpertTensor 
         return 0;
     if (!chk(x, 0, (size_t)hidden * 4, op, "x") || !chk(y, 0, (size_t)hidden * 4, op, "y")) return 0;
     if (!need_batch(op)) return 0;
-    const size_t need_f = mq_fuse_scratch(1, hidden, inter), need_s = ffn_scratch_bytes(1, inter, hidden);
-    uint8_t *scr = (uint8_t *)scratch(need_f > need_s ? need_f : need_s, op);
+    uint8_t *scr = (uint8_t *)scratch(ffn_scratch_bytes(1, inter, hidden), op);
     if (!scr) return 0;
-    if (!prep_in(gate->buf, op) || !prep_in(up->buf, op) || !prep_in(down->buf, op) || !prep_in(x, op) ||
-        !prep_out(y, op))
+    if (!prep_in_r(gate->buf, gate->off + (size_t)expert * gate->stride, (size_t)inter * g.row_bytes, op) ||
+        !prep_in_r(up->buf, up->off + (size_t)expert * up->stride, (size_t)inter * u.row_bytes, op) ||
+        !prep_in_r(down->buf, down->off + (size_t)expert * down->stride, (size_t)hidden * d.row_bytes, op) ||
+        !prep_in(x, op) || !prep_out(y, op))
         return 0;
-    MqFlowGeo flg;
-    unsigned fl_threads;
-    size_t fl_lds;
-    if (mq_flow_plan(&g, &u, &d, hidden, inter, &flg, &fl_threads, &fl_lds))
-        return mq_flow_launch(op, &g, &u, &d, expert, hidden, inter, x->dev, (float *)y->dev, scr, &flg, fl_threads,
-                              fl_lds);
-    MqFusePlan fp;
-    if (mq_fuse_plan(&g, &u, &d, &none, &none, &none, 1, 0, hidden, inter, 0, &fp)) {
-        MqFuseIo io;
-        memset(&io, 0, sizeof io);
-        io.x = (const float *)x->dev;
-        io.topk = 1;
-        io.fixed = expert;
-        io.inter = inter;
-        io.hidden = hidden;
-        io.y = (float *)y->dev;
-        return mq_fuse_launch(op, &g, &u, &d, &none, &none, &none, &io, scr, &fp);
-    }
     return ffn_launch(op, &g, &u, &d, &none, &none, &none, NULL, NULL, expert, 1, 0, hidden, inter, x->dev,
                       (float *)y->dev, scr, NULL);
 }

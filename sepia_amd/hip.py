@@ -82,6 +82,8 @@ PROTOTYPES = {
     "sepia_hip_profile_reset": (None, []),
     "sepia_hip_synth_blocks": (_I, [_I, _P, _SZ, _I64, ctypes.c_uint64, _F, _F]),
     "sepia_hip_set_iq2xxs_grid": (_I, [_P]),
+    "sepia_hip_reserve_scratch": (_I, [_SZ]),
+    "sepia_hip_uploaded_bytes": (ctypes.c_uint64, []),
     "sepia_hip_stream": (_P, []),
     "sepia_hip_set_option": (_I, [ctypes.c_char_p, _I]),
 }

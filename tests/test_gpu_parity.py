@@ -210,25 +210,17 @@ def test_matvec_q_config_shapes(dev, orc, name, t, out_dim, in_dim):
 @pytest.fixture
 def kernel_path(dev, request):
     """Force one kernel family: the matrix-core kernels (the default), the
-    matrix-core MoE layer / expert FFN as one launch ("fused"), the expert
-    FFN as one launch of gate/up and down waves side by side ("flow"), the
     generic per-row kernel, or the tile kernels with 1, 2 or 3 row steps per
     workgroup."""
     L = dev.L
     mode = request.param
-    if mode == "fused":
-        assert L.sepia_hip_set_option(b"fuse", 1) == 1
-    elif mode == "flow":
-        assert L.sepia_hip_set_option(b"flow", 1) == 1
-    elif mode != "mq":
+    if mode != "mq":
         assert L.sepia_hip_set_option(b"mq", 0) == 1
     if mode == "generic":
         assert L.sepia_hip_set_option(b"tile", 0) == 1
-    elif mode not in ("mq", "fused", "flow"):
+    elif mode != "mq":
         assert L.sepia_hip_set_option(b"tile_t", {"t1": 1, "t2": 2, "t3": 3}[mode]) == 1
     yield mode
-    L.sepia_hip_set_option(b"fuse", 0)
-    L.sepia_hip_set_option(b"flow", 0)
     L.sepia_hip_set_option(b"mq", 1)
     L.sepia_hip_set_option(b"tile", 1)
     L.sepia_hip_set_option(b"tile_t", 0)
@@ -287,7 +279,6 @@ def mq_geometry(dev, request):
     L = dev.L
     for k, v in zip(("mq_p", "mq_c", "mq_s"), request.param):
         assert L.sepia_hip_set_option(k.encode(), v) == 1
-    assert L.sepia_hip_set_option(b"fuse", 0) == 1      # the separate gate/up and down launches
     yield request.param
     for k in ("mq_p", "mq_c", "mq_s"):
         L.sepia_hip_set_option(k.encode(), 0)
@@ -458,6 +449,52 @@ def test_selftest_touch_and_wrap(dev):
     m.close()
 
 
+def test_shared_slab_uploaded_once(dev, orc):
+    """Shared-buffer synchronisation: a slab the host fills once through
+    host_ptr is uploaded once however many batches read it; an op uploads only
+    the 1 MiB chunks of the range it reads; a later host_ptr re-arms the slab
+    and the next op sees the host's new bytes."""
+    L = dev.L
+    t, rows, cols, n_exp, C = 12, 256, 4096, 16, 1 << 20
+    mb = rows * synth.row_bytes(t, cols)
+    rng = np.random.default_rng(808)
+    mats = [synth.random_matrix(t, rows, cols, rng) for _ in range(n_exp)]
+    slab = dev.alloc(n_exp * mb)
+    dev.upload(slab, np.concatenate(mats))
+    x = synth.normal_vector(rng, cols)
+    xb = dev.shared_from(x)
+    yb = dev.alloc(rows * 4)
+
+    def chunks(off, n, total):
+        c0, c1 = off // C, (off + n - 1) // C
+        return sum(min((c + 1) * C, total) - c * C for c in range(c0, c1 + 1))
+
+    def uploaded():
+        return int(L.sepia_hip_uploaded_bytes())
+
+    u0 = uploaded()
+    dev.run(L.sepia_gpu_matvec_q, t, slab, 3 * mb, xb, yb, rows, cols)
+    assert uploaded() - u0 == chunks(3 * mb, mb, n_exp * mb) + cols * 4
+    u1 = uploaded()
+    for _ in range(5):
+        dev.run(L.sepia_gpu_matvec_q, t, slab, 3 * mb, xb, yb, rows, cols)
+    assert uploaded() == u1, "a clean slab range was uploaded again"
+    assert_close(dev.download(yb, rows), orc.qlinear(t, mats[3], rows, cols, x, threads=THREADS), what="slab e3")
+    u2 = uploaded()
+    dev.run(L.sepia_gpu_matvec_q, t, slab, 7 * mb, xb, yb, rows, cols)
+    # expert 7's chunks (disjoint from expert 3's) and y, which the download above re-armed
+    assert uploaded() - u2 == chunks(7 * mb, mb, n_exp * mb) + rows * 4
+    assert_close(dev.download(yb, rows), orc.qlinear(t, mats[7], rows, cols, x, threads=THREADS), what="slab e7")
+    new3 = synth.random_matrix(t, rows, cols, rng)
+    dev.upload(slab, new3, offset=3 * mb)
+    u3 = uploaded()
+    dev.run(L.sepia_gpu_matvec_q, t, slab, 3 * mb, xb, yb, rows, cols)
+    assert uploaded() - u3 == chunks(3 * mb, mb, n_exp * mb) + rows * 4
+    assert_close(dev.download(yb, rows), orc.qlinear(t, new3, rows, cols, x, threads=THREADS), what="slab e3 new")
+    for b in (slab, xb, yb):
+        dev.free(b)
+
+
 # ------------------------------------------------------------------- MoE
 @pytest.fixture
 def mq_vector(dev, request):
@@ -540,7 +577,11 @@ def check_route(orc, spec, logits, idx_gpu, w_gpu):
         assert gap < 1e-5 and set(idx_gpu) ^ set(idx_ref), (idx_gpu, idx_ref, gap)
         w_ref = orc.route_weights(logits, spec["n_routed"], spec["n_shared"], idx_gpu, spec["route_scale"],
                                   spec["global_scale"])
-    assert np.allclose(w_gpu, w_ref, rtol=1e-5, atol=0)
+    # The weights are exp(logsigmoid(logit) - lse): a logit's absolute error is
+    # about their relative error. The GPU routers sum 6144 f32 products in
+    # another order than the oracle's double sum (|error| up to a few 1e-5 at
+    # C3's logit sizes), so 1e-4 relative; y is held to its own bar.
+    assert np.allclose(w_gpu, w_ref, rtol=1e-4, atol=0), (w_gpu, w_ref)
     return list(idx_gpu)
 
 
@@ -563,7 +604,7 @@ def test_moe_decode_small(dev, orc, types, seed):
         dev.free(b)
 
 
-@pytest.mark.parametrize("kernel_path", ["mq", "fused", "generic", "t1", "t3"], indirect=True)
+@pytest.mark.parametrize("kernel_path", ["mq", "generic", "t1", "t3"], indirect=True)
 @pytest.mark.parametrize("types", [(10, 10, 11, 12), (12, 12, 12, 10), (11, 11, 10, 11)],
                          ids=["q2k_q3k_q4k", "q4k_q4k_q2k", "q3k_q2k_q3k"])
 def test_moe_decode_tile_shapes(dev, orc, kernel_path, types):
@@ -624,64 +665,30 @@ def test_moe_decode_mq_geometries(dev, orc, mq_geometry):
         dev.free(b)
 
 
-@pytest.mark.parametrize("fuse", [1, 0], ids=["fused", "three_launches"])
-@pytest.mark.parametrize("types", [(10, 10, 11, 12), (12, 12, 12, 10), (11, 11, 10, 11)],
-                         ids=["q2k_q3k_q4k", "q4k_q4k_q2k", "q3k_q2k_q3k"])
-def test_moe_decode_fused(dev, orc, fuse, types):
-    """The one-launch layer (grid barriers) and the three-launch layer give the
-    oracle's result; the launch counts show which ran."""
-    rng = np.random.default_rng(9000 + 10 * fuse + types[0])
-    tg, tu, td, ts = types
-    desc, spec, bufs = make_layer(dev, rng, hidden=6144, inter=3072, n_routed=16, n_shared=2,
-                                  tg=tg, tu=tu, td=td, ts=ts)
-    assert dev.L.sepia_hip_set_option(b"fuse", fuse) == 1
-    try:
-        for rep in range(2):
-            x = synth.normal_vector(rng, 6144)
-            with Launches(dev) as n:
-                y, idx, w = run_moe(dev, desc, x)
-                assert n.count("sepia_mq_moe") == fuse
-                assert n.count("sepia_mq_gateup") == 1 - fuse
-            y_ref, logits, idx_ref, w_ref = orc.moe_layer(spec, x, threads=THREADS)
-            chosen = check_route(orc, spec, logits, idx, w)
-            if chosen != list(idx_ref):
-                y_ref, _, _, _ = orc.moe_layer(spec, x, force_idx=chosen, threads=THREADS)
-            assert_close(y, y_ref, what="moe fuse=%d rep %d" % (fuse, rep), gate=False)
-    finally:
-        dev.L.sepia_hip_set_option(b"fuse", 0)
-    for b in bufs.values():
-        dev.free(b)
-
-
 @pytest.mark.parametrize("types,n_routed,n_shared,topk",
                          [((10, 10, 11, 12), 16, 2, 6), ((12, 12, 12, 10), 16, 2, 6), ((11, 11, 10, 11), 16, 2, 6),
                           ((10, 10, 11, 12), 16, 0, 6), ((10, 10, 11, 12), 8, 1, 1)],
                          ids=["q2k_q3k_q4k", "q4k_q4k_q2k", "q3k_q2k_q3k", "no_shared", "top1"])
-@pytest.mark.parametrize("opt", ["mix", "dnrows", "dyn"])
-def test_moe_decode_mix(dev, orc, types, n_routed, n_shared, topk, opt):
-    """The gate/up launch that streams shared units while wave 0 selects
-    (sepia_mq_gateup_mix), the down launch with every slot of a row group in
-    one workgroup (sepia_mq_down_rows) and the down launch whose steps are
-    dealt at run time (dyn) give the oracle's result, twice in a row."""
+def test_moe_decode_slots(dev, orc, types, n_routed, n_shared, topk):
+    """C3 layer shapes with mixed formats, without shared experts and with a
+    single routed slot: the router and the two matrix-core FFN launches (the
+    launch counts show it) give the oracle's result twice in a row (the down
+    launch's arrival counters must be back at zero after the first)."""
     rng = np.random.default_rng(9100 + types[0] + n_shared + topk)
     tg, tu, td, ts = types
     desc, spec, bufs = make_layer(dev, rng, hidden=6144, inter=3072, n_routed=n_routed, n_shared=n_shared,
                                   tg=tg, tu=tu, td=td, ts=ts, topk=topk)
-    kname = {"mix": "sepia_mq_gateup_mix", "dnrows": "sepia_mq_down_rows", "dyn": "sepia_mq_down"}[opt]
-    assert dev.L.sepia_hip_set_option(opt.encode(), 1) == 1
-    try:
-        for rep in range(2):
-            x = synth.normal_vector(rng, 6144)
-            with Launches(dev) as n:
-                y, idx, w = run_moe(dev, desc, x)
-                assert n.count(kname) == 1
-            y_ref, logits, idx_ref, w_ref = orc.moe_layer(spec, x, threads=THREADS)
-            chosen = check_route(orc, spec, logits, idx, w)
-            if chosen != list(idx_ref):
-                y_ref, _, _, _ = orc.moe_layer(spec, x, force_idx=chosen, threads=THREADS)
-            assert_close(y, y_ref, what="moe %s rep %d" % (opt, rep), gate=False)
-    finally:
-        dev.L.sepia_hip_set_option(opt.encode(), 0)
+    for rep in range(2):
+        x = synth.normal_vector(rng, 6144)
+        with Launches(dev) as n:
+            y, idx, w = run_moe(dev, desc, x)
+            assert n.count("sepia_moe_route") == 1
+            assert n.count("sepia_mq_gateup") == 1 and n.count("sepia_mq_down") == 1
+        y_ref, logits, idx_ref, w_ref = orc.moe_layer(spec, x, threads=THREADS)
+        chosen = check_route(orc, spec, logits, idx, w)
+        if chosen != list(idx_ref):
+            y_ref, _, _, _ = orc.moe_layer(spec, x, force_idx=chosen, threads=THREADS)
+        assert_close(y, y_ref, what="moe slots rep %d" % rep, gate=False)
     for b in bufs.values():
         dev.free(b)
 
@@ -739,35 +746,30 @@ PREFILL_CASES = [
 ]
 
 
-@pytest.mark.parametrize("gu", [2, 1, 0])
+@pytest.mark.parametrize("reg", [1, 0])
 @pytest.mark.parametrize("x_kind", ["bf16", "f32"])
 @pytest.mark.parametrize("shape,types,T", PREFILL_CASES, ids=lambda v: str(v))
-def test_moe_prefill(dev, orc, shape, types, T, x_kind, gu):
+def test_moe_prefill(dev, orc, shape, types, T, x_kind, reg):
     """Every token of the batch against the oracle's single-token layer (its
     own routing, near-ties per the reference protocol); two runs bitwise equal.
     x either bf16-representable (the projections skip the zero lo terms) or
-    full f32. gu (option pf_gu): integer-format gate/up with the codes in
-    registers (2, the default), on 16 waves (1) or on the 8-wave kernel (0);
-    gu 0 also runs the integer-format down on sepia_pf_down (option pf_dn 0)
-    instead of sepia_pf_down_r and the router on sepia_pf_route (option
-    pf_route_m 0) instead of the matrix-core one."""
+    full f32. reg (option pf_reg): integer-format gate/up and down with the
+    codes in registers (1, the default) or on the LDS-tile kernels (0); reg 0
+    also runs the router on sepia_pf_route (option pf_route_m 0) instead of
+    the matrix-core one."""
     hidden, inter, n_routed, n_shared = shape
     tgu, td, ts = types
-    if gu == 1 and not ({tgu, ts} <= {10, 11, 12}):
-        pytest.skip("pf_gu 1 changes nothing in layers whose gate/up is not all Q2_K / Q3_K / Q4_K")
     rng = np.random.default_rng(hidden + 7 * T + tgu)
     desc, spec, bufs = make_layer(dev, rng, hidden=hidden, inter=inter, n_routed=n_routed, n_shared=n_shared,
                                   tg=tgu, tu=tgu, td=td, ts=ts)
     X = bf16_normal(rng, (T, hidden)) if x_kind == "bf16" else rng.standard_normal((T, hidden)).astype(np.float32)
-    assert dev.L.sepia_hip_set_option(b"pf_gu", gu) == 1
-    assert dev.L.sepia_hip_set_option(b"pf_dn", 1 if gu else 0) == 1
-    assert dev.L.sepia_hip_set_option(b"pf_route_m", 1 if gu else 0) == 1
+    assert dev.L.sepia_hip_set_option(b"pf_reg", reg) == 1
+    assert dev.L.sepia_hip_set_option(b"pf_route_m", reg) == 1
     try:
         y, idx, w = run_prefill(dev, desc, X)
         y2, _, _ = run_prefill(dev, desc, X)
     finally:
-        dev.L.sepia_hip_set_option(b"pf_gu", 2)
-        dev.L.sepia_hip_set_option(b"pf_dn", 1)
+        dev.L.sepia_hip_set_option(b"pf_reg", 1)
         dev.L.sepia_hip_set_option(b"pf_route_m", 1)
     assert np.array_equal(y.view(np.uint32), y2.view(np.uint32))
     for t in range(T):
@@ -782,16 +784,25 @@ def test_moe_prefill(dev, orc, shape, types, T, x_kind, gu):
 
 def test_moe_prefill_matches_decode(dev, orc):
     """A prefill batch and token-by-token decode of the same layer agree to the
-    layer bar (their routers sum the logits in different orders)."""
+    layer bar. Their routers sum the logits in different orders, so a token
+    may be routed differently only across a near-tie of the selection scores
+    (check_route against the oracle's logits); at least 10 of the 12 tokens
+    must be compared."""
     rng = np.random.default_rng(4242)
     desc, spec, bufs = make_layer(dev, rng, hidden=2048, inter=1024, n_routed=16, n_shared=2,
                                   tg=10, tu=10, td=11, ts=12)
     X = bf16_normal(rng, (12, 2048))
-    y, idx, _ = run_prefill(dev, desc, X)
+    y, idx, wp = run_prefill(dev, desc, X)
+    compared = 0
     for t in range(12):
-        yd, idd, _ = run_moe(dev, desc, X[t].copy())
+        yd, idd, wd = run_moe(dev, desc, X[t].copy())
+        logits = orc.linear_f32(spec["router_w"], X[t])
+        check_route(orc, spec, logits, idx[t], wp[t])
+        check_route(orc, spec, logits, idd, wd)
         if list(idd) == list(idx[t]):
             assert_close(y[t], yd, what="prefill vs decode token %d" % t, gate=False)
+            compared += 1
+    assert compared >= 10, "only %d of 12 tokens routed alike" % compared
     for b in bufs.values():
         dev.free(b)
 
@@ -808,7 +819,7 @@ def run_expert_ffn(dev, tensors, n_experts, expert, hidden, inter, x):
     return y
 
 
-@pytest.mark.parametrize("kernel_path", ["mq", "fused", "flow", "generic", "t1", "t2", "t3"], indirect=True)
+@pytest.mark.parametrize("kernel_path", ["mq", "generic", "t1", "t2", "t3"], indirect=True)
 @pytest.mark.parametrize("types,hidden,inter", [((10, 10, 11), 6144, 3072), ((12, 12, 12), 4096, 2048),
                                                 ((11, 11, 10), 2048, 1024)],
                          ids=["c2_q2k_q3k", "q4k_4096", "q3k_q2k_2048"])
@@ -835,12 +846,10 @@ def test_expert_ffn(dev, orc, kernel_path, types, hidden, inter):
                                                 ((11, 11, 12), 2048, 8192), ((10, 10, 10), 1024, 1024),
                                                 ((12, 12, 11), 3072, 4096)],
                          ids=["c2", "units_half", "two_units_per_wg", "tiny", "q4k_q3k"])
-def test_expert_ffn_flow(dev, orc, types, hidden, inter):
-    """The one-launch expert FFN with gate/up and down waves side by side,
-    over splits with free workgroups (fewer units than CUs), several units
-    per workgroup and fewer down row groups than workgroups. Each shape
-    runs twice: the second launch needs the h counters the first one put
-    back to zero."""
+def test_expert_ffn_shapes(dev, orc, types, hidden, inter):
+    """The expert FFN on the matrix-core launches over shapes with fewer row
+    groups than workgroups, several row groups per workgroup and long rows;
+    each shape runs twice."""
     rng = np.random.default_rng(7 * hidden + inter)
     tg, tu, td = types
     n_e, e = 2, 1
@@ -849,14 +858,14 @@ def test_expert_ffn_flow(dev, orc, types, hidden, inter):
     down = [synth.random_matrix(td, hidden, inter, rng) for _ in range(n_e)]
     bufs = [dev.shared_from(np.concatenate(v)) for v in (gate, up, down)]
     tensors = [hip.ExpertTensor(b, 0, v[0].nbytes, t) for b, v, t in zip(bufs, (gate, up, down), types)]
-    assert dev.L.sepia_hip_set_option(b"flow", 1) == 1
     try:
         for k in range(2):
             x = synth.normal_vector(rng, hidden)
-            y = run_expert_ffn(dev, tensors, n_e, e, hidden, inter, x)
+            with Launches(dev) as n:
+                y = run_expert_ffn(dev, tensors, n_e, e, hidden, inter, x)
+                assert n.count("sepia_mq_gateup") == 1 and n.count("sepia_mq_down") == 1
             want = orc.expert_ffn(tg, gate[e], tu, up[e], td, down[e], hidden, inter, x, threads=THREADS)
-            assert_close(y, want, what="flow expert ffn %dx%d run %d" % (hidden, inter, k), gate=False)
+            assert_close(y, want, what="expert ffn %dx%d run %d" % (hidden, inter, k), gate=False)
     finally:
-        dev.L.sepia_hip_set_option(b"flow", 0)
         for b in bufs:
             dev.free(b)

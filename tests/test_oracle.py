@@ -65,7 +65,7 @@ def test_sqlx_bitwise(orc):
 
 def test_f16_all_patterns(orc):
     """Every binary16 pattern: numpy's exact conversion for non-NaN values; NaNs keep
-    sign and payload with no quieting (src/quants.c:90-91)."""
+    sign and payload with no quieting (src/quants.c:71-72)."""
     bits = np.arange(65536, dtype=np.uint16)
     raw = bits.view(np.uint8)
     got = orc.dequantize(orc.F16, raw, 65536).view(np.uint32)
