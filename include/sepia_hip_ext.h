@@ -56,6 +56,21 @@ typedef struct {
 int sepia_gpu_moe_decode(const SepiaMoeLayerDesc *layer, SepiaGpuBuf *x, SepiaGpuBuf *y,
                          SepiaGpuBuf *route_out);
 
+/* sepia_gpu_moe_decode with no allocation. No counterpart in the
+ * reference: it is for callers that cannot allocate device memory -- code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc. Every scratch byte (router logits, selection, h, per-slot
+ * partial rows, arrival counters) lives in one fixed array of 4 MiB per
+ * device, part of the library's own device code; a C3 layer (hidden 6144,
+ * inter 3072, 8 slots) needs about 0.36 MiB of it. A layer that needs more
+ * is rejected (0 and a log line) before anything is queued. The caller
+ * still passes inputs and outputs. The array keeps the last call's contents
+ * and the call clears the counters it needs itself; calls that overlap on
+ * one device (another stream, another thread) race on it. Results are those
+ * of sepia_gpu_moe_decode, bit for bit. */
+int sepia_hip_moe_decode_noalloc(const SepiaMoeLayerDesc *layer, SepiaGpuBuf *x, SepiaGpuBuf *y,
+                                 SepiaGpuBuf *route_out);
+
 /* The same layer for n_tokens tokens at once (prefill; reference
  * src/sepia.c:1377-1470 applied to each token): y[t] = MoE(x[t]) with each
  * token's routing exactly as sepia_gpu_moe_decode's up to the summation

@@ -108,6 +108,11 @@ extern "C" __global__ __launch_bounds__(256) void sepia_copy_f32(
     if (i < n) out[i] = in[i];
 }
 
+extern "C" __global__ __launch_bounds__(256) void sepia_fill_u32(uint32_t *p, int64_t n, uint32_t v) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = v;
+}
+
 extern "C" __global__ __launch_bounds__(256) void sepia_touch_f32(float *x, int64_t n) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) x[i] += 0.0f;

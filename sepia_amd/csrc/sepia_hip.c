@@ -19,6 +19,7 @@
 
 #include "../../include/sepia_gpu.h"
 #include "../../include/sepia_hip_ext.h"
+#include "noalloc.h"
 
 #include <dlfcn.h>
 #include <stdarg.h>
@@ -61,6 +62,8 @@ enum {
     K_PF_GATEUP_R, K_PF_DOWN_R,
     /* prefill router logits on the f32 matrix cores (kernels/prefill.h) */
     K_PF_ROUTE_M,
+    /* u32 fill (counter words of caller-provided scratch) */
+    K_FILL_U32,
     K_COUNT
 };
 #define FFN_NAMES(p) "sepia_ffn_gateup_" p, "sepia_ffn_gateup_" p "_xp", "sepia_ffn_down_" p
@@ -83,7 +86,7 @@ static const char *const k_names[K_COUNT] = {
     "sepia_mq_mv_q2_k", "sepia_mq_mv_q3_k", "sepia_mq_mv_q4_k", "sepia_mq_mv_iq2_xs", "sepia_mq_mv_iq3_xxs",
     "sepia_mq_gateup", "sepia_mq_down",
     "sepia_pf_route", "sepia_pf_select", "sepia_pf_group", "sepia_pf_gateup", "sepia_pf_down", "sepia_pf_combine",
-    "sepia_pf_split", "sepia_pf_gateup_r", "sepia_pf_down_r", "sepia_pf_route_m",
+    "sepia_pf_split", "sepia_pf_gateup_r", "sepia_pf_down_r", "sepia_pf_route_m", "sepia_fill_u32",
 };
 #undef FFN_NAMES
 
@@ -168,6 +171,7 @@ static int g_available;
 static size_t g_lds_max = 65536;    /* per-workgroup LDS limit, from the device at init */
 static int g_cus = 0;               /* compute units, from the device at init */
 static int g_have_iq2xxs;
+static int g_noalloc_ok;            /* the allocation-free entry's device array is set up */
 static char g_device_name[256];
 static hipModule_t g_module;
 static hipStream_t g_stream;
@@ -519,6 +523,10 @@ int sepia_gpu_init(const char *kernel_dir) {
             return 0;
         }
     }
+    /* the allocation-free decode entry's array: its device address, once,
+     * with this device current */
+    g_noalloc_ok = sepia_noalloc_setup();
+    if (!g_noalloc_ok) LOG("init: the device array of sepia_hip_moe_decode_noalloc is unavailable");
     if (prop.name[0])
         snprintf(g_device_name, sizeof g_device_name, "%s", prop.name);
     else
@@ -1578,11 +1586,12 @@ int sepia_gpu_moe_prefill(const SepiaMoeLayerDesc *L, int64_t n_tokens, SepiaGpu
  * shared experts. One slot without weights stores y; several slots add
  * sel_w[s] * their output into y. Uses the matrix-core kernels when the
  * formats and shapes fit, else the tile kernels, else the generic
- * one-wave-per-row kernels. scr: scratch for the slots' f32 h vectors. */
+ * one-wave-per-row kernels. scr: scratch for the slots' f32 h vectors and
+ * partial rows; cnt_region: the counter words (zero on entry, left zero). */
 static int ffn_launch(const char *op, const MoeProj *g, const MoeProj *u, const MoeProj *d, const MoeProj *sg,
                       const MoeProj *su, const MoeProj *sd, const int32_t *sel_idx, const float *sel_w, int32_t fixed,
                       int32_t topk, int32_t n_shared, int64_t H, int64_t I, const uint8_t *xdev, float *ydev,
-                      uint8_t *scr, const MqRoute *route) {
+                      uint8_t *scr, uint8_t *cnt_region, const MqRoute *route) {
     int32_t n_slots = topk + n_shared;
     int64_t inter = I, hid = H;
     MqFfnPlan pl;
@@ -1590,7 +1599,7 @@ static int ffn_launch(const char *op, const MoeProj *g, const MoeProj *u, const 
         int32_t inter32 = (int32_t)I;
         float *h = (float *)scr;
         float *ypart = (float *)(scr + (size_t)n_slots * (size_t)I * 4);
-        uint32_t *cnt = (uint32_t *)g_scratch + MQ_DN_CNT_OFF;
+        uint32_t *cnt = (uint32_t *)cnt_region + MQ_DN_CNT_OFF;
         MqRoute rt;
         memset(&rt, 0, sizeof rt);
         if (route) rt = *route;
@@ -1634,8 +1643,11 @@ static int ffn_launch(const char *op, const MoeProj *g, const MoeProj *u, const 
     return launch(K_MOE_DOWN, blocks_for(H, 4), 256, a_dn, op);
 }
 
-int sepia_gpu_moe_decode(const SepiaMoeLayerDesc *L, SepiaGpuBuf *x, SepiaGpuBuf *y, SepiaGpuBuf *route_out) {
-    const char *op = "moe_decode";
+/* The MoE decode layer on scratch from the library's growable region
+ * (fixed == NULL) or from the allocation-free entry's device array: counter
+ * words at fixed, data after CNT_BYTES, at most fixed_bytes in all. */
+static int moe_decode_impl(const char *op, const SepiaMoeLayerDesc *L, SepiaGpuBuf *x, SepiaGpuBuf *y,
+                           SepiaGpuBuf *route_out, uint8_t *fixed, size_t fixed_bytes) {
     if (!L || !x || !y || L->hidden <= 0 || L->inter <= 0 || L->n_routed < 1 || L->n_routed > 1024 ||
         L->n_shared < 0 || L->topk < 1 || L->topk > L->n_routed || L->topk + L->n_shared > 64 || !L->router_w ||
         !L->router_bias) {
@@ -1680,14 +1692,37 @@ int sepia_gpu_moe_decode(const SepiaMoeLayerDesc *L, SepiaGpuBuf *x, SepiaGpuBuf
     const size_t o_idx = o_logits + (((size_t)n_tot * 4 + 255) & ~(size_t)255);
     const size_t o_w = o_idx + 256;
     const size_t o_h = o_w + 256;
-    uint8_t *s = (uint8_t *)scratch(o_h + ffn_scratch_bytes(n_slots, I, H), op);
-    if (!s) return 0;
+    const size_t need = o_h + ffn_scratch_bytes(n_slots, I, H);
+    uint8_t *s, *cnt_region;
+    if (fixed) {
+        if (CNT_BYTES + need > fixed_bytes) {
+            LOG("%s: the layer needs %zu bytes of scratch; the allocation-free entry's device array holds %zu",
+                op, CNT_BYTES + need, fixed_bytes);
+            return 0;
+        }
+        s = fixed + CNT_BYTES;
+        cnt_region = fixed;
+    } else {
+        s = (uint8_t *)scratch(need, op);
+        if (!s) return 0;
+        cnt_region = (uint8_t *)g_scratch;
+    }
     float *logits = (float *)(s + o_logits), *sel_w = (float *)(s + o_w);
     int32_t *sel_idx = (int32_t *)(s + o_idx);
-    uint32_t *counter = (uint32_t *)g_scratch;
+    uint32_t *counter = (uint32_t *)cnt_region;
 
     if (!prep_layer(L, &g, &u, &d, &sg, &su, &sd, x, (size_t)H * 4, op)) return 0;
     if (!prep_out(y, op) || (route_out && !prep_out(route_out, op))) return 0;
+    if (fixed) {
+        /* the array keeps the last call's contents: the router's and the
+         * down launch's arrival counters must start at zero */
+        uint32_t *cw = (uint32_t *)cnt_region;
+        int64_t nw = MQ_DN_CNT_OFF + (H + 15) / 16;
+        if (nw > (int64_t)(CNT_BYTES / 4)) nw = CNT_BYTES / 4;
+        uint32_t zero = 0;
+        void *a_fill[] = { &cw, &nw, &zero };
+        if (!launch(K_FILL_U32, blocks_for(nw, 256), 256, a_fill, op)) return 0;
+    }
 
     const float *rw = (const float *)(L->router_w->dev + L->router_w_off);
     const float *rb = (const float *)(L->router_bias->dev + L->router_bias_off);
@@ -1705,7 +1740,7 @@ int sepia_gpu_moe_decode(const SepiaMoeLayerDesc *L, SepiaGpuBuf *x, SepiaGpuBuf
 
     const MqRoute rt = { logits, rb, nr, ns, rs, gsc, sel_idx, sel_w };
     if (!ffn_launch(op, &g, &u, &d, &sg, &su, &sd, sel_idx, sel_w, 0, tk, ns, H, I, x->dev, (float *)y->dev, s + o_h,
-                    in_kernel ? &rt : NULL))
+                    cnt_region, in_kernel ? &rt : NULL))
         return 0;
 
     if (route_out) {
@@ -1719,6 +1754,25 @@ int sepia_gpu_moe_decode(const SepiaMoeLayerDesc *L, SepiaGpuBuf *x, SepiaGpuBuf
         }
     }
     return 1;
+}
+
+int sepia_gpu_moe_decode(const SepiaMoeLayerDesc *L, SepiaGpuBuf *x, SepiaGpuBuf *y, SepiaGpuBuf *route_out) {
+    return moe_decode_impl("moe_decode", L, x, y, route_out, NULL, 0);
+}
+
+/* The same layer with every scratch byte in the library's fixed device
+ * array (noalloc.hip): no allocation, so it may run under stream capture or
+ * where hipMalloc is forbidden. Calls that overlap on one device race on the
+ * array. */
+int sepia_hip_moe_decode_noalloc(const SepiaMoeLayerDesc *L, SepiaGpuBuf *x, SepiaGpuBuf *y, SepiaGpuBuf *route_out) {
+    const char *op = "moe_decode_noalloc";
+    if (!need_init(op)) return 0;
+    uint8_t *arr = g_noalloc_ok ? (uint8_t *)sepia_noalloc_ptr() : NULL;
+    if (!arr) {
+        LOG("%s: the device array is not set up on this device", op);
+        return 0;
+    }
+    return moe_decode_impl(op, L, x, y, route_out, arr, SEPIA_NOALLOC_BYTES);
 }
 
 int sepia_gpu_expert_ffn(const SepiaExpertTensor *gate, const SepiaExpertTensor *up, const SepiaExpertTensor *down,
@@ -1744,5 +1798,5 @@ int sepia_gpu_expert_ffn(const SepiaExpertTensor *gate, const SepiaExpertTensor 
         !prep_in(x, op) || !prep_out(y, op))
         return 0;
     return ffn_launch(op, &g, &u, &d, &none, &none, &none, NULL, NULL, expert, 1, 0, hidden, inter, x->dev,
-                      (float *)y->dev, scr, NULL);
+                      (float *)y->dev, scr, (uint8_t *)g_scratch, NULL);
 }

@@ -74,6 +74,7 @@ PROTOTYPES = {
     "sepia_gpu_sconv_hist_roll": (_I, [_P, _P, _I64, _I64, _I64]),
     "sepia_gpu_moe_decode": (_I, [ctypes.POINTER(MoeLayerDesc), _P, _P, _P]),
     "sepia_gpu_moe_prefill": (_I, [ctypes.POINTER(MoeLayerDesc), ctypes.c_int64, _P, _P, _P]),
+    "sepia_hip_moe_decode_noalloc": (_I, [ctypes.POINTER(MoeLayerDesc), _P, _P, _P]),
     "sepia_gpu_expert_ffn": (_I, [ctypes.POINTER(ExpertTensor), ctypes.POINTER(ExpertTensor),
                                   ctypes.POINTER(ExpertTensor), _I, _I, _I64, _I64, _P, _P]),
     "sepia_hip_profile_start": (_I, []),
