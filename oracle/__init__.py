@@ -72,6 +72,10 @@ def lib():
         L.orc_expert_ffn.argtypes = [ctypes.c_int, c_p, ctypes.c_int, c_p, ctypes.c_int, c_p,
                                      c_i64, c_i64, c_p, c_p, ctypes.c_int]
         L.orc_moe_layer.argtypes = [c_p, c_p, c_p, c_p, c_p, c_p, c_p, ctypes.c_int]
+        L.orc_rel_project.argtypes = [c_p, c_p, c_p, c_i64, c_i64, c_i64, c_i64]
+        L.orc_rel_project.restype = None
+        L.orc_banded_attn.argtypes = [c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_i64, c_i64, c_i64, c_i64, c_i64,
+                                      c_i64, c_i64, c_f]
         _lib = L
     return _lib
 
@@ -214,6 +218,28 @@ def moe_layer(spec, x, force_idx=None, threads=1):
     if not ok:
         raise ValueError("oracle: moe_layer failed")
     return y, logits, idx, w
+
+
+def rel_project(r_vec, rel_proj, T, H, d_rel, rel_extent):
+    r_vec = np.ascontiguousarray(r_vec, dtype=np.float32)
+    rel_proj = np.ascontiguousarray(rel_proj, dtype=np.float32)
+    out = np.empty(T * H * rel_extent, dtype=np.float32)
+    lib().orc_rel_project(_ptr(r_vec), _ptr(rel_proj), _ptr(out), T, H, d_rel, rel_extent)
+    return out
+
+
+def banded_attn(q, k, v, rel_logits, kv_lo, kv_hi, tau, T, H, Hkv, Dh, rel_extent, q_pos_base, kv_dim,
+                inv_head_dim):
+    arrs = [np.ascontiguousarray(a, dtype=np.float32) for a in (q, k, v, rel_logits, tau)]
+    lo = np.ascontiguousarray(kv_lo, dtype=np.int64)
+    hi = np.ascontiguousarray(kv_hi, dtype=np.int64)
+    out = np.empty(T * H * Dh, dtype=np.float32)
+    ok = lib().orc_banded_attn(_ptr(arrs[0]), _ptr(arrs[1]), _ptr(arrs[2]), _ptr(arrs[3]), _ptr(out), _ptr(lo),
+                               _ptr(hi), _ptr(arrs[4]), T, H, Hkv, Dh, rel_extent, q_pos_base, kv_dim,
+                               ctypes.c_float(inv_head_dim))
+    if not ok:
+        raise ValueError("oracle: banded_attn rejected its arguments")
+    return out
 
 
 # ---------------------------------------------------------------- reference

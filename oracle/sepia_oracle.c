@@ -562,3 +562,80 @@ int orc_moe_layer(const OrcMoeLayer *L, const float *x, float *y, const int *for
     free(u);
     return ok;
 }
+
+/* ---------------------------------------------------------- attention ---- */
+/* rel_logits[t,h,r] = sum_d r_vec[t,h,d] * rel_proj[d,r]: the dense
+ * relative-position projection of attn_forward_chunk (src/sepia.c:1203-1209,
+ * inside its per-(t,h) body from :1077), accumulated in double and rounded
+ * to float as there. */
+void orc_rel_project(const float *r_vec, const float *rel_proj, float *rel_logits, int64_t T, int64_t H,
+                     int64_t d_rel, int64_t rel_extent) {
+    for (int64_t th = 0; th < T * H; th++) {
+        const float *rv = r_vec + (size_t)th * (size_t)d_rel;
+        for (int64_t r = 0; r < rel_extent; r++) {
+            double acc = 0.0;
+            for (int64_t d = 0; d < d_rel; d++) acc += (double)rv[d] * (double)rel_proj[(size_t)d * (size_t)rel_extent + r];
+            rel_logits[(size_t)th * (size_t)rel_extent + r] = (float)acc;
+        }
+    }
+}
+
+/* The per-(t,h) banded attention of attn_forward_chunk (src/sepia.c:1211-1247) in the
+ * split the GPU ABI takes (src/sepia_gpu.h, sepia_gpu_banded_attn): q is
+ * already tau-scaled by the caller, tau scales the band bias only. For query
+ * token t at q_pos = q_pos_base + t and kv in [kv_lo[t], kv_hi[t]]:
+ * content = (double)dot_f32(q, k) * inv_head_dim (the reference's dotf, a
+ * double sum rounded to float), bias = dist < rel_extent ?
+ * (double)rel_logits[dist] * tau : 0 (dist = q_pos - kv), score =
+ * (float)(content + bias); softmax with exp in double over (score - max)
+ * and a double sum; out = sum of (double)p / sum * v in double, rounded to
+ * float. GQA: head h reads kv head h / (H / Hkv). Returns 0 on a bound
+ * that leaves [0, q_pos]. */
+int orc_banded_attn(const float *q, const float *k, const float *v, const float *rel_logits, float *out,
+                    const int64_t *kv_lo, const int64_t *kv_hi, const float *tau, int64_t T, int64_t H, int64_t Hkv,
+                    int64_t Dh, int64_t rel_extent, int64_t q_pos_base, int64_t kv_dim, float inv_head_dim) {
+    if (T < 1 || H < 1 || Hkv < 1 || H % Hkv || Dh < 1) return 0;
+    const int64_t group = H / Hkv;
+    for (int64_t t = 0; t < T; t++) {
+        const int64_t q_pos = q_pos_base + t, lo = kv_lo[t], hi = kv_hi[t];
+        if (lo < 0 || hi < lo || hi > q_pos) return 0;
+        const int64_t n = hi - lo + 1;
+        float *sc = (float *)malloc((size_t)n * sizeof(float));
+        double *acc = (double *)malloc((size_t)Dh * sizeof(double));
+        if (!sc || !acc) { free(sc); free(acc); return 0; }
+        for (int64_t h = 0; h < H; h++) {
+            const int64_t hk = h / group;
+            const float *qv = q + (size_t)(t * H + h) * (size_t)Dh;
+            const float *rl = rel_logits + (size_t)(t * H + h) * (size_t)rel_extent;
+            float mx = -INFINITY;
+            for (int64_t kv = lo; kv <= hi; kv++) {
+                const float *kr = k + (size_t)kv * (size_t)kv_dim + (size_t)hk * (size_t)Dh;
+                double dot = 0.0;
+                for (int64_t d = 0; d < Dh; d++) dot += (double)qv[d] * (double)kr[d];
+                const double content = (double)(float)dot * (double)inv_head_dim;
+                const int64_t dist = q_pos - kv;
+                const double bias = dist < rel_extent ? (double)rl[dist] * (double)tau[t] : 0.0;
+                const float s = (float)(content + bias);
+                sc[kv - lo] = s;
+                if (s > mx) mx = s;
+            }
+            double sum = 0.0;
+            for (int64_t i = 0; i < n; i++) {
+                const double e = exp((double)(sc[i] - mx));
+                sc[i] = (float)e;
+                sum += e;
+            }
+            for (int64_t d = 0; d < Dh; d++) acc[d] = 0.0;
+            for (int64_t i = 0; i < n; i++) {
+                const double wgt = (double)sc[i] / sum;
+                const float *vr = v + (size_t)(lo + i) * (size_t)kv_dim + (size_t)hk * (size_t)Dh;
+                for (int64_t d = 0; d < Dh; d++) acc[d] += wgt * (double)vr[d];
+            }
+            float *o = out + (size_t)(t * H + h) * (size_t)Dh;
+            for (int64_t d = 0; d < Dh; d++) o[d] = (float)acc[d];
+        }
+        free(sc);
+        free(acc);
+    }
+    return 1;
+}

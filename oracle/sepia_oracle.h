@@ -85,4 +85,12 @@ typedef struct {
 int orc_moe_layer(const OrcMoeLayer *L, const float *x, float *y, const int *force_idx,
                   float *logits_out, int *idx_out, float *w_out, int threads);
 
+/* Attention (src/sepia.c attn_forward_chunk, in the split of the GPU ABI
+ * src/sepia_gpu.h sepia_gpu_rel_project / sepia_gpu_banded_attn). */
+void orc_rel_project(const float *r_vec, const float *rel_proj, float *rel_logits, int64_t T, int64_t H,
+                     int64_t d_rel, int64_t rel_extent);
+int orc_banded_attn(const float *q, const float *k, const float *v, const float *rel_logits, float *out,
+                    const int64_t *kv_lo, const int64_t *kv_hi, const float *tau, int64_t T, int64_t H, int64_t Hkv,
+                    int64_t Dh, int64_t rel_extent, int64_t q_pos_base, int64_t kv_dim, float inv_head_dim);
+
 #endif

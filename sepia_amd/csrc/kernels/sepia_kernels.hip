@@ -230,6 +230,7 @@ SEPIA_FFN_PAIR(4, 4, ST_Q4_K, ST_Q4_K)
 #include "moe.h"
 #include "prefill.h"
 #include "synth.h"
+#include "attn.h"
 
 // ------------------------------------------------------------------------
 // Matrix-core quantized matvecs and expert FFN (mq.h).

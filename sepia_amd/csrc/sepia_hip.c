@@ -64,6 +64,8 @@ enum {
     K_PF_ROUTE_M,
     /* u32 fill (counter words of caller-provided scratch) */
     K_FILL_U32,
+    /* attention (kernels/attn.h): relative-position projection, banded attention partials and fold */
+    K_REL_PROJECT, K_ATTN_PARTIAL, K_ATTN_COMBINE,
     K_COUNT
 };
 #define FFN_NAMES(p) "sepia_ffn_gateup_" p, "sepia_ffn_gateup_" p "_xp", "sepia_ffn_down_" p
@@ -87,6 +89,7 @@ static const char *const k_names[K_COUNT] = {
     "sepia_mq_gateup", "sepia_mq_down",
     "sepia_pf_route", "sepia_pf_select", "sepia_pf_group", "sepia_pf_gateup", "sepia_pf_down", "sepia_pf_combine",
     "sepia_pf_split", "sepia_pf_gateup_r", "sepia_pf_down_r", "sepia_pf_route_m", "sepia_fill_u32",
+    "sepia_rel_project_f32", "sepia_attn_partial", "sepia_attn_combine",
 };
 #undef FFN_NAMES
 
@@ -620,25 +623,30 @@ extern hipError_t hipExtModuleLaunchKernel(hipFunction_t f, uint32_t globalWorkS
                                            hipStream_t hStream, void **kernelParams, void **extra,
                                            hipEvent_t startEvent, hipEvent_t stopEvent, uint32_t flags);
 
-/* Launch of kernel k on a gx x gy grid of `block`-thread workgroups with
- * `lds` bytes of dynamic LDS (timed when the profiler is on). */
-static int launch2(int k, unsigned gx, unsigned gy, unsigned block, size_t lds, void **args, const char *op) {
-    if (gx == 0 || gy == 0) return 1;
+/* Launch of kernel k on a gx x gy x gz grid of `block`-thread workgroups
+ * with `lds` bytes of dynamic LDS (timed when the profiler is on). */
+static int launch3(int k, unsigned gx, unsigned gy, unsigned gz, unsigned block, size_t lds, void **args,
+                   const char *op) {
+    if (gx == 0 || gy == 0 || gz == 0) return 1;
     hipError_t e;
     if (g_prof_on && g_prof_n < g_prof_ev_made) {
         const int slot = g_prof_n++;
         g_prof_kid[slot] = k;
-        e = hipExtModuleLaunchKernel(g_fn[k], gx * block, gy, 1, block, 1, 1, lds, g_stream, args, NULL,
+        e = hipExtModuleLaunchKernel(g_fn[k], gx * block, gy, gz, block, 1, 1, lds, g_stream, args, NULL,
                                      g_prof_ev[slot][0], g_prof_ev[slot][1], 0);
     } else {
         if (g_prof_on) g_prof_overflow = 1;
-        e = hipModuleLaunchKernel(g_fn[k], gx, gy, 1, block, 1, 1, (unsigned)lds, g_stream, args, NULL);
+        e = hipModuleLaunchKernel(g_fn[k], gx, gy, gz, block, 1, 1, (unsigned)lds, g_stream, args, NULL);
     }
     if (e != hipSuccess) {
         LOG("%s: launch of %s failed: %s", op, k_names[k], hipGetErrorString(e));
         return 0;
     }
     return 1;
+}
+
+static int launch2(int k, unsigned gx, unsigned gy, unsigned block, size_t lds, void **args, const char *op) {
+    return launch3(k, gx, gy, 1, block, lds, args, op);
 }
 
 static int launch_lds(int k, unsigned grid, unsigned block, size_t lds, void **args, const char *op) {
@@ -905,29 +913,132 @@ int sepia_gpu_sconv_hist_roll(SepiaGpuBuf *hist, SepiaGpuBuf *in, int64_t C, int
     return launch(K_SCONV_HIST, blocks_for(C, 256), 256, args, op);
 }
 
+/* ---------------------------------------------------------- attention --- */
+/* Relative-position projection (reference src/sepia_gpu.h:209, :253):
+ * rel_logits [T, H, rel_extent] = r_vec [T, H, d_rel] x rel_proj [d_rel,
+ * rel_extent], f32 (kernels/attn.h). */
+static int do_rel_project(const char *op, SepiaGpuBuf *r_vec, SepiaGpuBuf *rel_proj, size_t rp_off,
+                          SepiaGpuBuf *rel_logits, int64_t T, int64_t H, int64_t d_rel, int64_t rel_extent) {
+    if (!r_vec || !rel_proj || !rel_logits || T < 1 || H < 1 || d_rel < 1 || rel_extent < 1 ||
+        d_rel > 0x7FFFFFFF || rel_extent > 0x7FFFFFFF || (rel_extent + 255) / 256 > MAX_GRID ||
+        (T * H + 7) / 8 > 65535) {
+        LOG("%s: invalid arguments", op);
+        return 0;
+    }
+    const size_t th = (size_t)T * (size_t)H;
+    if (!f32_off_ok(rp_off, op, "rel_proj") || !chk(r_vec, 0, th * (size_t)d_rel * 4, op, "r_vec") ||
+        !chk(rel_proj, rp_off, (size_t)d_rel * (size_t)rel_extent * 4, op, "rel_proj") ||
+        !chk(rel_logits, 0, th * (size_t)rel_extent * 4, op, "rel_logits"))
+        return 0;
+    if (!need_batch(op) || !prep_in_r(r_vec, 0, th * (size_t)d_rel * 4, op) ||
+        !prep_in_r(rel_proj, rp_off, (size_t)d_rel * (size_t)rel_extent * 4, op) || !prep_out(rel_logits, op))
+        return 0;
+    const float *rp = (const float *)(rel_proj->dev + rp_off);
+    int64_t TH = (int64_t)th;
+    int32_t dr = (int32_t)d_rel, R = (int32_t)rel_extent;
+    void *args[] = { &r_vec->dev, &rp, &rel_logits->dev, &TH, &dr, &R };
+    return launch2(K_REL_PROJECT, (unsigned)((rel_extent + 255) / 256), (unsigned)((TH + 7) / 8), 256, 0, args, op);
+}
+
 int sepia_gpu_rel_project(SepiaGpuBuf *r_vec, SepiaGpuBuf *rel_proj, SepiaGpuBuf *rel_logits, int64_t T, int64_t H,
                           int64_t d_rel, int64_t rel_extent) {
-    (void)r_vec; (void)rel_proj; (void)rel_logits; (void)T; (void)H; (void)d_rel; (void)rel_extent;
-    LOG("rel_project: banded attention is not implemented by this backend");
-    return 0;
+    return do_rel_project("rel_project", r_vec, rel_proj, 0, rel_logits, T, H, d_rel, rel_extent);
 }
 
 int sepia_gpu_rel_project_off(SepiaGpuBuf *r_vec, SepiaGpuBuf *rel_proj, size_t rel_proj_off,
                               SepiaGpuBuf *rel_logits, int64_t T, int64_t H, int64_t d_rel, int64_t rel_extent) {
-    (void)r_vec; (void)rel_proj; (void)rel_proj_off; (void)rel_logits; (void)T; (void)H; (void)d_rel;
-    (void)rel_extent;
-    LOG("rel_project_off: banded attention is not implemented by this backend");
-    return 0;
+    return do_rel_project("rel_project_off", r_vec, rel_proj, rel_proj_off, rel_logits, T, H, d_rel, rel_extent);
 }
+
+/* Banded attention (reference src/sepia_gpu.h:226; CPU semantics
+ * src/sepia.c:1211-1247): per token a launch of span workgroups per kv head
+ * writes per-head partials to scratch, a second launch folds them. Tokens go
+ * ATT_TB a launch pair, their kv bounds and tau in the kernel arguments (the
+ * caller's host arrays are read here and need not outlive the call). Mirrors
+ * struct AttnTok in kernels/attn.h. */
+#define ATT_TB 64
+#define ATT_CH 128
+typedef struct {
+    int32_t lo[ATT_TB], hi[ATT_TB];
+    float tau[ATT_TB];
+} AttnTok;
 
 int sepia_gpu_banded_attn(SepiaGpuBuf *q, SepiaGpuBuf *k, SepiaGpuBuf *v, SepiaGpuBuf *rel_logits,
                           SepiaGpuBuf *attn_out, const int64_t *kv_lo, const int64_t *kv_hi, const float *tau,
                           int64_t T, int64_t H, int64_t Hkv, int64_t Dh, int64_t rel_extent, int64_t q_pos_base,
                           int64_t kv_dim, float inv_head_dim) {
-    (void)q; (void)k; (void)v; (void)rel_logits; (void)attn_out; (void)kv_lo; (void)kv_hi; (void)tau;
-    (void)T; (void)H; (void)Hkv; (void)Dh; (void)rel_extent; (void)q_pos_base; (void)kv_dim; (void)inv_head_dim;
-    LOG("banded_attn: banded attention is not implemented by this backend");
-    return 0;
+    const char *op = "banded_attn";
+    if (!q || !k || !v || !rel_logits || !attn_out || !kv_lo || !kv_hi || !tau || T < 1 || H < 1 || Hkv < 1 ||
+        H % Hkv || H / Hkv > 16 || rel_extent < 1 || rel_extent > 0x7FFFFFFF || q_pos_base < 0 ||
+        kv_dim < Hkv * Dh || H > 65535 || Hkv > 65535) {
+        LOG("%s: invalid arguments", op);
+        return 0;
+    }
+    if (Dh < 4 || Dh > 128 || Dh % 4) {
+        LOG("%s: head dim %lld not supported (a multiple of 4 up to 128)", op, (long long)Dh);
+        return 0;
+    }
+    int64_t max_hi = 0, max_n = 0;
+    for (int64_t t = 0; t < T; t++) {
+        if (kv_lo[t] < 0 || kv_hi[t] < kv_lo[t] || kv_hi[t] > q_pos_base + t || kv_hi[t] > 0x7FFFFFFF) {
+            LOG("%s: token %lld: kv range [%lld, %lld] outside [0, q_pos %lld]", op, (long long)t,
+                (long long)kv_lo[t], (long long)kv_hi[t], (long long)(q_pos_base + t));
+            return 0;
+        }
+        if (kv_hi[t] > max_hi) max_hi = kv_hi[t];
+        if (kv_hi[t] - kv_lo[t] + 1 > max_n) max_n = kv_hi[t] - kv_lo[t] + 1;
+    }
+    if (kv_dim % 4) {
+        LOG("%s: kv_dim %lld is not a multiple of 4 (k and v rows are read 16 bytes at a time)", op,
+            (long long)kv_dim);
+        return 0;
+    }
+    const size_t qb = (size_t)T * (size_t)H * (size_t)Dh * 4;
+    const size_t kvb = ((size_t)max_hi * (size_t)kv_dim + (size_t)Hkv * (size_t)Dh) * 4;
+    const size_t rlb = (size_t)T * (size_t)H * (size_t)rel_extent * 4;
+    if (!chk(q, 0, qb, op, "q") || !chk(k, 0, kvb, op, "k") || !chk(v, 0, kvb, op, "v") ||
+        !chk(rel_logits, 0, rlb, op, "rel_logits") || !chk(attn_out, 0, qb, op, "attn_out"))
+        return 0;
+    /* spans: enough workgroups to cover the CUs, each span whole steps */
+    const int64_t tb = T < ATT_TB ? T : ATT_TB;
+    int64_t nsplit = (1024 + Hkv * tb - 1) / (Hkv * tb);
+    const int64_t steps = (max_n + ATT_CH - 1) / ATT_CH;
+    if (nsplit > steps) nsplit = steps;
+    if (nsplit < 1) nsplit = 1;
+    int64_t span = ((steps + nsplit - 1) / nsplit) * ATT_CH;
+    nsplit = (max_n + span - 1) / span;
+    if (nsplit > 65535 || span > 0x7FFFFFFF) {
+        LOG("%s: kv range too long", op);
+        return 0;
+    }
+    if (!need_batch(op)) return 0;
+    const size_t part_bytes = (size_t)tb * (size_t)H * (size_t)nsplit * (size_t)(Dh + 2) * 8;
+    double *part = (double *)scratch(part_bytes, op);
+    if (!part) return 0;
+    if (!prep_in_r(q, 0, qb, op) || !prep_in_r(k, 0, kvb, op) || !prep_in_r(v, 0, kvb, op) ||
+        !prep_in_r(rel_logits, 0, rlb, op) || !prep_out(attn_out, op))
+        return 0;
+    int32_t H32 = (int32_t)H, Hkv32 = (int32_t)Hkv, Dh32 = (int32_t)Dh, R32 = (int32_t)rel_extent;
+    int32_t ns32 = (int32_t)nsplit, span32 = (int32_t)span;
+    int64_t qpb = q_pos_base, kvd = kv_dim;
+    float ihd = inv_head_dim;
+    for (int64_t t0 = 0; t0 < T; t0 += ATT_TB) {
+        const int64_t nt = T - t0 < ATT_TB ? T - t0 : ATT_TB;
+        AttnTok tok;
+        memset(&tok, 0, sizeof tok);
+        for (int64_t i = 0; i < nt; i++) {
+            tok.lo[i] = (int32_t)kv_lo[t0 + i];
+            tok.hi[i] = (int32_t)kv_hi[t0 + i];
+            tok.tau[i] = tau[t0 + i];
+        }
+        int32_t t032 = (int32_t)t0;
+        void *a_p[] = { &q->dev, &k->dev, &v->dev, &rel_logits->dev, &tok, &t032, &H32, &Hkv32, &Dh32, &R32, &qpb,
+                        &kvd, &ihd, &ns32, &span32, &part };
+        if (!launch3(K_ATTN_PARTIAL, (unsigned)nsplit, (unsigned)Hkv, (unsigned)nt, 256, 0, a_p, op)) return 0;
+        void *a_c[] = { &part, &tok, &t032, &H32, &Dh32, &ns32, &span32, &attn_out->dev };
+        if (!launch2(K_ATTN_COMBINE, (unsigned)H, (unsigned)nt, 128, 0, a_c, op)) return 0;
+    }
+    return 1;
 }
 
 int sepia_gpu_selftest_touch(SepiaGpuBuf *buf, size_t n_floats) {

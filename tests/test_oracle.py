@@ -328,3 +328,80 @@ def test_moe_layer_vs_transformers_inkling(orc):
         assert np.array_equal(np.sort(idx), d["idx"][t])
         want = d["y"][t]
         assert np.max(np.abs(y - want)) <= 2e-6 * np.max(np.abs(want))
+
+
+# ------------------------------------------------------------------ attention
+def test_rel_project_is_a_matrix_product(orc):
+    """rel_logits = r_vec @ rel_proj per (t, h) row: against numpy's float64 product."""
+    rng = np.random.default_rng(11)
+    T, H, d_rel, R = 3, 5, 16, 40
+    rv = rng.standard_normal((T, H, d_rel)).astype(np.float32)
+    rp = rng.standard_normal((d_rel, R)).astype(np.float32)
+    got = orc.rel_project(rv, rp, T, H, d_rel, R).reshape(T, H, R)
+    want = rv.reshape(T * H, d_rel).astype(np.float64) @ rp.astype(np.float64)
+    assert np.allclose(got, want.reshape(T, H, R), rtol=1e-6, atol=1e-6)
+
+
+def _attn_case(rng, T, H, Hkv, Dh, R, cap):
+    q = rng.standard_normal((T, H, Dh)).astype(np.float32)
+    k = rng.standard_normal((cap, Hkv, Dh)).astype(np.float32)
+    v = rng.standard_normal((cap, Hkv, Dh)).astype(np.float32)
+    rl = rng.standard_normal((T, H, R)).astype(np.float32)
+    return q, k, v, rl
+
+
+def test_banded_attn_single_key_returns_its_value(orc):
+    """One kv position: the softmax weight is exactly 1, so the output is that v row."""
+    rng = np.random.default_rng(12)
+    T, H, Hkv, Dh, R = 2, 4, 2, 8, 6
+    q, k, v, rl = _attn_case(rng, T, H, Hkv, Dh, R, 10)
+    lo, hi = [3, 9], [3, 9]
+    out = orc.banded_attn(q, k, v, rl, lo, hi, np.ones(T, np.float32), T, H, Hkv, Dh, R, 9, Hkv * Dh, 1 / Dh)
+    out = out.reshape(T, H, Dh)
+    for t, kv in enumerate(lo):
+        for h in range(H):
+            assert np.array_equal(out[t, h], v[kv, h // (H // Hkv)])
+
+
+def test_banded_attn_equal_scores_average_v(orc):
+    """Equal keys and a band bias of zero give equal weights: the output is the
+    mean of the window's v rows (GQA: heads of a group read the same kv head)."""
+    rng = np.random.default_rng(13)
+    T, H, Hkv, Dh, R, cap = 1, 4, 2, 8, 4, 12
+    q, k, v, rl = _attn_case(rng, T, H, Hkv, Dh, R, cap)
+    k[:] = k[0]
+    rl[:] = 0.0
+    out = orc.banded_attn(q, k, v, rl, [2], [11], np.ones(1, np.float32), T, H, Hkv, Dh, R, 11, Hkv * Dh, 1 / Dh)
+    out = out.reshape(H, Dh)
+    for h in range(H):
+        assert np.allclose(out[h], v[2:12, h // 2].astype(np.float64).mean(axis=0), rtol=1e-6, atol=1e-6)
+
+
+def test_banded_attn_brute_force(orc):
+    """Small cases against a float64 softmax written with numpy, covering the
+    band cut-off (dist >= rel_extent gets no bias), tau on the bias only,
+    sliding windows and GQA."""
+    rng = np.random.default_rng(14)
+    T, H, Hkv, Dh, R = 3, 6, 3, 8, 5
+    qpb, cap = 7, 10
+    q, k, v, rl = _attn_case(rng, T, H, Hkv, Dh, R, cap)
+    lo, hi, tau = [0, 4, 2], [7, 8, 9], np.array([1.0, 1.3, 0.7], np.float32)
+    got = orc.banded_attn(q, k, v, rl, lo, hi, tau, T, H, Hkv, Dh, R, qpb, Hkv * Dh, 1 / Dh).reshape(T, H, Dh)
+    for t in range(T):
+        q_pos = qpb + t
+        for h in range(H):
+            hk = h // (H // Hkv)
+            kvs = np.arange(lo[t], hi[t] + 1)
+            dist = q_pos - kvs
+            bias = np.where(dist < R, rl[t, h, np.minimum(dist, R - 1)].astype(np.float64) * tau[t], 0.0)
+            s = (k[kvs, hk].astype(np.float64) @ q[t, h].astype(np.float64)) / Dh + bias
+            p = np.exp(s - s.max())
+            want = (p / p.sum()) @ v[kvs, hk].astype(np.float64)
+            assert np.allclose(got[t, h], want, rtol=1e-5, atol=1e-6), (t, h)
+
+
+def test_banded_attn_rejects_kv_past_query(orc):
+    rng = np.random.default_rng(15)
+    q, k, v, rl = _attn_case(rng, 1, 2, 1, 4, 3, 6)
+    with pytest.raises(ValueError):
+        orc.banded_attn(q, k, v, rl, [0], [5], np.ones(1, np.float32), 1, 2, 1, 4, 3, 4, 4, 0.25)

@@ -10,7 +10,12 @@ weight-free and run here:
   --metal --gpu-quants F...  bitwise GPU dequant against the SQFX fixtures'
                              expected floats, then matvec_q against the
                              reference's CPU qlinear at its relative-error
-                             gate (src/sepia.c:5903-6061).
+                             gate (src/sepia.c:5903-6061);
+  --metal --gpu-compare-attn the attention path (f32 matvec, sconv, rmsnorm,
+                             rel_project, banded_attn) at the model's sliding
+                             and global geometries against its CPU
+                             attn_forward_chunk, kv ranges up to 130000
+                             (src/sepia.c:4900-5200, :5217-5326).
 
 The CPU tests check that the binary resolves every GPU symbol it calls in
 this library and that it fails cleanly when no GPU initialises.
@@ -76,3 +81,14 @@ def test_reference_gpu_quants_gate():
     # the seven quantized types the reference has GPU kernels for, dequant and matvec each
     assert len(dq) == 7 and all(ln.rstrip().endswith("ok") for ln in dq), dq
     assert len(mv) == 7 and all(ln.rstrip().endswith("ok") for ln in mv), mv
+
+
+@needs_bin
+@pytest.mark.gpu
+def test_reference_gpu_compare_attn_gate():
+    r = run("--metal", "--gpu-compare-attn", timeout=600)
+    assert r.returncode == 0, (r.stdout, r.stderr)
+    assert "gpu compare attn ok" in r.stdout, r.stdout
+    cases = [ln for ln in r.stdout.splitlines() if ln.startswith("gpu-compare-attn: ") and "max_rel_err" in ln
+             and "worst case" not in ln]
+    assert len(cases) == 7 and all(ln.rstrip().endswith("ok") for ln in cases), cases
