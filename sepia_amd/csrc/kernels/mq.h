@@ -903,8 +903,11 @@ struct MqItem {
 // last conv waves of the workgroup DMA the vector straight into its XQ
 // place and convert it there while the others stream and decode their
 // first step; xraw is then the LDS offset of 16 bytes of control words.
+// nw: the stepping waves (C x P); a launch may run more waves than that
+// (its other kind of workgroup needs more), which then take no items and no
+// ring.
 struct MqGeo {
-    int32_t P, ring, xraw, orings, conv;
+    int32_t P, ring, xraw, orings, conv, nw;
 };
 
 // The pipeline of one wave over n_items items of format T, in two halves:
@@ -1154,8 +1157,7 @@ __device__ __forceinline__ void mq_mv(const uint8_t *__restrict__ W, uint64_t ro
         it.red = i;
         return it;
     };
-    MqWave<T, decltype(item_of)> wv(item_of, nk, nb >> 2, n, (uint32_t)row_bytes, geo, rings, 0,
-                                    (int)(blockDim.x >> 6) - geo.conv);
+    MqWave<T, decltype(item_of)> wv(item_of, nk, nb >> 2, n, (uint32_t)row_bytes, geo, rings, 0, geo.nw);
     wv.tab = tab;
     wv.go(x, geo, smem, xoff, red);   // its first barrier also publishes the codebook
     __syncthreads();
@@ -1214,8 +1216,7 @@ __device__ __forceinline__ void mq_gateup_slot(const uint8_t *Wg, const uint8_t 
         it.red = i;
         return it;
     };
-    MqWave<T, decltype(item_of)> wv(item_of, 2 * nk, nb >> 2, n, (uint32_t)row_bytes, geo, rings, 0,
-                                    (int)(blockDim.x >> 6) - geo.conv);
+    MqWave<T, decltype(item_of)> wv(item_of, 2 * nk, nb >> 2, n, (uint32_t)row_bytes, geo, rings, 0, geo.nw);
     wv.x_issued = x_issued;
     wv.template go<false>(x, geo, smem, xoff, red);
     __syncthreads();
@@ -1239,21 +1240,22 @@ struct MqRoute {
     float *w_out;
 };
 
-// grid = topk * wps_r + n_shared * wps_s: the first topk * wps_r workgroups
-// serve the routed slots, wps_r each (workgroup k: slot k / wps_r, row
-// groups k % wps_r, + wps_r, ...), the rest the shared slots, wps_s each.
-// Routed slots take their expert from the selection, sel_idx or fixed +
-// slot; shared slot topk + i is shared expert i. h is [n_slots][inter] f32,
-// or with hxq each slot's XQ form (the same 4 inter bytes), which the down
-// launch then only DMAs into place.
+// Workgroups [0, topk * wps_r) serve the routed slots, wps_r each
+// (workgroup k: slot k / wps_r, row groups k % wps_r, + wps_r, ...), the
+// next n_shared * wps_s the shared slots, wps_s each; bid is the
+// workgroup's index among them. Routed slots take their expert from the
+// selection, sel_idx or fixed + slot; shared slot topk + i is shared expert
+// i. h is [n_slots][inter] f32. Each kind has its own geometry (geo_r,
+// geo_s), planned for its format, so the rings of routed workgroups hold
+// steps of the routed format, not of the larger shared one.
 __device__ __forceinline__ void mq_gateup(const MqProj &gate, const MqProj &up, const MqProj &s_gate,
                                           const MqProj &s_up, const int32_t *__restrict__ sel_idx, int32_t fixed,
                                           int32_t topk, int32_t inter, int32_t wps_r, int32_t wps_s,
-                                          const float *__restrict__ x, float *__restrict__ h, MqGeo geo,
-                                          const MqRoute &rt) {
+                                          const float *__restrict__ x, float *__restrict__ h, const MqGeo &geo_r,
+                                          const MqGeo &geo_s, const MqRoute &rt, int32_t bid) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    const int32_t bid = (int32_t)blockIdx.x;
     const bool rk = bid < topk * wps_r;
+    const MqGeo geo = rk ? geo_r : geo_s;
     const int32_t wps = rk ? wps_r : wps_s;
     const int32_t k0 = rk ? bid : bid - topk * wps_r;
     const int32_t slot = (rk ? 0 : topk) + k0 / wps, j0 = k0 % wps;
@@ -1272,7 +1274,7 @@ __device__ __forceinline__ void mq_gateup(const MqProj &gate, const MqProj &up, 
             route_pick_any<false>(rt.logits, rt.bias, rt.n_routed, rt.n_shared, topk, rt.route_scale,
                                   rt.global_scale, si, sw);
         __syncthreads();
-        if (blockIdx.x == 0 && threadIdx.x < topk + rt.n_shared) {
+        if (bid == 0 && threadIdx.x < topk + rt.n_shared) {
             if ((int)threadIdx.x < topk) rt.idx_out[threadIdx.x] = si[threadIdx.x];
             rt.w_out[threadIdx.x] = sw[threadIdx.x];
         }
@@ -1296,21 +1298,24 @@ __device__ __forceinline__ void mq_gateup(const MqProj &gate, const MqProj &up, 
     extern "C" __global__ __launch_bounds__(1024) void sepia_mq_gateup(                                  \
         MqProj gate, MqProj up, MqProj s_gate, MqProj s_up, const int32_t *__restrict__ sel_idx,         \
         int32_t fixed, int32_t topk, int32_t inter, int32_t wps_r, int32_t wps_s,                        \
-        const float *__restrict__ x, float *__restrict__ h, MqGeo geo, MqRoute rt) {                      \
-        mq_gateup(gate, up, s_gate, s_up, sel_idx, fixed, topk, inter, wps_r, wps_s, x, h, geo, rt);      \
+        const float *__restrict__ x, float *__restrict__ h, MqGeo geo_r, MqGeo geo_s, MqRoute rt) {      \
+        mq_gateup(gate, up, s_gate, s_up, sel_idx, fixed, topk, inter, wps_r, wps_s, x, h, geo_r, geo_s, \
+                  rt, (int32_t)blockIdx.x);                                                              \
     }
 
 // Down, one slot per workgroup: workgroups [0, topk * wps_r) serve the
-// routed slots (wps_r each), the rest the shared slots (wps_s each). A
-// workgroup owns row groups j0, j0 + jstep, ... of y for its slot (one item
-// each) and stages only its slot's h as XQ. With a single slot (the expert
-// FFN) it stores w * its rows into y. With several it publishes its rows to
-// ypart[slot] (agent-scope stores, waited for), then bumps each of its row
-// groups' arrival counters; the workgroup that completes a row group adds
-// the n_slots partial rows in slot order, weighted by sel_w (routed weights,
-// then the shared gammas; the shared gamma scales the down output as
-// src/sepia.c:3953-3957 does), into y and puts the counter back to zero --
-// deterministic whatever the arrival order.
+// routed slots (wps_r each), the next ones the shared slots (wps_s each);
+// bid is the workgroup's index among them. A workgroup owns row groups j0,
+// j0 + jstep, ... of y for its slot (one item each) and stages only its
+// slot's h as XQ. With a single slot (the expert FFN) it stores w * its rows
+// into y. Otherwise it publishes its rows to ypart[slot] (agent-scope
+// stores, waited for); with n_count > 0 it then bumps each of its row
+// groups' arrival counters, and the workgroup whose arrival is the
+// n_count-th adds the n_sum partial rows in slot order, weighted by sel_w
+// (routed weights, then the shared gammas; the shared gamma scales the down
+// output as src/sepia.c:3953-3957 does), into y and puts the counter back to
+// zero -- deterministic whatever the arrival order. n_count < n_sum: the
+// other slots' partial rows were published by an earlier launch.
 // LDS: [zero][XQ of h_slot][red: nk x P x 16 f32][flags: nk i32][raw h][rings].
 template <int T>
 __device__ __forceinline__ void mq_dn_slot(const uint8_t *Wd, uint64_t row_bytes, int32_t nb, int32_t inter,
@@ -1326,20 +1331,19 @@ __device__ __forceinline__ void mq_dn_slot(const uint8_t *Wd, uint64_t row_bytes
         it.red = i;
         return it;
     };
-    MqWave<T, decltype(item_of)> wv(item_of, nk, nb >> 2, inter, (uint32_t)row_bytes, geo, rings, 0,
-                                    (int)(blockDim.x >> 6) - geo.conv);
+    MqWave<T, decltype(item_of)> wv(item_of, nk, nb >> 2, inter, (uint32_t)row_bytes, geo, rings, 0, geo.nw);
     wv.template go<false>(hs, geo, lds0, MQ_ZERO, red);
 }
 
 __device__ __forceinline__ void mq_down(const MqProj &down, const MqProj &s_down, const int32_t *__restrict__ sel_idx,
                                         const float *__restrict__ sel_w, int32_t fixed, int32_t topk,
-                                        int32_t n_shared, int32_t inter, int64_t hidden, const float *__restrict__ h,
-                                        float *__restrict__ y, MqGeo geo, int32_t wps_r, int32_t wps_s,
-                                        float *__restrict__ ypart, uint32_t *__restrict__ cnt) {
+                                        int32_t n_count, int32_t n_sum, int32_t inter, int64_t hidden,
+                                        const float *__restrict__ h, float *__restrict__ y, const MqGeo &geo_r,
+                                        const MqGeo &geo_s, int32_t wps_r, int32_t wps_s, float *__restrict__ ypart,
+                                        uint32_t *__restrict__ cnt, int32_t bid) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    const int n_slots = topk + n_shared;
-    const int32_t bid = (int32_t)blockIdx.x;
     const bool routed = bid < topk * wps_r;
+    const MqGeo geo = routed ? geo_r : geo_s;
     const int32_t jstep = routed ? wps_r : wps_s;
     const int32_t k0 = routed ? bid : bid - topk * wps_r;
     const int32_t slot = (routed ? 0 : topk) + k0 / jstep, j0 = k0 % jstep;
@@ -1360,7 +1364,7 @@ __device__ __forceinline__ void mq_down(const MqProj &down, const MqProj &s_down
     default: mq_dn_slot<ST_Q4_K>(Wd, Pj.row_bytes, nb, inter, hidden, j0, jstep, nk, hs, geo, red, rings, smem); break;
     }
     __syncthreads();
-    if (n_slots == 1) {
+    if (n_sum == 1) {
         const float w = sel_w ? sel_w[0] : 1.0f;
         for (int i = threadIdx.x; i < nk * 16; i += blockDim.x) {
             const int64_t r = ((int64_t)j0 + (int64_t)(i >> 4) * jstep) * 16 + (i & 15);
@@ -1374,12 +1378,13 @@ __device__ __forceinline__ void mq_down(const MqProj &down, const MqProj &s_down
             __hip_atomic_store(&ypart[(int64_t)slot * hidden + r], mq_red_sum(red, i >> 4, geo.P, i & 15),
                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+    if (n_count == 0) return;
     __builtin_amdgcn_s_waitcnt(0);   // this thread's partial stores have completed
     __syncthreads();
     for (int k = threadIdx.x; k < nk; k += blockDim.x) {
         const uint32_t prev =
             __hip_atomic_fetch_add(&cnt[j0 + k * jstep], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        flag[k] = prev == (uint32_t)(n_slots - 1);
+        flag[k] = prev == (uint32_t)(n_count - 1);
     }
     __syncthreads();
     for (int i = threadIdx.x; i < nk * 16; i += blockDim.x) {
@@ -1387,7 +1392,7 @@ __device__ __forceinline__ void mq_down(const MqProj &down, const MqProj &s_down
         const int64_t r = ((int64_t)j0 + (int64_t)(i >> 4) * jstep) * 16 + (i & 15);
         if (r >= hidden) continue;
         float acc = 0.0f;
-        for (int sl = 0; sl < n_slots; sl++)
+        for (int sl = 0; sl < n_sum; sl++)
             acc = __builtin_fmaf(sel_w ? sel_w[sl] : 1.0f,
                                  __hip_atomic_load(&ypart[(int64_t)sl * hidden + r], __ATOMIC_RELAXED,
                                                    __HIP_MEMORY_SCOPE_AGENT),
@@ -1401,9 +1406,10 @@ __device__ __forceinline__ void mq_down(const MqProj &down, const MqProj &s_down
 #define SEPIA_MQ_DOWN()                                                                                  \
     extern "C" __global__ __launch_bounds__(1024) void sepia_mq_down(                                    \
         MqProj down, MqProj s_down, const int32_t *__restrict__ sel_idx, const float *__restrict__ sel_w, \
-        int32_t fixed, int32_t topk, int32_t n_shared, int32_t inter, int64_t hidden,                    \
-        const float *__restrict__ h, float *__restrict__ y, MqGeo geo, int32_t wps_r, int32_t wps_s,     \
-        float *__restrict__ ypart, uint32_t *__restrict__ cnt) {                                         \
-        mq_down(down, s_down, sel_idx, sel_w, fixed, topk, n_shared, inter, hidden, h, y, geo, wps_r,    \
-                wps_s, ypart, cnt);                                                                      \
+        int32_t fixed, int32_t topk, int32_t n_count, int32_t n_sum, int32_t inter, int64_t hidden,      \
+        const float *__restrict__ h, float *__restrict__ y, MqGeo geo_r, MqGeo geo_s, int32_t wps_r,     \
+        int32_t wps_s, float *__restrict__ ypart, uint32_t *__restrict__ cnt) {                          \
+        mq_down(down, s_down, sel_idx, sel_w, fixed, topk, n_count, n_sum, inter, hidden, h, y, geo_r,   \
+                geo_s, wps_r, wps_s, ypart, cnt, (int32_t)blockIdx.x);                                   \
     }
+

@@ -1123,7 +1123,7 @@ int sepia_hip_set_option(const char *name, int value) {
 #define MQ_CUS 256                  /* MI355X compute units */
 #define MQ_ZERO 768
 typedef struct {
-    int32_t P, ring, xraw, orings, conv;   /* as struct MqGeo in kernels/mq.h */
+    int32_t P, ring, xraw, orings, conv, nw;   /* as struct MqGeo in kernels/mq.h */
 } MqGeo;
 /* In-kernel selection by the gate/up launch (struct MqRoute in
  * kernels/mq.h); logits NULL: the experts come from sel_idx. */
@@ -1224,6 +1224,7 @@ static int mq_geo(int mc, int wmax, int64_t n_items, int64_t nq, size_t fixed, s
                     geo->xraw = mode ? (int32_t)o_raw : 0;
                     geo->orings = (int32_t)base;
                     geo->conv = cv;
+                    geo->nw = nw;
                     *threads = 64u * (unsigned)(nw + cv);
                     *lds = base + (size_t)nw * ring;
                 }
@@ -1486,7 +1487,7 @@ typedef struct {
     unsigned gu_threads, dn_threads, gu_grid, dn_grid;
     int32_t gu_wps_r, gu_wps_s, dn_wps_r, dn_wps_s;
     size_t gu_lds, dn_lds;
-    MqGeo gu_geo, dn_geo;
+    MqGeo gu_geo_r, gu_geo_s, dn_geo_r, dn_geo_s;   /* routed and shared workgroups, each for its format */
 } MqFfnPlan;
 #define MQ_DN_CNT_OFF 64            /* first down arrival counter (u32 index in the counter region) */
 static int mq_proj_ok(const MoeProj *p, int64_t rows) {
@@ -1516,6 +1517,22 @@ static void mq_split(int32_t topk, int32_t n_shared, double br, double bs, int64
     *wr = (int32_t)r;
     *ws = (int32_t)sh;
 }
+/* One launch's two geometries (routed and shared workgroups) and the
+ * launch's thread count and LDS (the larger of the two). */
+static int mq_geo2(int mc_r, int mc_s, int has_s, int64_t items_r, int64_t items_s, int64_t nq, size_t fixed_r,
+                   size_t fixed_s, size_t raw_bytes, unsigned *threads, MqGeo *geo_r, MqGeo *geo_s, size_t *lds) {
+    unsigned tr, ts = 0;
+    size_t lr, ls = 0;
+    if (!mq_geo(mc_r, k_mq_words[mc_r], items_r, nq, fixed_r, raw_bytes, 0, &tr, geo_r, &lr)) return 0;
+    if (has_s) {
+        if (!mq_geo(mc_s, k_mq_words[mc_s], items_s, nq, fixed_s, raw_bytes, 0, &ts, geo_s, &ls)) return 0;
+    } else {
+        *geo_s = *geo_r;
+    }
+    *threads = tr > ts ? tr : ts;
+    *lds = lr > ls ? lr : ls;
+    return 1;
+}
 static int mq_ffn_plan(const MoeProj *g, const MoeProj *u, const MoeProj *d, const MoeProj *sg, const MoeProj *su,
                        const MoeProj *sd, int32_t topk, int32_t n_shared, int64_t H, int64_t I, MqFfnPlan *pl) {
     if (!g_opt_mq || H % 1024 || I % 1024) return 0;
@@ -1526,25 +1543,22 @@ static int mq_ffn_plan(const MoeProj *g, const MoeProj *u, const MoeProj *d, con
     if (g->type != u->type || (n_shared > 0 && sg->type != su->type)) return 0;
     const int64_t tiles_i = (I + 15) / 16, tiles_h = (H + 15) / 16;
     if (n_shared + topk > 1 && MQ_DN_CNT_OFF + tiles_h > CNT_BYTES / 4) return 0;
-    /* both slot kinds share a geometry: planned for the format of the
-     * routed slots (the shared ones when there are none), with rings that
-     * hold a step of either */
-    const int kg = mq_code(topk > 0 ? g->type : sg->type), kd = mq_code(topk > 0 ? d->type : sd->type);
-    int wgu = k_mq_words[kg], wdn = k_mq_words[kd];
-    if (n_shared > 0 && k_mq_words[mq_code(sg->type)] > wgu) wgu = k_mq_words[mq_code(sg->type)];
-    if (n_shared > 0 && k_mq_words[mq_code(sd->type)] > wdn) wdn = k_mq_words[mq_code(sd->type)];
     mq_split(topk, n_shared, (double)g->row_bytes, n_shared > 0 ? (double)sg->row_bytes : 1.0, tiles_i,
              &pl->gu_wps_r, &pl->gu_wps_s);
     mq_split(topk, n_shared, (double)d->row_bytes, n_shared > 0 ? (double)sd->row_bytes : 1.0, tiles_h,
              &pl->dn_wps_r, &pl->dn_wps_s);
-    const int32_t gmin = pl->gu_wps_r < pl->gu_wps_s || n_shared == 0 ? pl->gu_wps_r : pl->gu_wps_s;
-    const int32_t dmin = pl->dn_wps_r < pl->dn_wps_s || n_shared == 0 ? pl->dn_wps_r : pl->dn_wps_s;
-    const int64_t nk_gu = (tiles_i + gmin - 1) / gmin, nk_dn = (tiles_h + dmin - 1) / dmin;
-    if (!mq_geo(kg, wgu, 2 * nk_gu, H / 1024, MQ_ZERO + mq_xq_bytes(H) + MQ_SEL_BYTES, (size_t)H * 4, 0,
-                &pl->gu_threads, &pl->gu_geo, &pl->gu_lds))
+    const int has_s = n_shared > 0;
+    const int kg = mq_code(g->type), kd = mq_code(d->type);
+    const int ksg = has_s ? mq_code(sg->type) : kg, ksd = has_s ? mq_code(sd->type) : kd;
+    const int64_t nk_gr = (tiles_i + pl->gu_wps_r - 1) / pl->gu_wps_r, nk_gs = (tiles_i + pl->gu_wps_s - 1) / pl->gu_wps_s;
+    const int64_t nk_dr = (tiles_h + pl->dn_wps_r - 1) / pl->dn_wps_r, nk_ds = (tiles_h + pl->dn_wps_s - 1) / pl->dn_wps_s;
+    const size_t gu_fixed = MQ_ZERO + mq_xq_bytes(H) + MQ_SEL_BYTES;
+    if (!mq_geo2(kg, ksg, has_s, 2 * nk_gr, 2 * nk_gs, H / 1024, gu_fixed, gu_fixed, (size_t)H * 4, &pl->gu_threads,
+                 &pl->gu_geo_r, &pl->gu_geo_s, &pl->gu_lds))
         return 0;
-    const size_t dn_fixed = MQ_ZERO + mq_xq_bytes(I) + (size_t)nk_dn * 4 + 256;
-    if (!mq_geo(kd, wdn, nk_dn, I / 1024, dn_fixed, (size_t)I * 4, 0, &pl->dn_threads, &pl->dn_geo, &pl->dn_lds))
+    if (!mq_geo2(kd, ksd, has_s, nk_dr, nk_ds, I / 1024, MQ_ZERO + mq_xq_bytes(I) + (size_t)nk_dr * 4 + 256,
+                 MQ_ZERO + mq_xq_bytes(I) + (size_t)nk_ds * 4 + 256, (size_t)I * 4, &pl->dn_threads, &pl->dn_geo_r,
+                 &pl->dn_geo_s, &pl->dn_lds))
         return 0;
     pl->gu_grid = (unsigned)(topk * pl->gu_wps_r + n_shared * pl->gu_wps_s);
     pl->dn_grid = (unsigned)(topk * pl->dn_wps_r + n_shared * pl->dn_wps_s);
@@ -1715,10 +1729,10 @@ static int ffn_launch(const char *op, const MoeProj *g, const MoeProj *u, const 
         memset(&rt, 0, sizeof rt);
         if (route) rt = *route;
         void *a_gu[] = { (void *)g, (void *)u, (void *)sg, (void *)su, &sel_idx, &fixed, &topk, &inter32,
-                         &pl.gu_wps_r, &pl.gu_wps_s, &xdev, &h, &pl.gu_geo, &rt };
+                         &pl.gu_wps_r, &pl.gu_wps_s, &xdev, &h, &pl.gu_geo_r, &pl.gu_geo_s, &rt };
         if (!launch_lds(K_MQ_GU, pl.gu_grid, pl.gu_threads, pl.gu_lds, a_gu, op)) return 0;
-        void *a_dn[] = { (void *)d, (void *)sd, &sel_idx, &sel_w, &fixed, &topk, &n_shared, &inter32, &hid, &h, &ydev,
-                         &pl.dn_geo, &pl.dn_wps_r, &pl.dn_wps_s, &ypart, &cnt };
+        void *a_dn[] = { (void *)d, (void *)sd, &sel_idx, &sel_w, &fixed, &topk, &n_slots, &n_slots, &inter32, &hid, &h,
+                         &ydev, &pl.dn_geo_r, &pl.dn_geo_s, &pl.dn_wps_r, &pl.dn_wps_s, &ypart, &cnt };
         return launch_lds(K_MQ_DN, pl.dn_grid, pl.dn_threads, pl.dn_lds, a_dn, op);
     }
     if (route) {
@@ -1752,6 +1766,21 @@ static int ffn_launch(const char *op, const MoeProj *g, const MoeProj *u, const 
     if (!launch(K_MOE_GATEUP, (unsigned)(n_slots * ((I + 3) / 4)), 256, a_gu, op)) return 0;
     void *a_dn[] = { (void *)d, (void *)sd, &sel_idx, &sel_w, &fixed, &topk, &n_shared, &inter, &hid, &h, &ydev };
     return launch(K_MOE_DOWN, blocks_for(H, 4), 256, a_dn, op);
+}
+
+/* The selection and weights into the caller's route_out (if any). */
+static int route_copy(const char *op, SepiaGpuBuf *route_out, const int32_t *sel_idx, const float *sel_w, int topk,
+                      int n_slots) {
+    if (!route_out) return 1;
+    hipError_t e = hipMemcpyAsync(route_out->dev, sel_idx, (size_t)topk * 4, hipMemcpyDeviceToDevice, g_stream);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(route_out->dev + (size_t)topk * 4, sel_w, (size_t)n_slots * 4, hipMemcpyDeviceToDevice,
+                           g_stream);
+    if (e != hipSuccess) {
+        LOG("%s: route_out copy failed: %s", op, hipGetErrorString(e));
+        return 0;
+    }
+    return 1;
 }
 
 /* The MoE decode layer on scratch from the library's growable region
@@ -1840,6 +1869,7 @@ static int moe_decode_impl(const char *op, const SepiaMoeLayerDesc *L, SepiaGpuB
     int64_t ld = H, hid = H;
     int32_t nr = L->n_routed, ns = L->n_shared, tk = L->topk;
     float rs = L->route_scale, gsc = L->global_scale;
+    const MqRoute rt = { logits, rb, nr, ns, rs, gsc, sel_idx, sel_w };
     /* with the matrix-core FFN the gate/up launch selects from the logits;
      * otherwise the router's last workgroup does */
     MqFfnPlan pl;
@@ -1849,22 +1879,10 @@ static int moe_decode_impl(const char *op, const SepiaMoeLayerDesc *L, SepiaGpuB
                         &select };
     if (!launch(K_MOE_ROUTE, (unsigned)n_tot, 256, a_route, op)) return 0;
 
-    const MqRoute rt = { logits, rb, nr, ns, rs, gsc, sel_idx, sel_w };
     if (!ffn_launch(op, &g, &u, &d, &sg, &su, &sd, sel_idx, sel_w, 0, tk, ns, H, I, x->dev, (float *)y->dev, s + o_h,
                     cnt_region, in_kernel ? &rt : NULL))
         return 0;
-
-    if (route_out) {
-        hipError_t e = hipMemcpyAsync(route_out->dev, sel_idx, (size_t)L->topk * 4, hipMemcpyDeviceToDevice, g_stream);
-        if (e == hipSuccess)
-            e = hipMemcpyAsync(route_out->dev + (size_t)L->topk * 4, sel_w, (size_t)n_slots * 4,
-                               hipMemcpyDeviceToDevice, g_stream);
-        if (e != hipSuccess) {
-            LOG("%s: route_out copy failed: %s", op, hipGetErrorString(e));
-            return 0;
-        }
-    }
-    return 1;
+    return route_copy(op, route_out, sel_idx, sel_w, L->topk, n_slots);
 }
 
 int sepia_gpu_moe_decode(const SepiaMoeLayerDesc *L, SepiaGpuBuf *x, SepiaGpuBuf *y, SepiaGpuBuf *route_out) {

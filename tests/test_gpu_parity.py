@@ -670,7 +670,8 @@ def test_moe_decode_mq_geometries(dev, orc, mq_geometry):
                           ((10, 10, 11, 12), 16, 0, 6), ((10, 10, 11, 12), 8, 1, 1)],
                          ids=["q2k_q3k_q4k", "q4k_q4k_q2k", "q3k_q2k_q3k", "no_shared", "top1"])
 def test_moe_decode_slots(dev, orc, types, n_routed, n_shared, topk):
-    """C3 layer shapes with mixed formats, without shared experts and with a
+    """C3 layer shapes with mixed formats (routed and shared workgroups on
+    geometries of their own formats), without shared experts and with a
     single routed slot: the router and the two matrix-core FFN launches (the
     launch counts show it) give the oracle's result twice in a row (the down
     launch's arrival counters must be back at zero after the first)."""
