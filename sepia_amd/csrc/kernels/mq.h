@@ -771,6 +771,262 @@ template <> struct MQ<ST_IQ3_XXS> {
     }
 };
 
+// ------------------------------------------- Q5_K, Q6_K, IQ4_XS, Q8_0
+// Codes above 15 (Q5_K 0..31, Q6_K 0..63, IQ4_XS and Q8_0 int8): the plane
+// dots combine in f32 (mq_combine_f).
+
+// Q5_K {d@0, dmin@2, scales[12]@4, qh[32]@16, qs[128]@48} (176 bytes = 11
+// words, reference src/quants.c:127-151). As Q4_K with a fifth bit: the low
+// nibble of qs[32u + l] (sub-block 2u) adds 16 when bit 2u of qh[l] is set,
+// the high nibble (sub-block 2u + 1) with bit 2u + 1. Segment s of unit u as
+// Q4_K: s & 1 picks bytes 16..31 of the unit (and of qh), s & 2 the high
+// nibbles.
+// Words: 0 = d | dmin, scales[12]; 1, 2 = qh; 3..10 = qs.
+template <> struct MQ<ST_Q5_K> {
+    static constexpr int bytes = 176, W = 11, Wp = 11, sum_sel = 1;
+    static constexpr uint32_t table_bytes = 0;
+    static constexpr bool has_pre = false;
+    __device__ static uint32_t shift(uint32_t) { return 0u; }
+    __device__ static uint32_t word(int k) { return 16u * (uint32_t)k; }
+    __device__ static float block(const uint4 (&w)[W], uint32_t, const MqCtx &x) {
+        float acc = 0.0f, mn = 0.0f;
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            mq_v4i D[4];
+#pragma unroll
+            for (int s = 0; s < 4; s++) {
+                const uint4 q = w[3 + 2 * u + (s & 1)], qh = w[1 + (s & 1)];
+                const uint32_t sh = (s & 2) ? 4u : 0u, hb = 2u * (uint32_t)u + (uint32_t)(s >> 1);
+                const uint32_t m = 0x0F0F0F0Fu, m1 = 0x01010101u;
+                D[s] = mq_mfma(mq_a(x, 64 * u + 16 * s),
+                               mq_v4i{(int32_t)(((q.x >> sh) & m) | (((qh.x >> hb) & m1) << 4)),
+                                      (int32_t)(((q.y >> sh) & m) | (((qh.y >> hb) & m1) << 4)),
+                                      (int32_t)(((q.z >> sh) & m) | (((qh.z >> hb) & m1) << 4)),
+                                      (int32_t)(((q.w >> sh) & m) | (((qh.w >> hb) & m1) << 4))});
+            }
+            float xs[4], gv[4];
+#pragma unroll
+            for (int s = 0; s < 4; s++) {
+                xs[s] = x.xsb[4 * u + s];
+                gv[s] = x.gvb[4 * u + s];
+            }
+            float sc0, mn0, sc1, mn1;
+            MQ<ST_Q4_K>::scale_min(w[0], u, 0, sc0, mn0);
+            MQ<ST_Q4_K>::scale_min(w[0], u, 1, sc1, mn1);
+            const float sub0 = __builtin_fmaf(mq_combine_f(D[0]), xs[0], mq_combine_f(D[1]) * xs[1]);
+            const float sub1 = __builtin_fmaf(mq_combine_f(D[2]), xs[2], mq_combine_f(D[3]) * xs[3]);
+            acc += __builtin_fmaf(sc0, sub0, sc1 * sub1);
+            mn += __builtin_fmaf(mn0, gv[0] + gv[1], mn1 * (gv[2] + gv[3]));
+        }
+        return __builtin_fmaf(mq_half_lo(w[0].x), acc, -(mq_half_hi(w[0].x) * mn));
+    }
+};
+
+// Q6_K {ql[128]@0, qh[64]@128, scales[16]@192 (int8), d@208} (210 bytes,
+// reference src/quants.c:153-176). Every other block of a row starts 2 bytes
+// past a 4-byte boundary: fetched from the boundary at or below and
+// realigned as Q3_K. The last word comes from bytes 196..211 of the fetch
+// (overlapping the one before), so a fetch ends at its block's end when the
+// block is 2 bytes off (the last block of a row always is: rows hold a
+// multiple of 4 blocks) and 2 bytes after it otherwise.
+// Column 128 hf + 32 r + 16 i + t (r < 4; i < 2; t < 16) has the code
+// q = ((ql[64 hf + 32 (r & 1) + 16 i + t] >> 4 (r >> 1)) & 15) |
+// ((qh[32 hf + 16 i + t] >> 2 r) & 3) << 4 and the weight d sc (q - 32),
+// sc the int8 scale of its 16 columns: scales[col / 16]. The B operand
+// holds q (0..63); the -32 returns through the segment sum of x^ (gq), as
+// Q3_K's -4 does.
+template <> struct MQ<ST_Q6_K> {
+    static constexpr int bytes = 210, W = 14, Wp = 15, sum_sel = 2;
+    static constexpr uint32_t table_bytes = 0;
+    static constexpr bool has_pre = false;
+    __device__ static uint32_t shift(uint32_t boff) { return boff & 3u; }
+    __device__ static uint32_t word(int k) { return k < 13 ? 16u * (uint32_t)k : 196u; }
+    __device__ static float block(const uint4 (&w)[W], uint32_t sh, const MqCtx &x) {
+        uint32_t raw[54];
+#pragma unroll
+        for (int k = 0; k < 13; k++) {
+            raw[4 * k] = w[k].x;
+            raw[4 * k + 1] = w[k].y;
+            raw[4 * k + 2] = w[k].z;
+            raw[4 * k + 3] = w[k].w;
+        }
+        raw[52] = w[13].w;   // fetch bytes 208..211
+        raw[53] = 0u;
+        auto L = [&](int m) { return __builtin_amdgcn_alignbyte(raw[m + 1], raw[m], sh); };
+        float acc = 0.0f;
+        // groups (hf, i) of four segments share their qh dwords and, two by
+        // two, their ql dwords; a group's words die before the next starts
+        // (the scheduling barrier keeps the groups apart, which keeps the
+        // block within the registers of 16 waves)
+#pragma unroll
+        for (int gi = 0; gi < 4; gi++) {
+            const int hf = gi >> 1, i = gi & 1;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int sg = 8 * hf + 2 * r + i;
+                const uint32_t nsh = 4u * (uint32_t)(r >> 1), hsh = 2u * (uint32_t)r;
+                mq_v4i b;
+#pragma unroll
+                for (int t = 0; t < 4; t++) {
+                    const uint32_t ql = L(16 * hf + 8 * (r & 1) + 4 * i + t), qh = L(32 + 8 * hf + 4 * i + t);
+                    b[t] = (int32_t)(((ql >> nsh) & 0x0F0F0F0Fu) | (((qh >> hsh) & 0x03030303u) << 4));
+                }
+                const mq_v4i D = mq_mfma(mq_a(x, 16 * sg), b);
+                // the int8 scale as (byte ^ 0x80) - 128 from an unsigned byte
+                // convert: a signed byte extract feeding the convert was
+                // folded into v_cvt_f32_u32 of the sign-extended byte, which
+                // turns a negative scale into about 2^32
+                const uint32_t scb = (L(48 + (sg >> 2)) >> (8 * (sg & 3))) & 0xFFu;
+                const float sc = (float)(scb ^ 0x80u) - 128.0f;
+                acc = __builtin_fmaf(sc, __builtin_fmaf(-32.0f, x.gvb[sg], mq_combine_f(D) * x.xsb[sg]), acc);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        return mq_half_lo(L(52)) * acc;
+    }
+};
+
+// IQ4_XS {d@0, scales_h@2 (u16), scales_l[4]@4, qs[128]@8} (136 bytes,
+// reference src/quants.c:228-249): group ib of 32 columns has the 6-bit
+// scale ls = nibble ib of scales_l | (bits 2 ib, 2 ib + 1 of scales_h) << 4
+// and the codes of qs[16 ib + j]: low nibble column 32 ib + j, high nibble
+// column 32 ib + 16 + j; w = d (ls - 32) values[code] with the 16 int8
+// levels of the IQ4 non-linear table. Segment sg = 2 ib + half. Blocks are
+// 4-byte aligned; the last word comes from bytes 120..135 (overlapping the
+// one before), so the fetch ends at the block's end.
+// Four codes at a time become their levels by byte permutes: code & 7
+// selects a byte of the table's first and of its second half (two
+// v_perm_b32 over two table dwords each), and a third permute keeps the
+// first or the second by bit 3.
+__device__ __forceinline__ constexpr uint32_t mq_iq4_word(int k) {
+    constexpr int8_t v[16] = SEPIA_IQ4NL_VALUES_INIT;
+    return (uint32_t)(uint8_t)v[4 * k] | ((uint32_t)(uint8_t)v[4 * k + 1] << 8) |
+           ((uint32_t)(uint8_t)v[4 * k + 2] << 16) | ((uint32_t)(uint8_t)v[4 * k + 3] << 24);
+}
+// Levels of the four codes in the low nibbles of the bytes of c.
+__device__ __forceinline__ uint32_t mq_iq4_levels(uint32_t c) {
+    constexpr uint32_t T0 = mq_iq4_word(0), T1 = mq_iq4_word(1), T2 = mq_iq4_word(2), T3 = mq_iq4_word(3);
+    const uint32_t sel = c & 0x07070707u;
+    const uint32_t lo = __builtin_amdgcn_perm(T1, T0, sel), hi = __builtin_amdgcn_perm(T3, T2, sel);
+    // byte k of the result: byte k of lo (selector k) or of hi (k + 4, bit 3 of the code moved to bit 2)
+    return __builtin_amdgcn_perm(hi, lo, ((c >> 1) & 0x04040404u) | 0x03020100u);
+}
+template <> struct MQ<ST_IQ4_XS> {
+    static constexpr int bytes = 136, W = 9, Wp = 9, sum_sel = 1;
+    static constexpr uint32_t table_bytes = 0;
+    static constexpr bool has_pre = false;
+    __device__ static uint32_t shift(uint32_t) { return 0u; }
+    __device__ static uint32_t word(int k) { return k < 8 ? 16u * (uint32_t)k : 120u; }
+    __device__ static float block(const uint4 (&w)[W], uint32_t, const MqCtx &x) {
+        uint32_t raw[34];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            raw[4 * k] = w[k].x;
+            raw[4 * k + 1] = w[k].y;
+            raw[4 * k + 2] = w[k].z;
+            raw[4 * k + 3] = w[k].w;
+        }
+        raw[32] = w[8].z;   // block bytes 128..135
+        raw[33] = w[8].w;
+        const float d = mq_half_lo(raw[0]);
+        const uint32_t sh_hi = raw[0] >> 16, sl = raw[1];
+        float acc = 0.0f;
+#pragma unroll
+        for (int ib = 0; ib < 8; ib++) {
+            const uint32_t ls = ((sl >> (4 * ib)) & 15u) | (((sh_hi >> (2 * ib)) & 3u) << 4);
+            const float dl = d * (float)((int32_t)ls - 32);
+            mq_v4i D[2];
+#pragma unroll
+            for (int half = 0; half < 2; half++) {
+                mq_v4i b;
+#pragma unroll
+                for (int t = 0; t < 4; t++) b[t] = (int32_t)mq_iq4_levels(raw[2 + 4 * ib + t] >> (4 * half));
+                D[half] = mq_mfma(mq_a(x, 32 * ib + 16 * half), b);
+            }
+            acc = __builtin_fmaf(dl, __builtin_fmaf(mq_combine_f(D[0]), x.xsb[2 * ib], mq_combine_f(D[1]) * x.xsb[2 * ib + 1]),
+                                 acc);
+        }
+        return acc;
+    }
+};
+
+// Q8_0 in super-blocks of 8 blocks {d@0, qs[32]@2} (34 bytes each,
+// reference src/quants.c:85-94): 272 bytes = 17 words and 256 columns, so a
+// row of a multiple of 1024 columns steps in the K-quants' quads of four
+// super-blocks (the host counts such rows in super-blocks). Block k sits at
+// byte 34 k: for even k its qs start 2 bytes past a 4-byte boundary (realigned
+// with v_alignbyte) and d is the low half of dword 34 k / 4; for odd k the
+// qs are aligned and d is the high half of dword (34 k - 2) / 4.
+template <> struct MQ<ST_Q8_0> {
+    static constexpr int bytes = 272, W = 17, Wp = 17, sum_sel = 1;
+    static constexpr uint32_t table_bytes = 0;
+    static constexpr bool has_pre = false;
+    // Read and decoded in two parts of 9 words (the whole block does not
+    // fit the registers of 16 waves beside the pipeline): words 0..8 hold
+    // blocks 0..3 (bytes 0..135), words 8..16 blocks 4..7 (bytes 136..271).
+    static constexpr int W1 = 9, O2 = 8;
+    __device__ static uint32_t shift(uint32_t) { return 0u; }
+    __device__ static uint32_t word(int k) { return 16u * (uint32_t)k; }
+    // Blocks 4 H .. 4 H + 3 from words 8 H .. 8 H + 8 (dword m of the
+    // super-block is raw[m - 32 H]).
+    template <int H>
+    __device__ static float part(const uint4 (&w)[9], const MqCtx &x) {
+        uint32_t raw[36];
+#pragma unroll
+        for (int k = 0; k < 9; k++) {
+            raw[4 * k] = w[k].x;
+            raw[4 * k + 1] = w[k].y;
+            raw[4 * k + 2] = w[k].z;
+            raw[4 * k + 3] = w[k].w;
+        }
+        constexpr int o = 32 * H;
+        float acc = 0.0f;
+#pragma unroll
+        for (int k = 4 * H; k < 4 * H + 4; k++) {
+            const float d = (k & 1) ? mq_half_hi(raw[(34 * k - 2) / 4 - o]) : mq_half_lo(raw[34 * k / 4 - o]);
+            mq_v4i D[2];
+#pragma unroll
+            for (int half = 0; half < 2; half++) {
+                const int m = (34 * k + 2 + 16 * half) / 4 - o;
+                mq_v4i b;
+#pragma unroll
+                for (int t = 0; t < 4; t++)
+                    b[t] = (int32_t)((k & 1) ? raw[m + t] : __builtin_amdgcn_alignbyte(raw[m + t + 1], raw[m + t], 2u));
+                D[half] = mq_mfma(mq_a(x, 32 * k + 16 * half), b);
+            }
+            acc = __builtin_fmaf(d, __builtin_fmaf(mq_combine_f(D[0]), x.xsb[2 * k], mq_combine_f(D[1]) * x.xsb[2 * k + 1]),
+                                 acc);
+            if (k & 1) __builtin_amdgcn_sched_barrier(0);   // two blocks at a time
+        }
+        return acc;
+    }
+};
+
+// Formats read in two parts declare W1 (words of the first part) and O2
+// (first word of the second, which runs to W - 1); the others read their
+// W words at once (W1 = 0).
+template <class M, class = void> struct MqSplit {
+    static constexpr int W1 = 0, O2 = 0;
+};
+template <class M> struct MqSplit<M, decltype((void)M::W1)> {
+    static constexpr int W1 = M::W1, O2 = M::O2;
+};
+
+// LDS codebook bytes of a format, by type code.
+__device__ __forceinline__ uint32_t mq_table_bytes(int32_t type) {
+    return type == ST_IQ2_XS ? MQ<ST_IQ2_XS>::table_bytes : type == ST_IQ3_XXS ? MQ<ST_IQ3_XXS>::table_bytes : 0u;
+}
+// The format's codebook into LDS at tab (IQ formats; nothing for the
+// others). Published by the caller's next barrier.
+template <int T>
+__device__ __forceinline__ void mq_fill_table(uint8_t *tab) {
+    if constexpr (T == ST_IQ2_XS) {
+        for (int i = threadIdx.x; i < 512; i += blockDim.x) ((uint64_t *)tab)[i] = c_iq2xs_grid[i];
+    } else if constexpr (T == ST_IQ3_XXS) {
+        for (int i = threadIdx.x; i < 256; i += blockDim.x) ((uint32_t *)tab)[i] = c_iq3xxs_grid[i];
+    }
+}
+
 // ------------------------------------------------------------ the waves ---
 struct MqLane {
     int lane, g, p;
@@ -958,9 +1214,15 @@ struct MqWave {
         const uint32_t dst = ring + (uint32_t)islot * (uint32_t)(Wp * 1024);
         const uint32_t rmax = (uint32_t)(it.rows - 1 - it.row0);   // last valid row of the item
         const uint32_t rbase = (uint32_t)it.row0 * rb;
+        // For the widest formats the lane number is made opaque here, so
+        // that the per-lane parts of the Wp offsets are recomputed at each
+        // issue instead of being held in registers across the whole loop
+        // (an empty asm statement: it emits nothing).
+        uint32_t lane = (uint32_t)L.lane;
+        if constexpr (Wp >= 15) asm volatile("" : "+v"(lane));
 #pragma unroll
         for (int d = 0; d < Wp; d++) {
-            const uint32_t i = 64u * (uint32_t)d + (uint32_t)L.lane;
+            const uint32_t i = 64u * (uint32_t)d + lane;
             const uint32_t cl = i / (uint32_t)Wp, k = i - cl * (uint32_t)Wp;
             const uint32_t j = cl & 15u, r = j < rmax ? j : rmax;
             const uint32_t boff = (uint32_t)MQ<T>::bytes * (q4 + (cl >> 4));
@@ -1092,13 +1354,7 @@ struct MqWave {
         for (int t = t0; t < Tn; t++) {
             const int after = (Tn - 1 - t) < (S - 1) ? (Tn - 1 - t) : (S - 1);
             mq_wait_stages<Wp>(after);
-            uint4 w[W];
             const uint8_t *src = ringp + (size_t)cslot * (Wp * 1024) + 16 * Wp * L.lane;
-#pragma unroll
-            for (int k = 0; k < W; k++) w[k] = *(const uint4 *)(src + 16 * k);
-            // the slot is refilled only after its words are in registers
-            __builtin_amdgcn_s_waitcnt(MQ_WC_LGKM0);
-            if (t + S < Tn) issue();
             const MqItem it = item_of(c + ck * C);
             const uint32_t b = 4u * (uint32_t)(p + cm * P) + (uint32_t)L.g;
             MqCtx x;
@@ -1107,7 +1363,29 @@ struct MqWave {
             x.xsb = (const float *)(lds0 + it.xoff + mq_xq_planes(n)) + 16u * b;
             x.gvb = x.xsb + MQ<T>::sum_sel * (n >> 4);
             x.tab = tab;
-            acc += MQ<T>::block(w, MQ<T>::shift((uint32_t)MQ<T>::bytes * b), x);
+            if constexpr (MqSplit<MQ<T>>::W1 > 0) {
+                constexpr int W1 = MqSplit<MQ<T>>::W1, O2 = MqSplit<MQ<T>>::O2;
+                uint4 wa[W1];
+#pragma unroll
+                for (int k = 0; k < W1; k++) wa[k] = *(const uint4 *)(src + 16 * k);
+                const float a0 = MQ<T>::template part<0>(wa, x);
+                // the second part's words are read only after the first is done with
+                __builtin_amdgcn_sched_barrier(0);
+                uint4 wb[W - O2];
+#pragma unroll
+                for (int k = 0; k < W - O2; k++) wb[k] = *(const uint4 *)(src + 16 * (O2 + k));
+                __builtin_amdgcn_s_waitcnt(MQ_WC_LGKM0);
+                if (t + S < Tn) issue();
+                acc += a0 + MQ<T>::template part<1>(wb, x);
+            } else {
+                uint4 w[W];
+#pragma unroll
+                for (int k = 0; k < W; k++) w[k] = *(const uint4 *)(src + 16 * k);
+                // the slot is refilled only after its words are in registers
+                __builtin_amdgcn_s_waitcnt(MQ_WC_LGKM0);
+                if (t + S < Tn) issue();
+                acc += MQ<T>::block(w, MQ<T>::shift((uint32_t)MQ<T>::bytes * b), x);
+            }
             if (++cm == nqw) {
                 cm = 0;
                 acc = mq_sum_units(acc);
@@ -1143,11 +1421,7 @@ __device__ __forceinline__ void mq_mv(const uint8_t *__restrict__ W, uint64_t ro
     uint8_t *tab = smem + xoff + mq_xq_bytes(n);   // codebook (IQ formats), then the row sums
     float *red = (float *)(tab + MQ<T>::table_bytes);
     uint8_t *rings = smem + geo.orings;
-    if constexpr (T == ST_IQ2_XS) {
-        for (int i = threadIdx.x; i < 512; i += blockDim.x) ((uint64_t *)tab)[i] = c_iq2xs_grid[i];
-    } else if constexpr (T == ST_IQ3_XXS) {
-        for (int i = threadIdx.x; i < 256; i += blockDim.x) ((uint32_t *)tab)[i] = c_iq3xxs_grid[i];
-    }
+    mq_fill_table<T>(tab);
     auto item_of = [&](int i) {
         MqItem it;
         it.base = W;
@@ -1176,7 +1450,8 @@ __device__ __forceinline__ void mq_mv(const uint8_t *__restrict__ W, uint64_t ro
 
 // --------------------------------------------------------- expert FFN ------
 // One projection family of a stack of experts: expert e's quant rows start
-// at base + e * stride, row r at + r * row_bytes.
+// at base + e * stride, row r at + r * row_bytes; n_blocks counts 256-column
+// blocks (Q8_0: super-blocks of 8 blocks).
 struct MqProj {
     const uint8_t *base;
     uint64_t stride;
@@ -1193,8 +1468,8 @@ __device__ __forceinline__ int64_t mq_slot_expert(const int32_t *sel_idx, int32_
 // Gate/up of one slot: the workgroup owns row groups j0, j0 + jstep, ... of
 // the slot's inter rows; item 2k is the gate rows of its k-th row group,
 // item 2k + 1 the up rows. h[r] = silu(gate_r . x) * (up_r . x) (f32).
-// LDS: [zero][XQ of x][selection: 64 i32 + 64 f32][red: 2 nk x P x 16 f32][raw x]
-//      [rings].
+// LDS: [zero][XQ of x][selection: 64 i32 + 64 f32][codebook (IQ formats)]
+//      [red: 2 nk x P x 16 f32][raw x][rings].
 #define MQ_SEL_BYTES 512
 template <int T>
 __device__ __forceinline__ void mq_gateup_slot(const uint8_t *Wg, const uint8_t *Wu, uint64_t row_bytes, int32_t nb,
@@ -1205,8 +1480,10 @@ __device__ __forceinline__ void mq_gateup_slot(const uint8_t *Wg, const uint8_t 
     const int tiles = (inter + 15) >> 4;
     const int nk = j0 < tiles ? (tiles - j0 + jstep - 1) / jstep : 0;
     const uint32_t xoff = MQ_ZERO;
-    float *red = (float *)(smem + xoff + mq_xq_bytes(n) + MQ_SEL_BYTES);
+    uint8_t *tab = smem + xoff + mq_xq_bytes(n) + MQ_SEL_BYTES;   // codebook (IQ formats), then the row sums
+    float *red = (float *)(tab + MQ<T>::table_bytes);
     uint8_t *rings = smem + geo.orings;
+    mq_fill_table<T>(tab);
     auto item_of = [&](int i) {
         MqItem it;
         it.base = (i & 1) ? Wu : Wg;
@@ -1218,6 +1495,7 @@ __device__ __forceinline__ void mq_gateup_slot(const uint8_t *Wg, const uint8_t 
     };
     MqWave<T, decltype(item_of)> wv(item_of, 2 * nk, nb >> 2, n, (uint32_t)row_bytes, geo, rings, 0, geo.nw);
     wv.x_issued = x_issued;
+    wv.tab = tab;
     wv.template go<false>(x, geo, smem, xoff, red);
     __syncthreads();
     for (int i = threadIdx.x; i < nk * 16; i += blockDim.x) {
@@ -1287,11 +1565,20 @@ __device__ __forceinline__ void mq_gateup(const MqProj &gate, const MqProj &up, 
     const uint8_t *wg = G.base + e * G.stride, *wu = U.base + e * U.stride;
     float *hs = h + (int64_t)slot * inter;
     const int32_t nb = (int32_t)G.n_blocks;
+#define MQ_GU_CASE(T) \
+    case T: mq_gateup_slot<T>(wg, wu, G.row_bytes, nb, inter, j0, wps, x, hs, geo, x_issued); break;
     switch (G.type) {
-    case ST_Q2_K: mq_gateup_slot<ST_Q2_K>(wg, wu, G.row_bytes, nb, inter, j0, wps, x, hs, geo, x_issued); break;
-    case ST_Q3_K: mq_gateup_slot<ST_Q3_K>(wg, wu, G.row_bytes, nb, inter, j0, wps, x, hs, geo, x_issued); break;
+        MQ_GU_CASE(ST_Q2_K)
+        MQ_GU_CASE(ST_Q3_K)
+        MQ_GU_CASE(ST_Q5_K)
+        MQ_GU_CASE(ST_Q6_K)
+        MQ_GU_CASE(ST_Q8_0)
+        MQ_GU_CASE(ST_IQ2_XS)
+        MQ_GU_CASE(ST_IQ3_XXS)
+        MQ_GU_CASE(ST_IQ4_XS)
     default: mq_gateup_slot<ST_Q4_K>(wg, wu, G.row_bytes, nb, inter, j0, wps, x, hs, geo, x_issued); break;
     }
+#undef MQ_GU_CASE
 }
 
 #define SEPIA_MQ_GATEUP()                                                                                \
@@ -1316,12 +1603,15 @@ __device__ __forceinline__ void mq_gateup(const MqProj &gate, const MqProj &up, 
 // output as src/sepia.c:3953-3957 does), into y and puts the counter back to
 // zero -- deterministic whatever the arrival order. n_count < n_sum: the
 // other slots' partial rows were published by an earlier launch.
-// LDS: [zero][XQ of h_slot][red: nk x P x 16 f32][flags: nk i32][raw h][rings].
+// LDS: [zero][XQ of h_slot][codebook (IQ formats)][red: nk x P x 16 f32][flags: nk i32][raw h]
+//      [rings].
 template <int T>
 __device__ __forceinline__ void mq_dn_slot(const uint8_t *Wd, uint64_t row_bytes, int32_t nb, int32_t inter,
                                            int64_t hidden, int32_t j0, int32_t jstep, int nk,
                                            const float *__restrict__ hs, MqGeo geo, float *red, uint8_t *rings,
                                            uint8_t *lds0) {
+    uint8_t *tab = lds0 + MQ_ZERO + mq_xq_bytes(inter);
+    mq_fill_table<T>(tab);
     auto item_of = [&](int i) {
         MqItem it;
         it.base = Wd;
@@ -1332,6 +1622,7 @@ __device__ __forceinline__ void mq_dn_slot(const uint8_t *Wd, uint64_t row_bytes
         return it;
     };
     MqWave<T, decltype(item_of)> wv(item_of, nk, nb >> 2, inter, (uint32_t)row_bytes, geo, rings, 0, geo.nw);
+    wv.tab = tab;
     wv.template go<false>(hs, geo, lds0, MQ_ZERO, red);
 }
 
@@ -1352,17 +1643,26 @@ __device__ __forceinline__ void mq_down(const MqProj &down, const MqProj &s_down
     const uint8_t *Wd = Pj.base + e * Pj.stride;
     const int tiles = (int)((hidden + 15) >> 4);
     const int nk = j0 < tiles ? (tiles - j0 + jstep - 1) / jstep : 0;
-    const size_t o_red = MQ_ZERO + mq_xq_bytes(inter);
+    const size_t o_red = MQ_ZERO + mq_xq_bytes(inter) + mq_table_bytes(Pj.type);
     float *red = (float *)(smem + o_red);
     int32_t *flag = (int32_t *)(smem + o_red + (size_t)nk * geo.P * 64);
     uint8_t *rings = smem + geo.orings;
     const float *hs = h + (int64_t)slot * inter;
     const int32_t nb = (int32_t)Pj.n_blocks;
+#define MQ_DN_CASE(T) \
+    case T: mq_dn_slot<T>(Wd, Pj.row_bytes, nb, inter, hidden, j0, jstep, nk, hs, geo, red, rings, smem); break;
     switch (Pj.type) {
-    case ST_Q2_K: mq_dn_slot<ST_Q2_K>(Wd, Pj.row_bytes, nb, inter, hidden, j0, jstep, nk, hs, geo, red, rings, smem); break;
-    case ST_Q3_K: mq_dn_slot<ST_Q3_K>(Wd, Pj.row_bytes, nb, inter, hidden, j0, jstep, nk, hs, geo, red, rings, smem); break;
+        MQ_DN_CASE(ST_Q2_K)
+        MQ_DN_CASE(ST_Q3_K)
+        MQ_DN_CASE(ST_Q5_K)
+        MQ_DN_CASE(ST_Q6_K)
+        MQ_DN_CASE(ST_Q8_0)
+        MQ_DN_CASE(ST_IQ2_XS)
+        MQ_DN_CASE(ST_IQ3_XXS)
+        MQ_DN_CASE(ST_IQ4_XS)
     default: mq_dn_slot<ST_Q4_K>(Wd, Pj.row_bytes, nb, inter, hidden, j0, jstep, nk, hs, geo, red, rings, smem); break;
     }
+#undef MQ_DN_CASE
     __syncthreads();
     if (n_sum == 1) {
         const float w = sel_w ? sel_w[0] : 1.0f;

@@ -239,5 +239,9 @@ SEPIA_MQ_MV(q3_k, ST_Q3_K)
 SEPIA_MQ_MV(q4_k, ST_Q4_K)
 SEPIA_MQ_MV(iq2_xs, ST_IQ2_XS)
 SEPIA_MQ_MV(iq3_xxs, ST_IQ3_XXS)
+SEPIA_MQ_MV(q5_k, ST_Q5_K)
+SEPIA_MQ_MV(q6_k, ST_Q6_K)
+SEPIA_MQ_MV(iq4_xs, ST_IQ4_XS)
+SEPIA_MQ_MV(q8_0, ST_Q8_0)
 SEPIA_MQ_GATEUP()
 SEPIA_MQ_DOWN()

@@ -51,10 +51,10 @@ enum {
     /* expert-FFN tile kernels: 9 (routed, shared) format pairs over
      * {Q2_K, Q3_K, Q4_K}, each gate/up (x f32), gate/up (x planes), down */
     K_FFN_BASE,
-    /* matrix-core matvecs (kernels/mq.h): Q2_K, Q3_K, Q4_K */
+    /* matrix-core matvecs (kernels/mq.h), by mq_code: Q2_K, Q3_K, Q4_K, IQ2_XS, IQ3_XXS, Q5_K, Q6_K, IQ4_XS, Q8_0 */
     K_MQ_MV = K_FFN_BASE + 27,
     /* matrix-core expert FFN: gate/up, down */
-    K_MQ_GU = K_MQ_MV + 5,
+    K_MQ_GU = K_MQ_MV + 9,
     K_MQ_DN = K_MQ_GU + 1,
     /* batched prefill MoE layer (kernels/prefill.h) */
     K_PF_ROUTE = K_MQ_DN + 1, K_PF_SELECT, K_PF_GROUP, K_PF_GATEUP, K_PF_DOWN, K_PF_COMBINE, K_PF_SPLIT,
@@ -86,6 +86,7 @@ static const char *const k_names[K_COUNT] = {
     FFN_NAMES("22"), FFN_NAMES("23"), FFN_NAMES("24"), FFN_NAMES("32"), FFN_NAMES("33"), FFN_NAMES("34"),
     FFN_NAMES("42"), FFN_NAMES("43"), FFN_NAMES("44"),
     "sepia_mq_mv_q2_k", "sepia_mq_mv_q3_k", "sepia_mq_mv_q4_k", "sepia_mq_mv_iq2_xs", "sepia_mq_mv_iq3_xxs",
+    "sepia_mq_mv_q5_k", "sepia_mq_mv_q6_k", "sepia_mq_mv_iq4_xs", "sepia_mq_mv_q8_0",
     "sepia_mq_gateup", "sepia_mq_down",
     "sepia_pf_route", "sepia_pf_select", "sepia_pf_group", "sepia_pf_gateup", "sepia_pf_down", "sepia_pf_combine",
     "sepia_pf_split", "sepia_pf_gateup_r", "sepia_pf_down_r", "sepia_pf_route_m", "sepia_fill_u32",
@@ -1142,8 +1143,8 @@ typedef struct {
                                      * 12.2 -> 11.2 us); the K-quants' stepping waves need all 16 */
 #define MQ_XQ_SEGS_PER_WAVE 128     /* segments a converter wave turns into XQ at most (MQ_XQP passes of 16) */
 static size_t mq_xq_bytes(int64_t n) { return (size_t)(n / 256) * 832 + 3 * (size_t)(n / 16) * 4; }
-/* matrix-core format codes: 0..2 the K-quants (matvec and the FFN kernels),
- * 3..4 IQ2_XS and IQ3_XXS (matvec) */
+/* matrix-core format codes (kernels/mq.h decoders, matvec and expert FFN):
+ * 0..2 Q2_K, Q3_K, Q4_K; 3..4 IQ2_XS, IQ3_XXS; 5..8 Q5_K, Q6_K, IQ4_XS, Q8_0 */
 static int mq_code(int t) {
     switch (t) {
     case SEPIA_T_Q2_K: return 0;
@@ -1151,11 +1152,27 @@ static int mq_code(int t) {
     case 12: return 2;
     case 17: return 3;
     case 18: return 4;
+    case 13: return 5;
+    case 14: return 6;
+    case 23: return 7;
+    case 8: return 8;
     default: return -1;
     }
 }
-static const int k_mq_words[5] = { 7, 7, 9, 5, 7 };   /* padded words per lane (MQ<T>::Wp) */
-static const size_t k_mq_table[5] = { 0, 0, 0, 4096, 1024 };   /* LDS codebook bytes (MQ<T>::table_bytes) */
+#define MQ_FORMATS 9
+static const int k_mq_words[MQ_FORMATS] = { 7, 7, 9, 5, 7, 11, 15, 9, 17 };   /* padded words per lane (MQ<T>::Wp) */
+static const size_t k_mq_table[MQ_FORMATS] = { 0, 0, 0, 4096, 1024, 0, 0, 0, 0 };   /* LDS codebook (MQ<T>::table_bytes) */
+/* Converter waves are planned only for the formats where they measured
+ * faster (the IQ2_XS / IQ3_XXS matvecs); the others' stepping waves need
+ * all 16. */
+static const int k_mq_conv[MQ_FORMATS] = { 0, 0, 0, 1, 1, 0, 0, 0, 0 };
+/* A row of n_blocks format blocks in the matrix-core kernels' 256-column
+ * blocks (Q8_0: super-blocks of 8 of its 32-column blocks); -1 if it does
+ * not divide. */
+static int64_t mq_nb(int type, int64_t n_blocks) {
+    if (type == 8) return n_blocks % 8 ? -1 : n_blocks / 8;
+    return n_blocks;
+}
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 /* Geometry for workgroups of n_items items of nq quads; mc is the format
@@ -1183,7 +1200,7 @@ static int mq_geo(int mc, int wmax, int64_t n_items, int64_t nq, size_t fixed, s
      * launches) leaves the choice to the planner */
     const int forced = (g_opt_mq_x == 3 && !allow_conv) ? 0 : g_opt_mq_x;
     for (int mode = 0; mode <= (raw_bytes > 0 ? (allow_conv ? 2 : 1) : 0); mode++) {
-        if (raw_bytes > 0 && (forced ? forced != mode + 1 : (mode == 2 && mc < 3))) continue;
+        if (raw_bytes > 0 && (forced ? forced != mode + 1 : (mode == 2 && !k_mq_conv[mc]))) continue;
         for (int P = 1; P <= 16 && P <= nq; P++) {
             if (g_opt_mq_p && P != g_opt_mq_p) continue;
             for (int C = 1; C * P <= 16 && C <= n_items; C++) {
@@ -1235,14 +1252,17 @@ static int mq_geo(int mc, int wmax, int64_t n_items, int64_t nq, size_t fixed, s
 }
 
 /* Shapes the matrix-core kernels take: a format with a decoder, 4-byte
- * aligned rows of a multiple of 4 blocks, row offsets within 32 bits. */
-static int mq_shape_ok(int type, int64_t n_blocks, int64_t rows, uintptr_t base, uint64_t row_bytes) {
-    return g_opt_mq && mq_code(type) >= 0 && n_blocks >= 4 && n_blocks % 4 == 0 && base % 4 == 0 &&
-           row_bytes % 4 == 0 && (uint64_t)rows * row_bytes < (1ull << 32);
+ * aligned rows of a multiple of 4 256-column blocks (nb, mq_nb), row
+ * offsets within 32 bits. */
+static int mq_shape_ok(int type, int64_t nb, int64_t rows, uintptr_t base, uint64_t row_bytes) {
+    return g_opt_mq && mq_code(type) >= 0 && nb >= 4 && nb % 4 == 0 && base % 4 == 0 && row_bytes % 4 == 0 &&
+           (uint64_t)rows * row_bytes < (1ull << 32);
 }
 
+/* n_blocks: the row's blocks of the format; the kernel takes mq_nb of it. */
 static int mq_plan(int type, int64_t n_blocks, int64_t rows, uintptr_t base, uint64_t row_bytes, unsigned *threads,
                    size_t *lds, unsigned *grid, MqGeo *geo) {
+    n_blocks = mq_nb(type, n_blocks);
     if (!mq_shape_ok(type, n_blocks, rows, base, row_bytes)) return -1;
     const int mc = mq_code(type);
     const int64_t tiles = (rows + 15) / 16;
@@ -1292,7 +1312,7 @@ int sepia_gpu_matvec_q(int ggml_type, SepiaGpuBuf *w, size_t w_off, SepiaGpuBuf 
     const int kmq = mq_plan(ggml_type, n_blocks, out_dim, (uintptr_t)wp, row_bytes, &mq_threads, &mq_lds, &mq_grid,
                             &mgeo);
     if (kmq >= 0) {
-        int32_t nb32 = (int32_t)n_blocks;
+        int32_t nb32 = (int32_t)mq_nb(ggml_type, n_blocks);
         void *args[] = { &wp, &row_bytes, &out_dim, &nb32, &x->dev, &y->dev, &mgeo };
         return launch_lds(kmq, mq_grid, mq_threads, mq_lds, args, op);
     }
@@ -1490,9 +1510,9 @@ typedef struct {
     MqGeo gu_geo_r, gu_geo_s, dn_geo_r, dn_geo_s;   /* routed and shared workgroups, each for its format */
 } MqFfnPlan;
 #define MQ_DN_CNT_OFF 64            /* first down arrival counter (u32 index in the counter region) */
+/* p: n_blocks already in 256-column blocks (mq_nb). */
 static int mq_proj_ok(const MoeProj *p, int64_t rows) {
-    return mq_code(p->type) <= 2 && mq_shape_ok(p->type, p->n_blocks, rows, (uintptr_t)p->base, p->row_bytes) &&
-           p->stride % 4 == 0;
+    return mq_shape_ok(p->type, p->n_blocks, rows, (uintptr_t)p->base, p->row_bytes) && p->stride % 4 == 0;
 }
 /* Workgroups per slot for slots of byte weights br (routed) and bs (shared):
  * at most MQ_CUS in all (unless one per slot is already more), at most
@@ -1553,16 +1573,30 @@ static int mq_ffn_plan(const MoeProj *g, const MoeProj *u, const MoeProj *d, con
     const int64_t nk_gr = (tiles_i + pl->gu_wps_r - 1) / pl->gu_wps_r, nk_gs = (tiles_i + pl->gu_wps_s - 1) / pl->gu_wps_s;
     const int64_t nk_dr = (tiles_h + pl->dn_wps_r - 1) / pl->dn_wps_r, nk_ds = (tiles_h + pl->dn_wps_s - 1) / pl->dn_wps_s;
     const size_t gu_fixed = MQ_ZERO + mq_xq_bytes(H) + MQ_SEL_BYTES;
-    if (!mq_geo2(kg, ksg, has_s, 2 * nk_gr, 2 * nk_gs, H / 1024, gu_fixed, gu_fixed, (size_t)H * 4, &pl->gu_threads,
-                 &pl->gu_geo_r, &pl->gu_geo_s, &pl->gu_lds))
+    if (!mq_geo2(kg, ksg, has_s, 2 * nk_gr, 2 * nk_gs, H / 1024, gu_fixed + k_mq_table[kg], gu_fixed + k_mq_table[ksg],
+                 (size_t)H * 4, &pl->gu_threads, &pl->gu_geo_r, &pl->gu_geo_s, &pl->gu_lds))
         return 0;
-    if (!mq_geo2(kd, ksd, has_s, nk_dr, nk_ds, I / 1024, MQ_ZERO + mq_xq_bytes(I) + (size_t)nk_dr * 4 + 256,
-                 MQ_ZERO + mq_xq_bytes(I) + (size_t)nk_ds * 4 + 256, (size_t)I * 4, &pl->dn_threads, &pl->dn_geo_r,
+    const size_t dn_fixed = MQ_ZERO + mq_xq_bytes(I) + 256;
+    if (!mq_geo2(kd, ksd, has_s, nk_dr, nk_ds, I / 1024, dn_fixed + k_mq_table[kd] + (size_t)nk_dr * 4,
+                 dn_fixed + k_mq_table[ksd] + (size_t)nk_ds * 4, (size_t)I * 4, &pl->dn_threads, &pl->dn_geo_r,
                  &pl->dn_geo_s, &pl->dn_lds))
         return 0;
     pl->gu_grid = (unsigned)(topk * pl->gu_wps_r + n_shared * pl->gu_wps_s);
     pl->dn_grid = (unsigned)(topk * pl->dn_wps_r + n_shared * pl->dn_wps_s);
     return 1;
+}
+
+/* mq_ffn_plan on copies of the six projections (mp) whose n_blocks count
+ * the matrix-core kernels' 256-column blocks. */
+static int mq_ffn_prep(const MoeProj *g, const MoeProj *u, const MoeProj *d, const MoeProj *sg, const MoeProj *su,
+                       const MoeProj *sd, int32_t topk, int32_t n_shared, int64_t H, int64_t I, MoeProj mp[6],
+                       MqFfnPlan *pl) {
+    const MoeProj *ps[6] = { g, u, d, sg, su, sd };
+    for (int i = 0; i < 6; i++) {
+        mp[i] = *ps[i];
+        mp[i].n_blocks = mq_nb(mp[i].type, mp[i].n_blocks);
+    }
+    return mq_ffn_plan(&mp[0], &mp[1], &mp[2], &mp[3], &mp[4], &mp[5], topk, n_shared, H, I, pl);
 }
 
 /* LDS of the prefill projection kernels (PF_LDS_BYTES in kernels/prefill.h):
@@ -1720,7 +1754,8 @@ static int ffn_launch(const char *op, const MoeProj *g, const MoeProj *u, const 
     int32_t n_slots = topk + n_shared;
     int64_t inter = I, hid = H;
     MqFfnPlan pl;
-    if (mq_ffn_plan(g, u, d, sg, su, sd, topk, n_shared, H, I, &pl)) {
+    MoeProj mp[6];
+    if (mq_ffn_prep(g, u, d, sg, su, sd, topk, n_shared, H, I, mp, &pl)) {
         int32_t inter32 = (int32_t)I;
         float *h = (float *)scr;
         float *ypart = (float *)(scr + (size_t)n_slots * (size_t)I * 4);
@@ -1728,10 +1763,10 @@ static int ffn_launch(const char *op, const MoeProj *g, const MoeProj *u, const 
         MqRoute rt;
         memset(&rt, 0, sizeof rt);
         if (route) rt = *route;
-        void *a_gu[] = { (void *)g, (void *)u, (void *)sg, (void *)su, &sel_idx, &fixed, &topk, &inter32,
+        void *a_gu[] = { &mp[0], &mp[1], &mp[3], &mp[4], &sel_idx, &fixed, &topk, &inter32,
                          &pl.gu_wps_r, &pl.gu_wps_s, &xdev, &h, &pl.gu_geo_r, &pl.gu_geo_s, &rt };
         if (!launch_lds(K_MQ_GU, pl.gu_grid, pl.gu_threads, pl.gu_lds, a_gu, op)) return 0;
-        void *a_dn[] = { (void *)d, (void *)sd, &sel_idx, &sel_w, &fixed, &topk, &n_slots, &n_slots, &inter32, &hid, &h,
+        void *a_dn[] = { &mp[2], &mp[5], &sel_idx, &sel_w, &fixed, &topk, &n_slots, &n_slots, &inter32, &hid, &h,
                          &ydev, &pl.dn_geo_r, &pl.dn_geo_s, &pl.dn_wps_r, &pl.dn_wps_s, &ypart, &cnt };
         return launch_lds(K_MQ_DN, pl.dn_grid, pl.dn_threads, pl.dn_lds, a_dn, op);
     }
@@ -1873,7 +1908,8 @@ static int moe_decode_impl(const char *op, const SepiaMoeLayerDesc *L, SepiaGpuB
     /* with the matrix-core FFN the gate/up launch selects from the logits;
      * otherwise the router's last workgroup does */
     MqFfnPlan pl;
-    const int in_kernel = mq_ffn_plan(&g, &u, &d, &sg, &su, &sd, tk, ns, H, I, &pl);
+    MoeProj mp[6];
+    const int in_kernel = mq_ffn_prep(&g, &u, &d, &sg, &su, &sd, tk, ns, H, I, mp, &pl);
     int32_t select = !in_kernel;
     void *a_route[] = { &rw, &ld, &rb, &x->dev, &hid, &nr, &ns, &tk, &rs, &gsc, &logits, &sel_idx, &sel_w, &counter,
                         &select };

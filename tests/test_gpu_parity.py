@@ -285,7 +285,8 @@ def mq_geometry(dev, request):
 
 
 MQ_NAMES = {10: "sepia_mq_mv_q2_k", 11: "sepia_mq_mv_q3_k", 12: "sepia_mq_mv_q4_k", 17: "sepia_mq_mv_iq2_xs",
-            18: "sepia_mq_mv_iq3_xxs"}
+            18: "sepia_mq_mv_iq3_xxs", 13: "sepia_mq_mv_q5_k", 14: "sepia_mq_mv_q6_k", 23: "sepia_mq_mv_iq4_xs",
+            8: "sepia_mq_mv_q8_0"}
 # (type, rows, cols, (P, C, S)): several items per workgroup (12288 and 8200
 # rows), long rows (12288 columns: 12 quads), partial row groups, every ring
 # depth, parts that do not divide the quads.
@@ -296,6 +297,10 @@ MQ_GEOMETRIES = [
     (12, 8200, 4096, (1, 1, 2)), (12, 8200, 4096, (4, 3, 1)), (12, 8200, 4096, (3, 2, 2)),
     (17, 12288, 2048, (1, 2, 2)), (17, 70, 12288, (3, 1, 3)), (17, 6144, 6144, (2, 2, 1)),
     (18, 12288, 2048, (2, 1, 2)), (18, 70, 12288, (4, 1, 2)), (18, 6144, 6144, (1, 2, 3)),
+    (13, 12288, 2048, (1, 1, 2)), (13, 70, 12288, (3, 1, 2)), (13, 3072, 6144, (2, 1, 1)),
+    (14, 12288, 2048, (2, 1, 1)), (14, 70, 12288, (5, 1, 1)), (14, 6144, 3072, (1, 2, 2)),
+    (23, 12288, 2048, (1, 2, 2)), (23, 70, 12288, (3, 1, 3)), (23, 6144, 3072, (2, 1, 2)),
+    (8, 12288, 2048, (1, 1, 1)), (8, 70, 12288, (4, 1, 1)), (8, 3072, 6144, (2, 1, 1)),
 ]
 
 
@@ -310,6 +315,18 @@ def test_matvec_mq_geometries(dev, orc, t, out_dim, in_dim, mq_geometry):
 @pytest.mark.parametrize("t,w_off", [(10, 4), (10, 132), (12, 4), (12, 1028), (11, 2), (11, 4)])
 def test_matvec_q_tile_offsets(dev, orc, t, w_off):
     check_matvec(dev, orc, t, 100, 2048, seed=3 + w_off, w_off=w_off)
+
+
+@pytest.mark.parametrize("t", [13, 14, 23, 8])
+@pytest.mark.parametrize("w_off", [4, 132, 2])
+def test_matvec_mq_offsets_new_formats(dev, orc, t, w_off):
+    """Q5_K, Q6_K, IQ4_XS and Q8_0 weights 4-byte aligned at an offset into
+    their buffer take the matrix-core kernel (the launch count shows it); at
+    a 2-byte offset another kernel, with the same result bar. 33 rows leave a
+    partial row group; the last row's last block ends at the buffer's end."""
+    with Launches(dev) as n:
+        check_matvec(dev, orc, t, 33, 2048, seed=41 + w_off + t, w_off=w_off)
+        assert n.count(MQ_NAMES[t]) == (0 if w_off % 4 else 1)
 
 
 def test_matvec_q_repeat_stable(dev, orc):
@@ -519,16 +536,18 @@ def test_matvec_mq_vector_paths(dev, orc, mq_vector, t, out_dim, in_dim):
         assert n.count(MQ_NAMES[t]) == 1
 
 
-def make_layer(dev, rng, hidden, inter, n_routed, n_shared, tg, tu, td, ts, rw_off=0, topk=6):
+def make_layer(dev, rng, hidden, inter, n_routed, n_shared, tg, tu, td, ts, rw_off=0, topk=6, tsd=None):
     """Shared buffers with seeded host data; returns (desc, spec, keep). The
     router matrix starts rw_off bytes into its buffer. Without shared experts
-    their buffers hold a placeholder (never read)."""
+    their buffers hold a placeholder (never read). ts: the shared experts'
+    format (tsd, if given, that of their down projection)."""
+    tsd = ts if tsd is None else tsd
     gate = [synth.random_matrix(tg, inter, hidden, rng) for _ in range(n_routed)]
     up = [synth.random_matrix(tu, inter, hidden, rng) for _ in range(n_routed)]
     down = [synth.random_matrix(td, hidden, inter, rng) for _ in range(n_routed)]
     sg = [synth.random_matrix(ts, inter, hidden, rng) for _ in range(n_shared)]
     su = [synth.random_matrix(ts, inter, hidden, rng) for _ in range(n_shared)]
-    sd = [synth.random_matrix(ts, hidden, inter, rng) for _ in range(n_shared)]
+    sd = [synth.random_matrix(tsd, hidden, inter, rng) for _ in range(n_shared)]
     rw = (rng.standard_normal((n_routed + n_shared, hidden)) * 0.02).astype(np.float32)
     rb = rng.uniform(-0.1, 0.1, n_routed).astype(np.float32)
     bufs = {k: dev.shared_from(np.concatenate(v) if v else np.zeros(256, np.uint8)) for k, v in
@@ -542,11 +561,11 @@ def make_layer(dev, rng, hidden, inter, n_routed, n_shared, tg, tu, td, ts, rw_o
     d.router_w, d.router_bias = bufs["rw"], bufs["rb"]
     d.router_w_off = rw_off
     for name, t, lst in (("gate", tg, gate), ("up", tu, up), ("down", td, down),
-                         ("s_gate", ts, sg), ("s_up", ts, su), ("s_down", ts, sd)):
+                         ("s_gate", ts, sg), ("s_up", ts, su), ("s_down", tsd, sd)):
         setattr(d, name, hip.ExpertTensor(bufs[name], 0, lst[0].nbytes if lst else 0, t))
     spec = dict(hidden=hidden, inter=inter, n_routed=n_routed, n_shared=n_shared, topk=topk, route_scale=8.0,
                 global_scale=1.0, router_w=rw, router_bias=rb, t_gate=tg, t_up=tu, t_down=td,
-                ts_gate=ts, ts_up=ts, ts_down=ts, gate=gate, up=up, down=down, s_gate=sg, s_up=su, s_down=sd)
+                ts_gate=ts, ts_up=ts, ts_down=tsd, gate=gate, up=up, down=down, s_gate=sg, s_up=su, s_down=sd)
     return d, spec, bufs
 
 
@@ -690,6 +709,41 @@ def test_moe_decode_slots(dev, orc, types, n_routed, n_shared, topk):
         if chosen != list(idx_ref):
             y_ref, _, _, _ = orc.moe_layer(spec, x, force_idx=chosen, threads=THREADS)
         assert_close(y, y_ref, what="moe slots rep %d" % rep, gate=False)
+    for b in bufs.values():
+        dev.free(b)
+
+
+# The real checkpoint's layers (reference docs/gguf-inventory-ud-q2_k_xl.md:
+# 72-111, 214-235): IQ2_XS gate/up with IQ3_XXS down (57 layers) or IQ4_XS
+# down (7 layers), IQ3_XXS gate/up on the last layer; shared experts Q5_K,
+# Q6_K or Q8_0. (gate, up, down, shared gate/up, shared down).
+REAL_LAYERS = [((17, 17, 18, 13, 14), "iq2xs_iq3xxs__q5k_q6k"), ((17, 17, 23, 13, 14), "iq2xs_iq4xs__q5k_q6k"),
+               ((18, 18, 18, 8, 8), "iq3xxs__q8_0"), ((17, 17, 18, 14, 13), "iq2xs_iq3xxs__q6k_q5k"),
+               ((17, 17, 23, 8, 14), "iq2xs_iq4xs__q8_0_q6k")]
+
+
+@pytest.mark.parametrize("types", [t for t, _ in REAL_LAYERS], ids=[n for _, n in REAL_LAYERS])
+def test_moe_decode_real_types(dev, orc, types):
+    """The real checkpoint's formats at its layer shape (hidden 6144, inter
+    3072, top-6 + 2 shared; 16 routed experts resident): the router and the
+    two matrix-core FFN launches, their codebooks in LDS, routed and shared
+    workgroups each on its own format (the launch counts show the path), twice
+    in a row (the arrival counters must be back at zero)."""
+    rng = np.random.default_rng(zlib.crc32(repr(types).encode()) & 0xFFFF)
+    tg, tu, td, ts, tsd = types
+    desc, spec, bufs = make_layer(dev, rng, hidden=6144, inter=3072, n_routed=16, n_shared=2,
+                                  tg=tg, tu=tu, td=td, ts=ts, tsd=tsd)
+    for rep in range(2):
+        x = synth.normal_vector(rng, 6144)
+        with Launches(dev) as n:
+            y, idx, w = run_moe(dev, desc, x)
+            assert n.count("sepia_moe_route") == 1
+            assert n.count("sepia_mq_gateup") == 1 and n.count("sepia_mq_down") == 1
+        y_ref, logits, idx_ref, w_ref = orc.moe_layer(spec, x, threads=THREADS)
+        chosen = check_route(orc, spec, logits, idx, w)
+        if chosen != list(idx_ref):
+            y_ref, _, _, _ = orc.moe_layer(spec, x, force_idx=chosen, threads=THREADS)
+        assert_close(y, y_ref, what="moe real types rep %d" % rep, gate=False)
     for b in bufs.values():
         dev.free(b)
 
@@ -845,8 +899,11 @@ def test_expert_ffn(dev, orc, kernel_path, types, hidden, inter):
 
 @pytest.mark.parametrize("types,hidden,inter", [((10, 10, 11), 6144, 3072), ((12, 12, 10), 4096, 2048),
                                                 ((11, 11, 12), 2048, 8192), ((10, 10, 10), 1024, 1024),
-                                                ((12, 12, 11), 3072, 4096)],
-                         ids=["c2", "units_half", "two_units_per_wg", "tiny", "q4k_q3k"])
+                                                ((12, 12, 11), 3072, 4096), ((17, 17, 23), 6144, 3072),
+                                                ((13, 13, 14), 4096, 2048), ((8, 8, 18), 2048, 3072),
+                                                ((14, 14, 8), 1024, 1024)],
+                         ids=["c2", "units_half", "two_units_per_wg", "tiny", "q4k_q3k", "iq2xs_iq4xs",
+                              "q5k_q6k", "q8_0_iq3xxs", "q6k_q8_0_tiny"])
 def test_expert_ffn_shapes(dev, orc, types, hidden, inter):
     """The expert FFN on the matrix-core launches over shapes with fewer row
     groups than workgroups, several row groups per workgroup and long rows;
