@@ -23,7 +23,8 @@ cpu_baseline = the C oracle's scalar MoE layer (the reference's
          host core, on the same token and experts, over a bounded sample.
 extra  = the other BASELINE configurations (C1 Q4_K matvec, C2 one expert
          FFN, C4 IQ matvecs, C5 512-token prefill MoE layer) measured the same
-         way.
+         way, and the C3 layer in the real checkpoint's formats (IQ2_XS
+         gate/up, IQ3_XXS down, Q5_K/Q6_K shared experts).
 """
 import argparse
 import ctypes
@@ -40,8 +41,14 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0
 METRIC = "quantized-weight GB/s (% of HBM peak); MoE layer µs/token at decode batch 1"
 SCALE_LO, SCALE_HI = 2.0 ** -10, 2.0 ** -6
-Q2_K, Q3_K, Q4_K, IQ2_XXS, IQ2_XS, IQ3_XXS = 10, 11, 12, 16, 17, 18
-GEOM = {10: (256, 84), 11: (256, 110), 12: (256, 144), 16: (256, 66), 17: (256, 74), 18: (256, 98)}
+Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, IQ2_XXS, IQ2_XS, IQ3_XXS, IQ4_XS = 8, 10, 11, 12, 13, 14, 16, 17, 18, 23
+GEOM = {8: (32, 34), 10: (256, 84), 11: (256, 110), 12: (256, 144), 13: (256, 176), 14: (256, 210),
+        16: (256, 66), 17: (256, 74), 18: (256, 98), 23: (256, 136)}
+# Formats of a MoE layer: (routed gate/up, routed down, shared gate/up, shared down).
+C3_TYPES = (Q2_K, Q3_K, Q4_K, Q4_K)
+# The real checkpoint's most common layer (reference docs/gguf-inventory-ud-q2_k_xl.md:72-111):
+# IQ2_XS gate/up, IQ3_XXS down; shared experts Q5_K gate/up, Q6_K down.
+REAL_TYPES = (IQ2_XS, IQ3_XXS, Q5_K, Q6_K)
 
 
 def log(*a):
@@ -331,25 +338,27 @@ def run_copy(B, steps):
                 avg_launch_us=kms["sepia_copy_f32"] * 1e3, gbs=8 * n / (kms["sepia_copy_f32"] * 1e-3) / 1e9)
 
 
-def build_moe_layers(B, n_layers):
-    """n_layers Inkling-shaped MoE layers resident in HBM: 256 routed experts (gate/up Q2_K
-    [3072x6144], down Q3_K [6144x3072]), 2 shared Q4_K, f32 router [258, 6144] ~ N(0, 0.02),
-    bias U(-0.1, 0.1). Returns (layers [(desc, buffers)], host routers [(rw, rb)], sizes)."""
+def build_moe_layers(B, n_layers, types=C3_TYPES):
+    """n_layers Inkling-shaped MoE layers resident in HBM: 256 routed experts (gate/up
+    [3072x6144], down [6144x3072]) and 2 shared ones of the given formats (C3: Q2_K, Q3_K routed;
+    Q4_K shared), f32 router [258, 6144] ~ N(0, 0.02), bias U(-0.1, 0.1). Returns (layers
+    [(desc, buffers)], host routers [(rw, rb)], sizes)."""
     hip, L = B.hip, B.L
     H, I, NR, NS = 6144, 3072, 256, 2
-    gb, db = mat_bytes(Q2_K, I, H), mat_bytes(Q3_K, H, I)
-    sgb, sdb = mat_bytes(Q4_K, I, H), mat_bytes(Q4_K, H, I)
+    tg, td, tsg, tsd = types
+    gb, db = mat_bytes(tg, I, H), mat_bytes(td, H, I)
+    sgb, sdb = mat_bytes(tsg, I, H), mat_bytes(tsd, H, I)
     rng = np.random.default_rng(31)
     layers, host_router = [], []
     for li in range(n_layers):
         lb = dict(gate=B.private(NR * gb), up=B.private(NR * gb), down=B.private(NR * db),
                   s_gate=B.private(NS * sgb), s_up=B.private(NS * sgb), s_down=B.private(NS * sdb))
-        B.synth(Q2_K, lb["gate"], NR * I * H // 256, 100 * li + 1)
-        B.synth(Q2_K, lb["up"], NR * I * H // 256, 100 * li + 2)
-        B.synth(Q3_K, lb["down"], NR * H * I // 256, 100 * li + 3)
-        B.synth(Q4_K, lb["s_gate"], NS * I * H // 256, 100 * li + 4)
-        B.synth(Q4_K, lb["s_up"], NS * I * H // 256, 100 * li + 5)
-        B.synth(Q4_K, lb["s_down"], NS * H * I // 256, 100 * li + 6)
+        B.synth(tg, lb["gate"], NR * I * H // GEOM[tg][0], 100 * li + 1)
+        B.synth(tg, lb["up"], NR * I * H // GEOM[tg][0], 100 * li + 2)
+        B.synth(td, lb["down"], NR * H * I // GEOM[td][0], 100 * li + 3)
+        B.synth(tsg, lb["s_gate"], NS * I * H // GEOM[tsg][0], 100 * li + 4)
+        B.synth(tsg, lb["s_up"], NS * I * H // GEOM[tsg][0], 100 * li + 5)
+        B.synth(tsd, lb["s_down"], NS * H * I // GEOM[tsd][0], 100 * li + 6)
         rw = (rng.standard_normal((NR + NS, H)) * 0.02).astype(np.float32)
         rb = rng.uniform(-0.1, 0.1, NR).astype(np.float32)
         for key, arr in (("rw", rw), ("rb", rb)):
@@ -360,21 +369,21 @@ def build_moe_layers(B, n_layers):
         host_router.append((rw, rb))
         d = hip.MoeLayerDesc(hidden=H, inter=I, n_routed=NR, n_shared=NS, topk=6, route_scale=8.0,
                              global_scale=1.0, router_w=lb["rw"], router_bias=lb["rb"])
-        d.gate, d.up, d.down = hip.ExpertTensor(lb["gate"], 0, gb, Q2_K), hip.ExpertTensor(lb["up"], 0, gb, Q2_K), \
-            hip.ExpertTensor(lb["down"], 0, db, Q3_K)
-        d.s_gate, d.s_up, d.s_down = hip.ExpertTensor(lb["s_gate"], 0, sgb, Q4_K), \
-            hip.ExpertTensor(lb["s_up"], 0, sgb, Q4_K), hip.ExpertTensor(lb["s_down"], 0, sdb, Q4_K)
+        d.gate, d.up, d.down = hip.ExpertTensor(lb["gate"], 0, gb, tg), hip.ExpertTensor(lb["up"], 0, gb, tg), \
+            hip.ExpertTensor(lb["down"], 0, db, td)
+        d.s_gate, d.s_up, d.s_down = hip.ExpertTensor(lb["s_gate"], 0, sgb, tsg), \
+            hip.ExpertTensor(lb["s_up"], 0, sgb, tsg), hip.ExpertTensor(lb["s_down"], 0, sdb, tsd)
         layers.append((d, lb))
-    return layers, host_router, (H, I, NR, NS, gb, db, sgb, sdb)
+    return layers, host_router, (H, I, NR, NS, gb, db, sgb, sdb, types)
 
 
 def layer_spec(B, lb, host_router, sizes, experts):
     """Oracle spec of a layer with the bytes of the given routed experts and the shared ones."""
-    H, I, NR, NS, gb, db, sgb, sdb = sizes
+    H, I, NR, NS, gb, db, sgb, sdb, (tg, td, tsg, tsd) = sizes
     rw, rb = host_router
     spec = dict(hidden=H, inter=I, n_routed=NR, n_shared=NS, topk=6, route_scale=8.0, global_scale=1.0,
-                router_w=rw, router_bias=rb, t_gate=Q2_K, t_up=Q2_K, t_down=Q3_K, ts_gate=Q4_K, ts_up=Q4_K,
-                ts_down=Q4_K, gate=[None] * NR, up=[None] * NR, down=[None] * NR,
+                router_w=rw, router_bias=rb, t_gate=tg, t_up=tg, t_down=td, ts_gate=tsg, ts_up=tsg,
+                ts_down=tsd, gate=[None] * NR, up=[None] * NR, down=[None] * NR,
                 s_gate=[B.fetch(lb["s_gate"], s * sgb, sgb) for s in range(NS)],
                 s_up=[B.fetch(lb["s_up"], s * sgb, sgb) for s in range(NS)],
                 s_down=[B.fetch(lb["s_down"], s * sdb, sdb) for s in range(NS)])
@@ -401,12 +410,13 @@ def check_selection(oracle, logits, rb, n_routed, n_shared, topk, idx_gpu, what)
     return np.asarray(idx_gpu, dtype=np.int32)
 
 
-def run_c3(B, warmup, steps, cpu_seconds, n_layers=8):
+def run_c3(B, warmup, steps, cpu_seconds, n_layers=8, types=C3_TYPES, what="C3"):
     """full MoE decode layer, 256 routed (Q2_K/Q3_K) + 2 shared (Q4_K)
-    experts resident, f32 router [258, 6144], top-6, no host round trip."""
+    experts resident, f32 router [258, 6144], top-6, no host round trip. types: the layer's
+    formats (routed gate/up, routed down, shared gate/up, shared down), e.g. REAL_TYPES."""
     L = B.L
-    layers, host_router, sizes = build_moe_layers(B, n_layers)
-    H, I, NR, NS, gb, db, sgb, sdb = sizes
+    layers, host_router, sizes = build_moe_layers(B, n_layers, types)
+    H, I, NR, NS, gb, db, sgb, sdb, _ = sizes
     nx = 64
     xh, xs = B.vectors(H, nx, 41)
     y = B.private(H * 4)
@@ -436,13 +446,13 @@ def run_c3(B, warmup, steps, cpu_seconds, n_layers=8):
     idx = B.dev.download(route, 6, dtype=np.int32)
     rw, rb = host_router[0]
     logits = oracle.linear_f32(rw, xh[0])
-    chosen = check_selection(oracle, logits, rb, NR, NS, 6, idx, "C3")
+    chosen = check_selection(oracle, logits, rb, NR, NS, 6, idx, what)
     spec = layer_spec(B, lb, host_router[0], sizes, idx)
     want, _, _, _ = oracle.moe_layer(spec, xh[0], force_idx=chosen, threads=nthr)
     err = float(np.max(np.abs(y_gpu - want)))
     scale = float(np.max(np.abs(want)))
     if err > 1e-4 * scale:
-        raise RuntimeError("C3 parity: max|diff| %g > 1e-4 * %g" % (err, scale))
+        raise RuntimeError("%s parity: max|diff| %g > 1e-4 * %g" % (what, err, scale))
     s1, n1 = cpu_sample(lambda: oracle.moe_layer(spec, xh[0], force_idx=chosen, threads=1), cpu_seconds, 100)
     sN, nN = cpu_sample(lambda: oracle.moe_layer(spec, xh[0], force_idx=chosen, threads=nthr), cpu_seconds / 4, 100)
     B.dev.free(route)
@@ -468,7 +478,7 @@ def run_c5(B, warmup, steps, cpu_seconds, T=512):
     2 shared experts resident, x ~ N(0,1) rounded to bf16-representable f32."""
     L = B.L
     layers, host_router, sizes = build_moe_layers(B, 1)
-    H, I, NR, NS, gb, db, sgb, sdb = sizes
+    H, I, NR, NS, gb, db, sgb, sdb, _ = sizes
     d, lb = layers[0]
     rng = np.random.default_rng(55)
     X = rng.standard_normal((T, H)).astype(np.float32)
@@ -532,7 +542,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--only", choices=["c3", "c2", "c1", "c4", "c5", "copy"], default=None,
+    ap.add_argument("--only", choices=["c3", "real", "c2", "c1", "c4", "c5", "copy"], default=None,
                     help="run one configuration (profiling runs; 'copy': the library's f32 copy kernel over "
                          "256 MiB, the reference for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE); default: all")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
@@ -554,6 +564,15 @@ def main():
         res = run_c3(B, args.warmup, args.steps, min(8.0, args.cpu_seconds))
         log("C3 %.2f us/token %.1f GB/s (%.1f%%) in %.0fs" % (res["us_per_token"], res["gbs"],
                                                               100 * res["gbs"] / HBM_PEAK_GBS, time.time() - t0))
+    if args.only in (None, "real"):
+        t1 = time.time()
+        r = run_c3(B, args.warmup, args.steps, min(4.0, args.cpu_seconds), types=REAL_TYPES, what="C3 real types")
+        r["workload"] = ("C3 shape with the real checkpoint's most common formats: IQ2_XS gate/up, IQ3_XXS down "
+                         "(256 routed), Q5_K gate/up and Q6_K down (2 shared); 8 layers rotated")
+        extra["C3_real_iq2xs_iq3xxs_q5k_q6k"] = r
+        log("C3 real types %.2f us/token %.1f GB/s (%.1f%%) in %.0fs" % (r["us_per_token"], r["gbs"],
+                                                                         100 * r["gbs"] / HBM_PEAK_GBS,
+                                                                         time.time() - t1))
     if args.only in (None, "c2"):
         extra["C2_expert_ffn"] = run_c2(B, args.warmup, args.steps, min(4.0, args.cpu_seconds))
         log("C2", json.dumps(extra["C2_expert_ffn"]))

@@ -662,6 +662,10 @@ template <> struct MQ<ST_Q4_K> {
 // codebook sits in LDS (MqCtx::tab). Both block sizes leave every other
 // block 2 bytes past a 4-byte boundary: the lane fetches W words from the
 // boundary at or below (shift 0 or 2) and realigns as Q3_K does.
+// The last word of a fetch comes from the end of the window (overlapping
+// the word before), so a window ends at its block's end when the block is 2
+// bytes off a boundary (the last block of a row always is) and 2 bytes after
+// it otherwise: no bytes of the next block are read twice.
 // Signs: bit j of the sign byte negates weight j (iq_signs adds the parity
 // bit); four bits become four 0x00 / 0xFF byte masks by the spread
 // s * 0x00204081, and a byte is negated as (g ^ m) + (m & 1) (no carries:
@@ -687,17 +691,21 @@ template <> struct MQ<ST_IQ2_XS> {
     static constexpr uint32_t table_bytes = 512 * 8;
     static constexpr bool has_pre = false;
     __device__ static uint32_t shift(uint32_t boff) { return boff & 3u; }
-    __device__ static uint32_t word(int k) { return 16u * (uint32_t)k; }
+    // window bytes 0..75: words at 0, 16, 32, 48 and 60
+    __device__ static uint32_t word(int k) { return k < 4 ? 16u * (uint32_t)k : 60u; }
     __device__ static float block(const uint4 (&w)[W], uint32_t sh, const MqCtx &x) {
-        uint32_t raw[4 * W + 1];
+        uint32_t raw[20];
 #pragma unroll
-        for (int k = 0; k < W; k++) {
+        for (int k = 0; k < 4; k++) {
             raw[4 * k] = w[k].x;
             raw[4 * k + 1] = w[k].y;
             raw[4 * k + 2] = w[k].z;
             raw[4 * k + 3] = w[k].w;
         }
-        raw[4 * W] = 0u;
+        raw[16] = w[4].y;   // window dwords 16..18 (w[4].x repeats dword 15)
+        raw[17] = w[4].z;
+        raw[18] = w[4].w;
+        raw[19] = 0u;
         auto L = [&](int m) { return __builtin_amdgcn_alignbyte(raw[m + 1], raw[m], sh); };
         const float d = mq_half_lo(L(0));
         // scales bytes 66..73: the 8 nibble pairs
@@ -735,17 +743,19 @@ template <> struct MQ<ST_IQ3_XXS> {
     static constexpr uint32_t table_bytes = 256 * 4;
     static constexpr bool has_pre = false;
     __device__ static uint32_t shift(uint32_t boff) { return boff & 3u; }
-    __device__ static uint32_t word(int k) { return 16u * (uint32_t)k; }
+    // window bytes 0..99: words at 0, 16, ..., 80 and 84
+    __device__ static uint32_t word(int k) { return k < 6 ? 16u * (uint32_t)k : 84u; }
     __device__ static float block(const uint4 (&w)[W], uint32_t sh, const MqCtx &x) {
-        uint32_t raw[4 * W + 1];
+        uint32_t raw[26];
 #pragma unroll
-        for (int k = 0; k < W; k++) {
+        for (int k = 0; k < 6; k++) {
             raw[4 * k] = w[k].x;
             raw[4 * k + 1] = w[k].y;
             raw[4 * k + 2] = w[k].z;
             raw[4 * k + 3] = w[k].w;
         }
-        raw[4 * W] = 0u;
+        raw[24] = w[6].w;   // window dword 24 (w[6].x .. .z repeat dwords 21..23)
+        raw[25] = 0u;
         auto L = [&](int m) { return __builtin_amdgcn_alignbyte(raw[m + 1], raw[m], sh); };
         const float d = mq_half_lo(L(0));
         float acc = 0.0f;
