@@ -130,8 +130,9 @@ void *sepia_hip_stream(void);
 
 /* Kernel-selection switches for tests and tuning (returns 1 if name and
  * value are known):
- *   "mq" 1/0      the matrix-core kernels for Q2_K/Q3_K/Q4_K and, in the
- *                 matvec, IQ2_XS/IQ3_XXS (default 1);
+ *   "mq" 1/0      the matrix-core kernels (matvec and expert FFN) for
+ *                 Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q8_0, IQ2_XS, IQ3_XXS and
+ *                 IQ4_XS (default 1);
  *   "tile" 1/0    the tile kernels where the matrix-core ones do not apply
  *                 (0 = the generic one-wave-per-row kernels);
  *   "tile_t" 0..  automatic or forced row steps per tile workgroup;
@@ -141,8 +142,10 @@ void *sepia_hip_stream(void);
  *                 planner's choice, 1 = loads from global memory, 2 = LDS
  *                 DMA issued ahead of the weight prologue, 3 = converter
  *                 waves (DMA into the XQ place, converted there while the
- *                 other waves decode their first step; matvec launches
- *                 only);
+ *                 other waves issue and decode their first step);
+ *   "mq_scope" 0..3  the mq_p/mq_c/mq_s/mq_x overrides apply to every
+ *                 matrix-core launch (0) or only to the matvec (1), the
+ *                 expert FFN's gate/up (2) or its down (3) launches;
  *   "pf_reg" 1/0  prefill gate/up and down of layers whose projections are
  *                 all Q2_K/Q3_K/Q4_K with the codes decoded into registers
  *                 (1, default), or on the LDS-tile kernels (0);

@@ -50,6 +50,22 @@ __device__ __forceinline__ float f16_bits_to_f32_exact(uint32_t h) {
     return __builtin_bit_cast(float, out);
 }
 
+// Kernel entry: one scalar load from each 64-byte line of the first BYTES
+// of the kernarg segment, all waited for at once. A kernel that reads its
+// arguments lazily (inside branches, a few at a time) otherwise waits one
+// memory round trip per dependent group of them, since the segment is not
+// in the scalar cache when the kernel starts; afterwards those loads hit.
+// BYTES must not exceed the kernel's kernarg segment.
+template <int BYTES>
+__device__ __forceinline__ void sepia_kernarg_warm() {
+    const __attribute__((address_space(4))) uint32_t *ka =
+        (const __attribute__((address_space(4))) uint32_t *)__builtin_amdgcn_kernarg_segment_ptr();
+    uint32_t acc = 0;
+#pragma unroll
+    for (int o = 0; o < BYTES; o += 64) acc ^= ka[o / 4];
+    asm volatile("" : : "s"(acc));
+}
+
 // Sum over the 64 lanes of a wave; every lane gets the total.
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

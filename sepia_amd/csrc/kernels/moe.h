@@ -36,6 +36,7 @@ extern "C" __global__ __launch_bounds__(RT_NT) void sepia_moe_route(
     int64_t hidden, int32_t n_routed, int32_t n_shared, int32_t topk, float route_scale, float global_scale,
     float *__restrict__ logits, int32_t *__restrict__ sel_idx, float *__restrict__ sel_w,
     uint32_t *__restrict__ counter, int32_t select) {
+    sepia_kernarg_warm<320>();
     __shared__ float part[RT_NT / SEPIA_WAVE][RT_ROWS];
     __shared__ int last;
     const int n_tot = n_routed + n_shared;

@@ -1172,9 +1172,17 @@ struct MqItem {
 // nw: the stepping waves (C x P); a launch may run more waves than that
 // (its other kind of workgroup needs more), which then take no items and no
 // ring.
+// C: items side by side (nw / P); S: ring stages, min(4, ring / Wp KB);
+// step: the stride between a workgroup's items (the launch's workgroups per
+// slot, or the matvec's grid). mP, mC, mstep: their reciprocals for mq_div,
+// computed by the host, so that no wave runs a division sequence.
 struct MqGeo {
     int32_t P, ring, xraw, orings, conv, nw;
+    int32_t C, S, step;
+    uint32_t mP, mC, mstep;
 };
+// floor(n / d) for n < 2^31 / d, with m = ceil(2^31 / d) from the host.
+__device__ __forceinline__ uint32_t mq_div(uint32_t n, uint32_t m) { return (uint32_t)(((uint64_t)n * m) >> 31); }
 
 // The pipeline of one wave over n_items items of format T, in two halves:
 // prologue() issues the first S stages (before the workgroup stages its XQ
@@ -1194,25 +1202,23 @@ struct MqWave {
     int ik, im, islot;         // issue cursor: item, quad, ring slot
     const uint8_t *tab = nullptr;   // codebook in LDS (IQ formats)
 
-    // Waves first, first + 1, ... (count of them, or all the rest) share the
-    // items as C = count / P columns of P parts; waves outside them and past
-    // the last full column get none. Wave first + k keeps ring k.
+    // Waves first, first + 1, ..., first + geo.nw - 1 share the items as
+    // geo.C columns of geo.P parts; other waves get none. Wave first + k
+    // keeps ring k.
     __device__ __forceinline__ MqWave(const ItemFn &f, int n_items_, int nq_, int n_, uint32_t rb_, MqGeo geo,
-                                      uint8_t *ring_lds, int first = 0, int count = -1)
+                                      uint8_t *ring_lds, int first = 0)
         : item_of(f), n_items(n_items_), nq(nq_), n(n_), rb(rb_) {
         const int w = mq_wave_id(), wk = w - first;
-        const int nw = count >= 0 ? count : (int)(blockDim.x >> 6) - first;
         P = geo.P;
-        S = geo.ring / (Wp * 1024);
-        S = S < 4 ? S : 4;
-        C = nw / P;
-        c = wk >= 0 ? wk / P : 0;
+        S = geo.S;
+        C = geo.C;
+        c = wk >= 0 ? (int)mq_div((uint32_t)wk, geo.mP) : 0;
         p = wk - c * P;
         ringp = ring_lds + (ptrdiff_t)wk * geo.ring;
         ring = mq_lds_addr(ringp);
         L = mq_lane();
-        const int ni = (wk >= 0 && wk < C * P && n_items > c) ? (n_items - c + C - 1) / C : 0;
-        nqw = nq > p ? (nq - p + P - 1) / P : 0;
+        const int ni = (wk >= 0 && wk < C * P && n_items > c) ? (int)mq_div((uint32_t)(n_items - c + C - 1), geo.mC) : 0;
+        nqw = nq > p ? (int)mq_div((uint32_t)(nq - p + P - 1), geo.mP) : 0;
         Tn = ni * nqw;
         ik = im = islot = 0;
     }
@@ -1256,6 +1262,10 @@ struct MqWave {
     // x_issued: the caller already DMA'd the vector into the raw copy (a
     // mode-1 geometry) before work of its own, e.g. the expert selection.
     bool x_issued = false;
+    // xq_ready: the workgroup already holds the XQ vector (converted in
+    // place while wave 0 selected the experts); go() then only issues the
+    // prologue and runs.
+    bool xq_ready = false;
     __device__ __forceinline__ void start(const float *src, const MqGeo &geo, uint8_t *lds0, uint32_t xoff) {
         if (geo.xraw) {
             if (!x_issued) mq_dma_vec(src, n, mq_lds_addr(lds0 + geo.xraw));
@@ -1314,6 +1324,13 @@ struct MqWave {
     // for its own pipeline.
     template <bool CONV = true>
     __device__ __forceinline__ void go(const float *src, const MqGeo &geo, uint8_t *lds0, uint32_t xoff, float *red) {
+        if (xq_ready) {
+            prologue();
+            // a codebook the caller wrote after the vector's barrier
+            if constexpr (MQ<T>::table_bytes > 0) __syncthreads();
+            run(lds0, red);
+            return;
+        }
         if (!CONV || geo.conv == 0) {
             start(src, geo, lds0, xoff);
             run(lds0, red);
@@ -1425,8 +1442,8 @@ __device__ __forceinline__ void mq_mv(const uint8_t *__restrict__ W, uint64_t ro
                                       const float *__restrict__ x, float *__restrict__ y, MqGeo geo) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int n = 256 * nb;
-    const int64_t tiles = (rows + 15) >> 4, G = gridDim.x;
-    const int nk = tiles > blockIdx.x ? (int)((tiles - blockIdx.x + G - 1) / G) : 0;
+    const int64_t tiles = (rows + 15) >> 4, G = geo.step;   // the grid
+    const int nk = tiles > blockIdx.x ? (int)mq_div((uint32_t)(tiles - blockIdx.x + G - 1), geo.mstep) : 0;
     const uint32_t xoff = MQ_ZERO;
     uint8_t *tab = smem + xoff + mq_xq_bytes(n);   // codebook (IQ formats), then the row sums
     float *red = (float *)(tab + MQ<T>::table_bytes);
@@ -1441,7 +1458,7 @@ __device__ __forceinline__ void mq_mv(const uint8_t *__restrict__ W, uint64_t ro
         it.red = i;
         return it;
     };
-    MqWave<T, decltype(item_of)> wv(item_of, nk, nb >> 2, n, (uint32_t)row_bytes, geo, rings, 0, geo.nw);
+    MqWave<T, decltype(item_of)> wv(item_of, nk, nb >> 2, n, (uint32_t)row_bytes, geo, rings, 0);
     wv.tab = tab;
     wv.go(x, geo, smem, xoff, red);   // its first barrier also publishes the codebook
     __syncthreads();
@@ -1455,6 +1472,7 @@ __device__ __forceinline__ void mq_mv(const uint8_t *__restrict__ W, uint64_t ro
     extern "C" __global__ __launch_bounds__(1024) void sepia_mq_mv_##name(                               \
         const uint8_t *__restrict__ W, uint64_t row_bytes, int64_t rows, int32_t nb,                      \
         const float *__restrict__ x, float *__restrict__ y, MqGeo geo) {                                  \
+        sepia_kernarg_warm<320>();                                                                        \
         mq_mv<T>(W, row_bytes, rows, nb, x, y, geo);                                                      \
     }
 
@@ -1480,15 +1498,17 @@ __device__ __forceinline__ int64_t mq_slot_expert(const int32_t *sel_idx, int32_
 // item 2k + 1 the up rows. h[r] = silu(gate_r . x) * (up_r . x) (f32).
 // LDS: [zero][XQ of x][selection: 64 i32 + 64 f32][codebook (IQ formats)]
 //      [red: 2 nk x P x 16 f32][raw x][rings].
-#define MQ_SEL_BYTES 512
+// The selection area: 64 i32 expert indices, 64 f32 weights, 16 bytes of
+// control words.
+#define MQ_SEL_BYTES 528
 template <int T>
 __device__ __forceinline__ void mq_gateup_slot(const uint8_t *Wg, const uint8_t *Wu, uint64_t row_bytes, int32_t nb,
                                                int32_t inter, int32_t j0, int32_t jstep, const float *__restrict__ x,
-                                               float *__restrict__ h, MqGeo geo, bool x_issued) {
+                                               float *__restrict__ h, MqGeo geo, bool x_issued, bool xq_ready) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int n = 256 * nb;
-    const int tiles = (inter + 15) >> 4;
-    const int nk = j0 < tiles ? (tiles - j0 + jstep - 1) / jstep : 0;
+    const int tiles = (inter + 15) >> 4;   // jstep == geo.step
+    const int nk = j0 < tiles ? (int)mq_div((uint32_t)(tiles - j0 + jstep - 1), geo.mstep) : 0;
     const uint32_t xoff = MQ_ZERO;
     uint8_t *tab = smem + xoff + mq_xq_bytes(n) + MQ_SEL_BYTES;   // codebook (IQ formats), then the row sums
     float *red = (float *)(tab + MQ<T>::table_bytes);
@@ -1503,10 +1523,11 @@ __device__ __forceinline__ void mq_gateup_slot(const uint8_t *Wg, const uint8_t 
         it.red = i;
         return it;
     };
-    MqWave<T, decltype(item_of)> wv(item_of, 2 * nk, nb >> 2, n, (uint32_t)row_bytes, geo, rings, 0, geo.nw);
+    MqWave<T, decltype(item_of)> wv(item_of, 2 * nk, nb >> 2, n, (uint32_t)row_bytes, geo, rings, 0);
     wv.x_issued = x_issued;
+    wv.xq_ready = xq_ready;
     wv.tab = tab;
-    wv.template go<false>(x, geo, smem, xoff, red);
+    wv.template go<true>(x, geo, smem, xoff, red);
     __syncthreads();
     for (int i = threadIdx.x; i < nk * 16; i += blockDim.x) {
         const int k = i >> 4, t = i & 15;
@@ -1544,29 +1565,55 @@ __device__ __forceinline__ void mq_gateup(const MqProj &gate, const MqProj &up, 
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const bool rk = bid < topk * wps_r;
     const MqGeo geo = rk ? geo_r : geo_s;
-    const int32_t wps = rk ? wps_r : wps_s;
+    const int32_t wps = rk ? wps_r : wps_s;   // == geo.step
     const int32_t k0 = rk ? bid : bid - topk * wps_r;
-    const int32_t slot = (rk ? 0 : topk) + k0 / wps, j0 = k0 % wps;
+    const int32_t kq = (int32_t)mq_div((uint32_t)k0, geo.mstep);
+    const int32_t slot = (rk ? 0 : topk) + kq, j0 = k0 - kq * wps;
     int64_t e;
-    bool x_issued = false;
-    if (rt.logits && slot < topk) {
-        // the vector does not depend on the selection: with a raw-copy
-        // geometry its DMA goes out first and lands while wave 0 selects
-        if (geo.xraw && geo.conv == 0) {
-            mq_dma_vec(x, (int)(256 * gate.n_blocks), mq_lds_addr(smem + geo.xraw));
+    bool x_issued = false, xq_ready = false;
+    // With the selection in this launch, one workgroup publishes it with its
+    // weights: the first shared one, which has time to spare (its slot needs
+    // no selection), or workgroup 0 without shared experts. The other routed
+    // workgroups select without the weights.
+    const bool publisher = rt.n_shared > 0 ? bid == topk * wps_r : bid == 0;
+    if (rt.logits && (slot < topk || publisher)) {
+        const int n = (int)(256 * gate.n_blocks);
+        int32_t *si = (int32_t *)(smem + MQ_ZERO + mq_xq_bytes(n));
+        float *sw = (float *)(si + 64);
+        uint32_t *ctl = (uint32_t *)(sw + 64);
+        // A routed workgroup's waves 1.. DMA x straight into its XQ place
+        // and convert it there while wave 0 selects, so the weight prologue
+        // is the only thing left once the expert is known.
+        const int conv = (int)blockDim.x - SEPIA_WAVE;
+        xq_ready = slot < topk && conv >= 64 && (n >> 4) <= MQ_XQP * (conv >> 2);
+        if (xq_ready) {
+            if (threadIdx.x == 0) ctl[0] = 0u;
+            __syncthreads();
+            if ((int)threadIdx.x >= SEPIA_WAVE) {
+                mq_xq_dma_by(x, n, smem, MQ_ZERO, SEPIA_WAVE, conv);
+                // the selection is the longer chain: wave 0 goes first
+                __builtin_amdgcn_s_setprio(0);
+            } else {
+                __builtin_amdgcn_s_setprio(3);
+            }
+        } else if (geo.xraw && geo.conv == 0) {
+            // the vector does not depend on the selection: its DMA goes out
+            // first and lands while wave 0 selects
+            mq_dma_vec(x, n, mq_lds_addr(smem + geo.xraw));
             x_issued = true;
         }
-        int32_t *si = (int32_t *)(smem + MQ_ZERO + mq_xq_bytes(256 * gate.n_blocks));
-        float *sw = (float *)(si + 64);
         if (threadIdx.x < SEPIA_WAVE)
             route_pick_any<false>(rt.logits, rt.bias, rt.n_routed, rt.n_shared, topk, rt.route_scale,
-                                  rt.global_scale, si, sw);
+                                  rt.global_scale, si, publisher ? sw : nullptr);
+        else if (xq_ready)
+            mq_xq_in_place_by(n, smem, MQ_ZERO, SEPIA_WAVE, conv, ctl, nullptr);
+        __builtin_amdgcn_s_setprio(0);
         __syncthreads();
-        if (bid == 0 && threadIdx.x < topk + rt.n_shared) {
+        if (publisher && threadIdx.x < topk + rt.n_shared) {
             if ((int)threadIdx.x < topk) rt.idx_out[threadIdx.x] = si[threadIdx.x];
             rt.w_out[threadIdx.x] = sw[threadIdx.x];
         }
-        e = __builtin_amdgcn_readfirstlane(si[slot]);
+        e = slot < topk ? (int64_t)__builtin_amdgcn_readfirstlane(si[slot]) : (int64_t)(slot - topk);
     } else {
         e = mq_slot_expert(sel_idx, fixed, slot, topk);
     }
@@ -1576,7 +1623,7 @@ __device__ __forceinline__ void mq_gateup(const MqProj &gate, const MqProj &up, 
     float *hs = h + (int64_t)slot * inter;
     const int32_t nb = (int32_t)G.n_blocks;
 #define MQ_GU_CASE(T) \
-    case T: mq_gateup_slot<T>(wg, wu, G.row_bytes, nb, inter, j0, wps, x, hs, geo, x_issued); break;
+    case T: mq_gateup_slot<T>(wg, wu, G.row_bytes, nb, inter, j0, wps, x, hs, geo, x_issued, xq_ready); break;
     switch (G.type) {
         MQ_GU_CASE(ST_Q2_K)
         MQ_GU_CASE(ST_Q3_K)
@@ -1586,7 +1633,7 @@ __device__ __forceinline__ void mq_gateup(const MqProj &gate, const MqProj &up, 
         MQ_GU_CASE(ST_IQ2_XS)
         MQ_GU_CASE(ST_IQ3_XXS)
         MQ_GU_CASE(ST_IQ4_XS)
-    default: mq_gateup_slot<ST_Q4_K>(wg, wu, G.row_bytes, nb, inter, j0, wps, x, hs, geo, x_issued); break;
+    default: mq_gateup_slot<ST_Q4_K>(wg, wu, G.row_bytes, nb, inter, j0, wps, x, hs, geo, x_issued, xq_ready); break;
     }
 #undef MQ_GU_CASE
 }
@@ -1596,6 +1643,7 @@ __device__ __forceinline__ void mq_gateup(const MqProj &gate, const MqProj &up, 
         MqProj gate, MqProj up, MqProj s_gate, MqProj s_up, const int32_t *__restrict__ sel_idx,         \
         int32_t fixed, int32_t topk, int32_t inter, int32_t wps_r, int32_t wps_s,                        \
         const float *__restrict__ x, float *__restrict__ h, MqGeo geo_r, MqGeo geo_s, MqRoute rt) {      \
+        sepia_kernarg_warm<512>();                                                                       \
         mq_gateup(gate, up, s_gate, s_up, sel_idx, fixed, topk, inter, wps_r, wps_s, x, h, geo_r, geo_s, \
                   rt, (int32_t)blockIdx.x);                                                              \
     }
@@ -1631,9 +1679,9 @@ __device__ __forceinline__ void mq_dn_slot(const uint8_t *Wd, uint64_t row_bytes
         it.red = i;
         return it;
     };
-    MqWave<T, decltype(item_of)> wv(item_of, nk, nb >> 2, inter, (uint32_t)row_bytes, geo, rings, 0, geo.nw);
+    MqWave<T, decltype(item_of)> wv(item_of, nk, nb >> 2, inter, (uint32_t)row_bytes, geo, rings, 0);
     wv.tab = tab;
-    wv.template go<false>(hs, geo, lds0, MQ_ZERO, red);
+    wv.template go<true>(hs, geo, lds0, MQ_ZERO, red);
 }
 
 __device__ __forceinline__ void mq_down(const MqProj &down, const MqProj &s_down, const int32_t *__restrict__ sel_idx,
@@ -1645,14 +1693,15 @@ __device__ __forceinline__ void mq_down(const MqProj &down, const MqProj &s_down
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const bool routed = bid < topk * wps_r;
     const MqGeo geo = routed ? geo_r : geo_s;
-    const int32_t jstep = routed ? wps_r : wps_s;
+    const int32_t jstep = routed ? wps_r : wps_s;   // == geo.step
     const int32_t k0 = routed ? bid : bid - topk * wps_r;
-    const int32_t slot = (routed ? 0 : topk) + k0 / jstep, j0 = k0 % jstep;
+    const int32_t kq = (int32_t)mq_div((uint32_t)k0, geo.mstep);
+    const int32_t slot = (routed ? 0 : topk) + kq, j0 = k0 - kq * jstep;
     const int64_t e = mq_slot_expert(sel_idx, fixed, slot, topk);
     const MqProj &Pj = routed ? down : s_down;
     const uint8_t *Wd = Pj.base + e * Pj.stride;
     const int tiles = (int)((hidden + 15) >> 4);
-    const int nk = j0 < tiles ? (tiles - j0 + jstep - 1) / jstep : 0;
+    const int nk = j0 < tiles ? (int)mq_div((uint32_t)(tiles - j0 + jstep - 1), geo.mstep) : 0;
     const size_t o_red = MQ_ZERO + mq_xq_bytes(inter) + mq_table_bytes(Pj.type);
     float *red = (float *)(smem + o_red);
     int32_t *flag = (int32_t *)(smem + o_red + (size_t)nk * geo.P * 64);
@@ -1719,6 +1768,7 @@ __device__ __forceinline__ void mq_down(const MqProj &down, const MqProj &s_down
         int32_t fixed, int32_t topk, int32_t n_count, int32_t n_sum, int32_t inter, int64_t hidden,      \
         const float *__restrict__ h, float *__restrict__ y, MqGeo geo_r, MqGeo geo_s, int32_t wps_r,     \
         int32_t wps_s, float *__restrict__ ypart, uint32_t *__restrict__ cnt) {                          \
+        sepia_kernarg_warm<448>();                                                                       \
         mq_down(down, s_down, sel_idx, sel_w, fixed, topk, n_count, n_sum, inter, hidden, h, y, geo_r,   \
                 geo_s, wps_r, wps_s, ypart, cnt, (int32_t)blockIdx.x);                                   \
     }

@@ -52,6 +52,7 @@ __device__ __forceinline__ double lanes_sum_f64(double v, int n) {
 // idx[k], lane k < topk + n_shared writes w[k] (idx and w may point to LDS
 // or global memory). ATOMIC: the logits come from other workgroups of the
 // same launch (agent-scope loads). n_routed <= 64 * EM, topk <= 64 - n_shared.
+// w NULL: the selection only (idx), without the weights' log-sum-exp.
 template <int EM, bool ATOMIC>
 __device__ void route_pick(const float *logits, const float *__restrict__ bias, int32_t n_routed, int32_t n_shared,
                            int32_t topk, float route_scale, float global_scale, int32_t *idx, float *w) {
@@ -98,6 +99,10 @@ __device__ void route_pick(const float *logits, const float *__restrict__ bias, 
             my_pick = win_lane * E + win_j;
             my_raw = raw;
         }
+    }
+    if (!w) {
+        if (lane < topk) idx[lane] = my_pick;
+        return;
     }
     const bool on = lane < n_sel;
     const float raw = on ? ((lane < topk) ? my_raw : sink) : 0.0f;

@@ -138,6 +138,9 @@ static int g_opt_mq = 1;     /* sepia_hip_set_option("mq", 0) disables the matri
  * workgroup geometry (parts per item, item lanes, ring stages of the largest
  * format; 0 = planned) */
 static int g_opt_mq_p = 0, g_opt_mq_c = 0, g_opt_mq_s = 0;
+static int g_opt_mq_scope = 0;     /* "mq_scope": the mq_p/mq_c/mq_s/mq_x overrides apply to every matrix-core
+                                    * launch (0) or only to the matvec (1), gate/up (2) or down (3) launches */
+static int g_mq_kind = 0;          /* the launch kind mq_geo is planning: 1 matvec, 2 gate/up, 3 down */
 static int g_opt_mq_x = 0;   /* "mq_x": 0 = planner's choice, 1 = vector from global, 2 = vector by LDS DMA,
                               * 3 = converter waves */
 static int g_opt_pf_route_m = 1;   /* "pf_route_m": 1 = prefill router logits on the f32 matrix cores
@@ -1093,6 +1096,10 @@ int sepia_hip_set_option(const char *name, int value) {
         g_opt_pf_route_m = value;
         return 1;
     }
+    if (strcmp(name, "mq_scope") == 0 && value >= 0 && value <= 3) {
+        g_opt_mq_scope = value;
+        return 1;
+    }
     if (strcmp(name, "mq_p") == 0 && value >= 0 && value <= 16) {
         g_opt_mq_p = value;
         return 1;
@@ -1125,7 +1132,17 @@ int sepia_hip_set_option(const char *name, int value) {
 #define MQ_ZERO 768
 typedef struct {
     int32_t P, ring, xraw, orings, conv, nw;   /* as struct MqGeo in kernels/mq.h */
+    int32_t C, S, step;                        /* items side by side, ring stages, workgroup stride of the items */
+    uint32_t mP, mC, mstep;                    /* mq_recip of P, C and step */
 } MqGeo;
+/* m with floor(n / d) = (n * m) >> 31 for every n < 2^31 / d (mq_div in
+ * kernels/mq.h): the kernels divide by the launch's P, C and stride this
+ * way instead of running a division sequence in every wave. */
+static uint32_t mq_recip(int64_t d) { return (uint32_t)(((1ull << 31) + (uint64_t)d - 1) / (uint64_t)d); }
+static void mq_geo_step(MqGeo *g, int64_t step) {
+    g->step = (int32_t)step;
+    g->mstep = mq_recip(step);
+}
 /* In-kernel selection by the gate/up launch (struct MqRoute in
  * kernels/mq.h); logits NULL: the experts come from sel_idx. */
 typedef struct {
@@ -1136,7 +1153,7 @@ typedef struct {
     int32_t *idx_out;
     float *w_out;
 } MqRoute;
-#define MQ_SEL_BYTES 512            /* the gate/up kernel's selection area in LDS */
+#define MQ_SEL_BYTES 528            /* the gate/up kernel's selection area in LDS (MQ_SEL_BYTES in kernels/mq.h) */
 #define MQ_XDMA_GAIN 40             /* mq_geo: cost units the vector's LDS DMA saves (measured ~2 us a launch) */
 #define MQ_CONV_GAIN 60             /* mq_geo: cost units converter waves save (XQ off the weights' path); by
                                      * default only for the IQ formats, where they measured faster (C4 IQ3_XXS
@@ -1198,13 +1215,19 @@ static int mq_geo(int mc, int wmax, int64_t n_items, int64_t nq, size_t fixed, s
     const int64_t segs = (int64_t)raw_bytes / 64, cv_need = (segs + MQ_XQ_SEGS_PER_WAVE - 1) / MQ_XQ_SEGS_PER_WAVE;
     /* a forced mode the launch cannot take (converter waves for the FFN
      * launches) leaves the choice to the planner */
-    const int forced = (g_opt_mq_x == 3 && !allow_conv) ? 0 : g_opt_mq_x;
+    const int ovr = !g_opt_mq_scope || g_opt_mq_scope == g_mq_kind;
+    const int opt_p = ovr ? g_opt_mq_p : 0, opt_c = ovr ? g_opt_mq_c : 0, opt_s = ovr ? g_opt_mq_s : 0;
+    const int forced = !ovr || (g_opt_mq_x == 3 && !allow_conv) ? 0 : g_opt_mq_x;
     for (int mode = 0; mode <= (raw_bytes > 0 ? (allow_conv ? 2 : 1) : 0); mode++) {
-        if (raw_bytes > 0 && (forced ? forced != mode + 1 : (mode == 2 && !k_mq_conv[mc]))) continue;
+        /* converter waves by default only in the matvecs of the formats that
+         * gain from them; the FFN launches measured slower with them (the
+         * IQ3_XXS down of a real-format layer 34.9 vs 31.1 us) */
+        if (raw_bytes > 0 && (forced ? forced != mode + 1 : (mode == 2 && !(k_mq_conv[mc] && g_mq_kind == 1))))
+            continue;
         for (int P = 1; P <= 16 && P <= nq; P++) {
-            if (g_opt_mq_p && P != g_opt_mq_p) continue;
+            if (opt_p && P != opt_p) continue;
             for (int C = 1; C * P <= 16 && C <= n_items; C++) {
-                if (g_opt_mq_c && C != g_opt_mq_c) continue;
+                if (opt_c && C != opt_c) continue;
                 const int nw = C * P;
                 int cv = 0;
                 if (mode == 2) {
@@ -1218,8 +1241,8 @@ static int mq_geo(int mc, int wmax, int64_t n_items, int64_t nq, size_t fixed, s
                 if (base + (size_t)nw * wm > g_lds_max) continue;
                 size_t ring = ((g_lds_max - base) / (size_t)nw) & ~(size_t)1023;
                 if (ring > 4 * wm) ring = 4 * wm;
-                if (g_opt_mq_s) {
-                    ring = (size_t)g_opt_mq_s * wm;
+                if (opt_s) {
+                    ring = (size_t)opt_s * wm;
                     if (base + (size_t)nw * ring > g_lds_max) continue;
                 }
                 int64_t S = (int64_t)(ring / w1);
@@ -1242,6 +1265,11 @@ static int mq_geo(int mc, int wmax, int64_t n_items, int64_t nq, size_t fixed, s
                     geo->orings = (int32_t)base;
                     geo->conv = cv;
                     geo->nw = nw;
+                    geo->C = C;
+                    geo->S = (int32_t)(ring / w1 < 4 ? ring / w1 : 4);
+                    geo->mP = mq_recip(P);
+                    geo->mC = mq_recip(C);
+                    mq_geo_step(geo, 1);
                     *threads = 64u * (unsigned)(nw + cv);
                     *lds = base + (size_t)nw * ring;
                 }
@@ -1268,9 +1296,11 @@ static int mq_plan(int type, int64_t n_blocks, int64_t rows, uintptr_t base, uin
     const int64_t tiles = (rows + 15) / 16;
     const int64_t per = (tiles + MQ_CUS - 1) / MQ_CUS;     /* row groups per workgroup */
     *grid = (unsigned)((tiles + per - 1) / per);
+    g_mq_kind = 1;
     if (!mq_geo(mc, k_mq_words[mc], per, n_blocks / 4, MQ_ZERO + mq_xq_bytes(256 * n_blocks) + k_mq_table[mc],
                 (size_t)1024 * n_blocks, 1, threads, geo, lds))
         return -1;
+    mq_geo_step(geo, *grid);
     return K_MQ_MV + mc;
 }
 
@@ -1540,12 +1570,13 @@ static void mq_split(int32_t topk, int32_t n_shared, double br, double bs, int64
 /* One launch's two geometries (routed and shared workgroups) and the
  * launch's thread count and LDS (the larger of the two). */
 static int mq_geo2(int mc_r, int mc_s, int has_s, int64_t items_r, int64_t items_s, int64_t nq, size_t fixed_r,
-                   size_t fixed_s, size_t raw_bytes, unsigned *threads, MqGeo *geo_r, MqGeo *geo_s, size_t *lds) {
+                   size_t fixed_s, size_t raw_r, size_t raw_s, unsigned *threads, MqGeo *geo_r, MqGeo *geo_s,
+                   size_t *lds) {
     unsigned tr, ts = 0;
     size_t lr, ls = 0;
-    if (!mq_geo(mc_r, k_mq_words[mc_r], items_r, nq, fixed_r, raw_bytes, 0, &tr, geo_r, &lr)) return 0;
+    if (!mq_geo(mc_r, k_mq_words[mc_r], items_r, nq, fixed_r, raw_r, 1, &tr, geo_r, &lr)) return 0;
     if (has_s) {
-        if (!mq_geo(mc_s, k_mq_words[mc_s], items_s, nq, fixed_s, raw_bytes, 0, &ts, geo_s, &ls)) return 0;
+        if (!mq_geo(mc_s, k_mq_words[mc_s], items_s, nq, fixed_s, raw_s, 1, &ts, geo_s, &ls)) return 0;
     } else {
         *geo_s = *geo_r;
     }
@@ -1553,8 +1584,12 @@ static int mq_geo2(int mc_r, int mc_s, int has_s, int64_t items_r, int64_t items
     *lds = lr > ls ? lr : ls;
     return 1;
 }
+/* route: the gate/up launch selects the experts itself; its routed
+ * workgroups then convert x into its XQ place during the selection and
+ * need no raw copy of it. */
 static int mq_ffn_plan(const MoeProj *g, const MoeProj *u, const MoeProj *d, const MoeProj *sg, const MoeProj *su,
-                       const MoeProj *sd, int32_t topk, int32_t n_shared, int64_t H, int64_t I, MqFfnPlan *pl) {
+                       const MoeProj *sd, int32_t topk, int32_t n_shared, int64_t H, int64_t I, int route,
+                       MqFfnPlan *pl) {
     if (!g_opt_mq || H % 1024 || I % 1024) return 0;
     const MoeProj *ps[6] = { g, u, d, sg, su, sd };
     const int64_t rows[6] = { I, I, H, I, I, H };
@@ -1573,14 +1608,25 @@ static int mq_ffn_plan(const MoeProj *g, const MoeProj *u, const MoeProj *d, con
     const int64_t nk_gr = (tiles_i + pl->gu_wps_r - 1) / pl->gu_wps_r, nk_gs = (tiles_i + pl->gu_wps_s - 1) / pl->gu_wps_s;
     const int64_t nk_dr = (tiles_h + pl->dn_wps_r - 1) / pl->dn_wps_r, nk_ds = (tiles_h + pl->dn_wps_s - 1) / pl->dn_wps_s;
     const size_t gu_fixed = MQ_ZERO + mq_xq_bytes(H) + MQ_SEL_BYTES;
+    g_mq_kind = 2;
     if (!mq_geo2(kg, ksg, has_s, 2 * nk_gr, 2 * nk_gs, H / 1024, gu_fixed + k_mq_table[kg], gu_fixed + k_mq_table[ksg],
-                 (size_t)H * 4, &pl->gu_threads, &pl->gu_geo_r, &pl->gu_geo_s, &pl->gu_lds))
+                 route ? 0 : (size_t)H * 4, (size_t)H * 4, &pl->gu_threads, &pl->gu_geo_r, &pl->gu_geo_s,
+                 &pl->gu_lds))
         return 0;
+    /* the routed workgroups' in-place conversion needs 3 waves besides the
+     * selecting one (MQ_XQP passes of a quarter of their lanes) */
+    if (route && (int64_t)pl->gu_threads - 64 < (H / 16 + MQ_XQ_SEGS_PER_WAVE - 1) / MQ_XQ_SEGS_PER_WAVE * 64)
+        pl->gu_threads = (unsigned)(((H / 16 + MQ_XQ_SEGS_PER_WAVE - 1) / MQ_XQ_SEGS_PER_WAVE + 1) * 64);
     const size_t dn_fixed = MQ_ZERO + mq_xq_bytes(I) + 256;
+    g_mq_kind = 3;
     if (!mq_geo2(kd, ksd, has_s, nk_dr, nk_ds, I / 1024, dn_fixed + k_mq_table[kd] + (size_t)nk_dr * 4,
-                 dn_fixed + k_mq_table[ksd] + (size_t)nk_ds * 4, (size_t)I * 4, &pl->dn_threads, &pl->dn_geo_r,
-                 &pl->dn_geo_s, &pl->dn_lds))
+                 dn_fixed + k_mq_table[ksd] + (size_t)nk_ds * 4, (size_t)I * 4, (size_t)I * 4, &pl->dn_threads,
+                 &pl->dn_geo_r, &pl->dn_geo_s, &pl->dn_lds))
         return 0;
+    mq_geo_step(&pl->gu_geo_r, pl->gu_wps_r);
+    mq_geo_step(&pl->gu_geo_s, pl->gu_wps_s);
+    mq_geo_step(&pl->dn_geo_r, pl->dn_wps_r);
+    mq_geo_step(&pl->dn_geo_s, pl->dn_wps_s);
     pl->gu_grid = (unsigned)(topk * pl->gu_wps_r + n_shared * pl->gu_wps_s);
     pl->dn_grid = (unsigned)(topk * pl->dn_wps_r + n_shared * pl->dn_wps_s);
     return 1;
@@ -1589,14 +1635,14 @@ static int mq_ffn_plan(const MoeProj *g, const MoeProj *u, const MoeProj *d, con
 /* mq_ffn_plan on copies of the six projections (mp) whose n_blocks count
  * the matrix-core kernels' 256-column blocks. */
 static int mq_ffn_prep(const MoeProj *g, const MoeProj *u, const MoeProj *d, const MoeProj *sg, const MoeProj *su,
-                       const MoeProj *sd, int32_t topk, int32_t n_shared, int64_t H, int64_t I, MoeProj mp[6],
+                       const MoeProj *sd, int32_t topk, int32_t n_shared, int64_t H, int64_t I, int route, MoeProj mp[6],
                        MqFfnPlan *pl) {
     const MoeProj *ps[6] = { g, u, d, sg, su, sd };
     for (int i = 0; i < 6; i++) {
         mp[i] = *ps[i];
         mp[i].n_blocks = mq_nb(mp[i].type, mp[i].n_blocks);
     }
-    return mq_ffn_plan(&mp[0], &mp[1], &mp[2], &mp[3], &mp[4], &mp[5], topk, n_shared, H, I, pl);
+    return mq_ffn_plan(&mp[0], &mp[1], &mp[2], &mp[3], &mp[4], &mp[5], topk, n_shared, H, I, route, pl);
 }
 
 /* LDS of the prefill projection kernels (PF_LDS_BYTES in kernels/prefill.h):
@@ -1755,7 +1801,7 @@ static int ffn_launch(const char *op, const MoeProj *g, const MoeProj *u, const 
     int64_t inter = I, hid = H;
     MqFfnPlan pl;
     MoeProj mp[6];
-    if (mq_ffn_prep(g, u, d, sg, su, sd, topk, n_shared, H, I, mp, &pl)) {
+    if (mq_ffn_prep(g, u, d, sg, su, sd, topk, n_shared, H, I, route != NULL, mp, &pl)) {
         int32_t inter32 = (int32_t)I;
         float *h = (float *)scr;
         float *ypart = (float *)(scr + (size_t)n_slots * (size_t)I * 4);
@@ -1909,7 +1955,7 @@ static int moe_decode_impl(const char *op, const SepiaMoeLayerDesc *L, SepiaGpuB
      * otherwise the router's last workgroup does */
     MqFfnPlan pl;
     MoeProj mp[6];
-    const int in_kernel = mq_ffn_prep(&g, &u, &d, &sg, &su, &sd, tk, ns, H, I, mp, &pl);
+    const int in_kernel = mq_ffn_prep(&g, &u, &d, &sg, &su, &sd, tk, ns, H, I, 1, mp, &pl);
     int32_t select = !in_kernel;
     void *a_route[] = { &rw, &ld, &rb, &x->dev, &hid, &nr, &ns, &tk, &rs, &gsc, &logits, &sel_idx, &sel_w, &counter,
                         &select };
