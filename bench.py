@@ -321,6 +321,78 @@ def run_matvec_rotation(B, name, t, rows, cols, warmup, steps, cpu_seconds, seed
                 cpu_1core_ms=s1 * 1e3, cpu_1core_gbs=mb / s1 / 1e9)
 
 
+def run_store(B, n_routed=32, reps=3):
+    """The on-disk stores into HBM: a C3-shaped MoE layer (n_routed routed Q2_K/Q3_K experts, 2 shared
+    Q4_K, f32 router) written in the reference's formats (GGUF part, sepia-index sidecar, resident.bin +
+    manifest) under a temporary directory, then uploaded through the C ABI: resident.bin whole, the
+    layer's experts into one buffer. GB/s of each upload from the page cache (the files were just
+    written), and the assembled layer's decode against the oracle."""
+    import shutil
+    import tempfile
+    import time
+    import oracle
+    from sepia_amd import store_synth
+    L, hip = B.L, B.hip
+    H, I, NS = 6144, 3072, 2
+    tmp = tempfile.mkdtemp(prefix="sepia-store-")
+    try:
+        t0 = time.time()
+        paths, host = store_synth.write_layer_store(tmp, np.random.default_rng(71), layer=2, hidden=H, inter=I,
+                                                    n_routed=n_routed, n_shared=NS, types=C3_TYPES,
+                                                    n_parts=1)
+        write_s = time.time() - t0
+        t = L.sepia_hip_manifest_load(paths["manifest"].encode(), paths["bin"].encode())
+        idx = L.sepia_hip_index_load(paths["index"].encode())
+        if not t or not idx:
+            raise RuntimeError("store: the sidecars did not parse")
+        res_bytes = os.path.getsize(paths["bin"])
+        up_s, lay_s = [], []
+        for _ in range(reps):
+            t1 = time.perf_counter()
+            rbuf = L.sepia_hip_manifest_upload(t)
+            t2 = time.perf_counter()
+            ex = (hip.ExpertTensor * 3)()
+            ebuf = L.sepia_hip_index_upload_layer(idx, None, 2, ex)
+            t3 = time.perf_counter()
+            if not rbuf or not ebuf:
+                raise RuntimeError("store: upload failed")
+            up_s.append(t2 - t1)
+            lay_s.append(t3 - t2)
+            last = (rbuf, ebuf, ex)
+            if _ + 1 < reps:
+                B.dev.free(rbuf)
+                B.dev.free(ebuf)
+        rbuf, ebuf, ex = last
+        layer_bytes = 3 * n_routed * ex[0].stride
+        desc = hip.MoeLayerDesc()
+        if L.sepia_hip_moe_layer_from_stores(t, rbuf, 2, ex, n_routed, 6, 8.0, ctypes.byref(desc)) != 1:
+            raise RuntimeError("store: layer descriptor failed")
+        x = np.random.default_rng(72).standard_normal(H).astype(np.float32)
+        xb, yb, rb = B.dev.shared_from(x), B.dev.alloc(H * 4), B.dev.alloc(64 * 4)
+        B.dev.run(L.sepia_gpu_moe_decode, ctypes.byref(desc), xb, yb, rb)
+        y = B.dev.download(yb, H)
+        sel = B.dev.download(rb, 6, dtype=np.int32)
+        spec = dict(host[2], topk=6, route_scale=8.0, global_scale=1.0)
+        logits = oracle.linear_f32(spec["router_w"], x)
+        chosen = check_selection(oracle, logits, spec["router_bias"], n_routed, NS, 6, sel, "store layer")
+        want, _, _, _ = oracle.moe_layer(spec, x, force_idx=chosen, threads=min(16, os.cpu_count() or 1))
+        err, scale = float(np.max(np.abs(y - want))), float(np.max(np.abs(want)))
+        if err > 1e-4 * scale:
+            raise RuntimeError("store layer parity: max|diff| %g > 1e-4 * %g" % (err, scale))
+        for b in (xb, yb, rb, rbuf, ebuf):
+            B.dev.free(b)
+        L.sepia_hip_manifest_free(t)
+        L.sepia_hip_index_free(idx)
+        return dict(n_routed=n_routed, write_s=write_s, resident_bytes=res_bytes, layer_bytes=layer_bytes,
+                    resident_upload_ms=1e3 * min(up_s), layer_upload_ms=1e3 * min(lay_s),
+                    resident_gbs=res_bytes / min(up_s) / 1e9, layer_gbs=layer_bytes / min(lay_s) / 1e9,
+                    source="page cache (files just written)",
+                    parity=dict(max_abs_diff=err, y_inf=scale, bound="1e-4*||y||_inf",
+                                selection=[int(v) for v in sel]))
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+
+
 def run_copy(B, steps):
     """sepia_copy_f32 over 256 MiB (read 256 MiB, write 256 MiB) per launch: the known-size
     kernel against which rocprofv3's FETCH_SIZE and WRITE_SIZE counters are scaled."""
@@ -542,7 +614,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--only", choices=["c3", "real", "c2", "c1", "c4", "c5", "copy"], default=None,
+    ap.add_argument("--only", choices=["c3", "real", "c2", "c1", "c4", "c5", "store", "copy"], default=None,
                     help="run one configuration (profiling runs; 'copy': the library's f32 copy kernel over "
                          "256 MiB, the reference for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE); default: all")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
@@ -588,6 +660,9 @@ def main():
     if args.only in (None, "c5"):
         extra["C5_moe_prefill_512"] = run_c5(B, min(args.warmup, 2), min(args.steps, 10), min(3.0, args.cpu_seconds))
         log("C5", json.dumps(extra["C5_moe_prefill_512"]))
+    if args.only in (None, "store"):
+        extra["store_upload_c3_layer"] = run_store(B)
+        log("store", json.dumps(extra["store_upload_c3_layer"]))
     if args.only == "copy":
         extra["copy_f32_256MiB"] = run_copy(B, args.steps)
         log("copy", json.dumps(extra["copy_f32_256MiB"]))

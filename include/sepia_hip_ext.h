@@ -153,6 +153,90 @@ void *sepia_hip_stream(void);
  *                 and the router rows are 16-byte aligned (default 1). */
 int sepia_hip_set_option(const char *name, int value);
 
+/* ---- The on-disk stores straight into HBM -------------------------------
+ * The reference reads resident-manifest.json + resident.bin (mmap'd) and
+ * the sepia-index sidecar, then preads each routed expert from the GGUF
+ * parts when it is used (src/sepia.c:1853-2104; docs/container.md:123-257).
+ * Here both stores go to device memory once: resident.bin as one private
+ * buffer, and every expert of a MoE layer into one private buffer per
+ * layer, so the layer runs with no host reads. Parsing is host-only; the
+ * uploads need sepia_gpu_init and run outside a batch (they synchronize the
+ * library's stream). Failures log one line and return NULL/0. */
+
+/* One tensor of resident-manifest.json. shape[0] is the fastest dimension
+ * (GGUF order): a 2-D weight is [in_dim, out_dim], a stacked 3-D one
+ * [in_dim, out_dim, n_stack]. */
+typedef struct {
+    const char *name;
+    int ggml_type;
+    int n_dims;
+    int64_t shape[4];
+    int64_t offset;     /* into resident.bin and its device copy */
+    int64_t nbytes;
+} SepiaResidentTensor;
+
+typedef struct SepiaResidentTable SepiaResidentTable;
+
+/* Replaces manifest_load (src/sepia.c:1876-1910): parses the manifest's
+ * "tensors" array ({name, ggml_type, offset, nbytes, shape[1..4]}) and
+ * checks every [offset, offset + nbytes) against resident_bin_path's size. */
+SepiaResidentTable *sepia_hip_manifest_load(const char *manifest_path, const char *resident_bin_path);
+size_t sepia_hip_manifest_count(const SepiaResidentTable *t);
+const SepiaResidentTensor *sepia_hip_manifest_tensor(const SepiaResidentTable *t, size_t i);
+/* Replaces resident_find (src/sepia.c:1912-1916): the first tensor of that
+ * name, NULL if none. */
+const SepiaResidentTensor *sepia_hip_manifest_find(const SepiaResidentTable *t, const char *name);
+/* resident.bin into one private device buffer (the manifest's offsets hold
+ * in it); the reference mmaps the file instead (src/sepia.c:2655-2670). */
+SepiaGpuBuf *sepia_hip_manifest_upload(const SepiaResidentTable *t);
+void sepia_hip_manifest_free(SepiaResidentTable *t);
+
+/* One routed expert's slice of a GGUF part (struct ExpertSlot,
+ * src/sepia.c:1995-2000). */
+typedef struct {
+    int part_idx;
+    int64_t abs_offset;
+    int64_t nbytes;
+    int ggml_type;
+} SepiaExpertSlot;
+
+typedef struct SepiaExpertIndex SepiaExpertIndex;
+
+/* Replaces index_load (src/sepia.c:2036-2080): n_experts_per_layer, the
+ * parts[] file list and every moe_layers{} layer's gate/up/down "experts"
+ * arrays of {part_file, abs_offset, nbytes, ggml_type}. */
+SepiaExpertIndex *sepia_hip_index_load(const char *index_path);
+int sepia_hip_index_n_experts(const SepiaExpertIndex *idx);
+int sepia_hip_index_n_parts(const SepiaExpertIndex *idx);
+const char *sepia_hip_index_part(const SepiaExpertIndex *idx, int i);
+/* 1 if the index has this MoE layer. */
+int sepia_hip_index_has_layer(const SepiaExpertIndex *idx, int layer);
+/* The slice of (layer, kind 0 gate / 1 up / 2 down, expert); 0 if absent. */
+int sepia_hip_index_slot(const SepiaExpertIndex *idx, int layer, int kind, int expert, SepiaExpertSlot *out);
+/* Every expert of one layer's gate, up and down from the GGUF parts under
+ * gguf_dir (NULL: "inkling-gguf" beside the index file, as the reference
+ * derives it, src/sepia.c:1823-1834) into one private device buffer: the
+ * three stacks back to back, expert e of kind k at out[k].off + e *
+ * out[k].stride. The slices of one kind must share their type and size;
+ * runs of experts that lie back to back in a part are read as one range.
+ * Replaces the reference's per-use pread (docs/container.md:245-252). */
+SepiaGpuBuf *sepia_hip_index_upload_layer(const SepiaExpertIndex *idx, const char *gguf_dir, int layer,
+                                          SepiaExpertTensor out[3]);
+void sepia_hip_index_free(SepiaExpertIndex *idx);
+
+/* A MoE layer's descriptor from the two stores, resolving what the
+ * reference's real_load does per layer (src/sepia.c:2770-2777):
+ * blk.<layer>.ffn_gate_inp.weight (f32 router [hidden, n_routed + n_shared]),
+ * exp_probs_b.bias (f32 [n_routed]), ffn_gscale.weight (f32 [1], read from
+ * resident.bin into global_scale), ffn_{gate,up,down}_shexp.weight (shared
+ * stacks, n_shared = their stack count; absent: no shared experts) in the
+ * resident upload, and the routed experts of upload_layer. hidden and inter
+ * come from the shapes, and every matrix's bytes are checked against them.
+ * 1 on success. */
+int sepia_hip_moe_layer_from_stores(const SepiaResidentTable *t, SepiaGpuBuf *resident, int layer,
+                                    const SepiaExpertTensor experts[3], int n_routed, int topk, float route_scale,
+                                    SepiaMoeLayerDesc *out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -19,6 +19,7 @@
 
 #include "../../include/sepia_gpu.h"
 #include "../../include/sepia_hip_ext.h"
+#include "internal.h"
 #include "noalloc.h"
 
 #include <dlfcn.h>
@@ -242,6 +243,30 @@ static int need_batch(const char *op) {
         return 0;
     }
     return 1;
+}
+
+/* ---- hooks for the other host files (internal.h) ---- */
+void sepia_log(const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    fprintf(stderr, "sepia: hip: ");
+    vfprintf(stderr, fmt, ap);
+    fprintf(stderr, "\n");
+    va_end(ap);
+}
+int sepia_ready(const char *op) { return need_init(op); }
+hipStream_t sepia_stream(void) { return g_stream; }
+uint8_t *sepia_buf_dev(SepiaGpuBuf *b) { return b ? b->dev : NULL; }
+size_t sepia_buf_len(const SepiaGpuBuf *b) { return b ? b->len : 0; }
+int64_t sepia_row_bytes(int ggml_type, int64_t n) {
+    if (n < 0) return -1;
+    if (ggml_type == 0) return 4 * n;   /* F32 */
+    for (size_t i = 0; i < sizeof k_types / sizeof k_types[0]; i++) {
+        if (k_types[i].type != ggml_type) continue;
+        if (n % k_types[i].elems) return -1;
+        return n / k_types[i].elems * k_types[i].bytes;
+    }
+    return -1;
 }
 
 /* b holds [off, off + n) */

@@ -38,7 +38,18 @@ class MoeLayerDesc(ctypes.Structure):
                 ("s_gate", ExpertTensor), ("s_up", ExpertTensor), ("s_down", ExpertTensor)]
 
 
+class ResidentTensor(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char_p), ("ggml_type", ctypes.c_int), ("n_dims", ctypes.c_int),
+                ("shape", ctypes.c_int64 * 4), ("offset", ctypes.c_int64), ("nbytes", ctypes.c_int64)]
+
+
+class ExpertSlot(ctypes.Structure):
+    _fields_ = [("part_idx", ctypes.c_int), ("abs_offset", ctypes.c_int64), ("nbytes", ctypes.c_int64),
+                ("ggml_type", ctypes.c_int)]
+
+
 _P, _SZ, _I64, _F, _I = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int64, ctypes.c_float, ctypes.c_int
+_RT = ctypes.POINTER(ResidentTensor)
 PROTOTYPES = {
     # name: (restype, argtypes)
     "sepia_gpu_available": (_I, []),
@@ -87,6 +98,23 @@ PROTOTYPES = {
     "sepia_hip_uploaded_bytes": (ctypes.c_uint64, []),
     "sepia_hip_stream": (_P, []),
     "sepia_hip_set_option": (_I, [ctypes.c_char_p, _I]),
+    # the on-disk stores (store.c)
+    "sepia_hip_manifest_load": (_P, [ctypes.c_char_p, ctypes.c_char_p]),
+    "sepia_hip_manifest_count": (_SZ, [_P]),
+    "sepia_hip_manifest_tensor": (_RT, [_P, _SZ]),
+    "sepia_hip_manifest_find": (_RT, [_P, ctypes.c_char_p]),
+    "sepia_hip_manifest_upload": (_P, [_P]),
+    "sepia_hip_manifest_free": (None, [_P]),
+    "sepia_hip_index_load": (_P, [ctypes.c_char_p]),
+    "sepia_hip_index_n_experts": (_I, [_P]),
+    "sepia_hip_index_n_parts": (_I, [_P]),
+    "sepia_hip_index_part": (ctypes.c_char_p, [_P, _I]),
+    "sepia_hip_index_has_layer": (_I, [_P, _I]),
+    "sepia_hip_index_slot": (_I, [_P, _I, _I, _I, ctypes.POINTER(ExpertSlot)]),
+    "sepia_hip_index_upload_layer": (_P, [_P, ctypes.c_char_p, _I, ctypes.POINTER(ExpertTensor)]),
+    "sepia_hip_index_free": (None, [_P]),
+    "sepia_hip_moe_layer_from_stores": (_I, [_P, _P, _I, ctypes.POINTER(ExpertTensor), _I, _I, _F,
+                                             ctypes.POINTER(MoeLayerDesc)]),
 }
 
 _lib = None
