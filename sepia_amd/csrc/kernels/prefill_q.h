@@ -1,0 +1,588 @@
+// prefill_q.h -- the prefill MoE projections of the K-quant formats Q2_K,
+// Q3_K and Q4_K on the int8 matrix cores (the batched layer of prefill.h
+// with these formats: the same grouping, units and combine).
+//
+// Activations (x per token for gate/up, h per pair for down) travel as "PQ"
+// rows: per row one f32 scale s = max|v| / MQ_QMAX and per column the
+// integer q = round(v / s), |q| <= MQ_QMAX + 1, written as three signed
+// base-256 digits q = 65536 p0 + 256 p1 + p2 exactly as the decode path's
+// XQ digits (mq.h); v^ = s q is within s / 2 + 2^-22 |v| of v (a 23-bit
+// representation relative to the row's largest |v|). A 256-column block of
+// a row is an 832-byte record: the digit planes p0, p1, p2 (256 bytes each,
+// column order), then the sixteen 16-column sums S_j = sum of q as bf16 hi
+// (32 bytes) and lo (32 bytes), hi + lo within 2^-16 |S_j| of S_j.
+//
+// The weights' integer codes are the B operand of v_mfma_i32_16x16x64_i8:
+// Q2_K as sc * q (0..45) and Q3_K as (32 - sc) * (q - 4) (-128..124), the
+// 16-weight sub-block scale folded in, each read from a per-sub-block table
+// by v_perm_b32 with the 2- or 3-bit codes as the selectors; Q4_K as two
+// operands q * (sc & 7) and q * (sc >> 3) whose sums combine as lo + 8 hi
+// (sc * q needs 10 bits). Per weight row n and
+// 256-column block (src/quants.c:104-125 and the ggml layouts of Q2_K and
+// Q3_K), with C the i32 dot of the codes with q:
+//   Q2_K  sum_k w_k v^_k = s (d_n C - dmin_n sum_j m_j S_j)
+//   Q3_K  sum_k w_k v^_k = -s d_n C
+//   Q4_K  sum_k w_k v^_k = s (d_n C - dmin_n sum_j m_j (S_2j + S_2j+1))
+// C = 65536 C0 + 256 C1 + C2 over the digit planes, each plane's sum an
+// exact i32 (|C_p| <= 256 * 128 * 128 = 2^22, so 256 C1 + C2 is exact too);
+// the block's C goes to f32 as fma(C0, 65536, 256 C1 + C2) and accumulates
+// in f32 with d_n. The min terms are 16x16x16 bf16 MFMAs over the sixteen
+// sums (m exact in bf16, S as hi + lo). The row scale s multiplies the
+// result once at the end.
+//
+// Workgroup: one unit (<= 32 pairs of one expert) x 256 weight rows (gate/up:
+// 128 rows of gate and the same 128 rows of up), 8 waves; wave w computes
+// 32 rows (two 16-row N tiles) x the unit's one or two 16-pair M tiles, so a
+// decoded B fragment feeds 3 (or 6) MFMAs per M tile and an A fragment
+// 2 N tiles. Each 256-column block arrives by LDS DMA one block ahead (two
+// stages): the unit's 32 PQ records (padded to 848 bytes, so the 16 pair
+// rows of an A read hit 16 bank groups) and each weight row's 16-byte-aligned
+// window that holds the block (an odd number of 16-byte pieces per row).
+#pragma once
+#include "prefill.h"
+
+#define PQ_REC 832                     // bytes of a 256-column PQ record
+#define PQ_PITCH 848                   // LDS bytes of a staged record
+#define PQ_A_BYTES (PF_MT * PQ_PITCH)  // staged records of a unit (27,136)
+#define PQ_ROWS 256                    // weight rows of a workgroup
+#define PQ_LDS_TOP (PF_LDS_BYTES - 3 * PF_MT * 4)   // row tables: roff, pair, scale
+
+template <int T> struct PqFmt;
+template <> struct PqFmt<ST_Q2_K> { static constexpr int BB = 84, PW = 7; };
+template <> struct PqFmt<ST_Q3_K> { static constexpr int BB = 110, PW = 9; };
+template <> struct PqFmt<ST_Q4_K> { static constexpr int BB = 144, PW = 11; };
+
+// ------------------------------------------------------------- rows -> PQ --
+// Wave max over 64 lanes.
+__device__ __forceinline__ float pq_wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+// One workgroup per row: src row r (K floats at src + r * ld) into its PQ
+// records at pq + r * ldq and its scale at scale[r].
+extern "C" __global__ __launch_bounds__(256) void sepia_pf_quant(const float *__restrict__ src, int64_t ld,
+                                                                 int64_t K, uint8_t *__restrict__ pq, int64_t ldq,
+                                                                 float *__restrict__ scale) {
+    __shared__ float red[4];
+    const int64_t r = blockIdx.x;
+    const float *row = src + r * ld;
+    float m = 0.0f;
+    for (int64_t c = 4 * (int64_t)threadIdx.x; c < K; c += 1024) {
+        const float4 v = *(const float4 *)(row + c);
+        m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    }
+    m = pq_wave_max(m);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    // |v * inv| <= QMAX (1 + 2^-22): rcp is within 1 ulp
+    const float inv = (m > 0.0f) ? MQ_QMAX * __builtin_amdgcn_rcpf(m) : 0.0f;
+    if (threadIdx.x == 0) scale[r] = m * (1.0f / MQ_QMAX);
+    uint8_t *out = pq + r * ldq;
+    for (int64_t seg = threadIdx.x; seg < K / 16; seg += 256) {
+        const float4 *x4 = (const float4 *)(row + 16 * seg);
+        uint32_t q[16];
+        int32_t sum = 0;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const float4 t = x4[c];
+            const float a[4] = {t.x, t.y, t.z, t.w};
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int32_t v = mq_round(a[i] * inv);
+                sum += v;
+                q[4 * c + i] = (uint32_t)v + 0x8080u;
+            }
+        }
+        uint32_t w0[4], w1[4], w2[4];
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            // as xq_segment (mq.h): byte 2 of q + 0x8080 is p0, bytes 1 and 0 are p1 + 128, p2 + 128
+            const uint32_t t01 = __builtin_amdgcn_perm(q[4 * w + 1], q[4 * w], 0x05010400u);
+            const uint32_t t23 = __builtin_amdgcn_perm(q[4 * w + 3], q[4 * w + 2], 0x05010400u);
+            const uint32_t u01 = __builtin_amdgcn_perm(q[4 * w + 1], q[4 * w], 0x06020602u);
+            const uint32_t u23 = __builtin_amdgcn_perm(q[4 * w + 3], q[4 * w + 2], 0x06020602u);
+            w2[w] = __builtin_amdgcn_perm(t23, t01, 0x05040100u) ^ 0x80808080u;
+            w1[w] = __builtin_amdgcn_perm(t23, t01, 0x07060302u) ^ 0x80808080u;
+            w0[w] = __builtin_amdgcn_perm(u23, u01, 0x05040100u);
+        }
+        uint8_t *rec = out + (seg >> 4) * PQ_REC;
+        const int j = (int)(seg & 15);
+        *(uint4 *)(rec + 16 * j) = make_uint4(w0[0], w0[1], w0[2], w0[3]);
+        *(uint4 *)(rec + 256 + 16 * j) = make_uint4(w1[0], w1[1], w1[2], w1[3]);
+        *(uint4 *)(rec + 512 + 16 * j) = make_uint4(w2[0], w2[1], w2[2], w2[3]);
+        // S = hi + lo: hi = bf16(S), lo = bf16 of the exact integer remainder
+        const __bf16 hi = (__bf16)(float)sum;
+        const __bf16 lo = (__bf16)(float)(sum - (int32_t)(float)hi);
+        *(__bf16 *)(rec + 768 + 2 * j) = hi;
+        *(__bf16 *)(rec + 800 + 2 * j) = lo;
+    }
+}
+
+// --------------------------------------------------------------- staging --
+// The unit's PQ records of block b into As (record m at As + PQ_PITCH m):
+// piece c < 52 of record m is bytes 16 c .. of pq + roff[m] + PQ_REC b; the
+// 53rd piece of a staged record is padding (piece 0 again).
+__device__ __forceinline__ void pq_issue_act(const uint8_t *pq, const uint32_t *roff, int64_t b, uint8_t *As) {
+    const int nw = (int)(blockDim.x >> 6), w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int lane = threadIdx.x & 63;
+    constexpr int NP = PQ_PITCH / 16, TOT = PF_MT * NP;
+    for (int j = w; j < (TOT + 63) / 64; j += nw) {
+        const int q = 64 * j + lane;
+        if (q < TOT) {
+            const int m = q / NP, c = q - m * NP;
+            const uint32_t voff = roff[m] + (uint32_t)b * PQ_REC + 16u * (uint32_t)(c < NP - 1 ? c : 0);
+            pf_dma16(pq, voff, pf_lds(As + 1024 * j));
+        }
+    }
+}
+
+// Block b of weight rows r0 .. r0 + nr - 1 of W into Ws: row k's 16-byte-
+// aligned window that holds the block at Ws + 16 PW k (pieces past the
+// window's end fetch its first piece again, so no read leaves the block's
+// row). `first` is the index of this call's first wave instruction among
+// the stage's (the gate rows of a gate/up stage, then the up rows).
+template <int T>
+__device__ __forceinline__ void pq_issue_w(const uint8_t *W, uint64_t row_bytes, int64_t r0, int nr, int64_t b,
+                                           uint8_t *Ws) {
+    constexpr int BB = PqFmt<T>::BB, PW = PqFmt<T>::PW;
+    const int nw = (int)(blockDim.x >> 6), w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int lane = threadIdx.x & 63;
+    const uint8_t *Wa = (const uint8_t *)((uintptr_t)W & ~(uintptr_t)15);
+    const uint32_t delta = (uint32_t)((uintptr_t)W & 15);
+    const int n_ins = nr * PW / 64;   // nr * PW is a multiple of 64 (nr a multiple of 64)
+    for (int j = w; j < n_ins; j += nw) {
+        const int q = 64 * j + lane, k = q / PW, c = q - k * PW;
+        const uint64_t off = delta + (uint64_t)(r0 + k) * row_bytes + (uint64_t)b * BB;
+        const uint32_t o = (uint32_t)off & 15u, n16 = (o + BB + 15) >> 4;
+        pf_dma16(Wa, (uint32_t)(off & ~(uint64_t)15) + 16u * ((uint32_t)c < n16 ? (uint32_t)c : 0u),
+                 pf_lds(Ws + 1024 * j));
+    }
+}
+
+// ------------------------------------------------------------- decoders --
+typedef const __attribute__((address_space(3))) uint32_t pq_lds_u32;
+typedef const __attribute__((address_space(3))) uint16_t pq_lds_u16;
+typedef const __attribute__((address_space(3))) uint8_t pq_lds_u8;
+__device__ __forceinline__ pq_lds_u32 *pq_w32(const uint8_t *p) { return (pq_lds_u32 *)(size_t)(pf_lds(p) & ~3u); }
+__device__ __forceinline__ uint32_t pq_u8(const uint8_t *p) { return *(pq_lds_u8 *)(size_t)pf_lds(p); }
+__device__ __forceinline__ uint32_t pq_u16(const uint8_t *p) { return *(pq_lds_u16 *)(size_t)pf_lds(p); }
+__device__ __forceinline__ float pq_h2f(const uint8_t *p) { return f16_bits_to_f32(pq_u16(p)); }
+// Five dwords from the dword holding p: with sh = 8 (p & 3), the funnel
+// shift of (D[i + 1], D[i]) by sh + t is bytes 4 i .. 4 i + 3 from p, moved
+// down t bits.
+struct PqWin {
+    uint32_t d[5];
+    uint32_t sh;
+};
+__device__ __forceinline__ PqWin pq_win(const uint8_t *p) {
+    PqWin r;
+    pq_lds_u32 *q = pq_w32(p);
+#pragma unroll
+    for (int i = 0; i < 5; i++) r.d[i] = q[i];
+    r.sh = 8u * (pf_lds(p) & 3u);
+    return r;
+}
+__device__ __forceinline__ uint32_t pq_fsh(uint32_t hi, uint32_t lo, uint32_t n) {
+    return __builtin_amdgcn_alignbit(hi, lo, n);
+}
+// u32 at a 2-byte-aligned LDS address.
+__device__ __forceinline__ uint32_t pq_u32u(const uint8_t *p) {
+    pq_lds_u32 *q = pq_w32(p);
+    return pq_fsh(q[1], q[0], 8u * (pf_lds(p) & 3u));
+}
+
+// Q2_K (ggml): weight k = 128 h + 32 s + 16 g' + l: q = (qs[32 h + 16 g' + l]
+// >> 2 s) & 3, sub-block k / 16 with scale byte (sc lo nibble, m hi nibble).
+// K step j (64 columns), lane group g: h = j >> 1, s = 2 (j & 1) + (g >> 1),
+// g' = g & 1, sub-block 4 j + g. Codes sc * q by v_perm from the table
+// [0, sc, 2 sc, 3 sc] (selector q | 4 picks its byte q).
+__device__ __forceinline__ mq_v4i pq_b_q2k(const uint8_t *blk, int j, int g) {
+    const uint32_t sc = pq_u8(blk + 4 * j + g) & 15u;
+    const uint32_t tab = (sc * 0x030201u) << 8;   // v_mul_u32_u24: sc < 16
+    const PqWin wq = pq_win(blk + 16 + 32 * (j >> 1) + 16 * (g & 1));
+    const uint32_t sh = wq.sh + 2u * (uint32_t)(2 * (j & 1) + (g >> 1));
+    mq_v4i r;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t u = (pq_fsh(wq.d[i + 1], wq.d[i], sh) & 0x03030303u) | 0x04040404u;
+        r[i] = (int32_t)__builtin_amdgcn_perm(tab, 0u, u);
+    }
+    return r;
+}
+// Q3_K (ggml): Q2_K's indexing of qs (at 32); the high bit of q is bit
+// (4 h + s) of hmask[16 g' + l] (at 0), q - 4 unless it is set; 6-bit scale
+// sc of sub-block 4 j + g (q3_scale's packing, at 96). Codes (32 - sc) *
+// (u - 4), u = low bits | high bit << 2, by v_perm from the 8-byte table
+// a * (u - 4), a = 32 - sc.
+__device__ __forceinline__ mq_v4i pq_b_q3k(const uint8_t *blk, int j, int g) {
+    const uint32_t lo4 = (pq_u8(blk + 96 + 4 * (j & 1) + g) >> (4 * (j >> 1))) & 15u;
+    const uint32_t hi2 = (pq_u8(blk + 104 + g) >> (2 * j)) & 3u;
+    const uint32_t a = 32u - (lo4 | (hi2 << 4));           // two's complement of a, a in [-31, 32]
+    const uint32_t a8 = a & 255u, na8 = (0u - a) & 255u;   // a and -a mod 256
+    const uint32_t t01 = a8 << 16, t23 = a8 * 0x030002u;   // 24-bit products (v_mul_u32_u24)
+    const uint32_t t45 = na8 * 0x030004u, t67 = na8 * 0x010002u;
+    const uint32_t thi = __builtin_amdgcn_perm(t23, t01, 0x06040200u);   // a * [0, 1, 2, 3]
+    const uint32_t tlo = __builtin_amdgcn_perm(t67, t45, 0x06040200u);   // a * [-4, -3, -2, -1]
+    const PqWin wq = pq_win(blk + 32 + 32 * (j >> 1) + 16 * (g & 1));
+    const PqWin wh = pq_win(blk + 16 * (g & 1));
+    const int s = 2 * (j & 1) + (g >> 1), bit = 4 * (j >> 1) + s;
+    const uint32_t shq = wq.sh + 2u * (uint32_t)s;
+    // bit `bit` of each hmask byte to bit 2: a right funnel shift by
+    // sh + bit - 2, or (sh = 0, bit < 2) a left rotate; the bits a rotate or
+    // shift brings in never reach bit 2 of a byte
+    const int hs = (int)wh.sh + bit - 2;
+    mq_v4i r;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t hsrc = (hs >= 0) ? wh.d[i + 1] : wh.d[i];
+        const uint32_t hb = pq_fsh(hsrc, wh.d[i], (uint32_t)hs & 31u);
+        const uint32_t u = (pq_fsh(wq.d[i + 1], wq.d[i], shq) & 0x03030303u) | (hb & 0x04040404u);
+        r[i] = (int32_t)__builtin_amdgcn_perm(thi, tlo, u);
+    }
+    return r;
+}
+// Q4_K (src/quants.c:104-125): weight k = 64 p + 32 n + l: nibble n of
+// qs[32 p + l] (at 16), 32-weight sub-block 2 p + n with its 6-bit (sc, m)
+// pair. K step j, lane group g: codes k = 64 j + 16 g + l = nibble g >> 1
+// of qs[32 j + 16 (g & 1) + l], sub-block 2 j + (g >> 1). sc * q needs 10
+// bits, so the codes go in as two operands, q * (sc & 7) and q * (sc >> 3)
+// (each <= 105; the products of a byte never carry into the next, so a
+// packed 16-bit multiply makes them), whose i32 sums combine as lo + 8 hi.
+struct PqQ4 {
+    mq_v4i lo, hi;
+};
+typedef unsigned short pq_u16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pq_mul16(uint32_t a, uint32_t b) {
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(pq_u16x2, a) * __builtin_bit_cast(pq_u16x2, b));
+}
+__device__ __forceinline__ PqQ4 pq_b_q4k(const uint8_t *blk, int j, int g, uint32_t sc) {
+    const PqWin wq = pq_win(blk + 16 + 32 * j + 16 * (g & 1));
+    const uint32_t sh = wq.sh + 4u * (uint32_t)(g >> 1);
+    const uint32_t slo = (sc & 7u) * 0x10001u, shi = (sc >> 3) * 0x10001u;
+    PqQ4 r;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t q = pq_fsh(wq.d[i + 1], wq.d[i], sh) & 0x0F0F0F0Fu;
+        r.lo[i] = (int32_t)pq_mul16(q, slo);
+        r.hi[i] = (int32_t)pq_mul16(q, shi);
+    }
+    return r;
+}
+// 6-bit (sc, m) of Q4_K sub-block jj (k4_scale_min over LDS bytes).
+__device__ __forceinline__ void pq_q4k_sm(const uint8_t *blk, int jj, uint32_t &sc, uint32_t &mn) {
+    const uint8_t *s = blk + 4;
+    if (jj < 4) {
+        sc = pq_u8(s + jj) & 63u;
+        mn = pq_u8(s + jj + 4) & 63u;
+    } else {
+        const uint32_t c = pq_u8(s + jj + 4);
+        sc = (c & 15u) | ((pq_u8(s + jj - 4) >> 6) << 4);
+        mn = (c >> 4) | ((pq_u8(s + jj) >> 6) << 4);
+    }
+}
+
+// ----------------------------------------------------------- projection --
+// acc (+)= this block's share for both N tiles and MT M tiles.
+typedef short pq_s16x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ pq_s16x4 pq_bf4(float a, float b, float c, float d) {
+    __bf16 h[4] = {(__bf16)a, (__bf16)b, (__bf16)c, (__bf16)d};
+    return *(const pq_s16x4 *)h;
+}
+// 256 C1 + C2 is exact in i32; the sum goes to f32 once.
+__device__ __forceinline__ float pq_comb(int32_t c0, int32_t c1, int32_t c2) {
+    return __builtin_fmaf((float)c0, 65536.0f, (float)(int32_t)(((uint32_t)c1 << 8) + (uint32_t)c2));
+}
+
+template <int T, int MT>
+__device__ __forceinline__ void pq_block(pf_f32x4 (&acc)[2][2], const uint8_t *As, const uint8_t *blk0,
+                                         const uint8_t *blk1) {
+    const int l = threadIdx.x & 63, n = l & 15, g = l >> 4;
+    const uint8_t *blk[2] = {blk0, blk1};
+    // A fragment of plane p, M tile mt, columns c0 .. (lane: pair 16 mt + n, 16 or 8 bytes at group g)
+    auto a_at = [&](int mt, int p, int col) { return As + (16 * mt + n) * PQ_PITCH + 256 * p + col; };
+    if constexpr (T == ST_Q2_K || T == ST_Q3_K) {
+        mq_v4i C[2][MT][3];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            mq_v4i B[2];
+#pragma unroll
+            for (int t = 0; t < 2; t++) B[t] = T == ST_Q2_K ? pq_b_q2k(blk[t], j, g) : pq_b_q3k(blk[t], j, g);
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++) {
+#pragma unroll
+                for (int p = 0; p < 3; p++) {
+                    const mq_v4i a = *(const mq_v4i *)a_at(mt, p, 64 * j + 16 * g);
+#pragma unroll
+                    for (int t = 0; t < 2; t++)
+                        C[t][mt][p] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, B[t], j ? C[t][mt][p] : mq_v4i{0, 0, 0, 0},
+                                                                           0, 0, 0);
+                }
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            const float d = pq_h2f(blk[t] + (T == ST_Q2_K ? 80 : 108)), dn = T == ST_Q2_K ? d : -d;
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    acc[t][mt][i] = __builtin_fmaf(dn, pq_comb(C[t][mt][0][i], C[t][mt][1][i], C[t][mt][2][i]),
+                                                   acc[t][mt][i]);
+        }
+    } else {   // Q4_K
+        mq_v4i C[2][MT][3][2];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            PqQ4 B[2];
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                uint32_t sc, mn;
+                pq_q4k_sm(blk[t], 2 * j + (g >> 1), sc, mn);
+                B[t] = pq_b_q4k(blk[t], j, g, sc);
+            }
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++) {
+#pragma unroll
+                for (int p = 0; p < 3; p++) {
+                    const mq_v4i a = *(const mq_v4i *)a_at(mt, p, 64 * j + 16 * g);
+#pragma unroll
+                    for (int t = 0; t < 2; t++) {
+                        C[t][mt][p][0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+                            a, B[t].lo, j ? C[t][mt][p][0] : mq_v4i{0, 0, 0, 0}, 0, 0, 0);
+                        C[t][mt][p][1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+                            a, B[t].hi, j ? C[t][mt][p][1] : mq_v4i{0, 0, 0, 0}, 0, 0, 0);
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            const float d = pq_h2f(blk[t]);
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    // plane sums lo + 8 hi: |.| <= 9 * 256 * 105 * 128 < 2^25, each to f32 on its own
+                    float c[3];
+#pragma unroll
+                    for (int p = 0; p < 3; p++)
+                        c[p] = (float)(int32_t)(((uint32_t)C[t][mt][p][1][i] << 3) + (uint32_t)C[t][mt][p][0][i]);
+                    const float f = __builtin_fmaf(c[0], 65536.0f, __builtin_fmaf(c[1], 256.0f, c[2]));
+                    acc[t][mt][i] = __builtin_fmaf(d, f, acc[t][mt][i]);
+                }
+        }
+    }
+    if constexpr (T == ST_Q2_K || T == ST_Q4_K) {
+        // min terms: B[k = sub-block 4 g + i][n] = m (Q4_K: m of 32-column sub-block k / 2)
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            pq_s16x4 bm;
+            float dmin;
+            if constexpr (T == ST_Q2_K) {
+                const uint32_t v = pq_u32u(blk[t] + 4 * g) >> 4;
+                bm = pq_bf4((float)(v & 15u), (float)((v >> 8) & 15u), (float)((v >> 16) & 15u), (float)((v >> 24) & 15u));
+                dmin = pq_h2f(blk[t] + 82);
+            } else {
+                uint32_t s0, m0, s1, m1;
+                pq_q4k_sm(blk[t], 2 * g, s0, m0);
+                pq_q4k_sm(blk[t], 2 * g + 1, s1, m1);
+                bm = pq_bf4((float)m0, (float)m0, (float)m1, (float)m1);
+                dmin = pq_h2f(blk[t] + 2);
+            }
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++) {
+                const uint8_t *sr = As + (16 * mt + n) * PQ_PITCH + 768 + 8 * g;
+                const pq_s16x4 shi = *(const pq_s16x4 *)sr, slo = *(const pq_s16x4 *)(sr + 32);
+                pf_f32x4 cm = {0.0f, 0.0f, 0.0f, 0.0f};
+                cm = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(shi, bm, cm, 0, 0, 0);
+                cm = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(slo, bm, cm, 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc[t][mt][i] = __builtin_fmaf(-dmin, cm[i], acc[t][mt][i]);
+            }
+        }
+    }
+}
+
+// One projection workgroup (see the top of the file). GU: rows r0 .. r0 +
+// 127 of gate (W0) and up (W1), h[pair][row] = silu(gate) * up in f32;
+// down: rows r0 .. r0 + 255 of W0, out[pair][row] in f32. ld_out: floats
+// per output row (I for h, H for the down partials).
+template <int T, bool GU, int MT>
+__device__ __forceinline__ void pq_proj(uint8_t *smem, const uint8_t *W0, const uint8_t *W1, uint64_t row_bytes,
+                                        int64_t nb, const uint8_t *pq, const uint32_t *roff, const int32_t *pair,
+                                        const float *srow, int nv, int64_t r0, float *__restrict__ out,
+                                        int64_t ld_out) {
+    constexpr int BB = PqFmt<T>::BB, PW = PqFmt<T>::PW;
+    constexpr uint32_t st_bytes = PQ_A_BYTES + PQ_ROWS * PW * 16;
+    const int w = threadIdx.x >> 6, l = threadIdx.x & 63, n = l & 15, g = l >> 4;
+    const int mat = GU ? (w >> 2) : 0;
+    const int rho0 = GU ? 128 * mat + 32 * (w & 3) : 32 * w;   // stage row of N tile 0
+    const int64_t grow0 = r0 + (GU ? 32 * (w & 3) : 32 * w);   // its global row
+    auto stage = [&](int64_t b) { return smem + (uint32_t)(b & 1) * st_bytes; };
+    auto issue = [&](int64_t b) {
+        uint8_t *st = stage(b);
+        pq_issue_act(pq, roff, b, st);
+        if (GU) {
+            pq_issue_w<T>(W0, row_bytes, r0, 128, b, st + PQ_A_BYTES);
+            pq_issue_w<T>(W1, row_bytes, r0, 128, b, st + PQ_A_BYTES + 128 * PW * 16);
+        } else {
+            pq_issue_w<T>(W0, row_bytes, r0, 256, b, st + PQ_A_BYTES);
+        }
+    };
+    // the lane's rows: byte offset (mod 16) of row (grow0 + 16 t + n)'s start
+    const uint8_t *Wm = mat ? W1 : W0;
+    uint32_t rofs[2];
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+        rofs[t] = (uint32_t)(((uint64_t)((uintptr_t)Wm & 15) + (uint64_t)(grow0 + 16 * t + n) * row_bytes) & 15);
+    pf_f32x4 acc[2][2];
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+#pragma unroll
+        for (int mt = 0; mt < 2; mt++) acc[t][mt] = pf_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    issue(0);
+    for (int64_t b = 0; b < nb; b++) {
+        __builtin_amdgcn_s_waitcnt(mq_wc_vm(0));
+        __syncthreads();   // block b staged by every wave; block b - 1's readers are done
+        if (b + 1 < nb) issue(b + 1);
+        const uint8_t *st = stage(b);
+        const uint8_t *Ws = st + PQ_A_BYTES;
+        const uint8_t *blk[2];
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+            blk[t] = Ws + (uint32_t)(rho0 + 16 * t + n) * (PW * 16) + ((rofs[t] + (uint32_t)b * BB) & 15u);
+        pq_block<T, MT>(acc, st, blk[0], blk[1]);
+    }
+    // y = s_pair * acc; lane: pairs 16 mt + 4 g + i, rows grow0 + 16 t + n
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float s = srow[16 * mt + 4 * g + i];
+#pragma unroll
+            for (int t = 0; t < 2; t++) acc[t][mt][i] *= s;
+        }
+    if constexpr (GU) {
+        __syncthreads();   // every wave is done with the stages
+        float *xch = (float *)smem + ((w & 3) * 64 + l) * 16;
+        if (mat) {
+#pragma unroll
+            for (int t = 0; t < 2; t++)
+#pragma unroll
+                for (int mt = 0; mt < 2; mt++) *(pf_f32x4 *)(xch + 8 * t + 4 * mt) = acc[t][mt];
+        }
+        __syncthreads();
+        if (mat) return;
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++) {
+                const pf_f32x4 u = *(const pf_f32x4 *)(xch + 8 * t + 4 * mt);
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int m = 16 * mt + 4 * g + i;
+                    if (m < nv) out[(int64_t)pair[m] * ld_out + grow0 + 16 * t + n] = silu_f32(acc[t][mt][i]) * u[i];
+                }
+            }
+    } else {
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int m = 16 * mt + 4 * g + i;
+                    if (m < nv) out[(int64_t)pair[m] * ld_out + grow0 + 16 * t + n] = acc[t][mt][i];
+                }
+    }
+}
+
+// The unit's tables at the top of the LDS: roff[m] = byte offset of pair
+// m's PQ row (rows past nv repeat pair 0's), pair[m], srow[m] = its scale.
+__device__ __forceinline__ void pq_unit_rows(const int32_t *pairs, int nv, bool by_token, int32_t n_sel,
+                                             int64_t ldq, const float *scale, uint8_t *smem, uint32_t *&roff,
+                                             int32_t *&pair, float *&srow) {
+    roff = (uint32_t *)(smem + PQ_LDS_TOP);
+    pair = (int32_t *)(roff + PF_MT);
+    srow = (float *)(pair + PF_MT);
+    if (threadIdx.x < PF_MT) {
+        const int m = threadIdx.x < (unsigned)nv ? (int)threadIdx.x : 0;
+        const int32_t p = pairs[m];
+        const int64_t row = by_token ? (int64_t)(p / n_sel) : (int64_t)p;
+        pair[threadIdx.x] = p;
+        roff[threadIdx.x] = (uint32_t)(row * ldq);
+        srow[threadIdx.x] = scale[row];
+    }
+    __syncthreads();
+}
+
+#define PQ_DISPATCH(TYPE, GU, ...)                                                                   \
+    do {                                                                                             \
+        if (nv > 16) {                                                                               \
+            switch (TYPE) {                                                                          \
+            case ST_Q2_K: pq_proj<ST_Q2_K, GU, 2>(__VA_ARGS__); break;                               \
+            case ST_Q3_K: pq_proj<ST_Q3_K, GU, 2>(__VA_ARGS__); break;                               \
+            case ST_Q4_K: pq_proj<ST_Q4_K, GU, 2>(__VA_ARGS__); break;                               \
+            default: break;                                                                          \
+            }                                                                                        \
+        } else {                                                                                     \
+            switch (TYPE) {                                                                          \
+            case ST_Q2_K: pq_proj<ST_Q2_K, GU, 1>(__VA_ARGS__); break;                               \
+            case ST_Q3_K: pq_proj<ST_Q3_K, GU, 1>(__VA_ARGS__); break;                               \
+            case ST_Q4_K: pq_proj<ST_Q4_K, GU, 1>(__VA_ARGS__); break;                               \
+            default: break;                                                                          \
+            }                                                                                        \
+        }                                                                                            \
+    } while (0)
+
+// Gate/up: workgroup (rows 128 bx .. 128 bx + 127 of I, unit by); hf[p][row]
+// = silu(gate . x_t) * (up . x_t) in f32 for the unit's pairs p (token t =
+// p / n_sel). The host launches it only when every projection of the layer
+// is Q2_K, Q3_K or Q4_K and I is a multiple of 128.
+extern "C" __global__ __launch_bounds__(512) void sepia_pf_gateup_q(
+    PfProj gate, PfProj up, PfProj s_gate, PfProj s_up, int32_t n_routed, int32_t n_sel, int64_t I, int64_t H,
+    const uint8_t *__restrict__ pqx, const float *__restrict__ pqxs, const int32_t *__restrict__ list,
+    const int32_t *__restrict__ units, const int32_t *__restrict__ n_units, float *__restrict__ hf) {
+    if ((int32_t)blockIdx.y >= n_units[0]) return;
+    extern __shared__ __attribute__((aligned(16))) uint8_t pf_smem[];
+    uint8_t *smem = pf_smem;
+    const int32_t *un = units + 3 * blockIdx.y;
+    const int32_t e = un[0], nv = un[2];
+    const bool routed = e < n_routed;
+    const PfProj &G = routed ? gate : s_gate, &U = routed ? up : s_up;
+    const int64_t ei = routed ? e : e - n_routed;
+    const uint8_t *wg = G.base + ei * G.stride, *wu = U.base + ei * U.stride;
+    const int64_t r0 = (int64_t)blockIdx.x * 128;
+    uint32_t *roff;
+    int32_t *pair;
+    float *srow;
+    pq_unit_rows(list + un[1], nv, true, n_sel, (H / 256) * PQ_REC, pqxs, smem, roff, pair, srow);
+    PQ_DISPATCH(G.type, true, smem, wg, wu, G.row_bytes, G.n_blocks, pqx, roff, pair, srow, nv, r0, hf, I);
+}
+
+// Down: workgroup (rows 256 bx .. 256 bx + 255 of H, unit by); yp[p][row] =
+// down_e . h_p in f32 (h_p the PQ row p). Same launch conditions, H a
+// multiple of 256.
+extern "C" __global__ __launch_bounds__(512) void sepia_pf_down_q(
+    PfProj down, PfProj s_down, int32_t n_routed, int64_t I, int64_t H, const uint8_t *__restrict__ pqh,
+    const float *__restrict__ pqhs, const int32_t *__restrict__ list, const int32_t *__restrict__ units,
+    const int32_t *__restrict__ n_units, float *__restrict__ yp) {
+    if ((int32_t)blockIdx.y >= n_units[0]) return;
+    extern __shared__ __attribute__((aligned(16))) uint8_t pf_smem[];
+    uint8_t *smem = pf_smem;
+    const int32_t *un = units + 3 * blockIdx.y;
+    const int32_t e = un[0], nv = un[2];
+    const bool routed = e < n_routed;
+    const PfProj &D = routed ? down : s_down;
+    const int64_t ei = routed ? e : e - n_routed;
+    const uint8_t *wd = D.base + ei * D.stride;
+    const int64_t r0 = (int64_t)blockIdx.x * 256;
+    uint32_t *roff;
+    int32_t *pair;
+    float *srow;
+    pq_unit_rows(list + un[1], nv, false, 1, (I / 256) * PQ_REC, pqhs, smem, roff, pair, srow);
+    PQ_DISPATCH(D.type, false, smem, wd, nullptr, D.row_bytes, D.n_blocks, pqh, roff, pair, srow, nv, r0, yp, H);
+}

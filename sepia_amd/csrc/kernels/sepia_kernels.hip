@@ -229,6 +229,7 @@ SEPIA_FFN_PAIR(4, 4, ST_Q4_K, ST_Q4_K)
 #include "mq.h"
 #include "moe.h"
 #include "prefill.h"
+#include "prefill_q.h"
 #include "synth.h"
 #include "attn.h"
 

@@ -67,6 +67,8 @@ enum {
     K_FILL_U32,
     /* attention (kernels/attn.h): relative-position projection, banded attention partials and fold */
     K_REL_PROJECT, K_ATTN_PARTIAL, K_ATTN_COMBINE,
+    /* prefill projections of Q2_K / Q3_K / Q4_K on the int8 matrix cores (kernels/prefill_q.h) */
+    K_PF_QUANT, K_PF_GATEUP_Q, K_PF_DOWN_Q,
     K_COUNT
 };
 #define FFN_NAMES(p) "sepia_ffn_gateup_" p, "sepia_ffn_gateup_" p "_xp", "sepia_ffn_down_" p
@@ -92,6 +94,7 @@ static const char *const k_names[K_COUNT] = {
     "sepia_pf_route", "sepia_pf_select", "sepia_pf_group", "sepia_pf_gateup", "sepia_pf_down", "sepia_pf_combine",
     "sepia_pf_split", "sepia_pf_gateup_r", "sepia_pf_down_r", "sepia_pf_route_m", "sepia_fill_u32",
     "sepia_rel_project_f32", "sepia_attn_partial", "sepia_attn_combine",
+    "sepia_pf_quant", "sepia_pf_gateup_q", "sepia_pf_down_q",
 };
 #undef FFN_NAMES
 
@@ -147,6 +150,9 @@ static int g_opt_mq_x = 0;   /* "mq_x": 0 = planner's choice, 1 = vector from gl
 static int g_opt_pf_route_m = 1;   /* "pf_route_m": 1 = prefill router logits on the f32 matrix cores
                                     * (sepia_pf_route_m) when x and the router rows are 16-byte aligned,
                                     * 0 = sepia_pf_route */
+static int g_opt_pf_q = 1;   /* "pf_q": 1 = a prefill layer whose six projections are all Q2_K, Q3_K or Q4_K
+                              * runs them on the int8 matrix cores (sepia_pf_quant, sepia_pf_gateup_q,
+                              * sepia_pf_down_q); 0 = as "pf_reg" says */
 static int g_opt_pf_reg = 1;   /* "pf_reg": 1 = a prefill layer whose gate/up (down) projections are all Q2_K,
                                 * Q3_K or Q4_K runs them as sepia_pf_gateup_r (sepia_pf_down_r), the codes
                                 * decoded into registers; 0 = the LDS-tile kernels sepia_pf_gateup / _down,
@@ -1113,6 +1119,10 @@ int sepia_hip_set_option(const char *name, int value) {
         g_opt_mq_x = value;
         return 1;
     }
+    if (strcmp(name, "pf_q") == 0 && (value == 0 || value == 1)) {
+        g_opt_pf_q = value;
+        return 1;
+    }
     if (strcmp(name, "pf_reg") == 0 && (value == 0 || value == 1)) {
         g_opt_pf_reg = value;
         return 1;
@@ -1729,14 +1739,20 @@ int sepia_gpu_moe_prefill(const SepiaMoeLayerDesc *L, int64_t n_tokens, SepiaGpu
      * each shared expert takes every token */
     const int64_t umax = (T * tk + 31) / 32 + nr + (int64_t)ns * ((T + 31) / 32) + 1;
     const int64_t P = T * n_sel;
-    /* the pipelines address activation rows with 32-bit byte offsets */
-    if (umax > 65535 || (H + 255) / 256 > MAX_GRID || (uint64_t)T * H * 2 >= (1ull << 32) ||
-        (uint64_t)P * I * 2 >= (1ull << 32) || (T * H + 255) / 256 > MAX_GRID) {
-        LOG("%s: batch too large", op);
-        return 0;
-    }
     if (H % 256 || I % 256) {
         LOG("%s: hidden and inter must be multiples of 256", op);
+        return 0;
+    }
+    /* int8 path: every projection Q2_K, Q3_K or Q4_K; activations as PQ rows
+     * (kernels/prefill_q.h: 832 bytes per 256 columns) */
+    const int use_q = g_opt_pf_q && pf_type_int(g.type) && pf_type_int(d.type) &&
+                      (ns == 0 || (pf_type_int(sg.type) && pf_type_int(sd.type)));
+    const int64_t ldqx = H / 256 * 832, ldqh = I / 256 * 832;
+    /* the pipelines address activation rows with 32-bit byte offsets */
+    if (umax > 65535 || (H + 255) / 256 > MAX_GRID || (uint64_t)T * H * 2 >= (1ull << 32) ||
+        (uint64_t)P * I * 2 >= (1ull << 32) || (T * H + 255) / 256 > MAX_GRID || P > MAX_GRID ||
+        (use_q && ((uint64_t)T * ldqx >= (1ull << 32) || (uint64_t)P * ldqh >= (1ull << 32)))) {
+        LOG("%s: batch too large", op);
         return 0;
     }
     if (!need_batch(op)) return 0;
@@ -1749,11 +1765,16 @@ int sepia_gpu_moe_prefill(const SepiaMoeLayerDesc *L, int64_t n_tokens, SepiaGpu
     PF_REGION(o_list, P * 4);
     PF_REGION(o_units, umax * 12);
     PF_REGION(o_nu, 8);   /* n_units, then the "x has a nonzero lo part" flag */
-    PF_REGION(o_s16, T * H / 16 * 4);
-    PF_REGION(o_xh, T * H * 2);
-    PF_REGION(o_xl, T * H * 2);
-    PF_REGION(o_hh, P * I * 2);
-    PF_REGION(o_hl, P * I * 2);
+    PF_REGION(o_s16, use_q ? 0 : T * H / 16 * 4);
+    PF_REGION(o_xh, use_q ? 0 : T * H * 2);
+    PF_REGION(o_xl, use_q ? 0 : T * H * 2);
+    PF_REGION(o_hh, use_q ? 0 : P * I * 2);
+    PF_REGION(o_hl, use_q ? 0 : P * I * 2);
+    PF_REGION(o_pqx, use_q ? T * ldqx : 0);
+    PF_REGION(o_pqxs, use_q ? T * 4 : 0);
+    PF_REGION(o_hf, use_q ? P * I * 4 : 0);
+    PF_REGION(o_pqh, use_q ? P * ldqh : 0);
+    PF_REGION(o_pqhs, use_q ? P * 4 : 0);
     PF_REGION(o_yp, P * H * 4);
 #undef PF_REGION
     uint8_t *s = (uint8_t *)scratch(o, op);
@@ -1781,6 +1802,20 @@ int sepia_gpu_moe_prefill(const SepiaMoeLayerDesc *L, int64_t n_tokens, SepiaGpu
     if (!launch(K_PF_SELECT, (unsigned)T, 64, a_sel, op)) return 0;
     void *a_grp[] = { &sel_idx, &tt, &nr32, &ns32, &tk32, &list, &units, &n_units, &lo_any };
     if (!launch(K_PF_GROUP, 1, 1024, a_grp, op)) return 0;
+    if (use_q) {
+        void *pqx = s + o_pqx, *pqxs = s + o_pqxs, *hf = s + o_hf, *pqh = s + o_pqh, *pqhs = s + o_pqhs;
+        int64_t ldq_x = ldqx, ldq_h = ldqh;
+        void *a_qx[] = { &x->dev, &hid, &hid, &pqx, &ldq_x, &pqxs };
+        if (!launch(K_PF_QUANT, (unsigned)T, 256, a_qx, op)) return 0;
+        void *a_gq[] = { (void *)&g, (void *)&u, (void *)&sg, (void *)&su, &nr32, &nsel32, &inter, &hid,
+                         &pqx, &pqxs, &list, &units, &n_units, &hf };
+        if (!launch2(K_PF_GATEUP_Q, (unsigned)(I / 128), (unsigned)umax, 512, PF_LDS_BYTES, a_gq, op)) return 0;
+        void *a_qh[] = { &hf, &inter, &inter, &pqh, &ldq_h, &pqhs };
+        if (!launch(K_PF_QUANT, (unsigned)P, 256, a_qh, op)) return 0;
+        void *a_dq[] = { (void *)&d, (void *)&sd, &nr32, &inter, &hid, &pqh, &pqhs, &list, &units, &n_units, &yp };
+        if (!launch2(K_PF_DOWN_Q, (unsigned)(H / 256), (unsigned)umax, 512, PF_LDS_BYTES, a_dq, op)) return 0;
+        goto combine;
+    }
     int64_t nseg = T * H / 16;
     void *a_sp[] = { &x->dev, &nseg, &xh, &xl, &s16, &lo_any };
     if (!launch(K_PF_SPLIT, (unsigned)((nseg + 255) / 256), 256, a_sp, op)) return 0;
@@ -1796,6 +1831,7 @@ int sepia_gpu_moe_prefill(const SepiaMoeLayerDesc *L, int64_t n_tokens, SepiaGpu
     if (!launch2(dn_r ? K_PF_DOWN_R : K_PF_DOWN, (unsigned)(dn_r ? (H + 127) / 128 : (H + 63) / 64), (unsigned)umax,
                  512, PF_LDS_BYTES, a_dn, op))
         return 0;
+combine:;
     void *a_cb[] = { &yp, &sel_w, &nsel32, &tt, &hid, &y->dev };
     if (!launch2(K_PF_COMBINE, (unsigned)((H + 255) / 256), (unsigned)T, 256, 0, a_cb, op)) return 0;
     if (route_out) {

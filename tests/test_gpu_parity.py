@@ -801,31 +801,36 @@ PREFILL_CASES = [
 ]
 
 
-@pytest.mark.parametrize("reg", [1, 0])
+PF_PATHS = {"q": dict(pf_q=1, pf_reg=1, pf_route_m=1), "reg": dict(pf_q=0, pf_reg=1, pf_route_m=1),
+            "tile": dict(pf_q=0, pf_reg=0, pf_route_m=0)}
+
+
+@pytest.mark.parametrize("path", ["q", "reg", "tile"])
 @pytest.mark.parametrize("x_kind", ["bf16", "f32"])
 @pytest.mark.parametrize("shape,types,T", PREFILL_CASES, ids=lambda v: str(v))
-def test_moe_prefill(dev, orc, shape, types, T, x_kind, reg):
+def test_moe_prefill(dev, orc, shape, types, T, x_kind, path):
     """Every token of the batch against the oracle's single-token layer (its
     own routing, near-ties per the reference protocol); two runs bitwise equal.
-    x either bf16-representable (the projections skip the zero lo terms) or
-    full f32. reg (option pf_reg): integer-format gate/up and down with the
-    codes in registers (1, the default) or on the LDS-tile kernels (0); reg 0
-    also runs the router on sepia_pf_route (option pf_route_m 0) instead of
-    the matrix-core one."""
+    x either bf16-representable (the bf16 projections skip the zero lo terms)
+    or full f32. path: a layer of Q2_K / Q3_K / Q4_K projections on the int8
+    matrix cores (q, the default; option pf_q), the bf16 kernels with the
+    codes in registers (reg; pf_q 0) or the LDS-tile kernels (tile; pf_reg 0,
+    which also runs the router on sepia_pf_route, pf_route_m 0). Layers with
+    other formats take the bf16 kernels under q and reg alike."""
     hidden, inter, n_routed, n_shared = shape
     tgu, td, ts = types
     rng = np.random.default_rng(hidden + 7 * T + tgu)
     desc, spec, bufs = make_layer(dev, rng, hidden=hidden, inter=inter, n_routed=n_routed, n_shared=n_shared,
                                   tg=tgu, tu=tgu, td=td, ts=ts)
     X = bf16_normal(rng, (T, hidden)) if x_kind == "bf16" else rng.standard_normal((T, hidden)).astype(np.float32)
-    assert dev.L.sepia_hip_set_option(b"pf_reg", reg) == 1
-    assert dev.L.sepia_hip_set_option(b"pf_route_m", reg) == 1
+    for k, v in PF_PATHS[path].items():
+        assert dev.L.sepia_hip_set_option(k.encode(), v) == 1
     try:
         y, idx, w = run_prefill(dev, desc, X)
         y2, _, _ = run_prefill(dev, desc, X)
     finally:
-        dev.L.sepia_hip_set_option(b"pf_reg", 1)
-        dev.L.sepia_hip_set_option(b"pf_route_m", 1)
+        for k, v in PF_PATHS["q"].items():
+            dev.L.sepia_hip_set_option(k.encode(), v)
     assert np.array_equal(y.view(np.uint32), y2.view(np.uint32))
     for t in range(T):
         y_ref, logits, idx_ref, w_ref = orc.moe_layer(spec, X[t], threads=THREADS)
