@@ -42,15 +42,18 @@
 #include "prefill.h"
 
 #define PQ_REC 832                     // bytes of a 256-column PQ record
-#define PQ_PITCH 848                   // LDS bytes of a staged record
-#define PQ_A_BYTES (PF_MT * PQ_PITCH)  // staged records of a unit (27,136)
 #define PQ_ROWS 256                    // weight rows of a workgroup
 #define PQ_LDS_TOP (PF_LDS_BYTES - 3 * PF_MT * 4)   // row tables: roff, pair, scale
 
 template <int T> struct PqFmt;
-template <> struct PqFmt<ST_Q2_K> { static constexpr int BB = 84, PW = 7; };
-template <> struct PqFmt<ST_Q3_K> { static constexpr int BB = 110, PW = 9; };
-template <> struct PqFmt<ST_Q4_K> { static constexpr int BB = 144, PW = 11; };
+// BB: block bytes; PW: 16-byte pieces of a staged weight row (odd, so the 16
+// rows of a lane group fall in different LDS banks); AP: pieces of a staged
+// PQ record (the planes, the sums where the format has min terms, one piece
+// of padding: odd too); SW: weight stages (LDS: 2 record stages + SW weight
+// stages of 256 rows within 160 KB).
+template <> struct PqFmt<ST_Q2_K> { static constexpr int BB = 84, PW = 7, AP = 53, SW = 3; };
+template <> struct PqFmt<ST_Q3_K> { static constexpr int BB = 110, PW = 9, AP = 49, SW = 3; };
+template <> struct PqFmt<ST_Q4_K> { static constexpr int BB = 144, PW = 11, AP = 53, SW = 2; };
 
 // ------------------------------------------------------------- rows -> PQ --
 // Wave max over 64 lanes.
@@ -122,45 +125,72 @@ extern "C" __global__ __launch_bounds__(256) void sepia_pf_quant(const float *__
 }
 
 // --------------------------------------------------------------- staging --
-// The unit's PQ records of block b into As (record m at As + PQ_PITCH m):
-// piece c < 52 of record m is bytes 16 c .. of pq + roff[m] + PQ_REC b; the
-// 53rd piece of a staged record is padding (piece 0 again).
-__device__ __forceinline__ void pq_issue_act(const uint8_t *pq, const uint32_t *roff, int64_t b, uint8_t *As) {
-    const int nw = (int)(blockDim.x >> 6), w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-    const int lane = threadIdx.x & 63;
-    constexpr int NP = PQ_PITCH / 16, TOT = PF_MT * NP;
-    for (int j = w; j < (TOT + 63) / 64; j += nw) {
-        const int q = 64 * j + lane;
-        if (q < TOT) {
-            const int m = q / NP, c = q - m * NP;
-            const uint32_t voff = roff[m] + (uint32_t)b * PQ_REC + 16u * (uint32_t)(c < NP - 1 ? c : 0);
-            pf_dma16(pq, voff, pf_lds(As + 1024 * j));
+// LDS: [records of block b: 2 stages][weight windows of block b: SW stages]
+// [row tables]. A record stage holds the unit's PQ records of the block
+// (record m at 16 AP m: its first AP - 1 pieces of 16 bytes, then a padding
+// piece, piece 0 again). A weight stage holds each weight row's 16-byte-
+// aligned window that holds the block (row k at 16 PW k, PW pieces; those
+// past the window's end fetch its first piece again, so no read leaves the
+// block's row): gate/up stages carry 128 gate rows, then the same 128 up
+// rows; down stages 256 rows. A wave instruction moves 64 pieces (1 KB) of
+// one stage; wave w issues instructions w, w + 8, ... of each. Their lane
+// offsets are fixed for the workgroup but for the block term, so they are
+// computed once.
+template <int T, bool GU>
+struct PqDma {
+    static constexpr int BB = PqFmt<T>::BB, PW = PqFmt<T>::PW, AP = PqFmt<T>::AP;
+    static constexpr int NA = (PF_MT * AP + 63) / 64, KA = (NA + 7) / 8;
+    static constexpr int NW = PQ_ROWS * PW / 64, KW = (NW + 7) / 8;   // NW: 28, 36, 44
+    uint32_t a[KA];            // record piece offsets at block 0, ~0u for an idle lane
+    uint32_t r[KW], c16[KW];   // row offset (from the 16-byte-aligned base), 16 * piece
+    __device__ __forceinline__ void init(const uint32_t *roff, const uint8_t *W0, const uint8_t *W1,
+                                         uint64_t row_bytes, int64_t r0) {
+        const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+#pragma unroll
+        for (int k = 0; k < KA; k++) {
+            const int q = 64 * (w + 8 * k) + lane, m = q / AP, c = q - m * AP;
+            a[k] = q < PF_MT * AP ? roff[m] + 16u * (uint32_t)(c < AP - 1 ? c : 0) : ~0u;
+        }
+#pragma unroll
+        for (int k = 0; k < KW; k++) {
+            const int jj = w + 8 * k;
+            const int mat = GU ? jj / (NW / 2) : 0, j1 = GU ? jj - mat * (NW / 2) : jj;
+            const int q = 64 * j1 + lane, kr = q / PW, c = q - kr * PW;
+            const uint8_t *W = mat ? W1 : W0;
+            r[k] = (uint32_t)(((uintptr_t)W & 15) + (uint64_t)(r0 + kr) * row_bytes);
+            c16[k] = 16u * (uint32_t)c;
         }
     }
-}
-
-// Block b of weight rows r0 .. r0 + nr - 1 of W into Ws: row k's 16-byte-
-// aligned window that holds the block at Ws + 16 PW k (pieces past the
-// window's end fetch its first piece again, so no read leaves the block's
-// row). `first` is the index of this call's first wave instruction among
-// the stage's (the gate rows of a gate/up stage, then the up rows).
-template <int T>
-__device__ __forceinline__ void pq_issue_w(const uint8_t *W, uint64_t row_bytes, int64_t r0, int nr, int64_t b,
-                                           uint8_t *Ws) {
-    constexpr int BB = PqFmt<T>::BB, PW = PqFmt<T>::PW;
-    const int nw = (int)(blockDim.x >> 6), w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-    const int lane = threadIdx.x & 63;
-    const uint8_t *Wa = (const uint8_t *)((uintptr_t)W & ~(uintptr_t)15);
-    const uint32_t delta = (uint32_t)((uintptr_t)W & 15);
-    const int n_ins = nr * PW / 64;   // nr * PW is a multiple of 64 (nr a multiple of 64)
-    for (int j = w; j < n_ins; j += nw) {
-        const int q = 64 * j + lane, k = q / PW, c = q - k * PW;
-        const uint64_t off = delta + (uint64_t)(r0 + k) * row_bytes + (uint64_t)b * BB;
-        const uint32_t o = (uint32_t)off & 15u, n16 = (o + BB + 15) >> 4;
-        pf_dma16(Wa, (uint32_t)(off & ~(uint64_t)15) + 16u * ((uint32_t)c < n16 ? (uint32_t)c : 0u),
-                 pf_lds(Ws + 1024 * j));
+    // this wave's weight instructions per block
+    static __device__ __forceinline__ int n_w() {
+        const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+        return w < NW ? (NW - w + 7) / 8 : 0;
     }
-}
+    __device__ __forceinline__ void issue_a(int64_t b, uint8_t *As, const uint8_t *pq) const {
+        const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+        const uint32_t ab = (uint32_t)b * PQ_REC;
+#pragma unroll
+        for (int k = 0; k < KA; k++) {
+            const int jj = w + 8 * k;
+            if (jj < NA && a[k] != ~0u) pf_dma16(pq, a[k] + ab, pf_lds(As + 1024 * jj));
+        }
+    }
+    __device__ __forceinline__ void issue_w(int64_t b, uint8_t *Ws, const uint8_t *W0, const uint8_t *W1) const {
+        const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+        const uint32_t wb = (uint32_t)b * BB;
+        const uint8_t *A0 = (const uint8_t *)((uintptr_t)W0 & ~(uintptr_t)15);
+        const uint8_t *A1 = GU ? (const uint8_t *)((uintptr_t)W1 & ~(uintptr_t)15) : A0;
+#pragma unroll
+        for (int k = 0; k < KW; k++) {
+            const int jj = w + 8 * k;
+            if (jj < NW) {
+                const uint32_t off = r[k] + wb, o = off & 15u;
+                const uint32_t voff = (off - o) + ((int)c16[k] < (int)(o + BB) ? c16[k] : 0u);
+                pf_dma16((GU && jj >= NW / 2) ? A1 : A0, voff, pf_lds(Ws + 1024 * jj));
+            }
+        }
+    }
+};
 
 // ------------------------------------------------------------- decoders --
 typedef const __attribute__((address_space(3))) uint32_t pq_lds_u32;
@@ -201,7 +231,10 @@ __device__ __forceinline__ uint32_t pq_u32u(const uint8_t *p) {
 // [0, sc, 2 sc, 3 sc] (selector q | 4 picks its byte q).
 __device__ __forceinline__ mq_v4i pq_b_q2k(const uint8_t *blk, int j, int g) {
     const uint32_t sc = pq_u8(blk + 4 * j + g) & 15u;
-    const uint32_t tab = (sc * 0x030201u) << 8;   // v_mul_u32_u24: sc < 16
+    // [0, sc, 2 sc, 3 sc]: the 24-bit product [sc, 2 sc, 3 sc, 0] moved up a byte by v_perm
+    // (a shift would fold into a 32-bit constant and a full-width multiply)
+    const uint32_t t3 = (uint32_t)__umul24(sc, 0x030201u);
+    const uint32_t tab = __builtin_amdgcn_perm(t3, t3, 0x0201000cu);
     const PqWin wq = pq_win(blk + 16 + 32 * (j >> 1) + 16 * (g & 1));
     const uint32_t sh = wq.sh + 2u * (uint32_t)(2 * (j & 1) + (g >> 1));
     mq_v4i r;
@@ -222,8 +255,8 @@ __device__ __forceinline__ mq_v4i pq_b_q3k(const uint8_t *blk, int j, int g) {
     const uint32_t hi2 = (pq_u8(blk + 104 + g) >> (2 * j)) & 3u;
     const uint32_t a = 32u - (lo4 | (hi2 << 4));           // two's complement of a, a in [-31, 32]
     const uint32_t a8 = a & 255u, na8 = (0u - a) & 255u;   // a and -a mod 256
-    const uint32_t t01 = a8 << 16, t23 = a8 * 0x030002u;   // 24-bit products (v_mul_u32_u24)
-    const uint32_t t45 = na8 * 0x030004u, t67 = na8 * 0x010002u;
+    const uint32_t t01 = a8 << 16, t23 = (uint32_t)__umul24(a8, 0x030002u);
+    const uint32_t t45 = (uint32_t)__umul24(na8, 0x030004u), t67 = (uint32_t)__umul24(na8, 0x010002u);
     const uint32_t thi = __builtin_amdgcn_perm(t23, t01, 0x06040200u);   // a * [0, 1, 2, 3]
     const uint32_t tlo = __builtin_amdgcn_perm(t67, t45, 0x06040200u);   // a * [-4, -3, -2, -1]
     const PqWin wq = pq_win(blk + 32 + 32 * (j >> 1) + 16 * (g & 1));
@@ -261,7 +294,7 @@ __device__ __forceinline__ uint32_t pq_mul16(uint32_t a, uint32_t b) {
 __device__ __forceinline__ PqQ4 pq_b_q4k(const uint8_t *blk, int j, int g, uint32_t sc) {
     const PqWin wq = pq_win(blk + 16 + 32 * j + 16 * (g & 1));
     const uint32_t sh = wq.sh + 4u * (uint32_t)(g >> 1);
-    const uint32_t slo = (sc & 7u) * 0x10001u, shi = (sc >> 3) * 0x10001u;
+    const uint32_t slo = (uint32_t)__umul24(sc & 7u, 0x10001u), shi = (uint32_t)__umul24(sc >> 3, 0x10001u);
     PqQ4 r;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
@@ -302,7 +335,8 @@ __device__ __forceinline__ void pq_block(pf_f32x4 (&acc)[2][2], const uint8_t *A
     const int l = threadIdx.x & 63, n = l & 15, g = l >> 4;
     const uint8_t *blk[2] = {blk0, blk1};
     // A fragment of plane p, M tile mt, columns c0 .. (lane: pair 16 mt + n, 16 or 8 bytes at group g)
-    auto a_at = [&](int mt, int p, int col) { return As + (16 * mt + n) * PQ_PITCH + 256 * p + col; };
+    constexpr int APB = 16 * PqFmt<T>::AP;
+    auto a_at = [&](int mt, int p, int col) { return As + (16 * mt + n) * APB + 256 * p + col; };
     if constexpr (T == ST_Q2_K || T == ST_Q3_K) {
         mq_v4i C[2][MT][3];
 #pragma unroll
@@ -394,7 +428,7 @@ __device__ __forceinline__ void pq_block(pf_f32x4 (&acc)[2][2], const uint8_t *A
             }
 #pragma unroll
             for (int mt = 0; mt < MT; mt++) {
-                const uint8_t *sr = As + (16 * mt + n) * PQ_PITCH + 768 + 8 * g;
+                const uint8_t *sr = As + (16 * mt + n) * APB + 768 + 8 * g;
                 const pq_s16x4 shi = *(const pq_s16x4 *)sr, slo = *(const pq_s16x4 *)(sr + 32);
                 pf_f32x4 cm = {0.0f, 0.0f, 0.0f, 0.0f};
                 cm = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(shi, bm, cm, 0, 0, 0);
@@ -415,23 +449,18 @@ __device__ __forceinline__ void pq_proj(uint8_t *smem, const uint8_t *W0, const 
                                         int64_t nb, const uint8_t *pq, const uint32_t *roff, const int32_t *pair,
                                         const float *srow, int nv, int64_t r0, float *__restrict__ out,
                                         int64_t ld_out) {
-    constexpr int BB = PqFmt<T>::BB, PW = PqFmt<T>::PW;
-    constexpr uint32_t st_bytes = PQ_A_BYTES + PQ_ROWS * PW * 16;
+    constexpr int BB = PqFmt<T>::BB, PW = PqFmt<T>::PW, SW = PqFmt<T>::SW;
+    constexpr uint32_t a_bytes = PF_MT * 16 * PqFmt<T>::AP, w_bytes = PQ_ROWS * PW * 16;
+    static_assert(2 * a_bytes + SW * w_bytes <= PQ_LDS_TOP, "LDS stages");
     const int w = threadIdx.x >> 6, l = threadIdx.x & 63, n = l & 15, g = l >> 4;
     const int mat = GU ? (w >> 2) : 0;
     const int rho0 = GU ? 128 * mat + 32 * (w & 3) : 32 * w;   // stage row of N tile 0
     const int64_t grow0 = r0 + (GU ? 32 * (w & 3) : 32 * w);   // its global row
-    auto stage = [&](int64_t b) { return smem + (uint32_t)(b & 1) * st_bytes; };
-    auto issue = [&](int64_t b) {
-        uint8_t *st = stage(b);
-        pq_issue_act(pq, roff, b, st);
-        if (GU) {
-            pq_issue_w<T>(W0, row_bytes, r0, 128, b, st + PQ_A_BYTES);
-            pq_issue_w<T>(W1, row_bytes, r0, 128, b, st + PQ_A_BYTES + 128 * PW * 16);
-        } else {
-            pq_issue_w<T>(W0, row_bytes, r0, 256, b, st + PQ_A_BYTES);
-        }
-    };
+    auto a_stage = [&](int64_t b) { return smem + (uint32_t)(b & 1) * a_bytes; };
+    auto w_stage = [&](int64_t b) { return smem + 2 * a_bytes + (uint32_t)(b % SW) * w_bytes; };
+    PqDma<T, GU> dma;
+    dma.init(roff, W0, W1, row_bytes, r0);
+    const int nwi = PqDma<T, GU>::n_w();
     // the lane's rows: byte offset (mod 16) of row (grow0 + 16 t + n)'s start
     const uint8_t *Wm = mat ? W1 : W0;
     uint32_t rofs[2];
@@ -443,18 +472,23 @@ __device__ __forceinline__ void pq_proj(uint8_t *smem, const uint8_t *W0, const 
     for (int t = 0; t < 2; t++)
 #pragma unroll
         for (int mt = 0; mt < 2; mt++) acc[t][mt] = pf_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    issue(0);
+    // records one block ahead, weights SW - 1 blocks ahead; in issue order
+    // the DMAs of a block b are A_b, then W_(b + SW - 2)
+    dma.issue_a(0, a_stage(0), pq);
+    for (int64_t c = 0; c < SW - 1 && c < nb; c++) dma.issue_w(c, w_stage(c), W0, W1);
     for (int64_t b = 0; b < nb; b++) {
-        __builtin_amdgcn_s_waitcnt(mq_wc_vm(0));
+        // everything up to A_b and W_b; the weights of blocks b + 1 .. b + SW - 2 may fly
+        const int64_t ahead = (nb - 1 - b) < (SW - 2) ? (nb - 1 - b) : (SW - 2);
+        pf_wait_vm(nwi * (int)ahead);
         __syncthreads();   // block b staged by every wave; block b - 1's readers are done
-        if (b + 1 < nb) issue(b + 1);
-        const uint8_t *st = stage(b);
-        const uint8_t *Ws = st + PQ_A_BYTES;
+        if (b + 1 < nb) dma.issue_a(b + 1, a_stage(b + 1), pq);
+        if (b + SW - 1 < nb) dma.issue_w(b + SW - 1, w_stage(b + SW - 1), W0, W1);
+        const uint8_t *Ws = w_stage(b);
         const uint8_t *blk[2];
 #pragma unroll
         for (int t = 0; t < 2; t++)
             blk[t] = Ws + (uint32_t)(rho0 + 16 * t + n) * (PW * 16) + ((rofs[t] + (uint32_t)b * BB) & 15u);
-        pq_block<T, MT>(acc, st, blk[0], blk[1]);
+        pq_block<T, MT>(acc, a_stage(b), blk[0], blk[1]);
     }
     // y = s_pair * acc; lane: pairs 16 mt + 4 g + i, rows grow0 + 16 t + n
 #pragma unroll
