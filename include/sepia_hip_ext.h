@@ -146,9 +146,9 @@ void *sepia_hip_stream(void);
  *   "mq_scope" 0..3  the mq_p/mq_c/mq_s/mq_x overrides apply to every
  *                 matrix-core launch (0) or only to the matvec (1), the
  *                 expert FFN's gate/up (2) or its down (3) launches;
- *   "pf_reg" 1/0  prefill gate/up and down of layers whose projections are
- *                 all Q2_K/Q3_K/Q4_K with the codes decoded into registers
- *                 (1, default), or on the LDS-tile kernels (0);
+ *   "pf_q" 1/0    prefill projections of layers whose six projections are
+ *                 all Q2_K/Q3_K/Q4_K on the int8 matrix cores (1, default),
+ *                 or on the bf16 kernels every other layer takes (0);
  *   "pf_route_m" 1/0  prefill router logits on the f32 matrix cores when x
  *                 and the router rows are 16-byte aligned (default 1). */
 int sepia_hip_set_option(const char *name, int value);

@@ -7,25 +7,28 @@
 //   y[t] = sum_{k < topk} w[t][k] down_e(silu(gate_e x_t) * up_e x_t)
 //        + sum_s w[t][topk + s] down_s(silu(gate_s x_t) * up_s x_t).
 // Launches:
-//   sepia_pf_route    logits[T][n_routed + n_shared] = x . Rw^T (f32 tiles)
+//   sepia_pf_route(_m) logits[T][n_routed + n_shared] = x . Rw^T (f32 tiles,
+//                     or the f32 matrix cores)
 //   sepia_pf_select   one wave per token: idx[T][topk], w[T][topk + n_shared]
 //   sepia_pf_group    one workgroup: the (token, slot) pairs p = t * n_sel + k
 //                     sorted by expert (shared expert s is expert
 //                     n_routed + s) and cut into units of <= 32 pairs
-//   sepia_pf_split    x as bf16 hi / lo and its 16-column sums
-//   sepia_pf_gateup   per (32-row tile, unit): h[p][.] = silu(g) * u (bf16 hi / lo)
-//   sepia_pf_down     per (64-row tile, unit): yp[p][.] = down_e . h[p]
+//   projections       a layer whose six projections are all Q2_K, Q3_K or
+//                     Q4_K runs them on the int8 matrix cores (prefill_q.h:
+//                     sepia_pf_quant, sepia_pf_gateup_q, sepia_pf_down_q);
+//                     any other layer on the bf16 matrix cores here:
+//     sepia_pf_split    x as bf16 hi / lo
+//     sepia_pf_gateup   per (32-row tile, unit): h[p][.] = silu(g) * u (bf16 hi / lo)
+//     sepia_pf_down     per (64-row tile, unit): yp[p][.] = down_e . h[p]
 //   sepia_pf_combine  y[t] = sum_k w[t][k] yp[t * n_sel + k], slot order
-// The projections stream raw weight blocks and the unit's activation rows
-// into LDS by DMA ahead of use and run the bf16 matrix cores with f32
-// accumulation. Q2_K, Q3_K and Q4_K go in as their exact integer codes
-// (scales applied per block or sub-block in f32), the other formats are
-// dequantized bit-exactly and split into bf16 hi + lo; activations are
-// always hi + lo (hi = bf16(v), lo = bf16(v - hi), together within 2^-17
-// |v|; a single bf16 term would miss the 1e-4 ||y||_inf bar by an order of
-// magnitude), and the lo terms are skipped when every lo is zero. Results do
-// not depend on how pairs are grouped into units: every output element is
-// its own dot product in a fixed column order.
+// The bf16 projections stream raw weight blocks and the unit's activation
+// rows into LDS by DMA ahead of use, dequantize the weights bit-exactly into
+// bf16 hi + lo tiles and run the bf16 matrix cores with f32 accumulation;
+// activations are hi + lo too (hi = bf16(v), lo = bf16(v - hi), together
+// within 2^-17 |v|; a single bf16 term would miss the 1e-4 ||y||_inf bar by
+// an order of magnitude), three MFMAs per 32 columns (hi.hi + hi.lo + lo.hi).
+// Results do not depend on how pairs are grouped into units: every output
+// element is its own dot product in a fixed column order.
 #pragma once
 #include "common.h"
 #include "decode.h"
@@ -152,9 +155,7 @@ extern "C" __global__ __launch_bounds__(1024) void sepia_pf_group(const int32_t 
                                                                   int32_t n_routed, int32_t n_shared, int32_t topk,
                                                                   int32_t *__restrict__ list,
                                                                   int32_t *__restrict__ units,
-                                                                  int32_t *__restrict__ n_units,
-                                                                  uint32_t *__restrict__ lo_any) {
-    if (threadIdx.x == 0) *lo_any = 0u;
+                                                                  int32_t *__restrict__ n_units) {
     __shared__ int32_t cnt[1088], off[1089], fill[1088], uoff[1089];
     const int E = n_routed + n_shared, n_sel = topk + n_shared;
     const int64_t P = T * n_sel;
@@ -203,14 +204,9 @@ __device__ __forceinline__ void pf_split(float v, __bf16 &hi, __bf16 &lo) {
     hi = (__bf16)v;
     lo = (__bf16)(v - (float)hi);
 }
-// Segment i (16 values) of x: hi / lo as above, s16[i] = their f32 sum in
-// column order (the K-quant min terms of the integer pipelines).
-// lo_any (zeroed by sepia_pf_group) becomes nonzero if any lo is: with it
-// zero, x is bf16-representable and the projections skip the lo terms (an
-// exact shortcut).
+// Segment i (16 values) of x: hi / lo as above.
 extern "C" __global__ __launch_bounds__(256) void sepia_pf_split(const float *__restrict__ x, int64_t n_seg,
-                                                                 __bf16 *__restrict__ hi, __bf16 *__restrict__ lo,
-                                                                 float *__restrict__ s16, uint32_t *__restrict__ lo_any) {
+                                                                 __bf16 *__restrict__ hi, __bf16 *__restrict__ lo) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= n_seg) return;
     const float4 *x4 = (const float4 *)(x + 16 * i);
@@ -224,22 +220,13 @@ extern "C" __global__ __launch_bounds__(256) void sepia_pf_split(const float *__
         v[4 * c + 3] = t.w;
     }
     __bf16 h[16], l[16];
-    float sum = 0.0f;
-    bool nz = false;
 #pragma unroll
-    for (int k = 0; k < 16; k++) {
-        pf_split(v[k], h[k], l[k]);
-        sum += v[k];
-        nz |= (float)l[k] != 0.0f;
-    }
-    if (__ballot(nz) && (threadIdx.x & 63) == __builtin_ctzll(__ballot(nz)))
-        __hip_atomic_fetch_or(lo_any, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int k = 0; k < 16; k++) pf_split(v[k], h[k], l[k]);
     uint4 *ho = (uint4 *)(hi + 16 * i), *lw = (uint4 *)(lo + 16 * i);
     ho[0] = ((const uint4 *)h)[0];
     ho[1] = ((const uint4 *)h)[1];
     lw[0] = ((const uint4 *)l)[0];
     lw[1] = ((const uint4 *)l)[1];
-    s16[i] = sum;
 }
 
 // ----------------------------------------------------------- pipelines ---
@@ -380,208 +367,6 @@ struct PfProj {
 #define PF_LDS_BYTES 163840                        // the whole 160 KB
 #define PF_O_ROFF (PF_LDS_BYTES - 2 * PF_MT * 4)   // row tables at the top (both paths)
 
-// ------------------------------------------------- integer K-quant path ---
-// For Q2_K, Q3_K and Q4_K the B operand is the weights' integer codes, exact
-// in bf16: Q2_K and Q3_K with their 16-weight sub-block scale folded in
-// (sc * q in 0..45 and (sc - 32) * q in -124..128), Q4_K the bare 4-bit
-// code. Per weight row n and block (src/quants.c and the ggml layouts):
-//   Q2_K  y += d_n sum_k B_k x_k - dmin_n sum_sb m_sb S_sb(x)
-//   Q3_K  y += d_n sum_k B_k x_k
-//   Q4_K  y += sum_j (d_n sc_j sum_{k in j} q_k x_k - dmin_n m_j S32_j(x))
-// with S the 16-column sums of x (S32_j = S_2j + S_2j+1). The Q2_K min term
-// is one K=16 MFMA over the 16 sub-blocks (m exact in bf16, S as hi + lo).
-// Only x carries a hi / lo split: two MFMAs per 32 columns, and a third of
-// the VALU work of decoding to f32 and splitting.
-#define PF_O_RS (PF_O_B + 2 * PF_TILE)   // per-row scalars [64][16] f32 (after the 32 KB of code tiles)
-#define PF_O_BM (PF_O_RS + 64 * 16 * 4)   // Q2_K mins [64][16] bf16
-#define PF_O_S16 (PF_O_BM + 64 * 16 * 2)  // 16-column sums of the unit's x rows [2][32][16] f32
-
-typedef short pf_s16x4 __attribute__((ext_vector_type(4)));
-
-// u32 at a 2-byte-aligned LDS address (LDS loads through an address-space-3
-// pointer: a generic one would become a flat load, which waits on vmcnt).
-typedef const __attribute__((address_space(3))) uint32_t pf_lds_u32;
-__device__ __forceinline__ uint32_t pf_ld32(const uint8_t *p) {
-    const uint32_t a = pf_lds(p);
-    pf_lds_u32 *q = (pf_lds_u32 *)(size_t)(a & ~3u);
-    if ((a & 3) == 0) return q[0];
-    return __builtin_amdgcn_alignbyte(q[1], q[0], a & 3u);   // byte shift
-}
-__device__ __forceinline__ uint4 pf_pack8(const float (&f)[8]) {
-    __bf16 h[8];
-#pragma unroll
-    for (int i = 0; i < 8; i++) h[i] = (__bf16)f[i];
-    return *(const uint4 *)h;
-}
-// Bytes of u (each < 256) as floats.
-__device__ __forceinline__ void pf_bytes(uint32_t u, float *f) {
-    f[0] = mq_ubyte<0>(u);
-    f[1] = mq_ubyte<1>(u);
-    f[2] = mq_ubyte<2>(u);
-    f[3] = mq_ubyte<3>(u);
-}
-
-template <int T> struct PfInt;
-// Q2_K (ggml): weight k = 128 h + 32 s + 16 g + l: q = (qs[32 h + 16 g + l]
-// >> 2 s) & 3, sub-block k / 16, scale byte lo nibble sc, hi nibble m.
-template <> struct PfInt<ST_Q2_K> {
-    static constexpr bool min16 = true, per_sub = false;
-    static __device__ __forceinline__ uint4 chunk(const uint8_t *b, int c) {
-        const int h = c >> 4, s = (c >> 2) & 3;
-        const uint8_t *q = b + 16 + 32 * h + 8 * (c & 3);
-        const uint32_t sc = ld_u8(b + (c >> 1)) & 15u;
-        const uint32_t v0 = ((pf_ld32(q) >> (2 * s)) & 0x03030303u) * sc;
-        const uint32_t v1 = ((pf_ld32(q + 4) >> (2 * s)) & 0x03030303u) * sc;
-        float f[8];
-        pf_bytes(v0, f);
-        pf_bytes(v1, f + 4);
-        return pf_pack8(f);
-    }
-    // item j (0 .. 15) of a row's scalars
-    static __device__ __forceinline__ void scalar(const uint8_t *b, int j, float *rs, __bf16 *bm) {
-        bm[j] = (__bf16)(float)(ld_u8(b + j) >> 4);
-        if (j < 2) rs[j] = h2f(b + 80 + 2 * j);
-    }
-};
-// Q3_K: Q2_K's indexing; q - 4 unless hmask[16 g + l] bit (4 h + s).
-template <> struct PfInt<ST_Q3_K> {
-    static constexpr bool min16 = false, per_sub = false;
-    static __device__ __forceinline__ uint4 chunk(const uint8_t *b, int c) {
-        const int h = c >> 4, s = (c >> 2) & 3, l0 = 8 * (c & 3);
-        const uint8_t *q = b + 32 + 32 * h + l0, *hm = b + l0;
-        const float sc = (float)q3_scale(b + 96, c >> 1);
-        const uint32_t v0 = ((pf_ld32(q) >> (2 * s)) & 0x03030303u) + 4u * ((pf_ld32(hm) >> (4 * h + s)) & 0x01010101u);
-        const uint32_t v1 =
-            ((pf_ld32(q + 4) >> (2 * s)) & 0x03030303u) + 4u * ((pf_ld32(hm + 4) >> (4 * h + s)) & 0x01010101u);
-        float f[8];
-        pf_bytes(v0, f);
-        pf_bytes(v1, f + 4);
-#pragma unroll
-        for (int i = 0; i < 8; i++) f[i] = (f[i] - 4.0f) * sc;
-        return pf_pack8(f);
-    }
-    static __device__ __forceinline__ void scalar(const uint8_t *b, int j, float *rs, __bf16 *) {
-        if (j == 0) rs[0] = h2f(b + 108);
-    }
-};
-// Q4_K: weight k = 64 p + 32 n + l: nibble n of qs[32 p + l], sub-block
-// j = 2 p + n with its (sc, m) pair.
-template <> struct PfInt<ST_Q4_K> {
-    static constexpr bool min16 = false, per_sub = true;
-    static __device__ __forceinline__ uint4 chunk(const uint8_t *b, int c) {
-        const int j = c >> 2;
-        const uint8_t *q = b + 16 + 32 * (j >> 1) + 8 * (c & 3);
-        const int sh = 4 * (j & 1);
-        float f[8];
-        pf_bytes((pf_ld32(q) >> sh) & 0x0F0F0F0Fu, f);
-        pf_bytes((pf_ld32(q + 4) >> sh) & 0x0F0F0F0Fu, f + 4);
-        return pf_pack8(f);
-    }
-    static __device__ __forceinline__ void scalar(const uint8_t *b, int j, float *rs, __bf16 *) {
-        if (j >= 8) return;
-        int sc, mn;
-        k4_scale_min(b + 4, j, sc, mn);
-        rs[j] = h2f(b) * (float)sc;
-        rs[8 + j] = h2f(b + 2) * (float)mn;
-    }
-};
-
-// B tiles (codes) and per-row scalars of the staged raw blocks: nper rows of
-// W0 into B0 and, with W1, nper rows of W1 into B1; rows counted across
-// both (rg) index rs[rg][16] and bm[rg][16]. 512 threads.
-template <int T>
-__device__ __forceinline__ void pf_int_build(const uint8_t *raw, const uint8_t *W0, const uint8_t *W1, int nper,
-                                             uint64_t row_bytes, int64_t rows, int64_t r0, int64_t b, uint8_t *B0,
-                                             uint8_t *B1, float *rs, __bf16 *bm) {
-    constexpr int BB = Fmt<T>::bytes, RD = (BB + 6) / 4;
-    const int nr = W1 ? 2 * nper : nper;
-    auto blk = [&](int rg) {
-        const int mat = rg >= nper, r = rg - mat * nper;
-        int64_t rr = r0 + r;
-        rr = rr < rows ? rr : rows - 1;
-        const uint32_t mis =
-            (uint32_t)((((uintptr_t)(mat ? W1 : W0)) & 3) + (uint64_t)rr * row_bytes + (uint64_t)b * BB) & 3u;
-        return raw + (size_t)rg * RD * 4 + mis;
-    };
-    // 64 rows x 32 chunks and 64 rows x 16 scalar items over 512 threads
-    // (4 chunks and 2 items each)
-    constexpr int NT = 512, NC = 2048 / NT, NI = 1024 / NT;
-    uint4 v[NC];
-#pragma unroll
-    for (int k = 0; k < NC; k++) {
-        const int i = threadIdx.x + NT * k, rg = i >> 5;
-        v[k] = rg < nr ? PfInt<T>::chunk(blk(rg), i & 31) : make_uint4(0, 0, 0, 0);
-    }
-#pragma unroll
-    for (int k = 0; k < NC; k++) {
-        const int i = threadIdx.x + NT * k, rg = i >> 5;
-        if (rg < nr) {
-            const int mat = rg >= nper, r = rg - mat * nper;
-            *(uint4 *)((mat ? B1 : B0) + pf_swz(r, i & 31)) = v[k];
-        }
-    }
-#pragma unroll
-    for (int k = 0; k < NI; k++) {
-        const int i = threadIdx.x + NT * k, rg = i >> 4;
-        if (rg < nr) PfInt<T>::scalar(blk(rg), i & 15, rs + 16 * rg, bm + 16 * rg);
-    }
-}
-
-// acc (rows m0.., columns n0.. of the tile) += this block's share. rsr, bmr:
-// the scalars of the lane's column n0 + (l & 15); s16: [32][16] sums of the
-// unit's x rows over this block.
-template <int T>
-__device__ __forceinline__ void pf_int_mma(pf_f32x4 &acc, const uint8_t *A, int m0, const uint8_t *B, int n0,
-                                           const float *rsr, const __bf16 *bmr, const float *s16, bool xlo) {
-    const int l = threadIdx.x & 63, r = l & 15, g = l >> 4;
-    if constexpr (!PfInt<T>::per_sub) {
-        pf_f32x4 bacc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int kk = 0; kk < 256; kk += 32) {
-            const uint32_t oa = pf_swz(m0 + r, kk / 8 + g), ob = pf_swz(n0 + r, kk / 8 + g);
-            const pf_bf16x8 a_h = *(const pf_bf16x8 *)(A + oa), a_l = *(const pf_bf16x8 *)(A + PF_TILE + oa);
-            const pf_bf16x8 bq = *(const pf_bf16x8 *)(B + ob);
-            bacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_h, bq, bacc, 0, 0, 0);
-            if (xlo) bacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_l, bq, bacc, 0, 0, 0);
-        }
-        const float d = rsr[0];
-#pragma unroll
-        for (int i = 0; i < 4; i++) acc[i] = __builtin_fmaf(d, bacc[i], acc[i]);
-        if constexpr (PfInt<T>::min16) {
-            // A[row r][k = 4 g + i] = S of token m0 + r, sub-block 4 g + i
-            __bf16 sh[4], sl[4];
-#pragma unroll
-            for (int i = 0; i < 4; i++) pf_split(s16[(m0 + r) * 16 + 4 * g + i], sh[i], sl[i]);
-            const pf_s16x4 ah = *(const pf_s16x4 *)sh, al = *(const pf_s16x4 *)sl;
-            const pf_s16x4 bv = *(const pf_s16x4 *)(bmr + 4 * g);
-            pf_f32x4 macc = {0.0f, 0.0f, 0.0f, 0.0f};
-            macc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ah, bv, macc, 0, 0, 0);
-            macc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(al, bv, macc, 0, 0, 0);
-            const float dmin = rsr[1];
-#pragma unroll
-            for (int i = 0; i < 4; i++) acc[i] = __builtin_fmaf(-dmin, macc[i], acc[i]);
-        }
-    } else {
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const int kk = 32 * j;
-            const uint32_t oa = pf_swz(m0 + r, kk / 8 + g), ob = pf_swz(n0 + r, kk / 8 + g);
-            const pf_bf16x8 a_h = *(const pf_bf16x8 *)(A + oa), a_l = *(const pf_bf16x8 *)(A + PF_TILE + oa);
-            const pf_bf16x8 bq = *(const pf_bf16x8 *)(B + ob);
-            pf_f32x4 bacc = {0.0f, 0.0f, 0.0f, 0.0f};
-            bacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_h, bq, bacc, 0, 0, 0);
-            if (xlo) bacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_l, bq, bacc, 0, 0, 0);
-            const float ds = rsr[j], dm = rsr[8 + j];
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const float *sr = s16 + (m0 + 4 * g + i) * 16 + 2 * j;
-                acc[i] = __builtin_fmaf(ds, bacc[i], acc[i]);
-                acc[i] = __builtin_fmaf(-dm, sr[0] + sr[1], acc[i]);
-            }
-        }
-    }
-}
-
 // ------------------------------------------------------------- gate/up ---
 // Workgroup (rows 32 bx .. 32 bx + 31 of I, unit by), 8 waves: wave w
 // computes the 16x16 tile (pairs 16 ((w >> 1) & 1) .., rows 16 (w & 1) ..)
@@ -636,18 +421,6 @@ __device__ __forceinline__ void pf_gateup_t(uint8_t *smem, const uint8_t *Wg, co
     }
 }
 
-// The unit's 16-column sums of x for block b into dst [32][16] f32 (two
-// wave instructions, 4 lanes per row).
-__device__ __forceinline__ void pf_issue_s16(const float *s16, const uint32_t *roff, int64_t b, uint8_t *dst) {
-    const int nw = (int)(blockDim.x >> 6), w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-    const int lane = threadIdx.x & 63;
-    for (int j = w; j < 2; j += nw) {
-        const int row = 16 * j + (lane >> 2), qd = lane & 3;
-        const uint32_t voff = 4u * (roff[row] / 16u + 16u * (uint32_t)b) + 16u * (uint32_t)qd;
-        pf_dma16(s16, voff, pf_lds(dst + 1024 * j));
-    }
-}
-
 // vmcnt(n) for a run-time n (0 .. 63).
 __device__ __forceinline__ void pf_wait_vm(int n) {
     switch (n) {
@@ -661,98 +434,6 @@ __device__ __forceinline__ void pf_wait_vm(int n) {
     default: __builtin_amdgcn_s_waitcnt(mq_wc_vm(0)); break;
     }
 }
-// Wave instructions of j = w, w + nw, ... below n.
-__device__ __forceinline__ int pf_share(int n, int w, int nw) { return n > w ? (n - w + nw - 1) / nw : 0; }
-
-// The integer path as an S-stage pipeline: stage s of a ring holds block b's
-// activation tiles (hi, and lo unless x is bf16-representable), raw weight
-// windows and 16-column sums; S - 1 blocks are in flight while one
-// computes (S = 2 .. 4, what the LDS holds for the format).
-// LDS: [codes: 32 KB][row scalars 4 KB][mins 2 KB][stages][row tables].
-// GU: 8 waves, wave w computes the 16x16 tile (pairs 16 ((w >> 1) & 1),
-// rows 16 (w & 1)) of gate (w < 4) or up (w >= 4) over 32 rows of each;
-// the down kernel: rows 16 (w & 3) of the M tile w >> 2 over 64 rows.
-#define PF_I_RS (2 * PF_TILE)
-#define PF_I_BM (PF_I_RS + 64 * 16 * 4)
-#define PF_I_ST (PF_I_BM + 64 * 16 * 2)
-template <int T, bool GU>
-__device__ __forceinline__ void pf_int_pipe(uint8_t *smem, const uint8_t *W0, const uint8_t *W1, uint64_t row_bytes,
-                                            int64_t nb, int64_t rows, const __bf16 *ah, const __bf16 *al,
-                                            const float *s16, const uint32_t *roff, const int32_t *pair, int nv,
-                                            int64_t r0, bool xlo, __bf16 *__restrict__ hh, __bf16 *__restrict__ hl,
-                                            float *__restrict__ yp, int64_t ld_out) {
-    constexpr int RD = (Fmt<T>::bytes + 6) / 4;
-    constexpr bool need_s = GU && (PfInt<T>::min16 || PfInt<T>::per_sub);
-    constexpr int nper = GU ? 32 : 64;
-    const int w = threadIdx.x >> 6, l = threadIdx.x & 63, nw = (int)(blockDim.x >> 6);
-    const int m0 = GU ? 16 * ((w >> 1) & 1) : 16 * (w >> 2), n0 = GU ? 16 * (w & 1) : 16 * (w & 3);
-    const int up_w = GU ? (w >> 2) : 0;
-    uint8_t *B0 = smem, *B1 = smem + PF_TILE;
-    float *rs = (float *)(smem + PF_I_RS);
-    __bf16 *bm = (__bf16 *)(smem + PF_I_BM);
-    const int rg = (GU ? 32 * up_w : 0) + n0 + (l & 15);
-    // stage layout
-    const uint32_t a_bytes = xlo ? 2 * PF_TILE : PF_TILE, raw_bytes = 64 * RD * 4, s_bytes = need_s ? 2048 : 0;
-    const uint32_t st_bytes = a_bytes + raw_bytes + s_bytes;
-    int S = (int)((PF_O_ROFF - PF_I_ST) / st_bytes);
-    S = S < 4 ? S : 4;
-    auto stage = [&](int64_t b) { return smem + PF_I_ST + (uint32_t)(b % S) * st_bytes; };
-    // DMA instructions of this wave per stage
-    const int n_raw = (nper * RD + 63) >> 6;
-    const int per_stage = pf_share(xlo ? 32 : 16, w, nw) + (GU ? 2 : 1) * pf_share(n_raw, w, nw) +
-                          (need_s ? pf_share(2, w, nw) : 0);
-    auto issue = [&](int64_t b) {
-        uint8_t *st = stage(b);
-        pf_issue_act(ah, al, roff, b, st, xlo);
-        uint8_t *raw = st + a_bytes;
-        pf_issue_raw<T>(W0, row_bytes, rows, r0, nper, b, raw);
-        if (GU) pf_issue_raw<T>(W1, row_bytes, rows, r0, nper, b, raw + nper * RD * 4);
-        if constexpr (need_s) pf_issue_s16(s16, roff, b, st + a_bytes + raw_bytes);
-    };
-    for (int64_t b = 0; b < S - 1 && b < nb; b++) issue(b);
-    pf_f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int64_t b = 0; b < nb; b++) {
-        // blocks b + 1 .. min(b + S - 2, nb - 1) may stay in flight
-        const int64_t ahead = (nb - 1 - b) < (S - 2) ? (nb - 1 - b) : (S - 2);
-        pf_wait_vm(per_stage * (int)ahead);
-        __syncthreads();
-        if (b + S - 1 < nb) issue(b + S - 1);
-        uint8_t *st = stage(b);
-        pf_int_build<T>(st + a_bytes, W0, GU ? W1 : nullptr, nper, row_bytes, rows, r0, b, B0, GU ? B1 : nullptr,
-                            rs, bm);
-        __syncthreads();
-        const uint8_t *Bw = (GU && up_w) ? B1 : B0;
-        const float *s16b = (const float *)(st + a_bytes + raw_bytes);
-        pf_int_mma<T>(acc, st, m0, Bw, n0, rs + 16 * rg, bm + 16 * rg, s16b, xlo);
-    }
-    if constexpr (GU) {
-        __syncthreads();
-        float *xch = (float *)(smem + PF_I_ST) + (w & 3) * 256 + l * 4;
-        if (up_w) *(pf_f32x4 *)xch = acc;
-        __syncthreads();
-        if (up_w) return;
-        const pf_f32x4 u = *(const pf_f32x4 *)xch;
-        const int64_t row = r0 + n0 + (l & 15);
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int m = m0 + 4 * (l >> 4) + i;
-            if (m < nv && row < rows) {
-                __bf16 a, c;
-                pf_split(silu_f32(acc[i]) * u[i], a, c);
-                hh[(int64_t)pair[m] * rows + row] = a;
-                hl[(int64_t)pair[m] * rows + row] = c;
-            }
-        }
-    } else {
-        const int64_t row = r0 + n0 + (l & 15);
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int m = m0 + 4 * (l >> 4) + i;
-            if (m < nv && row < rows) yp[(int64_t)pair[m] * ld_out + row] = acc[i];
-        }
-    }
-}
-
 // The unit's rows: roff[m] = element offset of pair m's activation row (rows
 // past nv repeat row 0), pair[m] its pair index.
 __device__ __forceinline__ void pf_unit_rows(const int32_t *pairs, int nv, bool by_token, int32_t n_sel, int64_t ld,
@@ -770,8 +451,8 @@ __device__ __forceinline__ void pf_unit_rows(const int32_t *pairs, int nv, bool 
 
 extern "C" __global__ __launch_bounds__(512) void sepia_pf_gateup(
     PfProj gate, PfProj up, PfProj s_gate, PfProj s_up, int32_t n_routed, int32_t n_sel, int64_t I, int64_t H,
-    const __bf16 *__restrict__ xh, const __bf16 *__restrict__ xl, const float *__restrict__ s16,
-    const uint32_t *__restrict__ lo_any, const int32_t *__restrict__ list, const int32_t *__restrict__ units,
+    const __bf16 *__restrict__ xh, const __bf16 *__restrict__ xl, const int32_t *__restrict__ list,
+    const int32_t *__restrict__ units,
     const int32_t *__restrict__ n_units, __bf16 *__restrict__ hh, __bf16 *__restrict__ hl) {
     if ((int32_t)blockIdx.y >= n_units[0]) return;
     extern __shared__ __attribute__((aligned(16))) uint8_t pf_smem[];
@@ -786,390 +467,11 @@ extern "C" __global__ __launch_bounds__(512) void sepia_pf_gateup(
     uint32_t *roff;
     int32_t *pair;
     pf_unit_rows(list + un[1], nv, true, n_sel, H, smem, roff, pair);
-    const bool xlo = __builtin_amdgcn_readfirstlane((int)*lo_any) != 0;
     switch (G.type) {
 #define PF_GU(TT) case TT: pf_gateup_t<TT>(smem, wg, wu, G.row_bytes, G.n_blocks, I, xh, xl, roff, pair, nv, r0, hh, hl); break;
-#define PF_GI(TT) case TT: pf_int_pipe<TT, true>(smem, wg, wu, G.row_bytes, G.n_blocks, I, xh, xl, s16, roff, pair, nv, r0, xlo, hh, hl, nullptr, 0); break;
-        PF_GI(ST_Q2_K) PF_GI(ST_Q3_K) PF_GI(ST_Q4_K) PF_GU(ST_Q5_K) PF_GU(ST_Q6_K)
+        PF_GU(ST_Q2_K) PF_GU(ST_Q3_K) PF_GU(ST_Q4_K) PF_GU(ST_Q5_K) PF_GU(ST_Q6_K)
         PF_GU(ST_IQ2_XS) PF_GU(ST_IQ3_XXS) PF_GU(ST_IQ4_XS)
 #undef PF_GU
-#undef PF_GI
-    default: break;
-    }
-}
-
-// Raw blocks b of nr rows as pf_issue_raw, in 16-byte pieces: row k's
-// 16-byte-aligned window of PF_P16 pieces that holds the block lands at
-// dst + 16 PF_P16 k (the block at byte (row address) & 15 of it). A wave
-// instruction moves 1 KB, a quarter of the instructions of 4-byte pieces.
-template <int T> struct PfP16 { static constexpr int n = (Fmt<T>::bytes + 15 + 15) / 16; };
-template <int T>
-__device__ __forceinline__ void pf_issue_raw16(const uint8_t *W, uint64_t row_bytes, int64_t rows, int64_t r0, int nr,
-                                               int64_t b, uint8_t *dst) {
-    constexpr int BB = Fmt<T>::bytes, P16 = PfP16<T>::n;
-    const int nw = (int)(blockDim.x >> 6), w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-    const int lane = threadIdx.x & 63;
-    const uint8_t *Wa = (const uint8_t *)((uintptr_t)W & ~(uintptr_t)15);
-    const uint32_t delta = (uint32_t)((uintptr_t)W & 15);
-    const int n_ins = (nr * P16 + 63) >> 6;
-    for (int j = w; j < n_ins; j += nw) {
-        const int i = 64 * j + lane;
-        if (i < nr * P16) {
-            const int r = i / P16, d = i - r * P16;
-            int64_t rr = r0 + r;
-            rr = rr < rows ? rr : rows - 1;
-            const uint64_t off = delta + (uint64_t)rr * row_bytes + (uint64_t)b * BB;
-            pf_dma16(Wa, (uint32_t)(off & ~(uint64_t)15) + 16u * (uint32_t)d, pf_lds(dst + 1024 * j));
-        }
-    }
-}
-
-// The staged raw window of a row for the register pipelines: 16-byte
-// pieces when their number is odd (Q2_K: 7), else pf_issue_raw's 4-byte
-// window (Q3_K: 29 dwords, Q4_K: 37). Either way the row stride is an odd
-// number of dwords times 4 at most, so the 16 rows a lane group decodes
-// from fall in different LDS banks (a stride of 32 dwords put them all in
-// one).
-template <int T> struct PfRaw {
-    static constexpr bool w16 = (PfP16<T>::n & 1) != 0;
-    static constexpr int bytes = w16 ? 16 * PfP16<T>::n : 4 * ((Fmt<T>::bytes + 6) / 4);
-    static constexpr uint32_t align = w16 ? 15u : 3u;
-    static __device__ __forceinline__ int ins(int nr) { return (nr * bytes / (w16 ? 16 : 4) + 63) >> 6; }
-    static __device__ __forceinline__ void issue(const uint8_t *W, uint64_t row_bytes, int64_t rows, int64_t r0,
-                                                 int nr, int64_t b, uint8_t *dst) {
-        if constexpr (w16) pf_issue_raw16<T>(W, row_bytes, rows, r0, nr, b, dst);
-        else pf_issue_raw<T>(W, row_bytes, rows, r0, nr, b, dst);
-    }
-};
-
-// ------------------------------------------ gate/up, codes in registers ---
-// Both M tiles (pairs 0 .. 15, 16 .. 31) of one 16-row N tile += this
-// block's share, the B fragments decoded by each lane from its own row's
-// staged raw block `blk` (lane l: row l & 15, codes k = 32 j + 8 (l >> 4) ..
-// + 7) and used for both tiles. Same per-block arithmetic as pf_int_mma.
-template <int T>
-__device__ __forceinline__ void pf_reg_mma(pf_f32x4 &acc0, pf_f32x4 &acc1, const uint8_t *A, const uint8_t *blk,
-                                           const float *s16, bool xlo) {
-    const int l = threadIdx.x & 63, r = l & 15, g = l >> 4;
-    if constexpr (!PfInt<T>::per_sub) {
-        pf_f32x4 b0 = {0.0f, 0.0f, 0.0f, 0.0f}, b1 = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const uint4 q = PfInt<T>::chunk(blk, 4 * j + g);
-            const pf_bf16x8 bq = *(const pf_bf16x8 *)&q;
-            const uint32_t o0 = pf_swz(r, 4 * j + g), o1 = pf_swz(16 + r, 4 * j + g);
-            b0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(const pf_bf16x8 *)(A + o0), bq, b0, 0, 0, 0);
-            b1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(const pf_bf16x8 *)(A + o1), bq, b1, 0, 0, 0);
-            if (xlo) {
-                b0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(const pf_bf16x8 *)(A + PF_TILE + o0), bq, b0, 0, 0, 0);
-                b1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(const pf_bf16x8 *)(A + PF_TILE + o1), bq, b1, 0, 0, 0);
-            }
-        }
-        const float d = h2f(blk + (T == ST_Q2_K ? 80 : 108));
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            acc0[i] = __builtin_fmaf(d, b0[i], acc0[i]);
-            acc1[i] = __builtin_fmaf(d, b1[i], acc1[i]);
-        }
-        if constexpr (PfInt<T>::min16) {
-            // B[k = 4 g + i][row r] = min of sub-block 4 g + i; A[pair][k] = S
-            __bf16 bmv[4];
-#pragma unroll
-            for (int i = 0; i < 4; i++) bmv[i] = (__bf16)(float)(ld_u8(blk + 4 * g + i) >> 4);
-            const pf_s16x4 bv = *(const pf_s16x4 *)bmv;
-            const float dmin = h2f(blk + 82);
-#pragma unroll
-            for (int mt = 0; mt < 2; mt++) {
-                __bf16 sh[4], sl[4];
-#pragma unroll
-                for (int i = 0; i < 4; i++) pf_split(s16[(16 * mt + r) * 16 + 4 * g + i], sh[i], sl[i]);
-                pf_f32x4 macc = {0.0f, 0.0f, 0.0f, 0.0f};
-                macc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(*(const pf_s16x4 *)sh, bv, macc, 0, 0, 0);
-                macc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(*(const pf_s16x4 *)sl, bv, macc, 0, 0, 0);
-                pf_f32x4 &acc = mt ? acc1 : acc0;
-#pragma unroll
-                for (int i = 0; i < 4; i++) acc[i] = __builtin_fmaf(-dmin, macc[i], acc[i]);
-            }
-        }
-    } else {
-        const float d = h2f(blk), dmin = h2f(blk + 2);
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            int sc, mn;
-            k4_scale_min(blk + 4, j, sc, mn);
-            const float ds = d * (float)sc, dm = dmin * (float)mn;
-            const uint4 q = PfInt<T>::chunk(blk, 4 * j + g);
-            const pf_bf16x8 bq = *(const pf_bf16x8 *)&q;
-            const uint32_t o0 = pf_swz(r, 4 * j + g), o1 = pf_swz(16 + r, 4 * j + g);
-            pf_f32x4 b0 = {0.0f, 0.0f, 0.0f, 0.0f}, b1 = {0.0f, 0.0f, 0.0f, 0.0f};
-            b0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(const pf_bf16x8 *)(A + o0), bq, b0, 0, 0, 0);
-            b1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(const pf_bf16x8 *)(A + o1), bq, b1, 0, 0, 0);
-            if (xlo) {
-                b0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(const pf_bf16x8 *)(A + PF_TILE + o0), bq, b0, 0, 0, 0);
-                b1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(const pf_bf16x8 *)(A + PF_TILE + o1), bq, b1, 0, 0, 0);
-            }
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const float *s0 = s16 + (4 * g + i) * 16 + 2 * j, *s1 = s16 + (16 + 4 * g + i) * 16 + 2 * j;
-                acc0[i] = __builtin_fmaf(ds, b0[i], acc0[i]);
-                acc0[i] = __builtin_fmaf(-dm, s0[0] + s0[1], acc0[i]);
-                acc1[i] = __builtin_fmaf(ds, b1[i], acc1[i]);
-                acc1[i] = __builtin_fmaf(-dm, s1[0] + s1[1], acc1[i]);
-            }
-        }
-    }
-}
-
-// Gate/up of the integer formats with the codes in registers: workgroup
-// (rows 64 bx .. 64 bx + 63 of I, unit by), 8 waves; wave w takes rows
-// 16 (w & 3) .. of gate (w < 4) or up (w >= 4) for all 32 pairs. A stage
-// holds block b's activation tiles, the raw windows of 64 gate and 64 up
-// rows and the 16-column sums; S - 1 blocks fly while one computes, one
-// barrier a step (no code tiles to build). The up waves hand their tiles
-// to the gate waves through LDS at the end.
-template <int T>
-__device__ __forceinline__ void pf_reg_gateup(uint8_t *smem, const uint8_t *Wg, const uint8_t *Wu, uint64_t row_bytes,
-                                              int64_t nb, int64_t rows, const __bf16 *ah, const __bf16 *al,
-                                              const float *s16, const uint32_t *roff, const int32_t *pair, int nv,
-                                              int64_t r0, bool xlo, __bf16 *__restrict__ hh, __bf16 *__restrict__ hl) {
-    constexpr int BB = Fmt<T>::bytes, RW = PfRaw<T>::bytes;   // raw window bytes a row
-    constexpr bool need_s = PfInt<T>::min16 || PfInt<T>::per_sub;
-    const int w = threadIdx.x >> 6, l = threadIdx.x & 63, r = l & 15, nw = (int)(blockDim.x >> 6);
-    const int mat = w >> 2, n0 = 16 * (w & 3);
-    const uint32_t a_bytes = xlo ? 2 * PF_TILE : PF_TILE, raw_bytes = 128 * RW, s_bytes = need_s ? 2048 : 0;
-    const uint32_t st_bytes = a_bytes + raw_bytes + s_bytes;
-    int S = (int)(PF_O_ROFF / st_bytes);
-    S = S < 4 ? S : 4;   // >= 3 for every format (Q4_K with lo terms: 53,760-byte stages)
-    auto stage = [&](int64_t b) { return smem + (uint32_t)((int)b % S) * st_bytes; };
-    const int n_raw = PfRaw<T>::ins(64);
-    const int per_stage =
-        pf_share(xlo ? 32 : 16, w, nw) + 2 * pf_share(n_raw, w, nw) + (need_s ? pf_share(2, w, nw) : 0);
-    auto issue = [&](int64_t b) {
-        uint8_t *st = stage(b);
-        pf_issue_act(ah, al, roff, b, st, xlo);
-        PfRaw<T>::issue(Wg, row_bytes, rows, r0, 64, b, st + a_bytes);
-        PfRaw<T>::issue(Wu, row_bytes, rows, r0, 64, b, st + a_bytes + 64 * RW);
-        if constexpr (need_s) pf_issue_s16(s16, roff, b, st + a_bytes + raw_bytes);
-    };
-    // this lane's row (clamped as the raw issue clamps it) and its byte offset
-    int64_t rr = r0 + n0 + r;
-    rr = rr < rows ? rr : rows - 1;
-    const uint64_t rowoff = (uint64_t)((uintptr_t)(mat ? Wu : Wg) & PfRaw<T>::align) + (uint64_t)rr * row_bytes;
-    const uint32_t slot = (uint32_t)(64 * mat + n0 + r) * RW;
-    for (int64_t b = 0; b < S - 1 && b < nb; b++) issue(b);
-    pf_f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int64_t b = 0; b < nb; b++) {
-        const int64_t ahead = (nb - 1 - b) < (S - 2) ? (nb - 1 - b) : (S - 2);
-        pf_wait_vm(per_stage * (int)ahead);
-        __syncthreads();   // every wave's DMAs of block b; block b - 1's reads are done
-        if (b + S - 1 < nb) issue(b + S - 1);
-        const uint8_t *st = stage(b);
-        const uint32_t mis = (uint32_t)(rowoff + (uint64_t)b * BB) & PfRaw<T>::align;
-        pf_reg_mma<T>(acc0, acc1, st, st + a_bytes + slot + mis, (const float *)(st + a_bytes + raw_bytes), xlo);
-    }
-    __syncthreads();
-    float *xch = (float *)smem + (w & 3) * 512 + l * 8;
-    if (mat) {
-        *(pf_f32x4 *)xch = acc0;
-        *(pf_f32x4 *)(xch + 4) = acc1;
-    }
-    __syncthreads();
-    if (mat) return;
-    const pf_f32x4 u0 = *(const pf_f32x4 *)xch, u1 = *(const pf_f32x4 *)(xch + 4);
-    const int64_t row = r0 + n0 + r;
-#pragma unroll
-    for (int mt = 0; mt < 2; mt++) {
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int m = 16 * mt + 4 * (l >> 4) + i;
-            if (m < nv && row < rows) {
-                __bf16 a, c;
-                pf_split(silu_f32(mt ? acc1[i] : acc0[i]) * (mt ? u1[i] : u0[i]), a, c);
-                hh[(int64_t)pair[m] * rows + row] = a;
-                hl[(int64_t)pair[m] * rows + row] = c;
-            }
-        }
-    }
-}
-
-// Gate/up of the integer formats with the codes in registers
-// (pf_reg_gateup): the same result layout as sepia_pf_gateup over 64-row
-// tiles. The host launches it only when every gate/up projection of the
-// layer is Q2_K, Q3_K or Q4_K.
-extern "C" __global__ __launch_bounds__(512) void sepia_pf_gateup_r(
-    PfProj gate, PfProj up, PfProj s_gate, PfProj s_up, int32_t n_routed, int32_t n_sel, int64_t I, int64_t H,
-    const __bf16 *__restrict__ xh, const __bf16 *__restrict__ xl, const float *__restrict__ s16,
-    const uint32_t *__restrict__ lo_any, const int32_t *__restrict__ list, const int32_t *__restrict__ units,
-    const int32_t *__restrict__ n_units, __bf16 *__restrict__ hh, __bf16 *__restrict__ hl) {
-    if ((int32_t)blockIdx.y >= n_units[0]) return;
-    extern __shared__ __attribute__((aligned(16))) uint8_t pf_smem[];
-    uint8_t *smem = pf_smem;
-    const int32_t *un = units + 3 * blockIdx.y;
-    const int32_t e = un[0], nv = un[2];
-    const bool routed = e < n_routed;
-    const PfProj &G = routed ? gate : s_gate, &U = routed ? up : s_up;
-    const int64_t ei = routed ? e : e - n_routed;
-    const uint8_t *wg = G.base + ei * G.stride, *wu = U.base + ei * U.stride;
-    const int64_t r0 = (int64_t)blockIdx.x * 64;
-    uint32_t *roff;
-    int32_t *pair;
-    pf_unit_rows(list + un[1], nv, true, n_sel, H, smem, roff, pair);
-    const bool xlo = __builtin_amdgcn_readfirstlane((int)*lo_any) != 0;
-    switch (G.type) {
-#define PF_GR(TT) case TT: pf_reg_gateup<TT>(smem, wg, wu, G.row_bytes, G.n_blocks, I, xh, xl, s16, roff, pair, nv, r0, xlo, hh, hl); break;
-        PF_GR(ST_Q2_K) PF_GR(ST_Q3_K) PF_GR(ST_Q4_K)
-#undef PF_GR
-    default: break;
-    }
-}
-
-// ---------------------------------------------- down, codes in registers ---
-// As pf_reg_mma for a projection whose input (h) has no staged 16-column
-// sums: the min terms come from one more MFMA per 32 columns with a B
-// fragment that holds the row's min code (Q2_K: the 16-column segment's min
-// nibble; Q4_K: ones, scaled by the sub-block's d_min m in f32).
-template <int T>
-__device__ __forceinline__ void pf_reg_mma_dn(pf_f32x4 &acc0, pf_f32x4 &acc1, const uint8_t *A, const uint8_t *blk,
-                                              bool xlo) {
-    const int l = threadIdx.x & 63, r = l & 15, g = l >> 4;
-    auto mm2 = [&](pf_f32x4 &c0, pf_f32x4 &c1, const pf_bf16x8 &bq, uint32_t o0, uint32_t o1) {
-        c0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(const pf_bf16x8 *)(A + o0), bq, c0, 0, 0, 0);
-        c1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(const pf_bf16x8 *)(A + o1), bq, c1, 0, 0, 0);
-        if (xlo) {
-            c0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(const pf_bf16x8 *)(A + PF_TILE + o0), bq, c0, 0, 0, 0);
-            c1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(const pf_bf16x8 *)(A + PF_TILE + o1), bq, c1, 0, 0, 0);
-        }
-    };
-    auto splat = [](float v) {
-        const __bf16 h = (__bf16)v;
-        pf_bf16x8 o;
-#pragma unroll
-        for (int i = 0; i < 8; i++) o[i] = h;
-        return o;
-    };
-    if constexpr (!PfInt<T>::per_sub) {
-        pf_f32x4 b0 = {0.0f, 0.0f, 0.0f, 0.0f}, b1 = {0.0f, 0.0f, 0.0f, 0.0f};
-        pf_f32x4 n0 = {0.0f, 0.0f, 0.0f, 0.0f}, n1 = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const uint4 q = PfInt<T>::chunk(blk, 4 * j + g);
-            const uint32_t o0 = pf_swz(r, 4 * j + g), o1 = pf_swz(16 + r, 4 * j + g);
-            mm2(b0, b1, *(const pf_bf16x8 *)&q, o0, o1);
-            if constexpr (PfInt<T>::min16) mm2(n0, n1, splat((float)(ld_u8(blk + 2 * j + (g >> 1)) >> 4)), o0, o1);
-        }
-        const float d = h2f(blk + (T == ST_Q2_K ? 80 : 108));
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            acc0[i] = __builtin_fmaf(d, b0[i], acc0[i]);
-            acc1[i] = __builtin_fmaf(d, b1[i], acc1[i]);
-        }
-        if constexpr (PfInt<T>::min16) {
-            const float dmin = h2f(blk + 82);
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                acc0[i] = __builtin_fmaf(-dmin, n0[i], acc0[i]);
-                acc1[i] = __builtin_fmaf(-dmin, n1[i], acc1[i]);
-            }
-        }
-    } else {
-        const float d = h2f(blk), dmin = h2f(blk + 2);
-        const pf_bf16x8 ones = splat(1.0f);
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            int sc, mn;
-            k4_scale_min(blk + 4, j, sc, mn);
-            const float ds = d * (float)sc, dm = dmin * (float)mn;
-            const uint4 q = PfInt<T>::chunk(blk, 4 * j + g);
-            const uint32_t o0 = pf_swz(r, 4 * j + g), o1 = pf_swz(16 + r, 4 * j + g);
-            pf_f32x4 b0 = {0.0f, 0.0f, 0.0f, 0.0f}, b1 = {0.0f, 0.0f, 0.0f, 0.0f};
-            pf_f32x4 s0 = {0.0f, 0.0f, 0.0f, 0.0f}, s1 = {0.0f, 0.0f, 0.0f, 0.0f};
-            mm2(b0, b1, *(const pf_bf16x8 *)&q, o0, o1);
-            mm2(s0, s1, ones, o0, o1);
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                acc0[i] = __builtin_fmaf(ds, b0[i], acc0[i]);
-                acc0[i] = __builtin_fmaf(-dm, s0[i], acc0[i]);
-                acc1[i] = __builtin_fmaf(ds, b1[i], acc1[i]);
-                acc1[i] = __builtin_fmaf(-dm, s1[i], acc1[i]);
-            }
-        }
-    }
-}
-
-// Down of the integer formats with the codes in registers: workgroup (rows
-// 128 bx .. 128 bx + 127 of H, unit by), 8 waves; wave w takes rows
-// 16 w .. for all 32 pairs. A stage holds block b's h tiles (hi and lo) and
-// the raw windows of 128 rows; S - 1 blocks fly while one computes.
-// yp[p][row] = down . h[p].
-template <int T>
-__device__ __forceinline__ void pf_reg_down(uint8_t *smem, const uint8_t *Wd, uint64_t row_bytes, int64_t nb,
-                                            int64_t rows, const __bf16 *ah, const __bf16 *al, const uint32_t *roff,
-                                            const int32_t *pair, int nv, int64_t r0, float *__restrict__ yp) {
-    constexpr int BB = Fmt<T>::bytes, RW = PfRaw<T>::bytes;   // raw window bytes a row
-    const int w = threadIdx.x >> 6, l = threadIdx.x & 63, r = l & 15, nw = (int)(blockDim.x >> 6);
-    const int n0 = 16 * w;
-    const uint32_t a_bytes = 2 * PF_TILE, raw_bytes = 128 * RW;
-    const uint32_t st_bytes = a_bytes + raw_bytes;
-    int S = (int)(PF_O_ROFF / st_bytes);
-    S = S < 4 ? S : 4;   // 3 for Q4_K (51,712-byte stages)
-    auto stage = [&](int64_t b) { return smem + (uint32_t)((int)b % S) * st_bytes; };
-    const int per_stage = pf_share(32, w, nw) + pf_share(PfRaw<T>::ins(128), w, nw);
-    auto issue = [&](int64_t b) {
-        uint8_t *st = stage(b);
-        pf_issue_act(ah, al, roff, b, st, true);
-        PfRaw<T>::issue(Wd, row_bytes, rows, r0, 128, b, st + a_bytes);
-    };
-    int64_t rr = r0 + n0 + r;
-    rr = rr < rows ? rr : rows - 1;
-    const uint64_t rowoff = (uint64_t)((uintptr_t)Wd & PfRaw<T>::align) + (uint64_t)rr * row_bytes;
-    const uint32_t slot = (uint32_t)(n0 + r) * RW;
-    for (int64_t b = 0; b < S - 1 && b < nb; b++) issue(b);
-    pf_f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int64_t b = 0; b < nb; b++) {
-        const int64_t ahead = (nb - 1 - b) < (S - 2) ? (nb - 1 - b) : (S - 2);
-        pf_wait_vm(per_stage * (int)ahead);
-        __syncthreads();   // every wave's DMAs of block b; block b - 1's reads are done
-        if (b + S - 1 < nb) issue(b + S - 1);
-        const uint8_t *st = stage(b);
-        const uint32_t mis = (uint32_t)(rowoff + (uint64_t)b * BB) & PfRaw<T>::align;
-        pf_reg_mma_dn<T>(acc0, acc1, st, st + a_bytes + slot + mis, true);
-    }
-    const int64_t row = r0 + n0 + r;
-#pragma unroll
-    for (int mt = 0; mt < 2; mt++) {
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int m = 16 * mt + 4 * (l >> 4) + i;
-            if (m < nv && row < rows) yp[(int64_t)pair[m] * rows + row] = mt ? acc1[i] : acc0[i];
-        }
-    }
-}
-
-// Down of the integer formats with the codes in registers (pf_reg_down):
-// the same result layout as sepia_pf_down over 128-row tiles. The host
-// launches it only when every down projection of the layer is Q2_K, Q3_K
-// or Q4_K.
-extern "C" __global__ __launch_bounds__(512) void sepia_pf_down_r(
-    PfProj down, PfProj s_down, int32_t n_routed, int64_t I, int64_t H, const __bf16 *__restrict__ hh,
-    const __bf16 *__restrict__ hl, const int32_t *__restrict__ list, const int32_t *__restrict__ units,
-    const int32_t *__restrict__ n_units, float *__restrict__ yp) {
-    if ((int32_t)blockIdx.y >= n_units[0]) return;
-    extern __shared__ __attribute__((aligned(16))) uint8_t pf_smem[];
-    uint8_t *smem = pf_smem;
-    const int32_t *un = units + 3 * blockIdx.y;
-    const int32_t e = un[0], nv = un[2];
-    const bool routed = e < n_routed;
-    const PfProj &D = routed ? down : s_down;
-    const int64_t ei = routed ? e : e - n_routed;
-    const uint8_t *wd = D.base + ei * D.stride;
-    const int64_t r0 = (int64_t)blockIdx.x * 128;
-    uint32_t *roff;
-    int32_t *pair;
-    pf_unit_rows(list + un[1], nv, false, 1, I, smem, roff, pair);
-    switch (D.type) {
-#define PF_DR(TT) case TT: pf_reg_down<TT>(smem, wd, D.row_bytes, D.n_blocks, H, hh, hl, roff, pair, nv, r0, yp); break;
-        PF_DR(ST_Q2_K) PF_DR(ST_Q3_K) PF_DR(ST_Q4_K)
-#undef PF_DR
     default: break;
     }
 }
@@ -1230,8 +532,7 @@ extern "C" __global__ __launch_bounds__(512) void sepia_pf_down(
     pf_unit_rows(list + un[1], nv, false, 1, I, smem, roff, pair);
     switch (D.type) {
 #define PF_DN(TT) case TT: pf_down_t<TT>(smem, wd, D.row_bytes, D.n_blocks, H, hh, hl, roff, pair, nv, r0, yp); break;
-    case ST_Q3_K: pf_int_pipe<ST_Q3_K, false>(smem, wd, nullptr, D.row_bytes, D.n_blocks, H, hh, hl, nullptr, roff, pair, nv, r0, true, nullptr, nullptr, yp, H); break;
-        PF_DN(ST_Q2_K) PF_DN(ST_Q4_K) PF_DN(ST_Q5_K) PF_DN(ST_Q6_K)
+        PF_DN(ST_Q2_K) PF_DN(ST_Q3_K) PF_DN(ST_Q4_K) PF_DN(ST_Q5_K) PF_DN(ST_Q6_K)
         PF_DN(ST_IQ2_XS) PF_DN(ST_IQ3_XXS) PF_DN(ST_IQ4_XS)
 #undef PF_DN
     default: break;

@@ -60,7 +60,6 @@ enum {
     /* batched prefill MoE layer (kernels/prefill.h) */
     K_PF_ROUTE = K_MQ_DN + 1, K_PF_SELECT, K_PF_GROUP, K_PF_GATEUP, K_PF_DOWN, K_PF_COMBINE, K_PF_SPLIT,
     /* prefill gate/up and down of the integer formats with the codes in registers (kernels/prefill.h) */
-    K_PF_GATEUP_R, K_PF_DOWN_R,
     /* prefill router logits on the f32 matrix cores (kernels/prefill.h) */
     K_PF_ROUTE_M,
     /* u32 fill (counter words of caller-provided scratch) */
@@ -92,7 +91,7 @@ static const char *const k_names[K_COUNT] = {
     "sepia_mq_mv_q5_k", "sepia_mq_mv_q6_k", "sepia_mq_mv_iq4_xs", "sepia_mq_mv_q8_0",
     "sepia_mq_gateup", "sepia_mq_down",
     "sepia_pf_route", "sepia_pf_select", "sepia_pf_group", "sepia_pf_gateup", "sepia_pf_down", "sepia_pf_combine",
-    "sepia_pf_split", "sepia_pf_gateup_r", "sepia_pf_down_r", "sepia_pf_route_m", "sepia_fill_u32",
+    "sepia_pf_split", "sepia_pf_route_m", "sepia_fill_u32",
     "sepia_rel_project_f32", "sepia_attn_partial", "sepia_attn_combine",
     "sepia_pf_quant", "sepia_pf_gateup_q", "sepia_pf_down_q",
 };
@@ -152,11 +151,8 @@ static int g_opt_pf_route_m = 1;   /* "pf_route_m": 1 = prefill router logits on
                                     * 0 = sepia_pf_route */
 static int g_opt_pf_q = 1;   /* "pf_q": 1 = a prefill layer whose six projections are all Q2_K, Q3_K or Q4_K
                               * runs them on the int8 matrix cores (sepia_pf_quant, sepia_pf_gateup_q,
-                              * sepia_pf_down_q); 0 = as "pf_reg" says */
-static int g_opt_pf_reg = 1;   /* "pf_reg": 1 = a prefill layer whose gate/up (down) projections are all Q2_K,
-                                * Q3_K or Q4_K runs them as sepia_pf_gateup_r (sepia_pf_down_r), the codes
-                                * decoded into registers; 0 = the LDS-tile kernels sepia_pf_gateup / _down,
-                                * which every other format always takes */
+                              * sepia_pf_down_q); 0 = the bf16 kernels sepia_pf_gateup / _down, which
+                              * every other layer always takes */
 static int g_opt_tile_t = 0; /* sepia_hip_set_option("tile_t", T) forces T steps per workgroup */
 
 /* Geometry for `mats` stacked copies of a [rows, 256 * n_blocks] matrix; 0
@@ -1123,10 +1119,6 @@ int sepia_hip_set_option(const char *name, int value) {
         g_opt_pf_q = value;
         return 1;
     }
-    if (strcmp(name, "pf_reg") == 0 && (value == 0 || value == 1)) {
-        g_opt_pf_reg = value;
-        return 1;
-    }
     if (strcmp(name, "pf_route_m") == 0 && (value == 0 || value == 1)) {
         g_opt_pf_route_m = value;
         return 1;
@@ -1687,7 +1679,7 @@ static int mq_ffn_prep(const MoeProj *g, const MoeProj *u, const MoeProj *d, con
 static int pf_type_ok(int t) {
     return t == SEPIA_T_Q2_K || t == SEPIA_T_Q3_K || t == 12 || t == 13 || t == 14 || t == 17 || t == 18 || t == 23;
 }
-/* Formats the prefill integer pipelines take as exact codes (Q2_K, Q3_K, Q4_K). */
+/* Formats of the int8 prefill projections (kernels/prefill_q.h): Q2_K, Q3_K, Q4_K. */
 static int pf_type_int(int t) { return t == SEPIA_T_Q2_K || t == SEPIA_T_Q3_K || t == 12; }
 
 int sepia_gpu_moe_prefill(const SepiaMoeLayerDesc *L, int64_t n_tokens, SepiaGpuBuf *x, SepiaGpuBuf *y,
@@ -1764,8 +1756,7 @@ int sepia_gpu_moe_prefill(const SepiaMoeLayerDesc *L, int64_t n_tokens, SepiaGpu
     PF_REGION(o_w, P * 4);
     PF_REGION(o_list, P * 4);
     PF_REGION(o_units, umax * 12);
-    PF_REGION(o_nu, 8);   /* n_units, then the "x has a nonzero lo part" flag */
-    PF_REGION(o_s16, use_q ? 0 : T * H / 16 * 4);
+    PF_REGION(o_nu, 4);   /* n_units */
     PF_REGION(o_xh, use_q ? 0 : T * H * 2);
     PF_REGION(o_xl, use_q ? 0 : T * H * 2);
     PF_REGION(o_hh, use_q ? 0 : P * I * 2);
@@ -1780,8 +1771,7 @@ int sepia_gpu_moe_prefill(const SepiaMoeLayerDesc *L, int64_t n_tokens, SepiaGpu
     uint8_t *s = (uint8_t *)scratch(o, op);
     if (!s) return 0;
     float *logits = (float *)(s + o_logits), *sel_w = (float *)(s + o_w), *yp = (float *)(s + o_yp);
-    void *xh = s + o_xh, *xl = s + o_xl, *hh = s + o_hh, *hl = s + o_hl, *s16 = s + o_s16;
-    uint32_t *lo_any = (uint32_t *)(s + o_nu) + 1;
+    void *xh = s + o_xh, *xl = s + o_xl, *hh = s + o_hh, *hl = s + o_hl;
     int32_t *sel_idx = (int32_t *)(s + o_idx), *list = (int32_t *)(s + o_list), *units = (int32_t *)(s + o_units),
             *n_units = (int32_t *)(s + o_nu);
 
@@ -1800,7 +1790,7 @@ int sepia_gpu_moe_prefill(const SepiaMoeLayerDesc *L, int64_t n_tokens, SepiaGpu
         return 0;
     void *a_sel[] = { &logits, &rb, &nr32, &ns32, &tk32, &rs, &gsc, &sel_idx, &sel_w };
     if (!launch(K_PF_SELECT, (unsigned)T, 64, a_sel, op)) return 0;
-    void *a_grp[] = { &sel_idx, &tt, &nr32, &ns32, &tk32, &list, &units, &n_units, &lo_any };
+    void *a_grp[] = { &sel_idx, &tt, &nr32, &ns32, &tk32, &list, &units, &n_units };
     if (!launch(K_PF_GROUP, 1, 1024, a_grp, op)) return 0;
     if (use_q) {
         void *pqx = s + o_pqx, *pqxs = s + o_pqxs, *hf = s + o_hf, *pqh = s + o_pqh, *pqhs = s + o_pqhs;
@@ -1814,24 +1804,16 @@ int sepia_gpu_moe_prefill(const SepiaMoeLayerDesc *L, int64_t n_tokens, SepiaGpu
         if (!launch(K_PF_QUANT, (unsigned)P, 256, a_qh, op)) return 0;
         void *a_dq[] = { (void *)&d, (void *)&sd, &nr32, &inter, &hid, &pqh, &pqhs, &list, &units, &n_units, &yp };
         if (!launch2(K_PF_DOWN_Q, (unsigned)(H / 256), (unsigned)umax, 512, PF_LDS_BYTES, a_dq, op)) return 0;
-        goto combine;
+    } else {
+        int64_t nseg = T * H / 16;
+        void *a_sp[] = { &x->dev, &nseg, &xh, &xl };
+        if (!launch(K_PF_SPLIT, (unsigned)((nseg + 255) / 256), 256, a_sp, op)) return 0;
+        void *a_gu[] = { (void *)&g, (void *)&u, (void *)&sg, (void *)&su, &nr32, &nsel32, &inter, &hid, &xh, &xl,
+                         &list, &units, &n_units, &hh, &hl };
+        if (!launch2(K_PF_GATEUP, (unsigned)((I + 31) / 32), (unsigned)umax, 512, PF_LDS_BYTES, a_gu, op)) return 0;
+        void *a_dn[] = { (void *)&d, (void *)&sd, &nr32, &inter, &hid, &hh, &hl, &list, &units, &n_units, &yp };
+        if (!launch2(K_PF_DOWN, (unsigned)((H + 63) / 64), (unsigned)umax, 512, PF_LDS_BYTES, a_dn, op)) return 0;
     }
-    int64_t nseg = T * H / 16;
-    void *a_sp[] = { &x->dev, &nseg, &xh, &xl, &s16, &lo_any };
-    if (!launch(K_PF_SPLIT, (unsigned)((nseg + 255) / 256), 256, a_sp, op)) return 0;
-    void *a_gu[] = { (void *)&g, (void *)&u, (void *)&sg, (void *)&su, &nr32, &nsel32, &inter, &hid, &xh, &xl, &s16,
-                     &lo_any, &list, &units, &n_units, &hh, &hl };
-    const int gu_r = g_opt_pf_reg && pf_type_int(g.type) && (ns == 0 || pf_type_int(sg.type));
-    const int64_t gu_rows = gu_r ? 64 : 32;
-    if (!launch2(gu_r ? K_PF_GATEUP_R : K_PF_GATEUP, (unsigned)((I + gu_rows - 1) / gu_rows), (unsigned)umax, 512,
-                 PF_LDS_BYTES, a_gu, op))
-        return 0;
-    void *a_dn[] = { (void *)&d, (void *)&sd, &nr32, &inter, &hid, &hh, &hl, &list, &units, &n_units, &yp };
-    const int dn_r = g_opt_pf_reg && pf_type_int(d.type) && (ns == 0 || pf_type_int(sd.type));
-    if (!launch2(dn_r ? K_PF_DOWN_R : K_PF_DOWN, (unsigned)(dn_r ? (H + 127) / 128 : (H + 63) / 64), (unsigned)umax,
-                 512, PF_LDS_BYTES, a_dn, op))
-        return 0;
-combine:;
     void *a_cb[] = { &yp, &sel_w, &nsel32, &tt, &hid, &y->dev };
     if (!launch2(K_PF_COMBINE, (unsigned)((H + 255) / 256), (unsigned)T, 256, 0, a_cb, op)) return 0;
     if (route_out) {

@@ -801,22 +801,20 @@ PREFILL_CASES = [
 ]
 
 
-PF_PATHS = {"q": dict(pf_q=1, pf_reg=1, pf_route_m=1), "reg": dict(pf_q=0, pf_reg=1, pf_route_m=1),
-            "tile": dict(pf_q=0, pf_reg=0, pf_route_m=0)}
+PF_PATHS = {"q": dict(pf_q=1, pf_route_m=1), "tile": dict(pf_q=0, pf_route_m=0)}
 
 
-@pytest.mark.parametrize("path", ["q", "reg", "tile"])
+@pytest.mark.parametrize("path", ["q", "tile"])
 @pytest.mark.parametrize("x_kind", ["bf16", "f32"])
 @pytest.mark.parametrize("shape,types,T", PREFILL_CASES, ids=lambda v: str(v))
 def test_moe_prefill(dev, orc, shape, types, T, x_kind, path):
     """Every token of the batch against the oracle's single-token layer (its
     own routing, near-ties per the reference protocol); two runs bitwise equal.
-    x either bf16-representable (the bf16 projections skip the zero lo terms)
-    or full f32. path: a layer of Q2_K / Q3_K / Q4_K projections on the int8
-    matrix cores (q, the default; option pf_q), the bf16 kernels with the
-    codes in registers (reg; pf_q 0) or the LDS-tile kernels (tile; pf_reg 0,
+    x either bf16-representable or full f32. path: a layer of Q2_K / Q3_K /
+    Q4_K projections on the int8 matrix cores (q, the default; option pf_q)
+    or on the bf16 kernels with bit-exact dequantized weights (tile; pf_q 0,
     which also runs the router on sepia_pf_route, pf_route_m 0). Layers with
-    other formats take the bf16 kernels under q and reg alike."""
+    other formats take the bf16 kernels on both paths."""
     hidden, inter, n_routed, n_shared = shape
     tgu, td, ts = types
     rng = np.random.default_rng(hidden + 7 * T + tgu)
