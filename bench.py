@@ -566,8 +566,8 @@ def run_c5(B, warmup, steps, cpu_seconds, T=512):
 
     ms = B.timed_steps(step, warmup, steps)
     knames = ["sepia_pf_route", "sepia_pf_route_m", "sepia_pf_select", "sepia_pf_group", "sepia_pf_split",
-              "sepia_pf_gateup", "sepia_pf_gateup_r", "sepia_pf_down_r", "sepia_pf_down", "sepia_pf_combine",
-              "sepia_pf_quant", "sepia_pf_gateup_q", "sepia_pf_down_q"]
+              "sepia_pf_gateup", "sepia_pf_down", "sepia_pf_combine", "sepia_pf_quant", "sepia_pf_gateup_q",
+              "sepia_pf_down_q"]
     kms = B.kernel_ms(step, min(steps, 5), knames)
     n_sel = 6 + NS
     route = B.dev.alloc(T * (6 + n_sel) * 4)
