@@ -203,8 +203,10 @@ class Bench:
 # own run) and scaled by what the same counters read for the copy kernel of known size
 # (profiles/*_hbm_traffic.md). Reported as roofline.traffic for the dominant kernel; None until
 # measured for the current build.
-MEASURED_TRAFFIC_C2 = {"sepia_mq_gateup": 12847014, "sepia_mq_down": 8474192}
-MEASURED_TRAFFIC_C3 = {}
+MEASURED_TRAFFIC_C2 = {"sepia_mq_gateup": 12894331, "sepia_mq_down": 8604806}
+MEASURED_TRAFFIC_C3 = {"sepia_moe_route": 6632135, "sepia_mq_gateup": 122062249, "sepia_mq_down": 72327164}
+MEASURED_TRAFFIC_REAL = {"sepia_moe_route": 6632066, "sepia_mq_gateup": 119343701, "sepia_mq_down": 84143688}
+MEASURED_TRAFFIC_C5 = {"sepia_pf_gateup_q": 2991873043, "sepia_pf_down_q": 1901268026}
 
 
 def cpu_sample(fn, min_seconds, max_calls):
@@ -534,7 +536,9 @@ def run_c3(B, warmup, steps, cpu_seconds, n_layers=8, types=C3_TYPES, what="C3")
             B.dev.free(b)
     for b in xs + [y]:
         B.dev.free(b)
-    kern = {k: dict(avg_launch_us=v * 1e3, bytes_per_launch=k_bytes[k], achieved_gbs=k_bytes[k] / (v * 1e-3) / 1e9)
+    measured = MEASURED_TRAFFIC_C3 if types == C3_TYPES else MEASURED_TRAFFIC_REAL if types == REAL_TYPES else {}
+    kern = {k: dict(avg_launch_us=v * 1e3, bytes_per_launch=k_bytes[k], achieved_gbs=k_bytes[k] / (v * 1e-3) / 1e9,
+                    traffic=measured.get(k))
             for k, v in kms.items()}
     return dict(ms=ms, us_per_token=ms * 1e3, bytes_per_token=per_token, gbs=per_token / (ms * 1e-3) / 1e9,
                 roofline_us=per_token / (HBM_PEAK_GBS * 1e9) * 1e6,
@@ -606,6 +610,7 @@ def run_c5(B, warmup, steps, cpu_seconds, T=512):
                 # the int8 path issues three digit planes per product, at the 5.0 POP/s int8 peak
                 mfma_util_int8_issued=3 * flops / sec / 5.0e15,
                 kernels_avg_ms={k: v for k, v in kms.items()},
+                traffic_bytes=MEASURED_TRAFFIC_C5,
                 parity=dict(tokens=sample, max_abs_diff=err, y_inf=scale, bound="1e-4*||y||_inf",
                             selections_checked=T),
                 cpu_1core_ms_per_token=s1 * 1e3)
@@ -702,7 +707,8 @@ def main():
                      "frac": round(kd["achieved_gbs"] / HBM_PEAK_GBS, 4), "traffic": MEASURED_TRAFFIC_C3.get(dom),
                      "kernel": dom, "bytes_per_launch": kd["bytes_per_launch"],
                      "avg_launch_us": round(kd["avg_launch_us"], 3),
-                     "other_kernels": {k: {kk: round(vv, 3) for kk, vv in v.items()}
+                     "other_kernels": {k: {kk: (round(vv, 3) if isinstance(vv, float) else vv)
+                                           for kk, vv in v.items() if kk != "traffic" or vv is not None}
                                        for k, v in res["kernels"].items() if k != dom}},
         "cpu_baseline": {"value": round(res["cpu"]["s1"] * 1e6, 1), "unit": "us/token", "cores": 1,
                          "kind": "port", "nproc": nproc,
