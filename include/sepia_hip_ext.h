@@ -146,6 +146,10 @@ void *sepia_hip_stream(void);
  *   "mq_scope" 0..3  the mq_p/mq_c/mq_s/mq_x overrides apply to every
  *                 matrix-core launch (0) or only to the matvec (1), the
  *                 expert FFN's gate/up (2) or its down (3) launches;
+ *   "mq_rdelay" 0..4096  KB of weights a routed gate/up workgroup of the MoE
+ *                 decode layer is charged for waiting on the selection when
+ *                 workgroups are split between routed and shared experts
+ *                 (default 80);
  *   "pf_q" 1/0    prefill projections of layers whose six projections are
  *                 all Q2_K/Q3_K/Q4_K on the int8 matrix cores (1, default),
  *                 or on the bf16 kernels every other layer takes (0);

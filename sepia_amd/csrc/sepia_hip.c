@@ -141,6 +141,10 @@ static int g_opt_mq = 1;     /* sepia_hip_set_option("mq", 0) disables the matri
  * workgroup geometry (parts per item, item lanes, ring stages of the largest
  * format; 0 = planned) */
 static int g_opt_mq_p = 0, g_opt_mq_c = 0, g_opt_mq_s = 0;
+static int g_opt_mq_rdelay = 80;  /* "mq_rdelay": KB of weights a routed gate/up workgroup of the MoE layer is
+                                   * charged for its late start (the selection) when workgroups are split
+                                   * between routed and shared experts; 80 measured best at C3 (57.8 vs
+                                   * 59.8 us per token with 0; the plateau spans 50-100) */
 static int g_opt_mq_scope = 0;     /* "mq_scope": the mq_p/mq_c/mq_s/mq_x overrides apply to every matrix-core
                                     * launch (0) or only to the matvec (1), gate/up (2) or down (3) launches */
 static int g_mq_kind = 0;          /* the launch kind mq_geo is planning: 1 matvec, 2 gate/up, 3 down */
@@ -1123,6 +1127,10 @@ int sepia_hip_set_option(const char *name, int value) {
         g_opt_pf_route_m = value;
         return 1;
     }
+    if (strcmp(name, "mq_rdelay") == 0 && value >= 0 && value <= 4096) {
+        g_opt_mq_rdelay = value;
+        return 1;
+    }
     if (strcmp(name, "mq_scope") == 0 && value >= 0 && value <= 3) {
         g_opt_mq_scope = value;
         return 1;
@@ -1576,23 +1584,33 @@ static int mq_proj_ok(const MoeProj *p, int64_t rows) {
  * `tiles` per slot, the bytes per workgroup as even as whole counts allow
  * (proportional shares rounded down, then one more workgroup at a time to
  * the kind with the most bytes per workgroup while it fits). */
-static void mq_split(int32_t topk, int32_t n_shared, double br, double bs, int64_t tiles, int32_t *wr, int32_t *ws) {
-    const double tot = topk * br + n_shared * bs;
-    int64_t r = (int64_t)(MQ_CUS * br / tot), sh = (int64_t)(MQ_CUS * bs / tot);
-    if (r < 1) r = 1;
-    if (sh < 1) sh = 1;
-    if (r > tiles) r = tiles;
-    if (sh > tiles) sh = tiles;
-    for (;;) {
-        const int64_t used = topk * r + n_shared * sh;
-        const int can_r = topk > 0 && r < tiles && used + topk <= MQ_CUS;
-        const int can_s = n_shared > 0 && sh < tiles && used + n_shared <= MQ_CUS;
-        if (can_r && (!can_s || br / (double)r >= bs / (double)sh)) r++;
-        else if (can_s) sh++;
-        else break;
+static void mq_split(int32_t topk, int32_t n_shared, double br, double bs, int64_t tiles, double delay,
+                     int32_t *wr, int32_t *ws) {
+    /* workgroups per routed slot (r) and per shared slot (sh) within MQ_CUS
+     * that minimise the larger per-workgroup cost: a routed workgroup's
+     * share of a row's bytes plus `delay` (its late start, in the same
+     * units), a shared one's share */
+    if (n_shared == 0) {
+        int64_t r = MQ_CUS / (topk > 0 ? topk : 1);
+        *wr = (int32_t)(r < 1 ? 1 : r > tiles ? tiles : r);
+        *ws = 1;
+        return;
     }
-    *wr = (int32_t)r;
-    *ws = (int32_t)sh;
+    double best = -1.0;
+    int64_t br_best = 1, bs_best = 1;
+    for (int64_t r = 1; r <= tiles && topk * r + n_shared <= MQ_CUS; r++) {
+        int64_t sh = (MQ_CUS - topk * r) / n_shared;
+        if (sh > tiles) sh = tiles;
+        const double cr = br / (double)r + delay, cs = bs / (double)sh;
+        const double c = cr > cs ? cr : cs;
+        if (best < 0.0 || c < best) {
+            best = c;
+            br_best = r;
+            bs_best = sh;
+        }
+    }
+    *wr = (int32_t)br_best;
+    *ws = (int32_t)bs_best;
 }
 /* One launch's two geometries (routed and shared workgroups) and the
  * launch's thread count and LDS (the larger of the two). */
@@ -1626,8 +1644,9 @@ static int mq_ffn_plan(const MoeProj *g, const MoeProj *u, const MoeProj *d, con
     const int64_t tiles_i = (I + 15) / 16, tiles_h = (H + 15) / 16;
     if (n_shared + topk > 1 && MQ_DN_CNT_OFF + tiles_h > CNT_BYTES / 4) return 0;
     mq_split(topk, n_shared, (double)g->row_bytes, n_shared > 0 ? (double)sg->row_bytes : 1.0, tiles_i,
+             route ? 1024.0 * g_opt_mq_rdelay / (32.0 * (double)tiles_i) : 0.0,   /* 16 gate + 16 up rows a tile */
              &pl->gu_wps_r, &pl->gu_wps_s);
-    mq_split(topk, n_shared, (double)d->row_bytes, n_shared > 0 ? (double)sd->row_bytes : 1.0, tiles_h,
+    mq_split(topk, n_shared, (double)d->row_bytes, n_shared > 0 ? (double)sd->row_bytes : 1.0, tiles_h, 0.0,
              &pl->dn_wps_r, &pl->dn_wps_s);
     const int has_s = n_shared > 0;
     const int kg = mq_code(g->type), kd = mq_code(d->type);
