@@ -150,6 +150,9 @@ void *sepia_hip_stream(void);
  *                 decode layer is charged for waiting on the selection when
  *                 workgroups are split between routed and shared experts
  *                 (default 80);
+ *   "mq_gufac", "mq_dnfac" 25..400  percent scale on the routed formats'
+ *                 relative decode cost in the gate/up and down splits
+ *                 between routed and shared experts (default 100);
  *   "pf_q" 1/0    prefill projections of layers whose six projections are
  *                 all Q2_K/Q3_K/Q4_K on the int8 matrix cores (1, default),
  *                 or on the bf16 kernels every other layer takes (0);

@@ -145,6 +145,9 @@ static int g_opt_mq_rdelay = 80;  /* "mq_rdelay": KB of weights a routed gate/up
                                    * charged for its late start (the selection) when workgroups are split
                                    * between routed and shared experts; 80 measured best at C3 (57.8 vs
                                    * 59.8 us per token with 0; the plateau spans 50-100) */
+static int g_opt_mq_gufac = 100, g_opt_mq_dnfac = 100;   /* "mq_gufac", "mq_dnfac": percent scale on the routed
+                                                         * formats' relative cost (k_mq_cost) in the gate/up
+                                                         * and down splits */
 static int g_opt_mq_scope = 0;     /* "mq_scope": the mq_p/mq_c/mq_s/mq_x overrides apply to every matrix-core
                                     * launch (0) or only to the matvec (1), gate/up (2) or down (3) launches */
 static int g_mq_kind = 0;          /* the launch kind mq_geo is planning: 1 matvec, 2 gate/up, 3 down */
@@ -1127,6 +1130,14 @@ int sepia_hip_set_option(const char *name, int value) {
         g_opt_pf_route_m = value;
         return 1;
     }
+    if (strcmp(name, "mq_gufac") == 0 && value >= 25 && value <= 400) {
+        g_opt_mq_gufac = value;
+        return 1;
+    }
+    if (strcmp(name, "mq_dnfac") == 0 && value >= 25 && value <= 400) {
+        g_opt_mq_dnfac = value;
+        return 1;
+    }
     if (strcmp(name, "mq_rdelay") == 0 && value >= 0 && value <= 4096) {
         g_opt_mq_rdelay = value;
         return 1;
@@ -1218,6 +1229,13 @@ static const size_t k_mq_table[MQ_FORMATS] = { 0, 0, 0, 4096, 1024, 0, 0, 0, 0 }
  * faster (the IQ2_XS / IQ3_XXS matvecs); the others' stepping waves need
  * all 16. */
 static const int k_mq_conv[MQ_FORMATS] = { 0, 0, 0, 1, 1, 0, 0, 0, 0 };
+/* Relative time per weight byte of the matrix-core decoders (percent; the
+ * K-quants Q4_K, Q5_K, Q6_K = 100), used to split an FFN launch's
+ * workgroups between routed and shared experts. Measured on the MoE decode
+ * layer: byte-balanced Q2_K against Q4_K is best, Q3_K against Q4_K at 115,
+ * IQ2_XS against Q5_K at 210-250 (87.0 -> 74.9 us per token) and IQ3_XXS
+ * against Q6_K at 135-160. IQ4_XS and Q8_0 are estimates. */
+static const int k_mq_cost[MQ_FORMATS] = { 100, 115, 100, 230, 145, 100, 100, 120, 80 };
 /* A row of n_blocks format blocks in the matrix-core kernels' 256-column
  * blocks (Q8_0: super-blocks of 8 of its 32-column blocks); -1 if it does
  * not divide. */
@@ -1584,7 +1602,7 @@ static int mq_proj_ok(const MoeProj *p, int64_t rows) {
  * `tiles` per slot, the bytes per workgroup as even as whole counts allow
  * (proportional shares rounded down, then one more workgroup at a time to
  * the kind with the most bytes per workgroup while it fits). */
-static void mq_split(int32_t topk, int32_t n_shared, double br, double bs, int64_t tiles, double delay,
+static void mq_split(int32_t topk, int32_t n_shared, double br, double bs, int64_t tiles, double delay, double rfac,
                      int32_t *wr, int32_t *ws) {
     /* workgroups per routed slot (r) and per shared slot (sh) within MQ_CUS
      * that minimise the larger per-workgroup cost: a routed workgroup's
@@ -1601,7 +1619,7 @@ static void mq_split(int32_t topk, int32_t n_shared, double br, double bs, int64
     for (int64_t r = 1; r <= tiles && topk * r + n_shared <= MQ_CUS; r++) {
         int64_t sh = (MQ_CUS - topk * r) / n_shared;
         if (sh > tiles) sh = tiles;
-        const double cr = br / (double)r + delay, cs = bs / (double)sh;
+        const double cr = rfac * br / (double)r + delay, cs = bs / (double)sh;
         const double c = cr > cs ? cr : cs;
         if (best < 0.0 || c < best) {
             best = c;
@@ -1645,8 +1663,10 @@ static int mq_ffn_plan(const MoeProj *g, const MoeProj *u, const MoeProj *d, con
     if (n_shared + topk > 1 && MQ_DN_CNT_OFF + tiles_h > CNT_BYTES / 4) return 0;
     mq_split(topk, n_shared, (double)g->row_bytes, n_shared > 0 ? (double)sg->row_bytes : 1.0, tiles_i,
              route ? 1024.0 * g_opt_mq_rdelay / (32.0 * (double)tiles_i) : 0.0,   /* 16 gate + 16 up rows a tile */
+             0.01 * g_opt_mq_gufac * k_mq_cost[mq_code(g->type)] / k_mq_cost[mq_code(n_shared > 0 ? sg->type : g->type)],
              &pl->gu_wps_r, &pl->gu_wps_s);
     mq_split(topk, n_shared, (double)d->row_bytes, n_shared > 0 ? (double)sd->row_bytes : 1.0, tiles_h, 0.0,
+             0.01 * g_opt_mq_dnfac * k_mq_cost[mq_code(d->type)] / k_mq_cost[mq_code(n_shared > 0 ? sd->type : d->type)],
              &pl->dn_wps_r, &pl->dn_wps_s);
     const int has_s = n_shared > 0;
     const int kg = mq_code(g->type), kd = mq_code(d->type);
