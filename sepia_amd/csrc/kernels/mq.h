@@ -1750,12 +1750,22 @@ __device__ __forceinline__ void mq_down(const MqProj &down, const MqProj &s_down
         if (!flag[i >> 4]) continue;
         const int64_t r = ((int64_t)j0 + (int64_t)(i >> 4) * jstep) * 16 + (i & 15);
         if (r >= hidden) continue;
+        // eight slots' loads in flight at a time, added in slot order
         float acc = 0.0f;
-        for (int sl = 0; sl < n_sum; sl++)
-            acc = __builtin_fmaf(sel_w ? sel_w[sl] : 1.0f,
-                                 __hip_atomic_load(&ypart[(int64_t)sl * hidden + r], __ATOMIC_RELAXED,
-                                                   __HIP_MEMORY_SCOPE_AGENT),
-                                 acc);
+        for (int s0 = 0; s0 < n_sum; s0 += 8) {
+            float v[8], wv[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const bool on = s0 + k < n_sum;
+                v[k] = on ? __hip_atomic_load(&ypart[(int64_t)(s0 + k) * hidden + r], __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT)
+                          : 0.0f;
+                wv[k] = on && sel_w ? sel_w[s0 + k] : 1.0f;
+            }
+#pragma unroll
+            for (int k = 0; k < 8; k++)
+                if (s0 + k < n_sum) acc = __builtin_fmaf(wv[k], v[k], acc);
+        }
         y[r] = acc;
     }
     for (int k = threadIdx.x; k < nk; k += blockDim.x)

@@ -30,6 +30,37 @@ __device__ __forceinline__ float wave_max_dpp(float v) {
     v = fmaxf(v, dpp_mov<0x140>(v));   // row_mirror
     return fmaxf(fmaxf(lane_f32(v, 0), lane_f32(v, 16)), fmaxf(lane_f32(v, 32), lane_f32(v, 48)));
 }
+// Signed-integer key with the order of a float score (finite or infinite;
+// -0 counts as +0). NaN and unused slots rank below every number: NaN at
+// INT32_MIN + 1, unused slots at INT32_MIN.
+__device__ __forceinline__ int32_t route_key(float v, bool ok) {
+    int32_t b = __builtin_bit_cast(int32_t, v + 0.0f);
+    b = b < 0 ? (b ^ 0x7FFFFFFF) : b;
+    return !ok ? INT32_MIN : (v == v ? b : INT32_MIN + 1);
+}
+template <int CTRL>
+__device__ __forceinline__ int32_t dpp_mov_i32(int32_t v) {
+    return __builtin_amdgcn_update_dpp(v, v, CTRL, 0xF, 0xF, false);
+}
+__device__ __forceinline__ int32_t wave_max_i32(int32_t v) {
+    v = max(v, dpp_mov_i32<0xB1>(v));    // quad_perm [1,0,3,2]
+    v = max(v, dpp_mov_i32<0x4E>(v));    // quad_perm [2,3,0,1]
+    v = max(v, dpp_mov_i32<0x141>(v));   // row_half_mirror
+    v = max(v, dpp_mov_i32<0x140>(v));   // row_mirror
+    return max(max(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
+               max(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
+}
+// Compare-exchange of two (key, slot) entries so that a comes first: the
+// larger key, or the lower slot among equal keys.
+__device__ __forceinline__ void route_cx(int32_t &ka, int32_t &ja, int32_t &kb, int32_t &jb) {
+    const bool sw = kb > ka || (kb == ka && jb < ja);
+    const int32_t tk = ka, tj = ja;
+    ka = sw ? kb : ka;
+    ja = sw ? jb : ja;
+    kb = sw ? tk : kb;
+    jb = sw ? tj : jb;
+}
+
 // Sum of lanes 0..n-1's doubles, added in lane order (the reference sums the
 // selected terms sequentially); n is at most a few dozen.
 __device__ __forceinline__ double lanes_sum_f64(double v, int n) {
@@ -77,7 +108,42 @@ __device__ void route_pick(const float *logits, const float *__restrict__ bias, 
     uint32_t taken = 0;
     int my_pick = 0;                   // lane k < topk: the k-th selected expert and its raw logit
     float my_raw = 0.0f;
-    for (int k = 0; k < topk; k++) {
+    if constexpr (EM == 4) {
+        // Each lane sorts its four (score key, slot) entries once, best
+        // first; a round then compares only the lanes' heads, and the
+        // winning lane pops its head. The same picks in the same order as
+        // the scan below: the largest score, the lowest expert index among
+        // equal scores (lanes hold ascending index ranges).
+        int32_t k0 = route_key(sc[0], ok[0]), k1 = route_key(sc[1], ok[1]);
+        int32_t k2 = route_key(sc[2], ok[2]), k3 = route_key(sc[3], ok[3]);
+        int32_t j0 = 0, j1 = 1, j2 = 2, j3 = 3;
+        route_cx(k0, j0, k1, j1);
+        route_cx(k2, j2, k3, j3);
+        route_cx(k0, j0, k2, j2);
+        route_cx(k1, j1, k3, j3);
+        route_cx(k1, j1, k2, j2);
+        uint32_t jl = (uint32_t)j0 | ((uint32_t)j1 << 2) | ((uint32_t)j2 << 4) | ((uint32_t)j3 << 6);
+        for (int k = 0; k < topk; k++) {
+            const int32_t wm = wave_max_i32(k0);
+            const uint64_t hit = __ballot(k0 == wm);
+            const int win_lane = (int)__builtin_ctzll(hit);
+            const int win_j = __builtin_amdgcn_readlane((int)(jl & 3u), win_lane);
+            if (w) {
+                const uint32_t hj = jl & 3u;
+                const float hr = hj == 0 ? lv[0] : hj == 1 ? lv[1] : hj == 2 ? lv[2] : lv[3];
+                const float raw = lane_f32(hr, win_lane);
+                if (lane == k) my_raw = raw;
+            }
+            if (lane == win_lane) {
+                k0 = k1;
+                k1 = k2;
+                k2 = k3;
+                k3 = INT32_MIN;
+                jl >>= 2;
+            }
+            if (lane == k) my_pick = win_lane * E + win_j;
+        }
+    } else for (int k = 0; k < topk; k++) {
         float best = -INFINITY, braw = 0.0f;
         int bj = -1;
 #pragma unroll

@@ -785,6 +785,44 @@ def run_prefill(dev, desc, X):
     return y, idx, w
 
 
+@pytest.mark.parametrize("kernel_path", ["mq", "generic"], indirect=True)
+def test_moe_route_exact_ties(dev, orc, kernel_path):
+    """Exactly equal selection scores: 200 routed experts (four to a lane of
+    the selecting wave) whose router rows and biases repeat in pairs over
+    three groups, so equal scores sit side by side in one lane and across
+    lanes. Each selection (the gate/up launch's on the matrix-core path, the
+    router's last workgroup on the generic one, and the prefill's per-token
+    one) must be the oracle's exactly: the largest score first, the lowest
+    expert index among equals."""
+    rng = np.random.default_rng(777)
+    n_routed, n_shared, topk, H = 200, 2, 6, 1024
+    desc, spec, bufs = make_layer(dev, rng, hidden=H, inter=1024, n_routed=n_routed, n_shared=n_shared,
+                                  tg=10, tu=10, td=11, ts=12)
+    grp = (np.arange(n_routed) // 2) % 3
+    base = (rng.standard_normal((3, H)) * 0.02).astype(np.float32)
+    rw = np.concatenate([base[grp], (rng.standard_normal((n_shared, H)) * 0.02).astype(np.float32)])
+    rb = np.array([0.05, -0.02, 0.01], dtype=np.float32)[grp]
+    dev.upload(bufs["rw"], rw)
+    dev.upload(bufs["rb"], rb)
+    spec["router_w"], spec["router_bias"] = rw, rb
+    for rep in range(2):
+        x = synth.normal_vector(rng, H)
+        y, idx, w = run_moe(dev, desc, x)
+        _, logits, idx_ref, _ = orc.moe_layer(spec, x, threads=THREADS)
+        assert list(idx) == list(idx_ref), (rep, list(idx), list(idx_ref))
+        assert len(set(grp[idx_ref])) == 1   # all six from one group of tied scores
+        w_ref = orc.route_weights(logits, n_routed, n_shared, idx_ref, 8.0, 1.0)
+        assert np.allclose(w, w_ref, rtol=1e-4, atol=0), (w, w_ref)
+    if kernel_path == "mq":
+        X = np.stack([synth.normal_vector(rng, H) for _ in range(3)])
+        _, pidx, _ = run_prefill(dev, desc, X)
+        for t in range(3):
+            _, _, idx_ref, _ = orc.moe_layer(spec, X[t], threads=THREADS)
+            assert list(pidx[t]) == list(idx_ref), (t, list(pidx[t]), list(idx_ref))
+    for b in bufs.values():
+        dev.free(b)
+
+
 def bf16_normal(rng, shape):
     """N(0,1) f32 values rounded toward zero to bf16 (exactly representable in bf16)."""
     v = rng.standard_normal(shape).astype(np.float32)
