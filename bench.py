@@ -412,6 +412,47 @@ def run_copy(B, steps):
                 avg_launch_us=kms["sepia_copy_f32"] * 1e3, gbs=8 * n / (kms["sepia_copy_f32"] * 1e-3) / 1e9)
 
 
+def ceiling_sizes():
+    """(label, bytes) of the single launches the HBM read ceiling is measured at: each kernel's
+    algorithmic weight bytes per launch (and the C3 layer's as one stream)."""
+    return [("C3_router_f32", (256 + 2) * 6144 * 4),
+            ("C1_q4_k_4096x4096", mat_bytes(Q4_K, 4096, 4096)),
+            ("C2_down_q3_k", mat_bytes(Q3_K, 6144, 3072)),
+            ("C4_iq2_xs_6144x6144", mat_bytes(IQ2_XS, 6144, 6144)),
+            ("C2_gateup_q2_k", 2 * mat_bytes(Q2_K, 3072, 6144)),
+            ("C4_iq3_xxs_6144x6144", mat_bytes(IQ3_XXS, 6144, 6144)),
+            ("C3_down", 6 * mat_bytes(Q3_K, 6144, 3072) + 2 * mat_bytes(Q4_K, 6144, 3072)),
+            ("C3_gateup", 12 * mat_bytes(Q2_K, 3072, 6144) + 4 * mat_bytes(Q4_K, 3072, 6144)),
+            ("C3_layer_one_stream", (256 + 2) * 6144 * 4 + 12 * mat_bytes(Q2_K, 3072, 6144) + 4 * mat_bytes(Q4_K, 3072, 6144)
+             + 6 * mat_bytes(Q3_K, 6144, 3072) + 2 * mat_bytes(Q4_K, 6144, 3072))]
+
+
+def run_ceiling(B):
+    """The HBM read ceiling of one launch at each size of ceiling_sizes(): the library's read probe
+    (plain 16-byte streaming loads, nothing else) over copies rotated through 1.6 GB so the 256 MB
+    Infinity Cache cannot serve them; per size the fastest of six grid shapes, average per-launch
+    HIP-event time."""
+    L = B.L
+    total = 1600 << 20
+    buf = B.private(total)
+    out = {}
+    for label, nbytes in ceiling_sizes():
+        span = (nbytes + 4095) & ~4095
+        ncopy = max(1, min(total // span, 64))
+        n = max(24, 3 * ncopy)
+        best = None
+        for grid in (256, 512, 1024, 2048, 4096, 8192):
+            def step(i, grid=grid):
+                return L.sepia_hip_read_probe(buf, (i % ncopy) * span, nbytes, grid)
+            us = B.kernel_ms(step, n, ["sepia_read_probe"])["sepia_read_probe"] * 1e3
+            if best is None or us < best[0]:
+                best = (us, grid)
+        out[label] = dict(bytes=nbytes, us=round(best[0], 3), gbs=round(nbytes / (best[0] * 1e-6) / 1e9, 1),
+                          grid=best[1], copies=ncopy)
+    B.dev.free(buf)
+    return out
+
+
 def build_moe_layers(B, n_layers, types=C3_TYPES):
     """n_layers Inkling-shaped MoE layers resident in HBM: 256 routed experts (gate/up
     [3072x6144], down [6144x3072]) and 2 shared ones of the given formats (C3: Q2_K, Q3_K routed;
@@ -621,9 +662,11 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--only", choices=["c3", "real", "c2", "c1", "c4", "c5", "store", "copy"], default=None,
+    ap.add_argument("--only", choices=["c3", "real", "c2", "c1", "c4", "c5", "store", "copy", "ceiling"],
+                    default=None,
                     help="run one configuration (profiling runs; 'copy': the library's f32 copy kernel over "
-                         "256 MiB, the reference for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE); default: all")
+                         "256 MiB, the reference for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE; 'ceiling': the "
+                         "HBM read ceiling of a single launch at each kernel's size); default: all")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -639,6 +682,11 @@ def main():
     extra = {}
     res = None
     t0 = time.time()
+    ceil = None
+    if args.only in (None, "ceiling"):
+        ceil = run_ceiling(B)
+        extra["hbm_read_ceiling"] = ceil
+        log("ceiling", json.dumps(ceil))
     if args.only in (None, "c3"):
         res = run_c3(B, args.warmup, args.steps, min(8.0, args.cpu_seconds))
         log("C3 %.2f us/token %.1f GB/s (%.1f%%) in %.0fs" % (res["us_per_token"], res["gbs"],
@@ -707,6 +755,8 @@ def main():
                      "frac": round(kd["achieved_gbs"] / HBM_PEAK_GBS, 4), "traffic": MEASURED_TRAFFIC_C3.get(dom),
                      "kernel": dom, "bytes_per_launch": kd["bytes_per_launch"],
                      "avg_launch_us": round(kd["avg_launch_us"], 3),
+                     "single_launch_ceiling_gbs": ceil["C3_gateup"]["gbs"] if ceil else None,
+                     "frac_of_ceiling": round(kd["achieved_gbs"] / ceil["C3_gateup"]["gbs"], 4) if ceil else None,
                      "other_kernels": {k: {kk: (round(vv, 3) if isinstance(vv, float) else vv)
                                            for kk, vv in v.items() if kk != "traffic" or vv is not None}
                                        for k, v in res["kernels"].items() if k != dom}},

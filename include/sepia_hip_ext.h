@@ -125,6 +125,12 @@ int sepia_hip_reserve_scratch(size_t bytes);
  * batches read it (tests read this counter to check that). */
 uint64_t sepia_hip_uploaded_bytes(void);
 
+/* Measurement support: one launch of `grid` workgroups that reads `bytes`
+ * of buf from byte `off` (both multiples of 16) with plain streaming loads
+ * and does nothing else, for the HBM read ceiling of a single launch at a
+ * given size. No counterpart in the reference. */
+int sepia_hip_read_probe(SepiaGpuBuf *buf, size_t off, size_t bytes, unsigned grid);
+
 /* The hipStream_t every op is issued on (for hipEvent timing). */
 void *sepia_hip_stream(void);
 

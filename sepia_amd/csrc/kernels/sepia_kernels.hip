@@ -113,6 +113,29 @@ extern "C" __global__ __launch_bounds__(256) void sepia_fill_u32(uint32_t *p, in
     if (i < n) p[i] = v;
 }
 
+// HBM read ceiling of one launch: every workgroup streams a contiguous
+// chunk of n16 16-byte words with four loads in flight per lane and nothing
+// else (a measurement reference for the weight-streaming kernels). The
+// sink is written only if the XOR of the chunk equals a fixed word, which
+// keeps the loads.
+extern "C" __global__ __launch_bounds__(256) void sepia_read_probe(const uint4 *__restrict__ p, int64_t n16,
+                                                                   uint32_t *__restrict__ sink) {
+    const int64_t per = (n16 + gridDim.x - 1) / gridDim.x;
+    const int64_t b = (int64_t)blockIdx.x * per, e = b + per < n16 ? b + per : n16;
+    uint32_t acc = 0;
+    for (int64_t i = b + threadIdx.x; i < e; i += 4 * 256) {
+        uint4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int64_t j = i + (int64_t)u * 256;
+            v[u] = j < e ? p[j] : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    }
+    if (acc == 0x9E3779B9u) sink[blockIdx.x] = acc;
+}
+
 extern "C" __global__ __launch_bounds__(256) void sepia_touch_f32(float *x, int64_t n) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) x[i] += 0.0f;

@@ -59,7 +59,6 @@ enum {
     K_MQ_DN = K_MQ_GU + 1,
     /* batched prefill MoE layer (kernels/prefill.h) */
     K_PF_ROUTE = K_MQ_DN + 1, K_PF_SELECT, K_PF_GROUP, K_PF_GATEUP, K_PF_DOWN, K_PF_COMBINE, K_PF_SPLIT,
-    /* prefill gate/up and down of the integer formats with the codes in registers (kernels/prefill.h) */
     /* prefill router logits on the f32 matrix cores (kernels/prefill.h) */
     K_PF_ROUTE_M,
     /* u32 fill (counter words of caller-provided scratch) */
@@ -68,6 +67,8 @@ enum {
     K_REL_PROJECT, K_ATTN_PARTIAL, K_ATTN_COMBINE,
     /* prefill projections of Q2_K / Q3_K / Q4_K on the int8 matrix cores (kernels/prefill_q.h) */
     K_PF_QUANT, K_PF_GATEUP_Q, K_PF_DOWN_Q,
+    /* HBM read ceiling probe (measurement) */
+    K_READ_PROBE,
     K_COUNT
 };
 #define FFN_NAMES(p) "sepia_ffn_gateup_" p, "sepia_ffn_gateup_" p "_xp", "sepia_ffn_down_" p
@@ -94,6 +95,7 @@ static const char *const k_names[K_COUNT] = {
     "sepia_pf_split", "sepia_pf_route_m", "sepia_fill_u32",
     "sepia_rel_project_f32", "sepia_attn_partial", "sepia_attn_combine",
     "sepia_pf_quant", "sepia_pf_gateup_q", "sepia_pf_down_q",
+    "sepia_read_probe",
 };
 #undef FFN_NAMES
 
@@ -885,6 +887,21 @@ int sepia_gpu_copy(SepiaGpuBuf *src, size_t src_off, SepiaGpuBuf *dst, size_t ds
     uint8_t *d = dst->dev + dst_off;
     void *args[] = { &s, &d, &n };
     return launch(K_COPY, blocks_for(n, 256), 256, args, op);
+}
+
+int sepia_hip_read_probe(SepiaGpuBuf *buf, size_t off, size_t bytes, unsigned grid) {
+    const char *op = "read_probe";
+    if (!buf || bytes == 0 || bytes % 16 || off % 16 || grid == 0 || grid > MAX_GRID) {
+        LOG("%s: invalid arguments (16-byte aligned offset and size, 1 <= grid <= %d)", op, MAX_GRID);
+        return 0;
+    }
+    if (!chk(buf, off, bytes, op, "buf") || !need_batch(op) || !prep_in_r(buf, off, bytes, op)) return 0;
+    uint32_t *sink = (uint32_t *)scratch((size_t)grid * 4, op);
+    if (!sink) return 0;
+    const uint8_t *p = buf->dev + off;
+    int64_t n16 = (int64_t)(bytes / 16);
+    void *args[] = { &p, &n16, &sink };
+    return launch(K_READ_PROBE, grid, 256, args, op);
 }
 
 int sepia_gpu_softmax(SepiaGpuBuf *x, SepiaGpuBuf *y, int64_t rows, int64_t n) {

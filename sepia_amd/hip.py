@@ -96,6 +96,7 @@ PROTOTYPES = {
     "sepia_hip_set_iq2xxs_grid": (_I, [_P]),
     "sepia_hip_reserve_scratch": (_I, [_SZ]),
     "sepia_hip_uploaded_bytes": (ctypes.c_uint64, []),
+    "sepia_hip_read_probe": (_I, [_P, _SZ, _SZ, ctypes.c_uint]),
     "sepia_hip_stream": (_P, []),
     "sepia_hip_set_option": (_I, [ctypes.c_char_p, _I]),
     # the on-disk stores (store.c)

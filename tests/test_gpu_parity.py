@@ -349,6 +349,26 @@ def test_matvec_q_repeat_stable(dev, orc):
         dev.free(b)
 
 
+def test_read_probe(dev):
+    """The measurement probe reads whole 16-byte words of a buffer and leaves
+    it unchanged; misaligned or out-of-range requests are refused."""
+    L = dev.L
+    data = np.arange(1 << 18, dtype=np.uint32)
+    b = dev.shared_from(data)
+    dev.begin()
+    try:
+        assert L.sepia_hip_read_probe(b, 0, data.nbytes, 1024) == 1
+        assert L.sepia_hip_read_probe(b, 4096, 65536, 7) == 1
+        assert L.sepia_hip_read_probe(b, 8, 4096, 4) == 0             # offset not a multiple of 16
+        assert L.sepia_hip_read_probe(b, 0, 4100, 4) == 0             # size not a multiple of 16
+        assert L.sepia_hip_read_probe(b, 16, data.nbytes, 4) == 0     # past the end
+        assert L.sepia_hip_read_probe(b, 0, 4096, 0) == 0             # no workgroups
+    finally:
+        assert L.sepia_gpu_end() == 1
+    assert np.array_equal(dev.download(b, data.size, dtype=np.uint32), data)
+    dev.free(b)
+
+
 def test_matvec_q_rejections(dev):
     L = dev.L
     w = dev.alloc(144 * 4)
