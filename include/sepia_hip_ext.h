@@ -144,11 +144,13 @@ void *sepia_hip_stream(void);
  *   "tile_t" 0..  automatic or forced row steps per tile workgroup;
  *   "mq_p", "mq_c", "mq_s" 0..  automatic or forced matrix-core geometry
  *                 (parts per item, items side by side, ring stages);
- *   "mq_x" 0..3   how matrix-core kernels fetch their vector: 0 = the
+ *   "mq_x" 0..4   how matrix-core kernels fetch their vector: 0 = the
  *                 planner's choice, 1 = loads from global memory, 2 = LDS
  *                 DMA issued ahead of the weight prologue, 3 = converter
  *                 waves (DMA into the XQ place, converted there while the
- *                 other waves issue and decode their first step);
+ *                 other waves issue and decode their first step), 4 = the
+ *                 same conversion by the first stepping waves before they
+ *                 issue their own weights;
  *   "mq_scope" 0..3  the mq_p/mq_c/mq_s/mq_x overrides apply to every
  *                 matrix-core launch (0) or only to the matvec (1), the
  *                 expert FFN's gate/up (2) or its down (3) launches;

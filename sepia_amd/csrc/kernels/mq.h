@@ -1169,6 +1169,10 @@ struct MqItem {
 // last conv waves of the workgroup DMA the vector straight into its XQ
 // place and convert it there while the others stream and decode their
 // first step; xraw is then the LDS offset of 16 bytes of control words.
+// conv < 0: the first -conv stepping waves do that conversion before they
+// issue their own weight prologue, while the other waves issue theirs (no
+// waves of its own, and the vector is in XQ form long before the weight
+// stream has been issued in full).
 // nw: the stepping waves (C x P); a launch may run more waves than that
 // (its other kind of workgroup needs more), which then take no items and no
 // ring.
@@ -1334,6 +1338,37 @@ struct MqWave {
         if (!CONV || geo.conv == 0) {
             start(src, geo, lds0, xoff);
             run(lds0, red);
+            return;
+        }
+        if (geo.conv < 0) {
+            const int nconv = -64 * geo.conv;
+            uint32_t *ctl = (uint32_t *)(lds0 + geo.xraw);
+            const bool cv = (int)threadIdx.x < nconv;
+            if (threadIdx.x == 0) ctl[0] = 0u;
+            if (cv) mq_xq_dma_by(src, n, lds0, xoff, 0, nconv);
+            // a bare barrier: the vector's DMAs are queued ahead of every
+            // weight DMA, and the control word is written
+            __builtin_amdgcn_s_waitcnt(MQ_WC_LGKM0);
+            __builtin_amdgcn_s_barrier();
+            const uint32_t ready = 3u * (uint32_t)(-geo.conv);
+            if (cv) {
+                mq_xq_in_place_by(n, lds0, xoff, 0, nconv, ctl, nullptr);
+                prologue();
+                mq_waves_wait(ctl, ready, L.lane, nullptr);
+                run(lds0, red);
+                return;
+            }
+            prologue();
+            if constexpr (MQ<T>::has_pre) {
+                if (Tn > 0) {
+                    const typename MQ<T>::Pre pr = pre_first();
+                    mq_waves_wait(ctl, ready, L.lane, nullptr);
+                    run_after(lds0, red, pr);
+                }
+            } else {
+                mq_waves_wait(ctl, ready, L.lane, nullptr);
+                run(lds0, red);
+            }
             return;
         }
         const int nconv = 64 * geo.conv, first = (int)blockDim.x - nconv;

@@ -152,6 +152,9 @@ static int g_opt_mq_gufac = 100, g_opt_mq_dnfac = 100;   /* "mq_gufac", "mq_dnfa
                                                          * and down splits */
 static int g_opt_mq_scope = 0;     /* "mq_scope": the mq_p/mq_c/mq_s/mq_x overrides apply to every matrix-core
                                     * launch (0) or only to the matvec (1), gate/up (2) or down (3) launches */
+static int g_mq_sconv = 0;         /* mq_geo may plan vector mode 3 (by default only the expert FFN's gate/up,
+                                    * where it measured faster: C2 16.5 -> 15.5 us; the MoE layer's launches,
+                                    * the matvecs and the FFN down measured slower or no faster with it) */
 static int g_mq_kind = 0;          /* the launch kind mq_geo is planning: 1 matvec, 2 gate/up, 3 down */
 static int g_opt_mq_x = 0;   /* "mq_x": 0 = planner's choice, 1 = vector from global, 2 = vector by LDS DMA,
                               * 3 = converter waves */
@@ -1135,7 +1138,7 @@ int sepia_hip_set_option(const char *name, int value) {
         g_opt_mq = value;
         return 1;
     }
-    if (strcmp(name, "mq_x") == 0 && value >= 0 && value <= 3) {
+    if (strcmp(name, "mq_x") == 0 && value >= 0 && value <= 4) {
         g_opt_mq_x = value;
         return 1;
     }
@@ -1222,6 +1225,8 @@ typedef struct {
                                      * default only for the IQ formats, where they measured faster (C4 IQ3_XXS
                                      * 12.2 -> 11.2 us); the K-quants' stepping waves need all 16 */
 #define MQ_XQ_SEGS_PER_WAVE 128     /* segments a converter wave turns into XQ at most (MQ_XQP passes of 16) */
+#define MQ_SCONV_GAIN 60            /* mq_geo: cost units the first stepping waves save by converting the vector
+                                     * before their own weight prologue (vector mode 3) */
 static size_t mq_xq_bytes(int64_t n) { return (size_t)(n / 256) * 832 + 3 * (size_t)(n / 16) * 4; }
 /* matrix-core format codes (kernels/mq.h decoders, matvec and expert FFN):
  * 0..2 Q2_K, Q3_K, Q4_K; 3..4 IQ2_XS, IQ3_XXS; 5..8 Q5_K, Q6_K, IQ4_XS, Q8_0 */
@@ -1280,19 +1285,21 @@ static int mq_geo(int mc, int wmax, int64_t n_items, int64_t nq, size_t fixed, s
     int64_t best_cost = 0, best_fl = 0;
     int best_nw = 0, found = 0;
     /* vector modes: 0 from global memory, 1 by LDS DMA into a raw copy, 2 by
-     * converter waves (DMA into the XQ place, converted there); 1 and 2 need
-     * the vector's size (raw_bytes) */
+     * converter waves (DMA into the XQ place, converted there), 3 the same
+     * by the first stepping waves before they issue their weights; 1..3
+     * need the vector's size (raw_bytes) */
     const int64_t segs = (int64_t)raw_bytes / 64, cv_need = (segs + MQ_XQ_SEGS_PER_WAVE - 1) / MQ_XQ_SEGS_PER_WAVE;
     /* a forced mode the launch cannot take (converter waves for the FFN
      * launches) leaves the choice to the planner */
     const int ovr = !g_opt_mq_scope || g_opt_mq_scope == g_mq_kind;
     const int opt_p = ovr ? g_opt_mq_p : 0, opt_c = ovr ? g_opt_mq_c : 0, opt_s = ovr ? g_opt_mq_s : 0;
-    const int forced = !ovr || (g_opt_mq_x == 3 && !allow_conv) ? 0 : g_opt_mq_x;
-    for (int mode = 0; mode <= (raw_bytes > 0 ? (allow_conv ? 2 : 1) : 0); mode++) {
+    const int forced = !ovr || (g_opt_mq_x >= 3 && !allow_conv) ? 0 : g_opt_mq_x;
+    for (int mode = 0; mode <= (raw_bytes > 0 ? (allow_conv ? 3 : 1) : 0); mode++) {
         /* converter waves by default only in the matvecs of the formats that
          * gain from them; the FFN launches measured slower with them (the
          * IQ3_XXS down of a real-format layer 34.9 vs 31.1 us) */
-        if (raw_bytes > 0 && (forced ? forced != mode + 1 : (mode == 2 && !(k_mq_conv[mc] && g_mq_kind == 1))))
+        if (raw_bytes > 0 && (forced ? forced != mode + 1 : ((mode == 2 && !(k_mq_conv[mc] && g_mq_kind == 1)) ||
+                                                            (mode == 3 && !g_mq_sconv))))
             continue;
         for (int P = 1; P <= 16 && P <= nq; P++) {
             if (opt_p && P != opt_p) continue;
@@ -1305,9 +1312,10 @@ static int mq_geo(int mc, int wmax, int64_t n_items, int64_t nq, size_t fixed, s
                     cv = 16 - nw < 4 ? 16 - nw : 4;
                     if (cv < cv_need) cv = (int)cv_need;
                 }
+                if (mode == 3 && nw < cv_need) continue;
                 const int64_t spw = ((n_items + C - 1) / C) * ((nq + P - 1) / P);
                 const size_t o_raw = align256(fixed + (size_t)n_items * P * 64);
-                const size_t base = mode == 1 ? align256(o_raw + raw_bytes) : mode == 2 ? align256(o_raw + 16) : o_raw;
+                const size_t base = mode == 1 ? align256(o_raw + raw_bytes) : mode >= 2 ? align256(o_raw + 16) : o_raw;
                 if (base + (size_t)nw * wm > g_lds_max) continue;
                 size_t ring = ((g_lds_max - base) / (size_t)nw) & ~(size_t)1023;
                 if (ring > 4 * wm) ring = 4 * wm;
@@ -1321,7 +1329,7 @@ static int mq_geo(int mc, int wmax, int64_t n_items, int64_t nq, size_t fixed, s
                 /* the vector by DMA ahead of the weights saves about as
                  * much as MQ_XDMA_GAIN cost units, converter waves more */
                 const int64_t cost = spw * ((S >= 2 || spw == 1) ? 10 : 16) -
-                                     (mode == 1 ? MQ_XDMA_GAIN : mode == 2 ? MQ_CONV_GAIN : 0);
+                                     (mode == 1 ? MQ_XDMA_GAIN : mode == 2 ? MQ_CONV_GAIN : mode == 3 ? MQ_SCONV_GAIN : 0);
                 const int64_t fl = (int64_t)nw * S;
                 if (!found || cost < best_cost ||
                     (cost == best_cost && (fl > best_fl || (fl == best_fl && nw > best_nw)))) {
@@ -1333,7 +1341,7 @@ static int mq_geo(int mc, int wmax, int64_t n_items, int64_t nq, size_t fixed, s
                     geo->ring = (int32_t)ring;
                     geo->xraw = mode ? (int32_t)o_raw : 0;
                     geo->orings = (int32_t)base;
-                    geo->conv = cv;
+                    geo->conv = mode == 3 ? -(int32_t)cv_need : cv;
                     geo->nw = nw;
                     geo->C = C;
                     geo->S = (int32_t)(ring / w1 < 4 ? ring / w1 : 4);
@@ -1692,10 +1700,12 @@ static int mq_ffn_plan(const MoeProj *g, const MoeProj *u, const MoeProj *d, con
     const int64_t nk_dr = (tiles_h + pl->dn_wps_r - 1) / pl->dn_wps_r, nk_ds = (tiles_h + pl->dn_wps_s - 1) / pl->dn_wps_s;
     const size_t gu_fixed = MQ_ZERO + mq_xq_bytes(H) + MQ_SEL_BYTES;
     g_mq_kind = 2;
-    if (!mq_geo2(kg, ksg, has_s, 2 * nk_gr, 2 * nk_gs, H / 1024, gu_fixed + k_mq_table[kg], gu_fixed + k_mq_table[ksg],
-                 route ? 0 : (size_t)H * 4, (size_t)H * 4, &pl->gu_threads, &pl->gu_geo_r, &pl->gu_geo_s,
-                 &pl->gu_lds))
-        return 0;
+    g_mq_sconv = !route && n_shared == 0;
+    const int gu_ok = mq_geo2(kg, ksg, has_s, 2 * nk_gr, 2 * nk_gs, H / 1024, gu_fixed + k_mq_table[kg],
+                              gu_fixed + k_mq_table[ksg], route ? 0 : (size_t)H * 4, (size_t)H * 4, &pl->gu_threads,
+                              &pl->gu_geo_r, &pl->gu_geo_s, &pl->gu_lds);
+    g_mq_sconv = 0;
+    if (!gu_ok) return 0;
     /* the routed workgroups' in-place conversion needs 3 waves besides the
      * selecting one (MQ_XQP passes of a quarter of their lanes) */
     if (route && (int64_t)pl->gu_threads - 64 < (H / 16 + MQ_XQ_SEGS_PER_WAVE - 1) / MQ_XQ_SEGS_PER_WAVE * 64)

@@ -538,14 +538,14 @@ def mq_vector(dev, request):
     """Force how the matrix-core kernels read their vector: 1 = from global
     memory after the weight prologue, 2 = by LDS DMA ahead of it, 3 = by
     converter waves (DMA into the XQ place, converted there while the other
-    waves decode their first step; matvec launches only, the FFN launches
-    then keep the planner's choice)."""
+    waves decode their first step), 4 = the same conversion by the first
+    stepping waves before they issue their own weights."""
     assert dev.L.sepia_hip_set_option(b"mq_x", request.param) == 1
     yield request.param
     dev.L.sepia_hip_set_option(b"mq_x", 0)
 
 
-@pytest.mark.parametrize("mq_vector", [1, 2, 3], indirect=True, ids=["global", "dma", "conv"])
+@pytest.mark.parametrize("mq_vector", [1, 2, 3, 4], indirect=True, ids=["global", "dma", "conv", "sconv"])
 @pytest.mark.parametrize("t,out_dim,in_dim", [(12, 4096, 4096), (10, 3072, 6144), (11, 6144, 3072),
                                               (10, 12288, 2048), (12, 40, 12288), (17, 6144, 6144),
                                               (18, 6144, 6144), (18, 257, 3072), (17, 33, 1024)],
@@ -768,7 +768,7 @@ def test_moe_decode_real_types(dev, orc, types):
         dev.free(b)
 
 
-@pytest.mark.parametrize("mq_vector", [1, 2, 3], indirect=True, ids=["global", "dma", "conv"])
+@pytest.mark.parametrize("mq_vector", [1, 2, 3, 4], indirect=True, ids=["global", "dma", "conv", "sconv"])
 def test_moe_decode_mq_vector_paths(dev, orc, mq_vector):
     """C3 layer shapes with 16 routed experts resident; gate/up and down read x
     and h either way."""
