@@ -203,10 +203,10 @@ class Bench:
 # own run) and scaled by what the same counters read for the copy kernel of known size
 # (profiles/*_hbm_traffic.md). Reported as roofline.traffic for the dominant kernel; None until
 # measured for the current build.
-MEASURED_TRAFFIC_C2 = {"sepia_mq_gateup": 12894331, "sepia_mq_down": 8604806}
-MEASURED_TRAFFIC_C3 = {"sepia_moe_route": 6632135, "sepia_mq_gateup": 122062249, "sepia_mq_down": 72327164}
-MEASURED_TRAFFIC_REAL = {"sepia_moe_route": 6632066, "sepia_mq_gateup": 119343701, "sepia_mq_down": 84143688}
-MEASURED_TRAFFIC_C5 = {"sepia_pf_gateup_q": 2991873043, "sepia_pf_down_q": 1901268026}
+MEASURED_TRAFFIC_C2 = {"sepia_mq_gateup": 12992283, "sepia_mq_down": 8618077}
+MEASURED_TRAFFIC_C3 = {"sepia_moe_route": 6612157, "sepia_mq_gateup": 122222317, "sepia_mq_down": 72136272}
+MEASURED_TRAFFIC_REAL = {"sepia_moe_route": 6612334, "sepia_mq_gateup": 124624225, "sepia_mq_down": 76621615}
+MEASURED_TRAFFIC_C5 = {"sepia_pf_gateup_q": 2991420485, "sepia_pf_down_q": 1900821931}
 
 
 def cpu_sample(fn, min_seconds, max_calls):
