@@ -150,7 +150,7 @@ void *sepia_hip_stream(void);
  *                 waves (DMA into the XQ place, converted there while the
  *                 other waves issue and decode their first step), 4 = the
  *                 same conversion by the first stepping waves before they
- *                 issue their own weights;
+ *                 issue their own weights (FFN gate/up launches only);
  *   "mq_scope" 0..3  the mq_p/mq_c/mq_s/mq_x overrides apply to every
  *                 matrix-core launch (0) or only to the matvec (1), the
  *                 expert FFN's gate/up (2) or its down (3) launches;

@@ -667,18 +667,19 @@ template <> struct MQ<ST_Q4_K> {
 // bytes off a boundary (the last block of a row always is) and 2 bytes after
 // it otherwise: no bytes of the next block are read twice.
 // Signs: bit j of the sign byte negates weight j (iq_signs adds the parity
-// bit); four bits become four 0x00 / 0xFF byte masks by the spread
-// s * 0x00204081, and a byte is negated as (g ^ m) + (m & 1) (no carries:
-// no codebook byte is 0).
+// bit). The 128 sign bytes' 0x00 / 0xFF byte masks (8 bytes each) follow
+// the codebook in LDS, so a sign index is one 8-byte read; a byte is
+// negated as (g ^ m) + (m & 1) (no carries: no codebook byte is 0).
 // The three plane dots of a segment combined in f32: with codebook weights
 // up to 62 the exact integer can pass 2^31 (mq_combine holds it for weights
 // <= 15 only); each term is exact in f32, their sum rounds once or twice.
 __device__ __forceinline__ float mq_combine_f(const mq_v4i &d) {
     return __builtin_fmaf((float)d[0], 65536.0f, __builtin_fmaf((float)d[1], 256.0f, (float)d[2]));
 }
-__device__ __forceinline__ uint32_t mq_iq_signed(uint32_t g, uint32_t s4) {
-    const uint32_t m = ((s4 * 0x00204081u) & 0x01010101u) * 0xFFu;
-    return (g ^ m) + (m & 0x01010101u);
+__device__ __forceinline__ uint32_t mq_iq_neg(uint32_t g, uint32_t m) { return (g ^ m) + (m & 0x01010101u); }
+// Byte masks of sign index idx7 (0..127) from the table at st.
+__device__ __forceinline__ uint2 mq_iq_mask(const uint8_t *st, uint32_t idx7) {
+    return *(const uint2 *)(st + 8u * idx7);
 }
 
 // IQ2_XS {d@0, u16 qs[32]@2, scales[8]@66} (74 bytes, reference
@@ -688,7 +689,7 @@ __device__ __forceinline__ uint32_t mq_iq_signed(uint32_t g, uint32_t s4) {
 // Segment sg = 2 ib + half covers entries l = 2 half, 2 half + 1.
 template <> struct MQ<ST_IQ2_XS> {
     static constexpr int bytes = 74, W = 5, Wp = 5, sum_sel = 1;
-    static constexpr uint32_t table_bytes = 512 * 8;
+    static constexpr uint32_t grid_bytes = 512 * 8, table_bytes = grid_bytes + 128 * 8;
     static constexpr bool has_pre = false;
     __device__ static uint32_t shift(uint32_t boff) { return boff & 3u; }
     // window bytes 0..75: words at 0, 16, 32, 48 and 60
@@ -719,9 +720,9 @@ template <> struct MQ<ST_IQ2_XS> {
             const uint32_t v0 = e & 0xFFFFu, v1 = e >> 16;
             const uint2 g0 = *(const uint2 *)(x.tab + 8u * (v0 & 511u));
             const uint2 g1 = *(const uint2 *)(x.tab + 8u * (v1 & 511u));
-            const uint32_t s0 = iq_signs(v0 >> 9), s1 = iq_signs(v1 >> 9);
-            const mq_v4i b = {(int32_t)mq_iq_signed(g0.x, s0 & 15u), (int32_t)mq_iq_signed(g0.y, s0 >> 4),
-                              (int32_t)mq_iq_signed(g1.x, s1 & 15u), (int32_t)mq_iq_signed(g1.y, s1 >> 4)};
+            const uint2 m0 = mq_iq_mask(x.tab + grid_bytes, v0 >> 9), m1 = mq_iq_mask(x.tab + grid_bytes, v1 >> 9);
+            const mq_v4i b = {(int32_t)mq_iq_neg(g0.x, m0.x), (int32_t)mq_iq_neg(g0.y, m0.y),
+                              (int32_t)mq_iq_neg(g1.x, m1.x), (int32_t)mq_iq_neg(g1.y, m1.y)};
             const mq_v4i D = mq_mfma(mq_a(x, 16 * sg), b);
             const uint32_t scb = ((ib < 4 ? sc_lo : sc_hi) >> (8 * (ib & 3))) & 0xFFu;
             const float nib = (float)(half ? (scb >> 4) : (scb & 15u));
@@ -740,7 +741,7 @@ template <> struct MQ<ST_IQ2_XS> {
 // index bytes 8 ib + 4 half .. + 3 and sign indices 2 half, 2 half + 1.
 template <> struct MQ<ST_IQ3_XXS> {
     static constexpr int bytes = 98, W = 7, Wp = 7, sum_sel = 1;
-    static constexpr uint32_t table_bytes = 256 * 4;
+    static constexpr uint32_t grid_bytes = 256 * 4, table_bytes = grid_bytes + 128 * 8;
     static constexpr bool has_pre = false;
     __device__ static uint32_t shift(uint32_t boff) { return boff & 3u; }
     // window bytes 0..99: words at 0, 16, ..., 80 and 84
@@ -767,12 +768,11 @@ template <> struct MQ<ST_IQ3_XXS> {
             for (int half = 0; half < 2; half++) {
                 const int sg = 2 * ib + half;
                 const uint32_t idx = __builtin_amdgcn_alignbyte(L(2 * ib + half + 1), L(2 * ib + half), 2u);
-                const uint32_t sa = iq_signs((aux >> (14 * half)) & 127u), sb = iq_signs((aux >> (14 * half + 7)) & 127u);
+                const uint2 ma = mq_iq_mask(x.tab + grid_bytes, (aux >> (14 * half)) & 127u);
+                const uint2 mb = mq_iq_mask(x.tab + grid_bytes, (aux >> (14 * half + 7)) & 127u);
                 const uint32_t *tab = (const uint32_t *)x.tab;
-                const mq_v4i b = {(int32_t)mq_iq_signed(tab[idx & 0xFFu], sa & 15u),
-                                  (int32_t)mq_iq_signed(tab[(idx >> 8) & 0xFFu], sa >> 4),
-                                  (int32_t)mq_iq_signed(tab[(idx >> 16) & 0xFFu], sb & 15u),
-                                  (int32_t)mq_iq_signed(tab[idx >> 24], sb >> 4)};
+                const mq_v4i b = {(int32_t)mq_iq_neg(tab[idx & 0xFFu], ma.x), (int32_t)mq_iq_neg(tab[(idx >> 8) & 0xFFu], ma.y),
+                                  (int32_t)mq_iq_neg(tab[(idx >> 16) & 0xFFu], mb.x), (int32_t)mq_iq_neg(tab[idx >> 24], mb.y)};
                 const mq_v4i D = mq_mfma(mq_a(x, 16 * sg), b);
                 acc = __builtin_fmaf(db * x.xsb[sg], mq_combine_f(D), acc);
             }
@@ -1028,12 +1028,27 @@ __device__ __forceinline__ uint32_t mq_table_bytes(int32_t type) {
 }
 // The format's codebook into LDS at tab (IQ formats; nothing for the
 // others). Published by the caller's next barrier.
+// IQ formats: then the byte masks of the 128 sign indices (byte j 0xFF when
+// bit j of iq_signs(index) is set).
+template <int T>
+__device__ __forceinline__ void mq_fill_signs(uint8_t *st) {
+    for (int i = threadIdx.x; i < 128; i += blockDim.x) {
+        const uint32_t s = iq_signs((uint32_t)i);
+        uint64_t m = 0;
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            if ((s >> j) & 1u) m |= (uint64_t)0xFF << (8 * j);
+        ((uint64_t *)st)[i] = m;
+    }
+}
 template <int T>
 __device__ __forceinline__ void mq_fill_table(uint8_t *tab) {
     if constexpr (T == ST_IQ2_XS) {
         for (int i = threadIdx.x; i < 512; i += blockDim.x) ((uint64_t *)tab)[i] = c_iq2xs_grid[i];
+        mq_fill_signs<T>(tab + MQ<T>::grid_bytes);
     } else if constexpr (T == ST_IQ3_XXS) {
         for (int i = threadIdx.x; i < 256; i += blockDim.x) ((uint32_t *)tab)[i] = c_iq3xxs_grid[i];
+        mq_fill_signs<T>(tab + MQ<T>::grid_bytes);
     }
 }
 
@@ -1326,7 +1341,9 @@ struct MqWave {
     // the workgroup calls this. CONV false compiles that path out (the host
     // never plans it for such a kernel), which keeps the kernel's registers
     // for its own pipeline.
-    template <bool CONV = true>
+    // SCONV: the kernel may be planned with conv < 0 (the FFN gate/up
+    // launch only; compiled out of the others, which keeps their registers).
+    template <bool CONV = true, bool SCONV = false>
     __device__ __forceinline__ void go(const float *src, const MqGeo &geo, uint8_t *lds0, uint32_t xoff, float *red) {
         if (xq_ready) {
             prologue();
@@ -1340,7 +1357,7 @@ struct MqWave {
             run(lds0, red);
             return;
         }
-        if (geo.conv < 0) {
+        if (SCONV && geo.conv < 0) {
             const int nconv = -64 * geo.conv;
             uint32_t *ctl = (uint32_t *)(lds0 + geo.xraw);
             const bool cv = (int)threadIdx.x < nconv;
@@ -1562,7 +1579,7 @@ __device__ __forceinline__ void mq_gateup_slot(const uint8_t *Wg, const uint8_t 
     wv.x_issued = x_issued;
     wv.xq_ready = xq_ready;
     wv.tab = tab;
-    wv.template go<true>(x, geo, smem, xoff, red);
+    wv.template go<true, true>(x, geo, smem, xoff, red);
     __syncthreads();
     for (int i = threadIdx.x; i < nk * 16; i += blockDim.x) {
         const int k = i >> 4, t = i & 15;

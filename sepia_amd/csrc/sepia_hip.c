@@ -1246,7 +1246,7 @@ static int mq_code(int t) {
 }
 #define MQ_FORMATS 9
 static const int k_mq_words[MQ_FORMATS] = { 7, 7, 9, 5, 7, 11, 15, 9, 17 };   /* padded words per lane (MQ<T>::Wp) */
-static const size_t k_mq_table[MQ_FORMATS] = { 0, 0, 0, 4096, 1024, 0, 0, 0, 0 };   /* LDS codebook (MQ<T>::table_bytes) */
+static const size_t k_mq_table[MQ_FORMATS] = { 0, 0, 0, 5120, 2048, 0, 0, 0, 0 };   /* LDS codebook and sign masks (MQ<T>::table_bytes) */
 /* Converter waves are planned only for the formats where they measured
  * faster (the IQ2_XS / IQ3_XXS matvecs); the others' stepping waves need
  * all 16. */
@@ -1293,7 +1293,8 @@ static int mq_geo(int mc, int wmax, int64_t n_items, int64_t nq, size_t fixed, s
      * launches) leaves the choice to the planner */
     const int ovr = !g_opt_mq_scope || g_opt_mq_scope == g_mq_kind;
     const int opt_p = ovr ? g_opt_mq_p : 0, opt_c = ovr ? g_opt_mq_c : 0, opt_s = ovr ? g_opt_mq_s : 0;
-    const int forced = !ovr || (g_opt_mq_x >= 3 && !allow_conv) ? 0 : g_opt_mq_x;
+    /* mode 3 exists only in the FFN gate/up kernel */
+    const int forced = !ovr || (g_opt_mq_x >= 3 && !allow_conv) || (g_opt_mq_x == 4 && g_mq_kind != 2) ? 0 : g_opt_mq_x;
     for (int mode = 0; mode <= (raw_bytes > 0 ? (allow_conv ? 3 : 1) : 0); mode++) {
         /* converter waves by default only in the matvecs of the formats that
          * gain from them; the FFN launches measured slower with them (the
@@ -1301,6 +1302,7 @@ static int mq_geo(int mc, int wmax, int64_t n_items, int64_t nq, size_t fixed, s
         if (raw_bytes > 0 && (forced ? forced != mode + 1 : ((mode == 2 && !(k_mq_conv[mc] && g_mq_kind == 1)) ||
                                                             (mode == 3 && !g_mq_sconv))))
             continue;
+        if (mode == 3 && g_mq_kind != 2) continue;
         for (int P = 1; P <= 16 && P <= nq; P++) {
             if (opt_p && P != opt_p) continue;
             for (int C = 1; C * P <= 16 && C <= n_items; C++) {

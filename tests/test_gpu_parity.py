@@ -539,7 +539,8 @@ def mq_vector(dev, request):
     memory after the weight prologue, 2 = by LDS DMA ahead of it, 3 = by
     converter waves (DMA into the XQ place, converted there while the other
     waves decode their first step), 4 = the same conversion by the first
-    stepping waves before they issue their own weights."""
+    stepping waves before they issue their own weights (the FFN gate/up
+    launch only; the others keep the planner's choice)."""
     assert dev.L.sepia_hip_set_option(b"mq_x", request.param) == 1
     yield request.param
     dev.L.sepia_hip_set_option(b"mq_x", 0)
