@@ -1255,9 +1255,10 @@ static const int k_mq_conv[MQ_FORMATS] = { 0, 0, 0, 1, 1, 0, 0, 0, 0 };
  * K-quants Q4_K, Q5_K, Q6_K = 100), used to split an FFN launch's
  * workgroups between routed and shared experts. Measured on the MoE decode
  * layer: byte-balanced Q2_K against Q4_K is best, Q3_K against Q4_K at 115,
- * IQ2_XS against Q5_K at 210-250 (87.0 -> 74.9 us per token) and IQ3_XXS
- * against Q6_K at 135-160. IQ4_XS and Q8_0 are estimates. */
-static const int k_mq_cost[MQ_FORMATS] = { 100, 115, 100, 230, 145, 100, 100, 120, 80 };
+ * IQ2_XS against Q5_K at 160 (with the sign masks from LDS the layer is
+ * within 0.5 us from 130 to 230, slower below) and IQ3_XXS against Q6_K at
+ * 145 (100-190 swept). IQ4_XS and Q8_0 are estimates. */
+static const int k_mq_cost[MQ_FORMATS] = { 100, 115, 100, 160, 145, 100, 100, 120, 80 };
 /* A row of n_blocks format blocks in the matrix-core kernels' 256-column
  * blocks (Q8_0: super-blocks of 8 of its 32-column blocks); -1 if it does
  * not divide. */
