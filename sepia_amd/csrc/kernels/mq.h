@@ -708,7 +708,7 @@ template <> struct MQ<ST_IQ2_XS> {
         raw[18] = w[4].w;
         raw[19] = 0u;
         auto L = [&](int m) { return __builtin_amdgcn_alignbyte(raw[m + 1], raw[m], sh); };
-        const float d = mq_half_lo(L(0));
+        const float d = mq_half_lo(L(0)), d4 = 0.25f * d, d8 = 0.125f * d;
         // scales bytes 66..73: the 8 nibble pairs
         const uint32_t sc_lo = __builtin_amdgcn_alignbyte(L(17), L(16), 2u), sc_hi = __builtin_amdgcn_alignbyte(L(18), L(17), 2u);
         float acc = 0.0f;
@@ -726,7 +726,9 @@ template <> struct MQ<ST_IQ2_XS> {
             const mq_v4i D = mq_mfma(mq_a(x, 16 * sg), b);
             const uint32_t scb = ((ib < 4 ? sc_lo : sc_hi) >> (8 * (ib & 3))) & 0xFFu;
             const float nib = (float)(half ? (scb >> 4) : (scb & 15u));
-            const float db = d * (0.5f + nib) * 0.25f;
+            // d (0.5 + nib) / 4 as one fma: the quarter and eighth of d are
+            // exact, so the single rounding gives the same float
+            const float db = __builtin_fmaf(nib, d4, d8);
             acc = __builtin_fmaf(db * x.xsb[sg], mq_combine_f(D), acc);
         }
         return acc;
@@ -758,12 +760,13 @@ template <> struct MQ<ST_IQ3_XXS> {
         raw[24] = w[6].w;   // window dword 24 (w[6].x .. .z repeat dwords 21..23)
         raw[25] = 0u;
         auto L = [&](int m) { return __builtin_amdgcn_alignbyte(raw[m + 1], raw[m], sh); };
-        const float d = mq_half_lo(L(0));
+        const float d = mq_half_lo(L(0)), d2 = 0.5f * d, d4 = 0.25f * d;
         float acc = 0.0f;
 #pragma unroll
         for (int ib = 0; ib < 8; ib++) {
             const uint32_t aux = __builtin_amdgcn_alignbyte(L(17 + ib), L(16 + ib), 2u);
-            const float db = d * (0.5f + (float)(aux >> 28)) * 0.5f;
+            // d (0.5 + aux >> 28) / 2 as one fma (half and quarter of d exact)
+            const float db = __builtin_fmaf((float)(aux >> 28), d2, d4);
 #pragma unroll
             for (int half = 0; half < 2; half++) {
                 const int sg = 2 * ib + half;
