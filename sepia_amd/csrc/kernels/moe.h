@@ -90,7 +90,7 @@ extern "C" __global__ __launch_bounds__(RT_NT) void sepia_moe_route(
     }
 #pragma unroll
     for (int r = 0; r < RT_ROWS; r++) {
-        const float v = wave_sum(acc[r]);
+        const float v = wave_sum_dpp(acc[r]);
         if ((t & 63) == 0) part[t >> 6][r] = v;
     }
     __syncthreads();

@@ -61,6 +61,17 @@ __device__ __forceinline__ void route_cx(int32_t &ka, int32_t &ja, int32_t &kb, 
     jb = sw ? tj : jb;
 }
 
+// Wave sum by DPP within each 16-lane row, then the four row sums read
+// back as uniform values: (row 0 + row 1) + (row 2 + row 3). No LDS round
+// trips (wave_sum's shuffles are LDS permutes).
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+    v += dpp_mov<0xB1>(v);    // quad_perm [1,0,3,2]
+    v += dpp_mov<0x4E>(v);    // quad_perm [2,3,0,1]
+    v += dpp_mov<0x141>(v);   // row_half_mirror
+    v += dpp_mov<0x140>(v);   // row_mirror
+    return (lane_f32(v, 0) + lane_f32(v, 16)) + (lane_f32(v, 32) + lane_f32(v, 48));
+}
+
 // Sum of lanes 0..n-1's doubles, added in lane order (the reference sums the
 // selected terms sequentially); n is at most a few dozen.
 __device__ __forceinline__ double lanes_sum_f64(double v, int n) {
