@@ -228,14 +228,19 @@ __device__ __forceinline__ uint32_t pq_u32u(const uint8_t *p) {
 // >> 2 s) & 3, sub-block k / 16 with scale byte (sc lo nibble, m hi nibble).
 // K step j (64 columns), lane group g: h = j >> 1, s = 2 (j & 1) + (g >> 1),
 // g' = g & 1, sub-block 4 j + g. Codes sc * q by v_perm from the table
-// [0, sc, 2 sc, 3 sc] (selector q | 4 picks its byte q).
-__device__ __forceinline__ mq_v4i pq_b_q2k(const uint8_t *blk, int j, int g) {
-    const uint32_t sc = pq_u8(blk + 4 * j + g) & 15u;
+// [0, sc, 2 sc, 3 sc] (selector q | 4 picks its byte q). The decoders take
+// their LDS bytes as arguments: the block loop reads a K step's window
+// ahead of the matrix ops of the step before (pq_block).
+__device__ __forceinline__ PqWin pq_w_q2k(const uint8_t *blk, int j, int g) {
+    return pq_win(blk + 16 + 32 * (j >> 1) + 16 * (g & 1));
+}
+// sb: scale byte 4 j + g; wq: pq_w_q2k(blk, j, g)
+__device__ __forceinline__ mq_v4i pq_b_q2k(uint32_t sb, const PqWin &wq, int j, int g) {
+    const uint32_t sc = sb & 15u;
     // [0, sc, 2 sc, 3 sc]: the 24-bit product [sc, 2 sc, 3 sc, 0] moved up a byte by v_perm
     // (a shift would fold into a 32-bit constant and a full-width multiply)
     const uint32_t t3 = (uint32_t)__umul24(sc, 0x030201u);
     const uint32_t tab = __builtin_amdgcn_perm(t3, t3, 0x0201000cu);
-    const PqWin wq = pq_win(blk + 16 + 32 * (j >> 1) + 16 * (g & 1));
     const uint32_t sh = wq.sh + 2u * (uint32_t)(2 * (j & 1) + (g >> 1));
     mq_v4i r;
 #pragma unroll
@@ -250,17 +255,21 @@ __device__ __forceinline__ mq_v4i pq_b_q2k(const uint8_t *blk, int j, int g) {
 // sc of sub-block 4 j + g (q3_scale's packing, at 96). Codes (32 - sc) *
 // (u - 4), u = low bits | high bit << 2, by v_perm from the 8-byte table
 // a * (u - 4), a = 32 - sc.
-__device__ __forceinline__ mq_v4i pq_b_q3k(const uint8_t *blk, int j, int g) {
-    const uint32_t lo4 = (pq_u8(blk + 96 + 4 * (j & 1) + g) >> (4 * (j >> 1))) & 15u;
-    const uint32_t hi2 = (pq_u8(blk + 104 + g) >> (2 * j)) & 3u;
+__device__ __forceinline__ PqWin pq_w_q3k(const uint8_t *blk, int j, int g) {
+    return pq_win(blk + 32 + 32 * (j >> 1) + 16 * (g & 1));
+}
+// lb: scale byte 96 + 4 (j & 1) + g; hb: byte 104 + g; wq: pq_w_q3k(blk, j,
+// g); wh: the hmask window pq_win(blk + 16 (g & 1))
+__device__ __forceinline__ mq_v4i pq_b_q3k(uint32_t lb, uint32_t hb, const PqWin &wq, const PqWin &wh, int j,
+                                           int g) {
+    const uint32_t lo4 = (lb >> (4 * (j >> 1))) & 15u;
+    const uint32_t hi2 = (hb >> (2 * j)) & 3u;
     const uint32_t a = 32u - (lo4 | (hi2 << 4));           // two's complement of a, a in [-31, 32]
     const uint32_t a8 = a & 255u, na8 = (0u - a) & 255u;   // a and -a mod 256
     const uint32_t t01 = a8 << 16, t23 = (uint32_t)__umul24(a8, 0x030002u);
     const uint32_t t45 = (uint32_t)__umul24(na8, 0x030004u), t67 = (uint32_t)__umul24(na8, 0x010002u);
     const uint32_t thi = __builtin_amdgcn_perm(t23, t01, 0x06040200u);   // a * [0, 1, 2, 3]
     const uint32_t tlo = __builtin_amdgcn_perm(t67, t45, 0x06040200u);   // a * [-4, -3, -2, -1]
-    const PqWin wq = pq_win(blk + 32 + 32 * (j >> 1) + 16 * (g & 1));
-    const PqWin wh = pq_win(blk + 16 * (g & 1));
     const int s = 2 * (j & 1) + (g >> 1), bit = 4 * (j >> 1) + s;
     const uint32_t shq = wq.sh + 2u * (uint32_t)s;
     // bit `bit` of each hmask byte to bit 2: a right funnel shift by
@@ -291,8 +300,11 @@ typedef unsigned short pq_u16x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t pq_mul16(uint32_t a, uint32_t b) {
     return __builtin_bit_cast(uint32_t, __builtin_bit_cast(pq_u16x2, a) * __builtin_bit_cast(pq_u16x2, b));
 }
-__device__ __forceinline__ PqQ4 pq_b_q4k(const uint8_t *blk, int j, int g, uint32_t sc) {
-    const PqWin wq = pq_win(blk + 16 + 32 * j + 16 * (g & 1));
+__device__ __forceinline__ PqWin pq_w_q4k(const uint8_t *blk, int j, int g) {
+    return pq_win(blk + 16 + 32 * j + 16 * (g & 1));
+}
+// wq: pq_w_q4k(blk, j, g); sc: the 6-bit scale of sub-block 2 j + (g >> 1)
+__device__ __forceinline__ PqQ4 pq_b_q4k(const PqWin &wq, int g, uint32_t sc) {
     const uint32_t sh = wq.sh + 4u * (uint32_t)(g >> 1);
     const uint32_t slo = (uint32_t)__umul24(sc & 7u, 0x10001u), shi = (uint32_t)__umul24(sc >> 3, 0x10001u);
     PqQ4 r;
@@ -339,11 +351,36 @@ __device__ __forceinline__ void pq_block(pf_f32x4 (&acc)[2][2], const uint8_t *A
     auto a_at = [&](int mt, int p, int col) { return As + (16 * mt + n) * APB + 256 * p + col; };
     if constexpr (T == ST_Q2_K || T == ST_Q3_K) {
         mq_v4i C[2][MT][3];
+        // the block's scale bytes and first window up front; a window serves
+        // two K steps, and the second is read after step 1's decode, ahead of
+        // step 1's matrix ops
+        uint32_t sb[2][4], hb[2];
+        PqWin wq[2], wh[2];
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            if constexpr (T == ST_Q2_K) {
+#pragma unroll
+                for (int j = 0; j < 4; j++) sb[t][j] = pq_u8(blk[t] + 4 * j + g);
+                wq[t] = pq_w_q2k(blk[t], 0, g);
+            } else {
+                sb[t][0] = pq_u8(blk[t] + 96 + g);
+                sb[t][1] = pq_u8(blk[t] + 100 + g);
+                hb[t] = pq_u8(blk[t] + 104 + g);
+                wh[t] = pq_win(blk[t] + 16 * (g & 1));
+                wq[t] = pq_w_q3k(blk[t], 0, g);
+            }
+        }
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             mq_v4i B[2];
 #pragma unroll
-            for (int t = 0; t < 2; t++) B[t] = T == ST_Q2_K ? pq_b_q2k(blk[t], j, g) : pq_b_q3k(blk[t], j, g);
+            for (int t = 0; t < 2; t++)
+                B[t] = T == ST_Q2_K ? pq_b_q2k(sb[t][j], wq[t], j, g) : pq_b_q3k(sb[t][j & 1], hb[t], wq[t], wh[t], j, g);
+            if (j == 1) {
+#pragma unroll
+                for (int t = 0; t < 2; t++) wq[t] = T == ST_Q2_K ? pq_w_q2k(blk[t], 2, g) : pq_w_q3k(blk[t], 2, g);
+                __builtin_amdgcn_sched_barrier(0);   // keep the reads ahead of the matrix ops
+            }
 #pragma unroll
             for (int mt = 0; mt < MT; mt++) {
 #pragma unroll
@@ -368,14 +405,29 @@ __device__ __forceinline__ void pq_block(pf_f32x4 (&acc)[2][2], const uint8_t *A
         }
     } else {   // Q4_K
         mq_v4i C[2][MT][3][2];
+        // step j + 1's window and scale are read after step j's decode,
+        // ahead of step j's matrix ops
+        PqWin wq[2];
+        uint32_t sc[2];
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            uint32_t mn;
+            pq_q4k_sm(blk[t], g >> 1, sc[t], mn);
+            wq[t] = pq_w_q4k(blk[t], 0, g);
+        }
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             PqQ4 B[2];
 #pragma unroll
-            for (int t = 0; t < 2; t++) {
-                uint32_t sc, mn;
-                pq_q4k_sm(blk[t], 2 * j + (g >> 1), sc, mn);
-                B[t] = pq_b_q4k(blk[t], j, g, sc);
+            for (int t = 0; t < 2; t++) B[t] = pq_b_q4k(wq[t], g, sc[t]);
+            if (j < 3) {
+#pragma unroll
+                for (int t = 0; t < 2; t++) {
+                    uint32_t mn;
+                    pq_q4k_sm(blk[t], 2 * (j + 1) + (g >> 1), sc[t], mn);
+                    wq[t] = pq_w_q4k(blk[t], j + 1, g);
+                }
+                __builtin_amdgcn_sched_barrier(0);   // keep the reads ahead of the matrix ops
             }
 #pragma unroll
             for (int mt = 0; mt < MT; mt++) {
@@ -440,6 +492,18 @@ __device__ __forceinline__ void pq_block(pf_f32x4 (&acc)[2][2], const uint8_t *A
     }
 }
 
+// s_waitcnt vmcnt(n) for a wave-uniform n <= MAX (a short compare chain
+// instead of pf_wait_vm's switch over every count).
+template <int MAX>
+__device__ __forceinline__ void pq_wait_vm(int n) {
+    if constexpr (MAX <= 0) {
+        __builtin_amdgcn_s_waitcnt(mq_wc_vm(0));
+    } else {
+        if (n >= MAX) __builtin_amdgcn_s_waitcnt(mq_wc_vm(MAX));
+        else pq_wait_vm<MAX - 1>(n);
+    }
+}
+
 // One projection workgroup (see the top of the file). GU: rows r0 .. r0 +
 // 127 of gate (W0) and up (W1), h[pair][row] = silu(gate) * up in f32;
 // down: rows r0 .. r0 + 255 of W0, out[pair][row] in f32. ld_out: floats
@@ -456,8 +520,8 @@ __device__ __forceinline__ void pq_proj(uint8_t *smem, const uint8_t *W0, const 
     const int mat = GU ? (w >> 2) : 0;
     const int rho0 = GU ? 128 * mat + 32 * (w & 3) : 32 * w;   // stage row of N tile 0
     const int64_t grow0 = r0 + (GU ? 32 * (w & 3) : 32 * w);   // its global row
-    auto a_stage = [&](int64_t b) { return smem + (uint32_t)(b & 1) * a_bytes; };
-    auto w_stage = [&](int64_t b) { return smem + 2 * a_bytes + (uint32_t)(b % SW) * w_bytes; };
+    auto a_stage = [&](int b) { return smem + (uint32_t)(b & 1) * a_bytes; };
+    auto w_stage = [&](int b) { return smem + 2 * a_bytes + (uint32_t)b % SW * w_bytes; };
     PqDma<T, GU> dma;
     dma.init(roff, W0, W1, row_bytes, r0);
     const int nwi = PqDma<T, GU>::n_w();
@@ -474,15 +538,16 @@ __device__ __forceinline__ void pq_proj(uint8_t *smem, const uint8_t *W0, const 
         for (int mt = 0; mt < 2; mt++) acc[t][mt] = pf_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     // records one block ahead, weights SW - 1 blocks ahead; in issue order
     // the DMAs of a block b are A_b, then W_(b + SW - 2)
+    const int nbi = (int)nb;   // 256-column blocks of a row (K / 256)
     dma.issue_a(0, a_stage(0), pq);
-    for (int64_t c = 0; c < SW - 1 && c < nb; c++) dma.issue_w(c, w_stage(c), W0, W1);
-    for (int64_t b = 0; b < nb; b++) {
+    for (int c = 0; c < SW - 1 && c < nbi; c++) dma.issue_w(c, w_stage(c), W0, W1);
+    for (int b = 0; b < nbi; b++) {
         // everything up to A_b and W_b; the weights of blocks b + 1 .. b + SW - 2 may fly
-        const int64_t ahead = (nb - 1 - b) < (SW - 2) ? (nb - 1 - b) : (SW - 2);
-        pf_wait_vm(nwi * (int)ahead);
+        const int ahead = (nbi - 1 - b) < (SW - 2) ? (nbi - 1 - b) : (SW - 2);
+        pq_wait_vm<PqDma<T, GU>::KW * (SW - 2)>(nwi * ahead);
         __syncthreads();   // block b staged by every wave; block b - 1's readers are done
-        if (b + 1 < nb) dma.issue_a(b + 1, a_stage(b + 1), pq);
-        if (b + SW - 1 < nb) dma.issue_w(b + SW - 1, w_stage(b + SW - 1), W0, W1);
+        if (b + 1 < nbi) dma.issue_a(b + 1, a_stage(b + 1), pq);
+        if (b + SW - 1 < nbi) dma.issue_w(b + SW - 1, w_stage(b + SW - 1), W0, W1);
         const uint8_t *Ws = w_stage(b);
         const uint8_t *blk[2];
 #pragma unroll
