@@ -9,8 +9,9 @@
 // XQ digits (mq.h); v^ = s q is within s / 2 + 2^-22 |v| of v (a 23-bit
 // representation relative to the row's largest |v|). A 256-column block of
 // a row is an 832-byte record: the digit planes p0, p1, p2 (256 bytes each,
-// column order), then the sixteen 16-column sums S_j = sum of q as bf16 hi
-// (32 bytes) and lo (32 bytes), hi + lo within 2^-16 |S_j| of S_j.
+// column order), then the sixteen 16-column sums S_j = sum of q as bf16 hi +
+// lo (hi + lo within 2^-16 |S_j| of S_j) in four 16-byte groups: group g
+// holds hi of S_4g .. S_4g+3, then their lo.
 //
 // The weights' integer codes are the B operand of v_mfma_i32_16x16x64_i8:
 // Q2_K as sc * q (0..45) and Q3_K as (32 - sc) * (q - 4) (-128..124), the
@@ -46,14 +47,28 @@
 #define PQ_LDS_TOP (PF_LDS_BYTES - 3 * PF_MT * 4)   // row tables: roff, pair, scale
 
 template <int T> struct PqFmt;
-// BB: block bytes; PW: 16-byte pieces of a staged weight row (odd, so the 16
-// rows of a lane group fall in different LDS banks); AP: pieces of a staged
-// PQ record (the planes, the sums where the format has min terms, one piece
-// of padding: odd too); SW: weight stages (LDS: 2 record stages + SW weight
-// stages of 256 rows within 160 KB).
-template <> struct PqFmt<ST_Q2_K> { static constexpr int BB = 84, PW = 7, AP = 53, SW = 3; };
-template <> struct PqFmt<ST_Q3_K> { static constexpr int BB = 110, PW = 9, AP = 49, SW = 3; };
-template <> struct PqFmt<ST_Q4_K> { static constexpr int BB = 144, PW = 11, AP = 53, SW = 2; };
+// BB: block bytes; PW: 16-byte pieces of a staged weight row; RP: pieces of
+// a PQ record the format reads (the planes, and the sums where it has min
+// terms); AP: pieces of a staged record (RP, then padding); SW: weight
+// stages (LDS: 2 record stages + SW weight stages of 256 rows within 160
+// KB); ALN: each row's block is staged from its own 4-byte-aligned start,
+// so a K step's codes are one aligned 16-byte read (else, Q3_K, the 16-byte-
+// aligned window that holds the block, read as dwords at any offset).
+// Strides: on gfx950, 16-byte reads of 16 rows at a stride of 2 mod 4
+// pieces measured free of bank conflicts (odd strides two-way), so AP and
+// the ALN formats' PW are 2 mod 4.
+template <> struct PqFmt<ST_Q2_K> {
+    static constexpr int BB = 84, PW = 6, RP = 52, AP = 54, SW = 3;
+    static constexpr bool ALN = true;
+};
+template <> struct PqFmt<ST_Q3_K> {
+    static constexpr int BB = 110, PW = 9, RP = 48, AP = 50, SW = 3;
+    static constexpr bool ALN = false;
+};
+template <> struct PqFmt<ST_Q4_K> {
+    static constexpr int BB = 144, PW = 10, RP = 52, AP = 54, SW = 2;
+    static constexpr bool ALN = true;
+};
 
 // ------------------------------------------------------------- rows -> PQ --
 // Wave max over 64 lanes.
@@ -119,37 +134,41 @@ extern "C" __global__ __launch_bounds__(256) void sepia_pf_quant(const float *__
         // S = hi + lo: hi = bf16(S), lo = bf16 of the exact integer remainder
         const __bf16 hi = (__bf16)(float)sum;
         const __bf16 lo = (__bf16)(float)(sum - (int32_t)(float)hi);
-        *(__bf16 *)(rec + 768 + 2 * j) = hi;
-        *(__bf16 *)(rec + 800 + 2 * j) = lo;
+        *(__bf16 *)(rec + 768 + 16 * (j >> 2) + 2 * (j & 3)) = hi;
+        *(__bf16 *)(rec + 776 + 16 * (j >> 2) + 2 * (j & 3)) = lo;
     }
 }
 
 // --------------------------------------------------------------- staging --
 // LDS: [records of block b: 2 stages][weight windows of block b: SW stages]
 // [row tables]. A record stage holds the unit's PQ records of the block
-// (record m at 16 AP m: its first AP - 1 pieces of 16 bytes, then a padding
-// piece, piece 0 again). A weight stage holds each weight row's 16-byte-
-// aligned window that holds the block (row k at 16 PW k, PW pieces; those
-// past the window's end fetch its first piece again, so no read leaves the
-// block's row): gate/up stages carry 128 gate rows, then the same 128 up
-// rows; down stages 256 rows. A wave instruction moves 64 pieces (1 KB) of
+// (record m at 16 AP m: its first RP pieces of 16 bytes, then padding
+// pieces, piece 0 again). A weight stage holds each weight row's block at
+// 16 PW k for row k, in PW pieces. ALN formats: from the block's start;
+// the last piece, where the block ends inside it, takes the block's last 16
+// bytes (Q2_K: bytes 68..83 at 80, so d and dmin sit at 92 and 94), and
+// pieces past the block's end take piece 0 again. Else the 16-byte-aligned
+// window that holds the block, pieces past the window's end fetching its
+// first piece again. No read leaves the block's row. Gate/up stages carry
+// 128 gate rows, then the same 128 up rows; down stages 256 rows. A wave instruction moves 64 pieces (1 KB) of
 // one stage; wave w issues instructions w, w + 8, ... of each. Their lane
 // offsets are fixed for the workgroup but for the block term, so they are
 // computed once.
 template <int T, bool GU>
 struct PqDma {
-    static constexpr int BB = PqFmt<T>::BB, PW = PqFmt<T>::PW, AP = PqFmt<T>::AP;
+    static constexpr int BB = PqFmt<T>::BB, PW = PqFmt<T>::PW, AP = PqFmt<T>::AP, RP = PqFmt<T>::RP;
+    static constexpr bool ALN = PqFmt<T>::ALN;
     static constexpr int NA = (PF_MT * AP + 63) / 64, KA = (NA + 7) / 8;
-    static constexpr int NW = PQ_ROWS * PW / 64, KW = (NW + 7) / 8;   // NW: 28, 36, 44
+    static constexpr int NW = PQ_ROWS * PW / 64, KW = (NW + 7) / 8;   // NW: 24, 36, 40
     uint32_t a[KA];            // record piece offsets at block 0, ~0u for an idle lane
-    uint32_t r[KW], c16[KW];   // row offset (from the 16-byte-aligned base), 16 * piece
+    uint32_t r[KW], c16[KW];   // row offset (ALN: from the base, else from the 16-byte-aligned base); piece offset
     __device__ __forceinline__ void init(const uint32_t *roff, const uint8_t *W0, const uint8_t *W1,
                                          uint64_t row_bytes, int64_t r0) {
         const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
 #pragma unroll
         for (int k = 0; k < KA; k++) {
             const int q = 64 * (w + 8 * k) + lane, m = q / AP, c = q - m * AP;
-            a[k] = q < PF_MT * AP ? roff[m] + 16u * (uint32_t)(c < AP - 1 ? c : 0) : ~0u;
+            a[k] = q < PF_MT * AP ? roff[m] + 16u * (uint32_t)(c < RP ? c : 0) : ~0u;
         }
 #pragma unroll
         for (int k = 0; k < KW; k++) {
@@ -157,8 +176,13 @@ struct PqDma {
             const int mat = GU ? jj / (NW / 2) : 0, j1 = GU ? jj - mat * (NW / 2) : jj;
             const int q = 64 * j1 + lane, kr = q / PW, c = q - kr * PW;
             const uint8_t *W = mat ? W1 : W0;
-            r[k] = (uint32_t)(((uintptr_t)W & 15) + (uint64_t)(r0 + kr) * row_bytes);
-            c16[k] = 16u * (uint32_t)c;
+            if constexpr (ALN) {
+                r[k] = (uint32_t)((uint64_t)(r0 + kr) * row_bytes);
+                c16[k] = 16 * c + 16 <= BB ? 16u * (uint32_t)c : 16 * c < BB ? (uint32_t)(BB - 16) : 0u;
+            } else {
+                r[k] = (uint32_t)(((uintptr_t)W & 15) + (uint64_t)(r0 + kr) * row_bytes);
+                c16[k] = 16u * (uint32_t)c;
+            }
         }
     }
     // this wave's weight instructions per block
@@ -178,14 +202,19 @@ struct PqDma {
     __device__ __forceinline__ void issue_w(int64_t b, uint8_t *Ws, const uint8_t *W0, const uint8_t *W1) const {
         const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
         const uint32_t wb = (uint32_t)b * BB;
-        const uint8_t *A0 = (const uint8_t *)((uintptr_t)W0 & ~(uintptr_t)15);
-        const uint8_t *A1 = GU ? (const uint8_t *)((uintptr_t)W1 & ~(uintptr_t)15) : A0;
+        const uint8_t *A0 = ALN ? W0 : (const uint8_t *)((uintptr_t)W0 & ~(uintptr_t)15);
+        const uint8_t *A1 = GU ? (ALN ? W1 : (const uint8_t *)((uintptr_t)W1 & ~(uintptr_t)15)) : A0;
 #pragma unroll
         for (int k = 0; k < KW; k++) {
             const int jj = w + 8 * k;
             if (jj < NW) {
-                const uint32_t off = r[k] + wb, o = off & 15u;
-                const uint32_t voff = (off - o) + ((int)c16[k] < (int)(o + BB) ? c16[k] : 0u);
+                uint32_t voff;
+                if constexpr (ALN) {
+                    voff = r[k] + wb + c16[k];
+                } else {
+                    const uint32_t off = r[k] + wb, o = off & 15u;
+                    voff = (off - o) + ((int)c16[k] < (int)(o + BB) ? c16[k] : 0u);
+                }
                 pf_dma16((GU && jj >= NW / 2) ? A1 : A0, voff, pf_lds(Ws + 1024 * jj));
             }
         }
@@ -218,11 +247,13 @@ __device__ __forceinline__ PqWin pq_win(const uint8_t *p) {
 __device__ __forceinline__ uint32_t pq_fsh(uint32_t hi, uint32_t lo, uint32_t n) {
     return __builtin_amdgcn_alignbit(hi, lo, n);
 }
-// u32 at a 2-byte-aligned LDS address.
-__device__ __forceinline__ uint32_t pq_u32u(const uint8_t *p) {
-    pq_lds_u32 *q = pq_w32(p);
-    return pq_fsh(q[1], q[0], 8u * (pf_lds(p) & 3u));
+typedef uint32_t pq_u4 __attribute__((ext_vector_type(4)));
+// 16 bytes at a 16-byte-aligned LDS address (one ds_read_b128); u32 at a
+// 4-byte-aligned one.
+__device__ __forceinline__ pq_u4 pq_b128(const uint8_t *p) {
+    return *(const __attribute__((address_space(3))) pq_u4 *)(size_t)pf_lds(p);
 }
+__device__ __forceinline__ uint32_t pq_u32(const uint8_t *p) { return *(pq_lds_u32 *)(size_t)pf_lds(p); }
 
 // Q2_K (ggml): weight k = 128 h + 32 s + 16 g' + l: q = (qs[32 h + 16 g' + l]
 // >> 2 s) & 3, sub-block k / 16 with scale byte (sc lo nibble, m hi nibble).
@@ -230,22 +261,23 @@ __device__ __forceinline__ uint32_t pq_u32u(const uint8_t *p) {
 // g' = g & 1, sub-block 4 j + g. Codes sc * q by v_perm from the table
 // [0, sc, 2 sc, 3 sc] (selector q | 4 picks its byte q). The decoders take
 // their LDS bytes as arguments: the block loop reads a K step's window
-// ahead of the matrix ops of the step before (pq_block).
-__device__ __forceinline__ PqWin pq_w_q2k(const uint8_t *blk, int j, int g) {
-    return pq_win(blk + 16 + 32 * (j >> 1) + 16 * (g & 1));
+// ahead of the matrix ops of the step before (pq_block). The staged block
+// is 16-byte aligned: a window is one 16-byte read.
+__device__ __forceinline__ pq_u4 pq_w_q2k(const uint8_t *blk, int j, int g) {
+    return pq_b128(blk + 16 + 32 * (j >> 1) + 16 * (g & 1));
 }
-// sb: scale byte 4 j + g; wq: pq_w_q2k(blk, j, g)
-__device__ __forceinline__ mq_v4i pq_b_q2k(uint32_t sb, const PqWin &wq, int j, int g) {
-    const uint32_t sc = sb & 15u;
+// sc4: scale bytes 0..15; wq: pq_w_q2k(blk, j, g)
+__device__ __forceinline__ mq_v4i pq_b_q2k(const pq_u4 &sc4, const pq_u4 &wq, int j, int g) {
+    const uint32_t sc = __builtin_amdgcn_ubfe(sc4[j], 8u * (uint32_t)g, 4u);   // byte 4 j + g, low nibble
     // [0, sc, 2 sc, 3 sc]: the 24-bit product [sc, 2 sc, 3 sc, 0] moved up a byte by v_perm
     // (a shift would fold into a 32-bit constant and a full-width multiply)
     const uint32_t t3 = (uint32_t)__umul24(sc, 0x030201u);
     const uint32_t tab = __builtin_amdgcn_perm(t3, t3, 0x0201000cu);
-    const uint32_t sh = wq.sh + 2u * (uint32_t)(2 * (j & 1) + (g >> 1));
+    const uint32_t sh = 2u * (uint32_t)(2 * (j & 1) + (g >> 1));
     mq_v4i r;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        const uint32_t u = (pq_fsh(wq.d[i + 1], wq.d[i], sh) & 0x03030303u) | 0x04040404u;
+        const uint32_t u = ((wq[i] >> sh) & 0x03030303u) | 0x04040404u;
         r[i] = (int32_t)__builtin_amdgcn_perm(tab, 0u, u);
     }
     return r;
@@ -300,17 +332,18 @@ typedef unsigned short pq_u16x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t pq_mul16(uint32_t a, uint32_t b) {
     return __builtin_bit_cast(uint32_t, __builtin_bit_cast(pq_u16x2, a) * __builtin_bit_cast(pq_u16x2, b));
 }
-__device__ __forceinline__ PqWin pq_w_q4k(const uint8_t *blk, int j, int g) {
-    return pq_win(blk + 16 + 32 * j + 16 * (g & 1));
+__device__ __forceinline__ pq_u4 pq_w_q4k(const uint8_t *blk, int j, int g) {
+    return pq_b128(blk + 16 + 32 * j + 16 * (g & 1));
 }
-// wq: pq_w_q4k(blk, j, g); sc: the 6-bit scale of sub-block 2 j + (g >> 1)
-__device__ __forceinline__ PqQ4 pq_b_q4k(const PqWin &wq, int g, uint32_t sc) {
-    const uint32_t sh = wq.sh + 4u * (uint32_t)(g >> 1);
+// wq: pq_w_q4k(blk, j, g) (16-byte-aligned staging); sc: the 6-bit scale of
+// sub-block 2 j + (g >> 1)
+__device__ __forceinline__ PqQ4 pq_b_q4k(const pq_u4 &wq, int g, uint32_t sc) {
+    const uint32_t sh = 4u * (uint32_t)(g >> 1);
     const uint32_t slo = (uint32_t)__umul24(sc & 7u, 0x10001u), shi = (uint32_t)__umul24(sc >> 3, 0x10001u);
     PqQ4 r;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        const uint32_t q = pq_fsh(wq.d[i + 1], wq.d[i], sh) & 0x0F0F0F0Fu;
+        const uint32_t q = (wq[i] >> sh) & 0x0F0F0F0Fu;
         r.lo[i] = (int32_t)pq_mul16(q, slo);
         r.hi[i] = (int32_t)pq_mul16(q, shi);
     }
@@ -332,6 +365,7 @@ __device__ __forceinline__ void pq_q4k_sm(const uint8_t *blk, int jj, uint32_t &
 // ----------------------------------------------------------- projection --
 // acc (+)= this block's share for both N tiles and MT M tiles.
 typedef short pq_s16x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t pq_u2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ pq_s16x4 pq_bf4(float a, float b, float c, float d) {
     __bf16 h[4] = {(__bf16)a, (__bf16)b, (__bf16)c, (__bf16)d};
     return *(const pq_s16x4 *)h;
@@ -354,14 +388,14 @@ __device__ __forceinline__ void pq_block(pf_f32x4 (&acc)[2][2], const uint8_t *A
         // the block's scale bytes and first window up front; a window serves
         // two K steps, and the second is read after step 1's decode, ahead of
         // step 1's matrix ops
-        uint32_t sb[2][4], hb[2];
+        uint32_t sb[2][2], hb[2];
+        pq_u4 sc4[2], w2[2];
         PqWin wq[2], wh[2];
 #pragma unroll
         for (int t = 0; t < 2; t++) {
             if constexpr (T == ST_Q2_K) {
-#pragma unroll
-                for (int j = 0; j < 4; j++) sb[t][j] = pq_u8(blk[t] + 4 * j + g);
-                wq[t] = pq_w_q2k(blk[t], 0, g);
+                sc4[t] = pq_b128(blk[t]);
+                w2[t] = pq_w_q2k(blk[t], 0, g);
             } else {
                 sb[t][0] = pq_u8(blk[t] + 96 + g);
                 sb[t][1] = pq_u8(blk[t] + 100 + g);
@@ -374,11 +408,16 @@ __device__ __forceinline__ void pq_block(pf_f32x4 (&acc)[2][2], const uint8_t *A
         for (int j = 0; j < 4; j++) {
             mq_v4i B[2];
 #pragma unroll
-            for (int t = 0; t < 2; t++)
-                B[t] = T == ST_Q2_K ? pq_b_q2k(sb[t][j], wq[t], j, g) : pq_b_q3k(sb[t][j & 1], hb[t], wq[t], wh[t], j, g);
+            for (int t = 0; t < 2; t++) {
+                if constexpr (T == ST_Q2_K) B[t] = pq_b_q2k(sc4[t], w2[t], j, g);
+                else B[t] = pq_b_q3k(sb[t][j & 1], hb[t], wq[t], wh[t], j, g);
+            }
             if (j == 1) {
 #pragma unroll
-                for (int t = 0; t < 2; t++) wq[t] = T == ST_Q2_K ? pq_w_q2k(blk[t], 2, g) : pq_w_q3k(blk[t], 2, g);
+                for (int t = 0; t < 2; t++) {
+                    if constexpr (T == ST_Q2_K) w2[t] = pq_w_q2k(blk[t], 2, g);
+                    else wq[t] = pq_w_q3k(blk[t], 2, g);
+                }
                 __builtin_amdgcn_sched_barrier(0);   // keep the reads ahead of the matrix ops
             }
 #pragma unroll
@@ -395,7 +434,7 @@ __device__ __forceinline__ void pq_block(pf_f32x4 (&acc)[2][2], const uint8_t *A
         }
 #pragma unroll
         for (int t = 0; t < 2; t++) {
-            const float d = pq_h2f(blk[t] + (T == ST_Q2_K ? 80 : 108)), dn = T == ST_Q2_K ? d : -d;
+            const float d = pq_h2f(blk[t] + (T == ST_Q2_K ? 92 : 108)), dn = T == ST_Q2_K ? d : -d;
 #pragma unroll
             for (int mt = 0; mt < MT; mt++)
 #pragma unroll
@@ -407,7 +446,7 @@ __device__ __forceinline__ void pq_block(pf_f32x4 (&acc)[2][2], const uint8_t *A
         mq_v4i C[2][MT][3][2];
         // step j + 1's window and scale are read after step j's decode,
         // ahead of step j's matrix ops
-        PqWin wq[2];
+        pq_u4 wq[2];
         uint32_t sc[2];
 #pragma unroll
         for (int t = 0; t < 2; t++) {
@@ -468,9 +507,9 @@ __device__ __forceinline__ void pq_block(pf_f32x4 (&acc)[2][2], const uint8_t *A
             pq_s16x4 bm;
             float dmin;
             if constexpr (T == ST_Q2_K) {
-                const uint32_t v = pq_u32u(blk[t] + 4 * g) >> 4;
+                const uint32_t v = pq_u32(blk[t] + 4 * g) >> 4;
                 bm = pq_bf4((float)(v & 15u), (float)((v >> 8) & 15u), (float)((v >> 16) & 15u), (float)((v >> 24) & 15u));
-                dmin = pq_h2f(blk[t] + 82);
+                dmin = pq_h2f(blk[t] + 94);
             } else {
                 uint32_t s0, m0, s1, m1;
                 pq_q4k_sm(blk[t], 2 * g, s0, m0);
@@ -480,8 +519,10 @@ __device__ __forceinline__ void pq_block(pf_f32x4 (&acc)[2][2], const uint8_t *A
             }
 #pragma unroll
             for (int mt = 0; mt < MT; mt++) {
-                const uint8_t *sr = As + (16 * mt + n) * APB + 768 + 8 * g;
-                const pq_s16x4 shi = *(const pq_s16x4 *)sr, slo = *(const pq_s16x4 *)(sr + 32);
+                // group g of the sums: hi of S_4g .. S_4g+3, then their lo
+                const pq_u4 sv = pq_b128(As + (16 * mt + n) * APB + 768 + 16 * g);
+                const pq_s16x4 shi = __builtin_bit_cast(pq_s16x4, (pq_u2){sv[0], sv[1]});
+                const pq_s16x4 slo = __builtin_bit_cast(pq_s16x4, (pq_u2){sv[2], sv[3]});
                 pf_f32x4 cm = {0.0f, 0.0f, 0.0f, 0.0f};
                 cm = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(shi, bm, cm, 0, 0, 0);
                 cm = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(slo, bm, cm, 0, 0, 0);
@@ -552,7 +593,8 @@ __device__ __forceinline__ void pq_proj(uint8_t *smem, const uint8_t *W0, const 
         const uint8_t *blk[2];
 #pragma unroll
         for (int t = 0; t < 2; t++)
-            blk[t] = Ws + (uint32_t)(rho0 + 16 * t + n) * (PW * 16) + ((rofs[t] + (uint32_t)b * BB) & 15u);
+            blk[t] = Ws + (uint32_t)(rho0 + 16 * t + n) * (PW * 16) +
+                     (PqFmt<T>::ALN ? 0u : ((rofs[t] + (uint32_t)b * BB) & 15u));
         pq_block<T, MT>(acc, a_stage(b), blk[0], blk[1]);
     }
     // y = s_pair * acc; lane: pairs 16 mt + 4 g + i, rows grow0 + 16 t + n

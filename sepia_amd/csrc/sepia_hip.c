@@ -1804,9 +1804,14 @@ int sepia_gpu_moe_prefill(const SepiaMoeLayerDesc *L, int64_t n_tokens, SepiaGpu
         LOG("%s: hidden and inter must be multiples of 256", op);
         return 0;
     }
-    /* int8 path: every projection Q2_K, Q3_K or Q4_K; activations as PQ rows
-     * (kernels/prefill_q.h: 832 bytes per 256 columns) */
-    const int use_q = g_opt_pf_q && pf_type_int(g.type) && pf_type_int(d.type) &&
+    /* int8 path: every projection Q2_K, Q3_K or Q4_K with 4-byte-aligned
+     * rows (its DMA stages Q2_K and Q4_K blocks from their own starts);
+     * activations as PQ rows (kernels/prefill_q.h: 832 bytes per 256
+     * columns) */
+    int q_aligned = 1;
+    for (int i = 0; i < (ns > 0 ? 6 : 3); i++)
+        if (((uintptr_t)ps[i]->base | ps[i]->stride | ps[i]->row_bytes) & 3) q_aligned = 0;
+    const int use_q = g_opt_pf_q && q_aligned && pf_type_int(g.type) && pf_type_int(d.type) &&
                       (ns == 0 || (pf_type_int(sg.type) && pf_type_int(sd.type)));
     const int64_t ldqx = H / 256 * 832, ldqh = I / 256 * 832;
     /* the pipelines address activation rows with 32-bit byte offsets */
