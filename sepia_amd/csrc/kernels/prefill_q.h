@@ -51,24 +51,16 @@ template <int T> struct PqFmt;
 // a PQ record the format reads (the planes, and the sums where it has min
 // terms); AP: pieces of a staged record (RP, then padding); SW: weight
 // stages (LDS: 2 record stages + SW weight stages of 256 rows within 160
-// KB); ALN: each row's block is staged from its own 4-byte-aligned start,
-// so a K step's codes are one aligned 16-byte read (else, Q3_K, the 16-byte-
-// aligned window that holds the block, read as dwords at any offset).
-// Strides: on gfx950, 16-byte reads of 16 rows at a stride of 2 mod 4
-// pieces measured free of bank conflicts (odd strides two-way), so AP and
-// the ALN formats' PW are 2 mod 4.
-template <> struct PqFmt<ST_Q2_K> {
-    static constexpr int BB = 84, PW = 6, RP = 52, AP = 54, SW = 3;
-    static constexpr bool ALN = true;
-};
-template <> struct PqFmt<ST_Q3_K> {
-    static constexpr int BB = 110, PW = 9, RP = 48, AP = 50, SW = 3;
-    static constexpr bool ALN = false;
-};
-template <> struct PqFmt<ST_Q4_K> {
-    static constexpr int BB = 144, PW = 10, RP = 52, AP = 54, SW = 2;
-    static constexpr bool ALN = true;
-};
+// KB). Each row's block is staged from the 4-byte boundary at or below its
+// start (every format here: rows of 4-byte multiples, so the offset o of
+// the block in its staged row is the same for every row of a block: 0, or 0
+// and 2 for Q3_K), so a K step's codes are one (Q3_K: two) aligned 16-byte
+// reads. Strides: on gfx950, 16-byte reads of 16 rows at a stride of 2 mod
+// 4 pieces measured free of bank conflicts (odd strides two-way), so AP and
+// PW are 2 mod 4.
+template <> struct PqFmt<ST_Q2_K> { static constexpr int BB = 84, PW = 6, RP = 52, AP = 54, SW = 3; };
+template <> struct PqFmt<ST_Q3_K> { static constexpr int BB = 110, PW = 10, RP = 48, AP = 50, SW = 2; };
+template <> struct PqFmt<ST_Q4_K> { static constexpr int BB = 144, PW = 10, RP = 52, AP = 54, SW = 2; };
 
 // ------------------------------------------------------------- rows -> PQ --
 // Wave max over 64 lanes.
@@ -144,24 +136,24 @@ extern "C" __global__ __launch_bounds__(256) void sepia_pf_quant(const float *__
 // [row tables]. A record stage holds the unit's PQ records of the block
 // (record m at 16 AP m: its first RP pieces of 16 bytes, then padding
 // pieces, piece 0 again). A weight stage holds each weight row's block at
-// 16 PW k for row k, in PW pieces. ALN formats: from the block's start;
-// the last piece, where the block ends inside it, takes the block's last 16
-// bytes (Q2_K: bytes 68..83 at 80, so d and dmin sit at 92 and 94), and
-// pieces past the block's end take piece 0 again. Else the 16-byte-aligned
-// window that holds the block, pieces past the window's end fetching its
-// first piece again. No read leaves the block's row. Gate/up stages carry
-// 128 gate rows, then the same 128 up rows; down stages 256 rows. A wave instruction moves 64 pieces (1 KB) of
+// 16 PW k + o for row k, in PW pieces from the 4-byte boundary at or below
+// the block's start (the offset o). A piece that would end more than 2
+// bytes past the block takes the block's last 16 bytes instead (Q2_K: bytes
+// 68..83 at 80, so d and dmin sit at 92 and 94); pieces past the block's
+// end take piece 0 again. So no read passes the 4-byte word that holds the
+// block's last byte (Q3_K reads at most 2 bytes past it, within that word).
+// Gate/up stages carry 128 gate rows, then the same 128 up rows; down
+// stages 256 rows. A wave instruction moves 64 pieces (1 KB) of
 // one stage; wave w issues instructions w, w + 8, ... of each. Their lane
 // offsets are fixed for the workgroup but for the block term, so they are
 // computed once.
 template <int T, bool GU>
 struct PqDma {
     static constexpr int BB = PqFmt<T>::BB, PW = PqFmt<T>::PW, AP = PqFmt<T>::AP, RP = PqFmt<T>::RP;
-    static constexpr bool ALN = PqFmt<T>::ALN;
     static constexpr int NA = (PF_MT * AP + 63) / 64, KA = (NA + 7) / 8;
-    static constexpr int NW = PQ_ROWS * PW / 64, KW = (NW + 7) / 8;   // NW: 24, 36, 40
+    static constexpr int NW = PQ_ROWS * PW / 64, KW = (NW + 7) / 8;   // NW: 24, 40, 40
     uint32_t a[KA];            // record piece offsets at block 0, ~0u for an idle lane
-    uint32_t r[KW], c16[KW];   // row offset (ALN: from the base, else from the 16-byte-aligned base); piece offset
+    uint32_t r[KW], c16[KW];   // row offset from the matrix base; offset of the lane's piece
     __device__ __forceinline__ void init(const uint32_t *roff, const uint8_t *W0, const uint8_t *W1,
                                          uint64_t row_bytes, int64_t r0) {
         const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -175,14 +167,8 @@ struct PqDma {
             const int jj = w + 8 * k;
             const int mat = GU ? jj / (NW / 2) : 0, j1 = GU ? jj - mat * (NW / 2) : jj;
             const int q = 64 * j1 + lane, kr = q / PW, c = q - kr * PW;
-            const uint8_t *W = mat ? W1 : W0;
-            if constexpr (ALN) {
-                r[k] = (uint32_t)((uint64_t)(r0 + kr) * row_bytes);
-                c16[k] = 16 * c + 16 <= BB ? 16u * (uint32_t)c : 16 * c < BB ? (uint32_t)(BB - 16) : 0u;
-            } else {
-                r[k] = (uint32_t)(((uintptr_t)W & 15) + (uint64_t)(r0 + kr) * row_bytes);
-                c16[k] = 16u * (uint32_t)c;
-            }
+            r[k] = (uint32_t)((uint64_t)(r0 + kr) * row_bytes);
+            c16[k] = 16 * c >= BB ? 0u : 16 * c + 16 <= BB + 2 ? 16u * (uint32_t)c : (uint32_t)(BB - 16);
         }
     }
     // this wave's weight instructions per block
@@ -202,21 +188,10 @@ struct PqDma {
     __device__ __forceinline__ void issue_w(int64_t b, uint8_t *Ws, const uint8_t *W0, const uint8_t *W1) const {
         const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
         const uint32_t wb = (uint32_t)b * BB;
-        const uint8_t *A0 = ALN ? W0 : (const uint8_t *)((uintptr_t)W0 & ~(uintptr_t)15);
-        const uint8_t *A1 = GU ? (ALN ? W1 : (const uint8_t *)((uintptr_t)W1 & ~(uintptr_t)15)) : A0;
 #pragma unroll
         for (int k = 0; k < KW; k++) {
             const int jj = w + 8 * k;
-            if (jj < NW) {
-                uint32_t voff;
-                if constexpr (ALN) {
-                    voff = r[k] + wb + c16[k];
-                } else {
-                    const uint32_t off = r[k] + wb, o = off & 15u;
-                    voff = (off - o) + ((int)c16[k] < (int)(o + BB) ? c16[k] : 0u);
-                }
-                pf_dma16((GU && jj >= NW / 2) ? A1 : A0, voff, pf_lds(Ws + 1024 * jj));
-            }
+            if (jj < NW) pf_dma16((GU && jj >= NW / 2) ? W1 : W0, ((r[k] + wb) & ~3u) + c16[k], pf_lds(Ws + 1024 * jj));
         }
     }
 };
@@ -225,29 +200,32 @@ struct PqDma {
 typedef const __attribute__((address_space(3))) uint32_t pq_lds_u32;
 typedef const __attribute__((address_space(3))) uint16_t pq_lds_u16;
 typedef const __attribute__((address_space(3))) uint8_t pq_lds_u8;
-__device__ __forceinline__ pq_lds_u32 *pq_w32(const uint8_t *p) { return (pq_lds_u32 *)(size_t)(pf_lds(p) & ~3u); }
 __device__ __forceinline__ uint32_t pq_u8(const uint8_t *p) { return *(pq_lds_u8 *)(size_t)pf_lds(p); }
 __device__ __forceinline__ uint32_t pq_u16(const uint8_t *p) { return *(pq_lds_u16 *)(size_t)pf_lds(p); }
 __device__ __forceinline__ float pq_h2f(const uint8_t *p) { return f16_bits_to_f32(pq_u16(p)); }
-// Five dwords from the dword holding p: with sh = 8 (p & 3), the funnel
-// shift of (D[i + 1], D[i]) by sh + t is bytes 4 i .. 4 i + 3 from p, moved
-// down t bits.
+// Five dwords from the dword holding p, for p at most 3 bytes past a
+// 16-byte boundary (two aligned 16-byte reads): with sh = 8 (p & 3), the
+// funnel shift of (D[i + 1], D[i]) by sh + t is bytes 4 i .. 4 i + 3 from
+// p, moved down t bits.
 struct PqWin {
     uint32_t d[5];
     uint32_t sh;
 };
+typedef uint32_t pq_u4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ PqWin pq_win(const uint8_t *p) {
+    const uint32_t a = pf_lds(p), a16 = a & ~15u;
+    const pq_u4 lo = *(const __attribute__((address_space(3))) pq_u4 *)(size_t)a16;
+    const pq_u4 hi = *(const __attribute__((address_space(3))) pq_u4 *)(size_t)(a16 + 16u);
     PqWin r;
-    pq_lds_u32 *q = pq_w32(p);
 #pragma unroll
-    for (int i = 0; i < 5; i++) r.d[i] = q[i];
-    r.sh = 8u * (pf_lds(p) & 3u);
+    for (int i = 0; i < 4; i++) r.d[i] = lo[i];
+    r.d[4] = hi[0];
+    r.sh = 8u * (a & 3u);
     return r;
 }
 __device__ __forceinline__ uint32_t pq_fsh(uint32_t hi, uint32_t lo, uint32_t n) {
     return __builtin_amdgcn_alignbit(hi, lo, n);
 }
-typedef uint32_t pq_u4 __attribute__((ext_vector_type(4)));
 // 16 bytes at a 16-byte-aligned LDS address (one ds_read_b128); u32 at a
 // 4-byte-aligned one.
 __device__ __forceinline__ pq_u4 pq_b128(const uint8_t *p) {
@@ -566,12 +544,6 @@ __device__ __forceinline__ void pq_proj(uint8_t *smem, const uint8_t *W0, const 
     PqDma<T, GU> dma;
     dma.init(roff, W0, W1, row_bytes, r0);
     const int nwi = PqDma<T, GU>::n_w();
-    // the lane's rows: byte offset (mod 16) of row (grow0 + 16 t + n)'s start
-    const uint8_t *Wm = mat ? W1 : W0;
-    uint32_t rofs[2];
-#pragma unroll
-    for (int t = 0; t < 2; t++)
-        rofs[t] = (uint32_t)(((uint64_t)((uintptr_t)Wm & 15) + (uint64_t)(grow0 + 16 * t + n) * row_bytes) & 15);
     pf_f32x4 acc[2][2];
 #pragma unroll
     for (int t = 0; t < 2; t++)
@@ -592,9 +564,8 @@ __device__ __forceinline__ void pq_proj(uint8_t *smem, const uint8_t *W0, const 
         const uint8_t *Ws = w_stage(b);
         const uint8_t *blk[2];
 #pragma unroll
-        for (int t = 0; t < 2; t++)
-            blk[t] = Ws + (uint32_t)(rho0 + 16 * t + n) * (PW * 16) +
-                     (PqFmt<T>::ALN ? 0u : ((rofs[t] + (uint32_t)b * BB) & 15u));
+        for (int t = 0; t < 2; t++)   // the block at offset o of its staged row (rows of 4-byte multiples)
+            blk[t] = Ws + (uint32_t)(rho0 + 16 * t + n) * (PW * 16) + (((uint32_t)b * BB) & 3u);
         pq_block<T, MT>(acc, a_stage(b), blk[0], blk[1]);
     }
     // y = s_pair * acc; lane: pairs 16 mt + 4 g + i, rows grow0 + 16 t + n
