@@ -152,7 +152,8 @@ struct PqDma {
     static constexpr int BB = PqFmt<T>::BB, PW = PqFmt<T>::PW, AP = PqFmt<T>::AP, RP = PqFmt<T>::RP;
     static constexpr int NA = (PF_MT * AP + 63) / 64, KA = (NA + 7) / 8;
     static constexpr int NW = PQ_ROWS * PW / 64, KW = (NW + 7) / 8;   // NW: 24, 40, 40
-    uint32_t a[KA];            // record piece offsets at block 0, ~0u for an idle lane
+    static_assert(PF_MT * AP % 64 == 0, "a record stage is whole DMA instructions");
+    uint32_t a[KA];            // record piece offsets at block 0
     uint32_t r[KW], c16[KW];   // row offset from the matrix base; offset of the lane's piece
     __device__ __forceinline__ void init(const uint32_t *roff, const uint8_t *W0, const uint8_t *W1,
                                          uint64_t row_bytes, int64_t r0) {
@@ -160,7 +161,7 @@ struct PqDma {
 #pragma unroll
         for (int k = 0; k < KA; k++) {
             const int q = 64 * (w + 8 * k) + lane, m = q / AP, c = q - m * AP;
-            a[k] = q < PF_MT * AP ? roff[m] + 16u * (uint32_t)(c < RP ? c : 0) : ~0u;
+            a[k] = q < PF_MT * AP ? roff[m] + 16u * (uint32_t)(c < RP ? c : 0) : 0u;
         }
 #pragma unroll
         for (int k = 0; k < KW; k++) {
@@ -182,7 +183,7 @@ struct PqDma {
 #pragma unroll
         for (int k = 0; k < KA; k++) {
             const int jj = w + 8 * k;
-            if (jj < NA && a[k] != ~0u) pf_dma16(pq, a[k] + ab, pf_lds(As + 1024 * jj));
+            if (jj < NA) pf_dma16(pq, a[k] + ab, pf_lds(As + 1024 * jj));
         }
     }
     __device__ __forceinline__ void issue_w(int64_t b, uint8_t *Ws, const uint8_t *W0, const uint8_t *W1) const {
@@ -327,16 +328,16 @@ __device__ __forceinline__ PqQ4 pq_b_q4k(const pq_u4 &wq, int g, uint32_t sc) {
     }
     return r;
 }
-// 6-bit (sc, m) of Q4_K sub-block jj (k4_scale_min over LDS bytes).
-__device__ __forceinline__ void pq_q4k_sm(const uint8_t *blk, int jj, uint32_t &sc, uint32_t &mn) {
-    const uint8_t *s = blk + 4;
+// 6-bit (sc, m) of Q4_K sub-block jj (k4_scale_min) from the block's first
+// 16 bytes p0 (d, dmin, then the 12 scale bytes: dwords 1..3).
+__device__ __forceinline__ void pq_q4k_sm(const pq_u4 &p0, int jj, uint32_t &sc, uint32_t &mn) {
     if (jj < 4) {
-        sc = pq_u8(s + jj) & 63u;
-        mn = pq_u8(s + jj + 4) & 63u;
+        sc = __builtin_amdgcn_ubfe(p0[1], 8u * (uint32_t)jj, 6u);
+        mn = __builtin_amdgcn_ubfe(p0[2], 8u * (uint32_t)jj, 6u);
     } else {
-        const uint32_t c = pq_u8(s + jj + 4);
-        sc = (c & 15u) | ((pq_u8(s + jj - 4) >> 6) << 4);
-        mn = (c >> 4) | ((pq_u8(s + jj) >> 6) << 4);
+        const uint32_t o = 8u * (uint32_t)(jj - 4);
+        sc = __builtin_amdgcn_ubfe(p0[3], o, 4u) | (__builtin_amdgcn_ubfe(p0[1], o + 6u, 2u) << 4);
+        mn = __builtin_amdgcn_ubfe(p0[3], o + 4u, 4u) | (__builtin_amdgcn_ubfe(p0[2], o + 6u, 2u) << 4);
     }
 }
 
@@ -424,12 +425,13 @@ __device__ __forceinline__ void pq_block(pf_f32x4 (&acc)[2][2], const uint8_t *A
         mq_v4i C[2][MT][3][2];
         // step j + 1's window and scale are read after step j's decode,
         // ahead of step j's matrix ops
-        pq_u4 wq[2];
+        pq_u4 wq[2], p0[2];   // p0: the block's first 16 bytes (d, dmin, scales)
         uint32_t sc[2];
 #pragma unroll
         for (int t = 0; t < 2; t++) {
             uint32_t mn;
-            pq_q4k_sm(blk[t], g >> 1, sc[t], mn);
+            p0[t] = pq_b128(blk[t]);
+            pq_q4k_sm(p0[t], g >> 1, sc[t], mn);
             wq[t] = pq_w_q4k(blk[t], 0, g);
         }
 #pragma unroll
@@ -441,7 +443,7 @@ __device__ __forceinline__ void pq_block(pf_f32x4 (&acc)[2][2], const uint8_t *A
 #pragma unroll
                 for (int t = 0; t < 2; t++) {
                     uint32_t mn;
-                    pq_q4k_sm(blk[t], 2 * (j + 1) + (g >> 1), sc[t], mn);
+                    pq_q4k_sm(p0[t], 2 * (j + 1) + (g >> 1), sc[t], mn);
                     wq[t] = pq_w_q4k(blk[t], j + 1, g);
                 }
                 __builtin_amdgcn_sched_barrier(0);   // keep the reads ahead of the matrix ops
@@ -490,8 +492,9 @@ __device__ __forceinline__ void pq_block(pf_f32x4 (&acc)[2][2], const uint8_t *A
                 dmin = pq_h2f(blk[t] + 94);
             } else {
                 uint32_t s0, m0, s1, m1;
-                pq_q4k_sm(blk[t], 2 * g, s0, m0);
-                pq_q4k_sm(blk[t], 2 * g + 1, s1, m1);
+                const pq_u4 p0 = pq_b128(blk[t]);
+                pq_q4k_sm(p0, 2 * g, s0, m0);
+                pq_q4k_sm(p0, 2 * g + 1, s1, m1);
                 bm = pq_bf4((float)m0, (float)m0, (float)m1, (float)m1);
                 dmin = pq_h2f(blk[t] + 2);
             }
