@@ -238,7 +238,7 @@ __device__ __forceinline__ uint32_t pq_u32(const uint8_t *p) { return *(pq_lds_u
 // >> 2 s) & 3, sub-block k / 16 with scale byte (sc lo nibble, m hi nibble).
 // K step j (64 columns), lane group g: h = j >> 1, s = 2 (j & 1) + (g >> 1),
 // g' = g & 1, sub-block 4 j + g. Codes sc * q by v_perm from the table
-// [0, sc, 2 sc, 3 sc] (selector q | 4 picks its byte q). The decoders take
+// [0, sc, 2 sc, 3 sc] (selector q picks its byte q). The decoders take
 // their LDS bytes as arguments: the block loop reads a K step's window
 // ahead of the matrix ops of the step before (pq_block). The staged block
 // is 16-byte aligned: a window is one 16-byte read.
@@ -256,8 +256,8 @@ __device__ __forceinline__ mq_v4i pq_b_q2k(const pq_u4 &sc4, const pq_u4 &wq, in
     mq_v4i r;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        const uint32_t u = ((wq[i] >> sh) & 0x03030303u) | 0x04040404u;
-        r[i] = (int32_t)__builtin_amdgcn_perm(tab, 0u, u);
+        // selectors 0..3 pick bytes of the second operand, the table
+        r[i] = (int32_t)__builtin_amdgcn_perm(0u, tab, (wq[i] >> sh) & 0x03030303u);
     }
     return r;
 }
