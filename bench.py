@@ -169,11 +169,10 @@ class Bench:
 
     def kernel_used(self, step, n, candidates):
         """(name, average ms) of the candidate kernel that the steps launch."""
-        self.kernel_ms(step, n, [])
+        st = self.kernel_stats(step, n, candidates, strict=False)
         for k in candidates:
-            cnt, tot = ctypes.c_int64(), ctypes.c_double()
-            if self.L.sepia_hip_profile_query(k.encode(), ctypes.byref(cnt), ctypes.byref(tot)) and cnt.value:
-                return k, tot.value / cnt.value
+            if st[k][0]:
+                return k, st[k][1]
         raise RuntimeError("none of %s ran" % candidates)
 
     def kernel_ms(self, step, n, kernels):
@@ -181,32 +180,42 @@ class Bench:
         (kernels that did not run are left out)."""
         return {k: ms for k, (cnt, ms) in self.kernel_stats(step, n, kernels).items() if cnt}
 
-    def kernel_stats(self, step, n, kernels):
-        """(launches, average ms per launch) of each named kernel over n eager steps."""
+    def kernel_stats(self, step, n, kernels, chunks=4, strict=True):
+        """(launches, average ms per launch) of each named kernel over n eager steps:
+        the median over `chunks` consecutive runs of about n / chunks steps of each
+        run's average, so that one stray slow launch does not move the figure.
+        strict False: names the library does not know count as not launched."""
         dev = self.dev
-        self.L.sepia_hip_profile_reset()
-        dev.begin()
-        dev.check(self.L.sepia_hip_profile_start(), "profile_start")
-        for i in range(n):
-            dev.check(step(i), "profiled step")
-        dev.check(self.L.sepia_hip_profile_stop(), "profile_stop")
-        dev.end()
-        out = {}
-        for k in kernels:
-            cnt, tot = ctypes.c_int64(), ctypes.c_double()
-            dev.check(self.L.sepia_hip_profile_query(k.encode(), ctypes.byref(cnt), ctypes.byref(tot)), "query")
-            out[k] = (cnt.value, tot.value / max(cnt.value, 1))
-        return out
+        per = max(1, n // chunks)
+        runs = {k: [] for k in kernels}
+        cnts = {k: 0 for k in kernels}
+        for c in range(chunks if n >= chunks else 1):
+            self.L.sepia_hip_profile_reset()
+            dev.begin()
+            dev.check(self.L.sepia_hip_profile_start(), "profile_start")
+            for i in range(c * per, (c + 1) * per if n >= chunks else n):
+                dev.check(step(i), "profiled step")
+            dev.check(self.L.sepia_hip_profile_stop(), "profile_stop")
+            dev.end()
+            for k in kernels:
+                cnt, tot = ctypes.c_int64(), ctypes.c_double()
+                ok = self.L.sepia_hip_profile_query(k.encode(), ctypes.byref(cnt), ctypes.byref(tot))
+                if strict:
+                    dev.check(ok, "query")
+                if ok and cnt.value:
+                    runs[k].append(tot.value / cnt.value)
+                    cnts[k] += cnt.value
+        return {k: (cnts[k], float(np.median(runs[k])) if runs[k] else 0.0) for k in kernels}
 
 
 # HBM bytes per launch, measured with rocprofv3's FETCH_SIZE and WRITE_SIZE counters (each in its
 # own run) and scaled by what the same counters read for the copy kernel of known size
 # (profiles/*_hbm_traffic.md). Reported as roofline.traffic for the dominant kernel; None until
 # measured for the current build.
-MEASURED_TRAFFIC_C2 = {"sepia_mq_gateup": 12992283, "sepia_mq_down": 8618077}
-MEASURED_TRAFFIC_C3 = {"sepia_moe_route": 6612157, "sepia_mq_gateup": 122222317, "sepia_mq_down": 72136272}
-MEASURED_TRAFFIC_REAL = {"sepia_moe_route": 6612334, "sepia_mq_gateup": 124624225, "sepia_mq_down": 76621615}
-MEASURED_TRAFFIC_C5 = {"sepia_pf_gateup_q": 2991420485, "sepia_pf_down_q": 1900821931}
+MEASURED_TRAFFIC_C2 = {"sepia_mq_gateup": 13008357, "sepia_mq_down": 8602116}
+MEASURED_TRAFFIC_C3 = {"sepia_moe_route": 6612701, "sepia_mq_gateup": 122249583, "sepia_mq_down": 72224654}
+MEASURED_TRAFFIC_REAL = {"sepia_moe_route": 6612603, "sepia_mq_gateup": 118554841, "sepia_mq_down": 76587903}
+MEASURED_TRAFFIC_C5 = {"sepia_pf_gateup_q": 3011933356, "sepia_pf_down_q": 1899945919}
 
 
 def cpu_sample(fn, min_seconds, max_calls):
