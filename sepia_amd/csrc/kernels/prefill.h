@@ -78,24 +78,29 @@ extern "C" __global__ __launch_bounds__(256) void sepia_pf_route(const float *__
         }
 }
 
-// The same logits on the f32 matrix cores: one wave per 16-token x 16-row
-// tile (grid: T / 16 x n_tot / 16 waves), K in steps of 16 columns. Lane l
+// The same logits on the f32 matrix cores: one workgroup of four waves per
+// 16-token x 16-row tile (grid: T / 16 x n_tot / 16), wave w taking the
+// columns [w H / 4, (w + 1) H / 4) in steps of 16 (so 544 tiles of C5 keep
+// every SIMD busy, with a quarter of the dependent MFMA chain each). Lane l
 // loads columns 4 (l >> 4) .. + 3 of the step for token / row l & 15 as one
 // float4; MFMA i of the step takes component i, so the four MFMAs cover the
-// step's 16 columns once each (f32 products, f32 sums; only the summation
-// order differs from sepia_pf_route). Needs x, rw and ld 16-byte aligned and
-// H a multiple of 128 (the host checks).
+// step's 16 columns once each. The four quarter sums are added in LDS in
+// wave order (f32 products, f32 sums; only the summation order differs
+// from sepia_pf_route). Needs x, rw and ld 16-byte aligned and H a multiple
+// of 512 (the host checks).
 typedef float pf_f32x4v __attribute__((ext_vector_type(4)));
-extern "C" __global__ __launch_bounds__(64) void sepia_pf_route_m(const float *__restrict__ x, int64_t T,
-                                                                  const float *__restrict__ rw, int64_t ld,
-                                                                  int64_t n_tot, int64_t H, float *__restrict__ logits) {
-    const int l = threadIdx.x & 63, r = l & 15, g = l >> 4;
+extern "C" __global__ __launch_bounds__(256) void sepia_pf_route_m(const float *__restrict__ x, int64_t T,
+                                                                   const float *__restrict__ rw, int64_t ld,
+                                                                   int64_t n_tot, int64_t H, float *__restrict__ logits) {
+    __shared__ pf_f32x4 part[3][64];
+    const int w = threadIdx.x >> 6, l = threadIdx.x & 63, r = l & 15, g = l >> 4;
     const int64_t t0 = (int64_t)blockIdx.x * 16, r0 = (int64_t)blockIdx.y * 16;
     const int64_t t = t0 + r < T ? t0 + r : T - 1, rr = r0 + r < n_tot ? r0 + r : n_tot - 1;
-    const pf_f32x4v *xa = (const pf_f32x4v *)(x + t * H) + g, *wa = (const pf_f32x4v *)(rw + rr * ld) + g;
+    const int64_t c0 = (int64_t)w * (H / 4);
+    const pf_f32x4v *xa = (const pf_f32x4v *)(x + t * H + c0) + g, *wa = (const pf_f32x4v *)(rw + rr * ld + c0) + g;
     pf_f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
     // eight steps in registers while the next eight load (n a multiple of 8)
-    const int64_t n = H / 16;
+    const int64_t n = H / 64;
     pf_f32x4v a[8], b[8];
 #pragma unroll
     for (int u = 0; u < 8; u++) {
@@ -125,7 +130,16 @@ extern "C" __global__ __launch_bounds__(64) void sepia_pf_route_m(const float *_
             }
         }
     }
-    // acc[i]: token t0 + 4 g + i, row r0 + r
+    // acc[i]: token t0 + 4 g + i, row r0 + r; quarters 1..3 to LDS, added to quarter 0 in order
+    if (w > 0) part[w - 1][l] = acc;
+    __syncthreads();
+    if (w > 0) return;
+#pragma unroll
+    for (int q = 0; q < 3; q++) {
+        const pf_f32x4 v = part[q][l];
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[i] += v[i];
+    }
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const int64_t tt = t0 + 4 * g + i, ro = r0 + r;

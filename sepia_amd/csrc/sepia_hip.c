@@ -159,7 +159,8 @@ static int g_mq_kind = 0;          /* the launch kind mq_geo is planning: 1 matv
 static int g_opt_mq_x = 0;   /* "mq_x": 0 = planner's choice, 1 = vector from global, 2 = vector by LDS DMA,
                               * 3 = converter waves */
 static int g_opt_pf_route_m = 1;   /* "pf_route_m": 1 = prefill router logits on the f32 matrix cores
-                                    * (sepia_pf_route_m) when x and the router rows are 16-byte aligned,
+                                    * (sepia_pf_route_m) when x and the router rows are 16-byte aligned
+                                    * and hidden is a multiple of 512,
                                     * 0 = sepia_pf_route */
 static int g_opt_pf_q = 1;   /* "pf_q": 1 = a prefill layer whose six projections are all Q2_K, Q3_K or Q4_K
                               * runs them on the int8 matrix cores (sepia_pf_quant, sepia_pf_gateup_q,
@@ -1858,8 +1859,8 @@ int sepia_gpu_moe_prefill(const SepiaMoeLayerDesc *L, int64_t n_tokens, SepiaGpu
     float rs = L->route_scale, gsc = L->global_scale;
     int32_t nr32 = nr, ns32 = ns, tk32 = tk, nsel32 = n_sel;
     void *a_rt[] = { &x->dev, &tt, &rw, &ld, &ntot, &hid, &logits };
-    const int rt_m = g_opt_pf_route_m && ((((uintptr_t)x->dev | (uintptr_t)rw) & 15) == 0) && (ld % 4) == 0 && H % 128 == 0;
-    if (rt_m ? !launch2(K_PF_ROUTE_M, (unsigned)((T + 15) / 16), (unsigned)((n_tot + 15) / 16), 64, 0, a_rt, op)
+    const int rt_m = g_opt_pf_route_m && ((((uintptr_t)x->dev | (uintptr_t)rw) & 15) == 0) && (ld % 4) == 0 && H % 512 == 0;
+    if (rt_m ? !launch2(K_PF_ROUTE_M, (unsigned)((T + 15) / 16), (unsigned)((n_tot + 15) / 16), 256, 0, a_rt, op)
              : !launch2(K_PF_ROUTE, (unsigned)((T + 31) / 32), (unsigned)((n_tot + 31) / 32), 256, 0, a_rt, op))
         return 0;
     void *a_sel[] = { &logits, &rb, &nr32, &ns32, &tk32, &rs, &gsc, &sel_idx, &sel_w };
