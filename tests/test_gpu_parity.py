@@ -899,6 +899,35 @@ def test_moe_prefill(dev, orc, shape, types, T, x_kind, path):
         dev.free(b)
 
 
+@pytest.mark.parametrize("off", [0, 2])
+def test_moe_prefill_row_alignment(dev, orc, off):
+    """The int8 prefill path stages weight blocks from 4-byte boundaries, so
+    the host takes it only when every projection's base, expert stride and
+    row bytes are multiples of 4. A Q2_K/Q3_K/Q4_K layer whose routed gate
+    starts 2 bytes into its buffer runs on the bf16 kernels instead (launch
+    counts asserted); both match the oracle."""
+    rng = np.random.default_rng(97 + off)
+    desc, spec, bufs = make_layer(dev, rng, hidden=2048, inter=1024, n_routed=8, n_shared=1,
+                                  tg=10, tu=10, td=11, ts=12)
+    g = np.concatenate(spec["gate"])
+    bufs["gate_off"] = dev.alloc(g.nbytes + off)
+    dev.upload(bufs["gate_off"], g, offset=off)
+    desc.gate = hip.ExpertTensor(bufs["gate_off"], off, spec["gate"][0].nbytes, 10)
+    X = bf16_normal(rng, (12, 2048))
+    with Launches(dev) as ln:
+        y, idx, w = run_prefill(dev, desc, X)
+    q = ln.count("sepia_pf_gateup_q")
+    assert (q > 0) == (off == 0) and (ln.count("sepia_pf_gateup") > 0) == (off != 0), (off, q)
+    for t in range(X.shape[0]):
+        y_ref, logits, idx_ref, w_ref = orc.moe_layer(spec, X[t], threads=THREADS)
+        chosen = check_route(orc, spec, logits, idx[t], w[t])
+        if chosen != list(idx_ref):
+            y_ref, _, _, _ = orc.moe_layer(spec, X[t], force_idx=chosen, threads=THREADS)
+        assert_close(y[t], y_ref, what="prefill rows at offset %d, token %d" % (off, t), gate=False)
+    for b in bufs.values():
+        dev.free(b)
+
+
 def test_moe_prefill_matches_decode(dev, orc):
     """A prefill batch and token-by-token decode of the same layer agree to the
     layer bar. Their routers sum the logits in different orders, so a token
