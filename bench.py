@@ -317,7 +317,8 @@ def run_matvec_rotation(B, name, t, rows, cols, warmup, steps, cpu_seconds, seed
 
     ms = B.timed_steps(step, warmup, steps)
     tname = {10: "q2_k", 11: "q3_k", 12: "q4_k", 17: "iq2_xs", 18: "iq3_xxs", 16: "iq2_xxs"}[t]
-    cands = ["sepia_mq_mv_%s" % tname, "sepia_mv_%s" % tname, "sepia_matvec_generic_%s" % tname]
+    cands = ["sepia_mq_mv_%s" % tname] + (["sepia_mv_%s" % tname] if t in (10, 11, 12) else []) + \
+        ["sepia_matvec_generic_%s" % tname]   # the tile kernels exist for Q2_K, Q3_K, Q4_K
     kname, kms = B.kernel_used(step, min(steps, 2 * ncopy), cands)
     nbytes = mb + cols * 4 + rows * 4
     import oracle
