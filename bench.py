@@ -212,10 +212,10 @@ class Bench:
 # own run) and scaled by what the same counters read for the copy kernel of known size
 # (profiles/*_hbm_traffic.md). Reported as roofline.traffic for the dominant kernel; None until
 # measured for the current build.
-MEASURED_TRAFFIC_C2 = {"sepia_mq_gateup": 13008357, "sepia_mq_down": 8602116}
-MEASURED_TRAFFIC_C3 = {"sepia_moe_route": 6612701, "sepia_mq_gateup": 122249583, "sepia_mq_down": 72224654}
-MEASURED_TRAFFIC_REAL = {"sepia_moe_route": 6612603, "sepia_mq_gateup": 118554841, "sepia_mq_down": 76587903}
-MEASURED_TRAFFIC_C5 = {"sepia_pf_gateup_q": 3011933356, "sepia_pf_down_q": 1899945919}
+MEASURED_TRAFFIC_C2 = {"sepia_mq_gateup": 13001871, "sepia_mq_down": 8582520}
+MEASURED_TRAFFIC_C3 = {"sepia_moe_route": 6612357, "sepia_mq_gateup": 122283851, "sepia_mq_down": 72124327}
+MEASURED_TRAFFIC_REAL = {"sepia_moe_route": 6612386, "sepia_mq_gateup": 118571552, "sepia_mq_down": 76561443}
+MEASURED_TRAFFIC_C5 = {"sepia_pf_gateup_q": 3011257196, "sepia_pf_down_q": 1899666537}
 
 
 def cpu_sample(fn, min_seconds, max_calls):
