@@ -151,7 +151,10 @@ template <int T, bool GU>
 struct PqDma {
     static constexpr int BB = PqFmt<T>::BB, PW = PqFmt<T>::PW, AP = PqFmt<T>::AP, RP = PqFmt<T>::RP;
     static constexpr int NA = (PF_MT * AP + 63) / 64, KA = (NA + 7) / 8;
-    static constexpr int NW = PQ_ROWS * PW / 64, KW = (NW + 7) / 8;   // NW: 24, 40, 40
+    static constexpr int NW = PQ_ROWS * PW / 64, KW = NW / 8;   // NW: 24, 40, 40
+    // wave w issues weight instructions KW w .. KW w + KW - 1: exactly the
+    // stage rows 32 w .. 32 w + 31 it decodes, so no other wave reads them
+    static_assert(NW % 8 == 0 && 64 * KW == 32 * PW, "a wave stages its own 32 rows");
     static_assert(PF_MT * AP % 64 == 0, "a record stage is whole DMA instructions");
     uint32_t a[KA];            // record piece offsets at block 0
     uint32_t r[KW], c16[KW];   // row offset from the matrix base; offset of the lane's piece
@@ -165,7 +168,7 @@ struct PqDma {
         }
 #pragma unroll
         for (int k = 0; k < KW; k++) {
-            const int jj = w + 8 * k;
+            const int jj = KW * w + k;
             const int mat = GU ? jj / (NW / 2) : 0, j1 = GU ? jj - mat * (NW / 2) : jj;
             const int q = 64 * j1 + lane, kr = q / PW, c = q - kr * PW;
             r[k] = (uint32_t)((uint64_t)(r0 + kr) * row_bytes);
@@ -173,10 +176,7 @@ struct PqDma {
         }
     }
     // this wave's weight instructions per block
-    static __device__ __forceinline__ int n_w() {
-        const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-        return w < NW ? (NW - w + 7) / 8 : 0;
-    }
+    static __device__ __forceinline__ int n_w() { return KW; }
     __device__ __forceinline__ void issue_a(int64_t b, uint8_t *As, const uint8_t *pq) const {
         const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
         const uint32_t ab = (uint32_t)b * PQ_REC;
@@ -191,8 +191,8 @@ struct PqDma {
         const uint32_t wb = (uint32_t)b * BB;
 #pragma unroll
         for (int k = 0; k < KW; k++) {
-            const int jj = w + 8 * k;
-            if (jj < NW) pf_dma16((GU && jj >= NW / 2) ? W1 : W0, ((r[k] + wb) & ~3u) + c16[k], pf_lds(Ws + 1024 * jj));
+            const int jj = KW * w + k;
+            pf_dma16((GU && jj >= NW / 2) ? W1 : W0, ((r[k] + wb) & ~3u) + c16[k], pf_lds(Ws + 1024 * jj));
         }
     }
 };
@@ -354,9 +354,44 @@ __device__ __forceinline__ float pq_comb(int32_t c0, int32_t c1, int32_t c2) {
     return __builtin_fmaf((float)c0, 65536.0f, (float)(int32_t)(((uint32_t)c1 << 8) + (uint32_t)c2));
 }
 
+// A block's first LDS reads of the lane's two weight rows (scales and the
+// first K steps' windows): the wave staged those rows itself, so pq_proj
+// issues them before the block's barrier.
+struct PqHead {
+    pq_u4 a[2], b[2];         // Q2_K: scale bytes, window 0; Q4_K: first 16 bytes, window 0
+    PqWin wq[2], wh[2];       // Q3_K: window 0, hmask window
+    uint32_t sb[2][2], hb[2];   // Q3_K scale bytes 96 + g, 100 + g and hmask bits byte 104 + g
+    uint32_t sc[2];           // Q4_K: 6-bit scale of sub-block g >> 1
+};
+template <int T>
+__device__ __forceinline__ PqHead pq_head(const uint8_t *blk0, const uint8_t *blk1) {
+    const int g = (threadIdx.x & 63) >> 4;
+    const uint8_t *blk[2] = {blk0, blk1};
+    PqHead h;
+#pragma unroll
+    for (int t = 0; t < 2; t++) {
+        if constexpr (T == ST_Q2_K) {
+            h.a[t] = pq_b128(blk[t]);
+            h.b[t] = pq_w_q2k(blk[t], 0, g);
+        } else if constexpr (T == ST_Q3_K) {
+            h.sb[t][0] = pq_u8(blk[t] + 96 + g);
+            h.sb[t][1] = pq_u8(blk[t] + 100 + g);
+            h.hb[t] = pq_u8(blk[t] + 104 + g);
+            h.wh[t] = pq_win(blk[t] + 16 * (g & 1));
+            h.wq[t] = pq_w_q3k(blk[t], 0, g);
+        } else {
+            uint32_t mn;
+            h.a[t] = pq_b128(blk[t]);
+            pq_q4k_sm(h.a[t], g >> 1, h.sc[t], mn);
+            h.b[t] = pq_w_q4k(blk[t], 0, g);
+        }
+    }
+    return h;
+}
+
 template <int T, int MT>
 __device__ __forceinline__ void pq_block(pf_f32x4 (&acc)[2][2], const uint8_t *As, const uint8_t *blk0,
-                                         const uint8_t *blk1) {
+                                         const uint8_t *blk1, const PqHead &hd) {
     const int l = threadIdx.x & 63, n = l & 15, g = l >> 4;
     const uint8_t *blk[2] = {blk0, blk1};
     // A fragment of plane p, M tile mt, columns c0 .. (lane: pair 16 mt + n, 16 or 8 bytes at group g)
@@ -364,24 +399,21 @@ __device__ __forceinline__ void pq_block(pf_f32x4 (&acc)[2][2], const uint8_t *A
     auto a_at = [&](int mt, int p, int col) { return As + (16 * mt + n) * APB + 256 * p + col; };
     if constexpr (T == ST_Q2_K || T == ST_Q3_K) {
         mq_v4i C[2][MT][3];
-        // the block's scale bytes and first window up front; a window serves
-        // two K steps, and the second is read after step 1's decode, ahead of
-        // step 1's matrix ops
+        // the block's scale bytes and first window come in the head; a
+        // window serves two K steps, and the second is read after step 1's
+        // decode, ahead of step 1's matrix ops
         uint32_t sb[2][2], hb[2];
         pq_u4 sc4[2], w2[2];
         PqWin wq[2], wh[2];
 #pragma unroll
         for (int t = 0; t < 2; t++) {
-            if constexpr (T == ST_Q2_K) {
-                sc4[t] = pq_b128(blk[t]);
-                w2[t] = pq_w_q2k(blk[t], 0, g);
-            } else {
-                sb[t][0] = pq_u8(blk[t] + 96 + g);
-                sb[t][1] = pq_u8(blk[t] + 100 + g);
-                hb[t] = pq_u8(blk[t] + 104 + g);
-                wh[t] = pq_win(blk[t] + 16 * (g & 1));
-                wq[t] = pq_w_q3k(blk[t], 0, g);
-            }
+            sc4[t] = hd.a[t];
+            w2[t] = hd.b[t];
+            sb[t][0] = hd.sb[t][0];
+            sb[t][1] = hd.sb[t][1];
+            hb[t] = hd.hb[t];
+            wh[t] = hd.wh[t];
+            wq[t] = hd.wq[t];
         }
 #pragma unroll
         for (int j = 0; j < 4; j++) {
@@ -429,10 +461,9 @@ __device__ __forceinline__ void pq_block(pf_f32x4 (&acc)[2][2], const uint8_t *A
         uint32_t sc[2];
 #pragma unroll
         for (int t = 0; t < 2; t++) {
-            uint32_t mn;
-            p0[t] = pq_b128(blk[t]);
-            pq_q4k_sm(p0[t], g >> 1, sc[t], mn);
-            wq[t] = pq_w_q4k(blk[t], 0, g);
+            p0[t] = hd.a[t];
+            sc[t] = hd.sc[t];
+            wq[t] = hd.b[t];
         }
 #pragma unroll
         for (int j = 0; j < 4; j++) {
@@ -561,15 +592,23 @@ __device__ __forceinline__ void pq_proj(uint8_t *smem, const uint8_t *W0, const 
         // everything up to A_b and W_b; the weights of blocks b + 1 .. b + SW - 2 may fly
         const int ahead = (nbi - 1 - b) < (SW - 2) ? (nbi - 1 - b) : (SW - 2);
         pq_wait_vm<PqDma<T, GU>::KW * (SW - 2)>(nwi * ahead);
-        __syncthreads();   // block b staged by every wave; block b - 1's readers are done
-        if (b + 1 < nbi) dma.issue_a(b + 1, a_stage(b + 1), pq);
-        if (b + SW - 1 < nbi) dma.issue_w(b + SW - 1, w_stage(b + SW - 1), W0, W1);
         const uint8_t *Ws = w_stage(b);
         const uint8_t *blk[2];
 #pragma unroll
         for (int t = 0; t < 2; t++)   // the block at offset o of its staged row (rows of 4-byte multiples)
             blk[t] = Ws + (uint32_t)(rho0 + 16 * t + n) * (PW * 16) + (((uint32_t)b * BB) & 3u);
-        pq_block<T, MT>(acc, a_stage(b), blk[0], blk[1]);
+        // this wave's own weight rows have landed: their first reads go out
+        // before the barrier, which then covers only the records (A_b staged
+        // by every wave; block b - 1's reads of the stage A_(b+1) refills are
+        // all used, so complete). The asm statements keep the compiler from
+        // moving memory accesses across the bare barrier.
+        const PqHead hd = pq_head<T>(blk[0], blk[1]);
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        if (b + 1 < nbi) dma.issue_a(b + 1, a_stage(b + 1), pq);
+        if (b + SW - 1 < nbi) dma.issue_w(b + SW - 1, w_stage(b + SW - 1), W0, W1);
+        pq_block<T, MT>(acc, a_stage(b), blk[0], blk[1], hd);
     }
     // y = s_pair * acc; lane: pairs 16 mt + 4 g + i, rows grow0 + 16 t + n
 #pragma unroll
