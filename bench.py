@@ -215,7 +215,7 @@ class Bench:
 MEASURED_TRAFFIC_C2 = {"sepia_mq_gateup": 13001871, "sepia_mq_down": 8582520}
 MEASURED_TRAFFIC_C3 = {"sepia_moe_route": 6612357, "sepia_mq_gateup": 122283851, "sepia_mq_down": 72124327}
 MEASURED_TRAFFIC_REAL = {"sepia_moe_route": 6612386, "sepia_mq_gateup": 118571552, "sepia_mq_down": 76561443}
-MEASURED_TRAFFIC_C5 = {"sepia_pf_gateup_q": 3011257196, "sepia_pf_down_q": 1899666537}
+MEASURED_TRAFFIC_C5 = {"sepia_pf_gateup_q": 2999146132, "sepia_pf_down_q": 1900014470}
 
 
 def cpu_sample(fn, min_seconds, max_calls):
