@@ -221,19 +221,23 @@ enum { BUF_SHARED = 0, BUF_PRIVATE = 1, BUF_WRAPPED = 2 };
 /* Shared buffers keep a pinned host copy beside the device allocation. The
  * host may write the copy only through a pointer from sepia_gpu_host_ptr,
  * so that call marks every chunk (SHADOW_CHUNK bytes) of the buffer
- * host-dirty; an op uploads the dirty chunks of the byte range it reads
- * right before it is queued and marks them clean, and a buffer a kernel
- * writes is downloaded whole at sepia_gpu_end. A slab the host fills once is
- * therefore uploaded once, however many batches read it, and a host write
- * that lands after an earlier op of the batch read other chunks still
- * reaches the op that reads it. */
-#define SHADOW_CHUNK ((size_t)1 << 20)
+ * host-dirty. An op uploads, right before it is queued, the dirty parts of
+ * exactly the byte range it reads, and marks clean only the chunks that
+ * range covers whole: the host may still be writing the rest of a chunk it
+ * covers in part (the reference's loader threads fill one expert slot of a
+ * slab while ops read another slot of the same slab, src/sepia.c:3249-3290),
+ * so such a chunk stays dirty until an op that reads it whole uploads it. A
+ * buffer a kernel writes is downloaded whole at sepia_gpu_end. A slab the
+ * host fills once is therefore uploaded once, however many batches read it,
+ * and a host write that lands after an earlier op of the batch read other
+ * bytes still reaches the op that reads it. */
+#define SHADOW_CHUNK ((size_t)1 << 16)
 struct SepiaGpuBuf {
     uint8_t *dev;
     void *host;        /* pinned copy (shared), caller's base (wrapped), NULL (private) */
     size_t len;
     int kind;
-    int host_dirty;    /* some chunk of the host copy is newer than the device copy */
+    size_t ndirty;     /* chunks of the host copy that may be newer than the device copy */
     uint64_t *dirty;   /* per-chunk host-dirty bits (shared buffers) */
     size_t nchunks;
     int dev_newer;     /* download at sepia_gpu_end */
@@ -302,33 +306,39 @@ static int chk(const SepiaGpuBuf *b, size_t off, size_t n, const char *op, const
 static uint64_t g_uploaded;
 
 /* Bring [off, off + n) of the device copy up to date before a kernel reads
- * it: upload its host-dirty chunks, coalesced into runs, and mark them clean. */
+ * it: upload the parts of that range that lie in host-dirty chunks,
+ * coalesced into runs, and mark clean the dirty chunks it covers whole. */
+static int dirty_bit(const SepiaGpuBuf *b, size_t c) { return (int)((b->dirty[c >> 6] >> (c & 63)) & 1u); }
 static int sync_in_range(SepiaGpuBuf *b, size_t off, size_t n, const char *op) {
-    if (b->kind != BUF_SHARED || !b->host_dirty || n == 0) return 1;
+    if (b->kind != BUF_SHARED || b->ndirty == 0 || n == 0) return 1;
     if (off >= b->len) return 1;
     if (n > b->len - off) n = b->len - off;
-    const size_t c0 = off / SHADOW_CHUNK, c1 = (off + n - 1) / SHADOW_CHUNK;
+    const size_t end = off + n;
+    const size_t c0 = off / SHADOW_CHUNK, c1 = (end - 1) / SHADOW_CHUNK;
     size_t c = c0;
     while (c <= c1) {
-        if (!((b->dirty[c >> 6] >> (c & 63)) & 1u)) {
+        if (!dirty_bit(b, c)) {
             c++;
             continue;
         }
         size_t e = c;
-        while (e + 1 <= c1 && ((b->dirty[(e + 1) >> 6] >> ((e + 1) & 63)) & 1u)) e++;
-        const size_t lo = c * SHADOW_CHUNK, hi = (e + 1) * SHADOW_CHUNK < b->len ? (e + 1) * SHADOW_CHUNK : b->len;
+        while (e + 1 <= c1 && dirty_bit(b, e + 1)) e++;
+        const size_t lo = c * SHADOW_CHUNK > off ? c * SHADOW_CHUNK : off;
+        const size_t hi = (e + 1) * SHADOW_CHUNK < end ? (e + 1) * SHADOW_CHUNK : end;
         hipError_t err = hipMemcpyAsync(b->dev + lo, (uint8_t *)b->host + lo, hi - lo, hipMemcpyHostToDevice, g_stream);
         if (err != hipSuccess) {
             LOG("%s: upload failed: %s", op, hipGetErrorString(err));
             return 0;
         }
         g_uploaded += hi - lo;
-        for (size_t k = c; k <= e; k++) b->dirty[k >> 6] &= ~((uint64_t)1 << (k & 63));
+        for (size_t k = c; k <= e; k++) {
+            const size_t klo = k * SHADOW_CHUNK, khi = klo + SHADOW_CHUNK < b->len ? klo + SHADOW_CHUNK : b->len;
+            if (klo < off || khi > end) continue;   /* covered in part: the rest may still change */
+            b->dirty[k >> 6] &= ~((uint64_t)1 << (k & 63));
+            b->ndirty--;
+        }
         c = e + 1;
     }
-    int any = 0;
-    for (size_t k = 0; k < (b->nchunks + 63) / 64 && !any; k++) any = b->dirty[k] != 0;
-    b->host_dirty = any;
     return 1;
 }
 static int sync_in(SepiaGpuBuf *b, const char *op) { return sync_in_range(b, 0, b->len, op); }
@@ -494,7 +504,7 @@ void *sepia_gpu_host_ptr(SepiaGpuBuf *b) {
         /* the caller may write anywhere in the copy from now on */
         memset(b->dirty, 0xFF, ((b->nchunks + 63) / 64) * sizeof(uint64_t));
         if (b->nchunks % 64) b->dirty[b->nchunks / 64] = ((uint64_t)1 << (b->nchunks % 64)) - 1;
-        b->host_dirty = 1;
+        b->ndirty = b->nchunks;
     }
     return b->host;
 }

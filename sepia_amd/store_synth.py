@@ -258,3 +258,120 @@ def write_layer_store(out_dir, rng, layer, hidden, inter, n_routed, n_shared, ty
         store.add_part("SYNTH/synth-%05d-of-%05d.gguf" % (p + 1, n_parts), parts[p])
     index_path, bin_path, manifest_path = store.write()
     return {"index": index_path, "bin": bin_path, "manifest": manifest_path, "store": store}, host
+
+
+# -------------------------------------------------------------- tiny model --
+def tiny_config(n_layers=4, hidden=512, vocab=272, unpadded=266):
+    """A small model config in the reference's config.json layout
+    (docs/inkling-config.json; read by src/sepia.c:455-560): sliding and
+    global attention layers of different head geometries, one dense FFN
+    layer then MoE layers, top-6 of 16 routed experts plus 2 shared. The
+    log-scaling floor is low enough that the attention temperature tau
+    changes within a short prompt."""
+    layer_types = ["hybrid_sliding" if (i % 3) != 2 else "hybrid" for i in range(n_layers)]
+    return {"architectures": ["InklingForConditionalGeneration"], "model_type": "inkling_mm_model",
+            "text_config": {
+                "hidden_size": hidden, "num_hidden_layers": n_layers, "vocab_size": vocab,
+                "unpadded_vocab_size": unpadded,
+                "num_attention_heads": 4, "num_key_value_heads": 2, "head_dim": 64,
+                "swa_num_attention_heads": 4, "swa_num_key_value_heads": 4, "swa_head_dim": 32,
+                "sliding_window_size": 8, "layer_types": layer_types,
+                "mlp_layer_types": ["dense"] + ["sparse"] * (n_layers - 1),
+                "d_rel": 16, "rel_extent": 32, "conv_kernel_size": 4,
+                "intermediate_size": 512, "moe_intermediate_size": 256,
+                "n_routed_experts": 16, "num_experts_per_tok": 6, "n_shared_experts": 2,
+                "route_scale": 8.0, "logits_mup_width_multiplier": 24.0, "rms_norm_eps": 1e-6,
+                "log_scaling_alpha": 0.1, "log_scaling_n_floor": 4}}
+
+
+# The real checkpoint's per-layer expert formats (reference
+# docs/gguf-inventory-ud-q2_k_xl.md:72-111, :214-235): routed gate/up IQ2_XS
+# with IQ3_XXS or IQ4_XS down, shared gate/up Q5_K with Q6_K down; the
+# attention projections Q8_0, token_embd Q5_K and output Q4_K.
+TINY_EXPERT_TYPES = ((17, 18, 13, 14), (17, 23, 13, 14), (18, 18, 13, 14))
+
+
+def _f32(name, dims, arr):
+    return (name, list(dims), 0, np.asarray(arr, dtype=np.float32).tobytes())
+
+
+def _q(name, t, in_dim, out_dim, rng, stack=None):
+    n = 1 if stack is None else stack
+    data = b"".join(synth.random_matrix(t, out_dim, in_dim, rng).tobytes() for _ in range(n))
+    dims = [in_dim, out_dim] + ([] if stack is None else [stack])
+    return (name, dims, t, data)
+
+
+def write_tiny_model(out_dir, rng, tokenizer_src, n_layers=4, n_parts=2):
+    """A complete model in the reference's real-checkpoint formats, small
+    enough to build in seconds: config.json, tokenizer.bin (copied from
+    tokenizer_src, an SPTK v1 sidecar), GGUF parts under inkling-gguf/, the
+    sepia-index sidecar (index.json) and resident.bin + its manifest. Every
+    tensor real_load resolves (reference src/sepia.c:2647-2861) is present:
+    token_embd / output / their norms, per layer the attention norms,
+    projections, relative-position projection and short-conv weights, the
+    dense FFN of layer 0, and for each MoE layer the router, its bias, the
+    global scale and the shared-expert stacks, with the routed experts as
+    3-D GGUF tensors reached through the index. Block contents are random
+    (f16 scales in [2^-10, 2^-6]); f32 norms ~ 1 + N(0, 0.1), short-conv taps
+    and relative projections ~ N(0, 0.3). Returns the four paths the
+    reference reads through SEPIA_REAL_{CONFIG,MANIFEST,INDEX,TOKENIZER}_PATH."""
+    cfg = tiny_config(n_layers)
+    tc = cfg["text_config"]
+    H, V = tc["hidden_size"], tc["vocab_size"]
+    K, d_rel, inter = tc["conv_kernel_size"], tc["d_rel"], tc["moe_intermediate_size"]
+    n_r, n_s = tc["n_routed_experts"], tc["n_shared_experts"]
+    norm = lambda n: 1.0 + 0.1 * rng.standard_normal(n)
+    small = lambda n: 0.3 * rng.standard_normal(n)
+    store = Store(out_dir, n_r)
+    parts = [[] for _ in range(n_parts)]
+    parts[0] += [_q("token_embd.weight", 13, H, V, rng), _q("output.weight", 12, H, V, rng),
+                 _f32("token_embd_norm.weight", [H], norm(H)), _f32("output_norm.weight", [H], norm(H))]
+    for L in range(n_layers):
+        sliding = tc["layer_types"][L] == "hybrid_sliding"
+        nh = tc["swa_num_attention_heads"] if sliding else tc["num_attention_heads"]
+        nkv = tc["swa_num_key_value_heads"] if sliding else tc["num_key_value_heads"]
+        dh = tc["swa_head_dim"] if sliding else tc["head_dim"]
+        ext = tc["sliding_window_size"] if sliding else tc["rel_extent"]
+        q_dim, kv_dim = nh * dh, nkv * dh
+        p = "blk.%d." % L
+        res = [_f32(p + "attn_norm.weight", [H], norm(H)), _f32(p + "ffn_norm.weight", [H], norm(H)),
+               _f32(p + "attn_q_norm.weight", [dh], norm(dh)), _f32(p + "attn_k_norm.weight", [dh], norm(dh)),
+               _f32(p + "attn_rel_proj.weight", [d_rel, ext], small(d_rel * ext)),
+               _f32(p + "shortconv_k.weight", [K, kv_dim], small(K * kv_dim)),
+               _f32(p + "shortconv_v.weight", [K, kv_dim], small(K * kv_dim)),
+               _f32(p + "shortconv_attn.weight", [K, H], small(K * H)),
+               _f32(p + "shortconv_mlp.weight", [K, H], small(K * H)),
+               _q(p + "attn_q.weight", 8, H, q_dim, rng), _q(p + "attn_k.weight", 8, H, kv_dim, rng),
+               _q(p + "attn_v.weight", 8, H, kv_dim, rng), _q(p + "attn_r.weight", 8, H, nh * d_rel, rng),
+               _q(p + "attn_output.weight", 8, q_dim, H, rng)]
+        if tc["mlp_layer_types"][L] == "dense":
+            di = tc["intermediate_size"]
+            res += [_q(p + "ffn_gate.weight", 12, H, di, rng), _q(p + "ffn_up.weight", 12, H, di, rng),
+                    _q(p + "ffn_down.weight", 14, di, H, rng), _f32(p + "ffn_gscale.weight", [1], [1.25])]
+        else:
+            tg, td, tsg, tsd = TINY_EXPERT_TYPES[L % len(TINY_EXPERT_TYPES)]
+            res += [_f32(p + "ffn_gate_inp.weight", [H, n_r + n_s], 0.02 * rng.standard_normal((n_r + n_s) * H)),
+                    _f32(p + "exp_probs_b.bias", [n_r], rng.uniform(-0.1, 0.1, n_r)),
+                    _f32(p + "ffn_gscale.weight", [1], [0.75]),
+                    _q(p + "ffn_gate_shexp.weight", tsg, H, inter, rng, stack=n_s),
+                    _q(p + "ffn_up_shexp.weight", tsg, H, inter, rng, stack=n_s),
+                    _q(p + "ffn_down_shexp.weight", tsd, inter, H, rng, stack=n_s)]
+            exps = [_q(p + "ffn_gate_exps.weight", tg, H, inter, rng, stack=n_r),
+                    _q(p + "ffn_up_exps.weight", tg, H, inter, rng, stack=n_r),
+                    _q(p + "ffn_down_exps.weight", td, inter, H, rng, stack=n_r)]
+            for k, ten in enumerate(exps):
+                parts[(k + L) % n_parts].append(ten)
+        parts[L % n_parts] += res
+    for i in range(n_parts):
+        store.add_part("TINY/tiny-%05d-of-%05d.gguf" % (i + 1, n_parts), parts[i])
+    index_path, _bin_path, manifest_path = store.write()
+    config_path = os.path.join(out_dir, "config.json")
+    with open(config_path, "w") as f:
+        json.dump(cfg, f, indent=2)
+        f.write("\n")
+    tok_path = os.path.join(out_dir, "tokenizer.bin")
+    with open(tokenizer_src, "rb") as src, open(tok_path, "wb") as dst:
+        dst.write(src.read())
+    return {"config": config_path, "manifest": manifest_path, "index": index_path, "tokenizer": tok_path,
+            "cfg": cfg}

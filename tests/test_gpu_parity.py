@@ -6,6 +6,7 @@ Bars:
     (which accumulates in float64), and the reference's own GPU gate
     (relative error with a 1e-3 * scale floor <= 2e-4, src/sepia.c:4557-4589).
 """
+import ctypes
 import glob
 import os
 import struct
@@ -489,10 +490,11 @@ def test_selftest_touch_and_wrap(dev):
 def test_shared_slab_uploaded_once(dev, orc):
     """Shared-buffer synchronisation: a slab the host fills once through
     host_ptr is uploaded once however many batches read it; an op uploads only
-    the 1 MiB chunks of the range it reads; a later host_ptr re-arms the slab
-    and the next op sees the host's new bytes."""
+    the range it reads (here whole 64 KiB chunks: an expert is 9 of them); a
+    later host_ptr re-arms the slab and the next op sees the host's new
+    bytes."""
     L = dev.L
-    t, rows, cols, n_exp, C = 12, 256, 4096, 16, 1 << 20
+    t, rows, cols, n_exp, C = 12, 256, 4096, 16, 1 << 16
     mb = rows * synth.row_bytes(t, cols)
     rng = np.random.default_rng(808)
     mats = [synth.random_matrix(t, rows, cols, rng) for _ in range(n_exp)]
@@ -531,6 +533,44 @@ def test_shared_slab_uploaded_once(dev, orc):
     for b in (slab, xb, yb):
         dev.free(b)
 
+
+
+def test_shared_slab_partial_chunk_writes(dev, orc):
+    """The reference's expert cache hands a slab's host pointer out once per
+    miss, and its loader threads fill that expert's slot while hit experts of
+    the same slab are already dispatched (src/sepia.c:3249-3290, :3908-3935).
+    Slots smaller than a chunk share chunks, so an op that reads one slot
+    must not mark the neighbouring bytes clean: a write the host makes there
+    afterwards, through the pointer it already holds, reaches the op that
+    reads it."""
+    L = dev.L
+    t, rows, cols, n_exp = 8, 5, 256, 12
+    mb = rows * synth.row_bytes(t, cols)        # 1360 bytes: many slots per 64 KiB chunk
+    rng = np.random.default_rng(809)
+    mats = [synth.random_matrix(t, rows, cols, rng) for _ in range(n_exp)]
+    slab = dev.alloc(n_exp * mb)
+    hp = L.sepia_gpu_host_ptr(slab)
+    dev.check(hp, "host_ptr")
+    for e in (0, 1, 2):
+        ctypes.memmove(hp + e * mb, mats[e].ctypes.data, mb)
+    x = synth.normal_vector(rng, cols)
+    xb = dev.shared_from(x)
+    yb = dev.alloc(rows * 4)
+    for e in (1, 0, 2):
+        dev.run(L.sepia_gpu_matvec_q, t, slab, e * mb, xb, yb, rows, cols)
+        assert_close(dev.download(yb, rows), orc.qlinear(t, mats[e], rows, cols, x), what="slot %d" % e)
+    # later "loader" writes through the same pointer, no new host_ptr call
+    for e in range(3, n_exp):
+        ctypes.memmove(hp + e * mb, mats[e].ctypes.data, mb)
+        dev.run(L.sepia_gpu_matvec_q, t, slab, e * mb, xb, yb, rows, cols)
+        assert_close(dev.download(yb, rows), orc.qlinear(t, mats[e], rows, cols, x), what="slot %d" % e)
+    # a slot rewritten after it was read, in the same way
+    new1 = synth.random_matrix(t, rows, cols, rng)
+    ctypes.memmove(hp + 1 * mb, new1.ctypes.data, mb)
+    dev.run(L.sepia_gpu_matvec_q, t, slab, 1 * mb, xb, yb, rows, cols)
+    assert_close(dev.download(yb, rows), orc.qlinear(t, new1, rows, cols, x), what="slot 1 rewritten")
+    for b in (slab, xb, yb):
+        dev.free(b)
 
 # ------------------------------------------------------------------- MoE
 @pytest.fixture
