@@ -119,11 +119,22 @@ int sepia_hip_set_iq2xxs_grid(const uint64_t *grid256);
 int sepia_hip_reserve_scratch(size_t bytes);
 
 /* Bytes copied from shared buffers' host copies to their device copies since
- * init. sepia_gpu_host_ptr marks a whole shared buffer host-written; each op
- * then uploads only the 1 MiB chunks of the ranges it reads that are still
- * marked, once, so a weight slab filled once is uploaded once however many
- * batches read it (tests read this counter to check that). */
+ * init. sepia_gpu_host_ptr marks every 64 KiB chunk of a shared buffer
+ * host-written; each op then uploads the marked parts of exactly the range
+ * it reads and unmarks the chunks that range covers whole, so a weight slab
+ * filled once is uploaded once however many batches read it (tests read
+ * this counter to check that), while bytes beside a range already read can
+ * still be written through the pointer handed out earlier. */
 uint64_t sepia_hip_uploaded_bytes(void);
+
+/* The first device error a kernel recorded since the last call, 0 if none,
+ * and clears it. A kernel records one when a bounded spin wait expires (code
+ * 5): its launch's outputs are then invalid. sepia_gpu_end checks and
+ * clears it itself and fails the batch (logging the code); callers that run
+ * the library's launches without ending a batch (a captured graph replayed
+ * on the library's stream) call this after synchronizing. No counterpart in
+ * the reference, whose Metal kernels have no spin waits. */
+unsigned sepia_hip_take_device_error(void);
 
 /* Measurement support: one launch of `grid` workgroups that reads `bytes`
  * of buf from byte `off` (both multiples of 16) with plain streaming loads
@@ -167,6 +178,8 @@ void *sepia_hip_stream(void);
  *   "pf_route_m" 1/0  prefill router logits on the f32 matrix cores when x
  *                 and the router rows are 16-byte aligned (default 1). */
 int sepia_hip_set_option(const char *name, int value);
+/*   ("wait_ticks" 0..  the kernels' spin-wait bound in 100 MHz ticks; 0 =
+ *                 the default 2 s. For tests of the expiry report.) */
 
 /* ---- The on-disk stores straight into HBM -------------------------------
  * The reference reads resident-manifest.json + resident.bin (mmap'd) and

@@ -66,6 +66,29 @@ __device__ __forceinline__ void sepia_kernarg_warm() {
     asm volatile("" : : "s"(acc));
 }
 
+// Device error word and wait bound, set by the host when it loads the code
+// object (sepia_hip.c): sepia_err_word points at a host-visible word that
+// the host reads after each batch, sepia_wait_ticks bounds every spin wait
+// of a kernel in s_memrealtime ticks (100 MHz). The whole library is one
+// code object, so these are its only definitions.
+extern "C" __device__ uint32_t *sepia_err_word;
+extern "C" __device__ uint64_t sepia_wait_ticks;
+// Record error `code` (first one wins) in *err, or in the device error word
+// when err is NULL; lane 0 of the calling wave writes.
+__device__ __forceinline__ void sepia_report_error(uint32_t *err, uint32_t code, int lane) {
+    if (lane != 0) return;
+    if (err) {
+        __hip_atomic_store(err, code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
+    uint32_t *w = sepia_err_word;
+    if (w) {
+        uint32_t zero = 0u;
+        __hip_atomic_compare_exchange_strong(w, &zero, code, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+}
+
 // Sum over the 64 lanes of a wave; every lane gets the total.
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

@@ -74,10 +74,19 @@ struct XqSeg {
     uint4 p0, p1, p2;
     float xs, gs, gq;
 };
+// A segment holding a NaN or an infinity gets m = +inf: every q is 0 and
+// xs, gq are inf and NaN, so each dot that uses the segment comes out NaN,
+// as the reference's double accumulation makes it non-finite
+// (src/sepia.c:731-735). fmaxf drops a NaN operand; the plain sum keeps it.
+__device__ __forceinline__ float mq_nonfinite_max(float m, float sum) { return (sum == sum) ? m : INFINITY; }
 __device__ __forceinline__ XqSeg xq_segment(const float (&a)[16]) {
     float m = 0.0f;
 #pragma unroll
     for (int i = 0; i < 16; i++) m = fmaxf(m, fabsf(a[i]));
+    float sum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; i++) sum += a[i];
+    m = mq_nonfinite_max(m, sum);
     // |a * inv| <= QMAX (1 + 2^-22): rcp is within 1 ulp
     const float inv = (m > 0.0f) ? MQ_QMAX * __builtin_amdgcn_rcpf(m) : 0.0f;
     const float xs = m * (1.0f / MQ_QMAX);
@@ -105,9 +114,6 @@ __device__ __forceinline__ XqSeg xq_segment(const float (&a)[16]) {
     r.p0 = make_uint4(w0[0], w0[1], w0[2], w0[3]);
     r.p1 = make_uint4(w1[0], w1[1], w1[2], w1[3]);
     r.p2 = make_uint4(w2[0], w2[1], w2[2], w2[3]);
-    float sum = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 16; i++) sum += a[i];
     r.xs = xs;
     r.gs = sum;
     r.gq = xs * (float)qs;
@@ -147,6 +153,10 @@ __device__ __forceinline__ XqQuad mq_xq_quad(const float (&a)[4]) {
     float m = fmaxf(fmaxf(fabsf(a[0]), fabsf(a[1])), fmaxf(fabsf(a[2]), fabsf(a[3])));
     m = fmaxf(m, mq_quad_x1(m));
     m = fmaxf(m, mq_quad_x2(m));
+    float sum = (a[0] + a[1]) + (a[2] + a[3]);
+    sum += mq_quad_x1(sum);
+    sum += mq_quad_x2(sum);
+    m = mq_nonfinite_max(m, sum);
     const float inv = (m > 0.0f) ? MQ_QMAX * __builtin_amdgcn_rcpf(m) : 0.0f;
     XqQuad r;
     r.xs = m * (1.0f / MQ_QMAX);
@@ -160,9 +170,6 @@ __device__ __forceinline__ XqQuad mq_xq_quad(const float (&a)[4]) {
     }
     qs += mq_quad_x1i(qs);
     qs += mq_quad_x2i(qs);
-    float sum = (a[0] + a[1]) + (a[2] + a[3]);
-    sum += mq_quad_x1(sum);
-    sum += mq_quad_x2(sum);
     const uint32_t t01 = __builtin_amdgcn_perm(q[1], q[0], 0x05010400u);
     const uint32_t t23 = __builtin_amdgcn_perm(q[3], q[2], 0x05010400u);
     const uint32_t u01 = __builtin_amdgcn_perm(q[1], q[0], 0x06020602u);
@@ -1071,17 +1078,17 @@ __device__ __forceinline__ MqLane mq_lane() {
 __device__ __forceinline__ int mq_wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
 
 // ------------------------------------------- vector by converter waves ----
-// Wait bounds in s_memrealtime ticks (100 MHz): 2 s (a grid barrier, an LDS
-// counter), twice that for the LDS flag that follows a grid barrier.
-#define MQ_WAIT_TICKS 200000000ull
-
-// Wait until the LDS counter c reaches target (acquire), bounded in time.
+// Wait until the LDS counter c reaches target (acquire), bounded in time:
+// sepia_wait_ticks of s_memrealtime (100 MHz; 2 s unless the host sets
+// another bound). On expiry the wave goes on and code 5 goes to err, or
+// else to the library's device error word, which the host checks when the
+// batch ends: the launch's outputs are then invalid.
 __device__ __forceinline__ void mq_waves_wait(uint32_t *c, uint32_t target, int lane, uint32_t *err) {
     const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
     while (__hip_atomic_load(c, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < target) {
         __builtin_amdgcn_s_sleep(1);
-        if (__builtin_amdgcn_s_memrealtime() - t0 > MQ_WAIT_TICKS) {
-            if (lane == 0 && err) __hip_atomic_store(err, 5u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (__builtin_amdgcn_s_memrealtime() - t0 > sepia_wait_ticks) {
+            sepia_report_error(err, 5u, lane);
             return;
         }
     }
@@ -1089,7 +1096,7 @@ __device__ __forceinline__ void mq_waves_wait(uint32_t *c, uint32_t target, int 
 
 // Waves first .. first + count - 1 of the workgroup wait for one another:
 // arrival k of each (k = 1, 2, ...) completes when the counter at c
-// reaches k * count. Bounded in time (error flag 5 on expiry).
+// reaches k * count. Bounded in time (error code 5 on expiry).
 __device__ __forceinline__ void mq_waves_sync(uint32_t *c, uint32_t target, int lane, uint32_t *err) {
     if (lane == 0) __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
     mq_waves_wait(c, target, lane, err);
@@ -1793,6 +1800,18 @@ __device__ __forceinline__ void mq_down(const MqProj &down, const MqProj &s_down
                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     if (n_count == 0) return;
+    // Publication without release/acquire fences. Every datum that crosses
+    // workgroups here is an agent-scope atomic: the partial rows are stored
+    // and loaded, and the counter incremented, with relaxed agent-scope
+    // atomics, which gfx950 performs at the agent's coherence point (sc1
+    // stores and loads, L2-coherent atomics; the LLVM AMDGPU memory model's
+    // code sequences for relaxed agent-scope atomics). What the fences would
+    // add is ordering, and the hardware gives it here: s_waitcnt vmcnt(0)
+    // returns only once this thread's stores are acknowledged at that point,
+    // the barrier then orders them before the counter increment, and the
+    // last arriver's loads are issued after it has read the final count. An
+    // agent-scope release fence would also write back the whole L2 (buffer
+    // write-back), which measured 0.6-1.3 us more per down launch at C3.
     __builtin_amdgcn_s_waitcnt(0);   // this thread's partial stores have completed
     __syncthreads();
     for (int k = threadIdx.x; k < nk; k += blockDim.x) {

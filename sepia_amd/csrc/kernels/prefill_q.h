@@ -81,7 +81,9 @@ extern "C" __global__ __launch_bounds__(256) void sepia_pf_quant(const float *__
     float m = 0.0f;
     for (int64_t c = 4 * (int64_t)threadIdx.x; c < K; c += 1024) {
         const float4 v = *(const float4 *)(row + c);
-        m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+        // a NaN or an infinity makes the row's scale infinite (mq_nonfinite_max)
+        m = mq_nonfinite_max(fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)))),
+                             (v.x + v.y) + (v.z + v.w));
     }
     m = pq_wave_max(m);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;

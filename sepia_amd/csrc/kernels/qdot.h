@@ -261,6 +261,12 @@ __device__ __forceinline__ XSeg xp_segment(const float4 (&v)[4]) {
     float m = 0.0f;
 #pragma unroll
     for (int i = 0; i < 16; i++) m = fmaxf(m, fabsf(a[i]));
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
+    // a NaN or an infinity makes the scale infinite, so every dot that uses
+    // the segment comes out non-finite, as the reference's double sum does
+    if (!(s == s)) m = INFINITY;
     // |x| * inv <= 8355000 (1 + 2^-22) < 2^23: q fits 24 signed bits.
     // inv * xs = rcp(m) * m is 1 within 2^-22, so x ~= xs * q.
     const float inv = (m > 0.0f) ? XP_QMAX * __builtin_amdgcn_rcpf(m) : 0.0f;
@@ -279,9 +285,6 @@ __device__ __forceinline__ XSeg xp_segment(const float4 (&v)[4]) {
         w1[w] = __builtin_amdgcn_perm(t23, t01, 0x07060302u);   // byte 1
         w0[w] = __builtin_amdgcn_perm(u23, u01, 0x05040100u);   // byte 2
     }
-    float s = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 4; i++) s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
     XSeg r;
     r.p0 = make_uint4(w0[0], w0[1], w0[2], w0[3]);
     r.p1 = make_uint4(w1[0], w1[1], w1[2], w1[3]);

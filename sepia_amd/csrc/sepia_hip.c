@@ -535,6 +535,65 @@ static int kernel_path(const char *dir, char *path, size_t cap) {
     return 1;
 }
 
+/* The device error word: a word of pinned host memory that kernels can
+ * write (a bounded spin wait that expired records its code there), read by
+ * the host after each batch. Its device address goes into the code object's
+ * sepia_err_word; sepia_wait_ticks takes the spin-wait bound. */
+static volatile uint32_t *g_err_host;
+static hipDeviceptr_t g_wait_ticks_dev;
+#define WAIT_TICKS_DEFAULT 200000000ull   /* 2 s of s_memrealtime (100 MHz) */
+
+static int set_wait_ticks(uint64_t ticks) {
+    hipError_t e = hipMemcpyHtoD(g_wait_ticks_dev, &ticks, sizeof ticks);
+    if (e != hipSuccess) {
+        LOG("setting the kernels' wait bound failed: %s", hipGetErrorString(e));
+        return 0;
+    }
+    return 1;
+}
+
+static int err_word_setup(void) {
+    hipDeviceptr_t gp;
+    size_t gsz = 0;
+    hipError_t e = hipModuleGetGlobal(&gp, &gsz, g_module, "sepia_err_word");
+    if (e != hipSuccess || gsz != sizeof(void *)) {
+        LOG("init: the code object has no device error word: %s", hipGetErrorString(e));
+        return 0;
+    }
+    e = hipModuleGetGlobal(&g_wait_ticks_dev, &gsz, g_module, "sepia_wait_ticks");
+    if (e != hipSuccess || gsz != sizeof(uint64_t)) {
+        LOG("init: the code object has no wait bound: %s", hipGetErrorString(e));
+        return 0;
+    }
+    if (!g_err_host) {
+        void *h = NULL;
+        e = hipHostMalloc(&h, 256, hipHostMallocMapped | hipHostMallocCoherent);
+        if (e != hipSuccess) {
+            LOG("init: pinned memory for the device error word failed: %s", hipGetErrorString(e));
+            return 0;
+        }
+        g_err_host = (volatile uint32_t *)h;
+    }
+    *g_err_host = 0;
+    void *dp = NULL;
+    e = hipHostGetDevicePointer(&dp, (void *)g_err_host, 0);
+    if (e == hipSuccess) e = hipMemcpyHtoD(gp, &dp, sizeof dp);
+    if (e != hipSuccess) {
+        LOG("init: publishing the device error word failed: %s", hipGetErrorString(e));
+        return 0;
+    }
+    return set_wait_ticks(WAIT_TICKS_DEFAULT);
+}
+
+/* The first error code a kernel recorded since the last call (0: none), and
+ * clear it. */
+unsigned sepia_hip_take_device_error(void) {
+    if (!g_err_host) return 0;
+    const unsigned code = *g_err_host;
+    if (code) *g_err_host = 0;
+    return code;
+}
+
 int sepia_gpu_init(const char *kernel_dir) {
     if (g_available) return 1;
     int n = 0;
@@ -579,6 +638,11 @@ int sepia_gpu_init(const char *kernel_dir) {
             hipStreamDestroy(g_stream);
             return 0;
         }
+    }
+    if (!err_word_setup()) {
+        hipModuleUnload(g_module);
+        hipStreamDestroy(g_stream);
+        return 0;
     }
     /* the allocation-free decode entry's array: its device address, once,
      * with this device current */
@@ -651,6 +715,11 @@ int sepia_gpu_end(void) {
     if (e == hipSuccess) e = s;
     if (e != hipSuccess) {
         LOG("end: batch failed: %s", hipGetErrorString(e));
+        return 0;
+    }
+    const unsigned code = sepia_hip_take_device_error();
+    if (code) {
+        LOG("end: a kernel's bounded wait expired (device error %u); the batch's outputs are invalid", code);
         return 0;
     }
     return 1;
@@ -1148,6 +1217,14 @@ int sepia_hip_set_option(const char *name, int value) {
     if (strcmp(name, "mq") == 0 && (value == 0 || value == 1)) {
         g_opt_mq = value;
         return 1;
+    }
+    if (strcmp(name, "wait_ticks") == 0 && value >= 0) {
+        /* the kernels' spin-wait bound in s_memrealtime ticks (100 MHz); 0
+         * restores the default of 2 s. Tests use a tiny bound to make the
+         * waits expire and check that the batch reports it. */
+        if (!need_init("set_option")) return 0;
+        hipStreamSynchronize(g_stream);
+        return set_wait_ticks(value ? (uint64_t)value : WAIT_TICKS_DEFAULT);
     }
     if (strcmp(name, "mq_x") == 0 && value >= 0 && value <= 4) {
         g_opt_mq_x = value;

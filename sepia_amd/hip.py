@@ -96,6 +96,7 @@ PROTOTYPES = {
     "sepia_hip_set_iq2xxs_grid": (_I, [_P]),
     "sepia_hip_reserve_scratch": (_I, [_SZ]),
     "sepia_hip_uploaded_bytes": (ctypes.c_uint64, []),
+    "sepia_hip_take_device_error": (ctypes.c_uint, []),
     "sepia_hip_read_probe": (_I, [_P, _SZ, _SZ, ctypes.c_uint]),
     "sepia_hip_stream": (_P, []),
     "sepia_hip_set_option": (_I, [ctypes.c_char_p, _I]),
@@ -153,7 +154,11 @@ class Device:
 
     def __init__(self):
         self.L = load()
-        if not self.L.sepia_gpu_init(LIB_DIR.encode()):
+        # the kernel directory handed to sepia_gpu_init (the reference passes
+        # its metal/ directory, src/sepia.c:6181): the built code object, or
+        # another build of it named by SEPIA_KERNEL_DIR
+        kdir = os.environ.get("SEPIA_KERNEL_DIR", LIB_DIR)
+        if not self.L.sepia_gpu_init(kdir.encode()):
             raise SepiaHipError("sepia_gpu_init failed (no MI355X, or the code object did not load)")
         self.name = self.L.sepia_gpu_device_name().decode()
 
