@@ -118,6 +118,15 @@ int sepia_hip_set_iq2xxs_grid(const uint64_t *grid256);
  * run the call once, or reserve, before beginning a capture. Needs init. */
 int sepia_hip_reserve_scratch(size_t bytes);
 
+/* Bytes of the library's growable scratch region (0 before its first use).
+ * No counterpart in the reference. */
+size_t sepia_hip_scratch_bytes(void);
+
+/* Device and pinned-host allocations the library has made since it loaded
+ * (hipMalloc, hipHostMalloc). No counterpart in the reference; tests of the
+ * allocation-free entry check that it leaves the count unchanged. */
+uint64_t sepia_hip_alloc_count(void);
+
 /* Bytes copied from shared buffers' host copies to their device copies since
  * init. sepia_gpu_host_ptr marks every 64 KiB chunk of a shared buffer
  * host-written; each op then uploads the marked parts of exactly the range

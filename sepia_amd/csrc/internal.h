@@ -26,5 +26,7 @@ SEPIA_HIDDEN size_t sepia_buf_len(const SepiaGpuBuf *b);
  * n that is not a whole number of blocks (reference quants_row_bytes,
  * src/quants.c:45-56). */
 SEPIA_HIDDEN int64_t sepia_row_bytes(int ggml_type, int64_t n);
+/* Count one device or pinned-host allocation (sepia_hip_alloc_count). */
+SEPIA_HIDDEN void sepia_count_alloc(void);
 
 #endif

@@ -304,6 +304,12 @@ static int chk(const SepiaGpuBuf *b, size_t off, size_t n, const char *op, const
 /* Bytes uploaded to shared buffers' device copies since init (tests read it
  * through sepia_hip_uploaded_bytes). */
 static uint64_t g_uploaded;
+/* Device and pinned-host allocations the library has made since it loaded
+ * (sepia_hip_alloc_count): the allocation-free entry's tests check that it
+ * leaves this unchanged. */
+static uint64_t g_allocs;
+uint64_t sepia_hip_alloc_count(void) { return g_allocs; }
+void sepia_count_alloc(void) { g_allocs++; }
 
 /* Bring [off, off + n) of the device copy up to date before a kernel reads
  * it: upload the parts of that range that lie in host-dirty chunks,
@@ -381,6 +387,7 @@ static void *scratch(size_t need, const char *op) {
     g_scratch = NULL;
     g_scratch_len = 0;
     size_t want = CNT_BYTES + (need < (4u << 20) ? (4u << 20) : need);
+    g_allocs++;
     hipError_t e = hipMalloc(&g_scratch, want);
     if (e == hipSuccess) e = hipMemsetAsync(g_scratch, 0, want, g_stream);
     if (e == hipSuccess) e = hipStreamSynchronize(g_stream);
@@ -393,6 +400,8 @@ static void *scratch(size_t need, const char *op) {
     g_scratch_len = want;
     return (uint8_t *)g_scratch + CNT_BYTES;
 }
+
+size_t sepia_hip_scratch_bytes(void) { return g_scratch_len; }
 
 int sepia_hip_reserve_scratch(size_t bytes) {
     if (!need_init("reserve_scratch")) return 0;
@@ -407,6 +416,7 @@ static SepiaGpuBuf *new_buf(size_t len, int kind) {
     }
     b->len = len;
     b->kind = kind;
+    g_allocs++;
     hipError_t e = hipMalloc((void **)&b->dev, dev_bytes(len));
     if (e != hipSuccess) {
         LOG("alloc: hipMalloc(%zu) failed: %s", dev_bytes(len), hipGetErrorString(e));
@@ -433,6 +443,7 @@ SepiaGpuBuf *sepia_gpu_alloc(size_t len, int gpu_private) {
         return NULL;
     }
     if (b->kind == BUF_SHARED) {
+        g_allocs++;
         e = hipHostMalloc(&b->host, len, hipHostMallocDefault);
         if (e != hipSuccess) {
             LOG("alloc: pinned host copy of %zu bytes failed: %s", len, hipGetErrorString(e));
@@ -567,6 +578,7 @@ static int err_word_setup(void) {
     }
     if (!g_err_host) {
         void *h = NULL;
+        g_allocs++;
         e = hipHostMalloc(&h, 256, hipHostMallocMapped | hipHostMallocCoherent);
         if (e != hipSuccess) {
             LOG("init: pinned memory for the device error word failed: %s", hipGetErrorString(e));

@@ -129,25 +129,35 @@ typedef struct {
     int k;
 } Stager;
 
-static int stager_open(Stager *s, const char *op) {
-    memset(s, 0, sizeof *s);
-    for (int i = 0; i < 2; i++) {
-        hipError_t e = hipHostMalloc(&s->host[i], STAGE_BYTES, hipHostMallocDefault);
-        if (e == hipSuccess) e = hipEventCreateWithFlags(&s->done[i], hipEventDisableTiming);
-        if (e != hipSuccess) {
-            LOG("%s: staging buffers: %s", op, hipGetErrorString(e));
-            return 0;
-        }
-    }
-    return 1;
-}
-
 static void stager_close(Stager *s) {
     hipStreamSynchronize(sepia_stream());
     for (int i = 0; i < 2; i++) {
         if (s->done[i]) hipEventDestroy(s->done[i]);
         if (s->host[i]) hipHostFree(s->host[i]);
+        s->done[i] = NULL;
+        s->host[i] = NULL;
     }
+}
+
+/* Two pinned staging buffers and their events; on failure whatever was
+ * created is released again and 0 returned. */
+static int stager_open(Stager *s, const char *op) {
+    memset(s, 0, sizeof *s);
+    for (int i = 0; i < 2; i++) {
+        sepia_count_alloc();
+        hipError_t e = hipHostMalloc(&s->host[i], STAGE_BYTES, hipHostMallocDefault);
+        if (e != hipSuccess) s->host[i] = NULL;
+        if (e == hipSuccess) {
+            e = hipEventCreateWithFlags(&s->done[i], hipEventDisableTiming);
+            if (e != hipSuccess) s->done[i] = NULL;
+        }
+        if (e != hipSuccess) {
+            LOG("%s: staging buffers: %s", op, hipGetErrorString(e));
+            stager_close(s);
+            return 0;
+        }
+    }
+    return 1;
 }
 
 /* [off, off + n) of file fd to device dst, in chunks through the two

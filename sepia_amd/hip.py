@@ -97,6 +97,8 @@ PROTOTYPES = {
     "sepia_hip_reserve_scratch": (_I, [_SZ]),
     "sepia_hip_uploaded_bytes": (ctypes.c_uint64, []),
     "sepia_hip_take_device_error": (ctypes.c_uint, []),
+    "sepia_hip_scratch_bytes": (ctypes.c_size_t, []),
+    "sepia_hip_alloc_count": (ctypes.c_uint64, []),
     "sepia_hip_read_probe": (_I, [_P, _SZ, _SZ, ctypes.c_uint]),
     "sepia_hip_stream": (_P, []),
     "sepia_hip_set_option": (_I, [ctypes.c_char_p, _I]),

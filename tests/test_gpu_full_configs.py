@@ -11,7 +11,8 @@ reference's strict '>' arg-max must keep the lower index.
 
 C5: the same layer for a 512-token batch (sepia_gpu_moe_prefill): every
 token's selection against the oracle (near-ties per the reference's
-protocol) and y against the oracle's single-token layer on 16 tokens.
+protocol) and y against the oracle's single-token layer, for all 512 tokens
+with the plain router (bf16-representable and full f32 x).
 
 Weights are generated on the GPU (sepia_hip_synth_blocks); only the experts
 a checked token selects are copied back for the oracle.
@@ -177,14 +178,19 @@ def test_c3_decode_ties(dev, orc, layer):
     assert_close(y, y_ref, what="C3 ties", gate=False)
 
 
-@pytest.mark.parametrize("router", ["plain", "ties"])
-def test_c5_prefill_full(dev, orc, layer, router):
-    """C5 at full size: 512 tokens over all 256 routed experts. Every token's
-    selection against the oracle; y on 16 tokens (8 leading, 8 spread)."""
+@pytest.mark.parametrize("router,x_kind", [("plain", "bf16"), ("plain", "f32"), ("ties", "bf16")])
+def test_c5_prefill_full(dev, orc, layer, router, x_kind):
+    """C5 at full size: 512 tokens over all 256 routed experts on the default
+    (int8) path. Every token's selection against the oracle; y of every token
+    for the plain router -- so every unit of up to 32 (token, expert) pairs,
+    the last partial unit of each expert included, is checked -- with x
+    bf16-representable and full f32; y on 16 tokens
+    for the router with constructed ties."""
     T = 512
-    rng = np.random.default_rng(55 if router == "plain" else 56)
+    rng = np.random.default_rng({"plain": 55, "ties": 56}[router] + (7 if x_kind == "f32" else 0))
     X = rng.standard_normal((T, H)).astype(np.float32)
-    X = (X.view(np.uint32) & np.uint32(0xFFFF0000)).view(np.float32)
+    if x_kind == "bf16":
+        X = (X.view(np.uint32) & np.uint32(0xFFFF0000)).view(np.float32)
     n_sel = TOPK + NS
     xb = dev.shared_from(X)
     yb, rb = dev.alloc(X.nbytes), dev.alloc(T * (TOPK + n_sel) * 4)
@@ -200,11 +206,13 @@ def test_c5_prefill_full(dev, orc, layer, router):
     if router == "plain":
         # 3072 (token, expert) pairs over 256 experts: well over half of them take tokens
         assert len(set(idx.ravel().tolist())) >= 128
-    check = list(range(8)) + [int(t) for t in np.linspace(8, T - 1, 8)]
+    check = list(range(T)) if router == "plain" else list(range(8)) + [int(t) for t in np.linspace(8, T - 1, 8)]
     sp = layer.spec(router, np.concatenate([idx[t] for t in check]))
-    for t in check:
+    for n, t in enumerate(check):
         y_ref, _, _, _ = orc.moe_layer(sp, X[t], force_idx=chosen[t], threads=THREADS)
-        assert_close(Y[t], y_ref, what="C5 %s token %d" % (router, t), gate=False)
+        assert_close(Y[t], y_ref, what="C5 %s %s token %d" % (router, x_kind, t), gate=False)
+        if n % 128 == 127:
+            print("C5 %s %s: %d tokens checked" % (router, x_kind, n + 1), flush=True)
 
 
 def test_decode_many_experts_em16(dev, orc):
