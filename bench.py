@@ -109,6 +109,9 @@ class HipRT:
         self.L.hipGraphExecDestroy(exe)
 
 
+TIMING = "graph"
+
+
 class Bench:
     def __init__(self, dev):
         from sepia_amd import hip
@@ -147,24 +150,45 @@ class Bench:
         return out
 
     def timed_steps(self, step, warmup, steps):
-        """W untimed warmup steps, then exactly `steps` steps replayed from one captured
-        HIP graph between two events; returns ms per step."""
+        """W untimed warmup steps, then exactly `steps` steps between two events on the
+        library's stream; returns ms per step. TIMING selects how the timed steps are issued:
+        "step-graphs" (default) captures each step as its own HIP graph and launches the
+        graphs back to back, "graph" replays all steps from one captured graph, "eager"
+        issues them through the C ABI directly. Every mode first runs the exact timed
+        sequence once untimed (graph upload, caches)."""
         dev = self.dev
         dev.begin()
         for i in range(warmup):
             dev.check(step(i), "warmup step")
         dev.end()
-        dev.begin()
-        g = self.rt.capture(self.stream, lambda: [dev.check(step(warmup + i), "captured step") for i in range(steps)])
-        dev.end()
-        self.rt.launch_graph(g, self.stream)         # first replay: graph upload, untimed
-        self.rt.sync(self.stream)
         e0, e1 = self.rt.event(), self.rt.event()
+        if TIMING == "eager":
+            for rep in range(2):
+                dev.begin()
+                self.rt.record(e0, self.stream)
+                for i in range(steps):
+                    dev.check(step(warmup + i), "timed step")
+                self.rt.record(e1, self.stream)
+                dev.end()
+            return self.rt.elapsed_ms(e0, e1) / steps
+        dev.begin()
+        if TIMING == "graph":
+            graphs = [self.rt.capture(self.stream, lambda: [dev.check(step(warmup + i), "captured step")
+                                                            for i in range(steps)])]
+        else:
+            graphs = [self.rt.capture(self.stream, lambda i=i: dev.check(step(warmup + i), "captured step"))
+                      for i in range(steps)]
+        dev.end()
+        for g in graphs:                               # first launch of each: graph upload, untimed
+            self.rt.launch_graph(g, self.stream)
+        self.rt.sync(self.stream)
         self.rt.record(e0, self.stream)
-        self.rt.launch_graph(g, self.stream)
+        for g in graphs:
+            self.rt.launch_graph(g, self.stream)
         self.rt.record(e1, self.stream)
         ms = self.rt.elapsed_ms(e0, e1)
-        self.rt.destroy_graph(g)
+        for g in graphs:
+            self.rt.destroy_graph(g)
         return ms / steps
 
     def kernel_used(self, step, n, candidates):
@@ -591,7 +615,8 @@ def run_c3(B, warmup, steps, cpu_seconds, n_layers=8, types=C3_TYPES, what="C3")
     kern = {k: dict(avg_launch_us=v * 1e3, bytes_per_launch=k_bytes[k], achieved_gbs=k_bytes[k] / (v * 1e-3) / 1e9,
                     traffic=measured.get(k))
             for k, v in kms.items()}
-    return dict(ms=ms, us_per_token=ms * 1e3, bytes_per_token=per_token, gbs=per_token / (ms * 1e-3) / 1e9,
+    return dict(ms=ms, us_per_token=ms * 1e3, kernel_sum_us=sum(kms.values()) * 1e3,
+                bytes_per_token=per_token, gbs=per_token / (ms * 1e-3) / 1e9,
                 roofline_us=per_token / (HBM_PEAK_GBS * 1e9) * 1e6,
                 target_us=1.5 * per_token / (HBM_PEAK_GBS * 1e9) * 1e6,
                 layers_rotated=n_layers, x_vectors=nx, kernels=kern,
@@ -678,7 +703,11 @@ def main():
                          "256 MiB, the reference for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE; 'ceiling': the "
                          "HBM read ceiling of a single launch at each kernel's size); default: all")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--timing", choices=["graph", "step-graphs", "eager"], default="graph",
+                    help="how the timed steps are issued (see Bench.timed_steps)")
     args = ap.parse_args()
+    global TIMING
+    TIMING = args.timing
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py: this build measures one GPU only (the path has no multi-GPU "
@@ -758,6 +787,7 @@ def main():
                                "+ 2 shared Q4_K experts; 8 layers (42 GB) resident in HBM and 64 x vectors, "
                                "rotated per step",
                    "bytes_per_token": res["bytes_per_token"], "us_per_token": round(res["us_per_token"], 3),
+                   "kernel_sum_us": round(res["kernel_sum_us"], 3), "timing": TIMING,
                    "target_us_per_token": round(res["target_us"], 2),
                    "hbm_bound_us_per_token": round(res["roofline_us"], 2),
                    "hbm_frac": round(res["gbs"] / HBM_PEAK_GBS, 4)},
