@@ -625,11 +625,13 @@ def run_c3(B, warmup, steps, cpu_seconds, n_layers=8, types=C3_TYPES, what="C3")
                 cpu=dict(s1=s1, n1=n1, sN=sN, nN=nN, threads=nthr))
 
 
-def run_c5(B, warmup, steps, cpu_seconds, T=512):
+def run_c5(B, warmup, steps, cpu_seconds, T=512, types=C3_TYPES):
     """the MoE layer for a batch of T tokens (prefill) with all 256 routed +
-    2 shared experts resident, x ~ N(0,1) rounded to bf16-representable f32."""
+    2 shared experts resident, x ~ N(0,1) rounded to bf16-representable f32. types: the layer's
+    formats (C3_TYPES: Q2_K / Q3_K routed, Q4_K shared, the int8 kernels; REAL_TYPES: the real
+    checkpoint's IQ2_XS / IQ3_XXS routed, Q5_K / Q6_K shared, the bf16 kernels)."""
     L = B.L
-    layers, host_router, sizes = build_moe_layers(B, 1)
+    layers, host_router, sizes = build_moe_layers(B, 1, types)
     H, I, NR, NS, gb, db, sgb, sdb, _ = sizes
     d, lb = layers[0]
     rng = np.random.default_rng(55)
@@ -684,9 +686,9 @@ def run_c5(B, warmup, steps, cpu_seconds, T=512):
                 hbm_roofline_ms=(wbytes + act_bytes) / (HBM_PEAK_GBS * 1e9) * 1e3,
                 gflop=flops / 1e9, tflops=flops / sec / 1e12, mfma_util_bf16=flops / sec / 2.5e15,
                 # the int8 path issues three digit planes per product, at the 5.0 POP/s int8 peak
-                mfma_util_int8_issued=3 * flops / sec / 5.0e15,
+                mfma_util_int8_issued=3 * flops / sec / 5.0e15 if types == C3_TYPES else None,
                 kernels_avg_ms={k: v for k, v in kms.items()},
-                traffic_bytes=MEASURED_TRAFFIC_C5,
+                traffic_bytes=MEASURED_TRAFFIC_C5 if types == C3_TYPES else None,
                 parity=dict(tokens=sample, max_abs_diff=err, y_inf=scale, bound="1e-4*||y||_inf",
                             selections_checked=T),
                 cpu_1core_ms_per_token=s1 * 1e3)
@@ -697,7 +699,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--only", choices=["c3", "real", "c2", "c1", "c4", "c5", "store", "copy", "ceiling"],
+    ap.add_argument("--only", choices=["c3", "real", "c2", "c1", "c4", "c5", "c5real", "store", "copy", "ceiling"],
                     default=None,
                     help="run one configuration (profiling runs; 'copy': the library's f32 copy kernel over "
                          "256 MiB, the reference for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE; 'ceiling': the "
@@ -754,6 +756,12 @@ def main():
     if args.only in (None, "c5"):
         extra["C5_moe_prefill_512"] = run_c5(B, min(args.warmup, 2), min(args.steps, 10), min(3.0, args.cpu_seconds))
         log("C5", json.dumps(extra["C5_moe_prefill_512"]))
+    if args.only in (None, "c5", "c5real"):
+        r = run_c5(B, min(args.warmup, 2), min(args.steps, 10), min(2.0, args.cpu_seconds), types=REAL_TYPES)
+        r["workload"] = ("C5 with the real checkpoint's most common formats: IQ2_XS gate/up, IQ3_XXS down "
+                         "(256 routed), Q5_K gate/up and Q6_K down (2 shared)")
+        extra["C5_real_iq2xs_iq3xxs_q5k_q6k"] = r
+        log("C5 real", json.dumps(r))
     if args.only in (None, "store"):
         extra["store_upload_c3_layer"] = run_store(B)
         log("store", json.dumps(extra["store_upload_c3_layer"]))

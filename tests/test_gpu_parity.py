@@ -890,13 +890,17 @@ def bf16_normal(rng, shape):
     return (v.view(np.uint32) & np.uint32(0xFFFF0000)).view(np.float32)
 
 
-# (hidden, inter, n_routed, n_shared), (gate/up, down, shared) formats, tokens
+# (hidden, inter, n_routed, n_shared), (gate/up, down, shared gate/up[, shared down]) formats, tokens
 PREFILL_CASES = [
     ((2048, 1024, 16, 2), (10, 11, 12), 40),
     ((6144, 3072, 16, 2), (10, 11, 12), 48),      # BASELINE configs[4] shapes, 16 experts resident
     ((2048, 1024, 12, 1), (17, 18, 14), 33),      # IQ2_XS / IQ3_XXS routed, Q6_K shared
-    ((1024, 2048, 8, 2), (13, 23, 11), 20),       # Q5_K / IQ4_XS routed, Q3_K shared
+    ((1024, 2048, 8, 2), (13, 23, 11), 20),       # Q5_K / IQ4_XS routed, Q3_K shared (bf16 kernels)
     ((2048, 1024, 12, 1), (11, 10, 10), 37),      # Q3_K / Q2_K routed, Q2_K shared
+    # the real checkpoint's format mixes (bf16 kernels)
+    ((6144, 3072, 16, 2), (17, 18, 13, 14), 48),  # IQ2_XS / IQ3_XXS routed, Q5_K / Q6_K shared
+    ((2048, 1024, 12, 2), (17, 23, 13, 14), 40),  # IQ4_XS down
+    ((1024, 2048, 8, 2), (13, 14, 13, 14), 20),   # Q5_K / Q6_K routed
 ]
 
 
@@ -913,12 +917,14 @@ def test_moe_prefill(dev, orc, shape, types, T, x_kind, path):
     Q4_K projections on the int8 matrix cores (q, the default; option pf_q)
     or on the bf16 kernels with bit-exact dequantized weights (tile; pf_q 0,
     which also runs the router on sepia_pf_route, pf_route_m 0). Layers with
-    other formats take the bf16 kernels on both paths."""
+    other formats (the real checkpoint's IQ2_XS, IQ3_XXS, IQ4_XS, Q5_K and
+    Q6_K mixes among them) take the bf16 kernels on both paths."""
     hidden, inter, n_routed, n_shared = shape
-    tgu, td, ts = types
+    tgu, td, ts = types[:3]
+    tsd = types[3] if len(types) > 3 else None
     rng = np.random.default_rng(hidden + 7 * T + tgu)
     desc, spec, bufs = make_layer(dev, rng, hidden=hidden, inter=inter, n_routed=n_routed, n_shared=n_shared,
-                                  tg=tgu, tu=tgu, td=td, ts=ts)
+                                  tg=tgu, tu=tgu, td=td, ts=ts, tsd=tsd)
     X = bf16_normal(rng, (T, hidden)) if x_kind == "bf16" else rng.standard_normal((T, hidden)).astype(np.float32)
     for k, v in PF_PATHS[path].items():
         assert dev.L.sepia_hip_set_option(k.encode(), v) == 1
