@@ -150,6 +150,15 @@ unsigned sepia_hip_take_device_error(void);
  * and does nothing else, for the HBM read ceiling of a single launch at a
  * given size. No counterpart in the reference. */
 int sepia_hip_read_probe(SepiaGpuBuf *buf, size_t off, size_t bytes, unsigned grid);
+/* The same read through the decode kernels' staging path (no counterpart in
+ * the reference; a measurement reference): grid workgroups of `threads`
+ * threads, each wave streaming its steps of kb KB (kb wave-wide 16-byte LDS
+ * DMAs) through a private ring of `stages` stages, waiting for the oldest
+ * stage, reading it back and refilling it, with no compute. (kb, stages) is
+ * one of (7,1) (7,2) (4,1) (4,2) (4,4) (2,4) (1,4); the rings must fit the
+ * LDS. Kernel sepia_read_probe_dma. */
+int sepia_hip_read_probe_dma(SepiaGpuBuf *buf, size_t off, size_t bytes, unsigned grid, unsigned threads, int kb,
+                             int stages);
 
 /* The hipStream_t every op is issued on (for hipEvent timing). */
 void *sepia_hip_stream(void);

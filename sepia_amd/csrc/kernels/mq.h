@@ -240,11 +240,17 @@ __device__ __forceinline__ uint32_t mq_lds_addr(const void *p) {
 // M0 holds the LDS address: the "{m0}" operand lets the compiler write it.
 // The base is uniform by construction; readfirstlane states it, so that the
 // "s" operand never depends on the compiler's uniformity analysis.
+// Wait states: the compiler's hazard recognizer does not look into an asm
+// statement, so the asm carries its own. On gfx9 a VMEM instruction that
+// reads an SGPR a VALU instruction wrote (v_readfirstlane, when the base
+// was in VGPRs) needs 5 wait states, and one that reads M0 after an SALU
+// write of it needs 1: s_nop 4 gives the 5 whatever precedes the asm.
+#define SEPIA_DMA_WAIT "s_nop 4\n\t"
 __device__ __forceinline__ void mq_dma16(const uint8_t *base, uint32_t voff, uint32_t lds) {
     const uint64_t b = (uint64_t)(uintptr_t)base;
     const uint64_t bs = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(b >> 32)) << 32) |
                         (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)b);
-    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"((const uint8_t *)(uintptr_t)bs), "{m0}"(lds) : "memory");
+    asm volatile(SEPIA_DMA_WAIT "global_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"((const uint8_t *)(uintptr_t)bs), "{m0}"(lds) : "memory");
 }
 // s_waitcnt immediates (gfx9 encoding): vmcnt(n) alone, and lgkmcnt(0) alone.
 __device__ __forceinline__ constexpr int mq_wc_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }

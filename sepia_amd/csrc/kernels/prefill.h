@@ -268,12 +268,14 @@ __device__ __forceinline__ const uint8_t *pf_uniform(const void *p) {
                                          << 32) |
                                         (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)b));
 }
-// LDS DMA: lane l's 16 (or 4) bytes at base + voff land at lds + 16 l (4 l).
+// LDS DMA: lane l's 16 (or 4) bytes at base + voff land at lds + 16 l (4 l),
+// after the five wait states of SEPIA_DMA_WAIT (mq.h: a VALU write of the
+// base's SGPRs or an SALU write of M0 may come right before the asm).
 __device__ __forceinline__ void pf_dma16(const void *base, uint32_t voff, uint32_t lds) {
-    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"(pf_uniform(base)), "{m0}"(lds) : "memory");
+    asm volatile(SEPIA_DMA_WAIT "global_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"(pf_uniform(base)), "{m0}"(lds) : "memory");
 }
 __device__ __forceinline__ void pf_dma4(const void *base, uint32_t voff, uint32_t lds) {
-    asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, %1" : : "v"(voff), "s"(pf_uniform(base)), "{m0}"(lds) : "memory");
+    asm volatile(SEPIA_DMA_WAIT "global_load_lds_dword %0, %1" : : "v"(voff), "s"(pf_uniform(base)), "{m0}"(lds) : "memory");
 }
 __device__ __forceinline__ uint32_t pf_swz(int r, int chunk) { return (uint32_t)r * 512u + ((uint32_t)(chunk ^ (r & 15)) << 4); }
 

@@ -274,3 +274,65 @@ SEPIA_MQ_MV(iq4_xs, ST_IQ4_XS)
 SEPIA_MQ_MV(q8_0, ST_Q8_0)
 SEPIA_MQ_GATEUP()
 SEPIA_MQ_DOWN()
+
+// ------------------------------------------------------------------------
+// HBM read ceiling through the decode kernels' own staging path: every wave
+// streams its steps of KB KB (KB wave-wide 16-byte LDS DMAs) through a
+// private ring of S stages, as MqWave does -- wait for the oldest stage,
+// read it back (one 16-byte word per lane per KB), refill it -- with no
+// decode. Workgroup b reads the contiguous chunk b of the n16 16-byte words;
+// its waves take its steps round robin. Lanes past the chunk's end read its
+// last word (every DMA is whole and in bounds). LDS: nw * S * KB KB.
+template <int KB, int S>
+__device__ __forceinline__ void read_probe_dma(const uint4 *__restrict__ p, int64_t n16, uint32_t *__restrict__ sink) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int nw = (int)(blockDim.x >> 6), w = mq_wave_id(), lane = (int)(threadIdx.x & 63);
+    const int64_t per = (n16 + gridDim.x - 1) / gridDim.x;
+    const int64_t b = (int64_t)blockIdx.x * per, e = b + per < n16 ? b + per : n16;
+    if (b >= e) return;
+    const int64_t steps = (e - b + 64 * KB - 1) / (64 * KB);
+    const int Tn = steps > w ? (int)((steps - w + nw - 1) / nw) : 0;
+    uint8_t *ring = smem + (size_t)w * S * KB * 1024;
+    const uint32_t rl = mq_lds_addr(ring);
+    const uint8_t *pb = (const uint8_t *)(p + b);
+    auto issue = [&](int t) {   // step t of this wave into ring slot t % S (32-bit offsets within the chunk)
+        const int64_t s = w + (int64_t)t * nw;
+        const uint32_t slot = (uint32_t)(t % S) * (uint32_t)(KB * 1024);
+#pragma unroll
+        for (int d = 0; d < KB; d++) {
+            int64_t j = s * 64 * KB + (int64_t)d * 64 + lane;
+            j = j < e - b ? j : e - b - 1;
+            mq_dma16(pb, (uint32_t)(16 * j), rl + slot + 1024u * (uint32_t)d);
+        }
+    };
+    for (int t = 0; t < S && t < Tn; t++) issue(t);
+    uint32_t acc = 0;
+    for (int t = 0; t < Tn; t++) {
+        const int after = (Tn - 1 - t) < (S - 1) ? (Tn - 1 - t) : (S - 1);
+        mq_wait_stages<KB>(after);
+        const uint8_t *src = ring + (size_t)(t % S) * (KB * 1024) + 16 * lane;
+        uint4 v[KB];
+#pragma unroll
+        for (int d = 0; d < KB; d++) v[d] = *(const uint4 *)(src + 1024 * d);
+        __builtin_amdgcn_s_waitcnt(MQ_WC_LGKM0);
+        if (t + S < Tn) issue(t + S);
+#pragma unroll
+        for (int d = 0; d < KB; d++) acc ^= v[d].x ^ v[d].y ^ v[d].z ^ v[d].w;
+    }
+    if (acc == 0x9E3779B9u) sink[blockIdx.x] = acc;
+}
+
+extern "C" __global__ __launch_bounds__(1024) void sepia_read_probe_dma(const uint4 *__restrict__ p, int64_t n16,
+                                                                       uint32_t *__restrict__ sink, int32_t kb,
+                                                                       int32_t s) {
+    switch (kb * 8 + s) {
+    case 7 * 8 + 1: read_probe_dma<7, 1>(p, n16, sink); break;
+    case 7 * 8 + 2: read_probe_dma<7, 2>(p, n16, sink); break;
+    case 4 * 8 + 1: read_probe_dma<4, 1>(p, n16, sink); break;
+    case 4 * 8 + 2: read_probe_dma<4, 2>(p, n16, sink); break;
+    case 4 * 8 + 4: read_probe_dma<4, 4>(p, n16, sink); break;
+    case 2 * 8 + 4: read_probe_dma<2, 4>(p, n16, sink); break;
+    case 1 * 8 + 4: read_probe_dma<1, 4>(p, n16, sink); break;
+    default: break;
+    }
+}

@@ -68,7 +68,7 @@ enum {
     /* prefill projections of Q2_K / Q3_K / Q4_K on the int8 matrix cores (kernels/prefill_q.h) */
     K_PF_QUANT, K_PF_GATEUP_Q, K_PF_DOWN_Q,
     /* HBM read ceiling probe (measurement) */
-    K_READ_PROBE,
+    K_READ_PROBE, K_READ_PROBE_DMA,
     K_COUNT
 };
 #define FFN_NAMES(p) "sepia_ffn_gateup_" p, "sepia_ffn_gateup_" p "_xp", "sepia_ffn_down_" p
@@ -95,7 +95,7 @@ static const char *const k_names[K_COUNT] = {
     "sepia_pf_split", "sepia_pf_route_m", "sepia_fill_u32",
     "sepia_rel_project_f32", "sepia_attn_partial", "sepia_attn_combine",
     "sepia_pf_quant", "sepia_pf_gateup_q", "sepia_pf_down_q",
-    "sepia_read_probe",
+    "sepia_read_probe", "sepia_read_probe_dma",
 };
 #undef FFN_NAMES
 
@@ -997,6 +997,30 @@ int sepia_hip_read_probe(SepiaGpuBuf *buf, size_t off, size_t bytes, unsigned gr
     int64_t n16 = (int64_t)(bytes / 16);
     void *args[] = { &p, &n16, &sink };
     return launch(K_READ_PROBE, grid, 256, args, op);
+}
+
+int sepia_hip_read_probe_dma(SepiaGpuBuf *buf, size_t off, size_t bytes, unsigned grid, unsigned threads, int kb,
+                             int stages) {
+    const char *op = "read_probe_dma";
+    const int shape = kb * 8 + stages;
+    const size_t lds = (size_t)(threads / 64) * (size_t)stages * (size_t)kb * 1024;
+    if (!buf || bytes == 0 || bytes % 16 || off % 16 || grid == 0 || grid > MAX_GRID || threads < 64 ||
+        threads > 1024 || threads % 64 ||
+        !(shape == 7 * 8 + 1 || shape == 7 * 8 + 2 || shape == 4 * 8 + 1 || shape == 4 * 8 + 2 ||
+          shape == 4 * 8 + 4 || shape == 2 * 8 + 4 || shape == 1 * 8 + 4) ||
+        lds > g_lds_max || (bytes / grid + 16) >= (1ull << 32)) {
+        LOG("%s: invalid arguments (16-byte aligned offset and size, 1 <= grid <= %d, 64..1024 threads in whole "
+            "waves, (kb, stages) one of (7,1) (7,2) (4,1) (4,2) (4,4) (2,4) (1,4) within the LDS)", op, MAX_GRID);
+        return 0;
+    }
+    if (!chk(buf, off, bytes, op, "buf") || !need_batch(op) || !prep_in_r(buf, off, bytes, op)) return 0;
+    uint32_t *sink = (uint32_t *)scratch((size_t)grid * 4, op);
+    if (!sink) return 0;
+    const uint8_t *p = buf->dev + off;
+    int64_t n16 = (int64_t)(bytes / 16);
+    int32_t kb32 = kb, s32 = stages;
+    void *args[] = { &p, &n16, &sink, &kb32, &s32 };
+    return launch_lds(K_READ_PROBE_DMA, grid, threads, lds, args, op);
 }
 
 int sepia_gpu_softmax(SepiaGpuBuf *x, SepiaGpuBuf *y, int64_t rows, int64_t n) {

@@ -100,6 +100,7 @@ PROTOTYPES = {
     "sepia_hip_scratch_bytes": (ctypes.c_size_t, []),
     "sepia_hip_alloc_count": (ctypes.c_uint64, []),
     "sepia_hip_read_probe": (_I, [_P, _SZ, _SZ, ctypes.c_uint]),
+    "sepia_hip_read_probe_dma": (_I, [_P, _SZ, _SZ, ctypes.c_uint, ctypes.c_uint, _I, _I]),
     "sepia_hip_stream": (_P, []),
     "sepia_hip_set_option": (_I, [ctypes.c_char_p, _I]),
     # the on-disk stores (store.c)

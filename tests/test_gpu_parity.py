@@ -364,6 +364,17 @@ def test_read_probe(dev):
         assert L.sepia_hip_read_probe(b, 0, 4100, 4) == 0             # size not a multiple of 16
         assert L.sepia_hip_read_probe(b, 16, data.nbytes, 4) == 0     # past the end
         assert L.sepia_hip_read_probe(b, 0, 4096, 0) == 0             # no workgroups
+        # through LDS-DMA rings: every allowed shape, chunks that do not
+        # fill their last step, more workgroups than steps
+        for kb, st, thr in ((7, 1, 1024), (7, 2, 512), (4, 1, 1024), (4, 2, 1024), (4, 4, 512), (2, 4, 1024),
+                            (1, 4, 1024)):
+            assert L.sepia_hip_read_probe_dma(b, 0, data.nbytes, 256, thr, kb, st) == 1
+            assert L.sepia_hip_read_probe_dma(b, 4096, 65536 + 48, 7, thr, kb, st) == 1
+            assert L.sepia_hip_read_probe_dma(b, 0, 4096, 64, thr, kb, st) == 1
+        assert L.sepia_hip_read_probe_dma(b, 0, 4096, 4, 1024, 7, 2) == 0   # rings beyond the LDS
+        assert L.sepia_hip_read_probe_dma(b, 0, 4096, 4, 256, 3, 1) == 0    # no such shape
+        assert L.sepia_hip_read_probe_dma(b, 0, 4096, 4, 100, 4, 1) == 0    # not whole waves
+        assert L.sepia_hip_read_probe_dma(b, 16, data.nbytes, 4, 256, 4, 1) == 0   # past the end
     finally:
         assert L.sepia_gpu_end() == 1
     assert np.array_equal(dev.download(b, data.size, dtype=np.uint32), data)
