@@ -629,7 +629,7 @@ def run_c5(B, warmup, steps, cpu_seconds, T=512, types=C3_TYPES):
     """the MoE layer for a batch of T tokens (prefill) with all 256 routed +
     2 shared experts resident, x ~ N(0,1) rounded to bf16-representable f32. types: the layer's
     formats (C3_TYPES: Q2_K / Q3_K routed, Q4_K shared, the int8 kernels; REAL_TYPES: the real
-    checkpoint's IQ2_XS / IQ3_XXS routed, Q5_K / Q6_K shared, the bf16 kernels)."""
+    checkpoint's IQ2_XS / IQ3_XXS routed, Q5_K / Q6_K shared, the f16 kernels)."""
     L = B.L
     layers, host_router, sizes = build_moe_layers(B, 1, types)
     H, I, NR, NS, gb, db, sgb, sdb, _ = sizes
@@ -649,7 +649,7 @@ def run_c5(B, warmup, steps, cpu_seconds, T=512, types=C3_TYPES):
     ms = B.timed_steps(step, warmup, steps)
     knames = ["sepia_pf_route", "sepia_pf_route_m", "sepia_pf_select", "sepia_pf_group", "sepia_pf_split",
               "sepia_pf_gateup", "sepia_pf_down", "sepia_pf_combine", "sepia_pf_quant", "sepia_pf_gateup_q",
-              "sepia_pf_down_q"]
+              "sepia_pf_down_q", "sepia_ph_quant", "sepia_ph_gateup", "sepia_ph_down"]
     kms = B.kernel_ms(step, min(steps, 5), knames)
     n_sel = 6 + NS
     route = B.dev.alloc(T * (6 + n_sel) * 4)

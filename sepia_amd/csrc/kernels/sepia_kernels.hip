@@ -258,6 +258,7 @@ SEPIA_FFN_PAIR(4, 4, ST_Q4_K, ST_Q4_K)
 #include "moe.h"
 #include "prefill.h"
 #include "prefill_q.h"
+#include "prefill_h.h"
 #include "synth.h"
 #include "attn.h"
 

@@ -67,6 +67,8 @@ enum {
     K_REL_PROJECT, K_ATTN_PARTIAL, K_ATTN_COMBINE,
     /* prefill projections of Q2_K / Q3_K / Q4_K on the int8 matrix cores (kernels/prefill_q.h) */
     K_PF_QUANT, K_PF_GATEUP_Q, K_PF_DOWN_Q,
+    /* prefill projections of the real checkpoint's formats on the f16 matrix cores (kernels/prefill_h.h) */
+    K_PH_QUANT, K_PH_GATEUP, K_PH_DOWN,
     /* HBM read ceiling probe (measurement) */
     K_READ_PROBE, K_READ_PROBE_DMA,
     K_COUNT
@@ -95,6 +97,7 @@ static const char *const k_names[K_COUNT] = {
     "sepia_pf_split", "sepia_pf_route_m", "sepia_fill_u32",
     "sepia_rel_project_f32", "sepia_attn_partial", "sepia_attn_combine",
     "sepia_pf_quant", "sepia_pf_gateup_q", "sepia_pf_down_q",
+    "sepia_ph_quant", "sepia_ph_gateup", "sepia_ph_down",
     "sepia_read_probe", "sepia_read_probe_dma",
 };
 #undef FFN_NAMES
@@ -162,6 +165,10 @@ static int g_opt_pf_route_m = 1;   /* "pf_route_m": 1 = prefill router logits on
                                     * (sepia_pf_route_m) when x and the router rows are 16-byte aligned
                                     * and hidden is a multiple of 512,
                                     * 0 = sepia_pf_route */
+static int g_opt_pf_h = 1;   /* "pf_h": 1 = a prefill layer whose six projections all have formats of the
+                              * real checkpoint (IQ2_XS, IQ3_XXS, IQ4_XS, Q5_K, Q6_K, Q8_0) runs them on the
+                              * f16 matrix cores (sepia_ph_quant, sepia_ph_gateup, sepia_ph_down); 0 = the
+                              * bf16 kernels */
 static int g_opt_pf_q = 1;   /* "pf_q": 1 = a prefill layer whose six projections are all Q2_K, Q3_K or Q4_K
                               * runs them on the int8 matrix cores (sepia_pf_quant, sepia_pf_gateup_q,
                               * sepia_pf_down_q); 0 = the bf16 kernels sepia_pf_gateup / _down, which
@@ -1266,6 +1273,10 @@ int sepia_hip_set_option(const char *name, int value) {
         g_opt_mq_x = value;
         return 1;
     }
+    if (strcmp(name, "pf_h") == 0 && (value == 0 || value == 1)) {
+        g_opt_pf_h = value;
+        return 1;
+    }
     if (strcmp(name, "pf_q") == 0 && (value == 0 || value == 1)) {
         g_opt_pf_q = value;
         return 1;
@@ -1874,6 +1885,10 @@ static int pf_type_ok(int t) {
 }
 /* Formats of the int8 prefill projections (kernels/prefill_q.h): Q2_K, Q3_K, Q4_K. */
 static int pf_type_int(int t) { return t == SEPIA_T_Q2_K || t == SEPIA_T_Q3_K || t == 12; }
+/* Formats of the f16 prefill projections (kernels/prefill_h.h): the real
+ * checkpoint's IQ2_XS, IQ3_XXS, IQ4_XS, Q5_K, Q6_K and Q8_0. */
+static int pf_type_h(int t) { return t == 17 || t == 18 || t == 23 || t == 13 || t == 14 || t == 8; }
+#define PH_REC 1056   /* bytes of a 256-column PH record (kernels/prefill_h.h) */
 
 int sepia_gpu_moe_prefill(const SepiaMoeLayerDesc *L, int64_t n_tokens, SepiaGpuBuf *x, SepiaGpuBuf *y,
                           SepiaGpuBuf *route_out) {
@@ -1903,8 +1918,19 @@ int sepia_gpu_moe_prefill(const SepiaMoeLayerDesc *L, int64_t n_tokens, SepiaGpu
                    !moe_proj(op, "shared down", &L->s_down, ns, H, I, &sd)))
         return 0;
     const MoeProj *ps[6] = { &g, &u, &d, &sg, &su, &sd };
+    /* 4-byte-aligned rows everywhere (the int8 and f16 paths stage blocks
+     * from 4-byte boundaries) */
+    int q_aligned = 1;
     for (int i = 0; i < (ns > 0 ? 6 : 3); i++)
-        if (!pf_type_ok(ps[i]->type) || ((uintptr_t)ps[i]->base | ps[i]->stride | ps[i]->row_bytes) & 1) {
+        if (((uintptr_t)ps[i]->base | ps[i]->stride | ps[i]->row_bytes) & 3) q_aligned = 0;
+    /* f16 path: every projection in the real checkpoint's formats, 4-byte
+     * aligned rows (activations as PH rows: kernels/prefill_h.h, 1056 bytes
+     * per 256 columns); Q8_0 has no other prefill kernels */
+    const int use_h_all = g_opt_pf_h && q_aligned && pf_type_h(g.type) && pf_type_h(d.type) &&
+                          (ns == 0 || (pf_type_h(sg.type) && pf_type_h(sd.type)));
+    for (int i = 0; i < (ns > 0 ? 6 : 3); i++)
+        if (!(pf_type_ok(ps[i]->type) || (use_h_all && pf_type_h(ps[i]->type))) ||
+            ((uintptr_t)ps[i]->base | ps[i]->stride | ps[i]->row_bytes) & 1) {
             LOG("%s: projection %d: ggml type %d or its layout is not supported by the prefill kernels", op, i,
                 ps[i]->type);
             return 0;
@@ -1932,16 +1958,15 @@ int sepia_gpu_moe_prefill(const SepiaMoeLayerDesc *L, int64_t n_tokens, SepiaGpu
      * rows (its DMA stages Q2_K and Q4_K blocks from their own starts);
      * activations as PQ rows (kernels/prefill_q.h: 832 bytes per 256
      * columns) */
-    int q_aligned = 1;
-    for (int i = 0; i < (ns > 0 ? 6 : 3); i++)
-        if (((uintptr_t)ps[i]->base | ps[i]->stride | ps[i]->row_bytes) & 3) q_aligned = 0;
     const int use_q = g_opt_pf_q && q_aligned && pf_type_int(g.type) && pf_type_int(d.type) &&
                       (ns == 0 || (pf_type_int(sg.type) && pf_type_int(sd.type)));
-    const int64_t ldqx = H / 256 * 832, ldqh = I / 256 * 832;
+    const int use_h = !use_q && use_h_all;
+    const int64_t ldqx = H / 256 * (use_h ? PH_REC : 832), ldqh = I / 256 * (use_h ? PH_REC : 832);
+    const int use_qh = use_q || use_h;
     /* the pipelines address activation rows with 32-bit byte offsets */
     if (umax > 65535 || (H + 255) / 256 > MAX_GRID || (uint64_t)T * H * 2 >= (1ull << 32) ||
         (uint64_t)P * I * 2 >= (1ull << 32) || (T * H + 255) / 256 > MAX_GRID || P > MAX_GRID ||
-        (use_q && ((uint64_t)T * ldqx >= (1ull << 32) || (uint64_t)P * ldqh >= (1ull << 32)))) {
+        (use_qh && ((uint64_t)T * ldqx >= (1ull << 32) || (uint64_t)P * ldqh >= (1ull << 32)))) {
         LOG("%s: batch too large", op);
         return 0;
     }
@@ -1955,15 +1980,15 @@ int sepia_gpu_moe_prefill(const SepiaMoeLayerDesc *L, int64_t n_tokens, SepiaGpu
     PF_REGION(o_list, P * 4);
     PF_REGION(o_units, umax * 12);
     PF_REGION(o_nu, 4);   /* n_units */
-    PF_REGION(o_xh, use_q ? 0 : T * H * 2);
-    PF_REGION(o_xl, use_q ? 0 : T * H * 2);
-    PF_REGION(o_hh, use_q ? 0 : P * I * 2);
-    PF_REGION(o_hl, use_q ? 0 : P * I * 2);
-    PF_REGION(o_pqx, use_q ? T * ldqx : 0);
-    PF_REGION(o_pqxs, use_q ? T * 4 : 0);
-    PF_REGION(o_hf, use_q ? P * I * 4 : 0);
-    PF_REGION(o_pqh, use_q ? P * ldqh : 0);
-    PF_REGION(o_pqhs, use_q ? P * 4 : 0);
+    PF_REGION(o_xh, use_qh ? 0 : T * H * 2);
+    PF_REGION(o_xl, use_qh ? 0 : T * H * 2);
+    PF_REGION(o_hh, use_qh ? 0 : P * I * 2);
+    PF_REGION(o_hl, use_qh ? 0 : P * I * 2);
+    PF_REGION(o_pqx, use_qh ? T * ldqx : 0);
+    PF_REGION(o_pqxs, use_qh ? T * 4 : 0);
+    PF_REGION(o_hf, use_qh ? P * I * 4 : 0);
+    PF_REGION(o_pqh, use_qh ? P * ldqh : 0);
+    PF_REGION(o_pqhs, use_qh ? P * 4 : 0);
     PF_REGION(o_yp, P * H * 4);
 #undef PF_REGION
     uint8_t *s = (uint8_t *)scratch(o, op);
@@ -1990,18 +2015,27 @@ int sepia_gpu_moe_prefill(const SepiaMoeLayerDesc *L, int64_t n_tokens, SepiaGpu
     if (!launch(K_PF_SELECT, (unsigned)T, 64, a_sel, op)) return 0;
     void *a_grp[] = { &sel_idx, &tt, &nr32, &ns32, &tk32, &list, &units, &n_units };
     if (!launch(K_PF_GROUP, 1, 1024, a_grp, op)) return 0;
-    if (use_q) {
+    if (use_qh) {
+        /* int8 (PQ rows) or f16 (PH rows): quantize x, gate/up to f32 h,
+         * quantize h, down to the per-pair partial rows. The f16 gate/up
+         * runs over 64-row slices of I, its down over 128-row slices of H
+         * (256-row formats take every other slice). */
         void *pqx = s + o_pqx, *pqxs = s + o_pqxs, *hf = s + o_hf, *pqh = s + o_pqh, *pqhs = s + o_pqhs;
         int64_t ldq_x = ldqx, ldq_h = ldqh;
+        const int kq = use_q ? K_PF_QUANT : K_PH_QUANT;
         void *a_qx[] = { &x->dev, &hid, &hid, &pqx, &ldq_x, &pqxs };
-        if (!launch(K_PF_QUANT, (unsigned)T, 256, a_qx, op)) return 0;
+        if (!launch(kq, (unsigned)T, 256, a_qx, op)) return 0;
         void *a_gq[] = { (void *)&g, (void *)&u, (void *)&sg, (void *)&su, &nr32, &nsel32, &inter, &hid,
                          &pqx, &pqxs, &list, &units, &n_units, &hf };
-        if (!launch2(K_PF_GATEUP_Q, (unsigned)(I / 128), (unsigned)umax, 512, PF_LDS_BYTES, a_gq, op)) return 0;
+        if (!launch2(use_q ? K_PF_GATEUP_Q : K_PH_GATEUP, (unsigned)(use_q ? I / 128 : I / 64), (unsigned)umax, 512,
+                     PF_LDS_BYTES, a_gq, op))
+            return 0;
         void *a_qh[] = { &hf, &inter, &inter, &pqh, &ldq_h, &pqhs };
-        if (!launch(K_PF_QUANT, (unsigned)P, 256, a_qh, op)) return 0;
+        if (!launch(kq, (unsigned)P, 256, a_qh, op)) return 0;
         void *a_dq[] = { (void *)&d, (void *)&sd, &nr32, &inter, &hid, &pqh, &pqhs, &list, &units, &n_units, &yp };
-        if (!launch2(K_PF_DOWN_Q, (unsigned)(H / 256), (unsigned)umax, 512, PF_LDS_BYTES, a_dq, op)) return 0;
+        if (!launch2(use_q ? K_PF_DOWN_Q : K_PH_DOWN, (unsigned)(use_q ? H / 256 : H / 128), (unsigned)umax, 512,
+                     PF_LDS_BYTES, a_dq, op))
+            return 0;
     } else {
         int64_t nseg = T * H / 16;
         void *a_sp[] = { &x->dev, &nseg, &xh, &xl };

@@ -90,16 +90,19 @@ def test_moe_decode_nan_x(dev, orc, types):
         dev.free(b)
 
 
-@pytest.mark.parametrize("pf_q", [1, 0], ids=["int8", "bf16"])
-def test_moe_prefill_nonfinite_token(dev, orc, pf_q):
+@pytest.mark.parametrize("kind", ["int8", "f16", "bf16"])
+def test_moe_prefill_nonfinite_token(dev, orc, kind):
     """One token of the batch with an infinity: its output row is
     non-finite; every other token's row is bitwise what it is when that
-    token is finite (each output element is its own dot product)."""
+    token is finite (each output element is its own dot product). int8: a
+    Q2_K / Q3_K / Q4_K layer on the int8 kernels; f16: a layer of the real
+    checkpoint's formats on the f16 kernels; bf16: the Q2_K layer on the bf16
+    kernels."""
     rng = np.random.default_rng(12)
-    desc, spec, bufs = make_layer(dev, rng, hidden=2048, inter=1024, n_routed=16, n_shared=2,
-                                  tg=10, tu=10, td=11, ts=12)
+    types = dict(tg=17, tu=17, td=18, ts=13, tsd=14) if kind == "f16" else dict(tg=10, tu=10, td=11, ts=12)
+    desc, spec, bufs = make_layer(dev, rng, hidden=2048, inter=1024, n_routed=16, n_shared=2, **types)
     X = rng.standard_normal((24, 2048)).astype(np.float32)
-    assert dev.L.sepia_hip_set_option(b"pf_q", pf_q) == 1
+    assert dev.L.sepia_hip_set_option(b"pf_q", 0 if kind == "bf16" else 1) == 1
     try:
         y0, _, _ = run_prefill(dev, desc, X)
         Xb = X.copy()

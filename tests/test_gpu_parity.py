@@ -908,14 +908,19 @@ PREFILL_CASES = [
     ((2048, 1024, 12, 1), (17, 18, 14), 33),      # IQ2_XS / IQ3_XXS routed, Q6_K shared
     ((1024, 2048, 8, 2), (13, 23, 11), 20),       # Q5_K / IQ4_XS routed, Q3_K shared (bf16 kernels)
     ((2048, 1024, 12, 1), (11, 10, 10), 37),      # Q3_K / Q2_K routed, Q2_K shared
-    # the real checkpoint's format mixes (bf16 kernels)
+    # the real checkpoint's format mixes (the f16 kernels on the default path)
     ((6144, 3072, 16, 2), (17, 18, 13, 14), 48),  # IQ2_XS / IQ3_XXS routed, Q5_K / Q6_K shared
     ((2048, 1024, 12, 2), (17, 23, 13, 14), 40),  # IQ4_XS down
     ((1024, 2048, 8, 2), (13, 14, 13, 14), 20),   # Q5_K / Q6_K routed
 ]
+# Layers with Q8_0 projections: the f16 kernels only (no bf16 kernel takes Q8_0).
+PREFILL_CASES_Q8 = [
+    ((2048, 1024, 12, 2), (18, 18, 8, 8), 37),    # IQ3_XXS gate/up (layer 65), Q8_0 shared
+    ((2048, 1024, 8, 1), (8, 23, 8, 14), 9),      # Q8_0 routed, one M tile per unit
+]
 
 
-PF_PATHS = {"q": dict(pf_q=1, pf_route_m=1), "tile": dict(pf_q=0, pf_route_m=0)}
+PF_PATHS = {"q": dict(pf_q=1, pf_h=1, pf_route_m=1), "tile": dict(pf_q=0, pf_h=0, pf_route_m=0)}
 
 
 @pytest.mark.parametrize("path", ["q", "tile"])
@@ -925,11 +930,12 @@ def test_moe_prefill(dev, orc, shape, types, T, x_kind, path):
     """Every token of the batch against the oracle's single-token layer (its
     own routing, near-ties per the reference protocol); two runs bitwise equal.
     x either bf16-representable or full f32. path: a layer of Q2_K / Q3_K /
-    Q4_K projections on the int8 matrix cores (q, the default; option pf_q)
-    or on the bf16 kernels with bit-exact dequantized weights (tile; pf_q 0,
-    which also runs the router on sepia_pf_route, pf_route_m 0). Layers with
-    other formats (the real checkpoint's IQ2_XS, IQ3_XXS, IQ4_XS, Q5_K and
-    Q6_K mixes among them) take the bf16 kernels on both paths."""
+    Q4_K projections on the int8 matrix cores, and a layer of the real
+    checkpoint's formats (IQ2_XS, IQ3_XXS, IQ4_XS, Q5_K, Q6_K) on the f16
+    ones (q, the default; options pf_q, pf_h), or either on the bf16 kernels
+    with bit-exact dequantized weights (tile; pf_q 0 and pf_h 0, which also
+    runs the router on sepia_pf_route, pf_route_m 0). Layers with other
+    format mixes take the bf16 kernels on both paths."""
     hidden, inter, n_routed, n_shared = shape
     tgu, td, ts = types[:3]
     tsd = types[3] if len(types) > 3 else None
@@ -953,6 +959,31 @@ def test_moe_prefill(dev, orc, shape, types, T, x_kind, path):
             y_ref, _, _, _ = orc.moe_layer(spec, X[t], force_idx=chosen, threads=THREADS)
         assert_close(y[t], y_ref, what="prefill %s token %d" % (types, t), gate=False)
     for b in bufs.values():
+        dev.free(b)
+
+
+@pytest.mark.parametrize("x_kind", ["bf16", "f32"])
+@pytest.mark.parametrize("shape,types,T", PREFILL_CASES_Q8, ids=lambda v: str(v))
+def test_moe_prefill_q8_0(dev, orc, shape, types, T, x_kind):
+    """Layers with Q8_0 projections on the f16 kernels (the default path)
+    against the oracle, two runs bitwise equal; with pf_h 0 the library
+    refuses them (no other prefill kernel takes Q8_0)."""
+    test_moe_prefill(dev, orc, shape, types, T, x_kind, "q")
+    rng = np.random.default_rng(5)
+    desc, _spec, bufs = make_layer(dev, rng, hidden=shape[0], inter=shape[1], n_routed=shape[2], n_shared=shape[3],
+                                   tg=types[0], tu=types[0], td=types[1], ts=types[2], tsd=types[3])
+    X = rng.standard_normal((4, shape[0])).astype(np.float32)
+    xb, yb = dev.shared_from(X), dev.alloc(X.nbytes)
+    assert dev.L.sepia_hip_set_option(b"pf_h", 0) == 1
+    try:
+        dev.begin()
+        try:
+            assert dev.L.sepia_gpu_moe_prefill(ctypes.byref(desc), 4, xb, yb, None) == 0
+        finally:
+            assert dev.L.sepia_gpu_end() == 1
+    finally:
+        dev.L.sepia_hip_set_option(b"pf_h", 1)
+    for b in list(bufs.values()) + [xb, yb]:
         dev.free(b)
 
 
