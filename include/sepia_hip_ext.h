@@ -75,11 +75,17 @@ int sepia_hip_moe_decode_noalloc(const SepiaMoeLayerDesc *layer, SepiaGpuBuf *x,
  * src/sepia.c:1377-1470 applied to each token): y[t] = MoE(x[t]) with each
  * token's routing exactly as sepia_gpu_moe_decode's up to the summation
  * order of the router's f32 dot products. Tokens are grouped by expert and
- * every expert's weights are read once per 32 tokens, on the bf16 matrix
- * cores (weights and activations as bf16 hi + lo pairs, f32 accumulate).
- * Projection formats: Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, IQ2_XS, IQ3_XXS,
- * IQ4_XS. x, y: f32 [n_tokens][hidden] at offset 0. route_out (optional):
- * int32 idx[n_tokens][topk] followed by f32 w[n_tokens][topk + n_shared]. */
+ * every expert's weights are read once per 32 tokens: a layer of Q2_K,
+ * Q3_K and Q4_K projections on the int8 matrix cores (activations as 23-bit
+ * digit planes, exact integer products), one of the real checkpoint's
+ * formats (IQ2_XS, IQ3_XXS, IQ4_XS, Q5_K, Q6_K, Q8_0) on the f16 ones
+ * (weights as exact f16 integer codes, activations as f16 hi + lo planes),
+ * any other mix of Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, IQ2_XS, IQ3_XXS, IQ4_XS on
+ * the bf16 ones (weights and activations as bf16 hi + lo pairs), all with
+ * f32 accumulation. Rows 4-byte aligned for the first two (else the bf16
+ * kernels; Q8_0 has no other). x, y: f32 [n_tokens][hidden] at offset 0.
+ * route_out (optional): int32 idx[n_tokens][topk] followed by f32
+ * w[n_tokens][topk + n_shared]. */
 int sepia_gpu_moe_prefill(const SepiaMoeLayerDesc *layer, int64_t n_tokens, SepiaGpuBuf *x, SepiaGpuBuf *y,
                           SepiaGpuBuf *route_out);
 
@@ -192,7 +198,12 @@ void *sepia_hip_stream(void);
  *                 between routed and shared experts (default 100);
  *   "pf_q" 1/0    prefill projections of layers whose six projections are
  *                 all Q2_K/Q3_K/Q4_K on the int8 matrix cores (1, default),
- *                 or on the bf16 kernels every other layer takes (0);
+ *                 or on the bf16 kernels (0);
+ *   "pf_h" 1/0    prefill projections of layers whose six projections are
+ *                 all in the real checkpoint's formats (IQ2_XS, IQ3_XXS,
+ *                 IQ4_XS, Q5_K, Q6_K, Q8_0) with 4-byte-aligned rows on the
+ *                 f16 matrix cores (1, default), or on the bf16 kernels (0;
+ *                 they take no Q8_0, so such layers are then refused);
  *   "pf_route_m" 1/0  prefill router logits on the f32 matrix cores when x
  *                 and the router rows are 16-byte aligned (default 1). */
 int sepia_hip_set_option(const char *name, int value);
