@@ -487,6 +487,37 @@ def run_ceiling(B):
     return out
 
 
+def run_ceiling_dma(B):
+    """The read of run_ceiling through the decode kernels' staging path (sepia_hip_read_probe_dma:
+    per-wave LDS-DMA rings, each stage waited for, read back and refilled, no compute) at the C3
+    down and gate/up sizes and C1's, for several grid / wave / ring shapes, with the plain probe at
+    three grids beside it. Per shape: average per-launch HIP-event time over copies rotated
+    through 1.6 GB."""
+    L = B.L
+    total = 1600 << 20
+    buf = B.private(total)
+    out = []
+    for label, nbytes in (("C3_down", 69894144), ("C3_gateup", 116785152), ("C1", 9437184)):
+        span = (nbytes + 4095) & ~4095
+        ncopy = max(1, min(total // span, 64))
+        n = max(24, 3 * ncopy)
+        for grid in (256, 1024, 8192):
+            us = B.kernel_ms(lambda i, g=grid: L.sepia_hip_read_probe(buf, (i % ncopy) * span, nbytes, g), n,
+                             ["sepia_read_probe"])["sepia_read_probe"] * 1e3
+            out.append(dict(size=label, probe="plain", grid=grid, threads=256, us=round(us, 2),
+                            tbs=round(nbytes / us / 1e6, 2)))
+        for grid, thr, kb, st in ((256, 1024, 7, 1), (256, 512, 7, 2), (256, 1024, 4, 1), (256, 1024, 4, 2),
+                                  (256, 512, 4, 4), (256, 1024, 2, 4), (256, 1024, 1, 4), (512, 512, 7, 1),
+                                  (512, 512, 4, 2), (1024, 256, 4, 2), (2048, 256, 4, 1)):
+            us = B.kernel_ms(lambda i, g=grid, t=thr, k=kb, s=st: L.sepia_hip_read_probe_dma(
+                buf, (i % ncopy) * span, nbytes, g, t, k, s), n, ["sepia_read_probe_dma"])["sepia_read_probe_dma"] * 1e3
+            out.append(dict(size=label, probe="dma", grid=grid, threads=thr, kb=kb, stages=st, us=round(us, 2),
+                            tbs=round(nbytes / us / 1e6, 2)))
+            log("ceiling_dma", json.dumps(out[-1]))
+    B.dev.free(buf)
+    return out
+
+
 def build_moe_layers(B, n_layers, types=C3_TYPES):
     """n_layers Inkling-shaped MoE layers resident in HBM: 256 routed experts (gate/up
     [3072x6144], down [6144x3072]) and 2 shared ones of the given formats (C3: Q2_K, Q3_K routed;
@@ -699,11 +730,13 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--only", choices=["c3", "real", "c2", "c1", "c4", "c5", "c5real", "store", "copy", "ceiling"],
+    ap.add_argument("--only", choices=["c3", "real", "c2", "c1", "c4", "c5", "c5real", "store", "copy", "ceiling",
+                                       "ceiling_dma"],
                     default=None,
                     help="run one configuration (profiling runs; 'copy': the library's f32 copy kernel over "
                          "256 MiB, the reference for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE; 'ceiling': the "
-                         "HBM read ceiling of a single launch at each kernel's size); default: all")
+                         "HBM read ceiling of a single launch at each kernel's size; 'ceiling_dma': the same read through "
+                         "the decode kernels' LDS-DMA staging path); default: all")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--timing", choices=["graph", "step-graphs", "eager"], default="graph",
                     help="how the timed steps are issued (see Bench.timed_steps)")
@@ -728,6 +761,8 @@ def main():
         ceil = run_ceiling(B)
         extra["hbm_read_ceiling"] = ceil
         log("ceiling", json.dumps(ceil))
+    if args.only == "ceiling_dma":
+        extra["hbm_read_ceiling_dma"] = run_ceiling_dma(B)
     if args.only in (None, "c3"):
         res = run_c3(B, args.warmup, args.steps, min(8.0, args.cpu_seconds))
         log("C3 %.2f us/token %.1f GB/s (%.1f%%) in %.0fs" % (res["us_per_token"], res["gbs"],
