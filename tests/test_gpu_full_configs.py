@@ -14,6 +14,10 @@ token's selection against the oracle (near-ties per the reference's
 protocol) and y against the oracle's single-token layer, for all 512 tokens
 with the plain router (bf16-representable and full f32 x).
 
+The real checkpoint's formats at the same size: IQ2_XS gate/up and IQ3_XXS
+down routed, Q5_K gate/up and Q6_K down shared (docs/gguf-inventory-ud-q2_k_xl.md
+in the reference): C3-shape decode, and C5 on the f16 prefill kernels.
+
 Weights are generated on the GPU (sepia_hip_synth_blocks); only the experts
 a checked token selects are copied back for the oracle.
 """
@@ -24,15 +28,15 @@ import numpy as np
 import pytest
 
 from sepia_amd import hip, synth
-from test_gpu_parity import assert_close, check_route
+from test_gpu_parity import Launches, assert_close, check_route
 
 pytestmark = pytest.mark.gpu
 
 THREADS = min(16, os.cpu_count() or 1)
 H, I, NR, NS, TOPK = 6144, 3072, 256, 2, 6
-Q2_K, Q3_K, Q4_K = 10, 11, 12
-GB, DB = synth.row_bytes(Q2_K, H) * I, synth.row_bytes(Q3_K, I) * H
-SGB, SDB = synth.row_bytes(Q4_K, H) * I, synth.row_bytes(Q4_K, I) * H
+Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, IQ2_XS, IQ3_XXS = 10, 11, 12, 13, 14, 17, 18
+C3_TYPES = (Q2_K, Q3_K, Q4_K, Q4_K)          # gate/up, down, shared gate/up, shared down
+REAL_TYPES = (IQ2_XS, IQ3_XXS, Q5_K, Q6_K)
 # constructed ties (expert ids; lane l of the selecting wave holds experts 4l .. 4l + 3)
 TIE_IN_LANE = (8, 10)        # lane 2, register slots 0 and 2
 TIE_ACROSS = (21, 100)       # lanes 5 and 25
@@ -65,19 +69,24 @@ def fetch(dev, buf, off, nbytes):
 
 
 class FullLayer:
-    """The C3 layer resident on the GPU, with a plain router and a router with
-    constructed ties over the same experts."""
+    """A full-size MoE layer resident on the GPU in the given formats, with a
+    plain router and a router with constructed ties over the same experts."""
 
-    def __init__(self, dev):
+    def __init__(self, dev, types=C3_TYPES):
         self.dev = dev
         L = dev.L
+        self.types = tg, td, tsg, tsd = types
+        self.gb, self.db = synth.row_bytes(tg, H) * I, synth.row_bytes(td, I) * H
+        self.sgb, self.sdb = synth.row_bytes(tsg, H) * I, synth.row_bytes(tsd, I) * H
+        GB, DB, SGB, SDB = self.gb, self.db, self.sgb, self.sdb
         self.bufs = dict(gate=dev.alloc(NR * GB, private=True), up=dev.alloc(NR * GB, private=True),
                          down=dev.alloc(NR * DB, private=True), s_gate=dev.alloc(NS * SGB, private=True),
                          s_up=dev.alloc(NS * SGB, private=True), s_down=dev.alloc(NS * SDB, private=True))
-        for k, t, nb, seed in (("gate", Q2_K, NR * I * H // 256, 71), ("up", Q2_K, NR * I * H // 256, 72),
-                               ("down", Q3_K, NR * H * I // 256, 73), ("s_gate", Q4_K, NS * I * H // 256, 74),
-                               ("s_up", Q4_K, NS * I * H // 256, 75), ("s_down", Q4_K, NS * H * I // 256, 76)):
-            dev.run(L.sepia_hip_synth_blocks, t, self.bufs[k], 0, nb, seed, synth.SCALE_LO, synth.SCALE_HI)
+        for k, t, n, seed in (("gate", tg, NR * I * H, 71), ("up", tg, NR * I * H, 72), ("down", td, NR * H * I, 73),
+                              ("s_gate", tsg, NS * I * H, 74), ("s_up", tsg, NS * I * H, 75),
+                              ("s_down", tsd, NS * H * I, 76)):
+            dev.run(L.sepia_hip_synth_blocks, t, self.bufs[k], 0, n // synth.GEOM[t][0], seed, synth.SCALE_LO,
+                    synth.SCALE_HI)
         rng = np.random.default_rng(2024)
         rw = (rng.standard_normal((NR + NS, H)) * 0.02).astype(np.float32)
         rb = rng.uniform(-0.1, 0.1, NR).astype(np.float32)
@@ -95,12 +104,12 @@ class FullLayer:
             d = hip.MoeLayerDesc(hidden=H, inter=I, n_routed=NR, n_shared=NS, topk=TOPK, route_scale=8.0,
                                  global_scale=1.0, router_w=self.bufs["rw_" + name],
                                  router_bias=self.bufs["rb_" + name])
-            d.gate = hip.ExpertTensor(self.bufs["gate"], 0, GB, Q2_K)
-            d.up = hip.ExpertTensor(self.bufs["up"], 0, GB, Q2_K)
-            d.down = hip.ExpertTensor(self.bufs["down"], 0, DB, Q3_K)
-            d.s_gate = hip.ExpertTensor(self.bufs["s_gate"], 0, SGB, Q4_K)
-            d.s_up = hip.ExpertTensor(self.bufs["s_up"], 0, SGB, Q4_K)
-            d.s_down = hip.ExpertTensor(self.bufs["s_down"], 0, SDB, Q4_K)
+            d.gate = hip.ExpertTensor(self.bufs["gate"], 0, GB, tg)
+            d.up = hip.ExpertTensor(self.bufs["up"], 0, GB, tg)
+            d.down = hip.ExpertTensor(self.bufs["down"], 0, DB, td)
+            d.s_gate = hip.ExpertTensor(self.bufs["s_gate"], 0, SGB, tsg)
+            d.s_up = hip.ExpertTensor(self.bufs["s_up"], 0, SGB, tsg)
+            d.s_down = hip.ExpertTensor(self.bufs["s_down"], 0, SDB, tsd)
             self.descs[name] = d
         self.shared = dict(s_gate=[fetch(dev, self.bufs["s_gate"], s * SGB, SGB) for s in range(NS)],
                            s_up=[fetch(dev, self.bufs["s_up"], s * SGB, SGB) for s in range(NS)],
@@ -110,9 +119,11 @@ class FullLayer:
     def spec(self, router, experts):
         """Oracle spec holding the bytes of the given routed experts."""
         rw, rb = self.routers[router]
+        tg, td, tsg, tsd = self.types
+        GB, DB = self.gb, self.db
         sp = dict(hidden=H, inter=I, n_routed=NR, n_shared=NS, topk=TOPK, route_scale=8.0, global_scale=1.0,
-                  router_w=rw, router_bias=rb, t_gate=Q2_K, t_up=Q2_K, t_down=Q3_K, ts_gate=Q4_K, ts_up=Q4_K,
-                  ts_down=Q4_K, gate=[None] * NR, up=[None] * NR, down=[None] * NR, **self.shared)
+                  router_w=rw, router_bias=rb, t_gate=tg, t_up=tg, t_down=td, ts_gate=tsg, ts_up=tsg,
+                  ts_down=tsd, gate=[None] * NR, up=[None] * NR, down=[None] * NR, **self.shared)
         for e in sorted(set(int(v) for v in experts)):
             if e not in self.cache:
                 self.cache[e] = (fetch(self.dev, self.bufs["gate"], e * GB, GB),
@@ -129,6 +140,13 @@ class FullLayer:
 @pytest.fixture(scope="module")
 def layer(dev):
     fl = FullLayer(dev)
+    yield fl
+    fl.close()
+
+
+@pytest.fixture(scope="module")
+def real_layer(dev):
+    fl = FullLayer(dev, REAL_TYPES)
     yield fl
     fl.close()
 
@@ -213,6 +231,54 @@ def test_c5_prefill_full(dev, orc, layer, router, x_kind):
         assert_close(Y[t], y_ref, what="C5 %s %s token %d" % (router, x_kind, t), gate=False)
         if n % 128 == 127:
             print("C5 %s %s: %d tokens checked" % (router, x_kind, n + 1), flush=True)
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_c3_real_types_decode_full(dev, orc, real_layer, seed):
+    """The C3 layer in the real checkpoint's formats at full size: selection
+    against the oracle, y within 1e-4 * ||y||_inf of the oracle's layer."""
+    rng = np.random.default_rng(seed + 20)
+    x = synth.normal_vector(rng, H)
+    y, idx, w = decode(dev, real_layer.descs["plain"], x)
+    rw, rb = real_layer.routers["plain"]
+    sp = real_layer.spec("plain", idx)
+    chosen = check_route(orc, sp, orc.linear_f32(rw, x), idx, w)
+    y_ref, _, _, _ = orc.moe_layer(sp, x, force_idx=chosen, threads=THREADS)
+    assert_close(y, y_ref, what="C3 real types seed %d" % seed, gate=False)
+
+
+@pytest.mark.timeout(600)
+def test_c5_real_types_prefill_full(dev, orc, real_layer):
+    """C5 in the real checkpoint's formats at full size on the f16 prefill
+    kernels (the default path for these formats): 512 tokens over all 256
+    routed experts, every token's selection and every token's y against the
+    oracle, so every unit of up to 32 pairs is checked, the shared experts'
+    16 units and each expert's last partial unit included."""
+    T = 512
+    rng = np.random.default_rng(57)
+    X = rng.standard_normal((T, H)).astype(np.float32)
+    X = (X.view(np.uint32) & np.uint32(0xFFFF0000)).view(np.float32)
+    n_sel = TOPK + NS
+    xb = dev.shared_from(X)
+    yb, rb = dev.alloc(X.nbytes), dev.alloc(T * (TOPK + n_sel) * 4)
+    with Launches(dev) as n:
+        dev.run(dev.L.sepia_gpu_moe_prefill, ctypes.byref(real_layer.descs["plain"]), T, xb, yb, rb)
+        assert n.count("sepia_ph_gateup") == 1 and n.count("sepia_ph_down") == 1
+    Y = dev.download(yb, T * H).reshape(T, H)
+    idx = dev.download(rb, T * TOPK, dtype=np.int32).reshape(T, TOPK)
+    w = dev.download(rb, T * n_sel, offset=T * TOPK * 4).reshape(T, n_sel)
+    for b in (xb, yb, rb):
+        dev.free(b)
+    rw, rb_h = real_layer.routers["plain"]
+    sp0 = dict(n_routed=NR, n_shared=NS, topk=TOPK, route_scale=8.0, global_scale=1.0, router_bias=rb_h)
+    chosen = [check_route(orc, sp0, orc.linear_f32(rw, X[t]), idx[t], w[t]) for t in range(T)]
+    assert len(set(idx.ravel().tolist())) >= 128
+    sp = real_layer.spec("plain", idx.ravel())
+    for t in range(T):
+        y_ref, _, _, _ = orc.moe_layer(sp, X[t], force_idx=chosen[t], threads=THREADS)
+        assert_close(Y[t], y_ref, what="C5 real types token %d" % t, gate=False)
+        if t % 128 == 127:
+            print("C5 real types: %d tokens checked" % (t + 1), flush=True)
 
 
 def test_decode_many_experts_em16(dev, orc):
