@@ -415,31 +415,61 @@ __device__ __forceinline__ void ph_proj(uint8_t *smem, const uint8_t *W0, const 
                 cb[t][mt] = pf_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
                 cb2[t][mt] = pf_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
             }
-#pragma unroll 2
-        for (int s = 0; s < 8; s++) {
-            PhB B[NT];
+        // Software-pipelined by one K step: step s + 1's codes (LDS
+        // gathers and their VALU) and activation planes are read before
+        // step s's matrix ops are issued (the scheduling barrier keeps that
+        // order), so the gathers' latency runs under the MFMAs.
+        PhB B[NT];
+        ph_h8 ah[MT], al[MT];
 #pragma unroll
-            for (int t = 0; t < NT; t++) B[t] = ph_decode<T>(blk[t], tab, signs, s, g);
+        for (int t = 0; t < NT; t++) B[t] = ph_decode<T>(blk[t], tab, signs, 0, g);
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) {
+            const uint8_t *ap = As + (16 * mt + n) * APB + 16 * g;
+            ah[mt] = *(const __attribute__((address_space(3))) ph_h8 *)(size_t)pf_lds(ap);
+            al[mt] = *(const __attribute__((address_space(3))) ph_h8 *)(size_t)pf_lds(ap + 512);
+        }
+#pragma unroll
+        for (int s = 0; s < 8; s++) {
+            PhB Bn[NT];
+            ph_h8 ahn[MT], aln[MT];
+            if (s + 1 < 8) {
+#pragma unroll
+                for (int t = 0; t < NT; t++) Bn[t] = ph_decode<T>(blk[t], tab, signs, s + 1, g);
+#pragma unroll
+                for (int mt = 0; mt < MT; mt++) {
+                    const uint8_t *ap = As + (16 * mt + n) * APB + 64 * (s + 1) + 16 * g;
+                    ahn[mt] = *(const __attribute__((address_space(3))) ph_h8 *)(size_t)pf_lds(ap);
+                    aln[mt] = *(const __attribute__((address_space(3))) ph_h8 *)(size_t)pf_lds(ap + 512);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int mt = 0; mt < MT; mt++) {
-                const uint8_t *ap = As + (16 * mt + n) * APB + 64 * s + 16 * g;
-                const ph_h8 ah = *(const __attribute__((address_space(3))) ph_h8 *)(size_t)pf_lds(ap);
-                const ph_h8 al = *(const __attribute__((address_space(3))) ph_h8 *)(size_t)pf_lds(ap + 512);
 #pragma unroll
                 for (int t = 0; t < NT; t++) {
                     if constexpr (PhFmt<T>::STEP) {
-                        pf_f32x4 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, B[t].b, pf_f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
-                        c = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, B[t].b, c, 0, 0, 0);
+                        pf_f32x4 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[mt], B[t].b, pf_f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+                        c = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[mt], B[t].b, c, 0, 0, 0);
 #pragma unroll
                         for (int i = 0; i < 4; i++) acc[t][mt][i] = __builtin_fmaf(B[t].sc, c[i], acc[t][mt][i]);
                     } else {
-                        cb[t][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, B[t].b, cb[t][mt], 0, 0, 0);
-                        cb[t][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, B[t].b, cb[t][mt], 0, 0, 0);
+                        cb[t][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[mt], B[t].b, cb[t][mt], 0, 0, 0);
+                        cb[t][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[mt], B[t].b, cb[t][mt], 0, 0, 0);
                         if constexpr (T == ST_Q6_K) {
-                            cb2[t][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, B[t].b2, cb2[t][mt], 0, 0, 0);
-                            cb2[t][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, B[t].b2, cb2[t][mt], 0, 0, 0);
+                            cb2[t][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[mt], B[t].b2, cb2[t][mt], 0, 0, 0);
+                            cb2[t][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[mt], B[t].b2, cb2[t][mt], 0, 0, 0);
                         }
                     }
+                }
+            }
+            if (s + 1 < 8) {
+#pragma unroll
+                for (int t = 0; t < NT; t++) B[t] = Bn[t];
+#pragma unroll
+                for (int mt = 0; mt < MT; mt++) {
+                    ah[mt] = ahn[mt];
+                    al[mt] = aln[mt];
                 }
             }
         }
