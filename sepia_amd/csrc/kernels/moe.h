@@ -27,9 +27,9 @@
 // logit, runs the selection and puts the counter back to zero (so the launch
 // can be replayed from a graph). Without it the logits are the only output
 // and the matrix-core gate/up kernel selects (mq.h).
-#define RT_NT 256
+#define RT_NT 512
 #define RT_ROWS 1
-#define RT_C4 8   // float4 chunks per thread and row: hidden <= 256 * 4 * 8
+#define RT_C4 4   // float4 chunks per thread and row: hidden <= 512 * 4 * 4
 
 extern "C" __global__ __launch_bounds__(RT_NT) void sepia_moe_route(
     const float *__restrict__ rw, int64_t ld, const float *__restrict__ bias, const float *__restrict__ x,

@@ -1656,6 +1656,7 @@ int sepia_hip_synth_blocks(int ggml_type, SepiaGpuBuf *buf, size_t off, int64_t 
 }
 
 /* --------------------------------------------------------------- MoE ---- */
+#define RT_THREADS 512   /* threads per router workgroup (RT_NT in kernels/moe.h) */
 /* Mirrors struct MoeProj in kernels/moe.h field for field. */
 typedef struct {
     const uint8_t *base;
@@ -2234,7 +2235,7 @@ static int moe_decode_impl(const char *op, const SepiaMoeLayerDesc *L, SepiaGpuB
     int32_t select = !in_kernel;
     void *a_route[] = { &rw, &ld, &rb, &x->dev, &hid, &nr, &ns, &tk, &rs, &gsc, &logits, &sel_idx, &sel_w, &counter,
                         &select };
-    if (!launch(K_MOE_ROUTE, (unsigned)n_tot, 256, a_route, op)) return 0;
+    if (!launch(K_MOE_ROUTE, (unsigned)n_tot, RT_THREADS, a_route, op)) return 0;
 
     if (!ffn_launch(op, &g, &u, &d, &sg, &su, &sd, sel_idx, sel_w, 0, tk, ns, H, I, x->dev, (float *)y->dev, s + o_h,
                     cnt_region, in_kernel ? &rt : NULL))
