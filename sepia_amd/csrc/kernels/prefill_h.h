@@ -243,6 +243,18 @@ __device__ __forceinline__ ph_h2 ph_splat(float v) {
     const _Float16 h = (_Float16)v;
     return ph_h2{h, h};
 }
+// A small integer's exact f16 in both halves (a direct 16-bit integer to f16
+// convert, no f32 step): |v| <= 2048.
+__device__ __forceinline__ ph_h2 ph_splat_u(uint32_t v) {
+    const _Float16 h = (_Float16)(uint16_t)v;
+    return ph_h2{h, h};
+}
+// The IQ formats' sub-scale sc = 2 s + 1 <= 31 and -1024 sc, both exact in
+// f16 (the second by one packed f16 multiply).
+__device__ __forceinline__ void ph_iq_scale(uint32_t sc, ph_h2 &s2, ph_h2 &nb) {
+    s2 = ph_splat_u(sc);
+    nb = s2 * ph_h2{(_Float16)-1024.0f, (_Float16)-1024.0f};
+}
 
 // The sign masks of the 128 IQ sign indices as f16 sign bits: 16 bytes
 // each, half j 0x8000 when bit j of iq_signs(index) is set.
@@ -307,7 +319,8 @@ __device__ __forceinline__ PhB ph_decode(const uint8_t *blk, const uint8_t *tab,
         const uint32_t sc = 2u * ((ph_u8(blk + 66 + s) >> (4 * (g >> 1))) & 15u) + 1u;
         const uint2 gr = *(const __attribute__((address_space(3))) uint2 *)(size_t)pf_lds(tab + 8 * (v & 511u));
         const ph_u4 sm = *(const __attribute__((address_space(3))) ph_u4 *)(size_t)pf_lds(signs + 16 * (v >> 9));
-        const ph_h2 s2 = ph_splat((float)sc), nb = ph_splat(-1024.0f * (float)sc);
+        ph_h2 s2, nb;
+        ph_iq_scale(sc, s2, nb);
         r.b = ph_codes_fma(gr, s2, nb, sm);
     } else if constexpr (T == ST_IQ3_XXS) {
         // qs bytes 8 s + 2 g, + 1 at 2 (grid indices, 4 bytes each); aux32 of
@@ -320,7 +333,8 @@ __device__ __forceinline__ PhB ph_decode(const uint8_t *blk, const uint8_t *tab,
         gr.y = *(const __attribute__((address_space(3))) uint32_t *)(size_t)pf_lds(tab + 4 * (ix >> 8));
         const ph_u4 sm =
             *(const __attribute__((address_space(3))) ph_u4 *)(size_t)pf_lds(signs + 16 * ((aux >> (7 * g)) & 127u));
-        const ph_h2 s2 = ph_splat((float)sc), nb = ph_splat(-1024.0f * (float)sc);
+        ph_h2 s2, nb;
+        ph_iq_scale(sc, s2, nb);
         r.b = ph_codes_fma(gr, s2, nb, sm);
     } else if constexpr (T == ST_IQ4_XS) {
         // qs[16 s + 8 (g & 1) + i] at 8, nibble g >> 1; 6-bit scale ls
@@ -340,7 +354,7 @@ __device__ __forceinline__ PhB ph_decode(const uint8_t *blk, const uint8_t *tab,
         const uint32_t c0 = ((q.x >> nsh) & 0x0F0F0F0Fu) | (((h.x >> s) & 0x01010101u) << 4);
         const uint32_t c1 = ((q.y >> nsh) & 0x0F0F0F0Fu) | (((h.y >> s) & 0x01010101u) << 4);
         const uint32_t sc = k_scale_6(blk + 4, s);
-        r.b = ph_codes_sub(make_uint2(c0, c1), ph_splat(1024.0f)) * (_Float16)sc;
+        r.b = ph_codes_sub(make_uint2(c0, c1), ph_splat(1024.0f)) * (_Float16)(uint16_t)sc;
     } else if constexpr (T == ST_Q6_K) {
         // 128-half n6 = s >> 2, quarter qq = s & 3: low 4 bits from
         // ql[64 n6 + 32 (qq & 1) + l] (nibble qq >> 1), high 2 bits from
@@ -353,8 +367,8 @@ __device__ __forceinline__ PhB ph_decode(const uint8_t *blk, const uint8_t *tab,
         const uint32_t c1 = ((q.y >> nsh) & 0x0F0F0F0Fu) | (((h.y >> hsh) & 0x03030303u) << 4);
         const int32_t sc = (int32_t)(int8_t)ph_u8(blk + 192 + 8 * n6 + 2 * qq + (g >> 1));
         const ph_h8 q32 = ph_codes_sub(make_uint2(c0, c1), ph_splat(1056.0f));   // q - 32
-        r.b = q32 * (_Float16)(float)(sc & 15);                                 // (q - 32) b
-        r.b2 = q32 * (_Float16)(float)(sc >> 4);                                 // (q - 32) a
+        r.b = q32 * (_Float16)(int16_t)(sc & 15);                               // (q - 32) b
+        r.b2 = q32 * (_Float16)(int16_t)(sc >> 4);                              // (q - 32) a
     } else {   // Q8_0: block s (34 bytes at 34 s): d, then int8 qs
         const uint2 q = ph_u64(blk + 34 * s + 2 + 8 * g);
         r.b = ph_codes_sub(make_uint2(q.x ^ 0x80808080u, q.y ^ 0x80808080u), ph_splat(1152.0f));
