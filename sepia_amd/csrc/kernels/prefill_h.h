@@ -40,10 +40,10 @@
 //
 // Workgroup: one unit (<= 32 pairs of one expert) x R weight rows (R = 256:
 // gate/up 128 gate + the same 128 up rows; R = 128 for the formats whose
-// staged blocks are too large for 256 rows: Q6_K, Q8_0), 8 waves; wave w
-// computes R / 8 rows (one or two 16-row N tiles) x the unit's one or two
-// 16-pair M tiles. Records are double-buffered; weights SW-buffered, and
-// wave w stages exactly the weight rows it decodes (each row's block from
+// staged blocks are too large for 256 rows: Q6_K, Q8_0), 16 waves; wave
+// w < R / 16 computes 16 rows (one N tile) x the unit's one or two 16-pair
+// M tiles. Records are double-buffered; weights SW-buffered, and a
+// stepping wave stages exactly the weight rows it decodes (each row's block from
 // the 4-byte boundary at or below its start, PW 16-byte pieces), so only
 // the records need the per-block barrier.
 #pragma once
@@ -52,6 +52,7 @@
 #define PH_REC 1056                    // bytes of a 256-column PH record
 #define PH_AP 66                       // its 16-byte pieces (2 mod 4: no LDS bank conflicts)
 #define PH_ABYTES (PF_MT * PH_REC)     // a record stage: the unit's 32 rows
+#define PH_WAVES 16                    // waves of a workgroup
 
 typedef _Float16 ph_h2 __attribute__((ext_vector_type(2)));
 typedef _Float16 ph_h8 __attribute__((ext_vector_type(8)));
@@ -134,9 +135,9 @@ extern "C" __global__ __launch_bounds__(256) void sepia_ph_quant(const float *__
 
 // ------------------------------------------------------------- staging --
 // Record pieces: the unit's 32 records of a block (66 pieces each, record m
-// at 1056 m) by 33 wave instructions over the 8 waves (the last partial).
-// Weight pieces: wave w stages its RW = R / 8 rows, piece c of row k at
-// 16 (PW (RW w + k) + c); a piece that starts past the block's bytes (plus
+// at 1056 m) by 33 wave instructions over the 16 waves. Weight pieces:
+// stepping wave w (w < R / 16) stages its 16 rows, piece c of row k at
+// 16 (PW (16 w + k) + c); a piece that starts past the block's bytes (plus
 // the 2 of the 4-byte alignment) takes piece 0's bytes again. The last
 // piece that holds block bytes may run up to 14 bytes past the block: into
 // the row's next block, the next row, or, after a matrix's last row, the
@@ -144,9 +145,9 @@ extern "C" __global__ __launch_bounds__(256) void sepia_ph_quant(const float *__
 // (dev_bytes in sepia_hip.c).
 template <int T, bool GU>
 struct PhDma {
-    static constexpr int BB = PhFmt<T>::BB, PW = PhFmt<T>::PW, R = PhFmt<T>::R, RW = R / 8;
-    static constexpr int NA = (PF_MT * PH_AP + 63) / 64, KA = (NA + 7) / 8;
-    static constexpr int NW = RW * PW, KW = (NW + 63) / 64;   // a wave's weight pieces and instructions
+    static constexpr int BB = PhFmt<T>::BB, PW = PhFmt<T>::PW, R = PhFmt<T>::R, AW = R / 16;
+    static constexpr int NA = (PF_MT * PH_AP + 63) / 64, KA = (NA + PH_WAVES - 1) / PH_WAVES;
+    static constexpr int NW = 16 * PW, KW = (NW + 63) / 64;   // a stepping wave's weight pieces and instructions
     uint32_t a[KA];            // record piece offsets at block 0
     uint32_t r[KW], c16[KW];   // row offset from the matrix base; offset of the lane's piece in the window
     bool aon[KA], won[KW];
@@ -154,16 +155,18 @@ struct PhDma {
         const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
 #pragma unroll
         for (int k = 0; k < KA; k++) {
-            const int q = 64 * (w + 8 * k) + lane, m = q / PH_AP, c = q - m * PH_AP;
-            aon[k] = w + 8 * k < NA && q < PF_MT * PH_AP;
+            const int q = 64 * (w + PH_WAVES * k) + lane, m = q / PH_AP, c = q - m * PH_AP;
+            aon[k] = w + PH_WAVES * k < NA && q < PF_MT * PH_AP;
             a[k] = aon[k] ? roff[m] + 16u * (uint32_t)c : 0u;
         }
-        // GU: waves 0..3 the gate rows, 4..7 the same up rows
-        const int64_t rw0 = r0 + (int64_t)(GU ? RW * (w & 3) : RW * w);
+        // stepping waves 0 .. AW - 1 take 16 rows each; GU: the first half
+        // the gate rows, the second half the same up rows
+        const bool on = w < AW;
+        const int64_t rw0 = r0 + (int64_t)(16 * (GU ? w % (AW / 2) : w));
 #pragma unroll
         for (int k = 0; k < KW; k++) {
             const int q = 64 * k + lane, kr = q / PW, c = q - kr * PW;
-            won[k] = q < NW;
+            won[k] = on && q < NW;
             r[k] = won[k] ? (uint32_t)((uint64_t)(rw0 + kr) * row_bytes) : 0u;
             c16[k] = 16 * c < BB + 2 ? 16u * (uint32_t)c : 0u;
         }
@@ -173,21 +176,20 @@ struct PhDma {
         const uint32_t ab = (uint32_t)b * PH_REC;
 #pragma unroll
         for (int k = 0; k < KA; k++) {
-            const int jj = w + 8 * k;
+            const int jj = w + PH_WAVES * k;
             if (jj < NA && aon[k]) pf_dma16(rec, a[k] + ab, pf_lds(As + 1024 * jj));
         }
     }
-    // this wave's weight instructions of one block
+    // a stepping wave's weight instructions of one block (other waves: none)
     __device__ __forceinline__ void issue_w(int64_t b, uint8_t *Ws, const uint8_t *Wm) const {
         const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+        if (w >= AW) return;
         const uint32_t wb = (uint32_t)b * BB;
         uint8_t *dst = Ws + 16 * NW * w;
 #pragma unroll
         for (int k = 0; k < KW; k++)
             if (won[k]) pf_dma16(Wm, ((r[k] + wb) & ~3u) + c16[k], pf_lds(dst + 1024 * k));
     }
-    // vmcnt of one block's weight instructions (a partial last one counts)
-    static __device__ __forceinline__ int n_w() { return KW; }
 };
 
 // ------------------------------------------------------------- decoders --
@@ -380,63 +382,61 @@ __device__ __forceinline__ PhB ph_decode(const uint8_t *blk, const uint8_t *tab,
 // ----------------------------------------------------------- projection --
 // One projection workgroup (see the top of the file). GU: rows r0 .. r0 +
 // R / 2 - 1 of gate (W0) and up (W1), h[pair][row] = silu(gate) * up in
-// f32; down: rows r0 .. r0 + R - 1 of W0, out[pair][row] in f32.
+// f32; down: rows r0 .. r0 + R - 1 of W0, out[pair][row] in f32. Stepping
+// wave w (w < R / 16) computes 16 rows x the unit's one or two 16-pair M
+// tiles (GU: waves w and w + R / 32 the same rows of gate and up); the
+// other waves stage records only.
 template <int T, bool GU, int MT>
 __device__ __forceinline__ void ph_proj(uint8_t *smem, const uint8_t *W0, const uint8_t *W1, uint64_t row_bytes,
                                         int64_t nb, const uint8_t *rec, const uint32_t *roff, const int32_t *pair,
                                         const float *srow, int nv, int64_t r0, float *__restrict__ out,
                                         int64_t ld_out) {
-    constexpr int BB = PhFmt<T>::BB, PW = PhFmt<T>::PW, SW = PhFmt<T>::SW, R = PhFmt<T>::R, RW = R / 8;
-    constexpr int NT = RW / 16;
-    const int w = threadIdx.x >> 6, l = threadIdx.x & 63, n = l & 15, g = l >> 4;
-    const uint8_t *Wm = (GU && w >= 4) ? W1 : W0;
-    const int64_t grow0 = r0 + (GU ? RW * (w & 3) : RW * w);   // global row of N tile 0
+    constexpr int BB = PhFmt<T>::BB, PW = PhFmt<T>::PW, SW = PhFmt<T>::SW, R = PhFmt<T>::R;
+    constexpr int AW = R / 16, HALF = AW / 2;
+    const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)), l = threadIdx.x & 63, n = l & 15,
+              g = l >> 4;
+    const bool on = w < AW;
+    const uint8_t *Wm = (GU && w >= HALF) ? W1 : W0;
+    const int64_t grow = r0 + 16 * (GU ? w % HALF : w);   // the wave's first global row
     auto a_stage = [&](int b) { return smem + (uint32_t)(b & 1) * PH_ABYTES; };
     auto w_stage = [&](int b) { return smem + 2 * PH_ABYTES + (uint32_t)b % SW * PhLds<T>::W; };
     const uint8_t *tab = smem + PhLds<T>::TAB, *signs = smem + PhLds<T>::SIGNS;
     ph_fill_tables<T>(smem);   // published by the first block's barrier
     PhDma<T, GU> dma;
     dma.init(roff, row_bytes, r0);
-    pf_f32x4 acc[NT][2];
+    pf_f32x4 acc[2];
 #pragma unroll
-    for (int t = 0; t < NT; t++)
-#pragma unroll
-        for (int mt = 0; mt < 2; mt++) acc[t][mt] = pf_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int mt = 0; mt < 2; mt++) acc[mt] = pf_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     const int nbi = (int)nb;
     dma.issue_a(0, a_stage(0), rec);
     for (int c = 0; c < SW - 1 && c < nbi; c++) dma.issue_w(c, w_stage(c), Wm);
     constexpr int APB = 16 * PH_AP;   // bytes of a staged record
+    constexpr int KW = PhDma<T, GU>::KW;
     for (int b = 0; b < nbi; b++) {
         // everything up to A_b and W_b; the weights of blocks b + 1 .. b + SW - 2 may fly
         const int ahead = (nbi - 1 - b) < (SW - 2) ? (nbi - 1 - b) : (SW - 2);
-        pq_wait_vm<PhDma<T, GU>::KW * (SW - 2)>(PhDma<T, GU>::n_w() * ahead);
-        const uint8_t *Ws = w_stage(b);
-        const uint8_t *blk[NT];
-#pragma unroll
-        for (int t = 0; t < NT; t++)   // the block at offset o of its staged row (rows of 4-byte multiples)
-            blk[t] = Ws + (uint32_t)(RW * w + 16 * t + n) * (PW * 16) + (((uint32_t)b * BB) & 3u);
+        pq_wait_vm<KW * (SW - 2)>((on ? KW : 0) * ahead);
+        // the block at offset o of its staged row (rows of 4-byte multiples)
+        const uint8_t *blk = w_stage(b) + (uint32_t)(16 * w + n) * (PW * 16) + (((uint32_t)b * BB) & 3u);
         asm volatile("" ::: "memory");
         __syncthreads();   // every wave's record pieces of A_b, the tables
         asm volatile("" ::: "memory");
         if (b + 1 < nbi) dma.issue_a(b + 1, a_stage(b + 1), rec);
         if (b + SW - 1 < nbi) dma.issue_w(b + SW - 1, w_stage(b + SW - 1), Wm);
+        if (!on) continue;
         const uint8_t *As = a_stage(b);
-        pf_f32x4 cb[NT][2], cb2[NT][2];
+        pf_f32x4 cb[2], cb2[2];
 #pragma unroll
-        for (int t = 0; t < NT; t++)
-#pragma unroll
-            for (int mt = 0; mt < 2; mt++) {
-                cb[t][mt] = pf_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-                cb2[t][mt] = pf_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-            }
+        for (int mt = 0; mt < 2; mt++) {
+            cb[mt] = pf_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            cb2[mt] = pf_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
         // Software-pipelined by one K step: step s + 1's codes (LDS
         // gathers and their VALU) and activation planes are read before
         // step s's matrix ops are issued (the scheduling barrier keeps that
         // order), so the gathers' latency runs under the MFMAs.
-        PhB B[NT];
+        PhB B = ph_decode<T>(blk, tab, signs, 0, g);
         ph_h8 ah[MT], al[MT];
-#pragma unroll
-        for (int t = 0; t < NT; t++) B[t] = ph_decode<T>(blk[t], tab, signs, 0, g);
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) {
             const uint8_t *ap = As + (16 * mt + n) * APB + 16 * g;
@@ -445,11 +445,10 @@ __device__ __forceinline__ void ph_proj(uint8_t *smem, const uint8_t *W0, const 
         }
 #pragma unroll
         for (int s = 0; s < 8; s++) {
-            PhB Bn[NT];
+            PhB Bn;
             ph_h8 ahn[MT], aln[MT];
             if (s + 1 < 8) {
-#pragma unroll
-                for (int t = 0; t < NT; t++) Bn[t] = ph_decode<T>(blk[t], tab, signs, s + 1, g);
+                Bn = ph_decode<T>(blk, tab, signs, s + 1, g);
 #pragma unroll
                 for (int mt = 0; mt < MT; mt++) {
                     const uint8_t *ap = As + (16 * mt + n) * APB + 64 * (s + 1) + 16 * g;
@@ -460,26 +459,22 @@ __device__ __forceinline__ void ph_proj(uint8_t *smem, const uint8_t *W0, const 
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int mt = 0; mt < MT; mt++) {
+                if constexpr (PhFmt<T>::STEP) {
+                    pf_f32x4 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[mt], B.b, pf_f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+                    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[mt], B.b, c, 0, 0, 0);
 #pragma unroll
-                for (int t = 0; t < NT; t++) {
-                    if constexpr (PhFmt<T>::STEP) {
-                        pf_f32x4 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[mt], B[t].b, pf_f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
-                        c = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[mt], B[t].b, c, 0, 0, 0);
-#pragma unroll
-                        for (int i = 0; i < 4; i++) acc[t][mt][i] = __builtin_fmaf(B[t].sc, c[i], acc[t][mt][i]);
-                    } else {
-                        cb[t][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[mt], B[t].b, cb[t][mt], 0, 0, 0);
-                        cb[t][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[mt], B[t].b, cb[t][mt], 0, 0, 0);
-                        if constexpr (T == ST_Q6_K) {
-                            cb2[t][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[mt], B[t].b2, cb2[t][mt], 0, 0, 0);
-                            cb2[t][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[mt], B[t].b2, cb2[t][mt], 0, 0, 0);
-                        }
+                    for (int i = 0; i < 4; i++) acc[mt][i] = __builtin_fmaf(B.sc, c[i], acc[mt][i]);
+                } else {
+                    cb[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[mt], B.b, cb[mt], 0, 0, 0);
+                    cb[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[mt], B.b, cb[mt], 0, 0, 0);
+                    if constexpr (T == ST_Q6_K) {
+                        cb2[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[mt], B.b2, cb2[mt], 0, 0, 0);
+                        cb2[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[mt], B.b2, cb2[mt], 0, 0, 0);
                     }
                 }
             }
             if (s + 1 < 8) {
-#pragma unroll
-                for (int t = 0; t < NT; t++) B[t] = Bn[t];
+                B = Bn;
 #pragma unroll
                 for (int mt = 0; mt < MT; mt++) {
                     ah[mt] = ahn[mt];
@@ -487,91 +482,76 @@ __device__ __forceinline__ void ph_proj(uint8_t *smem, const uint8_t *W0, const 
                 }
             }
         }
-        if constexpr (!PhFmt<T>::STEP) {
-#pragma unroll
-            for (int t = 0; t < NT; t++) {
-                if constexpr (T == ST_IQ2_XS || T == ST_IQ3_XXS) {
-                    const float d = ph_h2f(blk[t]) * (T == ST_IQ2_XS ? 0.125f : 0.25f);
-#pragma unroll
-                    for (int mt = 0; mt < MT; mt++)
-#pragma unroll
-                        for (int i = 0; i < 4; i++) acc[t][mt][i] = __builtin_fmaf(d, cb[t][mt][i], acc[t][mt][i]);
-                } else if constexpr (T == ST_Q6_K) {
-                    const float d = ph_h2f(blk[t] + 208);
-#pragma unroll
-                    for (int mt = 0; mt < MT; mt++)
-#pragma unroll
-                        for (int i = 0; i < 4; i++)
-                            acc[t][mt][i] = __builtin_fmaf(d, __builtin_fmaf(16.0f, cb2[t][mt][i], cb[t][mt][i]),
-                                                           acc[t][mt][i]);
-                } else {   // Q5_K: d C - dmin sum_j m_j S_j, the min terms on the f32 matrix cores
-                    const float d = ph_h2f(blk[t]), dmin = ph_h2f(blk[t] + 2);
-#pragma unroll
-                    for (int mt = 0; mt < MT; mt++) {
-                        pf_f32x4 cm = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-                        for (int h = 0; h < 2; h++) {
-                            // A[pair][k] = S_(4 h + k) of pair 16 mt + n; B[k][row n] = m_(4 h + k)
-                            const float sa = *(const __attribute__((address_space(3))) float *)(size_t)pf_lds(
-                                As + (16 * mt + n) * APB + 1024 + 4 * (4 * h + g));
-                            const float mb = (float)k_min_6(blk[t] + 4, 4 * h + g);
-                            cm = __builtin_amdgcn_mfma_f32_16x16x4f32(sa, mb, cm, 0, 0, 0);
-                        }
-#pragma unroll
-                        for (int i = 0; i < 4; i++)
-                            acc[t][mt][i] = __builtin_fmaf(-dmin, cm[i], __builtin_fmaf(d, cb[t][mt][i], acc[t][mt][i]));
-                    }
-                }
-            }
-        }
-    }
-    // y = s_pair * acc; lane: pairs 16 mt + 4 g + i, rows grow0 + 16 t + n
-#pragma unroll
-    for (int mt = 0; mt < MT; mt++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const float sp = srow[16 * mt + 4 * g + i];
-#pragma unroll
-            for (int t = 0; t < NT; t++) acc[t][mt][i] *= sp;
-        }
-    if constexpr (GU) {
-        __syncthreads();   // every wave is done with the stages
-        float *xch = (float *)smem + ((w & 3) * 64 + l) * 16;
-        if (w >= 4) {
-#pragma unroll
-            for (int t = 0; t < NT; t++)
-#pragma unroll
-                for (int mt = 0; mt < 2; mt++) *(pf_f32x4 *)(xch + 8 * t + 4 * mt) = acc[t][mt];
-        }
-        __syncthreads();
-        if (w >= 4) return;
-#pragma unroll
-        for (int t = 0; t < NT; t++)
-#pragma unroll
-            for (int mt = 0; mt < MT; mt++) {
-                const pf_f32x4 u = *(const pf_f32x4 *)(xch + 8 * t + 4 * mt);
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const int m = 16 * mt + 4 * g + i;
-                    if (m < nv) out[(int64_t)pair[m] * ld_out + grow0 + 16 * t + n] = silu_f32(acc[t][mt][i]) * u[i];
-                }
-            }
-    } else {
-#pragma unroll
-        for (int t = 0; t < NT; t++)
+        if constexpr (T == ST_IQ2_XS || T == ST_IQ3_XXS) {
+            const float d = ph_h2f(blk) * (T == ST_IQ2_XS ? 0.125f : 0.25f);
 #pragma unroll
             for (int mt = 0; mt < MT; mt++)
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const int m = 16 * mt + 4 * g + i;
-                    if (m < nv) out[(int64_t)pair[m] * ld_out + grow0 + 16 * t + n] = acc[t][mt][i];
+                for (int i = 0; i < 4; i++) acc[mt][i] = __builtin_fmaf(d, cb[mt][i], acc[mt][i]);
+        } else if constexpr (T == ST_Q6_K) {
+            const float d = ph_h2f(blk + 208);
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    acc[mt][i] = __builtin_fmaf(d, __builtin_fmaf(16.0f, cb2[mt][i], cb[mt][i]), acc[mt][i]);
+        } else if constexpr (T == ST_Q5_K) {   // d C - dmin sum_j m_j S_j, the min terms on the f32 matrix cores
+            const float d = ph_h2f(blk), dmin = ph_h2f(blk + 2);
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++) {
+                pf_f32x4 cm = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int h = 0; h < 2; h++) {
+                    // A[pair][k] = S_(4 h + k) of pair 16 mt + n; B[k][row n] = m_(4 h + k)
+                    const float sa = *(const __attribute__((address_space(3))) float *)(size_t)pf_lds(
+                        As + (16 * mt + n) * APB + 1024 + 4 * (4 * h + g));
+                    const float mb = (float)k_min_6(blk + 4, 4 * h + g);
+                    cm = __builtin_amdgcn_mfma_f32_16x16x4f32(sa, mb, cm, 0, 0, 0);
                 }
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    acc[mt][i] = __builtin_fmaf(-dmin, cm[i], __builtin_fmaf(d, cb[mt][i], acc[mt][i]));
+            }
+        }
+    }
+    // y = s_pair * acc; lane: pairs 16 mt + 4 g + i, rows grow + n
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[mt][i] *= srow[16 * mt + 4 * g + i];
+    if constexpr (GU) {
+        __syncthreads();   // every wave is done with the stages
+        float *xch = (float *)smem + ((w % HALF) * 64 + l) * 8;
+        if (on && w >= HALF) {
+#pragma unroll
+            for (int mt = 0; mt < 2; mt++) *(pf_f32x4 *)(xch + 4 * mt) = acc[mt];
+        }
+        __syncthreads();
+        if (!on || w >= HALF) return;
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) {
+            const pf_f32x4 u = *(const pf_f32x4 *)(xch + 4 * mt);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int m = 16 * mt + 4 * g + i;
+                if (m < nv) out[(int64_t)pair[m] * ld_out + grow + n] = silu_f32(acc[mt][i]) * u[i];
+            }
+        }
+    } else {
+        if (!on) return;
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int m = 16 * mt + 4 * g + i;
+                if (m < nv) out[(int64_t)pair[m] * ld_out + grow + n] = acc[mt][i];
+            }
     }
 }
 
-// Workgroup x of the launch starts at row SLICE x (gate/up: of each matrix,
-// SLICE 64; down: SLICE 128); a format with R = 256 rows covers two slices,
-// so the kernels run it only for even x.
+// The launch has one workgroup per row slice (gate/up: 64 rows of each
+// matrix; down: 128 rows); a format with R = 256 rows covers two slices (see
+// ph_slice).
 #define PH_DISPATCH(TYPE, GU, R0, ...)                                                               \
     do {                                                                                             \
         switch (TYPE) {                                                                              \
@@ -591,6 +571,15 @@ __device__ __forceinline__ void ph_proj(uint8_t *smem, const uint8_t *W0, const 
     } while (0)
 // Formats staged 128 rows at a time (the others 256).
 __device__ __forceinline__ bool ph_rows128(int32_t t) { return t == ST_Q6_K || t == ST_Q8_0; }
+// The first row slice of slot x, or -1 for none: formats staged 256
+// rows at a time take slices 2 x, 2 x + 1 in the slots x < gridDim.x / 2.
+// Keeping the active slots at consecutive x spreads them over all 8 XCDs
+// (the hardware deals consecutive workgroup ids to the XCDs in turn: with
+// rows of 48 workgroups, active even x alone would land on 4 of them).
+__device__ __forceinline__ int64_t ph_slice(int32_t t, int32_t x) {
+    if (ph_rows128(t)) return x;
+    return x < (int32_t)gridDim.x / 2 ? 2 * (int64_t)x : -1;
+}
 // 256-column blocks of a row (a projection's n_blocks counts Q8_0's
 // 32-column blocks; its 256-column block is eight of them, 272 bytes).
 __device__ __forceinline__ int64_t ph_nb(int32_t t, int64_t n_blocks) { return t == ST_Q8_0 ? n_blocks / 8 : n_blocks; }
@@ -600,48 +589,52 @@ __device__ __forceinline__ int64_t ph_nb(int32_t t, int64_t n_blocks) { return t
 // The host launches it only when every projection of the layer has one of
 // the formats above, with 4-byte-aligned rows, and H and I are multiples of
 // 256.
-extern "C" __global__ __launch_bounds__(512) void sepia_ph_gateup(
+extern "C" __global__ __launch_bounds__(64 * PH_WAVES) void sepia_ph_gateup(
     PfProj gate, PfProj up, PfProj s_gate, PfProj s_up, int32_t n_routed, int32_t n_sel, int64_t I, int64_t H,
     const uint8_t *__restrict__ phx, const float *__restrict__ phxs, const int32_t *__restrict__ list,
     const int32_t *__restrict__ units, const int32_t *__restrict__ n_units, float *__restrict__ hf) {
-    if ((int32_t)blockIdx.y >= n_units[0]) return;
+    const PfSlot slot = pf_slot();
+    if (slot.y >= n_units[0]) return;
     extern __shared__ __attribute__((aligned(16))) uint8_t pf_smem[];
     uint8_t *smem = pf_smem;
-    const int32_t *un = units + 3 * blockIdx.y;
+    const int32_t *un = units + 3 * slot.y;
     const int32_t e = un[0], nv = un[2];
     const bool routed = e < n_routed;
     const PfProj &G = routed ? gate : s_gate, &U = routed ? up : s_up;
     const int64_t ei = routed ? e : e - n_routed;
     const uint8_t *wg = G.base + ei * G.stride, *wu = U.base + ei * U.stride;
-    if (!ph_rows128(G.type) && (blockIdx.x & 1)) return;
+    const int64_t sl = ph_slice(G.type, slot.x);
+    if (sl < 0) return;
     uint32_t *roff;
     int32_t *pair;
     float *srow;
     pq_unit_rows(list + un[1], nv, true, n_sel, (H / 256) * PH_REC, phxs, smem, roff, pair, srow);
-    PH_DISPATCH(G.type, true, (int64_t)blockIdx.x * 64, smem, wg, wu, G.row_bytes, ph_nb(G.type, G.n_blocks), phx, roff,
+    PH_DISPATCH(G.type, true, sl * 64, smem, wg, wu, G.row_bytes, ph_nb(G.type, G.n_blocks), phx, roff,
                 pair, srow, nv, hf, I);
 }
 
 // Down: workgroup (128-row slice bx of H, unit by); yp[p][row] = down_e .
 // h_p in f32 (h_p the PH row p). Same launch conditions.
-extern "C" __global__ __launch_bounds__(512) void sepia_ph_down(
+extern "C" __global__ __launch_bounds__(64 * PH_WAVES) void sepia_ph_down(
     PfProj down, PfProj s_down, int32_t n_routed, int64_t I, int64_t H, const uint8_t *__restrict__ phh,
     const float *__restrict__ phhs, const int32_t *__restrict__ list, const int32_t *__restrict__ units,
     const int32_t *__restrict__ n_units, float *__restrict__ yp) {
-    if ((int32_t)blockIdx.y >= n_units[0]) return;
+    const PfSlot slot = pf_slot();
+    if (slot.y >= n_units[0]) return;
     extern __shared__ __attribute__((aligned(16))) uint8_t pf_smem[];
     uint8_t *smem = pf_smem;
-    const int32_t *un = units + 3 * blockIdx.y;
+    const int32_t *un = units + 3 * slot.y;
     const int32_t e = un[0], nv = un[2];
     const bool routed = e < n_routed;
     const PfProj &D = routed ? down : s_down;
     const int64_t ei = routed ? e : e - n_routed;
     const uint8_t *wd = D.base + ei * D.stride;
-    if (!ph_rows128(D.type) && (blockIdx.x & 1)) return;
+    const int64_t sl = ph_slice(D.type, slot.x);
+    if (sl < 0) return;
     uint32_t *roff;
     int32_t *pair;
     float *srow;
     pq_unit_rows(list + un[1], nv, false, 1, (I / 256) * PH_REC, phhs, smem, roff, pair, srow);
-    PH_DISPATCH(D.type, false, (int64_t)blockIdx.x * 128, smem, wd, wd, D.row_bytes, ph_nb(D.type, D.n_blocks), phh,
+    PH_DISPATCH(D.type, false, sl * 128, smem, wd, wd, D.row_bytes, ph_nb(D.type, D.n_blocks), phh,
                 roff, pair, srow, nv, yp, H);
 }

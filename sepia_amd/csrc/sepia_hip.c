@@ -1657,6 +1657,7 @@ int sepia_hip_synth_blocks(int ggml_type, SepiaGpuBuf *buf, size_t off, int64_t 
 
 /* --------------------------------------------------------------- MoE ---- */
 #define RT_THREADS 512   /* threads per router workgroup (RT_NT in kernels/moe.h) */
+#define PH_WAVES 16      /* waves of an f16 projection workgroup (kernels/prefill_h.h) */
 /* Mirrors struct MoeProj in kernels/moe.h field for field. */
 typedef struct {
     const uint8_t *base;
@@ -1950,6 +1951,9 @@ int sepia_gpu_moe_prefill(const SepiaMoeLayerDesc *L, int64_t n_tokens, SepiaGpu
     /* units of <= 32 pairs: routed pairs split over at most n_routed experts,
      * each shared expert takes every token */
     const int64_t umax = (T * tk + 31) / 32 + nr + (int64_t)ns * ((T + 31) / 32) + 1;
+    /* grid rows of the f16 unit kernels: a multiple of 8, so they deal the
+     * units to the 8 XCDs in turn (kernels/prefill.h pf_slot) */
+    const int64_t ugrid = (umax + 7) & ~(int64_t)7;
     const int64_t P = T * n_sel;
     if (H % 256 || I % 256) {
         LOG("%s: hidden and inter must be multiples of 256", op);
@@ -1965,7 +1969,7 @@ int sepia_gpu_moe_prefill(const SepiaMoeLayerDesc *L, int64_t n_tokens, SepiaGpu
     const int64_t ldqx = H / 256 * (use_h ? PH_REC : 832), ldqh = I / 256 * (use_h ? PH_REC : 832);
     const int use_qh = use_q || use_h;
     /* the pipelines address activation rows with 32-bit byte offsets */
-    if (umax > 65535 || (H + 255) / 256 > MAX_GRID || (uint64_t)T * H * 2 >= (1ull << 32) ||
+    if (ugrid > 65535 || (H + 255) / 256 > MAX_GRID || (uint64_t)T * H * 2 >= (1ull << 32) ||
         (uint64_t)P * I * 2 >= (1ull << 32) || (T * H + 255) / 256 > MAX_GRID || P > MAX_GRID ||
         (use_qh && ((uint64_t)T * ldqx >= (1ull << 32) || (uint64_t)P * ldqh >= (1ull << 32)))) {
         LOG("%s: batch too large", op);
@@ -2020,21 +2024,24 @@ int sepia_gpu_moe_prefill(const SepiaMoeLayerDesc *L, int64_t n_tokens, SepiaGpu
         /* int8 (PQ rows) or f16 (PH rows): quantize x, gate/up to f32 h,
          * quantize h, down to the per-pair partial rows. The f16 gate/up
          * runs over 64-row slices of I, its down over 128-row slices of H
-         * (256-row formats take every other slice). */
+         * (a 256-row format takes two slices, in the first half of the
+         * workgroups). */
         void *pqx = s + o_pqx, *pqxs = s + o_pqxs, *hf = s + o_hf, *pqh = s + o_pqh, *pqhs = s + o_pqhs;
         int64_t ldq_x = ldqx, ldq_h = ldqh;
         const int kq = use_q ? K_PF_QUANT : K_PH_QUANT;
+        const unsigned th_p = use_q ? 512 : 64 * PH_WAVES;   /* threads of a projection workgroup */
+        const unsigned gy = (unsigned)(use_q ? umax : ugrid);   /* its units */
         void *a_qx[] = { &x->dev, &hid, &hid, &pqx, &ldq_x, &pqxs };
         if (!launch(kq, (unsigned)T, 256, a_qx, op)) return 0;
         void *a_gq[] = { (void *)&g, (void *)&u, (void *)&sg, (void *)&su, &nr32, &nsel32, &inter, &hid,
                          &pqx, &pqxs, &list, &units, &n_units, &hf };
-        if (!launch2(use_q ? K_PF_GATEUP_Q : K_PH_GATEUP, (unsigned)(use_q ? I / 128 : I / 64), (unsigned)umax, 512,
+        if (!launch2(use_q ? K_PF_GATEUP_Q : K_PH_GATEUP, (unsigned)(use_q ? I / 128 : I / 64), gy, th_p,
                      PF_LDS_BYTES, a_gq, op))
             return 0;
         void *a_qh[] = { &hf, &inter, &inter, &pqh, &ldq_h, &pqhs };
         if (!launch(kq, (unsigned)P, 256, a_qh, op)) return 0;
         void *a_dq[] = { (void *)&d, (void *)&sd, &nr32, &inter, &hid, &pqh, &pqhs, &list, &units, &n_units, &yp };
-        if (!launch2(use_q ? K_PF_DOWN_Q : K_PH_DOWN, (unsigned)(use_q ? H / 256 : H / 128), (unsigned)umax, 512,
+        if (!launch2(use_q ? K_PF_DOWN_Q : K_PH_DOWN, (unsigned)(use_q ? H / 256 : H / 128), gy, th_p,
                      PF_LDS_BYTES, a_dq, op))
             return 0;
     } else {
