@@ -19,10 +19,12 @@
 // exact in f32; the matrix cores add them in f32). Per weight row n and
 // 256-column block, with C the f32 dot of the codes with v' (x is the
 // v' the record holds, w the weights of src/quants.c's dequant):
-//   IQ2_XS   code = +-grid * (2 s + 1), s the 4-bit scale of its 16 weights
-//            (|code| <= 43 * 31), sum w x = d C / 8     (quants.c:179-201)
-//   IQ3_XXS  code = +-grid * (2 s + 1), 4-bit s per 32 weights
-//            (|code| <= 62 * 31), sum w x = d C / 4     (quants.c:203-226)
+//   IQ2_XS   code = +-grid * (2 s + 1) * 2^-14, s the 4-bit scale of its
+//            16 weights (|code| <= 43 * 31 * 2^-14),
+//            sum w x = d C 2^14 / 8                     (quants.c:179-201)
+//   IQ3_XXS  code = +-grid * (2 s + 1) * 2^-14, 4-bit s per 32 weights
+//            (|code| <= 62 * 31 * 2^-14), sum w x = d C 2^14 / 4
+//            (quants.c:203-226)
 //   Q5_K     code = q * sc, 6-bit sc per 32 (<= 31 * 63);
 //            sum w x = d C - dmin sum_j m_j S_j, S_j the record's sums
 //            (quants.c:127-151)
@@ -33,10 +35,14 @@
 //            sum w x = sum_32 d (ls - 32) C_32          (quants.c:228-248)
 //   Q8_0     code = q, per 32 columns sum w x = sum_32 d_32 C_32
 //            (quants.c:85-94)
-// Every code is an integer of magnitude <= 2048, so exact in f16; the f16
-// value comes from the byte b by a permute that makes the half 0x64bb
-// (1024 + b, exact) and a packed f16 add or multiply-add that removes the
-// 1024 and applies the scale (every intermediate an exact f16 integer).
+// Every code is an integer of magnitude < 2048 (the IQ codes times 2^-14),
+// so exact in f16. The K-quant codes come from the byte b by a permute that
+// makes the half 0x64bb (1024 + b, exact) and a packed f16 add or
+// multiply-add that removes the 1024 and applies the scale. The IQ codes
+// come from the grid byte b and a sign byte (0x80 or 0x00, a table per sign
+// index) by one permute per two codes that makes the half +-b 2^-24 (the
+// f16 subnormal with mantissa b), then one packed f16 multiply by
+// (2 s + 1) 2^10: every intermediate exact.
 //
 // Workgroup: one unit (<= 32 pairs of one expert) x R weight rows (R = 256:
 // gate/up 128 gate + the same 128 up rows; R = 128 for the formats whose
@@ -71,14 +77,14 @@ template <> struct PhFmt<ST_Q6_K> { static constexpr int BB = 210, PW = 14, SW =
 template <> struct PhFmt<ST_Q8_0> { static constexpr int BB = 272, PW = 17, SW = 2, R = 128; static constexpr bool STEP = true; };
 
 // LDS: [record stages 2 x PH_ABYTES][weight stages SW x R x PW x 16]
-//      [tables: IQ2_XS grid 4 KB / IQ3_XXS grid 1 KB, then 128 x 16 bytes of
-//       sign masks][... row tables at PQ_LDS_TOP]
+//      [tables: IQ2_XS grid 4 KB / IQ3_XXS grid 1 KB, then 128 x 8 sign
+//       bytes][... row tables at PQ_LDS_TOP]
 template <int T> struct PhLds {
     static constexpr uint32_t W = (uint32_t)PhFmt<T>::R * PhFmt<T>::PW * 16;
     static constexpr uint32_t TAB = 2 * PH_ABYTES + PhFmt<T>::SW * W;
     static constexpr uint32_t GRID = T == ST_IQ2_XS ? 4096u : T == ST_IQ3_XXS ? 1024u : 0u;
     static constexpr uint32_t SIGNS = TAB + GRID;
-    static constexpr uint32_t END = SIGNS + (GRID ? 2048u : 0u);
+    static constexpr uint32_t END = SIGNS + (GRID ? 1024u : 0u);
     static_assert(END <= PQ_LDS_TOP, "LDS of a PH projection");
 };
 
@@ -134,8 +140,9 @@ extern "C" __global__ __launch_bounds__(256) void sepia_ph_quant(const float *__
 }
 
 // ------------------------------------------------------------- staging --
-// Record pieces: the unit's 32 records of a block (66 pieces each, record m
-// at 1056 m) by 33 wave instructions over the 16 waves. Weight pieces:
+// Record pieces: the unit's records of a block (its nv <= 32 pairs, 66
+// pieces each, record m at 1056 m) by up to 33 wave instructions over the 16
+// waves. Weight pieces:
 // stepping wave w (w < R / 16) stages its 16 rows, piece c of row k at
 // 16 (PW (16 w + k) + c); a piece that starts past the block's bytes (plus
 // the 2 of the 4-byte alignment) takes piece 0's bytes again. The last
@@ -151,12 +158,14 @@ struct PhDma {
     uint32_t a[KA];            // record piece offsets at block 0
     uint32_t r[KW], c16[KW];   // row offset from the matrix base; offset of the lane's piece in the window
     bool aon[KA], won[KW];
-    __device__ __forceinline__ void init(const uint32_t *roff, uint64_t row_bytes, int64_t r0) {
+    // nr: the records the unit's M tiles read (its pairs; the rest of the
+    // stage is not staged, and the M tile rows past the pairs are discarded)
+    __device__ __forceinline__ void init(const uint32_t *roff, uint64_t row_bytes, int64_t r0, int nr) {
         const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
 #pragma unroll
         for (int k = 0; k < KA; k++) {
             const int q = 64 * (w + PH_WAVES * k) + lane, m = q / PH_AP, c = q - m * PH_AP;
-            aon[k] = w + PH_WAVES * k < NA && q < PF_MT * PH_AP;
+            aon[k] = w + PH_WAVES * k < NA && q < PF_MT * PH_AP && m < nr;
             a[k] = aon[k] ? roff[m] + 16u * (uint32_t)c : 0u;
         }
         // stepping waves 0 .. AW - 1 take 16 rows each; GU: the first half
@@ -221,20 +230,6 @@ __device__ __forceinline__ ph_h2 ph_bias2(uint32_t v, uint32_t sel) {
 }
 #define PH_SEL_LO 0x04010400u
 #define PH_SEL_HI 0x04030402u
-// 8 codes from the 8 bytes of g (g.x bytes 0..3, g.y bytes 4..7): (b + 1024)
-// * sc - 1024 sc (an exact f16 integer), sign bits xor'd in from sm.
-__device__ __forceinline__ ph_h8 ph_codes_fma(uint2 g, ph_h2 sc, ph_h2 nb, ph_u4 sm) {
-    const ph_h2 c0 = __builtin_elementwise_fma(ph_bias2(g.x, PH_SEL_LO), sc, nb);
-    const ph_h2 c1 = __builtin_elementwise_fma(ph_bias2(g.x, PH_SEL_HI), sc, nb);
-    const ph_h2 c2 = __builtin_elementwise_fma(ph_bias2(g.y, PH_SEL_LO), sc, nb);
-    const ph_h2 c3 = __builtin_elementwise_fma(ph_bias2(g.y, PH_SEL_HI), sc, nb);
-    ph_u4 r;
-    r[0] = __builtin_bit_cast(uint32_t, c0) ^ sm[0];
-    r[1] = __builtin_bit_cast(uint32_t, c1) ^ sm[1];
-    r[2] = __builtin_bit_cast(uint32_t, c2) ^ sm[2];
-    r[3] = __builtin_bit_cast(uint32_t, c3) ^ sm[3];
-    return __builtin_bit_cast(ph_h8, r);
-}
 // 8 codes b - off from the 8 bytes of g (exact f16 integers)
 __device__ __forceinline__ ph_h8 ph_codes_sub(uint2 g, ph_h2 off) {
     ph_h2 c[4] = {ph_bias2(g.x, PH_SEL_LO) - off, ph_bias2(g.x, PH_SEL_HI) - off, ph_bias2(g.y, PH_SEL_LO) - off,
@@ -251,24 +246,29 @@ __device__ __forceinline__ ph_h2 ph_splat_u(uint32_t v) {
     const _Float16 h = (_Float16)(uint16_t)v;
     return ph_h2{h, h};
 }
-// The IQ formats' sub-scale sc = 2 s + 1 <= 31 and -1024 sc, both exact in
-// f16 (the second by one packed f16 multiply).
-__device__ __forceinline__ void ph_iq_scale(uint32_t sc, ph_h2 &s2, ph_h2 &nb) {
-    s2 = ph_splat_u(sc);
-    nb = s2 * ph_h2{(_Float16)-1024.0f, (_Float16)-1024.0f};
-}
-
-// The sign masks of the 128 IQ sign indices as f16 sign bits: 16 bytes
-// each, half j 0x8000 when bit j of iq_signs(index) is set.
+// The sign bytes of the 128 IQ sign indices, 8 bytes each: byte j 0x80
+// where bit j of iq_signs(index) is set (code j negative), else 0x00.
 __device__ __forceinline__ void ph_fill_signs(uint8_t *st) {
     for (int i = threadIdx.x; i < 128; i += blockDim.x) {
         const uint32_t s = iq_signs((uint32_t)i);
-        ph_u4 m;
+        uint2 m = make_uint2(0u, 0u);
 #pragma unroll
-        for (int p = 0; p < 4; p++)
-            m[p] = (((s >> (2 * p)) & 1u) ? 0x8000u : 0u) | (((s >> (2 * p + 1)) & 1u) ? 0x80000000u : 0u);
-        *(ph_u4 *)(st + 16 * i) = m;
+        for (int j = 0; j < 4; j++) {
+            m.x |= ((s >> j) & 1u) << (8 * j + 7);
+            m.y |= ((s >> (j + 4)) & 1u) << (8 * j + 7);
+        }
+        *(uint2 *)(st + 8 * i) = m;
     }
+}
+// 8 IQ codes from the grid bytes g and the sign bytes sg (codes 0..3 in .x,
+// 4..7 in .y): the halves +-b 2^-24 (low byte the grid byte, high byte the
+// sign byte) times s2 = (2 s + 1) 2^10
+__device__ __forceinline__ ph_h8 ph_codes_iq(uint2 g, uint2 sg, ph_h2 s2) {
+    const ph_h2 c[4] = {__builtin_bit_cast(ph_h2, __builtin_amdgcn_perm(sg.x, g.x, 0x05010400u)) * s2,
+                        __builtin_bit_cast(ph_h2, __builtin_amdgcn_perm(sg.x, g.x, 0x07030602u)) * s2,
+                        __builtin_bit_cast(ph_h2, __builtin_amdgcn_perm(sg.y, g.y, 0x05010400u)) * s2,
+                        __builtin_bit_cast(ph_h2, __builtin_amdgcn_perm(sg.y, g.y, 0x07030602u)) * s2};
+    return __builtin_bit_cast(ph_h8, c);
 }
 template <int T>
 __device__ __forceinline__ void ph_fill_tables(uint8_t *smem) {
@@ -320,10 +320,8 @@ __device__ __forceinline__ PhB ph_decode(const uint8_t *blk, const uint8_t *tab,
         const uint32_t v = ph_u16(blk + 2 + 2 * (4 * s + g));
         const uint32_t sc = 2u * ((ph_u8(blk + 66 + s) >> (4 * (g >> 1))) & 15u) + 1u;
         const uint2 gr = *(const __attribute__((address_space(3))) uint2 *)(size_t)pf_lds(tab + 8 * (v & 511u));
-        const ph_u4 sm = *(const __attribute__((address_space(3))) ph_u4 *)(size_t)pf_lds(signs + 16 * (v >> 9));
-        ph_h2 s2, nb;
-        ph_iq_scale(sc, s2, nb);
-        r.b = ph_codes_fma(gr, s2, nb, sm);
+        const uint2 sg = *(const __attribute__((address_space(3))) uint2 *)(size_t)pf_lds(signs + 8 * (v >> 9));
+        r.b = ph_codes_iq(gr, sg, ph_splat_u(sc << 10));
     } else if constexpr (T == ST_IQ3_XXS) {
         // qs bytes 8 s + 2 g, + 1 at 2 (grid indices, 4 bytes each); aux32 of
         // step s at 66 + 4 s: sign index g at bit 7 g, 4-bit scale at 28
@@ -333,11 +331,9 @@ __device__ __forceinline__ PhB ph_decode(const uint8_t *blk, const uint8_t *tab,
         uint2 gr;
         gr.x = *(const __attribute__((address_space(3))) uint32_t *)(size_t)pf_lds(tab + 4 * (ix & 255u));
         gr.y = *(const __attribute__((address_space(3))) uint32_t *)(size_t)pf_lds(tab + 4 * (ix >> 8));
-        const ph_u4 sm =
-            *(const __attribute__((address_space(3))) ph_u4 *)(size_t)pf_lds(signs + 16 * ((aux >> (7 * g)) & 127u));
-        ph_h2 s2, nb;
-        ph_iq_scale(sc, s2, nb);
-        r.b = ph_codes_fma(gr, s2, nb, sm);
+        const uint2 sg =
+            *(const __attribute__((address_space(3))) uint2 *)(size_t)pf_lds(signs + 8 * ((aux >> (7 * g)) & 127u));
+        r.b = ph_codes_iq(gr, sg, ph_splat_u(sc << 10));
     } else if constexpr (T == ST_IQ4_XS) {
         // qs[16 s + 8 (g & 1) + i] at 8, nibble g >> 1; 6-bit scale ls
         const uint2 q = ph_u64(blk + 8 + 16 * s + 8 * (g & 1));
@@ -403,7 +399,7 @@ __device__ __forceinline__ void ph_proj(uint8_t *smem, const uint8_t *W0, const 
     const uint8_t *tab = smem + PhLds<T>::TAB, *signs = smem + PhLds<T>::SIGNS;
     ph_fill_tables<T>(smem);   // published by the first block's barrier
     PhDma<T, GU> dma;
-    dma.init(roff, row_bytes, r0);
+    dma.init(roff, row_bytes, r0, nv);
     pf_f32x4 acc[2];
 #pragma unroll
     for (int mt = 0; mt < 2; mt++) acc[mt] = pf_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -483,7 +479,7 @@ __device__ __forceinline__ void ph_proj(uint8_t *smem, const uint8_t *W0, const 
             }
         }
         if constexpr (T == ST_IQ2_XS || T == ST_IQ3_XXS) {
-            const float d = ph_h2f(blk) * (T == ST_IQ2_XS ? 0.125f : 0.25f);
+            const float d = ph_h2f(blk) * (T == ST_IQ2_XS ? 2048.0f : 4096.0f);   // 2^14 / 8, 2^14 / 4
 #pragma unroll
             for (int mt = 0; mt < MT; mt++)
 #pragma unroll
