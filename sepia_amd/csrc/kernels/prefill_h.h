@@ -47,9 +47,10 @@
 // Workgroup: one unit (<= 32 pairs of one expert) x R weight rows (R = 256:
 // gate/up 128 gate + the same 128 up rows; R = 128 for the formats whose
 // staged blocks are too large for 256 rows: Q6_K, Q8_0), 16 waves; wave
-// w < R / 16 computes 16 rows (one N tile) x the unit's one or two 16-pair
-// M tiles. Records are double-buffered; weights SW-buffered, and a
-// stepping wave stages exactly the weight rows it decodes (each row's block from
+// w < R / (16 NT) computes 16 NT rows (NT N tiles: 2 for the 256-row
+// formats, so each activation read feeds two, else 1) x the unit's one or
+// two 16-pair M tiles; the other waves only stage records. Records are double-buffered; weights SW-buffered, and
+// a stepping wave stages exactly the weight rows it decodes (each row's block from
 // the 4-byte boundary at or below its start, PW 16-byte pieces), so only
 // the records need the per-block barrier.
 #pragma once
@@ -66,15 +67,16 @@ typedef uint32_t ph_u4 __attribute__((ext_vector_type(4)));
 
 // BB: block bytes (256 columns); PW: 16-byte pieces of a staged row (the
 // block from the 4-byte boundary at or below its start, at most 2 bytes
-// earlier); SW: weight stages; R: weight rows of a workgroup; STEP: scale
-// per 32-column step applied in f32 (else once per block).
+// earlier); SW: weight stages; R: weight rows of a workgroup; NT: 16-row N
+// tiles of a stepping wave; STEP: scale per 32-column step applied in f32
+// (else once per block).
 template <int T> struct PhFmt;
-template <> struct PhFmt<ST_IQ2_XS> { static constexpr int BB = 74, PW = 6, SW = 3, R = 256; static constexpr bool STEP = false; };
-template <> struct PhFmt<ST_IQ3_XXS> { static constexpr int BB = 98, PW = 10, SW = 2, R = 256; static constexpr bool STEP = false; };
-template <> struct PhFmt<ST_IQ4_XS> { static constexpr int BB = 136, PW = 10, SW = 2, R = 256; static constexpr bool STEP = true; };
-template <> struct PhFmt<ST_Q5_K> { static constexpr int BB = 176, PW = 11, SW = 2, R = 256; static constexpr bool STEP = false; };
-template <> struct PhFmt<ST_Q6_K> { static constexpr int BB = 210, PW = 14, SW = 2, R = 128; static constexpr bool STEP = false; };
-template <> struct PhFmt<ST_Q8_0> { static constexpr int BB = 272, PW = 17, SW = 2, R = 128; static constexpr bool STEP = true; };
+template <> struct PhFmt<ST_IQ2_XS> { static constexpr int BB = 74, PW = 6, SW = 3, R = 256, NT = 2; static constexpr bool STEP = false; };
+template <> struct PhFmt<ST_IQ3_XXS> { static constexpr int BB = 98, PW = 10, SW = 2, R = 256, NT = 2; static constexpr bool STEP = false; };
+template <> struct PhFmt<ST_IQ4_XS> { static constexpr int BB = 136, PW = 10, SW = 2, R = 256, NT = 2; static constexpr bool STEP = true; };
+template <> struct PhFmt<ST_Q5_K> { static constexpr int BB = 176, PW = 11, SW = 2, R = 256, NT = 2; static constexpr bool STEP = false; };
+template <> struct PhFmt<ST_Q6_K> { static constexpr int BB = 210, PW = 14, SW = 2, R = 128, NT = 1; static constexpr bool STEP = false; };
+template <> struct PhFmt<ST_Q8_0> { static constexpr int BB = 272, PW = 17, SW = 2, R = 128, NT = 1; static constexpr bool STEP = true; };
 
 // LDS: [record stages 2 x PH_ABYTES][weight stages SW x R x PW x 16]
 //      [tables: IQ2_XS grid 4 KB / IQ3_XXS grid 1 KB, then 128 x 8 sign
@@ -143,8 +145,8 @@ extern "C" __global__ __launch_bounds__(256) void sepia_ph_quant(const float *__
 // Record pieces: the unit's records of a block (its nv <= 32 pairs, 66
 // pieces each, record m at 1056 m) by up to 33 wave instructions over the 16
 // waves. Weight pieces:
-// stepping wave w (w < R / 16) stages its 16 rows, piece c of row k at
-// 16 (PW (16 w + k) + c); a piece that starts past the block's bytes (plus
+// stepping wave w (w < R / RW, RW = 16 NT) stages its RW rows, piece c of
+// row k at 16 (PW (RW w + k) + c); a piece that starts past the block's bytes (plus
 // the 2 of the 4-byte alignment) takes piece 0's bytes again. The last
 // piece that holds block bytes may run up to 14 bytes past the block: into
 // the row's next block, the next row, or, after a matrix's last row, the
@@ -152,9 +154,9 @@ extern "C" __global__ __launch_bounds__(256) void sepia_ph_quant(const float *__
 // (dev_bytes in sepia_hip.c).
 template <int T, bool GU>
 struct PhDma {
-    static constexpr int BB = PhFmt<T>::BB, PW = PhFmt<T>::PW, R = PhFmt<T>::R, AW = R / 16;
+    static constexpr int BB = PhFmt<T>::BB, PW = PhFmt<T>::PW, R = PhFmt<T>::R, RW = 16 * PhFmt<T>::NT, AW = R / RW;
     static constexpr int NA = (PF_MT * PH_AP + 63) / 64, KA = (NA + PH_WAVES - 1) / PH_WAVES;
-    static constexpr int NW = 16 * PW, KW = (NW + 63) / 64;   // a stepping wave's weight pieces and instructions
+    static constexpr int NW = RW * PW, KW = (NW + 63) / 64;   // a stepping wave's weight pieces and instructions
     uint32_t a[KA];            // record piece offsets at block 0
     uint32_t r[KW], c16[KW];   // row offset from the matrix base; offset of the lane's piece in the window
     bool aon[KA], won[KW];
@@ -168,10 +170,10 @@ struct PhDma {
             aon[k] = w + PH_WAVES * k < NA && q < PF_MT * PH_AP && m < nr;
             a[k] = aon[k] ? roff[m] + 16u * (uint32_t)c : 0u;
         }
-        // stepping waves 0 .. AW - 1 take 16 rows each; GU: the first half
+        // stepping waves 0 .. AW - 1 take RW rows each; GU: the first half
         // the gate rows, the second half the same up rows
         const bool on = w < AW;
-        const int64_t rw0 = r0 + (int64_t)(16 * (GU ? w % (AW / 2) : w));
+        const int64_t rw0 = r0 + (int64_t)(RW * (GU ? w % (AW / 2) : w));
 #pragma unroll
         for (int k = 0; k < KW; k++) {
             const int q = 64 * k + lane, kr = q / PW, c = q - kr * PW;
@@ -379,30 +381,32 @@ __device__ __forceinline__ PhB ph_decode(const uint8_t *blk, const uint8_t *tab,
 // One projection workgroup (see the top of the file). GU: rows r0 .. r0 +
 // R / 2 - 1 of gate (W0) and up (W1), h[pair][row] = silu(gate) * up in
 // f32; down: rows r0 .. r0 + R - 1 of W0, out[pair][row] in f32. Stepping
-// wave w (w < R / 16) computes 16 rows x the unit's one or two 16-pair M
-// tiles (GU: waves w and w + R / 32 the same rows of gate and up); the
-// other waves stage records only.
+// wave w (w < R / RW, RW = 16 NT) computes RW rows (NT N tiles) x the
+// unit's one or two 16-pair M tiles (GU: waves w and w + R / (2 RW) the
+// same rows of gate and up); the other waves stage records only.
 template <int T, bool GU, int MT>
 __device__ __forceinline__ void ph_proj(uint8_t *smem, const uint8_t *W0, const uint8_t *W1, uint64_t row_bytes,
                                         int64_t nb, const uint8_t *rec, const uint32_t *roff, const int32_t *pair,
                                         const float *srow, int nv, int64_t r0, float *__restrict__ out,
                                         int64_t ld_out) {
     constexpr int BB = PhFmt<T>::BB, PW = PhFmt<T>::PW, SW = PhFmt<T>::SW, R = PhFmt<T>::R;
-    constexpr int AW = R / 16, HALF = AW / 2;
+    constexpr int NT = PhFmt<T>::NT, RW = 16 * NT, AW = R / RW, HALF = AW / 2;
     const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)), l = threadIdx.x & 63, n = l & 15,
               g = l >> 4;
     const bool on = w < AW;
     const uint8_t *Wm = (GU && w >= HALF) ? W1 : W0;
-    const int64_t grow = r0 + 16 * (GU ? w % HALF : w);   // the wave's first global row
+    const int64_t grow = r0 + RW * (GU ? w % HALF : w);   // the wave's first global row
     auto a_stage = [&](int b) { return smem + (uint32_t)(b & 1) * PH_ABYTES; };
     auto w_stage = [&](int b) { return smem + 2 * PH_ABYTES + (uint32_t)b % SW * PhLds<T>::W; };
     const uint8_t *tab = smem + PhLds<T>::TAB, *signs = smem + PhLds<T>::SIGNS;
     ph_fill_tables<T>(smem);   // published by the first block's barrier
     PhDma<T, GU> dma;
     dma.init(roff, row_bytes, r0, nv);
-    pf_f32x4 acc[2];
+    pf_f32x4 acc[NT][2];
 #pragma unroll
-    for (int mt = 0; mt < 2; mt++) acc[mt] = pf_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int t = 0; t < NT; t++)
+#pragma unroll
+        for (int mt = 0; mt < 2; mt++) acc[t][mt] = pf_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     const int nbi = (int)nb;
     dma.issue_a(0, a_stage(0), rec);
     for (int c = 0; c < SW - 1 && c < nbi; c++) dma.issue_w(c, w_stage(c), Wm);
@@ -412,8 +416,11 @@ __device__ __forceinline__ void ph_proj(uint8_t *smem, const uint8_t *W0, const 
         // everything up to A_b and W_b; the weights of blocks b + 1 .. b + SW - 2 may fly
         const int ahead = (nbi - 1 - b) < (SW - 2) ? (nbi - 1 - b) : (SW - 2);
         pq_wait_vm<KW * (SW - 2)>((on ? KW : 0) * ahead);
-        // the block at offset o of its staged row (rows of 4-byte multiples)
-        const uint8_t *blk = w_stage(b) + (uint32_t)(16 * w + n) * (PW * 16) + (((uint32_t)b * BB) & 3u);
+        // the blocks at offset o of their staged rows (rows of 4-byte multiples)
+        const uint8_t *blk[NT];
+#pragma unroll
+        for (int t = 0; t < NT; t++)
+            blk[t] = w_stage(b) + (uint32_t)(RW * w + 16 * t + n) * (PW * 16) + (((uint32_t)b * BB) & 3u);
         asm volatile("" ::: "memory");
         __syncthreads();   // every wave's record pieces of A_b, the tables
         asm volatile("" ::: "memory");
@@ -421,17 +428,21 @@ __device__ __forceinline__ void ph_proj(uint8_t *smem, const uint8_t *W0, const 
         if (b + SW - 1 < nbi) dma.issue_w(b + SW - 1, w_stage(b + SW - 1), Wm);
         if (!on) continue;
         const uint8_t *As = a_stage(b);
-        pf_f32x4 cb[2], cb2[2];
+        pf_f32x4 cb[NT][2], cb2[NT][2];
 #pragma unroll
-        for (int mt = 0; mt < 2; mt++) {
-            cb[mt] = pf_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-            cb2[mt] = pf_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-        }
+        for (int t = 0; t < NT; t++)
+#pragma unroll
+            for (int mt = 0; mt < 2; mt++) {
+                cb[t][mt] = pf_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                cb2[t][mt] = pf_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            }
         // Software-pipelined by one K step: step s + 1's codes (LDS
         // gathers and their VALU) and activation planes are read before
         // step s's matrix ops are issued (the scheduling barrier keeps that
         // order), so the gathers' latency runs under the MFMAs.
-        PhB B = ph_decode<T>(blk, tab, signs, 0, g);
+        PhB B[NT];
+#pragma unroll
+        for (int t = 0; t < NT; t++) B[t] = ph_decode<T>(blk[t], tab, signs, 0, g);
         ph_h8 ah[MT], al[MT];
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) {
@@ -441,10 +452,11 @@ __device__ __forceinline__ void ph_proj(uint8_t *smem, const uint8_t *W0, const 
         }
 #pragma unroll
         for (int s = 0; s < 8; s++) {
-            PhB Bn;
+            PhB Bn[NT];
             ph_h8 ahn[MT], aln[MT];
             if (s + 1 < 8) {
-                Bn = ph_decode<T>(blk, tab, signs, s + 1, g);
+#pragma unroll
+                for (int t = 0; t < NT; t++) Bn[t] = ph_decode<T>(blk[t], tab, signs, s + 1, g);
 #pragma unroll
                 for (int mt = 0; mt < MT; mt++) {
                     const uint8_t *ap = As + (16 * mt + n) * APB + 64 * (s + 1) + 16 * g;
@@ -455,22 +467,26 @@ __device__ __forceinline__ void ph_proj(uint8_t *smem, const uint8_t *W0, const 
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int mt = 0; mt < MT; mt++) {
-                if constexpr (PhFmt<T>::STEP) {
-                    pf_f32x4 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[mt], B.b, pf_f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
-                    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[mt], B.b, c, 0, 0, 0);
 #pragma unroll
-                    for (int i = 0; i < 4; i++) acc[mt][i] = __builtin_fmaf(B.sc, c[i], acc[mt][i]);
-                } else {
-                    cb[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[mt], B.b, cb[mt], 0, 0, 0);
-                    cb[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[mt], B.b, cb[mt], 0, 0, 0);
-                    if constexpr (T == ST_Q6_K) {
-                        cb2[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[mt], B.b2, cb2[mt], 0, 0, 0);
-                        cb2[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[mt], B.b2, cb2[mt], 0, 0, 0);
+                for (int t = 0; t < NT; t++) {
+                    if constexpr (PhFmt<T>::STEP) {
+                        pf_f32x4 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[mt], B[t].b, pf_f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+                        c = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[mt], B[t].b, c, 0, 0, 0);
+#pragma unroll
+                        for (int i = 0; i < 4; i++) acc[t][mt][i] = __builtin_fmaf(B[t].sc, c[i], acc[t][mt][i]);
+                    } else {
+                        cb[t][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[mt], B[t].b, cb[t][mt], 0, 0, 0);
+                        cb[t][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[mt], B[t].b, cb[t][mt], 0, 0, 0);
+                        if constexpr (T == ST_Q6_K) {
+                            cb2[t][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[mt], B[t].b2, cb2[t][mt], 0, 0, 0);
+                            cb2[t][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[mt], B[t].b2, cb2[t][mt], 0, 0, 0);
+                        }
                     }
                 }
             }
             if (s + 1 < 8) {
-                B = Bn;
+#pragma unroll
+                for (int t = 0; t < NT; t++) B[t] = Bn[t];
 #pragma unroll
                 for (int mt = 0; mt < MT; mt++) {
                     ah[mt] = ahn[mt];
@@ -478,70 +494,84 @@ __device__ __forceinline__ void ph_proj(uint8_t *smem, const uint8_t *W0, const 
                 }
             }
         }
-        if constexpr (T == ST_IQ2_XS || T == ST_IQ3_XXS) {
-            const float d = ph_h2f(blk) * (T == ST_IQ2_XS ? 2048.0f : 4096.0f);   // 2^14 / 8, 2^14 / 4
 #pragma unroll
-            for (int mt = 0; mt < MT; mt++)
+        for (int t = 0; t < NT; t++) {
+            if constexpr (T == ST_IQ2_XS || T == ST_IQ3_XXS) {
+                const float d = ph_h2f(blk[t]) * (T == ST_IQ2_XS ? 2048.0f : 4096.0f);   // 2^14 / 8, 2^14 / 4
 #pragma unroll
-                for (int i = 0; i < 4; i++) acc[mt][i] = __builtin_fmaf(d, cb[mt][i], acc[mt][i]);
-        } else if constexpr (T == ST_Q6_K) {
-            const float d = ph_h2f(blk + 208);
+                for (int mt = 0; mt < MT; mt++)
 #pragma unroll
-            for (int mt = 0; mt < MT; mt++)
+                    for (int i = 0; i < 4; i++) acc[t][mt][i] = __builtin_fmaf(d, cb[t][mt][i], acc[t][mt][i]);
+            } else if constexpr (T == ST_Q6_K) {
+                const float d = ph_h2f(blk[t] + 208);
 #pragma unroll
-                for (int i = 0; i < 4; i++)
-                    acc[mt][i] = __builtin_fmaf(d, __builtin_fmaf(16.0f, cb2[mt][i], cb[mt][i]), acc[mt][i]);
-        } else if constexpr (T == ST_Q5_K) {   // d C - dmin sum_j m_j S_j, the min terms on the f32 matrix cores
-            const float d = ph_h2f(blk), dmin = ph_h2f(blk + 2);
+                for (int mt = 0; mt < MT; mt++)
 #pragma unroll
-            for (int mt = 0; mt < MT; mt++) {
-                pf_f32x4 cm = {0.0f, 0.0f, 0.0f, 0.0f};
+                    for (int i = 0; i < 4; i++)
+                        acc[t][mt][i] =
+                            __builtin_fmaf(d, __builtin_fmaf(16.0f, cb2[t][mt][i], cb[t][mt][i]), acc[t][mt][i]);
+            } else if constexpr (T == ST_Q5_K) {   // d C - dmin sum_j m_j S_j, the min terms on the f32 matrix cores
+                const float d = ph_h2f(blk[t]), dmin = ph_h2f(blk[t] + 2);
 #pragma unroll
-                for (int h = 0; h < 2; h++) {
-                    // A[pair][k] = S_(4 h + k) of pair 16 mt + n; B[k][row n] = m_(4 h + k)
-                    const float sa = *(const __attribute__((address_space(3))) float *)(size_t)pf_lds(
-                        As + (16 * mt + n) * APB + 1024 + 4 * (4 * h + g));
-                    const float mb = (float)k_min_6(blk + 4, 4 * h + g);
-                    cm = __builtin_amdgcn_mfma_f32_16x16x4f32(sa, mb, cm, 0, 0, 0);
+                for (int mt = 0; mt < MT; mt++) {
+                    pf_f32x4 cm = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                    for (int h = 0; h < 2; h++) {
+                        // A[pair][k] = S_(4 h + k) of pair 16 mt + n; B[k][row n] = m_(4 h + k)
+                        const float sa = *(const __attribute__((address_space(3))) float *)(size_t)pf_lds(
+                            As + (16 * mt + n) * APB + 1024 + 4 * (4 * h + g));
+                        const float mb = (float)k_min_6(blk[t] + 4, 4 * h + g);
+                        cm = __builtin_amdgcn_mfma_f32_16x16x4f32(sa, mb, cm, 0, 0, 0);
+                    }
+#pragma unroll
+                    for (int i = 0; i < 4; i++)
+                        acc[t][mt][i] = __builtin_fmaf(-dmin, cm[i], __builtin_fmaf(d, cb[t][mt][i], acc[t][mt][i]));
                 }
-#pragma unroll
-                for (int i = 0; i < 4; i++)
-                    acc[mt][i] = __builtin_fmaf(-dmin, cm[i], __builtin_fmaf(d, cb[mt][i], acc[mt][i]));
             }
         }
     }
-    // y = s_pair * acc; lane: pairs 16 mt + 4 g + i, rows grow + n
+    // y = s_pair * acc; lane: pairs 16 mt + 4 g + i, rows grow + 16 t + n
 #pragma unroll
     for (int mt = 0; mt < MT; mt++)
 #pragma unroll
-        for (int i = 0; i < 4; i++) acc[mt][i] *= srow[16 * mt + 4 * g + i];
+        for (int i = 0; i < 4; i++) {
+            const float sp = srow[16 * mt + 4 * g + i];
+#pragma unroll
+            for (int t = 0; t < NT; t++) acc[t][mt][i] *= sp;
+        }
     if constexpr (GU) {
         __syncthreads();   // every wave is done with the stages
-        float *xch = (float *)smem + ((w % HALF) * 64 + l) * 8;
+        float *xch = (float *)smem + ((w % HALF) * 64 + l) * (8 * NT);
         if (on && w >= HALF) {
 #pragma unroll
-            for (int mt = 0; mt < 2; mt++) *(pf_f32x4 *)(xch + 4 * mt) = acc[mt];
+            for (int t = 0; t < NT; t++)
+#pragma unroll
+                for (int mt = 0; mt < 2; mt++) *(pf_f32x4 *)(xch + 8 * t + 4 * mt) = acc[t][mt];
         }
         __syncthreads();
         if (!on || w >= HALF) return;
 #pragma unroll
-        for (int mt = 0; mt < MT; mt++) {
-            const pf_f32x4 u = *(const pf_f32x4 *)(xch + 4 * mt);
+        for (int t = 0; t < NT; t++)
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int m = 16 * mt + 4 * g + i;
-                if (m < nv) out[(int64_t)pair[m] * ld_out + grow + n] = silu_f32(acc[mt][i]) * u[i];
+            for (int mt = 0; mt < MT; mt++) {
+                const pf_f32x4 u = *(const pf_f32x4 *)(xch + 8 * t + 4 * mt);
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int m = 16 * mt + 4 * g + i;
+                    if (m < nv) out[(int64_t)pair[m] * ld_out + grow + 16 * t + n] = silu_f32(acc[t][mt][i]) * u[i];
+                }
             }
-        }
     } else {
         if (!on) return;
 #pragma unroll
-        for (int mt = 0; mt < MT; mt++)
+        for (int t = 0; t < NT; t++)
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int m = 16 * mt + 4 * g + i;
-                if (m < nv) out[(int64_t)pair[m] * ld_out + grow + n] = acc[mt][i];
-            }
+            for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int m = 16 * mt + 4 * g + i;
+                    if (m < nv) out[(int64_t)pair[m] * ld_out + grow + 16 * t + n] = acc[t][mt][i];
+                }
     }
 }
 
