@@ -680,17 +680,24 @@ template <> struct MQ<ST_Q4_K> {
 // bytes off a boundary (the last block of a row always is) and 2 bytes after
 // it otherwise: no bytes of the next block are read twice.
 // Signs: bit j of the sign byte negates weight j (iq_signs adds the parity
-// bit). The 128 sign bytes' 0x00 / 0xFF byte masks (8 bytes each) follow
-// the codebook in LDS, so a sign index is one 8-byte read; a byte is
-// negated as (g ^ m) + (m & 1) (no carries: no codebook byte is 0).
+// bit). The 128 sign indices' permute selectors (8 bytes each: byte j is j,
+// or j + 4 where weight j is negative) follow the codebook in LDS, so a
+// sign index is one 8-byte read and four signed codes are one v_perm_b32
+// of a codebook word and its bytewise negation. IQ3_XXS keeps each word's
+// negation beside it in LDS; IQ2_XS computes it (one subtract: no codebook
+// byte is 0, so 0x01010100 - g negates every byte without a borrow).
 // The three plane dots of a segment combined in f32: with codebook weights
 // up to 62 the exact integer can pass 2^31 (mq_combine holds it for weights
 // <= 15 only); each term is exact in f32, their sum rounds once or twice.
 __device__ __forceinline__ float mq_combine_f(const mq_v4i &d) {
     return __builtin_fmaf((float)d[0], 65536.0f, __builtin_fmaf((float)d[1], 256.0f, (float)d[2]));
 }
-__device__ __forceinline__ uint32_t mq_iq_neg(uint32_t g, uint32_t m) { return (g ^ m) + (m & 0x01010101u); }
-// Byte masks of sign index idx7 (0..127) from the table at st.
+// The four signed codes of codebook word g (ng: its bytewise negation) by
+// the selector word sel.
+__device__ __forceinline__ uint32_t mq_iq_signed(uint32_t g, uint32_t ng, uint32_t sel) {
+    return __builtin_amdgcn_perm(ng, g, sel);
+}
+// Permute selectors of sign index idx7 (0..127) from the table at st.
 __device__ __forceinline__ uint2 mq_iq_mask(const uint8_t *st, uint32_t idx7) {
     return *(const uint2 *)(st + 8u * idx7);
 }
@@ -734,8 +741,10 @@ template <> struct MQ<ST_IQ2_XS> {
             const uint2 g0 = *(const uint2 *)(x.tab + 8u * (v0 & 511u));
             const uint2 g1 = *(const uint2 *)(x.tab + 8u * (v1 & 511u));
             const uint2 m0 = mq_iq_mask(x.tab + grid_bytes, v0 >> 9), m1 = mq_iq_mask(x.tab + grid_bytes, v1 >> 9);
-            const mq_v4i b = {(int32_t)mq_iq_neg(g0.x, m0.x), (int32_t)mq_iq_neg(g0.y, m0.y),
-                              (int32_t)mq_iq_neg(g1.x, m1.x), (int32_t)mq_iq_neg(g1.y, m1.y)};
+            const mq_v4i b = {(int32_t)mq_iq_signed(g0.x, 0x01010100u - g0.x, m0.x),
+                              (int32_t)mq_iq_signed(g0.y, 0x01010100u - g0.y, m0.y),
+                              (int32_t)mq_iq_signed(g1.x, 0x01010100u - g1.x, m1.x),
+                              (int32_t)mq_iq_signed(g1.y, 0x01010100u - g1.y, m1.y)};
             const mq_v4i D = mq_mfma(mq_a(x, 16 * sg), b);
             const uint32_t scb = ((ib < 4 ? sc_lo : sc_hi) >> (8 * (ib & 3))) & 0xFFu;
             const float nib = (float)(half ? (scb >> 4) : (scb & 15u));
@@ -751,12 +760,13 @@ template <> struct MQ<ST_IQ2_XS> {
 // IQ3_XXS {d@0, qs[64]@2, scales_signs[32]@66} (98 bytes, reference
 // src/quants.c:203-226): group ib has the word aux = scales_signs[4 ib ..]
 // (4 x 7-bit sign indices, 4-bit scale on top) and bytes qs[8 ib .. 8 ib +
-// 7] (indices into the 256 x 4-byte codebook, two per 8 weights):
+// 7] (indices into the 256-entry codebook, two per 8 weights; in LDS each
+// 4-byte entry is followed by its negation):
 // w = d (0.5 + aux >> 28) / 2 * entry. Segment sg = 2 ib + half covers
 // index bytes 8 ib + 4 half .. + 3 and sign indices 2 half, 2 half + 1.
 template <> struct MQ<ST_IQ3_XXS> {
     static constexpr int bytes = 98, W = 7, Wp = 7, sum_sel = 1;
-    static constexpr uint32_t grid_bytes = 256 * 4, table_bytes = grid_bytes + 128 * 8;
+    static constexpr uint32_t grid_bytes = 256 * 8, table_bytes = grid_bytes + 128 * 8;
     static constexpr bool has_pre = false;
     __device__ static uint32_t shift(uint32_t boff) { return boff & 3u; }
     // window bytes 0..99: words at 0, 16, ..., 80 and 84
@@ -786,9 +796,11 @@ template <> struct MQ<ST_IQ3_XXS> {
                 const uint32_t idx = __builtin_amdgcn_alignbyte(L(2 * ib + half + 1), L(2 * ib + half), 2u);
                 const uint2 ma = mq_iq_mask(x.tab + grid_bytes, (aux >> (14 * half)) & 127u);
                 const uint2 mb = mq_iq_mask(x.tab + grid_bytes, (aux >> (14 * half + 7)) & 127u);
-                const uint32_t *tab = (const uint32_t *)x.tab;
-                const mq_v4i b = {(int32_t)mq_iq_neg(tab[idx & 0xFFu], ma.x), (int32_t)mq_iq_neg(tab[(idx >> 8) & 0xFFu], ma.y),
-                                  (int32_t)mq_iq_neg(tab[(idx >> 16) & 0xFFu], mb.x), (int32_t)mq_iq_neg(tab[idx >> 24], mb.y)};
+                const uint2 *tab = (const uint2 *)x.tab;
+                const uint2 t0 = tab[idx & 0xFFu], t1 = tab[(idx >> 8) & 0xFFu], t2 = tab[(idx >> 16) & 0xFFu],
+                            t3 = tab[idx >> 24];
+                const mq_v4i b = {(int32_t)mq_iq_signed(t0.x, t0.y, ma.x), (int32_t)mq_iq_signed(t1.x, t1.y, ma.y),
+                                  (int32_t)mq_iq_signed(t2.x, t2.y, mb.x), (int32_t)mq_iq_signed(t3.x, t3.y, mb.y)};
                 const mq_v4i D = mq_mfma(mq_a(x, 16 * sg), b);
                 acc = __builtin_fmaf(db * x.xsb[sg], mq_combine_f(D), acc);
             }
@@ -1044,17 +1056,23 @@ __device__ __forceinline__ uint32_t mq_table_bytes(int32_t type) {
 }
 // The format's codebook into LDS at tab (IQ formats; nothing for the
 // others). Published by the caller's next barrier.
-// IQ formats: then the byte masks of the 128 sign indices (byte j 0xFF when
-// bit j of iq_signs(index) is set).
+// IQ formats: the codebook (IQ3_XXS: each word followed by its bytewise
+// negation), then the permute selectors of the 128 sign indices (8 bytes
+// each: byte j is j mod 4, plus 4 when bit j of iq_signs(index) is set).
+__device__ __forceinline__ uint32_t mq_neg_bytes(uint32_t g) {
+    uint32_t r = 0;
+#pragma unroll
+    for (int j = 0; j < 4; j++) r |= ((256u - ((g >> (8 * j)) & 0xFFu)) & 0xFFu) << (8 * j);
+    return r;
+}
 template <int T>
 __device__ __forceinline__ void mq_fill_signs(uint8_t *st) {
     for (int i = threadIdx.x; i < 128; i += blockDim.x) {
         const uint32_t s = iq_signs((uint32_t)i);
-        uint64_t m = 0;
-#pragma unroll
-        for (int j = 0; j < 8; j++)
-            if ((s >> j) & 1u) m |= (uint64_t)0xFF << (8 * j);
-        ((uint64_t *)st)[i] = m;
+        uint2 m;
+        m.x = 0x03020100u | ((s & 1u) << 2) | ((s & 2u) << 9) | ((s & 4u) << 16) | ((s & 8u) << 23);
+        m.y = 0x03020100u | ((s & 16u) >> 2) | ((s & 32u) << 5) | ((s & 64u) << 12) | ((s & 128u) << 19);
+        ((uint2 *)st)[i] = m;
     }
 }
 template <int T>
@@ -1063,7 +1081,10 @@ __device__ __forceinline__ void mq_fill_table(uint8_t *tab) {
         for (int i = threadIdx.x; i < 512; i += blockDim.x) ((uint64_t *)tab)[i] = c_iq2xs_grid[i];
         mq_fill_signs<T>(tab + MQ<T>::grid_bytes);
     } else if constexpr (T == ST_IQ3_XXS) {
-        for (int i = threadIdx.x; i < 256; i += blockDim.x) ((uint32_t *)tab)[i] = c_iq3xxs_grid[i];
+        for (int i = threadIdx.x; i < 256; i += blockDim.x) {
+            const uint32_t g = c_iq3xxs_grid[i];
+            ((uint2 *)tab)[i] = make_uint2(g, mq_neg_bytes(g));
+        }
         mq_fill_signs<T>(tab + MQ<T>::grid_bytes);
     }
 }

@@ -1381,7 +1381,7 @@ static int mq_code(int t) {
 }
 #define MQ_FORMATS 9
 static const int k_mq_words[MQ_FORMATS] = { 7, 7, 9, 5, 7, 11, 15, 9, 17 };   /* padded words per lane (MQ<T>::Wp) */
-static const size_t k_mq_table[MQ_FORMATS] = { 0, 0, 0, 5120, 2048, 0, 0, 0, 0 };   /* LDS codebook and sign masks (MQ<T>::table_bytes) */
+static const size_t k_mq_table[MQ_FORMATS] = { 0, 0, 0, 5120, 3072, 0, 0, 0, 0 };   /* LDS codebook and sign selectors (MQ<T>::table_bytes) */
 /* Converter waves are planned only for the formats where they measured
  * faster (the IQ2_XS / IQ3_XXS matvecs); the others' stepping waves need
  * all 16. */
