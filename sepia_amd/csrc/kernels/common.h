@@ -71,8 +71,12 @@ __device__ __forceinline__ void sepia_kernarg_warm() {
 // the host reads after each batch, sepia_wait_ticks bounds every spin wait
 // of a kernel in s_memrealtime ticks (100 MHz). The whole library is one
 // code object, so these are its only definitions.
-extern "C" __device__ uint32_t *sepia_err_word;
-extern "C" __device__ uint64_t sepia_wait_ticks;
+// Both are constant memory: the kernels read them through the scalar cache.
+// (As plain device globals the bound was a vector load in every spin of a
+// wait, and under a launch's weight stream each such load took a loaded
+// memory round trip, so a wave saw its counter reached that much later.)
+extern "C" __constant__ uint32_t *sepia_err_word;
+extern "C" __constant__ uint64_t sepia_wait_ticks;
 // Record error `code` (first one wins) in *err, or in the device error word
 // when err is NULL; lane 0 of the calling wave writes.
 __device__ __forceinline__ void sepia_report_error(uint32_t *err, uint32_t code, int lane) {

@@ -7,8 +7,8 @@
 
 // The device error word's address and the spin-wait bound (common.h): the
 // host writes both right after loading this code object.
-extern "C" __device__ uint32_t *sepia_err_word = nullptr;
-extern "C" __device__ uint64_t sepia_wait_ticks = 200000000ull;
+extern "C" __constant__ uint32_t *sepia_err_word = nullptr;
+extern "C" __constant__ uint64_t sepia_wait_ticks = 200000000ull;
 
 // ------------------------------------------------------------------------
 // Standalone dequantization (reference metal/matvec_q.metal:578-660): one
