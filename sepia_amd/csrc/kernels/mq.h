@@ -1110,11 +1110,16 @@ __device__ __forceinline__ int mq_wave_id() { return __builtin_amdgcn_readfirstl
 // another bound). On expiry the wave goes on and code 5 goes to err, or
 // else to the library's device error word, which the host checks when the
 // batch ends: the launch's outputs are then invalid.
+// The elapsed time is compared in 32 bits (bounds up to 2^32 - 1 ticks, 42
+// s): a scalar compare, where a 64-bit one needs a VGPR copy of the bound
+// that can make the poll loop wait for the wave's outstanding loads.
 __device__ __forceinline__ void mq_waves_wait(uint32_t *c, uint32_t target, int lane, uint32_t *err) {
     const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+    const uint64_t b64 = sepia_wait_ticks;
+    const uint32_t bound = b64 > 0xFFFFFFFFull ? 0xFFFFFFFFu : (uint32_t)b64;
     while (__hip_atomic_load(c, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < target) {
         __builtin_amdgcn_s_sleep(1);
-        if (__builtin_amdgcn_s_memrealtime() - t0 > sepia_wait_ticks) {
+        if ((uint32_t)(__builtin_amdgcn_s_memrealtime() - t0) > bound) {
             sepia_report_error(err, 5u, lane);
             return;
         }
