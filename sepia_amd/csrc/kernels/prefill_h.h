@@ -42,7 +42,9 @@
 // come from the grid byte b and a sign byte (0x80 or 0x00, a table per sign
 // index) by one permute per two codes that makes the half +-b 2^-24 (the
 // f16 subnormal with mantissa b), then one packed f16 multiply by
-// (2 s + 1) 2^10: every intermediate exact.
+// (2 s + 1) 2^10: every intermediate exact. (The multiply reads the
+// subnormal as such: f16 denormals are on in the kernels' default FP mode,
+// and a flush would zero every IQ code, which every IQ parity case shows.)
 //
 // Workgroup: one unit (<= 32 pairs of one expert) x R weight rows (R = 256:
 // gate/up 128 gate + the same 128 up rows; R = 128 for the formats whose
