@@ -746,7 +746,7 @@ def main():
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py: this build measures one GPU only (the path has no multi-GPU "
-              "component; sharding is described in DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+              "component: each GPU would run it on its own experts' share). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
     from sepia_amd import hip
