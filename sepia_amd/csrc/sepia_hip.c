@@ -1382,10 +1382,15 @@ static int mq_code(int t) {
 #define MQ_FORMATS 9
 static const int k_mq_words[MQ_FORMATS] = { 7, 7, 9, 5, 7, 11, 15, 9, 17 };   /* padded words per lane (MQ<T>::Wp) */
 static const size_t k_mq_table[MQ_FORMATS] = { 0, 0, 0, 5120, 3072, 0, 0, 0, 0 };   /* LDS codebook and sign selectors (MQ<T>::table_bytes) */
-/* Converter waves are planned only for the formats where they measured
- * faster (the IQ2_XS / IQ3_XXS matvecs); the others' stepping waves need
- * all 16. */
-static const int k_mq_conv[MQ_FORMATS] = { 0, 0, 0, 1, 1, 0, 0, 0, 0 };
+/* Converter waves are planned in the matvecs of every format but Q2_K.
+ * Interleaved on one box, kernel us at 4096^2 / 6144^2, planner without
+ * them -> with them: Q3_K 6.22 -> 5.53 / 9.96 -> 8.26, Q4_K 6.55 -> 5.61 /
+ * 9.84 -> 8.50, Q5_K 6.93 -> 6.37 / 11.30 -> 9.40, Q6_K 7.21 -> 7.00 /
+ * 12.40 -> 11.83, Q8_0 7.34 -> 6.63 / 12.16 -> 10.90, IQ4_XS 7.06 -> 6.30 /
+ * 11.62 -> 9.50 (IQ2_XS and IQ3_XXS already had them); Q2_K 4.63 -> 5.08
+ * / 7.95 -> 7.08, its light decode needing all 16 waves stepping at the
+ * smaller size. */
+static const int k_mq_conv[MQ_FORMATS] = { 0, 1, 1, 1, 1, 1, 1, 1, 1 };
 /* Relative time per weight byte of the matrix-core decoders (percent; the
  * K-quants Q4_K, Q5_K, Q6_K = 100), used to split an FFN launch's
  * workgroups between routed and shared experts. Measured on the MoE decode
