@@ -689,8 +689,10 @@ template <> struct MQ<ST_Q4_K> {
 // The three plane dots of a segment combined in f32: with codebook weights
 // up to 62 the exact integer can pass 2^31 (mq_combine holds it for weights
 // <= 15 only); each term is exact in f32, their sum rounds once or twice.
+// 256 d1 + d2 stays exact in i32 (|d_p| <= 16 * 127 * 128 per segment), and
+// one convert rounds it exactly as the f32 fma of d1, 256 and d2 would.
 __device__ __forceinline__ float mq_combine_f(const mq_v4i &d) {
-    return __builtin_fmaf((float)d[0], 65536.0f, __builtin_fmaf((float)d[1], 256.0f, (float)d[2]));
+    return __builtin_fmaf((float)d[0], 65536.0f, (float)(int32_t)(((uint32_t)d[1] << 8) + (uint32_t)d[2]));
 }
 // The four signed codes of codebook word g (ng: its bytewise negation) by
 // the selector word sel.
