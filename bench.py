@@ -240,6 +240,7 @@ MEASURED_TRAFFIC_C2 = {"sepia_mq_gateup": 13001871, "sepia_mq_down": 8582520}
 MEASURED_TRAFFIC_C3 = {"sepia_moe_route": 6612357, "sepia_mq_gateup": 122283851, "sepia_mq_down": 72124327}
 MEASURED_TRAFFIC_REAL = {"sepia_moe_route": 6612386, "sepia_mq_gateup": 118571552, "sepia_mq_down": 76561443}
 MEASURED_TRAFFIC_C5 = {"sepia_pf_gateup_q": 2999146132, "sepia_pf_down_q": 1900014470}
+MEASURED_TRAFFIC_C5_REAL = {"sepia_ph_gateup": 3364945920, "sepia_ph_down": 2298700800}   # moe_prefill_c5_real_counters.md
 
 
 def cpu_sample(fn, min_seconds, max_calls):
@@ -719,7 +720,7 @@ def run_c5(B, warmup, steps, cpu_seconds, T=512, types=C3_TYPES):
                 # the int8 path issues three digit planes per product, at the 5.0 POP/s int8 peak
                 mfma_util_int8_issued=3 * flops / sec / 5.0e15 if types == C3_TYPES else None,
                 kernels_avg_ms={k: v for k, v in kms.items()},
-                traffic_bytes=MEASURED_TRAFFIC_C5 if types == C3_TYPES else None,
+                traffic_bytes=MEASURED_TRAFFIC_C5 if types == C3_TYPES else MEASURED_TRAFFIC_C5_REAL,
                 parity=dict(tokens=sample, max_abs_diff=err, y_inf=scale, bound="1e-4*||y||_inf",
                             selections_checked=T),
                 cpu_1core_ms_per_token=s1 * 1e3)
