@@ -152,9 +152,9 @@ class Bench:
     def timed_steps(self, step, warmup, steps):
         """W untimed warmup steps, then exactly `steps` steps between two events on the
         library's stream; returns ms per step. TIMING selects how the timed steps are issued:
-        "step-graphs" (default) captures each step as its own HIP graph and launches the
-        graphs back to back, "graph" replays all steps from one captured graph, "eager"
-        issues them through the C ABI directly. Every mode first runs the exact timed
+        "graph" (default) replays all steps from one captured graph, "step-graphs" captures
+        each step as its own HIP graph and launches the graphs back to back, "eager" issues
+        them through the C ABI directly. Every mode first runs the exact timed
         sequence once untimed (graph upload, caches)."""
         dev = self.dev
         dev.begin()
