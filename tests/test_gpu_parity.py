@@ -913,6 +913,8 @@ PREFILL_CASES = [
     ((2048, 1024, 12, 2), (17, 23, 13, 14), 40),  # IQ4_XS down
     ((1024, 2048, 8, 2), (13, 14, 13, 14), 20),   # Q5_K / Q6_K routed
     ((256, 512, 8, 1), (17, 18, 13, 14), 11),     # the smallest grids: one 256-row workgroup per slice row
+    ((2048, 1024, 8, 0), (17, 18, 13, 14), 15),   # no shared experts (f16 kernels)
+    ((2048, 1024, 8, 0), (10, 11, 12), 15),       # no shared experts (int8 kernels)
 ]
 # Layers with Q8_0 projections: the f16 kernels only (no bf16 kernel takes Q8_0).
 PREFILL_CASES_Q8 = [
