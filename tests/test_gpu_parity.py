@@ -915,6 +915,8 @@ PREFILL_CASES = [
     ((256, 512, 8, 1), (17, 18, 13, 14), 11),     # the smallest grids: one 256-row workgroup per slice row
     ((2048, 1024, 8, 0), (17, 18, 13, 14), 15),   # no shared experts (f16 kernels)
     ((2048, 1024, 8, 0), (10, 11, 12), 15),       # no shared experts (int8 kernels)
+    ((2048, 1024, 8, 2), (17, 18, 13, 14), 1),    # one token: every unit a single pair (f16)
+    ((2048, 1024, 8, 2), (10, 11, 12), 1),        # one token (int8)
 ]
 # Layers with Q8_0 projections: the f16 kernels only (no bf16 kernel takes Q8_0).
 PREFILL_CASES_Q8 = [
