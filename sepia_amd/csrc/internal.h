@@ -28,5 +28,7 @@ SEPIA_HIDDEN size_t sepia_buf_len(const SepiaGpuBuf *b);
 SEPIA_HIDDEN int64_t sepia_row_bytes(int ggml_type, int64_t n);
 /* Count one device or pinned-host allocation (sepia_hip_alloc_count). */
 SEPIA_HIDDEN void sepia_count_alloc(void);
+/* Release store.c's pinned staging buffers (sepia_gpu_shutdown calls it). */
+SEPIA_HIDDEN void sepia_store_shutdown(void);
 
 #endif

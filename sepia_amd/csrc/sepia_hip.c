@@ -680,6 +680,7 @@ int sepia_gpu_init(const char *kernel_dir) {
 void sepia_gpu_shutdown(void) {
     if (!g_available) return;
     hipStreamSynchronize(g_stream);
+    sepia_store_shutdown();
     if (g_scratch) hipFree(g_scratch);
     g_scratch = NULL;
     g_scratch_len = 0;
