@@ -433,13 +433,96 @@ static SepiaGpuBuf *new_buf(size_t len, int kind) {
     return b;
 }
 
+/* Freed buffers kept for reuse. The reference's host path allocates and
+ * frees its temporaries around single ops (src/sepia.c real_forward_chunk_gpu:
+ * about 36 buffers per token, most of them 0.1-400 KB), and a fresh shared
+ * buffer costs a pinned host allocation, a device allocation and a stream
+ * synchronisation (about 0.2 ms with its release). A freed shared or
+ * private buffer of at most POOL_BUF_MAX bytes therefore goes to this pool
+ * while it holds fewer than POOL_MAX buffers and POOL_BYTES_MAX bytes; an
+ * allocation of the same kind and length takes it back, cleared again as a
+ * new one is (device copy by a fill queued on the library's stream, host
+ * copy by memset) without another synchronisation. sepia_gpu_shutdown
+ * releases the pool. */
+#define POOL_MAX 256
+#define POOL_BUF_MAX ((size_t)64 << 20)
+#define POOL_BYTES_MAX ((size_t)512 << 20)
+typedef struct {
+    uint8_t *dev;
+    void *host;
+    uint64_t *dirty;
+    size_t len;
+    int kind;
+} PoolEnt;
+static PoolEnt g_pool[POOL_MAX];
+static int g_pool_n;
+static size_t g_pool_bytes;
+
+static size_t pool_cost(const PoolEnt *p) { return dev_bytes(p->len) + (p->host ? p->len : 0); }
+
+static void pool_release(PoolEnt *p) {
+    if (p->host) hipHostFree(p->host);
+    free(p->dirty);
+    hipFree(p->dev);
+}
+
+static void pool_release_all(void) {
+    for (int i = 0; i < g_pool_n; i++) pool_release(&g_pool[i]);
+    g_pool_n = 0;
+    g_pool_bytes = 0;
+}
+
+/* Keep b's memory for reuse; 0 if the pool does not take it (the caller
+ * frees it). The stream has been synchronised: nothing queued uses it. */
+static int pool_put(SepiaGpuBuf *b) {
+    if (b->kind == BUF_WRAPPED || b->len > POOL_BUF_MAX || g_pool_n == POOL_MAX) return 0;
+    const PoolEnt p = { b->dev, b->host, b->dirty, b->len, b->kind };
+    if (g_pool_bytes + pool_cost(&p) > POOL_BYTES_MAX) return 0;
+    g_pool[g_pool_n++] = p;
+    g_pool_bytes += pool_cost(&p);
+    return 1;
+}
+
+/* A cleared buffer of this kind and length from the pool, or NULL. */
+static SepiaGpuBuf *pool_take(size_t len, int kind) {
+    int i = g_pool_n - 1;
+    while (i >= 0 && (g_pool[i].kind != kind || g_pool[i].len != len)) i--;
+    if (i < 0) return NULL;
+    SepiaGpuBuf *b = (SepiaGpuBuf *)calloc(1, sizeof *b);
+    if (!b) return NULL;
+    PoolEnt p = g_pool[i];
+    g_pool[i] = g_pool[--g_pool_n];
+    g_pool_bytes -= pool_cost(&p);
+    if (hipMemsetAsync(p.dev, 0, dev_bytes(len), g_stream) != hipSuccess) {
+        pool_release(&p);
+        free(b);
+        return NULL;
+    }
+    b->dev = p.dev;
+    b->len = len;
+    b->kind = kind;
+    if (kind == BUF_SHARED) {
+        b->host = p.host;
+        memset(b->host, 0, len);
+        b->nchunks = (len + SHADOW_CHUNK - 1) / SHADOW_CHUNK;
+        b->dirty = p.dirty;
+        memset(b->dirty, 0, ((b->nchunks + 63) / 64) * sizeof(uint64_t));
+        b->next = g_shared;
+        if (g_shared) g_shared->prev = b;
+        g_shared = b;
+    }
+    return b;
+}
+
 SepiaGpuBuf *sepia_gpu_alloc(size_t len, int gpu_private) {
     if (!need_init("alloc")) return NULL;
     if (len == 0) {
         LOG("alloc: zero length");
         return NULL;
     }
-    SepiaGpuBuf *b = new_buf(len, gpu_private ? BUF_PRIVATE : BUF_SHARED);
+    SepiaGpuBuf *b = pool_take(len, gpu_private ? BUF_PRIVATE : BUF_SHARED);
+    if (b) return b;
+    b = new_buf(len, gpu_private ? BUF_PRIVATE : BUF_SHARED);
     if (!b) return NULL;
     hipError_t e = hipMemsetAsync(b->dev, 0, dev_bytes(len), g_stream);
     if (e == hipSuccess) e = hipStreamSynchronize(g_stream);
@@ -508,6 +591,12 @@ void sepia_gpu_free(SepiaGpuBuf *b) {
         if (b->prev) b->prev->next = b->next;
         else g_shared = b->next;
         if (b->next) b->next->prev = b->prev;
+    }
+    if (g_available && pool_put(b)) {
+        free(b);
+        return;
+    }
+    if (b->kind == BUF_SHARED) {
         if (b->host) hipHostFree(b->host);
         free(b->dirty);
     }
@@ -681,6 +770,7 @@ void sepia_gpu_shutdown(void) {
     if (!g_available) return;
     hipStreamSynchronize(g_stream);
     sepia_store_shutdown();
+    pool_release_all();
     if (g_scratch) hipFree(g_scratch);
     g_scratch = NULL;
     g_scratch_len = 0;

@@ -261,13 +261,14 @@ def write_layer_store(out_dir, rng, layer, hidden, inter, n_routed, n_shared, ty
 
 
 # -------------------------------------------------------------- tiny model --
-def tiny_config(n_layers=4, hidden=512, vocab=272, unpadded=266):
+def tiny_config(n_layers=4, hidden=512, vocab=272, unpadded=266, moe_inter=256, n_routed=16, sparse=True):
     """A small model config in the reference's config.json layout
     (docs/inkling-config.json; read by src/sepia.c:455-560): sliding and
     global attention layers of different head geometries, one dense FFN
-    layer then MoE layers, top-6 of 16 routed experts plus 2 shared. The
-    log-scaling floor is low enough that the attention temperature tau
-    changes within a short prompt."""
+    layer then MoE layers (every layer dense if not sparse), top-6 of
+    n_routed routed experts plus 2 shared. The log-scaling floor is low
+    enough that the attention temperature tau changes within a short
+    prompt."""
     layer_types = ["hybrid_sliding" if (i % 3) != 2 else "hybrid" for i in range(n_layers)]
     return {"architectures": ["InklingForConditionalGeneration"], "model_type": "inkling_mm_model",
             "text_config": {
@@ -276,10 +277,10 @@ def tiny_config(n_layers=4, hidden=512, vocab=272, unpadded=266):
                 "num_attention_heads": 4, "num_key_value_heads": 2, "head_dim": 64,
                 "swa_num_attention_heads": 4, "swa_num_key_value_heads": 4, "swa_head_dim": 32,
                 "sliding_window_size": 8, "layer_types": layer_types,
-                "mlp_layer_types": ["dense"] + ["sparse"] * (n_layers - 1),
+                "mlp_layer_types": ["dense"] + ["sparse" if sparse else "dense"] * (n_layers - 1),
                 "d_rel": 16, "rel_extent": 32, "conv_kernel_size": 4,
-                "intermediate_size": 512, "moe_intermediate_size": 256,
-                "n_routed_experts": 16, "num_experts_per_tok": 6, "n_shared_experts": 2,
+                "intermediate_size": 512, "moe_intermediate_size": moe_inter,
+                "n_routed_experts": n_routed, "num_experts_per_tok": 6, "n_shared_experts": 2,
                 "route_scale": 8.0, "logits_mup_width_multiplier": 24.0, "rms_norm_eps": 1e-6,
                 "log_scaling_alpha": 0.1, "log_scaling_n_floor": 4}}
 
@@ -302,9 +303,14 @@ def _q(name, t, in_dim, out_dim, rng, stack=None):
     return (name, dims, t, data)
 
 
-def write_tiny_model(out_dir, rng, tokenizer_src, n_layers=4, n_parts=2):
-    """A complete model in the reference's real-checkpoint formats, small
-    enough to build in seconds: config.json, tokenizer.bin (copied from
+def write_tiny_model(out_dir, rng, tokenizer_src, n_layers=4, n_parts=2, hidden=512, moe_inter=256, n_routed=16,
+                     sparse=True, expert_types=None):
+    """A complete model in the reference's real-checkpoint formats, by
+    default small enough to build in seconds (hidden, moe_inter and n_routed
+    set the MoE layers' shape; expert_types, a (gate/up, down, shared
+    gate/up, shared down) type tuple, replaces the per-layer rotation of
+    TINY_EXPERT_TYPES; sparse=False makes every layer dense): config.json,
+    tokenizer.bin (copied from
     tokenizer_src, an SPTK v1 sidecar), GGUF parts under inkling-gguf/, the
     sepia-index sidecar (index.json) and resident.bin + its manifest. Every
     tensor real_load resolves (reference src/sepia.c:2647-2861) is present:
@@ -316,7 +322,7 @@ def write_tiny_model(out_dir, rng, tokenizer_src, n_layers=4, n_parts=2):
     (f16 scales in [2^-10, 2^-6]); f32 norms ~ 1 + N(0, 0.1), short-conv taps
     and relative projections ~ N(0, 0.3). Returns the four paths the
     reference reads through SEPIA_REAL_{CONFIG,MANIFEST,INDEX,TOKENIZER}_PATH."""
-    cfg = tiny_config(n_layers)
+    cfg = tiny_config(n_layers, hidden=hidden, moe_inter=moe_inter, n_routed=n_routed, sparse=sparse)
     tc = cfg["text_config"]
     H, V = tc["hidden_size"], tc["vocab_size"]
     K, d_rel, inter = tc["conv_kernel_size"], tc["d_rel"], tc["moe_intermediate_size"]
@@ -350,7 +356,7 @@ def write_tiny_model(out_dir, rng, tokenizer_src, n_layers=4, n_parts=2):
             res += [_q(p + "ffn_gate.weight", 12, H, di, rng), _q(p + "ffn_up.weight", 12, H, di, rng),
                     _q(p + "ffn_down.weight", 14, di, H, rng), _f32(p + "ffn_gscale.weight", [1], [1.25])]
         else:
-            tg, td, tsg, tsd = TINY_EXPERT_TYPES[L % len(TINY_EXPERT_TYPES)]
+            tg, td, tsg, tsd = expert_types or TINY_EXPERT_TYPES[L % len(TINY_EXPERT_TYPES)]
             res += [_f32(p + "ffn_gate_inp.weight", [H, n_r + n_s], 0.02 * rng.standard_normal((n_r + n_s) * H)),
                     _f32(p + "exp_probs_b.bias", [n_r], rng.uniform(-0.1, 0.1, n_r)),
                     _f32(p + "ffn_gscale.weight", [1], [0.75]),
