@@ -15,6 +15,8 @@ engine (about a minute at this size) need not run on the GPU box.
 
 Run from the repository root after oracle/_ref is built:
     python tests/golden/make_ref_host_c3.py [scratch_dir]
+With --models-only DIR it only writes the model to DIR/moe and its twin
+with a dense FFN in layer 1 to DIR/dense (for profiling the GPU path).
 """
 import json
 import os
@@ -36,10 +38,10 @@ SPEC = dict(seed=2024, n_layers=2, hidden=6144, moe_inter=3072, n_routed=256, ex
             prompt="hello the thing in the end, hello", n_gen=8)
 
 
-def write_model(out_dir):
+def write_model(out_dir, sparse=True):
     return store_synth.write_tiny_model(out_dir, np.random.default_rng(SPEC["seed"]), TOKENIZER,
                                         n_layers=SPEC["n_layers"], hidden=SPEC["hidden"],
-                                        moe_inter=SPEC["moe_inter"], n_routed=SPEC["n_routed"],
+                                        moe_inter=SPEC["moe_inter"], n_routed=SPEC["n_routed"], sparse=sparse,
                                         expert_types=tuple(SPEC["expert_types"]))
 
 
@@ -55,6 +57,10 @@ def run(env, *args):
 
 
 def main():
+    if len(sys.argv) == 3 and sys.argv[1] == "--models-only":
+        write_model(os.path.join(sys.argv[2], "moe"))
+        write_model(os.path.join(sys.argv[2], "dense"), sparse=False)
+        return
     scratch = sys.argv[1] if len(sys.argv) > 1 else tempfile.mkdtemp(prefix="ref-host-c3-")
     paths = write_model(os.path.join(scratch, "model"))
     env = env_for(paths)
