@@ -483,8 +483,13 @@ static int pool_put(SepiaGpuBuf *b) {
     return 1;
 }
 
-/* A cleared buffer of this kind and length from the pool, or NULL. */
+/* A cleared buffer of this kind and length from the pool, or NULL. Not
+ * while the library's stream is being captured: the clearing fill would
+ * become a node of the caller's graph (a fresh allocation fails there, at
+ * its stream synchronisation, as before). */
 static SepiaGpuBuf *pool_take(size_t len, int kind) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(g_stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return NULL;
     int i = g_pool_n - 1;
     while (i >= 0 && (g_pool[i].kind != kind || g_pool[i].len != len)) i--;
     if (i < 0) return NULL;
