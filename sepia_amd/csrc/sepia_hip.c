@@ -438,12 +438,12 @@ static SepiaGpuBuf *new_buf(size_t len, int kind) {
  * about 36 buffers per token, most of them 0.1-400 KB), and a fresh shared
  * buffer costs a pinned host allocation, a device allocation and a stream
  * synchronisation (about 0.2 ms with its release). A freed shared or
- * private buffer of at most POOL_BUF_MAX bytes therefore goes to this pool
- * while it holds fewer than POOL_MAX buffers and POOL_BYTES_MAX bytes; an
- * allocation of the same kind and length takes it back, cleared again as a
- * new one is (device copy by a fill queued on the library's stream, host
- * copy by memset) without another synchronisation. sepia_gpu_shutdown
- * releases the pool. */
+ * private buffer of at most POOL_BUF_MAX bytes therefore goes to this pool,
+ * which releases its oldest buffers to stay within POOL_MAX buffers and
+ * POOL_BYTES_MAX bytes; an allocation of the same kind and length takes
+ * the newest such buffer back, cleared again as a new one is (device copy
+ * by a fill queued on the library's stream, host copy by memset) without
+ * another synchronisation. sepia_gpu_shutdown releases the pool. */
 #define POOL_MAX 256
 #define POOL_BUF_MAX ((size_t)64 << 20)
 #define POOL_BYTES_MAX ((size_t)512 << 20)
@@ -472,12 +472,25 @@ static void pool_release_all(void) {
     g_pool_bytes = 0;
 }
 
-/* Keep b's memory for reuse; 0 if the pool does not take it (the caller
- * frees it). The stream has been synchronised: nothing queued uses it. */
+/* Entry i out of the pool, the order of the others kept (oldest first). */
+static PoolEnt pool_remove(int i) {
+    const PoolEnt p = g_pool[i];
+    memmove(&g_pool[i], &g_pool[i + 1], (size_t)(g_pool_n - 1 - i) * sizeof g_pool[0]);
+    g_pool_n--;
+    g_pool_bytes -= pool_cost(&p);
+    return p;
+}
+
+/* Keep b's memory for reuse, releasing the oldest kept buffers as needed;
+ * 0 if the pool does not take it (the caller frees it). The stream has
+ * been synchronised: nothing queued uses b or the buffers released. */
 static int pool_put(SepiaGpuBuf *b) {
-    if (b->kind == BUF_WRAPPED || b->len > POOL_BUF_MAX || g_pool_n == POOL_MAX) return 0;
+    if (b->kind == BUF_WRAPPED || b->len > POOL_BUF_MAX) return 0;
     const PoolEnt p = { b->dev, b->host, b->dirty, b->len, b->kind };
-    if (g_pool_bytes + pool_cost(&p) > POOL_BYTES_MAX) return 0;
+    while (g_pool_n > 0 && (g_pool_n == POOL_MAX || g_pool_bytes + pool_cost(&p) > POOL_BYTES_MAX)) {
+        PoolEnt old = pool_remove(0);
+        pool_release(&old);
+    }
     g_pool[g_pool_n++] = p;
     g_pool_bytes += pool_cost(&p);
     return 1;
@@ -495,9 +508,7 @@ static SepiaGpuBuf *pool_take(size_t len, int kind) {
     if (i < 0) return NULL;
     SepiaGpuBuf *b = (SepiaGpuBuf *)calloc(1, sizeof *b);
     if (!b) return NULL;
-    PoolEnt p = g_pool[i];
-    g_pool[i] = g_pool[--g_pool_n];
-    g_pool_bytes -= pool_cost(&p);
+    PoolEnt p = pool_remove(i);
     if (hipMemsetAsync(p.dev, 0, dev_bytes(len), g_stream) != hipSuccess) {
         pool_release(&p);
         free(b);

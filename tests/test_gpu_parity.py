@@ -546,6 +546,34 @@ def test_shared_slab_uploaded_once(dev, orc):
 
 
 
+def test_freed_buffers_come_back_cleared(dev):
+    """sepia_gpu_free keeps buffers of up to 64 MB; an allocation of the same
+    kind and length takes one back without a new device or pinned
+    allocation, and finds it cleared like a new buffer: the host copy, and
+    the device copy an op reads before the host touches the buffer."""
+    L = dev.L
+    n = 3 * (1 << 16) + 256
+    sevens = np.full(n // 4, 7.0, np.float32)
+    a, out = dev.shared_from(sevens), dev.alloc(n)
+    dev.run(L.sepia_gpu_copy, a, 0, out, 0, n // 4)
+    assert np.all(dev.download(out, n // 4) == 7.0)
+    p = dev.alloc(n, private=True)
+    dev.run(L.sepia_gpu_copy, a, 0, p, 0, n // 4)
+    for buf in (a, out, p):
+        dev.free(buf)
+    c0 = L.sepia_hip_alloc_count()
+    b, c = dev.alloc(n), dev.alloc(n)
+    q = dev.alloc(n, private=True)
+    assert L.sepia_hip_alloc_count() == c0, "a freed buffer of the same length was not reused"
+    dev.run(L.sepia_gpu_copy, b, 0, c, 0, n // 4)        # b's device copy, untouched by the host
+    assert np.all(dev.download(c, n // 4) == 0.0)
+    dev.run(L.sepia_gpu_copy, q, 0, c, 0, n // 4)        # the private one's
+    assert np.all(dev.download(c, n // 4) == 0.0)
+    assert np.all(dev.download(b, n // 4) == 0.0)        # b's host copy
+    for buf in (b, c, q):
+        dev.free(buf)
+
+
 def test_shared_slab_partial_chunk_writes(dev, orc):
     """The reference's expert cache hands a slab's host pointer out once per
     miss, and its loader threads fill that expert's slot while hit experts of
