@@ -173,9 +173,10 @@ static Stager g_stager;
 static int g_stager_ready;
 static pthread_mutex_t g_stage_lock = PTHREAD_MUTEX_INITIALIZER;
 
-/* Lock the staging pair, allocating it on first use (one thread writes a
- * byte of each page once, so the readers never meet an unmapped page).
- * NULL, unlocked and logged, when the allocation fails. */
+/* Lock the staging pair, allocating it on first use; one thread then
+ * writes a byte of each page: four readers writing a freshly allocated
+ * pair ran at half one reader's rate, and at twice it once its pages had
+ * been written. NULL, unlocked and logged, when the allocation fails. */
 static Stager *stager_acquire(const char *op) {
     pthread_mutex_lock(&g_stage_lock);
     if (!g_stager_ready) {
